@@ -1,0 +1,117 @@
+// Per-lane channel vectors for the wave-per-row kernels: a wave64 covers one C-wide feature
+// row with CPL = C/64 consecutive channels per lane, so every row access is one coalesced
+// 256*CPL-byte transaction.
+#pragma once
+#include "fu_common.h"
+
+namespace fu {
+
+template <int CPL>
+struct Vec {
+  float v[CPL];
+  __device__ __forceinline__ float& operator[](int k) { return v[k]; }
+  __device__ __forceinline__ const float& operator[](int k) const { return v[k]; }
+};
+
+template <int CPL>
+__device__ __forceinline__ Vec<CPL> vload(const float* p) {
+  Vec<CPL> r;
+  if constexpr (CPL == 4) {
+    const float4 t = *reinterpret_cast<const float4*>(p);
+    r.v[0] = t.x; r.v[1] = t.y; r.v[2] = t.z; r.v[3] = t.w;
+  } else if constexpr (CPL == 2) {
+    const float2 t = *reinterpret_cast<const float2*>(p);
+    r.v[0] = t.x; r.v[1] = t.y;
+  } else {
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) r.v[k] = p[k];
+  }
+  return r;
+}
+
+template <int CPL>
+__device__ __forceinline__ void vstore(float* p, const Vec<CPL>& a) {
+  if constexpr (CPL == 4) {
+    *reinterpret_cast<float4*>(p) = make_float4(a.v[0], a.v[1], a.v[2], a.v[3]);
+  } else if constexpr (CPL == 2) {
+    *reinterpret_cast<float2*>(p) = make_float2(a.v[0], a.v[1]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) p[k] = a.v[k];
+  }
+}
+
+template <int CPL>
+__device__ __forceinline__ Vec<CPL> vzero() {
+  Vec<CPL> r;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) r.v[k] = 0.0f;
+  return r;
+}
+
+template <int CPL>
+__device__ __forceinline__ Vec<CPL> vmul(const Vec<CPL>& a, const Vec<CPL>& b) {
+  Vec<CPL> r;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) r.v[k] = a.v[k] * b.v[k];
+  return r;
+}
+
+template <int CPL>
+__device__ __forceinline__ Vec<CPL> vadd(const Vec<CPL>& a, const Vec<CPL>& b) {
+  Vec<CPL> r;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) r.v[k] = a.v[k] + b.v[k];
+  return r;
+}
+
+template <int CPL>
+__device__ __forceinline__ Vec<CPL> vscale(const Vec<CPL>& a, float s) {
+  Vec<CPL> r;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) r.v[k] = a.v[k] * s;
+  return r;
+}
+
+template <int CPL>
+__device__ __forceinline__ float vdot(const Vec<CPL>& a, const Vec<CPL>& b) {
+  float s = 0.0f;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) s += a.v[k] * b.v[k];
+  return s;
+}
+
+// Recursive halving over lane offsets V/2, V/4, ..., 1: at each step a lane keeps half of
+// its values and adds the partner's copy of that half.  Afterwards lane l holds the sum of
+// value (l mod V) over the 2^log2(V) lanes that share l's high bits.
+template <int V>
+__device__ __forceinline__ float halve_values(const float (&vals)[V], int lane) {
+  if constexpr (V == 1) {
+    return vals[0];
+  } else {
+    constexpr int H = V / 2;
+    const bool upper = (lane & H) != 0;
+    float nxt[H];
+#pragma unroll
+    for (int k = 0; k < H; ++k) {
+      const float send = upper ? vals[k] : vals[k + H];
+      const float keep = upper ? vals[k + H] : vals[k];
+      nxt[k] = keep + __shfl_xor(send, H, 64);
+    }
+    return halve_values<H>(nxt, lane);
+  }
+}
+
+// Sum V per-lane values over all 64 lanes of a wave (V a power of two <= 64).  Lane l
+// receives the total of value (l mod V).  Costs V - 1 + (6 - log2 V) shuffles instead of
+// 6 V for V independent butterflies.
+template <int V>
+__device__ __forceinline__ float wave_multi_sum(const float (&vals)[V], int lane) {
+  static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "V must be a power of two <= 64");
+  float r = halve_values<V>(vals, lane);
+#pragma unroll
+  for (int o = V; o < 64; o <<= 1) r += __shfl_xor(r, o, 64);
+  return r;
+}
+
+}  // namespace fu

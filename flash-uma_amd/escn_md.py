@@ -1,0 +1,251 @@
+"""Random-init stand-in for FAIRChem's UMA eSCN-MD backbone and its node-level modules.
+
+The reference wraps an official `eSCNMDBackbone` (fairchem.core.models.uma.escn_md) and
+copies its weights (wrapper.py:22-85); FAIRChem is not in the reference tree and cannot be
+installed offline.  This module provides an object with exactly the attributes
+`transfer_weights` and `ZeroAllocBackbone.__init__` read (wrapper.py:28-146), shaped like
+UMA-s, with seeded random weights, plus the node modules the reference attaches by
+reference (norm_1, norm_2, atom_wise, final norm, charge/spin embeddings).
+
+The node modules restate the FAIRChem designs from memory; their parity is unpinned (no
+reference code or fixtures exist here), so they are checked only by invariants (rotation
+equivariance, normalisation).  They run as torch modules on the GPU, outside the HIP hot
+path, exactly as the reference runs FAIRChem's modules in torch eager.
+
+Initialisation (seeded CPU torch.Generator, fixed creation order): nn.Linear default
+(kaiming-uniform weights, uniform bias), nn.Embedding N(0, 1), LayerNorm/affine weights 1,
+biases 0.
+"""
+from __future__ import annotations
+
+import math
+from types import SimpleNamespace
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+
+def num_coefficients(lmax: int) -> int:
+    return (lmax + 1) ** 2
+
+
+def degree_index(lmax: int) -> torch.Tensor:
+    """Degree l of every SH coefficient k (k = l^2 + l + m)."""
+    return torch.cat([torch.full((2 * l + 1,), l, dtype=torch.long) for l in range(lmax + 1)])
+
+
+class EquivariantRMSNormArraySphericalHarmonicsV2(nn.Module):
+    """Equivariant RMS norm over SH coefficients (FAIRChem's "rms_norm_sh" layer, recalled):
+    subtract the channel mean of l=0, scale every coefficient by
+    (mean_c sum_l w_l mean_{m} x_{lm,c}^2 + eps)^(-1/2) with degree-balanced weights
+    w_l = 1/(lmax+1), apply a per-(l, c) affine weight and an l=0 bias."""
+
+    def __init__(self, lmax: int, num_channels: int, eps: float = 1e-5):
+        super().__init__()
+        self.lmax = lmax
+        self.num_channels = num_channels
+        self.eps = eps
+        self.affine_weight = nn.Parameter(torch.ones(lmax + 1, num_channels))
+        self.affine_bias = nn.Parameter(torch.zeros(num_channels))
+        self.register_buffer("expand_index", degree_index(lmax), persistent=False)
+        bal = torch.zeros(num_coefficients(lmax), 1)
+        for l in range(lmax + 1):
+            bal[l * l:(l + 1) * (l + 1)] = 1.0 / (2 * l + 1)
+        self.register_buffer("balance_degree_weight", bal / (lmax + 1), persistent=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        l0 = x.narrow(1, 0, 1)
+        l0 = l0 - l0.mean(dim=2, keepdim=True)
+        feat = torch.cat([l0, x.narrow(1, 1, x.shape[1] - 1)], dim=1)
+        norm = (feat.pow(2) * self.balance_degree_weight.unsqueeze(0)).sum(dim=1, keepdim=True)
+        norm = norm.mean(dim=2, keepdim=True)
+        norm = (norm + self.eps).pow(-0.5)
+        w = self.affine_weight.index_select(0, self.expand_index).unsqueeze(0)
+        out = feat * (norm * w)
+        bias = torch.zeros_like(out[:1])
+        bias[:, 0, :] = self.affine_bias
+        return out + bias
+
+
+class SO3_Linear(nn.Module):
+    """Per-degree linear map: coefficient (l, m) of the output is W_l x_(l, m); l=0 has a bias."""
+
+    def __init__(self, in_features: int, out_features: int, lmax: int, generator=None):
+        super().__init__()
+        self.lmax = lmax
+        bound = 1.0 / math.sqrt(in_features)
+        self.weight = nn.Parameter(torch.empty(lmax + 1, out_features, in_features).uniform_(
+            -bound, bound, generator=generator))
+        self.bias = nn.Parameter(torch.empty(out_features).uniform_(-bound, bound, generator=generator))
+        self.register_buffer("expand_index", degree_index(lmax), persistent=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        w = self.weight.index_select(0, self.expand_index)          # (K, out, in)
+        out = torch.einsum("nki,koi->nko", x, w)
+        out[:, 0, :] = out[:, 0, :] + self.bias
+        return out
+
+
+class GateActivation(nn.Module):
+    """l=0 -> SiLU; coefficients of degree l>0 scaled by sigmoid(gate_l) per channel."""
+
+    def __init__(self, lmax: int, num_channels: int):
+        super().__init__()
+        self.lmax = lmax
+        self.num_channels = num_channels
+        self.register_buffer("gate_index", (degree_index(lmax)[1:] - 1), persistent=False)
+
+    def forward(self, gating_scalars: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+        gates = torch.sigmoid(gating_scalars).view(-1, self.lmax, self.num_channels)
+        gates = gates.index_select(1, self.gate_index)
+        return torch.cat([F.silu(x.narrow(1, 0, 1)), x.narrow(1, 1, x.shape[1] - 1) * gates], dim=1)
+
+
+class SpectralAtomwise(nn.Module):
+    """Per-node gated SO(3) feed-forward block (FAIRChem's spectral atom-wise FFN, recalled)."""
+
+    def __init__(self, sphere_channels: int, hidden_channels: int, lmax: int, generator=None):
+        super().__init__()
+        self.scalar_mlp = nn.Sequential(_linear(sphere_channels, lmax * hidden_channels, True, generator), nn.SiLU())
+        self.so3_linear_1 = SO3_Linear(sphere_channels, hidden_channels, lmax, generator)
+        self.act = GateActivation(lmax, hidden_channels)
+        self.so3_linear_2 = SO3_Linear(hidden_channels, sphere_channels, lmax, generator)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        gates = self.scalar_mlp(x.narrow(1, 0, 1)).squeeze(1)
+        h = self.so3_linear_1(x)
+        h = self.act(gates, h)
+        return self.so3_linear_2(h)
+
+
+def _linear(i: int, o: int, bias: bool, generator) -> nn.Linear:
+    lin = nn.Linear(i, o, bias=bias)
+    bound = 1.0 / math.sqrt(i)
+    with torch.no_grad():
+        lin.weight.uniform_(-bound, bound, generator=generator)
+        if bias:
+            lin.bias.uniform_(-bound, bound, generator=generator)
+    return lin
+
+
+def _embedding(n: int, d: int, generator) -> nn.Embedding:
+    emb = nn.Embedding(n, d)
+    with torch.no_grad():
+        emb.weight.normal_(0.0, 1.0, generator=generator)
+    return emb
+
+
+class RadialFunction(nn.Module):
+    """Radial MLP: net = [Linear, LayerNorm, SiLU, Linear, LayerNorm, SiLU, Linear]; the
+    Sequential indices 0/1/3/4/6 are the ones transfer_weights reads (wrapper.py:33-55)."""
+
+    def __init__(self, channels: list[int], generator=None):
+        super().__init__()
+        layers: list[nn.Module] = []
+        for k in range(len(channels) - 1):
+            layers.append(_linear(channels[k], channels[k + 1], True, generator))
+            if k < len(channels) - 2:
+                layers.append(nn.LayerNorm(channels[k + 1]))
+                layers.append(nn.SiLU())
+        self.net = nn.Sequential(*layers)
+
+    def forward(self, x):
+        return self.net(x)
+
+
+class SO2_m_Convolution(nn.Module):
+    def __init__(self, in_ch: int, out_ch: int, generator=None):
+        super().__init__()
+        # rows [:out] are the real part R, rows [out:] the imaginary part I (wrapper.py:57-71)
+        self.fc = _linear(in_ch, 2 * out_ch, False, generator)
+
+
+class SO2_Convolution(nn.Module):
+    """Parameter container of FAIRChem's SO2_Convolution for mmax = 2."""
+
+    def __init__(self, C: int, lmax: int, in_mult: int, out_mult_m0: int, out_mult_m: list[int],
+                 rad_channels: list[int] | None, generator=None):
+        super().__init__()
+        self.rad_func = RadialFunction(rad_channels, generator) if rad_channels else None
+        m0_in = in_mult * (lmax + 1) * C
+        self.fc_m0 = _linear(m0_in, out_mult_m0 * C, True, generator)
+        self.so2_m_conv = nn.ModuleList()
+        for m in (1, 2):
+            n_l = lmax + 1 - m
+            self.so2_m_conv.append(SO2_m_Convolution(in_mult * n_l * C, out_mult_m[m - 1] * C, generator))
+
+
+class Edgewise(nn.Module):
+    def __init__(self, C: int, B: int, lmax: int, generator=None):
+        super().__init__()
+        rad = [B + 2 * C, C, C, 6 * lmax * C]
+        # conv1: inputs are (sender, receiver) pairs -> in_mult 2; m0 output carries the
+        # (lmax+1)C values plus lmax*C gate scalars; m>0 outputs n_l * C per part.
+        self.so2_conv_1 = SO2_Convolution(C, lmax, 2, 2 * lmax + 1, [lmax, lmax - 1], rad, generator)
+        self.so2_conv_2 = SO2_Convolution(C, lmax, 1, lmax + 1, [lmax, lmax - 1], None, generator)
+
+
+class eSCNMD_Block(nn.Module):
+    def __init__(self, C: int, H: int, B: int, lmax: int, generator=None):
+        super().__init__()
+        self.norm_1 = EquivariantRMSNormArraySphericalHarmonicsV2(lmax, C)
+        self.edge_wise = Edgewise(C, B, lmax, generator)
+        self.norm_2 = EquivariantRMSNormArraySphericalHarmonicsV2(lmax, C)
+        self.atom_wise = SpectralAtomwise(C, H, lmax, generator)
+
+
+class ChgSpinEmbedding(nn.Module):
+    """Learned table indexed by the integer charge (offset 100) or spin multiplicity."""
+
+    def __init__(self, C: int, offset: int, size: int, generator=None):
+        super().__init__()
+        self.offset = offset
+        self.table = _embedding(size, C, generator)
+
+    def forward(self, v: torch.Tensor) -> torch.Tensor:
+        return self.table(v.long() + self.offset)
+
+
+class EdgeDegreeEmbedding(nn.Module):
+    def __init__(self, C: int, B: int, lmax: int, generator=None):
+        super().__init__()
+        self.rad_func = RadialFunction([B + 2 * C, C, C, (lmax + 1) * C], generator)
+        self.rescale_factor = 5.0
+
+
+class eSCNMDBackbone(nn.Module):
+    """UMA-s-shaped eSCN-MD backbone with seeded random weights (parameters only; the
+    forward pass is the ZeroAllocBackbone's)."""
+
+    def __init__(self, num_layers: int = 4, sphere_channels: int = 128, hidden_channels: int = 128,
+                 lmax: int = 2, mmax: int = 2, num_distance_basis: int = 64, cutoff: float = 6.0,
+                 max_neighbors: int = 30, max_num_elements: int = 100, seed: int = 0):
+        super().__init__()
+        if mmax != 2:
+            raise ValueError("only mmax = 2 is modelled")
+        g = torch.Generator().manual_seed(seed)
+        C = sphere_channels
+        self.lmax, self.mmax = lmax, mmax
+        self.num_layers = num_layers
+        self.sphere_channels = C
+        self.edge_channels = C
+        self.hidden_channels = hidden_channels
+        self.num_distance_basis = num_distance_basis
+        self.cutoff = cutoff
+        self.max_neighbors = max_neighbors
+        self.sphere_embedding = _embedding(max_num_elements, C, g)
+        self.source_embedding = _embedding(max_num_elements, C, g)
+        self.target_embedding = _embedding(max_num_elements, C, g)
+        self.edge_degree_embedding = EdgeDegreeEmbedding(C, num_distance_basis, lmax, g)
+        self.blocks = nn.ModuleList(
+            [eSCNMD_Block(C, hidden_channels, num_distance_basis, lmax, g) for _ in range(num_layers)])
+        self.norm = EquivariantRMSNormArraySphericalHarmonicsV2(lmax, C)
+        self.charge_embedding = ChgSpinEmbedding(C, 100, 201, g)
+        self.spin_embedding = ChgSpinEmbedding(C, 0, 101, g)
+        self.dataset_embedding = None
+        self.use_dataset_embedding = False
+        self.mix_csd = _linear(2 * C, C, True, g)
+        self.charge_channel_start = self.charge_channel_end = 0
+        self.spin_channel_start = self.spin_channel_end = 0
+        self.regress_config = SimpleNamespace(forces=True, stress=True, direct_forces=False)

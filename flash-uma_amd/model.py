@@ -1,0 +1,227 @@
+"""eSCN-MD inference model on the gfx950 kernels (mirrors the reference model.py).
+
+Public names and signatures follow the reference: reorder_graph_morton, build_csr_cached,
+clear_csr_cache (model.py:17-74), Packed_eSCN_Layer (model.py:81-157) and
+eSCN_Inference_Model (model.py:160-221).  Every per-edge and per-CSR operation runs in
+libflashuma_hip.so; the node-level FAIRChem modules attached by transfer_weights (norm_1,
+norm_2, atom_wise, final_norm) run as the torch modules they are.
+
+Differences in mechanism (not in results):
+  - the graph topology (Morton order, receiver-sorted edge order, receiver and sender CSRs)
+    is built once per edge_index on the GPU and cached (ops/topology.py);
+  - dense layers use the fp32 MFMA GEMM with pre-transposed frozen weights for the input
+    gradient (ops/linear.py).
+"""
+from __future__ import annotations
+
+from collections import OrderedDict
+
+import torch
+import torch.nn as nn
+
+from ops.gather import gather_wigner_split
+from ops.gating import fused_gating_split
+from ops.geom import precompute_geometry
+from ops.linear import linear
+from ops.ln_silu import layer_norm_silu
+from ops.scatter import init_node_scatter, rotate_scatter_split
+from ops.topology import (clear_topology_cache, get_topology, morton_permutation, receiver_csr, take)
+
+# ==============================================================================
+# 1. GRAPH PREPROCESSING (MORTON & CSR CACHING)
+# ==============================================================================
+
+_CSR_CACHE_CAPACITY = 8
+_csr_cache: "OrderedDict[tuple, tuple]" = OrderedDict()
+
+
+def build_csr_cached(idx_j: torch.Tensor, N: int):
+    """Receiver CSR (row_ptr int32 (N+1), col_idx int32 (E)) with an LRU cache (model.py:28-44).
+
+    The entry keeps idx_j alive, so the (data_ptr, _version) key cannot be matched by a
+    different tensor that reuses a freed address."""
+    key = (idx_j.data_ptr(), idx_j._version, idx_j.numel(), N,
+           idx_j.device.index if idx_j.device.type == "cuda" else -1)
+    hit = _csr_cache.get(key)
+    if hit is not None:
+        _csr_cache.move_to_end(key)
+        return hit[0], hit[1]
+    row_ptr, col_idx = receiver_csr(idx_j, N)
+    _csr_cache[key] = (row_ptr, col_idx, idx_j)
+    if len(_csr_cache) > _CSR_CACHE_CAPACITY:
+        _csr_cache.popitem(last=False)
+    return row_ptr, col_idx
+
+
+def clear_csr_cache():
+    _csr_cache.clear()
+    clear_topology_cache()
+
+
+def reorder_graph_morton(pos, Z, batch, idx_i, idx_j):
+    """Morton Z-order of the atoms and remapped edge endpoints (model.py:60-74).
+    Returns (pos[perm], Z[perm], batch[perm], inv[idx_i], inv[idx_j], perm, inv)."""
+    perm, inv = morton_permutation(pos, batch)
+    return (pos[perm], Z[perm], batch[perm], take(inv, idx_i.contiguous()), take(inv, idx_j.contiguous()),
+            perm, inv)
+
+
+# ==============================================================================
+# 2. MODEL DEFINITIONS
+# ==============================================================================
+
+
+def _frozen(t: torch.Tensor) -> torch.Tensor:
+    return t.detach().clone().contiguous()
+
+
+class Packed_eSCN_Layer(nn.Module):
+    """One eSCN-MD message-passing block (model.py:81-157)."""
+
+    def __init__(self, C: int, B: int):
+        super().__init__()
+        self.C = C
+        z = torch.zeros
+        self.W_rad1_1 = nn.Parameter(z(C, B + 2 * C)); self.b_rad1_1 = nn.Parameter(z(C))
+        self.gamma_rad1_1 = nn.Parameter(torch.ones(C)); self.beta_rad1_1 = nn.Parameter(z(C))
+        self.W_rad1_2 = nn.Parameter(z(C, C)); self.b_rad1_2 = nn.Parameter(z(C))
+        self.gamma_rad1_2 = nn.Parameter(torch.ones(C)); self.beta_rad1_2 = nn.Parameter(z(C))
+        self.W_rad1_3 = nn.Parameter(z(12 * C, C)); self.b_rad1_3 = nn.Parameter(z(12 * C))
+
+        self.W1_m0 = nn.Parameter(z(5 * C, 6 * C)); self.b1_m0 = nn.Parameter(z(5 * C))
+        self.W1_m1_R = nn.Parameter(z(2 * C, 4 * C)); self.W1_m1_I = nn.Parameter(z(2 * C, 4 * C))
+        self.W1_m2_R = nn.Parameter(z(1 * C, 2 * C)); self.W1_m2_I = nn.Parameter(z(1 * C, 2 * C))
+
+        self.W2_m0 = nn.Parameter(z(3 * C, 3 * C)); self.b2_m0 = nn.Parameter(z(3 * C))
+        self.W2_m1_R = nn.Parameter(z(2 * C, 2 * C)); self.W2_m1_I = nn.Parameter(z(2 * C, 2 * C))
+        self.W2_m2_R = nn.Parameter(z(1 * C, 1 * C)); self.W2_m2_I = nn.Parameter(z(1 * C, 1 * C))
+
+        self.norm_1 = None; self.norm_2 = None; self.atom_wise = None
+        self.prepared = False
+
+    @staticmethod
+    def _pack(R: torch.Tensor, I: torch.Tensor) -> torch.Tensor:
+        # complex map (R + iI) on [real; imag] stacked features as the real block matrix
+        # [[R, -I], [I, R]] (model.py:111-138)
+        return torch.cat([torch.cat([R, -I], 1), torch.cat([I, R], 1)], 0)
+
+    def _register(self, name: str, W: torch.Tensor, dtype) -> None:
+        W = W.to(dtype).contiguous()
+        self.register_buffer(name, W)
+        self.register_buffer(name + "_t", W.t().contiguous())
+
+    def prepare_for_inference(self, dtype=torch.float32):
+        if self.norm_1 is not None:
+            for mod in (self.norm_1, self.norm_2, self.atom_wise):
+                for p in mod.parameters():
+                    p.requires_grad = False
+        for name in ("W_rad1_1", "W_rad1_2", "W_rad1_3"):
+            W = getattr(self, name).data
+            self.register_buffer(name + "_t", W.to(dtype).t().contiguous())
+        self._register("W_conv1_m0", self.W1_m0.data, dtype)
+        self.register_buffer("b_conv1_m0", _frozen(self.b1_m0.data).to(dtype))
+        self._register("W_conv1_m1", self._pack(self.W1_m1_R.data, self.W1_m1_I.data), dtype)
+        self._register("W_conv1_m2", self._pack(self.W1_m2_R.data, self.W1_m2_I.data), dtype)
+        self._register("W_conv2_m0", self.W2_m0.data, dtype)
+        self.register_buffer("b_conv2_m0", _frozen(self.b2_m0.data).to(dtype))
+        self._register("W_conv2_m1", self._pack(self.W2_m1_R.data, self.W2_m1_I.data), dtype)
+        self._register("W_conv2_m2", self._pack(self.W2_m2_R.data, self.W2_m2_I.data), dtype)
+        del self.W1_m0, self.b1_m0, self.W1_m1_R, self.W1_m1_I, self.W1_m2_R, self.W1_m2_I
+        del self.W2_m0, self.b2_m0, self.W2_m1_R, self.W2_m1_I, self.W2_m2_R, self.W2_m2_I
+        self.prepared = True
+
+    def radial(self, x_edge_raw):
+        h1 = layer_norm_silu(linear(x_edge_raw, self.W_rad1_1, self.b_rad1_1, self.W_rad1_1_t),
+                             self.gamma_rad1_1, self.beta_rad1_1)
+        h2 = layer_norm_silu(linear(h1, self.W_rad1_2, self.b_rad1_2, self.W_rad1_2_t),
+                             self.gamma_rad1_2, self.beta_rad1_2)
+        return linear(h2, self.W_rad1_3, self.b_rad1_3, self.W_rad1_3_t)
+
+    def forward(self, x_in, x_edge_raw, wigner, env, idx_i, idx_j, row_ptr, col_idx, csd_emb, batch,
+                topology=None):
+        x_norm = self.norm_1(x_in)
+        rad_out = self.radial(x_edge_raw)
+        X_m0, X_m1, X_m2 = gather_wigner_split(x_norm, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology)
+        Y_m0 = linear(X_m0, self.W_conv1_m0, self.b_conv1_m0, self.W_conv1_m0_t)
+        Y_m1 = linear(X_m1, self.W_conv1_m1, None, self.W_conv1_m1_t)
+        Y_m2 = linear(X_m2, self.W_conv1_m2, None, self.W_conv1_m2_t)
+        Z_m0, Z_m1, Z_m2 = fused_gating_split(Y_m0, Y_m1, Y_m2, self.C)
+        Zo_m0 = linear(Z_m0, self.W_conv2_m0, self.b_conv2_m0, self.W_conv2_m0_t)
+        Zo_m1 = linear(Z_m1, self.W_conv2_m1, None, self.W_conv2_m1_t)
+        Zo_m2 = linear(Z_m2, self.W_conv2_m2, None, self.W_conv2_m2_t)
+        x_mid = rotate_scatter_split(Zo_m0, Zo_m1, Zo_m2, wigner, env, x_in, idx_j, row_ptr, col_idx,
+                                     x_in.shape[0])
+        return self.atom_wise(self.norm_2(x_mid)) + x_mid
+
+
+class eSCN_Inference_Model(nn.Module):
+    """eSCN-MD backbone forward (model.py:160-221)."""
+
+    def __init__(self, num_layers=4, sphere_channels=128, edge_channels=128, num_distance_basis=32, cutoff=5.0,
+                 coeff_g=-0.5):
+        super().__init__()
+        self.C, self.cutoff, self.coeff_g, self.B = sphere_channels, cutoff, coeff_g, num_distance_basis
+        C, B = self.C, self.B
+        self.W_sphere = nn.Parameter(torch.zeros(100, C))
+        self.W_src = nn.Parameter(torch.zeros(100, C)); self.W_tgt = nn.Parameter(torch.zeros(100, C))
+        self.offset_g = nn.Parameter(torch.linspace(0, cutoff, B))
+
+        self.W_rad1_1 = nn.Parameter(torch.zeros(C, B + 2 * C)); self.b_rad1_1 = nn.Parameter(torch.zeros(C))
+        self.gamma_rad1_1 = nn.Parameter(torch.ones(C)); self.beta_rad1_1 = nn.Parameter(torch.zeros(C))
+        self.W_rad1_2 = nn.Parameter(torch.zeros(C, C)); self.b_rad1_2 = nn.Parameter(torch.zeros(C))
+        self.gamma_rad1_2 = nn.Parameter(torch.ones(C)); self.beta_rad1_2 = nn.Parameter(torch.zeros(C))
+        self.W_rad1_3 = nn.Parameter(torch.zeros(3 * C, C)); self.b_rad1_3 = nn.Parameter(torch.zeros(3 * C))
+
+        self.layers = nn.ModuleList([Packed_eSCN_Layer(C, B) for _ in range(num_layers)])
+        self.final_norm = None
+        self.charge_start = 0; self.charge_end = 0; self.spin_start = 0; self.spin_end = 0
+
+    def prepare_for_inference(self, dtype=torch.float32):
+        self.eval()
+        for p in self.parameters():
+            p.requires_grad = False
+        if self.final_norm is not None:
+            for p in self.final_norm.parameters():
+                p.requires_grad = False
+        for name in ("W_rad1_1", "W_rad1_2", "W_rad1_3"):
+            self.register_buffer(name + "_t", getattr(self, name).data.to(dtype).t().contiguous())
+        for layer in self.layers:
+            layer.prepare_for_inference(dtype)
+        self.to(dtype)
+
+    def radial(self, x_edge_raw):
+        h1 = layer_norm_silu(linear(x_edge_raw, self.W_rad1_1, self.b_rad1_1, self.W_rad1_1_t),
+                             self.gamma_rad1_1, self.beta_rad1_1)
+        h2 = layer_norm_silu(linear(h1, self.W_rad1_2, self.b_rad1_2, self.W_rad1_2_t),
+                             self.gamma_rad1_2, self.beta_rad1_2)
+        return linear(h2, self.W_rad1_3, self.b_rad1_3, self.W_rad1_3_t)
+
+    def forward(self, pos, Z, batch, edge_index, shifts, csd_emb, charge=None, spin=None, natoms=None):
+        # 1. Topology (Morton order + receiver-sorted edges + both CSRs), cached per graph
+        topo = get_topology(pos, batch, edge_index)
+        pos_s = pos[topo.perm]
+        Z_s = Z[topo.perm]
+        batch_s = batch[topo.perm]
+        shifts_s = shifts[topo.edge_perm]
+        idx_i_s, idx_j_s = topo.idx_i, topo.idx_j
+        row_ptr, col_idx = topo.recv_ptr, topo.recv_idx
+        N = pos_s.shape[0]
+
+        # 2. Per-edge geometry
+        x_edge_raw, wigner, env = precompute_geometry(pos_s, Z_s, idx_i_s, idx_j_s, shifts_s, self.W_src,
+                                                      self.W_tgt, self.offset_g, self.coeff_g, self.cutoff,
+                                                      topo)
+        # 3. Edge-degree embedding
+        rad_out_p1 = self.radial(x_edge_raw)
+        x_node_s = init_node_scatter(rad_out_p1, wigner, env, Z_s, batch_s, self.W_sphere, csd_emb, idx_j_s,
+                                     row_ptr, col_idx, N)
+        # 4. Message-passing blocks
+        for layer in self.layers:
+            x_node_s = layer(x_node_s, x_edge_raw, wigner, env, idx_i_s, idx_j_s, row_ptr, col_idx, csd_emb,
+                             batch_s, topo)
+            if self.charge_end > self.charge_start or self.spin_end > self.spin_start:
+                raise NotImplementedError(
+                    "charge/spin channel balancing (FAIRChem balance_channels_batched) is not available")
+        x_node_s = self.final_norm(x_node_s)
+        # 5. Back to the input atom order
+        return x_node_s[topo.inv_perm]

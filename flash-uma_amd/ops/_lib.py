@@ -1,0 +1,108 @@
+"""ctypes binding of libflashuma_hip.so (the C-ABI declared in include/flashuma.h).
+
+The op modules call `lib.<entry point>(...)` through `call()`, passing raw device
+pointers (`tensor.data_ptr()`), sizes and the current HIP stream.  There is no fallback:
+if the library is missing, or the tensors are not on a ROCm device, the call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+_PKG_DIR = Path(__file__).resolve().parent.parent
+LIB_PATH = Path(os.environ.get("FLASHUMA_LIB", _PKG_DIR / "libflashuma_hip.so"))
+
+P = ctypes.c_void_p
+I64 = ctypes.c_int64
+I32 = ctypes.c_int32
+F32 = ctypes.c_float
+SZ_P = ctypes.POINTER(ctypes.c_size_t)
+
+# Argument types of every exported entry point, in header order.
+SIGNATURES: dict[str, list] = {
+    "fu_version": [],
+    "fu_last_error": [],
+    "fu_geom_fwd": [P, P, P, P, P, P, P, P, P, I64, P, P, I64, I64, I32, I32, F32, F32, P],
+    "fu_geom_bwd": [P, P, P, P, P, P, I64, P, P, P, I64, I64, I32, F32, F32, P],
+    "fu_edge_vec_reduce": [P, P, P, P, P, P, I64, I64, P],
+    "fu_gather_fwd": [P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, P],
+    "fu_gather_bwd": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, P],
+    "fu_gating_fwd": [P, P, P, P, P, P, I64, I32, P],
+    "fu_gating_bwd": [P, P, P, P, P, P, P, P, P, I64, I32, P],
+    "fu_scatter_fwd": [P, P, P, P, P, P, P, P, P, I64, I64, I32, P],
+    "fu_scatter_bwd": [P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I32, P],
+    "fu_init_scatter_fwd": [P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, I32, P],
+    "fu_init_scatter_bwd": [P, P, P, P, P, P, P, P, I64, I64, I32, P],
+    "fu_ln_silu_fwd": [P, P, P, P, P, P, I64, I32, F32, P],
+    "fu_ln_silu_bwd": [P, P, P, P, P, P, P, I64, I32, P],
+    "fu_linear": [P, I64, P, I64, P, P, I64, I64, I32, I32, P],
+    "fu_morton_keys": [P, P, P, I64, P],
+    "fu_sort_pairs_i64": [P, P, P, P, I64, I32, I32, P, SZ_P, P],
+    "fu_invert_perm": [P, P, I64, P],
+    "fu_take_i64": [P, I64, P, P, I64, P],
+    "fu_csr_row_ptr": [P, I64, P, I64, P],
+    "fu_narrow_i64_i32": [P, P, I64, P],
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+class FlashUMAError(RuntimeError):
+    """A C-ABI entry point returned a negative status."""
+
+
+def load() -> ctypes.CDLL:
+    """Load the shared library once and attach the argument types of every entry point."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise FlashUMAError(
+            f"{LIB_PATH} is missing: build it first (python flash-uma_amd/build_lib.py or "
+            "__graft_entry__.build()); there is no non-HIP fallback")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_char_p if name == "fu_last_error" else ctypes.c_int
+    _lib = lib
+    return lib
+
+
+def exported_symbols() -> list[str]:
+    return list(SIGNATURES)
+
+
+def stream_ptr(device: torch.device | None = None) -> int:
+    """hipStream_t of torch's current stream on `device`."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def call(name: str, *args) -> None:
+    """Invoke entry point `name`; raise FlashUMAError with the library message on failure."""
+    lib = load()
+    status = getattr(lib, name)(*args)
+    if status != 0:
+        msg = lib.fu_last_error().decode(errors="replace")
+        raise FlashUMAError(f"{name} failed with status {status}: {msg}")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    """Device address of a tensor (None for an absent optional operand)."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise FlashUMAError("FlashUMA kernels need tensors on a ROCm GPU device; got a CPU tensor")
+    return t.data_ptr()
+
+
+def require(t: torch.Tensor, dtype: torch.dtype, name: str) -> torch.Tensor:
+    """Return `t` as a contiguous tensor of `dtype` on its GPU (copying only if needed)."""
+    if not t.is_cuda:
+        raise FlashUMAError(f"{name}: FlashUMA kernels need a ROCm GPU tensor, got device {t.device}")
+    if t.dtype != dtype:
+        t = t.to(dtype)
+    return t.contiguous()

@@ -1,0 +1,151 @@
+"""ZeroAllocBackbone: drop-in replacement for FAIRChem's eSCNMDBackbone (wrapper.py of the
+reference) running the gfx950 HIP hot path.
+
+Usage, as with the reference (readme.md:64-69):
+    predict_unit.model.module.backbone = ZeroAllocBackbone(old_backbone, dtype=torch.float32)
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from model import eSCN_Inference_Model
+
+
+@torch.no_grad()
+def transfer_weights(off_model, cust_model):
+    """Copy parameters from an eSCNMDBackbone-shaped object (wrapper.py:22-85)."""
+    C = cust_model.C
+    cust_model.W_sphere.copy_(off_model.sphere_embedding.weight)
+    cust_model.W_src.copy_(off_model.source_embedding.weight)
+    cust_model.W_tgt.copy_(off_model.target_embedding.weight)
+
+    def copy_radial(dst, net):
+        dst.W_rad1_1.copy_(net[0].weight); dst.b_rad1_1.copy_(net[0].bias)
+        dst.gamma_rad1_1.copy_(net[1].weight); dst.beta_rad1_1.copy_(net[1].bias)
+        dst.W_rad1_2.copy_(net[3].weight); dst.b_rad1_2.copy_(net[3].bias)
+        dst.gamma_rad1_2.copy_(net[4].weight); dst.beta_rad1_2.copy_(net[4].bias)
+        dst.W_rad1_3.copy_(net[6].weight); dst.b_rad1_3.copy_(net[6].bias)
+
+    copy_radial(cust_model, off_model.edge_degree_embedding.rad_func.net)
+    for off_blk, cust_blk in zip(off_model.blocks, cust_model.layers):
+        so2_1 = off_blk.edge_wise.so2_conv_1
+        so2_2 = off_blk.edge_wise.so2_conv_2
+        copy_radial(cust_blk, so2_1.rad_func.net)
+        cust_blk.W1_m0.copy_(so2_1.fc_m0.weight); cust_blk.b1_m0.copy_(so2_1.fc_m0.bias)
+        w = so2_1.so2_m_conv[0].fc.weight
+        cust_blk.W1_m1_R.copy_(w[:2 * C, :]); cust_blk.W1_m1_I.copy_(w[2 * C:, :])
+        w = so2_1.so2_m_conv[1].fc.weight
+        cust_blk.W1_m2_R.copy_(w[:1 * C, :]); cust_blk.W1_m2_I.copy_(w[1 * C:, :])
+        cust_blk.W2_m0.copy_(so2_2.fc_m0.weight); cust_blk.b2_m0.copy_(so2_2.fc_m0.bias)
+        w = so2_2.so2_m_conv[0].fc.weight
+        cust_blk.W2_m1_R.copy_(w[:2 * C, :]); cust_blk.W2_m1_I.copy_(w[2 * C:, :])
+        w = so2_2.so2_m_conv[1].fc.weight
+        cust_blk.W2_m2_R.copy_(w[:1 * C, :]); cust_blk.W2_m2_I.copy_(w[1 * C:, :])
+        # node-level modules are attached by reference
+        cust_blk.norm_1 = off_blk.norm_1
+        cust_blk.norm_2 = off_blk.norm_2
+        cust_blk.atom_wise = off_blk.atom_wise
+    cust_model.final_norm = off_model.norm
+    cust_model.charge_start = off_model.charge_channel_start
+    cust_model.charge_end = off_model.charge_channel_end
+    cust_model.spin_start = off_model.spin_channel_start
+    cust_model.spin_end = off_model.spin_channel_end
+
+
+class ZeroAllocBackbone(nn.Module):
+    """Drop-in replacement for the FAIRChem eSCNMDBackbone (wrapper.py:88-212).
+
+    Inference only: parameters are repacked and frozen; autograd through the HIP kernels
+    gives dE/dpos and dE/dcell for conservative forces and stress.  Only lmax = mmax = 2 is
+    supported, as in the reference."""
+
+    def __init__(self, off_bb, dtype=torch.float32):
+        super().__init__()
+        lmax = getattr(off_bb, "lmax", None)
+        if lmax is not None and lmax != 2:
+            raise ValueError(f"ZeroAllocBackbone only supports lmax=2 (the kernels are built for the "
+                             f"9-coefficient layout); got lmax={lmax}.")
+        mmax = getattr(off_bb, "mmax", None)
+        if mmax is not None and mmax != 2:
+            raise ValueError(f"ZeroAllocBackbone only supports mmax=2; got mmax={mmax}.")
+        if dtype != torch.float32:
+            raise ValueError("ZeroAllocBackbone computes in float32 only")
+
+        device = next(off_bb.parameters()).device
+        B = off_bb.num_distance_basis
+        cutoff = off_bb.cutoff
+        offset_g = torch.linspace(0.0, cutoff, B)
+        coeff_g = -0.5 / (2.0 * (offset_g[1] - offset_g[0])) ** 2
+
+        self.ce = eSCN_Inference_Model(
+            num_layers=off_bb.num_layers,
+            sphere_channels=off_bb.sphere_channels,
+            edge_channels=off_bb.edge_channels,
+            num_distance_basis=B,
+            cutoff=cutoff,
+            coeff_g=coeff_g.item(),
+        ).to(device)
+        transfer_weights(off_bb, self.ce)
+        self.ce.prepare_for_inference(dtype=dtype)
+
+        self.charge_embedding = off_bb.charge_embedding
+        self.spin_embedding = off_bb.spin_embedding
+        self.dataset_embedding = getattr(off_bb, "dataset_embedding", None)
+        self.mix_csd = off_bb.mix_csd
+        self.use_dataset_embedding = getattr(off_bb, "use_dataset_embedding", False)
+        # inference only: the system-embedding modules are frozen like the rest
+        for mod in (self.charge_embedding, self.spin_embedding, self.dataset_embedding, self.mix_csd):
+            if mod is not None:
+                for p in mod.parameters():
+                    p.requires_grad = False
+        self.regress_config = off_bb.regress_config
+
+    def validate_atoms_data(self, atoms, task_name):
+        """Default charge and spin so ASE does not fail when they are missing."""
+        if "charge" not in atoms.info:
+            atoms.info["charge"] = 0
+        if "spin" not in atoms.info:
+            atoms.info["spin"] = 1 if task_name == "omol" else 0
+
+    def on_predict_check(self, data):
+        """The official MOLE consistency check is bypassed."""
+        pass
+
+    def prepare_for_inference(self, data, settings):
+        """No per-input graph changes are needed."""
+        return self
+
+    def csd_embedding(self, charge, spin, dataset=None):
+        chg_emb = self.charge_embedding(charge)
+        spin_emb = self.spin_embedding(spin)
+        if self.use_dataset_embedding and dataset is not None:
+            dataset_emb = self.dataset_embedding(dataset)
+            return F.silu(self.mix_csd(torch.cat((chg_emb, spin_emb, dataset_emb), dim=1)))
+        return F.silu(self.mix_csd(torch.cat((chg_emb, spin_emb), dim=1)))
+
+    def forward(self, data):
+        data.atomic_numbers = data.atomic_numbers.long()
+        data.atomic_numbers_full = data.atomic_numbers
+        data.batch_full = data.batch
+
+        if not self.regress_config.direct_forces:
+            if getattr(self.regress_config, "forces", False) or getattr(self.regress_config, "stress", False):
+                data.pos.requires_grad_(True)
+            if getattr(self.regress_config, "stress", False):
+                if data.cell is not None and data.cell.is_floating_point():
+                    data.cell.requires_grad_(True)
+
+        csd_mixed_emb = self.csd_embedding(charge=data.charge, spin=data.spin,
+                                           dataset=getattr(data, "dataset", None))
+        if len(data.natoms) == 1:
+            shifts = data.cell_offsets.to(data.cell.dtype) @ data.cell.squeeze(0)
+        else:
+            cell_per_edge = data.cell.repeat_interleave(data.nedges, dim=0)
+            shifts = torch.einsum("ij,ijk->ik", data.cell_offsets.to(cell_per_edge.dtype), cell_per_edge)
+
+        x_node = self.ce(pos=data.pos, Z=data.atomic_numbers, batch=data.batch, edge_index=data.edge_index,
+                         shifts=shifts, csd_emb=csd_mixed_emb, charge=data.charge, spin=data.spin,
+                         natoms=data.natoms)
+        return {"node_embedding": x_node, "batch": data.batch}

@@ -1,0 +1,202 @@
+/*
+ * flashuma.h — C-ABI of libflashuma_hip.so, the gfx950 (MI355X) kernels behind the
+ * FlashUMA ZeroAllocBackbone hot path.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensors are device pointers to dense, row-major (C-contiguous) arrays.
+ *     Features are fp32, graph indices are int64 (edge_index, Z, batch) and CSR arrays
+ *     are int32, exactly as in the reference (model.py:20-26 and the ops/ modules).
+ *   - Sizes are int64_t (E, N, M) or int32_t (channel widths).  Edge-feature offsets are
+ *     computed in 64 bits, so E * row_width may exceed 2^31.
+ *   - `stream` is a hipStream_t passed as void*; work is only enqueued, never awaited.
+ *   - No entry point allocates memory.  Scratch space, where needed, is an argument.
+ *   - Return value: FU_OK (0) or a negative FU_ERR_* code; fu_last_error() returns the
+ *     message of the last failure on the calling host thread.
+ *
+ * Edge layout contract (ops/constants.py:7-35): wigner is (E, 34) = row-major L=1 3x3
+ * block (0..8) then L=2 5x5 block (9..33).  Rotated-frame m-blocks are
+ *   X_m0 (E, 6C)  X_m1 (E, 8C)  X_m2 (E, 4C)     (gather output / conv1 input)
+ *   Y_m0 (E, 5C)  Y_m1 (E, 4C)  Y_m2 (E, 2C)     (conv1 output / gate input)
+ *   Z_m0 (E, 3C)  Z_m1 (E, 4C)  Z_m2 (E, 2C)     (gate output, conv2 in/out)
+ * with the slot orders of ops/gather.py:132-154 and ops/gating.py:63-103.
+ */
+#ifndef FLASHUMA_H_
+#define FLASHUMA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FU_OK 0
+#define FU_ERR_SHAPE (-1)       /* a size is negative, zero where it may not be, or unsupported */
+#define FU_ERR_UNSUPPORTED (-2) /* a configuration the kernels do not implement */
+#define FU_ERR_ALIGN (-3)       /* a pointer lacks the alignment the vector loads need */
+#define FU_ERR_LAUNCH (-4)      /* the HIP runtime rejected a launch */
+#define FU_ERR_NULL (-5)        /* a required pointer is NULL */
+#define FU_ERR_WORKSPACE (-6)   /* the workspace is too small */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int fu_version(void);
+
+/* Message of the last error returned on the calling host thread ("" if none). */
+const char* fu_last_error(void);
+
+/* ------------------------------------------------------------------------------------
+ * Geometry (replaces PrecomputeGeometry, ops/geom.py:496-589)
+ * ------------------------------------------------------------------------------------ */
+
+/* Per-edge geometry, ops/geom.py:36-214 (_geom_fwd_kernel).
+ * d = pos[idx_i] - pos[idx_j] + shifts[e]; env = polynomial envelope; the B Gaussians
+ * exp(coeff_g (|d| - offset_g[b])^2) go to x_edge_raw[e, 0:B]; when W_src and W_tgt are
+ * non-NULL, W_src[Z[idx_i]] and W_tgt[Z[idx_j]] (each C wide) go to x_edge_raw[e, B:B+2C].
+ * ld_xe is the row stride of x_edge_raw in floats (>= B, or >= B+2C with embeddings).
+ * wigner receives the 34 quaternion-Wigner scalars of the edge frame. */
+int fu_geom_fwd(const float* pos, const int64_t* Z, const int64_t* idx_i, const int64_t* idx_j,
+                const float* shifts, const float* W_src, const float* W_tgt, const float* offset_g,
+                float* x_edge_raw, int64_t ld_xe, float* wigner, float* env, int64_t E, int64_t N,
+                int32_t B, int32_t C, float cutoff, float coeff_g, void* stream);
+
+/* Per-edge vector-Jacobian product of fu_geom_fwd w.r.t. the edge vector d,
+ * ops/geom.py:220-493 (_geom_bwd_kernel) without its atomics: writes g_d (E, 3), which is
+ * also dE/dshifts (ops/geom.py:490-493).  g_x_edge_raw (row stride ld_gxe; only columns
+ * 0..B-1 are read), g_wigner and g_env may each be NULL (treated as zero). */
+int fu_geom_bwd(const float* pos, const int64_t* idx_i, const int64_t* idx_j, const float* shifts,
+                const float* offset_g, const float* g_x_edge_raw, int64_t ld_gxe,
+                const float* g_wigner, const float* g_env, float* g_d, int64_t E, int64_t N,
+                int32_t B, float cutoff, float coeff_g, void* stream);
+
+/* Deterministic replacement for the g_pos atomics of ops/geom.py:483-488:
+ * g_pos[n] = sum_{e in send(n)} g_d[e] - sum_{e in recv(n)} g_d[e], summed in CSR order
+ * in fp64.  send/recv are CSRs over senders (idx_i) and receivers (idx_j). */
+int fu_edge_vec_reduce(const float* g_d, const int32_t* recv_ptr, const int32_t* recv_idx,
+                       const int32_t* send_ptr, const int32_t* send_idx, float* g_pos, int64_t N,
+                       int64_t E, void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * Gather-rotate (replaces GatherWignerSplit, ops/gather.py:408-514)
+ * ------------------------------------------------------------------------------------ */
+
+/* ops/gather.py:34-154 (_gather_split_fwd_kernel): rotate sender/receiver rows of
+ * x (N, 9, C) (+ csd_emb[batch] on l=0) into the edge frame, scale by rad (E, 12C) and
+ * write the X_m0/X_m1/X_m2 blocks. */
+int fu_gather_fwd(const float* x, const int64_t* idx_i, const int64_t* idx_j, const float* wigner,
+                  const float* rad, const float* csd_emb, const int64_t* batch, float* X_m0,
+                  float* X_m1, float* X_m2, int64_t E, int64_t N, int64_t S, int32_t C,
+                  void* stream);
+
+/* ops/gather.py:160-405 (both backward kernels) without atomics.  One workgroup per node
+ * sums the node's receiver segment (recv CSR) and sender segment (send CSR) in CSR order,
+ * writing g_x (N, 9, C), g_rad (E, 12C) and g_wigner (E, 34).  g_wig_ws is an (E, 34)
+ * scratch array for the sender-side halves of g_wigner. */
+int fu_gather_bwd(const float* g_X_m0, const float* g_X_m1, const float* g_X_m2, const float* x,
+                  const int64_t* idx_i, const int64_t* idx_j, const float* wigner, const float* rad,
+                  const float* csd_emb, const int64_t* batch, const int32_t* recv_ptr,
+                  const int32_t* recv_idx, const int32_t* send_ptr, const int32_t* send_idx,
+                  float* g_x, float* g_wigner, float* g_rad, float* g_wig_ws, int64_t E,
+                  int64_t N, int64_t S, int32_t C, void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * Gate activation (replaces FusedGatingSplit, ops/gating.py:188-234)
+ * ------------------------------------------------------------------------------------ */
+
+/* ops/gating.py:32-103 (_gating_split_fwd_kernel). */
+int fu_gating_fwd(const float* Y_m0, const float* Y_m1, const float* Y_m2, float* Z_m0,
+                  float* Z_m1, float* Z_m2, int64_t E, int32_t C, void* stream);
+
+/* ops/gating.py:109-185 (_gating_split_bwd_kernel). */
+int fu_gating_bwd(const float* g_Z_m0, const float* g_Z_m1, const float* g_Z_m2, const float* Y_m0,
+                  const float* Y_m1, const float* Y_m2, float* g_Y_m0, float* g_Y_m1,
+                  float* g_Y_m2, int64_t E, int32_t C, void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * Rotate-scatter (replaces RotateScatterSplit, ops/scatter.py:295-352)
+ * ------------------------------------------------------------------------------------ */
+
+/* ops/scatter.py:45-140 (_scatter_split_fwd_kernel): x_out[j] = x_res[j] +
+ * sum_{e in CSR(j)} env_e * D_e^T * Zout_e, accumulated in fp64 in CSR order. */
+int fu_scatter_fwd(const int32_t* row_ptr, const int32_t* col_idx, const float* Z_m0,
+                   const float* Z_m1, const float* Z_m2, const float* wigner, const float* env,
+                   const float* x_res, float* x_out, int64_t N, int64_t E, int32_t C,
+                   void* stream);
+
+/* ops/scatter.py:146-292 (both backward kernels, fused into one pass over the edges):
+ * g_Z = env * D * g_out[idx_j], g_wigner and g_env channel reductions. */
+int fu_scatter_bwd(const float* g_out, const int64_t* idx_j, const float* Z_m0, const float* Z_m1,
+                   const float* Z_m2, const float* wigner, const float* env, float* g_Z_m0,
+                   float* g_Z_m1, float* g_Z_m2, float* g_wigner, float* g_env, int64_t E,
+                   int64_t N, int32_t C, void* stream);
+
+/* ops/scatter.py:360-423 (_init_scatter_fwd_kernel): edge-degree embedding,
+ * x0[j] = [W_sphere[Z_j] + csd_emb[batch_j], 0...] + sum_e env/5 * (r0; r1 D1[1,:]; r2 D2[2,:]). */
+int fu_init_scatter_fwd(const int32_t* row_ptr, const int32_t* col_idx, const float* rad,
+                        const float* wigner, const float* env, const int64_t* Z,
+                        const int64_t* batch, const float* W_sphere, const float* csd_emb,
+                        float* x_out, int64_t N, int64_t E, int64_t num_z, int64_t S, int32_t C,
+                        void* stream);
+
+/* ops/scatter.py:426-481 (_init_scatter_bwd_kernel): g_rad (E, 3C), g_wigner (E, 34; the
+ * 26 entries the forward does not read are written as 0) and g_env (E). */
+int fu_init_scatter_bwd(const float* g_out, const int64_t* idx_j, const float* rad,
+                        const float* wigner, const float* env, float* g_rad, float* g_wigner,
+                        float* g_env, int64_t E, int64_t N, int32_t C, void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * LayerNorm + SiLU (replaces _LayerNormSiLUFn, ops/ln_silu.py:126-185)
+ * ------------------------------------------------------------------------------------ */
+
+/* ops/ln_silu.py:29-72: out = silu(gamma * (x - mean) * rstd + beta) over rows of D. */
+int fu_ln_silu_fwd(const float* x, const float* gamma, const float* beta, float* out, float* mean,
+                   float* rstd, int64_t M, int32_t D, float eps, void* stream);
+
+/* ops/ln_silu.py:77-123: g_x only (gamma/beta are frozen). */
+int fu_ln_silu_bwd(const float* x, const float* gamma, const float* beta, const float* mean,
+                   const float* rstd, const float* g_out, float* g_x, int64_t M, int32_t D,
+                   void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * Dense contractions on fp32 MFMA (replaces torch F.linear at model.py:147-154,203-205)
+ * ------------------------------------------------------------------------------------ */
+
+/* Y[M, N] = A[M, K] @ W[N, K]^T (+ bias[N] when non-NULL), fp32 in and out, fp32 MFMA
+ * accumulation.  lda/ldw/ldy are row strides in floats.  K must be a multiple of 4. */
+int fu_linear(const float* A, int64_t lda, const float* W, int64_t ldw, const float* bias,
+              float* Y, int64_t ldy, int64_t M, int32_t N, int32_t K, void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * Graph preprocessing (replaces reorder_graph_morton / _build_csr_uncached, model.py:20-74)
+ * ------------------------------------------------------------------------------------ */
+
+/* model.py:60-68: sort keys morton3d(quantised pos) | batch << 32 for N atoms. */
+int fu_morton_keys(const float* pos, const int64_t* batch, int64_t* keys, int64_t N,
+                   void* stream);
+
+/* Stable LSD radix sort of (key, value) int64 pairs on bits [begin_bit, end_bit).
+ * With workspace == NULL, stores the needed workspace size in *ws_bytes and returns. */
+int fu_sort_pairs_i64(const int64_t* keys_in, int64_t* keys_out, const int64_t* vals_in,
+                      int64_t* vals_out, int64_t n, int32_t begin_bit, int32_t end_bit,
+                      void* workspace, size_t* ws_bytes, void* stream);
+
+/* inv[perm[k]] = k for k < n (model.py:71-72). */
+int fu_invert_perm(const int64_t* perm, int64_t* inv, int64_t n, void* stream);
+
+/* out[e] = table[idx[e]] for int64 arrays; every idx must lie in [0, table_len). */
+int fu_take_i64(const int64_t* table, int64_t table_len, const int64_t* idx, int64_t* out,
+                int64_t n, void* stream);
+
+/* row_ptr (N+1, int32) of a CSR whose edge keys are sorted ascending, model.py:22-24:
+ * row_ptr[v] = #{e : sorted_keys[e] < v} for v = 0..N.  The caller guarantees keys in
+ * [0, N) (the op layer checks index ranges before building a topology). */
+int fu_csr_row_ptr(const int64_t* sorted_keys, int64_t E, int32_t* row_ptr, int64_t N,
+                   void* stream);
+
+/* int64 -> int32 narrowing copy (col_idx = sort_order.to(int32), model.py:25). */
+int fu_narrow_i64_i32(const int64_t* in, int32_t* out, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHUMA_H_ */

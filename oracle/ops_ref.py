@@ -1,0 +1,297 @@
+"""CPU restatement of the reference op layer (ops/*.py) — test infrastructure only.
+
+Every function works on torch CPU tensors in float64 (the parity reference) or float32, and
+is differentiable with torch autograd; the backward passes the HIP kernels implement are
+checked against autograd of these forwards (the reference's hand-written VJPs in
+ops/geom.py:313-493, ops/gather.py:160-405, ops/scatter.py:146-292,426-481,
+ops/gating.py:109-185 and ops/ln_silu.py:77-123 compute the same derivatives).
+
+Pins (beyond agreement with the HIP path):
+  - edge_geometry: envelope closed form (env(0)=1, env(c)=env'(c)=env''(c)=0), Gaussian
+    closed form, R(q) e = y-axis, D1 = textbook quaternion rotation matrix, D2 equal to the
+    l=2 symmetric-traceless-tensor representation of D1 (wigner_l2_from_rotation, derived
+    independently), orthogonality and the homomorphism D(q1 q2) = D(q1) D(q2).
+  - gather/scatter: agreement with an explicit 9x9 block-diagonal rotation + slot map
+    (rotate_full), and scatter = adjoint of gather (inner-product identity).
+  - gating / ln_silu: textbook sigmoid/SiLU and torch.nn.functional.layer_norm.
+  - so2 packing: packed real block matrix equals the complex product (R + iI)(a + ib).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+# Flat index of the 34 Wigner scalars per edge (ops/constants.py:7-16): L=1 3x3 row-major
+# then L=2 5x5 row-major.
+L1_OFF = 0
+L2_OFF = 9
+ENV_RESCALE = 5.0  # edge-degree rescale of init_node_scatter (ops/scatter.py:409-411)
+
+
+def envelope(dist: torch.Tensor, cutoff: float) -> torch.Tensor:
+    """Polynomial envelope 1 - 21u^5 + 35u^6 - 15u^7 for u = d/cutoff < 1, else 0
+    (ops/geom.py:78-82)."""
+    u = dist / cutoff
+    u2 = u * u
+    u5 = u2 * u2 * u
+    env = 1.0 + u5 * (-21.0 + u * (35.0 - 15.0 * u))
+    return torch.where(u < 1.0, env, torch.zeros_like(env))
+
+
+def edge_frame_quaternion(ex: torch.Tensor, ey: torch.Tensor, ez: torch.Tensor) -> torch.Tensor:
+    """Two-chart quaternion blend that maps the unit edge direction onto +y
+    (ops/geom.py:106-131).  Returns (E, 4) as (w, x, y, z)."""
+    eps = 1e-7
+    # chart 1: q1 = n(1 + e_y, -e_z, 0, e_x); chart 2: q2 = n(-e_z, 1 - e_y, e_x, 0)
+    n1 = torch.sqrt((1.0 + ey) ** 2 + ez * ez + ex * ex + eps)
+    q1w, q1x, q1z = (1.0 + ey) / n1, -ez / n1, ex / n1
+    n2 = torch.sqrt(ez * ez + (1.0 - ey) ** 2 + ex * ex + eps)
+    q2w, q2x, q2y = -ez / n2, (1.0 - ey) / n2, ex / n2
+    # blend weight s(t), t = clamp((e_y + 0.9)/1.8, 0, 1)
+    t = torch.clamp((ey + 0.9) / 1.8, 0.0, 1.0)
+    num = 2.0 * t - 1.0
+    den = torch.clamp(t * (1.0 - t), min=eps)
+    s = torch.sigmoid(num / den)
+    s = torch.where(t < eps, torch.zeros_like(s), s)
+    s = torch.where(t > 1.0 - eps, torch.ones_like(s), s)
+    # align hemispheres before blending
+    flip = (q1w * q2w + q1x * q2x) < 0.0
+    sign = torch.where(flip, -torch.ones_like(q1w), torch.ones_like(q1w))
+    q1w, q1x, q1z = q1w * sign, q1x * sign, q1z * sign
+    qw = (1.0 - s) * q2w + s * q1w
+    qx = (1.0 - s) * q2x + s * q1x
+    qy = (1.0 - s) * q2y
+    qz = s * q1z
+    ne = torch.sqrt(qw * qw + qx * qx + qy * qy + qz * qz + eps)
+    return torch.stack([qw / ne, qx / ne, qy / ne, qz / ne], dim=-1)
+
+
+def rotation_from_quaternion(q: torch.Tensor) -> torch.Tensor:
+    """Textbook rotation matrix of a unit quaternion (w, x, y, z); the L=1 Wigner block
+    (ops/geom.py:137-139).  Returns (..., 3, 3)."""
+    w, x, y, z = q.unbind(-1)
+    r = [
+        [1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y)],
+        [2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x)],
+        [2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)],
+    ]
+    return torch.stack([torch.stack(row, -1) for row in r], -2)
+
+
+# L=2 block as quartic polynomials of the quaternion, ops/geom.py:141-178.  Each entry is a
+# list of (coefficient, exponents of (w, x, y, z)).  S = sqrt(3).
+_S = math.sqrt(3.0)
+_L2_POLY: list[list[list[tuple[float, tuple[int, int, int, int]]]]] = [
+    [  # row 0
+        [(1, (4, 0, 0, 0)), (-6, (2, 0, 2, 0)), (-1, (0, 4, 0, 0)), (6, (0, 2, 0, 2)), (1, (0, 0, 4, 0)), (-1, (0, 0, 0, 4))],
+        [(2, (3, 1, 0, 0)), (6, (2, 0, 1, 1)), (2, (1, 3, 0, 0)), (-6, (1, 1, 2, 0)), (-6, (1, 1, 0, 2)), (6, (0, 2, 1, 1)), (-2, (0, 0, 3, 1)), (-2, (0, 0, 1, 3))],
+        [(-4 * _S, (2, 1, 0, 1)), (4 * _S, (1, 2, 1, 0)), (-4 * _S, (1, 0, 1, 2)), (4 * _S, (0, 1, 2, 1))],
+        [(-2, (3, 0, 0, 1)), (6, (2, 1, 1, 0)), (6, (1, 2, 0, 1)), (6, (1, 0, 2, 1)), (-2, (1, 0, 0, 3)), (-2, (0, 3, 1, 0)), (-2, (0, 1, 3, 0)), (6, (0, 1, 1, 2))],
+        [(4, (3, 0, 1, 0)), (-4, (1, 0, 3, 0)), (-4, (0, 3, 0, 1)), (4, (0, 1, 0, 3))],
+    ],
+    [  # row 1
+        [(-2, (3, 1, 0, 0)), (6, (2, 0, 1, 1)), (-2, (1, 3, 0, 0)), (6, (1, 1, 2, 0)), (6, (1, 1, 0, 2)), (6, (0, 2, 1, 1)), (-2, (0, 0, 3, 1)), (-2, (0, 0, 1, 3))],
+        [(1, (4, 0, 0, 0)), (-6, (2, 0, 0, 2)), (-1, (0, 4, 0, 0)), (6, (0, 2, 2, 0)), (-1, (0, 0, 4, 0)), (1, (0, 0, 0, 4))],
+        [(-2 * _S, (3, 0, 0, 1)), (2 * _S, (2, 1, 1, 0)), (2 * _S, (1, 2, 0, 1)), (-2 * _S, (1, 0, 2, 1)), (2 * _S, (1, 0, 0, 3)), (-2 * _S, (0, 3, 1, 0)), (2 * _S, (0, 1, 3, 0)), (-2 * _S, (0, 1, 1, 2))],
+        [(2, (3, 0, 1, 0)), (6, (2, 1, 0, 1)), (-6, (1, 2, 1, 0)), (2, (1, 0, 3, 0)), (-6, (1, 0, 1, 2)), (-2, (0, 3, 0, 1)), (6, (0, 1, 2, 1)), (-2, (0, 1, 0, 3))],
+        [(-2, (3, 0, 0, 1)), (-6, (2, 1, 1, 0)), (-6, (1, 2, 0, 1)), (6, (1, 0, 2, 1)), (2, (1, 0, 0, 3)), (-2, (0, 3, 1, 0)), (2, (0, 1, 3, 0)), (6, (0, 1, 1, 2))],
+    ],
+    [  # row 2
+        [(-4 * _S, (2, 1, 0, 1)), (-4 * _S, (1, 2, 1, 0)), (4 * _S, (1, 0, 1, 2)), (4 * _S, (0, 1, 2, 1))],
+        [(2 * _S, (3, 0, 0, 1)), (2 * _S, (2, 1, 1, 0)), (-2 * _S, (1, 2, 0, 1)), (2 * _S, (1, 0, 2, 1)), (-2 * _S, (1, 0, 0, 3)), (-2 * _S, (0, 3, 1, 0)), (2 * _S, (0, 1, 3, 0)), (-2 * _S, (0, 1, 1, 2))],
+        [(1, (4, 0, 0, 0)), (-4, (2, 2, 0, 0)), (2, (2, 0, 2, 0)), (-4, (2, 0, 0, 2)), (1, (0, 4, 0, 0)), (-4, (0, 2, 2, 0)), (2, (0, 2, 0, 2)), (1, (0, 0, 4, 0)), (-4, (0, 0, 2, 2)), (1, (0, 0, 0, 4))],
+        [(-2 * _S, (3, 1, 0, 0)), (2 * _S, (2, 0, 1, 1)), (2 * _S, (1, 3, 0, 0)), (-2 * _S, (1, 1, 2, 0)), (2 * _S, (1, 1, 0, 2)), (-2 * _S, (0, 2, 1, 1)), (2 * _S, (0, 0, 3, 1)), (-2 * _S, (0, 0, 1, 3))],
+        [(2 * _S, (2, 2, 0, 0)), (-2 * _S, (2, 0, 0, 2)), (-8 * _S, (1, 1, 1, 1)), (-2 * _S, (0, 2, 2, 0)), (2 * _S, (0, 0, 2, 2))],
+    ],
+    [  # row 3
+        [(2, (3, 0, 0, 1)), (6, (2, 1, 1, 0)), (-6, (1, 2, 0, 1)), (-6, (1, 0, 2, 1)), (2, (1, 0, 0, 3)), (-2, (0, 3, 1, 0)), (-2, (0, 1, 3, 0)), (6, (0, 1, 1, 2))],
+        [(-2, (3, 0, 1, 0)), (6, (2, 1, 0, 1)), (6, (1, 2, 1, 0)), (-2, (1, 0, 3, 0)), (6, (1, 0, 1, 2)), (-2, (0, 3, 0, 1)), (6, (0, 1, 2, 1)), (-2, (0, 1, 0, 3))],
+        [(2 * _S, (3, 1, 0, 0)), (2 * _S, (2, 0, 1, 1)), (-2 * _S, (1, 3, 0, 0)), (2 * _S, (1, 1, 2, 0)), (-2 * _S, (1, 1, 0, 2)), (-2 * _S, (0, 2, 1, 1)), (2 * _S, (0, 0, 3, 1)), (-2 * _S, (0, 0, 1, 3))],
+        [(1, (4, 0, 0, 0)), (-6, (2, 2, 0, 0)), (1, (0, 4, 0, 0)), (-1, (0, 0, 4, 0)), (6, (0, 0, 2, 2)), (-1, (0, 0, 0, 4))],
+        [(-2, (3, 1, 0, 0)), (6, (2, 0, 1, 1)), (2, (1, 3, 0, 0)), (6, (1, 1, 2, 0)), (-6, (1, 1, 0, 2)), (-6, (0, 2, 1, 1)), (-2, (0, 0, 3, 1)), (2, (0, 0, 1, 3))],
+    ],
+    [  # row 4
+        [(-4, (3, 0, 1, 0)), (4, (1, 0, 3, 0)), (-4, (0, 3, 0, 1)), (4, (0, 1, 0, 3))],
+        [(2, (3, 0, 0, 1)), (-6, (2, 1, 1, 0)), (6, (1, 2, 0, 1)), (-6, (1, 0, 2, 1)), (-2, (1, 0, 0, 3)), (-2, (0, 3, 1, 0)), (2, (0, 1, 3, 0)), (6, (0, 1, 1, 2))],
+        [(2 * _S, (2, 2, 0, 0)), (-2 * _S, (2, 0, 0, 2)), (8 * _S, (1, 1, 1, 1)), (-2 * _S, (0, 2, 2, 0)), (2 * _S, (0, 0, 2, 2))],
+        [(2, (3, 1, 0, 0)), (6, (2, 0, 1, 1)), (-2, (1, 3, 0, 0)), (-6, (1, 1, 2, 0)), (6, (1, 1, 0, 2)), (-6, (0, 2, 1, 1)), (-2, (0, 0, 3, 1)), (2, (0, 0, 1, 3))],
+        [(1, (4, 0, 0, 0)), (-6, (2, 0, 2, 0)), (1, (0, 4, 0, 0)), (-6, (0, 2, 0, 2)), (1, (0, 0, 4, 0)), (1, (0, 0, 0, 4))],
+    ],
+]
+
+
+def wigner_l2_from_quaternion(q: torch.Tensor) -> torch.Tensor:
+    """L=2 block of the reference (ops/geom.py:141-178), evaluated from the coefficient
+    table above.  Returns (..., 5, 5)."""
+    w, x, y, z = q.unbind(-1)
+    pw = [torch.ones_like(w), w, w * w, w * w * w, w * w * w * w]
+    px = [torch.ones_like(x), x, x * x, x * x * x, x * x * x * x]
+    py = [torch.ones_like(y), y, y * y, y * y * y, y * y * y * y]
+    pz = [torch.ones_like(z), z, z * z, z * z * z, z * z * z * z]
+    rows = []
+    for r in range(5):
+        cols = []
+        for c in range(5):
+            acc = torch.zeros_like(w)
+            for coef, (a, b, cc, d) in _L2_POLY[r][c]:
+                acc = acc + coef * (pw[a] * px[b] * py[cc] * pz[d])
+            cols.append(acc)
+        rows.append(torch.stack(cols, -1))
+    return torch.stack(rows, -2)
+
+
+# Orthonormal basis of symmetric traceless 3x3 matrices, one per L=2 coefficient (row index
+# of the D2 block), in (x, y, z) components with y as the polar axis.  Derived from the
+# real l=2 harmonics; used only to check the quartic table independently.
+def _l2_basis(dtype=torch.float64) -> torch.Tensor:
+    r2 = math.sqrt(2.0)
+    r6 = math.sqrt(6.0)
+    B = torch.zeros(5, 3, 3, dtype=dtype)
+    B[0, 0, 2] = B[0, 2, 0] = 1.0 / r2                 # xz
+    B[1, 0, 1] = B[1, 1, 0] = 1.0 / r2                 # xy
+    B[2] = torch.diag(torch.tensor([-1.0, 2.0, -1.0], dtype=dtype)) / r6  # 3y^2 - r^2
+    B[3, 1, 2] = B[3, 2, 1] = 1.0 / r2                 # yz
+    B[4, 0, 0], B[4, 2, 2] = -1.0 / r2, 1.0 / r2       # z^2 - x^2
+    return B
+
+
+def wigner_l2_from_rotation(R: torch.Tensor, basis: torch.Tensor | None = None) -> torch.Tensor:
+    """D2[a, b] = <B_a, R B_b R^T> (Frobenius) for the basis of _l2_basis: the l=2
+    representation induced by the 3x3 rotation R, independent of the quartic table."""
+    B = _l2_basis(R.dtype) if basis is None else basis
+    RB = torch.einsum("...ij,bjk,...lk->...bil", R, B, R)
+    return torch.einsum("aij,...bij->...ab", B, RB)
+
+
+def edge_geometry(pos, Z, idx_i, idx_j, shifts, W_src, W_tgt, offset_g, coeff_g, cutoff):
+    """precompute_geometry forward (ops/geom.py:36-214).
+
+    Returns x_edge_raw (E, B+2C), wigner (E, 34), env (E)."""
+    d = pos[idx_i] - pos[idx_j] + shifts
+    dist = torch.sqrt((d * d).sum(-1))
+    dist_safe = torch.clamp(dist, min=1e-7)
+    env = envelope(dist, cutoff)
+    gauss = torch.exp(coeff_g * (dist[:, None] - offset_g[None, :]) ** 2)
+    x_edge_raw = torch.cat([gauss, W_src[Z[idx_i]], W_tgt[Z[idx_j]]], dim=1)
+    e = d / dist_safe[:, None]
+    q = edge_frame_quaternion(e[:, 0], e[:, 1], e[:, 2])
+    D1 = rotation_from_quaternion(q)
+    D2 = wigner_l2_from_quaternion(q)
+    wigner = torch.cat([D1.reshape(-1, 9), D2.reshape(-1, 25)], dim=1)
+    return x_edge_raw, wigner, env
+
+
+def block_diag_rotation(wigner: torch.Tensor) -> torch.Tensor:
+    """Explicit (E, 9, 9) block-diagonal rotation diag(1, D1, D2) from the 34 scalars."""
+    E = wigner.shape[0]
+    D = torch.zeros(E, 9, 9, dtype=wigner.dtype)
+    D[:, 0, 0] = 1.0
+    D[:, 1:4, 1:4] = wigner[:, 0:9].reshape(E, 3, 3)
+    D[:, 4:9, 4:9] = wigner[:, 9:34].reshape(E, 5, 5)
+    return D
+
+
+# Slot map of the rotated frame (ops/gather.py:82-154, ops/scatter.py:117-127): which
+# rotated coefficient feeds each C-wide column block.  m=0: k0, k2, k6; m=1: R = k3, k7,
+# I = k1, k5; m=2: R = k8, I = k4.
+M0_COEF = [0, 2, 6]
+M1_COEF = [3, 7, 1, 5]      # [R_l1, R_l2, I_l1, I_l2]
+M2_COEF = [8, 4]            # [R, I]
+# Radial block used by each X column block: X_m0 = [s r0, t r1, s r2, t r3, s r4, t r5],
+# X_m1 = [s r6, t r7, s r8, t r9, s r6, t r7, s r8, t r9], X_m2 = [s r10, t r11, s r10, t r11].
+X_M0_RAD = [0, 1, 2, 3, 4, 5]
+X_M1_RAD = [6, 7, 8, 9, 6, 7, 8, 9]
+X_M2_RAD = [10, 11, 10, 11]
+
+
+def gather_rotate(x, idx_i, idx_j, wigner, rad, csd_emb, batch):
+    """gather_wigner_split forward (ops/gather.py:34-154) via an explicit 9x9 rotation.
+
+    x (N, 9, C); rad (E, 12C); csd_emb (S, C); batch (N,).  Returns X_m0, X_m1, X_m2."""
+    N, _, C = x.shape
+    E = idx_i.shape[0]
+    D = block_diag_rotation(wigner)
+    vs = x[idx_i].clone()
+    vt = x[idx_j].clone()
+    vs = torch.cat([(vs[:, 0] + csd_emb[batch[idx_i]])[:, None], vs[:, 1:]], 1)
+    vt = torch.cat([(vt[:, 0] + csd_emb[batch[idx_j]])[:, None], vt[:, 1:]], 1)
+    rs = torch.einsum("eab,ebc->eac", D, vs)  # rotated sender (E, 9, C)
+    rt = torch.einsum("eab,ebc->eac", D, vt)
+    r = rad.reshape(E, 12, C)
+
+    def pair(coefs, rads):
+        cols = []
+        for n, k in enumerate(coefs):
+            cols.append(rs[:, k] * r[:, rads[2 * n]])
+            cols.append(rt[:, k] * r[:, rads[2 * n + 1]])
+        return cols
+
+    X_m0 = torch.cat(pair(M0_COEF, X_M0_RAD), 1)
+    # m=1 blocks interleave sender/receiver per coefficient: [s k3, t k3, s k7, t k7, ...]
+    X_m1 = torch.cat(pair(M1_COEF, X_M1_RAD), 1)
+    X_m2 = torch.cat(pair(M2_COEF, X_M2_RAD), 1)
+    return X_m0, X_m1, X_m2
+
+
+def gating(Y_m0, Y_m1, Y_m2, C):
+    """fused_gating_split forward (ops/gating.py:63-103)."""
+    g1 = torch.sigmoid(Y_m0[:, 0:C])
+    g2 = torch.sigmoid(Y_m0[:, C:2 * C])
+    y0 = Y_m0[:, 2 * C:3 * C]
+    Z_m0 = torch.cat([torch.nn.functional.silu(y0), Y_m0[:, 3 * C:4 * C] * g1, Y_m0[:, 4 * C:5 * C] * g2], 1)
+    Z_m1 = torch.cat([Y_m1[:, 0:C] * g1, Y_m1[:, C:2 * C] * g2, Y_m1[:, 2 * C:3 * C] * g1, Y_m1[:, 3 * C:4 * C] * g2], 1)
+    Z_m2 = torch.cat([Y_m2[:, 0:C] * g2, Y_m2[:, C:2 * C] * g2], 1)
+    return Z_m0, Z_m1, Z_m2
+
+
+def unrotate_to_frame(Z_m0, Z_m1, Z_m2, C):
+    """Place the Zout m-blocks back at their rotated coefficients: (E, 9, C) with
+    zr[k] = slot value (ops/scatter.py:117-127)."""
+    E = Z_m0.shape[0]
+    zr = torch.zeros(E, 9, C, dtype=Z_m0.dtype)
+    blocks = list(Z_m0.reshape(E, 3, C).unbind(1)) + list(Z_m1.reshape(E, 4, C).unbind(1)) + \
+        list(Z_m2.reshape(E, 2, C).unbind(1))
+    coefs = M0_COEF + M1_COEF + M2_COEF
+    zr = torch.stack([blocks[coefs.index(k)] for k in range(9)], 1)
+    return zr
+
+
+def rotate_scatter(Z_m0, Z_m1, Z_m2, wigner, env, x_res, idx_j, N):
+    """rotate_scatter_split forward (ops/scatter.py:45-140): x_res + sum over incoming
+    edges of env * D^T zr, accumulated in float64."""
+    C = Z_m0.shape[1] // 3
+    zr = unrotate_to_frame(Z_m0, Z_m1, Z_m2, C)
+    D = block_diag_rotation(wigner)
+    msg = torch.einsum("eba,ebc->eac", D, zr) * env[:, None, None]  # D^T zr
+    out = torch.zeros(N, 9, C, dtype=torch.float64)
+    out = out.index_add(0, idx_j, msg.to(torch.float64))
+    return (out + x_res.to(torch.float64)).to(x_res.dtype)
+
+
+def init_scatter(rad, wigner, env, Z, batch, W_sphere, csd_emb, idx_j, N):
+    """init_node_scatter forward (ops/scatter.py:360-423): edge-degree embedding."""
+    C = rad.shape[1] // 3
+    E = rad.shape[0]
+    D = block_diag_rotation(wigner)
+    zr = torch.zeros(E, 9, C, dtype=rad.dtype)
+    zr = torch.stack([rad[:, 0:C] if k == 0 else rad[:, C:2 * C] if k == 2 else
+                      rad[:, 2 * C:3 * C] if k == 6 else torch.zeros_like(rad[:, 0:C])
+                      for k in range(9)], 1)
+    msg = torch.einsum("eba,ebc->eac", D, zr) * (env / ENV_RESCALE)[:, None, None]
+    out = torch.zeros(N, 9, C, dtype=torch.float64)
+    out = out.index_add(0, idx_j, msg.to(torch.float64))
+    l0 = (W_sphere[Z] + csd_emb[batch]).to(torch.float64)
+    out = out + torch.cat([l0[:, None], torch.zeros(N, 8, C, dtype=torch.float64)], 1)
+    return out.to(rad.dtype)
+
+
+def layer_norm_silu(x, gamma, beta, eps=1e-7):
+    """ops/ln_silu.py:29-72: LayerNorm (biased variance) + affine + SiLU over the last dim."""
+    y = torch.nn.functional.layer_norm(x, (x.shape[-1],), gamma, beta, eps)
+    return torch.nn.functional.silu(y)
+
+
+def pack_so2(R: torch.Tensor, I: torch.Tensor) -> torch.Tensor:
+    """Real block matrix [[R, -I], [I, R]] of the complex map R + iI (model.py:111-138)."""
+    return torch.cat([torch.cat([R, -I], 1), torch.cat([I, R], 1)], 0)

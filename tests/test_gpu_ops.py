@@ -1,0 +1,229 @@
+"""GPU parity of every hot-path op (forward and backward) against the CPU oracle.
+
+Each HIP op is called through its autograd Function (which calls the C-ABI); its outputs
+are compared with oracle/ops_ref.py in float64, and its gradients with torch autograd of
+the same oracle forward under one random cotangent.  Tolerance: scale-relative error
+<= 2e-5 for fp32 kernels against the float64 oracle (fp32 rounding of short sums).
+"""
+import numpy as np
+import pytest
+import torch
+
+from _helpers import assert_close, axis_aligned_edges, random_graph
+from oracle import ops_ref as R
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-5
+
+
+def _ops():
+    from ops import gather, gating, geom, ln_silu, scatter, linear, topology
+    return gather, gating, geom, ln_silu, scatter, linear, topology
+
+
+def _vjp(fn, inputs, cot):
+    ins = [t.detach().double().clone().requires_grad_(True) if t.is_floating_point() else t for t in inputs]
+    outs = fn(*ins)
+    if not isinstance(outs, tuple):
+        outs = (outs,)
+    s = sum((o * c.double()).sum() for o, c in zip(outs, cot))
+    grads = torch.autograd.grad(s, [t for t in ins if t.is_floating_point() and t.requires_grad], allow_unused=True)
+    return outs, grads
+
+
+def test_gating(cuda):
+    _, gating, *_ = _ops()
+    torch.manual_seed(0)
+    E, C = 333, 128
+    Y = [torch.randn(E, m * C) for m in (5, 4, 2)]
+    Yg = [y.to(cuda).requires_grad_(True) for y in Y]
+    Z = gating.fused_gating_split(*Yg, C)
+    cot = [torch.randn_like(z.cpu()) for z in Z]
+    ref, gref = _vjp(lambda a, b, c: R.gating(a, b, c, C), Y, cot)
+    for z, r in zip(Z, ref):
+        assert_close(z, r, TOL, "gating fwd")
+    g = torch.autograd.grad(Z, Yg, [c.to(cuda) for c in cot])
+    for a, b in zip(g, gref):
+        assert_close(a, b, TOL, "gating bwd")
+
+
+def test_ln_silu(cuda):
+    _, _, _, ln_silu, *_ = _ops()
+    torch.manual_seed(1)
+    M, D = 1000, 128
+    x = torch.randn(M, D) * 3 + 0.5
+    gamma, beta = torch.rand(D) + 0.5, torch.randn(D)
+    xg = x.to(cuda).requires_grad_(True)
+    out = ln_silu.layer_norm_silu(xg, gamma.to(cuda), beta.to(cuda))
+    cot = torch.randn(M, D)
+    (ref,), (gref,) = _vjp(lambda a: R.layer_norm_silu(a, gamma.double(), beta.double(), 1e-7), [x], [cot])
+    assert_close(out, ref, TOL, "ln_silu fwd")
+    (g,) = torch.autograd.grad(out, xg, cot.to(cuda))
+    assert_close(g, gref, 1e-4, "ln_silu bwd")
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 128, 64), (300, 640, 768), (257, 64, 128), (1000, 384, 384), (77, 1536, 128)])
+def test_linear(cuda, M, N, K):
+    *_, linear, _ = _ops()
+    torch.manual_seed(M + N + K)
+    x = torch.randn(M, K)
+    W = torch.randn(N, K) / K ** 0.5
+    b = torch.randn(N)
+    xg = x.to(cuda).requires_grad_(True)
+    Wg = W.to(cuda)
+    y = linear.linear(xg, Wg, b.to(cuda), Wg.t().contiguous())
+    cot = torch.randn(M, N)
+    (ref,), (gref,) = _vjp(lambda a: a @ W.double().T + b.double(), [x], [cot])
+    assert_close(y, ref, TOL, "linear fwd")
+    (g,) = torch.autograd.grad(y, xg, cot.to(cuda))
+    assert_close(g, gref, TOL, "linear bwd")
+
+
+def _geom_inputs(seed=2, N=40, E=300, C=128, B=64):
+    pos, Z, ei, shifts = random_graph(N, E, seed=seed)
+    pos, shifts = axis_aligned_edges(pos, ei, shifts)
+    g = torch.Generator().manual_seed(seed)
+    W_src = torch.randn(100, C, generator=g)
+    W_tgt = torch.randn(100, C, generator=g)
+    offset_g = torch.linspace(0, 6.0, B)
+    coeff_g = float(-0.5 / (2.0 * (offset_g[1] - offset_g[0])) ** 2)
+    return (torch.from_numpy(pos), torch.from_numpy(Z), torch.from_numpy(ei), torch.from_numpy(shifts), W_src, W_tgt,
+            offset_g, coeff_g)
+
+
+def test_geometry(cuda):
+    _, _, geom, *_ = _ops()
+    pos, Z, ei, shifts, W_src, W_tgt, offset_g, coeff_g = _geom_inputs()
+    cutoff = 6.0
+    posg = pos.to(cuda).requires_grad_(True)
+    shg = shifts.to(cuda).requires_grad_(True)
+    xe, wig, env = geom.precompute_geometry(posg, Z.to(cuda), ei[0].to(cuda), ei[1].to(cuda), shg, W_src.to(cuda),
+                                            W_tgt.to(cuda), offset_g.to(cuda), coeff_g, cutoff)
+    torch.manual_seed(3)
+    cot = [torch.randn(xe.shape), torch.randn(wig.shape), torch.randn(env.shape)]
+
+    def f(p, s):
+        return R.edge_geometry(p, Z, ei[0], ei[1], s, W_src.double(), W_tgt.double(), offset_g.double(), coeff_g,
+                               cutoff)
+
+    ref, (gp_ref, gs_ref) = _vjp(f, [pos, shifts], cot)
+    assert_close(xe, ref[0], TOL, "x_edge_raw")
+    assert_close(wig, ref[1], 2e-6 * 10, "wigner")
+    assert_close(env, ref[2], TOL, "env")
+    assert float(env[4].item()) == 0.0  # edge 4 lies beyond the cutoff
+    gp, gs = torch.autograd.grad((xe, wig, env), (posg, shg), [c.to(cuda) for c in cot])
+    assert_close(gs, gs_ref, 1e-4, "g_shifts")
+    assert_close(gp, gp_ref, 1e-4, "g_pos")
+
+
+def _gather_inputs(seed=4, N=40, E=300, C=128, S=1):
+    pos, Z, ei, shifts = random_graph(N, E, seed=seed)
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(E, 4, generator=g, dtype=torch.float64)
+    q = q / q.norm(dim=1, keepdim=True)
+    D1 = R.rotation_from_quaternion(q)
+    D2 = R.wigner_l2_from_quaternion(q)
+    wig = torch.cat([D1.reshape(E, 9), D2.reshape(E, 25)], 1).float()
+    x = torch.randn(N, 9, C, generator=g)
+    rad = torch.randn(E, 12 * C, generator=g)
+    csd = torch.randn(S, C, generator=g)
+    batch = torch.zeros(N, dtype=torch.long)
+    return x, torch.from_numpy(ei), wig, rad, csd, batch
+
+
+def test_gather(cuda):
+    gather, *_ = _ops()
+    x, ei, wig, rad, csd, batch = _gather_inputs()
+    C = x.shape[2]
+    xg, wg, rg = (t.to(cuda).requires_grad_(True) for t in (x, wig, rad))
+    X = gather.gather_wigner_split(xg, ei[0].to(cuda), ei[1].to(cuda), wg, rg, csd.to(cuda), batch.to(cuda))
+    torch.manual_seed(5)
+    cot = [torch.randn(t.shape) for t in X]
+    ref, gref = _vjp(lambda a, w, r: R.gather_rotate(a, ei[0], ei[1], w, r, csd.double(), batch), [x, wig, rad], cot)
+    for a, b in zip(X, ref):
+        assert_close(a, b, TOL, "gather fwd")
+    g = torch.autograd.grad(X, (xg, wg, rg), [c.to(cuda) for c in cot])
+    for a, b, name in zip(g, gref, ("g_x", "g_wigner", "g_rad")):
+        assert_close(a, b, TOL, f"gather bwd {name}")
+
+
+def test_gather_deterministic(cuda):
+    gather, *_ = _ops()
+    x, ei, wig, rad, csd, batch = _gather_inputs(seed=6, N=64, E=2000)
+    outs = []
+    for _ in range(2):
+        xg = x.to(cuda).requires_grad_(True)
+        X = gather.gather_wigner_split(xg, ei[0].to(cuda), ei[1].to(cuda), wig.to(cuda), rad.to(cuda), csd.to(cuda),
+                                       batch.to(cuda))
+        torch.manual_seed(7)
+        (g,) = torch.autograd.grad(X, xg, [torch.randn(t.shape).to(cuda) for t in X])
+        outs.append(g.cpu())
+    assert torch.equal(outs[0], outs[1])
+
+
+def _scatter_inputs(seed=8, N=40, E=300, C=128):
+    x, ei, wig, _, _, _ = _gather_inputs(seed=seed, N=N, E=E, C=C)
+    g = torch.Generator().manual_seed(seed + 1)
+    Zs = [torch.randn(E, m * C, generator=g) for m in (3, 4, 2)]
+    env = torch.rand(E, generator=g)
+    return x, ei, wig, Zs, env
+
+
+def test_rotate_scatter(cuda):
+    *_, scatter, _, topology = _ops()[:7]
+    x, ei, wig, Zs, env = _scatter_inputs()
+    N, C = x.shape[0], x.shape[2]
+    idx_j = ei[1].to(cuda)
+    row_ptr, col_idx = topology.receiver_csr(idx_j, N)
+    Zg = [z.to(cuda).requires_grad_(True) for z in Zs]
+    wg, eg, xg = wig.to(cuda).requires_grad_(True), env.to(cuda).requires_grad_(True), x.to(cuda).requires_grad_(True)
+    out = scatter.rotate_scatter_split(*Zg, wg, eg, xg, idx_j, row_ptr, col_idx, N)
+    torch.manual_seed(9)
+    cot = [torch.randn(out.shape)]
+    (ref,), gref = _vjp(lambda a, b, c, w, e, xr: R.rotate_scatter(a, b, c, w, e, xr, ei[1], N), [*Zs, wig, env, x],
+                        cot)
+    assert_close(out, ref, TOL, "scatter fwd")
+    g = torch.autograd.grad(out, (*Zg, wg, eg, xg), cot[0].to(cuda))
+    for a, b, name in zip(g, gref, ("gZ0", "gZ1", "gZ2", "g_wigner", "g_env", "g_x_res")):
+        assert_close(a, b, TOL, f"scatter bwd {name}")
+
+
+def test_init_scatter(cuda):
+    *_, scatter, _, topology = _ops()[:7]
+    x, ei, wig, _, env = _scatter_inputs(seed=10)
+    N, C = x.shape[0], x.shape[2]
+    E = ei.shape[1]
+    g = torch.Generator().manual_seed(11)
+    rad = torch.randn(E, 3 * C, generator=g)
+    Zn = torch.randint(1, 90, (N,), generator=g)
+    W_sphere = torch.randn(100, C, generator=g)
+    csd = torch.randn(1, C, generator=g)
+    batch = torch.zeros(N, dtype=torch.long)
+    idx_j = ei[1].to(cuda)
+    row_ptr, col_idx = topology.receiver_csr(idx_j, N)
+    rg, wg, eg = (t.to(cuda).requires_grad_(True) for t in (rad, wig, env))
+    out = scatter.init_node_scatter(rg, wg, eg, Zn.to(cuda), batch.to(cuda), W_sphere.to(cuda), csd.to(cuda), idx_j,
+                                    row_ptr, col_idx, N)
+    cot = [torch.randn(out.shape, generator=g)]
+    (ref,), gref = _vjp(lambda r, w, e: R.init_scatter(r, w, e, Zn, batch, W_sphere.double(), csd.double(), ei[1], N),
+                        [rad, wig, env], cot)
+    assert_close(out, ref, TOL, "init scatter fwd")
+    gg = torch.autograd.grad(out, (rg, wg, eg), cot[0].to(cuda))
+    for a, b, name in zip(gg, gref, ("g_rad", "g_wigner", "g_env")):
+        assert_close(a, b, TOL, f"init scatter bwd {name}")
+
+
+def test_empty_graph(cuda):
+    """E = 0: every op returns correctly shaped outputs and the scatter is the residual."""
+    gather, gating, geom, ln_silu, scatter, linear, topology = _ops()
+    N, C = 5, 128
+    x = torch.randn(N, 9, C, device=cuda)
+    e0 = torch.zeros(0, dtype=torch.long, device=cuda)
+    wig = torch.zeros(0, 34, device=cuda)
+    Zs = [torch.zeros(0, m * C, device=cuda) for m in (3, 4, 2)]
+    row_ptr, col_idx = topology.receiver_csr(e0, N)
+    out = scatter.rotate_scatter_split(*Zs, wig, torch.zeros(0, device=cuda), x, e0, row_ptr, col_idx, N)
+    assert torch.equal(out, x)
+    X = gather.gather_wigner_split(x, e0, e0, wig, torch.zeros(0, 12 * C, device=cuda), torch.zeros(1, C, device=cuda),
+                                   torch.zeros(N, dtype=torch.long, device=cuda))
+    assert [t.shape for t in X] == [(0, 6 * C), (0, 8 * C), (0, 4 * C)]
