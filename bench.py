@@ -1,0 +1,177 @@
+"""Benchmark of the FlashUMA ZeroAllocBackbone hot path on one MI355X.
+
+A step is one energy + forces + stress evaluation (backbone forward through the HIP kernels,
+energy head, autograd backward to positions and cell) of the headline workload: bcc Fe
+16x16x16 conventional cells (8,192 atoms, 245,760 edges, cutoff 6 A, max 30 neighbours),
+UMA-s-shaped random-init weights (lmax = mmax = 2, 4 layers, C = 128, 64 Gaussians), fp32.
+The graph is built once on the host and its topology is cached (as across MD steps);
+all inputs are resident in HBM before the timed region.
+
+Prints one JSON line: atom-steps/s, ms/step, the roofline of the dominant kernel measured
+with HIP events on the launch stream during the timed steps, a per-kernel breakdown and the
+CPU baseline (the float32 torch-CPU oracle on a bounded sample of the same workload).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config bcc_fe] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "flash-uma_amd")
+sys.path[:0] = [ROOT, PKG]
+
+METRIC = "atom-steps/sec (energy+forces) on 1 MI355X; % HBM roofline per kernel"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_system(config: str):
+    import systems
+    if config == "bcc_fe":
+        return systems.bcc_fe(n_rep=16), True, "bcc_fe_16x16x16"
+    if config == "water_box":
+        return systems.water_box(), False, "water_box_333"
+    if config == "amorphous":
+        return systems.amorphous(), False, "amorphous_50k"
+    if config == "cu_slab_co":
+        return systems.cu_slab_co(), False, "cu_slab_co"
+    raise SystemExit(f"unknown config {config}")
+
+
+def cpu_baseline(budget_s: float = 20.0) -> dict:
+    """float32 torch-CPU oracle (reference-algorithm restatement) on bcc Fe 4x4x4
+    (128 atoms, same per-atom work as the headline: 30 edges/atom), E+F+S."""
+    import torch
+    import escn_md
+    import heads
+    import systems
+    from oracle.model_ref import energy_forces_stress
+
+    cores = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(cores)
+    bb = escn_md.eSCNMDBackbone(seed=0)
+    hd = heads.MLPEnergyHead(bb.sphere_channels, bb.hidden_channels, seed=1)
+    s = systems.bcc_fe(n_rep=4)
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, bb.cutoff, bb.max_neighbors)
+    energy_forces_stress(bb, hd, s.pos, s.Z, s.cell, ei, off, dtype=torch.float32)   # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 and time.perf_counter() - t_start < budget_s:
+        t0 = time.perf_counter()
+        energy_forces_stress(bb, hd, s.pos, s.Z, s.cell, ei, off, dtype=torch.float32)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(s.n_atoms / med, 2), "unit": "atom-steps/s", "cores": cores, "kind": "port",
+            "sample": f"bcc Fe 4x4x4 ({s.n_atoms} atoms, {ei.shape[1]} edges), E+F+S, float32 torch-CPU oracle "
+                      f"(oracle/model_ref.py), median of {len(times)} steps after 1 warm-up; CPU: {model}"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="bcc_fe")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-kernel-profile", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        raise SystemExit(2)
+
+    import numpy as np
+    import torch
+    import escn_md
+    import heads
+    import roofline
+    import systems
+    from ops import _lib
+    from wrapper import ZeroAllocBackbone
+
+    dev = torch.device("cuda:0")
+    _lib.load()
+    system, with_stress, wl_name = make_system(args.config)
+    bb = escn_md.eSCNMDBackbone(seed=0)
+    hd = heads.MLPEnergyHead(bb.sphere_channels, bb.hidden_channels, seed=1)
+    t0 = time.perf_counter()
+    ei, off = systems.neighbor_list(system.pos, system.cell, system.pbc, bb.cutoff, bb.max_neighbors)
+    log(f"[bench] {wl_name}: {system.n_atoms} atoms, {ei.shape[1]} edges (graph {time.perf_counter() - t0:.1f}s)")
+    model = heads.PotentialModel(ZeroAllocBackbone(bb.to(dev)), hd.to(dev))
+    data = heads.make_atomic_data(system, ei, off, dev)
+
+    def step():
+        return model(data, compute_forces=True, compute_stress=with_stress)
+
+    for k in range(args.warmup):
+        out = step()
+        torch.cuda.synchronize()
+        log(f"[bench] warm-up {k + 1}/{args.warmup}: E = {out['energy'].item():.6f}")
+    prof = None if args.no_kernel_profile else _lib.KernelProfiler()
+    _lib.set_profiler(prof)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    _lib.set_profiler(None)
+    ms = 1e3 * elapsed / args.steps
+    value = system.n_atoms / (elapsed / args.steps)
+    log(f"[bench] timed {args.steps} steps: {ms:.3f} ms/step, {value:.1f} atom-steps/s")
+
+    kernels = roofline.summarize(prof.durations()) if prof else {}
+    for rec in kernels.values():
+        rec["ms_per_step"] = round(rec["total_ms"] / args.steps, 4)
+    rl = None
+    if kernels:
+        dom = max(kernels, key=lambda k: kernels[k]["total_ms"])
+        d = kernels[dom]
+        rl = {"kernel": dom, "bound": d["bound"], "achieved": d["achieved"], "peak": d["peak"], "unit": d["unit"],
+              "frac": d["frac"], "traffic": None}
+        pmc = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+        if os.path.exists(pmc):
+            with open(pmc) as f:
+                tr = json.load(f).get(args.config, {}).get(dom)
+            if tr is not None:
+                rl["traffic"] = tr
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline (float32 torch-CPU oracle) ...")
+        cpu = cpu_baseline()
+        log(f"[bench] CPU baseline: {cpu['value']} atom-steps/s on {cpu['cores']} cores")
+
+    rec = {
+        "metric": METRIC, "value": round(value, 2), "unit": "atom-steps/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"{wl_name}: {system.n_atoms} atoms, {ei.shape[1]} edges, "
+                               f"{'E+F+S' if with_stress else 'E+F'}, UMA-s-shaped random-init eSCN-MD "
+                               f"(lmax=2, mmax=2, 4 layers, C=128, B=64, cutoff 6, max_neighbors 30)",
+                   "atoms": system.n_atoms, "edges": int(ei.shape[1]), "parallelism": "single GPU"},
+        "roofline": rl, "cpu_baseline": cpu, "kernels": kernels,
+        "energy": round(float(out["energy"].item()), 8),
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -81,10 +81,45 @@ def stream_ptr(device: torch.device | None = None) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+class KernelProfiler:
+    """Brackets selected entry points with HIP events on the stream they launch on (torch's
+    current stream, the one every op passes to the library) and keeps (name, args, start,
+    end) per call; durations are read after a synchronisation."""
+
+    def __init__(self, names=None):
+        self.names = set(names) if names else None
+        self.records: list = []
+
+    def wants(self, name: str) -> bool:
+        return self.names is None or name in self.names
+
+    def durations(self):
+        """[(name, args, milliseconds)] of all recorded calls (synchronises first)."""
+        torch.cuda.synchronize()
+        return [(n, a, s.elapsed_time(e)) for n, a, s, e in self.records]
+
+
+_profiler: KernelProfiler | None = None
+
+
+def set_profiler(profiler: KernelProfiler | None) -> None:
+    global _profiler
+    _profiler = profiler
+
+
 def call(name: str, *args) -> None:
     """Invoke entry point `name`; raise FlashUMAError with the library message on failure."""
     lib = load()
-    status = getattr(lib, name)(*args)
+    prof = _profiler
+    if prof is not None and prof.wants(name):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        status = getattr(lib, name)(*args)
+        end.record()
+        prof.records.append((name, args, start, end))
+    else:
+        status = getattr(lib, name)(*args)
     if status != 0:
         msg = lib.fu_last_error().decode(errors="replace")
         raise FlashUMAError(f"{name} failed with status {status}: {msg}")

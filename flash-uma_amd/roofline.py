@@ -1,0 +1,138 @@
+"""Algorithmic traffic and work of every C-ABI entry point, from its call arguments.
+
+Bytes count each tensor the kernel must touch exactly once (reads + writes, fp32 features,
+int64 graph indices, int32 CSR arrays); node-sized tables are counted once per launch.
+GEMMs count 2*M*N*K flops.  These are the denominators of the roofline fractions:
+achieved = algorithmic bytes (flops) / measured kernel time.
+
+Per-unit figures at C = 128, B = 64 (bytes per edge + bytes per node):
+  gating fwd 10240 / bwd 15872; gather fwd 15512 + 4616, bwd 21784 + 9232;
+  scatter fwd 4752 + 9220, bwd 9504 + 4608; init scatter fwd 1576 + 5640, bwd 3256 + 4608;
+  geom fwd 1448 (+ 1024 with embeddings) + 20, bwd 436 + 12; ln_silu 1032 / 1544 per row.
+"""
+from __future__ import annotations
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
+
+
+def _gating_fwd(a):
+    E, C = a[6], a[7]
+    return E * C * 20 * 4, 0
+
+
+def _gating_bwd(a):
+    E, C = a[9], a[10]
+    return E * C * 31 * 4, 0
+
+
+def _gather_fwd(a):
+    E, N, C = a[10], a[11], a[13]
+    return E * (30 * C * 4 + 34 * 4 + 16) + N * (9 * C * 4 + 8), 0
+
+
+def _gather_bwd(a):
+    E, N, C = a[18], a[19], a[21]
+    return E * (42 * C * 4 + 2 * 34 * 4 + 8) + N * (2 * 9 * C * 4 + 16), 0
+
+
+def _scatter_fwd(a):
+    N, E, C = a[9], a[10], a[11]
+    return E * (9 * C * 4 + 34 * 4 + 4 + 4) + N * (2 * 9 * C * 4 + 4), 0
+
+
+def _scatter_bwd(a):
+    E, N, C = a[12], a[13], a[14]
+    return E * (2 * 9 * C * 4 + 2 * 34 * 4 + 8 + 8) + N * 9 * C * 4, 0
+
+
+def _init_fwd(a):
+    N, E, C = a[10], a[11], a[14]
+    return E * (3 * C * 4 + 8 * 4 + 4 + 4) + N * (9 * C * 4 + 2 * C * 4 + 16), 0
+
+
+def _init_bwd(a):
+    E, N, C = a[8], a[9], a[10]
+    return E * (2 * 3 * C * 4 + 8 * 4 + 34 * 4 + 8 + 8) + N * 9 * C * 4, 0
+
+
+def _geom_fwd(a):
+    E, N, B, C = a[12], a[13], a[14], a[15]
+    width = B + 2 * C if a[5] is not None else B
+    return E * (16 + 12 + width * 4 + 34 * 4 + 4) + N * 20, 0
+
+
+def _geom_bwd(a):
+    E, N, B = a[10], a[11], a[12]
+    gx = B * 4 if a[5] is not None else 0
+    return E * (16 + 12 + gx + 34 * 4 + 4 + 12) + N * 12, 0
+
+
+def _edge_vec(a):
+    N, E = a[6], a[7]
+    return E * (12 + 4 + 4) + N * (12 + 8), 0
+
+
+def _ln_fwd(a):
+    M, D = a[6], a[7]
+    return M * (2 * D * 4 + 8), 0
+
+
+def _ln_bwd(a):
+    M, D = a[7], a[8]
+    return M * (3 * D * 4 + 8), 0
+
+
+def _linear(a):
+    M, N, K = a[7], a[8], a[9]
+    return 4 * (M * K + M * N + N * K), 2 * M * N * K
+
+
+WORK = {
+    "fu_gating_fwd": _gating_fwd,
+    "fu_gating_bwd": _gating_bwd,
+    "fu_gather_fwd": _gather_fwd,
+    "fu_gather_bwd": _gather_bwd,
+    "fu_scatter_fwd": _scatter_fwd,
+    "fu_scatter_bwd": _scatter_bwd,
+    "fu_init_scatter_fwd": _init_fwd,
+    "fu_init_scatter_bwd": _init_bwd,
+    "fu_geom_fwd": _geom_fwd,
+    "fu_geom_bwd": _geom_bwd,
+    "fu_edge_vec_reduce": _edge_vec,
+    "fu_ln_silu_fwd": _ln_fwd,
+    "fu_ln_silu_bwd": _ln_bwd,
+    "fu_linear": _linear,
+}
+
+MFMA_BOUND = {"fu_linear"}
+
+
+def summarize(durations) -> dict:
+    """Per entry point: calls, total/avg ms, algorithmic bytes/flops per launch and the
+    achieved fraction of the bounding roofline."""
+    agg: dict = {}
+    for name, args, ms in durations:
+        if name not in WORK:
+            continue
+        nbytes, flops = WORK[name](args)
+        a = agg.setdefault(name, {"calls": 0, "ms": 0.0, "bytes": 0, "flops": 0})
+        a["calls"] += 1
+        a["ms"] += ms
+        a["bytes"] += nbytes
+        a["flops"] += flops
+    out = {}
+    for name, a in agg.items():
+        sec = a["ms"] / 1e3
+        rec = {"calls": a["calls"], "total_ms": round(a["ms"], 4), "avg_us": round(1e3 * a["ms"] / a["calls"], 2)}
+        if name in MFMA_BOUND:
+            ach = a["flops"] / sec / 1e12 if sec > 0 else 0.0
+            rec.update(bound="mfma", unit="TFLOP/s", achieved=round(ach, 2), peak=FP32_MFMA_PEAK_TFLOPS,
+                       frac=round(ach / FP32_MFMA_PEAK_TFLOPS, 4), flops_per_launch=a["flops"] // a["calls"],
+                       hbm_gbs=round(a["bytes"] / sec / 1e9, 1) if sec > 0 else 0.0)
+        else:
+            ach = a["bytes"] / sec / 1e9 if sec > 0 else 0.0
+            rec.update(bound="hbm", unit="GB/s", achieved=round(ach, 1), peak=HBM_PEAK_GBS,
+                       frac=round(ach / HBM_PEAK_GBS, 4), bytes_per_launch=a["bytes"] // a["calls"])
+        out[name] = rec
+    return out
