@@ -1,0 +1,78 @@
+"""The C-ABI library loads, exports every symbol include/flashuma.h declares, and rejects bad
+arguments with the documented status codes before touching the GPU (no compute calls)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "flashuma.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fu_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_matches_binding():
+    from ops import _lib
+    assert header_symbols() == sorted(_lib.exported_symbols())
+
+
+def test_library_exports_all_symbols():
+    from ops import _lib
+    lib = _lib.load()
+    for name in header_symbols():
+        assert hasattr(lib, name), f"{name} not exported"
+    assert lib.fu_version() >= 100
+
+
+def _status(name, *args):
+    from ops import _lib
+    lib = _lib.load()
+    return getattr(lib, name)(*args), lib.fu_last_error().decode()
+
+
+def test_error_codes():
+    # FU_ERR_SHAPE = -1, UNSUPPORTED = -2, ALIGN = -3, NULL = -5, WORKSPACE = -6
+    st, msg = _status("fu_gating_fwd", None, None, None, None, None, None, 10, 6, None)
+    assert st == -2 and "multiple of 4" in msg
+    st, msg = _status("fu_gating_fwd", None, None, None, None, None, None, 10, 128, None)
+    assert st == -5
+    st, _ = _status("fu_gating_fwd", None, None, None, None, None, None, -1, 128, None)
+    assert st == -1
+    st, msg = _status("fu_linear", 16, 8, 16, 8, None, 16, 8, 10, 8, 6, None)
+    assert st == -2 and "multiples of 4" in msg
+    st, _ = _status("fu_linear", 3, 8, 16, 8, None, 16, 8, 10, 8, 8, None)
+    assert st == -3
+    st, _ = _status("fu_gather_fwd", *([None] * 10), 5, 5, 1, 96, None)
+    assert st == -2
+    st, _ = _status("fu_ln_silu_fwd", *([None] * 6), 4, 100, ctypes.c_float(1e-7), None)
+    assert st == -2
+    ws = ctypes.c_size_t(0)
+    st, _ = _status("fu_sort_pairs_i64", None, None, None, None, 10, 8, 8, None, ctypes.byref(ws), None)
+    assert st == -1
+    st, _ = _status("fu_geom_fwd", *([None] * 9), 4, None, None, 10, 5, 8, 4, ctypes.c_float(6.0),
+                    ctypes.c_float(-1.0), None)
+    assert st == -1  # ld_xe smaller than the embedding row width
+    st, _ = _status("fu_scatter_fwd", *([None] * 9), 3, 3, 192, None)
+    assert st == -2
+
+
+def test_zero_sized_calls_are_no_ops():
+    # E == 0 returns before any launch
+    st, _ = _status("fu_gating_fwd", 16, 16, 16, 16, 16, 16, 0, 128, None)
+    assert st == 0
+    st, _ = _status("fu_linear", 16, 8, 16, 8, None, 16, 8, 0, 8, 8, None)
+    assert st == 0
+
+
+def test_product_raises_without_gpu_tensors():
+    """The op layer has no CPU fallback: CPU tensors are rejected loudly."""
+    import torch
+    from ops import _lib
+    from ops.gating import fused_gating_split
+    with pytest.raises(_lib.FlashUMAError):
+        fused_gating_split(torch.zeros(4, 640), torch.zeros(4, 512), torch.zeros(4, 256), 128)
