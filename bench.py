@@ -91,6 +91,9 @@ def main() -> None:
     ap.add_argument("--config", default="bcc_fe")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernel-profile", action="store_true")
+    ap.add_argument("--pmc-calibration", action="store_true",
+                    help="first copy a 256 MiB buffer (a plain copy kernel of known size, the scale "
+                         "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -116,6 +119,13 @@ def main() -> None:
     log(f"[bench] {wl_name}: {system.n_atoms} atoms, {ei.shape[1]} edges (graph {time.perf_counter() - t0:.1f}s)")
     model = heads.PotentialModel(ZeroAllocBackbone(bb.to(dev)), hd.to(dev))
     data = heads.make_atomic_data(system, ei, off, dev)
+
+    if args.pmc_calibration:
+        src_buf = torch.ones(64 * 1024 * 1024, device=dev)
+        dst_buf = torch.empty_like(src_buf)
+        dst_buf.copy_(src_buf)
+        torch.cuda.synchronize()
+        del src_buf, dst_buf
 
     def step():
         return model(data, compute_forces=True, compute_stress=with_stress)
