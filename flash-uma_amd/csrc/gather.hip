@@ -118,7 +118,78 @@ __global__ __launch_bounds__(256) void gather_fwd_kernel(
   }
 }
 
-// One side (receiver: so = 1, sender: so = 0) of one node's gather backward.
+// Per-edge data of one side of the gather backward (receiver side: so = 1, sender: so = 0).
+template <int CPL>
+struct SideEdge {
+  float w[34];
+  Vec<CPL> g[9];   // this side's g_X slots: m0 a/b/c, m1 a/b/c/d, m2 a/b
+  Vec<CPL> r[6];   // this side's radial blocks so, 2+so, ..., 10+so
+};
+
+template <int CPL>
+__device__ __forceinline__ void side_load(const float* __restrict__ gX0, const float* __restrict__ gX1,
+                                          const float* __restrict__ gX2, const float* __restrict__ wig,
+                                          const float* __restrict__ rad, int64_t e, int so, int c, SideEdge<CPL>& d) {
+  constexpr int C = 64 * CPL;
+#pragma unroll
+  for (int q = 0; q < 34; ++q) d.w[q] = wig[e * 34 + q];
+  const float* g0 = gX0 + e * 6 * C + so * C + c;
+  const float* g1 = gX1 + e * 8 * C + so * C + c;
+  const float* g2 = gX2 + e * 4 * C + so * C + c;
+  d.g[0] = vload<CPL>(g0); d.g[1] = vload<CPL>(g0 + 2 * C); d.g[2] = vload<CPL>(g0 + 4 * C);
+  d.g[3] = vload<CPL>(g1); d.g[4] = vload<CPL>(g1 + 2 * C); d.g[5] = vload<CPL>(g1 + 4 * C);
+  d.g[6] = vload<CPL>(g1 + 6 * C);
+  d.g[7] = vload<CPL>(g2); d.g[8] = vload<CPL>(g2 + 2 * C);
+  const float* rp = rad + e * 12 * C + so * C + c;
+#pragma unroll
+  for (int q = 0; q < 6; ++q) d.r[q] = vload<CPL>(rp + 2 * q * C);
+}
+
+template <int CPL>
+__device__ __forceinline__ void side_apply(const SideEdge<CPL>& d, int64_t e, int so, int c, const Rows9<CPL>& v,
+                                           Rows9<CPL>& acc, float* __restrict__ g_rad, float* __restrict__ gw_out,
+                                           int lane) {
+  constexpr int C = 64 * CPL;
+  Rows9<CPL> rv;
+  rotate9(d.w, v, rv);
+  // this side's radial gradients (blocks so, 2+so, ..., 10+so)
+  float* gr = g_rad + e * 12 * C + so * C + c;
+  vstore(gr + 0 * C, vmul(d.g[0], rv.r[0]));
+  vstore(gr + 2 * C, vmul(d.g[1], rv.r[2]));
+  vstore(gr + 4 * C, vmul(d.g[2], rv.r[6]));
+  vstore(gr + 6 * C, vadd(vmul(d.g[3], rv.r[3]), vmul(d.g[5], rv.r[1])));
+  vstore(gr + 8 * C, vadd(vmul(d.g[4], rv.r[7]), vmul(d.g[6], rv.r[5])));
+  vstore(gr + 10 * C, vadd(vmul(d.g[7], rv.r[8]), vmul(d.g[8], rv.r[4])));
+  // gradient w.r.t. the rotated coefficients of this node's row
+  Rows9<CPL> grv;
+  grv.r[0] = vmul(d.g[0], d.r[0]);
+  grv.r[2] = vmul(d.g[1], d.r[1]);
+  grv.r[6] = vmul(d.g[2], d.r[2]);
+  grv.r[3] = vmul(d.g[3], d.r[3]);
+  grv.r[7] = vmul(d.g[4], d.r[4]);
+  grv.r[1] = vmul(d.g[5], d.r[3]);
+  grv.r[5] = vmul(d.g[6], d.r[4]);
+  grv.r[8] = vmul(d.g[7], d.r[5]);
+  grv.r[4] = vmul(d.g[8], d.r[5]);
+  add_rotate9_t(d.w, grv, acc);
+  // this side's g_wigner: dL/dD1[a][b] = sum_c grv[1+a] v[1+b], dL/dD2[a][b] = sum_c grv[4+a] v[4+b]
+  float part[64];
+#pragma unroll
+  for (int a = 0; a < 3; ++a)
+#pragma unroll
+    for (int b = 0; b < 3; ++b) part[3 * a + b] = vdot(grv.r[1 + a], v.r[1 + b]);
+#pragma unroll
+  for (int a = 0; a < 5; ++a)
+#pragma unroll
+    for (int b = 0; b < 5; ++b) part[9 + 5 * a + b] = vdot(grv.r[4 + a], v.r[4 + b]);
+#pragma unroll
+  for (int q = 34; q < 64; ++q) part[q] = 0.0f;
+  const float tot = wave_multi_sum<64>(part, lane);
+  if (lane < 34) gw_out[e * 34 + lane] = tot;
+}
+
+// One side of one node's gather backward: walk the node's CSR segment in order, two edges
+// per iteration so that their loads overlap.
 template <int CPL>
 __device__ __forceinline__ void gather_bwd_side(const float* __restrict__ gX0, const float* __restrict__ gX1,
                                                 const float* __restrict__ gX2, const float* __restrict__ wig,
@@ -126,61 +197,22 @@ __device__ __forceinline__ void gather_bwd_side(const float* __restrict__ gX0, c
                                                 const int32_t* __restrict__ idx, int64_t n, int so,
                                                 const Rows9<CPL>& v, Rows9<CPL>& acc, float* __restrict__ g_rad,
                                                 float* __restrict__ gw_out, int lane) {
-  constexpr int C = 64 * CPL;
   const int c = lane * CPL;
   const int32_t k0 = ptr[n], k1 = ptr[n + 1];
-  for (int32_t k = k0; k < k1; ++k) {
+  int32_t k = k0;
+  for (; k + 1 < k1; k += 2) {
+    const int64_t ea = idx[k], eb = idx[k + 1];
+    SideEdge<CPL> da, db;
+    side_load<CPL>(gX0, gX1, gX2, wig, rad, ea, so, c, da);
+    side_load<CPL>(gX0, gX1, gX2, wig, rad, eb, so, c, db);
+    side_apply<CPL>(da, ea, so, c, v, acc, g_rad, gw_out, lane);
+    side_apply<CPL>(db, eb, so, c, v, acc, g_rad, gw_out, lane);
+  }
+  if (k < k1) {
     const int64_t e = idx[k];
-    float w[34];
-#pragma unroll
-    for (int q = 0; q < 34; ++q) w[q] = wig[e * 34 + q];
-    Rows9<CPL> rv;
-    rotate9(w, v, rv);
-    const float* g0 = gX0 + e * 6 * C + so * C + c;
-    const float* g1 = gX1 + e * 8 * C + so * C + c;
-    const float* g2 = gX2 + e * 4 * C + so * C + c;
-    const Vec<CPL> gm0a = vload<CPL>(g0), gm0b = vload<CPL>(g0 + 2 * C), gm0c = vload<CPL>(g0 + 4 * C);
-    const Vec<CPL> gm1a = vload<CPL>(g1), gm1b = vload<CPL>(g1 + 2 * C), gm1c = vload<CPL>(g1 + 4 * C),
-                   gm1d = vload<CPL>(g1 + 6 * C);
-    const Vec<CPL> gm2a = vload<CPL>(g2), gm2b = vload<CPL>(g2 + 2 * C);
-    const float* rp = rad + e * 12 * C + so * C + c;
-    Vec<CPL> rr[6];
-#pragma unroll
-    for (int q = 0; q < 6; ++q) rr[q] = vload<CPL>(rp + 2 * q * C);
-    // this side's radial gradients (blocks so, 2+so, ..., 10+so)
-    float* gr = g_rad + e * 12 * C + so * C + c;
-    vstore(gr + 0 * C, vmul(gm0a, rv.r[0]));
-    vstore(gr + 2 * C, vmul(gm0b, rv.r[2]));
-    vstore(gr + 4 * C, vmul(gm0c, rv.r[6]));
-    vstore(gr + 6 * C, vadd(vmul(gm1a, rv.r[3]), vmul(gm1c, rv.r[1])));
-    vstore(gr + 8 * C, vadd(vmul(gm1b, rv.r[7]), vmul(gm1d, rv.r[5])));
-    vstore(gr + 10 * C, vadd(vmul(gm2a, rv.r[8]), vmul(gm2b, rv.r[4])));
-    // gradient w.r.t. the rotated coefficients of this node's row
-    Rows9<CPL> grv;
-    grv.r[0] = vmul(gm0a, rr[0]);
-    grv.r[2] = vmul(gm0b, rr[1]);
-    grv.r[6] = vmul(gm0c, rr[2]);
-    grv.r[3] = vmul(gm1a, rr[3]);
-    grv.r[7] = vmul(gm1b, rr[4]);
-    grv.r[1] = vmul(gm1c, rr[3]);
-    grv.r[5] = vmul(gm1d, rr[4]);
-    grv.r[8] = vmul(gm2a, rr[5]);
-    grv.r[4] = vmul(gm2b, rr[5]);
-    add_rotate9_t(w, grv, acc);
-    // this side's g_wigner: dL/dD1[a][b] = sum_c grv[1+a] v[1+b], dL/dD2[a][b] = sum_c grv[4+a] v[4+b]
-    float part[64];
-#pragma unroll
-    for (int a = 0; a < 3; ++a)
-#pragma unroll
-      for (int b = 0; b < 3; ++b) part[3 * a + b] = vdot(grv.r[1 + a], v.r[1 + b]);
-#pragma unroll
-    for (int a = 0; a < 5; ++a)
-#pragma unroll
-      for (int b = 0; b < 5; ++b) part[9 + 5 * a + b] = vdot(grv.r[4 + a], v.r[4 + b]);
-#pragma unroll
-    for (int q = 34; q < 64; ++q) part[q] = 0.0f;
-    const float tot = wave_multi_sum<64>(part, lane);
-    if (lane < 34) gw_out[e * 34 + lane] = tot;
+    SideEdge<CPL> d;
+    side_load<CPL>(gX0, gX1, gX2, wig, rad, e, so, c, d);
+    side_apply<CPL>(d, e, so, c, v, acc, g_rad, gw_out, lane);
   }
 }
 
@@ -235,8 +267,7 @@ template <int CPL>
 static void launch_gather_fwd(const float* x, const int64_t* idx_i, const int64_t* idx_j, const float* wigner,
                               const float* rad, const float* csd, const int64_t* batch, float* X0, float* X1,
                               float* X2, int64_t E, hipStream_t st) {
-  const int64_t blocks = std::min<int64_t>(cdiv(E, 4), 8192);
-  hipLaunchKernelGGL(gather_fwd_kernel<CPL>, dim3((unsigned)blocks), dim3(256), 0, st, x, idx_i, idx_j, wigner, rad,
+  hipLaunchKernelGGL(gather_fwd_kernel<CPL>, dim3((unsigned)std::min<int64_t>(cdiv(E, 4), 8192)), dim3(256), 0, st, x, idx_i, idx_j, wigner, rad,
                      csd, batch, X0, X1, X2, E);
 }
 

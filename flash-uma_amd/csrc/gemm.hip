@@ -6,18 +6,23 @@
 // pre-transposed weight).  No weight gradients are ever needed: parameters are frozen.
 //
 // Tiling: a 256-thread workgroup (4 wave64s in a 2x2 grid) owns a 128x128 output tile; each
-// wave owns 64x64 = 2x2 MFMA blocks of 32x32 (64 fp32 accumulators per lane).  K advances in
-// chunks of 32 staged through double-buffered LDS.  Within a chunk, lane l (row/col l%32,
-// half h = l/32) feeds the MFMA k-slot h with chunk column 16h + t at step t, so each lane
-// reads its 16 operands of a chunk with four 16-byte LDS reads.
+// wave owns 64x64 = 2x2 MFMA blocks of 32x32 (64 fp32 accumulators per lane, held in AGPRs).
+// K advances in chunks of 16 staged through double-buffered LDS (40 KB, so three workgroups
+// fit on a CU).  Within a chunk, lane l (row/col l%32, half h = l/32) feeds the MFMA k-slot h
+// with chunk column 8h + t at step t, so each lane reads its 8 operands of a chunk with two
+// 16-byte LDS reads.  The epilogue stages each wave's 32-row slabs through LDS and writes
+// bias-added rows with 16-byte stores.
 #include "fu_common.h"
 
 namespace fu {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int GBM = 128, GBN = 128, GBK = 32;
-constexpr int GLDS = GBK + 4;  // padded LDS row (floats) to spread banks
+constexpr int GBM = 128, GBN = 128, GBK = 16;
+constexpr int GLDS = GBK + 4;      // padded LDS operand row (floats)
+constexpr int GES = 64 + 4;        // padded LDS epilogue row (floats)
+constexpr int G_LDS_FLOATS = 2 * (GBM + GBN) * GLDS;
+static_assert(4 * 32 * GES <= G_LDS_FLOATS, "epilogue staging must fit in the operand buffers");
 
 __global__ __launch_bounds__(256) void linear_mfma_kernel(const float* __restrict__ A, int64_t lda,
                                                           const float* __restrict__ W, int64_t ldw,
@@ -25,12 +30,13 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(const float* __restric
                                                           float* __restrict__ Y, int64_t ldy,
                                                           int64_t M, int32_t N, int32_t K,
                                                           int32_t n_tiles, int64_t total_tiles) {
-  __shared__ __attribute__((aligned(16))) float As[2][GBM * GLDS];
-  __shared__ __attribute__((aligned(16))) float Bs[2][GBN * GLDS];
+  __shared__ __attribute__((aligned(16))) float smem[G_LDS_FLOATS];
+  float* As = smem;                      // [2][GBM][GLDS]
+  float* Bs = smem + 2 * GBM * GLDS;     // [2][GBN][GLDS]
 
   // XCD-aware tile order: hardware deals consecutive workgroups round-robin over the 8 XCDs;
-  // remap so that each XCD walks a contiguous range of tiles (tiles sharing an A row-panel
-  // then share that XCD's L2).
+  // remap so that each XCD walks a contiguous range of tiles (the column tiles of one A
+  // row-panel then share that XCD's L2).
   int64_t wg = blockIdx.x;
   if ((total_tiles & 7) == 0) wg = (wg & 7) * (total_tiles >> 3) + (wg >> 3);
   const int64_t m_tile = wg / n_tiles;
@@ -44,14 +50,15 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(const float* __restric
   const int wr = (wave >> 1) * 64;  // wave's row offset inside the tile
   const int wc = (wave & 1) * 64;   // wave's col offset inside the tile
 
-  // Global -> register staging: 4 float4 of A and 4 float4 of W per thread per chunk.
-  float4 ra[4], rb[4];
+  // Global -> register staging: 2 float4 of A and 2 float4 of W per thread per chunk
+  // (4 threads cover the 16 floats of one row).
+  float4 ra[2], rb[2];
   auto load_chunk = [&](int k0) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
+    for (int p = 0; p < 2; ++p) {
       const int lin = tid + 256 * p;
-      const int r = lin >> 3;
-      const int kc = (lin & 7) * 4;
+      const int r = lin >> 2;
+      const int kc = (lin & 3) * 4;
       const int64_t gr = row0 + r;
       const int gk = k0 + kc;
       ra[p] = (gr < M && gk < K) ? ld4(A + gr * lda + gk) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -61,12 +68,12 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(const float* __restric
   };
   auto store_chunk = [&](int buf) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
+    for (int p = 0; p < 2; ++p) {
       const int lin = tid + 256 * p;
-      const int r = lin >> 3;
-      const int kc = (lin & 7) * 4;
-      st4(&As[buf][r * GLDS + kc], ra[p]);
-      st4(&Bs[buf][r * GLDS + kc], rb[p]);
+      const int r = lin >> 2;
+      const int kc = (lin & 3) * 4;
+      st4(&As[(buf * GBM + r) * GLDS + kc], ra[p]);
+      st4(&Bs[(buf * GBN + r) * GLDS + kc], rb[p]);
     }
   };
 
@@ -83,20 +90,20 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(const float* __restric
   store_chunk(0);
   __syncthreads();
 
-  const int fr = lane & 31;        // operand row (A) / column (W) within a 32-block
-  const int fk = (lane >> 5) * 16;  // first chunk column this lane feeds
+  const int fr = lane & 31;         // operand row (A) / column (W) within a 32-block
+  const int fk = (lane >> 5) * 8;   // first chunk column this lane feeds
 
   for (int kc = 0; kc < nk; ++kc) {
     const int buf = kc & 1;
     if (kc + 1 < nk) load_chunk((kc + 1) * GBK);
 
-    float af[2][16], bf[2][16];
+    float af[2][8], bf[2][8];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const float* pa = &As[buf][(wr + i * 32 + fr) * GLDS + fk];
-      const float* pb = &Bs[buf][(wc + i * 32 + fr) * GLDS + fk];
+      const float* pa = &As[(buf * GBM + wr + i * 32 + fr) * GLDS + fk];
+      const float* pb = &Bs[(buf * GBN + wc + i * 32 + fr) * GLDS + fk];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < 2; ++q) {
         const float4 va = ld4(pa + 4 * q);
         const float4 vb = ld4(pb + 4 * q);
         af[i][4 * q + 0] = va.x; af[i][4 * q + 1] = va.y; af[i][4 * q + 2] = va.z; af[i][4 * q + 3] = va.w;
@@ -104,7 +111,7 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(const float* __restric
       }
     }
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
+    for (int t = 0; t < 8; ++t) {
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -112,27 +119,37 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(const float* __restric
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][t], bf[j][t], acc[i][j], 0, 0, 0);
     }
 
-    if (kc + 1 < nk) {
-      store_chunk(buf ^ 1);
-    }
+    if (kc + 1 < nk) store_chunk(buf ^ 1);
     __syncthreads();
   }
 
   // Accumulator layout of the 32x32 MFMA: lane l, register r -> column l%32,
-  // row 8*(r/4) + 4*(l/32) + r%4.
+  // row 8*(r/4) + 4*(l/32) + r%4.  Each wave stages one 32x64 slab at a time in LDS and
+  // writes it back as rows of 16-byte stores.
   const int oc = lane & 31;
   const int orow = (lane >> 5) * 4;
+  float* ws = smem + wave * 32 * GES;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int gc = col0 + wc + j * 32 + oc;
-    if (gc >= N) continue;
-    const float bv = bias ? bias[gc] : 0.0f;
+  for (int i = 0; i < 2; ++i) {
+    __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t gr = row0 + wr + i * 32 + 8 * (r >> 2) + orow + (r & 3);
-        if (gr < M) Y[gr * ldy + gc] = acc[i][j][r] + bv;
+      for (int r = 0; r < 16; ++r) ws[(8 * (r >> 2) + orow + (r & 3)) * GES + j * 32 + oc] = acc[i][j][r];
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int lin = lane + 64 * q;
+      const int r = lin >> 4;
+      const int c = (lin & 15) * 4;
+      const int64_t gr = row0 + wr + i * 32 + r;
+      const int gc = col0 + wc + c;
+      if (gr < M && gc < N) {
+        float4 v = ld4(&ws[r * GES + c]);
+        if (bias) {
+          v.x += bias[gc]; v.y += bias[gc + 1]; v.z += bias[gc + 2]; v.w += bias[gc + 3];
+        }
+        st4(Y + gr * ldy + gc, v);
       }
     }
   }
@@ -149,10 +166,13 @@ extern "C" int fu_linear(const float* A, int64_t lda, const float* W, int64_t ld
   if (K % 4 != 0 || lda % 4 != 0 || ldw % 4 != 0)
     return set_error(FU_ERR_UNSUPPORTED, "fu_linear: K=%d, lda=%lld, ldw=%lld must be multiples of 4",
                      K, (long long)lda, (long long)ldw);
+  if (N % 4 != 0 || ldy % 4 != 0)
+    return set_error(FU_ERR_UNSUPPORTED, "fu_linear: N=%d and ldy=%lld must be multiples of 4", N, (long long)ldy);
   if (lda < K || ldw < K || ldy < N)
     return set_error(FU_ERR_SHAPE, "fu_linear: leading dimensions smaller than the rows");
   if (!A || !W || !Y) return set_error(FU_ERR_NULL, "fu_linear: NULL operand");
-  if (!aligned16(A) || !aligned16(W)) return set_error(FU_ERR_ALIGN, "fu_linear: operands must be 16-byte aligned");
+  if (!aligned16(A) || !aligned16(W) || !aligned16(Y))
+    return set_error(FU_ERR_ALIGN, "fu_linear: operands must be 16-byte aligned");
   if (M == 0) return FU_OK;
   const int n_tiles = (N + GBN - 1) / GBN;
   const int64_t m_tiles = (M + GBM - 1) / GBM;

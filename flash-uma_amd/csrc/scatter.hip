@@ -55,14 +55,8 @@ __global__ __launch_bounds__(256) void scatter_fwd_kernel(const int32_t* __restr
     for (int q = 0; q < CPL; ++q) acc[k][q] = (double)t[q];
   }
   const int32_t k0 = rptr[n], k1 = rptr[n + 1];
-  for (int32_t k = k0; k < k1; ++k) {
-    const int64_t e = col[k];
-    float w[34];
-#pragma unroll
-    for (int q = 0; q < 34; ++q) w[q] = wig[e * 34 + q];
-    const float en = env[e];
-    Vec<CPL> zr[9];
-    load_zr<CPL>(Z0, Z1, Z2, e, c, zr);
+  // one edge's message env * D^T zr, accumulated into the fp64 registers
+  auto accumulate = [&](const float* w, float en, const Vec<CPL>(&zr)[9]) {
 #pragma unroll
     for (int q = 0; q < CPL; ++q) {
       acc[0][q] += (double)(zr[0][q] * en);
@@ -78,6 +72,32 @@ __global__ __launch_bounds__(256) void scatter_fwd_kernel(const int32_t* __restr
         acc[4 + b][q] += (double)(m * en);
       }
     }
+  };
+  int32_t k = k0;
+  // two edges in flight per iteration (their loads overlap); summed in CSR order
+  for (; k + 1 < k1; k += 2) {
+    const int64_t ea = col[k], eb = col[k + 1];
+    float wa[34], wb[34];
+#pragma unroll
+    for (int q = 0; q < 34; ++q) {
+      wa[q] = wig[ea * 34 + q];
+      wb[q] = wig[eb * 34 + q];
+    }
+    const float ena = env[ea], enb = env[eb];
+    Vec<CPL> za[9], zb[9];
+    load_zr<CPL>(Z0, Z1, Z2, ea, c, za);
+    load_zr<CPL>(Z0, Z1, Z2, eb, c, zb);
+    accumulate(wa, ena, za);
+    accumulate(wb, enb, zb);
+  }
+  if (k < k1) {
+    const int64_t e = col[k];
+    float w[34];
+#pragma unroll
+    for (int q = 0; q < 34; ++q) w[q] = wig[e * 34 + q];
+    Vec<CPL> zr[9];
+    load_zr<CPL>(Z0, Z1, Z2, e, c, zr);
+    accumulate(w, env[e], zr);
   }
   float* xo = x_out + n * 9 * C + c;
 #pragma unroll
@@ -293,8 +313,7 @@ template <int CPL>
 static void launch_scatter_bwd(const float* g_out, const int64_t* idx_j, const float* Z0, const float* Z1,
                                const float* Z2, const float* wig, const float* env, float* gZ0, float* gZ1, float* gZ2,
                                float* g_wig, float* g_env, int64_t E, hipStream_t st) {
-  const int64_t blocks = std::min<int64_t>(cdiv(E, 4), 8192);
-  hipLaunchKernelGGL(scatter_bwd_kernel<CPL>, dim3((unsigned)blocks), dim3(256), 0, st, g_out, idx_j, Z0, Z1, Z2, wig,
+  hipLaunchKernelGGL(scatter_bwd_kernel<CPL>, dim3((unsigned)std::min<int64_t>(cdiv(E, 4), 8192)), dim3(256), 0, st, g_out, idx_j, Z0, Z1, Z2, wig,
                      env, gZ0, gZ1, gZ2, g_wig, g_env, E);
 }
 

@@ -161,7 +161,8 @@ int fu_ln_silu_bwd(const float* x, const float* gamma, const float* beta, const 
  * ------------------------------------------------------------------------------------ */
 
 /* Y[M, N] = A[M, K] @ W[N, K]^T (+ bias[N] when non-NULL), fp32 in and out, fp32 MFMA
- * accumulation.  lda/ldw/ldy are row strides in floats.  K must be a multiple of 4. */
+ * accumulation.  lda/ldw/ldy are row strides in floats; K, N, lda, ldw and ldy must be
+ * multiples of 4 and A, W, Y 16-byte aligned. */
 int fu_linear(const float* A, int64_t lda, const float* W, int64_t ldw, const float* bias,
               float* Y, int64_t ldy, int64_t M, int32_t N, int32_t K, void* stream);
 
