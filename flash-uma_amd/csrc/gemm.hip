@@ -24,12 +24,21 @@ constexpr int GES = 64 + 4;        // padded LDS epilogue row (floats)
 constexpr int G_LDS_FLOATS = 2 * (GBM + GBN) * GLDS;
 static_assert(4 * 32 * GES <= G_LDS_FLOATS, "epilogue staging must fit in the operand buffers");
 
-__global__ __launch_bounds__(256) void linear_mfma_kernel(const float* __restrict__ A, int64_t lda,
-                                                          const float* __restrict__ W, int64_t ldw,
-                                                          const float* __restrict__ bias,
-                                                          float* __restrict__ Y, int64_t ldy,
-                                                          int64_t M, int32_t N, int32_t K,
+// Batch index blockIdx.y offsets A, W and Y by sA, sW and sY floats; bias (stride sBias) is
+// added in batches [0, bias_batches).
+__global__ __launch_bounds__(256) void linear_mfma_kernel(const float* __restrict__ A, int64_t lda, int64_t sA,
+                                                          const float* __restrict__ W, int64_t ldw, int64_t sW,
+                                                          const float* __restrict__ bias, int64_t sBias,
+                                                          int32_t bias_batches, float* __restrict__ Y, int64_t ldy,
+                                                          int64_t sY, int64_t M, int32_t N, int32_t K,
                                                           int32_t n_tiles, int64_t total_tiles) {
+  {
+    const int64_t bt = blockIdx.y;
+    A += bt * sA;
+    W += bt * sW;
+    Y += bt * sY;
+    bias = (bias != nullptr && bt < bias_batches) ? bias + bt * sBias : nullptr;
+  }
   __shared__ __attribute__((aligned(16))) float smem[G_LDS_FLOATS];
   float* As = smem;                      // [2][GBM][GLDS]
   float* Bs = smem + 2 * GBM * GLDS;     // [2][GBN][GLDS]
@@ -159,26 +168,52 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(const float* __restric
 
 using namespace fu;
 
-extern "C" int fu_linear(const float* A, int64_t lda, const float* W, int64_t ldw, const float* bias,
-                         float* Y, int64_t ldy, int64_t M, int32_t N, int32_t K, void* stream) {
+static int linear_check(const float* A, int64_t lda, const float* W, int64_t ldw, const float* Y, int64_t ldy,
+                        int64_t M, int32_t N, int32_t K, const char* who) {
   if (M < 0 || N <= 0 || K <= 0)
-    return set_error(FU_ERR_SHAPE, "fu_linear: bad shape M=%lld N=%d K=%d", (long long)M, N, K);
+    return set_error(FU_ERR_SHAPE, "%s: bad shape M=%lld N=%d K=%d", who, (long long)M, N, K);
   if (K % 4 != 0 || lda % 4 != 0 || ldw % 4 != 0)
-    return set_error(FU_ERR_UNSUPPORTED, "fu_linear: K=%d, lda=%lld, ldw=%lld must be multiples of 4",
-                     K, (long long)lda, (long long)ldw);
+    return set_error(FU_ERR_UNSUPPORTED, "%s: K=%d, lda=%lld, ldw=%lld must be multiples of 4", who, K,
+                     (long long)lda, (long long)ldw);
   if (N % 4 != 0 || ldy % 4 != 0)
-    return set_error(FU_ERR_UNSUPPORTED, "fu_linear: N=%d and ldy=%lld must be multiples of 4", N, (long long)ldy);
-  if (lda < K || ldw < K || ldy < N)
-    return set_error(FU_ERR_SHAPE, "fu_linear: leading dimensions smaller than the rows");
-  if (!A || !W || !Y) return set_error(FU_ERR_NULL, "fu_linear: NULL operand");
+    return set_error(FU_ERR_UNSUPPORTED, "%s: N=%d and ldy=%lld must be multiples of 4", who, N, (long long)ldy);
+  if (lda < K || ldw < K || ldy < N) return set_error(FU_ERR_SHAPE, "%s: leading dimensions smaller than the rows", who);
+  if (!A || !W || !Y) return set_error(FU_ERR_NULL, "%s: NULL operand", who);
   if (!aligned16(A) || !aligned16(W) || !aligned16(Y))
-    return set_error(FU_ERR_ALIGN, "fu_linear: operands must be 16-byte aligned");
-  if (M == 0) return FU_OK;
+    return set_error(FU_ERR_ALIGN, "%s: operands must be 16-byte aligned", who);
+  return FU_OK;
+}
+
+static int linear_launch(const float* A, int64_t lda, int64_t sA, const float* W, int64_t ldw, int64_t sW,
+                         const float* bias, int64_t sBias, int32_t bias_batches, float* Y, int64_t ldy, int64_t sY,
+                         int64_t M, int32_t N, int32_t K, int32_t batch, hipStream_t stream, const char* who) {
   const int n_tiles = (N + GBN - 1) / GBN;
   const int64_t m_tiles = (M + GBM - 1) / GBM;
   const int64_t total = m_tiles * n_tiles;
-  if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "fu_linear: M too large");
-  hipLaunchKernelGGL(linear_mfma_kernel, dim3((unsigned)total), dim3(256), 0, as_stream(stream), A, lda,
-                     W, ldw, bias, Y, ldy, M, N, K, n_tiles, total);
-  return check_launch("fu_linear");
+  if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
+  hipLaunchKernelGGL(linear_mfma_kernel, dim3((unsigned)total, (unsigned)batch), dim3(256), 0, stream, A, lda, sA, W,
+                     ldw, sW, bias, sBias, bias_batches, Y, ldy, sY, M, N, K, n_tiles, total);
+  return check_launch(who);
+}
+
+extern "C" int fu_linear(const float* A, int64_t lda, const float* W, int64_t ldw, const float* bias, float* Y,
+                         int64_t ldy, int64_t M, int32_t N, int32_t K, void* stream) {
+  int st = linear_check(A, lda, W, ldw, Y, ldy, M, N, K, "fu_linear");
+  if (st != FU_OK) return st;
+  if (M == 0) return FU_OK;
+  return linear_launch(A, lda, 0, W, ldw, 0, bias, 0, 1, Y, ldy, 0, M, N, K, 1, as_stream(stream), "fu_linear");
+}
+
+extern "C" int fu_linear_batched(const float* A, int64_t lda, int64_t stride_a, const float* W, int64_t ldw,
+                                 int64_t stride_w, const float* bias, int64_t stride_bias, int32_t bias_batches,
+                                 float* Y, int64_t ldy, int64_t stride_y, int64_t M, int32_t N, int32_t K,
+                                 int32_t batch, void* stream) {
+  int st = linear_check(A, lda, W, ldw, Y, ldy, M, N, K, "fu_linear_batched");
+  if (st != FU_OK) return st;
+  if (batch < 1 || batch > 65535) return set_error(FU_ERR_SHAPE, "fu_linear_batched: batch=%d out of range", batch);
+  if ((stride_a | stride_w | stride_y) % 4 != 0 || stride_a < 0 || stride_w < 0 || stride_y < 0)
+    return set_error(FU_ERR_ALIGN, "fu_linear_batched: batch strides must be non-negative multiples of 4");
+  if (M == 0) return FU_OK;
+  return linear_launch(A, lda, stride_a, W, ldw, stride_w, bias, stride_bias, bias_batches, Y, ldy, stride_y, M, N, K,
+                       batch, as_stream(stream), "fu_linear_batched");
 }

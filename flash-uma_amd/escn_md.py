@@ -9,8 +9,9 @@ reference (norm_1, norm_2, atom_wise, final norm, charge/spin embeddings).
 
 The node modules restate the FAIRChem designs from memory; their parity is unpinned (no
 reference code or fixtures exist here), so they are checked only by invariants (rotation
-equivariance, normalisation).  They run as torch modules on the GPU, outside the HIP hot
-path, exactly as the reference runs FAIRChem's modules in torch eager.
+equivariance, normalisation).  Their forward passes run on the gfx950 node kernels
+(ops/node.py: RMS norm, batched per-degree MFMA GEMM, gate activation); like the rest of
+the backbone they need GPU tensors.
 
 Initialisation (seeded CPU torch.Generator, fixed creation order): nn.Linear default
 (kaiming-uniform weights, uniform bias), nn.Embedding N(0, 1), LayerNorm/affine weights 1,
@@ -24,6 +25,9 @@ from types import SimpleNamespace
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
+
+from ops.linear import linear
+from ops.node import gate_act, rms_norm_sh, so3_linear
 
 
 def num_coefficients(lmax: int) -> int:
@@ -55,17 +59,7 @@ class EquivariantRMSNormArraySphericalHarmonicsV2(nn.Module):
         self.register_buffer("balance_degree_weight", bal / (lmax + 1), persistent=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        l0 = x.narrow(1, 0, 1)
-        l0 = l0 - l0.mean(dim=2, keepdim=True)
-        feat = torch.cat([l0, x.narrow(1, 1, x.shape[1] - 1)], dim=1)
-        norm = (feat.pow(2) * self.balance_degree_weight.unsqueeze(0)).sum(dim=1, keepdim=True)
-        norm = norm.mean(dim=2, keepdim=True)
-        norm = (norm + self.eps).pow(-0.5)
-        w = self.affine_weight.index_select(0, self.expand_index).unsqueeze(0)
-        out = feat * (norm * w)
-        bias = torch.zeros_like(out[:1])
-        bias[:, 0, :] = self.affine_bias
-        return out + bias
+        return rms_norm_sh(x, self.affine_weight, self.affine_bias, self.lmax, self.eps)
 
 
 class SO3_Linear(nn.Module):
@@ -80,11 +74,15 @@ class SO3_Linear(nn.Module):
         self.bias = nn.Parameter(torch.empty(out_features).uniform_(-bound, bound, generator=generator))
         self.register_buffer("expand_index", degree_index(lmax), persistent=False)
 
+    def per_coefficient_weights(self):
+        """(W_k, W_k^T) stacked over the (lmax+1)^2 coefficients (weights are frozen)."""
+        w = self.weight.detach().index_select(0, self.expand_index).contiguous()
+        return w, w.transpose(1, 2).contiguous()
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        w = self.weight.index_select(0, self.expand_index)          # (K, out, in)
-        out = torch.einsum("nki,koi->nko", x, w)
-        out[:, 0, :] = out[:, 0, :] + self.bias
-        return out
+        if getattr(self, "_wk", None) is None or self._wk[0].device != x.device:
+            self._wk = self.per_coefficient_weights()
+        return so3_linear(x, self._wk[0], self._wk[1], self.bias.detach())
 
 
 class GateActivation(nn.Module):
@@ -96,10 +94,11 @@ class GateActivation(nn.Module):
         self.num_channels = num_channels
         self.register_buffer("gate_index", (degree_index(lmax)[1:] - 1), persistent=False)
 
-    def forward(self, gating_scalars: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
-        gates = torch.sigmoid(gating_scalars).view(-1, self.lmax, self.num_channels)
-        gates = gates.index_select(1, self.gate_index)
-        return torch.cat([F.silu(x.narrow(1, 0, 1)), x.narrow(1, 1, x.shape[1] - 1) * gates], dim=1)
+    def forward(self, pre: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+        """pre: the scalar MLP's pre-activation (N, lmax * H); the gate is
+        sigmoid(silu(pre)) per degree (FAIRChem applies SiLU in the scalar MLP and the
+        sigmoid here)."""
+        return gate_act(pre, x, self.lmax)
 
 
 class SpectralAtomwise(nn.Module):
@@ -113,9 +112,12 @@ class SpectralAtomwise(nn.Module):
         self.so3_linear_2 = SO3_Linear(hidden_channels, sphere_channels, lmax, generator)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        gates = self.scalar_mlp(x.narrow(1, 0, 1)).squeeze(1)
+        lin = self.scalar_mlp[0]
+        if getattr(self, "_wt", None) is None or self._wt.device != x.device:
+            self._wt = lin.weight.detach().t().contiguous()
+        pre = linear(x[:, 0, :], lin.weight.detach(), lin.bias.detach(), self._wt)
         h = self.so3_linear_1(x)
-        h = self.act(gates, h)
+        h = self.act(pre, h)
         return self.so3_linear_2(h)
 
 

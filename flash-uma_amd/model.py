@@ -4,7 +4,8 @@ Public names and signatures follow the reference: reorder_graph_morton, build_cs
 clear_csr_cache (model.py:17-74), Packed_eSCN_Layer (model.py:81-157) and
 eSCN_Inference_Model (model.py:160-221).  Every per-edge and per-CSR operation runs in
 libflashuma_hip.so; the node-level FAIRChem modules attached by transfer_weights (norm_1,
-norm_2, atom_wise, final_norm) run as the torch modules they are.
+norm_2, atom_wise, final_norm) are called as given (the stand-ins in escn_md.py run on the
+node kernels of ops/node.py).
 
 Differences in mechanism (not in results):
   - the graph topology (Morton order, receiver-sorted edge order, receiver and sender CSRs)
@@ -24,6 +25,7 @@ from ops.gating import fused_gating_split
 from ops.geom import precompute_geometry
 from ops.linear import linear
 from ops.ln_silu import layer_norm_silu
+from ops.node import permute_rows
 from ops.scatter import init_node_scatter, rotate_scatter_split
 from ops.topology import (clear_topology_cache, get_topology, morton_permutation, receiver_csr, take)
 
@@ -199,10 +201,10 @@ class eSCN_Inference_Model(nn.Module):
     def forward(self, pos, Z, batch, edge_index, shifts, csd_emb, charge=None, spin=None, natoms=None):
         # 1. Topology (Morton order + receiver-sorted edges + both CSRs), cached per graph
         topo = get_topology(pos, batch, edge_index)
-        pos_s = pos[topo.perm]
-        Z_s = Z[topo.perm]
-        batch_s = batch[topo.perm]
-        shifts_s = shifts[topo.edge_perm]
+        pos_s = permute_rows(pos, topo.perm)
+        Z_s = take(Z.contiguous(), topo.perm)
+        batch_s = take(batch.contiguous(), topo.perm)
+        shifts_s = permute_rows(shifts, topo.edge_perm)
         idx_i_s, idx_j_s = topo.idx_i, topo.idx_j
         row_ptr, col_idx = topo.recv_ptr, topo.recv_idx
         N = pos_s.shape[0]
@@ -224,4 +226,4 @@ class eSCN_Inference_Model(nn.Module):
                     "charge/spin channel balancing (FAIRChem balance_channels_batched) is not available")
         x_node_s = self.final_norm(x_node_s)
         # 5. Back to the input atom order
-        return x_node_s[topo.inv_perm]
+        return permute_rows(x_node_s, topo.inv_perm)

@@ -39,6 +39,15 @@ SIGNATURES: dict[str, list] = {
     "fu_ln_silu_fwd": [P, P, P, P, P, P, I64, I32, F32, P],
     "fu_ln_silu_bwd": [P, P, P, P, P, P, P, I64, I32, P],
     "fu_linear": [P, I64, P, I64, P, P, I64, I64, I32, I32, P],
+    "fu_linear_batched": [P, I64, I64, P, I64, I64, P, I64, I32, P, I64, I64, I64, I32, I32, I32, P],
+    "fu_rms_norm_sh_fwd": [P, P, P, P, P, I64, I32, I32, F32, P],
+    "fu_rms_norm_sh_bwd": [P, P, P, P, P, I64, I32, I32, P],
+    "fu_gate_act_fwd": [P, P, P, I64, I32, I32, P],
+    "fu_gate_act_bwd": [P, P, P, P, P, I64, I32, I32, P],
+    "fu_gather_rows": [P, P, P, I64, I32, P],
+    "fu_scatter_rows": [P, P, P, I64, I32, P],
+    "fu_edge_shifts": [P, P, P, P, I64, P],
+    "fu_outer_sum3": [P, P, P, P, P, I64, I64, P],
     "fu_morton_keys": [P, P, P, I64, P],
     "fu_sort_pairs_i64": [P, P, P, P, I64, I32, I32, P, SZ_P, P],
     "fu_invert_perm": [P, P, I64, P],

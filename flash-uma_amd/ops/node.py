@@ -1,0 +1,164 @@
+"""Node-level ops on the gfx950 kernels: the equivariant RMS norm over SH coefficients, the
+per-degree SO(3) linear and the gate activation of the atom-wise FFN (the FAIRChem modules
+the reference attaches to each block, model.py:145,157,218), plus row permutations and the
+PBC shift product used around the hot path (model.py:72-74,221; wrapper.py:193-194).
+
+All parameters are frozen: backward passes return input gradients only."""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+class RmsNormSH(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, bias, lmax, eps):
+        x = _lib.require(x, torch.float32, "x")
+        weight = _lib.require(weight, torch.float32, "weight")
+        bias = _lib.require(bias, torch.float32, "bias")
+        N, _, C = x.shape
+        out = torch.empty_like(x)
+        inv = torch.empty(N, device=x.device, dtype=torch.float32)
+        _lib.call("fu_rms_norm_sh_fwd", x.data_ptr(), weight.data_ptr(), bias.data_ptr(), out.data_ptr(),
+                  inv.data_ptr(), N, C, lmax, float(eps), _lib.stream_ptr(x.device))
+        ctx.save_for_backward(x, weight, inv)
+        ctx.lmax = lmax
+        return out
+
+    @staticmethod
+    def backward(ctx, g_out):
+        x, weight, inv = ctx.saved_tensors
+        N, _, C = x.shape
+        g_out = g_out.contiguous()
+        g_x = torch.empty_like(x)
+        _lib.call("fu_rms_norm_sh_bwd", x.data_ptr(), weight.data_ptr(), inv.data_ptr(), g_out.data_ptr(),
+                  g_x.data_ptr(), N, C, ctx.lmax, _lib.stream_ptr(x.device))
+        return g_x, None, None, None, None
+
+
+def rms_norm_sh(x, weight, bias, lmax: int, eps: float):
+    return RmsNormSH.apply(x, weight, bias, lmax, eps)
+
+
+def _so3_apply(x: torch.Tensor, Wk: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+    """y[:, k] = x[:, k] @ Wk[k]^T (+ bias on k = 0) as one batched MFMA GEMM over k."""
+    N, K9, Cin = x.shape
+    Cout = Wk.shape[1]
+    y = torch.empty(N, K9, Cout, device=x.device, dtype=torch.float32)
+    _lib.call("fu_linear_batched", x.data_ptr(), K9 * Cin, Cin, Wk.data_ptr(), Cin, Cout * Cin,
+              None if bias is None else bias.data_ptr(), 0, 1, y.data_ptr(), K9 * Cout, Cout, N, Cout, Cin, K9,
+              _lib.stream_ptr(x.device))
+    return y
+
+
+class So3Linear(torch.autograd.Function):
+    """x (N, K, Cin) -> (N, K, Cout) with a weight per coefficient k: W_k (Cout, Cin)
+    (the weight of k's degree), bias on k = 0.  Wt_k = W_k^T for the input gradient."""
+
+    @staticmethod
+    def forward(ctx, x, Wk, Wtk, bias):
+        x = _lib.require(x, torch.float32, "x")
+        ctx.save_for_backward(Wtk)
+        return _so3_apply(x, Wk, bias)
+
+    @staticmethod
+    def backward(ctx, g_y):
+        (Wtk,) = ctx.saved_tensors
+        return _so3_apply(g_y.contiguous(), Wtk, None), None, None, None
+
+
+def so3_linear(x, Wk, Wtk, bias):
+    return So3Linear.apply(x, Wk, Wtk, bias)
+
+
+class GateAct(torch.autograd.Function):
+    """gate_l = sigmoid(silu(pre_l)); out_0 = silu(h_0); out_k = h_k gate_{l_k}."""
+
+    @staticmethod
+    def forward(ctx, pre, h, lmax):
+        pre = _lib.require(pre, torch.float32, "pre")
+        h = _lib.require(h, torch.float32, "h")
+        out = torch.empty_like(h)
+        N, _, H = h.shape
+        _lib.call("fu_gate_act_fwd", pre.data_ptr(), h.data_ptr(), out.data_ptr(), N, H, lmax,
+                  _lib.stream_ptr(h.device))
+        ctx.save_for_backward(pre, h)
+        ctx.lmax = lmax
+        return out
+
+    @staticmethod
+    def backward(ctx, g_out):
+        pre, h = ctx.saved_tensors
+        N, _, H = h.shape
+        g_out = g_out.contiguous()
+        g_pre = torch.empty_like(pre)
+        g_h = torch.empty_like(h)
+        _lib.call("fu_gate_act_bwd", pre.data_ptr(), h.data_ptr(), g_out.data_ptr(), g_pre.data_ptr(), g_h.data_ptr(),
+                  N, H, ctx.lmax, _lib.stream_ptr(h.device))
+        return g_pre, g_h, None
+
+
+def gate_act(pre, h, lmax: int):
+    return GateAct.apply(pre, h, lmax)
+
+
+class PermuteRows(torch.autograd.Function):
+    """out[r] = src[perm[r]] for a permutation perm; the backward scatters rows back
+    (each row once: no accumulation, deterministic)."""
+
+    @staticmethod
+    def forward(ctx, src, perm):
+        src = _lib.require(src, torch.float32, "src")
+        rows = perm.numel()
+        width = src[0].numel() if src.shape[0] else 1
+        out = torch.empty((rows,) + tuple(src.shape[1:]), device=src.device, dtype=torch.float32)
+        _lib.call("fu_gather_rows", src.data_ptr(), perm.data_ptr(), out.data_ptr(), rows, width,
+                  _lib.stream_ptr(src.device))
+        ctx.save_for_backward(perm)
+        ctx.width = width
+        return out
+
+    @staticmethod
+    def backward(ctx, g_out):
+        (perm,) = ctx.saved_tensors
+        g_out = g_out.contiguous()
+        g_src = torch.empty_like(g_out)
+        _lib.call("fu_scatter_rows", g_out.data_ptr(), perm.data_ptr(), g_src.data_ptr(), perm.numel(), ctx.width,
+                  _lib.stream_ptr(g_out.device))
+        return g_src, None
+
+
+def permute_rows(src, perm):
+    return PermuteRows.apply(src, perm)
+
+
+class EdgeShifts(torch.autograd.Function):
+    """shifts = cell_offsets @ cell for one system; dE/dcell = cell_offsets^T dE/dshifts,
+    reduced deterministically in fp64."""
+
+    @staticmethod
+    def forward(ctx, cell_offsets, cell):
+        off = _lib.require(cell_offsets, torch.float32, "cell_offsets")
+        c = _lib.require(cell.reshape(3, 3), torch.float32, "cell")
+        E = off.shape[0]
+        shifts = torch.empty(E, 3, device=off.device, dtype=torch.float32)
+        _lib.call("fu_edge_shifts", off.data_ptr(), c.data_ptr(), None, shifts.data_ptr(), E,
+                  _lib.stream_ptr(off.device))
+        ctx.save_for_backward(off)
+        ctx.cell_shape = cell.shape
+        return shifts
+
+    @staticmethod
+    def backward(ctx, g_shifts):
+        (off,) = ctx.saved_tensors
+        g_shifts = g_shifts.contiguous()
+        g_cell = torch.empty(3, 3, device=off.device, dtype=torch.float32)
+        partial = torch.empty(256 * 9, device=off.device, dtype=torch.float64)
+        _lib.call("fu_outer_sum3", off.data_ptr(), None, g_shifts.data_ptr(), g_cell.data_ptr(), partial.data_ptr(),
+                  partial.numel(), off.shape[0], _lib.stream_ptr(off.device))
+        return None, g_cell.reshape(ctx.cell_shape)
+
+
+def edge_shifts(cell_offsets, cell):
+    return EdgeShifts.apply(cell_offsets, cell)

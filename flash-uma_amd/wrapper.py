@@ -11,6 +11,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from model import eSCN_Inference_Model
+from ops.node import edge_shifts
 
 
 @torch.no_grad()
@@ -140,7 +141,7 @@ class ZeroAllocBackbone(nn.Module):
         csd_mixed_emb = self.csd_embedding(charge=data.charge, spin=data.spin,
                                            dataset=getattr(data, "dataset", None))
         if len(data.natoms) == 1:
-            shifts = data.cell_offsets.to(data.cell.dtype) @ data.cell.squeeze(0)
+            shifts = edge_shifts(data.cell_offsets, data.cell)
         else:
             cell_per_edge = data.cell.repeat_interleave(data.nedges, dim=0)
             shifts = torch.einsum("ij,ijk->ik", data.cell_offsets.to(cell_per_edge.dtype), cell_per_edge)

@@ -166,6 +166,54 @@ int fu_ln_silu_bwd(const float* x, const float* gamma, const float* beta, const 
 int fu_linear(const float* A, int64_t lda, const float* W, int64_t ldw, const float* bias,
               float* Y, int64_t ldy, int64_t M, int32_t N, int32_t K, void* stream);
 
+/* Strided batch of fu_linear in one launch: for b < batch,
+ * Y_b = A_b @ W_b^T (+ bias_b for b < bias_batches), X_b = X + b * stride_x (floats).
+ * Used for the per-degree SO(3) linears of the atom-wise FFN (W_b = the weight of the
+ * degree of coefficient b, bias on l = 0 only). */
+int fu_linear_batched(const float* A, int64_t lda, int64_t stride_a, const float* W, int64_t ldw,
+                      int64_t stride_w, const float* bias, int64_t stride_bias, int32_t bias_batches,
+                      float* Y, int64_t ldy, int64_t stride_y, int64_t M, int32_t N, int32_t K,
+                      int32_t batch, void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * Node-level modules attached to the backbone (model.py:145,157,218) and input plumbing
+ * ------------------------------------------------------------------------------------ */
+
+/* Equivariant RMS norm over SH coefficients (FAIRChem rms_norm_sh, the norm_1 / norm_2 /
+ * final norm of model.py:145,157,218): l=0 centred over channels, scaled by
+ * (mean_c sum_k x_kc^2 / ((2 l_k + 1)(lmax + 1)) + eps)^-1/2, per-(l, c) weight, l=0 bias.
+ * x, out (N, 9, C); weight (lmax + 1, C); bias (C); inv_rms (N) is saved for the backward. */
+int fu_rms_norm_sh_fwd(const float* x, const float* weight, const float* bias, float* out,
+                       float* inv_rms, int64_t N, int32_t C, int32_t lmax, float eps, void* stream);
+int fu_rms_norm_sh_bwd(const float* x, const float* weight, const float* inv_rms,
+                       const float* g_out, float* g_x, int64_t N, int32_t C, int32_t lmax,
+                       void* stream);
+
+/* Gate activation of the atom-wise FFN: gate_l = sigmoid(silu(pre[:, l-1])) for l >= 1,
+ * out_0 = silu(h_0), out_k = h_k * gate_{l_k}.  pre (N, lmax * H), h and out (N, 9, H). */
+int fu_gate_act_fwd(const float* pre, const float* h, float* out, int64_t N, int32_t H,
+                    int32_t lmax, void* stream);
+int fu_gate_act_bwd(const float* pre, const float* h, const float* g_out, float* g_pre,
+                    float* g_h, int64_t N, int32_t H, int32_t lmax, void* stream);
+
+/* Row permutations (model.py:72-74,221): gather dst[r] = src[idx[r]]; scatter
+ * dst[idx[r]] = src[r] (idx a permutation, each destination row written once). */
+int fu_gather_rows(const float* src, const int64_t* idx, float* dst, int64_t rows, int32_t width,
+                   void* stream);
+int fu_scatter_rows(const float* src, const int64_t* idx, float* dst, int64_t rows,
+                    int32_t width, void* stream);
+
+/* PBC shifts (wrapper.py:193-194): shifts[e] = cell_offsets[perm[e]] @ cell for a single
+ * system (perm NULL = identity). */
+int fu_edge_shifts(const float* cell_offsets, const float* cell, const int64_t* perm,
+                   float* shifts, int64_t E, void* stream);
+
+/* out (3x3) = sum_e A[perm_a[e]]^T B[e] over E rows of 3 (perm_a NULL = identity), in fp64
+ * with a fixed two-stage order (deterministic); the cell gradient of the shifts product.
+ * partial is a workspace of at least 256 * 9 doubles. */
+int fu_outer_sum3(const float* A, const int64_t* perm_a, const float* B, float* out,
+                  double* partial, int64_t partial_len, int64_t E, void* stream);
+
 /* ------------------------------------------------------------------------------------
  * Graph preprocessing (replaces reorder_graph_morton / _build_csr_uncached, model.py:20-74)
  * ------------------------------------------------------------------------------------ */
