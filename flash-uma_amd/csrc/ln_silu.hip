@@ -1,8 +1,15 @@
 // Row LayerNorm (biased variance) + affine + SiLU and its input gradient
 // (ops/ln_silu.py:29-123), for the radial-MLP hidden rows (D = edge channels).
 //
-// LPR = D/4 lanes own one row (4 consecutive floats per lane, one float4 access), so a
-// wave64 covers 64/LPR rows; row statistics are butterfly sums within the LPR-lane group.
+// General ("grouped") form: a row of the input matrix holds G groups of D values; group g of
+// row e is normalised on its own, with its own gamma/beta/bias, after adding optional
+// per-element table rows tab_src[z[isrc[e]]] and tab_dst[z[idst[e]]] (z = atomic numbers,
+// isrc/idst = edge endpoints).  This lets the first radial
+// layer of all blocks run as one GEMM over the Gaussian basis while the element-embedding
+// part of that layer (W1[:, B:] [W_src[Z_i]; W_tgt[Z_j]]) comes from precomputed tables.
+//
+// LPR = D/4 lanes own one (row, group) (4 consecutive floats per lane, one float4 access), so
+// a wave64 covers 64/LPR of them; statistics are butterfly sums within the LPR-lane group.
 #include "fu_common.h"
 
 namespace fu {
@@ -14,32 +21,55 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+struct LnArgs {
+  const float* x; int64_t ldx;
+  const float* tab_src; const float* tab_dst; int64_t ldt;
+  const int64_t* z; const int64_t* isrc; const int64_t* idst;
+  const float* bias; const float* gamma; const float* beta;
+  int64_t M; int32_t G;
+};
+
+// x + tables + bias for the 4 values of this lane in (row, group)
+template <int D>
+__device__ __forceinline__ float4 ln_input(const LnArgs& a, int64_t row, int g, int sub) {
+  const int col = g * D + 4 * sub;
+  float4 v = ld4(a.x + row * a.ldx + col);
+  if (a.tab_src != nullptr) {
+    v = v + ld4(a.tab_src + a.z[a.isrc[row]] * a.ldt + col);
+    v = v + ld4(a.tab_dst + a.z[a.idst[row]] * a.ldt + col);
+  }
+  if (a.bias != nullptr) v = v + ld4(a.bias + col);
+  return v;
+}
+
 template <int LPR>
-__global__ __launch_bounds__(256) void ln_silu_fwd_kernel(const float* __restrict__ x, const float* __restrict__ gamma,
-                                                          const float* __restrict__ beta, float* __restrict__ out,
+__global__ __launch_bounds__(256) void ln_silu_fwd_kernel(LnArgs a, float* __restrict__ out, int64_t ldo,
                                                           float* __restrict__ mean_out, float* __restrict__ rstd_out,
-                                                          int64_t M, float eps) {
+                                                          float eps) {
   constexpr int D = 4 * LPR;
-  constexpr int RPB = 256 / LPR;  // rows per block
+  constexpr int RPB = 256 / LPR;  // (row, group) items per block
   const int sub = threadIdx.x % LPR;
-  const int64_t rows_step = (int64_t)gridDim.x * RPB;
-  const float4 g = ld4(gamma + 4 * sub), b = ld4(beta + 4 * sub);
-  for (int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR; row < M; row += rows_step) {
-    const float4 v = ld4(x + row * D + 4 * sub);
+  const int64_t items = a.M * a.G;
+  const int64_t step = (int64_t)gridDim.x * RPB;
+  for (int64_t it = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR; it < items; it += step) {
+    const int64_t row = it / a.G;
+    const int g = (int)(it - row * a.G);
+    const float4 v = ln_input<D>(a, row, g, sub);
     const float mean = group_sum<LPR>(v.x + v.y + v.z + v.w) / D;
     const float4 xc = make_float4(v.x - mean, v.y - mean, v.z - mean, v.w - mean);
     const float var = group_sum<LPR>(xc.x * xc.x + xc.y * xc.y + xc.z * xc.z + xc.w * xc.w) / D;
     const float rstd = 1.0f / sqrtf(var + eps);
+    const float4 gm = ld4(a.gamma + g * D + 4 * sub), bt = ld4(a.beta + g * D + 4 * sub);
     float4 y;
-    y.x = xc.x * rstd * g.x + b.x;
-    y.y = xc.y * rstd * g.y + b.y;
-    y.z = xc.z * rstd * g.z + b.z;
-    y.w = xc.w * rstd * g.w + b.w;
-    st4(out + row * D + 4 * sub,
+    y.x = xc.x * rstd * gm.x + bt.x;
+    y.y = xc.y * rstd * gm.y + bt.y;
+    y.z = xc.z * rstd * gm.z + bt.z;
+    y.w = xc.w * rstd * gm.w + bt.w;
+    st4(out + row * ldo + g * D + 4 * sub,
         make_float4(y.x * sigmoidf_(y.x), y.y * sigmoidf_(y.y), y.z * sigmoidf_(y.z), y.w * sigmoidf_(y.w)));
     if (sub == 0) {
-      mean_out[row] = mean;
-      rstd_out[row] = rstd;
+      mean_out[it] = mean;
+      rstd_out[it] = rstd;
     }
   }
 }
@@ -50,23 +80,24 @@ __device__ __forceinline__ float dsilu(float y) {
 }
 
 template <int LPR>
-__global__ __launch_bounds__(256) void ln_silu_bwd_kernel(const float* __restrict__ x, const float* __restrict__ gamma,
-                                                          const float* __restrict__ beta,
-                                                          const float* __restrict__ mean_in,
+__global__ __launch_bounds__(256) void ln_silu_bwd_kernel(LnArgs a, const float* __restrict__ mean_in,
                                                           const float* __restrict__ rstd_in,
-                                                          const float* __restrict__ g_out, float* __restrict__ g_x,
-                                                          int64_t M) {
+                                                          const float* __restrict__ g_out, int64_t ldg,
+                                                          float* __restrict__ g_x, int64_t ldgx) {
   constexpr int D = 4 * LPR;
   constexpr int RPB = 256 / LPR;
   const int sub = threadIdx.x % LPR;
-  const int64_t rows_step = (int64_t)gridDim.x * RPB;
-  const float4 g = ld4(gamma + 4 * sub), b = ld4(beta + 4 * sub);
-  for (int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR; row < M; row += rows_step) {
-    const float4 v = ld4(x + row * D + 4 * sub);
-    const float4 go = ld4(g_out + row * D + 4 * sub);
-    const float mean = mean_in[row], rstd = rstd_in[row];
+  const int64_t items = a.M * a.G;
+  const int64_t step = (int64_t)gridDim.x * RPB;
+  for (int64_t it = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR; it < items; it += step) {
+    const int64_t row = it / a.G;
+    const int g = (int)(it - row * a.G);
+    const float4 v = ln_input<D>(a, row, g, sub);
+    const float4 go = ld4(g_out + row * ldg + g * D + 4 * sub);
+    const float4 gm = ld4(a.gamma + g * D + 4 * sub), bt = ld4(a.beta + g * D + 4 * sub);
+    const float mean = mean_in[it], rstd = rstd_in[it];
     const float xh[4] = {(v.x - mean) * rstd, (v.y - mean) * rstd, (v.z - mean) * rstd, (v.w - mean) * rstd};
-    const float gg[4] = {g.x, g.y, g.z, g.w}, bb[4] = {b.x, b.y, b.z, b.w}, gov[4] = {go.x, go.y, go.z, go.w};
+    const float gg[4] = {gm.x, gm.y, gm.z, gm.w}, bb[4] = {bt.x, bt.y, bt.z, bt.w}, gov[4] = {go.x, go.y, go.z, go.w};
     float gxh[4];
     float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
@@ -83,44 +114,92 @@ __global__ __launch_bounds__(256) void ln_silu_bwd_kernel(const float* __restric
     o.y = rstd * (gxh[1] - (s1 + xh[1] * s2) / D);
     o.z = rstd * (gxh[2] - (s1 + xh[2] * s2) / D);
     o.w = rstd * (gxh[3] - (s1 + xh[3] * s2) / D);
-    st4(g_x + row * D + 4 * sub, o);
+    st4(g_x + row * ldgx + g * D + 4 * sub, o);
   }
+}
+
+static unsigned ln_blocks(int64_t items, int D) {
+  const int rpb = 256 / (D / 4);
+  return (unsigned)std::min<int64_t>(cdiv(items, rpb), 65536);
+}
+
+static int ln_check(const LnArgs& a, int64_t ld_out, int32_t D, const char* who) {
+  if (a.M < 0 || a.G < 1) return set_error(FU_ERR_SHAPE, "%s: bad shape", who);
+  if (D != 64 && D != 128 && D != 256) return set_error(FU_ERR_UNSUPPORTED, "%s: D=%d unsupported", who, D);
+  if (a.ldx < (int64_t)a.G * D || ld_out < (int64_t)a.G * D) return set_error(FU_ERR_SHAPE, "%s: row stride < G*D", who);
+  if ((a.ldx | ld_out) % 4 != 0 || (a.tab_src && a.ldt % 4 != 0))
+    return set_error(FU_ERR_ALIGN, "%s: row strides must be multiples of 4", who);
+  if ((a.tab_src == nullptr) != (a.tab_dst == nullptr) || (a.tab_src && (!a.z || !a.isrc || !a.idst)))
+    return set_error(FU_ERR_NULL, "%s: tables need both sides and their element ids", who);
+  if (a.M > 0 && (!a.x || !a.gamma || !a.beta)) return set_error(FU_ERR_NULL, "%s: NULL argument", who);
+  const void* al[] = {a.x, a.tab_src, a.tab_dst, a.bias, a.gamma, a.beta};
+  for (const void* p : al)
+    if (p && !aligned16(p)) return set_error(FU_ERR_ALIGN, "%s: arrays must be 16-byte aligned", who);
+  return FU_OK;
+}
+
+template <typename F>
+static void ln_dispatch(int32_t D, F f) {
+  if (D == 64) f(std::integral_constant<int, 16>{});
+  else if (D == 128) f(std::integral_constant<int, 32>{});
+  else f(std::integral_constant<int, 64>{});
 }
 
 }  // namespace fu
 
 using namespace fu;
 
+extern "C" int fu_ln_silu_grouped_fwd(const float* x, int64_t ldx, const float* tab_src, const float* tab_dst,
+                                      int64_t ldt, const int64_t* z, const int64_t* isrc, const int64_t* idst,
+                                      const float* bias, const float* gamma, const float* beta, float* out, int64_t ldo, float* mean,
+                                      float* rstd, int64_t M, int32_t G, int32_t D, float eps, void* stream) {
+  LnArgs a{x, ldx, tab_src, tab_dst, ldt, z, isrc, idst, bias, gamma, beta, M, G};
+  int st = ln_check(a, ldo, D, "fu_ln_silu_grouped_fwd");
+  if (st != FU_OK) return st;
+  if (M == 0) return FU_OK;
+  if (!out || !mean || !rstd || !aligned16(out)) return set_error(FU_ERR_NULL, "fu_ln_silu_grouped_fwd: bad output");
+  hipStream_t s = as_stream(stream);
+  const unsigned blocks = ln_blocks(M * G, D);
+  ln_dispatch(D, [&](auto lpr) {
+    hipLaunchKernelGGL(ln_silu_fwd_kernel<decltype(lpr)::value>, dim3(blocks), dim3(256), 0, s, a, out, ldo, mean,
+                       rstd, eps);
+  });
+  return check_launch("fu_ln_silu_grouped_fwd");
+}
+
+extern "C" int fu_ln_silu_grouped_bwd(const float* x, int64_t ldx, const float* tab_src, const float* tab_dst,
+                                      int64_t ldt, const int64_t* z, const int64_t* isrc, const int64_t* idst,
+                                      const float* bias, const float* gamma, const float* beta, const float* mean, const float* rstd,
+                                      const float* g_out, int64_t ldg, float* g_x, int64_t ldgx, int64_t M, int32_t G,
+                                      int32_t D, void* stream) {
+  LnArgs a{x, ldx, tab_src, tab_dst, ldt, z, isrc, idst, bias, gamma, beta, M, G};
+  int st = ln_check(a, ldgx, D, "fu_ln_silu_grouped_bwd");
+  if (st != FU_OK) return st;
+  if (M == 0) return FU_OK;
+  if (!mean || !rstd || !g_out || !g_x || ldg < (int64_t)G * D || ldg % 4 != 0 || !aligned16(g_out) ||
+      !aligned16(g_x))
+    return set_error(FU_ERR_NULL, "fu_ln_silu_grouped_bwd: bad gradient arguments");
+  hipStream_t s = as_stream(stream);
+  const unsigned blocks = ln_blocks(M * G, D);
+  ln_dispatch(D, [&](auto lpr) {
+    hipLaunchKernelGGL(ln_silu_bwd_kernel<decltype(lpr)::value>, dim3(blocks), dim3(256), 0, s, a, mean, rstd, g_out,
+                       ldg, g_x, ldgx);
+  });
+  return check_launch("fu_ln_silu_grouped_bwd");
+}
+
 extern "C" int fu_ln_silu_fwd(const float* x, const float* gamma, const float* beta, float* out, float* mean,
                               float* rstd, int64_t M, int32_t D, float eps, void* stream) {
   if (M < 0) return set_error(FU_ERR_SHAPE, "fu_ln_silu_fwd: bad shape");
   if (D != 64 && D != 128 && D != 256) return set_error(FU_ERR_UNSUPPORTED, "fu_ln_silu_fwd: D=%d unsupported", D);
-  if (M == 0) return FU_OK;
-  if (!x || !gamma || !beta || !out || !mean || !rstd) return set_error(FU_ERR_NULL, "fu_ln_silu_fwd: NULL argument");
-  if (!aligned16(x) || !aligned16(out) || !aligned16(gamma) || !aligned16(beta))
-    return set_error(FU_ERR_ALIGN, "fu_ln_silu_fwd: rows must be 16-byte aligned");
-  hipStream_t s = as_stream(stream);
-  const int rpb = 256 / (D / 4);
-  const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(M, rpb), 65536);
-  if (D == 64) hipLaunchKernelGGL(ln_silu_fwd_kernel<16>, dim3(blocks), dim3(256), 0, s, x, gamma, beta, out, mean, rstd, M, eps);
-  else if (D == 128) hipLaunchKernelGGL(ln_silu_fwd_kernel<32>, dim3(blocks), dim3(256), 0, s, x, gamma, beta, out, mean, rstd, M, eps);
-  else hipLaunchKernelGGL(ln_silu_fwd_kernel<64>, dim3(blocks), dim3(256), 0, s, x, gamma, beta, out, mean, rstd, M, eps);
-  return check_launch("fu_ln_silu_fwd");
+  return fu_ln_silu_grouped_fwd(x, D, nullptr, nullptr, 0, nullptr, nullptr, nullptr, nullptr, gamma, beta, out, D, mean, rstd,
+                                M, 1, D, eps, stream);
 }
 
 extern "C" int fu_ln_silu_bwd(const float* x, const float* gamma, const float* beta, const float* mean,
                               const float* rstd, const float* g_out, float* g_x, int64_t M, int32_t D, void* stream) {
   if (M < 0) return set_error(FU_ERR_SHAPE, "fu_ln_silu_bwd: bad shape");
   if (D != 64 && D != 128 && D != 256) return set_error(FU_ERR_UNSUPPORTED, "fu_ln_silu_bwd: D=%d unsupported", D);
-  if (M == 0) return FU_OK;
-  if (!x || !gamma || !beta || !mean || !rstd || !g_out || !g_x) return set_error(FU_ERR_NULL, "fu_ln_silu_bwd: NULL argument");
-  if (!aligned16(x) || !aligned16(g_out) || !aligned16(g_x) || !aligned16(gamma) || !aligned16(beta))
-    return set_error(FU_ERR_ALIGN, "fu_ln_silu_bwd: rows must be 16-byte aligned");
-  hipStream_t s = as_stream(stream);
-  const int rpb = 256 / (D / 4);
-  const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(M, rpb), 65536);
-  if (D == 64) hipLaunchKernelGGL(ln_silu_bwd_kernel<16>, dim3(blocks), dim3(256), 0, s, x, gamma, beta, mean, rstd, g_out, g_x, M);
-  else if (D == 128) hipLaunchKernelGGL(ln_silu_bwd_kernel<32>, dim3(blocks), dim3(256), 0, s, x, gamma, beta, mean, rstd, g_out, g_x, M);
-  else hipLaunchKernelGGL(ln_silu_bwd_kernel<64>, dim3(blocks), dim3(256), 0, s, x, gamma, beta, mean, rstd, g_out, g_x, M);
-  return check_launch("fu_ln_silu_bwd");
+  return fu_ln_silu_grouped_bwd(x, D, nullptr, nullptr, 0, nullptr, nullptr, nullptr, nullptr, gamma, beta, mean, rstd, g_out,
+                                D, g_x, D, M, 1, D, stream);
 }

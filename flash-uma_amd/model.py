@@ -26,6 +26,7 @@ from ops.geom import precompute_geometry
 from ops.linear import linear
 from ops.ln_silu import layer_norm_silu
 from ops.node import permute_rows
+from ops.radial import RadialBank
 from ops.scatter import init_node_scatter, rotate_scatter_split
 from ops.topology import (clear_topology_cache, get_topology, morton_permutation, receiver_csr, take)
 
@@ -139,10 +140,18 @@ class Packed_eSCN_Layer(nn.Module):
                              self.gamma_rad1_2, self.beta_rad1_2)
         return linear(h2, self.W_rad1_3, self.b_rad1_3, self.W_rad1_3_t)
 
+    def radial_mlp(self):
+        """This block's radial-MLP parameters in RadialBank order."""
+        return (self.W_rad1_1, self.b_rad1_1, self.gamma_rad1_1, self.beta_rad1_1, self.W_rad1_2, self.b_rad1_2,
+                self.gamma_rad1_2, self.beta_rad1_2, self.W_rad1_3, self.b_rad1_3)
+
     def forward(self, x_in, x_edge_raw, wigner, env, idx_i, idx_j, row_ptr, col_idx, csd_emb, batch,
-                topology=None):
+                topology=None, rad_out=None):
+        """rad_out, when given, is this block's radial-MLP output (computed by the model's
+        RadialBank); otherwise it is computed here from x_edge_raw (E, B+2C)."""
         x_norm = self.norm_1(x_in)
-        rad_out = self.radial(x_edge_raw)
+        if rad_out is None:
+            rad_out = self.radial(x_edge_raw)
         X_m0, X_m1, X_m2 = gather_wigner_split(x_norm, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology)
         Y_m0 = linear(X_m0, self.W_conv1_m0, self.b_conv1_m0, self.W_conv1_m0_t)
         Y_m1 = linear(X_m1, self.W_conv1_m1, None, self.W_conv1_m1_t)
@@ -189,6 +198,11 @@ class eSCN_Inference_Model(nn.Module):
             self.register_buffer(name + "_t", getattr(self, name).data.to(dtype).t().contiguous())
         for layer in self.layers:
             layer.prepare_for_inference(dtype)
+        mlps = [(self.W_rad1_1, self.b_rad1_1, self.gamma_rad1_1, self.beta_rad1_1, self.W_rad1_2, self.b_rad1_2,
+                 self.gamma_rad1_2, self.beta_rad1_2, self.W_rad1_3, self.b_rad1_3)]
+        mlps += [layer.radial_mlp() for layer in self.layers]
+        self.radial_bank = RadialBank([tuple(t.data for t in m) for m in mlps], self.W_src.data, self.W_tgt.data,
+                                      self.B, dtype=dtype)
         self.to(dtype)
 
     def radial(self, x_edge_raw):
@@ -209,21 +223,22 @@ class eSCN_Inference_Model(nn.Module):
         row_ptr, col_idx = topo.recv_ptr, topo.recv_idx
         N = pos_s.shape[0]
 
-        # 2. Per-edge geometry
-        x_edge_raw, wigner, env = precompute_geometry(pos_s, Z_s, idx_i_s, idx_j_s, shifts_s, self.W_src,
-                                                      self.W_tgt, self.offset_g, self.coeff_g, self.cutoff,
-                                                      topo)
-        # 3. Edge-degree embedding
-        rad_out_p1 = self.radial(x_edge_raw)
-        x_node_s = init_node_scatter(rad_out_p1, wigner, env, Z_s, batch_s, self.W_sphere, csd_emb, idx_j_s,
+        # 2. Per-edge geometry: Gaussians, Wigner blocks, envelope.  The element-embedding
+        #    columns of x_edge_raw are folded into the radial bank's per-element tables.
+        gauss, wigner, env = precompute_geometry(pos_s, Z_s, idx_i_s, idx_j_s, shifts_s, self.W_src, self.W_tgt,
+                                                 self.offset_g, self.coeff_g, self.cutoff, topo, False)
+        # 3. Every radial MLP (edge-degree embedding + one per block) as one bank
+        rads = self.radial_bank(gauss, Z_s, idx_i_s, idx_j_s)
+        # 4. Edge-degree embedding
+        x_node_s = init_node_scatter(rads[0], wigner, env, Z_s, batch_s, self.W_sphere, csd_emb, idx_j_s,
                                      row_ptr, col_idx, N)
-        # 4. Message-passing blocks
-        for layer in self.layers:
-            x_node_s = layer(x_node_s, x_edge_raw, wigner, env, idx_i_s, idx_j_s, row_ptr, col_idx, csd_emb,
-                             batch_s, topo)
+        # 5. Message-passing blocks
+        for layer, rad in zip(self.layers, rads[1:]):
+            x_node_s = layer(x_node_s, None, wigner, env, idx_i_s, idx_j_s, row_ptr, col_idx, csd_emb,
+                             batch_s, topo, rad_out=rad)
             if self.charge_end > self.charge_start or self.spin_end > self.spin_start:
                 raise NotImplementedError(
                     "charge/spin channel balancing (FAIRChem balance_channels_batched) is not available")
         x_node_s = self.final_norm(x_node_s)
-        # 5. Back to the input atom order
+        # 6. Back to the input atom order
         return permute_rows(x_node_s, topo.inv_perm)

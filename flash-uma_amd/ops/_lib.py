@@ -38,6 +38,8 @@ SIGNATURES: dict[str, list] = {
     "fu_init_scatter_bwd": [P, P, P, P, P, P, P, P, I64, I64, I32, P],
     "fu_ln_silu_fwd": [P, P, P, P, P, P, I64, I32, F32, P],
     "fu_ln_silu_bwd": [P, P, P, P, P, P, P, I64, I32, P],
+    "fu_ln_silu_grouped_fwd": [P, I64, P, P, I64, P, P, P, P, P, P, P, I64, P, P, I64, I32, I32, F32, P],
+    "fu_ln_silu_grouped_bwd": [P, I64, P, P, I64, P, P, P, P, P, P, P, P, P, I64, P, I64, I64, I32, I32, P],
     "fu_linear": [P, I64, P, I64, P, P, I64, I64, I32, I32, P],
     "fu_linear_batched": [P, I64, I64, P, I64, I64, P, I64, I32, P, I64, I64, I64, I32, I32, I32, P],
     "fu_rms_norm_sh_fwd": [P, P, P, P, P, I64, I32, I32, F32, P],

@@ -1,0 +1,152 @@
+"""All radial MLPs of the model as one bank (the per-block radial MLP of model.py:147-149 and
+the edge-degree one of model.py:203-205, each Linear -> LNSiLU -> Linear -> LNSiLU -> Linear).
+
+Every radial MLP reads the same edge features x_edge_raw = [g | W_src[Z_i] | W_tgt[Z_j]]
+(Gaussians g (B), source and target element embeddings (C each), ops/geom.py:196-214).  Its
+first linear therefore splits as
+
+    W1 x_edge_raw + b1 = W1[:, :B] g + (W1[:, B:B+C] W_src^T)[:, Z_i] + (W1[:, B+C:] W_tgt^T)[:, Z_j] + b1
+
+and the two element terms are tables of 100 rows per block, computed once when the model is
+frozen.  The bank runs the Gaussian part of all G blocks as ONE GEMM (E x B -> E x G*C), adds
+the table rows inside the grouped LayerNorm+SiLU kernel, runs the G second linears as one
+batched GEMM, a second grouped LayerNorm+SiLU, then each block's output linear.  The
+backward mirrors it and returns one gradient for the Gaussians: the per-block (E, B+2C)
+x_edge_raw gradients and their G-way sum are never formed.  Element embeddings are frozen
+and the geometry backward ignores their columns (ops/geom.py:588-589), so no gradient is
+lost.  Results equal the per-block MLPs up to fp32 rounding order."""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .constants import LN_EPS
+
+
+def _ln_grouped_fwd(x, tabs, z, isrc, idst, bias, gamma, beta, G, D, eps):
+    M = x.shape[0]
+    out = torch.empty_like(x)
+    mean = torch.empty(M * G, device=x.device, dtype=torch.float32)
+    rstd = torch.empty(M * G, device=x.device, dtype=torch.float32)
+    ts, td = tabs if tabs is not None else (None, None)
+    _lib.call("fu_ln_silu_grouped_fwd", x.data_ptr(), x.stride(0), _lib.ptr(ts), _lib.ptr(td),
+              0 if ts is None else ts.stride(0), _lib.ptr(z), _lib.ptr(isrc), _lib.ptr(idst), _lib.ptr(bias),
+              gamma.data_ptr(), beta.data_ptr(), out.data_ptr(), out.stride(0), mean.data_ptr(), rstd.data_ptr(),
+              M, G, D, float(eps), _lib.stream_ptr(x.device))
+    return out, mean, rstd
+
+
+def _ln_grouped_bwd(x, tabs, z, isrc, idst, bias, gamma, beta, mean, rstd, g_out, G, D):
+    M = x.shape[0]
+    g_x = torch.empty_like(x)
+    ts, td = tabs if tabs is not None else (None, None)
+    _lib.call("fu_ln_silu_grouped_bwd", x.data_ptr(), x.stride(0), _lib.ptr(ts), _lib.ptr(td),
+              0 if ts is None else ts.stride(0), _lib.ptr(z), _lib.ptr(isrc), _lib.ptr(idst), _lib.ptr(bias),
+              gamma.data_ptr(), beta.data_ptr(), mean.data_ptr(), rstd.data_ptr(), g_out.data_ptr(),
+              g_out.stride(0), g_x.data_ptr(), g_x.stride(0), M, G, D, _lib.stream_ptr(x.device))
+    return g_x
+
+
+def _batched(A, W, bias, G, C_in, C_out, out):
+    """out[:, g*C_out:(g+1)*C_out] = A[:, g*C_in:(g+1)*C_in] @ W[g]^T (+ bias[g]) for all g."""
+    M = A.shape[0]
+    _lib.call("fu_linear_batched", A.data_ptr(), A.stride(0), C_in, W.data_ptr(), C_in, C_out * C_in,
+              _lib.ptr(bias), C_out if bias is not None else 0, G if bias is not None else 0, out.data_ptr(),
+              out.stride(0), C_out, M, C_out, C_in, G, _lib.stream_ptr(A.device))
+    return out
+
+
+def _gemm(A, W, bias, out):
+    M, K = A.shape
+    N = W.shape[0]
+    _lib.call("fu_linear", A.data_ptr(), A.stride(0), W.data_ptr(), W.stride(0), _lib.ptr(bias), out.data_ptr(),
+              out.stride(0), M, N, K, _lib.stream_ptr(A.device))
+    return out
+
+
+class RadialBank(torch.nn.Module):
+    """Frozen bank of G radial MLPs sharing the edge features.
+
+    mlps: list of (W1 (C, B+2C), b1, gamma1, beta1, W2 (C, C), b2, gamma2, beta2, W3 (n_k, C), b3),
+    one per block in the order their outputs are returned."""
+
+    def __init__(self, mlps, W_src: torch.Tensor, W_tgt: torch.Tensor, B: int, eps: float = LN_EPS,
+                 dtype=torch.float32):
+        super().__init__()
+        C = mlps[0][4].shape[0]
+        self.G, self.C, self.B, self.eps = len(mlps), C, B, eps
+        f64 = torch.float64
+        W1g = torch.cat([m[0][:, :B] for m in mlps], 0)                                         # (G*C, B)
+        tab_src = torch.cat([W_src.to(f64) @ m[0][:, B:B + C].to(f64).t() for m in mlps], 1)  # (100, G*C)
+        tab_tgt = torch.cat([W_tgt.to(f64) @ m[0][:, B + C:].to(f64).t() for m in mlps], 1)
+        reg = lambda n, t: self.register_buffer(n, t.detach().to(dtype).contiguous())
+        reg("W1g", W1g)
+        reg("W1g_t", W1g.t())
+        reg("tab_src", tab_src)
+        reg("tab_tgt", tab_tgt)
+        reg("b1", torch.cat([m[1] for m in mlps]))
+        reg("gamma1", torch.cat([m[2] for m in mlps]))
+        reg("beta1", torch.cat([m[3] for m in mlps]))
+        reg("W2", torch.stack([m[4] for m in mlps]))                 # (G, C, C)
+        reg("W2_t", torch.stack([m[4].t() for m in mlps]))
+        reg("b2", torch.cat([m[5] for m in mlps]))
+        reg("gamma2", torch.cat([m[6] for m in mlps]))
+        reg("beta2", torch.cat([m[7] for m in mlps]))
+        for k, m in enumerate(mlps):
+            reg(f"W3_{k}", m[8])
+            reg(f"W3_{k}_t", m[8].t())
+            reg(f"b3_{k}", m[9])
+
+    def forward(self, gauss, Z, idx_i, idx_j):
+        """gauss (E, B) -> tuple of G radial outputs (E, n_k)."""
+        W3 = [(getattr(self, f"W3_{k}"), getattr(self, f"W3_{k}_t"), getattr(self, f"b3_{k}")) for k in range(self.G)]
+        return _RadialBankFn.apply(gauss, Z, idx_i, idx_j, self, *[w for t in W3 for w in t])
+
+
+class _RadialBankFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, gauss, Z, idx_i, idx_j, bank, *W3):
+        gauss = _lib.require(gauss, torch.float32, "gauss")
+        Z = _lib.require(Z, torch.int64, "Z")
+        idx_i = _lib.require(idx_i, torch.int64, "idx_i")
+        idx_j = _lib.require(idx_j, torch.int64, "idx_j")
+        E, G, C = gauss.shape[0], bank.G, bank.C
+        dev = gauss.device
+        if gauss.shape[1] != bank.B:
+            raise _lib.FlashUMAError(f"radial bank: expected {bank.B} Gaussians per edge, got {gauss.shape[1]}")
+        tabs = (bank.tab_src, bank.tab_tgt)
+        p1 = _gemm(gauss, bank.W1g, None, torch.empty(E, G * C, device=dev, dtype=torch.float32))
+        h1, m1, r1 = _ln_grouped_fwd(p1, tabs, Z, idx_i, idx_j, bank.b1, bank.gamma1, bank.beta1, G, C, bank.eps)
+        p2 = _batched(h1, bank.W2, bank.b2, G, C, C, torch.empty_like(h1))
+        del h1
+        h2, m2, r2 = _ln_grouped_fwd(p2, None, None, None, None, None, bank.gamma2, bank.beta2, G, C, bank.eps)
+        outs = []
+        for k in range(G):
+            W, _, b = W3[3 * k:3 * k + 3]
+            outs.append(_gemm(h2[:, k * C:(k + 1) * C], W, b,
+                              torch.empty(E, W.shape[0], device=dev, dtype=torch.float32)))
+        ctx.save_for_backward(p1, m1, r1, p2, m2, r2, Z, idx_i, idx_j)
+        ctx.bank, ctx.W3 = bank, W3
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, *g_outs):
+        p1, m1, r1, p2, m2, r2, Z, idx_i, idx_j = ctx.saved_tensors
+        bank, W3 = ctx.bank, ctx.W3
+        E, G, C = p1.shape[0], bank.G, bank.C
+        g_h2 = torch.empty_like(p2)
+        for k in range(G):
+            sl = g_h2[:, k * C:(k + 1) * C]
+            if g_outs[k] is None:
+                sl.zero_()
+            else:
+                _gemm(g_outs[k].contiguous(), W3[3 * k + 1], None, sl)
+        g_p2 = _ln_grouped_bwd(p2, None, None, None, None, None, bank.gamma2, bank.beta2, m2, r2, g_h2, G, C)
+        del g_h2
+        g_h1 = _batched(g_p2, bank.W2_t, None, G, C, C, torch.empty_like(g_p2))
+        del g_p2
+        g_p1 = _ln_grouped_bwd(p1, (bank.tab_src, bank.tab_tgt), Z, idx_i, idx_j, bank.b1, bank.gamma1, bank.beta1,
+                               m1, r1, g_h1, G, C)
+        del g_h1
+        g_gauss = _gemm(g_p1, bank.W1g_t, None, torch.empty(E, bank.B, device=p1.device, dtype=torch.float32))
+        return (g_gauss, None, None, None, None) + (None,) * len(W3)

@@ -156,6 +156,26 @@ int fu_ln_silu_bwd(const float* x, const float* gamma, const float* beta, const 
                    const float* rstd, const float* g_out, float* g_x, int64_t M, int32_t D,
                    void* stream);
 
+/* The first LayerNorm+SiLU of every radial MLP at once (model.py:147, 203 with
+ * ops/ln_silu.py:29-72 per block).  Row e of x (stride ldx) holds G groups of D values, the
+ * Gaussian part W1[:, :B] g_e of each block's first linear.  Group g is normalised after
+ * adding bias[g*D:], tab_src[z[isrc[e]]][g*D:] and tab_dst[z[idst[e]]][g*D:] (the
+ * element-embedding part of the same linear, precomputed per element; tables optional,
+ * stride ldt); gamma/beta are G*D long.  mean/rstd hold M*G entries, (row, group) order. */
+int fu_ln_silu_grouped_fwd(const float* x, int64_t ldx, const float* tab_src, const float* tab_dst,
+                           int64_t ldt, const int64_t* z, const int64_t* isrc, const int64_t* idst,
+                           const float* bias, const float* gamma, const float* beta, float* out,
+                           int64_t ldo, float* mean, float* rstd, int64_t M, int32_t G, int32_t D,
+                           float eps, void* stream);
+
+/* Input gradient of fu_ln_silu_grouped_fwd (ops/ln_silu.py:77-123 per group); the gradient
+ * with respect to x equals the gradient with respect to the table rows and bias. */
+int fu_ln_silu_grouped_bwd(const float* x, int64_t ldx, const float* tab_src, const float* tab_dst,
+                           int64_t ldt, const int64_t* z, const int64_t* isrc, const int64_t* idst,
+                           const float* bias, const float* gamma, const float* beta,
+                           const float* mean, const float* rstd, const float* g_out, int64_t ldg,
+                           float* g_x, int64_t ldgx, int64_t M, int32_t G, int32_t D, void* stream);
+
 /* ------------------------------------------------------------------------------------
  * Dense contractions on fp32 MFMA (replaces torch F.linear at model.py:147-154,203-205)
  * ------------------------------------------------------------------------------------ */

@@ -79,6 +79,50 @@ def test_linear(cuda, M, N, K):
     assert_close(g, gref, TOL, "linear bwd")
 
 
+@pytest.mark.parametrize("C", [128, 64])
+def test_radial_bank(cuda, C):
+    """All radial MLPs as one bank (element embeddings folded into per-element tables) against
+    the textbook per-block MLP on x_edge_raw = [g | W_src[Z_i] | W_tgt[Z_j]] in float64."""
+    from ops.radial import RadialBank
+    g = torch.Generator().manual_seed(C)
+    N, E, B = 50, 777, 64
+    outs = [3 * C, 12 * C, 12 * C]
+    Z = torch.randint(1, 100, (N,), generator=g)
+    ii = torch.randint(0, N, (E,), generator=g)
+    jj = torch.randint(0, N, (E,), generator=g)
+    W_src, W_tgt = torch.randn(100, C, generator=g), torch.randn(100, C, generator=g)
+    mlps = []
+    for n in outs:
+        r = lambda *s: torch.randn(*s, generator=g)
+        mlps.append((r(C, B + 2 * C) / (B + 2 * C) ** 0.5, r(C) * 0.1, r(C).abs() + 0.5, r(C) * 0.1,
+                     r(C, C) / C ** 0.5, r(C) * 0.1, r(C).abs() + 0.5, r(C) * 0.1, r(n, C) / C ** 0.5, r(n) * 0.1))
+    gauss = torch.rand(E, B, generator=g)
+    cot = [torch.randn(E, n, generator=g) for n in outs]
+
+    def ref(gs):
+        xe = torch.cat([gs, W_src.double()[Z[ii]], W_tgt.double()[Z[jj]]], 1)
+        res = []
+        for m in mlps:
+            m = [t.double() for t in m]
+            h = R.layer_norm_silu(xe @ m[0].T + m[1], m[2], m[3], 1e-7)
+            h = R.layer_norm_silu(h @ m[4].T + m[5], m[6], m[7], 1e-7)
+            res.append(h @ m[8].T + m[9])
+        return tuple(res)
+
+    rref, (gref,) = _vjp(ref, [gauss], cot)
+    bank = RadialBank([tuple(t.to(cuda) for t in m) for m in mlps], W_src.to(cuda), W_tgt.to(cuda), B)
+    gg = gauss.to(cuda).requires_grad_(True)
+    rads = bank(gg, Z.to(cuda), ii.to(cuda), jj.to(cuda))
+    for a, b in zip(rads, rref):
+        assert_close(a, b, TOL, "radial bank fwd")
+    (gr,) = torch.autograd.grad(rads, gg, [c.to(cuda) for c in cot], retain_graph=True)
+    assert_close(gr, gref, 1e-4, "radial bank bwd")
+    # a block without a gradient counts as zero
+    (gr1,) = torch.autograd.grad(rads[1:], gg, [c.to(cuda) for c in cot[1:]])
+    _, (gref1,) = _vjp(lambda a: ref(a)[1:], [gauss], cot[1:])
+    assert_close(gr1, gref1, 1e-4, "radial bank bwd (partial)")
+
+
 def _geom_inputs(seed=2, N=40, E=300, C=128, B=64):
     pos, Z, ei, shifts = random_graph(N, E, seed=seed)
     pos, shifts = axis_aligned_edges(pos, ei, shifts)
