@@ -60,12 +60,57 @@ __device__ __forceinline__ float4 scale4(float4 a, float s) {
   return make_float4(a.x * s, a.y * s, a.z * s, a.w * s);
 }
 
-// Full-wavefront (64 lanes) butterfly sum; every lane receives the total.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+// Cross-lane exchanges without LDS traffic (gfx950):
+//   swap_halves<32>(a, b): v_permlane32_swap; afterwards lanes 0-31 of the first result hold
+//     a[0..31] and lanes 32-63 hold b[0..31], the second result holds a[32..63] | b[32..63];
+//   swap_halves<16>(a, b): v_permlane16_swap, the same within each pair of 16-lane rows;
+//   partner<H>(v) for H = 8, 2, 1: v of lane l ^ H (DPP row_ror:8, quad_perm); for H = 4:
+//     v of lane 7 - (l mod 8) in l's 8-lane group (DPP row_half_mirror), which also pairs
+//     every lane with bit 2 clear with one with bit 2 set inside the same 8-lane group.
+template <int H>
+__device__ __forceinline__ void swap_halves(float a, float b, float& lo, float& hi) {
+  static_assert(H == 32 || H == 16, "swap_halves: H must be 32 or 16");
+  if constexpr (H == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    lo = __uint_as_float(r[0]);
+    hi = __uint_as_float(r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    lo = __uint_as_float(r[0]);
+    hi = __uint_as_float(r[1]);
+  }
+}
+
+template <int H>
+__device__ __forceinline__ float partner(float v) {
+  constexpr int ctrl = H == 8 ? 0x128 : H == 4 ? 0x141 : H == 2 ? 0x4E : 0xB1;
+  static_assert(H == 8 || H == 4 || H == 2 || H == 1, "partner: H must be 8, 4, 2 or 1");
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xf, 0xf, false));
+}
+
+// Sum over each aligned group of G lanes (G = 2, 4, ..., 64); every lane of a group receives
+// the group total (the same value in every lane: each step adds commuted operand pairs).
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (G >= 64) {
+    float lo, hi;
+    swap_halves<32>(v, v, lo, hi);
+    v = lo + hi;
+  }
+  if constexpr (G >= 32) {
+    float lo, hi;
+    swap_halves<16>(v, v, lo, hi);
+    v = lo + hi;
+  }
+  if constexpr (G >= 16) v += partner<8>(v);
+  if constexpr (G >= 8) v += partner<4>(v);
+  if constexpr (G >= 4) v += partner<2>(v);
+  if constexpr (G >= 2) v += partner<1>(v);
   return v;
 }
+
+// Full-wavefront (64 lanes) sum; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 __device__ __forceinline__ double wave_sum_d(double v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);

@@ -81,36 +81,60 @@ __device__ __forceinline__ float vdot(const Vec<CPL>& a, const Vec<CPL>& b) {
   return s;
 }
 
-// Recursive halving over lane offsets V/2, V/4, ..., 1: at each step a lane keeps half of
-// its values and adds the partner's copy of that half.  Afterwards lane l holds the sum of
-// value (l mod V) over the 2^log2(V) lanes that share l's high bits.
+// Recursive halving over lane bits H = V/2, V/4, ..., 1: at each step a lane keeps half of its
+// values (the upper half if bit H of its index is set) and adds its partner's copy of that
+// half, the partner having the opposite bit H and the same higher bits.  Afterwards lane l
+// holds the sum of value (l mod V) over the V lanes that share l's bits above log2(V).
+// H = 32 and 16 use the permlane swaps (both halves exchanged in one instruction, no
+// selects), H <= 8 DPP moves.
 template <int V>
 __device__ __forceinline__ float halve_values(const float (&vals)[V], int lane) {
   if constexpr (V == 1) {
     return vals[0];
   } else {
     constexpr int H = V / 2;
-    const bool upper = (lane & H) != 0;
     float nxt[H];
+    if constexpr (H >= 16) {
 #pragma unroll
-    for (int k = 0; k < H; ++k) {
-      const float send = upper ? vals[k] : vals[k + H];
-      const float keep = upper ? vals[k + H] : vals[k];
-      nxt[k] = keep + __shfl_xor(send, H, 64);
+      for (int k = 0; k < H; ++k) {
+        float lo, hi;
+        swap_halves<H>(vals[k], vals[k + H], lo, hi);
+        nxt[k] = lo + hi;
+      }
+    } else {
+      const bool upper = (lane & H) != 0;
+#pragma unroll
+      for (int k = 0; k < H; ++k) {
+        const float send = upper ? vals[k] : vals[k + H];
+        const float keep = upper ? vals[k + H] : vals[k];
+        nxt[k] = keep + partner<H>(send);
+      }
     }
     return halve_values<H>(nxt, lane);
   }
 }
 
 // Sum V per-lane values over all 64 lanes of a wave (V a power of two <= 64).  Lane l
-// receives the total of value (l mod V).  Costs V - 1 + (6 - log2 V) shuffles instead of
-// 6 V for V independent butterflies.
+// receives the total of value (l mod V).  Costs V - 1 exchanges plus 6 - log2 V full-wave
+// steps, instead of 6 V for V independent reductions.
 template <int V>
 __device__ __forceinline__ float wave_multi_sum(const float (&vals)[V], int lane) {
   static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "V must be a power of two <= 64");
   float r = halve_values<V>(vals, lane);
-#pragma unroll
-  for (int o = V; o < 64; o <<= 1) r += __shfl_xor(r, o, 64);
+  if constexpr (V < 64) {
+    // the V-lane groups hold equal value sets: add them across the remaining lane bits
+    if constexpr (V <= 16) {
+      float lo, hi;
+      swap_halves<16>(r, r, lo, hi);
+      r = lo + hi;
+    }
+    if constexpr (V <= 32) {
+      float lo, hi;
+      swap_halves<32>(r, r, lo, hi);
+      r = lo + hi;
+    }
+    static_assert(V >= 16, "wave_multi_sum: V below 16 needs more cross-group steps");
+  }
   return r;
 }
 

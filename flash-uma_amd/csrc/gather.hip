@@ -5,9 +5,9 @@
 // indices and its 34 Wigner scalars are wave-uniform (scalar loads); every node row, radial
 // row and output slot is one coalesced row access.
 //
-// Backward: node-centric.  A 256-thread workgroup owns two nodes; for each node one wave
-// walks the node's receiver segment (edges e with idx_j[e] = n, receiver CSR) and one wave
-// its sender segment (idx_i[e] = n, sender CSR).  Each wave recomputes the rotated own row,
+// Backward: node-centric.  A 128-thread workgroup owns one node: one wave walks the node's
+// receiver segment (edges e with idx_j[e] = n, receiver CSR) and the other its sender
+// segment (idx_i[e] = n, sender CSR).  Each wave recomputes the rotated own row,
 // writes its half of g_rad, accumulates D^T g into the node gradient in CSR order, and
 // reduces its half of g_wigner across lanes.  The two node partials are added through LDS
 // (receiver part + sender part) and g_x[n] is written once: deterministic, no atomics.
@@ -63,7 +63,16 @@ __device__ __forceinline__ int wave_id_uniform() {
   return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
 }
 
-template <int CPL>
+// Column block of slot q of side so (0 = sender, 1 = receiver) in an array holding `per_side`
+// slots per side.  Layout 0 is the reference order (sides interleaved: 2q + so,
+// ops/gather.py:132-154); layout 1 keeps each side's slots contiguous (so * per_side + q), so
+// that one side's share of an edge row is a single contiguous run.
+template <int L>
+__device__ __forceinline__ constexpr int slot(int per_side, int so, int q) {
+  return L ? so * per_side + q : 2 * q + so;
+}
+
+template <int CPL, int L>
 __global__ __launch_bounds__(256) void gather_fwd_kernel(
     const float* __restrict__ x, const int64_t* __restrict__ idx_i, const int64_t* __restrict__ idx_j,
     const float* __restrict__ wig, const float* __restrict__ rad, const float* __restrict__ csd,
@@ -90,76 +99,99 @@ __global__ __launch_bounds__(256) void gather_fwd_kernel(
     vt.r[0] = vadd(vt.r[0], vload<CPL>(csd + batch[j] * C + c));
     rotate9(w, vs, rs);
     rotate9(w, vt, rt);
+    // radial block k (reference numbering: even = sender, odd = receiver)
     const float* rr = rad + e * 12 * C + c;
     Vec<CPL> r[12];
 #pragma unroll
-    for (int k = 0; k < 12; ++k) r[k] = vload<CPL>(rr + k * C);
+    for (int k = 0; k < 12; ++k) r[k] = vload<CPL>(rr + slot<L>(6, k & 1, k >> 1) * C);
     float* o0 = X0 + e * 6 * C + c;
     float* o1 = X1 + e * 8 * C + c;
     float* o2 = X2 + e * 4 * C + c;
-    vstore(o0 + 0 * C, vmul(rs.r[0], r[0]));
-    vstore(o0 + 1 * C, vmul(rt.r[0], r[1]));
-    vstore(o0 + 2 * C, vmul(rs.r[2], r[2]));
-    vstore(o0 + 3 * C, vmul(rt.r[2], r[3]));
-    vstore(o0 + 4 * C, vmul(rs.r[6], r[4]));
-    vstore(o0 + 5 * C, vmul(rt.r[6], r[5]));
-    vstore(o1 + 0 * C, vmul(rs.r[3], r[6]));
-    vstore(o1 + 1 * C, vmul(rt.r[3], r[7]));
-    vstore(o1 + 2 * C, vmul(rs.r[7], r[8]));
-    vstore(o1 + 3 * C, vmul(rt.r[7], r[9]));
-    vstore(o1 + 4 * C, vmul(rs.r[1], r[6]));
-    vstore(o1 + 5 * C, vmul(rt.r[1], r[7]));
-    vstore(o1 + 6 * C, vmul(rs.r[5], r[8]));
-    vstore(o1 + 7 * C, vmul(rt.r[5], r[9]));
-    vstore(o2 + 0 * C, vmul(rs.r[8], r[10]));
-    vstore(o2 + 1 * C, vmul(rt.r[8], r[11]));
-    vstore(o2 + 2 * C, vmul(rs.r[4], r[10]));
-    vstore(o2 + 3 * C, vmul(rt.r[4], r[11]));
+    // m0 slots: rotated coefficient k0, k2, k6; m1: k3, k7 (R) and k1, k5 (I); m2: k8 (R), k4 (I)
+    constexpr int K0[3] = {0, 2, 6}, K1[4] = {3, 7, 1, 5}, K2[2] = {8, 4};
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      vstore(o0 + slot<L>(3, 0, q) * C, vmul(rs.r[K0[q]], r[2 * q]));
+      vstore(o0 + slot<L>(3, 1, q) * C, vmul(rt.r[K0[q]], r[2 * q + 1]));
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      vstore(o1 + slot<L>(4, 0, q) * C, vmul(rs.r[K1[q]], r[6 + 2 * (q & 1)]));
+      vstore(o1 + slot<L>(4, 1, q) * C, vmul(rt.r[K1[q]], r[7 + 2 * (q & 1)]));
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      vstore(o2 + slot<L>(2, 0, q) * C, vmul(rs.r[K2[q]], r[10]));
+      vstore(o2 + slot<L>(2, 1, q) * C, vmul(rt.r[K2[q]], r[11]));
+    }
   }
 }
 
 // Per-edge data of one side of the gather backward (receiver side: so = 1, sender: so = 0).
+// The Wigner scalars arrive as one vector load (lane q < 34 holds scalar q) so that every
+// load of an edge is counted by vmcnt and the next edge's loads stay in flight while this
+// edge is processed; they are broadcast with readlane when used.
 template <int CPL>
 struct SideEdge {
-  float w[34];
+  float wl;
   Vec<CPL> g[9];   // this side's g_X slots: m0 a/b/c, m1 a/b/c/d, m2 a/b
   Vec<CPL> r[6];   // this side's radial blocks so, 2+so, ..., 10+so
 };
 
-template <int CPL>
-__device__ __forceinline__ void side_load(const float* __restrict__ gX0, const float* __restrict__ gX1,
-                                          const float* __restrict__ gX2, const float* __restrict__ wig,
-                                          const float* __restrict__ rad, int64_t e, int so, int c, SideEdge<CPL>& d) {
-  constexpr int C = 64 * CPL;
-#pragma unroll
-  for (int q = 0; q < 34; ++q) d.w[q] = wig[e * 34 + q];
-  const float* g0 = gX0 + e * 6 * C + so * C + c;
-  const float* g1 = gX1 + e * 8 * C + so * C + c;
-  const float* g2 = gX2 + e * 4 * C + so * C + c;
-  d.g[0] = vload<CPL>(g0); d.g[1] = vload<CPL>(g0 + 2 * C); d.g[2] = vload<CPL>(g0 + 4 * C);
-  d.g[3] = vload<CPL>(g1); d.g[4] = vload<CPL>(g1 + 2 * C); d.g[5] = vload<CPL>(g1 + 4 * C);
-  d.g[6] = vload<CPL>(g1 + 6 * C);
-  d.g[7] = vload<CPL>(g2); d.g[8] = vload<CPL>(g2 + 2 * C);
-  const float* rp = rad + e * 12 * C + so * C + c;
-#pragma unroll
-  for (int q = 0; q < 6; ++q) d.r[q] = vload<CPL>(rp + 2 * q * C);
+__device__ __forceinline__ float read_lane(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+template <int CPL, int L>
+__device__ __forceinline__ void side_load(const float* __restrict__ gX0, const float* __restrict__ gX1,
+                                          const float* __restrict__ gX2, const float* __restrict__ wig,
+                                          const float* __restrict__ rad, int64_t e, int so, int c, int lane,
+                                          SideEdge<CPL>& d) {
+  constexpr int C = 64 * CPL;
+  d.wl = lane < 34 ? wig[e * 34 + lane] : 0.0f;
+  const float* g0 = gX0 + e * 6 * C + c;
+  const float* g1 = gX1 + e * 8 * C + c;
+  const float* g2 = gX2 + e * 4 * C + c;
+#pragma unroll
+  for (int q = 0; q < 3; ++q) d.g[q] = vload<CPL>(g0 + slot<L>(3, so, q) * C);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) d.g[3 + q] = vload<CPL>(g1 + slot<L>(4, so, q) * C);
+#pragma unroll
+  for (int q = 0; q < 2; ++q) d.g[7 + q] = vload<CPL>(g2 + slot<L>(2, so, q) * C);
+  const float* rp = rad + e * 12 * C + c;
+#pragma unroll
+  for (int q = 0; q < 6; ++q) d.r[q] = vload<CPL>(rp + slot<L>(6, so, q) * C);
+}
+
+// v (the node's own row, csd added) is read from the wave's LDS copy, so that it holds no
+// VGPRs across the loop; the registers go to the edges in flight instead.
 template <int CPL>
-__device__ __forceinline__ void side_apply(const SideEdge<CPL>& d, int64_t e, int so, int c, const Rows9<CPL>& v,
+__device__ __forceinline__ Vec<CPL> lds_row(const float* sv, int k, int c) {
+  return vload<CPL>(sv + k * (64 * CPL) + c);
+}
+
+template <int CPL, int L>
+__device__ __forceinline__ void side_apply(const SideEdge<CPL>& d, int64_t e, int so, int c, const float* sv,
                                            Rows9<CPL>& acc, float* __restrict__ g_rad, float* __restrict__ gw_out,
                                            int lane) {
   constexpr int C = 64 * CPL;
-  Rows9<CPL> rv;
-  rotate9(d.w, v, rv);
-  // this side's radial gradients (blocks so, 2+so, ..., 10+so)
-  float* gr = g_rad + e * 12 * C + so * C + c;
-  vstore(gr + 0 * C, vmul(d.g[0], rv.r[0]));
-  vstore(gr + 2 * C, vmul(d.g[1], rv.r[2]));
-  vstore(gr + 4 * C, vmul(d.g[2], rv.r[6]));
-  vstore(gr + 6 * C, vadd(vmul(d.g[3], rv.r[3]), vmul(d.g[5], rv.r[1])));
-  vstore(gr + 8 * C, vadd(vmul(d.g[4], rv.r[7]), vmul(d.g[6], rv.r[5])));
-  vstore(gr + 10 * C, vadd(vmul(d.g[7], rv.r[8]), vmul(d.g[8], rv.r[4])));
+  float w[34];
+#pragma unroll
+  for (int q = 0; q < 34; ++q) w[q] = read_lane(d.wl, q);
+  {
+    Rows9<CPL> v, rv;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) v.r[k] = lds_row<CPL>(sv, k, c);
+    rotate9(w, v, rv);
+    // this side's radial gradients (reference blocks so, 2+so, ..., 10+so)
+    float* gr = g_rad + e * 12 * C + c;
+    vstore(gr + slot<L>(6, so, 0) * C, vmul(d.g[0], rv.r[0]));
+    vstore(gr + slot<L>(6, so, 1) * C, vmul(d.g[1], rv.r[2]));
+    vstore(gr + slot<L>(6, so, 2) * C, vmul(d.g[2], rv.r[6]));
+    vstore(gr + slot<L>(6, so, 3) * C, vadd(vmul(d.g[3], rv.r[3]), vmul(d.g[5], rv.r[1])));
+    vstore(gr + slot<L>(6, so, 4) * C, vadd(vmul(d.g[4], rv.r[7]), vmul(d.g[6], rv.r[5])));
+    vstore(gr + slot<L>(6, so, 5) * C, vadd(vmul(d.g[7], rv.r[8]), vmul(d.g[8], rv.r[4])));
+  }
   // gradient w.r.t. the rotated coefficients of this node's row
   Rows9<CPL> grv;
   grv.r[0] = vmul(d.g[0], d.r[0]);
@@ -171,53 +203,86 @@ __device__ __forceinline__ void side_apply(const SideEdge<CPL>& d, int64_t e, in
   grv.r[5] = vmul(d.g[6], d.r[4]);
   grv.r[8] = vmul(d.g[7], d.r[5]);
   grv.r[4] = vmul(d.g[8], d.r[5]);
-  add_rotate9_t(d.w, grv, acc);
-  // this side's g_wigner: dL/dD1[a][b] = sum_c grv[1+a] v[1+b], dL/dD2[a][b] = sum_c grv[4+a] v[4+b]
-  float part[64];
+  add_rotate9_t(w, grv, acc);
+  // this side's g_wigner: dL/dD1[a][b] = sum_c grv[1+a] v[1+b], dL/dD2[a][b] = sum_c grv[4+a] v[4+b],
+  // reduced in two batches (entries 0..23 as 32 values, 24..33 as 16) to bound live registers
+  {
+    float part[32];
 #pragma unroll
-  for (int a = 0; a < 3; ++a)
+    for (int b = 0; b < 3; ++b) {
+      const Vec<CPL> vb = lds_row<CPL>(sv, 1 + b, c);
 #pragma unroll
-    for (int b = 0; b < 3; ++b) part[3 * a + b] = vdot(grv.r[1 + a], v.r[1 + b]);
+      for (int a = 0; a < 3; ++a) part[3 * a + b] = vdot(grv.r[1 + a], vb);
+    }
 #pragma unroll
-  for (int a = 0; a < 5; ++a)
+    for (int b = 0; b < 5; ++b) {
+      const Vec<CPL> vb = lds_row<CPL>(sv, 4 + b, c);
 #pragma unroll
-    for (int b = 0; b < 5; ++b) part[9 + 5 * a + b] = vdot(grv.r[4 + a], v.r[4 + b]);
+      for (int a = 0; a < 3; ++a) part[9 + 5 * a + b] = vdot(grv.r[4 + a], vb);
+    }
 #pragma unroll
-  for (int q = 34; q < 64; ++q) part[q] = 0.0f;
-  const float tot = wave_multi_sum<64>(part, lane);
-  if (lane < 34) gw_out[e * 34 + lane] = tot;
+    for (int q = 24; q < 32; ++q) part[q] = 0.0f;
+    const float tot = wave_multi_sum<32>(part, lane);
+    if (lane < 24) gw_out[e * 34 + lane] = tot;
+  }
+  {
+    float part[16];
+#pragma unroll
+    for (int b = 0; b < 5; ++b) {
+      const Vec<CPL> vb = lds_row<CPL>(sv, 4 + b, c);
+#pragma unroll
+      for (int a = 3; a < 5; ++a) part[5 * (a - 3) + b] = vdot(grv.r[4 + a], vb);
+    }
+#pragma unroll
+    for (int q = 10; q < 16; ++q) part[q] = 0.0f;
+    const float tot = wave_multi_sum<16>(part, lane);
+    if (lane < 10) gw_out[e * 34 + 24 + lane] = tot;
+  }
 }
 
-// One side of one node's gather backward: walk the node's CSR segment in order, two edges
-// per iteration so that their loads overlap.
-template <int CPL>
+// One side of one node's gather backward: walk the node's CSR segment in order.  The
+// segment's edge ids are fetched 64 at a time into one VGPR (lane t holds the t-th id) and
+// broadcast with readlane; the loads of edge t+1 are issued before edge t is processed.
+template <int CPL, int L>
 __device__ __forceinline__ void gather_bwd_side(const float* __restrict__ gX0, const float* __restrict__ gX1,
                                                 const float* __restrict__ gX2, const float* __restrict__ wig,
                                                 const float* __restrict__ rad, const int32_t* __restrict__ ptr,
-                                                const int32_t* __restrict__ idx, int64_t n, int so,
-                                                const Rows9<CPL>& v, Rows9<CPL>& acc, float* __restrict__ g_rad,
+                                                const int32_t* __restrict__ idx, int64_t n, int so, const float* sv,
+                                                Rows9<CPL>& acc, float* __restrict__ g_rad,
                                                 float* __restrict__ gw_out, int lane) {
   const int c = lane * CPL;
   const int32_t k0 = ptr[n], k1 = ptr[n + 1];
-  int32_t k = k0;
-  for (; k + 1 < k1; k += 2) {
-    const int64_t ea = idx[k], eb = idx[k + 1];
-    SideEdge<CPL> da, db;
-    side_load<CPL>(gX0, gX1, gX2, wig, rad, ea, so, c, da);
-    side_load<CPL>(gX0, gX1, gX2, wig, rad, eb, so, c, db);
-    side_apply<CPL>(da, ea, so, c, v, acc, g_rad, gw_out, lane);
-    side_apply<CPL>(db, eb, so, c, v, acc, g_rad, gw_out, lane);
-  }
-  if (k < k1) {
-    const int64_t e = idx[k];
-    SideEdge<CPL> d;
-    side_load<CPL>(gX0, gX1, gX2, wig, rad, e, so, c, d);
-    side_apply<CPL>(d, e, so, c, v, acc, g_rad, gw_out, lane);
+  for (int32_t base = k0; base < k1; base += 64) {
+    const int cnt = (int)std::min<int32_t>(64, k1 - base);
+    const int32_t ids = lane < cnt ? idx[base + lane] : 0;
+    SideEdge<CPL> d0, d1;
+    int64_t e0 = __builtin_amdgcn_readlane(ids, 0);
+    side_load<CPL, L>(gX0, gX1, gX2, wig, rad, e0, so, c, lane, d0);
+    int t = 0;
+    // sched_barrier(0) keeps the scheduler from sinking the next edge's loads into the
+    // current edge's arithmetic, which would shrink the prefetch distance below one edge.
+    for (; t + 2 <= cnt; t += 2) {
+      const int64_t e1 = __builtin_amdgcn_readlane(ids, t + 1);
+      side_load<CPL, L>(gX0, gX1, gX2, wig, rad, e1, so, c, lane, d1);
+      __builtin_amdgcn_sched_barrier(0);
+      side_apply<CPL, L>(d0, e0, so, c, sv, acc, g_rad, gw_out, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + 2 < cnt) {
+        e0 = __builtin_amdgcn_readlane(ids, t + 2);
+        side_load<CPL, L>(gX0, gX1, gX2, wig, rad, e0, so, c, lane, d0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      side_apply<CPL, L>(d1, e1, so, c, sv, acc, g_rad, gw_out, lane);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (t < cnt) side_apply<CPL, L>(d0, e0, so, c, sv, acc, g_rad, gw_out, lane);
   }
 }
 
-template <int CPL>
-__global__ __launch_bounds__(256) void gather_bwd_kernel(
+// One node per 128-thread workgroup (wave 0: receiver segment, wave 1: sender segment); at
+// least 3 waves per SIMD, since the loop is bound by the number of edge loads in flight.
+template <int CPL, int L>
+__global__ __launch_bounds__(128, 3) void gather_bwd_kernel(
     const float* __restrict__ gX0, const float* __restrict__ gX1, const float* __restrict__ gX2,
     const float* __restrict__ x, const float* __restrict__ wig, const float* __restrict__ rad,
     const float* __restrict__ csd, const int64_t* __restrict__ batch, const int32_t* __restrict__ rptr,
@@ -225,26 +290,32 @@ __global__ __launch_bounds__(256) void gather_bwd_kernel(
     float* __restrict__ g_x, float* __restrict__ g_wig, float* __restrict__ g_rad, float* __restrict__ ws,
     int64_t N) {
   constexpr int C = 64 * CPL;
-  __shared__ __attribute__((aligned(16))) float s_send[2][9 * C];
+  __shared__ __attribute__((aligned(16))) float s_send[1][9 * C];
+  __shared__ __attribute__((aligned(16))) float s_v[2][9 * C];
   const int lane = threadIdx.x & 63;
   const int wave = wave_id_uniform();
-  const int node_local = wave >> 1;
-  const int side = wave & 1;  // 0: receiver segment, 1: sender segment
-  const int64_t n = (int64_t)blockIdx.x * 2 + node_local;
+  const int node_local = 0;
+  const int side = wave;  // 0: receiver segment, 1: sender segment
+  const int64_t n = (int64_t)blockIdx.x;
   const int c = lane * CPL;
   Rows9<CPL> acc;
 #pragma unroll
   for (int k = 0; k < 9; ++k) acc.r[k] = vzero<CPL>();
   if (n < N) {
-    Rows9<CPL> v;
+    // the node's own row (csd added on l = 0) in this wave's LDS slot; each lane reads back
+    // only the channels it wrote, so no barrier is needed
+    float* sv = s_v[wave];
     const float* xn = x + n * 9 * C + c;
 #pragma unroll
-    for (int k = 0; k < 9; ++k) v.r[k] = vload<CPL>(xn + k * C);
-    v.r[0] = vadd(v.r[0], vload<CPL>(csd + batch[n] * C + c));
+    for (int k = 0; k < 9; ++k) {
+      Vec<CPL> r = vload<CPL>(xn + k * C);
+      if (k == 0) r = vadd(r, vload<CPL>(csd + batch[n] * C + c));
+      vstore(sv + k * C + c, r);
+    }
     if (side == 0) {
-      gather_bwd_side<CPL>(gX0, gX1, gX2, wig, rad, rptr, ridx, n, 1, v, acc, g_rad, g_wig, lane);
+      gather_bwd_side<CPL, L>(gX0, gX1, gX2, wig, rad, rptr, ridx, n, 1, sv, acc, g_rad, g_wig, lane);
     } else {
-      gather_bwd_side<CPL>(gX0, gX1, gX2, wig, rad, sptr, sidx, n, 0, v, acc, g_rad, ws, lane);
+      gather_bwd_side<CPL, L>(gX0, gX1, gX2, wig, rad, sptr, sidx, n, 0, sv, acc, g_rad, ws, lane);
 #pragma unroll
       for (int k = 0; k < 9; ++k) vstore(&s_send[node_local][k * C + c], acc.r[k]);
     }
@@ -263,26 +334,39 @@ __global__ __launch_bounds__(256) void add_inplace_kernel(float* __restrict__ a,
     a[k] += b[k];
 }
 
-template <int CPL>
+template <int CPL, int L>
 static void launch_gather_fwd(const float* x, const int64_t* idx_i, const int64_t* idx_j, const float* wigner,
                               const float* rad, const float* csd, const int64_t* batch, float* X0, float* X1,
                               float* X2, int64_t E, hipStream_t st) {
-  hipLaunchKernelGGL(gather_fwd_kernel<CPL>, dim3((unsigned)std::min<int64_t>(cdiv(E, 4), 8192)), dim3(256), 0, st, x, idx_i, idx_j, wigner, rad,
+  hipLaunchKernelGGL((gather_fwd_kernel<CPL, L>), dim3((unsigned)std::min<int64_t>(cdiv(E, 4), 8192)), dim3(256), 0, st, x, idx_i, idx_j, wigner, rad,
                      csd, batch, X0, X1, X2, E);
 }
 
-template <int CPL>
+template <int CPL, int L>
 static void launch_gather_bwd(const float* gX0, const float* gX1, const float* gX2, const float* x,
                               const float* wigner, const float* rad, const float* csd, const int64_t* batch,
                               const int32_t* rptr, const int32_t* ridx, const int32_t* sptr, const int32_t* sidx,
                               float* g_x, float* g_wig, float* g_rad, float* ws, int64_t N, hipStream_t st) {
-  hipLaunchKernelGGL(gather_bwd_kernel<CPL>, dim3(cdiv(N, 2)), dim3(256), 0, st, gX0, gX1, gX2, x, wigner, rad, csd,
+  hipLaunchKernelGGL((gather_bwd_kernel<CPL, L>), dim3((unsigned)N), dim3(128), 0, st, gX0, gX1, gX2, x, wigner, rad, csd,
                      batch, rptr, ridx, sptr, sidx, g_x, g_wig, g_rad, ws, N);
 }
 
 }  // namespace fu
 
 using namespace fu;
+
+// Instantiate f for CPL = C / 64 and the slot layout.
+template <typename F>
+static void with_c_layout(int32_t C, int32_t layout, F f) {
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I4 = std::integral_constant<int, 4>;
+  using L0 = std::integral_constant<int, 0>;
+  using L1 = std::integral_constant<int, 1>;
+  if (C == 64) layout ? f(I1{}, L1{}) : f(I1{}, L0{});
+  else if (C == 128) layout ? f(I2{}, L1{}) : f(I2{}, L0{});
+  else layout ? f(I4{}, L1{}) : f(I4{}, L0{});
+}
 
 static int check_c(int32_t C, const char* who) {
   if (C != 64 && C != 128 && C != 256)
@@ -292,8 +376,10 @@ static int check_c(int32_t C, const char* who) {
 
 extern "C" int fu_gather_fwd(const float* x, const int64_t* idx_i, const int64_t* idx_j, const float* wigner,
                              const float* rad, const float* csd_emb, const int64_t* batch, float* X_m0, float* X_m1,
-                             float* X_m2, int64_t E, int64_t N, int64_t S, int32_t C, void* stream) {
+                             float* X_m2, int64_t E, int64_t N, int64_t S, int32_t C, int32_t layout,
+                             void* stream) {
   if (E < 0 || N < 0 || S < 1) return set_error(FU_ERR_SHAPE, "fu_gather_fwd: bad shape");
+  if (layout != 0 && layout != 1) return set_error(FU_ERR_UNSUPPORTED, "fu_gather_fwd: layout %d", layout);
   int st = check_c(C, "fu_gather_fwd");
   if (st != FU_OK) return st;
   if (E == 0) return FU_OK;
@@ -303,9 +389,10 @@ extern "C" int fu_gather_fwd(const float* x, const int64_t* idx_i, const int64_t
   for (const void* p : al)
     if (!aligned16(p)) return set_error(FU_ERR_ALIGN, "fu_gather_fwd: feature arrays must be 16-byte aligned");
   hipStream_t s = as_stream(stream);
-  if (C == 64) launch_gather_fwd<1>(x, idx_i, idx_j, wigner, rad, csd_emb, batch, X_m0, X_m1, X_m2, E, s);
-  else if (C == 128) launch_gather_fwd<2>(x, idx_i, idx_j, wigner, rad, csd_emb, batch, X_m0, X_m1, X_m2, E, s);
-  else launch_gather_fwd<4>(x, idx_i, idx_j, wigner, rad, csd_emb, batch, X_m0, X_m1, X_m2, E, s);
+  with_c_layout(C, layout, [&](auto cpl, auto lay) {
+    launch_gather_fwd<decltype(cpl)::value, decltype(lay)::value>(x, idx_i, idx_j, wigner, rad, csd_emb, batch, X_m0,
+                                                                  X_m1, X_m2, E, s);
+  });
   return check_launch("fu_gather_fwd");
 }
 
@@ -314,28 +401,26 @@ extern "C" int fu_gather_bwd(const float* g_X_m0, const float* g_X_m1, const flo
                              const float* csd_emb, const int64_t* batch, const int32_t* recv_ptr,
                              const int32_t* recv_idx, const int32_t* send_ptr, const int32_t* send_idx, float* g_x,
                              float* g_wigner, float* g_rad, float* g_wig_ws, int64_t E, int64_t N, int64_t S,
-                             int32_t C, void* stream) {
+                             int32_t C, int32_t layout, void* stream) {
   (void)idx_i;
   (void)idx_j;
   if (E < 0 || N < 0 || S < 1) return set_error(FU_ERR_SHAPE, "fu_gather_bwd: bad shape");
+  if (layout != 0 && layout != 1) return set_error(FU_ERR_UNSUPPORTED, "fu_gather_bwd: layout %d", layout);
   int st = check_c(C, "fu_gather_bwd");
   if (st != FU_OK) return st;
   if (N == 0) return FU_OK;
+  if (N > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "fu_gather_bwd: N too large");
   if (!x || !csd_emb || !batch || !recv_ptr || !send_ptr || !g_x)
     return set_error(FU_ERR_NULL, "fu_gather_bwd: NULL argument");
   if (E > 0 && (!g_X_m0 || !g_X_m1 || !g_X_m2 || !wigner || !rad || !recv_idx || !send_idx || !g_wigner || !g_rad ||
                 !g_wig_ws))
     return set_error(FU_ERR_NULL, "fu_gather_bwd: NULL argument");
   hipStream_t s = as_stream(stream);
-  if (C == 64)
-    launch_gather_bwd<1>(g_X_m0, g_X_m1, g_X_m2, x, wigner, rad, csd_emb, batch, recv_ptr, recv_idx, send_ptr,
-                         send_idx, g_x, g_wigner, g_rad, g_wig_ws, N, s);
-  else if (C == 128)
-    launch_gather_bwd<2>(g_X_m0, g_X_m1, g_X_m2, x, wigner, rad, csd_emb, batch, recv_ptr, recv_idx, send_ptr,
-                         send_idx, g_x, g_wigner, g_rad, g_wig_ws, N, s);
-  else
-    launch_gather_bwd<4>(g_X_m0, g_X_m1, g_X_m2, x, wigner, rad, csd_emb, batch, recv_ptr, recv_idx, send_ptr,
-                         send_idx, g_x, g_wigner, g_rad, g_wig_ws, N, s);
+  with_c_layout(C, layout, [&](auto cpl, auto lay) {
+    launch_gather_bwd<decltype(cpl)::value, decltype(lay)::value>(g_X_m0, g_X_m1, g_X_m2, x, wigner, rad, csd_emb,
+                                                                  batch, recv_ptr, recv_idx, send_ptr, send_idx, g_x,
+                                                                  g_wigner, g_rad, g_wig_ws, N, s);
+  });
   st = check_launch("fu_gather_bwd");
   if (st != FU_OK || E == 0) return st;
   const int64_t tot = E * 34;

@@ -14,13 +14,6 @@
 
 namespace fu {
 
-template <int LPR>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
 struct LnArgs {
   const float* x; int64_t ldx;
   const float* tab_src; const float* tab_dst; int64_t ldt;
@@ -29,48 +22,64 @@ struct LnArgs {
   int64_t M; int32_t G;
 };
 
+// Table rows of one input row (nullptr without tables).
+struct RowTabs {
+  const float* src;
+  const float* dst;
+};
+
+__device__ __forceinline__ RowTabs row_tables(const LnArgs& a, int64_t row) {
+  if (a.tab_src == nullptr) return {nullptr, nullptr};
+  return {a.tab_src + a.z[a.isrc[row]] * a.ldt, a.tab_dst + a.z[a.idst[row]] * a.ldt};
+}
+
 // x + tables + bias for the 4 values of this lane in (row, group)
 template <int D>
-__device__ __forceinline__ float4 ln_input(const LnArgs& a, int64_t row, int g, int sub) {
+__device__ __forceinline__ float4 ln_input(const LnArgs& a, const RowTabs& t, int64_t row, int g, int sub) {
   const int col = g * D + 4 * sub;
   float4 v = ld4(a.x + row * a.ldx + col);
-  if (a.tab_src != nullptr) {
-    v = v + ld4(a.tab_src + a.z[a.isrc[row]] * a.ldt + col);
-    v = v + ld4(a.tab_dst + a.z[a.idst[row]] * a.ldt + col);
-  }
+  if (t.src != nullptr) v = v + ld4(t.src + col) + ld4(t.dst + col);
   if (a.bias != nullptr) v = v + ld4(a.bias + col);
   return v;
 }
 
+// One (row, group) of the forward: LayerNorm statistics over the group's D values, affine, SiLU.
+template <int LPR>
+__device__ __forceinline__ void ln_fwd_item(const LnArgs& a, const RowTabs& t, int64_t row, int g, int sub,
+                                            float* __restrict__ out, int64_t ldo, float* __restrict__ mean_out,
+                                            float* __restrict__ rstd_out, float eps) {
+  constexpr int D = 4 * LPR;
+  const float4 v = ln_input<D>(a, t, row, g, sub);
+  const float mean = group_sum<LPR>(v.x + v.y + v.z + v.w) / D;
+  const float4 xc = make_float4(v.x - mean, v.y - mean, v.z - mean, v.w - mean);
+  const float var = group_sum<LPR>(xc.x * xc.x + xc.y * xc.y + xc.z * xc.z + xc.w * xc.w) / D;
+  const float rstd = 1.0f / sqrtf(var + eps);
+  const float4 gm = ld4(a.gamma + g * D + 4 * sub), bt = ld4(a.beta + g * D + 4 * sub);
+  float4 y;
+  y.x = xc.x * rstd * gm.x + bt.x;
+  y.y = xc.y * rstd * gm.y + bt.y;
+  y.z = xc.z * rstd * gm.z + bt.z;
+  y.w = xc.w * rstd * gm.w + bt.w;
+  st4(out + row * ldo + g * D + 4 * sub,
+      make_float4(y.x * sigmoidf_(y.x), y.y * sigmoidf_(y.y), y.z * sigmoidf_(y.z), y.w * sigmoidf_(y.w)));
+  if (sub == 0) {
+    mean_out[row * a.G + g] = mean;
+    rstd_out[row * a.G + g] = rstd;
+  }
+}
+
+// Rows are spread over LPR-lane groups (256 / LPR rows per block, grid-stride); each group
+// walks the G column groups of its row, so the table rows are located once per row.
 template <int LPR>
 __global__ __launch_bounds__(256) void ln_silu_fwd_kernel(LnArgs a, float* __restrict__ out, int64_t ldo,
                                                           float* __restrict__ mean_out, float* __restrict__ rstd_out,
                                                           float eps) {
-  constexpr int D = 4 * LPR;
-  constexpr int RPB = 256 / LPR;  // (row, group) items per block
+  constexpr int RPB = 256 / LPR;
   const int sub = threadIdx.x % LPR;
-  const int64_t items = a.M * a.G;
   const int64_t step = (int64_t)gridDim.x * RPB;
-  for (int64_t it = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR; it < items; it += step) {
-    const int64_t row = it / a.G;
-    const int g = (int)(it - row * a.G);
-    const float4 v = ln_input<D>(a, row, g, sub);
-    const float mean = group_sum<LPR>(v.x + v.y + v.z + v.w) / D;
-    const float4 xc = make_float4(v.x - mean, v.y - mean, v.z - mean, v.w - mean);
-    const float var = group_sum<LPR>(xc.x * xc.x + xc.y * xc.y + xc.z * xc.z + xc.w * xc.w) / D;
-    const float rstd = 1.0f / sqrtf(var + eps);
-    const float4 gm = ld4(a.gamma + g * D + 4 * sub), bt = ld4(a.beta + g * D + 4 * sub);
-    float4 y;
-    y.x = xc.x * rstd * gm.x + bt.x;
-    y.y = xc.y * rstd * gm.y + bt.y;
-    y.z = xc.z * rstd * gm.z + bt.z;
-    y.w = xc.w * rstd * gm.w + bt.w;
-    st4(out + row * ldo + g * D + 4 * sub,
-        make_float4(y.x * sigmoidf_(y.x), y.y * sigmoidf_(y.y), y.z * sigmoidf_(y.z), y.w * sigmoidf_(y.w)));
-    if (sub == 0) {
-      mean_out[it] = mean;
-      rstd_out[it] = rstd;
-    }
+  for (int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR; row < a.M; row += step) {
+    const RowTabs t = row_tables(a, row);
+    for (int g = 0; g < a.G; ++g) ln_fwd_item<LPR>(a, t, row, g, sub, out, ldo, mean_out, rstd_out, eps);
   }
 }
 
@@ -80,47 +89,53 @@ __device__ __forceinline__ float dsilu(float y) {
 }
 
 template <int LPR>
+__device__ __forceinline__ void ln_bwd_item(const LnArgs& a, const RowTabs& t, int64_t row, int g, int sub,
+                                            const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
+                                            const float* __restrict__ g_out, int64_t ldg, float* __restrict__ g_x,
+                                            int64_t ldgx) {
+  constexpr int D = 4 * LPR;
+  const float4 v = ln_input<D>(a, t, row, g, sub);
+  const float4 go = ld4(g_out + row * ldg + g * D + 4 * sub);
+  const float4 gm = ld4(a.gamma + g * D + 4 * sub), bt = ld4(a.beta + g * D + 4 * sub);
+  const float mean = mean_in[row * a.G + g], rstd = rstd_in[row * a.G + g];
+  const float xh[4] = {(v.x - mean) * rstd, (v.y - mean) * rstd, (v.z - mean) * rstd, (v.w - mean) * rstd};
+  const float gg[4] = {gm.x, gm.y, gm.z, gm.w}, bb[4] = {bt.x, bt.y, bt.z, bt.w}, gov[4] = {go.x, go.y, go.z, go.w};
+  float gxh[4];
+  float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float y = xh[k] * gg[k] + bb[k];
+    gxh[k] = gov[k] * dsilu(y) * gg[k];
+    s1 += gxh[k];
+    s2 += gxh[k] * xh[k];
+  }
+  s1 = group_sum<LPR>(s1);
+  s2 = group_sum<LPR>(s2);
+  float4 o;
+  o.x = rstd * (gxh[0] - (s1 + xh[0] * s2) / D);
+  o.y = rstd * (gxh[1] - (s1 + xh[1] * s2) / D);
+  o.z = rstd * (gxh[2] - (s1 + xh[2] * s2) / D);
+  o.w = rstd * (gxh[3] - (s1 + xh[3] * s2) / D);
+  st4(g_x + row * ldgx + g * D + 4 * sub, o);
+}
+
+template <int LPR>
 __global__ __launch_bounds__(256) void ln_silu_bwd_kernel(LnArgs a, const float* __restrict__ mean_in,
                                                           const float* __restrict__ rstd_in,
                                                           const float* __restrict__ g_out, int64_t ldg,
                                                           float* __restrict__ g_x, int64_t ldgx) {
-  constexpr int D = 4 * LPR;
   constexpr int RPB = 256 / LPR;
   const int sub = threadIdx.x % LPR;
-  const int64_t items = a.M * a.G;
   const int64_t step = (int64_t)gridDim.x * RPB;
-  for (int64_t it = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR; it < items; it += step) {
-    const int64_t row = it / a.G;
-    const int g = (int)(it - row * a.G);
-    const float4 v = ln_input<D>(a, row, g, sub);
-    const float4 go = ld4(g_out + row * ldg + g * D + 4 * sub);
-    const float4 gm = ld4(a.gamma + g * D + 4 * sub), bt = ld4(a.beta + g * D + 4 * sub);
-    const float mean = mean_in[it], rstd = rstd_in[it];
-    const float xh[4] = {(v.x - mean) * rstd, (v.y - mean) * rstd, (v.z - mean) * rstd, (v.w - mean) * rstd};
-    const float gg[4] = {gm.x, gm.y, gm.z, gm.w}, bb[4] = {bt.x, bt.y, bt.z, bt.w}, gov[4] = {go.x, go.y, go.z, go.w};
-    float gxh[4];
-    float s1 = 0.0f, s2 = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float y = xh[k] * gg[k] + bb[k];
-      gxh[k] = gov[k] * dsilu(y) * gg[k];
-      s1 += gxh[k];
-      s2 += gxh[k] * xh[k];
-    }
-    s1 = group_sum<LPR>(s1);
-    s2 = group_sum<LPR>(s2);
-    float4 o;
-    o.x = rstd * (gxh[0] - (s1 + xh[0] * s2) / D);
-    o.y = rstd * (gxh[1] - (s1 + xh[1] * s2) / D);
-    o.z = rstd * (gxh[2] - (s1 + xh[2] * s2) / D);
-    o.w = rstd * (gxh[3] - (s1 + xh[3] * s2) / D);
-    st4(g_x + row * ldgx + g * D + 4 * sub, o);
+  for (int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR; row < a.M; row += step) {
+    const RowTabs t = row_tables(a, row);
+    for (int g = 0; g < a.G; ++g) ln_bwd_item<LPR>(a, t, row, g, sub, mean_in, rstd_in, g_out, ldg, g_x, ldgx);
   }
 }
 
-static unsigned ln_blocks(int64_t items, int D) {
+static unsigned ln_blocks(int64_t rows, int D) {
   const int rpb = 256 / (D / 4);
-  return (unsigned)std::min<int64_t>(cdiv(items, rpb), 65536);
+  return (unsigned)std::min<int64_t>(cdiv(rows, rpb), 65536);
 }
 
 static int ln_check(const LnArgs& a, int64_t ld_out, int32_t D, const char* who) {
@@ -159,7 +174,7 @@ extern "C" int fu_ln_silu_grouped_fwd(const float* x, int64_t ldx, const float* 
   if (M == 0) return FU_OK;
   if (!out || !mean || !rstd || !aligned16(out)) return set_error(FU_ERR_NULL, "fu_ln_silu_grouped_fwd: bad output");
   hipStream_t s = as_stream(stream);
-  const unsigned blocks = ln_blocks(M * G, D);
+  const unsigned blocks = ln_blocks(M, D);
   ln_dispatch(D, [&](auto lpr) {
     hipLaunchKernelGGL(ln_silu_fwd_kernel<decltype(lpr)::value>, dim3(blocks), dim3(256), 0, s, a, out, ldo, mean,
                        rstd, eps);
@@ -180,7 +195,7 @@ extern "C" int fu_ln_silu_grouped_bwd(const float* x, int64_t ldx, const float* 
       !aligned16(g_x))
     return set_error(FU_ERR_NULL, "fu_ln_silu_grouped_bwd: bad gradient arguments");
   hipStream_t s = as_stream(stream);
-  const unsigned blocks = ln_blocks(M * G, D);
+  const unsigned blocks = ln_blocks(M, D);
   ln_dispatch(D, [&](auto lpr) {
     hipLaunchKernelGGL(ln_silu_bwd_kernel<decltype(lpr)::value>, dim3(blocks), dim3(256), 0, s, a, mean, rstd, g_out,
                        ldg, g_x, ldgx);

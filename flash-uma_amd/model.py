@@ -20,7 +20,7 @@ from collections import OrderedDict
 import torch
 import torch.nn as nn
 
-from ops.gather import gather_wigner_split
+from ops.gather import SIDE_MAJOR_PERM, block_permutation, gather_wigner_split
 from ops.gating import fused_gating_split
 from ops.geom import precompute_geometry
 from ops.linear import linear
@@ -101,6 +101,7 @@ class Packed_eSCN_Layer(nn.Module):
 
         self.norm_1 = None; self.norm_2 = None; self.atom_wise = None
         self.prepared = False
+        self.layout = 0  # gather slot layout; 1 (side-major) after prepare_for_inference
 
     @staticmethod
     def _pack(R: torch.Tensor, I: torch.Tensor) -> torch.Tensor:
@@ -118,13 +119,22 @@ class Packed_eSCN_Layer(nn.Module):
             for mod in (self.norm_1, self.norm_2, self.atom_wise):
                 for p in mod.parameters():
                     p.requires_grad = False
+        # Side-major slot layout (ops/gather.py): the radial output blocks and the conv1 input
+        # columns are permuted alike, so rad -> X -> conv1 computes the same products while
+        # each side's share of an edge row is contiguous for the gather backward.
+        C = self.C
+        p_rad = block_permutation(SIDE_MAJOR_PERM["rad"], C).to(self.W_rad1_3.device)
+        self.W_rad1_3.data = self.W_rad1_3.data[p_rad].contiguous()
+        self.b_rad1_3.data = self.b_rad1_3.data[p_rad].contiguous()
+        cols = {m: block_permutation(SIDE_MAJOR_PERM[m], C).to(self.W1_m0.device) for m in ("m0", "m1", "m2")}
         for name in ("W_rad1_1", "W_rad1_2", "W_rad1_3"):
             W = getattr(self, name).data
             self.register_buffer(name + "_t", W.to(dtype).t().contiguous())
-        self._register("W_conv1_m0", self.W1_m0.data, dtype)
+        self._register("W_conv1_m0", self.W1_m0.data[:, cols["m0"]], dtype)
         self.register_buffer("b_conv1_m0", _frozen(self.b1_m0.data).to(dtype))
-        self._register("W_conv1_m1", self._pack(self.W1_m1_R.data, self.W1_m1_I.data), dtype)
-        self._register("W_conv1_m2", self._pack(self.W1_m2_R.data, self.W1_m2_I.data), dtype)
+        self._register("W_conv1_m1", self._pack(self.W1_m1_R.data, self.W1_m1_I.data)[:, cols["m1"]], dtype)
+        self._register("W_conv1_m2", self._pack(self.W1_m2_R.data, self.W1_m2_I.data)[:, cols["m2"]], dtype)
+        self.layout = 1
         self._register("W_conv2_m0", self.W2_m0.data, dtype)
         self.register_buffer("b_conv2_m0", _frozen(self.b2_m0.data).to(dtype))
         self._register("W_conv2_m1", self._pack(self.W2_m1_R.data, self.W2_m1_I.data), dtype)
@@ -152,7 +162,8 @@ class Packed_eSCN_Layer(nn.Module):
         x_norm = self.norm_1(x_in)
         if rad_out is None:
             rad_out = self.radial(x_edge_raw)
-        X_m0, X_m1, X_m2 = gather_wigner_split(x_norm, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology)
+        X_m0, X_m1, X_m2 = gather_wigner_split(x_norm, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology,
+                                               self.layout)
         Y_m0 = linear(X_m0, self.W_conv1_m0, self.b_conv1_m0, self.W_conv1_m0_t)
         Y_m1 = linear(X_m1, self.W_conv1_m1, None, self.W_conv1_m1_t)
         Y_m2 = linear(X_m2, self.W_conv1_m2, None, self.W_conv1_m2_t)

@@ -28,8 +28,8 @@ SIGNATURES: dict[str, list] = {
     "fu_geom_fwd": [P, P, P, P, P, P, P, P, P, I64, P, P, I64, I64, I32, I32, F32, F32, P],
     "fu_geom_bwd": [P, P, P, P, P, P, I64, P, P, P, I64, I64, I32, F32, F32, P],
     "fu_edge_vec_reduce": [P, P, P, P, P, P, I64, I64, P],
-    "fu_gather_fwd": [P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, P],
-    "fu_gather_bwd": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, P],
+    "fu_gather_fwd": [P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, I32, P],
+    "fu_gather_bwd": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, I32, P],
     "fu_gating_fwd": [P, P, P, P, P, P, I64, I32, P],
     "fu_gating_bwd": [P, P, P, P, P, P, P, P, P, I64, I32, P],
     "fu_scatter_fwd": [P, P, P, P, P, P, P, P, P, I64, I64, I32, P],

@@ -1,7 +1,13 @@
 """gather_wigner_split (ops/gather.py:408-516) on the gfx950 gather kernels.
 
 The backward is node-centric over the receiver and sender CSRs (no atomics, bitwise
-reproducible); it needs both CSRs, taken from the cached topology when given."""
+reproducible); it needs both CSRs, taken from the cached topology when given.
+
+layout 0 keeps the reference's column-block order of X_m* and rad_out (sender/receiver
+slots interleaved, ops/gather.py:132-154).  layout 1 ("side-major") stores each array's
+sender slots first and receiver slots second (SIDE_MAJOR_PERM below); the model uses it
+with conv1 and radial weights permuted to match, which leaves every product unchanged and
+lets each side of the backward read and write one contiguous run per edge."""
 from __future__ import annotations
 
 import torch
@@ -11,9 +17,23 @@ from .constants import RAD_MULT, X_M0_MULT, X_M1_MULT, X_M2_MULT
 from .topology import receiver_csr, sender_csr
 
 
+# Column-block permutation of layout 1: new block b holds reference block perm[b].
+SIDE_MAJOR_PERM = {
+    "m0": [0, 2, 4, 1, 3, 5],
+    "m1": [0, 2, 4, 6, 1, 3, 5, 7],
+    "m2": [0, 2, 1, 3],
+    "rad": [0, 2, 4, 6, 8, 10, 1, 3, 5, 7, 9, 11],
+}
+
+
+def block_permutation(perm, C: int) -> torch.Tensor:
+    """Column index map (len(perm) * C) of a block permutation with blocks of C columns."""
+    return torch.cat([torch.arange(p * C, (p + 1) * C) for p in perm])
+
+
 class GatherWignerSplit(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology=None):
+    def forward(ctx, x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology=None, layout=0):
         x_in = _lib.require(x_in, torch.float32, "x_in")
         idx_i = _lib.require(idx_i, torch.int64, "idx_i")
         idx_j = _lib.require(idx_j, torch.int64, "idx_j")
@@ -31,9 +51,9 @@ class GatherWignerSplit(torch.autograd.Function):
         X_m2 = torch.empty((E, X_M2_MULT * C), device=dev, dtype=torch.float32)
         _lib.call("fu_gather_fwd", x_in.data_ptr(), idx_i.data_ptr(), idx_j.data_ptr(), wigner.data_ptr(),
                   rad_out.data_ptr(), csd_emb.data_ptr(), batch.data_ptr(), X_m0.data_ptr(), X_m1.data_ptr(),
-                  X_m2.data_ptr(), E, N, csd_emb.shape[0], C, _lib.stream_ptr(dev))
+                  X_m2.data_ptr(), E, N, csd_emb.shape[0], C, int(layout), _lib.stream_ptr(dev))
         ctx.save_for_backward(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch)
-        ctx.topology = topology
+        ctx.topology, ctx.layout = topology, int(layout)
         return X_m0, X_m1, X_m2
 
     @staticmethod
@@ -59,10 +79,10 @@ class GatherWignerSplit(torch.autograd.Function):
                   idx_i.data_ptr(), idx_j.data_ptr(), wigner.data_ptr(), rad_out.data_ptr(), csd_emb.data_ptr(),
                   batch.data_ptr(), rptr.data_ptr(), ridx.data_ptr(), sptr.data_ptr(), sidx.data_ptr(),
                   g_x.data_ptr(), g_wigner.data_ptr(), g_rad.data_ptr(), ws.data_ptr(), E, N, csd_emb.shape[0], C,
-                  _lib.stream_ptr(dev))
+                  ctx.layout, _lib.stream_ptr(dev))
         # no gradient for csd_emb or batch (ops/gather.py:513-514)
-        return g_x, None, None, g_wigner, g_rad, None, None, None
+        return g_x, None, None, g_wigner, g_rad, None, None, None, None
 
 
-def gather_wigner_split(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology=None):
-    return GatherWignerSplit.apply(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology)
+def gather_wigner_split(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology=None, layout=0):
+    return GatherWignerSplit.apply(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology, layout)

@@ -81,22 +81,28 @@ int fu_edge_vec_reduce(const float* g_d, const int32_t* recv_ptr, const int32_t*
 
 /* ops/gather.py:34-154 (_gather_split_fwd_kernel): rotate sender/receiver rows of
  * x (N, 9, C) (+ csd_emb[batch] on l=0) into the edge frame, scale by rad (E, 12C) and
- * write the X_m0/X_m1/X_m2 blocks. */
+ * write the X_m0/X_m1/X_m2 blocks.
+ * layout 0: the reference column-block order of X and rad (sender/receiver slots
+ * interleaved, ops/gather.py:132-154).  layout 1: per array, all sender slots first, then
+ * all receiver slots, each side in reference order (block q of side s at s*per_side + q);
+ * the model pairs it with conv1 / radial weights permuted the same way, which leaves every
+ * product unchanged and makes each side's share of an edge row contiguous. */
 int fu_gather_fwd(const float* x, const int64_t* idx_i, const int64_t* idx_j, const float* wigner,
                   const float* rad, const float* csd_emb, const int64_t* batch, float* X_m0,
                   float* X_m1, float* X_m2, int64_t E, int64_t N, int64_t S, int32_t C,
-                  void* stream);
+                  int32_t layout, void* stream);
 
 /* ops/gather.py:160-405 (both backward kernels) without atomics.  One workgroup per node
  * sums the node's receiver segment (recv CSR) and sender segment (send CSR) in CSR order,
  * writing g_x (N, 9, C), g_rad (E, 12C) and g_wigner (E, 34).  g_wig_ws is an (E, 34)
- * scratch array for the sender-side halves of g_wigner. */
+ * scratch array for the sender-side halves of g_wigner.  layout as in fu_gather_fwd (g_X and
+ * g_rad use the same order as X and rad). */
 int fu_gather_bwd(const float* g_X_m0, const float* g_X_m1, const float* g_X_m2, const float* x,
                   const int64_t* idx_i, const int64_t* idx_j, const float* wigner, const float* rad,
                   const float* csd_emb, const int64_t* batch, const int32_t* recv_ptr,
                   const int32_t* recv_idx, const int32_t* send_ptr, const int32_t* send_idx,
                   float* g_x, float* g_wigner, float* g_rad, float* g_wig_ws, int64_t E,
-                  int64_t N, int64_t S, int32_t C, void* stream);
+                  int64_t N, int64_t S, int32_t C, int32_t layout, void* stream);
 
 /* ------------------------------------------------------------------------------------
  * Gate activation (replaces FusedGatingSplit, ops/gating.py:188-234)

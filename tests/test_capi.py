@@ -47,8 +47,10 @@ def test_error_codes():
     assert st == -2 and "multiples of 4" in msg
     st, _ = _status("fu_linear", 3, 8, 16, 8, None, 16, 8, 10, 8, 8, None)
     assert st == -3
-    st, _ = _status("fu_gather_fwd", *([None] * 10), 5, 5, 1, 96, None)
+    st, _ = _status("fu_gather_fwd", *([None] * 10), 5, 5, 1, 96, 0, None)
     assert st == -2
+    st, msg = _status("fu_gather_fwd", *([None] * 10), 5, 5, 1, 128, 2, None)
+    assert st == -2 and "layout" in msg
     st, _ = _status("fu_ln_silu_fwd", *([None] * 6), 4, 100, ctypes.c_float(1e-7), None)
     assert st == -2
     ws = ctypes.c_size_t(0)

@@ -175,15 +175,30 @@ def _gather_inputs(seed=4, N=40, E=300, C=128, S=1):
     return x, torch.from_numpy(ei), wig, rad, csd, batch
 
 
-def test_gather(cuda):
+@pytest.mark.parametrize("layout", [0, 1])
+def test_gather(cuda, layout):
+    """layout 1 stores the blocks of X_m* and rad side-major: the same values as the reference
+    layout under the block permutations SIDE_MAJOR_PERM (checked against the oracle, whose
+    outputs are in the reference order, by permuting its columns)."""
     gather, *_ = _ops()
     x, ei, wig, rad, csd, batch = _gather_inputs()
     C = x.shape[2]
-    xg, wg, rg = (t.to(cuda).requires_grad_(True) for t in (x, wig, rad))
-    X = gather.gather_wigner_split(xg, ei[0].to(cuda), ei[1].to(cuda), wg, rg, csd.to(cuda), batch.to(cuda))
+    if layout:
+        cols = {k: gather.block_permutation(v, C) for k, v in gather.SIDE_MAJOR_PERM.items()}
+        inv_rad = torch.argsort(cols["rad"])
+    perm = (lambda t, k: t[:, cols[k]]) if layout else (lambda t, k: t)
+    rad_k = perm(rad, "rad")  # the kernel's input in its own layout
+    xg, wg, rg = (t.to(cuda).requires_grad_(True) for t in (x, wig, rad_k))
+    X = gather.gather_wigner_split(xg, ei[0].to(cuda), ei[1].to(cuda), wg, rg, csd.to(cuda), batch.to(cuda),
+                                   None, layout)
     torch.manual_seed(5)
     cot = [torch.randn(t.shape) for t in X]
-    ref, gref = _vjp(lambda a, w, r: R.gather_rotate(a, ei[0], ei[1], w, r, csd.double(), batch), [x, wig, rad], cot)
+
+    def ref_fn(a, w, r):
+        out = R.gather_rotate(a, ei[0], ei[1], w, r[:, inv_rad] if layout else r, csd.double(), batch)
+        return tuple(perm(o, k) for o, k in zip(out, ("m0", "m1", "m2")))
+
+    ref, gref = _vjp(ref_fn, [x, wig, rad_k], cot)
     for a, b in zip(X, ref):
         assert_close(a, b, TOL, "gather fwd")
     g = torch.autograd.grad(X, (xg, wg, rg), [c.to(cuda) for c in cot])
@@ -198,7 +213,7 @@ def test_gather_deterministic(cuda):
     for _ in range(2):
         xg = x.to(cuda).requires_grad_(True)
         X = gather.gather_wigner_split(xg, ei[0].to(cuda), ei[1].to(cuda), wig.to(cuda), rad.to(cuda), csd.to(cuda),
-                                       batch.to(cuda))
+                                       batch.to(cuda), None, 1)
         torch.manual_seed(7)
         (g,) = torch.autograd.grad(X, xg, [torch.randn(t.shape).to(cuda) for t in X])
         outs.append(g.cpu())
