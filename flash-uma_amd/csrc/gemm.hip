@@ -7,10 +7,13 @@
 //
 // Tiling: a 256-thread workgroup (4 wave64s in a 2x2 grid) owns a 128x128 output tile; each
 // wave owns 64x64 = 2x2 MFMA blocks of 32x32 (64 fp32 accumulators per lane, held in AGPRs).
-// K advances in chunks of 16 staged through double-buffered LDS (40 KB, so three workgroups
-// fit on a CU).  Within a chunk, lane l (row/col l%32, half h = l/32) feeds the MFMA k-slot h
-// with chunk column 8h + t at step t, so each lane reads its 8 operands of a chunk with two
-// 16-byte LDS reads.  The epilogue stages each wave's 32-row slabs through LDS and writes
+// K advances in chunks of 16 staged through double-buffered LDS (32 KB of operands, 36 KB with
+// the epilogue staging: four workgroups per CU).  Within a chunk, lane l (row/col l%32, half h = l/32) feeds the MFMA k-slot h with
+// chunk column 8h + t at step t, so each lane reads its 8 operands of a chunk with two
+// 16-byte LDS reads.  LDS rows are 64 bytes (four 16-byte chunks) without padding; the chunk
+// index is XOR-swizzled with f(row) = ((row >> 1) ^ (row >> 2)) & 3, which makes both the
+// row-wise tile stores and the column-of-rows operand reads free of bank conflicts (for 32
+// and for 64 banks).  The epilogue stages each wave's 32-row slabs through LDS and writes
 // bias-added rows with 16-byte stores.
 #include "fu_common.h"
 
@@ -19,14 +22,18 @@ namespace fu {
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int GBM = 128, GBN = 128, GBK = 16;
-constexpr int GLDS = GBK + 4;      // padded LDS operand row (floats)
-constexpr int GES = 64 + 4;        // padded LDS epilogue row (floats)
-constexpr int G_LDS_FLOATS = 2 * (GBM + GBN) * GLDS;
-static_assert(4 * 32 * GES <= G_LDS_FLOATS, "epilogue staging must fit in the operand buffers");
+constexpr int GLDS = GBK;          // LDS operand row (floats): four swizzled 16-byte chunks
+constexpr int GES = 64 + 8;        // LDS epilogue row (floats); 4 * GES = 32 mod 64 banks
+constexpr int G_LDS_FLOATS = 2 * (GBM + GBN) * GLDS > 4 * 32 * GES ? 2 * (GBM + GBN) * GLDS : 4 * 32 * GES;
+
+// Float offset of 16-byte chunk `chunk` of LDS operand row `row`.
+__device__ __forceinline__ int lds_chunk(int row, int chunk) {
+  return row * GLDS + 4 * (chunk ^ (((row >> 1) ^ (row >> 2)) & 3));
+}
 
 // Batch index blockIdx.y offsets A, W and Y by sA, sW and sY floats; bias (stride sBias) is
 // added in batches [0, bias_batches).
-__global__ __launch_bounds__(256) void linear_mfma_kernel(const float* __restrict__ A, int64_t lda, int64_t sA,
+__global__ __launch_bounds__(256, 4) void linear_mfma_kernel(const float* __restrict__ A, int64_t lda, int64_t sA,
                                                           const float* __restrict__ W, int64_t ldw, int64_t sW,
                                                           const float* __restrict__ bias, int64_t sBias,
                                                           int32_t bias_batches, float* __restrict__ Y, int64_t ldy,
@@ -80,9 +87,8 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(const float* __restric
     for (int p = 0; p < 2; ++p) {
       const int lin = tid + 256 * p;
       const int r = lin >> 2;
-      const int kc = (lin & 3) * 4;
-      st4(&As[(buf * GBM + r) * GLDS + kc], ra[p]);
-      st4(&Bs[(buf * GBN + r) * GLDS + kc], rb[p]);
+      st4(&As[buf * GBM * GLDS + lds_chunk(r, lin & 3)], ra[p]);
+      st4(&Bs[buf * GBN * GLDS + lds_chunk(r, lin & 3)], rb[p]);
     }
   };
 
@@ -100,7 +106,7 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(const float* __restric
   __syncthreads();
 
   const int fr = lane & 31;         // operand row (A) / column (W) within a 32-block
-  const int fk = (lane >> 5) * 8;   // first chunk column this lane feeds
+  const int fh = lane >> 5;         // this lane feeds chunk columns 8 fh .. 8 fh + 7
 
   for (int kc = 0; kc < nk; ++kc) {
     const int buf = kc & 1;
@@ -109,12 +115,10 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(const float* __restric
     float af[2][8], bf[2][8];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const float* pa = &As[(buf * GBM + wr + i * 32 + fr) * GLDS + fk];
-      const float* pb = &Bs[(buf * GBN + wc + i * 32 + fr) * GLDS + fk];
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        const float4 va = ld4(pa + 4 * q);
-        const float4 vb = ld4(pb + 4 * q);
+        const float4 va = ld4(&As[buf * GBM * GLDS + lds_chunk(wr + i * 32 + fr, 2 * fh + q)]);
+        const float4 vb = ld4(&Bs[buf * GBN * GLDS + lds_chunk(wc + i * 32 + fr, 2 * fh + q)]);
         af[i][4 * q + 0] = va.x; af[i][4 * q + 1] = va.y; af[i][4 * q + 2] = va.z; af[i][4 * q + 3] = va.w;
         bf[i][4 * q + 0] = vb.x; bf[i][4 * q + 1] = vb.y; bf[i][4 * q + 2] = vb.z; bf[i][4 * q + 3] = vb.w;
       }
