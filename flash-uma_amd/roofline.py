@@ -8,7 +8,8 @@ achieved = algorithmic bytes (flops) / measured kernel time.
 Per-unit figures at C = 128, B = 64 (bytes per edge + bytes per node):
   gating fwd 10240 / bwd 15872; gather fwd 15512 + 4616, bwd 21784 + 9232;
   scatter fwd 4752 + 9220, bwd 9504 + 4608; init scatter fwd 1576 + 5640, bwd 3256 + 4608;
-  geom fwd 1448 (+ 1024 with embeddings) + 20, bwd 436 + 12; ln_silu 1032 / 1544 per row.
+  geom fwd 1448 (+ 1024 with embeddings) + 20, bwd 436 + 12; ln_silu 1032 / 1544 per row
+  (grouped: per row and group, plus 16 B of edge ids per row when the tables are used).
 """
 from __future__ import annotations
 
@@ -88,6 +89,25 @@ def _linear(a):
     return 4 * (M * K + M * N + N * K), 2 * M * N * K
 
 
+def _linear_batched(a):
+    M, N, K, B = a[12], a[13], a[14], a[15]
+    return 4 * B * (M * K + M * N + N * K), 2 * B * M * N * K
+
+
+def _ln_grouped_fwd(a):
+    # x read + out written per row and group, mean/rstd; with tables: two int64 edge ids per
+    # row and the (L2-resident) 100-row tables once per launch
+    M, G, D = a[15], a[16], a[17]
+    tab = (M * 16 + 2 * 100 * G * D * 4) if a[2] is not None else 0
+    return M * G * (2 * D * 4 + 8) + tab, 0
+
+
+def _ln_grouped_bwd(a):
+    M, G, D = a[17], a[18], a[19]
+    tab = (M * 16 + 2 * 100 * G * D * 4) if a[2] is not None else 0
+    return M * G * (3 * D * 4 + 8) + tab, 0
+
+
 WORK = {
     "fu_gating_fwd": _gating_fwd,
     "fu_gating_bwd": _gating_bwd,
@@ -102,10 +122,13 @@ WORK = {
     "fu_edge_vec_reduce": _edge_vec,
     "fu_ln_silu_fwd": _ln_fwd,
     "fu_ln_silu_bwd": _ln_bwd,
+    "fu_ln_silu_grouped_fwd": _ln_grouped_fwd,
+    "fu_ln_silu_grouped_bwd": _ln_grouped_bwd,
     "fu_linear": _linear,
+    "fu_linear_batched": _linear_batched,
 }
 
-MFMA_BOUND = {"fu_linear"}
+MFMA_BOUND = {"fu_linear", "fu_linear_batched"}
 
 
 def summarize(durations) -> dict:
