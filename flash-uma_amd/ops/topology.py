@@ -129,6 +129,7 @@ def build_topology(pos: torch.Tensor, batch: torch.Tensor, edge_index: torch.Ten
 
 _TOPO_CAPACITY = 8
 _topo_cache: "OrderedDict[tuple, GraphTopology]" = OrderedDict()
+_topo_stats = {"hits": 0, "builds": 0}
 
 
 def get_topology(pos: torch.Tensor, batch: torch.Tensor, edge_index: torch.Tensor) -> GraphTopology:
@@ -143,8 +144,10 @@ def get_topology(pos: torch.Tensor, batch: torch.Tensor, edge_index: torch.Tenso
     hit = _topo_cache.get(key)
     if hit is not None:
         _topo_cache.move_to_end(key)
+        _topo_stats["hits"] += 1
         return hit
     topo = build_topology(pos, batch, edge_index)
+    _topo_stats["builds"] += 1
     _topo_cache[key] = topo
     if len(_topo_cache) > _TOPO_CAPACITY:
         _topo_cache.popitem(last=False)
@@ -153,6 +156,12 @@ def get_topology(pos: torch.Tensor, batch: torch.Tensor, edge_index: torch.Tenso
 
 def clear_topology_cache() -> None:
     _topo_cache.clear()
+    _topo_stats["hits"] = _topo_stats["builds"] = 0
+
+
+def topology_cache_stats() -> dict:
+    """{'entries', 'hits', 'builds'} since the last clear_topology_cache()."""
+    return {"entries": len(_topo_cache), **_topo_stats}
 
 
 def sender_csr(idx_i: torch.Tensor, N: int):

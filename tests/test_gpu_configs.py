@@ -1,0 +1,127 @@
+"""The BASELINE workloads other than the headline one, run through the GPU path.
+
+* Liquid water, 333 H2O (999 atoms, cubic 21.5 A): a 100-step velocity-Verlet MD loop of
+  energy + forces with the graph built once at step 0 and the topology cached (one build,
+  99 cache hits), then parity against the float64 oracle at the final positions, and the
+  total-energy drift of the trajectory.
+* Amorphous 8-element cell: 50,000 atoms / 1.5 M edges (E * 12C > 2^31, so every per-edge
+  offset must be 64-bit; sender degrees 15..44).  No oracle can run at this size inside a
+  test, so the full size is checked through size-independent properties: bitwise
+  reproducibility, sum of forces = 0, invariance of the energy and covariance of the forces
+  under a rigid rotation of positions and cell, and translation invariance.  A 1,500-atom
+  cell from the same generator (same density, same elements) is checked against the
+  float64 oracle directly.
+Tolerances as everywhere: energy per atom rel <= 1e-6, forces max-abs <= 1e-4 eV/A."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+AMU_A2_FS2_IN_EV = 103.642697   # 1 amu * A^2 / fs^2 in eV
+KB_EV = 8.617333262e-5
+
+
+def _build(cuda, seed=0):
+    import escn_md
+    import heads
+    from wrapper import ZeroAllocBackbone
+    bb = escn_md.eSCNMDBackbone(seed=seed)
+    hd = heads.MLPEnergyHead(bb.sphere_channels, bb.hidden_channels, seed=seed + 1)
+    return bb, hd, heads.PotentialModel(ZeroAllocBackbone(bb.to(cuda)), hd.to(cuda))
+
+
+def _oracle_check(bb, hd, pos, Z, cell, ei, off, out):
+    from oracle.model_ref import energy_forces_stress
+    ref = energy_forces_stress(bb.cpu(), hd.cpu(), pos, Z, cell, ei, off, dtype=torch.float64, stress=False)
+    e_rel = abs(out["energy"].double().item() - ref["energy"].item()) / abs(ref["energy"].item())
+    f_err = (out["forces"].detach().cpu().double() - ref["forces"]).abs().max().item()
+    print(f"energy rel {e_rel:.2e}  forces max-abs {f_err:.2e}", flush=True)
+    assert e_rel <= 1e-6 and f_err <= 1e-4, (e_rel, f_err)
+
+
+def test_water_md_cached_topology(cuda):
+    import heads
+    import systems
+    from ops import topology
+    bb, hd, model = _build(cuda)
+    s = systems.water_box(n_mol=333, L=21.5, seed=0)
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, bb.cutoff, bb.max_neighbors)
+    data = heads.make_atomic_data(s, ei, off, cuda)
+    masses = torch.tensor(np.where(s.Z == 8, 15.999, 1.008), dtype=torch.float64, device=cuda)[:, None]
+    g = torch.Generator().manual_seed(0)
+    v = torch.randn(s.n_atoms, 3, generator=g, dtype=torch.float64).to(cuda)
+    v *= torch.sqrt(KB_EV * 300.0 / (masses * AMU_A2_FS2_IN_EV))
+    v -= (masses * v).sum(0) / masses.sum()
+    x = data.pos.double()
+    dt = 0.5
+    topology.clear_topology_cache()
+    out = model(data, compute_forces=True, compute_stress=False)
+    f = out["forces"].double()
+    e_tot = []
+    for step in range(100):
+        kin = 0.5 * (masses * v * v).sum().item() * AMU_A2_FS2_IN_EV
+        e_tot.append(out["energy"].item() + kin)
+        v = v + 0.5 * dt * f / (masses * AMU_A2_FS2_IN_EV)
+        x = x + dt * v
+        data.pos = x.float()
+        out = model(data, compute_forces=True, compute_stress=False)
+        f = out["forces"].double()
+        v = v + 0.5 * dt * f / (masses * AMU_A2_FS2_IN_EV)
+    st = topology.topology_cache_stats()
+    assert st["builds"] == 1 and st["hits"] == 100, st
+    kin = 0.5 * (masses * v * v).sum().item() * AMU_A2_FS2_IN_EV
+    e_tot.append(out["energy"].item() + kin)
+    drift = (max(e_tot) - min(e_tot)) / s.n_atoms
+    print(f"total-energy spread over 100 steps: {drift:.2e} eV/atom", flush=True)
+    assert math.isfinite(drift) and drift < 2e-5
+    _oracle_check(bb, hd, data.pos.detach().cpu().numpy().astype(np.float64), s.Z, s.cell, ei, off, out)
+
+
+def _rotation(seed):
+    g = np.random.default_rng(seed)
+    q, r = np.linalg.qr(g.standard_normal((3, 3)))
+    q = q * np.sign(np.diag(r))
+    if np.linalg.det(q) < 0:
+        q[:, 0] = -q[:, 0]
+    return q
+
+
+def test_amorphous_small_parity(cuda):
+    import heads
+    import systems
+    bb, hd, model = _build(cuda)
+    s = systems.amorphous(n_atoms=1500, seed=1)
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, bb.cutoff, bb.max_neighbors)
+    out = model(heads.make_atomic_data(s, ei, off, cuda), compute_forces=True, compute_stress=False)
+    _oracle_check(bb, hd, s.pos, s.Z, s.cell, ei, off, out)
+
+
+def test_amorphous_50k_invariants(cuda):
+    import heads
+    import systems
+    bb, hd, model = _build(cuda)
+    s = systems.amorphous()
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, bb.cutoff, bb.max_neighbors)
+    E, C = ei.shape[1], bb.sphere_channels
+    assert E * 12 * C > 2 ** 31
+    print(f"{s.n_atoms} atoms, {E} edges", flush=True)
+
+    def run(pos, cell):
+        sys_ = systems.AtomicSystem("amorphous", pos, s.Z, cell)
+        o = model(heads.make_atomic_data(sys_, ei, off, cuda), compute_forces=True, compute_stress=False)
+        return o["energy"].double().item(), o["forces"].detach().cpu().double()
+
+    e0, f0 = run(s.pos, s.cell)
+    e1, f1 = run(s.pos, s.cell)
+    assert e0 == e1 and torch.equal(f0, f1), "not bitwise reproducible"
+    assert f0.sum(0).abs().max().item() < 1e-3, f0.sum(0)
+    Rm = _rotation(7)
+    e_r, f_r = run(s.pos @ Rm.T, np.asarray(s.cell).reshape(3, 3) @ Rm.T)
+    assert abs(e_r - e0) / abs(e0) <= 1e-6, (e_r, e0)
+    assert (f_r - f0 @ torch.from_numpy(Rm).T).abs().max().item() <= 1e-4
+    e_t, f_t = run(s.pos + np.array([0.37, -1.1, 2.3]), s.cell)
+    assert abs(e_t - e0) / abs(e0) <= 1e-6
+    assert (f_t - f0).abs().max().item() <= 1e-4
