@@ -78,3 +78,15 @@ def test_product_raises_without_gpu_tensors():
     from ops.gating import fused_gating_split
     with pytest.raises(_lib.FlashUMAError):
         fused_gating_split(torch.zeros(4, 640), torch.zeros(4, 512), torch.zeros(4, 256), 128)
+
+
+@pytest.mark.parametrize("attr,value", [("lmax", 4), ("mmax", 4)])
+def test_backbone_rejects_other_lmax_mmax(attr, value):
+    """The lmax = 4 workload is rejected exactly as the reference rejects it
+    (wrapper.py:109-118): the kernels implement the 9-coefficient lmax = mmax = 2 layout."""
+    import escn_md
+    from wrapper import ZeroAllocBackbone
+    bb = escn_md.eSCNMDBackbone(seed=0)
+    setattr(bb, attr, value)
+    with pytest.raises(ValueError, match=f"{attr}=4"):
+        ZeroAllocBackbone(bb)
