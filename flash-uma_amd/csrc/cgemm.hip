@@ -1,0 +1,161 @@
+// Complex dense layer on fp32 MFMA with three real products (Gauss's multiplication).
+//
+// The SO(2) m = 1 and m = 2 convolutions of eSCN apply a complex weight R + iI to complex
+// features x_r + i x_i.  The reference packs them into one real GEMM against
+// [[R, -I], [I, R]] (model.py:108-138), which costs four real products.  This kernel computes
+//     T1 = a_r P^T,  T2 = a_i Q^T,  T3 = (a_r + a_i)(P + Q)^T
+//     out_r = T1 - T2,  out_i = T3 - T1 - T2
+// i.e. out_r = a_r P^T - a_i Q^T and out_i = a_r Q^T + a_i P^T with three products: 25 % fewer
+// MFMA flops for the same result up to fp32 rounding.  The sums a_r + a_i and P + Q are
+// formed in registers from the operands already staged in LDS, so no extra memory traffic.
+//
+// Tiling: 256 threads (4 waves, 2 x 2), an output tile of 128 rows x 64 columns of both
+// out_r and out_i; each wave owns 64 x 32 of each of T1, T2, T3 (2 MFMA blocks each, six
+// accumulator chains).  K advances in chunks of 16 through double-buffered LDS with the
+// same XOR-swizzled 64-byte rows as the real GEMM (a_r, a_i: 128 rows; P, Q: 64 rows).
+#include "fu_common.h"
+
+namespace fu {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int CBM = 128, CBN = 64;
+constexpr int CTA = CBM * 16, CTB = CBN * 16;
+constexpr int CBUF = 2 * CTA + 2 * CTB;  // a_r | a_i | P | Q
+
+__device__ __forceinline__ int clds(int row, int chunk) {
+  return row * 16 + 4 * (chunk ^ (((row >> 1) ^ (row >> 2)) & 3));
+}
+
+__global__ __launch_bounds__(256, 2) void complex_linear_kernel(
+    const float* __restrict__ Ar, const float* __restrict__ Ai, int64_t lda, const float* __restrict__ P,
+    const float* __restrict__ Q, int64_t ldw, float* __restrict__ Yr, float* __restrict__ Yi, int64_t ldy,
+    int64_t M, int32_t Nc, int32_t Kc, int32_t n_tiles, int64_t total_tiles) {
+  __shared__ __attribute__((aligned(16))) float smem[2 * CBUF];
+  // XCD-aware tile order, as in the real GEMM
+  int64_t wg = blockIdx.x;
+  if ((total_tiles & 7) == 0) wg = (wg & 7) * (total_tiles >> 3) + (wg >> 3);
+  const int64_t m_tile = wg / n_tiles;
+  const int n_tile = (int)(wg - m_tile * n_tiles);
+  const int64_t row0 = m_tile * CBM;
+  const int col0 = n_tile * CBN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = (wave >> 1) * 64, wc = (wave & 1) * 32;
+
+  float4 sr[2], si[2], sp, sq;
+  auto load_chunk = [&](int k0) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int lin = tid + 256 * p, r = lin >> 2, kc = (lin & 3) * 4;
+      const int64_t row = row0 + r;
+      const int gk = k0 + kc;
+      const bool ok = row < M && gk < Kc;
+      sr[p] = ok ? ld4(Ar + row * lda + gk) : make_float4(0.f, 0.f, 0.f, 0.f);
+      si[p] = ok ? ld4(Ai + row * lda + gk) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const int r = tid >> 2, kc = (tid & 3) * 4;
+    const int gn = col0 + r, gk = k0 + kc;
+    const bool ok = gn < Nc && gk < Kc;
+    sp = ok ? ld4(P + (int64_t)gn * ldw + gk) : make_float4(0.f, 0.f, 0.f, 0.f);
+    sq = ok ? ld4(Q + (int64_t)gn * ldw + gk) : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  auto store_chunk = [&](int buf) {
+    float* b = smem + buf * CBUF;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int lin = tid + 256 * p;
+      st4(&b[clds(lin >> 2, lin & 3)], sr[p]);
+      st4(&b[CTA + clds(lin >> 2, lin & 3)], si[p]);
+    }
+    st4(&b[2 * CTA + clds(tid >> 2, tid & 3)], sp);
+    st4(&b[2 * CTA + CTB + clds(tid >> 2, tid & 3)], sq);
+  };
+
+  floatx16 T[3][2];
+#pragma unroll
+  for (int p = 0; p < 3; ++p)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) T[p][i][r] = 0.0f;
+
+  const int fr = lane & 31, fh = lane >> 5;
+  const int nk = (Kc + 15) / 16;
+  load_chunk(0);
+  store_chunk(0);
+  __syncthreads();
+  for (int kc = 0; kc < nk; ++kc) {
+    const int buf = kc & 1;
+    if (kc + 1 < nk) load_chunk((kc + 1) * 16);
+    const float* b = smem + buf * CBUF;
+    float ar[2][8], ai[2][8], pv[8], qv[8];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const float4 vr = ld4(&b[clds(wr + i * 32 + fr, 2 * fh + q)]);
+        const float4 vi = ld4(&b[CTA + clds(wr + i * 32 + fr, 2 * fh + q)]);
+        ar[i][4 * q] = vr.x; ar[i][4 * q + 1] = vr.y; ar[i][4 * q + 2] = vr.z; ar[i][4 * q + 3] = vr.w;
+        ai[i][4 * q] = vi.x; ai[i][4 * q + 1] = vi.y; ai[i][4 * q + 2] = vi.z; ai[i][4 * q + 3] = vi.w;
+      }
+      const float4 vp = ld4(&b[2 * CTA + clds(wc + fr, 2 * fh + q)]);
+      const float4 vq = ld4(&b[2 * CTA + CTB + clds(wc + fr, 2 * fh + q)]);
+      pv[4 * q] = vp.x; pv[4 * q + 1] = vp.y; pv[4 * q + 2] = vp.z; pv[4 * q + 3] = vp.w;
+      qv[4 * q] = vq.x; qv[4 * q + 1] = vq.y; qv[4 * q + 2] = vq.z; qv[4 * q + 3] = vq.w;
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const float sv = pv[t] + qv[t];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        T[0][i] = __builtin_amdgcn_mfma_f32_32x32x2f32(ar[i][t], pv[t], T[0][i], 0, 0, 0);
+        T[1][i] = __builtin_amdgcn_mfma_f32_32x32x2f32(ai[i][t], qv[t], T[1][i], 0, 0, 0);
+        T[2][i] = __builtin_amdgcn_mfma_f32_32x32x2f32(ar[i][t] + ai[i][t], sv, T[2][i], 0, 0, 0);
+      }
+    }
+    if (kc + 1 < nk) store_chunk(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Accumulator layout of the 32x32 MFMA: lane l, register r -> column l % 32, row
+  // 8 (r / 4) + 4 (l / 32) + r % 4; each store instruction writes 128 contiguous bytes of a row.
+  const int gc = col0 + wc + fr;
+  if (gc < Nc) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = row0 + wr + i * 32 + 8 * (r >> 2) + 4 * fh + (r & 3);
+        if (row < M) {
+          const float t1 = T[0][i][r], t2 = T[1][i][r];
+          Yr[row * ldy + gc] = t1 - t2;
+          Yi[row * ldy + gc] = T[2][i][r] - t1 - t2;
+        }
+      }
+  }
+}
+
+}  // namespace fu
+
+using namespace fu;
+
+extern "C" int fu_complex_linear(const float* A_r, const float* A_i, int64_t lda, const float* P, const float* Q,
+                                 int64_t ldw, float* Y_r, float* Y_i, int64_t ldy, int64_t M, int32_t Nc,
+                                 int32_t Kc, void* stream) {
+  const char* who = "fu_complex_linear";
+  if (M < 0 || Nc <= 0 || Kc <= 0) return set_error(FU_ERR_SHAPE, "%s: bad shape M=%lld Nc=%d Kc=%d", who, (long long)M, Nc, Kc);
+  if (Kc % 4 != 0 || lda % 4 != 0 || ldw % 4 != 0)
+    return set_error(FU_ERR_UNSUPPORTED, "%s: Kc=%d, lda=%lld, ldw=%lld must be multiples of 4", who, Kc,
+                     (long long)lda, (long long)ldw);
+  if (lda < Kc || ldw < Kc || ldy < Nc) return set_error(FU_ERR_SHAPE, "%s: leading dimensions smaller than the rows", who);
+  if (!A_r || !A_i || !P || !Q || !Y_r || !Y_i) return set_error(FU_ERR_NULL, "%s: NULL operand", who);
+  if (!aligned16(A_r) || !aligned16(A_i) || !aligned16(P) || !aligned16(Q))
+    return set_error(FU_ERR_ALIGN, "%s: operands must be 16-byte aligned", who);
+  if (M == 0) return FU_OK;
+  const int n_tiles = (Nc + CBN - 1) / CBN;
+  const int64_t total = ((M + CBM - 1) / CBM) * n_tiles;
+  if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
+  hipLaunchKernelGGL(complex_linear_kernel, dim3((unsigned)total), dim3(256), 0, as_stream(stream), A_r, A_i, lda, P, Q,
+                     ldw, Y_r, Y_i, ldy, M, Nc, Kc, n_tiles, total);
+  return check_launch(who);
+}

@@ -63,14 +63,22 @@ __device__ __forceinline__ int wave_id_uniform() {
   return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
 }
 
-// Column block of slot q of side so (0 = sender, 1 = receiver) in an array holding `per_side`
-// slots per side.  Layout 0 is the reference order (sides interleaved: 2q + so,
-// ops/gather.py:132-154); layout 1 keeps each side's slots contiguous (so * per_side + q), so
-// that one side's share of an edge row is a single contiguous run.
+// Column block of slot q of side so (0 = sender, 1 = receiver) in each edge array.  Layout 0
+// is the reference order, sides interleaved (2q + so, ops/gather.py:132-154).  Layout 1:
+//   X_m0, rad: each side's slots contiguous (so * per_side + q);
+//   X_m1: real slots (q = 0, 1) then imaginary slots (q = 2, 3), each half side-major, so
+//         that x_r and x_i are the two contiguous halves the complex layer reads;
+//   X_m2: reference order (already [x_r | x_i]).
 template <int L>
-__device__ __forceinline__ constexpr int slot(int per_side, int so, int q) {
-  return L ? so * per_side + q : 2 * q + so;
+__device__ __forceinline__ constexpr int slot_m0(int so, int q) { return L ? so * 3 + q : 2 * q + so; }
+template <int L>
+__device__ __forceinline__ constexpr int slot_m1(int so, int q) {
+  return L ? (q >> 1) * 4 + so * 2 + (q & 1) : 2 * q + so;
 }
+template <int L>
+__device__ __forceinline__ constexpr int slot_m2(int so, int q) { return 2 * q + so; }
+template <int L>
+__device__ __forceinline__ constexpr int slot_rad(int so, int q) { return L ? so * 6 + q : 2 * q + so; }
 
 template <int CPL, int L>
 __global__ __launch_bounds__(256) void gather_fwd_kernel(
@@ -103,7 +111,7 @@ __global__ __launch_bounds__(256) void gather_fwd_kernel(
     const float* rr = rad + e * 12 * C + c;
     Vec<CPL> r[12];
 #pragma unroll
-    for (int k = 0; k < 12; ++k) r[k] = vload<CPL>(rr + slot<L>(6, k & 1, k >> 1) * C);
+    for (int k = 0; k < 12; ++k) r[k] = vload<CPL>(rr + slot_rad<L>(k & 1, k >> 1) * C);
     float* o0 = X0 + e * 6 * C + c;
     float* o1 = X1 + e * 8 * C + c;
     float* o2 = X2 + e * 4 * C + c;
@@ -111,18 +119,18 @@ __global__ __launch_bounds__(256) void gather_fwd_kernel(
     constexpr int K0[3] = {0, 2, 6}, K1[4] = {3, 7, 1, 5}, K2[2] = {8, 4};
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
-      vstore(o0 + slot<L>(3, 0, q) * C, vmul(rs.r[K0[q]], r[2 * q]));
-      vstore(o0 + slot<L>(3, 1, q) * C, vmul(rt.r[K0[q]], r[2 * q + 1]));
+      vstore(o0 + slot_m0<L>(0, q) * C, vmul(rs.r[K0[q]], r[2 * q]));
+      vstore(o0 + slot_m0<L>(1, q) * C, vmul(rt.r[K0[q]], r[2 * q + 1]));
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      vstore(o1 + slot<L>(4, 0, q) * C, vmul(rs.r[K1[q]], r[6 + 2 * (q & 1)]));
-      vstore(o1 + slot<L>(4, 1, q) * C, vmul(rt.r[K1[q]], r[7 + 2 * (q & 1)]));
+      vstore(o1 + slot_m1<L>(0, q) * C, vmul(rs.r[K1[q]], r[6 + 2 * (q & 1)]));
+      vstore(o1 + slot_m1<L>(1, q) * C, vmul(rt.r[K1[q]], r[7 + 2 * (q & 1)]));
     }
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      vstore(o2 + slot<L>(2, 0, q) * C, vmul(rs.r[K2[q]], r[10]));
-      vstore(o2 + slot<L>(2, 1, q) * C, vmul(rt.r[K2[q]], r[11]));
+      vstore(o2 + slot_m2<L>(0, q) * C, vmul(rs.r[K2[q]], r[10]));
+      vstore(o2 + slot_m2<L>(1, q) * C, vmul(rt.r[K2[q]], r[11]));
     }
   }
 }
@@ -153,14 +161,14 @@ __device__ __forceinline__ void side_load(const float* __restrict__ gX0, const f
   const float* g1 = gX1 + e * 8 * C + c;
   const float* g2 = gX2 + e * 4 * C + c;
 #pragma unroll
-  for (int q = 0; q < 3; ++q) d.g[q] = vload<CPL>(g0 + slot<L>(3, so, q) * C);
+  for (int q = 0; q < 3; ++q) d.g[q] = vload<CPL>(g0 + slot_m0<L>(so, q) * C);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) d.g[3 + q] = vload<CPL>(g1 + slot<L>(4, so, q) * C);
+  for (int q = 0; q < 4; ++q) d.g[3 + q] = vload<CPL>(g1 + slot_m1<L>(so, q) * C);
 #pragma unroll
-  for (int q = 0; q < 2; ++q) d.g[7 + q] = vload<CPL>(g2 + slot<L>(2, so, q) * C);
+  for (int q = 0; q < 2; ++q) d.g[7 + q] = vload<CPL>(g2 + slot_m2<L>(so, q) * C);
   const float* rp = rad + e * 12 * C + c;
 #pragma unroll
-  for (int q = 0; q < 6; ++q) d.r[q] = vload<CPL>(rp + slot<L>(6, so, q) * C);
+  for (int q = 0; q < 6; ++q) d.r[q] = vload<CPL>(rp + slot_rad<L>(so, q) * C);
 }
 
 // v (the node's own row, csd added) is read from the wave's LDS copy, so that it holds no
@@ -185,12 +193,12 @@ __device__ __forceinline__ void side_apply(const SideEdge<CPL>& d, int64_t e, in
     rotate9(w, v, rv);
     // this side's radial gradients (reference blocks so, 2+so, ..., 10+so)
     float* gr = g_rad + e * 12 * C + c;
-    vstore(gr + slot<L>(6, so, 0) * C, vmul(d.g[0], rv.r[0]));
-    vstore(gr + slot<L>(6, so, 1) * C, vmul(d.g[1], rv.r[2]));
-    vstore(gr + slot<L>(6, so, 2) * C, vmul(d.g[2], rv.r[6]));
-    vstore(gr + slot<L>(6, so, 3) * C, vadd(vmul(d.g[3], rv.r[3]), vmul(d.g[5], rv.r[1])));
-    vstore(gr + slot<L>(6, so, 4) * C, vadd(vmul(d.g[4], rv.r[7]), vmul(d.g[6], rv.r[5])));
-    vstore(gr + slot<L>(6, so, 5) * C, vadd(vmul(d.g[7], rv.r[8]), vmul(d.g[8], rv.r[4])));
+    vstore(gr + slot_rad<L>(so, 0) * C, vmul(d.g[0], rv.r[0]));
+    vstore(gr + slot_rad<L>(so, 1) * C, vmul(d.g[1], rv.r[2]));
+    vstore(gr + slot_rad<L>(so, 2) * C, vmul(d.g[2], rv.r[6]));
+    vstore(gr + slot_rad<L>(so, 3) * C, vadd(vmul(d.g[3], rv.r[3]), vmul(d.g[5], rv.r[1])));
+    vstore(gr + slot_rad<L>(so, 4) * C, vadd(vmul(d.g[4], rv.r[7]), vmul(d.g[6], rv.r[5])));
+    vstore(gr + slot_rad<L>(so, 5) * C, vadd(vmul(d.g[7], rv.r[8]), vmul(d.g[8], rv.r[4])));
   }
   // gradient w.r.t. the rotated coefficients of this node's row
   Rows9<CPL> grv;

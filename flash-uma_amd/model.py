@@ -11,7 +11,10 @@ Differences in mechanism (not in results):
   - the graph topology (Morton order, receiver-sorted edge order, receiver and sender CSRs)
     is built once per edge_index on the GPU and cached (ops/topology.py);
   - dense layers use the fp32 MFMA GEMM with pre-transposed frozen weights for the input
-    gradient (ops/linear.py).
+    gradient (ops/linear.py);
+  - the m = 1, 2 SO(2) layers keep their weights as complex pairs (R, I) and run the
+    three-product complex layer instead of the packed [[R, -I], [I, R]] GEMM: the same
+    product, one quarter fewer flops.
 """
 from __future__ import annotations
 
@@ -20,10 +23,10 @@ from collections import OrderedDict
 import torch
 import torch.nn as nn
 
-from ops.gather import SIDE_MAJOR_PERM, block_permutation, gather_wigner_split
+from ops.gather import LAYOUT1_PERM, block_permutation, gather_wigner_split
 from ops.gating import fused_gating_split
 from ops.geom import precompute_geometry
-from ops.linear import linear
+from ops.linear import complex_linear, linear
 from ops.ln_silu import layer_norm_silu
 from ops.node import permute_rows
 from ops.radial import RadialBank
@@ -101,44 +104,59 @@ class Packed_eSCN_Layer(nn.Module):
 
         self.norm_1 = None; self.norm_2 = None; self.atom_wise = None
         self.prepared = False
-        self.layout = 0  # gather slot layout; 1 (side-major) after prepare_for_inference
-
-    @staticmethod
-    def _pack(R: torch.Tensor, I: torch.Tensor) -> torch.Tensor:
-        # complex map (R + iI) on [real; imag] stacked features as the real block matrix
-        # [[R, -I], [I, R]] (model.py:111-138)
-        return torch.cat([torch.cat([R, -I], 1), torch.cat([I, R], 1)], 0)
+        self.layout = 0  # gather slot layout; 1 after prepare_for_inference
 
     def _register(self, name: str, W: torch.Tensor, dtype) -> None:
         W = W.to(dtype).contiguous()
         self.register_buffer(name, W)
         self.register_buffer(name + "_t", W.t().contiguous())
 
+    def _register_complex(self, name: str, R: torch.Tensor, I: torch.Tensor, dtype) -> None:
+        # The reference packs (R + iI) on [real; imag] stacked features as the real block
+        # matrix [[R, -I], [I, R]] (model.py:111-138); the complex layer takes R and I
+        # themselves, plus R^T and -I^T for its input gradient.
+        R = R.to(dtype).contiguous()
+        I = I.to(dtype).contiguous()
+        self.register_buffer(name + "_R", R)
+        self.register_buffer(name + "_I", I)
+        self.register_buffer(name + "_Rt", R.t().contiguous())
+        self.register_buffer(name + "_It_neg", (-I).t().contiguous())
+
+    def _complex(self, x: torch.Tensor, name: str) -> torch.Tensor:
+        return complex_linear(x, getattr(self, name + "_R"), getattr(self, name + "_I"), getattr(self, name + "_Rt"),
+                              getattr(self, name + "_It_neg"))
+
     def prepare_for_inference(self, dtype=torch.float32):
         if self.norm_1 is not None:
             for mod in (self.norm_1, self.norm_2, self.atom_wise):
                 for p in mod.parameters():
                     p.requires_grad = False
-        # Side-major slot layout (ops/gather.py): the radial output blocks and the conv1 input
-        # columns are permuted alike, so rad -> X -> conv1 computes the same products while
-        # each side's share of an edge row is contiguous for the gather backward.
+        # Slot layout 1 of the gather (ops/gather.py): the radial output blocks and the conv1
+        # input columns are permuted alike, so rad -> X -> conv1 computes the same products
+        # while each side's share of an edge row is contiguous for the gather backward and
+        # X_m1 = [x_r | x_i] for the complex layer.
         C = self.C
-        p_rad = block_permutation(SIDE_MAJOR_PERM["rad"], C).to(self.W_rad1_3.device)
+        dev = self.W1_m0.device
+        p_rad = block_permutation(LAYOUT1_PERM["rad"], C).to(dev)
         self.W_rad1_3.data = self.W_rad1_3.data[p_rad].contiguous()
         self.b_rad1_3.data = self.b_rad1_3.data[p_rad].contiguous()
-        cols = {m: block_permutation(SIDE_MAJOR_PERM[m], C).to(self.W1_m0.device) for m in ("m0", "m1", "m2")}
+        pm1 = LAYOUT1_PERM["m1"]
+        re_order, im_order = pm1[:4], [b - 4 for b in pm1[4:]]
+        assert re_order == im_order, "x_r and x_i blocks must be permuted alike"
+        c_m1 = block_permutation(re_order, C).to(dev)
+        assert LAYOUT1_PERM["m2"] == [0, 1, 2, 3]
         for name in ("W_rad1_1", "W_rad1_2", "W_rad1_3"):
             W = getattr(self, name).data
             self.register_buffer(name + "_t", W.to(dtype).t().contiguous())
-        self._register("W_conv1_m0", self.W1_m0.data[:, cols["m0"]], dtype)
+        self._register("W_conv1_m0", self.W1_m0.data[:, block_permutation(LAYOUT1_PERM["m0"], C).to(dev)], dtype)
         self.register_buffer("b_conv1_m0", _frozen(self.b1_m0.data).to(dtype))
-        self._register("W_conv1_m1", self._pack(self.W1_m1_R.data, self.W1_m1_I.data)[:, cols["m1"]], dtype)
-        self._register("W_conv1_m2", self._pack(self.W1_m2_R.data, self.W1_m2_I.data)[:, cols["m2"]], dtype)
+        self._register_complex("W_conv1_m1", self.W1_m1_R.data[:, c_m1], self.W1_m1_I.data[:, c_m1], dtype)
+        self._register_complex("W_conv1_m2", self.W1_m2_R.data, self.W1_m2_I.data, dtype)
         self.layout = 1
         self._register("W_conv2_m0", self.W2_m0.data, dtype)
         self.register_buffer("b_conv2_m0", _frozen(self.b2_m0.data).to(dtype))
-        self._register("W_conv2_m1", self._pack(self.W2_m1_R.data, self.W2_m1_I.data), dtype)
-        self._register("W_conv2_m2", self._pack(self.W2_m2_R.data, self.W2_m2_I.data), dtype)
+        self._register_complex("W_conv2_m1", self.W2_m1_R.data, self.W2_m1_I.data, dtype)
+        self._register_complex("W_conv2_m2", self.W2_m2_R.data, self.W2_m2_I.data, dtype)
         del self.W1_m0, self.b1_m0, self.W1_m1_R, self.W1_m1_I, self.W1_m2_R, self.W1_m2_I
         del self.W2_m0, self.b2_m0, self.W2_m1_R, self.W2_m1_I, self.W2_m2_R, self.W2_m2_I
         self.prepared = True
@@ -165,12 +183,12 @@ class Packed_eSCN_Layer(nn.Module):
         X_m0, X_m1, X_m2 = gather_wigner_split(x_norm, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology,
                                                self.layout)
         Y_m0 = linear(X_m0, self.W_conv1_m0, self.b_conv1_m0, self.W_conv1_m0_t)
-        Y_m1 = linear(X_m1, self.W_conv1_m1, None, self.W_conv1_m1_t)
-        Y_m2 = linear(X_m2, self.W_conv1_m2, None, self.W_conv1_m2_t)
+        Y_m1 = self._complex(X_m1, "W_conv1_m1")
+        Y_m2 = self._complex(X_m2, "W_conv1_m2")
         Z_m0, Z_m1, Z_m2 = fused_gating_split(Y_m0, Y_m1, Y_m2, self.C)
         Zo_m0 = linear(Z_m0, self.W_conv2_m0, self.b_conv2_m0, self.W_conv2_m0_t)
-        Zo_m1 = linear(Z_m1, self.W_conv2_m1, None, self.W_conv2_m1_t)
-        Zo_m2 = linear(Z_m2, self.W_conv2_m2, None, self.W_conv2_m2_t)
+        Zo_m1 = self._complex(Z_m1, "W_conv2_m1")
+        Zo_m2 = self._complex(Z_m2, "W_conv2_m2")
         x_mid = rotate_scatter_split(Zo_m0, Zo_m1, Zo_m2, wigner, env, x_in, idx_j, row_ptr, col_idx,
                                      x_in.shape[0])
         return self.atom_wise(self.norm_2(x_mid)) + x_mid

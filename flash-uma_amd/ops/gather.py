@@ -4,10 +4,11 @@ The backward is node-centric over the receiver and sender CSRs (no atomics, bitw
 reproducible); it needs both CSRs, taken from the cached topology when given.
 
 layout 0 keeps the reference's column-block order of X_m* and rad_out (sender/receiver
-slots interleaved, ops/gather.py:132-154).  layout 1 ("side-major") stores each array's
-sender slots first and receiver slots second (SIDE_MAJOR_PERM below); the model uses it
-with conv1 and radial weights permuted to match, which leaves every product unchanged and
-lets each side of the backward read and write one contiguous run per edge."""
+slots interleaved, ops/gather.py:132-154).  layout 1 (LAYOUT1_PERM below) stores X_m0 and
+rad side-major (sender blocks, then receiver blocks), X_m1 as [real half | imaginary half]
+with each half side-major, and X_m2 in reference order; the model uses it with conv1 and
+radial weights permuted to match, which leaves every product unchanged, gives each side of
+the backward contiguous runs, and hands the complex m = 1, 2 layers contiguous x_r, x_i."""
 from __future__ import annotations
 
 import torch
@@ -18,10 +19,10 @@ from .topology import receiver_csr, sender_csr
 
 
 # Column-block permutation of layout 1: new block b holds reference block perm[b].
-SIDE_MAJOR_PERM = {
+LAYOUT1_PERM = {
     "m0": [0, 2, 4, 1, 3, 5],
-    "m1": [0, 2, 4, 6, 1, 3, 5, 7],
-    "m2": [0, 2, 1, 3],
+    "m1": [0, 2, 1, 3, 4, 6, 5, 7],
+    "m2": [0, 1, 2, 3],
     "rad": [0, 2, 4, 6, 8, 10, 1, 3, 5, 7, 9, 11],
 }
 

@@ -42,3 +42,39 @@ class _LinearFn(torch.autograd.Function):
 def linear(x: torch.Tensor, W: torch.Tensor, bias: torch.Tensor | None, Wt: torch.Tensor) -> torch.Tensor:
     """x W^T + b with a frozen weight; Wt must be W.t().contiguous()."""
     return _LinearFn.apply(x, W, bias, Wt)
+
+
+def complex_gemm(x: torch.Tensor, P: torch.Tensor, Q: torch.Tensor) -> torch.Tensor:
+    """[y_r | y_i] = complex product of x = [x_r | x_i] (M, 2 Kc) with (P + iQ)^T, P, Q (Nc, Kc):
+    y_r = x_r P^T - x_i Q^T, y_i = x_r Q^T + x_i P^T (three real MFMA products)."""
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    M = x.shape[0]
+    Nc, Kc = P.shape
+    if x.shape[1] != 2 * Kc or Q.shape != P.shape:
+        raise _lib.FlashUMAError(f"complex_gemm: x {tuple(x.shape)} vs P {tuple(P.shape)}, Q {tuple(Q.shape)}")
+    y = torch.empty((M, 2 * Nc), device=x.device, dtype=torch.float32)
+    _lib.call("fu_complex_linear", x.data_ptr(), x[:, Kc:].data_ptr(), x.stride(0), P.data_ptr(), Q.data_ptr(),
+              P.stride(0), y.data_ptr(), y[:, Nc:].data_ptr(), y.stride(0), M, Nc, Kc, _lib.stream_ptr(x.device))
+    return y
+
+
+class _ComplexLinearFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, P, Q, Pt, Qt_neg):
+        x = _lib.require(x, torch.float32, "x")
+        ctx.save_for_backward(Pt, Qt_neg)
+        return complex_gemm(x, P, Q)
+
+    @staticmethod
+    def backward(ctx, g_y):
+        Pt, Qt_neg = ctx.saved_tensors
+        return complex_gemm(g_y.contiguous(), Pt, Qt_neg), None, None, None, None
+
+
+def complex_linear(x: torch.Tensor, P: torch.Tensor, Q: torch.Tensor, Pt: torch.Tensor,
+                   Qt_neg: torch.Tensor) -> torch.Tensor:
+    """Frozen complex layer: equals x @ [[P, -Q], [Q, P]]^T (the reference's packed SO(2)
+    weight, model.py:108-138).  Pt = P^T and Qt_neg = -Q^T (contiguous) give the input
+    gradient through the same kernel: g_x_r = g_r P + g_i Q, g_x_i = g_i P - g_r Q."""
+    return _ComplexLinearFn.apply(x, P, Q, Pt, Qt_neg)

@@ -2,7 +2,8 @@
 
 Bytes count each tensor the kernel must touch exactly once (reads + writes, fp32 features,
 int64 graph indices, int32 CSR arrays); node-sized tables are counted once per launch.
-GEMMs count 2*M*N*K flops.  These are the denominators of the roofline fractions:
+GEMMs count 2*M*N*K flops; the complex layer counts the 6*M*Nc*Kc flops of its three real
+products.  These are the denominators of the roofline fractions:
 achieved = algorithmic bytes (flops) / measured kernel time.
 
 Per-unit figures at C = 128, B = 64 (bytes per edge + bytes per node):
@@ -94,6 +95,13 @@ def _linear_batched(a):
     return 4 * B * (M * K + M * N + N * K), 2 * B * M * N * K
 
 
+def _complex_linear(a):
+    # executed MFMA work: three real (M x Kc) x (Kc x Nc) products (the packed real form
+    # of the reference would be four)
+    M, Nc, Kc = a[9], a[10], a[11]
+    return 4 * (2 * M * Kc + 2 * M * Nc + 2 * Nc * Kc), 6 * M * Nc * Kc
+
+
 def _ln_grouped_fwd(a):
     # x read + out written per row and group, mean/rstd; with tables: two int64 edge ids per
     # row and the (L2-resident) 100-row tables once per launch
@@ -126,9 +134,10 @@ WORK = {
     "fu_ln_silu_grouped_bwd": _ln_grouped_bwd,
     "fu_linear": _linear,
     "fu_linear_batched": _linear_batched,
+    "fu_complex_linear": _complex_linear,
 }
 
-MFMA_BOUND = {"fu_linear", "fu_linear_batched"}
+MFMA_BOUND = {"fu_linear", "fu_linear_batched", "fu_complex_linear"}
 
 
 def summarize(durations) -> dict:

@@ -83,10 +83,10 @@ int fu_edge_vec_reduce(const float* g_d, const int32_t* recv_ptr, const int32_t*
  * x (N, 9, C) (+ csd_emb[batch] on l=0) into the edge frame, scale by rad (E, 12C) and
  * write the X_m0/X_m1/X_m2 blocks.
  * layout 0: the reference column-block order of X and rad (sender/receiver slots
- * interleaved, ops/gather.py:132-154).  layout 1: per array, all sender slots first, then
- * all receiver slots, each side in reference order (block q of side s at s*per_side + q);
- * the model pairs it with conv1 / radial weights permuted the same way, which leaves every
- * product unchanged and makes each side's share of an edge row contiguous. */
+ * interleaved, ops/gather.py:132-154).  layout 1: X_m0 and rad side-major (all sender
+ * blocks, then all receiver blocks); X_m1 as [real half | imaginary half], each half
+ * side-major; X_m2 in reference order.  The model pairs it with conv1 / radial weights
+ * permuted the same way, which leaves every product unchanged. */
 int fu_gather_fwd(const float* x, const int64_t* idx_i, const int64_t* idx_j, const float* wigner,
                   const float* rad, const float* csd_emb, const int64_t* batch, float* X_m0,
                   float* X_m1, float* X_m2, int64_t E, int64_t N, int64_t S, int32_t C,
@@ -200,6 +200,18 @@ int fu_linear_batched(const float* A, int64_t lda, int64_t stride_a, const float
                       int64_t stride_w, const float* bias, int64_t stride_bias, int32_t bias_batches,
                       float* Y, int64_t ldy, int64_t stride_y, int64_t M, int32_t N, int32_t K,
                       int32_t batch, void* stream);
+
+/* Complex dense layer, the SO(2) m = 1, 2 convolutions (model.py:152,154 with the packed
+ * weights of model.py:108-138): for features a_r + i a_i (two (M, Kc) arrays, row stride lda)
+ * and weight P + iQ ((Nc, Kc) each, row stride ldw),
+ *   Y_r = A_r P^T - A_i Q^T,   Y_i = A_r Q^T + A_i P^T      ((M, Nc), row stride ldy),
+ * i.e. X [[P, -Q], [Q, P]]^T with X = [A_r | A_i] -- the reference's packed product -- computed
+ * with three real MFMA products (Gauss) instead of four.  The input gradient of the layer is
+ * the same operation with (P^T, -Q^T).  Kc, lda, ldw multiples of 4; A_r, A_i, P, Q 16-byte
+ * aligned. */
+int fu_complex_linear(const float* A_r, const float* A_i, int64_t lda, const float* P, const float* Q,
+                      int64_t ldw, float* Y_r, float* Y_i, int64_t ldy, int64_t M, int32_t Nc,
+                      int32_t Kc, void* stream);
 
 /* ------------------------------------------------------------------------------------
  * Node-level modules attached to the backbone (model.py:145,157,218) and input plumbing

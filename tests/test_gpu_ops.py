@@ -79,6 +79,26 @@ def test_linear(cuda, M, N, K):
     assert_close(g, gref, TOL, "linear bwd")
 
 
+@pytest.mark.parametrize("M,Kc,Nc", [(300, 512, 256), (257, 128, 256), (1, 96, 64), (1000, 128, 128)])
+def test_complex_linear(cuda, M, Kc, Nc):
+    """The three-product complex layer against the reference's packed real GEMM
+    x @ [[R, -I], [I, R]]^T (oracle pack_so2) in float64, forward and input gradient."""
+    from ops.linear import complex_linear
+    g = torch.Generator().manual_seed(M + Kc + Nc)
+    x = torch.randn(M, 2 * Kc, generator=g)
+    Rw = torch.randn(Nc, Kc, generator=g) / Kc ** 0.5
+    Iw = torch.randn(Nc, Kc, generator=g) / Kc ** 0.5
+    xg = x.to(cuda).requires_grad_(True)
+    Rg, Ig = Rw.to(cuda), Iw.to(cuda)
+    y = complex_linear(xg, Rg, Ig, Rg.t().contiguous(), (-Ig).t().contiguous())
+    cot = torch.randn(M, 2 * Nc, generator=g)
+    Wp = R.pack_so2(Rw.double(), Iw.double())
+    (ref,), (gref,) = _vjp(lambda a: a @ Wp.T, [x], [cot])
+    assert_close(y, ref, TOL, "complex linear fwd")
+    (gx,) = torch.autograd.grad(y, xg, cot.to(cuda))
+    assert_close(gx, gref, TOL, "complex linear bwd")
+
+
 @pytest.mark.parametrize("C", [128, 64])
 def test_radial_bank(cuda, C):
     """All radial MLPs as one bank (element embeddings folded into per-element tables) against
@@ -178,13 +198,13 @@ def _gather_inputs(seed=4, N=40, E=300, C=128, S=1):
 @pytest.mark.parametrize("layout", [0, 1])
 def test_gather(cuda, layout):
     """layout 1 stores the blocks of X_m* and rad side-major: the same values as the reference
-    layout under the block permutations SIDE_MAJOR_PERM (checked against the oracle, whose
+    layout under the block permutations LAYOUT1_PERM (checked against the oracle, whose
     outputs are in the reference order, by permuting its columns)."""
     gather, *_ = _ops()
     x, ei, wig, rad, csd, batch = _gather_inputs()
     C = x.shape[2]
     if layout:
-        cols = {k: gather.block_permutation(v, C) for k, v in gather.SIDE_MAJOR_PERM.items()}
+        cols = {k: gather.block_permutation(v, C) for k, v in gather.LAYOUT1_PERM.items()}
         inv_rad = torch.argsort(cols["rad"])
     perm = (lambda t, k: t[:, cols[k]]) if layout else (lambda t, k: t)
     rad_k = perm(rad, "rad")  # the kernel's input in its own layout
