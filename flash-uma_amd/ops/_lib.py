@@ -57,6 +57,10 @@ SIGNATURES: dict[str, list] = {
     "fu_take_i64": [P, I64, P, P, I64, P],
     "fu_csr_row_ptr": [P, I64, P, I64, P],
     "fu_narrow_i64_i32": [P, P, I64, P],
+    "fu_nlist_bin": [P, I64, P, P, P, P, P, P, P, P],
+    "fu_nlist_search": [P, P, P, P, P, I64, P, P, P, P, P, ctypes.c_double, I32, P, P, P, P, P],
+    "fu_nlist_scan": [P, P, I64, P],
+    "fu_nlist_emit": [P, P, P, P, I64, I32, P, P, I64, P],
 }
 
 _lib: ctypes.CDLL | None = None

@@ -282,6 +282,41 @@ int fu_csr_row_ptr(const int64_t* sorted_keys, int64_t E, int32_t* row_ptr, int6
 /* int64 -> int32 narrowing copy (col_idx = sort_order.to(int32), model.py:25). */
 int fu_narrow_i64_i32(const int64_t* in, int32_t* out, int64_t n, void* stream);
 
+/* ------------------------------------------------------------------------------------
+ * Radius graph (the input graph of the reference: FAIRChem a2g, readme.md:34; definition of
+ * the host builder systems.neighbor_list).  For receiver j: all (i, o), o an integer cell
+ * offset (0 on non-periodic axes), (i, o) != (j, 0), with d = (pos_i - pos_j) +
+ * ((o0 c0 + o1 c1) + o2 c2) evaluated in float64 from the float32 inputs in that order and
+ * |d|^2 = (dx dx + dy dy) + dz dz < cutoff^2; ordered by (|d|^2, i, o0, o1, o2); the first
+ * max_neighbors kept; receivers ascending.  Geometry arguments are HOST arrays: cell (9
+ * doubles, lattice vectors as rows), inv_cell (its inverse), nbins / reach / pbc (3 int32
+ * each: cell-list bins per axis, at least cutoff + 1e-3 wide; bins searched per side; axis
+ * periodicity).  Non-periodic axes use nbins = 1, reach = 0.
+ * ------------------------------------------------------------------------------------ */
+
+/* Cell-list bin key (N int64) and wrap count floor(s) per axis (N x 3 int32) of each atom. */
+int fu_nlist_bin(const float* pos, int64_t N, const double* cell, const double* inv_cell,
+                 const int32_t* nbins, const int32_t* reach, const int32_t* pbc, int64_t* bin_key,
+                 int32_t* wrap, void* stream);
+
+/* Per receiver: the max_neighbors first candidates (out_sender N x K int32, out_off N x K x 3
+ * int32), the number kept (nout) and the number within the cutoff (count; results are only
+ * complete when every count <= 512).  sorted_atoms: atoms stably sorted by bin_key; bin_ptr:
+ * nbins_total + 1 bin starts into sorted_atoms. */
+int fu_nlist_search(const float* pos, const int64_t* sorted_atoms, const int32_t* bin_ptr,
+                    const int32_t* wrap, const int64_t* bin_key, int64_t N, const double* cell,
+                    const double* inv_cell, const int32_t* nbins, const int32_t* reach,
+                    const int32_t* pbc, double cutoff, int32_t max_neighbors, int32_t* out_sender,
+                    int32_t* out_off, int32_t* count, int32_t* nout, void* stream);
+
+/* row_ptr (N + 1 int64) = exclusive scan of nout; row_ptr[N] = E. */
+int fu_nlist_scan(const int32_t* nout, int64_t* row_ptr, int64_t N, void* stream);
+
+/* edge_index (2 x E int64: senders, then receivers) and cell_offsets (E x 3 float32). */
+int fu_nlist_emit(const int32_t* sender, const int32_t* off, const int32_t* nout, const int64_t* row_ptr,
+                  int64_t N, int32_t max_neighbors, int64_t* edge_index, float* cell_offsets, int64_t E,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -49,3 +49,65 @@ def test_topology_consistency(cuda):
     sptr, sidx = G.csr(ii[rcol], N)
     assert np.array_equal(topo.send_ptr.cpu().numpy(), sptr)
     assert np.array_equal(topo.send_idx.cpu().numpy(), sidx)
+
+
+def _triclinic(n=300, seed=5, outside=0.02):
+    import systems
+    g = np.random.default_rng(seed)
+    cell = np.array([[14.0, 0.0, 0.0], [3.1, 13.2, 0.0], [-2.4, 1.7, 12.5]])
+    frac = g.uniform(-outside, 1.0 + outside, size=(n, 3))
+    pos = (frac @ cell).astype(np.float32)
+    Z = g.choice([1, 6, 8, 26], size=n).astype(np.int64)
+    return systems.AtomicSystem("triclinic", pos, Z, cell.astype(np.float32))
+
+
+def _graph_cases():
+    import systems
+    return {
+        "cu_slab": (systems.cu_slab_co, 30),
+        "water999": (lambda: systems.water_box(n_mol=333, L=21.5, seed=0), 30),
+        "bcc_fe_8192": (lambda: systems.bcc_fe(16), 30),
+        "amorphous_50k": (systems.amorphous, 30),
+        "triclinic": (_triclinic, 30),
+        "triclinic_cap8": (_triclinic, 8),
+        "slab_open_z": (lambda: _open_z(), 30),
+    }
+
+
+def _open_z():
+    import systems
+    s = _triclinic(n=200, seed=9, outside=0.0)
+    return systems.AtomicSystem("open_z", s.pos, s.Z, s.cell, pbc=(True, True, False))
+
+
+@pytest.mark.parametrize("case", ["cu_slab", "water999", "bcc_fe_8192", "amorphous_50k", "triclinic", "triclinic_cap8",
+                                  "slab_open_z"])
+def test_radius_graph_bit_exact(cuda, case):
+    """GPU radius graph == host builder (edge order, senders, receivers, offsets), including
+    a triclinic cell with atoms slightly outside it, a small cap and a non-periodic axis."""
+    import systems
+    from ops.neighbors import radius_graph
+    build, K = _graph_cases()[case]
+    s = build()
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, 6.0, K)
+    gei, goff = radius_graph(torch.from_numpy(np.asarray(s.pos)).to(cuda), s.cell, s.pbc, 6.0, K)
+    print(case, s.n_atoms, "atoms", ei.shape[1], "edges", flush=True)
+    assert gei.shape == ei.shape and np.array_equal(gei.cpu().numpy(), ei)
+    assert np.array_equal(goff.cpu().numpy(), off)
+
+
+def test_radius_graph_brute_force_and_skin(cuda):
+    """Against the oracle's all-pairs, all-images enumeration; and the skin policy of
+    NeighborList (no rebuild below skin / 2 of motion, rebuild above)."""
+    from oracle.graph import neighbor_list_bruteforce
+    from ops.neighbors import NeighborList, radius_graph
+    s = _triclinic(n=120, seed=11)
+    ref_ei, ref_off = neighbor_list_bruteforce(s.pos, s.cell, s.pbc, 6.0, 30)
+    pos = torch.from_numpy(s.pos).to(cuda)
+    gei, goff = radius_graph(pos, s.cell, s.pbc, 6.0, 30)
+    assert np.array_equal(gei.cpu().numpy(), ref_ei) and np.array_equal(goff.cpu().numpy(), ref_off)
+    nl = NeighborList(6.0, 30, skin=0.5)
+    g0 = nl(pos, s.cell, s.pbc)
+    assert nl(pos + 0.1, s.cell, s.pbc)[0] is g0[0] and nl.builds == 1
+    nl(pos + torch.tensor([0.3, 0.0, 0.0], device=cuda), s.cell, s.pbc)
+    assert nl.builds == 2
