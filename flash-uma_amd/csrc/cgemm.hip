@@ -27,7 +27,7 @@ __device__ __forceinline__ int clds(int row, int chunk) {
   return row * 16 + 4 * (chunk ^ (((row >> 1) ^ (row >> 2)) & 3));
 }
 
-__global__ __launch_bounds__(256, 2) void complex_linear_kernel(
+__global__ __launch_bounds__(256, 3) void complex_linear_kernel(
     const float* __restrict__ Ar, const float* __restrict__ Ai, int64_t lda, const float* __restrict__ P,
     const float* __restrict__ Q, int64_t ldw, float* __restrict__ Yr, float* __restrict__ Yi, int64_t ldy,
     int64_t M, int32_t Nc, int32_t Kc, int32_t n_tiles, int64_t total_tiles) {
