@@ -14,6 +14,7 @@ from __future__ import annotations
 import math
 from types import SimpleNamespace
 
+import numpy as np
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
@@ -44,12 +45,12 @@ class MLPEnergyHead(nn.Module):
         return h.squeeze(-1)
 
 
-def system_sum(values: torch.Tensor, batch: torch.Tensor, n_systems: int) -> torch.Tensor:
-    """Deterministic per-system sum (batch ids are sorted per system in every input here)."""
-    if n_systems == 1:
-        return values.sum().reshape(1)
-    out = torch.zeros(n_systems, dtype=values.dtype, device=values.device)
-    return out.index_add(0, batch, values)
+def system_sum(values: torch.Tensor, natoms: list) -> torch.Tensor:
+    """Per-system sum over the leading (atom) dimension; systems are contiguous runs of
+    natoms[s] atoms (FAIRChem batches).  One fixed-order reduction per system, no atomics."""
+    if len(natoms) == 1:
+        return values.sum(0, keepdim=True)
+    return torch.stack([v.sum(0) for v in values.split(natoms)])
 
 
 class PotentialModel(nn.Module):
@@ -65,8 +66,8 @@ class PotentialModel(nn.Module):
     def forward(self, data, compute_forces: bool = True, compute_stress: bool = False) -> dict:
         emb = self.backbone(data)
         e_atom = self.head.atom_energy(emb["node_embedding"])
-        n_sys = int(data.natoms.numel())
-        energy = system_sum(e_atom, data.batch, n_sys)
+        natoms = [int(n) for n in data.natoms.tolist()]
+        energy = system_sum(e_atom, natoms)
         out = {"energy": energy, "atom_energy": e_atom, "node_embedding": emb["node_embedding"]}
         if compute_forces or compute_stress:
             inputs = [data.pos] + ([data.cell] if compute_stress else [])
@@ -75,20 +76,17 @@ class PotentialModel(nn.Module):
             out["forces"] = -g_pos
             if compute_stress:
                 g_cell = grads[1] if grads[1] is not None else torch.zeros_like(data.cell)
-                out["stress"] = stress_from_gradients(data.pos, data.cell, g_pos, g_cell, data.batch, n_sys)
+                out["stress"] = stress_from_gradients(data.pos, data.cell, g_pos, g_cell, natoms)
         return out
 
 
-def stress_from_gradients(pos, cell, g_pos, g_cell, batch, n_sys):
+def stress_from_gradients(pos, cell, g_pos, g_cell, natoms: list):
     """(1/V) (sum_i pos_i^T g_pos_i + cell^T g_cell) per system, (S, 3, 3)."""
+    n_sys = len(natoms)
     pos = pos.detach()
     cell = cell.detach().reshape(n_sys, 3, 3)
     g_cell = g_cell.reshape(n_sys, 3, 3)
-    outer = pos[:, :, None] * g_pos[:, None, :]
-    if n_sys == 1:
-        w = outer.sum(0, keepdim=True)
-    else:
-        w = torch.zeros(n_sys, 3, 3, dtype=pos.dtype, device=pos.device).index_add(0, batch, outer)
+    w = system_sum(pos[:, :, None] * g_pos[:, None, :], natoms)
     w = w + cell.transpose(1, 2) @ g_cell
     vol = torch.linalg.det(cell).abs().reshape(n_sys, 1, 1)
     return w / vol
@@ -113,3 +111,32 @@ def make_atomic_data(system, edge_index, cell_offsets, device, dtype=torch.float
         spin=torch.tensor([spin], dtype=torch.long, device=device),
         batch=torch.zeros(n, dtype=torch.long, device=device),
     )
+
+
+def make_batch_data(items, device, dtype=torch.float32):
+    """One FAIRChem-style batch of several systems: items = [(system, edge_index,
+    cell_offsets, charge, spin), ...].  Atoms and edges are concatenated system by system,
+    edge indices offset by the atoms before, batch / natoms / nedges / cell / charge / spin
+    per system (the layout wrapper.py:173-210 reads)."""
+    pos, Z, cells, ei, off, batch, natoms, nedges, chg, spn = [], [], [], [], [], [], [], [], [], []
+    base = 0
+    for s, (system, edge_index, cell_offsets, charge, spin) in enumerate(items):
+        n = system.n_atoms
+        pos.append(np.asarray(system.pos, dtype=np.float32))
+        Z.append(np.asarray(system.Z, dtype=np.int64))
+        cells.append(np.asarray(system.cell, dtype=np.float32).reshape(1, 3, 3))
+        ei.append(np.asarray(edge_index, dtype=np.int64) + base)
+        off.append(np.asarray(cell_offsets, dtype=np.float32))
+        batch.append(np.full(n, s, dtype=np.int64))
+        natoms.append(n)
+        nedges.append(np.asarray(edge_index).shape[1])
+        chg.append(charge)
+        spn.append(spin)
+        base += n
+    t = lambda a, dt: torch.as_tensor(a, dtype=dt, device=device)
+    return SimpleNamespace(
+        pos=t(np.concatenate(pos), dtype).clone(), atomic_numbers=t(np.concatenate(Z), torch.long),
+        cell=t(np.concatenate(cells), dtype).clone(), natoms=t(natoms, torch.long),
+        edge_index=t(np.concatenate(ei, axis=1), torch.long), cell_offsets=t(np.concatenate(off), dtype),
+        nedges=t(nedges, torch.long), charge=t(chg, torch.long), spin=t(spn, torch.long),
+        batch=t(np.concatenate(batch), torch.long), pbc=t(np.ones((len(items), 3), dtype=bool), torch.bool))

@@ -76,3 +76,40 @@ def test_deterministic_and_translation(cuda):
     for k in ("energy", "forces", "stress", "node_embedding"):
         assert torch.equal(a[k], b[k]), f"{k} not bitwise reproducible"
     assert a["forces"].double().sum(0).abs().max().item() < 1e-5
+
+
+def test_batch_of_three_systems(cuda):
+    """A FAIRChem-style batch of three systems with different cells, sizes, charges and
+    spins (per-edge cell shifts, per-system charge/spin embedding through the kernels,
+    per-system energy and stress): each system's energy, forces and stress must match the
+    float64 oracle of that system alone, and the single-system GPU run."""
+    import copy
+    import heads
+    import systems
+    from oracle.model_ref import energy_forces_stress
+    bb, hd, model = _build(cuda)
+    specs = ((systems.cu_slab_co, 0, 0), (lambda: systems.water_box(n_mol=20, L=8.5, seed=4), 1, 2),
+             (lambda: systems.bcc_fe(n_rep=2), -1, 1))
+    items = []
+    for build, chg, spn in specs:
+        s = build()
+        ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, bb.cutoff, bb.max_neighbors)
+        items.append((s, ei, off, chg, spn))
+    out = model(heads.make_batch_data(items, cuda), compute_forces=True, compute_stress=True)
+    natoms = [it[0].n_atoms for it in items]
+    forces = out["forces"].detach().cpu().split(natoms)
+    singles = []
+    for s, ei, off, chg, spn in items:
+        o = model(heads.make_atomic_data(s, ei, off, cuda, charge=chg, spin=spn), compute_forces=True,
+                  compute_stress=True)
+        singles.append({k: o[k].detach().cpu() for k in ("energy", "forces", "stress")})
+    bb_cpu, hd_cpu = copy.deepcopy(bb).cpu(), copy.deepcopy(hd).cpu()
+    for k, (s, ei, off, chg, spn) in enumerate(items):
+        ref = energy_forces_stress(bb_cpu, hd_cpu, s.pos, s.Z, s.cell, ei, off, charge=chg, spin=spn,
+                                   dtype=torch.float64)
+        e = out["energy"][k].double().item()
+        assert abs(e - ref["energy"].item()) / abs(ref["energy"].item()) <= 1e-6, (k, e, ref["energy"].item())
+        assert (forces[k].double() - ref["forces"]).abs().max().item() <= 1e-4
+        assert (out["stress"][k].detach().cpu().double() - ref["stress"][0]).abs().max().item() <= 1e-4
+        assert abs(e - singles[k]["energy"].double().item()) <= 1e-6 * abs(e)
+        assert (forces[k] - singles[k]["forces"]).abs().max().item() <= 1e-5
