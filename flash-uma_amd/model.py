@@ -241,7 +241,25 @@ class eSCN_Inference_Model(nn.Module):
                              self.gamma_rad1_2, self.beta_rad1_2)
         return linear(h2, self.W_rad1_3, self.b_rad1_3, self.W_rad1_3_t)
 
+    def _check_atoms(self, Z, batch, n_systems: int) -> None:
+        """Atomic numbers index the 100-row element tables and batch ids the per-system
+        embedding inside the kernels, so both are range-checked on the host (once per pair
+        of tensors: an MD loop passes the same ones every step)."""
+        key = (Z.data_ptr(), Z._version, batch.data_ptr(), batch._version, Z.numel(), n_systems)
+        if key == getattr(self, "_checked_atoms", None):
+            return
+        n_el = self.W_sphere.shape[0]
+        if Z.numel():
+            zlo, zhi = (int(v) for v in torch.aminmax(Z))
+            blo, bhi = (int(v) for v in torch.aminmax(batch))
+            if zlo < 0 or zhi >= n_el:
+                raise ValueError(f"atomic numbers must lie in [0, {n_el}); got [{zlo}, {zhi}]")
+            if blo < 0 or bhi >= n_systems:
+                raise ValueError(f"batch ids must lie in [0, {n_systems}); got [{blo}, {bhi}]")
+        self._checked_atoms = key
+
     def forward(self, pos, Z, batch, edge_index, shifts, csd_emb, charge=None, spin=None, natoms=None):
+        self._check_atoms(Z, batch, csd_emb.shape[0])
         # 1. Topology (Morton order + receiver-sorted edges + both CSRs), cached per graph
         topo = get_topology(pos, batch, edge_index)
         pos_s = permute_rows(pos, topo.perm)

@@ -113,3 +113,23 @@ def test_batch_of_three_systems(cuda):
         assert (out["stress"][k].detach().cpu().double() - ref["stress"][0]).abs().max().item() <= 1e-4
         assert abs(e - singles[k]["energy"].double().item()) <= 1e-6 * abs(e)
         assert (forces[k] - singles[k]["forces"]).abs().max().item() <= 1e-5
+
+
+def test_rejects_out_of_range_atoms(cuda):
+    """Atomic numbers and batch ids index tables inside the kernels: out-of-range values are
+    refused on the host before any launch."""
+    import heads
+    import systems
+    bb, hd, model = _build(cuda)
+    s = systems.cu_slab_co()
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, bb.cutoff, bb.max_neighbors)
+    data = heads.make_atomic_data(s, ei, off, cuda)
+    data.atomic_numbers = data.atomic_numbers.clone()
+    data.atomic_numbers[3] = 100
+    with pytest.raises(ValueError, match="atomic numbers"):
+        model(data, compute_forces=False)
+    data = heads.make_atomic_data(s, ei, off, cuda)
+    data.batch = data.batch.clone()
+    data.batch[0] = 1
+    with pytest.raises(ValueError, match="batch ids"):
+        model(data, compute_forces=False)
