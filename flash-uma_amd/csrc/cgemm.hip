@@ -12,7 +12,8 @@
 // Tiling: 256 threads (4 waves, 2 x 2), an output tile of 128 rows x 64 columns of both
 // out_r and out_i; each wave owns 64 x 32 of each of T1, T2, T3 (2 MFMA blocks each, six
 // accumulator chains).  K advances in chunks of 16 through double-buffered LDS with the
-// same XOR-swizzled 64-byte rows as the real GEMM (a_r, a_i: 128 rows; P, Q: 64 rows).
+// same XOR-swizzled 64-byte rows as the real GEMM (a_r, a_i: 128 rows; P, Q: 64 rows).  The
+// epilogue stages the outputs through LDS and writes 16-byte row pieces.
 #include "fu_common.h"
 
 namespace fu {
@@ -27,10 +28,22 @@ __device__ __forceinline__ int clds(int row, int chunk) {
   return row * 16 + 4 * (chunk ^ (((row >> 1) ^ (row >> 2)) & 3));
 }
 
+// Gate epilogue (conv1 m = 1, 2 fused with the gate activation): Z_r = Y_r s and
+// Z_i = Y_i s with s = S[row][s_off + column].
+struct CGate {
+  float* Zr;
+  float* Zi;
+  int64_t ldz;
+  const float* S;
+  int64_t lds;
+  int32_t s_off;
+};
+
+template <bool GATE>
 __global__ __launch_bounds__(256, 3) void complex_linear_kernel(
     const float* __restrict__ Ar, const float* __restrict__ Ai, int64_t lda, const float* __restrict__ P,
     const float* __restrict__ Q, int64_t ldw, float* __restrict__ Yr, float* __restrict__ Yi, int64_t ldy,
-    int64_t M, int32_t Nc, int32_t Kc, int32_t n_tiles, int64_t total_tiles) {
+    int64_t M, int32_t Nc, int32_t Kc, int32_t n_tiles, int64_t total_tiles, CGate g) {
   __shared__ __attribute__((aligned(16))) float smem[2 * CBUF];
   // XCD-aware tile order, as in the real GEMM
   int64_t wg = blockIdx.x;
@@ -118,20 +131,39 @@ __global__ __launch_bounds__(256, 3) void complex_linear_kernel(
   }
 
   // Accumulator layout of the 32x32 MFMA: lane l, register r -> column l % 32, row
-  // 8 (r / 4) + 4 (l / 32) + r % 4; each store instruction writes 128 contiguous bytes of a row.
-  const int gc = col0 + wc + fr;
-  if (gc < Nc) {
+  // 8 (r / 4) + 4 (l / 32) + r % 4.  Each wave stages a 32-row slab of [out_r | out_i] (32 + 32
+  // columns) in LDS and writes it back as 16-byte row pieces (plus the gated copies).
+  constexpr int CES = 64 + 8;
+  static_assert(4 * 32 * CES <= 2 * CBUF, "epilogue staging must fit in the operand buffers");
+  float* ws = smem + wave * 32 * CES;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 2; ++i) {
+    __syncthreads();
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = row0 + wr + i * 32 + 8 * (r >> 2) + 4 * fh + (r & 3);
-        if (row < M) {
-          const float t1 = T[0][i][r], t2 = T[1][i][r];
-          Yr[row * ldy + gc] = t1 - t2;
-          Yi[row * ldy + gc] = T[2][i][r] - t1 - t2;
-        }
+    for (int r = 0; r < 16; ++r) {
+      const int rr = 8 * (r >> 2) + 4 * fh + (r & 3);
+      const float t1 = T[0][i][r], t2 = T[1][i][r];
+      ws[rr * CES + fr] = t1 - t2;
+      ws[rr * CES + 32 + fr] = T[2][i][r] - t1 - t2;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int lin = lane + 64 * q;
+      const int r = lin >> 3;
+      const int c = (lin & 7) * 4;
+      const int64_t row = row0 + wr + i * 32 + r;
+      const int gc = col0 + wc + c;
+      if (row >= M || gc >= Nc) continue;
+      const float4 yr = ld4(&ws[r * CES + c]), yi = ld4(&ws[r * CES + 32 + c]);
+      st4(Yr + row * ldy + gc, yr);
+      st4(Yi + row * ldy + gc, yi);
+      if constexpr (GATE) {
+        const float4 sg = ld4(g.S + row * g.lds + g.s_off + gc);
+        st4(g.Zr + row * g.ldz + gc, yr * sg);
+        st4(g.Zi + row * g.ldz + gc, yi * sg);
       }
+    }
   }
 }
 
@@ -139,23 +171,55 @@ __global__ __launch_bounds__(256, 3) void complex_linear_kernel(
 
 using namespace fu;
 
-extern "C" int fu_complex_linear(const float* A_r, const float* A_i, int64_t lda, const float* P, const float* Q,
-                                 int64_t ldw, float* Y_r, float* Y_i, int64_t ldy, int64_t M, int32_t Nc,
-                                 int32_t Kc, void* stream) {
-  const char* who = "fu_complex_linear";
+static int complex_check(const float* A_r, const float* A_i, int64_t lda, const float* P, const float* Q,
+                         int64_t ldw, const float* Y_r, const float* Y_i, int64_t ldy, int64_t M, int32_t Nc,
+                         int32_t Kc, const char* who) {
   if (M < 0 || Nc <= 0 || Kc <= 0) return set_error(FU_ERR_SHAPE, "%s: bad shape M=%lld Nc=%d Kc=%d", who, (long long)M, Nc, Kc);
   if (Kc % 4 != 0 || lda % 4 != 0 || ldw % 4 != 0)
     return set_error(FU_ERR_UNSUPPORTED, "%s: Kc=%d, lda=%lld, ldw=%lld must be multiples of 4", who, Kc,
                      (long long)lda, (long long)ldw);
   if (lda < Kc || ldw < Kc || ldy < Nc) return set_error(FU_ERR_SHAPE, "%s: leading dimensions smaller than the rows", who);
   if (!A_r || !A_i || !P || !Q || !Y_r || !Y_i) return set_error(FU_ERR_NULL, "%s: NULL operand", who);
-  if (!aligned16(A_r) || !aligned16(A_i) || !aligned16(P) || !aligned16(Q))
+  if (!aligned16(A_r) || !aligned16(A_i) || !aligned16(P) || !aligned16(Q) || !aligned16(Y_r) || !aligned16(Y_i))
     return set_error(FU_ERR_ALIGN, "%s: operands must be 16-byte aligned", who);
-  if (M == 0) return FU_OK;
+  if (Nc % 4 != 0 || ldy % 4 != 0) return set_error(FU_ERR_UNSUPPORTED, "%s: Nc and ldy must be multiples of 4", who);
+  const int64_t total = ((M + CBM - 1) / CBM) * ((Nc + CBN - 1) / CBN);
+  if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
+  return FU_OK;
+}
+
+template <bool GATE>
+static int complex_launch(const float* A_r, const float* A_i, int64_t lda, const float* P, const float* Q, int64_t ldw,
+                          float* Y_r, float* Y_i, int64_t ldy, int64_t M, int32_t Nc, int32_t Kc, CGate g,
+                          void* stream, const char* who) {
   const int n_tiles = (Nc + CBN - 1) / CBN;
   const int64_t total = ((M + CBM - 1) / CBM) * n_tiles;
-  if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
-  hipLaunchKernelGGL(complex_linear_kernel, dim3((unsigned)total), dim3(256), 0, as_stream(stream), A_r, A_i, lda, P, Q,
-                     ldw, Y_r, Y_i, ldy, M, Nc, Kc, n_tiles, total);
+  hipLaunchKernelGGL((complex_linear_kernel<GATE>), dim3((unsigned)total), dim3(256), 0, as_stream(stream), A_r, A_i,
+                     lda, P, Q, ldw, Y_r, Y_i, ldy, M, Nc, Kc, n_tiles, total, g);
   return check_launch(who);
+}
+
+extern "C" int fu_complex_linear(const float* A_r, const float* A_i, int64_t lda, const float* P, const float* Q,
+                                 int64_t ldw, float* Y_r, float* Y_i, int64_t ldy, int64_t M, int32_t Nc,
+                                 int32_t Kc, void* stream) {
+  int st = complex_check(A_r, A_i, lda, P, Q, ldw, Y_r, Y_i, ldy, M, Nc, Kc, "fu_complex_linear");
+  if (st != FU_OK || M == 0) return st;
+  return complex_launch<false>(A_r, A_i, lda, P, Q, ldw, Y_r, Y_i, ldy, M, Nc, Kc, CGate{}, stream,
+                               "fu_complex_linear");
+}
+
+extern "C" int fu_complex_linear_gate(const float* A_r, const float* A_i, int64_t lda, const float* P, const float* Q,
+                                      int64_t ldw, float* Y_r, float* Y_i, int64_t ldy, float* Z_r, float* Z_i,
+                                      int64_t ldz, const float* S, int64_t lds, int32_t s_off, int64_t M, int32_t Nc,
+                                      int32_t Kc, void* stream) {
+  const char* who = "fu_complex_linear_gate";
+  int st = complex_check(A_r, A_i, lda, P, Q, ldw, Y_r, Y_i, ldy, M, Nc, Kc, who);
+  if (st != FU_OK) return st;
+  if (!Z_r || !Z_i || !S) return set_error(FU_ERR_NULL, "%s: NULL gate operand", who);
+  if (ldz < Nc || s_off < 0 || lds < s_off + Nc) return set_error(FU_ERR_SHAPE, "%s: gate strides too small", who);
+  if ((ldz | lds | s_off) % 4 != 0 || !aligned16(Z_r) || !aligned16(Z_i) || !aligned16(S))
+    return set_error(FU_ERR_ALIGN, "%s: gate operands must be 16-byte aligned with strides multiples of 4", who);
+  if (M == 0) return FU_OK;
+  return complex_launch<true>(A_r, A_i, lda, P, Q, ldw, Y_r, Y_i, ldy, M, Nc, Kc, CGate{Z_r, Z_i, ldz, S, lds, s_off},
+                              stream, who);
 }

@@ -6,10 +6,31 @@
 //
 // Pure streaming work (HBM-bound): one thread per (edge, 4 channels), float4 loads and
 // stores, 64-bit offsets.  Forward moves 20 floats per (edge, channel) and backward 31.
+//
+// Y_m0 (and g_Y_m0) come in one of two column orders: layout 0 is the order above; layout 1
+// is the gate-paired order of the fused conv1 epilogue (fu_linear_gate): 64-column pairs
+// [gate_l1 | y_l1m0] x C/32, [gate_l2 | y_l2m0] x C/32, then y_l0.
 #include "fu_common.h"
 
 namespace fu {
 
+// Column offsets of gate_l1, gate_l2, y_l0, y_l1m0, y_l2m0 for channel c (c % 4 == 0).
+template <int L>
+__device__ __forceinline__ void y0_offsets(int64_t c, int64_t C, int64_t* o) {
+  if constexpr (L == 0) {
+#pragma unroll
+    for (int k = 0; k < 5; ++k) o[k] = k * C + c;
+  } else {
+    const int64_t blk = c >> 5, in = c & 31;
+    o[0] = 64 * blk + in;
+    o[3] = o[0] + 32;
+    o[1] = 64 * ((C >> 5) + blk) + in;
+    o[4] = o[1] + 32;
+    o[2] = 4 * C + c;
+  }
+}
+
+template <int L>
 __global__ __launch_bounds__(256) void gating_fwd_kernel(const float* __restrict__ Y0,
                                                          const float* __restrict__ Y1,
                                                          const float* __restrict__ Y2,
@@ -22,11 +43,13 @@ __global__ __launch_bounds__(256) void gating_fwd_kernel(const float* __restrict
        t += (int64_t)gridDim.x * blockDim.x) {
     const int64_t e = t / C4;
     const int64_t c = 4 * (t - e * C4);
-    const float* y0 = Y0 + e * 5 * C + c;
+    int64_t o[5];
+    y0_offsets<L>(c, C, o);
+    const float* y0 = Y0 + e * 5 * C;
     const float* y1 = Y1 + e * 4 * C + c;
     const float* y2 = Y2 + e * 2 * C + c;
-    const float4 a0 = ld4(y0), a1 = ld4(y0 + C), l0 = ld4(y0 + 2 * C), l1 = ld4(y0 + 3 * C),
-                 l2 = ld4(y0 + 4 * C);
+    const float4 a0 = ld4(y0 + o[0]), a1 = ld4(y0 + o[1]), l0 = ld4(y0 + o[2]), l1 = ld4(y0 + o[3]),
+                 l2 = ld4(y0 + o[4]);
     const float4 r1 = ld4(y1), r2 = ld4(y1 + C), i1 = ld4(y1 + 2 * C), i2 = ld4(y1 + 3 * C);
     const float4 mr = ld4(y2), mi = ld4(y2 + C);
     const float4 s1 = make_float4(sigmoidf_(a0.x), sigmoidf_(a0.y), sigmoidf_(a0.z), sigmoidf_(a0.w));
@@ -68,6 +91,7 @@ __device__ __forceinline__ void gate_bwd_lane(float a0, float a1, float l0, floa
   o[10] = gmi * s2;
 }
 
+template <int L>
 __global__ __launch_bounds__(256) void gating_bwd_kernel(
     const float* __restrict__ gZ0, const float* __restrict__ gZ1, const float* __restrict__ gZ2,
     const float* __restrict__ Y0, const float* __restrict__ Y1, const float* __restrict__ Y2,
@@ -78,13 +102,15 @@ __global__ __launch_bounds__(256) void gating_bwd_kernel(
        t += (int64_t)gridDim.x * blockDim.x) {
     const int64_t e = t / C4;
     const int64_t c = 4 * (t - e * C4);
-    const float* y0 = Y0 + e * 5 * C + c;
+    int64_t o[5];
+    y0_offsets<L>(c, C, o);
+    const float* y0 = Y0 + e * 5 * C;
     const float* y1 = Y1 + e * 4 * C + c;
     const float* y2 = Y2 + e * 2 * C + c;
     const float* g0 = gZ0 + e * 3 * C + c;
     const float* g1 = gZ1 + e * 4 * C + c;
     const float* g2 = gZ2 + e * 2 * C + c;
-    const float* srcs[20] = {y0, y0 + C, y0 + 2 * C, y0 + 3 * C, y0 + 4 * C, y1, y1 + C,
+    const float* srcs[20] = {y0 + o[0], y0 + o[1], y0 + o[2], y0 + o[3], y0 + o[4], y1, y1 + C,
                              y1 + 2 * C, y1 + 3 * C, y2, y2 + C, g0, g0 + C, g0 + 2 * C, g1,
                              g1 + C, g1 + 2 * C, g1 + 3 * C, g2, g2 + C};
     float v[20][4];
@@ -100,19 +126,22 @@ __global__ __launch_bounds__(256) void gating_bwd_kernel(
                     v[8][q], v[9][q], v[10][q], v[11][q], v[12][q], v[13][q], v[14][q], v[15][q],
                     v[16][q], v[17][q], v[18][q], v[19][q], out[q]);
     }
-    float* o0 = gY0 + e * 5 * C + c;
+    float* o0 = gY0 + e * 5 * C;
     float* o1 = gY1 + e * 4 * C + c;
     float* o2 = gY2 + e * 2 * C + c;
-    float* dst[11] = {o0, o0 + C, o0 + 2 * C, o0 + 3 * C, o0 + 4 * C, o1, o1 + C, o1 + 2 * C,
+    float* dst[11] = {o0 + o[0], o0 + o[1], o0 + o[2], o0 + o[3], o0 + o[4], o1, o1 + C, o1 + 2 * C,
                       o1 + 3 * C, o2, o2 + C};
 #pragma unroll
     for (int s = 0; s < 11; ++s) st4(dst[s], make_float4(out[0][s], out[1][s], out[2][s], out[3][s]));
   }
 }
 
-static int gating_check(const void* const* ptrs, int n, int64_t E, int32_t C, const char* who) {
+static int gating_check(const void* const* ptrs, int n, int64_t E, int32_t C, int32_t layout, const char* who) {
   if (E < 0 || C <= 0) return set_error(FU_ERR_SHAPE, "%s: bad shape E=%lld C=%d", who, (long long)E, C);
   if (C % 4 != 0) return set_error(FU_ERR_UNSUPPORTED, "%s: C=%d must be a multiple of 4", who, C);
+  if (layout != 0 && layout != 1) return set_error(FU_ERR_UNSUPPORTED, "%s: layout %d", who, layout);
+  if (layout == 1 && C % 64 != 0)
+    return set_error(FU_ERR_UNSUPPORTED, "%s: the gate-paired layout needs C a multiple of 64", who);
   for (int k = 0; k < n; ++k) {
     if (ptrs[k] == nullptr) return set_error(FU_ERR_NULL, "%s: pointer %d is NULL", who, k);
     if (!aligned16(ptrs[k])) return set_error(FU_ERR_ALIGN, "%s: pointer %d not 16-byte aligned", who, k);
@@ -125,29 +154,37 @@ static int gating_check(const void* const* ptrs, int n, int64_t E, int32_t C, co
 using namespace fu;
 
 extern "C" int fu_gating_fwd(const float* Y_m0, const float* Y_m1, const float* Y_m2, float* Z_m0,
-                             float* Z_m1, float* Z_m2, int64_t E, int32_t C, void* stream) {
+                             float* Z_m1, float* Z_m2, int64_t E, int32_t C, int32_t layout, void* stream) {
   const void* ptrs[] = {Y_m0, Y_m1, Y_m2, Z_m0, Z_m1, Z_m2};
-  int st = gating_check(ptrs, 6, E, C, "fu_gating_fwd");
+  int st = gating_check(ptrs, 6, E, C, layout, "fu_gating_fwd");
   if (st != FU_OK) return st;
   if (E == 0) return FU_OK;
   const int64_t total = E * (C / 4);
   const int64_t blocks = std::min<int64_t>(cdiv(total, 256), kMaxBlocks);
-  hipLaunchKernelGGL(gating_fwd_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
-                     Y_m0, Y_m1, Y_m2, Z_m0, Z_m1, Z_m2, total, C / 4);
+  if (layout)
+    hipLaunchKernelGGL(gating_fwd_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                       Y_m0, Y_m1, Y_m2, Z_m0, Z_m1, Z_m2, total, C / 4);
+  else
+    hipLaunchKernelGGL(gating_fwd_kernel<0>, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                       Y_m0, Y_m1, Y_m2, Z_m0, Z_m1, Z_m2, total, C / 4);
   return check_launch("fu_gating_fwd");
 }
 
 extern "C" int fu_gating_bwd(const float* g_Z_m0, const float* g_Z_m1, const float* g_Z_m2,
                              const float* Y_m0, const float* Y_m1, const float* Y_m2, float* g_Y_m0,
-                             float* g_Y_m1, float* g_Y_m2, int64_t E, int32_t C, void* stream) {
+                             float* g_Y_m1, float* g_Y_m2, int64_t E, int32_t C, int32_t layout,
+                             void* stream) {
   const void* ptrs[] = {g_Z_m0, g_Z_m1, g_Z_m2, Y_m0, Y_m1, Y_m2, g_Y_m0, g_Y_m1, g_Y_m2};
-  int st = gating_check(ptrs, 9, E, C, "fu_gating_bwd");
+  int st = gating_check(ptrs, 9, E, C, layout, "fu_gating_bwd");
   if (st != FU_OK) return st;
   if (E == 0) return FU_OK;
   const int64_t total = E * (C / 4);
   const int64_t blocks = std::min<int64_t>(cdiv(total, 256), kMaxBlocks);
-  hipLaunchKernelGGL(gating_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
-                     g_Z_m0, g_Z_m1, g_Z_m2, Y_m0, Y_m1, Y_m2, g_Y_m0, g_Y_m1, g_Y_m2, total,
-                     C / 4);
+  if (layout)
+    hipLaunchKernelGGL(gating_bwd_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                       g_Z_m0, g_Z_m1, g_Z_m2, Y_m0, Y_m1, Y_m2, g_Y_m0, g_Y_m1, g_Y_m2, total, C / 4);
+  else
+    hipLaunchKernelGGL(gating_bwd_kernel<0>, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                       g_Z_m0, g_Z_m1, g_Z_m2, Y_m0, Y_m1, Y_m2, g_Y_m0, g_Y_m1, g_Y_m2, total, C / 4);
   return check_launch("fu_gating_bwd");
 }

@@ -31,14 +31,30 @@ __device__ __forceinline__ int lds_chunk(int row, int chunk) {
   return row * GLDS + 4 * (chunk ^ (((row >> 1) ^ (row >> 2)) & 3));
 }
 
+// Extra outputs of the gate epilogue (conv1 m = 0 fused with the gate activation).
+struct GateOut {
+  float* Z;     // (M, 3C): [silu(y_l0), y_l1m0 s1, y_l2m0 s2]
+  int64_t ldz;
+  float* S;     // (M, 2C): [s1, s2] = sigmoid of the two gate blocks
+  int64_t lds;
+  int32_t C;
+};
+
 // Batch index blockIdx.y offsets A, W and Y by sA, sW and sY floats; bias (stride sBias) is
 // added in batches [0, bias_batches).
+//
+// GATE: Y has N = 5C columns in the gate-paired order -- every 64-column pair p holds
+// [32 gate channels | the 32 channels they gate]: pairs 0 .. C/32-1 are (gate_l1, y_l1m0),
+// the next C/32 are (gate_l2, y_l2m0), the last C/64 hold y_l0 -- so a wave's two 32x32
+// accumulator blocks are a gate and its values in the same lanes and registers.  The
+// epilogue writes Y (kept for the backward), Z and S without going through LDS.
+template <bool GATE>
 __global__ __launch_bounds__(256, 4) void linear_mfma_kernel(const float* __restrict__ A, int64_t lda, int64_t sA,
                                                           const float* __restrict__ W, int64_t ldw, int64_t sW,
                                                           const float* __restrict__ bias, int64_t sBias,
                                                           int32_t bias_batches, float* __restrict__ Y, int64_t ldy,
                                                           int64_t sY, int64_t M, int32_t N, int32_t K,
-                                                          int32_t n_tiles, int64_t total_tiles) {
+                                                          int32_t n_tiles, int64_t total_tiles, GateOut go) {
   {
     const int64_t bt = blockIdx.y;
     A += bt * sA;
@@ -137,10 +153,59 @@ __global__ __launch_bounds__(256, 4) void linear_mfma_kernel(const float* __rest
   }
 
   // Accumulator layout of the 32x32 MFMA: lane l, register r -> column l%32,
-  // row 8*(r/4) + 4*(l/32) + r%4.  Each wave stages one 32x64 slab at a time in LDS and
-  // writes it back as rows of 16-byte stores.
+  // row 8*(r/4) + 4*(l/32) + r%4.
   const int oc = lane & 31;
   const int orow = (lane >> 5) * 4;
+  if constexpr (GATE) {
+    // Each wave stages its 32-row slabs of (gate | value) in LDS, then every lane handles
+    // 16-byte pieces: Y rows (64 columns), and for gate pairs S and Z rows (32 columns).
+    const int C = go.C, n1 = C / 32;
+    const int q0 = col0 + wc;  // first column of this wave's pair
+    const int p = q0 / 64;
+    const bool live = q0 < N;
+    float* ws = smem + wave * 32 * GES;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ws[(8 * (r >> 2) + orow + (r & 3)) * GES + j * 32 + oc] = acc[i][j][r];
+      __syncthreads();
+      if (!live) continue;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int lin = lane + 64 * q;
+        const int r = lin >> 3;
+        const int c = (lin & 7) * 4;  // 0..28 within the 32-column half
+        const int64_t row = row0 + wr + i * 32 + r;
+        if (row >= M) continue;
+        float4 g = ld4(&ws[r * GES + c]), v = ld4(&ws[r * GES + 32 + c]);
+        if (bias) {
+          g = g + ld4(bias + q0 + c);
+          v = v + ld4(bias + q0 + 32 + c);
+        }
+        st4(Y + row * ldy + q0 + c, g);
+        st4(Y + row * ldy + q0 + 32 + c, v);
+        if (p < 2 * n1) {
+          const int kind = p < n1 ? 0 : 1;
+          const int ch = 32 * (p - kind * n1) + c;
+          const float4 sg = make_float4(sigmoidf_(g.x), sigmoidf_(g.y), sigmoidf_(g.z), sigmoidf_(g.w));
+          st4(go.S + row * go.lds + kind * C + ch, sg);
+          st4(go.Z + row * go.ldz + (1 + kind) * C + ch, v * sg);
+        } else {
+          const int ch = q0 - 4 * C + c;
+          st4(go.Z + row * go.ldz + ch,
+              make_float4(g.x * sigmoidf_(g.x), g.y * sigmoidf_(g.y), g.z * sigmoidf_(g.z), g.w * sigmoidf_(g.w)));
+          st4(go.Z + row * go.ldz + ch + 32,
+              make_float4(v.x * sigmoidf_(v.x), v.y * sigmoidf_(v.y), v.z * sigmoidf_(v.z), v.w * sigmoidf_(v.w)));
+        }
+      }
+    }
+    return;
+  }
+  // Each wave stages one 32x64 slab at a time in LDS and writes it back as rows of 16-byte
+  // stores.
   float* ws = smem + wave * 32 * GES;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -195,8 +260,8 @@ static int linear_launch(const float* A, int64_t lda, int64_t sA, const float* W
   const int64_t m_tiles = (M + GBM - 1) / GBM;
   const int64_t total = m_tiles * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
-  hipLaunchKernelGGL(linear_mfma_kernel, dim3((unsigned)total, (unsigned)batch), dim3(256), 0, stream, A, lda, sA, W,
-                     ldw, sW, bias, sBias, bias_batches, Y, ldy, sY, M, N, K, n_tiles, total);
+  hipLaunchKernelGGL((linear_mfma_kernel<false>), dim3((unsigned)total, (unsigned)batch), dim3(256), 0, stream, A, lda,
+                     sA, W, ldw, sW, bias, sBias, bias_batches, Y, ldy, sY, M, N, K, n_tiles, total, GateOut{});
   return check_launch(who);
 }
 
@@ -220,4 +285,26 @@ extern "C" int fu_linear_batched(const float* A, int64_t lda, int64_t stride_a, 
   if (M == 0) return FU_OK;
   return linear_launch(A, lda, stride_a, W, ldw, stride_w, bias, stride_bias, bias_batches, Y, ldy, stride_y, M, N, K,
                        batch, as_stream(stream), "fu_linear_batched");
+}
+
+extern "C" int fu_linear_gate(const float* A, int64_t lda, const float* W, int64_t ldw, const float* bias, float* Y,
+                              int64_t ldy, float* Z, int64_t ldz, float* S, int64_t lds, int64_t M, int32_t C,
+                              int32_t K, void* stream) {
+  const char* who = "fu_linear_gate";
+  if (C <= 0 || C % 64 != 0) return set_error(FU_ERR_UNSUPPORTED, "%s: C=%d must be a multiple of 64", who, C);
+  const int32_t N = 5 * C;
+  int st = linear_check(A, lda, W, ldw, Y, ldy, M, N, K, who);
+  if (st != FU_OK) return st;
+  if (!Z || !S) return set_error(FU_ERR_NULL, "%s: NULL output", who);
+  if (ldz < 3 * C || lds < 2 * C) return set_error(FU_ERR_SHAPE, "%s: Z / S row strides too small", who);
+  if (ldz % 4 != 0 || lds % 4 != 0 || !aligned16(Z) || !aligned16(S) || (bias && !aligned16(bias)))
+    return set_error(FU_ERR_ALIGN, "%s: Z, S and bias must be 16-byte aligned with row strides multiples of 4", who);
+  if (M == 0) return FU_OK;
+  const int n_tiles = (N + GBN - 1) / GBN;
+  const int64_t total = ((M + GBM - 1) / GBM) * n_tiles;
+  if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
+  hipLaunchKernelGGL((linear_mfma_kernel<true>), dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), A, lda,
+                     (int64_t)0, W, ldw, (int64_t)0, bias, (int64_t)0, 1, Y, ldy, (int64_t)0, M, N, K, n_tiles, total,
+                     GateOut{Z, ldz, S, lds, C});
+  return check_launch(who);
 }

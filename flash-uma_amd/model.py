@@ -24,7 +24,7 @@ import torch
 import torch.nn as nn
 
 from ops.gather import LAYOUT1_PERM, block_permutation, gather_wigner_split
-from ops.gating import fused_gating_split
+from ops.gating import conv1_gate, gate_paired_rows
 from ops.geom import precompute_geometry
 from ops.linear import complex_linear, linear
 from ops.ln_silu import layer_norm_silu
@@ -148,8 +148,11 @@ class Packed_eSCN_Layer(nn.Module):
         for name in ("W_rad1_1", "W_rad1_2", "W_rad1_3"):
             W = getattr(self, name).data
             self.register_buffer(name + "_t", W.to(dtype).t().contiguous())
-        self._register("W_conv1_m0", self.W1_m0.data[:, block_permutation(LAYOUT1_PERM["m0"], C).to(dev)], dtype)
-        self.register_buffer("b_conv1_m0", _frozen(self.b1_m0.data).to(dtype))
+        # conv1 m = 0 output rows in the gate-paired order of the fused gate epilogue
+        rows = gate_paired_rows(C).to(dev)
+        self._register("W_conv1_m0", self.W1_m0.data[rows][:, block_permutation(LAYOUT1_PERM["m0"], C).to(dev)],
+                       dtype)
+        self.register_buffer("b_conv1_m0", _frozen(self.b1_m0.data[rows]).to(dtype))
         self._register_complex("W_conv1_m1", self.W1_m1_R.data[:, c_m1], self.W1_m1_I.data[:, c_m1], dtype)
         self._register_complex("W_conv1_m2", self.W1_m2_R.data, self.W1_m2_I.data, dtype)
         self.layout = 1
@@ -182,10 +185,9 @@ class Packed_eSCN_Layer(nn.Module):
             rad_out = self.radial(x_edge_raw)
         X_m0, X_m1, X_m2 = gather_wigner_split(x_norm, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology,
                                                self.layout)
-        Y_m0 = linear(X_m0, self.W_conv1_m0, self.b_conv1_m0, self.W_conv1_m0_t)
-        Y_m1 = self._complex(X_m1, "W_conv1_m1")
-        Y_m2 = self._complex(X_m2, "W_conv1_m2")
-        Z_m0, Z_m1, Z_m2 = fused_gating_split(Y_m0, Y_m1, Y_m2, self.C)
+        c1 = [getattr(self, "W_conv1_m" + m + sfx) for m in "12" for sfx in ("_R", "_I", "_Rt", "_It_neg")]
+        Z_m0, Z_m1, Z_m2 = conv1_gate(X_m0, X_m1, X_m2, self.W_conv1_m0, self.b_conv1_m0, self.W_conv1_m0_t, *c1,
+                                      self.C)
         Zo_m0 = linear(Z_m0, self.W_conv2_m0, self.b_conv2_m0, self.W_conv2_m0_t)
         Zo_m1 = self._complex(Z_m1, "W_conv2_m1")
         Zo_m2 = self._complex(Z_m2, "W_conv2_m2")

@@ -30,8 +30,8 @@ SIGNATURES: dict[str, list] = {
     "fu_edge_vec_reduce": [P, P, P, P, P, P, I64, I64, P],
     "fu_gather_fwd": [P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, I32, P],
     "fu_gather_bwd": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, I32, P],
-    "fu_gating_fwd": [P, P, P, P, P, P, I64, I32, P],
-    "fu_gating_bwd": [P, P, P, P, P, P, P, P, P, I64, I32, P],
+    "fu_gating_fwd": [P, P, P, P, P, P, I64, I32, I32, P],
+    "fu_gating_bwd": [P, P, P, P, P, P, P, P, P, I64, I32, I32, P],
     "fu_scatter_fwd": [P, P, P, P, P, P, P, P, P, I64, I64, I32, P],
     "fu_scatter_bwd": [P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I32, P],
     "fu_init_scatter_fwd": [P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, I32, P],
@@ -43,6 +43,8 @@ SIGNATURES: dict[str, list] = {
     "fu_linear": [P, I64, P, I64, P, P, I64, I64, I32, I32, P],
     "fu_linear_batched": [P, I64, I64, P, I64, I64, P, I64, I32, P, I64, I64, I64, I32, I32, I32, P],
     "fu_complex_linear": [P, P, I64, P, P, I64, P, P, I64, I64, I32, I32, P],
+    "fu_linear_gate": [P, I64, P, I64, P, P, I64, P, I64, P, I64, I64, I32, I32, P],
+    "fu_complex_linear_gate": [P, P, I64, P, P, I64, P, P, I64, P, P, I64, P, I64, I32, I64, I32, I32, P],
     "fu_rms_norm_sh_fwd": [P, P, P, P, P, I64, I32, I32, F32, P],
     "fu_rms_norm_sh_bwd": [P, P, P, P, P, I64, I32, I32, P],
     "fu_gate_act_fwd": [P, P, P, I64, I32, I32, P],

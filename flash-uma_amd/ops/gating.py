@@ -1,15 +1,39 @@
-"""fused_gating_split (ops/gating.py:188-236) on the gfx950 gate kernels."""
+"""fused_gating_split (ops/gating.py:188-236) on the gfx950 gate kernels, and conv1_gate:
+the SO(2) conv1 of a block (model.py:152) with the gate activation (model.py:153) in the
+GEMM epilogues, so the gated features are written once and the gating pass over Y is gone.
+
+layout 1 of Y_m0 is the gate-paired column order (gate_paired_rows): 64-column pairs
+[32 gate_l1 channels | the 32 y_l1m0 channels they gate], then [gate_l2 | y_l2m0], then
+y_l0; the conv1 m = 0 weight rows are permuted to it at freeze time."""
 from __future__ import annotations
 
 import torch
 
 from . import _lib
 from .constants import Z_M0_MULT, Z_M1_MULT, Z_M2_MULT
+from .linear import complex_gemm, gemm
+
+
+def gate_paired_rows(C: int) -> torch.Tensor:
+    """Reference column of Y_m0 (= [gate_l1, gate_l2, y_l0, y_l1m0, y_l2m0], C each) for each
+    column of the gate-paired order."""
+    n1 = C // 32
+    cols = []
+    for p in range(5 * C // 64):
+        for h in range(2):
+            for c in range(32):
+                if p < n1:
+                    cols.append((0 if h == 0 else 3 * C) + 32 * p + c)
+                elif p < 2 * n1:
+                    cols.append((C if h == 0 else 4 * C) + 32 * (p - n1) + c)
+                else:
+                    cols.append(2 * C + 64 * p + 32 * h + c - 4 * C)
+    return torch.tensor(cols, dtype=torch.long)
 
 
 class FusedGatingSplit(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, Y_m0, Y_m1, Y_m2, C):
+    def forward(ctx, Y_m0, Y_m1, Y_m2, C, layout=0):
         Y_m0 = _lib.require(Y_m0, torch.float32, "Y_m0")
         Y_m1 = _lib.require(Y_m1, torch.float32, "Y_m1")
         Y_m2 = _lib.require(Y_m2, torch.float32, "Y_m2")
@@ -19,25 +43,73 @@ class FusedGatingSplit(torch.autograd.Function):
         Z_m1 = torch.empty((E, Z_M1_MULT * C), device=dev, dtype=torch.float32)
         Z_m2 = torch.empty((E, Z_M2_MULT * C), device=dev, dtype=torch.float32)
         _lib.call("fu_gating_fwd", Y_m0.data_ptr(), Y_m1.data_ptr(), Y_m2.data_ptr(), Z_m0.data_ptr(),
-                  Z_m1.data_ptr(), Z_m2.data_ptr(), E, C, _lib.stream_ptr(dev))
+                  Z_m1.data_ptr(), Z_m2.data_ptr(), E, C, int(layout), _lib.stream_ptr(dev))
         ctx.save_for_backward(Y_m0, Y_m1, Y_m2)
-        ctx.C = C
+        ctx.C, ctx.layout = C, int(layout)
         return Z_m0, Z_m1, Z_m2
 
     @staticmethod
     def backward(ctx, g_z_m0, g_z_m1, g_z_m2):
         Y_m0, Y_m1, Y_m2 = ctx.saved_tensors
-        E, C = Y_m0.shape[0], ctx.C
-        g_z_m0 = torch.zeros_like(Y_m0[:, : 3 * C]) if g_z_m0 is None else g_z_m0.contiguous()
-        g_z_m1 = torch.zeros_like(Y_m1) if g_z_m1 is None else g_z_m1.contiguous()
-        g_z_m2 = torch.zeros_like(Y_m2) if g_z_m2 is None else g_z_m2.contiguous()
-        g_y_m0 = torch.empty_like(Y_m0)
-        g_y_m1 = torch.empty_like(Y_m1)
-        g_y_m2 = torch.empty_like(Y_m2)
-        _lib.call("fu_gating_bwd", g_z_m0.data_ptr(), g_z_m1.data_ptr(), g_z_m2.data_ptr(), Y_m0.data_ptr(),
-                  Y_m1.data_ptr(), Y_m2.data_ptr(), g_y_m0.data_ptr(), g_y_m1.data_ptr(), g_y_m2.data_ptr(), E, C,
-                  _lib.stream_ptr(Y_m0.device))
-        return g_y_m0, g_y_m1, g_y_m2, None
+        return _gating_bwd(Y_m0, Y_m1, Y_m2, g_z_m0, g_z_m1, g_z_m2, ctx.C, ctx.layout) + (None, None)
 
 
-fused_gating_split = FusedGatingSplit.apply
+def _gating_bwd(Y_m0, Y_m1, Y_m2, g_z_m0, g_z_m1, g_z_m2, C, layout):
+    E = Y_m0.shape[0]
+    g_z_m0 = torch.zeros(E, 3 * C, device=Y_m0.device) if g_z_m0 is None else g_z_m0.contiguous()
+    g_z_m1 = torch.zeros_like(Y_m1) if g_z_m1 is None else g_z_m1.contiguous()
+    g_z_m2 = torch.zeros_like(Y_m2) if g_z_m2 is None else g_z_m2.contiguous()
+    g_y_m0 = torch.empty_like(Y_m0)
+    g_y_m1 = torch.empty_like(Y_m1)
+    g_y_m2 = torch.empty_like(Y_m2)
+    _lib.call("fu_gating_bwd", g_z_m0.data_ptr(), g_z_m1.data_ptr(), g_z_m2.data_ptr(), Y_m0.data_ptr(),
+              Y_m1.data_ptr(), Y_m2.data_ptr(), g_y_m0.data_ptr(), g_y_m1.data_ptr(), g_y_m2.data_ptr(), E, C,
+              int(layout), _lib.stream_ptr(Y_m0.device))
+    return g_y_m0, g_y_m1, g_y_m2
+
+
+def fused_gating_split(Y_m0, Y_m1, Y_m2, C, layout=0):
+    return FusedGatingSplit.apply(Y_m0, Y_m1, Y_m2, C, layout)
+
+
+class Conv1Gate(torch.autograd.Function):
+    """X_m0, X_m1, X_m2 -> Z_m0, Z_m1, Z_m2: conv1 m = 0 (W0 rows and b0 in the gate-paired
+    order, W0t = W0^T) and the complex m = 1, 2 layers (P + iQ, with Pt = P^T, Qtn = -Q^T for
+    the input gradient), gated in their epilogues.  Saves Y (pre-activation) for the gate
+    backward, which runs as the separate kernel before the input-gradient GEMMs."""
+
+    @staticmethod
+    def forward(ctx, X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C):
+        X0 = _lib.require(X0, torch.float32, "X_m0")
+        X1 = _lib.require(X1, torch.float32, "X_m1")
+        X2 = _lib.require(X2, torch.float32, "X_m2")
+        E = X0.shape[0]
+        dev = X0.device
+        st = _lib.stream_ptr(dev)
+        f = lambda *s: torch.empty(*s, device=dev, dtype=torch.float32)
+        Y0, Z0, S = f(E, 5 * C), f(E, Z_M0_MULT * C), f(E, 2 * C)
+        _lib.call("fu_linear_gate", X0.data_ptr(), X0.stride(0), W0.data_ptr(), W0.stride(0), _lib.ptr(b0),
+                  Y0.data_ptr(), Y0.stride(0), Z0.data_ptr(), Z0.stride(0), S.data_ptr(), S.stride(0), E, C,
+                  W0.shape[1], st)
+        outs = []
+        for X, P, Q, s_off in ((X1, P1, Q1, 0), (X2, P2, Q2, C)):
+            Nc, Kc = P.shape
+            Y, Z = f(E, 2 * Nc), f(E, 2 * Nc)
+            _lib.call("fu_complex_linear_gate", X.data_ptr(), X[:, Kc:].data_ptr(), X.stride(0), P.data_ptr(),
+                      Q.data_ptr(), P.stride(0), Y.data_ptr(), Y[:, Nc:].data_ptr(), Y.stride(0), Z.data_ptr(),
+                      Z[:, Nc:].data_ptr(), Z.stride(0), S.data_ptr(), S.stride(0), s_off, E, Nc, Kc, st)
+            outs += [Y, Z]
+        Y1, Z1, Y2, Z2 = outs
+        ctx.save_for_backward(Y0, Y1, Y2, W0t, P1t, Q1tn, P2t, Q2tn)
+        ctx.C = C
+        return Z0, Z1, Z2
+
+    @staticmethod
+    def backward(ctx, g_z0, g_z1, g_z2):
+        Y0, Y1, Y2, W0t, P1t, Q1tn, P2t, Q2tn = ctx.saved_tensors
+        g_y0, g_y1, g_y2 = _gating_bwd(Y0, Y1, Y2, g_z0, g_z1, g_z2, ctx.C, 1)
+        return (gemm(g_y0, W0t), complex_gemm(g_y1, P1t, Q1tn), complex_gemm(g_y2, P2t, Q2tn)) + (None,) * 12
+
+
+def conv1_gate(X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C):
+    return Conv1Gate.apply(X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C)

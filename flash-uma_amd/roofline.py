@@ -102,6 +102,19 @@ def _complex_linear(a):
     return 4 * (2 * M * Kc + 2 * M * Nc + 2 * Nc * Kc), 6 * M * Nc * Kc
 
 
+def _linear_gate(a):
+    # N = 5C outputs Y plus the gate's sigmoids S (2C) and gated / SiLU copies Z (3C)
+    M, C, K = a[11], a[12], a[13]
+    N = 5 * C
+    return 4 * (M * K + N * K + M * N + 5 * M * C), 2 * M * N * K
+
+
+def _complex_linear_gate(a):
+    # complex product plus the sigmoid read S (Nc) and the gated copies Z_r, Z_i (2 Nc)
+    M, Nc, Kc = a[15], a[16], a[17]
+    return 4 * (2 * M * Kc + 2 * M * Nc + 2 * Nc * Kc + 3 * M * Nc), 6 * M * Nc * Kc
+
+
 def _ln_grouped_fwd(a):
     # x read + out written per row and group, mean/rstd; with tables: two int64 edge ids per
     # row and the (L2-resident) 100-row tables once per launch
@@ -135,9 +148,11 @@ WORK = {
     "fu_linear": _linear,
     "fu_linear_batched": _linear_batched,
     "fu_complex_linear": _complex_linear,
+    "fu_linear_gate": _linear_gate,
+    "fu_complex_linear_gate": _complex_linear_gate,
 }
 
-MFMA_BOUND = {"fu_linear", "fu_linear_batched", "fu_complex_linear"}
+MFMA_BOUND = {"fu_linear", "fu_linear_batched", "fu_complex_linear", "fu_linear_gate", "fu_complex_linear_gate"}
 
 
 def summarize(durations) -> dict:

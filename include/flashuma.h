@@ -108,14 +108,18 @@ int fu_gather_bwd(const float* g_X_m0, const float* g_X_m1, const float* g_X_m2,
  * Gate activation (replaces FusedGatingSplit, ops/gating.py:188-234)
  * ------------------------------------------------------------------------------------ */
 
-/* ops/gating.py:32-103 (_gating_split_fwd_kernel). */
+/* ops/gating.py:32-103 (_gating_split_fwd_kernel).  layout 0: Y_m0 in the reference column
+ * order [gate_l1, gate_l2, y_l0, y_l1m0, y_l2m0]; layout 1: the gate-paired order of
+ * fu_linear_gate (64-column pairs [gate_l1 | y_l1m0] x C/32, [gate_l2 | y_l2m0] x C/32, then
+ * y_l0; C a multiple of 64). */
 int fu_gating_fwd(const float* Y_m0, const float* Y_m1, const float* Y_m2, float* Z_m0,
-                  float* Z_m1, float* Z_m2, int64_t E, int32_t C, void* stream);
+                  float* Z_m1, float* Z_m2, int64_t E, int32_t C, int32_t layout, void* stream);
 
-/* ops/gating.py:109-185 (_gating_split_bwd_kernel). */
+/* ops/gating.py:109-185 (_gating_split_bwd_kernel).  layout as in fu_gating_fwd, for Y_m0 and
+ * g_Y_m0. */
 int fu_gating_bwd(const float* g_Z_m0, const float* g_Z_m1, const float* g_Z_m2, const float* Y_m0,
                   const float* Y_m1, const float* Y_m2, float* g_Y_m0, float* g_Y_m1,
-                  float* g_Y_m2, int64_t E, int32_t C, void* stream);
+                  float* g_Y_m2, int64_t E, int32_t C, int32_t layout, void* stream);
 
 /* ------------------------------------------------------------------------------------
  * Rotate-scatter (replaces RotateScatterSplit, ops/scatter.py:295-352)
@@ -212,6 +216,23 @@ int fu_linear_batched(const float* A, int64_t lda, int64_t stride_a, const float
 int fu_complex_linear(const float* A_r, const float* A_i, int64_t lda, const float* P, const float* Q,
                       int64_t ldw, float* Y_r, float* Y_i, int64_t ldy, int64_t M, int32_t Nc,
                       int32_t Kc, void* stream);
+
+/* conv1 m = 0 fused with the gate activation (model.py:152-153 with ops/gating.py:32-103):
+ * Y = A W^T + bias with N = 5C columns in the gate-paired order (W and bias rows permuted to
+ * it, see fu_gating_fwd layout 1), written for the backward, plus Z (M, 3C) =
+ * [silu(y_l0), y_l1m0 s1, y_l2m0 s2] and S (M, 2C) = [s1, s2], s = sigmoid(gate).
+ * C a multiple of 64; other constraints as fu_linear. */
+int fu_linear_gate(const float* A, int64_t lda, const float* W, int64_t ldw, const float* bias,
+                   float* Y, int64_t ldy, float* Z, int64_t ldz, float* S, int64_t lds, int64_t M,
+                   int32_t C, int32_t K, void* stream);
+
+/* conv1 m = 1, 2 fused with the gate activation: fu_complex_linear, then
+ * Z_r = Y_r s, Z_i = Y_i s with s = S[row][s_off + column] (S from fu_linear_gate: s_off = 0
+ * for m = 1, whose columns are [l1 | l2]; s_off = C for m = 2). */
+int fu_complex_linear_gate(const float* A_r, const float* A_i, int64_t lda, const float* P,
+                           const float* Q, int64_t ldw, float* Y_r, float* Y_i, int64_t ldy,
+                           float* Z_r, float* Z_i, int64_t ldz, const float* S, int64_t lds,
+                           int32_t s_off, int64_t M, int32_t Nc, int32_t Kc, void* stream);
 
 /* ------------------------------------------------------------------------------------
  * Node-level modules attached to the backbone (model.py:145,157,218) and input plumbing

@@ -37,11 +37,11 @@ def _status(name, *args):
 
 def test_error_codes():
     # FU_ERR_SHAPE = -1, UNSUPPORTED = -2, ALIGN = -3, NULL = -5, WORKSPACE = -6
-    st, msg = _status("fu_gating_fwd", None, None, None, None, None, None, 10, 6, None)
+    st, msg = _status("fu_gating_fwd", None, None, None, None, None, None, 10, 6, 0, None)
     assert st == -2 and "multiple of 4" in msg
-    st, msg = _status("fu_gating_fwd", None, None, None, None, None, None, 10, 128, None)
+    st, msg = _status("fu_gating_fwd", None, None, None, None, None, None, 10, 128, 0, None)
     assert st == -5
-    st, _ = _status("fu_gating_fwd", None, None, None, None, None, None, -1, 128, None)
+    st, _ = _status("fu_gating_fwd", None, None, None, None, None, None, -1, 128, 0, None)
     assert st == -1
     st, msg = _status("fu_linear", 16, 8, 16, 8, None, 16, 8, 10, 8, 6, None)
     assert st == -2 and "multiples of 4" in msg
@@ -65,7 +65,7 @@ def test_error_codes():
 
 def test_zero_sized_calls_are_no_ops():
     # E == 0 returns before any launch
-    st, _ = _status("fu_gating_fwd", 16, 16, 16, 16, 16, 16, 0, 128, None)
+    st, _ = _status("fu_gating_fwd", 16, 16, 16, 16, 16, 16, 0, 128, 0, None)
     assert st == 0
     st, _ = _status("fu_linear", 16, 8, 16, 8, None, 16, 8, 0, 8, 8, None)
     assert st == 0

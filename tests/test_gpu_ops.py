@@ -31,20 +31,57 @@ def _vjp(fn, inputs, cot):
     return outs, grads
 
 
-def test_gating(cuda):
+@pytest.mark.parametrize("layout", [0, 1])
+def test_gating(cuda, layout):
+    """layout 1: Y_m0 (and its gradient) in the gate-paired column order."""
     _, gating, *_ = _ops()
     torch.manual_seed(0)
     E, C = 333, 128
     Y = [torch.randn(E, m * C) for m in (5, 4, 2)]
-    Yg = [y.to(cuda).requires_grad_(True) for y in Y]
-    Z = gating.fused_gating_split(*Yg, C)
+    rows = gating.gate_paired_rows(C) if layout else torch.arange(5 * C)
+    Yg = [Y[0][:, rows].to(cuda).requires_grad_(True)] + [y.to(cuda).requires_grad_(True) for y in Y[1:]]
+    Z = gating.fused_gating_split(*Yg, C, layout)
     cot = [torch.randn_like(z.cpu()) for z in Z]
     ref, gref = _vjp(lambda a, b, c: R.gating(a, b, c, C), Y, cot)
     for z, r in zip(Z, ref):
         assert_close(z, r, TOL, "gating fwd")
     g = torch.autograd.grad(Z, Yg, [c.to(cuda) for c in cot])
-    for a, b in zip(g, gref):
+    for a, b in zip(g, [gref[0][:, rows]] + list(gref[1:])):
         assert_close(a, b, TOL, "gating bwd")
+
+
+@pytest.mark.parametrize("M,C", [(300, 128), (77, 64)])
+def test_conv1_gate(cuda, M, C):
+    """conv1 (m0 real with bias, m1 and m2 complex) with the gate activation in the GEMM
+    epilogues, against the textbook Y = X W^T (+ b) and the oracle gating in float64."""
+    _, gating, *_ = _ops()
+    g = torch.Generator().manual_seed(M + C)
+    r = lambda *s: torch.randn(*s, generator=g)
+    X = [r(M, 6 * C), r(M, 8 * C), r(M, 4 * C)]
+    W0, b0 = r(5 * C, 6 * C) / (6 * C) ** 0.5, r(5 * C) * 0.3
+    R1, I1 = r(2 * C, 4 * C) / (4 * C) ** 0.5, r(2 * C, 4 * C) / (4 * C) ** 0.5
+    R2, I2 = r(C, 2 * C) / (2 * C) ** 0.5, r(C, 2 * C) / (2 * C) ** 0.5
+    rows = gating.gate_paired_rows(C)
+    dv = lambda t: t.contiguous().to(cuda)
+    W0p = W0[rows]
+    args = [dv(W0p), dv(b0[rows]), dv(W0p.t()), dv(R1), dv(I1), dv(R1.t()), dv(-I1.t()), dv(R2), dv(I2), dv(R2.t()),
+            dv(-I2.t())]
+    Xg = [x.to(cuda).requires_grad_(True) for x in X]
+    Z = gating.conv1_gate(*Xg, *args, C)
+    cot = [r(*z.shape) for z in Z]
+
+    def ref_fn(x0, x1, x2):
+        y0 = x0 @ W0.double().T + b0.double()
+        y1 = x1 @ R.pack_so2(R1.double(), I1.double()).T
+        y2 = x2 @ R.pack_so2(R2.double(), I2.double()).T
+        return R.gating(y0, y1, y2, C)
+
+    ref, gref = _vjp(ref_fn, X, cot)
+    for z, rr in zip(Z, ref):
+        assert_close(z, rr, TOL, "conv1+gate fwd")
+    gx = torch.autograd.grad(Z, Xg, [c.to(cuda) for c in cot])
+    for a, b in zip(gx, gref):
+        assert_close(a, b, 1e-4, "conv1+gate bwd")
 
 
 def test_ln_silu(cuda):
