@@ -4,24 +4,27 @@
 // row permutations of node and edge arrays (model.py:72-74,221) and the PBC shift product
 // with its deterministic cell-gradient reduction (wrapper.py:193-194).
 //
-// Norm / gate: one wave64 per atom, lanes across channels, the 9 (lmax = 2) coefficient rows
-// in registers; row statistics are wave reductions.
+// Norm / gate: one wave64 per atom, lanes across channels, the (lmax + 1)^2 coefficient rows
+// (lmax = 2, 3 or 4) in registers; row statistics are wave reductions.
 #include "fu_vec.h"
 
 namespace fu {
 
-constexpr int NK = 9;  // (lmax + 1)^2 with lmax = 2
-__device__ __forceinline__ int deg_of(int k) { return k == 0 ? 0 : (k < 4 ? 1 : 2); }
+// degree l of SH coefficient k = l^2 + l + m
+__device__ __forceinline__ constexpr int deg_of(int k) { return k < 1 ? 0 : k < 4 ? 1 : k < 9 ? 2 : k < 16 ? 3 : 4; }
+// degree-balanced weight 1 / ((2l + 1)(lmax + 1))
+template <int L>
+__device__ __forceinline__ constexpr float bal_of(int l) { return 1.0f / (float)((2 * l + 1) * (L + 1)); }
 
 __device__ __forceinline__ int wave_id_n() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
 // out = feat * (ms + eps)^-1/2 * w[deg] (+ b on l=0), feat = x with l=0 centred over channels,
 // ms = mean_c sum_k feat_kc^2 / ((2 l_k + 1)(lmax + 1)).
-template <int CPL>
+template <int CPL, int L>
 __global__ __launch_bounds__(256) void rms_norm_fwd_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                            const float* __restrict__ b, float* __restrict__ out,
                                                            float* __restrict__ inv_rms, int64_t N, float eps) {
-  constexpr int C = 64 * CPL;
+  constexpr int C = 64 * CPL, NK = (L + 1) * (L + 1);
   const int lane = threadIdx.x & 63, c = lane * CPL;
   const int64_t n = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave_id_n();
   if (n >= N) return;
@@ -35,10 +38,9 @@ __global__ __launch_bounds__(256) void rms_norm_fwd_kernel(const float* __restri
   const float mean0 = wave_sum(s0) / C;
 #pragma unroll
   for (int q = 0; q < CPL; ++q) f[0][q] -= mean0;
-  const float bal[3] = {1.0f / 3.0f, 1.0f / 9.0f, 1.0f / 15.0f};  // 1 / ((2l+1)(lmax+1))
   float ss = 0.0f;
 #pragma unroll
-  for (int k = 0; k < NK; ++k) ss += bal[deg_of(k)] * vdot(f[k], f[k]);
+  for (int k = 0; k < NK; ++k) ss += bal_of<L>(deg_of(k)) * vdot(f[k], f[k]);
   const float ms = wave_sum(ss) / C;
   const float inv = 1.0f / sqrtf(ms + eps);
   if (lane == 0) inv_rms[n] = inv;
@@ -54,12 +56,12 @@ __global__ __launch_bounds__(256) void rms_norm_fwd_kernel(const float* __restri
   }
 }
 
-template <int CPL>
+template <int CPL, int L>
 __global__ __launch_bounds__(256) void rms_norm_bwd_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                            const float* __restrict__ inv_rms,
                                                            const float* __restrict__ g_out, float* __restrict__ g_x,
                                                            int64_t N) {
-  constexpr int C = 64 * CPL;
+  constexpr int C = 64 * CPL, NK = (L + 1) * (L + 1);
   const int lane = threadIdx.x & 63, c = lane * CPL;
   const int64_t n = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave_id_n();
   if (n >= N) return;
@@ -75,7 +77,6 @@ __global__ __launch_bounds__(256) void rms_norm_bwd_kernel(const float* __restri
 #pragma unroll
   for (int q = 0; q < CPL; ++q) f[0][q] -= mean0;
   const float inv = inv_rms[n];
-  const float bal[3] = {1.0f / 3.0f, 1.0f / 9.0f, 1.0f / 15.0f};
   float s = 0.0f;  // sum_kc g_out w feat
 #pragma unroll
   for (int k = 0; k < NK; ++k) {
@@ -90,7 +91,7 @@ __global__ __launch_bounds__(256) void rms_norm_bwd_kernel(const float* __restri
 #pragma unroll
   for (int k = 0; k < NK; ++k)
 #pragma unroll
-    for (int q = 0; q < CPL; ++q) gf[k][q] = inv * gw[k][q] - coef * bal[deg_of(k)] * f[k][q];
+    for (int q = 0; q < CPL; ++q) gf[k][q] = inv * gw[k][q] - coef * bal_of<L>(deg_of(k)) * f[k][q];
   float t0 = 0.0f;
 #pragma unroll
   for (int q = 0; q < CPL; ++q) t0 += gf[0][q];
@@ -103,19 +104,19 @@ __global__ __launch_bounds__(256) void rms_norm_bwd_kernel(const float* __restri
 }
 
 // Gate activation of the atom-wise FFN: gates = sigmoid(silu(pre)) per degree l >= 1 and
-// channel; out_0 = silu(h_0), out_k = h_k * gate[l_k] for k >= 1.  pre is (N, 2H), h and out
-// are (N, 9, H).
-template <int CPL>
+// channel; out_0 = silu(h_0), out_k = h_k * gate[l_k] for k >= 1.  pre is (N, lmax H), h and
+// out are (N, (lmax + 1)^2, H).
+template <int CPL, int L>
 __global__ __launch_bounds__(256) void gate_fwd_kernel(const float* __restrict__ pre, const float* __restrict__ h,
                                                        float* __restrict__ out, int64_t N) {
-  constexpr int H = 64 * CPL;
+  constexpr int H = 64 * CPL, NK = (L + 1) * (L + 1);
   const int lane = threadIdx.x & 63, c = lane * CPL;
   const int64_t n = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave_id_n();
   if (n >= N) return;
-  Vec<CPL> gate[2];
+  Vec<CPL> gate[L];
 #pragma unroll
-  for (int l = 0; l < 2; ++l) {
-    const Vec<CPL> p = vload<CPL>(pre + n * 2 * H + l * H + c);
+  for (int l = 0; l < L; ++l) {
+    const Vec<CPL> p = vload<CPL>(pre + n * L * H + l * H + c);
 #pragma unroll
     for (int q = 0; q < CPL; ++q) gate[l][q] = sigmoidf_(p[q] * sigmoidf_(p[q]));
   }
@@ -132,18 +133,18 @@ __global__ __launch_bounds__(256) void gate_fwd_kernel(const float* __restrict__
   for (int k = 1; k < NK; ++k) vstore(on + k * H, vmul(vload<CPL>(hn + k * H), gate[deg_of(k) - 1]));
 }
 
-template <int CPL>
+template <int CPL, int L>
 __global__ __launch_bounds__(256) void gate_bwd_kernel(const float* __restrict__ pre, const float* __restrict__ h,
                                                        const float* __restrict__ g_out, float* __restrict__ g_pre,
                                                        float* __restrict__ g_h, int64_t N) {
-  constexpr int H = 64 * CPL;
+  constexpr int H = 64 * CPL, NK = (L + 1) * (L + 1);
   const int lane = threadIdx.x & 63, c = lane * CPL;
   const int64_t n = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave_id_n();
   if (n >= N) return;
-  Vec<CPL> p[2], gate[2], ggate[2];
+  Vec<CPL> p[L], gate[L], ggate[L];
 #pragma unroll
-  for (int l = 0; l < 2; ++l) {
-    p[l] = vload<CPL>(pre + n * 2 * H + l * H + c);
+  for (int l = 0; l < L; ++l) {
+    p[l] = vload<CPL>(pre + n * L * H + l * H + c);
 #pragma unroll
     for (int q = 0; q < CPL; ++q) gate[l][q] = sigmoidf_(p[l][q] * sigmoidf_(p[l][q]));
     ggate[l] = vzero<CPL>();
@@ -170,7 +171,7 @@ __global__ __launch_bounds__(256) void gate_bwd_kernel(const float* __restrict__
     for (int q = 0; q < CPL; ++q) ggate[l][q] += gk[q] * hk[q];
   }
 #pragma unroll
-  for (int l = 0; l < 2; ++l) {
+  for (int l = 0; l < L; ++l) {
     Vec<CPL> o;
 #pragma unroll
     for (int q = 0; q < CPL; ++q) {
@@ -179,7 +180,7 @@ __global__ __launch_bounds__(256) void gate_bwd_kernel(const float* __restrict__
       const float g = gate[l][q];
       o[q] = ggate[l][q] * g * (1.0f - g) * du;
     }
-    vstore(g_pre + n * 2 * H + l * H + c, o);
+    vstore(g_pre + n * L * H + l * H + c, o);
   }
 }
 
@@ -256,11 +257,17 @@ __global__ void outer_sum3_stage2(const double* __restrict__ partial, int nblock
   }
 }
 
-template <typename K1, typename K2, typename K4>
-static int launch_cpl(int32_t C, K1 k1, K2 k2, K4 k4) {
-  if (C == 64) return k1(), FU_OK;
-  if (C == 128) return k2(), FU_OK;
-  if (C == 256) return k4(), FU_OK;
+// Calls f(CPL, lmax) as integral constants; FU_ERR_UNSUPPORTED for other C.
+template <typename F>
+static int launch_cpl_l(int32_t C, int32_t lmax, F f) {
+  auto by_l = [&](auto cpl) {
+    if (lmax == 2) f(cpl, std::integral_constant<int, 2>{});
+    else if (lmax == 3) f(cpl, std::integral_constant<int, 3>{});
+    else f(cpl, std::integral_constant<int, 4>{});
+  };
+  if (C == 64) return by_l(std::integral_constant<int, 1>{}), FU_OK;
+  if (C == 128) return by_l(std::integral_constant<int, 2>{}), FU_OK;
+  if (C == 256) return by_l(std::integral_constant<int, 4>{}), FU_OK;
   return FU_ERR_UNSUPPORTED;
 }
 
@@ -268,18 +275,20 @@ static int launch_cpl(int32_t C, K1 k1, K2 k2, K4 k4) {
 
 using namespace fu;
 
+#define FU_LMAX_CHECK(who)                                                                        \
+  if (lmax < 2 || lmax > 4) return set_error(FU_ERR_UNSUPPORTED, who ": lmax=%d unsupported (2, 3 or 4)", lmax)
+
 extern "C" int fu_rms_norm_sh_fwd(const float* x, const float* weight, const float* bias, float* out, float* inv_rms,
                                   int64_t N, int32_t C, int32_t lmax, float eps, void* stream) {
   if (N < 0) return set_error(FU_ERR_SHAPE, "fu_rms_norm_sh_fwd: bad shape");
-  if (lmax != 2) return set_error(FU_ERR_UNSUPPORTED, "fu_rms_norm_sh_fwd: lmax=%d unsupported (2)", lmax);
+  FU_LMAX_CHECK("fu_rms_norm_sh_fwd");
   if (N == 0) return FU_OK;
   if (!x || !weight || !bias || !out || !inv_rms) return set_error(FU_ERR_NULL, "fu_rms_norm_sh_fwd: NULL argument");
   hipStream_t s = as_stream(stream);
-  const dim3 g(cdiv(N, 4)), b(256);
-  int st = launch_cpl(
-      C, [&] { hipLaunchKernelGGL(rms_norm_fwd_kernel<1>, g, b, 0, s, x, weight, bias, out, inv_rms, N, eps); },
-      [&] { hipLaunchKernelGGL(rms_norm_fwd_kernel<2>, g, b, 0, s, x, weight, bias, out, inv_rms, N, eps); },
-      [&] { hipLaunchKernelGGL(rms_norm_fwd_kernel<4>, g, b, 0, s, x, weight, bias, out, inv_rms, N, eps); });
+  int st = launch_cpl_l(C, lmax, [&](auto cpl, auto lv) {
+    hipLaunchKernelGGL((rms_norm_fwd_kernel<decltype(cpl)::value, decltype(lv)::value>), dim3(cdiv(N, 4)), dim3(256),
+                       0, s, x, weight, bias, out, inv_rms, N, eps);
+  });
   if (st != FU_OK) return set_error(st, "fu_rms_norm_sh_fwd: C=%d unsupported (64, 128 or 256)", C);
   return check_launch("fu_rms_norm_sh_fwd");
 }
@@ -287,15 +296,14 @@ extern "C" int fu_rms_norm_sh_fwd(const float* x, const float* weight, const flo
 extern "C" int fu_rms_norm_sh_bwd(const float* x, const float* weight, const float* inv_rms, const float* g_out,
                                   float* g_x, int64_t N, int32_t C, int32_t lmax, void* stream) {
   if (N < 0) return set_error(FU_ERR_SHAPE, "fu_rms_norm_sh_bwd: bad shape");
-  if (lmax != 2) return set_error(FU_ERR_UNSUPPORTED, "fu_rms_norm_sh_bwd: lmax=%d unsupported (2)", lmax);
+  FU_LMAX_CHECK("fu_rms_norm_sh_bwd");
   if (N == 0) return FU_OK;
   if (!x || !weight || !inv_rms || !g_out || !g_x) return set_error(FU_ERR_NULL, "fu_rms_norm_sh_bwd: NULL argument");
   hipStream_t s = as_stream(stream);
-  const dim3 g(cdiv(N, 4)), b(256);
-  int st = launch_cpl(
-      C, [&] { hipLaunchKernelGGL(rms_norm_bwd_kernel<1>, g, b, 0, s, x, weight, inv_rms, g_out, g_x, N); },
-      [&] { hipLaunchKernelGGL(rms_norm_bwd_kernel<2>, g, b, 0, s, x, weight, inv_rms, g_out, g_x, N); },
-      [&] { hipLaunchKernelGGL(rms_norm_bwd_kernel<4>, g, b, 0, s, x, weight, inv_rms, g_out, g_x, N); });
+  int st = launch_cpl_l(C, lmax, [&](auto cpl, auto lv) {
+    hipLaunchKernelGGL((rms_norm_bwd_kernel<decltype(cpl)::value, decltype(lv)::value>), dim3(cdiv(N, 4)), dim3(256),
+                       0, s, x, weight, inv_rms, g_out, g_x, N);
+  });
   if (st != FU_OK) return set_error(st, "fu_rms_norm_sh_bwd: C=%d unsupported (64, 128 or 256)", C);
   return check_launch("fu_rms_norm_sh_bwd");
 }
@@ -303,15 +311,14 @@ extern "C" int fu_rms_norm_sh_bwd(const float* x, const float* weight, const flo
 extern "C" int fu_gate_act_fwd(const float* pre, const float* h, float* out, int64_t N, int32_t H, int32_t lmax,
                                void* stream) {
   if (N < 0) return set_error(FU_ERR_SHAPE, "fu_gate_act_fwd: bad shape");
-  if (lmax != 2) return set_error(FU_ERR_UNSUPPORTED, "fu_gate_act_fwd: lmax=%d unsupported (2)", lmax);
+  FU_LMAX_CHECK("fu_gate_act_fwd");
   if (N == 0) return FU_OK;
   if (!pre || !h || !out) return set_error(FU_ERR_NULL, "fu_gate_act_fwd: NULL argument");
   hipStream_t s = as_stream(stream);
-  const dim3 g(cdiv(N, 4)), b(256);
-  int st = launch_cpl(
-      H, [&] { hipLaunchKernelGGL(gate_fwd_kernel<1>, g, b, 0, s, pre, h, out, N); },
-      [&] { hipLaunchKernelGGL(gate_fwd_kernel<2>, g, b, 0, s, pre, h, out, N); },
-      [&] { hipLaunchKernelGGL(gate_fwd_kernel<4>, g, b, 0, s, pre, h, out, N); });
+  int st = launch_cpl_l(H, lmax, [&](auto cpl, auto lv) {
+    hipLaunchKernelGGL((gate_fwd_kernel<decltype(cpl)::value, decltype(lv)::value>), dim3(cdiv(N, 4)), dim3(256), 0,
+                       s, pre, h, out, N);
+  });
   if (st != FU_OK) return set_error(st, "fu_gate_act_fwd: H=%d unsupported (64, 128 or 256)", H);
   return check_launch("fu_gate_act_fwd");
 }
@@ -319,15 +326,14 @@ extern "C" int fu_gate_act_fwd(const float* pre, const float* h, float* out, int
 extern "C" int fu_gate_act_bwd(const float* pre, const float* h, const float* g_out, float* g_pre, float* g_h,
                                int64_t N, int32_t H, int32_t lmax, void* stream) {
   if (N < 0) return set_error(FU_ERR_SHAPE, "fu_gate_act_bwd: bad shape");
-  if (lmax != 2) return set_error(FU_ERR_UNSUPPORTED, "fu_gate_act_bwd: lmax=%d unsupported (2)", lmax);
+  FU_LMAX_CHECK("fu_gate_act_bwd");
   if (N == 0) return FU_OK;
   if (!pre || !h || !g_out || !g_pre || !g_h) return set_error(FU_ERR_NULL, "fu_gate_act_bwd: NULL argument");
   hipStream_t s = as_stream(stream);
-  const dim3 g(cdiv(N, 4)), b(256);
-  int st = launch_cpl(
-      H, [&] { hipLaunchKernelGGL(gate_bwd_kernel<1>, g, b, 0, s, pre, h, g_out, g_pre, g_h, N); },
-      [&] { hipLaunchKernelGGL(gate_bwd_kernel<2>, g, b, 0, s, pre, h, g_out, g_pre, g_h, N); },
-      [&] { hipLaunchKernelGGL(gate_bwd_kernel<4>, g, b, 0, s, pre, h, g_out, g_pre, g_h, N); });
+  int st = launch_cpl_l(H, lmax, [&](auto cpl, auto lv) {
+    hipLaunchKernelGGL((gate_bwd_kernel<decltype(cpl)::value, decltype(lv)::value>), dim3(cdiv(N, 4)), dim3(256), 0,
+                       s, pre, h, g_out, g_pre, g_h, N);
+  });
   if (st != FU_OK) return set_error(st, "fu_gate_act_bwd: H=%d unsupported (64, 128 or 256)", H);
   return check_launch("fu_gate_act_bwd");
 }

@@ -15,6 +15,11 @@ Differences in mechanism (not in results):
   - the m = 1, 2 SO(2) layers keep their weights as complex pairs (R, I) and run the
     three-product complex layer instead of the packed [[R, -I], [I, R]] GEMM: the same
     product, one quarter fewer flops.
+
+lmax: the reference builds lmax = 2 only (wrapper.py:105-118).  Here lmax = 3 and 4 are
+supported too (mmax = 2): the per-edge blocks grow degree by degree in the reference's order
+(ops/lmax.py), the Wigner rows of degree 3 and 4 come from fu_wigner_ext_fwd, and the layer
+runs the unfused conv1 + gate of that order.  lmax = 2 keeps the fused, permuted layout below.
 """
 from __future__ import annotations
 
@@ -27,6 +32,7 @@ from ops.gather import LAYOUT1_PERM, block_permutation, gather_wigner_split
 from ops.gating import conv1_gate, gate_paired_rows
 from ops.geom import precompute_geometry
 from ops.linear import complex_linear, linear
+from ops.lmax import gating_lmax, gather_rotate_lmax, init_node_scatter_lmax, rotate_scatter_lmax, wigner_extend
 from ops.ln_silu import layer_norm_silu
 from ops.node import permute_rows
 from ops.radial import RadialBank
@@ -84,23 +90,29 @@ def _frozen(t: torch.Tensor) -> torch.Tensor:
 class Packed_eSCN_Layer(nn.Module):
     """One eSCN-MD message-passing block (model.py:81-157)."""
 
-    def __init__(self, C: int, B: int):
+    def __init__(self, C: int, B: int, lmax: int = 2):
         super().__init__()
-        self.C = C
+        if lmax not in (2, 3, 4):
+            raise ValueError(f"lmax={lmax} unsupported (2, 3 or 4)")
+        self.C, self.lmax = C, lmax
+        L = lmax
         z = torch.zeros
         self.W_rad1_1 = nn.Parameter(z(C, B + 2 * C)); self.b_rad1_1 = nn.Parameter(z(C))
         self.gamma_rad1_1 = nn.Parameter(torch.ones(C)); self.beta_rad1_1 = nn.Parameter(z(C))
         self.W_rad1_2 = nn.Parameter(z(C, C)); self.b_rad1_2 = nn.Parameter(z(C))
         self.gamma_rad1_2 = nn.Parameter(torch.ones(C)); self.beta_rad1_2 = nn.Parameter(z(C))
-        self.W_rad1_3 = nn.Parameter(z(12 * C, C)); self.b_rad1_3 = nn.Parameter(z(12 * C))
+        self.W_rad1_3 = nn.Parameter(z(6 * L * C, C)); self.b_rad1_3 = nn.Parameter(z(6 * L * C))
 
-        self.W1_m0 = nn.Parameter(z(5 * C, 6 * C)); self.b1_m0 = nn.Parameter(z(5 * C))
-        self.W1_m1_R = nn.Parameter(z(2 * C, 4 * C)); self.W1_m1_I = nn.Parameter(z(2 * C, 4 * C))
-        self.W1_m2_R = nn.Parameter(z(1 * C, 2 * C)); self.W1_m2_I = nn.Parameter(z(1 * C, 2 * C))
+        # m = 0: (L+1) degrees x (sender, receiver) in, L gates + (L+1) values out; m = 1, 2:
+        # complex maps over the n = L + 1 - m degrees that carry order m
+        self.W1_m0 = nn.Parameter(z((2 * L + 1) * C, 2 * (L + 1) * C)); self.b1_m0 = nn.Parameter(z((2 * L + 1) * C))
+        self.W1_m1_R = nn.Parameter(z(L * C, 2 * L * C)); self.W1_m1_I = nn.Parameter(z(L * C, 2 * L * C))
+        self.W1_m2_R = nn.Parameter(z((L - 1) * C, 2 * (L - 1) * C))
+        self.W1_m2_I = nn.Parameter(z((L - 1) * C, 2 * (L - 1) * C))
 
-        self.W2_m0 = nn.Parameter(z(3 * C, 3 * C)); self.b2_m0 = nn.Parameter(z(3 * C))
-        self.W2_m1_R = nn.Parameter(z(2 * C, 2 * C)); self.W2_m1_I = nn.Parameter(z(2 * C, 2 * C))
-        self.W2_m2_R = nn.Parameter(z(1 * C, 1 * C)); self.W2_m2_I = nn.Parameter(z(1 * C, 1 * C))
+        self.W2_m0 = nn.Parameter(z((L + 1) * C, (L + 1) * C)); self.b2_m0 = nn.Parameter(z((L + 1) * C))
+        self.W2_m1_R = nn.Parameter(z(L * C, L * C)); self.W2_m1_I = nn.Parameter(z(L * C, L * C))
+        self.W2_m2_R = nn.Parameter(z((L - 1) * C, (L - 1) * C)); self.W2_m2_I = nn.Parameter(z((L - 1) * C, (L - 1) * C))
 
         self.norm_1 = None; self.norm_2 = None; self.atom_wise = None
         self.prepared = False
@@ -131,6 +143,9 @@ class Packed_eSCN_Layer(nn.Module):
             for mod in (self.norm_1, self.norm_2, self.atom_wise):
                 for p in mod.parameters():
                     p.requires_grad = False
+        if self.lmax != 2:
+            self._prepare_reference_order(dtype)
+            return
         # Slot layout 1 of the gather (ops/gather.py): the radial output blocks and the conv1
         # input columns are permuted alike, so rad -> X -> conv1 computes the same products
         # while each side's share of an edge row is contiguous for the gather backward and
@@ -164,6 +179,25 @@ class Packed_eSCN_Layer(nn.Module):
         del self.W2_m0, self.b2_m0, self.W2_m1_R, self.W2_m1_I, self.W2_m2_R, self.W2_m2_I
         self.prepared = True
 
+    def _prepare_reference_order(self, dtype):
+        """lmax > 2: weights in the reference's block order (ops/lmax.py); conv1 m = 0 and the
+        gate run as separate kernels."""
+        for name in ("W_rad1_1", "W_rad1_2", "W_rad1_3"):
+            W = getattr(self, name).data
+            self.register_buffer(name + "_t", W.to(dtype).t().contiguous())
+        self._register("W_conv1_m0", self.W1_m0.data, dtype)
+        self.register_buffer("b_conv1_m0", _frozen(self.b1_m0.data).to(dtype))
+        self._register_complex("W_conv1_m1", self.W1_m1_R.data, self.W1_m1_I.data, dtype)
+        self._register_complex("W_conv1_m2", self.W1_m2_R.data, self.W1_m2_I.data, dtype)
+        self._register("W_conv2_m0", self.W2_m0.data, dtype)
+        self.register_buffer("b_conv2_m0", _frozen(self.b2_m0.data).to(dtype))
+        self._register_complex("W_conv2_m1", self.W2_m1_R.data, self.W2_m1_I.data, dtype)
+        self._register_complex("W_conv2_m2", self.W2_m2_R.data, self.W2_m2_I.data, dtype)
+        del self.W1_m0, self.b1_m0, self.W1_m1_R, self.W1_m1_I, self.W1_m2_R, self.W1_m2_I
+        del self.W2_m0, self.b2_m0, self.W2_m1_R, self.W2_m1_I, self.W2_m2_R, self.W2_m2_I
+        self.layout = 0
+        self.prepared = True
+
     def radial(self, x_edge_raw):
         h1 = layer_norm_silu(linear(x_edge_raw, self.W_rad1_1, self.b_rad1_1, self.W_rad1_1_t),
                              self.gamma_rad1_1, self.beta_rad1_1)
@@ -177,12 +211,16 @@ class Packed_eSCN_Layer(nn.Module):
                 self.gamma_rad1_2, self.beta_rad1_2, self.W_rad1_3, self.b_rad1_3)
 
     def forward(self, x_in, x_edge_raw, wigner, env, idx_i, idx_j, row_ptr, col_idx, csd_emb, batch,
-                topology=None, rad_out=None):
+                topology=None, rad_out=None, wig_ext=None):
         """rad_out, when given, is this block's radial-MLP output (computed by the model's
-        RadialBank); otherwise it is computed here from x_edge_raw (E, B+2C)."""
+        RadialBank); otherwise it is computed here from x_edge_raw (E, B+2C).  wig_ext: the
+        degree-3/4 Wigner rows (ops/lmax.wigner_extend), needed for lmax > 2."""
         x_norm = self.norm_1(x_in)
         if rad_out is None:
             rad_out = self.radial(x_edge_raw)
+        if self.lmax != 2:
+            return self._forward_reference_order(x_in, x_norm, rad_out, wigner, wig_ext, env, idx_i, idx_j, row_ptr,
+                                                 col_idx, csd_emb, batch, topology)
         X_m0, X_m1, X_m2 = gather_wigner_split(x_norm, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology,
                                                self.layout)
         c1 = [getattr(self, "W_conv1_m" + m + sfx) for m in "12" for sfx in ("_R", "_I", "_Rt", "_It_neg")]
@@ -195,14 +233,31 @@ class Packed_eSCN_Layer(nn.Module):
                                      x_in.shape[0])
         return self.atom_wise(self.norm_2(x_mid)) + x_mid
 
+    def _forward_reference_order(self, x_in, x_norm, rad_out, wigner, wig_ext, env, idx_i, idx_j, row_ptr, col_idx,
+                                 csd_emb, batch, topology):
+        L, C = self.lmax, self.C
+        X_m0, X_m1, X_m2 = gather_rotate_lmax(x_norm, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, topology,
+                                              L)
+        Y_m0 = linear(X_m0, self.W_conv1_m0, self.b_conv1_m0, self.W_conv1_m0_t)
+        Y_m1 = self._complex(X_m1, "W_conv1_m1")
+        Y_m2 = self._complex(X_m2, "W_conv1_m2")
+        Z_m0, Z_m1, Z_m2 = gating_lmax(Y_m0, Y_m1, Y_m2, C, L)
+        Zo_m0 = linear(Z_m0, self.W_conv2_m0, self.b_conv2_m0, self.W_conv2_m0_t)
+        Zo_m1 = self._complex(Z_m1, "W_conv2_m1")
+        Zo_m2 = self._complex(Z_m2, "W_conv2_m2")
+        x_mid = rotate_scatter_lmax(Zo_m0, Zo_m1, Zo_m2, wigner, wig_ext, env, x_in, idx_j, row_ptr, col_idx,
+                                    x_in.shape[0], L)
+        return self.atom_wise(self.norm_2(x_mid)) + x_mid
+
 
 class eSCN_Inference_Model(nn.Module):
     """eSCN-MD backbone forward (model.py:160-221)."""
 
     def __init__(self, num_layers=4, sphere_channels=128, edge_channels=128, num_distance_basis=32, cutoff=5.0,
-                 coeff_g=-0.5):
+                 coeff_g=-0.5, lmax=2):
         super().__init__()
         self.C, self.cutoff, self.coeff_g, self.B = sphere_channels, cutoff, coeff_g, num_distance_basis
+        self.lmax = lmax
         C, B = self.C, self.B
         self.W_sphere = nn.Parameter(torch.zeros(100, C))
         self.W_src = nn.Parameter(torch.zeros(100, C)); self.W_tgt = nn.Parameter(torch.zeros(100, C))
@@ -212,9 +267,10 @@ class eSCN_Inference_Model(nn.Module):
         self.gamma_rad1_1 = nn.Parameter(torch.ones(C)); self.beta_rad1_1 = nn.Parameter(torch.zeros(C))
         self.W_rad1_2 = nn.Parameter(torch.zeros(C, C)); self.b_rad1_2 = nn.Parameter(torch.zeros(C))
         self.gamma_rad1_2 = nn.Parameter(torch.ones(C)); self.beta_rad1_2 = nn.Parameter(torch.zeros(C))
-        self.W_rad1_3 = nn.Parameter(torch.zeros(3 * C, C)); self.b_rad1_3 = nn.Parameter(torch.zeros(3 * C))
+        self.W_rad1_3 = nn.Parameter(torch.zeros((lmax + 1) * C, C))
+        self.b_rad1_3 = nn.Parameter(torch.zeros((lmax + 1) * C))
 
-        self.layers = nn.ModuleList([Packed_eSCN_Layer(C, B) for _ in range(num_layers)])
+        self.layers = nn.ModuleList([Packed_eSCN_Layer(C, B, lmax) for _ in range(num_layers)])
         self.final_norm = None
         self.charge_start = 0; self.charge_end = 0; self.spin_start = 0; self.spin_end = 0
 
@@ -278,13 +334,19 @@ class eSCN_Inference_Model(nn.Module):
                                                  self.offset_g, self.coeff_g, self.cutoff, topo, False)
         # 3. Every radial MLP (edge-degree embedding + one per block) as one bank
         rads = self.radial_bank(gauss, Z_s, idx_i_s, idx_j_s)
-        # 4. Edge-degree embedding
-        x_node_s = init_node_scatter(rads[0], wigner, env, Z_s, batch_s, self.W_sphere, csd_emb, idx_j_s,
-                                     row_ptr, col_idx, N)
+        # 4. Edge-degree embedding (lmax > 2: with the degree-3/4 Wigner rows)
+        wig_ext = None
+        if self.lmax == 2:
+            x_node_s = init_node_scatter(rads[0], wigner, env, Z_s, batch_s, self.W_sphere, csd_emb, idx_j_s,
+                                         row_ptr, col_idx, N)
+        else:
+            wig_ext = wigner_extend(wigner, self.lmax)
+            x_node_s = init_node_scatter_lmax(rads[0], wigner, wig_ext, env, Z_s, batch_s, self.W_sphere, csd_emb,
+                                              idx_j_s, row_ptr, col_idx, N, self.lmax)
         # 5. Message-passing blocks
         for layer, rad in zip(self.layers, rads[1:]):
             x_node_s = layer(x_node_s, None, wigner, env, idx_i_s, idx_j_s, row_ptr, col_idx, csd_emb,
-                             batch_s, topo, rad_out=rad)
+                             batch_s, topo, rad_out=rad, wig_ext=wig_ext)
             if self.charge_end > self.charge_start or self.spin_end > self.spin_start:
                 raise NotImplementedError(
                     "charge/spin channel balancing (FAIRChem balance_channels_batched) is not available")

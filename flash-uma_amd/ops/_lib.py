@@ -63,6 +63,17 @@ SIGNATURES: dict[str, list] = {
     "fu_nlist_search": [P, P, P, P, P, I64, P, P, P, P, P, ctypes.c_double, I32, P, P, P, P, P],
     "fu_nlist_scan": [P, P, I64, P],
     "fu_nlist_emit": [P, P, P, P, I64, I32, P, P, I64, P],
+    "fu_wigner_ext_width": [I32],
+    "fu_wigner_ext_fwd": [P, P, I64, I32, P],
+    "fu_wigner_ext_bwd": [P, P, P, I64, I32, P],
+    "fu_gather_fwd_lmax": [P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, I32, P],
+    "fu_gather_bwd_lmax": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, I32, P],
+    "fu_scatter_fwd_lmax": [P, P, P, P, P, P, P, P, P, P, I64, I64, I32, I32, P],
+    "fu_scatter_bwd_lmax": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I32, I32, P],
+    "fu_init_scatter_fwd_lmax": [P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, I32, I32, P],
+    "fu_init_scatter_bwd_lmax": [P, P, P, P, P, P, P, P, P, P, I64, I64, I32, I32, P],
+    "fu_gating_fwd_lmax": [P, P, P, P, P, P, I64, I32, I32, P],
+    "fu_gating_bwd_lmax": [P, P, P, P, P, P, P, P, P, I64, I32, I32, P],
 }
 
 _lib: ctypes.CDLL | None = None

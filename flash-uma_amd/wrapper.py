@@ -17,7 +17,7 @@ from ops.node import edge_shifts
 @torch.no_grad()
 def transfer_weights(off_model, cust_model):
     """Copy parameters from an eSCNMDBackbone-shaped object (wrapper.py:22-85)."""
-    C = cust_model.C
+    C, L = cust_model.C, cust_model.lmax
     cust_model.W_sphere.copy_(off_model.sphere_embedding.weight)
     cust_model.W_src.copy_(off_model.source_embedding.weight)
     cust_model.W_tgt.copy_(off_model.target_embedding.weight)
@@ -35,15 +35,16 @@ def transfer_weights(off_model, cust_model):
         so2_2 = off_blk.edge_wise.so2_conv_2
         copy_radial(cust_blk, so2_1.rad_func.net)
         cust_blk.W1_m0.copy_(so2_1.fc_m0.weight); cust_blk.b1_m0.copy_(so2_1.fc_m0.bias)
+        # m > 0 weights: rows [:n C] real part, [n C:] imaginary part, n = L (m = 1) or L - 1 (m = 2)
         w = so2_1.so2_m_conv[0].fc.weight
-        cust_blk.W1_m1_R.copy_(w[:2 * C, :]); cust_blk.W1_m1_I.copy_(w[2 * C:, :])
+        cust_blk.W1_m1_R.copy_(w[:L * C, :]); cust_blk.W1_m1_I.copy_(w[L * C:, :])
         w = so2_1.so2_m_conv[1].fc.weight
-        cust_blk.W1_m2_R.copy_(w[:1 * C, :]); cust_blk.W1_m2_I.copy_(w[1 * C:, :])
+        cust_blk.W1_m2_R.copy_(w[:(L - 1) * C, :]); cust_blk.W1_m2_I.copy_(w[(L - 1) * C:, :])
         cust_blk.W2_m0.copy_(so2_2.fc_m0.weight); cust_blk.b2_m0.copy_(so2_2.fc_m0.bias)
         w = so2_2.so2_m_conv[0].fc.weight
-        cust_blk.W2_m1_R.copy_(w[:2 * C, :]); cust_blk.W2_m1_I.copy_(w[2 * C:, :])
+        cust_blk.W2_m1_R.copy_(w[:L * C, :]); cust_blk.W2_m1_I.copy_(w[L * C:, :])
         w = so2_2.so2_m_conv[1].fc.weight
-        cust_blk.W2_m2_R.copy_(w[:1 * C, :]); cust_blk.W2_m2_I.copy_(w[1 * C:, :])
+        cust_blk.W2_m2_R.copy_(w[:(L - 1) * C, :]); cust_blk.W2_m2_I.copy_(w[(L - 1) * C:, :])
         # node-level modules are attached by reference
         cust_blk.norm_1 = off_blk.norm_1
         cust_blk.norm_2 = off_blk.norm_2
@@ -59,15 +60,15 @@ class ZeroAllocBackbone(nn.Module):
     """Drop-in replacement for the FAIRChem eSCNMDBackbone (wrapper.py:88-212).
 
     Inference only: parameters are repacked and frozen; autograd through the HIP kernels
-    gives dE/dpos and dE/dcell for conservative forces and stress.  Only lmax = mmax = 2 is
-    supported, as in the reference."""
+    gives dE/dpos and dE/dcell for conservative forces and stress.  mmax = 2; lmax = 2 as in
+    the reference, and also 3 or 4 (the reference raises ValueError for lmax != 2,
+    wrapper.py:105-118; here the kernels cover (lmax + 1)^2 = 16 or 25 coefficients)."""
 
     def __init__(self, off_bb, dtype=torch.float32):
         super().__init__()
         lmax = getattr(off_bb, "lmax", None)
-        if lmax is not None and lmax != 2:
-            raise ValueError(f"ZeroAllocBackbone only supports lmax=2 (the kernels are built for the "
-                             f"9-coefficient layout); got lmax={lmax}.")
+        if lmax is not None and lmax not in (2, 3, 4):
+            raise ValueError(f"ZeroAllocBackbone supports lmax = 2, 3 or 4; got lmax={lmax}.")
         mmax = getattr(off_bb, "mmax", None)
         if mmax is not None and mmax != 2:
             raise ValueError(f"ZeroAllocBackbone only supports mmax=2; got mmax={mmax}.")
@@ -87,6 +88,7 @@ class ZeroAllocBackbone(nn.Module):
             num_distance_basis=B,
             cutoff=cutoff,
             coeff_g=coeff_g.item(),
+            lmax=2 if lmax is None else lmax,
         ).to(device)
         transfer_weights(off_bb, self.ce)
         self.ce.prepare_for_inference(dtype=dtype)

@@ -241,7 +241,8 @@ int fu_complex_linear_gate(const float* A_r, const float* A_i, int64_t lda, cons
 /* Equivariant RMS norm over SH coefficients (FAIRChem rms_norm_sh, the norm_1 / norm_2 /
  * final norm of model.py:145,157,218): l=0 centred over channels, scaled by
  * (mean_c sum_k x_kc^2 / ((2 l_k + 1)(lmax + 1)) + eps)^-1/2, per-(l, c) weight, l=0 bias.
- * x, out (N, 9, C); weight (lmax + 1, C); bias (C); inv_rms (N) is saved for the backward. */
+ * x, out (N, (lmax + 1)^2, C), lmax 2..4; weight (lmax + 1, C); bias (C); inv_rms (N) is
+ * saved for the backward. */
 int fu_rms_norm_sh_fwd(const float* x, const float* weight, const float* bias, float* out,
                        float* inv_rms, int64_t N, int32_t C, int32_t lmax, float eps, void* stream);
 int fu_rms_norm_sh_bwd(const float* x, const float* weight, const float* inv_rms,
@@ -249,7 +250,8 @@ int fu_rms_norm_sh_bwd(const float* x, const float* weight, const float* inv_rms
                        void* stream);
 
 /* Gate activation of the atom-wise FFN: gate_l = sigmoid(silu(pre[:, l-1])) for l >= 1,
- * out_0 = silu(h_0), out_k = h_k * gate_{l_k}.  pre (N, lmax * H), h and out (N, 9, H). */
+ * out_0 = silu(h_0), out_k = h_k * gate_{l_k}.  pre (N, lmax * H), h and out
+ * (N, (lmax + 1)^2, H), lmax 2..4. */
 int fu_gate_act_fwd(const float* pre, const float* h, float* out, int64_t N, int32_t H,
                     int32_t lmax, void* stream);
 int fu_gate_act_bwd(const float* pre, const float* h, const float* g_out, float* g_pre,
@@ -337,6 +339,83 @@ int fu_nlist_scan(const int32_t* nout, int64_t* row_ptr, int64_t N, void* stream
 int fu_nlist_emit(const int32_t* sender, const int32_t* off, const int32_t* nout, const int64_t* row_ptr,
                   int64_t N, int32_t max_neighbors, int64_t* edge_index, float* cell_offsets, int64_t E,
                   void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * Degrees above 2 (lmax = 3 or 4, mmax = 2).  The reference rejects lmax != 2
+ * (wrapper.py:105-118); these entry points generalise its lmax = 2 kernels degree by degree.
+ * They also accept lmax = 2, where every array has the reference's shape and order.
+ *
+ * Shapes (C channels, L = lmax): node rows x (N, (L+1)^2, C); rad (E, 6L C); X_m0 (E, 2(L+1) C),
+ * X_m1 (E, 4L C), X_m2 (E, 4(L-1) C); Y_m0 (E, (2L+1) C), Y_m1 (E, 2L C), Y_m2 (E, 2(L-1) C);
+ * Z_m0 (E, (L+1) C), Z_m1 (E, 2L C), Z_m2 (E, 2(L-1) C); init rad (E, (L+1) C).  Column blocks
+ * follow the reference order extended by degree (csrc/edge_lmax.hip states the map).
+ * wigner is the reference's (E, 34) array; wig_ext (E, fu_wigner_ext_width(L)) holds rows
+ * m = -2..2 of D^3 (5 x 7) and D^4 (5 x 9), row-major; it may be NULL for L = 2.
+ * ------------------------------------------------------------------------------------ */
+
+/* Scalars per edge of wig_ext: 0 (lmax 2), 35 (lmax 3), 80 (lmax 4); -1 otherwise. */
+int fu_wigner_ext_width(int32_t lmax);
+
+/* wig_ext from the reference's L=1 and L=2 blocks, by the recursion
+ * D^l = U_l^T (D^(l-1) (x) D^1) U_l (no reference counterpart: ops/geom.py:137-178 stops at
+ * L=2).  lmax 3 or 4. */
+int fu_wigner_ext_fwd(const float* wigner, float* wig_ext, int64_t E, int32_t lmax, void* stream);
+
+/* Vector-Jacobian product of fu_wigner_ext_fwd: g_wigner (E, 34) = dL/dwigner through wig_ext
+ * (overwritten, not accumulated). */
+int fu_wigner_ext_bwd(const float* wigner, const float* g_wig_ext, float* g_wigner, int64_t E,
+                      int32_t lmax, void* stream);
+
+/* fu_gather_fwd for lmax 2..4 in the extended reference order (ops/gather.py:34-154). */
+int fu_gather_fwd_lmax(const float* x, const int64_t* idx_i, const int64_t* idx_j,
+                       const float* wigner, const float* wig_ext, const float* rad,
+                       const float* csd_emb, const int64_t* batch, float* X_m0, float* X_m1,
+                       float* X_m2, int64_t E, int64_t N, int64_t S, int32_t C, int32_t lmax,
+                       void* stream);
+
+/* fu_gather_bwd for lmax 2..4 (ops/gather.py:160-405, node-centric, no atomics).  ws is a
+ * scratch array of E * (34 + fu_wigner_ext_width(lmax)) floats. */
+int fu_gather_bwd_lmax(const float* g_X_m0, const float* g_X_m1, const float* g_X_m2,
+                       const float* x, const float* wigner, const float* wig_ext, const float* rad,
+                       const float* csd_emb, const int64_t* batch, const int32_t* recv_ptr,
+                       const int32_t* recv_idx, const int32_t* send_ptr, const int32_t* send_idx,
+                       float* g_x, float* g_wigner, float* g_wig_ext, float* g_rad, float* ws,
+                       int64_t E, int64_t N, int64_t S, int32_t C, int32_t lmax, void* stream);
+
+/* fu_scatter_fwd for lmax 2..4 (ops/scatter.py:45-140, fp64 CSR accumulation). */
+int fu_scatter_fwd_lmax(const int32_t* row_ptr, const int32_t* col_idx, const float* Z_m0,
+                        const float* Z_m1, const float* Z_m2, const float* wigner,
+                        const float* wig_ext, const float* env, const float* x_res, float* x_out,
+                        int64_t N, int64_t E, int32_t C, int32_t lmax, void* stream);
+
+/* fu_scatter_bwd for lmax 2..4 (ops/scatter.py:146-292). */
+int fu_scatter_bwd_lmax(const float* g_out, const int64_t* idx_j, const float* Z_m0,
+                        const float* Z_m1, const float* Z_m2, const float* wigner,
+                        const float* wig_ext, const float* env, float* g_Z_m0, float* g_Z_m1,
+                        float* g_Z_m2, float* g_wigner, float* g_wig_ext, float* g_env, int64_t E,
+                        int64_t N, int32_t C, int32_t lmax, void* stream);
+
+/* fu_init_scatter_fwd for lmax 2..4 (ops/scatter.py:360-423): rad (E, (L+1) C). */
+int fu_init_scatter_fwd_lmax(const int32_t* row_ptr, const int32_t* col_idx, const float* rad,
+                             const float* wigner, const float* wig_ext, const float* env,
+                             const int64_t* Z, const int64_t* batch, const float* W_sphere,
+                             const float* csd_emb, float* x_out, int64_t N, int64_t E,
+                             int64_t num_z, int64_t S, int32_t C, int32_t lmax, void* stream);
+
+/* fu_init_scatter_bwd for lmax 2..4 (ops/scatter.py:426-481); g_wigner / g_wig_ext entries the
+ * forward does not read are written as 0. */
+int fu_init_scatter_bwd_lmax(const float* g_out, const int64_t* idx_j, const float* rad,
+                             const float* wigner, const float* wig_ext, const float* env,
+                             float* g_rad, float* g_wigner, float* g_wig_ext, float* g_env,
+                             int64_t E, int64_t N, int32_t C, int32_t lmax, void* stream);
+
+/* fu_gating_fwd / fu_gating_bwd (layout 0) for lmax 2..4 (ops/gating.py:32-185). */
+int fu_gating_fwd_lmax(const float* Y_m0, const float* Y_m1, const float* Y_m2, float* Z_m0,
+                       float* Z_m1, float* Z_m2, int64_t E, int32_t C, int32_t lmax, void* stream);
+int fu_gating_bwd_lmax(const float* g_Z_m0, const float* g_Z_m1, const float* g_Z_m2,
+                       const float* Y_m0, const float* Y_m1, const float* Y_m2, float* g_Y_m0,
+                       float* g_Y_m1, float* g_Y_m2, int64_t E, int32_t C, int32_t lmax,
+                       void* stream);
 
 #ifdef __cplusplus
 }

@@ -18,6 +18,7 @@ import torch
 import torch.nn.functional as F
 
 from . import ops_ref as R
+from . import sh_ref
 
 
 def _p(t: torch.Tensor, dtype) -> torch.Tensor:
@@ -67,7 +68,7 @@ def radial_mlp(x, P: dict, prefix: str):
 def energy_forces_stress(backbone, head, pos, Z, cell, edge_index, cell_offsets, charge: int = 0, spin: int = 0,
                          dtype=torch.float64, stress: bool = True):
     """Returns dict(energy (1,), atom_energy (N,), forces (N, 3), stress (1, 3, 3) or None,
-    node_embedding (N, 9, C)) computed on the CPU in `dtype`."""
+    node_embedding (N, (lmax+1)^2, C)) computed on the CPU in `dtype`."""
     P = {k: _p(v, dtype) for k, v in backbone.state_dict().items()}
     H = {k: _p(v, dtype) for k, v in head.state_dict().items()}
     lmax = backbone.lmax
@@ -95,29 +96,42 @@ def energy_forces_stress(backbone, head, pos, Z, cell, edge_index, cell_offsets,
     shifts = torch.as_tensor(cell_offsets).to(dtype) @ cell          # wrapper.py:193-194
     x_edge_raw, wigner, env = R.edge_geometry(pos, Z, idx_i, idx_j, shifts, P["source_embedding.weight"],
                                               P["target_embedding.weight"], offset_g, coeff_g, cutoff)
+    L = lmax
+    # lmax > 2: rows |m| <= 2 of D^3, D^4 from the rotation D^1 (tensor representation)
+    wig_ext = sh_ref.wigner_ext(wigner[:, :9].reshape(-1, 3, 3), L) if L > 2 else None
     rad0 = radial_mlp(x_edge_raw, P, "edge_degree_embedding.rad_func.net.")
-    x = R.init_scatter(rad0, wigner, env, Z, batch, P["sphere_embedding.weight"], csd, idx_j, N)
+    if L == 2:
+        x = R.init_scatter(rad0, wigner, env, Z, batch, P["sphere_embedding.weight"], csd, idx_j, N)
+    else:
+        x = R.init_scatter_lmax(rad0, wigner, wig_ext, env, Z, batch, P["sphere_embedding.weight"], csd, idx_j, N, L)
     for l in range(backbone.num_layers):
         pre = f"blocks.{l}."
         c1 = pre + "edge_wise.so2_conv_1."
         c2 = pre + "edge_wise.so2_conv_2."
         xn = rms_norm_sh(x, P[pre + "norm_1.affine_weight"], P[pre + "norm_1.affine_bias"], lmax, 1e-5)
         rad = radial_mlp(x_edge_raw, P, c1 + "rad_func.net.")
-        X0, X1, X2 = R.gather_rotate(xn, idx_i, idx_j, wigner, rad, csd, batch)
+        if L == 2:
+            X0, X1, X2 = R.gather_rotate(xn, idx_i, idx_j, wigner, rad, csd, batch)
+        else:
+            X0, X1, X2 = R.gather_rotate_lmax(xn, idx_i, idx_j, wigner, wig_ext, rad, csd, batch, L)
+        # SO(2) m > 0 weights: rows [:n C] are R, [n C:] are I, n = L (m = 1) or L - 1 (m = 2)
         w1 = P[c1 + "so2_m_conv.0.fc.weight"]
         w2 = P[c1 + "so2_m_conv.1.fc.weight"]
-        W1_m1 = R.pack_so2(w1[:2 * C], w1[2 * C:])
-        W1_m2 = R.pack_so2(w2[:C], w2[C:])
+        W1_m1 = R.pack_so2(w1[:L * C], w1[L * C:])
+        W1_m2 = R.pack_so2(w2[:(L - 1) * C], w2[(L - 1) * C:])
         Y0 = X0 @ P[c1 + "fc_m0.weight"].T + P[c1 + "fc_m0.bias"]
         Y1 = X1 @ W1_m1.T
         Y2 = X2 @ W1_m2.T
-        Z0, Z1, Z2 = R.gating(Y0, Y1, Y2, C)
+        Z0, Z1, Z2 = R.gating(Y0, Y1, Y2, C) if L == 2 else R.gating_lmax(Y0, Y1, Y2, C, L)
         v1 = P[c2 + "so2_m_conv.0.fc.weight"]
         v2 = P[c2 + "so2_m_conv.1.fc.weight"]
         Zo0 = Z0 @ P[c2 + "fc_m0.weight"].T + P[c2 + "fc_m0.bias"]
-        Zo1 = Z1 @ R.pack_so2(v1[:2 * C], v1[2 * C:]).T
-        Zo2 = Z2 @ R.pack_so2(v2[:C], v2[C:]).T
-        x_mid = R.rotate_scatter(Zo0, Zo1, Zo2, wigner, env, x, idx_j, N)
+        Zo1 = Z1 @ R.pack_so2(v1[:L * C], v1[L * C:]).T
+        Zo2 = Z2 @ R.pack_so2(v2[:(L - 1) * C], v2[(L - 1) * C:]).T
+        if L == 2:
+            x_mid = R.rotate_scatter(Zo0, Zo1, Zo2, wigner, env, x, idx_j, N)
+        else:
+            x_mid = R.rotate_scatter_lmax(Zo0, Zo1, Zo2, wigner, wig_ext, env, x, idx_j, N, L)
         h = rms_norm_sh(x_mid, P[pre + "norm_2.affine_weight"], P[pre + "norm_2.affine_bias"], lmax, 1e-5)
         x = spectral_atomwise(h, P, pre + "atom_wise.", lmax, Hc) + x_mid
     x = rms_norm_sh(x, P["norm.affine_weight"], P["norm.affine_bias"], lmax, 1e-5)

@@ -295,3 +295,120 @@ def layer_norm_silu(x, gamma, beta, eps=1e-7):
 def pack_so2(R: torch.Tensor, I: torch.Tensor) -> torch.Tensor:
     """Real block matrix [[R, -I], [I, R]] of the complex map R + iI (model.py:111-138)."""
     return torch.cat([torch.cat([R, -I], 1), torch.cat([I, R], 1)], 0)
+
+
+# ---------------------------------------------------------------------------------------
+# lmax = 3, 4 (mmax = 2): the reference handles lmax = 2 only (wrapper.py:105-118).  The
+# functions below extend the ones above degree by degree in the reference's block order
+# continued over the degrees; with lmax = 2 they equal gather_rotate / gating /
+# rotate_scatter / init_scatter above (tests/test_oracle_pins.py).  The l >= 3 Wigner rows
+# come from oracle.sh_ref (tensor representation of the rotation).
+# ---------------------------------------------------------------------------------------
+
+def coef_index(l: int, m: int) -> int:
+    return l * l + l + m
+
+
+def slot_maps(L: int):
+    """Rotated coefficients feeding each C-wide block of X_m0 / X_m1 / X_m2 (per side) and the
+    radial block each uses (sender index; the receiver uses index + 1)."""
+    m0 = [coef_index(l, 0) for l in range(L + 1)]
+    m1 = [coef_index(l, 1) for l in range(1, L + 1)] + [coef_index(l, -1) for l in range(1, L + 1)]
+    m2 = [coef_index(l, 2) for l in range(2, L + 1)] + [coef_index(l, -2) for l in range(2, L + 1)]
+    r0 = [2 * l for l in range(L + 1)]
+    r1 = [2 * (L + 1) + 2 * (l - 1) for l in range(1, L + 1)] * 2
+    r2 = [4 * L + 2 + 2 * (l - 2) for l in range(2, L + 1)] * 2
+    return m0, m1, m2, r0, r1, r2
+
+
+def rotation_lmax(wigner: torch.Tensor, wig_ext: torch.Tensor, L: int) -> torch.Tensor:
+    """(E, K, K) block-diagonal rotation, K = (L+1)^2; for l >= 3 only the rows |m| <= 2 are
+    filled (the edge frame never uses the others)."""
+    from .sh_ref import wigner_rows
+    E = wigner.shape[0]
+    K = (L + 1) ** 2
+    D = torch.zeros(E, K, K, dtype=wigner.dtype)
+    D[:, 0:9, 0:9] = block_diag_rotation(wigner)
+    off = 0
+    for l in range(3, L + 1):
+        rows = wigner_rows(l)
+        n = 2 * l + 1
+        blk = wig_ext[:, off:off + len(rows) * n].reshape(E, len(rows), n)
+        for a, r in enumerate(rows):
+            D[:, l * l + r, l * l:l * l + n] = blk[:, a]
+        off += len(rows) * n
+    return D
+
+
+def gather_rotate_lmax(x, idx_i, idx_j, wigner, wig_ext, rad, csd_emb, batch, L: int):
+    """gather_rotate for lmax = L: x (N, (L+1)^2, C), rad (E, 6LC)."""
+    N, K, C = x.shape
+    E = idx_i.shape[0]
+    D = rotation_lmax(wigner, wig_ext, L)
+    vs = x[idx_i].clone()
+    vt = x[idx_j].clone()
+    vs = torch.cat([(vs[:, 0] + csd_emb[batch[idx_i]])[:, None], vs[:, 1:]], 1)
+    vt = torch.cat([(vt[:, 0] + csd_emb[batch[idx_j]])[:, None], vt[:, 1:]], 1)
+    rs = torch.einsum("eab,ebc->eac", D, vs)
+    rt = torch.einsum("eab,ebc->eac", D, vt)
+    r = rad.reshape(E, 6 * L, C)
+    m0, m1, m2, r0, r1, r2 = slot_maps(L)
+
+    def pair(coefs, rads):
+        cols = []
+        for k, rb in zip(coefs, rads):
+            cols.append(rs[:, k] * r[:, rb])
+            cols.append(rt[:, k] * r[:, rb + 1])
+        return torch.cat(cols, 1)
+
+    return pair(m0, r0), pair(m1, r1), pair(m2, r2)
+
+
+def gating_lmax(Y_m0, Y_m1, Y_m2, C: int, L: int):
+    """gating for lmax = L: Y_m0 = [gate_1..gate_L, y_0..y_L]."""
+    g = [None] + [torch.sigmoid(Y_m0[:, (l - 1) * C:l * C]) for l in range(1, L + 1)]
+    blk = lambda Y, b: Y[:, b * C:(b + 1) * C]
+    y0 = blk(Y_m0, L)
+    Z_m0 = torch.cat([torch.nn.functional.silu(y0)] + [blk(Y_m0, L + l) * g[l] for l in range(1, L + 1)], 1)
+    Z_m1 = torch.cat([blk(Y_m1, l - 1) * g[l] for l in range(1, L + 1)] +
+                     [blk(Y_m1, L + l - 1) * g[l] for l in range(1, L + 1)], 1)
+    Z_m2 = torch.cat([blk(Y_m2, l - 2) * g[l] for l in range(2, L + 1)] +
+                     [blk(Y_m2, L - 1 + l - 2) * g[l] for l in range(2, L + 1)], 1)
+    return Z_m0, Z_m1, Z_m2
+
+
+def _frame_from_blocks(Z_m0, Z_m1, Z_m2, C: int, L: int):
+    E = Z_m0.shape[0]
+    K = (L + 1) ** 2
+    m0, m1, m2, *_ = slot_maps(L)
+    zr = [torch.zeros(E, C, dtype=Z_m0.dtype)] * K
+    zr = list(zr)
+    for Zb, coefs in ((Z_m0, m0), (Z_m1, m1), (Z_m2, m2)):
+        for b, k in enumerate(coefs):
+            zr[k] = Zb[:, b * C:(b + 1) * C]
+    return torch.stack(zr, 1)
+
+
+def rotate_scatter_lmax(Z_m0, Z_m1, Z_m2, wigner, wig_ext, env, x_res, idx_j, N: int, L: int):
+    C = Z_m0.shape[1] // (L + 1)
+    zr = _frame_from_blocks(Z_m0, Z_m1, Z_m2, C, L)
+    D = rotation_lmax(wigner, wig_ext, L)
+    msg = torch.einsum("eba,ebc->eac", D, zr) * env[:, None, None]
+    out = torch.zeros(N, (L + 1) ** 2, C, dtype=torch.float64).index_add(0, idx_j, msg.to(torch.float64))
+    return (out + x_res.to(torch.float64)).to(x_res.dtype)
+
+
+def init_scatter_lmax(rad, wigner, wig_ext, env, Z, batch, W_sphere, csd_emb, idx_j, N: int, L: int):
+    C = rad.shape[1] // (L + 1)
+    E = rad.shape[0]
+    K = (L + 1) ** 2
+    D = rotation_lmax(wigner, wig_ext, L)
+    zr = [torch.zeros(E, C, dtype=rad.dtype) for _ in range(K)]
+    for l in range(L + 1):
+        zr[coef_index(l, 0)] = rad[:, l * C:(l + 1) * C]
+    zr = torch.stack(zr, 1)
+    msg = torch.einsum("eba,ebc->eac", D, zr) * (env / ENV_RESCALE)[:, None, None]
+    out = torch.zeros(N, K, C, dtype=torch.float64).index_add(0, idx_j, msg.to(torch.float64))
+    l0 = (W_sphere[Z] + csd_emb[batch]).to(torch.float64)
+    out = out + torch.cat([l0[:, None], torch.zeros(N, K - 1, C, dtype=torch.float64)], 1)
+    return out.to(rad.dtype)

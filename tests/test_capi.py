@@ -80,13 +80,34 @@ def test_product_raises_without_gpu_tensors():
         fused_gating_split(torch.zeros(4, 640), torch.zeros(4, 512), torch.zeros(4, 256), 128)
 
 
-@pytest.mark.parametrize("attr,value", [("lmax", 4), ("mmax", 4)])
-def test_backbone_rejects_other_lmax_mmax(attr, value):
-    """The lmax = 4 workload is rejected exactly as the reference rejects it
-    (wrapper.py:109-118): the kernels implement the 9-coefficient lmax = mmax = 2 layout."""
+@pytest.mark.parametrize("attr,value", [("lmax", 5), ("lmax", 1), ("mmax", 4)])
+def test_backbone_rejects_unsupported_lmax_mmax(attr, value):
+    """lmax 2, 3 and 4 are built (the reference stops at 2, wrapper.py:109-118); anything else,
+    and mmax != 2, is rejected with a ValueError before any kernel runs."""
     import escn_md
     from wrapper import ZeroAllocBackbone
     bb = escn_md.eSCNMDBackbone(seed=0)
     setattr(bb, attr, value)
-    with pytest.raises(ValueError, match=f"{attr}=4"):
+    with pytest.raises(ValueError, match=f"{attr}={value}"):
         ZeroAllocBackbone(bb)
+
+
+def test_lmax_entry_points_reject_bad_arguments():
+    """The lmax-general entry points check lmax, C and pointers on the host (no GPU needed)."""
+    import ctypes
+    from ops import _lib
+    lib = _lib.load()
+    assert lib.fu_wigner_ext_width(2) == 0 and lib.fu_wigner_ext_width(3) == 35 and lib.fu_wigner_ext_width(4) == 80
+    assert lib.fu_wigner_ext_width(5) == -1
+    assert lib.fu_wigner_ext_fwd(None, None, 10, 2, None) != 0      # lmax 2 needs no extension
+    assert b"lmax" in lib.fu_last_error()
+    assert lib.fu_gating_fwd_lmax(None, None, None, None, None, None, 10, 128, 5, None) != 0
+    assert b"lmax" in lib.fu_last_error()
+    assert lib.fu_scatter_fwd_lmax(None, None, None, None, None, None, None, None, None, None, 4, 8, 96, 4, None) != 0
+    assert b"C=96" in lib.fu_last_error()
+    assert lib.fu_gather_fwd_lmax(None, None, None, None, None, None, None, None, None, None, None, 8, 4, 1, 128, 4,
+                                  None) != 0
+    assert b"NULL" in lib.fu_last_error()
+    # lmax 3 and 4 need the extension rows; lmax 2 accepts NULL there (checked before any launch)
+    assert lib.fu_init_scatter_bwd_lmax(None, None, None, None, None, None, None, None, None, None, 0, 4, 128, 4,
+                                        None) == 0
