@@ -12,6 +12,8 @@ with HIP events on the launch stream during the timed steps, a per-kernel breakd
 CPU baseline (the float32 torch-CPU oracle on a bounded sample of the same workload).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config bcc_fe] [--no-cpu-baseline]
+
+--config bcc_fe_lmax4 runs BASELINE config 5 instead (same input, lmax = 4, 8 layers, E+F).
 """
 from __future__ import annotations
 
@@ -32,10 +34,17 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+# backbone shape per workload: the UMA-s-shaped headline model, and BASELINE config 5
+# (lmax = 4, 8 layers, E+F) on the same bcc Fe input
+MODELS = {"bcc_fe_lmax4": dict(lmax=4, num_layers=8)}
+
+
 def make_system(config: str):
     import systems
     if config == "bcc_fe":
         return systems.bcc_fe(n_rep=16), True, "bcc_fe_16x16x16"
+    if config == "bcc_fe_lmax4":
+        return systems.bcc_fe(n_rep=16), False, "bcc_fe_16x16x16_lmax4"
     if config == "water_box":
         return systems.water_box(), False, "water_box_333"
     if config == "amorphous":
@@ -45,7 +54,7 @@ def make_system(config: str):
     raise SystemExit(f"unknown config {config}")
 
 
-def cpu_baseline(budget_s: float = 20.0) -> dict:
+def cpu_baseline(budget_s: float = 20.0, model_kw: dict | None = None, stress: bool = True) -> dict:
     """float32 torch-CPU oracle (reference-algorithm restatement) on bcc Fe 4x4x4
     (128 atoms, same per-atom work as the headline: 30 edges/atom), E+F+S."""
     import torch
@@ -56,16 +65,16 @@ def cpu_baseline(budget_s: float = 20.0) -> dict:
 
     cores = min(16, len(os.sched_getaffinity(0)))
     torch.set_num_threads(cores)
-    bb = escn_md.eSCNMDBackbone(seed=0)
+    bb = escn_md.eSCNMDBackbone(seed=0, **(model_kw or {}))
     hd = heads.MLPEnergyHead(bb.sphere_channels, bb.hidden_channels, seed=1)
     s = systems.bcc_fe(n_rep=4)
     ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, bb.cutoff, bb.max_neighbors)
-    energy_forces_stress(bb, hd, s.pos, s.Z, s.cell, ei, off, dtype=torch.float32)   # warm-up
+    energy_forces_stress(bb, hd, s.pos, s.Z, s.cell, ei, off, dtype=torch.float32, stress=stress)   # warm-up
     times = []
     t_start = time.perf_counter()
     while len(times) < 5 and time.perf_counter() - t_start < budget_s:
         t0 = time.perf_counter()
-        energy_forces_stress(bb, hd, s.pos, s.Z, s.cell, ei, off, dtype=torch.float32)
+        energy_forces_stress(bb, hd, s.pos, s.Z, s.cell, ei, off, dtype=torch.float32, stress=stress)
         times.append(time.perf_counter() - t0)
     times.sort()
     med = times[len(times) // 2]
@@ -79,7 +88,8 @@ def cpu_baseline(budget_s: float = 20.0) -> dict:
     except OSError:
         pass
     return {"value": round(s.n_atoms / med, 2), "unit": "atom-steps/s", "cores": cores, "kind": "port",
-            "sample": f"bcc Fe 4x4x4 ({s.n_atoms} atoms, {ei.shape[1]} edges), E+F+S, float32 torch-CPU oracle "
+            "sample": f"bcc Fe 4x4x4 ({s.n_atoms} atoms, {ei.shape[1]} edges), {'E+F+S' if stress else 'E+F'}, "
+                      f"lmax={bb.lmax}, {bb.num_layers} layers, float32 torch-CPU oracle "
                       f"(oracle/model_ref.py), median of {len(times)} steps after 1 warm-up; CPU: {model}"}
 
 
@@ -112,7 +122,8 @@ def main() -> None:
     dev = torch.device("cuda:0")
     _lib.load()
     system, with_stress, wl_name = make_system(args.config)
-    bb = escn_md.eSCNMDBackbone(seed=0)
+    model_kw = MODELS.get(args.config, {})
+    bb = escn_md.eSCNMDBackbone(seed=0, **model_kw)
     hd = heads.MLPEnergyHead(bb.sphere_channels, bb.hidden_channels, seed=1)
     t0 = time.perf_counter()
     ei, off = systems.neighbor_list(system.pos, system.cell, system.pbc, bb.cutoff, bb.max_neighbors)
@@ -166,7 +177,7 @@ def main() -> None:
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (float32 torch-CPU oracle) ...")
-        cpu = cpu_baseline()
+        cpu = cpu_baseline(model_kw=model_kw, stress=with_stress)
         log(f"[bench] CPU baseline: {cpu['value']} atom-steps/s on {cpu['cores']} cores")
 
     rec = {
@@ -175,7 +186,8 @@ def main() -> None:
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": f"{wl_name}: {system.n_atoms} atoms, {ei.shape[1]} edges, "
                                f"{'E+F+S' if with_stress else 'E+F'}, UMA-s-shaped random-init eSCN-MD "
-                               f"(lmax=2, mmax=2, 4 layers, C=128, B=64, cutoff 6, max_neighbors 30)",
+                               f"(lmax={bb.lmax}, mmax=2, {bb.num_layers} layers, C=128, B=64, cutoff 6, "
+                               f"max_neighbors 30)",
                    "atoms": system.n_atoms, "edges": int(ei.shape[1]), "parallelism": "single GPU"},
         "roofline": rl, "cpu_baseline": cpu, "kernels": kernels,
         "energy": round(float(out["energy"].item()), 8),

@@ -85,6 +85,62 @@ def _ln_bwd(a):
     return M * (3 * D * 4 + 8), 0
 
 
+# lmax-general entry points: K = (L+1)^2 node rows, 34 + ext Wigner scalars, X 10L-2 and rad
+# 6L blocks per edge, Y 6L-1 and Z 5L-1 blocks (the lmax = 2 formulas above at L = 2).
+def _ext(L):
+    return {2: 0, 3: 35, 4: 80}[L]
+
+
+def _gather_fwd_l(a):
+    E, N, C, L = a[11], a[12], a[14], a[15]
+    return E * ((16 * L - 2) * C * 4 + (34 + _ext(L)) * 4 + 16) + N * ((L + 1) ** 2 * C * 4 + 8), 0
+
+
+def _gather_bwd_l(a):
+    E, N, C, L = a[18], a[19], a[21], a[22]
+    return E * ((22 * L - 2) * C * 4 + 2 * (34 + _ext(L)) * 4 + 8) + N * (2 * (L + 1) ** 2 * C * 4 + 16), 0
+
+
+def _scatter_fwd_l(a):
+    N, E, C, L = a[10], a[11], a[12], a[13]
+    return E * ((5 * L - 1) * C * 4 + (34 + _ext(L)) * 4 + 8) + N * (2 * (L + 1) ** 2 * C * 4 + 4), 0
+
+
+def _scatter_bwd_l(a):
+    E, N, C, L = a[14], a[15], a[16], a[17]
+    return E * (2 * (5 * L - 1) * C * 4 + 2 * (34 + _ext(L)) * 4 + 16) + N * (L + 1) ** 2 * C * 4, 0
+
+
+def _init_fwd_l(a):
+    N, E, C, L = a[11], a[12], a[15], a[16]
+    return E * ((L + 1) * C * 4 + ((L + 1) ** 2 - 1) * 4 + 8) + N * ((L + 1) ** 2 * C * 4 + 2 * C * 4 + 16), 0
+
+
+def _init_bwd_l(a):
+    E, N, C, L = a[10], a[11], a[12], a[13]
+    return E * (2 * (L + 1) * C * 4 + ((L + 1) ** 2 - 1) * 4 + (34 + _ext(L)) * 4 + 16) + N * (L + 1) ** 2 * C * 4, 0
+
+
+def _gating_fwd_l(a):
+    E, C, L = a[6], a[7], a[8]
+    return E * C * (11 * L - 2) * 4, 0
+
+
+def _gating_bwd_l(a):
+    E, C, L = a[9], a[10], a[11]
+    return E * C * (17 * L - 3) * 4, 0
+
+
+def _wig_ext_fwd(a):
+    E, L = a[2], a[3]
+    return E * (34 + _ext(L)) * 4, 0
+
+
+def _wig_ext_bwd(a):
+    E, L = a[3], a[4]
+    return E * (2 * 34 + _ext(L)) * 4, 0
+
+
 def _linear(a):
     M, N, K = a[7], a[8], a[9]
     return 4 * (M * K + M * N + N * K), 2 * M * N * K
@@ -149,6 +205,16 @@ WORK = {
     "fu_linear_batched": _linear_batched,
     "fu_complex_linear": _complex_linear,
     "fu_linear_gate": _linear_gate,
+    "fu_gather_fwd_lmax": _gather_fwd_l,
+    "fu_gather_bwd_lmax": _gather_bwd_l,
+    "fu_scatter_fwd_lmax": _scatter_fwd_l,
+    "fu_scatter_bwd_lmax": _scatter_bwd_l,
+    "fu_init_scatter_fwd_lmax": _init_fwd_l,
+    "fu_init_scatter_bwd_lmax": _init_bwd_l,
+    "fu_gating_fwd_lmax": _gating_fwd_l,
+    "fu_gating_bwd_lmax": _gating_bwd_l,
+    "fu_wigner_ext_fwd": _wig_ext_fwd,
+    "fu_wigner_ext_bwd": _wig_ext_bwd,
     "fu_complex_linear_gate": _complex_linear_gate,
 }
 
