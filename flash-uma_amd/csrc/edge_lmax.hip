@@ -18,7 +18,7 @@
 // gives rows m = -2..2 of D^3 (5 x 7) and D^4 (5 x 9).
 //
 // Mapping (HBM-bound, like the lmax = 2 kernels): forward gather and backward scatter one
-// wave64 per edge, lanes across channels; forward scatters one wave per receiver with fp64
+// wave64 per edge, lanes across channels, a contiguous XCD-aware edge range per workgroup; forward scatters one wave per receiver with fp64
 // accumulators, segments in CSR order; backward gather node-centric (one wave per CSR
 // segment of the node, as receiver and as sender), so no kernel uses atomics.  The l blocks
 // are processed one at a time to bound registers.
@@ -112,8 +112,9 @@ __global__ __launch_bounds__(256) void gather_fwd_lmax_kernel(
   constexpr int C = 64 * CPL, K = ncoef(L), EW = extw(L);
   const int lane = threadIdx.x & 63;
   const int c = lane * CPL;
-  const int64_t waves = (int64_t)gridDim.x * (blockDim.x >> 6);
-  for (int64_t e = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave_uniform(); e < E; e += waves) {
+  int64_t e0, e1;
+  block_edge_range(E, e0, e1);
+  for (int64_t e = e0 + wave_uniform(); e < e1; e += (blockDim.x >> 6)) {
     const float* wl = wig + e * 34;
     const float* we = ext + e * EW;
     const float* rade = rad + e * wrad(L) * C + c;
@@ -401,8 +402,9 @@ __global__ __launch_bounds__(256) void scatter_bwd_lmax_kernel(
   constexpr int C = 64 * CPL, K = ncoef(L), EW = extw(L);
   const int lane = threadIdx.x & 63;
   const int c = lane * CPL;
-  const int64_t waves = (int64_t)gridDim.x * (blockDim.x >> 6);
-  for (int64_t e = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave_uniform(); e < E; e += waves) {
+  int64_t e0, e1;
+  block_edge_range(E, e0, e1);
+  for (int64_t e = e0 + wave_uniform(); e < e1; e += (blockDim.x >> 6)) {
     const float en = env[e];
     const float* wl = wig + e * 34;
     const float* we = ext + e * EW;
@@ -522,8 +524,9 @@ __global__ __launch_bounds__(256) void init_scatter_bwd_lmax_kernel(
   constexpr int NP = (L + 1) * (L + 1) - 1 + 1;
   const int lane = threadIdx.x & 63;
   const int c = lane * CPL;
-  const int64_t waves = (int64_t)gridDim.x * (blockDim.x >> 6);
-  for (int64_t e = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave_uniform(); e < E; e += waves) {
+  int64_t e0, e1;
+  block_edge_range(E, e0, e1);
+  for (int64_t e = e0 + wave_uniform(); e < e1; e += (blockDim.x >> 6)) {
     const float en = env[e];
     const float* wl = wig + e * 34;
     const float* we = ext + e * EW;
@@ -736,7 +739,7 @@ extern "C" int fu_gather_fwd_lmax(const float* x, const int64_t* idx_i, const in
   hipStream_t s = as_stream(stream);
   with_c_lmax(C, lmax, [&](auto cpl, auto lv) {
     constexpr int P = decltype(cpl)::value, L = decltype(lv)::value;
-    hipLaunchKernelGGL((gather_fwd_lmax_kernel<P, L>), dim3((unsigned)std::min<int64_t>(cdiv(E, 4), 8192)), dim3(256),
+    hipLaunchKernelGGL((gather_fwd_lmax_kernel<P, L>), dim3(edge_grid(E)), dim3(256),
                        0, s, x, idx_i, idx_j, wigner, wig_ext, rad, csd_emb, batch, X_m0, X_m1, X_m2, E);
   });
   return check_launch("fu_gather_fwd_lmax");
@@ -812,7 +815,7 @@ extern "C" int fu_scatter_bwd_lmax(const float* g_out, const int64_t* idx_j, con
   hipStream_t s = as_stream(stream);
   with_c_lmax(C, lmax, [&](auto cpl, auto lv) {
     constexpr int P = decltype(cpl)::value, L = decltype(lv)::value;
-    hipLaunchKernelGGL((scatter_bwd_lmax_kernel<P, L>), dim3((unsigned)std::min<int64_t>(cdiv(E, 4), 8192)),
+    hipLaunchKernelGGL((scatter_bwd_lmax_kernel<P, L>), dim3(edge_grid(E)),
                        dim3(256), 0, s, g_out, idx_j, Z_m0, Z_m1, Z_m2, wigner, wig_ext, env, g_Z_m0, g_Z_m1, g_Z_m2,
                        g_wigner, g_wig_ext, g_env, E);
   });
@@ -854,7 +857,7 @@ extern "C" int fu_init_scatter_bwd_lmax(const float* g_out, const int64_t* idx_j
   hipStream_t s = as_stream(stream);
   with_c_lmax(C, lmax, [&](auto cpl, auto lv) {
     constexpr int P = decltype(cpl)::value, L = decltype(lv)::value;
-    hipLaunchKernelGGL((init_scatter_bwd_lmax_kernel<P, L>), dim3((unsigned)std::min<int64_t>(cdiv(E, 4), 8192)),
+    hipLaunchKernelGGL((init_scatter_bwd_lmax_kernel<P, L>), dim3(edge_grid(E)),
                        dim3(256), 0, s, g_out, idx_j, rad, wigner, wig_ext, env, g_rad, g_wigner, g_wig_ext, g_env, E);
   });
   return check_launch("fu_init_scatter_bwd_lmax");

@@ -45,6 +45,32 @@ inline unsigned int cdiv(int64_t a, int64_t b) { return static_cast<unsigned int
 // Largest grid dimension used by the 1-D launches; kernels grid-stride beyond it.
 constexpr int64_t kMaxBlocks = 1 << 20;
 
+// Workgroups of a launch are dealt round-robin over the 8 XCDs (each with its own L2).
+// xcd_block renumbers them so that XCD k runs the k-th contiguous eighth of the logical
+// workgroups (grid a multiple of 8; identity otherwise).
+__device__ __forceinline__ int64_t xcd_block(int64_t b, int64_t nblocks) {
+  return (nblocks & 7) == 0 ? (b & 7) * (nblocks >> 3) + (b >> 3) : b;
+}
+
+// Wave-per-edge kernels: this workgroup's contiguous edge range [e0, e1).  With the XCD
+// renumbering, a receiver's CSR segment (consecutive edges) stays in one workgroup and each
+// XCD walks one Morton-ordered eighth of the edges, so receiver and (spatially close)
+// sender rows are re-read from that XCD's L2 rather than fetched by every XCD.
+__device__ __forceinline__ void block_edge_range(int64_t E, int64_t& e0, int64_t& e1) {
+  const int64_t nb = gridDim.x;
+  const int64_t chunk = (E + nb - 1) / nb;
+  e0 = xcd_block(blockIdx.x, nb) * chunk;
+  e0 = e0 < E ? e0 : E;
+  e1 = e0 + chunk < E ? e0 + chunk : E;
+}
+
+// Grid for block_edge_range: about 4 edges per wave of 4-wave workgroups, a multiple of 8.
+inline unsigned int edge_grid(int64_t E) {
+  int64_t nb = (E + 15) / 16;
+  nb = nb < 8192 ? nb : 8192;
+  return static_cast<unsigned int>(((nb + 7) / 8) * 8);
+}
+
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }

@@ -1,9 +1,10 @@
 // Gather-rotate of sender/receiver SH rows into the edge frame (ops/gather.py:34-154) and
 // its backward pass (ops/gather.py:160-405) without atomics.
 //
-// Forward: one wave64 per edge, lanes across channels (CPL = C/64 per lane).  The edge's
-// indices and its 34 Wigner scalars are wave-uniform (scalar loads); every node row, radial
-// row and output slot is one coalesced row access.
+// Forward: one wave64 per edge, lanes across channels (CPL = C/64 per lane); each workgroup
+// takes a contiguous edge range, XCD-aware (block_edge_range).  The edge's indices and its 34
+// Wigner scalars are wave-uniform (scalar loads); every node row, radial row and output slot
+// is one coalesced row access.
 //
 // Backward: node-centric.  A 128-thread workgroup owns one node: one wave walks the node's
 // receiver segment (edges e with idx_j[e] = n, receiver CSR) and the other its sender
@@ -89,8 +90,9 @@ __global__ __launch_bounds__(256) void gather_fwd_kernel(
   constexpr int C = 64 * CPL;
   const int lane = threadIdx.x & 63;
   const int c = lane * CPL;
-  const int64_t waves = (int64_t)gridDim.x * (blockDim.x >> 6);
-  for (int64_t e = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave_id_uniform(); e < E; e += waves) {
+  int64_t e0, e1;
+  block_edge_range(E, e0, e1);
+  for (int64_t e = e0 + wave_id_uniform(); e < e1; e += (blockDim.x >> 6)) {
     const int64_t i = idx_i[e], j = idx_j[e];
     float w[34];
 #pragma unroll
@@ -346,7 +348,7 @@ template <int CPL, int L>
 static void launch_gather_fwd(const float* x, const int64_t* idx_i, const int64_t* idx_j, const float* wigner,
                               const float* rad, const float* csd, const int64_t* batch, float* X0, float* X1,
                               float* X2, int64_t E, hipStream_t st) {
-  hipLaunchKernelGGL((gather_fwd_kernel<CPL, L>), dim3((unsigned)std::min<int64_t>(cdiv(E, 4), 8192)), dim3(256), 0, st, x, idx_i, idx_j, wigner, rad,
+  hipLaunchKernelGGL((gather_fwd_kernel<CPL, L>), dim3(edge_grid(E)), dim3(256), 0, st, x, idx_i, idx_j, wigner, rad,
                      csd, batch, X0, X1, X2, E);
 }
 

@@ -5,8 +5,9 @@
 // Forward kernels: one wave64 per receiver node, lanes across channels; the node's CSR
 // segment is walked in order and every edge message (computed in fp32 exactly as the
 // reference forms it) is accumulated into fp64 registers, then rounded once to fp32.
-// Backward kernels: one wave64 per edge; the per-edge channel reductions for g_wigner and
-// g_env use one multi-value wave reduction.
+// Backward kernels: one wave64 per edge, contiguous XCD-aware edge range per workgroup
+// (block_edge_range); the per-edge channel reductions for g_wigner and g_env use one
+// multi-value wave reduction.
 #include "fu_vec.h"
 
 namespace fu {
@@ -121,8 +122,9 @@ __global__ __launch_bounds__(256) void scatter_bwd_kernel(const float* __restric
   constexpr int C = 64 * CPL;
   const int lane = threadIdx.x & 63;
   const int c = lane * CPL;
-  const int64_t waves = (int64_t)gridDim.x * (blockDim.x >> 6);
-  for (int64_t e = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave_id_u(); e < E; e += waves) {
+  int64_t e0, e1;
+  block_edge_range(E, e0, e1);
+  for (int64_t e = e0 + wave_id_u(); e < e1; e += (blockDim.x >> 6)) {
     const int64_t j = idx_j[e];
     float w[34];
 #pragma unroll
@@ -254,8 +256,9 @@ __global__ __launch_bounds__(256) void init_scatter_bwd_kernel(const float* __re
   constexpr int C = 64 * CPL;
   const int lane = threadIdx.x & 63;
   const int c = lane * CPL;
-  const int64_t waves = (int64_t)gridDim.x * (blockDim.x >> 6);
-  for (int64_t e = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave_id_u(); e < E; e += waves) {
+  int64_t e0, e1;
+  block_edge_range(E, e0, e1);
+  for (int64_t e = e0 + wave_id_u(); e < e1; e += (blockDim.x >> 6)) {
     const int64_t j = idx_j[e];
     const float en = env[e];
     float w1[3], w2[5];
@@ -313,7 +316,7 @@ template <int CPL>
 static void launch_scatter_bwd(const float* g_out, const int64_t* idx_j, const float* Z0, const float* Z1,
                                const float* Z2, const float* wig, const float* env, float* gZ0, float* gZ1, float* gZ2,
                                float* g_wig, float* g_env, int64_t E, hipStream_t st) {
-  hipLaunchKernelGGL(scatter_bwd_kernel<CPL>, dim3((unsigned)std::min<int64_t>(cdiv(E, 4), 8192)), dim3(256), 0, st, g_out, idx_j, Z0, Z1, Z2, wig,
+  hipLaunchKernelGGL(scatter_bwd_kernel<CPL>, dim3(edge_grid(E)), dim3(256), 0, st, g_out, idx_j, Z0, Z1, Z2, wig,
                      env, gZ0, gZ1, gZ2, g_wig, g_env, E);
 }
 
@@ -398,7 +401,7 @@ extern "C" int fu_init_scatter_bwd(const float* g_out, const int64_t* idx_j, con
   if (!g_out || !idx_j || !rad || !wigner || !env || !g_rad || !g_wigner || !g_env)
     return set_error(FU_ERR_NULL, "fu_init_scatter_bwd: NULL argument");
   hipStream_t s = as_stream(stream);
-  const dim3 grid((unsigned)std::min<int64_t>(cdiv(E, 4), 8192));
+  const dim3 grid(edge_grid(E));
   if (C == 64)
     hipLaunchKernelGGL(init_scatter_bwd_kernel<1>, grid, dim3(256), 0, s, g_out, idx_j, rad, wigner, env, g_rad,
                        g_wigner, g_env, E);
