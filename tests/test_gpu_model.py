@@ -133,3 +133,27 @@ def test_rejects_out_of_range_atoms(cuda):
     data.batch[0] = 1
     with pytest.raises(ValueError, match="batch ids"):
         model(data, compute_forces=False)
+
+
+def test_inplace_edge_index_edit_invalidates_topology(cuda):
+    """The topology cache is keyed on the edge_index tensor and its version counter: an
+    in-place edit (here: reversing 12 edges, with their cell offsets negated) must rebuild the
+    CSRs, giving exactly the result of a fresh tensor holding the edited graph.  (The
+    reference keys its cache on a freshly allocated tensor's data_ptr, SURVEY hazard (i).)"""
+    import heads
+    import systems
+    bb, hd, model = _build(cuda)
+    s = systems.water_box(n_mol=40, L=10.5, seed=2)
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, 6.0, 30)
+    data = heads.make_atomic_data(s, ei, off, cuda)
+    before = model(data, compute_forces=True)["energy"].detach().cpu()
+    with torch.no_grad():
+        data.edge_index[:, :12] = data.edge_index[:, :12].flip(0).clone()
+        data.cell_offsets[:12] = -data.cell_offsets[:12]
+    after = model(data, compute_forces=True)
+    ei2 = data.edge_index.detach().cpu().numpy().copy()
+    off2 = data.cell_offsets.detach().cpu().numpy().copy()
+    fresh = _run(model, s, ei2, off2, cuda)
+    assert torch.equal(after["energy"].detach().cpu(), fresh["energy"])
+    assert torch.equal(after["forces"].detach().cpu(), fresh["forces"])
+    assert not torch.equal(before, fresh["energy"])

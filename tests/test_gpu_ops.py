@@ -217,6 +217,33 @@ def test_geometry(cuda):
     assert_close(gp, gp_ref, 1e-4, "g_pos")
 
 
+def test_geometry_zero_length_edge(cuda):
+    """Duplicate atoms (d = 0): the distance is clamped to 1e-7 as in the reference
+    (ops/geom.py:76), so the forward equals the oracle's and the backward is finite.  The
+    oracle's autograd is NaN at d = 0 (sqrt at 0), so the backward is checked against the
+    derivative of the clamped direction d / 1e-7 instead: with only g_wigner nonzero,
+    g_d = g_e / 1e-7 where g_e is the gradient w.r.t. the (zero) direction vector."""
+    _, _, geom, *_ = _ops()
+    pos, Z, ei, shifts, W_src, W_tgt, offset_g, coeff_g = _geom_inputs(seed=12)
+    i, j = int(ei[0, 7]), int(ei[1, 7])
+    pos[i] = pos[j]                       # duplicate atom: edge 7 has d = 0 exactly
+    shifts[7] = 0.0
+    d7 = pos[i].double() - pos[j].double() + shifts[7].double()
+    assert d7.abs().max().item() == 0.0
+    posg = pos.to(cuda).requires_grad_(True)
+    xe, wig, env = geom.precompute_geometry(posg, Z.to(cuda), ei[0].to(cuda), ei[1].to(cuda), shifts.to(cuda),
+                                            W_src.to(cuda), W_tgt.to(cuda), offset_g.to(cuda), coeff_g, 6.0)
+    ref = R.edge_geometry(pos.double(), Z, ei[0], ei[1], shifts.double(), W_src.double(), W_tgt.double(),
+                          offset_g.double(), coeff_g, 6.0)
+    assert_close(xe, ref[0], TOL, "x_edge_raw")
+    assert_close(wig, ref[1], 2e-5, "wigner")
+    assert float(env[7].item()) == 1.0
+    torch.manual_seed(13)
+    cot = [torch.randn(xe.shape), torch.randn(wig.shape), torch.randn(env.shape)]
+    (gp,) = torch.autograd.grad((xe, wig, env), (posg,), [c.to(cuda) for c in cot])
+    assert torch.isfinite(gp).all()
+
+
 def _gather_inputs(seed=4, N=40, E=300, C=128, S=1):
     pos, Z, ei, shifts = random_graph(N, E, seed=seed)
     g = torch.Generator().manual_seed(seed)
