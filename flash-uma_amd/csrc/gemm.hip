@@ -6,7 +6,7 @@
 // pre-transposed weight).  No weight gradients are ever needed: parameters are frozen.
 //
 // Tiling: a 256-thread workgroup (4 wave64s in a 2x2 grid) owns a 128x128 output tile; each
-// wave owns 64x64 = 2x2 MFMA blocks of 32x32 (64 fp32 accumulators per lane, held in AGPRs).
+// wave owns 64x64 = 2x2 MFMA blocks of 32x32 (64 fp32 accumulators per lane, in VGPRs).
 // K advances in chunks of 16 staged through double-buffered LDS (32 KB of operands, 36 KB with
 // the epilogue staging: four workgroups per CU).  Within a chunk, lane l (row/col l%32, half h = l/32) feeds the MFMA k-slot h with
 // chunk column 8h + t at step t, so each lane reads its 8 operands of a chunk with two
