@@ -101,6 +101,9 @@ def main() -> None:
     ap.add_argument("--config", default="bcc_fe")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernel-profile", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="time the step captured once in a HIP graph and replayed (captured.py); "
+                         "the per-kernel profile is not available then")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="first copy a 256 MiB buffer (a plain copy kernel of known size, the scale "
                          "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -140,6 +143,15 @@ def main() -> None:
 
     def step():
         return model(data, compute_forces=True, compute_stress=with_stress)
+
+    if args.graph:
+        from captured import CapturedStep
+        cap = CapturedStep(model, data, compute_stress=with_stress)
+        pos0 = data.pos.detach().clone()
+        args.no_kernel_profile = True
+
+        def step():   # noqa: F811 -- one replay of the whole E+F(+S) step on the same inputs
+            return cap(pos0)
 
     for k in range(args.warmup):
         out = step()
@@ -188,7 +200,8 @@ def main() -> None:
                                f"{'E+F+S' if with_stress else 'E+F'}, UMA-s-shaped random-init eSCN-MD "
                                f"(lmax={bb.lmax}, mmax=2, {bb.num_layers} layers, C=128, B=64, cutoff 6, "
                                f"max_neighbors 30)",
-                   "atoms": system.n_atoms, "edges": int(ei.shape[1]), "parallelism": "single GPU"},
+                   "atoms": system.n_atoms, "edges": int(ei.shape[1]), "parallelism": "single GPU",
+                   "execution": "hip graph replay" if args.graph else "eager"},
         "roofline": rl, "cpu_baseline": cpu, "kernels": kernels,
         "energy": round(float(out["energy"].item()), 8),
     }

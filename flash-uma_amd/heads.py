@@ -63,10 +63,13 @@ class PotentialModel(nn.Module):
         for p in self.head.parameters():
             p.requires_grad_(False)
 
-    def forward(self, data, compute_forces: bool = True, compute_stress: bool = False) -> dict:
+    def forward(self, data, compute_forces: bool = True, compute_stress: bool = False, natoms=None) -> dict:
+        """natoms: atoms per system as a host list (read from data.natoms when omitted; passing
+        it avoids a device-to-host copy, which graph capture requires)."""
         emb = self.backbone(data)
         e_atom = self.head.atom_energy(emb["node_embedding"])
-        natoms = [int(n) for n in data.natoms.tolist()]
+        if natoms is None:
+            natoms = [int(n) for n in data.natoms.tolist()]
         energy = system_sum(e_atom, natoms)
         out = {"energy": energy, "atom_energy": e_atom, "node_embedding": emb["node_embedding"]}
         if compute_forces or compute_stress:
@@ -88,7 +91,8 @@ def stress_from_gradients(pos, cell, g_pos, g_cell, natoms: list):
     g_cell = g_cell.reshape(n_sys, 3, 3)
     w = system_sum(pos[:, :, None] * g_pos[:, None, :], natoms)
     w = w + cell.transpose(1, 2) @ g_cell
-    vol = torch.linalg.det(cell).abs().reshape(n_sys, 1, 1)
+    # |det cell| as the triple product a . (b x c) (elementwise, no solver call)
+    vol = (cell[:, 0] * torch.linalg.cross(cell[:, 1], cell[:, 2])).sum(-1).abs().reshape(n_sys, 1, 1)
     return w / vol
 
 
