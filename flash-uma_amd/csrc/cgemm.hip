@@ -28,8 +28,11 @@ __device__ __forceinline__ int clds(int row, int chunk) {
   return row * 16 + 4 * (chunk ^ (((row >> 1) ^ (row >> 2)) & 3));
 }
 
-// Gate epilogue (conv1 m = 1, 2 fused with the gate activation): Z_r = Y_r s and
-// Z_i = Y_i s with s = S[row][s_off + column].
+// Gate epilogues, s = S[row][s_off + column]:
+//   MODE 1 (conv1 m = 1, 2 fused with the gate activation): also writes Z_r = Y_r s, Z_i = Y_i s;
+//   MODE 2 (conv2 m = 1, 2 input gradient fused with the gate backward): the product is
+//   g_Z; Y receives g_Y = g_Z s and Pout the gate sum g_Zr F_r + g_Zi F_i, F being the
+//   forward pre-activation of the same block.
 struct CGate {
   float* Zr;
   float* Zi;
@@ -37,9 +40,14 @@ struct CGate {
   const float* S;
   int64_t lds;
   int32_t s_off;
+  const float* Fr;
+  const float* Fi;
+  int64_t ldf;
+  float* Pout;
+  int64_t ldp;
 };
 
-template <bool GATE>
+template <int MODE>
 __global__ __launch_bounds__(256, 3) void complex_linear_kernel(
     const float* __restrict__ Ar, const float* __restrict__ Ai, int64_t lda, const float* __restrict__ P,
     const float* __restrict__ Q, int64_t ldw, float* __restrict__ Yr, float* __restrict__ Yi, int64_t ldy,
@@ -156,9 +164,16 @@ __global__ __launch_bounds__(256, 3) void complex_linear_kernel(
       const int gc = col0 + wc + c;
       if (row >= M || gc >= Nc) continue;
       const float4 yr = ld4(&ws[r * CES + c]), yi = ld4(&ws[r * CES + 32 + c]);
+      if constexpr (MODE == 2) {
+        const float4 sg = ld4(g.S + row * g.lds + g.s_off + gc);
+        st4(Yr + row * ldy + gc, yr * sg);
+        st4(Yi + row * ldy + gc, yi * sg);
+        st4(g.Pout + row * g.ldp + gc, yr * ld4(g.Fr + row * g.ldf + gc) + yi * ld4(g.Fi + row * g.ldf + gc));
+        continue;
+      }
       st4(Yr + row * ldy + gc, yr);
       st4(Yi + row * ldy + gc, yi);
-      if constexpr (GATE) {
+      if constexpr (MODE == 1) {
         const float4 sg = ld4(g.S + row * g.lds + g.s_off + gc);
         st4(g.Zr + row * g.ldz + gc, yr * sg);
         st4(g.Zi + row * g.ldz + gc, yi * sg);
@@ -188,13 +203,13 @@ static int complex_check(const float* A_r, const float* A_i, int64_t lda, const 
   return FU_OK;
 }
 
-template <bool GATE>
+template <int MODE>
 static int complex_launch(const float* A_r, const float* A_i, int64_t lda, const float* P, const float* Q, int64_t ldw,
                           float* Y_r, float* Y_i, int64_t ldy, int64_t M, int32_t Nc, int32_t Kc, CGate g,
                           void* stream, const char* who) {
   const int n_tiles = (Nc + CBN - 1) / CBN;
   const int64_t total = ((M + CBM - 1) / CBM) * n_tiles;
-  hipLaunchKernelGGL((complex_linear_kernel<GATE>), dim3((unsigned)total), dim3(256), 0, as_stream(stream), A_r, A_i,
+  hipLaunchKernelGGL((complex_linear_kernel<MODE>), dim3((unsigned)total), dim3(256), 0, as_stream(stream), A_r, A_i,
                      lda, P, Q, ldw, Y_r, Y_i, ldy, M, Nc, Kc, n_tiles, total, g);
   return check_launch(who);
 }
@@ -204,8 +219,8 @@ extern "C" int fu_complex_linear(const float* A_r, const float* A_i, int64_t lda
                                  int32_t Kc, void* stream) {
   int st = complex_check(A_r, A_i, lda, P, Q, ldw, Y_r, Y_i, ldy, M, Nc, Kc, "fu_complex_linear");
   if (st != FU_OK || M == 0) return st;
-  return complex_launch<false>(A_r, A_i, lda, P, Q, ldw, Y_r, Y_i, ldy, M, Nc, Kc, CGate{}, stream,
-                               "fu_complex_linear");
+  return complex_launch<0>(A_r, A_i, lda, P, Q, ldw, Y_r, Y_i, ldy, M, Nc, Kc, CGate{}, stream,
+                           "fu_complex_linear");
 }
 
 extern "C" int fu_complex_linear_gate(const float* A_r, const float* A_i, int64_t lda, const float* P, const float* Q,
@@ -220,6 +235,24 @@ extern "C" int fu_complex_linear_gate(const float* A_r, const float* A_i, int64_
   if ((ldz | lds | s_off) % 4 != 0 || !aligned16(Z_r) || !aligned16(Z_i) || !aligned16(S))
     return set_error(FU_ERR_ALIGN, "%s: gate operands must be 16-byte aligned with strides multiples of 4", who);
   if (M == 0) return FU_OK;
-  return complex_launch<true>(A_r, A_i, lda, P, Q, ldw, Y_r, Y_i, ldy, M, Nc, Kc, CGate{Z_r, Z_i, ldz, S, lds, s_off},
-                              stream, who);
+  return complex_launch<1>(A_r, A_i, lda, P, Q, ldw, Y_r, Y_i, ldy, M, Nc, Kc,
+                           CGate{Z_r, Z_i, ldz, S, lds, s_off, nullptr, nullptr, 0, nullptr, 0}, stream, who);
+}
+
+extern "C" int fu_complex_linear_gate_bwd(const float* A_r, const float* A_i, int64_t lda, const float* P,
+                                          const float* Q, int64_t ldw, float* gY_r, float* gY_i, int64_t ldg,
+                                          const float* F_r, const float* F_i, int64_t ldf, const float* S, int64_t lds,
+                                          int32_t s_off, float* Pout, int64_t ldp, int64_t M, int32_t Nc, int32_t Kc,
+                                          void* stream) {
+  const char* who = "fu_complex_linear_gate_bwd";
+  int st = complex_check(A_r, A_i, lda, P, Q, ldw, gY_r, gY_i, ldg, M, Nc, Kc, who);
+  if (st != FU_OK) return st;
+  if (!F_r || !F_i || !S || !Pout) return set_error(FU_ERR_NULL, "%s: NULL gate operand", who);
+  if (ldf < Nc || ldp < Nc || s_off < 0 || lds < s_off + Nc)
+    return set_error(FU_ERR_SHAPE, "%s: gate strides too small", who);
+  if ((ldf | ldp | lds | s_off) % 4 != 0 || !aligned16(F_r) || !aligned16(F_i) || !aligned16(S) || !aligned16(Pout))
+    return set_error(FU_ERR_ALIGN, "%s: gate operands must be 16-byte aligned with strides multiples of 4", who);
+  if (M == 0) return FU_OK;
+  return complex_launch<2>(A_r, A_i, lda, P, Q, ldw, gY_r, gY_i, ldg, M, Nc, Kc,
+                           CGate{nullptr, nullptr, 0, S, lds, s_off, F_r, F_i, ldf, Pout, ldp}, stream, who);
 }

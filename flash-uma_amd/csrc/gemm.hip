@@ -40,21 +40,40 @@ struct GateOut {
   int32_t C;
 };
 
+// Operands of the gate-backward epilogue (conv2 m = 0 input gradient fused with the gate
+// backward).  The GEMM computes g_Z_m0 (M, 3C) = [g_l0, g_l1m0, g_l2m0]; the epilogue writes
+// g_Y_m0 (M, 5C) in the gate-paired order instead: g_y_l0 = g silu'(y_l0), g_y_lm0 = g s_l
+// and g_gate_l = s_l (1 - s_l) (g y_lm0 + P1[l] (+ P2 for l = 2)), where P1 (M, 2C) and
+// P2 (M, C) are the gate sums sum_m g_z y of the m = 1 and m = 2 blocks (written by
+// fu_complex_linear_gate_bwd).
+struct GateBwd {
+  const float* Y0;  // (M, 5C) forward pre-activation, gate-paired
+  int64_t ldy0;
+  const float* S;   // (M, 2C) [s1, s2]
+  int64_t lds;
+  const float* P1;
+  int64_t ldp1;
+  const float* P2;
+  int64_t ldp2;
+  int32_t C;
+};
+
 // Batch index blockIdx.y offsets A, W and Y by sA, sW and sY floats; bias (stride sBias) is
 // added in batches [0, bias_batches).
 //
-// GATE: Y has N = 5C columns in the gate-paired order -- every 64-column pair p holds
-// [32 gate channels | the 32 channels they gate]: pairs 0 .. C/32-1 are (gate_l1, y_l1m0),
-// the next C/32 are (gate_l2, y_l2m0), the last C/64 hold y_l0 -- so a wave's two 32x32
-// accumulator blocks are a gate and its values in the same lanes and registers.  The
-// epilogue writes Y (kept for the backward), Z and S without going through LDS.
-template <bool GATE>
+// MODE 0: plain.  MODE 1 (gate): Y has N = 5C columns in the gate-paired order -- every
+// 64-column pair p holds [32 gate channels | the 32 channels they gate]: pairs 0 .. C/32-1 are
+// (gate_l1, y_l1m0), the next C/32 are (gate_l2, y_l2m0), the last C/64 hold y_l0 -- so a
+// wave's 64 staged columns are a gate and its values; the epilogue writes Y (kept for the
+// backward), Z and S.  MODE 2 (gate backward): see GateBwd; Y receives g_Y_m0 (5C columns).
+template <int MODE>
 __global__ __launch_bounds__(256, 4) void linear_mfma_kernel(const float* __restrict__ A, int64_t lda, int64_t sA,
                                                           const float* __restrict__ W, int64_t ldw, int64_t sW,
                                                           const float* __restrict__ bias, int64_t sBias,
                                                           int32_t bias_batches, float* __restrict__ Y, int64_t ldy,
                                                           int64_t sY, int64_t M, int32_t N, int32_t K,
-                                                          int32_t n_tiles, int64_t total_tiles, GateOut go) {
+                                                          int32_t n_tiles, int64_t total_tiles, GateOut go,
+                                                          GateBwd gb) {
   {
     const int64_t bt = blockIdx.y;
     A += bt * sA;
@@ -156,7 +175,61 @@ __global__ __launch_bounds__(256, 4) void linear_mfma_kernel(const float* __rest
   // row 8*(r/4) + 4*(l/32) + r%4.
   const int oc = lane & 31;
   const int orow = (lane >> 5) * 4;
-  if constexpr (GATE) {
+  if constexpr (MODE == 2) {
+    // Stage 32-row slabs of g_Z in LDS; each lane then handles 16-byte pieces (4 channels of
+    // one degree, inside one 32-channel group of the gate-paired order).
+    const int C = gb.C, n1 = C / 32;
+    float* ws = smem + wave * 32 * GES;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ws[(8 * (r >> 2) + orow + (r & 3)) * GES + j * 32 + oc] = acc[i][j][r];
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int lin = lane + 64 * q;
+        const int r = lin >> 4;
+        const int c = (lin & 15) * 4;
+        const int64_t gr = row0 + wr + i * 32 + r;
+        const int gc = col0 + wc + c;
+        if (gr >= M || gc >= N) continue;
+        const float4 g = ld4(&ws[r * GES + c]);
+        const int kb = gc / C, ch = gc - kb * C;
+        const float* y0 = gb.Y0 + gr * gb.ldy0;
+        float* out = Y + gr * ldy;
+        if (kb == 0) {
+          const float4 y = ld4(y0 + 4 * C + ch);
+          float4 o;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float yt = (&y.x)[t], sl = sigmoidf_(yt);
+            (&o.x)[t] = (&g.x)[t] * (sl + yt * (sl * (1.0f - sl)));
+          }
+          st4(out + 4 * C + ch, o);
+        } else {
+          const int gate_col = 64 * ((kb - 1) * n1 + (ch >> 5)) + (ch & 31);
+          const float4 sg = ld4(gb.S + gr * gb.lds + (kb - 1) * C + ch);
+          const float4 y = ld4(y0 + gate_col + 32);
+          float4 p = ld4(gb.P1 + gr * gb.ldp1 + (kb - 1) * C + ch);
+          if (kb == 2) p = p + ld4(gb.P2 + gr * gb.ldp2 + ch);
+          float4 og, ov;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float st = (&sg.x)[t], gt = (&g.x)[t];
+            (&ov.x)[t] = gt * st;
+            (&og.x)[t] = (st * (1.0f - st)) * (gt * (&y.x)[t] + (&p.x)[t]);
+          }
+          st4(out + gate_col, og);
+          st4(out + gate_col + 32, ov);
+        }
+      }
+    }
+    return;
+  }
+  if constexpr (MODE == 1) {
     // Each wave stages its 32-row slabs of (gate | value) in LDS, then every lane handles
     // 16-byte pieces: Y rows (64 columns), and for gate pairs S and Z rows (32 columns).
     const int C = go.C, n1 = C / 32;
@@ -260,8 +333,9 @@ static int linear_launch(const float* A, int64_t lda, int64_t sA, const float* W
   const int64_t m_tiles = (M + GBM - 1) / GBM;
   const int64_t total = m_tiles * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
-  hipLaunchKernelGGL((linear_mfma_kernel<false>), dim3((unsigned)total, (unsigned)batch), dim3(256), 0, stream, A, lda,
-                     sA, W, ldw, sW, bias, sBias, bias_batches, Y, ldy, sY, M, N, K, n_tiles, total, GateOut{});
+  hipLaunchKernelGGL((linear_mfma_kernel<0>), dim3((unsigned)total, (unsigned)batch), dim3(256), 0, stream, A, lda,
+                     sA, W, ldw, sW, bias, sBias, bias_batches, Y, ldy, sY, M, N, K, n_tiles, total, GateOut{},
+                     GateBwd{});
   return check_launch(who);
 }
 
@@ -303,8 +377,33 @@ extern "C" int fu_linear_gate(const float* A, int64_t lda, const float* W, int64
   const int n_tiles = (N + GBN - 1) / GBN;
   const int64_t total = ((M + GBM - 1) / GBM) * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
-  hipLaunchKernelGGL((linear_mfma_kernel<true>), dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), A, lda,
+  hipLaunchKernelGGL((linear_mfma_kernel<1>), dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), A, lda,
                      (int64_t)0, W, ldw, (int64_t)0, bias, (int64_t)0, 1, Y, ldy, (int64_t)0, M, N, K, n_tiles, total,
-                     GateOut{Z, ldz, S, lds, C});
+                     GateOut{Z, ldz, S, lds, C}, GateBwd{});
+  return check_launch(who);
+}
+
+extern "C" int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* Wt, int64_t ldw, const float* Y0,
+                                  int64_t ldy0, const float* S, int64_t lds, const float* P1, int64_t ldp1,
+                                  const float* P2, int64_t ldp2, float* gY0, int64_t ldg, int64_t M, int32_t C,
+                                  int32_t K, void* stream) {
+  const char* who = "fu_linear_gate_bwd";
+  if (C <= 0 || C % 64 != 0) return set_error(FU_ERR_UNSUPPORTED, "%s: C=%d must be a multiple of 64", who, C);
+  const int32_t N = 3 * C;
+  // the GEMM's own output (g_Z_m0, N = 3C columns) is never stored; gY0 (5C) is checked here
+  int st = linear_check(gZo, ldgz, Wt, ldw, gY0, ldg, M, N, K, who);
+  if (st != FU_OK) return st;
+  if (ldg < 5 * C || ldy0 < 5 * C || lds < 2 * C || ldp1 < 2 * C || ldp2 < C)
+    return set_error(FU_ERR_SHAPE, "%s: row strides too small", who);
+  if (!Y0 || !S || !P1 || !P2) return set_error(FU_ERR_NULL, "%s: NULL operand", who);
+  if ((ldy0 | lds | ldp1 | ldp2) % 4 != 0 || !aligned16(Y0) || !aligned16(S) || !aligned16(P1) || !aligned16(P2))
+    return set_error(FU_ERR_ALIGN, "%s: operands must be 16-byte aligned with row strides multiples of 4", who);
+  if (M == 0) return FU_OK;
+  const int n_tiles = (N + GBN - 1) / GBN;
+  const int64_t total = ((M + GBM - 1) / GBM) * n_tiles;
+  if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
+  hipLaunchKernelGGL((linear_mfma_kernel<2>), dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), gZo, ldgz,
+                     (int64_t)0, Wt, ldw, (int64_t)0, (const float*)nullptr, (int64_t)0, 1, gY0, ldg, (int64_t)0, M, N,
+                     K, n_tiles, total, GateOut{}, GateBwd{Y0, ldy0, S, lds, P1, ldp1, P2, ldp2, C});
   return check_launch(who);
 }

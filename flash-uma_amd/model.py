@@ -29,7 +29,7 @@ import torch
 import torch.nn as nn
 
 from ops.gather import LAYOUT1_PERM, block_permutation, gather_wigner_split
-from ops.gating import conv1_gate, gate_paired_rows
+from ops.gating import conv1_gate_conv2, gate_paired_rows
 from ops.geom import precompute_geometry
 from ops.linear import complex_linear, linear
 from ops.lmax import gating_lmax, gather_rotate_lmax, init_node_scatter_lmax, rotate_scatter_lmax, wigner_extend
@@ -223,12 +223,12 @@ class Packed_eSCN_Layer(nn.Module):
                                                  col_idx, csd_emb, batch, topology)
         X_m0, X_m1, X_m2 = gather_wigner_split(x_norm, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology,
                                                self.layout)
-        c1 = [getattr(self, "W_conv1_m" + m + sfx) for m in "12" for sfx in ("_R", "_I", "_Rt", "_It_neg")]
-        Z_m0, Z_m1, Z_m2 = conv1_gate(X_m0, X_m1, X_m2, self.W_conv1_m0, self.b_conv1_m0, self.W_conv1_m0_t, *c1,
-                                      self.C)
-        Zo_m0 = linear(Z_m0, self.W_conv2_m0, self.b_conv2_m0, self.W_conv2_m0_t)
-        Zo_m1 = self._complex(Z_m1, "W_conv2_m1")
-        Zo_m2 = self._complex(Z_m2, "W_conv2_m2")
+        sfx = ("_R", "_I", "_Rt", "_It_neg")
+        c1 = [self.W_conv1_m0, self.b_conv1_m0, self.W_conv1_m0_t] + \
+            [getattr(self, "W_conv1_m" + m + x) for m in "12" for x in sfx]
+        c2 = [self.W_conv2_m0, self.b_conv2_m0, self.W_conv2_m0_t] + \
+            [getattr(self, "W_conv2_m" + m + x) for m in "12" for x in sfx]
+        Zo_m0, Zo_m1, Zo_m2 = conv1_gate_conv2(X_m0, X_m1, X_m2, c1, c2, self.C)
         x_mid = rotate_scatter_split(Zo_m0, Zo_m1, Zo_m2, wigner, env, x_in, idx_j, row_ptr, col_idx,
                                      x_in.shape[0])
         return self.atom_wise(self.norm_2(x_mid)) + x_mid

@@ -113,3 +113,76 @@ class Conv1Gate(torch.autograd.Function):
 
 def conv1_gate(X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C):
     return Conv1Gate.apply(X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C)
+
+
+class Conv1GateConv2(torch.autograd.Function):
+    """The edge-wise SO(2) pair of a block (model.py:152-154): conv1 + gate as in Conv1Gate,
+    then conv2 (m = 0 real with bias V0 / c0, m = 1, 2 complex R + iI).  Its backward fuses the
+    gate backward into the conv2 input-gradient epilogues: the m = 1, 2 complex GEMMs write
+    g_Y = g_Z s and their gate sums, then the m = 0 GEMM finishes g_Y_m0 (gate-paired) with
+    the gate gradients; g_Z is never stored and no separate gating pass runs."""
+
+    @staticmethod
+    def forward(ctx, X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, V0, c0, V0t, R1, I1, R1t, I1tn, R2,
+                I2, R2t, I2tn, C):
+        X0 = _lib.require(X0, torch.float32, "X_m0")
+        X1 = _lib.require(X1, torch.float32, "X_m1")
+        X2 = _lib.require(X2, torch.float32, "X_m2")
+        E = X0.shape[0]
+        dev = X0.device
+        st = _lib.stream_ptr(dev)
+        f = lambda *s: torch.empty(*s, device=dev, dtype=torch.float32)
+        Y0, Z0, S = f(E, 5 * C), f(E, Z_M0_MULT * C), f(E, 2 * C)
+        _lib.call("fu_linear_gate", X0.data_ptr(), X0.stride(0), W0.data_ptr(), W0.stride(0), _lib.ptr(b0),
+                  Y0.data_ptr(), Y0.stride(0), Z0.data_ptr(), Z0.stride(0), S.data_ptr(), S.stride(0), E, C,
+                  W0.shape[1], st)
+        outs = []
+        for X, P, Q, s_off in ((X1, P1, Q1, 0), (X2, P2, Q2, C)):
+            Nc, Kc = P.shape
+            Y, Z = f(E, 2 * Nc), f(E, 2 * Nc)
+            _lib.call("fu_complex_linear_gate", X.data_ptr(), X[:, Kc:].data_ptr(), X.stride(0), P.data_ptr(),
+                      Q.data_ptr(), P.stride(0), Y.data_ptr(), Y[:, Nc:].data_ptr(), Y.stride(0), Z.data_ptr(),
+                      Z[:, Nc:].data_ptr(), Z.stride(0), S.data_ptr(), S.stride(0), s_off, E, Nc, Kc, st)
+            outs += [Y, Z]
+        Y1, Z1, Y2, Z2 = outs
+        Zo0 = gemm(Z0, V0, c0)
+        Zo1 = complex_gemm(Z1, R1, I1)
+        Zo2 = complex_gemm(Z2, R2, I2)
+        ctx.save_for_backward(Y0, Y1, Y2, S, W0t, P1t, Q1tn, P2t, Q2tn, V0t, R1t, I1tn, R2t, I2tn)
+        ctx.C = C
+        return Zo0, Zo1, Zo2
+
+    @staticmethod
+    def backward(ctx, g0, g1, g2):
+        Y0, Y1, Y2, S, W0t, P1t, Q1tn, P2t, Q2tn, V0t, R1t, I1tn, R2t, I2tn = ctx.saved_tensors
+        C = ctx.C
+        E = Y0.shape[0]
+        dev = Y0.device
+        st = _lib.stream_ptr(dev)
+        f = lambda *s: torch.empty(*s, device=dev, dtype=torch.float32)
+        g0 = torch.zeros(E, 3 * C, device=dev) if g0 is None else g0.contiguous()
+        g1 = torch.zeros(E, 4 * C, device=dev) if g1 is None else g1.contiguous()
+        g2 = torch.zeros(E, 2 * C, device=dev) if g2 is None else g2.contiguous()
+        gys, psums = [], []
+        for g, Rt, Itn, F, s_off in ((g1, R1t, I1tn, Y1, 0), (g2, R2t, I2tn, Y2, C)):
+            Nc, Kc = Rt.shape
+            gy, ps = f(E, 2 * Nc), f(E, Nc)
+            _lib.call("fu_complex_linear_gate_bwd", g.data_ptr(), g[:, Kc:].data_ptr(), g.stride(0), Rt.data_ptr(),
+                      Itn.data_ptr(), Rt.stride(0), gy.data_ptr(), gy[:, Nc:].data_ptr(), gy.stride(0), F.data_ptr(),
+                      F[:, Nc:].data_ptr(), F.stride(0), S.data_ptr(), S.stride(0), s_off, ps.data_ptr(),
+                      ps.stride(0), E, Nc, Kc, st)
+            gys.append(gy)
+            psums.append(ps)
+        gy0 = f(E, 5 * C)
+        _lib.call("fu_linear_gate_bwd", g0.data_ptr(), g0.stride(0), V0t.data_ptr(), V0t.stride(0), Y0.data_ptr(),
+                  Y0.stride(0), S.data_ptr(), S.stride(0), psums[0].data_ptr(), psums[0].stride(0),
+                  psums[1].data_ptr(), psums[1].stride(0), gy0.data_ptr(), gy0.stride(0), E, C, V0t.shape[1], st)
+        return ((gemm(gy0, W0t), complex_gemm(gys[0], P1t, Q1tn), complex_gemm(gys[1], P2t, Q2tn)) +
+                (None,) * 23)
+
+
+def conv1_gate_conv2(X0, X1, X2, conv1, conv2, C):
+    """conv1 = (W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn) as for conv1_gate; conv2 =
+    (V0, c0, V0t, R1, I1, R1t, I1tn, R2, I2, R2t, I2tn) (m = 0 weight, bias and transpose; the
+    complex m = 1, 2 weights with R^T and -I^T).  Returns Zout_m0, Zout_m1, Zout_m2."""
+    return Conv1GateConv2.apply(X0, X1, X2, *conv1, *conv2, C)

@@ -85,6 +85,18 @@ def _ln_bwd(a):
     return M * (3 * D * 4 + 8), 0
 
 
+def _linear_gate_bwd(a):
+    # g_Z never stored: reads y_l0 + y_lm0 (3C) of Y0, S (2C), P1 (2C), P2 (C); writes gY0 (5C)
+    M, C, K = a[14], a[15], a[16]
+    return 4 * (M * K + 3 * C * K + 13 * M * C), 2 * M * 3 * C * K
+
+
+def _complex_linear_gate_bwd(a):
+    # reads F (2 Nc) and S (Nc), writes gY (2 Nc) and the gate sums (Nc)
+    M, Nc, Kc = a[17], a[18], a[19]
+    return 4 * (2 * M * Kc + 2 * Nc * Kc + 6 * M * Nc), 6 * M * Nc * Kc
+
+
 # lmax-general entry points: K = (L+1)^2 node rows, 34 + ext Wigner scalars, X 10L-2 and rad
 # 6L blocks per edge, Y 6L-1 and Z 5L-1 blocks (the lmax = 2 formulas above at L = 2).
 def _ext(L):
@@ -205,6 +217,8 @@ WORK = {
     "fu_linear_batched": _linear_batched,
     "fu_complex_linear": _complex_linear,
     "fu_linear_gate": _linear_gate,
+    "fu_linear_gate_bwd": _linear_gate_bwd,
+    "fu_complex_linear_gate_bwd": _complex_linear_gate_bwd,
     "fu_gather_fwd_lmax": _gather_fwd_l,
     "fu_gather_bwd_lmax": _gather_bwd_l,
     "fu_scatter_fwd_lmax": _scatter_fwd_l,
@@ -218,7 +232,8 @@ WORK = {
     "fu_complex_linear_gate": _complex_linear_gate,
 }
 
-MFMA_BOUND = {"fu_linear", "fu_linear_batched", "fu_complex_linear", "fu_linear_gate", "fu_complex_linear_gate"}
+MFMA_BOUND = {"fu_linear", "fu_linear_batched", "fu_complex_linear", "fu_linear_gate", "fu_complex_linear_gate",
+              "fu_linear_gate_bwd", "fu_complex_linear_gate_bwd"}
 
 
 def summarize(durations) -> dict:

@@ -234,6 +234,27 @@ int fu_complex_linear_gate(const float* A_r, const float* A_i, int64_t lda, cons
                            float* Z_r, float* Z_i, int64_t ldz, const float* S, int64_t lds,
                            int32_t s_off, int64_t M, int32_t Nc, int32_t Kc, void* stream);
 
+/* conv2 m = 0 input gradient (model.py:154) fused with the gate backward (ops/gating.py:
+ * 109-185): the GEMM g_Z_m0 = gZo (M, 3C) @ Wt^T is not stored; gY0 (M, 5C, gate-paired as Y0)
+ * receives g_y_l0 = g silu'(y_l0), g_y_lm0 = g s_l and g_gate_l = s_l (1 - s_l)
+ * (g y_lm0 + P1[:, (l-1)C:] + (l = 2: P2)).  Y0: the forward output of fu_linear_gate; S its
+ * sigmoids; P1 (M, 2C), P2 (M, C): the m = 1, 2 gate sums from fu_complex_linear_gate_bwd.
+ * K = 3C (the conv2 m = 0 width), Wt = W2_m0^T (no bias).  C a multiple of 64. */
+int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* Wt, int64_t ldw, const float* Y0,
+                       int64_t ldy0, const float* S, int64_t lds, const float* P1, int64_t ldp1,
+                       const float* P2, int64_t ldp2, float* gY0, int64_t ldg, int64_t M, int32_t C,
+                       int32_t K, void* stream);
+
+/* conv2 m = 1 or 2 input gradient fused with the gate backward: the complex product
+ * g_Z = (A_r + i A_i)(P + iQ)^T (P = R^T, Q = -I^T of the conv2 weight) is not stored;
+ * gY_r/gY_i = g_Z s with s = S[row][s_off + column], and Pout = g_Zr F_r + g_Zi F_i (the
+ * gate sum of this block; F = the forward pre-activation Y from fu_complex_linear_gate). */
+int fu_complex_linear_gate_bwd(const float* A_r, const float* A_i, int64_t lda, const float* P,
+                               const float* Q, int64_t ldw, float* gY_r, float* gY_i, int64_t ldg,
+                               const float* F_r, const float* F_i, int64_t ldf, const float* S,
+                               int64_t lds, int32_t s_off, float* Pout, int64_t ldp, int64_t M,
+                               int32_t Nc, int32_t Kc, void* stream);
+
 /* ------------------------------------------------------------------------------------
  * Node-level modules attached to the backbone (model.py:145,157,218) and input plumbing
  * ------------------------------------------------------------------------------------ */

@@ -84,6 +84,47 @@ def test_conv1_gate(cuda, M, C):
         assert_close(a, b, 1e-4, "conv1+gate bwd")
 
 
+@pytest.mark.parametrize("M,C", [(300, 128), (77, 64)])
+def test_conv1_gate_conv2(cuda, M, C):
+    """conv1 + gate + conv2 as one function whose backward fuses the gate backward into the
+    conv2 input-gradient epilogues, against the textbook products and oracle gating (float64)."""
+    _, gating, *_ = _ops()
+    g = torch.Generator().manual_seed(M + 3 * C)
+    r = lambda *s: torch.randn(*s, generator=g)
+    X = [r(M, 6 * C), r(M, 8 * C), r(M, 4 * C)]
+    W0, b0 = r(5 * C, 6 * C) / (6 * C) ** 0.5, r(5 * C) * 0.3
+    R1, I1 = r(2 * C, 4 * C) / (4 * C) ** 0.5, r(2 * C, 4 * C) / (4 * C) ** 0.5
+    R2, I2 = r(C, 2 * C) / (2 * C) ** 0.5, r(C, 2 * C) / (2 * C) ** 0.5
+    V0, c0 = r(3 * C, 3 * C) / (3 * C) ** 0.5, r(3 * C) * 0.3
+    S1, T1 = r(2 * C, 2 * C) / (2 * C) ** 0.5, r(2 * C, 2 * C) / (2 * C) ** 0.5
+    S2, T2 = r(C, C) / C ** 0.5, r(C, C) / C ** 0.5
+    rows = gating.gate_paired_rows(C)
+    dv = lambda t: t.contiguous().to(cuda)
+    W0p = W0[rows]
+    conv1 = [dv(W0p), dv(b0[rows]), dv(W0p.t()), dv(R1), dv(I1), dv(R1.t()), dv(-I1.t()), dv(R2), dv(I2), dv(R2.t()),
+             dv(-I2.t())]
+    conv2 = [dv(V0), dv(c0), dv(V0.t()), dv(S1), dv(T1), dv(S1.t()), dv(-T1.t()), dv(S2), dv(T2), dv(S2.t()),
+             dv(-T2.t())]
+    Xg = [x.to(cuda).requires_grad_(True) for x in X]
+    Zo = gating.conv1_gate_conv2(*Xg, conv1, conv2, C)
+    cot = [r(*z.shape) for z in Zo]
+
+    def ref_fn(x0, x1, x2):
+        y0 = x0 @ W0.double().T + b0.double()
+        y1 = x1 @ R.pack_so2(R1.double(), I1.double()).T
+        y2 = x2 @ R.pack_so2(R2.double(), I2.double()).T
+        z0, z1, z2 = R.gating(y0, y1, y2, C)
+        return (z0 @ V0.double().T + c0.double(), z1 @ R.pack_so2(S1.double(), T1.double()).T,
+                z2 @ R.pack_so2(S2.double(), T2.double()).T)
+
+    ref, gref = _vjp(ref_fn, X, cot)
+    for z, rr in zip(Zo, ref):
+        assert_close(z, rr, TOL, "conv1+gate+conv2 fwd")
+    gx = torch.autograd.grad(Zo, Xg, [c.to(cuda) for c in cot])
+    for a, b in zip(gx, gref):
+        assert_close(a, b, 1e-4, "conv1+gate+conv2 bwd")
+
+
 def test_ln_silu(cuda):
     _, _, _, ln_silu, *_ = _ops()
     torch.manual_seed(1)
