@@ -33,39 +33,42 @@ __device__ __forceinline__ int lds_chunk(int row, int chunk) {
 
 // Extra outputs of the gate epilogue (conv1 m = 0 fused with the gate activation).
 struct GateOut {
-  float* Z;     // (M, 3C): [silu(y_l0), y_l1m0 s1, y_l2m0 s2]
+  float* Z;     // (M, (L+1)C): [silu(y_l0), y_l1m0 s1, ..., y_lLm0 sL]
   int64_t ldz;
-  float* S;     // (M, 2C): [s1, s2] = sigmoid of the two gate blocks
+  float* S;     // (M, LC): [s1, ..., sL] = sigmoid of the L gate blocks
   int64_t lds;
   int32_t C;
+  int32_t L;    // lmax
 };
 
 // Operands of the gate-backward epilogue (conv2 m = 0 input gradient fused with the gate
-// backward).  The GEMM computes g_Z_m0 (M, 3C) = [g_l0, g_l1m0, g_l2m0]; the epilogue writes
-// g_Y_m0 (M, 5C) in the gate-paired order instead: g_y_l0 = g silu'(y_l0), g_y_lm0 = g s_l
-// and g_gate_l = s_l (1 - s_l) (g y_lm0 + P1[l] (+ P2 for l = 2)), where P1 (M, 2C) and
-// P2 (M, C) are the gate sums sum_m g_z y of the m = 1 and m = 2 blocks (written by
-// fu_complex_linear_gate_bwd).
+// backward).  The GEMM computes g_Z_m0 (M, (L+1)C) = [g_l0, g_l1m0, ..., g_lLm0]; the epilogue
+// writes g_Y_m0 (M, (2L+1)C) in the gate-paired order instead: g_y_l0 = g silu'(y_l0),
+// g_y_lm0 = g s_l and g_gate_l = s_l (1 - s_l) (g y_lm0 + P1[l] (+ P2[l] for l >= 2)), where
+// P1 (M, LC) and P2 (M, (L-1)C) are the gate sums sum_m g_z y of the m = 1 and m = 2 blocks
+// (written by fu_complex_linear_gate_bwd).
 struct GateBwd {
-  const float* Y0;  // (M, 5C) forward pre-activation, gate-paired
+  const float* Y0;  // (M, (2L+1)C) forward pre-activation, gate-paired
   int64_t ldy0;
-  const float* S;   // (M, 2C) [s1, s2]
+  const float* S;   // (M, LC) [s1, ..., sL]
   int64_t lds;
   const float* P1;
   int64_t ldp1;
   const float* P2;
   int64_t ldp2;
   int32_t C;
+  int32_t L;
 };
 
 // Batch index blockIdx.y offsets A, W and Y by sA, sW and sY floats; bias (stride sBias) is
 // added in batches [0, bias_batches).
 //
-// MODE 0: plain.  MODE 1 (gate): Y has N = 5C columns in the gate-paired order -- every
-// 64-column pair p holds [32 gate channels | the 32 channels they gate]: pairs 0 .. C/32-1 are
-// (gate_l1, y_l1m0), the next C/32 are (gate_l2, y_l2m0), the last C/64 hold y_l0 -- so a
+// MODE 0: plain.  MODE 1 (gate): Y has N = (2L+1)C columns in the gate-paired order -- every
+// 64-column pair p holds [32 gate channels | the 32 channels they gate]: pairs
+// (l-1) C/32 .. l C/32 - 1 are (gate_l, y_lm0) for l = 1..L, the last C/64 hold y_l0 -- so a
 // wave's 64 staged columns are a gate and its values; the epilogue writes Y (kept for the
-// backward), Z and S.  MODE 2 (gate backward): see GateBwd; Y receives g_Y_m0 (5C columns).
+// backward), Z and S.  MODE 2 (gate backward): see GateBwd; Y receives g_Y_m0 ((2L+1)C
+// columns).
 template <int MODE>
 __global__ __launch_bounds__(256, 4) void linear_mfma_kernel(const float* __restrict__ A, int64_t lda, int64_t sA,
                                                           const float* __restrict__ W, int64_t ldw, int64_t sW,
@@ -178,7 +181,7 @@ __global__ __launch_bounds__(256, 4) void linear_mfma_kernel(const float* __rest
   if constexpr (MODE == 2) {
     // Stage 32-row slabs of g_Z in LDS; each lane then handles 16-byte pieces (4 channels of
     // one degree, inside one 32-channel group of the gate-paired order).
-    const int C = gb.C, n1 = C / 32;
+    const int C = gb.C, n1 = C / 32, L = gb.L;
     float* ws = smem + wave * 32 * GES;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -201,20 +204,20 @@ __global__ __launch_bounds__(256, 4) void linear_mfma_kernel(const float* __rest
         const float* y0 = gb.Y0 + gr * gb.ldy0;
         float* out = Y + gr * ldy;
         if (kb == 0) {
-          const float4 y = ld4(y0 + 4 * C + ch);
+          const float4 y = ld4(y0 + 2 * L * C + ch);
           float4 o;
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             const float yt = (&y.x)[t], sl = sigmoidf_(yt);
             (&o.x)[t] = (&g.x)[t] * (sl + yt * (sl * (1.0f - sl)));
           }
-          st4(out + 4 * C + ch, o);
+          st4(out + 2 * L * C + ch, o);
         } else {
           const int gate_col = 64 * ((kb - 1) * n1 + (ch >> 5)) + (ch & 31);
           const float4 sg = ld4(gb.S + gr * gb.lds + (kb - 1) * C + ch);
           const float4 y = ld4(y0 + gate_col + 32);
           float4 p = ld4(gb.P1 + gr * gb.ldp1 + (kb - 1) * C + ch);
-          if (kb == 2) p = p + ld4(gb.P2 + gr * gb.ldp2 + ch);
+          if (kb >= 2) p = p + ld4(gb.P2 + gr * gb.ldp2 + (kb - 2) * C + ch);
           float4 og, ov;
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
@@ -232,7 +235,7 @@ __global__ __launch_bounds__(256, 4) void linear_mfma_kernel(const float* __rest
   if constexpr (MODE == 1) {
     // Each wave stages its 32-row slabs of (gate | value) in LDS, then every lane handles
     // 16-byte pieces: Y rows (64 columns), and for gate pairs S and Z rows (32 columns).
-    const int C = go.C, n1 = C / 32;
+    const int C = go.C, n1 = C / 32, L = go.L;
     const int q0 = col0 + wc;  // first column of this wave's pair
     const int p = q0 / 64;
     const bool live = q0 < N;
@@ -260,14 +263,14 @@ __global__ __launch_bounds__(256, 4) void linear_mfma_kernel(const float* __rest
         }
         st4(Y + row * ldy + q0 + c, g);
         st4(Y + row * ldy + q0 + 32 + c, v);
-        if (p < 2 * n1) {
-          const int kind = p < n1 ? 0 : 1;
+        if (p < L * n1) {
+          const int kind = p / n1;
           const int ch = 32 * (p - kind * n1) + c;
           const float4 sg = make_float4(sigmoidf_(g.x), sigmoidf_(g.y), sigmoidf_(g.z), sigmoidf_(g.w));
           st4(go.S + row * go.lds + kind * C + ch, sg);
           st4(go.Z + row * go.ldz + (1 + kind) * C + ch, v * sg);
         } else {
-          const int ch = q0 - 4 * C + c;
+          const int ch = q0 - 2 * L * C + c;
           st4(go.Z + row * go.ldz + ch,
               make_float4(g.x * sigmoidf_(g.x), g.y * sigmoidf_(g.y), g.z * sigmoidf_(g.z), g.w * sigmoidf_(g.w)));
           st4(go.Z + row * go.ldz + ch + 32,
@@ -363,14 +366,15 @@ extern "C" int fu_linear_batched(const float* A, int64_t lda, int64_t stride_a, 
 
 extern "C" int fu_linear_gate(const float* A, int64_t lda, const float* W, int64_t ldw, const float* bias, float* Y,
                               int64_t ldy, float* Z, int64_t ldz, float* S, int64_t lds, int64_t M, int32_t C,
-                              int32_t K, void* stream) {
+                              int32_t K, int32_t lmax, void* stream) {
   const char* who = "fu_linear_gate";
   if (C <= 0 || C % 64 != 0) return set_error(FU_ERR_UNSUPPORTED, "%s: C=%d must be a multiple of 64", who, C);
-  const int32_t N = 5 * C;
+  if (lmax < 2 || lmax > 4) return set_error(FU_ERR_UNSUPPORTED, "%s: lmax=%d unsupported (2, 3 or 4)", who, lmax);
+  const int32_t N = (2 * lmax + 1) * C;
   int st = linear_check(A, lda, W, ldw, Y, ldy, M, N, K, who);
   if (st != FU_OK) return st;
   if (!Z || !S) return set_error(FU_ERR_NULL, "%s: NULL output", who);
-  if (ldz < 3 * C || lds < 2 * C) return set_error(FU_ERR_SHAPE, "%s: Z / S row strides too small", who);
+  if (ldz < (lmax + 1) * C || lds < lmax * C) return set_error(FU_ERR_SHAPE, "%s: Z / S row strides too small", who);
   if (ldz % 4 != 0 || lds % 4 != 0 || !aligned16(Z) || !aligned16(S) || (bias && !aligned16(bias)))
     return set_error(FU_ERR_ALIGN, "%s: Z, S and bias must be 16-byte aligned with row strides multiples of 4", who);
   if (M == 0) return FU_OK;
@@ -379,21 +383,23 @@ extern "C" int fu_linear_gate(const float* A, int64_t lda, const float* W, int64
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
   hipLaunchKernelGGL((linear_mfma_kernel<1>), dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), A, lda,
                      (int64_t)0, W, ldw, (int64_t)0, bias, (int64_t)0, 1, Y, ldy, (int64_t)0, M, N, K, n_tiles, total,
-                     GateOut{Z, ldz, S, lds, C}, GateBwd{});
+                     GateOut{Z, ldz, S, lds, C, lmax}, GateBwd{});
   return check_launch(who);
 }
 
 extern "C" int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* Wt, int64_t ldw, const float* Y0,
                                   int64_t ldy0, const float* S, int64_t lds, const float* P1, int64_t ldp1,
                                   const float* P2, int64_t ldp2, float* gY0, int64_t ldg, int64_t M, int32_t C,
-                                  int32_t K, void* stream) {
+                                  int32_t K, int32_t lmax, void* stream) {
   const char* who = "fu_linear_gate_bwd";
   if (C <= 0 || C % 64 != 0) return set_error(FU_ERR_UNSUPPORTED, "%s: C=%d must be a multiple of 64", who, C);
-  const int32_t N = 3 * C;
-  // the GEMM's own output (g_Z_m0, N = 3C columns) is never stored; gY0 (5C) is checked here
+  if (lmax < 2 || lmax > 4) return set_error(FU_ERR_UNSUPPORTED, "%s: lmax=%d unsupported (2, 3 or 4)", who, lmax);
+  const int32_t N = (lmax + 1) * C;
+  // the GEMM's own output (g_Z_m0, N = (L+1)C columns) is never stored; gY0 ((2L+1)C) is checked here
   int st = linear_check(gZo, ldgz, Wt, ldw, gY0, ldg, M, N, K, who);
   if (st != FU_OK) return st;
-  if (ldg < 5 * C || ldy0 < 5 * C || lds < 2 * C || ldp1 < 2 * C || ldp2 < C)
+  if (ldg < (2 * lmax + 1) * C || ldy0 < (2 * lmax + 1) * C || lds < lmax * C || ldp1 < lmax * C ||
+      ldp2 < (lmax - 1) * C)
     return set_error(FU_ERR_SHAPE, "%s: row strides too small", who);
   if (!Y0 || !S || !P1 || !P2) return set_error(FU_ERR_NULL, "%s: NULL operand", who);
   if ((ldy0 | lds | ldp1 | ldp2) % 4 != 0 || !aligned16(Y0) || !aligned16(S) || !aligned16(P1) || !aligned16(P2))
@@ -404,6 +410,6 @@ extern "C" int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* W
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
   hipLaunchKernelGGL((linear_mfma_kernel<2>), dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), gZo, ldgz,
                      (int64_t)0, Wt, ldw, (int64_t)0, (const float*)nullptr, (int64_t)0, 1, gY0, ldg, (int64_t)0, M, N,
-                     K, n_tiles, total, GateOut{}, GateBwd{Y0, ldy0, S, lds, P1, ldp1, P2, ldp2, C});
+                     K, n_tiles, total, GateOut{}, GateBwd{Y0, ldy0, S, lds, P1, ldp1, P2, ldp2, C, lmax});
   return check_launch(who);
 }

@@ -19,7 +19,8 @@ Differences in mechanism (not in results):
 lmax: the reference builds lmax = 2 only (wrapper.py:105-118).  Here lmax = 3 and 4 are
 supported too (mmax = 2): the per-edge blocks grow degree by degree in the reference's order
 (ops/lmax.py), the Wigner rows of degree 3 and 4 come from fu_wigner_ext_fwd, and the layer
-runs the unfused conv1 + gate of that order.  lmax = 2 keeps the fused, permuted layout below.
+runs the same fused conv1 + gate + conv2 as lmax = 2 (gate-paired conv1 m = 0 rows); only
+lmax = 2 also permutes the gather blocks side-major.
 """
 from __future__ import annotations
 
@@ -32,7 +33,7 @@ from ops.gather import LAYOUT1_PERM, block_permutation, gather_wigner_split
 from ops.gating import conv1_gate_conv2, gate_paired_rows
 from ops.geom import precompute_geometry
 from ops.linear import complex_linear, linear
-from ops.lmax import gating_lmax, gather_rotate_lmax, init_node_scatter_lmax, rotate_scatter_lmax, wigner_extend
+from ops.lmax import gather_rotate_lmax, init_node_scatter_lmax, rotate_scatter_lmax, wigner_extend
 from ops.ln_silu import layer_norm_silu
 from ops.node import permute_rows
 from ops.radial import RadialBank
@@ -180,13 +181,15 @@ class Packed_eSCN_Layer(nn.Module):
         self.prepared = True
 
     def _prepare_reference_order(self, dtype):
-        """lmax > 2: weights in the reference's block order (ops/lmax.py); conv1 m = 0 and the
-        gate run as separate kernels."""
+        """lmax > 2: gather blocks in the reference's order extended by degree (ops/lmax.py);
+        conv1 m = 0 rows gate-paired for the fused conv1 + gate + conv2."""
         for name in ("W_rad1_1", "W_rad1_2", "W_rad1_3"):
             W = getattr(self, name).data
             self.register_buffer(name + "_t", W.to(dtype).t().contiguous())
-        self._register("W_conv1_m0", self.W1_m0.data, dtype)
-        self.register_buffer("b_conv1_m0", _frozen(self.b1_m0.data).to(dtype))
+        # conv1 m = 0 output rows in the gate-paired order of the fused gate epilogue
+        rows = gate_paired_rows(self.C, self.lmax).to(self.W1_m0.device)
+        self._register("W_conv1_m0", self.W1_m0.data[rows], dtype)
+        self.register_buffer("b_conv1_m0", _frozen(self.b1_m0.data[rows]).to(dtype))
         self._register_complex("W_conv1_m1", self.W1_m1_R.data, self.W1_m1_I.data, dtype)
         self._register_complex("W_conv1_m2", self.W1_m2_R.data, self.W1_m2_I.data, dtype)
         self._register("W_conv2_m0", self.W2_m0.data, dtype)
@@ -238,13 +241,12 @@ class Packed_eSCN_Layer(nn.Module):
         L, C = self.lmax, self.C
         X_m0, X_m1, X_m2 = gather_rotate_lmax(x_norm, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, topology,
                                               L)
-        Y_m0 = linear(X_m0, self.W_conv1_m0, self.b_conv1_m0, self.W_conv1_m0_t)
-        Y_m1 = self._complex(X_m1, "W_conv1_m1")
-        Y_m2 = self._complex(X_m2, "W_conv1_m2")
-        Z_m0, Z_m1, Z_m2 = gating_lmax(Y_m0, Y_m1, Y_m2, C, L)
-        Zo_m0 = linear(Z_m0, self.W_conv2_m0, self.b_conv2_m0, self.W_conv2_m0_t)
-        Zo_m1 = self._complex(Z_m1, "W_conv2_m1")
-        Zo_m2 = self._complex(Z_m2, "W_conv2_m2")
+        sfx = ("_R", "_I", "_Rt", "_It_neg")
+        c1 = [self.W_conv1_m0, self.b_conv1_m0, self.W_conv1_m0_t] + \
+            [getattr(self, "W_conv1_m" + m + x) for m in "12" for x in sfx]
+        c2 = [self.W_conv2_m0, self.b_conv2_m0, self.W_conv2_m0_t] + \
+            [getattr(self, "W_conv2_m" + m + x) for m in "12" for x in sfx]
+        Zo_m0, Zo_m1, Zo_m2 = conv1_gate_conv2(X_m0, X_m1, X_m2, c1, c2, C)
         x_mid = rotate_scatter_lmax(Zo_m0, Zo_m1, Zo_m2, wigner, wig_ext, env, x_in, idx_j, row_ptr, col_idx,
                                     x_in.shape[0], L)
         return self.atom_wise(self.norm_2(x_mid)) + x_mid

@@ -3,8 +3,9 @@ the SO(2) conv1 of a block (model.py:152) with the gate activation (model.py:153
 GEMM epilogues, so the gated features are written once and the gating pass over Y is gone.
 
 layout 1 of Y_m0 is the gate-paired column order (gate_paired_rows): 64-column pairs
-[32 gate_l1 channels | the 32 y_l1m0 channels they gate], then [gate_l2 | y_l2m0], then
-y_l0; the conv1 m = 0 weight rows are permuted to it at freeze time."""
+[32 gate_l channels | the 32 y_lm0 channels they gate] for l = 1..lmax, then y_l0; the
+conv1 m = 0 weight rows are permuted to it at freeze time.  conv1_gate_conv2 handles lmax
+2, 3 and 4 (the degree count is read from the conv1 m = 0 weight)."""
 from __future__ import annotations
 
 import torch
@@ -14,21 +15,26 @@ from .constants import Z_M0_MULT, Z_M1_MULT, Z_M2_MULT
 from .linear import complex_gemm, gemm
 
 
-def gate_paired_rows(C: int) -> torch.Tensor:
-    """Reference column of Y_m0 (= [gate_l1, gate_l2, y_l0, y_l1m0, y_l2m0], C each) for each
-    column of the gate-paired order."""
-    n1 = C // 32
+def gate_paired_rows(C: int, lmax: int = 2) -> torch.Tensor:
+    """Reference column of Y_m0 (= [gate_1 .. gate_L, y_0, y_1m0 .. y_Lm0], C each, L = lmax)
+    for each column of the gate-paired order: 64-column pairs [gate_l | y_lm0] x C/32 for
+    l = 1..L, then y_0."""
+    L, n1 = lmax, C // 32
     cols = []
-    for p in range(5 * C // 64):
+    for p in range((2 * L + 1) * C // 64):
         for h in range(2):
             for c in range(32):
-                if p < n1:
-                    cols.append((0 if h == 0 else 3 * C) + 32 * p + c)
-                elif p < 2 * n1:
-                    cols.append((C if h == 0 else 4 * C) + 32 * (p - n1) + c)
+                if p < L * n1:
+                    l, q = p // n1 + 1, p % n1
+                    cols.append(((l - 1) * C if h == 0 else (L + l) * C) + 32 * q + c)
                 else:
-                    cols.append(2 * C + 64 * p + 32 * h + c - 4 * C)
+                    cols.append(L * C + 64 * (p - L * n1) + 32 * h + c)
     return torch.tensor(cols, dtype=torch.long)
+
+
+def _degrees(W0: torch.Tensor, C: int) -> int:
+    """lmax from the conv1 m = 0 weight ((2 lmax + 1) C rows)."""
+    return (W0.shape[0] // C - 1) // 2
 
 
 class FusedGatingSplit(torch.autograd.Function):
@@ -87,10 +93,11 @@ class Conv1Gate(torch.autograd.Function):
         dev = X0.device
         st = _lib.stream_ptr(dev)
         f = lambda *s: torch.empty(*s, device=dev, dtype=torch.float32)
-        Y0, Z0, S = f(E, 5 * C), f(E, Z_M0_MULT * C), f(E, 2 * C)
+        L = _degrees(W0, C)
+        Y0, Z0, S = f(E, (2 * L + 1) * C), f(E, (L + 1) * C), f(E, L * C)
         _lib.call("fu_linear_gate", X0.data_ptr(), X0.stride(0), W0.data_ptr(), W0.stride(0), _lib.ptr(b0),
                   Y0.data_ptr(), Y0.stride(0), Z0.data_ptr(), Z0.stride(0), S.data_ptr(), S.stride(0), E, C,
-                  W0.shape[1], st)
+                  W0.shape[1], L, st)
         outs = []
         for X, P, Q, s_off in ((X1, P1, Q1, 0), (X2, P2, Q2, C)):
             Nc, Kc = P.shape
@@ -100,6 +107,8 @@ class Conv1Gate(torch.autograd.Function):
                       Z[:, Nc:].data_ptr(), Z.stride(0), S.data_ptr(), S.stride(0), s_off, E, Nc, Kc, st)
             outs += [Y, Z]
         Y1, Z1, Y2, Z2 = outs
+        if L != 2:
+            raise _lib.FlashUMAError("conv1_gate: lmax 2 only (use conv1_gate_conv2 for lmax 3, 4)")
         ctx.save_for_backward(Y0, Y1, Y2, W0t, P1t, Q1tn, P2t, Q2tn)
         ctx.C = C
         return Z0, Z1, Z2
@@ -132,10 +141,11 @@ class Conv1GateConv2(torch.autograd.Function):
         dev = X0.device
         st = _lib.stream_ptr(dev)
         f = lambda *s: torch.empty(*s, device=dev, dtype=torch.float32)
-        Y0, Z0, S = f(E, 5 * C), f(E, Z_M0_MULT * C), f(E, 2 * C)
+        L = _degrees(W0, C)
+        Y0, Z0, S = f(E, (2 * L + 1) * C), f(E, (L + 1) * C), f(E, L * C)
         _lib.call("fu_linear_gate", X0.data_ptr(), X0.stride(0), W0.data_ptr(), W0.stride(0), _lib.ptr(b0),
                   Y0.data_ptr(), Y0.stride(0), Z0.data_ptr(), Z0.stride(0), S.data_ptr(), S.stride(0), E, C,
-                  W0.shape[1], st)
+                  W0.shape[1], L, st)
         outs = []
         for X, P, Q, s_off in ((X1, P1, Q1, 0), (X2, P2, Q2, C)):
             Nc, Kc = P.shape
@@ -149,20 +159,20 @@ class Conv1GateConv2(torch.autograd.Function):
         Zo1 = complex_gemm(Z1, R1, I1)
         Zo2 = complex_gemm(Z2, R2, I2)
         ctx.save_for_backward(Y0, Y1, Y2, S, W0t, P1t, Q1tn, P2t, Q2tn, V0t, R1t, I1tn, R2t, I2tn)
-        ctx.C = C
+        ctx.C, ctx.L = C, L
         return Zo0, Zo1, Zo2
 
     @staticmethod
     def backward(ctx, g0, g1, g2):
         Y0, Y1, Y2, S, W0t, P1t, Q1tn, P2t, Q2tn, V0t, R1t, I1tn, R2t, I2tn = ctx.saved_tensors
-        C = ctx.C
+        C, L = ctx.C, ctx.L
         E = Y0.shape[0]
         dev = Y0.device
         st = _lib.stream_ptr(dev)
         f = lambda *s: torch.empty(*s, device=dev, dtype=torch.float32)
-        g0 = torch.zeros(E, 3 * C, device=dev) if g0 is None else g0.contiguous()
-        g1 = torch.zeros(E, 4 * C, device=dev) if g1 is None else g1.contiguous()
-        g2 = torch.zeros(E, 2 * C, device=dev) if g2 is None else g2.contiguous()
+        g0 = torch.zeros(E, (L + 1) * C, device=dev) if g0 is None else g0.contiguous()
+        g1 = torch.zeros(E, 2 * L * C, device=dev) if g1 is None else g1.contiguous()
+        g2 = torch.zeros(E, 2 * (L - 1) * C, device=dev) if g2 is None else g2.contiguous()
         gys, psums = [], []
         for g, Rt, Itn, F, s_off in ((g1, R1t, I1tn, Y1, 0), (g2, R2t, I2tn, Y2, C)):
             Nc, Kc = Rt.shape
@@ -173,10 +183,11 @@ class Conv1GateConv2(torch.autograd.Function):
                       ps.stride(0), E, Nc, Kc, st)
             gys.append(gy)
             psums.append(ps)
-        gy0 = f(E, 5 * C)
+        gy0 = f(E, (2 * L + 1) * C)
         _lib.call("fu_linear_gate_bwd", g0.data_ptr(), g0.stride(0), V0t.data_ptr(), V0t.stride(0), Y0.data_ptr(),
                   Y0.stride(0), S.data_ptr(), S.stride(0), psums[0].data_ptr(), psums[0].stride(0),
-                  psums[1].data_ptr(), psums[1].stride(0), gy0.data_ptr(), gy0.stride(0), E, C, V0t.shape[1], st)
+                  psums[1].data_ptr(), psums[1].stride(0), gy0.data_ptr(), gy0.stride(0), E, C, V0t.shape[1], L,
+                  st)
         return ((gemm(gy0, W0t), complex_gemm(gys[0], P1t, Q1tn), complex_gemm(gys[1], P2t, Q2tn)) +
                 (None,) * 23)
 

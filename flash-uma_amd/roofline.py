@@ -86,9 +86,11 @@ def _ln_bwd(a):
 
 
 def _linear_gate_bwd(a):
-    # g_Z never stored: reads y_l0 + y_lm0 (3C) of Y0, S (2C), P1 (2C), P2 (C); writes gY0 (5C)
-    M, C, K = a[14], a[15], a[16]
-    return 4 * (M * K + 3 * C * K + 13 * M * C), 2 * M * 3 * C * K
+    # g_Z never stored: reads y_l0 + y_lm0 ((L+1)C) of Y0, S (LC), P1 (LC), P2 ((L-1)C);
+    # writes gY0 ((2L+1)C)
+    M, C, K, L = a[14], a[15], a[16], a[17]
+    N = (L + 1) * C
+    return 4 * (M * K + N * K + (6 * L + 1) * M * C), 2 * M * N * K
 
 
 def _complex_linear_gate_bwd(a):
@@ -171,10 +173,10 @@ def _complex_linear(a):
 
 
 def _linear_gate(a):
-    # N = 5C outputs Y plus the gate's sigmoids S (2C) and gated / SiLU copies Z (3C)
-    M, C, K = a[11], a[12], a[13]
-    N = 5 * C
-    return 4 * (M * K + N * K + M * N + 5 * M * C), 2 * M * N * K
+    # N = (2L+1)C outputs Y plus the gate's sigmoids S (LC) and gated / SiLU copies Z ((L+1)C)
+    M, C, K, L = a[11], a[12], a[13], a[14]
+    N = (2 * L + 1) * C
+    return 4 * (M * K + N * K + M * N + (2 * L + 1) * M * C), 2 * M * N * K
 
 
 def _complex_linear_gate(a):

@@ -218,32 +218,34 @@ int fu_complex_linear(const float* A_r, const float* A_i, int64_t lda, const flo
                       int32_t Kc, void* stream);
 
 /* conv1 m = 0 fused with the gate activation (model.py:152-153 with ops/gating.py:32-103):
- * Y = A W^T + bias with N = 5C columns in the gate-paired order (W and bias rows permuted to
- * it, see fu_gating_fwd layout 1), written for the backward, plus Z (M, 3C) =
- * [silu(y_l0), y_l1m0 s1, y_l2m0 s2] and S (M, 2C) = [s1, s2], s = sigmoid(gate).
- * C a multiple of 64; other constraints as fu_linear. */
+ * Y = A W^T + bias with N = (2L+1)C columns (L = lmax) in the gate-paired order: 64-column
+ * pairs [gate_l | y_lm0] x C/32 for l = 1..L, then y_l0 (W and bias rows permuted to it; at
+ * lmax 2 this is fu_gating_fwd layout 1), written for the backward, plus Z (M, (L+1)C) =
+ * [silu(y_l0), y_l1m0 s1, ..., y_lLm0 sL] and S (M, LC) = [s1 .. sL], s = sigmoid(gate).
+ * lmax 2..4; C a multiple of 64; other constraints as fu_linear. */
 int fu_linear_gate(const float* A, int64_t lda, const float* W, int64_t ldw, const float* bias,
                    float* Y, int64_t ldy, float* Z, int64_t ldz, float* S, int64_t lds, int64_t M,
-                   int32_t C, int32_t K, void* stream);
+                   int32_t C, int32_t K, int32_t lmax, void* stream);
 
 /* conv1 m = 1, 2 fused with the gate activation: fu_complex_linear, then
  * Z_r = Y_r s, Z_i = Y_i s with s = S[row][s_off + column] (S from fu_linear_gate: s_off = 0
- * for m = 1, whose columns are [l1 | l2]; s_off = C for m = 2). */
+ * for m = 1, whose columns are [l1 | .. | lL]; s_off = C for m = 2, columns [l2 | .. | lL]). */
 int fu_complex_linear_gate(const float* A_r, const float* A_i, int64_t lda, const float* P,
                            const float* Q, int64_t ldw, float* Y_r, float* Y_i, int64_t ldy,
                            float* Z_r, float* Z_i, int64_t ldz, const float* S, int64_t lds,
                            int32_t s_off, int64_t M, int32_t Nc, int32_t Kc, void* stream);
 
 /* conv2 m = 0 input gradient (model.py:154) fused with the gate backward (ops/gating.py:
- * 109-185): the GEMM g_Z_m0 = gZo (M, 3C) @ Wt^T is not stored; gY0 (M, 5C, gate-paired as Y0)
- * receives g_y_l0 = g silu'(y_l0), g_y_lm0 = g s_l and g_gate_l = s_l (1 - s_l)
- * (g y_lm0 + P1[:, (l-1)C:] + (l = 2: P2)).  Y0: the forward output of fu_linear_gate; S its
- * sigmoids; P1 (M, 2C), P2 (M, C): the m = 1, 2 gate sums from fu_complex_linear_gate_bwd.
- * K = 3C (the conv2 m = 0 width), Wt = W2_m0^T (no bias).  C a multiple of 64. */
+ * 109-185): the GEMM g_Z_m0 = gZo (M, (L+1)C) @ Wt^T is not stored; gY0 (M, (2L+1)C,
+ * gate-paired as Y0) receives g_y_l0 = g silu'(y_l0), g_y_lm0 = g s_l and
+ * g_gate_l = s_l (1 - s_l) (g y_lm0 + P1[:, (l-1)C:] + (l >= 2: P2[:, (l-2)C:])).  Y0: the
+ * forward output of fu_linear_gate; S its sigmoids; P1 (M, LC), P2 (M, (L-1)C): the m = 1, 2
+ * gate sums from fu_complex_linear_gate_bwd.  K = (L+1)C (the conv2 m = 0 width),
+ * Wt = W2_m0^T (no bias).  lmax 2..4; C a multiple of 64. */
 int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* Wt, int64_t ldw, const float* Y0,
                        int64_t ldy0, const float* S, int64_t lds, const float* P1, int64_t ldp1,
                        const float* P2, int64_t ldp2, float* gY0, int64_t ldg, int64_t M, int32_t C,
-                       int32_t K, void* stream);
+                       int32_t K, int32_t lmax, void* stream);
 
 /* conv2 m = 1 or 2 input gradient fused with the gate backward: the complex product
  * g_Z = (A_r + i A_i)(P + iQ)^T (P = R^T, Q = -I^T of the conv2 weight) is not stored;

@@ -84,21 +84,23 @@ def test_conv1_gate(cuda, M, C):
         assert_close(a, b, 1e-4, "conv1+gate bwd")
 
 
-@pytest.mark.parametrize("M,C", [(300, 128), (77, 64)])
-def test_conv1_gate_conv2(cuda, M, C):
+@pytest.mark.parametrize("M,C,L", [(300, 128, 2), (77, 64, 2), (150, 64, 4), (100, 128, 3)])
+def test_conv1_gate_conv2(cuda, M, C, L):
     """conv1 + gate + conv2 as one function whose backward fuses the gate backward into the
-    conv2 input-gradient epilogues, against the textbook products and oracle gating (float64)."""
+    conv2 input-gradient epilogues, against the textbook products and oracle gating (float64);
+    lmax = L (3 and 4 use the degree-extended block order of oracle.ops_ref.gating_lmax)."""
     _, gating, *_ = _ops()
-    g = torch.Generator().manual_seed(M + 3 * C)
+    g = torch.Generator().manual_seed(M + 3 * C + L)
     r = lambda *s: torch.randn(*s, generator=g)
-    X = [r(M, 6 * C), r(M, 8 * C), r(M, 4 * C)]
-    W0, b0 = r(5 * C, 6 * C) / (6 * C) ** 0.5, r(5 * C) * 0.3
-    R1, I1 = r(2 * C, 4 * C) / (4 * C) ** 0.5, r(2 * C, 4 * C) / (4 * C) ** 0.5
-    R2, I2 = r(C, 2 * C) / (2 * C) ** 0.5, r(C, 2 * C) / (2 * C) ** 0.5
-    V0, c0 = r(3 * C, 3 * C) / (3 * C) ** 0.5, r(3 * C) * 0.3
-    S1, T1 = r(2 * C, 2 * C) / (2 * C) ** 0.5, r(2 * C, 2 * C) / (2 * C) ** 0.5
-    S2, T2 = r(C, C) / C ** 0.5, r(C, C) / C ** 0.5
-    rows = gating.gate_paired_rows(C)
+    X = [r(M, 2 * (L + 1) * C), r(M, 4 * L * C), r(M, 4 * (L - 1) * C)]
+    W0, b0 = r((2 * L + 1) * C, 2 * (L + 1) * C) / (2 * (L + 1) * C) ** 0.5, r((2 * L + 1) * C) * 0.3
+    R1, I1 = r(L * C, 2 * L * C) / (2 * L * C) ** 0.5, r(L * C, 2 * L * C) / (2 * L * C) ** 0.5
+    n2 = (L - 1) * C
+    R2, I2 = r(n2, 2 * n2) / (2 * n2) ** 0.5, r(n2, 2 * n2) / (2 * n2) ** 0.5
+    V0, c0 = r((L + 1) * C, (L + 1) * C) / ((L + 1) * C) ** 0.5, r((L + 1) * C) * 0.3
+    S1, T1 = r(L * C, L * C) / (L * C) ** 0.5, r(L * C, L * C) / (L * C) ** 0.5
+    S2, T2 = r(n2, n2) / n2 ** 0.5, r(n2, n2) / n2 ** 0.5
+    rows = gating.gate_paired_rows(C, L)
     dv = lambda t: t.contiguous().to(cuda)
     W0p = W0[rows]
     conv1 = [dv(W0p), dv(b0[rows]), dv(W0p.t()), dv(R1), dv(I1), dv(R1.t()), dv(-I1.t()), dv(R2), dv(I2), dv(R2.t()),
@@ -113,7 +115,7 @@ def test_conv1_gate_conv2(cuda, M, C):
         y0 = x0 @ W0.double().T + b0.double()
         y1 = x1 @ R.pack_so2(R1.double(), I1.double()).T
         y2 = x2 @ R.pack_so2(R2.double(), I2.double()).T
-        z0, z1, z2 = R.gating(y0, y1, y2, C)
+        z0, z1, z2 = R.gating(y0, y1, y2, C) if L == 2 else R.gating_lmax(y0, y1, y2, C, L)
         return (z0 @ V0.double().T + c0.double(), z1 @ R.pack_so2(S1.double(), T1.double()).T,
                 z2 @ R.pack_so2(S2.double(), T2.double()).T)
 
