@@ -336,8 +336,10 @@ class eSCN_Inference_Model(nn.Module):
                                                  self.offset_g, self.coeff_g, self.cutoff, topo, False)
         # 3. Every radial MLP (edge-degree embedding + one per block) as one bank
         rads = self.radial_bank(gauss, Z_s, idx_i_s, idx_j_s)
-        # 4. Edge-degree embedding (lmax > 2: with the degree-3/4 Wigner rows)
+        # 4. Edge-degree embedding (lmax > 2: with the degree-3/4 Wigner rows); the bank's
+        #    output layers run on a side stream, so each output is waited for before use
         wig_ext = None
+        self.radial_bank.wait(0)
         if self.lmax == 2:
             x_node_s = init_node_scatter(rads[0], wigner, env, Z_s, batch_s, self.W_sphere, csd_emb, idx_j_s,
                                          row_ptr, col_idx, N)
@@ -346,7 +348,8 @@ class eSCN_Inference_Model(nn.Module):
             x_node_s = init_node_scatter_lmax(rads[0], wigner, wig_ext, env, Z_s, batch_s, self.W_sphere, csd_emb,
                                               idx_j_s, row_ptr, col_idx, N, self.lmax)
         # 5. Message-passing blocks
-        for layer, rad in zip(self.layers, rads[1:]):
+        for k, (layer, rad) in enumerate(zip(self.layers, rads[1:])):
+            self.radial_bank.wait(k + 1)
             x_node_s = layer(x_node_s, None, wigner, env, idx_i_s, idx_j_s, row_ptr, col_idx, csd_emb,
                              batch_s, topo, rad_out=rad, wig_ext=wig_ext)
             if self.charge_end > self.charge_start or self.spin_end > self.spin_start:

@@ -97,15 +97,65 @@ class RadialBank(torch.nn.Module):
             reg(f"W3_{k}_t", m[8].t())
             reg(f"b3_{k}", m[9])
 
-    def forward(self, gauss, Z, idx_i, idx_j):
-        """gauss (E, B) -> tuple of G radial outputs (E, n_k)."""
-        W3 = [(getattr(self, f"W3_{k}"), getattr(self, f"W3_{k}_t"), getattr(self, f"b3_{k}")) for k in range(self.G)]
-        return _RadialBankFn.apply(gauss, Z, idx_i, idx_j, self, *[w for t in W3 for w in t])
+    def forward(self, gauss, Z, idx_i, idx_j, streams: bool = True):
+        """gauss (E, B) -> tuple of G radial outputs (E, n_k).
+
+        The trunk (first two layers of all MLPs) runs on the current stream.  Each block's
+        output layer is its own autograd node launched on a side stream (streams=True), so
+        blocks 2..G are computed while the caller already consumes block 1, and in the
+        backward each block's input gradient runs as soon as its output gradient exists,
+        concurrently with the caller's remaining backward: the autograd engine runs every
+        backward on the stream of its forward and orders the streams with events.  Call
+        wait(k) on the consuming stream before reading output k."""
+        holder = _GradHolder()
+        h2s = _RadialTrunkFn.apply(gauss, Z, idx_i, idx_j, self, holder)
+        main = torch.cuda.current_stream(gauss.device)
+        side = self._side_stream(gauss.device) if streams else main
+        cross = side is not main
+        outs, self._events = [], []
+        if cross:
+            side.wait_stream(main)
+            if holder.g is not None:
+                holder.g.record_stream(side)
+        with torch.cuda.stream(side):
+            for k in range(self.G):
+                W, Wt, b = getattr(self, f"W3_{k}"), getattr(self, f"W3_{k}_t"), getattr(self, f"b3_{k}")
+                if cross:
+                    h2s[k].record_stream(side)
+                out = _RadialOutFn.apply(h2s[k], W, b, Wt, holder, k, cross)
+                if cross:
+                    out.record_stream(main)
+                    ev = torch.cuda.Event()
+                    ev.record(side)
+                    self._events.append(ev)
+                outs.append(out)
+        return tuple(outs)
+
+    def wait(self, k: int) -> None:
+        """Make the current stream wait until output k has been computed."""
+        if self._events:
+            torch.cuda.current_stream().wait_event(self._events[k])
+
+    def _side_stream(self, device):
+        st = getattr(self, "_side", None)
+        if st is None or st.device != device:
+            st = torch.cuda.Stream(device)   # default priority
+            self._side = st
+        return st
 
 
-class _RadialBankFn(torch.autograd.Function):
+class _GradHolder:
+    """The (E, G*C) gradient of the trunk output: allocated by the trunk forward on the main
+    stream, filled slice by slice by the blocks' output-layer backwards and consumed by the
+    trunk backward; it lives as long as the autograd graph."""
+
+    def __init__(self):
+        self.g = None
+
+
+class _RadialTrunkFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, gauss, Z, idx_i, idx_j, bank, *W3):
+    def forward(ctx, gauss, Z, idx_i, idx_j, bank, holder):
         gauss = _lib.require(gauss, torch.float32, "gauss")
         Z = _lib.require(Z, torch.int64, "Z")
         idx_i = _lib.require(idx_i, torch.int64, "idx_i")
@@ -120,27 +170,25 @@ class _RadialBankFn(torch.autograd.Function):
         p2 = _batched(h1, bank.W2, bank.b2, G, C, C, torch.empty_like(h1))
         del h1
         h2, m2, r2 = _ln_grouped_fwd(p2, None, None, None, None, None, bank.gamma2, bank.beta2, G, C, bank.eps)
-        outs = []
-        for k in range(G):
-            W, _, b = W3[3 * k:3 * k + 3]
-            outs.append(_gemm(h2[:, k * C:(k + 1) * C], W, b,
-                              torch.empty(E, W.shape[0], device=dev, dtype=torch.float32)))
+        if ctx.needs_input_grad[0]:
+            holder.g = torch.empty_like(p2)
         ctx.save_for_backward(p1, m1, r1, p2, m2, r2, Z, idx_i, idx_j)
-        ctx.bank, ctx.W3 = bank, W3
-        return tuple(outs)
+        ctx.bank, ctx.holder = bank, holder
+        return tuple(h2[:, k * C:(k + 1) * C] for k in range(G))
 
     @staticmethod
-    def backward(ctx, *g_outs):
+    def backward(ctx, *g_views):
         p1, m1, r1, p2, m2, r2, Z, idx_i, idx_j = ctx.saved_tensors
-        bank, W3 = ctx.bank, ctx.W3
+        bank, holder = ctx.bank, ctx.holder
         E, G, C = p1.shape[0], bank.G, bank.C
-        g_h2 = torch.empty_like(p2)
-        for k in range(G):
+        g_h2 = holder.g if holder.g is not None else torch.empty_like(p2)
+        for k, gv in enumerate(g_views):
             sl = g_h2[:, k * C:(k + 1) * C]
-            if g_outs[k] is None:
+            if gv is None:
                 sl.zero_()
-            else:
-                _gemm(g_outs[k].contiguous(), W3[3 * k + 1], None, sl)
+            elif gv.data_ptr() != sl.data_ptr() or gv.stride() != sl.stride():
+                sl.copy_(gv)
+        # holder.g stays with the graph (a retained graph may run its backward again)
         g_p2 = _ln_grouped_bwd(p2, None, None, None, None, None, bank.gamma2, bank.beta2, m2, r2, g_h2, G, C)
         del g_h2
         g_h1 = _batched(g_p2, bank.W2_t, None, G, C, C, torch.empty_like(g_p2))
@@ -149,4 +197,29 @@ class _RadialBankFn(torch.autograd.Function):
                                m1, r1, g_h1, G, C)
         del g_h1
         g_gauss = _gemm(g_p1, bank.W1g_t, None, torch.empty(E, bank.B, device=p1.device, dtype=torch.float32))
-        return (g_gauss, None, None, None, None) + (None,) * len(W3)
+        return g_gauss, None, None, None, None, None
+
+
+class _RadialOutFn(torch.autograd.Function):
+    """Output layer of block k: rad = h2_k W3^T + b3.  Its backward writes g_h2_k straight into
+    the trunk's gradient buffer and returns that slice."""
+
+    @staticmethod
+    def forward(ctx, h2k, W, b, Wt, holder, k, cross):
+        ctx.save_for_backward(Wt)
+        ctx.holder, ctx.k, ctx.cross = holder, k, cross
+        return _gemm(h2k, W, b, torch.empty(h2k.shape[0], W.shape[0], device=h2k.device, dtype=torch.float32))
+
+    @staticmethod
+    def backward(ctx, g_rad):
+        (Wt,) = ctx.saved_tensors
+        g_rad = g_rad.contiguous()
+        if ctx.cross:
+            # produced on the main stream, read here on the side stream
+            g_rad.record_stream(torch.cuda.current_stream())
+        if ctx.holder.g is None:
+            raise _lib.FlashUMAError("radial bank: backward through an output built without input gradients")
+        C = Wt.shape[0]
+        sl = ctx.holder.g[:, ctx.k * C:(ctx.k + 1) * C]
+        _gemm(g_rad, Wt, None, sl)
+        return sl, None, None, None, None, None, None
