@@ -104,6 +104,9 @@ def main() -> None:
     ap.add_argument("--graph", action="store_true",
                     help="time the step captured once in a HIP graph and replayed (captured.py); "
                          "the per-kernel profile is not available then")
+    ap.add_argument("--matmul", choices=["split_bf16", "fp32"], default="split_bf16",
+                    help="matrix-core mode of the fp32 contractions: exact three-way bf16 split with six "
+                         "bf16 MFMA products and fp32 accumulation (default), or fp32 MFMA")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="first copy a 256 MiB buffer (a plain copy kernel of known size, the scale "
                          "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -124,6 +127,8 @@ def main() -> None:
 
     dev = torch.device("cuda:0")
     _lib.load()
+    mm_mode = _lib.MATMUL_SPLIT_BF16 if args.matmul == "split_bf16" else _lib.MATMUL_FP32
+    _lib.set_matmul_mode(mm_mode)
     system, with_stress, wl_name = make_system(args.config)
     model_kw = MODELS.get(args.config, {})
     bb = escn_md.eSCNMDBackbone(seed=0, **model_kw)
@@ -170,7 +175,7 @@ def main() -> None:
     value = system.n_atoms / (elapsed / args.steps)
     log(f"[bench] timed {args.steps} steps: {ms:.3f} ms/step, {value:.1f} atom-steps/s")
 
-    kernels = roofline.summarize(prof.durations()) if prof else {}
+    kernels = roofline.summarize(prof.durations(), mm_mode) if prof else {}
     for rec in kernels.values():
         rec["ms_per_step"] = round(rec["total_ms"] / args.steps, 4)
     rl = None
@@ -179,6 +184,8 @@ def main() -> None:
         d = kernels[dom]
         rl = {"kernel": dom, "bound": d["bound"], "achieved": d["achieved"], "peak": d["peak"], "unit": d["unit"],
               "frac": d["frac"], "traffic": None}
+        if "matrix_op" in d:
+            rl.update(matrix_op=d["matrix_op"], fp32_tflops=d["fp32_tflops"])
         pmc = os.path.join(ROOT, "profiles", "pmc_traffic.json")
         if os.path.exists(pmc):
             with open(pmc) as f:
@@ -201,7 +208,9 @@ def main() -> None:
                                f"(lmax={bb.lmax}, mmax=2, {bb.num_layers} layers, C=128, B=64, cutoff 6, "
                                f"max_neighbors 30)",
                    "atoms": system.n_atoms, "edges": int(ei.shape[1]), "parallelism": "single GPU",
-                   "execution": "hip graph replay" if args.graph else "eager"},
+                   "execution": "hip graph replay" if args.graph else "eager",
+                   "matmul": ("fp32 operands split exactly into three bf16 planes, six bf16 MFMA products, "
+                              "fp32 accumulation" if mm_mode == _lib.MATMUL_SPLIT_BF16 else "fp32 MFMA")},
         "roofline": rl, "cpu_baseline": cpu, "kernels": kernels,
         "energy": round(float(out["energy"].item()), 8),
     }

@@ -1,4 +1,4 @@
-// Complex dense layer on fp32 MFMA with three real products (Gauss's multiplication).
+// Complex dense layer on the matrix cores.
 //
 // The SO(2) m = 1 and m = 2 convolutions of eSCN apply a complex weight R + iI to complex
 // features x_r + i x_i.  The reference packs them into one real GEMM against
@@ -10,19 +10,29 @@
 // formed in registers from the operands already staged in LDS, so no extra memory traffic.
 //
 // Tiling: 256 threads (4 waves, 2 x 2), an output tile of 128 rows x 64 columns of both
-// out_r and out_i; each wave owns 64 x 32 of each of T1, T2, T3 (2 MFMA blocks each, six
-// accumulator chains).  K advances in chunks of 16 through double-buffered LDS with the
-// same XOR-swizzled 64-byte rows as the real GEMM (a_r, a_i: 128 rows; P, Q: 64 rows).  The
-// epilogue stages the outputs through LDS and writes 16-byte row pieces.
-#include "fu_common.h"
+// out_r and out_i; K advances in chunks of 16 through double-buffered LDS.  Two main loops
+// (fu_set_matmul_mode):
+//  * split bf16 (default): a_r, a_i, P and Q are split into three bf16 planes each as they
+//    are staged (split_bf16.h; 36 KB of planes per buffer, two workgroups per CU).  The
+//    three-product form would need planes of a_r + a_i and P + Q as well (54 KB per buffer,
+//    one workgroup per CU), so this loop uses the four products directly,
+//        out_r = a_r P^T + a_i (-Q)^T,  out_i = a_r Q^T + a_i P^T,
+//    with -Q formed by flipping the sign bits of the Q planes in registers; each wave owns
+//    64 x 32 of out_r and out_i (four accumulator chains) and issues 6 x 8 MFMAs per chunk.
+//  * fp32: the three products above on v_mfma_f32_32x32x2_f32; each wave owns 64 x 32 of each
+//    of T1, T2, T3 (six accumulator chains); fp32 LDS rows as in the real GEMM (a_r, a_i: 128
+//    rows; P, Q: 64 rows).
+// The epilogue stages the outputs through LDS and writes 16-byte row pieces.
+#include "split_bf16.h"
 
 namespace fu {
 
-typedef float floatx16 __attribute__((ext_vector_type(16)));
-
 constexpr int CBM = 128, CBN = 64;
 constexpr int CTA = CBM * 16, CTB = CBN * 16;
-constexpr int CBUF = 2 * CTA + 2 * CTB;  // a_r | a_i | P | Q
+constexpr int CBUF = 2 * CTA + 2 * CTB;          // fp32: a_r | a_i | P | Q
+constexpr int CBUF_SPLIT = 6 * CTA + 6 * CTB;    // bf16: a_r, a_i planes (CTA each) | P, Q planes (CTB each)
+constexpr int C_LDS_FLOATS = 2 * CBUF;
+constexpr int C_LDS_FLOATS_SPLIT = CBUF_SPLIT;   // two buffers of bf16 = CBUF_SPLIT floats
 
 __device__ __forceinline__ int clds(int row, int chunk) {
   return row * 16 + 4 * (chunk ^ (((row >> 1) ^ (row >> 2)) & 3));
@@ -47,12 +57,12 @@ struct CGate {
   int64_t ldp;
 };
 
-template <int MODE>
-__global__ __launch_bounds__(256, 3) void complex_linear_kernel(
+template <int MODE, bool SPLIT>
+__global__ __launch_bounds__(256, SPLIT ? 2 : 3) void complex_linear_kernel(
     const float* __restrict__ Ar, const float* __restrict__ Ai, int64_t lda, const float* __restrict__ P,
     const float* __restrict__ Q, int64_t ldw, float* __restrict__ Yr, float* __restrict__ Yi, int64_t ldy,
     int64_t M, int32_t Nc, int32_t Kc, int32_t n_tiles, int64_t total_tiles, CGate g) {
-  __shared__ __attribute__((aligned(16))) float smem[2 * CBUF];
+  __shared__ __attribute__((aligned(16))) float smem[SPLIT ? C_LDS_FLOATS_SPLIT : C_LDS_FLOATS];
   // XCD-aware tile order, as in the real GEMM
   int64_t wg = blockIdx.x;
   if ((total_tiles & 7) == 0) wg = (wg & 7) * (total_tiles >> 3) + (wg >> 3);
@@ -63,86 +73,169 @@ __global__ __launch_bounds__(256, 3) void complex_linear_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wr = (wave >> 1) * 64, wc = (wave & 1) * 32;
 
-  float4 sr[2], si[2], sp, sq;
-  auto load_chunk = [&](int k0) {
+  // split: T[0] = out_r, T[1] = out_i; fp32: T1, T2, T3 of the three-product form
+  constexpr int NT = SPLIT ? 2 : 3;
+  floatx16 T[NT][2];
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int lin = tid + 256 * p, r = lin >> 2, kc = (lin & 3) * 4;
-      const int64_t row = row0 + r;
-      const int gk = k0 + kc;
-      const bool ok = row < M && gk < Kc;
-      sr[p] = ok ? ld4(Ar + row * lda + gk) : make_float4(0.f, 0.f, 0.f, 0.f);
-      si[p] = ok ? ld4(Ai + row * lda + gk) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    const int r = tid >> 2, kc = (tid & 3) * 4;
-    const int gn = col0 + r, gk = k0 + kc;
-    const bool ok = gn < Nc && gk < Kc;
-    sp = ok ? ld4(P + (int64_t)gn * ldw + gk) : make_float4(0.f, 0.f, 0.f, 0.f);
-    sq = ok ? ld4(Q + (int64_t)gn * ldw + gk) : make_float4(0.f, 0.f, 0.f, 0.f);
-  };
-  auto store_chunk = [&](int buf) {
-    float* b = smem + buf * CBUF;
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int lin = tid + 256 * p;
-      st4(&b[clds(lin >> 2, lin & 3)], sr[p]);
-      st4(&b[CTA + clds(lin >> 2, lin & 3)], si[p]);
-    }
-    st4(&b[2 * CTA + clds(tid >> 2, tid & 3)], sp);
-    st4(&b[2 * CTA + CTB + clds(tid >> 2, tid & 3)], sq);
-  };
-
-  floatx16 T[3][2];
-#pragma unroll
-  for (int p = 0; p < 3; ++p)
+  for (int p = 0; p < NT; ++p)
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) T[p][i][r] = 0.0f;
 
   const int fr = lane & 31, fh = lane >> 5;
-  const int nk = (Kc + 15) / 16;
-  load_chunk(0);
-  store_chunk(0);
-  __syncthreads();
-  for (int kc = 0; kc < nk; ++kc) {
-    const int buf = kc & 1;
-    if (kc + 1 < nk) load_chunk((kc + 1) * 16);
-    const float* b = smem + buf * CBUF;
-    float ar[2][8], ai[2][8], pv[8], qv[8];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const float4 vr = ld4(&b[clds(wr + i * 32 + fr, 2 * fh + q)]);
-        const float4 vi = ld4(&b[CTA + clds(wr + i * 32 + fr, 2 * fh + q)]);
-        ar[i][4 * q] = vr.x; ar[i][4 * q + 1] = vr.y; ar[i][4 * q + 2] = vr.z; ar[i][4 * q + 3] = vr.w;
-        ai[i][4 * q] = vi.x; ai[i][4 * q + 1] = vi.y; ai[i][4 * q + 2] = vi.z; ai[i][4 * q + 3] = vi.w;
-      }
-      const float4 vp = ld4(&b[2 * CTA + clds(wc + fr, 2 * fh + q)]);
-      const float4 vq = ld4(&b[2 * CTA + CTB + clds(wc + fr, 2 * fh + q)]);
-      pv[4 * q] = vp.x; pv[4 * q + 1] = vp.y; pv[4 * q + 2] = vp.z; pv[4 * q + 3] = vp.w;
-      qv[4 * q] = vq.x; qv[4 * q + 1] = vq.y; qv[4 * q + 2] = vq.z; qv[4 * q + 3] = vq.w;
-    }
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const float sv = pv[t] + qv[t];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        T[0][i] = __builtin_amdgcn_mfma_f32_32x32x2f32(ar[i][t], pv[t], T[0][i], 0, 0, 0);
-        T[1][i] = __builtin_amdgcn_mfma_f32_32x32x2f32(ai[i][t], qv[t], T[1][i], 0, 0, 0);
-        T[2][i] = __builtin_amdgcn_mfma_f32_32x32x2f32(ar[i][t] + ai[i][t], sv, T[2][i], 0, 0, 0);
-      }
-    }
-    if (kc + 1 < nk) store_chunk(buf ^ 1);
+  if constexpr (SPLIT) {
+    // [buf][a_r hi, mid, lo | a_i hi, mid, lo (CTA each) | P hi, mid, lo | Q hi, mid, lo (CTB each)]
+    __bf16* sp = reinterpret_cast<__bf16*>(smem);
+    const int sr = tid >> 1, sh = tid & 1;                    // a_r, a_i: tile row sr, k 8 sh ..
+    const int bq = tid >> 7, br = (tid & 127) >> 1, bh = tid & 1;  // P (bq 0) or Q (bq 1): row br, k 8 bh ..
+    const int soff_a = plane_off(sr, sh), soff_b = plane_off(br, bh);
+    const float* Bsrc = bq ? Q : P;
+    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 gr[2], gi[2], gb[2];
+    // unconditional 16-byte loads; pieces outside an operand read its first float4 and are zeroed
+    auto load_chunk = [&](int k0) {
+      const int64_t row = row0 + sr;
+      const int gk = k0 + 8 * sh;
+      const bool a0 = row < M && gk < Kc, a1 = row < M && gk + 4 < Kc;
+      const int64_t ao = row * lda + gk;
+      const float4 r0 = ld4(a0 ? Ar + ao : Ar), r1 = ld4(a1 ? Ar + ao + 4 : Ar);
+      const float4 i0 = ld4(a0 ? Ai + ao : Ai), i1 = ld4(a1 ? Ai + ao + 4 : Ai);
+      const int gn = col0 + br, gkb = k0 + 8 * bh;
+      const bool b0 = gn < Nc && gkb < Kc, b1 = gn < Nc && gkb + 4 < Kc;
+      const int64_t bo = (int64_t)gn * ldw + gkb;
+      const float4 w0 = ld4(b0 ? Bsrc + bo : Bsrc), w1 = ld4(b1 ? Bsrc + bo + 4 : Bsrc);
+      gr[0] = a0 ? r0 : z4;
+      gr[1] = a1 ? r1 : z4;
+      gi[0] = a0 ? i0 : z4;
+      gi[1] = a1 ? i1 : z4;
+      gb[0] = b0 ? w0 : z4;
+      gb[1] = b1 ? w1 : z4;
+    };
+    auto store_chunk = [&](int buf) {
+      __bf16* b = sp + buf * CBUF_SPLIT;
+      uint4 h, m, l;
+      split3(gr[0], gr[1], h, m, l);
+      st_planes(b, CTA, soff_a, h, m, l);
+      split3(gi[0], gi[1], h, m, l);
+      st_planes(b + 3 * CTA, CTA, soff_a, h, m, l);
+      split3(gb[0], gb[1], h, m, l);
+      st_planes(b + 6 * CTA + bq * 3 * CTB, CTB, soff_b, h, m, l);
+    };
+    const int nk = (Kc + 15) / 16;
+    load_chunk(0);
+    store_chunk(0);
+    load_chunk((nk > 1 ? 1 : 0) * 16);
     __syncthreads();
+    for (int kc = 0; kc < nk; ++kc) {
+      const __bf16* b = sp + (kc & 1) * CBUF_SPLIT;
+      bf16x8 pf[3], qf[3], nqf[3];
+      ld_planes(b + 6 * CTA, CTB, plane_off(wc + fr, fh), pf);
+      ld_planes(b + 6 * CTA + 3 * CTB, CTB, plane_off(wc + fr, fh), qf);
+#pragma unroll
+      for (int p = 0; p < 3; ++p) {
+        uint4 u = __builtin_bit_cast(uint4, qf[p]);
+        u.x ^= 0x80008000u; u.y ^= 0x80008000u; u.z ^= 0x80008000u; u.w ^= 0x80008000u;
+        nqf[p] = __builtin_bit_cast(bf16x8, u);
+      }
+      bf16x8 arf[2][3], aif[2][3];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        ld_planes(b, CTA, plane_off(wr + 32 * i + fr, fh), arf[i]);
+        ld_planes(b + 3 * CTA, CTA, plane_off(wr + 32 * i + fr, fh), aif[i]);
+      }
+#pragma unroll
+      for (int q = 0; q < 6; ++q) {
+        const int pa = kSplitA[q], pb = kSplitB[q];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          T[0][i] = mfma_bf16(arf[i][pa], pf[pb], T[0][i]);
+          T[1][i] = mfma_bf16(arf[i][pa], qf[pb], T[1][i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          T[0][i] = mfma_bf16(aif[i][pa], nqf[pb], T[0][i]);
+          T[1][i] = mfma_bf16(aif[i][pa], pf[pb], T[1][i]);
+        }
+      }
+      store_chunk((kc & 1) ^ 1);
+      load_chunk((kc + 2 < nk ? kc + 2 : nk - 1) * 16);
+      __syncthreads();
+    }
+  } else {
+    float4 sr[2], si[2], sp, sq;
+    auto load_chunk = [&](int k0) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int lin = tid + 256 * p, r = lin >> 2, kc = (lin & 3) * 4;
+        const int64_t row = row0 + r;
+        const int gk = k0 + kc;
+        const bool ok = row < M && gk < Kc;
+        sr[p] = ok ? ld4(Ar + row * lda + gk) : make_float4(0.f, 0.f, 0.f, 0.f);
+        si[p] = ok ? ld4(Ai + row * lda + gk) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      const int r = tid >> 2, kc = (tid & 3) * 4;
+      const int gn = col0 + r, gk = k0 + kc;
+      const bool ok = gn < Nc && gk < Kc;
+      sp = ok ? ld4(P + (int64_t)gn * ldw + gk) : make_float4(0.f, 0.f, 0.f, 0.f);
+      sq = ok ? ld4(Q + (int64_t)gn * ldw + gk) : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    auto store_chunk = [&](int buf) {
+      float* b = smem + buf * CBUF;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int lin = tid + 256 * p;
+        st4(&b[clds(lin >> 2, lin & 3)], sr[p]);
+        st4(&b[CTA + clds(lin >> 2, lin & 3)], si[p]);
+      }
+      st4(&b[2 * CTA + clds(tid >> 2, tid & 3)], sp);
+      st4(&b[2 * CTA + CTB + clds(tid >> 2, tid & 3)], sq);
+    };
+
+    const int nk = (Kc + 15) / 16;
+    load_chunk(0);
+    store_chunk(0);
+    __syncthreads();
+    for (int kc = 0; kc < nk; ++kc) {
+      const int buf = kc & 1;
+      if (kc + 1 < nk) load_chunk((kc + 1) * 16);
+      const float* b = smem + buf * CBUF;
+      float ar[2][8], ai[2][8], pv[8], qv[8];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const float4 vr = ld4(&b[clds(wr + i * 32 + fr, 2 * fh + q)]);
+          const float4 vi = ld4(&b[CTA + clds(wr + i * 32 + fr, 2 * fh + q)]);
+          ar[i][4 * q] = vr.x; ar[i][4 * q + 1] = vr.y; ar[i][4 * q + 2] = vr.z; ar[i][4 * q + 3] = vr.w;
+          ai[i][4 * q] = vi.x; ai[i][4 * q + 1] = vi.y; ai[i][4 * q + 2] = vi.z; ai[i][4 * q + 3] = vi.w;
+        }
+        const float4 vp = ld4(&b[2 * CTA + clds(wc + fr, 2 * fh + q)]);
+        const float4 vq = ld4(&b[2 * CTA + CTB + clds(wc + fr, 2 * fh + q)]);
+        pv[4 * q] = vp.x; pv[4 * q + 1] = vp.y; pv[4 * q + 2] = vp.z; pv[4 * q + 3] = vp.w;
+        qv[4 * q] = vq.x; qv[4 * q + 1] = vq.y; qv[4 * q + 2] = vq.z; qv[4 * q + 3] = vq.w;
+      }
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const float sv = pv[t] + qv[t];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          T[0][i] = __builtin_amdgcn_mfma_f32_32x32x2f32(ar[i][t], pv[t], T[0][i], 0, 0, 0);
+          T[1][i] = __builtin_amdgcn_mfma_f32_32x32x2f32(ai[i][t], qv[t], T[1][i], 0, 0, 0);
+          T[2][i] = __builtin_amdgcn_mfma_f32_32x32x2f32(ar[i][t] + ai[i][t], sv, T[2][i], 0, 0, 0);
+        }
+      }
+      if (kc + 1 < nk) store_chunk(buf ^ 1);
+      __syncthreads();
+    }
   }
 
   // Accumulator layout of the 32x32 MFMA: lane l, register r -> column l % 32, row
   // 8 (r / 4) + 4 (l / 32) + r % 4.  Each wave stages a 32-row slab of [out_r | out_i] (32 + 32
   // columns) in LDS and writes it back as 16-byte row pieces (plus the gated copies).
   constexpr int CES = 64 + 8;
-  static_assert(4 * 32 * CES <= 2 * CBUF, "epilogue staging must fit in the operand buffers");
+  static_assert(4 * 32 * CES <= C_LDS_FLOATS && 4 * 32 * CES <= C_LDS_FLOATS_SPLIT,
+                "epilogue staging must fit in the operand buffers");
   float* ws = smem + wave * 32 * CES;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -151,8 +244,13 @@ __global__ __launch_bounds__(256, 3) void complex_linear_kernel(
     for (int r = 0; r < 16; ++r) {
       const int rr = 8 * (r >> 2) + 4 * fh + (r & 3);
       const float t1 = T[0][i][r], t2 = T[1][i][r];
-      ws[rr * CES + fr] = t1 - t2;
-      ws[rr * CES + 32 + fr] = T[2][i][r] - t1 - t2;
+      if constexpr (SPLIT) {
+        ws[rr * CES + fr] = t1;
+        ws[rr * CES + 32 + fr] = t2;
+      } else {
+        ws[rr * CES + fr] = t1 - t2;
+        ws[rr * CES + 32 + fr] = T[NT - 1][i][r] - t1 - t2;
+      }
     }
     __syncthreads();
 #pragma unroll
@@ -209,8 +307,9 @@ static int complex_launch(const float* A_r, const float* A_i, int64_t lda, const
                           void* stream, const char* who) {
   const int n_tiles = (Nc + CBN - 1) / CBN;
   const int64_t total = ((M + CBM - 1) / CBM) * n_tiles;
-  hipLaunchKernelGGL((complex_linear_kernel<MODE>), dim3((unsigned)total), dim3(256), 0, as_stream(stream), A_r, A_i,
-                     lda, P, Q, ldw, Y_r, Y_i, ldy, M, Nc, Kc, n_tiles, total, g);
+  auto kern = matmul_mode() == FU_MATMUL_FP32 ? complex_linear_kernel<MODE, false> : complex_linear_kernel<MODE, true>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(256), 0, as_stream(stream), A_r, A_i, lda, P, Q, ldw, Y_r, Y_i,
+                     ldy, M, Nc, Kc, n_tiles, total, g);
   return check_launch(who);
 }
 

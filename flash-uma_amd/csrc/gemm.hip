@@ -1,4 +1,4 @@
-// Dense fp32 contractions on the gfx950 matrix cores (v_mfma_f32_32x32x2_f32).
+// Dense fp32 contractions on the gfx950 matrix cores.
 //
 // Y[M, N] = A[M, K] @ W[N, K]^T (+ bias[N]).  Both operands are K-contiguous, so one kernel
 // serves the SO(2) conv1/conv2 forward (W = packed weight, model.py:152,154), the radial-MLP
@@ -7,24 +7,31 @@
 //
 // Tiling: a 256-thread workgroup (4 wave64s in a 2x2 grid) owns a 128x128 output tile; each
 // wave owns 64x64 = 2x2 MFMA blocks of 32x32 (64 fp32 accumulators per lane, in VGPRs).
-// K advances in chunks of 16 staged through double-buffered LDS (32 KB of operands, 36 KB with
-// the epilogue staging: four workgroups per CU).  Within a chunk, lane l (row/col l%32, half h = l/32) feeds the MFMA k-slot h with
-// chunk column 8h + t at step t, so each lane reads its 8 operands of a chunk with two
-// 16-byte LDS reads.  LDS rows are 64 bytes (four 16-byte chunks) without padding; the chunk
-// index is XOR-swizzled with f(row) = ((row >> 1) ^ (row >> 2)) & 3, which makes both the
-// row-wise tile stores and the column-of-rows operand reads free of bank conflicts (for 32
-// and for 64 banks).  The epilogue stages each wave's 32-row slabs through LDS and writes
-// bias-added rows with 16-byte stores.
-#include "fu_common.h"
+// K advances in chunks of 16 staged through double-buffered LDS.  Two main loops share the
+// tiling and the epilogues (fu_set_matmul_mode):
+//  * split bf16 (default): each staged fp32 element is split into three bf16 planes
+//    (split_bf16.h) as it is written to LDS (48 KB of planes, two workgroups per CU); per chunk
+//    a wave reads 3 planes of each operand fragment and issues six v_mfma_f32_32x32x16_bf16
+//    per 32x32 block.  The loop body has no branches (the last prefetch re-reads the last
+//    chunk), so the compiler interleaves the next chunk's split with this chunk's MFMAs.
+//  * fp32: v_mfma_f32_32x32x2_f32, lane l (row/col l%32, half h = l/32) feeding k-slot h with
+//    chunk column 8h + t at step t; fp32 LDS rows of 64 bytes (four 16-byte chunks) without
+//    padding, the chunk index XOR-swizzled with f(row) = ((row >> 1) ^ (row >> 2)) & 3, so
+//    the row-wise tile stores and the column-of-rows operand reads are free of bank
+//    conflicts (32 KB of operands, 36 KB with the epilogue staging: four workgroups per CU).
+// The epilogue stages each wave's 32-row slabs through LDS and writes rows with 16-byte stores.
+#include "split_bf16.h"
 
 namespace fu {
-
-typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int GBM = 128, GBN = 128, GBK = 16;
 constexpr int GLDS = GBK;          // LDS operand row (floats): four swizzled 16-byte chunks
 constexpr int GES = 64 + 8;        // LDS epilogue row (floats); 4 * GES = 32 mod 64 banks
 constexpr int G_LDS_FLOATS = 2 * (GBM + GBN) * GLDS > 4 * 32 * GES ? 2 * (GBM + GBN) * GLDS : 4 * 32 * GES;
+constexpr int G_PLANE = GBM * GBK;                       // bf16 per split plane of one tile
+constexpr int G_LDS_FLOATS_SPLIT = 2 * 6 * G_PLANE / 2;  // [buf][A planes | W planes], 48 KB
+static_assert(GBM == GBN, "the split planes of A and W tiles share one layout");
+static_assert(4 * 32 * GES <= G_LDS_FLOATS_SPLIT, "epilogue staging must fit in the split planes");
 
 // Float offset of 16-byte chunk `chunk` of LDS operand row `row`.
 __device__ __forceinline__ int lds_chunk(int row, int chunk) {
@@ -69,8 +76,8 @@ struct GateBwd {
 // wave's 64 staged columns are a gate and its values; the epilogue writes Y (kept for the
 // backward), Z and S.  MODE 2 (gate backward): see GateBwd; Y receives g_Y_m0 ((2L+1)C
 // columns).
-template <int MODE>
-__global__ __launch_bounds__(256, 4) void linear_mfma_kernel(const float* __restrict__ A, int64_t lda, int64_t sA,
+template <int MODE, bool SPLIT>
+__global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const float* __restrict__ A, int64_t lda, int64_t sA,
                                                           const float* __restrict__ W, int64_t ldw, int64_t sW,
                                                           const float* __restrict__ bias, int64_t sBias,
                                                           int32_t bias_batches, float* __restrict__ Y, int64_t ldy,
@@ -84,9 +91,7 @@ __global__ __launch_bounds__(256, 4) void linear_mfma_kernel(const float* __rest
     Y += bt * sY;
     bias = (bias != nullptr && bt < bias_batches) ? bias + bt * sBias : nullptr;
   }
-  __shared__ __attribute__((aligned(16))) float smem[G_LDS_FLOATS];
-  float* As = smem;                      // [2][GBM][GLDS]
-  float* Bs = smem + 2 * GBM * GLDS;     // [2][GBN][GLDS]
+  __shared__ __attribute__((aligned(16))) float smem[SPLIT ? G_LDS_FLOATS_SPLIT : G_LDS_FLOATS];
 
   // XCD-aware tile order: hardware deals consecutive workgroups round-robin over the 8 XCDs;
   // remap so that each XCD walks a contiguous range of tiles (the column tiles of one A
@@ -104,32 +109,6 @@ __global__ __launch_bounds__(256, 4) void linear_mfma_kernel(const float* __rest
   const int wr = (wave >> 1) * 64;  // wave's row offset inside the tile
   const int wc = (wave & 1) * 64;   // wave's col offset inside the tile
 
-  // Global -> register staging: 2 float4 of A and 2 float4 of W per thread per chunk
-  // (4 threads cover the 16 floats of one row).
-  float4 ra[2], rb[2];
-  auto load_chunk = [&](int k0) {
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int lin = tid + 256 * p;
-      const int r = lin >> 2;
-      const int kc = (lin & 3) * 4;
-      const int64_t gr = row0 + r;
-      const int gk = k0 + kc;
-      ra[p] = (gr < M && gk < K) ? ld4(A + gr * lda + gk) : make_float4(0.f, 0.f, 0.f, 0.f);
-      const int gn = col0 + r;
-      rb[p] = (gn < N && gk < K) ? ld4(W + (int64_t)gn * ldw + gk) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-  };
-  auto store_chunk = [&](int buf) {
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int lin = tid + 256 * p;
-      const int r = lin >> 2;
-      st4(&As[buf * GBM * GLDS + lds_chunk(r, lin & 3)], ra[p]);
-      st4(&Bs[buf * GBN * GLDS + lds_chunk(r, lin & 3)], rb[p]);
-    }
-  };
-
   floatx16 acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -137,41 +116,122 @@ __global__ __launch_bounds__(256, 4) void linear_mfma_kernel(const float* __rest
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  const int nk = (K + GBK - 1) / GBK;
-  load_chunk(0);
-  store_chunk(0);
-  __syncthreads();
-
-  const int fr = lane & 31;         // operand row (A) / column (W) within a 32-block
-  const int fh = lane >> 5;         // this lane feeds chunk columns 8 fh .. 8 fh + 7
-
-  for (int kc = 0; kc < nk; ++kc) {
-    const int buf = kc & 1;
-    if (kc + 1 < nk) load_chunk((kc + 1) * GBK);
-
-    float af[2][8], bf[2][8];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const float4 va = ld4(&As[buf * GBM * GLDS + lds_chunk(wr + i * 32 + fr, 2 * fh + q)]);
-        const float4 vb = ld4(&Bs[buf * GBN * GLDS + lds_chunk(wc + i * 32 + fr, 2 * fh + q)]);
-        af[i][4 * q + 0] = va.x; af[i][4 * q + 1] = va.y; af[i][4 * q + 2] = va.z; af[i][4 * q + 3] = va.w;
-        bf[i][4 * q + 0] = vb.x; bf[i][4 * q + 1] = vb.y; bf[i][4 * q + 2] = vb.z; bf[i][4 * q + 3] = vb.w;
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][t], bf[j][t], acc[i][j], 0, 0, 0);
-    }
-
-    if (kc + 1 < nk) store_chunk(buf ^ 1);
+  const int fr = lane & 31;  // operand row (A) / column (W) within a 32-block
+  const int fh = lane >> 5;  // this lane feeds chunk columns 8 fh .. 8 fh + 7
+  if constexpr (SPLIT) {
+    __bf16* sp = reinterpret_cast<__bf16*>(smem);  // [buf][A hi, mid, lo | W hi, mid, lo][G_PLANE]
+    const int sr = tid >> 1, sh = tid & 1;         // staging: tile row sr, k 8 sh .. 8 sh + 7
+    const int soff = plane_off(sr, sh);
+    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 ga[2], gw[2];
+    // Every lane issues its four 16-byte loads unconditionally (guarded loads would be
+    // scalarised into dword loads); a piece outside the operand reads the operand's first
+    // float4 instead and is replaced by zeros.
+    auto load_chunk = [&](int k0) {
+      const int64_t gr = row0 + sr;
+      const int gn = col0 + sr;
+      const int gk = k0 + 8 * sh;
+      const bool a0 = gr < M && gk < K, a1 = gr < M && gk + 4 < K;
+      const bool w0 = gn < N && gk < K, w1 = gn < N && gk + 4 < K;
+      const float4 va0 = ld4(a0 ? A + gr * lda + gk : A), va1 = ld4(a1 ? A + gr * lda + gk + 4 : A);
+      const float4 vw0 = ld4(w0 ? W + (int64_t)gn * ldw + gk : W), vw1 = ld4(w1 ? W + (int64_t)gn * ldw + gk + 4 : W);
+      ga[0] = a0 ? va0 : z4;
+      ga[1] = a1 ? va1 : z4;
+      gw[0] = w0 ? vw0 : z4;
+      gw[1] = w1 ? vw1 : z4;
+    };
+    auto store_chunk = [&](int buf) {
+      __bf16* b = sp + buf * 6 * G_PLANE;
+      uint4 h, m, l;
+      split3(ga[0], ga[1], h, m, l);
+      st_planes(b, G_PLANE, soff, h, m, l);
+      split3(gw[0], gw[1], h, m, l);
+      st_planes(b + 3 * G_PLANE, G_PLANE, soff, h, m, l);
+    };
+    const int nk = (K + GBK - 1) / GBK;
+    load_chunk(0);
+    store_chunk(0);
+    load_chunk((nk > 1 ? 1 : 0) * GBK);
     __syncthreads();
+    for (int kc = 0; kc < nk; ++kc) {
+      const __bf16* b = sp + (kc & 1) * 6 * G_PLANE;
+      bf16x8 bq[2][3];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) ld_planes(b + 3 * G_PLANE, G_PLANE, plane_off(wc + 32 * j + fr, fh), bq[j]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        bf16x8 aq[3];
+        ld_planes(b, G_PLANE, plane_off(wr + 32 * i + fr, fh), aq);
+#pragma unroll
+        for (int q = 0; q < 6; ++q)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16(aq[kSplitA[q]], bq[j][kSplitB[q]], acc[i][j]);
+      }
+      // chunk kc + 1 (loaded during the previous iteration) into the other buffer, whose last
+      // readers finished before the previous barrier; then prefetch chunk kc + 2
+      store_chunk((kc & 1) ^ 1);
+      load_chunk((kc + 2 < nk ? kc + 2 : nk - 1) * GBK);
+      __syncthreads();
+    }
+  } else {
+    // Global -> register staging: 2 float4 of A and 2 float4 of W per thread per chunk
+    // (4 threads cover the 16 floats of one row).
+    float* As = smem;                      // [2][GBM][GLDS]
+    float* Bs = smem + 2 * GBM * GLDS;     // [2][GBN][GLDS]
+    float4 ra[2], rb[2];
+    auto load_chunk = [&](int k0) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int lin = tid + 256 * p;
+        const int r = lin >> 2;
+        const int kc = (lin & 3) * 4;
+        const int64_t gr = row0 + r;
+        const int gk = k0 + kc;
+        ra[p] = (gr < M && gk < K) ? ld4(A + gr * lda + gk) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int gn = col0 + r;
+        rb[p] = (gn < N && gk < K) ? ld4(W + (int64_t)gn * ldw + gk) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    };
+    auto store_chunk = [&](int buf) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int lin = tid + 256 * p;
+        const int r = lin >> 2;
+        st4(&As[buf * GBM * GLDS + lds_chunk(r, lin & 3)], ra[p]);
+        st4(&Bs[buf * GBN * GLDS + lds_chunk(r, lin & 3)], rb[p]);
+      }
+    };
+    const int nk = (K + GBK - 1) / GBK;
+    load_chunk(0);
+    store_chunk(0);
+    __syncthreads();
+    for (int kc = 0; kc < nk; ++kc) {
+      const int buf = kc & 1;
+      if (kc + 1 < nk) load_chunk((kc + 1) * GBK);
+
+      float af[2][8], bf[2][8];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const float4 va = ld4(&As[buf * GBM * GLDS + lds_chunk(wr + i * 32 + fr, 2 * fh + q)]);
+          const float4 vb = ld4(&Bs[buf * GBN * GLDS + lds_chunk(wc + i * 32 + fr, 2 * fh + q)]);
+          af[i][4 * q + 0] = va.x; af[i][4 * q + 1] = va.y; af[i][4 * q + 2] = va.z; af[i][4 * q + 3] = va.w;
+          bf[i][4 * q + 0] = vb.x; bf[i][4 * q + 1] = vb.y; bf[i][4 * q + 2] = vb.z; bf[i][4 * q + 3] = vb.w;
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][t], bf[j][t], acc[i][j], 0, 0, 0);
+      }
+
+      if (kc + 1 < nk) store_chunk(buf ^ 1);
+      __syncthreads();
+    }
   }
 
   // Accumulator layout of the 32x32 MFMA: lane l, register r -> column l%32,
@@ -336,9 +396,9 @@ static int linear_launch(const float* A, int64_t lda, int64_t sA, const float* W
   const int64_t m_tiles = (M + GBM - 1) / GBM;
   const int64_t total = m_tiles * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
-  hipLaunchKernelGGL((linear_mfma_kernel<0>), dim3((unsigned)total, (unsigned)batch), dim3(256), 0, stream, A, lda,
-                     sA, W, ldw, sW, bias, sBias, bias_batches, Y, ldy, sY, M, N, K, n_tiles, total, GateOut{},
-                     GateBwd{});
+  auto kern = matmul_mode() == FU_MATMUL_FP32 ? linear_mfma_kernel<0, false> : linear_mfma_kernel<0, true>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)total, (unsigned)batch), dim3(256), 0, stream, A, lda, sA, W, ldw, sW, bias,
+                     sBias, bias_batches, Y, ldy, sY, M, N, K, n_tiles, total, GateOut{}, GateBwd{});
   return check_launch(who);
 }
 
@@ -381,7 +441,8 @@ extern "C" int fu_linear_gate(const float* A, int64_t lda, const float* W, int64
   const int n_tiles = (N + GBN - 1) / GBN;
   const int64_t total = ((M + GBM - 1) / GBM) * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
-  hipLaunchKernelGGL((linear_mfma_kernel<1>), dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), A, lda,
+  auto kern = matmul_mode() == FU_MATMUL_FP32 ? linear_mfma_kernel<1, false> : linear_mfma_kernel<1, true>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), A, lda,
                      (int64_t)0, W, ldw, (int64_t)0, bias, (int64_t)0, 1, Y, ldy, (int64_t)0, M, N, K, n_tiles, total,
                      GateOut{Z, ldz, S, lds, C, lmax}, GateBwd{});
   return check_launch(who);
@@ -408,7 +469,8 @@ extern "C" int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* W
   const int n_tiles = (N + GBN - 1) / GBN;
   const int64_t total = ((M + GBM - 1) / GBM) * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
-  hipLaunchKernelGGL((linear_mfma_kernel<2>), dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), gZo, ldgz,
+  auto kern = matmul_mode() == FU_MATMUL_FP32 ? linear_mfma_kernel<2, false> : linear_mfma_kernel<2, true>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), gZo, ldgz,
                      (int64_t)0, Wt, ldw, (int64_t)0, (const float*)nullptr, (int64_t)0, 1, gY0, ldg, (int64_t)0, M, N,
                      K, n_tiles, total, GateOut{}, GateBwd{Y0, ldy0, S, lds, P1, ldp1, P2, ldp2, C, lmax});
   return check_launch(who);

@@ -6,6 +6,7 @@ if the library is missing, or the tensors are not on a ROCm device, the call rai
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 from pathlib import Path
@@ -25,6 +26,8 @@ SZ_P = ctypes.POINTER(ctypes.c_size_t)
 SIGNATURES: dict[str, list] = {
     "fu_version": [],
     "fu_last_error": [],
+    "fu_set_matmul_mode": [I32],
+    "fu_matmul_mode": [],
     "fu_geom_fwd": [P, P, P, P, P, P, P, P, P, I64, P, P, I64, I64, I32, I32, F32, F32, P],
     "fu_geom_bwd": [P, P, P, P, P, P, I64, P, P, P, I64, I64, I32, F32, F32, P],
     "fu_edge_vec_reduce": [P, P, P, P, P, P, I64, I64, P],
@@ -155,6 +158,31 @@ def call(name: str, *args) -> None:
     if status != 0:
         msg = lib.fu_last_error().decode(errors="replace")
         raise FlashUMAError(f"{name} failed with status {status}: {msg}")
+
+
+MATMUL_SPLIT_BF16 = 0  # fp32 operands split exactly into three bf16 planes, six MFMA products
+MATMUL_FP32 = 1        # v_mfma_f32_32x32x2_f32
+
+
+def get_matmul_mode() -> int:
+    """Matrix-core mode of the library's fp32 contractions (MATMUL_SPLIT_BF16 or MATMUL_FP32)."""
+    return load().fu_matmul_mode()
+
+
+def set_matmul_mode(mode: int) -> None:
+    """Select the matrix-core mode of every later fp32 contraction (process-wide)."""
+    call("fu_set_matmul_mode", int(mode))
+
+
+@contextlib.contextmanager
+def matmul_mode(mode: int):
+    """Run the enclosed launches in matrix-core `mode`; restores the previous mode after."""
+    prev = get_matmul_mode()
+    set_matmul_mode(mode)
+    try:
+        yield
+    finally:
+        set_matmul_mode(prev)
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

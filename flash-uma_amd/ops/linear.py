@@ -46,7 +46,7 @@ def linear(x: torch.Tensor, W: torch.Tensor, bias: torch.Tensor | None, Wt: torc
 
 def complex_gemm(x: torch.Tensor, P: torch.Tensor, Q: torch.Tensor) -> torch.Tensor:
     """[y_r | y_i] = complex product of x = [x_r | x_i] (M, 2 Kc) with (P + iQ)^T, P, Q (Nc, Kc):
-    y_r = x_r P^T - x_i Q^T, y_i = x_r Q^T + x_i P^T (three real MFMA products)."""
+    y_r = x_r P^T - x_i Q^T, y_i = x_r Q^T + x_i P^T (fu_complex_linear)."""
     if x.stride(-1) != 1:
         x = x.contiguous()
     M = x.shape[0]

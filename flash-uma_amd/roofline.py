@@ -6,6 +6,12 @@ GEMMs count 2*M*N*K flops; the complex layer counts the 6*M*Nc*Kc flops of its t
 products.  These are the denominators of the roofline fractions:
 achieved = algorithmic bytes (flops) / measured kernel time.
 
+Matrix-core kernels run in one of two modes (fu_set_matmul_mode).  fp32 mode executes the
+fp32 flops on v_mfma_f32_32x32x2_f32 (peak 157.3 TFLOP/s).  The default split mode executes
+each fp32 product as six bf16 products of the operands' exact three-way bf16 splits, so the
+matrix cores execute 6x the fp32 flops at the dense bf16 peak (2.5 PFLOP/s); its roofline
+is that executed bf16 work against 2.5 PFLOP/s, with the fp32-equivalent rate alongside.
+
 Per-unit figures at C = 128, B = 64 (bytes per edge + bytes per node):
   gating fwd 10240 / bwd 15872; gather fwd 15512 + 4616, bwd 21784 + 9232;
   scatter fwd 4752 + 9220, bwd 9504 + 4608; init scatter fwd 1576 + 5640, bwd 3256 + 4608;
@@ -16,6 +22,9 @@ from __future__ import annotations
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix
+SPLIT_PRODUCTS = 6              # bf16 products per fp32 product in the split mode
+MATMUL_SPLIT_BF16, MATMUL_FP32 = 0, 1
 
 
 def _gating_fwd(a):
@@ -238,9 +247,9 @@ MFMA_BOUND = {"fu_linear", "fu_linear_batched", "fu_complex_linear", "fu_linear_
               "fu_linear_gate_bwd", "fu_complex_linear_gate_bwd"}
 
 
-def summarize(durations) -> dict:
+def summarize(durations, matmul_mode: int = MATMUL_SPLIT_BF16) -> dict:
     """Per entry point: calls, total/avg ms, algorithmic bytes/flops per launch and the
-    achieved fraction of the bounding roofline."""
+    achieved fraction of the bounding roofline (matrix-core kernels in `matmul_mode`)."""
     agg: dict = {}
     for name, args, ms in durations:
         if name not in WORK:
@@ -256,9 +265,13 @@ def summarize(durations) -> dict:
         sec = a["ms"] / 1e3
         rec = {"calls": a["calls"], "total_ms": round(a["ms"], 4), "avg_us": round(1e3 * a["ms"] / a["calls"], 2)}
         if name in MFMA_BOUND:
-            ach = a["flops"] / sec / 1e12 if sec > 0 else 0.0
-            rec.update(bound="mfma", unit="TFLOP/s", achieved=round(ach, 2), peak=FP32_MFMA_PEAK_TFLOPS,
-                       frac=round(ach / FP32_MFMA_PEAK_TFLOPS, 4), flops_per_launch=a["flops"] // a["calls"],
+            fp32_rate = a["flops"] / sec / 1e12 if sec > 0 else 0.0
+            if matmul_mode == MATMUL_FP32:
+                ach, peak, op = fp32_rate, FP32_MFMA_PEAK_TFLOPS, "fp32 mfma"
+            else:
+                ach, peak, op = SPLIT_PRODUCTS * fp32_rate, BF16_MFMA_PEAK_TFLOPS, "bf16 mfma, 6 products per fp32 product"
+            rec.update(bound="mfma", unit="TFLOP/s", achieved=round(ach, 2), peak=peak, frac=round(ach / peak, 4),
+                       matrix_op=op, fp32_tflops=round(fp32_rate, 2), flops_per_launch=a["flops"] // a["calls"],
                        hbm_gbs=round(a["bytes"] / sec / 1e9, 1) if sec > 0 else 0.0)
         else:
             ach = a["bytes"] / sec / 1e9 if sec > 0 else 0.0

@@ -44,6 +44,18 @@ int fu_version(void);
 /* Message of the last error returned on the calling host thread ("" if none). */
 const char* fu_last_error(void);
 
+/* Matrix-core mode of every fp32 contraction (fu_linear*, fu_complex_linear*); no reference
+ * counterpart (the reference's dense layers are cuBLAS fp32 GEMMs with TF32 off, model.py:152,154,
+ * reached through torch.nn.functional.linear).
+ *   0 (default): each fp32 operand is split exactly into three bf16 planes (x = hi + mid + lo)
+ *      and the six significant partial products run on v_mfma_f32_32x32x16_bf16 with fp32
+ *      accumulation; error against fp64 at or below that of the fp32 MFMA.
+ *   1: v_mfma_f32_32x32x2_f32.
+ * The mode is process-wide and read at each launch; switch it only between launches.
+ * fu_set_matmul_mode returns FU_OK or FU_ERR_UNSUPPORTED; fu_matmul_mode returns the mode. */
+int fu_set_matmul_mode(int32_t mode);
+int fu_matmul_mode(void);
+
 /* ------------------------------------------------------------------------------------
  * Geometry (replaces PrecomputeGeometry, ops/geom.py:496-589)
  * ------------------------------------------------------------------------------------ */

@@ -142,8 +142,17 @@ def test_ln_silu(cuda):
     assert_close(g, gref, 1e-4, "ln_silu bwd")
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 128, 64), (300, 640, 768), (257, 64, 128), (1000, 384, 384), (77, 1536, 128)])
-def test_linear(cuda, M, N, K):
+@pytest.fixture(params=[0, 1], ids=["split_bf16", "fp32"])
+def matmul_mode(request, cuda):
+    """Both matrix-core modes of the fp32 contractions (fu_set_matmul_mode)."""
+    from ops import _lib
+    with _lib.matmul_mode(request.param):
+        yield request.param
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 128, 64), (300, 640, 768), (257, 64, 128), (1000, 384, 384), (77, 1536, 128),
+                                   (130, 68, 36)])
+def test_linear(cuda, matmul_mode, M, N, K):
     *_, linear, _ = _ops()
     torch.manual_seed(M + N + K)
     x = torch.randn(M, K)
@@ -160,7 +169,7 @@ def test_linear(cuda, M, N, K):
 
 
 @pytest.mark.parametrize("M,Kc,Nc", [(300, 512, 256), (257, 128, 256), (1, 96, 64), (1000, 128, 128)])
-def test_complex_linear(cuda, M, Kc, Nc):
+def test_complex_linear(cuda, matmul_mode, M, Kc, Nc):
     """The three-product complex layer against the reference's packed real GEMM
     x @ [[R, -I], [I, R]]^T (oracle pack_so2) in float64, forward and input gradient."""
     from ops.linear import complex_linear
@@ -177,6 +186,66 @@ def test_complex_linear(cuda, M, Kc, Nc):
     assert_close(y, ref, TOL, "complex linear fwd")
     (gx,) = torch.autograd.grad(y, xg, cot.to(cuda))
     assert_close(gx, gref, TOL, "complex linear bwd")
+
+
+@pytest.mark.parametrize("N,K", [(640, 768), (384, 384)])
+def test_split_gemm_accuracy(cuda, N, K):
+    """The split-bf16 product (x = hi + mid + lo exactly; six of the nine partial products) is
+    an fp32-accurate GEMM: on an SO(2) layer shape its error against float64 is at most that
+    of the fp32 MFMA on the same inputs (rms within 10 %, max within 50 %), and well inside the
+    fp32 class (rms-relative 1e-6); dropping a plane (a two-term split) would give ~4e-6."""
+    from ops import _lib
+    *_, linear, _ = _ops()
+    g = torch.Generator().manual_seed(N + K)
+    M = 16384
+    x = torch.randn(M, K, generator=g).to(cuda)
+    W = (torch.randn(N, K, generator=g) / K ** 0.5).to(cuda)
+    ref = x.double() @ W.double().T
+    err = {}
+    for mode in (_lib.MATMUL_SPLIT_BF16, _lib.MATMUL_FP32):
+        with _lib.matmul_mode(mode):
+            y = linear.gemm(x, W)
+        d = y.double() - ref
+        err[mode] = (d.norm().item() / ref.norm().item(), d.abs().max().item() / ref.abs().max().item())
+    rms_s, max_s = err[_lib.MATMUL_SPLIT_BF16]
+    rms_f, max_f = err[_lib.MATMUL_FP32]
+    assert rms_s < 1e-6 and max_s < 5e-6, err
+    assert rms_s <= 1.1 * rms_f and max_s <= 1.5 * max_f, err
+
+
+def test_split_complex_accuracy(cuda):
+    """The complex layer in split mode (four products of split planes) against the fp32 mode
+    (three fp32 products, whose out_i = T3 - T1 - T2 cancels) on an m = 1 conv1 shape: both
+    fp32-class against float64, the split one no less accurate."""
+    from ops import _lib
+    from ops.linear import complex_gemm
+    g = torch.Generator().manual_seed(7)
+    M, Kc, Nc = 16384, 512, 256
+    x = torch.randn(M, 2 * Kc, generator=g)
+    Rw = torch.randn(Nc, Kc, generator=g) / Kc ** 0.5
+    Iw = torch.randn(Nc, Kc, generator=g) / Kc ** 0.5
+    ref = (x.double() @ R.pack_so2(Rw.double(), Iw.double()).T).to(cuda)
+    err = {}
+    for mode in (_lib.MATMUL_SPLIT_BF16, _lib.MATMUL_FP32):
+        with _lib.matmul_mode(mode):
+            y = complex_gemm(x.to(cuda), Rw.to(cuda), Iw.to(cuda))
+        d = y.double() - ref
+        err[mode] = (d.norm().item() / ref.norm().item(), d.abs().max().item() / ref.abs().max().item())
+    rms_s, max_s = err[_lib.MATMUL_SPLIT_BF16]
+    rms_f, max_f = err[_lib.MATMUL_FP32]
+    assert rms_s < 1e-6 and max_s < 5e-6, err
+    assert rms_s <= 1.1 * rms_f and max_s <= 1.5 * max_f, err
+
+
+def test_matmul_mode_switch(cuda):
+    from ops import _lib
+    prev = _lib.get_matmul_mode()
+    assert prev == _lib.MATMUL_SPLIT_BF16
+    with _lib.matmul_mode(_lib.MATMUL_FP32):
+        assert _lib.get_matmul_mode() == _lib.MATMUL_FP32
+    assert _lib.get_matmul_mode() == prev
+    with pytest.raises(_lib.FlashUMAError, match="mode=7"):
+        _lib.set_matmul_mode(7)
 
 
 @pytest.mark.parametrize("C", [128, 64])
