@@ -10,18 +10,22 @@
 // formed in registers from the operands already staged in LDS, so no extra memory traffic.
 //
 // Tiling: 256 threads (4 waves, 2 x 2), an output tile of 128 rows x 64 columns of both
-// out_r and out_i; K advances in chunks of 16 through double-buffered LDS.  Two main loops
-// (fu_set_matmul_mode):
-//  * split bf16 (default): a_r, a_i, P and Q are split into three bf16 planes each as they
-//    are staged (split_bf16.h; 36 KB of planes per buffer, two workgroups per CU).  The
-//    three-product form would need planes of a_r + a_i and P + Q as well (54 KB per buffer,
-//    one workgroup per CU), so this loop uses the four products directly,
+// out_r and out_i; K advances in chunks of 16 through double-buffered LDS.  Three main loops:
+//  * split bf16 with a pre-split weight (default when the caller passes W3, built once per
+//    frozen weight by fu_complex_weight_split): P, Q and S = P + Q are stored as bf16 planes
+//    in MFMA-fragment order ([32-column block][16-k chunk][P, Q, S][hi, mid, lo][lane], 16 B
+//    per lane), so each wave loads its B fragments with 1 KB coalesced loads straight into
+//    registers, one chunk ahead.  Only a_r, a_i and a_s = a_r + a_i are split in the kernel
+//    and staged as planes in LDS (36 KB per buffer, two workgroups per CU).  The three
+//    products above run as 6 x 3 MFMAs per 32-row block and chunk (six accumulator chains
+//    per wave, 64 x 32 of each of T1, T2, T3).
+//  * split bf16 without W3: a_r, a_i, P and Q are all split as they are staged (36 KB of
+//    planes per buffer); planes of a_r + a_i and P + Q as well would not fit two workgroups
+//    per CU, so this loop runs the four products directly,
 //        out_r = a_r P^T + a_i (-Q)^T,  out_i = a_r Q^T + a_i P^T,
-//    with -Q formed by flipping the sign bits of the Q planes in registers; each wave owns
-//    64 x 32 of out_r and out_i (four accumulator chains) and issues 6 x 8 MFMAs per chunk.
-//  * fp32: the three products above on v_mfma_f32_32x32x2_f32; each wave owns 64 x 32 of each
-//    of T1, T2, T3 (six accumulator chains); fp32 LDS rows as in the real GEMM (a_r, a_i: 128
-//    rows; P, Q: 64 rows).
+//    with -Q formed by flipping the sign bits of the Q planes in registers (four chains).
+//  * fp32 (fu_set_matmul_mode(1)): the three products on v_mfma_f32_32x32x2_f32, fp32 LDS
+//    rows as in the real GEMM (a_r, a_i: 128 rows; P, Q: 64 rows).
 // The epilogue stages the outputs through LDS and writes 16-byte row pieces.
 #include "split_bf16.h"
 
@@ -31,8 +35,19 @@ constexpr int CBM = 128, CBN = 64;
 constexpr int CTA = CBM * 16, CTB = CBN * 16;
 constexpr int CBUF = 2 * CTA + 2 * CTB;          // fp32: a_r | a_i | P | Q
 constexpr int CBUF_SPLIT = 6 * CTA + 6 * CTB;    // bf16: a_r, a_i planes (CTA each) | P, Q planes (CTB each)
+constexpr int CBUF_PRE = 9 * CTA;                // bf16: a_r, a_i, a_s planes
 constexpr int C_LDS_FLOATS = 2 * CBUF;
 constexpr int C_LDS_FLOATS_SPLIT = CBUF_SPLIT;   // two buffers of bf16 = CBUF_SPLIT floats
+static_assert(CBUF_PRE == CBUF_SPLIT, "both split loops use the same LDS size");
+
+// Main loops of complex_linear_kernel.
+enum { CPATH_FP32 = 0, CPATH_SPLIT4 = 1, CPATH_SPLIT3_PRE = 2 };
+
+// Fragment-order planes of a pre-split complex weight: per (32-column block, 16-k chunk),
+// 9 x 64 lanes x 16 B (P, Q, S = P + Q, each hi, mid, lo).
+__host__ __device__ inline int64_t complex_weight_split_vectors(int32_t Nc, int32_t Kc) {
+  return (int64_t)((Nc + 31) / 32) * ((Kc + 15) / 16) * 9 * 64;
+}
 
 __device__ __forceinline__ int clds(int row, int chunk) {
   return row * 16 + 4 * (chunk ^ (((row >> 1) ^ (row >> 2)) & 3));
@@ -57,11 +72,13 @@ struct CGate {
   int64_t ldp;
 };
 
-template <int MODE, bool SPLIT>
-__global__ __launch_bounds__(256, SPLIT ? 2 : 3) void complex_linear_kernel(
+template <int MODE, int PATH>
+__global__ __launch_bounds__(256, PATH == CPATH_FP32 ? 3 : 2) void complex_linear_kernel(
     const float* __restrict__ Ar, const float* __restrict__ Ai, int64_t lda, const float* __restrict__ P,
-    const float* __restrict__ Q, int64_t ldw, float* __restrict__ Yr, float* __restrict__ Yi, int64_t ldy,
-    int64_t M, int32_t Nc, int32_t Kc, int32_t n_tiles, int64_t total_tiles, CGate g) {
+    const float* __restrict__ Q, int64_t ldw, const uint4* __restrict__ W3, float* __restrict__ Yr,
+    float* __restrict__ Yi, int64_t ldy, int64_t M, int32_t Nc, int32_t Kc, int32_t n_tiles, int64_t total_tiles,
+    CGate g) {
+  constexpr bool SPLIT = PATH != CPATH_FP32;
   __shared__ __attribute__((aligned(16))) float smem[SPLIT ? C_LDS_FLOATS_SPLIT : C_LDS_FLOATS];
   // XCD-aware tile order, as in the real GEMM
   int64_t wg = blockIdx.x;
@@ -73,8 +90,8 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 3) void complex_linear_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wr = (wave >> 1) * 64, wc = (wave & 1) * 32;
 
-  // split: T[0] = out_r, T[1] = out_i; fp32: T1, T2, T3 of the three-product form
-  constexpr int NT = SPLIT ? 2 : 3;
+  // four-product split: T[0] = out_r, T[1] = out_i; otherwise T1, T2, T3 of the three products
+  constexpr int NT = PATH == CPATH_SPLIT4 ? 2 : 3;
   floatx16 T[NT][2];
 #pragma unroll
   for (int p = 0; p < NT; ++p)
@@ -84,7 +101,81 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 3) void complex_linear_kernel(
       for (int r = 0; r < 16; ++r) T[p][i][r] = 0.0f;
 
   const int fr = lane & 31, fh = lane >> 5;
-  if constexpr (SPLIT) {
+  if constexpr (PATH == CPATH_SPLIT3_PRE) {
+    // [buf][a_r hi, mid, lo | a_i hi, mid, lo | a_s hi, mid, lo][CTA]
+    __bf16* sp = reinterpret_cast<__bf16*>(smem);
+    const int sr = tid >> 1, sh = tid & 1;  // tile row sr, k 8 sh .. 8 sh + 7
+    const int soff = plane_off(sr, sh);
+    const int nkc = (Kc + 15) / 16;
+    const int nbt = (Nc + 31) / 32;
+    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 gr[2], gi[2];
+    // unconditional 16-byte loads; pieces outside the operand read its first float4 and are zeroed
+    auto load_chunk = [&](int k0) {
+      const int64_t row = row0 + sr;
+      const int gk = k0 + 8 * sh;
+      const bool a0 = row < M && gk < Kc, a1 = row < M && gk + 4 < Kc;
+      const int64_t ao = row * lda + gk;
+      const float4 r0 = ld4(a0 ? Ar + ao : Ar), r1 = ld4(a1 ? Ar + ao + 4 : Ar);
+      const float4 i0 = ld4(a0 ? Ai + ao : Ai), i1 = ld4(a1 ? Ai + ao + 4 : Ai);
+      gr[0] = a0 ? r0 : z4;
+      gr[1] = a1 ? r1 : z4;
+      gi[0] = a0 ? i0 : z4;
+      gi[1] = a1 ? i1 : z4;
+    };
+    auto store_chunk = [&](int buf) {
+      __bf16* b = sp + buf * CBUF_PRE;
+      uint4 h, m, l;
+      split3(gr[0], gr[1], h, m, l);
+      st_planes(b, CTA, soff, h, m, l);
+      split3(gi[0], gi[1], h, m, l);
+      st_planes(b + 3 * CTA, CTA, soff, h, m, l);
+      split3(gr[0] + gi[0], gr[1] + gi[1], h, m, l);
+      st_planes(b + 6 * CTA, CTA, soff, h, m, l);
+    };
+    // this wave's B fragments of chunk kc (a column block past Nc reads block 0; its outputs
+    // are never stored)
+    int nb = (col0 + wc) / 32;
+    nb = nb < nbt ? nb : 0;
+    const uint4* wb = W3 + (int64_t)nb * nkc * 9 * 64 + lane;
+    auto load_b = [&](int kc, uint4 (&bf)[9]) {
+#pragma unroll
+      for (int u = 0; u < 9; ++u) bf[u] = wb[(kc * 9 + u) * 64];
+    };
+    auto step = [&](int kc, const uint4 (&bc)[9], uint4 (&bn)[9]) {
+      load_b(kc + 1 < nkc ? kc + 1 : nkc - 1, bn);
+      const __bf16* b = sp + (kc & 1) * CBUF_PRE;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int off = plane_off(wr + 32 * i + fr, fh);
+        bf16x8 af[9];  // a_r, a_i, a_s planes
+#pragma unroll
+        for (int u = 0; u < 9; ++u) af[u] = *reinterpret_cast<const bf16x8*>(b + u * CTA + off);
+#pragma unroll
+        for (int q = 0; q < 6; ++q)
+#pragma unroll
+          for (int op = 0; op < 3; ++op)
+            T[op][i] = mfma_bf16(af[3 * op + kSplitA[q]], __builtin_bit_cast(bf16x8, bc[3 * op + kSplitB[q]]),
+                                 T[op][i]);
+      }
+      // chunk kc + 1 into the other buffer (its last readers finished before the previous
+      // barrier), then prefetch chunk kc + 2
+      store_chunk((kc & 1) ^ 1);
+      load_chunk((kc + 2 < nkc ? kc + 2 : nkc - 1) * 16);
+      __syncthreads();
+    };
+    uint4 b0[9], b1[9];
+    load_chunk(0);
+    store_chunk(0);
+    load_chunk((nkc > 1 ? 1 : 0) * 16);
+    load_b(0, b0);
+    __syncthreads();
+    // unrolled by two so that the fragment double buffer stays in fixed registers
+    for (int kc = 0; kc < nkc; kc += 2) {
+      step(kc, b0, b1);
+      if (kc + 1 < nkc) step(kc + 1, b1, b0);
+    }
+  } else if constexpr (PATH == CPATH_SPLIT4) {
     // [buf][a_r hi, mid, lo | a_i hi, mid, lo (CTA each) | P hi, mid, lo | Q hi, mid, lo (CTB each)]
     __bf16* sp = reinterpret_cast<__bf16*>(smem);
     const int sr = tid >> 1, sh = tid & 1;                    // a_r, a_i: tile row sr, k 8 sh ..
@@ -244,7 +335,7 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 3) void complex_linear_kernel(
     for (int r = 0; r < 16; ++r) {
       const int rr = 8 * (r >> 2) + 4 * fh + (r & 3);
       const float t1 = T[0][i][r], t2 = T[1][i][r];
-      if constexpr (SPLIT) {
+      if constexpr (PATH == CPATH_SPLIT4) {
         ws[rr * CES + fr] = t1;
         ws[rr * CES + 32 + fr] = t2;
       } else {
@@ -303,27 +394,77 @@ static int complex_check(const float* A_r, const float* A_i, int64_t lda, const 
 
 template <int MODE>
 static int complex_launch(const float* A_r, const float* A_i, int64_t lda, const float* P, const float* Q, int64_t ldw,
-                          float* Y_r, float* Y_i, int64_t ldy, int64_t M, int32_t Nc, int32_t Kc, CGate g,
-                          void* stream, const char* who) {
+                          const void* W3, float* Y_r, float* Y_i, int64_t ldy, int64_t M, int32_t Nc, int32_t Kc,
+                          CGate g, void* stream, const char* who) {
+  if (W3 && !aligned16(W3)) return set_error(FU_ERR_ALIGN, "%s: W3 must be 16-byte aligned", who);
   const int n_tiles = (Nc + CBN - 1) / CBN;
   const int64_t total = ((M + CBM - 1) / CBM) * n_tiles;
-  auto kern = matmul_mode() == FU_MATMUL_FP32 ? complex_linear_kernel<MODE, false> : complex_linear_kernel<MODE, true>;
-  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(256), 0, as_stream(stream), A_r, A_i, lda, P, Q, ldw, Y_r, Y_i,
-                     ldy, M, Nc, Kc, n_tiles, total, g);
+  auto kern = matmul_mode() == FU_MATMUL_FP32 ? complex_linear_kernel<MODE, CPATH_FP32>
+              : W3                              ? complex_linear_kernel<MODE, CPATH_SPLIT3_PRE>
+                                                : complex_linear_kernel<MODE, CPATH_SPLIT4>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(256), 0, as_stream(stream), A_r, A_i, lda, P, Q, ldw,
+                     static_cast<const uint4*>(W3), Y_r, Y_i, ldy, M, Nc, Kc, n_tiles, total, g);
+  return check_launch(who);
+}
+
+// Builds the fragment-order bf16 planes of (P, Q, P + Q): one thread per (32-column block,
+// 16-k chunk, lane) writes the lane's 8 consecutive k of one column, zero-padded past Nc / Kc.
+__global__ void complex_weight_split_kernel(const float* __restrict__ P, const float* __restrict__ Q, int64_t ldw,
+                                            int32_t Nc, int32_t Kc, uint4* __restrict__ W3) {
+  const int nkc = (Kc + 15) / 16;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= complex_weight_split_vectors(Nc, Kc) / 9) return;
+  const int lane = (int)(t & 63);
+  const int64_t q = t >> 6;  // (block, chunk)
+  const int n = (int)(q / nkc) * 32 + (lane & 31);
+  const int k0 = (int)(q % nkc) * 16 + (lane >> 5) * 8;
+  float p[8], r[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const bool ok = n < Nc && k0 + u < Kc;
+    p[u] = ok ? P[(int64_t)n * ldw + k0 + u] : 0.0f;
+    r[u] = ok ? Q[(int64_t)n * ldw + k0 + u] : 0.0f;
+  }
+  uint4* o = W3 + q * 9 * 64 + lane;
+  uint4 h, m, l;
+  split3(make_float4(p[0], p[1], p[2], p[3]), make_float4(p[4], p[5], p[6], p[7]), h, m, l);
+  o[0] = h; o[64] = m; o[128] = l;
+  split3(make_float4(r[0], r[1], r[2], r[3]), make_float4(r[4], r[5], r[6], r[7]), h, m, l);
+  o[192] = h; o[256] = m; o[320] = l;
+  split3(make_float4(p[0] + r[0], p[1] + r[1], p[2] + r[2], p[3] + r[3]),
+         make_float4(p[4] + r[4], p[5] + r[5], p[6] + r[6], p[7] + r[7]), h, m, l);
+  o[384] = h; o[448] = m; o[512] = l;
+}
+
+extern "C" int64_t fu_complex_weight_split_bytes(int32_t Nc, int32_t Kc) {
+  if (Nc <= 0 || Kc <= 0) return set_error(FU_ERR_SHAPE, "fu_complex_weight_split_bytes: Nc=%d Kc=%d", Nc, Kc);
+  return complex_weight_split_vectors(Nc, Kc) * 16;
+}
+
+extern "C" int fu_complex_weight_split(const float* P, const float* Q, int64_t ldw, int32_t Nc, int32_t Kc, void* W3,
+                                       void* stream) {
+  const char* who = "fu_complex_weight_split";
+  if (Nc <= 0 || Kc <= 0 || ldw < Kc) return set_error(FU_ERR_SHAPE, "%s: Nc=%d Kc=%d ldw=%lld", who, Nc, Kc, (long long)ldw);
+  if (!P || !Q || !W3) return set_error(FU_ERR_NULL, "%s: NULL argument", who);
+  if (!aligned16(W3)) return set_error(FU_ERR_ALIGN, "%s: W3 must be 16-byte aligned", who);
+  const int64_t threads = complex_weight_split_vectors(Nc, Kc) / 9;
+  hipLaunchKernelGGL(complex_weight_split_kernel, dim3(cdiv(threads, 256)), dim3(256), 0, as_stream(stream), P, Q, ldw,
+                     Nc, Kc, static_cast<uint4*>(W3));
   return check_launch(who);
 }
 
 extern "C" int fu_complex_linear(const float* A_r, const float* A_i, int64_t lda, const float* P, const float* Q,
-                                 int64_t ldw, float* Y_r, float* Y_i, int64_t ldy, int64_t M, int32_t Nc,
-                                 int32_t Kc, void* stream) {
+                                 int64_t ldw, const void* W3, float* Y_r, float* Y_i, int64_t ldy, int64_t M,
+                                 int32_t Nc, int32_t Kc, void* stream) {
   int st = complex_check(A_r, A_i, lda, P, Q, ldw, Y_r, Y_i, ldy, M, Nc, Kc, "fu_complex_linear");
   if (st != FU_OK || M == 0) return st;
-  return complex_launch<0>(A_r, A_i, lda, P, Q, ldw, Y_r, Y_i, ldy, M, Nc, Kc, CGate{}, stream,
+  return complex_launch<0>(A_r, A_i, lda, P, Q, ldw, W3, Y_r, Y_i, ldy, M, Nc, Kc, CGate{}, stream,
                            "fu_complex_linear");
 }
 
 extern "C" int fu_complex_linear_gate(const float* A_r, const float* A_i, int64_t lda, const float* P, const float* Q,
-                                      int64_t ldw, float* Y_r, float* Y_i, int64_t ldy, float* Z_r, float* Z_i,
+                                      int64_t ldw, const void* W3, float* Y_r, float* Y_i, int64_t ldy, float* Z_r,
+                                      float* Z_i,
                                       int64_t ldz, const float* S, int64_t lds, int32_t s_off, int64_t M, int32_t Nc,
                                       int32_t Kc, void* stream) {
   const char* who = "fu_complex_linear_gate";
@@ -334,12 +475,13 @@ extern "C" int fu_complex_linear_gate(const float* A_r, const float* A_i, int64_
   if ((ldz | lds | s_off) % 4 != 0 || !aligned16(Z_r) || !aligned16(Z_i) || !aligned16(S))
     return set_error(FU_ERR_ALIGN, "%s: gate operands must be 16-byte aligned with strides multiples of 4", who);
   if (M == 0) return FU_OK;
-  return complex_launch<1>(A_r, A_i, lda, P, Q, ldw, Y_r, Y_i, ldy, M, Nc, Kc,
+  return complex_launch<1>(A_r, A_i, lda, P, Q, ldw, W3, Y_r, Y_i, ldy, M, Nc, Kc,
                            CGate{Z_r, Z_i, ldz, S, lds, s_off, nullptr, nullptr, 0, nullptr, 0}, stream, who);
 }
 
 extern "C" int fu_complex_linear_gate_bwd(const float* A_r, const float* A_i, int64_t lda, const float* P,
-                                          const float* Q, int64_t ldw, float* gY_r, float* gY_i, int64_t ldg,
+                                          const float* Q, int64_t ldw, const void* W3, float* gY_r, float* gY_i,
+                                          int64_t ldg,
                                           const float* F_r, const float* F_i, int64_t ldf, const float* S, int64_t lds,
                                           int32_t s_off, float* Pout, int64_t ldp, int64_t M, int32_t Nc, int32_t Kc,
                                           void* stream) {
@@ -352,6 +494,6 @@ extern "C" int fu_complex_linear_gate_bwd(const float* A_r, const float* A_i, in
   if ((ldf | ldp | lds | s_off) % 4 != 0 || !aligned16(F_r) || !aligned16(F_i) || !aligned16(S) || !aligned16(Pout))
     return set_error(FU_ERR_ALIGN, "%s: gate operands must be 16-byte aligned with strides multiples of 4", who);
   if (M == 0) return FU_OK;
-  return complex_launch<2>(A_r, A_i, lda, P, Q, ldw, gY_r, gY_i, ldg, M, Nc, Kc,
+  return complex_launch<2>(A_r, A_i, lda, P, Q, ldw, W3, gY_r, gY_i, ldg, M, Nc, Kc,
                            CGate{nullptr, nullptr, 0, S, lds, s_off, F_r, F_i, ldf, Pout, ldp}, stream, who);
 }

@@ -32,7 +32,7 @@ import torch.nn as nn
 from ops.gather import LAYOUT1_PERM, block_permutation, gather_wigner_split
 from ops.gating import conv1_gate_conv2, gate_paired_rows
 from ops.geom import precompute_geometry
-from ops.linear import complex_linear, linear
+from ops.linear import complex_linear, complex_weight_split, linear
 from ops.lmax import gather_rotate_lmax, init_node_scatter_lmax, rotate_scatter_lmax, wigner_extend
 from ops.ln_silu import layer_norm_silu
 from ops.node import permute_rows
@@ -130,14 +130,31 @@ class Packed_eSCN_Layer(nn.Module):
         # themselves, plus R^T and -I^T for its input gradient.
         R = R.to(dtype).contiguous()
         I = I.to(dtype).contiguous()
+        self._splits_dev = None  # pre-split copies are rebuilt from the new buffers on next use
         self.register_buffer(name + "_R", R)
         self.register_buffer(name + "_I", I)
         self.register_buffer(name + "_Rt", R.t().contiguous())
         self.register_buffer(name + "_It_neg", (-I).t().contiguous())
 
     def _complex(self, x: torch.Tensor, name: str) -> torch.Tensor:
+        k = 2 * self._COMPLEX.index(name)
+        sp = self._complex_splits(x.device)[k:k + 2]
         return complex_linear(x, getattr(self, name + "_R"), getattr(self, name + "_I"), getattr(self, name + "_Rt"),
-                              getattr(self, name + "_It_neg"))
+                              getattr(self, name + "_It_neg"), *sp)
+
+    _COMPLEX = ("W_conv1_m1", "W_conv1_m2", "W_conv2_m1", "W_conv2_m2")
+
+    def _complex_splits(self, dev: torch.device) -> tuple:
+        """complex_weight_split of each frozen complex weight and of its transpose pair, in the
+        order conv1_gate_conv2 takes them; built on first use on a device (the weights are
+        frozen), not part of the state dict."""
+        if getattr(self, "_splits_dev", None) != dev:
+            sp = []
+            for name in self._COMPLEX:
+                sp.append(complex_weight_split(getattr(self, name + "_R"), getattr(self, name + "_I")))
+                sp.append(complex_weight_split(getattr(self, name + "_Rt"), getattr(self, name + "_It_neg")))
+            self._splits, self._splits_dev = tuple(sp), dev
+        return self._splits
 
     def prepare_for_inference(self, dtype=torch.float32):
         if self.norm_1 is not None:
@@ -231,7 +248,7 @@ class Packed_eSCN_Layer(nn.Module):
             [getattr(self, "W_conv1_m" + m + x) for m in "12" for x in sfx]
         c2 = [self.W_conv2_m0, self.b_conv2_m0, self.W_conv2_m0_t] + \
             [getattr(self, "W_conv2_m" + m + x) for m in "12" for x in sfx]
-        Zo_m0, Zo_m1, Zo_m2 = conv1_gate_conv2(X_m0, X_m1, X_m2, c1, c2, self.C)
+        Zo_m0, Zo_m1, Zo_m2 = conv1_gate_conv2(X_m0, X_m1, X_m2, c1, c2, self.C, self._complex_splits(X_m0.device))
         x_mid = rotate_scatter_split(Zo_m0, Zo_m1, Zo_m2, wigner, env, x_in, idx_j, row_ptr, col_idx,
                                      x_in.shape[0])
         return self.atom_wise(self.norm_2(x_mid)) + x_mid
@@ -246,7 +263,7 @@ class Packed_eSCN_Layer(nn.Module):
             [getattr(self, "W_conv1_m" + m + x) for m in "12" for x in sfx]
         c2 = [self.W_conv2_m0, self.b_conv2_m0, self.W_conv2_m0_t] + \
             [getattr(self, "W_conv2_m" + m + x) for m in "12" for x in sfx]
-        Zo_m0, Zo_m1, Zo_m2 = conv1_gate_conv2(X_m0, X_m1, X_m2, c1, c2, C)
+        Zo_m0, Zo_m1, Zo_m2 = conv1_gate_conv2(X_m0, X_m1, X_m2, c1, c2, C, self._complex_splits(X_m0.device))
         x_mid = rotate_scatter_lmax(Zo_m0, Zo_m1, Zo_m2, wigner, wig_ext, env, x_in, idx_j, row_ptr, col_idx,
                                     x_in.shape[0], L)
         return self.atom_wise(self.norm_2(x_mid)) + x_mid

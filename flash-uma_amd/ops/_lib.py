@@ -45,12 +45,13 @@ SIGNATURES: dict[str, list] = {
     "fu_ln_silu_grouped_bwd": [P, I64, P, P, I64, P, P, P, P, P, P, P, P, P, I64, P, I64, I64, I32, I32, P],
     "fu_linear": [P, I64, P, I64, P, P, I64, I64, I32, I32, P],
     "fu_linear_batched": [P, I64, I64, P, I64, I64, P, I64, I32, P, I64, I64, I64, I32, I32, I32, P],
-    "fu_complex_linear": [P, P, I64, P, P, I64, P, P, I64, I64, I32, I32, P],
+    "fu_complex_linear": [P, P, I64, P, P, I64, P, P, P, I64, I64, I32, I32, P],
+    "fu_complex_weight_split_bytes": [I32, I32],
+    "fu_complex_weight_split": [P, P, I64, I32, I32, P, P],
     "fu_linear_gate": [P, I64, P, I64, P, P, I64, P, I64, P, I64, I64, I32, I32, I32, P],
-    "fu_complex_linear_gate": [P, P, I64, P, P, I64, P, P, I64, P, P, I64, P, I64, I32, I64, I32, I32, P],
+    "fu_complex_linear_gate": [P, P, I64, P, P, I64, P, P, P, I64, P, P, I64, P, I64, I32, I64, I32, I32, P],
     "fu_linear_gate_bwd": [P, I64, P, I64, P, I64, P, I64, P, I64, P, I64, P, I64, I64, I32, I32, I32, P],
-    "fu_complex_linear_gate_bwd": [P, P, I64, P, P, I64, P, P, I64, P, P, I64, P, I64, I32, P, I64, I64, I32, I32,
-                                   P],
+    "fu_complex_linear_gate_bwd": [P, P, I64, P, P, I64, P, P, P, I64, P, P, I64, P, I64, I32, P, I64, I64, I32, I32, P],
     "fu_rms_norm_sh_fwd": [P, P, P, P, P, I64, I32, I32, F32, P],
     "fu_rms_norm_sh_bwd": [P, P, P, P, P, I64, I32, I32, P],
     "fu_gate_act_fwd": [P, P, P, I64, I32, I32, P],
@@ -102,7 +103,8 @@ def load() -> ctypes.CDLL:
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes
-        fn.restype = ctypes.c_char_p if name == "fu_last_error" else ctypes.c_int
+        fn.restype = (ctypes.c_char_p if name == "fu_last_error" else
+                      ctypes.c_int64 if name.endswith("_bytes") else ctypes.c_int)
     _lib = lib
     return lib
 

@@ -85,7 +85,7 @@ class Conv1Gate(torch.autograd.Function):
     backward, which runs as the separate kernel before the input-gradient GEMMs."""
 
     @staticmethod
-    def forward(ctx, X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C):
+    def forward(ctx, X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C, splits):
         X0 = _lib.require(X0, torch.float32, "X_m0")
         X1 = _lib.require(X1, torch.float32, "X_m1")
         X2 = _lib.require(X2, torch.float32, "X_m2")
@@ -98,30 +98,35 @@ class Conv1Gate(torch.autograd.Function):
         _lib.call("fu_linear_gate", X0.data_ptr(), X0.stride(0), W0.data_ptr(), W0.stride(0), _lib.ptr(b0),
                   Y0.data_ptr(), Y0.stride(0), Z0.data_ptr(), Z0.stride(0), S.data_ptr(), S.stride(0), E, C,
                   W0.shape[1], L, st)
+        sp = splits or (None,) * 4
         outs = []
-        for X, P, Q, s_off in ((X1, P1, Q1, 0), (X2, P2, Q2, C)):
+        for X, P, Q, W3, s_off in ((X1, P1, Q1, sp[0], 0), (X2, P2, Q2, sp[2], C)):
             Nc, Kc = P.shape
             Y, Z = f(E, 2 * Nc), f(E, 2 * Nc)
             _lib.call("fu_complex_linear_gate", X.data_ptr(), X[:, Kc:].data_ptr(), X.stride(0), P.data_ptr(),
-                      Q.data_ptr(), P.stride(0), Y.data_ptr(), Y[:, Nc:].data_ptr(), Y.stride(0), Z.data_ptr(),
-                      Z[:, Nc:].data_ptr(), Z.stride(0), S.data_ptr(), S.stride(0), s_off, E, Nc, Kc, st)
+                      Q.data_ptr(), P.stride(0), _lib.ptr(W3), Y.data_ptr(), Y[:, Nc:].data_ptr(), Y.stride(0),
+                      Z.data_ptr(), Z[:, Nc:].data_ptr(), Z.stride(0), S.data_ptr(), S.stride(0), s_off, E, Nc, Kc,
+                      st)
             outs += [Y, Z]
         Y1, Z1, Y2, Z2 = outs
         if L != 2:
             raise _lib.FlashUMAError("conv1_gate: lmax 2 only (use conv1_gate_conv2 for lmax 3, 4)")
         ctx.save_for_backward(Y0, Y1, Y2, W0t, P1t, Q1tn, P2t, Q2tn)
-        ctx.C = C
+        ctx.C, ctx.sp = C, sp
         return Z0, Z1, Z2
 
     @staticmethod
     def backward(ctx, g_z0, g_z1, g_z2):
         Y0, Y1, Y2, W0t, P1t, Q1tn, P2t, Q2tn = ctx.saved_tensors
+        sp = ctx.sp
         g_y0, g_y1, g_y2 = _gating_bwd(Y0, Y1, Y2, g_z0, g_z1, g_z2, ctx.C, 1)
-        return (gemm(g_y0, W0t), complex_gemm(g_y1, P1t, Q1tn), complex_gemm(g_y2, P2t, Q2tn)) + (None,) * 12
+        return ((gemm(g_y0, W0t), complex_gemm(g_y1, P1t, Q1tn, sp[1]), complex_gemm(g_y2, P2t, Q2tn, sp[3])) +
+                (None,) * 13)
 
 
-def conv1_gate(X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C):
-    return Conv1Gate.apply(X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C)
+def conv1_gate(X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C, splits=None):
+    """splits: None or complex_weight_split of (P1, Q1), (P1t, Q1tn), (P2, Q2), (P2t, Q2tn)."""
+    return Conv1Gate.apply(X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C, splits)
 
 
 class Conv1GateConv2(torch.autograd.Function):
@@ -133,7 +138,7 @@ class Conv1GateConv2(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, V0, c0, V0t, R1, I1, R1t, I1tn, R2,
-                I2, R2t, I2tn, C):
+                I2, R2t, I2tn, C, splits):
         X0 = _lib.require(X0, torch.float32, "X_m0")
         X1 = _lib.require(X1, torch.float32, "X_m1")
         X2 = _lib.require(X2, torch.float32, "X_m2")
@@ -146,20 +151,22 @@ class Conv1GateConv2(torch.autograd.Function):
         _lib.call("fu_linear_gate", X0.data_ptr(), X0.stride(0), W0.data_ptr(), W0.stride(0), _lib.ptr(b0),
                   Y0.data_ptr(), Y0.stride(0), Z0.data_ptr(), Z0.stride(0), S.data_ptr(), S.stride(0), E, C,
                   W0.shape[1], L, st)
+        sp = splits or (None,) * 8
         outs = []
-        for X, P, Q, s_off in ((X1, P1, Q1, 0), (X2, P2, Q2, C)):
+        for X, P, Q, W3, s_off in ((X1, P1, Q1, sp[0], 0), (X2, P2, Q2, sp[2], C)):
             Nc, Kc = P.shape
             Y, Z = f(E, 2 * Nc), f(E, 2 * Nc)
             _lib.call("fu_complex_linear_gate", X.data_ptr(), X[:, Kc:].data_ptr(), X.stride(0), P.data_ptr(),
-                      Q.data_ptr(), P.stride(0), Y.data_ptr(), Y[:, Nc:].data_ptr(), Y.stride(0), Z.data_ptr(),
-                      Z[:, Nc:].data_ptr(), Z.stride(0), S.data_ptr(), S.stride(0), s_off, E, Nc, Kc, st)
+                      Q.data_ptr(), P.stride(0), _lib.ptr(W3), Y.data_ptr(), Y[:, Nc:].data_ptr(), Y.stride(0),
+                      Z.data_ptr(), Z[:, Nc:].data_ptr(), Z.stride(0), S.data_ptr(), S.stride(0), s_off, E, Nc, Kc,
+                      st)
             outs += [Y, Z]
         Y1, Z1, Y2, Z2 = outs
         Zo0 = gemm(Z0, V0, c0)
-        Zo1 = complex_gemm(Z1, R1, I1)
-        Zo2 = complex_gemm(Z2, R2, I2)
+        Zo1 = complex_gemm(Z1, R1, I1, sp[4])
+        Zo2 = complex_gemm(Z2, R2, I2, sp[6])
         ctx.save_for_backward(Y0, Y1, Y2, S, W0t, P1t, Q1tn, P2t, Q2tn, V0t, R1t, I1tn, R2t, I2tn)
-        ctx.C, ctx.L = C, L
+        ctx.C, ctx.L, ctx.sp = C, L, sp
         return Zo0, Zo1, Zo2
 
     @staticmethod
@@ -173,14 +180,15 @@ class Conv1GateConv2(torch.autograd.Function):
         g0 = torch.zeros(E, (L + 1) * C, device=dev) if g0 is None else g0.contiguous()
         g1 = torch.zeros(E, 2 * L * C, device=dev) if g1 is None else g1.contiguous()
         g2 = torch.zeros(E, 2 * (L - 1) * C, device=dev) if g2 is None else g2.contiguous()
+        sp = ctx.sp
         gys, psums = [], []
-        for g, Rt, Itn, F, s_off in ((g1, R1t, I1tn, Y1, 0), (g2, R2t, I2tn, Y2, C)):
+        for g, Rt, Itn, W3, F, s_off in ((g1, R1t, I1tn, sp[5], Y1, 0), (g2, R2t, I2tn, sp[7], Y2, C)):
             Nc, Kc = Rt.shape
             gy, ps = f(E, 2 * Nc), f(E, Nc)
             _lib.call("fu_complex_linear_gate_bwd", g.data_ptr(), g[:, Kc:].data_ptr(), g.stride(0), Rt.data_ptr(),
-                      Itn.data_ptr(), Rt.stride(0), gy.data_ptr(), gy[:, Nc:].data_ptr(), gy.stride(0), F.data_ptr(),
-                      F[:, Nc:].data_ptr(), F.stride(0), S.data_ptr(), S.stride(0), s_off, ps.data_ptr(),
-                      ps.stride(0), E, Nc, Kc, st)
+                      Itn.data_ptr(), Rt.stride(0), _lib.ptr(W3), gy.data_ptr(), gy[:, Nc:].data_ptr(),
+                      gy.stride(0), F.data_ptr(), F[:, Nc:].data_ptr(), F.stride(0), S.data_ptr(), S.stride(0),
+                      s_off, ps.data_ptr(), ps.stride(0), E, Nc, Kc, st)
             gys.append(gy)
             psums.append(ps)
         gy0 = f(E, (2 * L + 1) * C)
@@ -188,12 +196,14 @@ class Conv1GateConv2(torch.autograd.Function):
                   Y0.stride(0), S.data_ptr(), S.stride(0), psums[0].data_ptr(), psums[0].stride(0),
                   psums[1].data_ptr(), psums[1].stride(0), gy0.data_ptr(), gy0.stride(0), E, C, V0t.shape[1], L,
                   st)
-        return ((gemm(gy0, W0t), complex_gemm(gys[0], P1t, Q1tn), complex_gemm(gys[1], P2t, Q2tn)) +
-                (None,) * 23)
+        return ((gemm(gy0, W0t), complex_gemm(gys[0], P1t, Q1tn, sp[1]), complex_gemm(gys[1], P2t, Q2tn, sp[3])) +
+                (None,) * 24)
 
 
-def conv1_gate_conv2(X0, X1, X2, conv1, conv2, C):
+def conv1_gate_conv2(X0, X1, X2, conv1, conv2, C, splits=None):
     """conv1 = (W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn) as for conv1_gate; conv2 =
     (V0, c0, V0t, R1, I1, R1t, I1tn, R2, I2, R2t, I2tn) (m = 0 weight, bias and transpose; the
-    complex m = 1, 2 weights with R^T and -I^T).  Returns Zout_m0, Zout_m1, Zout_m2."""
-    return Conv1GateConv2.apply(X0, X1, X2, *conv1, *conv2, C)
+    complex m = 1, 2 weights with R^T and -I^T).  splits: None or the complex_weight_split of
+    (P1, Q1), (P1t, Q1tn), (P2, Q2), (P2t, Q2tn), (R1, I1), (R1t, I1tn), (R2, I2), (R2t, I2tn).
+    Returns Zout_m0, Zout_m1, Zout_m2."""
+    return Conv1GateConv2.apply(X0, X1, X2, *conv1, *conv2, C, splits)

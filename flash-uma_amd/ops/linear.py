@@ -1,4 +1,4 @@
-"""Dense layers on the gfx950 fp32 MFMA GEMM (replaces torch F.linear at model.py:147-154,203-205).
+"""Dense layers on the gfx950 matrix cores (replaces torch F.linear at model.py:147-154,203-205).
 
 y = x W^T + b.  Weights are frozen; the backward returns the input gradient
 g_x = g_y W, computed by the same kernel against the pre-transposed weight W^T."""
@@ -44,9 +44,27 @@ def linear(x: torch.Tensor, W: torch.Tensor, bias: torch.Tensor | None, Wt: torc
     return _LinearFn.apply(x, W, bias, Wt)
 
 
-def complex_gemm(x: torch.Tensor, P: torch.Tensor, Q: torch.Tensor) -> torch.Tensor:
+def complex_weight_split(P: torch.Tensor, Q: torch.Tensor) -> torch.Tensor:
+    """The frozen complex weight P + iQ (Nc, Kc each) pre-split for fu_complex_linear's W3
+    argument: exact three-way bf16 splits of P, Q and P + Q in MFMA-fragment order."""
+    P = _lib.require(P, torch.float32, "P")
+    Q = _lib.require(Q, torch.float32, "Q")
+    Nc, Kc = P.shape
+    if Q.shape != P.shape:
+        raise _lib.FlashUMAError(f"complex_weight_split: P {tuple(P.shape)} vs Q {tuple(Q.shape)}")
+    nbytes = _lib.load().fu_complex_weight_split_bytes(Nc, Kc)
+    if nbytes < 0:
+        raise _lib.FlashUMAError(f"complex_weight_split: bad shape {(Nc, Kc)}")
+    W3 = torch.empty(nbytes // 16, 4, device=P.device, dtype=torch.int32)
+    _lib.call("fu_complex_weight_split", P.data_ptr(), Q.data_ptr(), P.stride(0), Nc, Kc, W3.data_ptr(),
+              _lib.stream_ptr(P.device))
+    return W3
+
+
+def complex_gemm(x: torch.Tensor, P: torch.Tensor, Q: torch.Tensor, W3: torch.Tensor | None = None) -> torch.Tensor:
     """[y_r | y_i] = complex product of x = [x_r | x_i] (M, 2 Kc) with (P + iQ)^T, P, Q (Nc, Kc):
-    y_r = x_r P^T - x_i Q^T, y_i = x_r Q^T + x_i P^T (fu_complex_linear)."""
+    y_r = x_r P^T - x_i Q^T, y_i = x_r Q^T + x_i P^T (fu_complex_linear; W3 = complex_weight_split(P, Q)
+    or None)."""
     if x.stride(-1) != 1:
         x = x.contiguous()
     M = x.shape[0]
@@ -55,26 +73,29 @@ def complex_gemm(x: torch.Tensor, P: torch.Tensor, Q: torch.Tensor) -> torch.Ten
         raise _lib.FlashUMAError(f"complex_gemm: x {tuple(x.shape)} vs P {tuple(P.shape)}, Q {tuple(Q.shape)}")
     y = torch.empty((M, 2 * Nc), device=x.device, dtype=torch.float32)
     _lib.call("fu_complex_linear", x.data_ptr(), x[:, Kc:].data_ptr(), x.stride(0), P.data_ptr(), Q.data_ptr(),
-              P.stride(0), y.data_ptr(), y[:, Nc:].data_ptr(), y.stride(0), M, Nc, Kc, _lib.stream_ptr(x.device))
+              P.stride(0), _lib.ptr(W3), y.data_ptr(), y[:, Nc:].data_ptr(), y.stride(0), M, Nc, Kc, _lib.stream_ptr(x.device))
     return y
 
 
 class _ComplexLinearFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, P, Q, Pt, Qt_neg):
+    def forward(ctx, x, P, Q, Pt, Qt_neg, W3, W3t):
         x = _lib.require(x, torch.float32, "x")
         ctx.save_for_backward(Pt, Qt_neg)
-        return complex_gemm(x, P, Q)
+        ctx.W3t = W3t
+        return complex_gemm(x, P, Q, W3)
 
     @staticmethod
     def backward(ctx, g_y):
         Pt, Qt_neg = ctx.saved_tensors
-        return complex_gemm(g_y.contiguous(), Pt, Qt_neg), None, None, None, None
+        return complex_gemm(g_y.contiguous(), Pt, Qt_neg, ctx.W3t), None, None, None, None, None, None
 
 
 def complex_linear(x: torch.Tensor, P: torch.Tensor, Q: torch.Tensor, Pt: torch.Tensor,
-                   Qt_neg: torch.Tensor) -> torch.Tensor:
+                   Qt_neg: torch.Tensor, W3: torch.Tensor | None = None,
+                   W3t: torch.Tensor | None = None) -> torch.Tensor:
     """Frozen complex layer: equals x @ [[P, -Q], [Q, P]]^T (the reference's packed SO(2)
     weight, model.py:108-138).  Pt = P^T and Qt_neg = -Q^T (contiguous) give the input
-    gradient through the same kernel: g_x_r = g_r P + g_i Q, g_x_i = g_i P - g_r Q."""
-    return _ComplexLinearFn.apply(x, P, Q, Pt, Qt_neg)
+    gradient through the same kernel: g_x_r = g_r P + g_i Q, g_x_i = g_i P - g_r Q.  W3, W3t:
+    optional complex_weight_split of (P, Q) and (Pt, Qt_neg)."""
+    return _ComplexLinearFn.apply(x, P, Q, Pt, Qt_neg, W3, W3t)

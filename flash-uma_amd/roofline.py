@@ -104,7 +104,7 @@ def _linear_gate_bwd(a):
 
 def _complex_linear_gate_bwd(a):
     # reads F (2 Nc) and S (Nc), writes gY (2 Nc) and the gate sums (Nc)
-    M, Nc, Kc = a[17], a[18], a[19]
+    M, Nc, Kc = a[18], a[19], a[20]
     return 4 * (2 * M * Kc + 2 * Nc * Kc + 6 * M * Nc), 6 * M * Nc * Kc
 
 
@@ -175,9 +175,9 @@ def _linear_batched(a):
 
 
 def _complex_linear(a):
-    # executed MFMA work: three real (M x Kc) x (Kc x Nc) products (the packed real form
-    # of the reference would be four)
-    M, Nc, Kc = a[9], a[10], a[11]
+    # three real (M x Kc) x (Kc x Nc) products (the packed real form of the reference would be
+    # four; so is the split path without a pre-split weight, which executes 4/3 of this)
+    M, Nc, Kc = a[10], a[11], a[12]
     return 4 * (2 * M * Kc + 2 * M * Nc + 2 * Nc * Kc), 6 * M * Nc * Kc
 
 
@@ -190,7 +190,7 @@ def _linear_gate(a):
 
 def _complex_linear_gate(a):
     # complex product plus the sigmoid read S (Nc) and the gated copies Z_r, Z_i (2 Nc)
-    M, Nc, Kc = a[15], a[16], a[17]
+    M, Nc, Kc = a[16], a[17], a[18]
     return 4 * (2 * M * Kc + 2 * M * Nc + 2 * Nc * Kc + 3 * M * Nc), 6 * M * Nc * Kc
 
 

@@ -222,12 +222,25 @@ int fu_linear_batched(const float* A, int64_t lda, int64_t stride_a, const float
  * and weight P + iQ ((Nc, Kc) each, row stride ldw),
  *   Y_r = A_r P^T - A_i Q^T,   Y_i = A_r Q^T + A_i P^T      ((M, Nc), row stride ldy),
  * i.e. X [[P, -Q], [Q, P]]^T with X = [A_r | A_i] -- the reference's packed product -- computed
- * with three real MFMA products (Gauss) instead of four.  The input gradient of the layer is
+ * with three real products (Gauss) instead of four.  The input gradient of the layer is
  * the same operation with (P^T, -Q^T).  Kc, lda, ldw multiples of 4; A_r, A_i, P, Q 16-byte
- * aligned. */
+ * aligned.  W3: NULL, or the same weight pre-split by fu_complex_weight_split (16-byte
+ * aligned); in the split matrix-core mode (fu_set_matmul_mode) it is read instead of P and Q
+ * (three split products, B fragments loaded straight into registers); without it the
+ * operands are split in the kernel (four split products).  The fp32 mode ignores W3. */
 int fu_complex_linear(const float* A_r, const float* A_i, int64_t lda, const float* P, const float* Q,
-                      int64_t ldw, float* Y_r, float* Y_i, int64_t ldy, int64_t M, int32_t Nc,
-                      int32_t Kc, void* stream);
+                      int64_t ldw, const void* W3, float* Y_r, float* Y_i, int64_t ldy, int64_t M,
+                      int32_t Nc, int32_t Kc, void* stream);
+
+/* Pre-split complex weight for the W3 argument of fu_complex_linear*; no reference counterpart
+ * (a frozen weight of model.py:108-138, prepared once at freeze time).  P, Q (Nc, Kc) with row
+ * stride ldw; W3 receives the exact three-way bf16 splits of P, Q and P + Q in MFMA-fragment
+ * order ([32-column block][16-k chunk][P, Q, P + Q][hi, mid, lo][64 lanes] x 16 bytes, zero
+ * padded to Nc = 32 n, Kc = 16 k), fu_complex_weight_split_bytes(Nc, Kc) bytes, 16-byte
+ * aligned.  The bytes query returns a negative FU_ERR_* for Nc or Kc <= 0. */
+int64_t fu_complex_weight_split_bytes(int32_t Nc, int32_t Kc);
+int fu_complex_weight_split(const float* P, const float* Q, int64_t ldw, int32_t Nc, int32_t Kc, void* W3,
+                            void* stream);
 
 /* conv1 m = 0 fused with the gate activation (model.py:152-153 with ops/gating.py:32-103):
  * Y = A W^T + bias with N = (2L+1)C columns (L = lmax) in the gate-paired order: 64-column
@@ -243,8 +256,8 @@ int fu_linear_gate(const float* A, int64_t lda, const float* W, int64_t ldw, con
  * Z_r = Y_r s, Z_i = Y_i s with s = S[row][s_off + column] (S from fu_linear_gate: s_off = 0
  * for m = 1, whose columns are [l1 | .. | lL]; s_off = C for m = 2, columns [l2 | .. | lL]). */
 int fu_complex_linear_gate(const float* A_r, const float* A_i, int64_t lda, const float* P,
-                           const float* Q, int64_t ldw, float* Y_r, float* Y_i, int64_t ldy,
-                           float* Z_r, float* Z_i, int64_t ldz, const float* S, int64_t lds,
+                           const float* Q, int64_t ldw, const void* W3, float* Y_r, float* Y_i,
+                           int64_t ldy, float* Z_r, float* Z_i, int64_t ldz, const float* S, int64_t lds,
                            int32_t s_off, int64_t M, int32_t Nc, int32_t Kc, void* stream);
 
 /* conv2 m = 0 input gradient (model.py:154) fused with the gate backward (ops/gating.py:
@@ -264,8 +277,8 @@ int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* Wt, int64_t 
  * gY_r/gY_i = g_Z s with s = S[row][s_off + column], and Pout = g_Zr F_r + g_Zi F_i (the
  * gate sum of this block; F = the forward pre-activation Y from fu_complex_linear_gate). */
 int fu_complex_linear_gate_bwd(const float* A_r, const float* A_i, int64_t lda, const float* P,
-                               const float* Q, int64_t ldw, float* gY_r, float* gY_i, int64_t ldg,
-                               const float* F_r, const float* F_i, int64_t ldf, const float* S,
+                               const float* Q, int64_t ldw, const void* W3, float* gY_r, float* gY_i,
+                               int64_t ldg, const float* F_r, const float* F_i, int64_t ldf, const float* S,
                                int64_t lds, int32_t s_off, float* Pout, int64_t ldp, int64_t M,
                                int32_t Nc, int32_t Kc, void* stream);
 

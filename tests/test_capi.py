@@ -111,3 +111,29 @@ def test_lmax_entry_points_reject_bad_arguments():
     # lmax 3 and 4 need the extension rows; lmax 2 accepts NULL there (checked before any launch)
     assert lib.fu_init_scatter_bwd_lmax(None, None, None, None, None, None, None, None, None, None, 0, 4, 128, 4,
                                         None) == 0
+
+
+def test_complex_weight_split_arguments():
+    # one (32-column, 16-k) block holds 9 planes x 64 lanes x 16 B; sizes round up to whole blocks
+    st, _ = _status("fu_complex_weight_split_bytes", 32, 16)
+    assert st == 9 * 64 * 16
+    st, _ = _status("fu_complex_weight_split_bytes", 33, 17)
+    assert st == 4 * 9 * 64 * 16
+    st, _ = _status("fu_complex_weight_split_bytes", 0, 16)
+    assert st == -1
+    st, _ = _status("fu_complex_weight_split", None, None, 16, 32, 16, None, None)
+    assert st == -5
+    st, msg = _status("fu_complex_weight_split", 16, 16, 8, 32, 16, 16, None)
+    assert st == -1 and "ldw" in msg
+    st, msg = _status("fu_complex_weight_split", 16, 16, 16, 32, 16, 8, None)
+    assert st == -3 and "aligned" in msg
+    # a misaligned pre-split weight is rejected before any launch
+    st, msg = _status("fu_complex_linear", 16, 16, 16, 16, 16, 16, 8, 16, 16, 16, 4, 4, 16, None)
+    assert st == -3 and "W3" in msg
+
+
+def test_matmul_mode_rejects_unknown():
+    st, msg = _status("fu_set_matmul_mode", 5)
+    assert st == -2 and "mode=5" in msg
+    st, _ = _status("fu_matmul_mode")
+    assert st in (0, 1)

@@ -168,18 +168,23 @@ def test_linear(cuda, matmul_mode, M, N, K):
     assert_close(g, gref, TOL, "linear bwd")
 
 
-@pytest.mark.parametrize("M,Kc,Nc", [(300, 512, 256), (257, 128, 256), (1, 96, 64), (1000, 128, 128)])
-def test_complex_linear(cuda, matmul_mode, M, Kc, Nc):
-    """The three-product complex layer against the reference's packed real GEMM
-    x @ [[R, -I], [I, R]]^T (oracle pack_so2) in float64, forward and input gradient."""
-    from ops.linear import complex_linear
+@pytest.mark.parametrize("presplit", [False, True], ids=["in_kernel", "presplit"])
+@pytest.mark.parametrize("M,Kc,Nc", [(300, 512, 256), (257, 128, 256), (1, 96, 64), (1000, 128, 128), (130, 36, 68)])
+def test_complex_linear(cuda, matmul_mode, presplit, M, Kc, Nc):
+    """The complex layer against the reference's packed real GEMM x @ [[R, -I], [I, R]]^T
+    (oracle pack_so2) in float64, forward and input gradient; with the weights split in the
+    kernel and pre-split (complex_weight_split, the three-product register path; Kc = 36 and
+    Nc = 68 leave partial k chunks and column blocks in the fragment layout)."""
+    from ops.linear import complex_linear, complex_weight_split
     g = torch.Generator().manual_seed(M + Kc + Nc)
     x = torch.randn(M, 2 * Kc, generator=g)
     Rw = torch.randn(Nc, Kc, generator=g) / Kc ** 0.5
     Iw = torch.randn(Nc, Kc, generator=g) / Kc ** 0.5
     xg = x.to(cuda).requires_grad_(True)
     Rg, Ig = Rw.to(cuda), Iw.to(cuda)
-    y = complex_linear(xg, Rg, Ig, Rg.t().contiguous(), (-Ig).t().contiguous())
+    Rt, Itn = Rg.t().contiguous(), (-Ig).t().contiguous()
+    W3 = (complex_weight_split(Rg, Ig), complex_weight_split(Rt, Itn)) if presplit else (None, None)
+    y = complex_linear(xg, Rg, Ig, Rt, Itn, *W3)
     cot = torch.randn(M, 2 * Nc, generator=g)
     Wp = R.pack_so2(Rw.double(), Iw.double())
     (ref,), (gref,) = _vjp(lambda a: a @ Wp.T, [x], [cot])
@@ -213,12 +218,13 @@ def test_split_gemm_accuracy(cuda, N, K):
     assert rms_s <= 1.1 * rms_f and max_s <= 1.5 * max_f, err
 
 
-def test_split_complex_accuracy(cuda):
-    """The complex layer in split mode (four products of split planes) against the fp32 mode
-    (three fp32 products, whose out_i = T3 - T1 - T2 cancels) on an m = 1 conv1 shape: both
-    fp32-class against float64, the split one no less accurate."""
+@pytest.mark.parametrize("presplit", [False, True], ids=["in_kernel", "presplit"])
+def test_split_complex_accuracy(cuda, presplit):
+    """The complex layer in split mode -- four split products with the weight split in the
+    kernel, or three with a pre-split weight -- against the fp32 mode (three fp32 products) on
+    an m = 1 conv1 shape: both fp32-class against float64, the split one no less accurate."""
     from ops import _lib
-    from ops.linear import complex_gemm
+    from ops.linear import complex_gemm, complex_weight_split
     g = torch.Generator().manual_seed(7)
     M, Kc, Nc = 16384, 512, 256
     x = torch.randn(M, 2 * Kc, generator=g)
@@ -226,9 +232,10 @@ def test_split_complex_accuracy(cuda):
     Iw = torch.randn(Nc, Kc, generator=g) / Kc ** 0.5
     ref = (x.double() @ R.pack_so2(Rw.double(), Iw.double()).T).to(cuda)
     err = {}
+    W3 = complex_weight_split(Rw.to(cuda), Iw.to(cuda)) if presplit else None
     for mode in (_lib.MATMUL_SPLIT_BF16, _lib.MATMUL_FP32):
         with _lib.matmul_mode(mode):
-            y = complex_gemm(x.to(cuda), Rw.to(cuda), Iw.to(cuda))
+            y = complex_gemm(x.to(cuda), Rw.to(cuda), Iw.to(cuda), W3)
         d = y.double() - ref
         err[mode] = (d.norm().item() / ref.norm().item(), d.abs().max().item() / ref.abs().max().item())
     rms_s, max_s = err[_lib.MATMUL_SPLIT_BF16]

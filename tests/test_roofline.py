@@ -1,0 +1,67 @@
+"""The roofline accounting reads each entry point's sizes from the right argument positions:
+for every entry point with a work function, the size parameters are located by name in
+include/flashuma.h and the work computed from a call with distinct sizes is checked against
+the formula stated for it."""
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "flashuma.h")
+
+
+def _params(name):
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    m = re.search(r"\b" + name + r"\s*\(([^)]*)\)\s*;", text)
+    assert m, name
+    return [p.split()[-1].lstrip("*") for p in m.group(1).split(",")]
+
+
+def _args(name, **sizes):
+    params = _params(name)
+    args = [0] * len(params)
+    for key, val in sizes.items():
+        args[params.index(key)] = val
+    return tuple(args)
+
+
+GEMMS = {
+    # entry point: (sizes, algorithmic flops)
+    "fu_linear": (dict(M=1000, N=384, K=640), 2 * 1000 * 384 * 640),
+    "fu_linear_batched": (dict(M=1000, N=128, K=256, batch=5), 2 * 5 * 1000 * 128 * 256),
+    "fu_linear_gate": (dict(M=1000, C=128, K=768, lmax=2), 2 * 1000 * 640 * 768),
+    "fu_linear_gate_bwd": (dict(M=1000, C=128, K=384, lmax=2), 2 * 1000 * 384 * 384),
+    "fu_complex_linear": (dict(M=1000, Nc=256, Kc=512), 6 * 1000 * 256 * 512),
+    "fu_complex_linear_gate": (dict(M=1000, Nc=256, Kc=512), 6 * 1000 * 256 * 512),
+    "fu_complex_linear_gate_bwd": (dict(M=1000, Nc=128, Kc=256), 6 * 1000 * 128 * 256),
+}
+
+
+@pytest.mark.parametrize("name", sorted(GEMMS))
+def test_gemm_work_reads_the_size_arguments(name):
+    import roofline
+    sizes, flops = GEMMS[name]
+    nbytes, got = roofline.WORK[name](_args(name, **sizes))
+    assert got == flops
+    assert nbytes > 0
+
+
+def test_every_work_function_names_a_declared_entry_point():
+    import roofline
+    text = open(HEADER).read()
+    for name in roofline.WORK:
+        assert re.search(r"\b" + name + r"\s*\(", text), name
+
+
+def test_split_mode_accounting():
+    import roofline
+    args = _args("fu_linear", M=1000, N=384, K=640)
+    flops = 2 * 1000 * 384 * 640
+    ms = 1.0
+    split = roofline.summarize([("fu_linear", args, ms)], roofline.MATMUL_SPLIT_BF16)["fu_linear"]
+    fp32 = roofline.summarize([("fu_linear", args, ms)], roofline.MATMUL_FP32)["fu_linear"]
+    rate = flops / 1e-3 / 1e12
+    assert fp32["peak"] == 157.3 and abs(fp32["achieved"] - rate) < 0.01
+    assert split["peak"] == 2500.0 and abs(split["achieved"] - 6 * rate) < 0.05
+    assert abs(split["fp32_tflops"] - rate) < 0.01
