@@ -255,10 +255,12 @@ def test_matmul_mode_switch(cuda):
         _lib.set_matmul_mode(7)
 
 
+@pytest.mark.parametrize("side_stream", [True, False], ids=["side_stream", "one_stream"])
 @pytest.mark.parametrize("C", [128, 64])
-def test_radial_bank(cuda, C):
+def test_radial_bank(cuda, C, side_stream):
     """All radial MLPs as one bank (element embeddings folded into per-element tables) against
-    the textbook per-block MLP on x_edge_raw = [g | W_src[Z_i] | W_tgt[Z_j]] in float64."""
+    the textbook per-block MLP on x_edge_raw = [g | W_src[Z_i] | W_tgt[Z_j]] in float64; with
+    the output layers on the side stream (the threshold lowered to this graph) and without."""
     from ops.radial import RadialBank
     g = torch.Generator().manual_seed(C)
     N, E, B = 50, 777, 64
@@ -287,8 +289,11 @@ def test_radial_bank(cuda, C):
 
     rref, (gref,) = _vjp(ref, [gauss], cot)
     bank = RadialBank([tuple(t.to(cuda) for t in m) for m in mlps], W_src.to(cuda), W_tgt.to(cuda), B)
+    bank.SIDE_STREAM_MIN_EDGES = 0 if side_stream else 1 << 62
     gg = gauss.to(cuda).requires_grad_(True)
     rads = bank(gg, Z.to(cuda), ii.to(cuda), jj.to(cuda))
+    for k in range(len(rads)):
+        bank.wait(k)
     for a, b in zip(rads, rref):
         assert_close(a, b, TOL, "radial bank fwd")
     (gr,) = torch.autograd.grad(rads, gg, [c.to(cuda) for c in cot], retain_graph=True)
