@@ -72,7 +72,7 @@ struct CGate {
   int64_t ldp;
 };
 
-template <int MODE, int PATH>
+template <int MODE, int PATH, bool KTAIL = false>
 __global__ __launch_bounds__(256, PATH == CPATH_FP32 ? 3 : 2) void complex_linear_kernel(
     const float* __restrict__ Ar, const float* __restrict__ Ai, int64_t lda, const float* __restrict__ P,
     const float* __restrict__ Q, int64_t ldw, const uint4* __restrict__ W3, float* __restrict__ Yr,
@@ -110,18 +110,30 @@ __global__ __launch_bounds__(256, PATH == CPATH_FP32 ? 3 : 2) void complex_linea
     const int nbt = (Nc + 31) / 32;
     const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
     float4 gr[2], gi[2];
-    // unconditional 16-byte loads; pieces outside the operand read its first float4 and are zeroed
+    // fixed row pointers (a row past M reads row M-1; its outputs are never stored).  Without a
+    // K tail: plain 16-byte loads; with one (KTAIL): unconditional loads from a valid address
+    // and selects zeroing the pieces at or past Kc.  No branch in the loader (an if/else
+    // choosing the form per chunk was miscompiled here: a prefetched operand register reused
+    // before its read).
+    const int64_t row = row0 + sr;
+    const int64_t ao = (row < M ? row : M - 1) * lda + 8 * sh;
+    const float *par = Ar + ao, *pai = Ai + ao;
     auto load_chunk = [&](int k0) {
-      const int64_t row = row0 + sr;
-      const int gk = k0 + 8 * sh;
-      const bool a0 = row < M && gk < Kc, a1 = row < M && gk + 4 < Kc;
-      const int64_t ao = row * lda + gk;
-      const float4 r0 = ld4(a0 ? Ar + ao : Ar), r1 = ld4(a1 ? Ar + ao + 4 : Ar);
-      const float4 i0 = ld4(a0 ? Ai + ao : Ai), i1 = ld4(a1 ? Ai + ao + 4 : Ai);
-      gr[0] = a0 ? r0 : z4;
-      gr[1] = a1 ? r1 : z4;
-      gi[0] = a0 ? i0 : z4;
-      gi[1] = a1 ? i1 : z4;
+      if constexpr (!KTAIL) {
+        gr[0] = ld4(par + k0);
+        gr[1] = ld4(par + k0 + 4);
+        gi[0] = ld4(pai + k0);
+        gi[1] = ld4(pai + k0 + 4);
+      } else {
+        const int gk = k0 + 8 * sh;
+        const bool a0 = gk < Kc, a1 = gk + 4 < Kc;
+        const float4 r0 = ld4(a0 ? par + k0 : Ar), r1 = ld4(a1 ? par + k0 + 4 : Ar);
+        const float4 i0 = ld4(a0 ? pai + k0 : Ai), i1 = ld4(a1 ? pai + k0 + 4 : Ai);
+        gr[0] = a0 ? r0 : z4;
+        gr[1] = a1 ? r1 : z4;
+        gi[0] = a0 ? i0 : z4;
+        gi[1] = a1 ? i1 : z4;
+      }
     };
     auto store_chunk = [&](int buf) {
       __bf16* b = sp + buf * CBUF_PRE;
@@ -184,24 +196,34 @@ __global__ __launch_bounds__(256, PATH == CPATH_FP32 ? 3 : 2) void complex_linea
     const float* Bsrc = bq ? Q : P;
     const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
     float4 gr[2], gi[2], gb[2];
-    // unconditional 16-byte loads; pieces outside an operand read its first float4 and are zeroed
+    // fixed row pointers (a row past M / Nc reads the last row; its outputs are never
+    // stored); K tail handled as in the pre-split path, without a branch in the loader
+    const int64_t row = row0 + sr;
+    const int64_t ao = (row < M ? row : M - 1) * lda + 8 * sh;
+    const float *par = Ar + ao, *pai = Ai + ao;
+    const int gn = col0 + br;
+    const float* pb = Bsrc + (int64_t)(gn < Nc ? gn : Nc - 1) * ldw + 8 * bh;
     auto load_chunk = [&](int k0) {
-      const int64_t row = row0 + sr;
-      const int gk = k0 + 8 * sh;
-      const bool a0 = row < M && gk < Kc, a1 = row < M && gk + 4 < Kc;
-      const int64_t ao = row * lda + gk;
-      const float4 r0 = ld4(a0 ? Ar + ao : Ar), r1 = ld4(a1 ? Ar + ao + 4 : Ar);
-      const float4 i0 = ld4(a0 ? Ai + ao : Ai), i1 = ld4(a1 ? Ai + ao + 4 : Ai);
-      const int gn = col0 + br, gkb = k0 + 8 * bh;
-      const bool b0 = gn < Nc && gkb < Kc, b1 = gn < Nc && gkb + 4 < Kc;
-      const int64_t bo = (int64_t)gn * ldw + gkb;
-      const float4 w0 = ld4(b0 ? Bsrc + bo : Bsrc), w1 = ld4(b1 ? Bsrc + bo + 4 : Bsrc);
-      gr[0] = a0 ? r0 : z4;
-      gr[1] = a1 ? r1 : z4;
-      gi[0] = a0 ? i0 : z4;
-      gi[1] = a1 ? i1 : z4;
-      gb[0] = b0 ? w0 : z4;
-      gb[1] = b1 ? w1 : z4;
+      if constexpr (!KTAIL) {
+        gr[0] = ld4(par + k0);
+        gr[1] = ld4(par + k0 + 4);
+        gi[0] = ld4(pai + k0);
+        gi[1] = ld4(pai + k0 + 4);
+        gb[0] = ld4(pb + k0);
+        gb[1] = ld4(pb + k0 + 4);
+      } else {
+        const int gk = k0 + 8 * sh, gkb = k0 + 8 * bh;
+        const bool a0 = gk < Kc, a1 = gk + 4 < Kc, b0 = gkb < Kc, b1 = gkb + 4 < Kc;
+        const float4 r0 = ld4(a0 ? par + k0 : Ar), r1 = ld4(a1 ? par + k0 + 4 : Ar);
+        const float4 i0 = ld4(a0 ? pai + k0 : Ai), i1 = ld4(a1 ? pai + k0 + 4 : Ai);
+        const float4 w0 = ld4(b0 ? pb + k0 : Bsrc), w1 = ld4(b1 ? pb + k0 + 4 : Bsrc);
+        gr[0] = a0 ? r0 : z4;
+        gr[1] = a1 ? r1 : z4;
+        gi[0] = a0 ? i0 : z4;
+        gi[1] = a1 ? i1 : z4;
+        gb[0] = b0 ? w0 : z4;
+        gb[1] = b1 ? w1 : z4;
+      }
     };
     auto store_chunk = [&](int buf) {
       __bf16* b = sp + buf * CBUF_SPLIT;
@@ -399,9 +421,12 @@ static int complex_launch(const float* A_r, const float* A_i, int64_t lda, const
   if (W3 && !aligned16(W3)) return set_error(FU_ERR_ALIGN, "%s: W3 must be 16-byte aligned", who);
   const int n_tiles = (Nc + CBN - 1) / CBN;
   const int64_t total = ((M + CBM - 1) / CBM) * n_tiles;
+  const bool tail = Kc % 16 != 0;
   auto kern = matmul_mode() == FU_MATMUL_FP32 ? complex_linear_kernel<MODE, CPATH_FP32>
-              : W3                              ? complex_linear_kernel<MODE, CPATH_SPLIT3_PRE>
-                                                : complex_linear_kernel<MODE, CPATH_SPLIT4>;
+              : W3 ? (tail ? complex_linear_kernel<MODE, CPATH_SPLIT3_PRE, true>
+                           : complex_linear_kernel<MODE, CPATH_SPLIT3_PRE, false>)
+                   : (tail ? complex_linear_kernel<MODE, CPATH_SPLIT4, true>
+                           : complex_linear_kernel<MODE, CPATH_SPLIT4, false>);
   hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(256), 0, as_stream(stream), A_r, A_i, lda, P, Q, ldw,
                      static_cast<const uint4*>(W3), Y_r, Y_i, ldy, M, Nc, Kc, n_tiles, total, g);
   return check_launch(who);

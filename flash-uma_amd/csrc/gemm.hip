@@ -76,7 +76,7 @@ struct GateBwd {
 // wave's 64 staged columns are a gate and its values; the epilogue writes Y (kept for the
 // backward), Z and S.  MODE 2 (gate backward): see GateBwd; Y receives g_Y_m0 ((2L+1)C
 // columns).
-template <int MODE, bool SPLIT>
+template <int MODE, bool SPLIT, bool KTAIL = false>
 __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const float* __restrict__ A, int64_t lda, int64_t sA,
                                                           const float* __restrict__ W, int64_t ldw, int64_t sW,
                                                           const float* __restrict__ bias, int64_t sBias,
@@ -124,21 +124,34 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
     const int soff = plane_off(sr, sh);
     const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
     float4 ga[2], gw[2];
-    // Every lane issues its four 16-byte loads unconditionally (guarded loads would be
-    // scalarised into dword loads); a piece outside the operand reads the operand's first
-    // float4 instead and is replaced by zeros.
+    // A thread stages the same tile row (of A and of W) for the whole K loop, so its row
+    // pointers are fixed: a row past M (N) reads row M-1 (N-1) instead, whose products land in
+    // output rows (columns) that are never stored.  Without a K tail (KTAIL false: K a multiple
+    // of 16) every chunk is four plain 16-byte loads.  With one, every load is unconditional
+    // from a valid address followed by a select that zeroes the pieces at or past K (guarded
+    // loads would be scalarised into dword loads).  The loader has no branch either way:
+    // an if/else here, selecting between the two forms per chunk, was miscompiled in the
+    // pre-split complex kernel (a prefetched operand register reused before its read).
+    const int64_t gr = row0 + sr;
+    const int gn = col0 + sr;
+    const float* pa = A + (gr < M ? gr : M - 1) * lda + 8 * sh;
+    const float* pw = W + (int64_t)(gn < N ? gn : N - 1) * ldw + 8 * sh;
     auto load_chunk = [&](int k0) {
-      const int64_t gr = row0 + sr;
-      const int gn = col0 + sr;
-      const int gk = k0 + 8 * sh;
-      const bool a0 = gr < M && gk < K, a1 = gr < M && gk + 4 < K;
-      const bool w0 = gn < N && gk < K, w1 = gn < N && gk + 4 < K;
-      const float4 va0 = ld4(a0 ? A + gr * lda + gk : A), va1 = ld4(a1 ? A + gr * lda + gk + 4 : A);
-      const float4 vw0 = ld4(w0 ? W + (int64_t)gn * ldw + gk : W), vw1 = ld4(w1 ? W + (int64_t)gn * ldw + gk + 4 : W);
-      ga[0] = a0 ? va0 : z4;
-      ga[1] = a1 ? va1 : z4;
-      gw[0] = w0 ? vw0 : z4;
-      gw[1] = w1 ? vw1 : z4;
+      if constexpr (!KTAIL) {
+        ga[0] = ld4(pa + k0);
+        ga[1] = ld4(pa + k0 + 4);
+        gw[0] = ld4(pw + k0);
+        gw[1] = ld4(pw + k0 + 4);
+      } else {
+        const int gk = k0 + 8 * sh;
+        const bool k0ok = gk < K, k1ok = gk + 4 < K;
+        const float4 va0 = ld4(k0ok ? pa + k0 : A), va1 = ld4(k1ok ? pa + k0 + 4 : A);
+        const float4 vw0 = ld4(k0ok ? pw + k0 : W), vw1 = ld4(k1ok ? pw + k0 + 4 : W);
+        ga[0] = k0ok ? va0 : z4;
+        ga[1] = k1ok ? va1 : z4;
+        gw[0] = k0ok ? vw0 : z4;
+        gw[1] = k1ok ? vw1 : z4;
+      }
     };
     auto store_chunk = [&](int buf) {
       __bf16* b = sp + buf * 6 * G_PLANE;
@@ -373,6 +386,14 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
 
 using namespace fu;
 
+// The kernel for MODE in the current matrix-core mode; KTAIL instances handle K % 16 != 0.
+template <int MODE>
+static auto linear_kernel(int32_t K) {
+  return matmul_mode() == FU_MATMUL_FP32 ? linear_mfma_kernel<MODE, false>
+         : (K % GBK != 0)               ? linear_mfma_kernel<MODE, true, true>
+                                          : linear_mfma_kernel<MODE, true, false>;
+}
+
 static int linear_check(const float* A, int64_t lda, const float* W, int64_t ldw, const float* Y, int64_t ldy,
                         int64_t M, int32_t N, int32_t K, const char* who) {
   if (M < 0 || N <= 0 || K <= 0)
@@ -396,7 +417,7 @@ static int linear_launch(const float* A, int64_t lda, int64_t sA, const float* W
   const int64_t m_tiles = (M + GBM - 1) / GBM;
   const int64_t total = m_tiles * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
-  auto kern = matmul_mode() == FU_MATMUL_FP32 ? linear_mfma_kernel<0, false> : linear_mfma_kernel<0, true>;
+  auto kern = linear_kernel<0>(K);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, (unsigned)batch), dim3(256), 0, stream, A, lda, sA, W, ldw, sW, bias,
                      sBias, bias_batches, Y, ldy, sY, M, N, K, n_tiles, total, GateOut{}, GateBwd{});
   return check_launch(who);
@@ -441,7 +462,7 @@ extern "C" int fu_linear_gate(const float* A, int64_t lda, const float* W, int64
   const int n_tiles = (N + GBN - 1) / GBN;
   const int64_t total = ((M + GBM - 1) / GBM) * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
-  auto kern = matmul_mode() == FU_MATMUL_FP32 ? linear_mfma_kernel<1, false> : linear_mfma_kernel<1, true>;
+  auto kern = linear_kernel<1>(K);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), A, lda,
                      (int64_t)0, W, ldw, (int64_t)0, bias, (int64_t)0, 1, Y, ldy, (int64_t)0, M, N, K, n_tiles, total,
                      GateOut{Z, ldz, S, lds, C, lmax}, GateBwd{});
@@ -469,7 +490,7 @@ extern "C" int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* W
   const int n_tiles = (N + GBN - 1) / GBN;
   const int64_t total = ((M + GBM - 1) / GBM) * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
-  auto kern = matmul_mode() == FU_MATMUL_FP32 ? linear_mfma_kernel<2, false> : linear_mfma_kernel<2, true>;
+  auto kern = linear_kernel<2>(K);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), gZo, ldgz,
                      (int64_t)0, Wt, ldw, (int64_t)0, (const float*)nullptr, (int64_t)0, 1, gY0, ldg, (int64_t)0, M, N,
                      K, n_tiles, total, GateOut{}, GateBwd{Y0, ldy0, S, lds, P1, ldp1, P2, ldp2, C, lmax});

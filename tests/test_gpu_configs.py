@@ -74,6 +74,8 @@ def test_water_md_cached_topology(cuda):
     assert st["builds"] == 1 and st["hits"] == 100, st
     kin = 0.5 * (masses * v * v).sum().item() * AMU_A2_FS2_IN_EV
     e_tot.append(out["energy"].item() + kin)
+    # every step's total energy must be finite (max/min alone skip a NaN that is not first)
+    assert all(math.isfinite(e) for e in e_tot), [i for i, e in enumerate(e_tot) if not math.isfinite(e)][:5]
     drift = (max(e_tot) - min(e_tot)) / s.n_atoms
     print(f"total-energy spread over 100 steps: {drift:.2e} eV/atom", flush=True)
     assert math.isfinite(drift) and drift < 2e-5

@@ -84,11 +84,13 @@ def test_conv1_gate(cuda, M, C):
         assert_close(a, b, 1e-4, "conv1+gate bwd")
 
 
+@pytest.mark.parametrize("presplit", [False, True], ids=["in_kernel", "presplit"])
 @pytest.mark.parametrize("M,C,L", [(300, 128, 2), (77, 64, 2), (150, 64, 4), (100, 128, 3)])
-def test_conv1_gate_conv2(cuda, M, C, L):
+def test_conv1_gate_conv2(cuda, M, C, L, presplit):
     """conv1 + gate + conv2 as one function whose backward fuses the gate backward into the
     conv2 input-gradient epilogues, against the textbook products and oracle gating (float64);
-    lmax = L (3 and 4 use the degree-extended block order of oracle.ops_ref.gating_lmax)."""
+    lmax = L (3 and 4 use the degree-extended block order of oracle.ops_ref.gating_lmax); with
+    the complex weights split in the kernels and pre-split (the model's path)."""
     _, gating, *_ = _ops()
     g = torch.Generator().manual_seed(M + 3 * C + L)
     r = lambda *s: torch.randn(*s, generator=g)
@@ -107,8 +109,13 @@ def test_conv1_gate_conv2(cuda, M, C, L):
              dv(-I2.t())]
     conv2 = [dv(V0), dv(c0), dv(V0.t()), dv(S1), dv(T1), dv(S1.t()), dv(-T1.t()), dv(S2), dv(T2), dv(S2.t()),
              dv(-T2.t())]
+    splits = None
+    if presplit:
+        from ops.linear import complex_weight_split
+        pairs = [conv1[3:5], conv1[5:7], conv1[7:9], conv1[9:11], conv2[3:5], conv2[5:7], conv2[7:9], conv2[9:11]]
+        splits = tuple(complex_weight_split(P, Q) for P, Q in pairs)
     Xg = [x.to(cuda).requires_grad_(True) for x in X]
-    Zo = gating.conv1_gate_conv2(*Xg, conv1, conv2, C)
+    Zo = gating.conv1_gate_conv2(*Xg, conv1, conv2, C, splits)
     cot = [r(*z.shape) for z in Zo]
 
     def ref_fn(x0, x1, x2):
