@@ -67,6 +67,13 @@ struct GateBwd {
   int32_t L;
 };
 
+// Residual added by the plain epilogue (MODE 0): Y += R, R with row stride ldr, batch stride sR.
+struct Resid {
+  const float* R;
+  int64_t ldr;
+  int64_t sR;
+};
+
 // Batch index blockIdx.y offsets A, W and Y by sA, sW and sY floats; bias (stride sBias) is
 // added in batches [0, bias_batches).
 //
@@ -83,13 +90,14 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
                                                           int32_t bias_batches, float* __restrict__ Y, int64_t ldy,
                                                           int64_t sY, int64_t M, int32_t N, int32_t K,
                                                           int32_t n_tiles, int64_t total_tiles, GateOut go,
-                                                          GateBwd gb) {
+                                                          GateBwd gb, Resid rs) {
   {
     const int64_t bt = blockIdx.y;
     A += bt * sA;
     W += bt * sW;
     Y += bt * sY;
     bias = (bias != nullptr && bt < bias_batches) ? bias + bt * sBias : nullptr;
+    if (rs.R) rs.R += bt * rs.sR;
   }
   __shared__ __attribute__((aligned(16))) float smem[SPLIT ? G_LDS_FLOATS_SPLIT : G_LDS_FLOATS];
 
@@ -376,6 +384,7 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
         if (bias) {
           v.x += bias[gc]; v.y += bias[gc + 1]; v.z += bias[gc + 2]; v.w += bias[gc + 3];
         }
+        if (rs.R) v = v + ld4(rs.R + gr * rs.ldr + gc);
         st4(Y + gr * ldy + gc, v);
       }
     }
@@ -412,14 +421,15 @@ static int linear_check(const float* A, int64_t lda, const float* W, int64_t ldw
 
 static int linear_launch(const float* A, int64_t lda, int64_t sA, const float* W, int64_t ldw, int64_t sW,
                          const float* bias, int64_t sBias, int32_t bias_batches, float* Y, int64_t ldy, int64_t sY,
-                         int64_t M, int32_t N, int32_t K, int32_t batch, hipStream_t stream, const char* who) {
+                         int64_t M, int32_t N, int32_t K, int32_t batch, hipStream_t stream, const char* who,
+                         Resid rs = Resid{}) {
   const int n_tiles = (N + GBN - 1) / GBN;
   const int64_t m_tiles = (M + GBM - 1) / GBM;
   const int64_t total = m_tiles * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
   auto kern = linear_kernel<0>(K);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, (unsigned)batch), dim3(256), 0, stream, A, lda, sA, W, ldw, sW, bias,
-                     sBias, bias_batches, Y, ldy, sY, M, N, K, n_tiles, total, GateOut{}, GateBwd{});
+                     sBias, bias_batches, Y, ldy, sY, M, N, K, n_tiles, total, GateOut{}, GateBwd{}, rs);
   return check_launch(who);
 }
 
@@ -433,16 +443,18 @@ extern "C" int fu_linear(const float* A, int64_t lda, const float* W, int64_t ld
 
 extern "C" int fu_linear_batched(const float* A, int64_t lda, int64_t stride_a, const float* W, int64_t ldw,
                                  int64_t stride_w, const float* bias, int64_t stride_bias, int32_t bias_batches,
-                                 float* Y, int64_t ldy, int64_t stride_y, int64_t M, int32_t N, int32_t K,
-                                 int32_t batch, void* stream) {
+                                 const float* R, int64_t ldr, int64_t stride_r, float* Y, int64_t ldy,
+                                 int64_t stride_y, int64_t M, int32_t N, int32_t K, int32_t batch, void* stream) {
   int st = linear_check(A, lda, W, ldw, Y, ldy, M, N, K, "fu_linear_batched");
   if (st != FU_OK) return st;
   if (batch < 1 || batch > 65535) return set_error(FU_ERR_SHAPE, "fu_linear_batched: batch=%d out of range", batch);
   if ((stride_a | stride_w | stride_y) % 4 != 0 || stride_a < 0 || stride_w < 0 || stride_y < 0)
     return set_error(FU_ERR_ALIGN, "fu_linear_batched: batch strides must be non-negative multiples of 4");
+  if (R && ((ldr | stride_r) % 4 != 0 || ldr < N || stride_r < 0 || !aligned16(R)))
+    return set_error(FU_ERR_ALIGN, "fu_linear_batched: R must be 16-byte aligned with ldr >= N, strides multiples of 4");
   if (M == 0) return FU_OK;
   return linear_launch(A, lda, stride_a, W, ldw, stride_w, bias, stride_bias, bias_batches, Y, ldy, stride_y, M, N, K,
-                       batch, as_stream(stream), "fu_linear_batched");
+                       batch, as_stream(stream), "fu_linear_batched", Resid{R, ldr, stride_r});
 }
 
 extern "C" int fu_linear_gate(const float* A, int64_t lda, const float* W, int64_t ldw, const float* bias, float* Y,
@@ -465,7 +477,7 @@ extern "C" int fu_linear_gate(const float* A, int64_t lda, const float* W, int64
   auto kern = linear_kernel<1>(K);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), A, lda,
                      (int64_t)0, W, ldw, (int64_t)0, bias, (int64_t)0, 1, Y, ldy, (int64_t)0, M, N, K, n_tiles, total,
-                     GateOut{Z, ldz, S, lds, C, lmax}, GateBwd{});
+                     GateOut{Z, ldz, S, lds, C, lmax}, GateBwd{}, Resid{});
   return check_launch(who);
 }
 
@@ -493,6 +505,6 @@ extern "C" int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* W
   auto kern = linear_kernel<2>(K);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), gZo, ldgz,
                      (int64_t)0, Wt, ldw, (int64_t)0, (const float*)nullptr, (int64_t)0, 1, gY0, ldg, (int64_t)0, M, N,
-                     K, n_tiles, total, GateOut{}, GateBwd{Y0, ldy0, S, lds, P1, ldp1, P2, ldp2, C, lmax});
+                     K, n_tiles, total, GateOut{}, GateBwd{Y0, ldy0, S, lds, P1, ldp1, P2, ldp2, C, lmax}, Resid{});
   return check_launch(who);
 }

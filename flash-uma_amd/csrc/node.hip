@@ -59,7 +59,8 @@ __global__ __launch_bounds__(256) void rms_norm_fwd_kernel(const float* __restri
 template <int CPL, int L>
 __global__ __launch_bounds__(256) void rms_norm_bwd_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                            const float* __restrict__ inv_rms,
-                                                           const float* __restrict__ g_out, float* __restrict__ g_x,
+                                                           const float* __restrict__ g_out,
+                                                           const float* __restrict__ g_res, float* __restrict__ g_x,
                                                            int64_t N) {
   constexpr int C = 64 * CPL, NK = (L + 1) * (L + 1);
   const int lane = threadIdx.x & 63, c = lane * CPL;
@@ -99,6 +100,11 @@ __global__ __launch_bounds__(256) void rms_norm_bwd_kernel(const float* __restri
 #pragma unroll
   for (int q = 0; q < CPL; ++q) gf[0][q] -= mg0;
   float* go = g_x + n * NK * C + c;
+  if (g_res) {  // the gradient of a residual branch that read the same x
+    const float* gr = g_res + n * NK * C + c;
+#pragma unroll
+    for (int k = 0; k < NK; ++k) gf[k] = vadd(gf[k], vload<CPL>(gr + k * C));
+  }
 #pragma unroll
   for (int k = 0; k < NK; ++k) vstore(go + k * C, gf[k]);
 }
@@ -294,7 +300,7 @@ extern "C" int fu_rms_norm_sh_fwd(const float* x, const float* weight, const flo
 }
 
 extern "C" int fu_rms_norm_sh_bwd(const float* x, const float* weight, const float* inv_rms, const float* g_out,
-                                  float* g_x, int64_t N, int32_t C, int32_t lmax, void* stream) {
+                                  const float* g_res, float* g_x, int64_t N, int32_t C, int32_t lmax, void* stream) {
   if (N < 0) return set_error(FU_ERR_SHAPE, "fu_rms_norm_sh_bwd: bad shape");
   FU_LMAX_CHECK("fu_rms_norm_sh_bwd");
   if (N == 0) return FU_OK;
@@ -302,7 +308,7 @@ extern "C" int fu_rms_norm_sh_bwd(const float* x, const float* weight, const flo
   hipStream_t s = as_stream(stream);
   int st = launch_cpl_l(C, lmax, [&](auto cpl, auto lv) {
     hipLaunchKernelGGL((rms_norm_bwd_kernel<decltype(cpl)::value, decltype(lv)::value>), dim3(cdiv(N, 4)), dim3(256),
-                       0, s, x, weight, inv_rms, g_out, g_x, N);
+                       0, s, x, weight, inv_rms, g_out, g_res, g_x, N);
   });
   if (st != FU_OK) return set_error(st, "fu_rms_norm_sh_bwd: C=%d unsupported (64, 128 or 256)", C);
   return check_launch("fu_rms_norm_sh_bwd");

@@ -27,7 +27,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from ops.linear import linear
-from ops.node import gate_act, rms_norm_sh, so3_linear
+from ops.node import (gate_act, rms_norm_sh, rms_norm_sh_residual, scalar_gemm_so3, so3_linear,
+                      so3_linear_residual)
 
 
 def num_coefficients(lmax: int) -> int:
@@ -61,6 +62,11 @@ class EquivariantRMSNormArraySphericalHarmonicsV2(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return rms_norm_sh(x, self.affine_weight, self.affine_bias, self.lmax, self.eps)
 
+    def forward_with_residual(self, x: torch.Tensor):
+        """(norm(x), x) for an x that also feeds a residual skip; the backward sums the two
+        gradients inside the norm's backward kernel."""
+        return rms_norm_sh_residual(x, self.affine_weight, self.affine_bias, self.lmax, self.eps)
+
 
 class SO3_Linear(nn.Module):
     """Per-degree linear map: coefficient (l, m) of the output is W_l x_(l, m); l=0 has a bias."""
@@ -79,10 +85,14 @@ class SO3_Linear(nn.Module):
         w = self.weight.detach().index_select(0, self.expand_index).contiguous()
         return w, w.transpose(1, 2).contiguous()
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if getattr(self, "_wk", None) is None or self._wk[0].device != x.device:
+    def weights(self, device) -> tuple:
+        """(W_k, W_k^T, bias) on `device`, built once per device (weights are frozen)."""
+        if getattr(self, "_wk", None) is None or self._wk[0].device != device:
             self._wk = self.per_coefficient_weights()
-        return so3_linear(x, self._wk[0], self._wk[1], self.bias.detach())
+        return self._wk[0], self._wk[1], self.bias.detach()
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return so3_linear(x, *self.weights(x.device))
 
 
 class GateActivation(nn.Module):
@@ -119,6 +129,17 @@ class SpectralAtomwise(nn.Module):
         h = self.so3_linear_1(x)
         h = self.act(pre, h)
         return self.so3_linear_2(h)
+
+    def forward_residual(self, x: torch.Tensor, skip: torch.Tensor) -> torch.Tensor:
+        """forward(x) + skip with no node-sized elementwise pass: the scalar and SO(3) reads of
+        x share one backward, and skip is added in the last GEMM's epilogue."""
+        lin = self.scalar_mlp[0]
+        if getattr(self, "_wt", None) is None or self._wt.device != x.device:
+            self._wt = lin.weight.detach().t().contiguous()
+        pre, h = scalar_gemm_so3(x, lin.weight.detach(), lin.bias.detach(), self._wt,
+                                 *self.so3_linear_1.weights(x.device))
+        h = self.act(pre, h)
+        return so3_linear_residual(h, *self.so3_linear_2.weights(x.device), skip)
 
 
 def _linear(i: int, o: int, bias: bool, generator) -> nn.Linear:

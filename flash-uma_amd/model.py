@@ -235,12 +235,12 @@ class Packed_eSCN_Layer(nn.Module):
         """rad_out, when given, is this block's radial-MLP output (computed by the model's
         RadialBank); otherwise it is computed here from x_edge_raw (E, B+2C).  wig_ext: the
         degree-3/4 Wigner rows (ops/lmax.wigner_extend), needed for lmax > 2."""
-        x_norm = self.norm_1(x_in)
+        x_norm, x_skip = self._norm_skip(x_in)
         if rad_out is None:
             rad_out = self.radial(x_edge_raw)
         if self.lmax != 2:
-            return self._forward_reference_order(x_in, x_norm, rad_out, wigner, wig_ext, env, idx_i, idx_j, row_ptr,
-                                                 col_idx, csd_emb, batch, topology)
+            return self._forward_reference_order(x_skip, x_norm, rad_out, wigner, wig_ext, env, idx_i, idx_j,
+                                                 row_ptr, col_idx, csd_emb, batch, topology)
         X_m0, X_m1, X_m2 = gather_wigner_split(x_norm, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology,
                                                self.layout)
         sfx = ("_R", "_I", "_Rt", "_It_neg")
@@ -249,8 +249,23 @@ class Packed_eSCN_Layer(nn.Module):
         c2 = [self.W_conv2_m0, self.b_conv2_m0, self.W_conv2_m0_t] + \
             [getattr(self, "W_conv2_m" + m + x) for m in "12" for x in sfx]
         Zo_m0, Zo_m1, Zo_m2 = conv1_gate_conv2(X_m0, X_m1, X_m2, c1, c2, self.C, self._complex_splits(X_m0.device))
-        x_mid = rotate_scatter_split(Zo_m0, Zo_m1, Zo_m2, wigner, env, x_in, idx_j, row_ptr, col_idx,
-                                     x_in.shape[0])
+        x_mid = rotate_scatter_split(Zo_m0, Zo_m1, Zo_m2, wigner, env, x_skip, idx_j, row_ptr, col_idx,
+                                     x_skip.shape[0])
+        return self._ffn_residual(x_mid)
+
+    def _norm_skip(self, x_in):
+        """(norm_1(x_in), x_in): with this build's norm the second is a view whose gradient the
+        norm's backward kernel adds (model.py:145 and the x_in skip of model.py:155)."""
+        if hasattr(self.norm_1, "forward_with_residual"):
+            return self.norm_1.forward_with_residual(x_in)
+        return self.norm_1(x_in), x_in
+
+    def _ffn_residual(self, x_mid):
+        """atom_wise(norm_2(x_mid)) + x_mid (model.py:157); with this build's modules the skip
+        is added in the atom-wise block's last GEMM and its gradient in norm_2's backward."""
+        if hasattr(self.norm_2, "forward_with_residual") and hasattr(self.atom_wise, "forward_residual"):
+            x_n2, skip = self.norm_2.forward_with_residual(x_mid)
+            return self.atom_wise.forward_residual(x_n2, skip)
         return self.atom_wise(self.norm_2(x_mid)) + x_mid
 
     def _forward_reference_order(self, x_in, x_norm, rad_out, wigner, wig_ext, env, idx_i, idx_j, row_ptr, col_idx,
@@ -266,7 +281,7 @@ class Packed_eSCN_Layer(nn.Module):
         Zo_m0, Zo_m1, Zo_m2 = conv1_gate_conv2(X_m0, X_m1, X_m2, c1, c2, C, self._complex_splits(X_m0.device))
         x_mid = rotate_scatter_lmax(Zo_m0, Zo_m1, Zo_m2, wigner, wig_ext, env, x_in, idx_j, row_ptr, col_idx,
                                     x_in.shape[0], L)
-        return self.atom_wise(self.norm_2(x_mid)) + x_mid
+        return self._ffn_residual(x_mid)
 
 
 class eSCN_Inference_Model(nn.Module):

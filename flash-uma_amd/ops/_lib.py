@@ -44,7 +44,7 @@ SIGNATURES: dict[str, list] = {
     "fu_ln_silu_grouped_fwd": [P, I64, P, P, I64, P, P, P, P, P, P, P, I64, P, P, I64, I32, I32, F32, P],
     "fu_ln_silu_grouped_bwd": [P, I64, P, P, I64, P, P, P, P, P, P, P, P, P, I64, P, I64, I64, I32, I32, P],
     "fu_linear": [P, I64, P, I64, P, P, I64, I64, I32, I32, P],
-    "fu_linear_batched": [P, I64, I64, P, I64, I64, P, I64, I32, P, I64, I64, I64, I32, I32, I32, P],
+    "fu_linear_batched": [P, I64, I64, P, I64, I64, P, I64, I32, P, I64, I64, P, I64, I64, I64, I32, I32, I32, P],
     "fu_complex_linear": [P, P, I64, P, P, I64, P, P, P, I64, I64, I32, I32, P],
     "fu_complex_weight_split_bytes": [I32, I32],
     "fu_complex_weight_split": [P, P, I64, I32, I32, P, P],
@@ -53,7 +53,7 @@ SIGNATURES: dict[str, list] = {
     "fu_linear_gate_bwd": [P, I64, P, I64, P, I64, P, I64, P, I64, P, I64, P, I64, I64, I32, I32, I32, P],
     "fu_complex_linear_gate_bwd": [P, P, I64, P, P, I64, P, P, P, I64, P, P, I64, P, I64, I32, P, I64, I64, I32, I32, P],
     "fu_rms_norm_sh_fwd": [P, P, P, P, P, I64, I32, I32, F32, P],
-    "fu_rms_norm_sh_bwd": [P, P, P, P, P, I64, I32, I32, P],
+    "fu_rms_norm_sh_bwd": [P, P, P, P, P, P, I64, I32, I32, P],
     "fu_gate_act_fwd": [P, P, P, I64, I32, I32, P],
     "fu_gate_act_bwd": [P, P, P, P, P, I64, I32, I32, P],
     "fu_gather_rows": [P, P, P, I64, I32, P],

@@ -29,26 +29,58 @@ class RmsNormSH(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g_out):
         x, weight, inv = ctx.saved_tensors
-        N, _, C = x.shape
-        g_out = g_out.contiguous()
-        g_x = torch.empty_like(x)
-        _lib.call("fu_rms_norm_sh_bwd", x.data_ptr(), weight.data_ptr(), inv.data_ptr(), g_out.data_ptr(),
-                  g_x.data_ptr(), N, C, ctx.lmax, _lib.stream_ptr(x.device))
-        return g_x, None, None, None, None
+        return _rms_norm_bwd(x, weight, inv, g_out, None, ctx.lmax), None, None, None, None
+
+
+def _rms_norm_bwd(x, weight, inv, g_out, g_res, lmax):
+    N, _, C = x.shape
+    g_x = torch.empty_like(x)
+    if g_out is None:
+        g_out = torch.zeros_like(x)
+    g_out = g_out.contiguous()
+    g_res = None if g_res is None else g_res.contiguous()
+    _lib.call("fu_rms_norm_sh_bwd", x.data_ptr(), weight.data_ptr(), inv.data_ptr(), g_out.data_ptr(),
+              _lib.ptr(g_res), g_x.data_ptr(), N, C, lmax, _lib.stream_ptr(x.device))
+    return g_x
 
 
 def rms_norm_sh(x, weight, bias, lmax: int, eps: float):
     return RmsNormSH.apply(x, weight, bias, lmax, eps)
 
 
-def _so3_apply(x: torch.Tensor, Wk: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
-    """y[:, k] = x[:, k] @ Wk[k]^T (+ bias on k = 0) as one batched MFMA GEMM over k."""
+class RmsNormSHResidual(torch.autograd.Function):
+    """(norm(x), x) for an x that also feeds a residual skip: the second output is x itself
+    (a new view), and the backward returns norm^T g_norm + g_skip from one kernel, so autograd
+    never sums the two node-sized gradients."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, lmax, eps):
+        out = RmsNormSH.forward(ctx, x, weight, bias, lmax, eps)
+        return out, x.view_as(x)
+
+    @staticmethod
+    def backward(ctx, g_out, g_skip):
+        x, weight, inv = ctx.saved_tensors
+        if g_out is None and g_skip is None:
+            return None, None, None, None, None
+        return _rms_norm_bwd(x, weight, inv, g_out, g_skip, ctx.lmax), None, None, None, None
+
+
+def rms_norm_sh_residual(x, weight, bias, lmax: int, eps: float):
+    return RmsNormSHResidual.apply(x, weight, bias, lmax, eps)
+
+
+def _so3_apply(x: torch.Tensor, Wk: torch.Tensor, bias: torch.Tensor | None,
+               res: torch.Tensor | None = None) -> torch.Tensor:
+    """y[:, k] = x[:, k] @ Wk[k]^T (+ bias on k = 0) (+ res) as one batched MFMA GEMM over k."""
     N, K9, Cin = x.shape
     Cout = Wk.shape[1]
     y = torch.empty(N, K9, Cout, device=x.device, dtype=torch.float32)
+    if res is not None:
+        res = _lib.require(res, torch.float32, "res")
     _lib.call("fu_linear_batched", x.data_ptr(), K9 * Cin, Cin, Wk.data_ptr(), Cin, Cout * Cin,
-              None if bias is None else bias.data_ptr(), 0, 1, y.data_ptr(), K9 * Cout, Cout, N, Cout, Cin, K9,
-              _lib.stream_ptr(x.device))
+              None if bias is None else bias.data_ptr(), 0, 1, _lib.ptr(res), K9 * Cout, Cout, y.data_ptr(),
+              K9 * Cout, Cout, N, Cout, Cin, K9, _lib.stream_ptr(x.device))
     return y
 
 
@@ -70,6 +102,56 @@ class So3Linear(torch.autograd.Function):
 
 def so3_linear(x, Wk, Wtk, bias):
     return So3Linear.apply(x, Wk, Wtk, bias)
+
+
+class So3LinearResidual(torch.autograd.Function):
+    """so3_linear(x) + res with the residual added in the GEMM epilogue; the residual's
+    gradient is the output gradient itself (no copy, no add)."""
+
+    @staticmethod
+    def forward(ctx, x, Wk, Wtk, bias, res):
+        x = _lib.require(x, torch.float32, "x")
+        ctx.save_for_backward(Wtk)
+        return _so3_apply(x, Wk, bias, res)
+
+    @staticmethod
+    def backward(ctx, g_y):
+        (Wtk,) = ctx.saved_tensors
+        g_y = g_y.contiguous()
+        return _so3_apply(g_y, Wtk, None), None, None, None, g_y
+
+
+def so3_linear_residual(x, Wk, Wtk, bias, res):
+    return So3LinearResidual.apply(x, Wk, Wtk, bias, res)
+
+
+class ScalarGemmSo3(torch.autograd.Function):
+    """(pre, h) = (x[:, 0] @ W^T + b, so3_linear(x)) for the atom-wise block's two reads of x:
+    the backward adds the scalar branch's (N, C) gradient into the l = 0 rows of the SO(3)
+    branch's gradient in place, instead of autograd zero-filling an (N, K, C) tensor for the
+    slice and summing two node-sized gradients."""
+
+    @staticmethod
+    def forward(ctx, x, W, b, Wt, Wk, Wtk, bias):
+        from .linear import gemm
+        x = _lib.require(x, torch.float32, "x")
+        pre = gemm(x[:, 0, :], W, b)
+        h = _so3_apply(x, Wk, bias)
+        ctx.save_for_backward(Wt, Wtk)
+        return pre, h
+
+    @staticmethod
+    def backward(ctx, g_pre, g_h):
+        from .linear import gemm
+        Wt, Wtk = ctx.saved_tensors
+        g_x = _so3_apply(g_h.contiguous(), Wtk, None)
+        if g_pre is not None:
+            g_x[:, 0, :] += gemm(g_pre.contiguous(), Wt)
+        return g_x, None, None, None, None, None, None
+
+
+def scalar_gemm_so3(x, W, b, Wt, Wk, Wtk, bias):
+    return ScalarGemmSo3.apply(x, W, b, Wt, Wk, Wtk, bias)
 
 
 class GateAct(torch.autograd.Function):

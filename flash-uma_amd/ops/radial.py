@@ -51,7 +51,8 @@ def _batched(A, W, bias, G, C_in, C_out, out):
     """out[:, g*C_out:(g+1)*C_out] = A[:, g*C_in:(g+1)*C_in] @ W[g]^T (+ bias[g]) for all g."""
     M = A.shape[0]
     _lib.call("fu_linear_batched", A.data_ptr(), A.stride(0), C_in, W.data_ptr(), C_in, C_out * C_in,
-              _lib.ptr(bias), C_out if bias is not None else 0, G if bias is not None else 0, out.data_ptr(),
+              _lib.ptr(bias), C_out if bias is not None else 0, G if bias is not None else 0, None, 0, 0,
+              out.data_ptr(),
               out.stride(0), C_out, M, C_out, C_in, G, _lib.stream_ptr(A.device))
     return out
 

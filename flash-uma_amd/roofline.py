@@ -170,8 +170,9 @@ def _linear(a):
 
 
 def _linear_batched(a):
-    M, N, K, B = a[12], a[13], a[14], a[15]
-    return 4 * B * (M * K + M * N + N * K), 2 * B * M * N * K
+    M, N, K, B = a[15], a[16], a[17], a[18]
+    r = M * N if a[9] else 0   # the residual, read once
+    return 4 * B * (M * K + M * N + N * K + r), 2 * B * M * N * K
 
 
 def _complex_linear(a):

@@ -209,13 +209,15 @@ int fu_linear(const float* A, int64_t lda, const float* W, int64_t ldw, const fl
               float* Y, int64_t ldy, int64_t M, int32_t N, int32_t K, void* stream);
 
 /* Strided batch of fu_linear in one launch: for b < batch,
- * Y_b = A_b @ W_b^T (+ bias_b for b < bias_batches), X_b = X + b * stride_x (floats).
+ * Y_b = A_b @ W_b^T (+ bias_b for b < bias_batches) (+ R_b), X_b = X + b * stride_x (floats).
  * Used for the per-degree SO(3) linears of the atom-wise FFN (W_b = the weight of the
- * degree of coefficient b, bias on l = 0 only). */
+ * degree of coefficient b, bias on l = 0 only) and the radial bank's second layers.  R
+ * (NULL, or row stride ldr >= N, batch stride stride_r, 16-byte aligned) is a residual added
+ * in the epilogue: the skip x_mid + atom_wise(...) of model.py:157 without a separate add. */
 int fu_linear_batched(const float* A, int64_t lda, int64_t stride_a, const float* W, int64_t ldw,
                       int64_t stride_w, const float* bias, int64_t stride_bias, int32_t bias_batches,
-                      float* Y, int64_t ldy, int64_t stride_y, int64_t M, int32_t N, int32_t K,
-                      int32_t batch, void* stream);
+                      const float* R, int64_t ldr, int64_t stride_r, float* Y, int64_t ldy,
+                      int64_t stride_y, int64_t M, int32_t N, int32_t K, int32_t batch, void* stream);
 
 /* Complex dense layer, the SO(2) m = 1, 2 convolutions (model.py:152,154 with the packed
  * weights of model.py:108-138): for features a_r + i a_i (two (M, Kc) arrays, row stride lda)
@@ -290,12 +292,14 @@ int fu_complex_linear_gate_bwd(const float* A_r, const float* A_i, int64_t lda, 
  * final norm of model.py:145,157,218): l=0 centred over channels, scaled by
  * (mean_c sum_k x_kc^2 / ((2 l_k + 1)(lmax + 1)) + eps)^-1/2, per-(l, c) weight, l=0 bias.
  * x, out (N, (lmax + 1)^2, C), lmax 2..4; weight (lmax + 1, C); bias (C); inv_rms (N) is
- * saved for the backward. */
+ * saved for the backward.  The backward adds g_res (NULL or the shape of x) to g_x: the
+ * gradient of a residual branch that read the same x (the x_in + ... and x_mid + ... skips of
+ * model.py:143-157), which then needs no separate accumulation. */
 int fu_rms_norm_sh_fwd(const float* x, const float* weight, const float* bias, float* out,
                        float* inv_rms, int64_t N, int32_t C, int32_t lmax, float eps, void* stream);
 int fu_rms_norm_sh_bwd(const float* x, const float* weight, const float* inv_rms,
-                       const float* g_out, float* g_x, int64_t N, int32_t C, int32_t lmax,
-                       void* stream);
+                       const float* g_out, const float* g_res, float* g_x, int64_t N, int32_t C,
+                       int32_t lmax, void* stream);
 
 /* Gate activation of the atom-wise FFN: gate_l = sigmoid(silu(pre[:, l-1])) for l >= 1,
  * out_0 = silu(h_0), out_k = h_k * gate_{l_k}.  pre (N, lmax * H), h and out

@@ -540,6 +540,51 @@ def test_atomwise_ffn(cuda):
     assert_close(gx, gref, 1e-4, "atom-wise bwd")
 
 
+def test_rms_norm_sh_residual(cuda):
+    """(norm(x), x) with the skip's gradient added inside the norm backward: against the oracle
+    norm and the identity skip, with independent cotangents on both outputs (and on each alone)."""
+    from ops.node import rms_norm_sh_residual
+    from oracle import model_ref as M
+    g = torch.Generator().manual_seed(23)
+    N, C = 37, 128
+    x = torch.randn(N, 9, C, generator=g) * 2 + 0.3
+    w = torch.rand(3, C, generator=g) + 0.5
+    b = torch.randn(C, generator=g)
+    c_n, c_s = torch.randn(N, 9, C, generator=g), torch.randn(N, 9, C, generator=g)
+    (ref, _), (gref,) = _vjp(lambda a: (M.rms_norm_sh(a, w.double(), b.double(), 2, 1e-5), a), [x], [c_n, c_s])
+    xg = x.to(cuda).requires_grad_(True)
+    out, skip = rms_norm_sh_residual(xg, w.to(cuda), b.to(cuda), 2, 1e-5)
+    assert_close(out, ref, TOL, "norm+skip fwd")
+    assert torch.equal(skip, xg)
+    (gx,) = torch.autograd.grad((out, skip), xg, (c_n.to(cuda), c_s.to(cuda)), retain_graph=True)
+    assert_close(gx, gref, 1e-4, "norm+skip bwd")
+    (gs,) = torch.autograd.grad(skip, xg, c_s.to(cuda), retain_graph=True)
+    assert torch.equal(gs, c_s.to(cuda))
+    (gn,) = torch.autograd.grad(out, xg, c_n.to(cuda))
+    _, (gref_n,) = _vjp(lambda a: M.rms_norm_sh(a, w.double(), b.double(), 2, 1e-5), [x], [c_n])
+    assert_close(gn, gref_n, 1e-4, "norm+skip bwd (norm only)")
+
+
+def test_atomwise_ffn_residual(cuda):
+    """atom_wise(x) + skip with the skip added in the last GEMM epilogue and the scalar / SO(3)
+    reads of x sharing one backward, against the oracle block plus the identity skip."""
+    import escn_md
+    from oracle import model_ref as M
+    g = torch.Generator().manual_seed(24)
+    mod = escn_md.SpectralAtomwise(128, 128, 2, generator=g)
+    P = {"m." + k: v.double() for k, v in mod.state_dict().items()}
+    N = 41
+    x, sk = torch.randn(N, 9, 128, generator=g), torch.randn(N, 9, 128, generator=g)
+    xg, sg = x.to(cuda).requires_grad_(True), sk.to(cuda).requires_grad_(True)
+    out = mod.to(cuda).forward_residual(xg, sg)
+    cot = torch.randn(N, 9, 128, generator=g)
+    (ref,), (gref, gsref) = _vjp(lambda a, s: M.spectral_atomwise(a, P, "m.", 2, 128) + s, [x, sk], [cot])
+    assert_close(out, ref, TOL, "atom-wise+skip fwd")
+    gx, gs = torch.autograd.grad(out, (xg, sg), cot.to(cuda))
+    assert_close(gx, gref, 1e-4, "atom-wise+skip bwd x")
+    assert_close(gs, gsref, 1e-6, "atom-wise+skip bwd skip")
+
+
 def test_edge_shifts_and_permutation(cuda):
     from ops.node import edge_shifts, permute_rows
     g = torch.Generator().manual_seed(22)
