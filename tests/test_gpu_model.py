@@ -53,15 +53,19 @@ def test_cu_slab_parity(cuda):
     _check(out, ref, s.n_atoms)
 
 
-def test_water_fixture_parity(cuda):
-    """Against the committed float64 oracle fixture (tests/golden/water64_oracle.npz)."""
+@pytest.mark.parametrize("mode", [0, 1], ids=["split_bf16", "fp32"])
+def test_water_fixture_parity(cuda, mode):
+    """Against the committed float64 oracle fixture (tests/golden/water64_oracle.npz), in both
+    matrix-core modes of the fp32 contractions."""
     import os
     import systems
+    from ops import _lib
     path = os.path.join(os.path.dirname(__file__), "golden", "water64_oracle.npz")
     g = np.load(path)
     bb, hd, model = _build(cuda)
     s = systems.AtomicSystem("water64", g["pos"], g["Z"], g["cell"])
-    out = _run(model, s, g["edge_index"], g["cell_offsets"], cuda)
+    with _lib.matmul_mode(mode):
+        out = _run(model, s, g["edge_index"], g["cell_offsets"], cuda)
     ref = {k: torch.from_numpy(g[k]) for k in ("energy", "forces", "stress", "atom_energy")}
     _check(out, ref, s.n_atoms)
 
