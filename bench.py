@@ -162,18 +162,26 @@ def main() -> None:
         out = step()
         torch.cuda.synchronize()
         log(f"[bench] warm-up {k + 1}/{args.warmup}: E = {out['energy'].item():.6f}")
-    prof = None if args.no_kernel_profile else _lib.KernelProfiler()
-    _lib.set_profiler(prof)
+    # the timed steps run without instrumentation; the per-kernel roofline comes from a
+    # separate pass over the same number of steps with HIP events around every library call
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         out = step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    _lib.set_profiler(None)
     ms = 1e3 * elapsed / args.steps
     value = system.n_atoms / (elapsed / args.steps)
     log(f"[bench] timed {args.steps} steps: {ms:.3f} ms/step, {value:.1f} atom-steps/s")
+    prof = None
+    if not args.no_kernel_profile:
+        prof = _lib.KernelProfiler()
+        _lib.set_profiler(prof)
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        _lib.set_profiler(None)
+        log(f"[bench] profiled {args.steps} more steps for the per-kernel roofline")
 
     kernels = roofline.summarize(prof.durations(), mm_mode) if prof else {}
     for rec in kernels.values():
