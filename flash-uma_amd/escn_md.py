@@ -7,9 +7,11 @@ installed offline.  This module provides an object with exactly the attributes
 UMA-s, with seeded random weights, plus the node modules the reference attaches by
 reference (norm_1, norm_2, atom_wise, final norm, charge/spin embeddings).
 
-The node modules restate the FAIRChem designs from memory; their parity is unpinned (no
-reference code or fixtures exist here), so they are checked only by invariants (rotation
-equivariance, normalisation).  Their forward passes run on the gfx950 node kernels
+The node modules restate the published FAIRChem eSCN-MD designs (no FAIRChem code or
+fixtures exist here).  Their GPU forward and backward are checked against the CPU oracle's
+restatement, which is itself checked against the library routines the modules reduce to at
+lmax = 0 (LayerNorm, Linear, a Linear-SiLU-Linear MLP), hand-derived known answers and
+equivariance.  Their forward passes run on the gfx950 node kernels
 (ops/node.py: RMS norm, batched per-degree MFMA GEMM, gate activation); like the rest of
 the backbone they need GPU tensors.
 

@@ -13,7 +13,7 @@ package, and only as the checker (or the timed CPU baseline).  The product path
 (flash-uma_amd/) never imports it: it runs the HIP library or raises.
 
 Parity pins (what each function is checked against besides the HIP path) are listed in
-each module's docstring.  Functions marked "parity unpinned" have no check beyond
-self-consistency invariants because the reference code they restate (FAIRChem node
-modules) is absent from the reference tree.
+each module's docstring.  The FAIRChem node modules in model_ref.py, whose code is absent
+from the reference tree, are pinned by tests/test_oracle_node_pins.py (library routines
+they reduce to, known answers, equivariance).
 """

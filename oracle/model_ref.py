@@ -7,10 +7,13 @@ transfer_weights reads them, wrapper.py:22-85) and of the energy head.  All arit
 in the requested dtype (float64 for parity references) on the CPU, in input atom and edge
 order; the Morton permutation and edge sorting of the GPU path only change memory order.
 
-Node modules (rms_norm_sh, spectral atom-wise FFN, system embedding, energy head) restate
-the FAIRChem designs the build uses in their place; their parity is unpinned (no FAIRChem
-code or fixtures exist in the reference tree) and they are checked only by invariants
-(rotation equivariance, normalisation) in the tests.
+Node modules (rms_norm_sh, so3_linear, spectral atom-wise FFN, energy head) restate the
+published FAIRChem eSCN-MD modules (fairchem-core, which the reference's setup.sh clones at
+git main) that the reference calls at model.py:145,157,218; no FAIRChem code or fixtures
+exist in the reference tree.  tests/test_oracle_node_pins.py pins them against the library
+routines they reduce to at lmax = 0 (LayerNorm, Linear, a Linear-SiLU-Linear MLP),
+hand-derived known answers, per-module equivariance and the gate wiring; the head through
+finite differences of the energy.
 """
 from __future__ import annotations
 

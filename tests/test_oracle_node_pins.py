@@ -1,0 +1,304 @@
+"""Pins of the node-module restatements in oracle/model_ref.py (rms_norm_sh, so3_linear,
+spectral_atomwise).
+
+Their algorithms live in FAIRChem (fairchem-core, which the reference's setup.sh clones at
+git main: the eSCN-MD release line that ships uma-s-1p2), not in the reference tree, and no
+FAIRChem code or fixtures are available here.  The reference fixes only their call sites
+(model.py:145,157,218: norm_1 before the edge-wise block, norm_2 + atom_wise with a residual
+after it, the final norm).  The restatements are therefore pinned against:
+
+* library routines they reduce to in special cases: at lmax = 0 the equivariant RMS norm is
+  torch's LayerNorm over channels, SO3_Linear is torch's Linear per degree, and the l = 0
+  output of the spectral FFN is a Linear -> SiLU -> Linear MLP;
+* hand-derived known answers for the degree-balanced mean square (each degree weighs
+  1 / (lmax + 1) whatever its 2l + 1 components);
+* equivariance of every module under the Wigner matrices of random rotations (a bias or a
+  weight that differs between the m of one degree breaks it);
+* the gate wiring of the FFN: gate block l - 1 drives degree l and nothing else.
+
+Every check is also run on a planted mistake (a variant of the restatement with a plausible
+error), which it must reject.
+"""
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import model_ref as M
+from oracle import sh_ref
+
+DT = torch.float64
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _rand(*shape, seed=0):
+    return torch.randn(*shape, generator=_gen(seed), dtype=DT)
+
+
+def _rotations(n, seed):
+    q = _rand(n, 4, seed=seed)
+    q = q / q.norm(dim=1, keepdim=True)
+    w, x, y, z = q.unbind(1)
+    R = torch.stack([1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y),
+                     2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x),
+                     2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)], 1)
+    return R.reshape(n, 3, 3)
+
+
+def _wigner_blocks(R, lmax):
+    """(n, (lmax+1)^2, (lmax+1)^2) block-diagonal D^0 + D^1 + ... + D^lmax."""
+    n = R.shape[0]
+    K = (lmax + 1) ** 2
+    D = torch.zeros(n, K, K, dtype=DT)
+    for l in range(lmax + 1):
+        s = l * l
+        D[:, s:s + 2 * l + 1, s:s + 2 * l + 1] = sh_ref.wigner_from_rotation(R, l)
+    return D
+
+
+def _rotate(D, x):
+    return torch.einsum("nij,njc->nic", D, x)
+
+
+def _equivariance_error(f, lmax, C, seed):
+    x = _rand(12, (lmax + 1) ** 2, C, seed=seed)
+    D = _wigner_blocks(_rotations(12, seed + 1), lmax)
+    return (f(_rotate(D, x)) - _rotate(D, f(x))).abs().max().item()
+
+
+# --- planted mistakes (variants of the restatements, CPU only) -------------------------
+
+def _norm_unbalanced(x, weight, bias, lmax, eps):
+    """Plain mean over all (lmax+1)^2 components instead of the degree-balanced one."""
+    l0 = x[:, :1] - x[:, :1].mean(dim=2, keepdim=True)
+    feat = torch.cat([l0, x[:, 1:]], 1)
+    ms = feat.pow(2).mean(1, keepdim=True).mean(2, keepdim=True)
+    out = feat * (ms + eps).pow(-0.5) * weight[M.degree_index(lmax)][None]
+    return out + torch.cat([bias[None, None], torch.zeros(1, x.shape[1] - 1, x.shape[2], dtype=x.dtype)], 1)
+
+
+def _norm_eps_outside(x, weight, bias, lmax, eps):
+    """eps added to the root instead of under it."""
+    deg = M.degree_index(lmax)
+    l0 = x[:, :1] - x[:, :1].mean(dim=2, keepdim=True)
+    feat = torch.cat([l0, x[:, 1:]], 1)
+    w_deg = torch.tensor([1.0 / ((2 * l + 1) * (lmax + 1)) for l in deg.tolist()], dtype=x.dtype)
+    ms = (feat.pow(2) * w_deg[None, :, None]).sum(1, keepdim=True).mean(2, keepdim=True)
+    out = feat / (ms.sqrt() + eps) * weight[deg][None]
+    return out + torch.cat([bias[None, None], torch.zeros(1, x.shape[1] - 1, x.shape[2], dtype=x.dtype)], 1)
+
+
+def _norm_no_centering(x, weight, bias, lmax, eps):
+    deg = M.degree_index(lmax)
+    w_deg = torch.tensor([1.0 / ((2 * l + 1) * (lmax + 1)) for l in deg.tolist()], dtype=x.dtype)
+    ms = (x.pow(2) * w_deg[None, :, None]).sum(1, keepdim=True).mean(2, keepdim=True)
+    out = x * (ms + eps).pow(-0.5) * weight[deg][None]
+    return out + torch.cat([bias[None, None], torch.zeros(1, x.shape[1] - 1, x.shape[2], dtype=x.dtype)], 1)
+
+
+def _norm_bias_everywhere(x, weight, bias, lmax, eps):
+    return M.rms_norm_sh(x, weight, torch.zeros_like(bias), lmax, eps) + bias[None, None]
+
+
+def _so3_linear_transposed(x, weight, bias, lmax):
+    """Weight read as (in, out) instead of torch's (out, in)."""
+    deg = M.degree_index(lmax)
+    out = torch.einsum("nki,kio->nko", x, weight[deg])
+    return torch.cat([out[:, :1] + bias[None, None], out[:, 1:]], 1)
+
+
+def _so3_linear_bias_everywhere(x, weight, bias, lmax):
+    return M.so3_linear(x, weight, torch.zeros_like(bias), lmax) + bias[None, None]
+
+
+# --- equivariant RMS norm ------------------------------------------------------------------
+
+@pytest.mark.parametrize("eps", [1e-5, 0.3])
+def test_rms_norm_sh_lmax0_is_layer_norm(eps):
+    """lmax = 0: centring over channels, mean square over channels (biased), eps under the
+    root, per-channel weight and bias -- exactly torch's LayerNorm."""
+    C = 24
+    x = _rand(50, 1, C, seed=1) * 3 + 0.7
+    w = _rand(1, C, seed=2)
+    b = _rand(C, seed=3)
+    ref = F.layer_norm(x[:, 0], (C,), w[0], b, eps)
+    assert (M.rms_norm_sh(x, w, b, 0, eps)[:, 0] - ref).abs().max() < 1e-13
+    assert (_norm_no_centering(x, w, b, 0, eps)[:, 0] - ref).abs().max() > 1e-3
+    if eps > 0.1:  # where eps sits only shows at a large eps
+        assert (_norm_eps_outside(x, w, b, 0, eps)[:, 0] - ref).abs().max() > 1e-3
+
+
+def test_rms_norm_sh_degree_balance_known_answers():
+    """lmax = 2, C = 4, eps = 0, unit weights, zero bias.  The degree-balanced mean square is
+    (1/3) * sum_l mean_{m, c} x_{l m c}^2 (each degree 1/(lmax+1), each of its 2l+1
+    components 1/(2l+1)); the l = 0 row is centred over channels first."""
+    L, C = 2, 4
+    w = torch.ones(L + 1, C, dtype=DT)
+    b = torch.zeros(C, dtype=DT)
+
+    def case(blocks):
+        x = torch.zeros(1, 9, C, dtype=DT)
+        for l, v in blocks.items():
+            x[0, l * l:(l + 1) ** 2] = v
+        return x
+
+    # degree 2 only, all ones: mean square 1/3 -> scale sqrt(3)
+    x = case({2: 1.0})
+    assert (M.rms_norm_sh(x, w, b, L, 0.0) - math.sqrt(3.0) * x).abs().max() < 1e-14
+    assert (_norm_unbalanced(x, w, b, L, 0.0) - math.sqrt(3.0) * x).abs().max() > 0.1
+    # degree 1 only, all ones: also 1/3 -> sqrt(3)
+    x = case({1: 1.0})
+    assert (M.rms_norm_sh(x, w, b, L, 0.0) - math.sqrt(3.0) * x).abs().max() < 1e-14
+    # degree 1 = 1, degree 2 = 2: (1 + 4) / 3 -> scale sqrt(3/5)
+    x = case({1: 1.0, 2: 2.0})
+    assert (M.rms_norm_sh(x, w, b, L, 0.0) - math.sqrt(0.6) * x).abs().max() < 1e-14
+    # l = 0 row (1, 2, 3, 4): centred (-1.5, -0.5, 0.5, 1.5), mean square 1.25 / 3
+    x = torch.zeros(1, 9, C, dtype=DT)
+    x[0, 0] = torch.tensor([1.0, 2.0, 3.0, 4.0], dtype=DT)
+    want = torch.zeros_like(x)
+    want[0, 0] = torch.tensor([-1.5, -0.5, 0.5, 1.5], dtype=DT) * math.sqrt(3.0 / 1.25)
+    assert (M.rms_norm_sh(x, w, b, L, 0.0) - want).abs().max() < 1e-14
+    assert (_norm_no_centering(x, w, b, L, 0.0) - want).abs().max() > 0.1
+
+
+def test_rms_norm_sh_affine_per_degree():
+    """The weight is one row per degree, shared by the 2l+1 components; the bias is on
+    l = 0 only.  With a single nonzero degree the output is that degree's weight row times
+    the unit-affine output."""
+    L, C = 3, 5
+    x = _rand(7, (L + 1) ** 2, C, seed=4)
+    w = _rand(L + 1, C, seed=5)
+    b = _rand(C, seed=6)
+    unit = M.rms_norm_sh(x, torch.ones_like(w), torch.zeros_like(b), L, 1e-5)
+    out = M.rms_norm_sh(x, w, b, L, 1e-5)
+    for l in range(L + 1):
+        s = slice(l * l, (l + 1) ** 2)
+        want = unit[:, s] * w[l][None, None] + (b[None, None] if l == 0 else 0)
+        assert (out[:, s] - want).abs().max() < 1e-13
+
+
+@pytest.mark.parametrize("lmax", [1, 2, 4])
+def test_rms_norm_sh_equivariant(lmax):
+    C = 6
+    w = _rand(lmax + 1, C, seed=7)
+    b = _rand(C, seed=8)
+    assert _equivariance_error(lambda x: M.rms_norm_sh(x, w, b, lmax, 1e-5), lmax, C, 9) < 1e-12
+    assert _equivariance_error(lambda x: _norm_bias_everywhere(x, w, b, lmax, 1e-5), lmax, C, 9) > 1e-3
+
+
+# --- SO3_Linear ----------------------------------------------------------------------------
+
+def test_so3_linear_is_torch_linear_per_degree():
+    """Weight (lmax+1, out, in) applied as torch's Linear (y = x W^T) to every component of
+    degree l with W[l]; the bias on l = 0 only.  in != out so a transposed operand cannot
+    even be applied."""
+    L, Cin, Cout = 2, 6, 5
+    x = _rand(9, (L + 1) ** 2, Cin, seed=10)
+    W = _rand(L + 1, Cout, Cin, seed=11)
+    b = _rand(Cout, seed=12)
+    out = M.so3_linear(x, W, b, L)
+    assert out.shape == (9, 9, Cout)
+    for k, l in enumerate(M.degree_index(L).tolist()):
+        want = F.linear(x[:, k], W[l], b if k == 0 else None)
+        assert (out[:, k] - want).abs().max() < 1e-13
+    with pytest.raises(RuntimeError):
+        _so3_linear_transposed(x, W, b, L)
+
+
+@pytest.mark.parametrize("lmax", [2, 4])
+def test_so3_linear_equivariant(lmax):
+    W = _rand(lmax + 1, 7, 6, seed=13)
+    b = _rand(7, seed=14)
+    assert _equivariance_error(lambda x: M.so3_linear(x, W, b, lmax), lmax, 6, 15) < 1e-12
+    assert _equivariance_error(lambda x: _so3_linear_bias_everywhere(x, W, b, lmax), lmax, 6, 15) > 1e-3
+
+
+# --- SpectralAtomwise FFN ------------------------------------------------------------------
+
+def _ffn_params(L, C, H, seed):
+    return {
+        "f.scalar_mlp.0.weight": _rand(L * H, C, seed=seed),
+        "f.scalar_mlp.0.bias": _rand(L * H, seed=seed + 1),
+        "f.so3_linear_1.weight": _rand(L + 1, H, C, seed=seed + 2) / math.sqrt(C),
+        "f.so3_linear_1.bias": _rand(H, seed=seed + 3),
+        "f.so3_linear_2.weight": _rand(L + 1, C, H, seed=seed + 4) / math.sqrt(H),
+        "f.so3_linear_2.bias": _rand(C, seed=seed + 5),
+    }
+
+
+def test_spectral_atomwise_l0_is_mlp():
+    """The l = 0 output is torch's Linear(C, H) -> SiLU -> Linear(H, C) on the l = 0 input,
+    whatever the gates and the l > 0 inputs."""
+    L, C, H = 2, 8, 12
+    P = _ffn_params(L, C, H, 20)
+    x = _rand(10, 9, C, seed=30)
+    mlp = torch.nn.Sequential(torch.nn.Linear(C, H), torch.nn.SiLU(), torch.nn.Linear(H, C)).to(DT)
+    with torch.no_grad():
+        mlp[0].weight.copy_(P["f.so3_linear_1.weight"][0])
+        mlp[0].bias.copy_(P["f.so3_linear_1.bias"])
+        mlp[2].weight.copy_(P["f.so3_linear_2.weight"][0])
+        mlp[2].bias.copy_(P["f.so3_linear_2.bias"])
+        want = mlp(x[:, 0])
+    out = M.spectral_atomwise(x, P, "f.", L, H)
+    assert (out[:, 0] - want).abs().max() < 1e-13
+    x2 = x.clone()
+    x2[:, 1:] = _rand(10, 8, C, seed=31)
+    assert (M.spectral_atomwise(x2, P, "f.", L, H)[:, 0] - want).abs().max() < 1e-13
+
+
+def test_spectral_atomwise_gate_wiring():
+    """scalar_mlp rows (l-1) H .. l H - 1 gate degree l: changing them changes degree l only.
+    Degree-l output depends on degree-l input only (no bias on l > 0)."""
+    L, C, H = 3, 6, 4
+    P = _ffn_params(L, C, H, 40)
+    x = _rand(8, (L + 1) ** 2, C, seed=50)
+    base = M.spectral_atomwise(x, P, "f.", L, H)
+    for l in range(1, L + 1):
+        Q = dict(P)
+        Wg = P["f.scalar_mlp.0.weight"].clone()
+        Wg[(l - 1) * H:l * H] += _rand(H, C, seed=60 + l)
+        Q["f.scalar_mlp.0.weight"] = Wg
+        out = M.spectral_atomwise(x, Q, "f.", L, H)
+        for k in range(L + 1):
+            s = slice(k * k, (k + 1) ** 2)
+            diff = (out[:, s] - base[:, s]).abs().max().item()
+            if k == l:
+                assert diff > 1e-3
+            else:
+                assert diff < 1e-14
+    for l in range(1, L + 1):
+        x0 = x.clone()
+        x0[:, l * l:(l + 1) ** 2] = 0
+        out = M.spectral_atomwise(x0, P, "f.", L, H)
+        assert out[:, l * l:(l + 1) ** 2].abs().max() < 1e-14
+
+
+def test_spectral_atomwise_gate_is_sigmoid_of_silu():
+    """One channel, lmax = 1, identity SO3 linears, zero scalar weights: the degree-1 output
+    is x_1 * sigmoid(silu(b)) for gate bias b, and the l = 0 output is silu(x_0)."""
+    L, C, H = 1, 1, 1
+    P = {
+        "f.scalar_mlp.0.weight": torch.zeros(1, 1, dtype=DT),
+        "f.scalar_mlp.0.bias": torch.tensor([0.8], dtype=DT),
+        "f.so3_linear_1.weight": torch.ones(2, 1, 1, dtype=DT),
+        "f.so3_linear_1.bias": torch.zeros(1, dtype=DT),
+        "f.so3_linear_2.weight": torch.ones(2, 1, 1, dtype=DT),
+        "f.so3_linear_2.bias": torch.zeros(1, dtype=DT),
+    }
+    x = torch.tensor([[[0.5], [1.0], [-2.0], [3.0]]], dtype=DT)
+    out = M.spectral_atomwise(x, P, "f.", L, H)
+    silu_b = 0.8 / (1 + math.exp(-0.8))
+    g = 1 / (1 + math.exp(-silu_b))
+    want = torch.tensor([[[0.5 / (1 + math.exp(-0.5))], [g], [-2 * g], [3 * g]]], dtype=DT)
+    assert (out - want).abs().max() < 1e-15
+
+
+@pytest.mark.parametrize("lmax", [2, 4])
+def test_spectral_atomwise_equivariant(lmax):
+    C, H = 6, 5
+    P = _ffn_params(lmax, C, H, 70)
+    assert _equivariance_error(lambda x: M.spectral_atomwise(x, P, "f.", lmax, H), lmax, C, 80) < 1e-12
