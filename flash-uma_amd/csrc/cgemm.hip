@@ -405,10 +405,11 @@ static int complex_check(const float* A_r, const float* A_i, int64_t lda, const 
     return set_error(FU_ERR_UNSUPPORTED, "%s: Kc=%d, lda=%lld, ldw=%lld must be multiples of 4", who, Kc,
                      (long long)lda, (long long)ldw);
   if (lda < Kc || ldw < Kc || ldy < Nc) return set_error(FU_ERR_SHAPE, "%s: leading dimensions smaller than the rows", who);
+  if (Nc % 4 != 0 || ldy % 4 != 0) return set_error(FU_ERR_UNSUPPORTED, "%s: Nc and ldy must be multiples of 4", who);
+  if (M == 0) return FU_OK;  // no rows: the operands may be empty (NULL) arrays
   if (!A_r || !A_i || !P || !Q || !Y_r || !Y_i) return set_error(FU_ERR_NULL, "%s: NULL operand", who);
   if (!aligned16(A_r) || !aligned16(A_i) || !aligned16(P) || !aligned16(Q) || !aligned16(Y_r) || !aligned16(Y_i))
     return set_error(FU_ERR_ALIGN, "%s: operands must be 16-byte aligned", who);
-  if (Nc % 4 != 0 || ldy % 4 != 0) return set_error(FU_ERR_UNSUPPORTED, "%s: Nc and ldy must be multiples of 4", who);
   const int64_t total = ((M + CBM - 1) / CBM) * ((Nc + CBN - 1) / CBN);
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
   return FU_OK;
@@ -495,11 +496,11 @@ extern "C" int fu_complex_linear_gate(const float* A_r, const float* A_i, int64_
   const char* who = "fu_complex_linear_gate";
   int st = complex_check(A_r, A_i, lda, P, Q, ldw, Y_r, Y_i, ldy, M, Nc, Kc, who);
   if (st != FU_OK) return st;
-  if (!Z_r || !Z_i || !S) return set_error(FU_ERR_NULL, "%s: NULL gate operand", who);
   if (ldz < Nc || s_off < 0 || lds < s_off + Nc) return set_error(FU_ERR_SHAPE, "%s: gate strides too small", who);
+  if (M == 0) return FU_OK;
+  if (!Z_r || !Z_i || !S) return set_error(FU_ERR_NULL, "%s: NULL gate operand", who);
   if ((ldz | lds | s_off) % 4 != 0 || !aligned16(Z_r) || !aligned16(Z_i) || !aligned16(S))
     return set_error(FU_ERR_ALIGN, "%s: gate operands must be 16-byte aligned with strides multiples of 4", who);
-  if (M == 0) return FU_OK;
   return complex_launch<1>(A_r, A_i, lda, P, Q, ldw, W3, Y_r, Y_i, ldy, M, Nc, Kc,
                            CGate{Z_r, Z_i, ldz, S, lds, s_off, nullptr, nullptr, 0, nullptr, 0}, stream, who);
 }
@@ -513,12 +514,12 @@ extern "C" int fu_complex_linear_gate_bwd(const float* A_r, const float* A_i, in
   const char* who = "fu_complex_linear_gate_bwd";
   int st = complex_check(A_r, A_i, lda, P, Q, ldw, gY_r, gY_i, ldg, M, Nc, Kc, who);
   if (st != FU_OK) return st;
-  if (!F_r || !F_i || !S || !Pout) return set_error(FU_ERR_NULL, "%s: NULL gate operand", who);
   if (ldf < Nc || ldp < Nc || s_off < 0 || lds < s_off + Nc)
     return set_error(FU_ERR_SHAPE, "%s: gate strides too small", who);
+  if (M == 0) return FU_OK;
+  if (!F_r || !F_i || !S || !Pout) return set_error(FU_ERR_NULL, "%s: NULL gate operand", who);
   if ((ldf | ldp | lds | s_off) % 4 != 0 || !aligned16(F_r) || !aligned16(F_i) || !aligned16(S) || !aligned16(Pout))
     return set_error(FU_ERR_ALIGN, "%s: gate operands must be 16-byte aligned with strides multiples of 4", who);
-  if (M == 0) return FU_OK;
   return complex_launch<2>(A_r, A_i, lda, P, Q, ldw, W3, gY_r, gY_i, ldg, M, Nc, Kc,
                            CGate{nullptr, nullptr, 0, S, lds, s_off, F_r, F_i, ldf, Pout, ldp}, stream, who);
 }

@@ -867,7 +867,7 @@ static int gating_lmax_check(const void* const* ptrs, int n, int64_t E, int32_t 
   if (E < 0 || C <= 0) return set_error(FU_ERR_SHAPE, "%s: bad shape E=%lld C=%d", who, (long long)E, C);
   if (C % 4 != 0) return set_error(FU_ERR_UNSUPPORTED, "%s: C=%d must be a multiple of 4", who, C);
   if (lmax < 2 || lmax > 4) return set_error(FU_ERR_UNSUPPORTED, "%s: lmax=%d unsupported (2, 3 or 4)", who, lmax);
-  for (int k = 0; k < n; ++k) {
+  for (int k = 0; k < n && E > 0; ++k) {
     if (ptrs[k] == nullptr) return set_error(FU_ERR_NULL, "%s: pointer %d is NULL", who, k);
     if (!aligned16(ptrs[k])) return set_error(FU_ERR_ALIGN, "%s: pointer %d not 16-byte aligned", who, k);
   }

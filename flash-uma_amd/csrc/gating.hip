@@ -142,7 +142,7 @@ static int gating_check(const void* const* ptrs, int n, int64_t E, int32_t C, in
   if (layout != 0 && layout != 1) return set_error(FU_ERR_UNSUPPORTED, "%s: layout %d", who, layout);
   if (layout == 1 && C % 64 != 0)
     return set_error(FU_ERR_UNSUPPORTED, "%s: the gate-paired layout needs C a multiple of 64", who);
-  for (int k = 0; k < n; ++k) {
+  for (int k = 0; k < n && E > 0; ++k) {
     if (ptrs[k] == nullptr) return set_error(FU_ERR_NULL, "%s: pointer %d is NULL", who, k);
     if (!aligned16(ptrs[k])) return set_error(FU_ERR_ALIGN, "%s: pointer %d not 16-byte aligned", who, k);
   }

@@ -413,6 +413,7 @@ static int linear_check(const float* A, int64_t lda, const float* W, int64_t ldw
   if (N % 4 != 0 || ldy % 4 != 0)
     return set_error(FU_ERR_UNSUPPORTED, "%s: N=%d and ldy=%lld must be multiples of 4", who, N, (long long)ldy);
   if (lda < K || ldw < K || ldy < N) return set_error(FU_ERR_SHAPE, "%s: leading dimensions smaller than the rows", who);
+  if (M == 0) return FU_OK;  // no rows: the operands may be empty (NULL) arrays
   if (!A || !W || !Y) return set_error(FU_ERR_NULL, "%s: NULL operand", who);
   if (!aligned16(A) || !aligned16(W) || !aligned16(Y))
     return set_error(FU_ERR_ALIGN, "%s: operands must be 16-byte aligned", who);
@@ -466,11 +467,11 @@ extern "C" int fu_linear_gate(const float* A, int64_t lda, const float* W, int64
   const int32_t N = (2 * lmax + 1) * C;
   int st = linear_check(A, lda, W, ldw, Y, ldy, M, N, K, who);
   if (st != FU_OK) return st;
-  if (!Z || !S) return set_error(FU_ERR_NULL, "%s: NULL output", who);
   if (ldz < (lmax + 1) * C || lds < lmax * C) return set_error(FU_ERR_SHAPE, "%s: Z / S row strides too small", who);
+  if (M == 0) return FU_OK;
+  if (!Z || !S) return set_error(FU_ERR_NULL, "%s: NULL output", who);
   if (ldz % 4 != 0 || lds % 4 != 0 || !aligned16(Z) || !aligned16(S) || (bias && !aligned16(bias)))
     return set_error(FU_ERR_ALIGN, "%s: Z, S and bias must be 16-byte aligned with row strides multiples of 4", who);
-  if (M == 0) return FU_OK;
   const int n_tiles = (N + GBN - 1) / GBN;
   const int64_t total = ((M + GBM - 1) / GBM) * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
@@ -495,10 +496,10 @@ extern "C" int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* W
   if (ldg < (2 * lmax + 1) * C || ldy0 < (2 * lmax + 1) * C || lds < lmax * C || ldp1 < lmax * C ||
       ldp2 < (lmax - 1) * C)
     return set_error(FU_ERR_SHAPE, "%s: row strides too small", who);
+  if (M == 0) return FU_OK;
   if (!Y0 || !S || !P1 || !P2) return set_error(FU_ERR_NULL, "%s: NULL operand", who);
   if ((ldy0 | lds | ldp1 | ldp2) % 4 != 0 || !aligned16(Y0) || !aligned16(S) || !aligned16(P1) || !aligned16(P2))
     return set_error(FU_ERR_ALIGN, "%s: operands must be 16-byte aligned with row strides multiples of 4", who);
-  if (M == 0) return FU_OK;
   const int n_tiles = (N + GBN - 1) / GBN;
   const int64_t total = ((M + GBM - 1) / GBM) * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);

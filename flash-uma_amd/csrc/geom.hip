@@ -374,10 +374,10 @@ extern "C" int fu_geom_fwd(const float* pos, const int64_t* Z, const int64_t* id
     return set_error(FU_ERR_NULL, "fu_geom_fwd: W_src and W_tgt must both be given or both NULL");
   const int width = W_src ? B + 2 * C : B;
   if (ld_xe < width) return set_error(FU_ERR_SHAPE, "fu_geom_fwd: ld_xe=%lld < row width %d", (long long)ld_xe, width);
-  if (!pos || !idx_i || !idx_j || !shifts || !offset_g || !x_edge_raw || !wigner || !env || (W_src && !Z))
-    return set_error(FU_ERR_NULL, "fu_geom_fwd: NULL argument");
   if (!(cutoff > 0.0f)) return set_error(FU_ERR_SHAPE, "fu_geom_fwd: cutoff must be > 0");
   if (E == 0) return FU_OK;
+  if (!pos || !idx_i || !idx_j || !shifts || !offset_g || !x_edge_raw || !wigner || !env || (W_src && !Z))
+    return set_error(FU_ERR_NULL, "fu_geom_fwd: NULL argument");
   hipLaunchKernelGGL(geom_fwd_kernel, dim3(cdiv(E, GEOM_BLOCK)), dim3(GEOM_BLOCK), 0, as_stream(stream), pos, Z,
                      idx_i, idx_j, shifts, W_src, W_tgt, offset_g, x_edge_raw, ld_xe, wigner, env, E, B, C, cutoff,
                      coeff_g);
@@ -390,8 +390,8 @@ extern "C" int fu_geom_bwd(const float* pos, const int64_t* idx_i, const int64_t
                            float coeff_g, void* stream) {
   if (E < 0 || N < 0 || B <= 0 || B > 256) return set_error(FU_ERR_SHAPE, "fu_geom_bwd: bad shape (B must be 1..256)");
   if (g_x_edge_raw && ld_gxe < B) return set_error(FU_ERR_SHAPE, "fu_geom_bwd: ld_gxe < B");
-  if (!pos || !idx_i || !idx_j || !shifts || !offset_g || !g_d) return set_error(FU_ERR_NULL, "fu_geom_bwd: NULL argument");
   if (E == 0) return FU_OK;
+  if (!pos || !idx_i || !idx_j || !shifts || !offset_g || !g_d) return set_error(FU_ERR_NULL, "fu_geom_bwd: NULL argument");
   const size_t lds = sizeof(float) * (GEOM_BLOCK * 34 + GEOM_BLOCK * (B + 1));
   hipLaunchKernelGGL(geom_bwd_kernel, dim3(cdiv(E, GEOM_BLOCK)), dim3(GEOM_BLOCK), lds, as_stream(stream), pos, idx_i,
                      idx_j, shifts, offset_g, g_x_edge_raw, ld_gxe, g_wigner, g_env, g_d, E, B, cutoff, coeff_g);

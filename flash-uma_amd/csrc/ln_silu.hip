@@ -144,7 +144,7 @@ static int ln_check(const LnArgs& a, int64_t ld_out, int32_t D, const char* who)
   if (a.ldx < (int64_t)a.G * D || ld_out < (int64_t)a.G * D) return set_error(FU_ERR_SHAPE, "%s: row stride < G*D", who);
   if ((a.ldx | ld_out) % 4 != 0 || (a.tab_src && a.ldt % 4 != 0))
     return set_error(FU_ERR_ALIGN, "%s: row strides must be multiples of 4", who);
-  if ((a.tab_src == nullptr) != (a.tab_dst == nullptr) || (a.tab_src && (!a.z || !a.isrc || !a.idst)))
+  if ((a.tab_src == nullptr) != (a.tab_dst == nullptr) || (a.tab_src && a.M > 0 && (!a.z || !a.isrc || !a.idst)))
     return set_error(FU_ERR_NULL, "%s: tables need both sides and their element ids", who);
   if (a.M > 0 && (!a.x || !a.gamma || !a.beta)) return set_error(FU_ERR_NULL, "%s: NULL argument", who);
   const void* al[] = {a.x, a.tab_src, a.tab_dst, a.bias, a.gamma, a.beta};

@@ -9,6 +9,10 @@
  *   - Sizes are int64_t (E, N, M) or int32_t (channel widths).  Edge-feature offsets are
  *     computed in 64 bits, so E * row_width may exceed 2^31.
  *   - `stream` is a hipStream_t passed as void*; work is only enqueued, never awaited.
+ *   - Zero rows: with E = 0 (or M, n = 0) an entry point writes only what it owes per
+ *     node (a scatter's residual copy, a zeroed node gradient, a CSR of zeros) and arrays
+ *     sized by the zero count may be NULL, as the storage of an empty torch tensor is.
+ *     An isolated atom or a graph without edges therefore needs no special casing.
  *   - No entry point allocates memory.  Scratch space, where needed, is an argument.
  *   - Return value: FU_OK (0) or a negative FU_ERR_* code; fu_last_error() returns the
  *     message of the last failure on the calling host thread.

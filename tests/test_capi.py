@@ -71,6 +71,52 @@ def test_zero_sized_calls_are_no_ops():
     assert st == 0
 
 
+def test_zero_rows_accept_empty_arrays():
+    """A graph without edges hands the per-edge entry points empty torch tensors, whose
+    storage pointer is NULL: with zero rows every such call is a no-op returning FU_OK, while
+    the shape checks still apply."""
+    f = ctypes.c_float
+    calls = {
+        "fu_geom_fwd": (*([None] * 9), 8, None, None, 0, 5, 8, 0, f(6.0), f(-1.0), None),
+        "fu_geom_bwd": (*([None] * 6), 8, None, None, None, 0, 5, 8, f(6.0), f(-1.0), None),
+        "fu_gating_fwd": (*([None] * 6), 0, 128, 1, None),
+        "fu_gating_bwd": (*([None] * 9), 0, 128, 1, None),
+        "fu_linear": (None, 16, None, 16, None, None, 16, 0, 16, 16, None),
+        "fu_linear_batched": (None, 640, 128, None, 128, 16384, None, 128, 5, None, 0, 0, None, 640, 128, 0, 128,
+                              128, 5, None),
+        "fu_linear_gate": (None, 768, None, 768, None, None, 640, None, 384, None, 256, 0, 128, 768, 2, None),
+        "fu_linear_gate_bwd": (None, 384, None, 384, None, 640, None, 256, None, 256, None, 128, None, 640, 0, 128,
+                               384, 2, None),
+        "fu_complex_linear": (None, None, 256, None, None, 256, None, None, None, 128, 0, 128, 256, None),
+        "fu_complex_linear_gate": (None, None, 256, None, None, 256, None, None, None, 128, None, None, 128, None,
+                                   256, 0, 0, 128, 256, None),
+        "fu_complex_linear_gate_bwd": (None, None, 256, None, None, 256, None, None, None, 128, None, None, 128,
+                                       None, 256, 0, None, 128, 0, 128, 256, None),
+        # element tables present (a weight), per-edge element ids empty
+        "fu_ln_silu_grouped_fwd": (None, 640, 16, 16, 128, 16, None, None, None, None, None, None, 640, None, None, 0,
+                                   5, 128, f(1e-7), None),
+        "fu_ln_silu_grouped_bwd": (None, 640, 16, 16, 128, 16, None, None, None, None, None, None, None, None, 640,
+                                   None, 640, 0, 5, 128, None),
+        "fu_scatter_bwd": (*([None] * 12), 0, 5, 128, None),
+        "fu_init_scatter_bwd": (*([None] * 8), 0, 5, 128, None),
+        "fu_gather_fwd": (*([None] * 10), 0, 5, 1, 128, 1, None),
+        "fu_edge_shifts": (None, None, None, None, 0, None),
+        "fu_wigner_ext_fwd": (None, None, 0, 4, None),
+        "fu_wigner_ext_bwd": (None, None, None, 0, 4, None),
+        "fu_gating_fwd_lmax": (*([None] * 6), 0, 128, 4, None),
+        "fu_scatter_bwd_lmax": (*([None] * 14), 0, 5, 128, 4, None),
+    }
+    for name, args in calls.items():
+        st, msg = _status(name, *args)
+        assert st == 0, (name, msg)
+    # the shape checks still run with zero rows
+    st, _ = _status("fu_linear", None, 16, None, 16, None, None, 16, 0, 16, 6, None)
+    assert st == -2
+    st, _ = _status("fu_complex_linear_gate", None, None, 256, None, None, 256, None, None, None, 128, None, None,
+                    64, None, 256, 0, 0, 128, 256, None)
+    assert st == -1
+
+
 def test_product_raises_without_gpu_tensors():
     """The op layer has no CPU fallback: CPU tensors are rejected loudly."""
     import torch

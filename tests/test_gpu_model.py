@@ -161,3 +161,38 @@ def test_inplace_edge_index_edit_invalidates_topology(cuda):
     assert torch.equal(after["energy"].detach().cpu(), fresh["energy"])
     assert torch.equal(after["forces"].detach().cpu(), fresh["forces"])
     assert not torch.equal(before, fresh["energy"])
+
+
+def _lone_atom_systems():
+    import systems
+    s = systems.cu_slab_co()
+    cell = s.cell.copy()
+    cell[2, 2] = 40.0
+    # a Fe atom 12 A above the CO and 21 A below the slab's periodic image: no neighbour
+    pos = np.concatenate([s.pos, np.array([[1.0, 2.0, 27.0]], dtype=np.float32)])
+    Z = np.concatenate([s.Z, np.array([26])])
+    lone = systems.AtomicSystem("cu_slab_co_lone_fe", pos, Z, cell)
+    single = systems.AtomicSystem("single_cu", np.array([[1.0, 1.0, 1.0]], dtype=np.float32), np.array([29]),
+                                  np.eye(3, dtype=np.float32) * 10.0)
+    return {"lone_atom": lone, "no_edges": single}
+
+
+@pytest.mark.parametrize("case", ["lone_atom", "no_edges"])
+def test_atoms_without_neighbours(cuda, case):
+    """An atom with no neighbour within the cutoff (empty receiver and sender segments) and a
+    one-atom system whose graph has no edges at all (E = 0: every per-edge array is empty
+    and every per-edge launch is skipped): energy, forces and stress match the float64
+    oracle, and an atom without neighbours feels exactly zero force."""
+    import systems
+    from oracle.model_ref import energy_forces_stress
+    bb, hd, model = _build(cuda)
+    s = _lone_atom_systems()[case]
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, bb.cutoff, bb.max_neighbors)
+    assert not (ei == s.n_atoms - 1).any()
+    print(case, "atoms", s.n_atoms, "edges", ei.shape[1], flush=True)
+    out = _run(model, s, ei, off, cuda)
+    ref = energy_forces_stress(bb.cpu(), hd.cpu(), s.pos, s.Z, s.cell, ei, off, dtype=torch.float64)
+    _check(out, ref, s.n_atoms)
+    assert torch.equal(out["forces"][-1], torch.zeros(3))
+    if case == "no_edges":
+        assert torch.equal(out["stress"], torch.zeros(1, 3, 3))
