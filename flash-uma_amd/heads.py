@@ -64,12 +64,17 @@ class PotentialModel(nn.Module):
             p.requires_grad_(False)
 
     def forward(self, data, compute_forces: bool = True, compute_stress: bool = False, natoms=None) -> dict:
-        """natoms: atoms per system as a host list (read from data.natoms when omitted; passing
-        it avoids a device-to-host copy, which graph capture requires)."""
+        """natoms: atoms per system as a host list.  When omitted it is the atom count for a
+        single system (known on the host) and data.natoms read back otherwise; that read is a
+        device-to-host copy, which stalls the launch queue mid-step and which graph capture
+        forbids, so batched callers on a hot loop pass natoms."""
         emb = self.backbone(data)
         e_atom = self.head.atom_energy(emb["node_embedding"])
         if natoms is None:
-            natoms = [int(n) for n in data.natoms.tolist()]
+            if data.natoms.numel() == 1:
+                natoms = [int(data.pos.shape[0])]
+            else:
+                natoms = [int(n) for n in data.natoms.tolist()]
         energy = system_sum(e_atom, natoms)
         out = {"energy": energy, "atom_energy": e_atom, "node_embedding": emb["node_embedding"]}
         if compute_forces or compute_stress:
