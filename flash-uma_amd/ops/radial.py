@@ -98,16 +98,23 @@ class RadialBank(torch.nn.Module):
             reg(f"W3_{k}_t", m[8].t())
             reg(f"b3_{k}", m[9])
 
-    # below this many edges the output layers stay on the caller's stream: the events and
-    # stream bookkeeping cost more host time than the overlap saves on a small graph
+    # Below SIDE_STREAM_MIN_EDGES the output layers stay on the caller's stream: the events
+    # and stream bookkeeping cost more host time than the overlap saves on a small graph.
+    # Above SIDE_STREAM_MAX_EDGES they stay there too: the side stream's allocations form a
+    # second caching-allocator pool, and on a graph whose step needs a large share of HBM
+    # (50,000 atoms / 1.5 M edges: 138 GiB allocated, over 216 GiB reserved with two pools,
+    # 151 GiB with one) the reserve approaches the card's capacity and the allocator starts
+    # freeing and re-mapping memory inside the step (up to twice the step time), while the
+    # overlap itself is worth under 1 % there.
     SIDE_STREAM_MIN_EDGES = 100_000
+    SIDE_STREAM_MAX_EDGES = 600_000
 
     def forward(self, gauss, Z, idx_i, idx_j, streams: bool = True):
         """gauss (E, B) -> tuple of G radial outputs (E, n_k).
 
         The trunk (first two layers of all MLPs) runs on the current stream.  Each block's
-        output layer is its own autograd node launched on a side stream (streams=True and at
-        least SIDE_STREAM_MIN_EDGES edges), so
+        output layer is its own autograd node launched on a side stream (streams=True and
+        SIDE_STREAM_MIN_EDGES to SIDE_STREAM_MAX_EDGES edges), so
         blocks 2..G are computed while the caller already consumes block 1, and in the
         backward each block's input gradient runs as soon as its output gradient exists,
         concurrently with the caller's remaining backward: the autograd engine runs every
@@ -116,7 +123,7 @@ class RadialBank(torch.nn.Module):
         holder = _GradHolder()
         h2s = _RadialTrunkFn.apply(gauss, Z, idx_i, idx_j, self, holder)
         main = torch.cuda.current_stream(gauss.device)
-        use_side = streams and gauss.shape[0] >= self.SIDE_STREAM_MIN_EDGES
+        use_side = streams and self.SIDE_STREAM_MIN_EDGES <= gauss.shape[0] <= self.SIDE_STREAM_MAX_EDGES
         side = self._side_stream(gauss.device) if use_side else main
         cross = side is not main
         outs, self._events = [], []
