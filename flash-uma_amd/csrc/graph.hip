@@ -8,7 +8,9 @@
 
 namespace fu {
 
-// Spread the low 10 bits of v so that bit k lands on bit 3k (model.py:48-54).
+// Spread the low 10 bits of v so that bit k lands on bit 3k.  The key places the x, y, z cell
+// indices at 3k + 1, 3k + 2, 3k + 3, as the reference's helpers do (their spread has a fifth
+// step that lifts bit 3k to 3k + 1, model.py:48-58), so keys equal the reference's bit for bit.
 __device__ __forceinline__ int64_t spread3(int64_t v) {
   v &= 0x3ff;
   int64_t r = 0;
@@ -63,7 +65,7 @@ __global__ __launch_bounds__(1024) void morton_keys_kernel(const float* __restri
     for (int d = 0; d < 3; ++d) {
       const float sub = __fsub_rn(pos[3 * n + d], lo[d]);
       const int q = (int)__fmul_rn(sub, scale[d]);
-      code |= spread3(q) << d;
+      code |= spread3(q) << (d + 1);
     }
     keys[n] = code | (batch[n] << 32);
   }

@@ -71,6 +71,21 @@ def clear_csr_cache():
     clear_topology_cache()
 
 
+def expand_bits_torch(v: torch.Tensor) -> torch.Tensor:
+    """Bit k (k < 10) of the integer tensor v moved to bit 3k + 1 (model.py:48-54)."""
+    out = torch.zeros_like(v)
+    for k in range(10):
+        out |= ((v >> k) & 1) << (3 * k + 1)
+    return out
+
+
+def morton3d_torch(x: torch.Tensor, y: torch.Tensor, z: torch.Tensor) -> torch.Tensor:
+    """Morton code of 10-bit cell indices: x on bits 3k+1, y on 3k+2, z on 3k+3
+    (model.py:56-58).  The model computes its sort keys with fu_morton_keys on the GPU; this
+    is the reference's public helper, for callers that build keys themselves."""
+    return expand_bits_torch(x) | (expand_bits_torch(y) << 1) | (expand_bits_torch(z) << 2)
+
+
 def reorder_graph_morton(pos, Z, batch, idx_i, idx_j):
     """Morton Z-order of the atoms and remapped edge endpoints (model.py:60-74).
     Returns (pos[perm], Z[perm], batch[perm], inv[idx_i], inv[idx_j], perm, inv)."""

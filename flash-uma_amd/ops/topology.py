@@ -66,7 +66,7 @@ def morton_permutation(pos: torch.Tensor, batch: torch.Tensor):
     keys = torch.empty(N, dtype=torch.int64, device=dev)
     _lib.call("fu_morton_keys", pos.data_ptr(), batch.data_ptr(), keys.data_ptr(), N, st)
     n_sys = int(batch.max().item()) + 1 if N > 0 else 1
-    end_bit = 30 if n_sys == 1 else 32 + _bits_for(n_sys)
+    end_bit = 31 if n_sys == 1 else 32 + _bits_for(n_sys)   # Morton codes occupy bits 1..30
     ar = torch.arange(N, dtype=torch.int64, device=dev)
     _, perm = sort_pairs(keys, ar, end_bit)
     inv = torch.empty_like(perm)

@@ -19,26 +19,28 @@ import numpy as np
 
 
 def expand_bits(v: np.ndarray) -> np.ndarray:
-    """Spread the low 10 bits of v to every third bit (model.py:48-54)."""
+    """Spread the low 10 bits of v, bit k -> bit 3k + 1 (model.py:48-54: the four mask steps of
+    the usual 3k spread, then a fifth that lifts every bit by one)."""
     v = v.astype(np.int64)
     v = (v | (v << 16)) & 0x030000FF
     v = (v | (v << 8)) & 0x0300F00F
     v = (v | (v << 4)) & 0x030C30C3
     v = (v | (v << 2)) & 0x09249249
+    v = (v | (v << 1)) & 0x12492492
     return v
 
 
 def expand_bits_loop(v: int) -> int:
-    """Same map as expand_bits by an explicit bit loop: bit k of v -> bit 3k."""
+    """Same map as expand_bits by an explicit bit loop: bit k of v -> bit 3k + 1."""
     out = 0
     for k in range(10):
         if (v >> k) & 1:
-            out |= 1 << (3 * k)
+            out |= 1 << (3 * k + 1)
     return out
 
 
 def morton_code(ix: np.ndarray, iy: np.ndarray, iz: np.ndarray) -> np.ndarray:
-    """x -> bit 3k, y -> bit 3k+1, z -> bit 3k+2 (model.py:56-58)."""
+    """x -> bit 3k+1, y -> bit 3k+2, z -> bit 3k+3 (model.py:56-58)."""
     return expand_bits(ix) | (expand_bits(iy) << 1) | (expand_bits(iz) << 2)
 
 

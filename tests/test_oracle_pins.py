@@ -158,6 +158,10 @@ def test_morton_bit_interleave_all_values():
     g = np.random.default_rng(7)
     for ix, iy, iz in g.integers(0, 1024, size=(500, 3)):
         assert int(G.morton_code(np.array([ix]), np.array([iy]), np.array([iz]))[0]) == G.morton_code_loop(ix, iy, iz)
+    # known answers: the reference's keys start at bit 1 (x), 2 (y), 3 (z) and end at bit 30
+    one = lambda a, b, c: int(G.morton_code(np.array([a]), np.array([b]), np.array([c]))[0])
+    assert (one(1, 0, 0), one(0, 1, 0), one(0, 0, 1), one(2, 0, 0)) == (2, 4, 8, 16)
+    assert one(1023, 1023, 1023) == 2**31 - 2
 
 
 def test_csr_matches_loop():
