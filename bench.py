@@ -51,6 +51,12 @@ def make_system(config: str):
         return systems.amorphous(), False, "amorphous_50k"
     if config == "cu_slab_co":
         return systems.cu_slab_co(), False, "cu_slab_co"
+    if config in ("sweep_1000x30", "sweep_2000x50"):
+        # the reference's own sweep workloads (examples/sweep.py:33-81, E+F+S), explicit edges
+        n, deg = (int(v) for v in config.split("_")[1].split("x"))
+        system, ei, off = systems.sweep_graph(n, deg)
+        system.info["edges"] = (ei, off)
+        return system, True, f"random_{n}_atoms_{deg}_edges_per_atom"
     raise SystemExit(f"unknown config {config}")
 
 
@@ -134,7 +140,10 @@ def main() -> None:
     bb = escn_md.eSCNMDBackbone(seed=0, **model_kw)
     hd = heads.MLPEnergyHead(bb.sphere_channels, bb.hidden_channels, seed=1)
     t0 = time.perf_counter()
-    ei, off = systems.neighbor_list(system.pos, system.cell, system.pbc, bb.cutoff, bb.max_neighbors)
+    if "edges" in system.info:
+        ei, off = system.info["edges"]
+    else:
+        ei, off = systems.neighbor_list(system.pos, system.cell, system.pbc, bb.cutoff, bb.max_neighbors)
     log(f"[bench] {wl_name}: {system.n_atoms} atoms, {ei.shape[1]} edges (graph {time.perf_counter() - t0:.1f}s)")
     model = heads.PotentialModel(ZeroAllocBackbone(bb.to(dev)), hd.to(dev))
     data = heads.make_atomic_data(system, ei, off, dev)

@@ -160,6 +160,30 @@ def amorphous(n_atoms: int = 50000, density: float = 0.08, dmin: float = 1.2,
                         np.diag([L, L, L]).astype(np.float32))
 
 
+def sweep_graph(n_atoms: int, degree: int, cutoff: float = 6.0, seed: int = 0):
+    """The synthetic graphs of the reference's own benchmark sweep (examples/sweep.py:33-81),
+    generated here with numpy: uniform random positions in a cube scaled so that about
+    n_atoms * degree ordered pairs lie within the cutoff, every such pair an edge (no
+    per-receiver cap), random elements 1..99, a unit cell without periodicity and random
+    cell offsets in {-1, 0, 1} per edge (shift vectors of up to 1 A per axis).  Returns the
+    system and its explicit (edge_index, cell_offsets)."""
+    rng = np.random.default_rng(seed)
+    p = rng.random((n_atoms, 3))
+    d = np.linalg.norm(p[:, None, :] - p[None, :, :], axis=-1)
+    k = min(n_atoms * degree + n_atoms, n_atoms * n_atoms)   # the diagonal's n zeros first
+    kth = np.partition(d.ravel(), k - 1)[k - 1]
+    scale = (cutoff - 1e-4) / kth
+    pos = (p * scale).astype(np.float32)
+    Z = rng.integers(1, 100, n_atoms).astype(np.int64)
+    within = (d * scale < cutoff) & ~np.eye(n_atoms, dtype=bool)
+    send, recv = np.nonzero(within)   # row-major: sender-major, as the reference's pair list
+    ei = np.stack([send, recv]).astype(np.int64)
+    off = rng.integers(-1, 2, (ei.shape[1], 3)).astype(np.float32)
+    system = AtomicSystem(f"sweep_{n_atoms}x{degree}", pos, Z, np.eye(3, dtype=np.float32),
+                          pbc=(False, False, False))
+    return system, ei, off
+
+
 def _image_reps(cell: np.ndarray, pbc, cutoff: float):
     reps = []
     for ax in range(3):

@@ -3,7 +3,10 @@
 Run from the repository root:  python tests/golden/make_fixtures.py
 Fixture water64_oracle.npz: a 64-molecule periodic water box (seed 3, L = 12.42 A), its
 capped radius graph, and the oracle's energy, per-atom energies, forces and stress for the
-seed-0 UMA-s-shaped random-init backbone and the seed-1 energy head."""
+seed-0 UMA-s-shaped random-init backbone and the seed-1 energy head.
+Fixture sweep200_oracle.npz: systems.sweep_graph(200, 100) (the reference's benchmark graph
+construction: every pair within the cutoff, no per-receiver cap, up to 171 edges per atom,
+unit cell, random cell offsets) with the same backbone, head and oracle outputs."""
 import os
 import sys
 
@@ -32,5 +35,20 @@ def water64():
     print(f"wrote {path}: N={s.n_atoms} E={ei.shape[1]} energy={ref['energy'].item():.10f}")
 
 
+def sweep200():
+    bb = escn_md.eSCNMDBackbone(seed=0)
+    hd = heads.MLPEnergyHead(bb.sphere_channels, bb.hidden_channels, seed=1)
+    s, ei, off = systems.sweep_graph(200, 100)
+    ref = energy_forces_stress(bb, hd, s.pos, s.Z, s.cell, ei, off, dtype=torch.float64)
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "sweep200_oracle.npz")
+    np.savez_compressed(path, pos=s.pos, Z=s.Z.astype(np.int8), cell=s.cell, edge_index=ei.astype(np.int16),
+                        cell_offsets=off.astype(np.int8), energy=ref["energy"].numpy(),
+                        atom_energy=ref["atom_energy"].numpy(), forces=ref["forces"].numpy(),
+                        stress=ref["stress"].numpy())
+    print(f"wrote {path}: N={s.n_atoms} E={ei.shape[1]} energy={ref['energy'].item():.10f}")
+
+
 if __name__ == "__main__":
-    water64()
+    which = sys.argv[1:] or ["water64", "sweep200"]
+    for name in which:
+        globals()[name]()

@@ -29,13 +29,13 @@ def _run(model, system, ei, off, cuda, stress=True):
     return {k: (v.detach().cpu() if torch.is_tensor(v) else v) for k, v in out.items()}
 
 
-def _check(out, ref, n_atoms, stress=True):
+def _check(out, ref, n_atoms, stress=True, atom_rel=2e-5):
     e_rel = abs(out["energy"].double().item() - ref["energy"].item()) / abs(ref["energy"].item())
     assert e_rel <= 1e-6, f"energy per atom rel err {e_rel:.2e}"
     f_err = (out["forces"].double() - ref["forces"]).abs().max().item()
     assert f_err <= 1e-4, f"forces max abs err {f_err:.2e}"
     a_rel = ((out["atom_energy"].double() - ref["atom_energy"]) / ref["atom_energy"].abs().clamp_min(1e-3)).abs().max()
-    assert a_rel.item() <= 2e-5, f"per-atom energy rel err {a_rel.item():.2e}"
+    assert a_rel.item() <= atom_rel, f"per-atom energy rel err {a_rel.item():.2e}"
     if stress:
         s_err = (out["stress"].double() - ref["stress"]).abs().max().item()
         assert s_err <= 1e-4, f"stress max abs err {s_err:.2e}"
@@ -68,6 +68,27 @@ def test_water_fixture_parity(cuda, mode):
         out = _run(model, s, g["edge_index"], g["cell_offsets"], cuda)
     ref = {k: torch.from_numpy(g[k]) for k in ("energy", "forces", "stress", "atom_energy")}
     _check(out, ref, s.n_atoms)
+
+
+def test_uncapped_sweep_fixture_parity(cuda):
+    """The reference's own benchmark graphs (examples/sweep.py:33-81): every pair within the
+    cutoff is an edge with no per-receiver cap (here up to 171 edges per atom, so the
+    node-centric backward walks several 64-edge chunks of one segment), a unit cell without
+    periodicity and random cell offsets.  Against the committed float64 oracle fixture
+    (tests/golden/sweep200_oracle.npz)."""
+    import os
+    import systems
+    path = os.path.join(os.path.dirname(__file__), "golden", "sweep200_oracle.npz")
+    g = np.load(path)
+    bb, hd, model = _build(cuda)
+    s = systems.AtomicSystem("sweep200", g["pos"], g["Z"].astype(np.int64), g["cell"], pbc=(False, False, False))
+    ei = g["edge_index"].astype(np.int64)
+    assert np.bincount(ei[1]).max() > 128
+    out = _run(model, s, ei, g["cell_offsets"].astype(np.float32), cuda)
+    ref = {k: torch.from_numpy(g[k]) for k in ("energy", "forces", "stress", "atom_energy")}
+    # per-atom bar 1e-4: with up to 171 messages summed per atom the float32 oracle itself is
+    # 7.3e-5 from float64 here (energy 5.5e-7, forces 6.7e-8, stress 8.4e-7)
+    _check(out, ref, s.n_atoms, atom_rel=1e-4)
 
 
 def test_deterministic_and_translation(cuda):

@@ -102,3 +102,16 @@ def test_stress_matches_strain_derivative_and_virial(small):
     # symmetric up to the frame regulariser
     st = ref["stress"][0]
     assert (st - st.T).abs().max() < 1e-9
+
+
+def test_sweep_fixture_graph_is_reproducible():
+    """systems.sweep_graph(200, 100) still builds the graph stored in the committed fixture
+    (the GPU parity test reads the fixture; this pins the generator the bench uses)."""
+    import os
+    import numpy as np
+    import systems
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "sweep200_oracle.npz"))
+    s, ei, off = systems.sweep_graph(200, 100)
+    assert np.array_equal(s.pos, g["pos"]) and np.array_equal(s.Z, g["Z"].astype(np.int64))
+    assert np.array_equal(ei, g["edge_index"].astype(np.int64))
+    assert np.array_equal(off, g["cell_offsets"].astype(np.float32))
