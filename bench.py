@@ -223,7 +223,8 @@ def main() -> None:
         "config": {"workload": f"{wl_name}: {system.n_atoms} atoms, {ei.shape[1]} edges, "
                                f"{'E+F+S' if with_stress else 'E+F'}, UMA-s-shaped random-init eSCN-MD "
                                f"(lmax={bb.lmax}, mmax=2, {bb.num_layers} layers, C=128, B=64, cutoff 6, "
-                               f"max_neighbors 30)",
+                               + ("every pair within the cutoff, no per-atom cap)" if "edges" in system.info
+                                  else "max_neighbors 30)"),
                    "atoms": system.n_atoms, "edges": int(ei.shape[1]), "parallelism": "single GPU",
                    "execution": "hip graph replay" if args.graph else "eager",
                    "matmul": ("fp32 operands split exactly into three bf16 planes, six bf16 MFMA products, "
