@@ -1,4 +1,4 @@
-"""The BASELINE workloads other than the headline one, run through the GPU path.
+"""The BASELINE workloads run through the GPU path at full size.
 
 * Liquid water, 333 H2O (999 atoms, cubic 21.5 A): a 100-step velocity-Verlet MD loop of
   energy + forces with the graph built once at step 0 and the topology cached (one build,
@@ -11,6 +11,8 @@
   under a rigid rotation of positions and cell, and translation invariance.  A 1,500-atom
   cell from the same generator (same density, same elements) is checked against the
   float64 oracle directly.
+* The headline bcc Fe 16^3 (8,192 atoms) with stress, through the same kind of properties
+  plus the stress against a finite difference of the energy under strain.
 Tolerances as everywhere: energy per atom rel <= 1e-6, forces max-abs <= 1e-4 eV/A."""
 import math
 
@@ -127,3 +129,57 @@ def test_amorphous_50k_invariants(cuda):
     e_t, f_t = run(s.pos + np.array([0.37, -1.1, 2.3]), s.cell)
     assert abs(e_t - e0) / abs(e0) <= 1e-6
     assert (f_t - f0).abs().max().item() <= 1e-4
+
+
+def test_headline_bcc_fe_invariants(cuda):
+    """The headline workload at full size: bcc Fe 16^3 (8,192 atoms, 245,760 edges), energy +
+    forces + stress.  No oracle finishes at this size inside a test, so it is checked through
+    size-independent properties: bitwise reproducibility, zero net force, a rigid rotation
+    of positions and cell (energy invariant, forces and stress covariant: S' = R S R^T),
+    a translation, and the stress against a central finite difference of the energy under a
+    small homogeneous strain (V S_ab = dE/d eps_ab)."""
+    import heads
+    import systems
+    bb, hd, model = _build(cuda)
+    s = systems.bcc_fe(16)
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, bb.cutoff, bb.max_neighbors)
+    print(f"{s.n_atoms} atoms, {ei.shape[1]} edges", flush=True)
+    pos0 = np.asarray(s.pos, dtype=np.float64)
+    cell0 = np.asarray(s.cell, dtype=np.float64).reshape(3, 3)
+
+    def run(pos, cell, stress=True):
+        sys_ = systems.AtomicSystem("fe", np.asarray(pos, dtype=np.float32), s.Z, np.asarray(cell, dtype=np.float32))
+        o = model(heads.make_atomic_data(sys_, ei, off, cuda), compute_forces=True, compute_stress=stress)
+        return (o["energy"].double().item(), o["forces"].detach().cpu().double(),
+                o["stress"].detach().cpu().double()[0] if stress else None)
+
+    e0, f0, s0 = run(pos0, cell0)
+    e1, f1, s1 = run(pos0, cell0)
+    assert e0 == e1 and torch.equal(f0, f1) and torch.equal(s0, s1), "not bitwise reproducible"
+    fmax = f0.abs().max().item()
+    assert f0.sum(0).abs().max().item() < 1e-5 * s.n_atoms * max(fmax, 1e-3)
+    Rm = np.array([[np.cos(0.7), -np.sin(0.7), 0], [np.sin(0.7), np.cos(0.7), 0], [0, 0, 1]]) @ \
+        np.array([[1, 0, 0], [0, np.cos(0.4), -np.sin(0.4)], [0, np.sin(0.4), np.cos(0.4)]])
+    e_r, f_r, s_r = run(pos0 @ Rm.T, cell0 @ Rm.T)
+    R = torch.from_numpy(Rm)
+    smax = s0.abs().max().item()
+    print(f"E {e0:.6f}  max|F| {fmax:.3e}  max|S| {smax:.3e}", flush=True)
+    assert abs(e_r - e0) / abs(e0) <= 1e-6
+    assert (f_r - f0 @ R.T).abs().max().item() <= 1e-4
+    assert (s_r - R @ s0 @ R.T).abs().max().item() <= 1e-4
+    e_t, f_t, s_t = run(pos0 + np.array([0.41, -0.9, 1.7]), cell0)
+    assert abs(e_t - e0) / abs(e0) <= 1e-6 and (f_t - f0).abs().max().item() <= 1e-4
+    assert (s_t - s0).abs().max().item() <= 1e-4
+    # stress against the energy under strain: pos, cell -> (I + eps)
+    V = abs(np.linalg.det(cell0))
+    h = 1e-3
+    for a, b in ((0, 0), (2, 2), (0, 1)):
+        eps = np.zeros((3, 3))
+        eps[a, b] += 0.5 * h
+        eps[b, a] += 0.5 * h
+        ep, _, _ = run(pos0 @ (np.eye(3) + eps).T, cell0 @ (np.eye(3) + eps).T, stress=False)
+        em, _, _ = run(pos0 @ (np.eye(3) - eps).T, cell0 @ (np.eye(3) - eps).T, stress=False)
+        fd = (ep - em) / (2 * h) / V
+        sym = 0.5 * (s0[a, b].item() + s0[b, a].item())   # a symmetric strain probes S_ab + S_ba
+        print(f"S[{a}{b}] = {sym:.6e}  finite difference {fd:.6e}", flush=True)
+        assert abs(fd - sym) <= 5e-4 * smax + 5e-7   # measured: 4e-9 (xx), 2e-7 (zz), 8e-8 (xy)
