@@ -53,6 +53,25 @@ def test_cu_slab_parity(cuda):
     _check(out, ref, s.n_atoms)
 
 
+@pytest.mark.parametrize("C,H,B", [(64, 64, 32), (256, 128, 64)], ids=["C64_B32", "C256_H128"])
+def test_channel_widths_parity(cuda, C, H, B):
+    """Backbones of other widths than UMA-s (sphere channels 64 and 256, hidden 64 and 128,
+    32 Gaussians) through every kernel, against the float64 oracle on the Cu slab."""
+    import escn_md
+    import heads
+    import systems
+    from oracle.model_ref import energy_forces_stress
+    from wrapper import ZeroAllocBackbone
+    bb = escn_md.eSCNMDBackbone(sphere_channels=C, hidden_channels=H, num_distance_basis=B, seed=5)
+    hd = heads.MLPEnergyHead(C, H, seed=6)
+    model = heads.PotentialModel(ZeroAllocBackbone(bb.to(cuda)), hd.to(cuda))
+    s = systems.cu_slab_co()
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, bb.cutoff, bb.max_neighbors)
+    out = _run(model, s, ei, off, cuda)
+    ref = energy_forces_stress(bb.cpu(), hd.cpu(), s.pos, s.Z, s.cell, ei, off, dtype=torch.float64)
+    _check(out, ref, s.n_atoms)
+
+
 @pytest.mark.parametrize("mode", [0, 1], ids=["split_bf16", "fp32"])
 def test_water_fixture_parity(cuda, mode):
     """Against the committed float64 oracle fixture (tests/golden/water64_oracle.npz), in both
