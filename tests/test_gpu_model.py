@@ -183,7 +183,8 @@ def test_inplace_edge_index_edit_invalidates_topology(cuda):
     """The topology cache is keyed on the edge_index tensor and its version counter: an
     in-place edit (here: reversing 12 edges, with their cell offsets negated) must rebuild the
     CSRs, giving exactly the result of a fresh tensor holding the edited graph.  (The
-    reference keys its cache on a freshly allocated tensor's data_ptr, SURVEY hazard (i).)"""
+    reference keys its cache on the data_ptr of a tensor it allocates afresh on every call,
+    model.py:36, so an address reused by a different graph could match a stale entry.)"""
     import heads
     import systems
     bb, hd, model = _build(cuda)
