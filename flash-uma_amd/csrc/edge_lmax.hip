@@ -442,7 +442,7 @@ __device__ __forceinline__ void init_fwd_block(const float* wl, const float* we,
   for (int mp = -l; mp <= l; ++mp) {
     const float w = dwig<l>(wl, we, 0, mp);
 #pragma unroll
-    for (int q = 0; q < CPL; ++q) acc[l * l + l + mp][q] += (double)((r[q] * w * en) / 5.0f);
+    for (int q = 0; q < CPL; ++q) acc[l * l + l + mp][q] += (double)(r[q] * w * en);
   }
 }
 
@@ -457,14 +457,14 @@ __global__ __launch_bounds__(256) void init_scatter_fwd_lmax_kernel(
   const int c = lane * CPL;
   const int64_t n = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave_uniform();
   if (n >= N) return;
-  double acc[K][CPL];
+  double acc[K][CPL], base[CPL];
   {
     const Vec<CPL> ws = vload<CPL>(W_sphere + Z[n] * C + c);
     const Vec<CPL> cs = vload<CPL>(csd + batch[n] * C + c);
 #pragma unroll
-    for (int q = 0; q < CPL; ++q) acc[0][q] = (double)(ws[q] + cs[q]);
+    for (int q = 0; q < CPL; ++q) base[q] = (double)(ws[q] + cs[q]);
 #pragma unroll
-    for (int k = 1; k < K; ++k)
+    for (int k = 0; k < K; ++k)
 #pragma unroll
       for (int q = 0; q < CPL; ++q) acc[k][q] = 0.0;
   }
@@ -476,18 +476,19 @@ __global__ __launch_bounds__(256) void init_scatter_fwd_lmax_kernel(
     const float* rp = rad + e * (L + 1) * C + c;
     const Vec<CPL> r0 = vload<CPL>(rp);
 #pragma unroll
-    for (int q = 0; q < CPL; ++q) acc[0][q] += (double)((r0[q] * en) / 5.0f);
+    for (int q = 0; q < CPL; ++q) acc[0][q] += (double)(r0[q] * en);
     init_fwd_block<L, CPL, 1>(wl, we, en, rp, acc);
     init_fwd_block<L, CPL, 2>(wl, we, en, rp, acc);
     if constexpr (L >= 3) init_fwd_block<L, CPL, 3>(wl, we, en, rp, acc);
     if constexpr (L >= 4) init_fwd_block<L, CPL, 4>(wl, we, en, rp, acc);
   }
+  // messages summed in fp64, divided by the rescale factor 5 once per node
   float* xo = x_out + n * K * C + c;
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     Vec<CPL> t;
 #pragma unroll
-    for (int q = 0; q < CPL; ++q) t[q] = (float)acc[k][q];
+    for (int q = 0; q < CPL; ++q) t[q] = (float)(k == 0 ? base[q] + acc[0][q] / 5.0 : acc[k][q] / 5.0);
     vstore(xo + k * C, t);
   }
 }

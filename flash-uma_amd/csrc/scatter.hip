@@ -204,14 +204,14 @@ __global__ __launch_bounds__(256) void init_scatter_fwd_kernel(
   const int c = lane * CPL;
   const int64_t n = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave_id_u();
   if (n >= N) return;
-  double acc[9][CPL];
+  double acc[9][CPL], base[CPL];
   {
     const Vec<CPL> ws = vload<CPL>(W_sphere + Z[n] * C + c);
     const Vec<CPL> cs = vload<CPL>(csd + batch[n] * C + c);
 #pragma unroll
-    for (int q = 0; q < CPL; ++q) acc[0][q] = (double)(ws[q] + cs[q]);
+    for (int q = 0; q < CPL; ++q) base[q] = (double)(ws[q] + cs[q]);
 #pragma unroll
-    for (int k = 1; k < 9; ++k)
+    for (int k = 0; k < 9; ++k)
 #pragma unroll
       for (int q = 0; q < CPL; ++q) acc[k][q] = 0.0;
   }
@@ -226,13 +226,15 @@ __global__ __launch_bounds__(256) void init_scatter_fwd_kernel(
     for (int b = 0; b < 5; ++b) w2[b] = wig[e * 34 + 19 + b];  // L=2 row 2
     const float* rp = rad + e * 3 * C + c;
     const Vec<CPL> r0 = vload<CPL>(rp), r1 = vload<CPL>(rp + C), r2 = vload<CPL>(rp + 2 * C);
+    // messages summed in fp64 and divided by the rescale factor 5 once per node (the
+    // reference divides each message, ops/scatter.py:409-411; same value to fp32 rounding)
 #pragma unroll
     for (int q = 0; q < CPL; ++q) {
-      acc[0][q] += (double)((r0[q] * en) / 5.0f);
+      acc[0][q] += (double)(r0[q] * en);
 #pragma unroll
-      for (int b = 0; b < 3; ++b) acc[1 + b][q] += (double)((r1[q] * w1[b] * en) / 5.0f);
+      for (int b = 0; b < 3; ++b) acc[1 + b][q] += (double)(r1[q] * w1[b] * en);
 #pragma unroll
-      for (int b = 0; b < 5; ++b) acc[4 + b][q] += (double)((r2[q] * w2[b] * en) / 5.0f);
+      for (int b = 0; b < 5; ++b) acc[4 + b][q] += (double)(r2[q] * w2[b] * en);
     }
   }
   float* xo = x_out + n * 9 * C + c;
@@ -240,7 +242,7 @@ __global__ __launch_bounds__(256) void init_scatter_fwd_kernel(
   for (int k = 0; k < 9; ++k) {
     Vec<CPL> t;
 #pragma unroll
-    for (int q = 0; q < CPL; ++q) t[q] = (float)acc[k][q];
+    for (int q = 0; q < CPL; ++q) t[q] = (float)(k == 0 ? base[q] + acc[0][q] / 5.0 : acc[k][q] / 5.0);
     vstore(xo + k * C, t);
   }
 }
