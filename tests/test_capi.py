@@ -183,3 +183,33 @@ def test_matmul_mode_rejects_unknown():
     assert st == -2 and "mode=5" in msg
     st, _ = _status("fu_matmul_mode")
     assert st in (0, 1)
+
+
+def test_binding_types_match_header():
+    """Every ctypes signature in ops/_lib.py has the argument count and kinds the header
+    declares (pointer, int64_t, int32_t, float, double), so no argument is marshalled with
+    the wrong width or register class."""
+    from ops import _lib
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    kinds = {"int64_t": ctypes.c_int64, "int32_t": ctypes.c_int32, "float": ctypes.c_float,
+             "double": ctypes.c_double}
+    checked = 0
+    for m in re.finditer(r"\b(?:int|int64_t|const char\*)\s+(fu_\w+)\s*\(([^)]*)\)\s*;", text):
+        name, params = m.group(1), m.group(2).strip()
+        want = []
+        if params and params != "void":
+            for p in params.split(","):
+                p = " ".join(p.split())
+                if "*" in p:
+                    want.append("ptr")
+                else:
+                    want.append(kinds[p.rsplit(" ", 1)[0].replace("const ", "")])
+        got = _lib.SIGNATURES[name]
+        assert len(got) == len(want), (name, len(got), len(want))
+        for k, (g, w) in enumerate(zip(got, want)):
+            if w == "ptr":
+                assert g in (ctypes.c_void_p, _lib.SZ_P), (name, k, g)
+            else:
+                assert g is w, (name, k, g, w)
+        checked += 1
+    assert checked == len(_lib.SIGNATURES)
