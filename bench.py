@@ -174,11 +174,13 @@ def main() -> None:
     # the timed steps run without instrumentation; the per-kernel roofline comes from a
     # separate pass over the same number of steps with HIP events around every library call
     torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         out = step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    peak_mib = torch.cuda.max_memory_allocated(dev) / 2**20
     ms = 1e3 * elapsed / args.steps
     value = system.n_atoms / (elapsed / args.steps)
     log(f"[bench] timed {args.steps} steps: {ms:.3f} ms/step, {value:.1f} atom-steps/s")
@@ -230,6 +232,7 @@ def main() -> None:
                    "matmul": ("fp32 operands split exactly into three bf16 planes, six bf16 MFMA products, "
                               "fp32 accumulation" if mm_mode == _lib.MATMUL_SPLIT_BF16 else "fp32 MFMA")},
         "roofline": rl, "cpu_baseline": cpu, "kernels": kernels,
+        "peak_memory_mib": round(peak_mib, 1),   # torch allocator peak over the timed steps
         "energy": round(float(out["energy"].item()), 8),
     }
     print(json.dumps(rec), flush=True)
