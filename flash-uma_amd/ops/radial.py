@@ -99,14 +99,15 @@ class RadialBank(torch.nn.Module):
             reg(f"b3_{k}", m[9])
 
     # Below SIDE_STREAM_MIN_EDGES the output layers stay on the caller's stream: the events
-    # and stream bookkeeping cost more host time than the overlap saves on a small graph.
+    # and stream bookkeeping cost more host time than the overlap saves on a small graph
+    # (Cu slab, 859 edges: +0.4 ms/step with the side stream; 30 k edges: -0.06 ms).
     # Above SIDE_STREAM_MAX_EDGES they stay there too: the side stream's allocations form a
     # second caching-allocator pool, and on a graph whose step needs a large share of HBM
     # (50,000 atoms / 1.5 M edges: 138 GiB allocated, over 216 GiB reserved with two pools,
     # 151 GiB with one) the reserve approaches the card's capacity and the allocator starts
     # freeing and re-mapping memory inside the step (up to twice the step time), while the
     # overlap itself is worth under 1 % there.
-    SIDE_STREAM_MIN_EDGES = 100_000
+    SIDE_STREAM_MIN_EDGES = 20_000
     SIDE_STREAM_MAX_EDGES = 600_000
 
     def forward(self, gauss, Z, idx_i, idx_j, streams: bool = True):
