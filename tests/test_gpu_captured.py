@@ -21,12 +21,15 @@ def _setup(cuda, system):
     return model, ei, off
 
 
-@pytest.mark.parametrize("name", ["water64", "cu_slab"])
+@pytest.mark.parametrize("name", ["water64", "cu_slab", "water333"])
 def test_captured_step_equals_eager(cuda, name):
+    """water333 (29,970 edges) runs the radial output layers on the side stream, so the
+    captured graph holds the fork to that stream and the per-block joins."""
     import heads
     import systems
     from captured import CapturedStep
-    s = systems.water_box(n_mol=64, L=12.42, seed=3) if name == "water64" else systems.cu_slab_co()
+    s = {"water64": lambda: systems.water_box(n_mol=64, L=12.42, seed=3), "cu_slab": systems.cu_slab_co,
+         "water333": systems.water_box}[name]()
     model, ei, off = _setup(cuda, s)
     data_c = heads.make_atomic_data(s, ei, off, cuda)
     cap = CapturedStep(model, data_c, compute_stress=True)
