@@ -113,7 +113,7 @@ __global__ __launch_bounds__(256) void gather_fwd_kernel(
     const float* rr = rad + e * 12 * C + c;
     Vec<CPL> r[12];
 #pragma unroll
-    for (int k = 0; k < 12; ++k) r[k] = vload_nt<CPL>(rr + slot_rad<L>(k & 1, k >> 1) * C);
+    for (int k = 0; k < 12; ++k) r[k] = vload<CPL>(rr + slot_rad<L>(k & 1, k >> 1) * C);
     float* o0 = X0 + e * 6 * C + c;
     float* o1 = X1 + e * 8 * C + c;
     float* o2 = X2 + e * 4 * C + c;
@@ -163,14 +163,14 @@ __device__ __forceinline__ void side_load(const float* __restrict__ gX0, const f
   const float* g1 = gX1 + e * 8 * C + c;
   const float* g2 = gX2 + e * 4 * C + c;
 #pragma unroll
-  for (int q = 0; q < 3; ++q) d.g[q] = vload_nt<CPL>(g0 + slot_m0<L>(so, q) * C);
+  for (int q = 0; q < 3; ++q) d.g[q] = vload<CPL>(g0 + slot_m0<L>(so, q) * C);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) d.g[3 + q] = vload_nt<CPL>(g1 + slot_m1<L>(so, q) * C);
+  for (int q = 0; q < 4; ++q) d.g[3 + q] = vload<CPL>(g1 + slot_m1<L>(so, q) * C);
 #pragma unroll
-  for (int q = 0; q < 2; ++q) d.g[7 + q] = vload_nt<CPL>(g2 + slot_m2<L>(so, q) * C);
+  for (int q = 0; q < 2; ++q) d.g[7 + q] = vload<CPL>(g2 + slot_m2<L>(so, q) * C);
   const float* rp = rad + e * 12 * C + c;
 #pragma unroll
-  for (int q = 0; q < 6; ++q) d.r[q] = vload_nt<CPL>(rp + slot_rad<L>(so, q) * C);
+  for (int q = 0; q < 6; ++q) d.r[q] = vload<CPL>(rp + slot_rad<L>(so, q) * C);
 }
 
 // v (the node's own row, csd added) is read from the wave's LDS copy, so that it holds no
