@@ -29,24 +29,6 @@ __device__ __forceinline__ Vec<CPL> vload(const float* p) {
   return r;
 }
 
-// vstore with the nontemporal hint: for large write-once streams that no kernel re-reads
-// while they could still sit in L2.
-template <int CPL>
-__device__ __forceinline__ void vstore_nt(float* p, const Vec<CPL>& a) {
-  if constexpr (CPL == 4) {
-    typedef float f4 __attribute__((ext_vector_type(4)));
-    const f4 v = {a.v[0], a.v[1], a.v[2], a.v[3]};
-    __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p));
-  } else if constexpr (CPL == 2) {
-    typedef float f2 __attribute__((ext_vector_type(2)));
-    const f2 v = {a.v[0], a.v[1]};
-    __builtin_nontemporal_store(v, reinterpret_cast<f2*>(p));
-  } else {
-#pragma unroll
-    for (int k = 0; k < CPL; ++k) __builtin_nontemporal_store(a.v[k], p + k);
-  }
-}
-
 template <int CPL>
 __device__ __forceinline__ void vstore(float* p, const Vec<CPL>& a) {
   if constexpr (CPL == 4) {

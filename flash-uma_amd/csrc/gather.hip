@@ -121,18 +121,18 @@ __global__ __launch_bounds__(256) void gather_fwd_kernel(
     constexpr int K0[3] = {0, 2, 6}, K1[4] = {3, 7, 1, 5}, K2[2] = {8, 4};
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
-      vstore_nt(o0 + slot_m0<L>(0, q) * C, vmul(rs.r[K0[q]], r[2 * q]));
-      vstore_nt(o0 + slot_m0<L>(1, q) * C, vmul(rt.r[K0[q]], r[2 * q + 1]));
+      vstore(o0 + slot_m0<L>(0, q) * C, vmul(rs.r[K0[q]], r[2 * q]));
+      vstore(o0 + slot_m0<L>(1, q) * C, vmul(rt.r[K0[q]], r[2 * q + 1]));
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      vstore_nt(o1 + slot_m1<L>(0, q) * C, vmul(rs.r[K1[q]], r[6 + 2 * (q & 1)]));
-      vstore_nt(o1 + slot_m1<L>(1, q) * C, vmul(rt.r[K1[q]], r[7 + 2 * (q & 1)]));
+      vstore(o1 + slot_m1<L>(0, q) * C, vmul(rs.r[K1[q]], r[6 + 2 * (q & 1)]));
+      vstore(o1 + slot_m1<L>(1, q) * C, vmul(rt.r[K1[q]], r[7 + 2 * (q & 1)]));
     }
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      vstore_nt(o2 + slot_m2<L>(0, q) * C, vmul(rs.r[K2[q]], r[10]));
-      vstore_nt(o2 + slot_m2<L>(1, q) * C, vmul(rt.r[K2[q]], r[11]));
+      vstore(o2 + slot_m2<L>(0, q) * C, vmul(rs.r[K2[q]], r[10]));
+      vstore(o2 + slot_m2<L>(1, q) * C, vmul(rt.r[K2[q]], r[11]));
     }
   }
 }
@@ -195,12 +195,12 @@ __device__ __forceinline__ void side_apply(const SideEdge<CPL>& d, int64_t e, in
     rotate9(w, v, rv);
     // this side's radial gradients (reference blocks so, 2+so, ..., 10+so)
     float* gr = g_rad + e * 12 * C + c;
-    vstore_nt(gr + slot_rad<L>(so, 0) * C, vmul(d.g[0], rv.r[0]));
-    vstore_nt(gr + slot_rad<L>(so, 1) * C, vmul(d.g[1], rv.r[2]));
-    vstore_nt(gr + slot_rad<L>(so, 2) * C, vmul(d.g[2], rv.r[6]));
-    vstore_nt(gr + slot_rad<L>(so, 3) * C, vadd(vmul(d.g[3], rv.r[3]), vmul(d.g[5], rv.r[1])));
-    vstore_nt(gr + slot_rad<L>(so, 4) * C, vadd(vmul(d.g[4], rv.r[7]), vmul(d.g[6], rv.r[5])));
-    vstore_nt(gr + slot_rad<L>(so, 5) * C, vadd(vmul(d.g[7], rv.r[8]), vmul(d.g[8], rv.r[4])));
+    vstore(gr + slot_rad<L>(so, 0) * C, vmul(d.g[0], rv.r[0]));
+    vstore(gr + slot_rad<L>(so, 1) * C, vmul(d.g[1], rv.r[2]));
+    vstore(gr + slot_rad<L>(so, 2) * C, vmul(d.g[2], rv.r[6]));
+    vstore(gr + slot_rad<L>(so, 3) * C, vadd(vmul(d.g[3], rv.r[3]), vmul(d.g[5], rv.r[1])));
+    vstore(gr + slot_rad<L>(so, 4) * C, vadd(vmul(d.g[4], rv.r[7]), vmul(d.g[6], rv.r[5])));
+    vstore(gr + slot_rad<L>(so, 5) * C, vadd(vmul(d.g[7], rv.r[8]), vmul(d.g[8], rv.r[4])));
   }
   // gradient w.r.t. the rotated coefficients of this node's row
   Rows9<CPL> grv;
