@@ -4,10 +4,14 @@ readme.md:34), bit-identical to the host builder `systems.neighbor_list`.
 radius_graph(pos, cell, pbc, cutoff, max_neighbors) -> (edge_index (2, E) int64,
 cell_offsets (E, 3) float32), both on the positions' device; definition in csrc/nlist.hip.
 
-NeighborList adds the MD-side policy: it keeps the graph (and so the cached topology) while
-no atom has moved more than skin / 2 since the last build, and rebuilds otherwise.  With
-skin = 0 (default) it rebuilds on every call, which reproduces the host graph of the current
-positions; the BASELINE water loop instead holds the step-0 graph for the whole run."""
+NeighborList adds the MD-side policy.  With skin = 0 (default) it rebuilds on every call,
+which reproduces the capped host graph of the current positions.  With skin > 0 it builds an
+uncapped graph at cutoff + skin and keeps it (and so the cached topology) while no atom has
+moved more than skin / 2 and the cell and periodicity are unchanged: every pair within the
+cutoff of the current positions is then still in the graph, and the extra pairs lie at or
+beyond the cutoff, where the envelope and its derivative vanish, so energies and forces
+equal those of a fresh uncapped graph.  A per-receiver cap cannot be kept under reuse (the
+nearest-K set changes as atoms move), so skin > 0 refuses max_neighbors."""
 from __future__ import annotations
 
 import math
@@ -82,23 +86,42 @@ def radius_graph(pos: torch.Tensor, cell, pbc, cutoff: float, max_neighbors: int
 
 
 class NeighborList:
-    """Graph holder for MD: rebuilds when some atom moved more than skin / 2 since the last
-    build (skin = 0: every call), otherwise returns the same edge_index tensor, so the
+    """Graph holder for MD.
+
+    skin = 0: radius_graph(pos, cell, pbc, cutoff, max_neighbors) on every call.
+    skin > 0 (max_neighbors must be None): an uncapped graph at cutoff + skin, rebuilt when
+    some atom has moved more than skin / 2 since the last build or when the cell or the
+    periodic axes change; otherwise the same edge_index tensor is returned, so the
     backbone's topology cache (keyed on that tensor) is reused."""
 
-    def __init__(self, cutoff: float, max_neighbors: int, skin: float = 0.0):
-        self.cutoff, self.max_neighbors, self.skin = float(cutoff), int(max_neighbors), float(skin)
+    def __init__(self, cutoff: float, max_neighbors: int | None, skin: float = 0.0):
+        if skin < 0.0:
+            raise ValueError("skin must be >= 0")
+        if skin > 0.0 and max_neighbors is not None:
+            raise ValueError("a neighbour cap cannot be kept while a graph is reused: NeighborList with "
+                             "skin > 0 needs max_neighbors=None (uncapped)")
+        if skin == 0.0 and max_neighbors is None:
+            max_neighbors = NL_CAP
+        self.cutoff, self.skin = float(cutoff), float(skin)
+        self.max_neighbors = NL_CAP if max_neighbors is None else int(max_neighbors)
         self._ref_pos = None
+        self._ref_cell = None
+        self._ref_pbc = None
         self._graph = None
         self.builds = 0
 
     def __call__(self, pos: torch.Tensor, cell, pbc):
         pos = pos.detach()
-        if self._graph is not None and self.skin > 0.0:
-            moved = (pos - self._ref_pos).norm(dim=1).max().item()
+        cell64 = np.asarray(cell, dtype=np.float64).reshape(3, 3)
+        pbc_t = tuple(bool(p) for p in pbc)
+        if (self._graph is not None and self.skin > 0.0 and pbc_t == self._ref_pbc
+                and np.array_equal(cell64, self._ref_cell) and pos.shape == self._ref_pos.shape):
+            moved = (pos - self._ref_pos).norm(dim=1).max().item() if pos.shape[0] else 0.0
             if moved <= 0.5 * self.skin:
                 return self._graph
-        self._graph = radius_graph(pos, cell, pbc, self.cutoff, self.max_neighbors)
+        self._graph = radius_graph(pos, cell, pbc, self.cutoff + self.skin, self.max_neighbors)
         self._ref_pos = pos.clone()
+        self._ref_cell = cell64.copy()
+        self._ref_pbc = pbc_t
         self.builds += 1
         return self._graph

@@ -109,6 +109,9 @@ def check_indices(edge_index: torch.Tensor, N: int) -> None:
 
 
 def build_topology(pos: torch.Tensor, batch: torch.Tensor, edge_index: torch.Tensor) -> GraphTopology:
+    # the cache keys on the caller's tensor, so that tensor (not a converted copy) is the
+    # one kept alive in the entry
+    source = edge_index
     edge_index = _lib.require(edge_index, torch.int64, "edge_index")
     batch = _lib.require(batch, torch.int64, "batch")
     N = pos.shape[0]
@@ -124,7 +127,7 @@ def build_topology(pos: torch.Tensor, batch: torch.Tensor, edge_index: torch.Ten
     recv_idx = torch.arange(E, dtype=torch.int32, device=dev)
     return GraphTopology(N=N, E=E, perm=perm, inv_perm=inv, edge_perm=edge_perm, idx_i=idx_i_sorted,
                          idx_j=idx_j_sorted, recv_ptr=recv_ptr, recv_idx=recv_idx, send_ptr=send_ptr,
-                         send_idx=narrow32(send_order), source=edge_index)
+                         send_idx=narrow32(send_order), source=source)
 
 
 _TOPO_CAPACITY = 8

@@ -96,18 +96,65 @@ def test_radius_graph_bit_exact(cuda, case):
     assert np.array_equal(goff.cpu().numpy(), off)
 
 
-def test_radius_graph_brute_force_and_skin(cuda):
-    """Against the oracle's all-pairs, all-images enumeration; and the skin policy of
-    NeighborList (no rebuild below skin / 2 of motion, rebuild above)."""
+def test_radius_graph_brute_force(cuda):
+    """Against the oracle's all-pairs, all-images enumeration."""
     from oracle.graph import neighbor_list_bruteforce
-    from ops.neighbors import NeighborList, radius_graph
+    from ops.neighbors import radius_graph
     s = _triclinic(n=120, seed=11)
     ref_ei, ref_off = neighbor_list_bruteforce(s.pos, s.cell, s.pbc, 6.0, 30)
     pos = torch.from_numpy(s.pos).to(cuda)
     gei, goff = radius_graph(pos, s.cell, s.pbc, 6.0, 30)
     assert np.array_equal(gei.cpu().numpy(), ref_ei) and np.array_equal(goff.cpu().numpy(), ref_off)
-    nl = NeighborList(6.0, 30, skin=0.5)
-    g0 = nl(pos, s.cell, s.pbc)
-    assert nl(pos + 0.1, s.cell, s.pbc)[0] is g0[0] and nl.builds == 1
-    nl(pos + torch.tensor([0.3, 0.0, 0.0], device=cuda), s.cell, s.pbc)
+
+
+def _pairs_within(ei, off, pos, cell, cutoff):
+    """{(sender, receiver, o0, o1, o2)} of the edges shorter than cutoff (float64)."""
+    ei, off = ei.cpu().numpy(), off.cpu().numpy()
+    p = pos.detach().cpu().numpy().astype(np.float64)
+    d = p[ei[0]] - p[ei[1]] + off.astype(np.float64) @ np.asarray(cell, np.float64)
+    keep = np.sqrt((d * d).sum(1)) < cutoff
+    return set(map(tuple, np.concatenate([ei.T, off.astype(np.int64)], 1)[keep].tolist()))
+
+
+def test_neighbor_list_skin_reuse(cuda):
+    """NeighborList(skin): the reused graph holds every pair within the cutoff of the moved
+    positions (the same set as a fresh uncapped graph), energies and forces through the
+    model equal those of the fresh graph, and a move beyond skin / 2 or a cell change
+    rebuilds; a cap together with a skin is refused."""
+    import heads
+    import systems
+    from ops.neighbors import NL_CAP, NeighborList, radius_graph
+    with pytest.raises(ValueError):
+        NeighborList(6.0, 30, skin=0.5)
+    s = systems.water_box(n_mol=40, L=10.5, seed=1)
+    pos0 = torch.from_numpy(s.pos).to(cuda)
+    nl = NeighborList(6.0, None, skin=0.6)
+    g0 = nl(pos0, s.cell, s.pbc)
+    rng = np.random.default_rng(3)
+    step = rng.normal(size=s.pos.shape)
+    step *= 0.29 / np.linalg.norm(step, axis=1).max()          # largest move 0.29 < skin / 2
+    pos1 = pos0 + torch.from_numpy(step.astype(np.float32)).to(cuda)
+    g1 = nl(pos1, s.cell, s.pbc)
+    assert g1[0] is g0[0] and nl.builds == 1
+    fresh = radius_graph(pos1, s.cell, s.pbc, 6.0, NL_CAP)
+    assert _pairs_within(*g1, pos1, s.cell, 6.0) == _pairs_within(*fresh, pos1, s.cell, 6.0)
+    assert g1[0].shape[1] > fresh[0].shape[1]          # the reused graph carries extra pairs
+
+    from test_gpu_model import _build
+    _, _, model = _build(cuda)
+    moved = systems.AtomicSystem("water_moved", pos1.cpu().numpy(), s.Z, s.cell, s.pbc)
+    outs = []
+    for ei, off in (g1, fresh):
+        data = heads.make_atomic_data(moved, ei.cpu().numpy(), off.cpu().numpy(), cuda)
+        out = model(data, compute_forces=True, compute_stress=False)
+        outs.append({k: v.detach().double().cpu() for k, v in out.items() if torch.is_tensor(v)})
+    e_rel = abs(outs[0]["energy"].item() - outs[1]["energy"].item()) / abs(outs[1]["energy"].item())
+    f_err = (outs[0]["forces"] - outs[1]["forces"]).abs().max().item()
+    print(f"reused vs fresh graph: E rel {e_rel:.2e}, F max-abs {f_err:.2e}")
+    assert e_rel <= 1e-6 and f_err <= 1e-4
+
+    nl(pos0 + 0.31 * torch.tensor([1.0, 0.0, 0.0], device=cuda), s.cell, s.pbc)   # 0.31 > skin / 2
     assert nl.builds == 2
+    cell2 = np.asarray(s.cell, np.float64) * 1.001
+    nl(pos0 + 0.31 * torch.tensor([1.0, 0.0, 0.0], device=cuda), cell2, s.pbc)
+    assert nl.builds == 3

@@ -66,3 +66,29 @@ def test_constants_names_match_reference():
     assert (K.W11, K.W13, K.W21, K.W33, K.W44, K.W48, K.W54, K.W88) == (0, 2, 3, 8, 9, 13, 14, 33)
     assert (K.X_M0_MULT, K.Y_M0_MULT, K.Z_M0_MULT, K.TRUNC_Y_M0_MULT, K.TRUNC_Z_M0_MULT) == (6, 5, 3, 5, 3)
     assert abs(K.S3X4 - 8 * 3 ** 0.5) < 1e-12 and abs(K.S3 - 2 * 3 ** 0.5) < 1e-12
+
+
+def test_atom_range_check_is_not_skipped_for_a_new_tensor():
+    """The host range check of atomic numbers and batch ids runs again for a new tensor even
+    when it reuses the address of a freed, already-checked one, and after an in-place edit."""
+    import torch
+    import model
+    m = model.eSCN_Inference_Model(num_layers=1, sphere_channels=8, num_distance_basis=4)
+    batch = torch.zeros(64, dtype=torch.long)
+    Z = torch.full((64,), 26, dtype=torch.long)
+    m._check_atoms(Z, batch, 1)
+    m._check_atoms(Z, batch, 1)                 # same tensors: cached
+    del Z
+    for _ in range(4):                          # likely to land on the freed address
+        Z_bad = torch.full((64,), 26, dtype=torch.long)
+        Z_bad[5] = 250
+        with pytest.raises(ValueError):
+            m._check_atoms(Z_bad, batch, 1)
+        del Z_bad
+    Z = torch.full((64,), 8, dtype=torch.long)
+    m._check_atoms(Z, batch, 1)
+    Z[3] = -1                                   # in-place edit bumps the version
+    with pytest.raises(ValueError):
+        m._check_atoms(Z, batch, 1)
+    with pytest.raises(ValueError):
+        m._check_atoms(torch.full((64,), 8, dtype=torch.long), batch, 0)   # batch id 0 >= 0 systems
