@@ -245,7 +245,8 @@ class eSCNMDBackbone(nn.Module):
 
     def __init__(self, num_layers: int = 4, sphere_channels: int = 128, hidden_channels: int = 128,
                  lmax: int = 2, mmax: int = 2, num_distance_basis: int = 64, cutoff: float = 6.0,
-                 max_neighbors: int = 30, max_num_elements: int = 100, seed: int = 0):
+                 max_neighbors: int = 30, max_num_elements: int = 100, seed: int = 0,
+                 charge_channels: tuple = (0, 0), spin_channels: tuple = (0, 0)):
         super().__init__()
         if mmax != 2:
             raise ValueError("only mmax = 2 is modelled")
@@ -271,6 +272,7 @@ class eSCNMDBackbone(nn.Module):
         self.dataset_embedding = None
         self.use_dataset_embedding = False
         self.mix_csd = _linear(2 * C, C, True, g)
-        self.charge_channel_start = self.charge_channel_end = 0
-        self.spin_channel_start = self.spin_channel_end = 0
+        # l = 0 channel ranges balanced to the system charge / spin after every block
+        self.charge_channel_start, self.charge_channel_end = (int(v) for v in charge_channels)
+        self.spin_channel_start, self.spin_channel_end = (int(v) for v in spin_channels)
         self.regress_config = SimpleNamespace(forces=True, stress=True, direct_forces=False)

@@ -244,3 +244,64 @@ class EdgeShifts(torch.autograd.Function):
 
 def edge_shifts(cell_offsets, cell):
     return EdgeShifts.apply(cell_offsets, cell)
+
+
+def system_ptr(batch: torch.Tensor, n_systems: int) -> torch.Tensor:
+    """(S + 1,) int32 segment pointers of a batch vector sorted ascending (atoms of system s
+    are rows [ptr[s], ptr[s + 1]))."""
+    batch = _lib.require(batch, torch.int64, "batch")
+    ptr = torch.empty(n_systems + 1, dtype=torch.int32, device=batch.device)
+    _lib.call("fu_csr_row_ptr", batch.data_ptr(), batch.numel(), ptr.data_ptr(), n_systems,
+              _lib.stream_ptr(batch.device))
+    return ptr
+
+
+def _balance(x, batch, sys_ptr, target, offset, S, start, end):
+    N, K, C = x.shape
+    out = torch.empty_like(x)
+    corr = torch.empty(max(S * (end - start), 1), device=x.device, dtype=torch.float32)
+    _lib.call("fu_balance_channels", x.data_ptr(), out.data_ptr(), batch.data_ptr(), sys_ptr.data_ptr(),
+              _lib.ptr(target), float(offset), corr.data_ptr(), corr.numel(), N, K, C, S, start, end,
+              _lib.stream_ptr(x.device))
+    return out
+
+
+class BalanceChannels(torch.autograd.Function):
+    """FAIRChem balance_channels_batched (model.py:213-216) on fu_balance_channels: the l = 0
+    coefficients of channels [start, end) are shifted per system so that they sum to
+    target - target_offset over the system's atoms.  Affine in x, so the input gradient
+    removes the per-system mean of those channels' output gradient."""
+
+    @staticmethod
+    def forward(ctx, emb, target, batch, sys_ptr, start, end, offset):
+        emb = _lib.require(emb, torch.float32, "emb")
+        batch = _lib.require(batch, torch.int64, "batch")
+        target = _lib.require(target.reshape(-1), torch.float32, "target")
+        S = target.numel()
+        ctx.save_for_backward(batch, sys_ptr)
+        ctx.S, ctx.start, ctx.end = S, start, end
+        return _balance(emb, batch, sys_ptr, target, offset, S, start, end)
+
+    @staticmethod
+    def backward(ctx, g_out):
+        batch, sys_ptr = ctx.saved_tensors
+        g = _balance(g_out.contiguous(), batch, sys_ptr, None, 0.0, ctx.S, ctx.start, ctx.end)
+        return g, None, None, None, None, None, None
+
+
+def balance_channels_batched(emb, target, natoms, batch, start_idx: int, end_idx: int, target_offset: float = 0.0,
+                             sys_ptr=None):
+    """FAIRChem's balance_channels_batched with its argument meaning (emb (N, K, C), target
+    (S,) per-system charge or spin, natoms (S,) atoms per system, batch (N,) sorted
+    ascending).  The divisor n_s is the length of system s's batch segment, which equals
+    natoms[s] for consistent inputs.  sys_ptr: the system segments of batch when already
+    known (system_ptr)."""
+    if target is None:
+        raise ValueError("balance_channels_batched: the backbone balances channels but no per-system target "
+                         "(charge or spin) was given")
+    S = int(target.numel())
+    if natoms is not None and int(natoms.numel()) != S:
+        raise ValueError(f"balance_channels_batched: {int(natoms.numel())} systems in natoms, {S} targets")
+    if sys_ptr is None:
+        sys_ptr = system_ptr(batch, S)
+    return BalanceChannels.apply(emb, target, batch, sys_ptr, int(start_idx), int(end_idx), float(target_offset))

@@ -98,65 +98,26 @@ class RadialBank(torch.nn.Module):
             reg(f"W3_{k}_t", m[8].t())
             reg(f"b3_{k}", m[9])
 
-    # Below SIDE_STREAM_MIN_EDGES the output layers stay on the caller's stream: the events
-    # and stream bookkeeping cost more host time than the overlap saves on a small graph
-    # (Cu slab, 859 edges: +0.4 ms/step with the side stream; 30 k edges: -0.06 ms).
-    # Above SIDE_STREAM_MAX_EDGES they stay there too: the side stream's allocations form a
-    # second caching-allocator pool, and on a graph whose step needs a large share of HBM
-    # (50,000 atoms / 1.5 M edges: 138 GiB allocated, over 216 GiB reserved with two pools,
-    # 151 GiB with one) the reserve approaches the card's capacity and the allocator starts
-    # freeing and re-mapping memory inside the step (up to twice the step time), while the
-    # overlap itself is worth under 1 % there.
-    SIDE_STREAM_MIN_EDGES = 20_000
-    SIDE_STREAM_MAX_EDGES = 600_000
+    # All layers run on the caller's stream.  A side stream for the output layers (tried:
+    # under 1 % of step time at best) makes the caching allocator hold every block it
+    # touched across streams until the other stream's events complete; with the host
+    # enqueueing steps ahead of the GPU, as it does in an MD loop without host reads, the
+    # reserve then grew from 31 to 230 GB on the 8,192-atom Fe cell, and the allocations
+    # on that path stalled the host for seconds in some processes.
 
-    def forward(self, gauss, Z, idx_i, idx_j, streams: bool = True):
+    def forward(self, gauss, Z, idx_i, idx_j):
         """gauss (E, B) -> tuple of G radial outputs (E, n_k).
 
-        The trunk (first two layers of all MLPs) runs on the current stream.  Each block's
-        output layer is its own autograd node launched on a side stream (streams=True and
-        SIDE_STREAM_MIN_EDGES to SIDE_STREAM_MAX_EDGES edges), so
-        blocks 2..G are computed while the caller already consumes block 1, and in the
-        backward each block's input gradient runs as soon as its output gradient exists,
-        concurrently with the caller's remaining backward: the autograd engine runs every
-        backward on the stream of its forward and orders the streams with events.  Call
-        wait(k) on the consuming stream before reading output k."""
+        The trunk (first two layers of all MLPs) is one autograd node; each block's output
+        layer is its own node, whose backward writes its input gradient straight into the
+        trunk's gradient buffer."""
         holder = _GradHolder()
         h2s = _RadialTrunkFn.apply(gauss, Z, idx_i, idx_j, self, holder)
-        main = torch.cuda.current_stream(gauss.device)
-        use_side = streams and self.SIDE_STREAM_MIN_EDGES <= gauss.shape[0] <= self.SIDE_STREAM_MAX_EDGES
-        side = self._side_stream(gauss.device) if use_side else main
-        cross = side is not main
-        outs, self._events = [], []
-        if cross:
-            side.wait_stream(main)
-            if holder.g is not None:
-                holder.g.record_stream(side)
-        with torch.cuda.stream(side):
-            for k in range(self.G):
-                W, Wt, b = getattr(self, f"W3_{k}"), getattr(self, f"W3_{k}_t"), getattr(self, f"b3_{k}")
-                if cross:
-                    h2s[k].record_stream(side)
-                out = _RadialOutFn.apply(h2s[k], W, b, Wt, holder, k, cross)
-                if cross:
-                    out.record_stream(main)
-                    ev = torch.cuda.Event()
-                    ev.record(side)
-                    self._events.append(ev)
-                outs.append(out)
+        outs = []
+        for k in range(self.G):
+            W, Wt, b = getattr(self, f"W3_{k}"), getattr(self, f"W3_{k}_t"), getattr(self, f"b3_{k}")
+            outs.append(_RadialOutFn.apply(h2s[k], W, b, Wt, holder, k))
         return tuple(outs)
-
-    def wait(self, k: int) -> None:
-        """Make the current stream wait until output k has been computed."""
-        if self._events:
-            torch.cuda.current_stream().wait_event(self._events[k])
-
-    def _side_stream(self, device):
-        st = getattr(self, "_side", None)
-        if st is None or st.device != device:
-            st = torch.cuda.Stream(device)   # default priority
-            self._side = st
-        return st
 
 
 class _GradHolder:
@@ -220,21 +181,18 @@ class _RadialOutFn(torch.autograd.Function):
     the trunk's gradient buffer and returns that slice."""
 
     @staticmethod
-    def forward(ctx, h2k, W, b, Wt, holder, k, cross):
+    def forward(ctx, h2k, W, b, Wt, holder, k):
         ctx.save_for_backward(Wt)
-        ctx.holder, ctx.k, ctx.cross = holder, k, cross
+        ctx.holder, ctx.k = holder, k
         return _gemm(h2k, W, b, torch.empty(h2k.shape[0], W.shape[0], device=h2k.device, dtype=torch.float32))
 
     @staticmethod
     def backward(ctx, g_rad):
         (Wt,) = ctx.saved_tensors
         g_rad = g_rad.contiguous()
-        if ctx.cross:
-            # produced on the main stream, read here on the side stream
-            g_rad.record_stream(torch.cuda.current_stream())
         if ctx.holder.g is None:
             raise _lib.FlashUMAError("radial bank: backward through an output built without input gradients")
         C = Wt.shape[0]
         sl = ctx.holder.g[:, ctx.k * C:(ctx.k + 1) * C]
         _gemm(g_rad, Wt, None, sl)
-        return sl, None, None, None, None, None, None
+        return sl, None, None, None, None, None

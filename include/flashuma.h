@@ -313,6 +313,19 @@ int fu_gate_act_fwd(const float* pre, const float* h, float* out, int64_t N, int
 int fu_gate_act_bwd(const float* pre, const float* h, const float* g_out, float* g_pre,
                     float* g_h, int64_t N, int32_t H, int32_t lmax, void* stream);
 
+/* Charge / spin channel balancing (FAIRChem balance_channels_batched, called per block at
+ * model.py:213-216).  x, out (N, K, C) fp32; batch (N) sorted ascending with ids in [0, S);
+ * sys_ptr (S + 1, int32) the system segments of batch (fu_csr_row_ptr over batch).  For
+ * each system s and channel c in [c0, c1):
+ *   out[a][0][c] = x[a][0][c] + (target[s] - target_offset - sum_{a in s} x[a][0][c]) / n_s,
+ * everything else copied.  target NULL means 0 (the input gradient: pass the output
+ * gradient as x and target_offset 0).  corr is a workspace of S * (c1 - c0) floats.  Sums
+ * in fp64 in a fixed order (deterministic). */
+int fu_balance_channels(const float* x, float* out, const int64_t* batch, const int32_t* sys_ptr,
+                        const float* target, float target_offset, float* corr, int64_t corr_len,
+                        int64_t N, int32_t K, int32_t C, int32_t S, int32_t c0, int32_t c1,
+                        void* stream);
+
 /* Row permutations (model.py:72-74,221): gather dst[r] = src[idx[r]]; scatter
  * dst[idx[r]] = src[r] (idx a permutation, each destination row written once). */
 int fu_gather_rows(const float* src, const int64_t* idx, float* dst, int64_t rows, int32_t width,

@@ -137,6 +137,13 @@ def energy_forces_stress(backbone, head, pos, Z, cell, edge_index, cell_offsets,
             x_mid = R.rotate_scatter_lmax(Zo0, Zo1, Zo2, wigner, wig_ext, env, x, idx_j, N, L)
         h = rms_norm_sh(x_mid, P[pre + "norm_2.affine_weight"], P[pre + "norm_2.affine_bias"], lmax, 1e-5)
         x = spectral_atomwise(h, P, pre + "atom_wise.", lmax, Hc) + x_mid
+        # charge / spin channel balancing after every block (model.py:213-216)
+        if backbone.charge_channel_end > backbone.charge_channel_start:
+            x = R.balance_channels(x, torch.tensor([charge]), batch, 1, backbone.charge_channel_start,
+                                   backbone.charge_channel_end, 0.0)
+        if backbone.spin_channel_end > backbone.spin_channel_start:
+            x = R.balance_channels(x, torch.tensor([spin]), batch, 1, backbone.spin_channel_start,
+                                   backbone.spin_channel_end, 1.0)
     x = rms_norm_sh(x, P["norm.affine_weight"], P["norm.affine_bias"], lmax, 1e-5)
 
     h = x[:, 0]

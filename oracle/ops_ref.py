@@ -292,6 +292,20 @@ def layer_norm_silu(x, gamma, beta, eps=1e-7):
     return torch.nn.functional.silu(y)
 
 
+def balance_channels(emb, target, batch, n_systems: int, start: int, end: int, offset: float):
+    """FAIRChem balance_channels_batched as the reference calls it after every block
+    (model.py:213-216; target = per-system charge with offset 0, or spin with offset 1).
+    FAIRChem is absent, so this restates its published definition: the l = 0 coefficients
+    of channels [start, end) of each system's atoms are shifted by one common amount per
+    channel so that they sum to target - offset over the system; all else is unchanged."""
+    ch = emb[:, 0, start:end]
+    sums = torch.zeros(n_systems, end - start, dtype=emb.dtype).index_add(0, batch, ch)
+    n = torch.bincount(batch, minlength=n_systems).to(emb.dtype).clamp_min(1.0)
+    corr = (target.to(emb.dtype)[:, None] - offset - sums) / n[:, None]
+    l0 = torch.cat([emb[:, 0, :start], ch + corr[batch], emb[:, 0, end:]], 1)
+    return torch.cat([l0[:, None], emb[:, 1:]], 1)
+
+
 def pack_so2(R: torch.Tensor, I: torch.Tensor) -> torch.Tensor:
     """Real block matrix [[R, -I], [I, R]] of the complex map R + iI (model.py:111-138)."""
     return torch.cat([torch.cat([R, -I], 1), torch.cat([I, R], 1)], 0)

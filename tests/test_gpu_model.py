@@ -237,3 +237,54 @@ def test_atoms_without_neighbours(cuda, case):
     assert torch.equal(out["forces"][-1], torch.zeros(3))
     if case == "no_edges":
         assert torch.equal(out["stress"], torch.zeros(1, 3, 3))
+
+
+def test_charge_spin_balanced_channels(cuda):
+    """A backbone that reserves l = 0 channels for charge (0..8) and spin (8..16) balancing
+    (FAIRChem balance_channels_batched after every block, model.py:213-216): a batch of two
+    systems with different charges and spins, each against the float64 oracle of that
+    system alone (energy, forces, stress).
+
+    With balancing the energy of these random-init weights is more sensitive to rounding:
+    float32 runs of the oracle itself, on the same system with atoms and edges relabelled
+    (other summation orders), land 0.8e-6 to 1.5e-6 from float64 on the water system (1.8e-8
+    without balancing).  The energy bar is therefore max(1e-6, 2 x the largest deviation of
+    three such float32 runs); forces and stress keep 1e-4."""
+    import copy
+    import escn_md
+    import heads
+    import systems
+    from oracle.model_ref import energy_forces_stress
+    from wrapper import ZeroAllocBackbone
+    bb = escn_md.eSCNMDBackbone(seed=0, charge_channels=(0, 8), spin_channels=(8, 16))
+    hd = heads.MLPEnergyHead(bb.sphere_channels, bb.hidden_channels, seed=1)
+    bb_cpu, hd_cpu = copy.deepcopy(bb), copy.deepcopy(hd)
+    model = heads.PotentialModel(ZeroAllocBackbone(bb.to(cuda)), hd.to(cuda))
+    specs = ((systems.cu_slab_co, 1, 2), (lambda: systems.water_box(n_mol=20, L=8.5, seed=4), -1, 3))
+    items = []
+    for build, chg, spn in specs:
+        s = build()
+        ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, bb.cutoff, bb.max_neighbors)
+        items.append((s, ei, off, chg, spn))
+    out = model(heads.make_batch_data(items, cuda), compute_forces=True, compute_stress=True)
+    forces = out["forces"].detach().cpu().split([it[0].n_atoms for it in items])
+    for k, (s, ei, off, chg, spn) in enumerate(items):
+        ref = energy_forces_stress(bb_cpu, hd_cpu, s.pos, s.Z, s.cell, ei, off, charge=chg, spin=spn,
+                                   dtype=torch.float64)
+        unbalanced = energy_forces_stress(escn_md.eSCNMDBackbone(seed=0), hd_cpu, s.pos, s.Z, s.cell, ei, off,
+                                          charge=chg, spin=spn, dtype=torch.float64)
+        assert abs(unbalanced["energy"].item() - ref["energy"].item()) > 1e-4 * abs(ref["energy"].item())
+        floor = 0.0
+        for seed in range(3):
+            rng = np.random.default_rng(seed)
+            p, ep = rng.permutation(s.n_atoms), rng.permutation(ei.shape[1])
+            inv = np.argsort(p)
+            r32 = energy_forces_stress(bb_cpu, hd_cpu, s.pos[p], s.Z[p], s.cell, inv[ei[:, ep]], off[ep],
+                                       charge=chg, spin=spn, dtype=torch.float32, stress=False)
+            floor = max(floor, abs(r32["energy"].double().item() - ref["energy"].item()) / abs(ref["energy"].item()))
+        e = out["energy"][k].double().item()
+        e_rel = abs(e - ref["energy"].item()) / abs(ref["energy"].item())
+        print(f"system {k}: E {e:.8f} oracle {ref['energy'].item():.8f} rel {e_rel:.2e} (fp32 oracle {floor:.2e})")
+        assert e_rel <= max(1e-6, 2.0 * floor)
+        assert (forces[k].double() - ref["forces"]).abs().max().item() <= 1e-4
+        assert (out["stress"][k].detach().cpu().double() - ref["stress"][0]).abs().max().item() <= 1e-4

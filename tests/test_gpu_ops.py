@@ -262,12 +262,10 @@ def test_matmul_mode_switch(cuda):
         _lib.set_matmul_mode(7)
 
 
-@pytest.mark.parametrize("side_stream", [True, False], ids=["side_stream", "one_stream"])
 @pytest.mark.parametrize("C", [128, 64])
-def test_radial_bank(cuda, C, side_stream):
+def test_radial_bank(cuda, C):
     """All radial MLPs as one bank (element embeddings folded into per-element tables) against
-    the textbook per-block MLP on x_edge_raw = [g | W_src[Z_i] | W_tgt[Z_j]] in float64; with
-    the output layers on the side stream (the threshold lowered to this graph) and without."""
+    the textbook per-block MLP on x_edge_raw = [g | W_src[Z_i] | W_tgt[Z_j]] in float64."""
     from ops.radial import RadialBank
     g = torch.Generator().manual_seed(C)
     N, E, B = 50, 777, 64
@@ -296,11 +294,8 @@ def test_radial_bank(cuda, C, side_stream):
 
     rref, (gref,) = _vjp(ref, [gauss], cot)
     bank = RadialBank([tuple(t.to(cuda) for t in m) for m in mlps], W_src.to(cuda), W_tgt.to(cuda), B)
-    bank.SIDE_STREAM_MIN_EDGES = 0 if side_stream else 1 << 62
     gg = gauss.to(cuda).requires_grad_(True)
     rads = bank(gg, Z.to(cuda), ii.to(cuda), jj.to(cuda))
-    for k in range(len(rads)):
-        bank.wait(k)
     for a, b in zip(rads, rref):
         assert_close(a, b, TOL, "radial bank fwd")
     (gr,) = torch.autograd.grad(rads, gg, [c.to(cuda) for c in cot], retain_graph=True)
@@ -607,3 +602,25 @@ def test_edge_shifts_and_permutation(cuda):
     ref_g = torch.zeros_like(cot)
     ref_g[perm] = cot
     assert torch.equal(gs.cpu(), ref_g)
+
+
+@pytest.mark.parametrize("start,end,offset", [(0, 16, 0.0), (5, 13, 1.0), (120, 128, 1.0)])
+def test_balance_channels(cuda, start, end, offset):
+    """fu_balance_channels against the float64 restatement (forward and input gradient) on
+    three systems of different sizes, and the defining property on the GPU output."""
+    from ops.node import balance_channels_batched
+    g = torch.Generator().manual_seed(start)
+    sizes = [37, 5, 130]
+    batch = torch.repeat_interleave(torch.arange(3), torch.tensor(sizes))
+    emb = torch.randn(sum(sizes), 9, 128, generator=g)
+    target = torch.tensor([1, -2, 0])
+    cot = torch.randn(emb.shape, generator=g)
+    ref, (gref,) = _vjp(lambda e: (R.balance_channels(e, target, batch, 3, start, end, offset),), [emb], [cot])
+    eg = emb.to(cuda).requires_grad_(True)
+    out = balance_channels_batched(eg, target.to(cuda), torch.tensor(sizes).to(cuda), batch.to(cuda), start, end,
+                                   offset)
+    (gg,) = torch.autograd.grad(out, eg, cot.to(cuda))
+    assert_close(out, ref[0], TOL, "balance fwd")
+    assert_close(gg, gref, TOL, "balance bwd")
+    sums = torch.zeros(3, end - start, dtype=torch.float64).index_add(0, batch, out.detach().cpu().double()[:, 0, start:end])
+    assert (sums - (target.double() - offset)[:, None]).abs().max().item() < 1e-4

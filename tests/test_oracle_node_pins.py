@@ -302,3 +302,68 @@ def test_spectral_atomwise_equivariant(lmax):
     C, H = 6, 5
     P = _ffn_params(lmax, C, H, 70)
     assert _equivariance_error(lambda x: M.spectral_atomwise(x, P, "f.", lmax, H), lmax, C, 80) < 1e-12
+
+
+# ---- charge / spin channel balancing (FAIRChem balance_channels_batched, model.py:213-216) ----
+#
+# Parity with FAIRChem is unpinned (absent); the restatement is pinned by its defining
+# properties: after balancing, every system's l = 0 sum of each balanced channel equals
+# target - offset; the shift is one constant per (system, channel); nothing else changes;
+# balancing is idempotent.  Planted mistakes (offset added instead of subtracted, one global
+# atom count instead of each system's, the shift spread over every coefficient) fail them.
+
+def _balance_case():
+    g = _gen(11)
+    sizes = [5, 9, 3]
+    batch = torch.repeat_interleave(torch.arange(3), torch.tensor(sizes))
+    emb = torch.randn(sum(sizes), 9, 16, generator=g, dtype=DT)
+    target = torch.tensor([1.0, -2.0, 0.0], dtype=DT)
+    return emb, target, batch, 3
+
+
+def _balance_ok(fn):
+    from oracle import ops_ref as R
+    emb, target, batch, S = _balance_case()
+    start, end, off = 3, 9, 1.0
+    out = fn(emb, target, batch, S, start, end, off)
+    sums = torch.zeros(S, end - start, dtype=DT).index_add(0, batch, out[:, 0, start:end])
+    ok = torch.allclose(sums, (target - off)[:, None].expand_as(sums), atol=1e-12)
+    shift = out[:, 0, start:end] - emb[:, 0, start:end]
+    for s in range(S):
+        seg = shift[batch == s]
+        ok &= bool(torch.allclose(seg, seg[:1].expand_as(seg), atol=1e-12))
+    rest = out.clone()
+    rest[:, 0, start:end] = emb[:, 0, start:end]
+    ok &= torch.equal(rest, emb)
+    ok &= torch.allclose(fn(out, target, batch, S, start, end, off), out, atol=1e-12)
+    return bool(ok)
+
+
+def test_balance_channels_defining_properties():
+    from oracle import ops_ref as R
+    assert _balance_ok(R.balance_channels)
+
+
+def test_balance_channels_planted_mistakes_fail():
+    from oracle import ops_ref as R
+
+    def plus_offset(emb, target, batch, S, start, end, off):
+        return R.balance_channels(emb, target, batch, S, start, end, -off)
+
+    def global_count(emb, target, batch, S, start, end, off):
+        ch = emb[:, 0, start:end]
+        sums = torch.zeros(S, end - start, dtype=emb.dtype).index_add(0, batch, ch)
+        corr = (target[:, None] - off - sums) / emb.shape[0]
+        out = emb.clone()
+        out[:, 0, start:end] = ch + corr[batch]
+        return out
+
+    def every_coefficient(emb, target, batch, S, start, end, off):
+        out = R.balance_channels(emb, target, batch, S, start, end, off)
+        d = out[:, 0:1, start:end] - emb[:, 0:1, start:end]
+        res = emb.clone()
+        res[:, :, start:end] = emb[:, :, start:end] + d
+        return res
+
+    for bad in (plus_offset, global_count, every_coefficient):
+        assert not _balance_ok(bad), bad.__name__
