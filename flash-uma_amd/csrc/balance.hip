@@ -13,6 +13,8 @@
 // bits), so a system is the CSR segment [sys_ptr[s], sys_ptr[s + 1]).  One workgroup per
 // system sums its segment in fp64 with a fixed lane assignment and a fixed tree: the result
 // is deterministic.  A second, bandwidth-bound pass writes the output rows.
+#include <mutex>
+
 #include "fu_common.h"
 
 namespace fu {
@@ -83,24 +85,15 @@ __global__ __launch_bounds__(256) void balance_apply_kernel(const float* __restr
 
 using namespace fu;
 
-extern "C" int fu_balance_channels(const float* x, float* out, const int64_t* batch, const int32_t* sys_ptr,
-                                   const float* target, float target_offset, float* corr, int64_t corr_len,
-                                   int64_t N, int32_t K, int32_t C, int32_t S, int32_t c0, int32_t c1,
-                                   void* stream) {
-  if (N < 0 || K <= 0 || C <= 0 || S <= 0 || c0 < 0 || c1 < c0 || c1 > C)
-    return set_error(FU_ERR_SHAPE, "fu_balance_channels: bad shape (N=%lld K=%d C=%d S=%d range [%d, %d))",
-                     (long long)N, K, C, S, c0, c1);
+namespace {
+
+int balance_launch(const char* who, const float* x, float* out, const int64_t* batch, const int32_t* sys_ptr,
+                   const float* target, float target_offset, float* corr, int64_t N, int32_t K, int32_t C,
+                   int32_t S, int32_t c0, int32_t c1, hipStream_t s) {
   const int32_t nch = c1 - c0;
   const int64_t row = (int64_t)K * C;
-  if (row % 4 != 0) return set_error(FU_ERR_SHAPE, "fu_balance_channels: K*C=%lld not a multiple of 4", (long long)row);
-  if (corr_len < (int64_t)S * nch)
-    return set_error(FU_ERR_WORKSPACE, "fu_balance_channels: corr workspace needs %lld floats",
-                     (long long)S * nch);
-  if (N == 0) return FU_OK;
-  if (!x || !out || !batch || !sys_ptr || (nch > 0 && !corr))
-    return set_error(FU_ERR_NULL, "fu_balance_channels: NULL argument");
-  if (!aligned16(x) || !aligned16(out)) return set_error(FU_ERR_ALIGN, "fu_balance_channels: x/out not 16-byte aligned");
-  hipStream_t s = as_stream(stream);
+  if (!x || !out || !batch || !sys_ptr || (nch > 0 && !corr)) return set_error(FU_ERR_NULL, "%s: NULL argument", who);
+  if (!aligned16(x) || !aligned16(out)) return set_error(FU_ERR_ALIGN, "%s: x/out not 16-byte aligned", who);
   if (nch > 0) {
     int W = 1;
     while (W < nch && W < 64) W <<= 1;
@@ -110,5 +103,76 @@ extern "C" int fu_balance_channels(const float* x, float* out, const int64_t* ba
   const int64_t n4 = N * row / 4;
   hipLaunchKernelGGL(balance_apply_kernel, dim3((unsigned)std::min<int64_t>(cdiv(n4, 256), 8192)), dim3(256), 0, s, x,
                      batch, corr, out, n4, row, c0, nch);
-  return check_launch("fu_balance_channels");
+  return check_launch(who);
+}
+
+int balance_check_shape(const char* who, int64_t N, int32_t K, int32_t C, int32_t S, int32_t c0, int32_t c1) {
+  if (N < 0 || K <= 0 || C <= 0 || S <= 0 || c0 < 0 || c1 < c0 || c1 > C)
+    return set_error(FU_ERR_SHAPE, "%s: bad shape (N=%lld K=%d C=%d S=%d range [%d, %d))", who, (long long)N, K, C,
+                     S, c0, c1);
+  if (((int64_t)K * C) % 4 != 0)
+    return set_error(FU_ERR_SHAPE, "%s: K*C=%lld not a multiple of 4", who, (long long)K * C);
+  return FU_OK;
+}
+
+// Scratch of the allocation-free entry point: the per-(system, channel) corrections.  One
+// copy per GPU, held until the process ends; every call on a GPU reuses it.
+constexpr int64_t kBalanceScratchFloats = FU_BALANCE_NOALLOC_MAX_CORR;
+__device__ __align__(256) float scratch[kBalanceScratchFloats];
+
+// Device address of `scratch` on each GPU, looked up once per device (with that device
+// current) on the first call there.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+int scratch_for_current_device(float** ptr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(FU_ERR_LAUNCH, "fu_balance_channels_noalloc: no current HIP device (or device id >= %d)",
+                     kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(FU_ERR_LAUNCH, "fu_balance_channels_noalloc: hipGetSymbolAddress failed on device %d: %s", dev,
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *ptr = g_scratch_ptr[dev];
+  return FU_OK;
+}
+
+}  // namespace
+
+extern "C" int fu_balance_channels(const float* x, float* out, const int64_t* batch, const int32_t* sys_ptr,
+                                   const float* target, float target_offset, float* corr, int64_t corr_len,
+                                   int64_t N, int32_t K, int32_t C, int32_t S, int32_t c0, int32_t c1,
+                                   void* stream) {
+  const char* who = "fu_balance_channels";
+  int st = balance_check_shape(who, N, K, C, S, c0, c1);
+  if (st != FU_OK) return st;
+  if (corr_len < (int64_t)S * (c1 - c0))
+    return set_error(FU_ERR_WORKSPACE, "%s: corr workspace needs %lld floats", who, (long long)S * (c1 - c0));
+  if (N == 0) return FU_OK;
+  return balance_launch(who, x, out, batch, sys_ptr, target, target_offset, corr, N, K, C, S, c0, c1,
+                        as_stream(stream));
+}
+
+extern "C" int fu_balance_channels_noalloc(const float* x, float* out, const int64_t* batch, const int32_t* sys_ptr,
+                                           const float* target, float target_offset, int64_t N, int32_t K,
+                                           int32_t C, int32_t S, int32_t c0, int32_t c1, void* stream) {
+  const char* who = "fu_balance_channels_noalloc";
+  int st = balance_check_shape(who, N, K, C, S, c0, c1);
+  if (st != FU_OK) return st;
+  if ((int64_t)S * (c1 - c0) > kBalanceScratchFloats)
+    return set_error(FU_ERR_WORKSPACE, "%s: S * (c1 - c0) = %lld exceeds the built-in scratch of %lld floats", who,
+                     (long long)S * (c1 - c0), (long long)kBalanceScratchFloats);
+  if (N == 0) return FU_OK;
+  float* corr = nullptr;
+  st = scratch_for_current_device(&corr);
+  if (st != FU_OK) return st;
+  return balance_launch(who, x, out, batch, sys_ptr, target, target_offset, corr, N, K, C, S, c0, c1,
+                        as_stream(stream));
 }

@@ -57,6 +57,7 @@ SIGNATURES: dict[str, list] = {
     "fu_gate_act_fwd": [P, P, P, I64, I32, I32, P],
     "fu_gate_act_bwd": [P, P, P, P, P, I64, I32, I32, P],
     "fu_balance_channels": [P, P, P, P, P, F32, P, I64, I64, I32, I32, I32, I32, I32, P],
+    "fu_balance_channels_noalloc": [P, P, P, P, P, F32, I64, I32, I32, I32, I32, I32, P],
     "fu_gather_rows": [P, P, P, I64, I32, P],
     "fu_scatter_rows": [P, P, P, I64, I32, P],
     "fu_edge_shifts": [P, P, P, P, I64, P],

@@ -326,6 +326,20 @@ int fu_balance_channels(const float* x, float* out, const int64_t* batch, const 
                         int64_t N, int32_t K, int32_t C, int32_t S, int32_t c0, int32_t c1,
                         void* stream);
 
+/* Allocation-free variant of fu_balance_channels: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The corr workspace is a library-owned device
+ * array of FU_BALANCE_NOALLOC_MAX_CORR floats per GPU (256 KiB, held until the process ends;
+ * its address is looked up on the first call on each device, which must be the current
+ * device); S * (c1 - c0) above that returns FU_ERR_WORKSPACE.  Results equal
+ * fu_balance_channels bit for bit.  Calls that overlap on one GPU (several streams or host
+ * threads at once) share that array and race. */
+#define FU_BALANCE_NOALLOC_MAX_CORR 65536
+int fu_balance_channels_noalloc(const float* x, float* out, const int64_t* batch,
+                                const int32_t* sys_ptr, const float* target, float target_offset,
+                                int64_t N, int32_t K, int32_t C, int32_t S, int32_t c0, int32_t c1,
+                                void* stream);
+
 /* Row permutations (model.py:72-74,221): gather dst[r] = src[idx[r]]; scatter
  * dst[idx[r]] = src[r] (idx a permutation, each destination row written once). */
 int fu_gather_rows(const float* src, const int64_t* idx, float* dst, int64_t rows, int32_t width,
