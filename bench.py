@@ -69,7 +69,11 @@ def cpu_baseline(budget_s: float = 20.0, model_kw: dict | None = None, stress: b
     import systems
     from oracle.model_ref import energy_forces_stress
 
-    cores = min(16, len(os.sched_getaffinity(0)))
+    # the threads of the host share this process may use: the harness states it in
+    # OMP_NUM_THREADS (16 per GPU on the MI355X boxes, whatever the affinity mask shows);
+    # without it, every core of the affinity mask
+    affinity = len(os.sched_getaffinity(0))
+    cores = min(affinity, int(os.environ.get("OMP_NUM_THREADS", affinity)))
     torch.set_num_threads(cores)
     bb = escn_md.eSCNMDBackbone(seed=0, **(model_kw or {}))
     hd = heads.MLPEnergyHead(bb.sphere_channels, bb.hidden_channels, seed=1)
@@ -205,12 +209,18 @@ def main() -> None:
               "frac": d["frac"], "traffic": None}
         if "matrix_op" in d:
             rl.update(matrix_op=d["matrix_op"], fp32_tflops=d["fp32_tflops"])
+        # HBM bytes per launch of the dominant kernel from two rocprofv3 counter passes
+        # (FETCH_SIZE, WRITE_SIZE; profiles/<config>_pmc_traffic.md), labelled with the
+        # commit they were measured at: counters cannot be read inside this process
         pmc = os.path.join(ROOT, "profiles", "pmc_traffic.json")
         if os.path.exists(pmc):
             with open(pmc) as f:
-                tr = json.load(f).get(args.config, {}).get(dom)
+                js = json.load(f)
+            tr = js.get(args.config, {}).get(dom)
             if tr is not None:
                 rl["traffic"] = tr
+                rl["traffic_source"] = (f"rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, profiles/{args.config}_pmc_traffic.md, "
+                                        f"measured at commit {js.get('measured_at', 'unrecorded')}")
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -159,14 +159,27 @@ class Packed_eSCN_Layer(nn.Module):
 
     _COMPLEX = ("W_conv1_m1", "W_conv1_m2", "W_conv2_m1", "W_conv2_m2")
 
+    # The pre-split weights select the three-product (Gauss) complex kernel: y_i = T3 - T1 - T2
+    # loses relative accuracy when y_i is much smaller than T1 = x_r P^T, which needs one of P, Q
+    # to dominate the other.  A weight whose parts differ in Frobenius norm by more than this
+    # factor keeps the four-product kernel (no pre-split copy).
+    GAUSS_MAX_NORM_RATIO = 10.0
+
     def _complex_splits(self, dev: torch.device) -> tuple:
         """complex_weight_split of each frozen complex weight and of its transpose pair, in the
         order conv1_gate_conv2 takes them; built on first use on a device (the weights are
-        frozen), not part of the state dict."""
+        frozen), not part of the state dict.  None (four-product kernel) for an unbalanced
+        weight."""
         if getattr(self, "_splits_dev", None) != dev:
             sp = []
             for name in self._COMPLEX:
-                sp.append(complex_weight_split(getattr(self, name + "_R"), getattr(self, name + "_I")))
+                R, I = getattr(self, name + "_R"), getattr(self, name + "_I")
+                nr, ni = R.norm().item(), I.norm().item()
+                r = self.GAUSS_MAX_NORM_RATIO
+                if not (nr <= r * ni and ni <= r * nr):
+                    sp += [None, None]
+                    continue
+                sp.append(complex_weight_split(R, I))
                 sp.append(complex_weight_split(getattr(self, name + "_Rt"), getattr(self, name + "_It_neg")))
             self._splits, self._splits_dev = tuple(sp), dev
         return self._splits

@@ -248,6 +248,26 @@ def test_model_lmax_parity(cuda, L, layers):
     assert e_rel <= 1e-6 and f_err <= 1e-4 and s_err <= 1e-4
 
 
+def test_config5_model_on_fe54_fixture(cuda):
+    """BASELINE config 5's backbone (lmax = 4, mmax = 2, 8 layers, C = 128) on bcc Fe 3x3x3
+    (54 atoms, 30 edges per atom, E+F+S) against the committed float64 oracle fixture
+    (tests/golden/fe54_lmax4_oracle.npz).  Bars as for lmax = 2; per-atom contributions rel
+    1e-5 (a float32 oracle run is 1.6e-6 from float64 here)."""
+    import os
+    import systems
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "fe54_lmax4_oracle.npz"))
+    bb, hd, model = _model(cuda, 4, 8)
+    s = systems.AtomicSystem("fe54", g["pos"], g["Z"].astype(np.int64), g["cell"])
+    out = _run(model, s, g["edge_index"].astype(np.int64), g["cell_offsets"].astype(np.float32), cuda)
+    e_rel = abs(out["energy"].double().item() - g["energy"][0]) / abs(g["energy"][0])
+    f_err = np.abs(out["forces"].double().numpy() - g["forces"]).max()
+    s_err = np.abs(out["stress"].double().numpy() - g["stress"]).max()
+    a_rel = (np.abs(out["atom_energy"].double().numpy() - g["atom_energy"]) /
+             np.maximum(np.abs(g["atom_energy"]), 1e-3)).max()
+    print(f"fe54 lmax4: E rel {e_rel:.2e}, F {f_err:.2e}, S {s_err:.2e}, per-atom {a_rel:.2e}")
+    assert e_rel <= 1e-6 and f_err <= 1e-4 and s_err <= 1e-4 and a_rel <= 1e-5
+
+
 def test_config5_bcc_fe_lmax4_invariants(cuda):
     """BASELINE config 5 at full size: bcc Fe 16^3 (8,192 atoms), lmax = 4, 8 layers, C = 128,
     energy + forces.  No CPU oracle finishes at this size; checked through invariants."""
@@ -273,4 +293,4 @@ def test_config5_bcc_fe_lmax4_invariants(cuda):
     e_rel = abs(c["energy"].double().item() - a["energy"].double().item()) / abs(a["energy"].double().item())
     f_err = (c["forces"].double() - a["forces"].double() @ torch.tensor(Rm).T).abs().max().item()
     print(f"config 5 rotated: E rel {e_rel:.2e}, F max-abs {f_err:.2e}")
-    assert e_rel < 1e-5 and f_err < 1e-3
+    assert e_rel < 1e-6 and f_err < 1e-4

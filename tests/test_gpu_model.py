@@ -89,6 +89,27 @@ def test_water_fixture_parity(cuda, mode):
     _check(out, ref, s.n_atoms)
 
 
+@pytest.mark.parametrize("mode", [0, 1], ids=["split_bf16", "fp32"])
+def test_fe432_fixture_parity(cuda, mode):
+    """The headline workload's local structure (bcc Fe, a = 2.87, 30 edges per atom, E+F+S)
+    at 6x6x6 = 432 atoms against the committed float64 oracle fixture
+    (tests/golden/fe432_oracle.npz), in both matrix-core modes.  Bars: energy per atom rel
+    1e-6, forces and stress max-abs 1e-4, each atom's energy contribution rel 1e-5 (a float32
+    run of the oracle itself is 1.2e-7 / 5.9e-8 / 2.4e-9 / 2.3e-6 from float64 here)."""
+    import os
+    import systems
+    from ops import _lib
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "fe432_oracle.npz"))
+    bb, hd, model = _build(cuda)
+    s = systems.AtomicSystem("fe432", g["pos"], g["Z"].astype(np.int64), g["cell"])
+    with _lib.matmul_mode(mode):
+        out = _run(model, s, g["edge_index"].astype(np.int64), g["cell_offsets"].astype(np.float32), cuda)
+    ref = {k: torch.from_numpy(g[k]) for k in ("energy", "forces", "stress", "atom_energy")}
+    e_rel = abs(out["energy"].double().item() - ref["energy"].item()) / abs(ref["energy"].item())
+    print(f"fe432 mode {mode}: E rel {e_rel:.2e}, F {(out['forces'].double() - ref['forces']).abs().max().item():.2e}")
+    _check(out, ref, s.n_atoms, atom_rel=1e-5)
+
+
 def test_uncapped_sweep_fixture_parity(cuda):
     """The reference's own benchmark graphs (examples/sweep.py:33-81): every pair within the
     cutoff is an edge with no per-receiver cap (here up to 171 edges per atom, so the
@@ -288,3 +309,32 @@ def test_charge_spin_balanced_channels(cuda):
         assert e_rel <= max(1e-6, 2.0 * floor)
         assert (forces[k].double() - ref["forces"]).abs().max().item() <= 1e-4
         assert (out["stress"][k].detach().cpu().double() - ref["stress"][0]).abs().max().item() <= 1e-4
+
+
+def test_unbalanced_complex_weight_keeps_four_products(cuda):
+    """A block whose m = 1 conv1 weight has an imaginary part 1e-3 the size of its real part:
+    the model keeps the four-product complex kernel for it (no pre-split copy, so no Gauss
+    cancellation), the other weights keep the three-product form, and the result matches
+    the float64 oracle at the headline bars."""
+    import systems
+    from oracle.model_ref import energy_forces_stress
+    import escn_md
+    import heads
+    from wrapper import ZeroAllocBackbone
+    bb = escn_md.eSCNMDBackbone(seed=0)
+    w = bb.blocks[1].edge_wise.so2_conv_1.so2_m_conv[0].fc.weight
+    C2 = w.shape[0] // 2
+    with torch.no_grad():
+        w[C2:] *= 1e-3
+    hd = heads.MLPEnergyHead(bb.sphere_channels, bb.hidden_channels, seed=1)
+    import copy
+    bb_cpu, hd_cpu = copy.deepcopy(bb), copy.deepcopy(hd)
+    model = heads.PotentialModel(ZeroAllocBackbone(bb.to(cuda)), hd.to(cuda))
+    s = systems.cu_slab_co()
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, bb_cpu.cutoff, bb_cpu.max_neighbors)
+    out = _run(model, s, ei, off, cuda)
+    layers = model.backbone.ce.layers
+    assert layers[1]._splits[0] is None and layers[1]._splits[1] is None
+    assert all(t is not None for t in layers[1]._splits[2:]) and all(t is not None for t in layers[0]._splits)
+    ref = energy_forces_stress(bb_cpu, hd_cpu, s.pos, s.Z, s.cell, ei, off, dtype=torch.float64)
+    _check(out, ref, s.n_atoms)

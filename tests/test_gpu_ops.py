@@ -624,3 +624,38 @@ def test_balance_channels(cuda, start, end, offset):
     assert_close(gg, gref, TOL, "balance bwd")
     sums = torch.zeros(3, end - start, dtype=torch.float64).index_add(0, batch, out.detach().cpu().double()[:, 0, start:end])
     assert (sums - (target.double() - offset)[:, None]).abs().max().item() < 1e-4
+
+
+@pytest.mark.parametrize("presplit", [False, True], ids=["in_kernel", "presplit"])
+def test_complex_linear_cancellation_bound(cuda, presplit):
+    """Adversarial cancellation for the three-product (Gauss) complex layer: x_i = 0 and
+    |Q| = 1e-3 |P|, so y_i = x_r Q^T is 1e-3 of the products T3 = (x_r + x_i)(P + Q)^T and
+    T1 = x_r P^T it is formed from (y_i = T3 - T1 - T2).  Against the float64 four-product
+    packed GEMM (the reference's x @ [[P, -Q], [Q, P]]^T): every output stays within 2^-20 of
+    the Gauss magnitude sum |x_r||P|^T + |x_i||Q|^T + |x_r + x_i||P + Q|^T (fp32 class,
+    normwise), y_r keeps the plain fp32 GEMM accuracy; the loss is confined to y_i, whose
+    error relative to |y_i| is reported.  (Without a pre-split weight the kernel runs four
+    products, so there y_i keeps fp32 accuracy too.)"""
+    from ops.linear import complex_gemm, complex_weight_split
+    g = torch.Generator().manual_seed(11)
+    M, Kc, Nc = 4096, 256, 128
+    xr = torch.randn(M, Kc, generator=g)
+    x = torch.cat([xr, torch.zeros(M, Kc)], 1)
+    P = torch.randn(Nc, Kc, generator=g) / Kc ** 0.5
+    Q = 1e-3 * torch.randn(Nc, Kc, generator=g) / Kc ** 0.5
+    ref = x.double() @ R.pack_so2(P.double(), Q.double()).T
+    W3 = complex_weight_split(P.to(cuda), Q.to(cuda)) if presplit else None
+    y = complex_gemm(x.to(cuda), P.to(cuda), Q.to(cuda), W3).double().cpu()
+    ax, aP, aQ = xr.abs().double(), P.abs().double(), Q.abs().double()
+    gauss_mag = ax @ aP.T + ax @ (P + Q).abs().double().T        # x_i = 0
+    err = (y - ref).abs()
+    err_r, err_i = err[:, :Nc], err[:, Nc:]
+    ratio = (err / torch.cat([gauss_mag, gauss_mag], 1)).max().item()
+    rel_r = err_r.max().item() / ref[:, :Nc].abs().max().item()
+    rel_i = err_i.max().item() / ref[:, Nc:].abs().max().item()
+    print(f"presplit={presplit}: max err / Gauss magnitude {ratio:.2e} (bound 2^-20 = {2**-20:.2e}); "
+          f"y_r rel {rel_r:.2e}, y_i rel {rel_i:.2e}")
+    assert ratio <= 2.0 ** -20
+    assert rel_r < 5e-6
+    if not presplit:
+        assert rel_i < 5e-6
