@@ -53,7 +53,9 @@ __device__ __forceinline__ int clds(int row, int chunk) {
   return row * 16 + 4 * (chunk ^ (((row >> 1) ^ (row >> 2)) & 3));
 }
 
-// Gate epilogues, s = S[row][s_off + column]:
+// Gate epilogues, s = sigmoid(gate) for gate-column index t = s_off + column (degree
+// l = 1 + t / C, channel t % C), read from the gate-paired conv1 m = 0 output G = Y0:
+// G[row][64 ((l - 1) C / 32 + c / 32) + c % 32] (fu_linear_gate's column order).
 //   MODE 1 (conv1 m = 1, 2 fused with the gate activation): also writes Z_r = Y_r s, Z_i = Y_i s;
 //   MODE 2 (conv2 m = 1, 2 input gradient fused with the gate backward): the product is
 //   g_Z; Y receives g_Y = g_Z s and Pout the gate sum g_Zr F_r + g_Zi F_i, F being the
@@ -62,9 +64,10 @@ struct CGate {
   float* Zr;
   float* Zi;
   int64_t ldz;
-  const float* S;
-  int64_t lds;
+  const float* G;
+  int64_t ldg;
   int32_t s_off;
+  int32_t C;
   const float* Fr;
   const float* Fi;
   int64_t ldf;
@@ -375,8 +378,13 @@ __global__ __launch_bounds__(256, PATH == CPATH_FP32 ? 3 : 2) void complex_linea
       const int gc = col0 + wc + c;
       if (row >= M || gc >= Nc) continue;
       const float4 yr = ld4(&ws[r * CES + c]), yi = ld4(&ws[r * CES + 32 + c]);
+      float4 sg;
+      if constexpr (MODE != 0) {
+        const int t = g.s_off + gc, l1 = t / g.C, ch = t - l1 * g.C;
+        const float4 gp = ld4(g.G + row * g.ldg + 64 * (l1 * (g.C >> 5) + (ch >> 5)) + (ch & 31));
+        sg = make_float4(sigmoidf_(gp.x), sigmoidf_(gp.y), sigmoidf_(gp.z), sigmoidf_(gp.w));
+      }
       if constexpr (MODE == 2) {
-        const float4 sg = ld4(g.S + row * g.lds + g.s_off + gc);
         st4(Yr + row * ldy + gc, yr * sg);
         st4(Yi + row * ldy + gc, yi * sg);
         st4(g.Pout + row * g.ldp + gc, yr * ld4(g.Fr + row * g.ldf + gc) + yi * ld4(g.Fi + row * g.ldf + gc));
@@ -385,7 +393,6 @@ __global__ __launch_bounds__(256, PATH == CPATH_FP32 ? 3 : 2) void complex_linea
       st4(Yr + row * ldy + gc, yr);
       st4(Yi + row * ldy + gc, yi);
       if constexpr (MODE == 1) {
-        const float4 sg = ld4(g.S + row * g.lds + g.s_off + gc);
         st4(g.Zr + row * g.ldz + gc, yr * sg);
         st4(g.Zi + row * g.ldz + gc, yi * sg);
       }
@@ -412,6 +419,19 @@ static int complex_check(const float* A_r, const float* A_i, int64_t lda, const 
     return set_error(FU_ERR_ALIGN, "%s: operands must be 16-byte aligned", who);
   const int64_t total = ((M + CBM - 1) / CBM) * ((Nc + CBN - 1) / CBN);
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
+  return FU_OK;
+}
+
+// The gate source of the gate epilogues: the gate-paired conv1 m = 0 output Y0, whose gate
+// columns for degrees 1 + (s_off + column) / C must exist: s_off + Nc <= L C with
+// (2L + 1) C <= ldy0 columns, i.e. (2 (s_off + Nc) / C + 1) C <= ldy0.
+static int gate_source_check(const char* who, const float* Y0, int64_t ldy0, int32_t s_off, int32_t C, int32_t Nc) {
+  if (C <= 0 || C % 32 != 0) return set_error(FU_ERR_UNSUPPORTED, "%s: C=%d must be a multiple of 32", who, C);
+  if (s_off < 0 || s_off % 4 != 0 || ldy0 % 4 != 0)
+    return set_error(FU_ERR_ALIGN, "%s: s_off and ldy0 must be non-negative multiples of 4", who);
+  const int64_t degrees = ((int64_t)s_off + Nc + C - 1) / C;
+  if ((2 * degrees + 1) * C > ldy0) return set_error(FU_ERR_SHAPE, "%s: Y0 rows too short for the gate columns", who);
+  (void)Y0;
   return FU_OK;
 }
 
@@ -490,36 +510,38 @@ extern "C" int fu_complex_linear(const float* A_r, const float* A_i, int64_t lda
 
 extern "C" int fu_complex_linear_gate(const float* A_r, const float* A_i, int64_t lda, const float* P, const float* Q,
                                       int64_t ldw, const void* W3, float* Y_r, float* Y_i, int64_t ldy, float* Z_r,
-                                      float* Z_i,
-                                      int64_t ldz, const float* S, int64_t lds, int32_t s_off, int64_t M, int32_t Nc,
-                                      int32_t Kc, void* stream) {
+                                      float* Z_i, int64_t ldz, const float* Y0, int64_t ldy0, int32_t s_off, int32_t C,
+                                      int64_t M, int32_t Nc, int32_t Kc, void* stream) {
   const char* who = "fu_complex_linear_gate";
   int st = complex_check(A_r, A_i, lda, P, Q, ldw, Y_r, Y_i, ldy, M, Nc, Kc, who);
   if (st != FU_OK) return st;
-  if (ldz < Nc || s_off < 0 || lds < s_off + Nc) return set_error(FU_ERR_SHAPE, "%s: gate strides too small", who);
+  st = gate_source_check(who, Y0, ldy0, s_off, C, Nc);
+  if (st != FU_OK) return st;
+  if (ldz < Nc) return set_error(FU_ERR_SHAPE, "%s: gate strides too small", who);
   if (M == 0) return FU_OK;
-  if (!Z_r || !Z_i || !S) return set_error(FU_ERR_NULL, "%s: NULL gate operand", who);
-  if ((ldz | lds | s_off) % 4 != 0 || !aligned16(Z_r) || !aligned16(Z_i) || !aligned16(S))
+  if (!Z_r || !Z_i || !Y0) return set_error(FU_ERR_NULL, "%s: NULL gate operand", who);
+  if (ldz % 4 != 0 || !aligned16(Z_r) || !aligned16(Z_i) || !aligned16(Y0))
     return set_error(FU_ERR_ALIGN, "%s: gate operands must be 16-byte aligned with strides multiples of 4", who);
   return complex_launch<1>(A_r, A_i, lda, P, Q, ldw, W3, Y_r, Y_i, ldy, M, Nc, Kc,
-                           CGate{Z_r, Z_i, ldz, S, lds, s_off, nullptr, nullptr, 0, nullptr, 0}, stream, who);
+                           CGate{Z_r, Z_i, ldz, Y0, ldy0, s_off, C, nullptr, nullptr, 0, nullptr, 0}, stream, who);
 }
 
 extern "C" int fu_complex_linear_gate_bwd(const float* A_r, const float* A_i, int64_t lda, const float* P,
                                           const float* Q, int64_t ldw, const void* W3, float* gY_r, float* gY_i,
                                           int64_t ldg,
-                                          const float* F_r, const float* F_i, int64_t ldf, const float* S, int64_t lds,
-                                          int32_t s_off, float* Pout, int64_t ldp, int64_t M, int32_t Nc, int32_t Kc,
-                                          void* stream) {
+                                          const float* F_r, const float* F_i, int64_t ldf, const float* Y0,
+                                          int64_t ldy0, int32_t s_off, int32_t C, float* Pout, int64_t ldp, int64_t M,
+                                          int32_t Nc, int32_t Kc, void* stream) {
   const char* who = "fu_complex_linear_gate_bwd";
   int st = complex_check(A_r, A_i, lda, P, Q, ldw, gY_r, gY_i, ldg, M, Nc, Kc, who);
   if (st != FU_OK) return st;
-  if (ldf < Nc || ldp < Nc || s_off < 0 || lds < s_off + Nc)
-    return set_error(FU_ERR_SHAPE, "%s: gate strides too small", who);
+  st = gate_source_check(who, Y0, ldy0, s_off, C, Nc);
+  if (st != FU_OK) return st;
+  if (ldf < Nc || ldp < Nc) return set_error(FU_ERR_SHAPE, "%s: gate strides too small", who);
   if (M == 0) return FU_OK;
-  if (!F_r || !F_i || !S || !Pout) return set_error(FU_ERR_NULL, "%s: NULL gate operand", who);
-  if ((ldf | ldp | lds | s_off) % 4 != 0 || !aligned16(F_r) || !aligned16(F_i) || !aligned16(S) || !aligned16(Pout))
+  if (!F_r || !F_i || !Y0 || !Pout) return set_error(FU_ERR_NULL, "%s: NULL gate operand", who);
+  if ((ldf | ldp) % 4 != 0 || !aligned16(F_r) || !aligned16(F_i) || !aligned16(Y0) || !aligned16(Pout))
     return set_error(FU_ERR_ALIGN, "%s: gate operands must be 16-byte aligned with strides multiples of 4", who);
   return complex_launch<2>(A_r, A_i, lda, P, Q, ldw, W3, gY_r, gY_i, ldg, M, Nc, Kc,
-                           CGate{nullptr, nullptr, 0, S, lds, s_off, F_r, F_i, ldf, Pout, ldp}, stream, who);
+                           CGate{nullptr, nullptr, 0, Y0, ldy0, s_off, C, F_r, F_i, ldf, Pout, ldp}, stream, who);
 }

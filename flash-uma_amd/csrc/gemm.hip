@@ -42,7 +42,7 @@ __device__ __forceinline__ int lds_chunk(int row, int chunk) {
 struct GateOut {
   float* Z;     // (M, (L+1)C): [silu(y_l0), y_l1m0 s1, ..., y_lLm0 sL]
   int64_t ldz;
-  float* S;     // (M, LC): [s1, ..., sL] = sigmoid of the L gate blocks
+  float* S;     // optional (M, LC): [s1, ..., sL] = sigmoid of the L gate blocks
   int64_t lds;
   int32_t C;
   int32_t L;    // lmax
@@ -52,13 +52,12 @@ struct GateOut {
 // backward).  The GEMM computes g_Z_m0 (M, (L+1)C) = [g_l0, g_l1m0, ..., g_lLm0]; the epilogue
 // writes g_Y_m0 (M, (2L+1)C) in the gate-paired order instead: g_y_l0 = g silu'(y_l0),
 // g_y_lm0 = g s_l and g_gate_l = s_l (1 - s_l) (g y_lm0 + P1[l] (+ P2[l] for l >= 2)), where
-// P1 (M, LC) and P2 (M, (L-1)C) are the gate sums sum_m g_z y of the m = 1 and m = 2 blocks
-// (written by fu_complex_linear_gate_bwd).
+// s_l = sigmoid(gate_l) is recomputed from the gate columns of Y0, and P1 (M, LC) and
+// P2 (M, (L-1)C) are the gate sums sum_m g_z y of the m = 1 and m = 2 blocks (written by
+// fu_complex_linear_gate_bwd).
 struct GateBwd {
   const float* Y0;  // (M, (2L+1)C) forward pre-activation, gate-paired
   int64_t ldy0;
-  const float* S;   // (M, LC) [s1, ..., sL]
-  int64_t lds;
   const float* P1;
   int64_t ldp1;
   const float* P2;
@@ -295,7 +294,8 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
           st4(out + 2 * L * C + ch, o);
         } else {
           const int gate_col = 64 * ((kb - 1) * n1 + (ch >> 5)) + (ch & 31);
-          const float4 sg = ld4(gb.S + gr * gb.lds + (kb - 1) * C + ch);
+          const float4 gp = ld4(y0 + gate_col);
+          const float4 sg = make_float4(sigmoidf_(gp.x), sigmoidf_(gp.y), sigmoidf_(gp.z), sigmoidf_(gp.w));
           const float4 y = ld4(y0 + gate_col + 32);
           float4 p = ld4(gb.P1 + gr * gb.ldp1 + (kb - 1) * C + ch);
           if (kb >= 2) p = p + ld4(gb.P2 + gr * gb.ldp2 + (kb - 2) * C + ch);
@@ -348,7 +348,7 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
           const int kind = p / n1;
           const int ch = 32 * (p - kind * n1) + c;
           const float4 sg = make_float4(sigmoidf_(g.x), sigmoidf_(g.y), sigmoidf_(g.z), sigmoidf_(g.w));
-          st4(go.S + row * go.lds + kind * C + ch, sg);
+          if (go.S) st4(go.S + row * go.lds + kind * C + ch, sg);
           st4(go.Z + row * go.ldz + (1 + kind) * C + ch, v * sg);
         } else {
           const int ch = q0 - 2 * L * C + c;
@@ -467,10 +467,11 @@ extern "C" int fu_linear_gate(const float* A, int64_t lda, const float* W, int64
   const int32_t N = (2 * lmax + 1) * C;
   int st = linear_check(A, lda, W, ldw, Y, ldy, M, N, K, who);
   if (st != FU_OK) return st;
-  if (ldz < (lmax + 1) * C || lds < lmax * C) return set_error(FU_ERR_SHAPE, "%s: Z / S row strides too small", who);
+  if (ldz < (lmax + 1) * C || (S && lds < lmax * C))
+    return set_error(FU_ERR_SHAPE, "%s: Z / S row strides too small", who);
   if (M == 0) return FU_OK;
-  if (!Z || !S) return set_error(FU_ERR_NULL, "%s: NULL output", who);
-  if (ldz % 4 != 0 || lds % 4 != 0 || !aligned16(Z) || !aligned16(S) || (bias && !aligned16(bias)))
+  if (!Z) return set_error(FU_ERR_NULL, "%s: NULL output", who);
+  if (ldz % 4 != 0 || !aligned16(Z) || (S && (lds % 4 != 0 || !aligned16(S))) || (bias && !aligned16(bias)))
     return set_error(FU_ERR_ALIGN, "%s: Z, S and bias must be 16-byte aligned with row strides multiples of 4", who);
   const int n_tiles = (N + GBN - 1) / GBN;
   const int64_t total = ((M + GBM - 1) / GBM) * n_tiles;
@@ -483,9 +484,9 @@ extern "C" int fu_linear_gate(const float* A, int64_t lda, const float* W, int64
 }
 
 extern "C" int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* Wt, int64_t ldw, const float* Y0,
-                                  int64_t ldy0, const float* S, int64_t lds, const float* P1, int64_t ldp1,
-                                  const float* P2, int64_t ldp2, float* gY0, int64_t ldg, int64_t M, int32_t C,
-                                  int32_t K, int32_t lmax, void* stream) {
+                                  int64_t ldy0, const float* P1, int64_t ldp1, const float* P2, int64_t ldp2,
+                                  float* gY0, int64_t ldg, int64_t M, int32_t C, int32_t K, int32_t lmax,
+                                  void* stream) {
   const char* who = "fu_linear_gate_bwd";
   if (C <= 0 || C % 64 != 0) return set_error(FU_ERR_UNSUPPORTED, "%s: C=%d must be a multiple of 64", who, C);
   if (lmax < 2 || lmax > 4) return set_error(FU_ERR_UNSUPPORTED, "%s: lmax=%d unsupported (2, 3 or 4)", who, lmax);
@@ -493,12 +494,11 @@ extern "C" int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* W
   // the GEMM's own output (g_Z_m0, N = (L+1)C columns) is never stored; gY0 ((2L+1)C) is checked here
   int st = linear_check(gZo, ldgz, Wt, ldw, gY0, ldg, M, N, K, who);
   if (st != FU_OK) return st;
-  if (ldg < (2 * lmax + 1) * C || ldy0 < (2 * lmax + 1) * C || lds < lmax * C || ldp1 < lmax * C ||
-      ldp2 < (lmax - 1) * C)
+  if (ldg < (2 * lmax + 1) * C || ldy0 < (2 * lmax + 1) * C || ldp1 < lmax * C || ldp2 < (lmax - 1) * C)
     return set_error(FU_ERR_SHAPE, "%s: row strides too small", who);
   if (M == 0) return FU_OK;
-  if (!Y0 || !S || !P1 || !P2) return set_error(FU_ERR_NULL, "%s: NULL operand", who);
-  if ((ldy0 | lds | ldp1 | ldp2) % 4 != 0 || !aligned16(Y0) || !aligned16(S) || !aligned16(P1) || !aligned16(P2))
+  if (!Y0 || !P1 || !P2) return set_error(FU_ERR_NULL, "%s: NULL operand", who);
+  if ((ldy0 | ldp1 | ldp2) % 4 != 0 || !aligned16(Y0) || !aligned16(P1) || !aligned16(P2))
     return set_error(FU_ERR_ALIGN, "%s: operands must be 16-byte aligned with row strides multiples of 4", who);
   const int n_tiles = (N + GBN - 1) / GBN;
   const int64_t total = ((M + GBM - 1) / GBM) * n_tiles;
@@ -506,6 +506,6 @@ extern "C" int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* W
   auto kern = linear_kernel<2>(K);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), gZo, ldgz,
                      (int64_t)0, Wt, ldw, (int64_t)0, (const float*)nullptr, (int64_t)0, 1, gY0, ldg, (int64_t)0, M, N,
-                     K, n_tiles, total, GateOut{}, GateBwd{Y0, ldy0, S, lds, P1, ldp1, P2, ldp2, C, lmax}, Resid{});
+                     K, n_tiles, total, GateOut{}, GateBwd{Y0, ldy0, P1, ldp1, P2, ldp2, C, lmax}, Resid{});
   return check_launch(who);
 }

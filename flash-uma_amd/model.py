@@ -29,11 +29,11 @@ from collections import OrderedDict
 import torch
 import torch.nn as nn
 
-from ops.gather import LAYOUT1_PERM, block_permutation, gather_wigner_split
-from ops.gating import conv1_gate_conv2, gate_paired_rows
+from ops.gather import LAYOUT1_PERM, block_permutation
+from ops.gating import edge_block, gate_paired_rows
 from ops.geom import precompute_geometry
 from ops.linear import complex_linear, complex_weight_split, linear
-from ops.lmax import gather_rotate_lmax, init_node_scatter_lmax, rotate_scatter_lmax, wigner_extend
+from ops.lmax import init_node_scatter_lmax, rotate_scatter_lmax, wigner_extend
 from ops.ln_silu import layer_norm_silu
 from ops.node import balance_channels_batched, permute_rows, system_ptr
 from ops.radial import RadialBank
@@ -259,26 +259,30 @@ class Packed_eSCN_Layer(nn.Module):
                 self.gamma_rad1_2, self.beta_rad1_2, self.W_rad1_3, self.b_rad1_3)
 
     def forward(self, x_in, x_edge_raw, wigner, env, idx_i, idx_j, row_ptr, col_idx, csd_emb, batch,
-                topology=None, rad_out=None, wig_ext=None):
+                topology=None, rad_out=None, wig_ext=None, rad_src=None):
         """rad_out, when given, is this block's radial-MLP output (computed by the model's
         RadialBank); otherwise it is computed here from x_edge_raw (E, B+2C).  wig_ext: the
         degree-3/4 Wigner rows (ops/lmax.wigner_extend), needed for lmax > 2."""
         x_norm, x_skip = self._norm_skip(x_in)
         if rad_out is None:
             rad_out = self.radial(x_edge_raw)
-        if self.lmax != 2:
-            return self._forward_reference_order(x_skip, x_norm, rad_out, wigner, wig_ext, env, idx_i, idx_j,
-                                                 row_ptr, col_idx, csd_emb, batch, topology)
-        X_m0, X_m1, X_m2 = gather_wigner_split(x_norm, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology,
-                                               self.layout)
+        # gather -> conv1 + gate -> conv2 as one node: the (E, 18C) gather output X never
+        # outlives the block (model.py:150-154)
         sfx = ("_R", "_I", "_Rt", "_It_neg")
         c1 = [self.W_conv1_m0, self.b_conv1_m0, self.W_conv1_m0_t] + \
             [getattr(self, "W_conv1_m" + m + x) for m in "12" for x in sfx]
         c2 = [self.W_conv2_m0, self.b_conv2_m0, self.W_conv2_m0_t] + \
             [getattr(self, "W_conv2_m" + m + x) for m in "12" for x in sfx]
-        Zo_m0, Zo_m1, Zo_m2 = conv1_gate_conv2(X_m0, X_m1, X_m2, c1, c2, self.C, self._complex_splits(X_m0.device))
-        x_mid = rotate_scatter_split(Zo_m0, Zo_m1, Zo_m2, wigner, env, x_skip, idx_j, row_ptr, col_idx,
-                                     x_skip.shape[0])
+        Zo_m0, Zo_m1, Zo_m2 = edge_block(x_norm, wigner, wig_ext, rad_out, idx_i, idx_j, csd_emb, batch, topology,
+                                         self.layout, self.lmax, c1, c2, self.C, self._complex_splits(x_norm.device),
+                                         rad_src)
+        del rad_out
+        if self.lmax == 2:
+            x_mid = rotate_scatter_split(Zo_m0, Zo_m1, Zo_m2, wigner, env, x_skip, idx_j, row_ptr, col_idx,
+                                         x_skip.shape[0])
+        else:
+            x_mid = rotate_scatter_lmax(Zo_m0, Zo_m1, Zo_m2, wigner, wig_ext, env, x_skip, idx_j, row_ptr, col_idx,
+                                        x_skip.shape[0], self.lmax)
         return self._ffn_residual(x_mid)
 
     def _norm_skip(self, x_in):
@@ -296,24 +300,14 @@ class Packed_eSCN_Layer(nn.Module):
             return self.atom_wise.forward_residual(x_n2, skip)
         return self.atom_wise(self.norm_2(x_mid)) + x_mid
 
-    def _forward_reference_order(self, x_in, x_norm, rad_out, wigner, wig_ext, env, idx_i, idx_j, row_ptr, col_idx,
-                                 csd_emb, batch, topology):
-        L, C = self.lmax, self.C
-        X_m0, X_m1, X_m2 = gather_rotate_lmax(x_norm, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, topology,
-                                              L)
-        sfx = ("_R", "_I", "_Rt", "_It_neg")
-        c1 = [self.W_conv1_m0, self.b_conv1_m0, self.W_conv1_m0_t] + \
-            [getattr(self, "W_conv1_m" + m + x) for m in "12" for x in sfx]
-        c2 = [self.W_conv2_m0, self.b_conv2_m0, self.W_conv2_m0_t] + \
-            [getattr(self, "W_conv2_m" + m + x) for m in "12" for x in sfx]
-        Zo_m0, Zo_m1, Zo_m2 = conv1_gate_conv2(X_m0, X_m1, X_m2, c1, c2, C, self._complex_splits(X_m0.device))
-        x_mid = rotate_scatter_lmax(Zo_m0, Zo_m1, Zo_m2, wigner, wig_ext, env, x_in, idx_j, row_ptr, col_idx,
-                                    x_in.shape[0], L)
-        return self._ffn_residual(x_mid)
-
 
 class eSCN_Inference_Model(nn.Module):
     """eSCN-MD backbone forward (model.py:160-221)."""
+
+    # From this many edges on, each block recomputes its radial-MLP output in the backward
+    # instead of keeping it (about 100 KB per edge are held otherwise, e.g. 138 GiB at 1.5 M
+    # edges; the recompute lowers that by ~22 KB per edge for ~5 % more step time).
+    RAD_RECOMPUTE_MIN_EDGES = 1_000_000
 
     def __init__(self, num_layers=4, sphere_channels=128, edge_channels=128, num_distance_basis=32, cutoff=5.0,
                  coeff_g=-0.5, lmax=2):
@@ -397,8 +391,16 @@ class eSCN_Inference_Model(nn.Module):
         #    columns of x_edge_raw are folded into the radial bank's per-element tables.
         gauss, wigner, env = precompute_geometry(pos_s, Z_s, idx_i_s, idx_j_s, shifts_s, self.W_src, self.W_tgt,
                                                  self.offset_g, self.coeff_g, self.cutoff, topo, False)
-        # 3. Every radial MLP (edge-degree embedding + one per block) as one bank
-        rads = self.radial_bank(gauss, Z_s, idx_i_s, idx_j_s)
+        # 3. Every radial MLP (edge-degree embedding + one per block) as one bank.  On large
+        #    graphs the blocks keep each radial output's (E, C) source instead of the (E, 12C)
+        #    output and recompute it in their backward (one GEMM per block, ~5 % of the step,
+        #    for ~22 KB less per edge held through the step).
+        recompute = idx_i_s.shape[0] >= self.RAD_RECOMPUTE_MIN_EDGES
+        if recompute:
+            rads, srcs = self.radial_bank(gauss, Z_s, idx_i_s, idx_j_s, with_sources=True)
+        else:
+            rads, srcs = self.radial_bank(gauss, Z_s, idx_i_s, idx_j_s), None
+        rads = list(rads)
         # 4. Edge-degree embedding (lmax > 2: with the degree-3/4 Wigner rows)
         wig_ext = None
         if self.lmax == 2:
@@ -412,9 +414,13 @@ class eSCN_Inference_Model(nn.Module):
         #    the backbone reserves channels for them (model.py:213-216)
         balance = self.charge_end > self.charge_start or self.spin_end > self.spin_start
         sys_ptr = system_ptr(batch_s, csd_emb.shape[0]) if balance else None   # batch_s is sorted
-        for k, (layer, rad) in enumerate(zip(self.layers, rads[1:])):
+        rads[0] = None
+        for k, layer in enumerate(self.layers):
+            rad, rads[k + 1] = rads[k + 1], None
             x_node_s = layer(x_node_s, None, wigner, env, idx_i_s, idx_j_s, row_ptr, col_idx, csd_emb,
-                             batch_s, topo, rad_out=rad, wig_ext=wig_ext)
+                             batch_s, topo, rad_out=rad, wig_ext=wig_ext,
+                             rad_src=srcs[k + 1] if srcs else None)
+            del rad
             if self.charge_end > self.charge_start:
                 x_node_s = balance_channels_batched(x_node_s, charge, natoms, batch_s, self.charge_start,
                                                     self.charge_end, 0.0, sys_ptr)

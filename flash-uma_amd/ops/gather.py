@@ -32,55 +32,68 @@ def block_permutation(perm, C: int) -> torch.Tensor:
     return torch.cat([torch.arange(p * C, (p + 1) * C) for p in perm])
 
 
+def gather_fwd(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch, layout):
+    """fu_gather_fwd: (X_m0, X_m1, X_m2) for contiguous, correctly typed operands."""
+    N, _, C = x_in.shape
+    E = idx_i.shape[0]
+    if rad_out.shape != (E, RAD_MULT * C):
+        raise _lib.FlashUMAError(f"rad_out must be ({E}, {RAD_MULT * C}), got {tuple(rad_out.shape)}")
+    dev = x_in.device
+    X_m0 = torch.empty((E, X_M0_MULT * C), device=dev, dtype=torch.float32)
+    X_m1 = torch.empty((E, X_M1_MULT * C), device=dev, dtype=torch.float32)
+    X_m2 = torch.empty((E, X_M2_MULT * C), device=dev, dtype=torch.float32)
+    _lib.call("fu_gather_fwd", x_in.data_ptr(), idx_i.data_ptr(), idx_j.data_ptr(), wigner.data_ptr(),
+              rad_out.data_ptr(), csd_emb.data_ptr(), batch.data_ptr(), X_m0.data_ptr(), X_m1.data_ptr(),
+              X_m2.data_ptr(), E, N, csd_emb.shape[0], C, int(layout), _lib.stream_ptr(dev))
+    return X_m0, X_m1, X_m2
+
+
+def gather_bwd(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology, layout, g_x_m0, g_x_m1, g_x_m2):
+    """fu_gather_bwd (node-centric over both CSRs): (g_x, g_wigner, g_rad)."""
+    N, _, C = x_in.shape
+    E = idx_i.shape[0]
+    dev = x_in.device
+    g_x_m0 = torch.zeros(E, X_M0_MULT * C, device=dev) if g_x_m0 is None else g_x_m0.contiguous()
+    g_x_m1 = torch.zeros(E, X_M1_MULT * C, device=dev) if g_x_m1 is None else g_x_m1.contiguous()
+    g_x_m2 = torch.zeros(E, X_M2_MULT * C, device=dev) if g_x_m2 is None else g_x_m2.contiguous()
+    topo = topology
+    if topo is not None and topo.E == E and topo.N == N:
+        rptr, ridx, sptr, sidx = topo.recv_ptr, topo.recv_idx, topo.send_ptr, topo.send_idx
+    else:
+        rptr, ridx = receiver_csr(idx_j, N)
+        sptr, sidx = sender_csr(idx_i, N)
+    g_x = torch.empty_like(x_in)
+    g_wigner = torch.empty_like(wigner)
+    g_rad = torch.empty_like(rad_out)
+    ws = torch.empty_like(wigner)
+    _lib.call("fu_gather_bwd", g_x_m0.data_ptr(), g_x_m1.data_ptr(), g_x_m2.data_ptr(), x_in.data_ptr(),
+              idx_i.data_ptr(), idx_j.data_ptr(), wigner.data_ptr(), rad_out.data_ptr(), csd_emb.data_ptr(),
+              batch.data_ptr(), rptr.data_ptr(), ridx.data_ptr(), sptr.data_ptr(), sidx.data_ptr(),
+              g_x.data_ptr(), g_wigner.data_ptr(), g_rad.data_ptr(), ws.data_ptr(), E, N, csd_emb.shape[0], C,
+              int(layout), _lib.stream_ptr(dev))
+    return g_x, g_wigner, g_rad
+
+
+def gather_operands(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch):
+    """The gather's operands as contiguous tensors of the kernel's types."""
+    return (_lib.require(x_in, torch.float32, "x_in"), _lib.require(idx_i, torch.int64, "idx_i"),
+            _lib.require(idx_j, torch.int64, "idx_j"), _lib.require(wigner, torch.float32, "wigner"),
+            _lib.require(rad_out, torch.float32, "rad_out"), _lib.require(csd_emb, torch.float32, "csd_emb"),
+            _lib.require(batch, torch.int64, "batch"))
+
+
 class GatherWignerSplit(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology=None, layout=0):
-        x_in = _lib.require(x_in, torch.float32, "x_in")
-        idx_i = _lib.require(idx_i, torch.int64, "idx_i")
-        idx_j = _lib.require(idx_j, torch.int64, "idx_j")
-        wigner = _lib.require(wigner, torch.float32, "wigner")
-        rad_out = _lib.require(rad_out, torch.float32, "rad_out")
-        csd_emb = _lib.require(csd_emb, torch.float32, "csd_emb")
-        batch = _lib.require(batch, torch.int64, "batch")
-        N, _, C = x_in.shape
-        E = idx_i.shape[0]
-        if rad_out.shape != (E, RAD_MULT * C):
-            raise _lib.FlashUMAError(f"rad_out must be ({E}, {RAD_MULT * C}), got {tuple(rad_out.shape)}")
-        dev = x_in.device
-        X_m0 = torch.empty((E, X_M0_MULT * C), device=dev, dtype=torch.float32)
-        X_m1 = torch.empty((E, X_M1_MULT * C), device=dev, dtype=torch.float32)
-        X_m2 = torch.empty((E, X_M2_MULT * C), device=dev, dtype=torch.float32)
-        _lib.call("fu_gather_fwd", x_in.data_ptr(), idx_i.data_ptr(), idx_j.data_ptr(), wigner.data_ptr(),
-                  rad_out.data_ptr(), csd_emb.data_ptr(), batch.data_ptr(), X_m0.data_ptr(), X_m1.data_ptr(),
-                  X_m2.data_ptr(), E, N, csd_emb.shape[0], C, int(layout), _lib.stream_ptr(dev))
-        ctx.save_for_backward(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch)
+        ops = gather_operands(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch)
+        X = gather_fwd(*ops, layout)
+        ctx.save_for_backward(*ops)
         ctx.topology, ctx.layout = topology, int(layout)
-        return X_m0, X_m1, X_m2
+        return X
 
     @staticmethod
     def backward(ctx, g_x_m0, g_x_m1, g_x_m2):
-        x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch = ctx.saved_tensors
-        N, _, C = x_in.shape
-        E = idx_i.shape[0]
-        dev = x_in.device
-        g_x_m0 = torch.zeros(E, X_M0_MULT * C, device=dev) if g_x_m0 is None else g_x_m0.contiguous()
-        g_x_m1 = torch.zeros(E, X_M1_MULT * C, device=dev) if g_x_m1 is None else g_x_m1.contiguous()
-        g_x_m2 = torch.zeros(E, X_M2_MULT * C, device=dev) if g_x_m2 is None else g_x_m2.contiguous()
-        topo = ctx.topology
-        if topo is not None and topo.E == E and topo.N == N:
-            rptr, ridx, sptr, sidx = topo.recv_ptr, topo.recv_idx, topo.send_ptr, topo.send_idx
-        else:
-            rptr, ridx = receiver_csr(idx_j, N)
-            sptr, sidx = sender_csr(idx_i, N)
-        g_x = torch.empty_like(x_in)
-        g_wigner = torch.empty_like(wigner)
-        g_rad = torch.empty_like(rad_out)
-        ws = torch.empty_like(wigner)
-        _lib.call("fu_gather_bwd", g_x_m0.data_ptr(), g_x_m1.data_ptr(), g_x_m2.data_ptr(), x_in.data_ptr(),
-                  idx_i.data_ptr(), idx_j.data_ptr(), wigner.data_ptr(), rad_out.data_ptr(), csd_emb.data_ptr(),
-                  batch.data_ptr(), rptr.data_ptr(), ridx.data_ptr(), sptr.data_ptr(), sidx.data_ptr(),
-                  g_x.data_ptr(), g_wigner.data_ptr(), g_rad.data_ptr(), ws.data_ptr(), E, N, csd_emb.shape[0], C,
-                  ctx.layout, _lib.stream_ptr(dev))
+        g_x, g_wigner, g_rad = gather_bwd(*ctx.saved_tensors, ctx.topology, ctx.layout, g_x_m0, g_x_m1, g_x_m2)
         # no gradient for csd_emb or batch (ops/gather.py:513-514)
         return g_x, None, None, g_wigner, g_rad, None, None, None, None
 

@@ -78,6 +78,33 @@ def fused_gating_split(Y_m0, Y_m1, Y_m2, C, layout=0):
     return FusedGatingSplit.apply(Y_m0, Y_m1, Y_m2, C, layout)
 
 
+def _conv1_gate_m0(X0, W0, b0, C, L, st):
+    """fu_linear_gate: Y0 (gate-paired pre-activations, kept for the backward) and Z0."""
+    E = X0.shape[0]
+    Y0 = torch.empty(E, (2 * L + 1) * C, device=X0.device, dtype=torch.float32)
+    Z0 = torch.empty(E, (L + 1) * C, device=X0.device, dtype=torch.float32)
+    _lib.call("fu_linear_gate", X0.data_ptr(), X0.stride(0), W0.data_ptr(), W0.stride(0), _lib.ptr(b0),
+              Y0.data_ptr(), Y0.stride(0), Z0.data_ptr(), Z0.stride(0), None, 0, E, C, W0.shape[1], L, st)
+    return Y0, Z0
+
+
+def _conv1_gate_m12(X1, X2, P1, Q1, P2, Q2, W3_1, W3_2, Y0, C, st):
+    """fu_complex_linear_gate for m = 1 (gates of degrees 1..L, s_off 0) and m = 2 (degrees
+    2..L, s_off C), the sigmoids recomputed from the gate columns of Y0: (Y1, Z1, Y2, Z2)."""
+    E = X1.shape[0]
+    outs = []
+    for X, P, Q, W3, s_off in ((X1, P1, Q1, W3_1, 0), (X2, P2, Q2, W3_2, C)):
+        Nc, Kc = P.shape
+        Y = torch.empty(E, 2 * Nc, device=X.device, dtype=torch.float32)
+        Z = torch.empty(E, 2 * Nc, device=X.device, dtype=torch.float32)
+        _lib.call("fu_complex_linear_gate", X.data_ptr(), X[:, Kc:].data_ptr(), X.stride(0), P.data_ptr(),
+                  Q.data_ptr(), P.stride(0), _lib.ptr(W3), Y.data_ptr(), Y[:, Nc:].data_ptr(), Y.stride(0),
+                  Z.data_ptr(), Z[:, Nc:].data_ptr(), Z.stride(0), Y0.data_ptr(), Y0.stride(0), s_off, C, E, Nc,
+                  Kc, st)
+        outs += [Y, Z]
+    return tuple(outs)
+
+
 class Conv1Gate(torch.autograd.Function):
     """X_m0, X_m1, X_m2 -> Z_m0, Z_m1, Z_m2: conv1 m = 0 (W0 rows and b0 in the gate-paired
     order, W0t = W0^T) and the complex m = 1, 2 layers (P + iQ, with Pt = P^T, Qtn = -Q^T for
@@ -94,21 +121,9 @@ class Conv1Gate(torch.autograd.Function):
         st = _lib.stream_ptr(dev)
         f = lambda *s: torch.empty(*s, device=dev, dtype=torch.float32)
         L = _degrees(W0, C)
-        Y0, Z0, S = f(E, (2 * L + 1) * C), f(E, (L + 1) * C), f(E, L * C)
-        _lib.call("fu_linear_gate", X0.data_ptr(), X0.stride(0), W0.data_ptr(), W0.stride(0), _lib.ptr(b0),
-                  Y0.data_ptr(), Y0.stride(0), Z0.data_ptr(), Z0.stride(0), S.data_ptr(), S.stride(0), E, C,
-                  W0.shape[1], L, st)
+        Y0, Z0 = _conv1_gate_m0(X0, W0, b0, C, L, st)
         sp = splits or (None,) * 4
-        outs = []
-        for X, P, Q, W3, s_off in ((X1, P1, Q1, sp[0], 0), (X2, P2, Q2, sp[2], C)):
-            Nc, Kc = P.shape
-            Y, Z = f(E, 2 * Nc), f(E, 2 * Nc)
-            _lib.call("fu_complex_linear_gate", X.data_ptr(), X[:, Kc:].data_ptr(), X.stride(0), P.data_ptr(),
-                      Q.data_ptr(), P.stride(0), _lib.ptr(W3), Y.data_ptr(), Y[:, Nc:].data_ptr(), Y.stride(0),
-                      Z.data_ptr(), Z[:, Nc:].data_ptr(), Z.stride(0), S.data_ptr(), S.stride(0), s_off, E, Nc, Kc,
-                      st)
-            outs += [Y, Z]
-        Y1, Z1, Y2, Z2 = outs
+        Y1, Z1, Y2, Z2 = _conv1_gate_m12(X1, X2, P1, Q1, P2, Q2, sp[0], sp[2], Y0, C, st)
         if L != 2:
             raise _lib.FlashUMAError("conv1_gate: lmax 2 only (use conv1_gate_conv2 for lmax 3, 4)")
         ctx.save_for_backward(Y0, Y1, Y2, W0t, P1t, Q1tn, P2t, Q2tn)
@@ -129,75 +144,95 @@ def conv1_gate(X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C,
     return Conv1Gate.apply(X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C, splits)
 
 
+def conv_pair_fwd(X: list, conv1, conv2, C: int, splits):
+    """conv1 + gate + conv2 of one block on X = [X_m0, X_m1, X_m2].  Each entry of X is set
+    to None once its GEMM has read it, so a caller that hands over its only references
+    frees the (E, 18C) gather output while the block runs.  Returns (Zo0, Zo1, Zo2) and the
+    pre-activations (Y0, Y1, Y2) the backward needs."""
+    W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn = conv1
+    V0, c0, V0t, R1, I1, R1t, I1tn, R2, I2, R2t, I2tn = conv2
+    st = _lib.stream_ptr(X[0].device)
+    L = _degrees(W0, C)
+    sp = splits or (None,) * 8
+    Y0, Z0 = _conv1_gate_m0(_lib.require(X[0], torch.float32, "X_m0"), W0, b0, C, L, st)
+    X[0] = None
+    X1, X2 = _lib.require(X[1], torch.float32, "X_m1"), _lib.require(X[2], torch.float32, "X_m2")
+    X[1] = X[2] = None
+    Y1, Z1, Y2, Z2 = _conv1_gate_m12(X1, X2, P1, Q1, P2, Q2, sp[0], sp[2], Y0, C, st)
+    del X1, X2
+    Zo0 = gemm(Z0, V0, c0)
+    del Z0
+    Zo1 = complex_gemm(Z1, R1, I1, sp[4])
+    del Z1
+    Zo2 = complex_gemm(Z2, R2, I2, sp[6])
+    return (Zo0, Zo1, Zo2), (Y0, Y1, Y2)
+
+
+def conv_pair_bwd(Y, conv1, conv2, C: int, splits, g: list):
+    """Input gradient of conv_pair_fwd: g = [g_Zo0, g_Zo1, g_Zo2] -> (g_X0, g_X1, g_X2).  The
+    gate backward runs in the conv2 input-gradient epilogues (the m = 1, 2 complex GEMMs write
+    g_Y = g_Z s and their gate sums, then the m = 0 GEMM finishes the gate-paired g_Y_m0 with
+    the gate gradients, s recomputed from Y0); g_Z is never stored.  The entries of g are
+    released once read."""
+    Y0, Y1, Y2 = Y
+    W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn = conv1
+    V0, c0, V0t, R1, I1, R1t, I1tn, R2, I2, R2t, I2tn = conv2
+    L = _degrees(W0, C)
+    E = Y0.shape[0]
+    dev = Y0.device
+    st = _lib.stream_ptr(dev)
+    f = lambda *s: torch.empty(*s, device=dev, dtype=torch.float32)
+    sp = splits or (None,) * 8
+    g0 = torch.zeros(E, (L + 1) * C, device=dev) if g[0] is None else g[0].contiguous()
+    g1 = torch.zeros(E, 2 * L * C, device=dev) if g[1] is None else g[1].contiguous()
+    g2 = torch.zeros(E, 2 * (L - 1) * C, device=dev) if g[2] is None else g[2].contiguous()
+    g[0] = g[1] = g[2] = None
+    gys, psums = [], []
+    for gz, Rt, Itn, W3, F, s_off in ((g1, R1t, I1tn, sp[5], Y1, 0), (g2, R2t, I2tn, sp[7], Y2, C)):
+        Nc, Kc = Rt.shape
+        gy, ps = f(E, 2 * Nc), f(E, Nc)
+        _lib.call("fu_complex_linear_gate_bwd", gz.data_ptr(), gz[:, Kc:].data_ptr(), gz.stride(0), Rt.data_ptr(),
+                  Itn.data_ptr(), Rt.stride(0), _lib.ptr(W3), gy.data_ptr(), gy[:, Nc:].data_ptr(),
+                  gy.stride(0), F.data_ptr(), F[:, Nc:].data_ptr(), F.stride(0), Y0.data_ptr(), Y0.stride(0),
+                  s_off, C, ps.data_ptr(), ps.stride(0), E, Nc, Kc, st)
+        gys.append(gy)
+        psums.append(ps)
+    del g1, g2, gz
+    gy0 = f(E, (2 * L + 1) * C)
+    _lib.call("fu_linear_gate_bwd", g0.data_ptr(), g0.stride(0), V0t.data_ptr(), V0t.stride(0), Y0.data_ptr(),
+              Y0.stride(0), psums[0].data_ptr(), psums[0].stride(0), psums[1].data_ptr(), psums[1].stride(0),
+              gy0.data_ptr(), gy0.stride(0), E, C, V0t.shape[1], L, st)
+    # release each intermediate as soon as it is consumed: the backward of a block runs near
+    # the step's memory peak (every earlier layer's saved tensors are still alive)
+    del psums, g0
+    g_x0 = gemm(gy0, W0t)
+    del gy0
+    g_x1 = complex_gemm(gys[0], P1t, Q1tn, sp[1])
+    gys[0] = None
+    g_x2 = complex_gemm(gys[1], P2t, Q2tn, sp[3])
+    del gys
+    return g_x0, g_x1, g_x2
+
+
 class Conv1GateConv2(torch.autograd.Function):
     """The edge-wise SO(2) pair of a block (model.py:152-154): conv1 + gate as in Conv1Gate,
-    then conv2 (m = 0 real with bias V0 / c0, m = 1, 2 complex R + iI).  Its backward fuses the
-    gate backward into the conv2 input-gradient epilogues: the m = 1, 2 complex GEMMs write
-    g_Y = g_Z s and their gate sums, then the m = 0 GEMM finishes g_Y_m0 (gate-paired) with
-    the gate gradients; g_Z is never stored and no separate gating pass runs."""
+    then conv2 (m = 0 real with bias V0 / c0, m = 1, 2 complex R + iI); see conv_pair_fwd and
+    conv_pair_bwd."""
 
     @staticmethod
     def forward(ctx, X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, V0, c0, V0t, R1, I1, R1t, I1tn, R2,
                 I2, R2t, I2tn, C, splits):
-        X0 = _lib.require(X0, torch.float32, "X_m0")
-        X1 = _lib.require(X1, torch.float32, "X_m1")
-        X2 = _lib.require(X2, torch.float32, "X_m2")
-        E = X0.shape[0]
-        dev = X0.device
-        st = _lib.stream_ptr(dev)
-        f = lambda *s: torch.empty(*s, device=dev, dtype=torch.float32)
-        L = _degrees(W0, C)
-        Y0, Z0, S = f(E, (2 * L + 1) * C), f(E, (L + 1) * C), f(E, L * C)
-        _lib.call("fu_linear_gate", X0.data_ptr(), X0.stride(0), W0.data_ptr(), W0.stride(0), _lib.ptr(b0),
-                  Y0.data_ptr(), Y0.stride(0), Z0.data_ptr(), Z0.stride(0), S.data_ptr(), S.stride(0), E, C,
-                  W0.shape[1], L, st)
-        sp = splits or (None,) * 8
-        outs = []
-        for X, P, Q, W3, s_off in ((X1, P1, Q1, sp[0], 0), (X2, P2, Q2, sp[2], C)):
-            Nc, Kc = P.shape
-            Y, Z = f(E, 2 * Nc), f(E, 2 * Nc)
-            _lib.call("fu_complex_linear_gate", X.data_ptr(), X[:, Kc:].data_ptr(), X.stride(0), P.data_ptr(),
-                      Q.data_ptr(), P.stride(0), _lib.ptr(W3), Y.data_ptr(), Y[:, Nc:].data_ptr(), Y.stride(0),
-                      Z.data_ptr(), Z[:, Nc:].data_ptr(), Z.stride(0), S.data_ptr(), S.stride(0), s_off, E, Nc, Kc,
-                      st)
-            outs += [Y, Z]
-        Y1, Z1, Y2, Z2 = outs
-        Zo0 = gemm(Z0, V0, c0)
-        Zo1 = complex_gemm(Z1, R1, I1, sp[4])
-        Zo2 = complex_gemm(Z2, R2, I2, sp[6])
-        ctx.save_for_backward(Y0, Y1, Y2, S, W0t, P1t, Q1tn, P2t, Q2tn, V0t, R1t, I1tn, R2t, I2tn)
-        ctx.C, ctx.L, ctx.sp = C, L, sp
-        return Zo0, Zo1, Zo2
+        conv1 = (W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn)
+        conv2 = (V0, c0, V0t, R1, I1, R1t, I1tn, R2, I2, R2t, I2tn)
+        Zo, Y = conv_pair_fwd([X0, X1, X2], conv1, conv2, C, splits)
+        ctx.save_for_backward(*Y)
+        ctx.conv1, ctx.conv2, ctx.C, ctx.sp = conv1, conv2, C, splits
+        return Zo
 
     @staticmethod
     def backward(ctx, g0, g1, g2):
-        Y0, Y1, Y2, S, W0t, P1t, Q1tn, P2t, Q2tn, V0t, R1t, I1tn, R2t, I2tn = ctx.saved_tensors
-        C, L = ctx.C, ctx.L
-        E = Y0.shape[0]
-        dev = Y0.device
-        st = _lib.stream_ptr(dev)
-        f = lambda *s: torch.empty(*s, device=dev, dtype=torch.float32)
-        g0 = torch.zeros(E, (L + 1) * C, device=dev) if g0 is None else g0.contiguous()
-        g1 = torch.zeros(E, 2 * L * C, device=dev) if g1 is None else g1.contiguous()
-        g2 = torch.zeros(E, 2 * (L - 1) * C, device=dev) if g2 is None else g2.contiguous()
-        sp = ctx.sp
-        gys, psums = [], []
-        for g, Rt, Itn, W3, F, s_off in ((g1, R1t, I1tn, sp[5], Y1, 0), (g2, R2t, I2tn, sp[7], Y2, C)):
-            Nc, Kc = Rt.shape
-            gy, ps = f(E, 2 * Nc), f(E, Nc)
-            _lib.call("fu_complex_linear_gate_bwd", g.data_ptr(), g[:, Kc:].data_ptr(), g.stride(0), Rt.data_ptr(),
-                      Itn.data_ptr(), Rt.stride(0), _lib.ptr(W3), gy.data_ptr(), gy[:, Nc:].data_ptr(),
-                      gy.stride(0), F.data_ptr(), F[:, Nc:].data_ptr(), F.stride(0), S.data_ptr(), S.stride(0),
-                      s_off, ps.data_ptr(), ps.stride(0), E, Nc, Kc, st)
-            gys.append(gy)
-            psums.append(ps)
-        gy0 = f(E, (2 * L + 1) * C)
-        _lib.call("fu_linear_gate_bwd", g0.data_ptr(), g0.stride(0), V0t.data_ptr(), V0t.stride(0), Y0.data_ptr(),
-                  Y0.stride(0), S.data_ptr(), S.stride(0), psums[0].data_ptr(), psums[0].stride(0),
-                  psums[1].data_ptr(), psums[1].stride(0), gy0.data_ptr(), gy0.stride(0), E, C, V0t.shape[1], L,
-                  st)
-        return ((gemm(gy0, W0t), complex_gemm(gys[0], P1t, Q1tn, sp[1]), complex_gemm(gys[1], P2t, Q2tn, sp[3])) +
-                (None,) * 24)
+        gx = conv_pair_bwd(ctx.saved_tensors, ctx.conv1, ctx.conv2, ctx.C, ctx.sp, [g0, g1, g2])
+        return tuple(gx) + (None,) * 24
 
 
 def conv1_gate_conv2(X0, X1, X2, conv1, conv2, C, splits=None):
@@ -207,3 +242,72 @@ def conv1_gate_conv2(X0, X1, X2, conv1, conv2, C, splits=None):
     (P1, Q1), (P1t, Q1tn), (P2, Q2), (P2t, Q2tn), (R1, I1), (R1t, I1tn), (R2, I2), (R2t, I2tn).
     Returns Zout_m0, Zout_m1, Zout_m2."""
     return Conv1GateConv2.apply(X0, X1, X2, *conv1, *conv2, C, splits)
+
+
+class EdgeBlock(torch.autograd.Function):
+    """One block's edge-wise path as one autograd node: gather-rotate (ops/gather.py), conv1 +
+    gate + conv2 (model.py:150-154).  The (E, 18C) gather output X lives only inside the
+    forward (each part freed after its GEMM) and its gradient only inside the backward, which
+    runs conv_pair_bwd and then the node-centric gather backward.  lmax = 2 (layout 0 or 1) or
+    lmax = 3, 4 (reference block order with the degree-3/4 Wigner rows wig_ext)."""
+
+    @staticmethod
+    def forward(ctx, x_in, wigner, wig_ext, rad_out, idx_i, idx_j, csd_emb, batch, topology, layout, lmax, conv1,
+                conv2, C, splits, rad_src):
+        from .gather import gather_fwd, gather_operands
+        from .lmax import gather_lmax_fwd, gather_lmax_operands
+        L = int(lmax)
+        if L == 2:
+            ops = gather_operands(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch)
+            X = list(gather_fwd(*ops, layout))
+        else:
+            ops = gather_lmax_operands(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, L)
+            X = list(gather_lmax_fwd(*ops, L))
+        Zo, Y = conv_pair_fwd(X, conv1, conv2, C, splits)
+        r = 4 if L == 2 else 5   # position of rad_out among the gather operands
+        if rad_src is not None:
+            # keep the (E, C) source of the radial output instead of the (E, 6 L C) output
+            ops = ops[:r] + (rad_src[0],) + ops[r + 1:]
+            ctx.rad_w = rad_src[1:]
+        else:
+            ctx.rad_w = None
+        ctx.save_for_backward(*ops, *Y)
+        ctx.n_ops, ctx.r, ctx.topology, ctx.layout, ctx.L = len(ops), r, topology, int(layout), L
+        ctx.conv1, ctx.conv2, ctx.C, ctx.sp = conv1, conv2, C, splits
+        return Zo
+
+    @staticmethod
+    def backward(ctx, g0, g1, g2):
+        from .gather import gather_bwd
+        from .lmax import gather_lmax_bwd
+        from .radial import recompute_output
+        saved = ctx.saved_tensors
+        ops, Y = list(saved[:ctx.n_ops]), saved[ctx.n_ops:]
+        if ctx.rad_w is not None:
+            ops[ctx.r] = recompute_output((ops[ctx.r],) + tuple(ctx.rad_w))
+        gz = [g0, g1, g2]
+        gx = list(conv_pair_bwd(Y, ctx.conv1, ctx.conv2, ctx.C, ctx.sp, list(gz)))
+        # The incoming gradients are the rotate-scatter backward's fresh g_Zout buffers, read
+        # only by conv_pair_bwd above.  The autograd engine keeps its references until this
+        # function returns, through the gather backward below, where the step's memory peaks;
+        # their device memory is handed back now (queued after the kernels that read it).
+        for t in gz:
+            if t is not None and t.is_contiguous() and t._base is None:
+                t.untyped_storage().resize_(0)
+        del g0, g1, g2, gz
+        if ctx.L == 2:
+            g_x, g_w, g_rad = gather_bwd(*ops, ctx.topology, ctx.layout, *gx)
+            g_ext = None
+        else:
+            g_x, g_w, g_ext, g_rad = gather_lmax_bwd(*ops, ctx.topology, ctx.L, *gx)
+        return g_x, g_w, g_ext, g_rad, None, None, None, None, None, None, None, None, None, None, None, None
+
+
+def edge_block(x_in, wigner, wig_ext, rad_out, idx_i, idx_j, csd_emb, batch, topology, layout, lmax, conv1, conv2, C,
+               splits=None, rad_src=None):
+    """gather_wigner_split (or gather_rotate_lmax) followed by conv1_gate_conv2, as one node
+    whose gather output never outlives the block: returns (Zout_m0, Zout_m1, Zout_m2).
+    rad_src: None, or the radial bank's (h2_k, W3_k, b3_k) source of rad_out; the backward
+    then recomputes rad_out from it instead of keeping it (memory for one extra GEMM)."""
+    return EdgeBlock.apply(x_in, wigner, wig_ext, rad_out, idx_i, idx_j, csd_emb, batch, topology, layout, lmax,
+                           tuple(conv1), tuple(conv2), C, splits, rad_src)

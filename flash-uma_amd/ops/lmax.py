@@ -62,54 +62,67 @@ def _csrs(topology, idx_i, idx_j, N, E):
     return rptr, ridx, sptr, sidx
 
 
+def gather_lmax_operands(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, L):
+    ops = (_lib.require(x_in, torch.float32, "x_in"), _lib.require(idx_i, torch.int64, "idx_i"),
+           _lib.require(idx_j, torch.int64, "idx_j"), _lib.require(wigner, torch.float32, "wigner"),
+           _lib.require(wig_ext, torch.float32, "wig_ext"), _lib.require(rad_out, torch.float32, "rad_out"),
+           _lib.require(csd_emb, torch.float32, "csd_emb"), _lib.require(batch, torch.int64, "batch"))
+    N, K, C = ops[0].shape
+    E = ops[1].shape[0]
+    if K != (L + 1) ** 2 or ops[5].shape != (E, 6 * L * C) or ops[4].shape != (E, ext_width(L)):
+        raise _lib.FlashUMAError(f"gather_rotate_lmax: shapes do not match lmax={L}")
+    return ops
+
+
+def gather_lmax_fwd(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, L):
+    """fu_gather_fwd_lmax: (X_m0, X_m1, X_m2) for operands from gather_lmax_operands."""
+    N, _, C = x_in.shape
+    E = idx_i.shape[0]
+    dev = x_in.device
+    X_m0 = torch.empty(E, 2 * (L + 1) * C, device=dev)
+    X_m1 = torch.empty(E, 4 * L * C, device=dev)
+    X_m2 = torch.empty(E, 4 * (L - 1) * C, device=dev)
+    _lib.call("fu_gather_fwd_lmax", x_in.data_ptr(), idx_i.data_ptr(), idx_j.data_ptr(), wigner.data_ptr(),
+              _ext_ptr(wig_ext), rad_out.data_ptr(), csd_emb.data_ptr(), batch.data_ptr(), X_m0.data_ptr(),
+              X_m1.data_ptr(), X_m2.data_ptr(), E, N, csd_emb.shape[0], C, L, _lib.stream_ptr(dev))
+    return X_m0, X_m1, X_m2
+
+
+def gather_lmax_bwd(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, topology, L, g0, g1, g2):
+    """fu_gather_bwd_lmax: (g_x, g_wigner, g_wig_ext, g_rad)."""
+    N, _, C = x_in.shape
+    E = idx_i.shape[0]
+    dev = x_in.device
+    g0 = torch.zeros(E, 2 * (L + 1) * C, device=dev) if g0 is None else g0.contiguous()
+    g1 = torch.zeros(E, 4 * L * C, device=dev) if g1 is None else g1.contiguous()
+    g2 = torch.zeros(E, 4 * (L - 1) * C, device=dev) if g2 is None else g2.contiguous()
+    rptr, ridx, sptr, sidx = _csrs(topology, idx_i, idx_j, N, E)
+    g_x = torch.empty_like(x_in)
+    g_w = torch.empty_like(wigner)
+    g_ext = torch.empty_like(wig_ext)
+    g_rad = torch.empty_like(rad_out)
+    ws = torch.empty(E * (34 + ext_width(L)), device=dev)
+    _lib.call("fu_gather_bwd_lmax", g0.data_ptr(), g1.data_ptr(), g2.data_ptr(), x_in.data_ptr(),
+              wigner.data_ptr(), _ext_ptr(wig_ext), rad_out.data_ptr(), csd_emb.data_ptr(), batch.data_ptr(),
+              rptr.data_ptr(), ridx.data_ptr(), sptr.data_ptr(), sidx.data_ptr(), g_x.data_ptr(), g_w.data_ptr(),
+              _ext_ptr(g_ext), g_rad.data_ptr(), ws.data_ptr(), E, N, csd_emb.shape[0], C, L,
+              _lib.stream_ptr(dev))
+    return g_x, g_w, g_ext, g_rad
+
+
 class GatherRotateLmax(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, topology, lmax):
         L = int(lmax)
-        x_in = _lib.require(x_in, torch.float32, "x_in")
-        idx_i = _lib.require(idx_i, torch.int64, "idx_i")
-        idx_j = _lib.require(idx_j, torch.int64, "idx_j")
-        wigner = _lib.require(wigner, torch.float32, "wigner")
-        wig_ext = _lib.require(wig_ext, torch.float32, "wig_ext")
-        rad_out = _lib.require(rad_out, torch.float32, "rad_out")
-        csd_emb = _lib.require(csd_emb, torch.float32, "csd_emb")
-        batch = _lib.require(batch, torch.int64, "batch")
-        N, K, C = x_in.shape
-        E = idx_i.shape[0]
-        if K != (L + 1) ** 2 or rad_out.shape != (E, 6 * L * C) or wig_ext.shape != (E, ext_width(L)):
-            raise _lib.FlashUMAError(f"gather_rotate_lmax: shapes do not match lmax={L}")
-        dev = x_in.device
-        X_m0 = torch.empty(E, 2 * (L + 1) * C, device=dev)
-        X_m1 = torch.empty(E, 4 * L * C, device=dev)
-        X_m2 = torch.empty(E, 4 * (L - 1) * C, device=dev)
-        _lib.call("fu_gather_fwd_lmax", x_in.data_ptr(), idx_i.data_ptr(), idx_j.data_ptr(), wigner.data_ptr(),
-                  _ext_ptr(wig_ext), rad_out.data_ptr(), csd_emb.data_ptr(), batch.data_ptr(), X_m0.data_ptr(),
-                  X_m1.data_ptr(), X_m2.data_ptr(), E, N, csd_emb.shape[0], C, L, _lib.stream_ptr(dev))
-        ctx.save_for_backward(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch)
+        ops = gather_lmax_operands(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, L)
+        X = gather_lmax_fwd(*ops, L)
+        ctx.save_for_backward(*ops)
         ctx.topology, ctx.lmax = topology, L
-        return X_m0, X_m1, X_m2
+        return X
 
     @staticmethod
     def backward(ctx, g0, g1, g2):
-        x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch = ctx.saved_tensors
-        L = ctx.lmax
-        N, _, C = x_in.shape
-        E = idx_i.shape[0]
-        dev = x_in.device
-        g0 = torch.zeros(E, 2 * (L + 1) * C, device=dev) if g0 is None else g0.contiguous()
-        g1 = torch.zeros(E, 4 * L * C, device=dev) if g1 is None else g1.contiguous()
-        g2 = torch.zeros(E, 4 * (L - 1) * C, device=dev) if g2 is None else g2.contiguous()
-        rptr, ridx, sptr, sidx = _csrs(ctx.topology, idx_i, idx_j, N, E)
-        g_x = torch.empty_like(x_in)
-        g_w = torch.empty_like(wigner)
-        g_ext = torch.empty_like(wig_ext)
-        g_rad = torch.empty_like(rad_out)
-        ws = torch.empty(E * (34 + ext_width(L)), device=dev)
-        _lib.call("fu_gather_bwd_lmax", g0.data_ptr(), g1.data_ptr(), g2.data_ptr(), x_in.data_ptr(),
-                  wigner.data_ptr(), _ext_ptr(wig_ext), rad_out.data_ptr(), csd_emb.data_ptr(), batch.data_ptr(),
-                  rptr.data_ptr(), ridx.data_ptr(), sptr.data_ptr(), sidx.data_ptr(), g_x.data_ptr(), g_w.data_ptr(),
-                  _ext_ptr(g_ext), g_rad.data_ptr(), ws.data_ptr(), E, N, csd_emb.shape[0], C, L,
-                  _lib.stream_ptr(dev))
+        g_x, g_w, g_ext, g_rad = gather_lmax_bwd(*ctx.saved_tensors, ctx.topology, ctx.lmax, g0, g1, g2)
         return g_x, None, None, g_w, g_ext, g_rad, None, None, None, None
 
 

@@ -105,28 +105,48 @@ class RadialBank(torch.nn.Module):
     # reserve then grew from 31 to 230 GB on the 8,192-atom Fe cell, and the allocations
     # on that path stalled the host for seconds in some processes.
 
-    def forward(self, gauss, Z, idx_i, idx_j):
+    def forward(self, gauss, Z, idx_i, idx_j, with_sources: bool = False):
         """gauss (E, B) -> tuple of G radial outputs (E, n_k).
 
         The trunk (first two layers of all MLPs) is one autograd node; each block's output
         layer is its own node, whose backward writes its input gradient straight into the
-        trunk's gradient buffer."""
+        trunk's gradient buffer.  with_sources: also return, per block, (h2_k, W3_k, b3_k), from
+        which a consumer can recompute the output bit for bit (source(...)) instead of keeping
+        it for its backward."""
         holder = _GradHolder()
         h2s = _RadialTrunkFn.apply(gauss, Z, idx_i, idx_j, self, holder)
-        outs = []
+        outs, srcs = [], []
         for k in range(self.G):
             W, Wt, b = getattr(self, f"W3_{k}"), getattr(self, f"W3_{k}_t"), getattr(self, f"b3_{k}")
             outs.append(_RadialOutFn.apply(h2s[k], W, b, Wt, holder, k))
-        return tuple(outs)
+            srcs.append((h2s[k].detach(), W, b))
+        return (tuple(outs), tuple(srcs)) if with_sources else tuple(outs)
+
+
+def recompute_output(src) -> torch.Tensor:
+    """A block's radial output from its (h2_k, W3_k, b3_k) source: the forward's GEMM on the
+    same operands, so bitwise the tensor the bank returned."""
+    h2k, W, b = src
+    return _gemm(h2k, W, b, torch.empty(h2k.shape[0], W.shape[0], device=h2k.device, dtype=torch.float32))
 
 
 class _GradHolder:
-    """The (E, G*C) gradient of the trunk output: allocated by the trunk forward on the main
-    stream, filled slice by slice by the blocks' output-layer backwards and consumed by the
-    trunk backward; it lives as long as the autograd graph."""
+    """The (E, G*C) gradient of the trunk output: allocated by the first output-layer backward,
+    filled slice by slice by the blocks' output-layer backwards and released by the trunk
+    backward that consumes it (the holder outlives the backward inside the autograd graph,
+    which the returned outputs keep referenced, so it must not keep device memory)."""
 
     def __init__(self):
         self.g = None
+        self.shape = None
+        self.device = None
+
+    def buffer(self) -> torch.Tensor:
+        if self.g is None:
+            if self.shape is None:
+                raise _lib.FlashUMAError("radial bank: backward through an output built without input gradients")
+            self.g = torch.empty(self.shape, device=self.device, dtype=torch.float32)
+        return self.g
 
 
 class _RadialTrunkFn(torch.autograd.Function):
@@ -146,33 +166,39 @@ class _RadialTrunkFn(torch.autograd.Function):
         p2 = _batched(h1, bank.W2, bank.b2, G, C, C, torch.empty_like(h1))
         del h1
         h2, m2, r2 = _ln_grouped_fwd(p2, None, None, None, None, None, bank.gamma2, bank.beta2, G, C, bank.eps)
-        if ctx.needs_input_grad[0]:
-            holder.g = torch.empty_like(p2)
-        ctx.save_for_backward(p1, m1, r1, p2, m2, r2, Z, idx_i, idx_j)
+        # the trunk gradient buffer is allocated by the first output-layer backward, not here:
+        # it is not needed before the backward, and the forward's end is a memory peak
+        holder.shape = tuple(p2.shape) if ctx.needs_input_grad[0] else None
+        holder.device = p2.device
+        # p1 (E, G*C) is not kept: the backward recomputes it from the (E, B) Gaussians with
+        # the K = B GEMM (10x fewer bytes held through the step for one small GEMM)
+        del p1
+        ctx.save_for_backward(gauss, m1, r1, p2, m2, r2, Z, idx_i, idx_j)
         ctx.bank, ctx.holder = bank, holder
         return tuple(h2[:, k * C:(k + 1) * C] for k in range(G))
 
     @staticmethod
     def backward(ctx, *g_views):
-        p1, m1, r1, p2, m2, r2, Z, idx_i, idx_j = ctx.saved_tensors
+        gauss, m1, r1, p2, m2, r2, Z, idx_i, idx_j = ctx.saved_tensors
         bank, holder = ctx.bank, ctx.holder
-        E, G, C = p1.shape[0], bank.G, bank.C
+        E, G, C = gauss.shape[0], bank.G, bank.C
         g_h2 = holder.g if holder.g is not None else torch.empty_like(p2)
+        holder.g = None   # a retained graph's next backward allocates a fresh buffer
         for k, gv in enumerate(g_views):
             sl = g_h2[:, k * C:(k + 1) * C]
             if gv is None:
                 sl.zero_()
             elif gv.data_ptr() != sl.data_ptr() or gv.stride() != sl.stride():
                 sl.copy_(gv)
-        # holder.g stays with the graph (a retained graph may run its backward again)
         g_p2 = _ln_grouped_bwd(p2, None, None, None, None, None, bank.gamma2, bank.beta2, m2, r2, g_h2, G, C)
         del g_h2
         g_h1 = _batched(g_p2, bank.W2_t, None, G, C, C, torch.empty_like(g_p2))
         del g_p2
+        p1 = _gemm(gauss, bank.W1g, None, torch.empty(E, G * C, device=gauss.device, dtype=torch.float32))
         g_p1 = _ln_grouped_bwd(p1, (bank.tab_src, bank.tab_tgt), Z, idx_i, idx_j, bank.b1, bank.gamma1, bank.beta1,
                                m1, r1, g_h1, G, C)
-        del g_h1
-        g_gauss = _gemm(g_p1, bank.W1g_t, None, torch.empty(E, bank.B, device=p1.device, dtype=torch.float32))
+        del g_h1, p1
+        g_gauss = _gemm(g_p1, bank.W1g_t, None, torch.empty(E, bank.B, device=gauss.device, dtype=torch.float32))
         return g_gauss, None, None, None, None, None
 
 
@@ -190,9 +216,7 @@ class _RadialOutFn(torch.autograd.Function):
     def backward(ctx, g_rad):
         (Wt,) = ctx.saved_tensors
         g_rad = g_rad.contiguous()
-        if ctx.holder.g is None:
-            raise _lib.FlashUMAError("radial bank: backward through an output built without input gradients")
         C = Wt.shape[0]
-        sl = ctx.holder.g[:, ctx.k * C:(ctx.k + 1) * C]
+        sl = ctx.holder.buffer()[:, ctx.k * C:(ctx.k + 1) * C]
         _gemm(g_rad, Wt, None, sl)
         return sl, None, None, None, None, None

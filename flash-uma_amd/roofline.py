@@ -95,16 +95,16 @@ def _ln_bwd(a):
 
 
 def _linear_gate_bwd(a):
-    # g_Z never stored: reads y_l0 + y_lm0 ((L+1)C) of Y0, S (LC), P1 (LC), P2 ((L-1)C);
-    # writes gY0 ((2L+1)C)
-    M, C, K, L = a[14], a[15], a[16], a[17]
+    # g_Z never stored: reads Y0 ((2L+1)C: values and gate pre-activations), P1 (LC),
+    # P2 ((L-1)C); writes gY0 ((2L+1)C)
+    M, C, K, L = a[12], a[13], a[14], a[15]
     N = (L + 1) * C
     return 4 * (M * K + N * K + (6 * L + 1) * M * C), 2 * M * N * K
 
 
 def _complex_linear_gate_bwd(a):
-    # reads F (2 Nc) and S (Nc), writes gY (2 Nc) and the gate sums (Nc)
-    M, Nc, Kc = a[18], a[19], a[20]
+    # reads F (2 Nc) and the gate columns of Y0 (Nc), writes gY (2 Nc) and the gate sums (Nc)
+    M, Nc, Kc = a[19], a[20], a[21]
     return 4 * (2 * M * Kc + 2 * Nc * Kc + 6 * M * Nc), 6 * M * Nc * Kc
 
 
@@ -183,15 +183,17 @@ def _complex_linear(a):
 
 
 def _linear_gate(a):
-    # N = (2L+1)C outputs Y plus the gate's sigmoids S (LC) and gated / SiLU copies Z ((L+1)C)
+    # N = (2L+1)C outputs Y plus the gated / SiLU copies Z ((L+1)C) (and the sigmoids S (LC)
+    # when requested)
     M, C, K, L = a[11], a[12], a[13], a[14]
     N = (2 * L + 1) * C
-    return 4 * (M * K + N * K + M * N + (2 * L + 1) * M * C), 2 * M * N * K
+    zs = (2 * L + 1) if a[9] is not None else (L + 1)
+    return 4 * (M * K + N * K + M * N + zs * M * C), 2 * M * N * K
 
 
 def _complex_linear_gate(a):
-    # complex product plus the sigmoid read S (Nc) and the gated copies Z_r, Z_i (2 Nc)
-    M, Nc, Kc = a[16], a[17], a[18]
+    # complex product plus the gate columns of Y0 read (Nc) and the gated copies Z_r, Z_i (2 Nc)
+    M, Nc, Kc = a[17], a[18], a[19]
     return 4 * (2 * M * Kc + 2 * M * Nc + 2 * Nc * Kc + 3 * M * Nc), 6 * M * Nc * Kc
 
 

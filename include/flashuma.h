@@ -252,41 +252,46 @@ int fu_complex_weight_split(const float* P, const float* Q, int64_t ldw, int32_t
  * Y = A W^T + bias with N = (2L+1)C columns (L = lmax) in the gate-paired order: 64-column
  * pairs [gate_l | y_lm0] x C/32 for l = 1..L, then y_l0 (W and bias rows permuted to it; at
  * lmax 2 this is fu_gating_fwd layout 1), written for the backward, plus Z (M, (L+1)C) =
- * [silu(y_l0), y_l1m0 s1, ..., y_lLm0 sL] and S (M, LC) = [s1 .. sL], s = sigmoid(gate).
+ * [silu(y_l0), y_l1m0 s1, ..., y_lLm0 sL], and, if S is not NULL, S (M, LC) = [s1 .. sL],
+ * s = sigmoid(gate) (the model passes NULL: the gate epilogues below recompute s from Y).
  * lmax 2..4; C a multiple of 64; other constraints as fu_linear. */
 int fu_linear_gate(const float* A, int64_t lda, const float* W, int64_t ldw, const float* bias,
                    float* Y, int64_t ldy, float* Z, int64_t ldz, float* S, int64_t lds, int64_t M,
                    int32_t C, int32_t K, int32_t lmax, void* stream);
 
 /* conv1 m = 1, 2 fused with the gate activation: fu_complex_linear, then
- * Z_r = Y_r s, Z_i = Y_i s with s = S[row][s_off + column] (S from fu_linear_gate: s_off = 0
- * for m = 1, whose columns are [l1 | .. | lL]; s_off = C for m = 2, columns [l2 | .. | lL]). */
+ * Z_r = Y_r s, Z_i = Y_i s with s = sigmoid(gate) of gate column t = s_off + column (degree
+ * 1 + t / C, channel t % C), read from Y0, the gate-paired output of fu_linear_gate (row
+ * stride ldy0): s_off = 0 for m = 1, whose columns are [l1 | .. | lL]; s_off = C for m = 2,
+ * columns [l2 | .. | lL].  C a multiple of 32, s_off and ldy0 multiples of 4. */
 int fu_complex_linear_gate(const float* A_r, const float* A_i, int64_t lda, const float* P,
                            const float* Q, int64_t ldw, const void* W3, float* Y_r, float* Y_i,
-                           int64_t ldy, float* Z_r, float* Z_i, int64_t ldz, const float* S, int64_t lds,
-                           int32_t s_off, int64_t M, int32_t Nc, int32_t Kc, void* stream);
+                           int64_t ldy, float* Z_r, float* Z_i, int64_t ldz, const float* Y0,
+                           int64_t ldy0, int32_t s_off, int32_t C, int64_t M, int32_t Nc, int32_t Kc,
+                           void* stream);
 
 /* conv2 m = 0 input gradient (model.py:154) fused with the gate backward (ops/gating.py:
  * 109-185): the GEMM g_Z_m0 = gZo (M, (L+1)C) @ Wt^T is not stored; gY0 (M, (2L+1)C,
  * gate-paired as Y0) receives g_y_l0 = g silu'(y_l0), g_y_lm0 = g s_l and
  * g_gate_l = s_l (1 - s_l) (g y_lm0 + P1[:, (l-1)C:] + (l >= 2: P2[:, (l-2)C:])).  Y0: the
- * forward output of fu_linear_gate; S its sigmoids; P1 (M, LC), P2 (M, (L-1)C): the m = 1, 2
- * gate sums from fu_complex_linear_gate_bwd.  K = (L+1)C (the conv2 m = 0 width),
- * Wt = W2_m0^T (no bias).  lmax 2..4; C a multiple of 64. */
+ * forward output of fu_linear_gate (s_l = sigmoid of its gate columns); P1 (M, LC),
+ * P2 (M, (L-1)C): the m = 1, 2 gate sums from fu_complex_linear_gate_bwd.  K = (L+1)C (the
+ * conv2 m = 0 width), Wt = W2_m0^T (no bias).  lmax 2..4; C a multiple of 64. */
 int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* Wt, int64_t ldw, const float* Y0,
-                       int64_t ldy0, const float* S, int64_t lds, const float* P1, int64_t ldp1,
-                       const float* P2, int64_t ldp2, float* gY0, int64_t ldg, int64_t M, int32_t C,
-                       int32_t K, int32_t lmax, void* stream);
+                       int64_t ldy0, const float* P1, int64_t ldp1, const float* P2, int64_t ldp2,
+                       float* gY0, int64_t ldg, int64_t M, int32_t C, int32_t K, int32_t lmax,
+                       void* stream);
 
 /* conv2 m = 1 or 2 input gradient fused with the gate backward: the complex product
  * g_Z = (A_r + i A_i)(P + iQ)^T (P = R^T, Q = -I^T of the conv2 weight) is not stored;
- * gY_r/gY_i = g_Z s with s = S[row][s_off + column], and Pout = g_Zr F_r + g_Zi F_i (the
- * gate sum of this block; F = the forward pre-activation Y from fu_complex_linear_gate). */
+ * gY_r/gY_i = g_Z s with s recomputed from Y0 as in fu_complex_linear_gate (same s_off, C),
+ * and Pout = g_Zr F_r + g_Zi F_i (the gate sum of this block; F = the forward pre-activation
+ * Y from fu_complex_linear_gate). */
 int fu_complex_linear_gate_bwd(const float* A_r, const float* A_i, int64_t lda, const float* P,
                                const float* Q, int64_t ldw, const void* W3, float* gY_r, float* gY_i,
-                               int64_t ldg, const float* F_r, const float* F_i, int64_t ldf, const float* S,
-                               int64_t lds, int32_t s_off, float* Pout, int64_t ldp, int64_t M,
-                               int32_t Nc, int32_t Kc, void* stream);
+                               int64_t ldg, const float* F_r, const float* F_i, int64_t ldf,
+                               const float* Y0, int64_t ldy0, int32_t s_off, int32_t C, float* Pout,
+                               int64_t ldp, int64_t M, int32_t Nc, int32_t Kc, void* stream);
 
 /* ------------------------------------------------------------------------------------
  * Node-level modules attached to the backbone (model.py:145,157,218) and input plumbing

@@ -85,13 +85,13 @@ def test_zero_rows_accept_empty_arrays():
         "fu_linear_batched": (None, 640, 128, None, 128, 16384, None, 128, 5, None, 0, 0, None, 640, 128, 0, 128,
                               128, 5, None),
         "fu_linear_gate": (None, 768, None, 768, None, None, 640, None, 384, None, 256, 0, 128, 768, 2, None),
-        "fu_linear_gate_bwd": (None, 384, None, 384, None, 640, None, 256, None, 256, None, 128, None, 640, 0, 128,
-                               384, 2, None),
+        "fu_linear_gate_bwd": (None, 384, None, 384, None, 640, None, 256, None, 128, None, 640, 0, 128, 384, 2,
+                               None),
         "fu_complex_linear": (None, None, 256, None, None, 256, None, None, None, 128, 0, 128, 256, None),
         "fu_complex_linear_gate": (None, None, 256, None, None, 256, None, None, None, 128, None, None, 128, None,
-                                   256, 0, 0, 128, 256, None),
+                                   640, 0, 128, 0, 128, 256, None),
         "fu_complex_linear_gate_bwd": (None, None, 256, None, None, 256, None, None, None, 128, None, None, 128,
-                                       None, 256, 0, None, 128, 0, 128, 256, None),
+                                       None, 640, 0, 128, None, 128, 0, 128, 256, None),
         # element tables present (a weight), per-edge element ids empty
         "fu_ln_silu_grouped_fwd": (None, 640, 16, 16, 128, 16, None, None, None, None, None, None, 640, None, None, 0,
                                    5, 128, f(1e-7), None),
@@ -113,7 +113,11 @@ def test_zero_rows_accept_empty_arrays():
     st, _ = _status("fu_linear", None, 16, None, 16, None, None, 16, 0, 16, 6, None)
     assert st == -2
     st, _ = _status("fu_complex_linear_gate", None, None, 256, None, None, 256, None, None, None, 128, None, None,
-                    64, None, 256, 0, 0, 128, 256, None)
+                    64, None, 640, 0, 128, 0, 128, 256, None)
+    assert st == -1
+    # gate columns beyond the rows of Y0
+    st, _ = _status("fu_complex_linear_gate", None, None, 256, None, None, 256, None, None, None, 128, None, None,
+                    128, None, 256, 0, 128, 0, 128, 256, None)
     assert st == -1
 
 

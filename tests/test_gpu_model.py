@@ -338,3 +338,23 @@ def test_unbalanced_complex_weight_keeps_four_products(cuda):
     assert all(t is not None for t in layers[1]._splits[2:]) and all(t is not None for t in layers[0]._splits)
     ref = energy_forces_stress(bb_cpu, hd_cpu, s.pos, s.Z, s.cell, ei, off, dtype=torch.float64)
     _check(out, ref, s.n_atoms)
+
+
+def test_radial_recompute_mode_is_bitwise_equal(cuda):
+    """The large-graph mode (each block recomputes its radial-MLP output in the backward
+    instead of keeping it) gives bitwise the same energy, forces and stress as the default
+    mode, since the recompute runs the forward's GEMM on the same operands."""
+    import systems
+    bb, hd, model = _build(cuda)
+    s = systems.water_box(n_mol=64, L=12.42, seed=3)
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, 6.0, 30)
+    ce = model.backbone.ce
+    a = _run(model, s, ei, off, cuda)
+    old = ce.RAD_RECOMPUTE_MIN_EDGES
+    try:
+        ce.RAD_RECOMPUTE_MIN_EDGES = 0
+        b = _run(model, s, ei, off, cuda)
+    finally:
+        ce.RAD_RECOMPUTE_MIN_EDGES = old
+    for k in ("energy", "forces", "stress", "node_embedding"):
+        assert torch.equal(a[k], b[k]), k
