@@ -9,16 +9,23 @@
 // MFMA flops for the same result up to fp32 rounding.  The sums a_r + a_i and P + Q are
 // formed in registers from the operands already staged in LDS, so no extra memory traffic.
 //
-// Tiling: 256 threads (4 waves, 2 x 2), an output tile of 128 rows x 64 columns of both
-// out_r and out_i; K advances in chunks of 16 through double-buffered LDS.  Three main loops:
+// Tiling: 256 threads (4 waves); K advances in chunks of 16 through double-buffered LDS.
+// Three main loops:
 //  * split bf16 with a pre-split weight (default when the caller passes W3, built once per
 //    frozen weight by fu_complex_weight_split): P, Q and S = P + Q are stored as bf16 planes
 //    in MFMA-fragment order ([32-column block][16-k chunk][P, Q, S][hi, mid, lo][lane], 16 B
 //    per lane), so each wave loads its B fragments with 1 KB coalesced loads straight into
 //    registers, one chunk ahead.  Only a_r, a_i and a_s = a_r + a_i are split in the kernel
-//    and staged as planes in LDS (36 KB per buffer, two workgroups per CU).  The three
-//    products above run as 6 x 3 MFMAs per 32-row block and chunk (six accumulator chains
-//    per wave, 64 x 32 of each of T1, T2, T3).
+//    and staged as planes in LDS (36 KB per buffer).  The output tile is 128 rows x 128
+//    columns of both out_r and out_i, the four waves side by side: each wave owns all 128
+//    rows of one 32-column block (four 32-row blocks x T1, T2, T3: twelve accumulator chains,
+//    192 accumulator registers, one workgroup per CU), so every B fragment it loads feeds
+//    4 x 6 MFMAs and every staged A chunk feeds four waves.  Against 64 x 32 per wave (two
+//    workgroups per CU) this halves the global loads per MFMA: 1.08-1.13x faster on the
+//    model's shapes (fetching the operands, not the MFMAs, was the limit: the same kernel
+//    without its B loads, or without its A loads, ran 1.25-1.35x faster).
+//  The two loops below keep an output tile of 128 rows x 64 columns (2 x 2 waves of
+//  64 x 32):
 //  * split bf16 without W3: a_r, a_i, P and Q are all split as they are staged (36 KB of
 //    planes per buffer); planes of a_r + a_i and P + Q as well would not fit two workgroups
 //    per CU, so this loop runs the four products directly,
@@ -33,6 +40,7 @@ namespace fu {
 
 constexpr int CBM = 128, CBN = 64;
 constexpr int CTA = CBM * 16, CTB = CBN * 16;
+constexpr int CBN_PRE = 128;  // output columns per tile of the pre-split path
 constexpr int CBUF = 2 * CTA + 2 * CTB;          // fp32: a_r | a_i | P | Q
 constexpr int CBUF_SPLIT = 6 * CTA + 6 * CTB;    // bf16: a_r, a_i planes (CTA each) | P, Q planes (CTB each)
 constexpr int CBUF_PRE = 9 * CTA;                // bf16: a_r, a_i, a_s planes
@@ -75,8 +83,13 @@ struct CGate {
   int64_t ldp;
 };
 
+// Output columns per tile, 32-row blocks per wave and workgroups per CU of each path.
+constexpr int cbn_of(int path) { return path == CPATH_SPLIT3_PRE ? CBN_PRE : CBN; }
+constexpr int rb_of(int path) { return path == CPATH_SPLIT3_PRE ? 4 : 2; }
+constexpr int wg_per_cu(int path) { return path == CPATH_FP32 ? 3 : path == CPATH_SPLIT3_PRE ? 1 : 2; }
+
 template <int MODE, int PATH, bool KTAIL = false>
-__global__ __launch_bounds__(256, PATH == CPATH_FP32 ? 3 : 2) void complex_linear_kernel(
+__global__ __launch_bounds__(256, wg_per_cu(PATH)) void complex_linear_kernel(
     const float* __restrict__ Ar, const float* __restrict__ Ai, int64_t lda, const float* __restrict__ P,
     const float* __restrict__ Q, int64_t ldw, const uint4* __restrict__ W3, float* __restrict__ Yr,
     float* __restrict__ Yi, int64_t ldy, int64_t M, int32_t Nc, int32_t Kc, int32_t n_tiles, int64_t total_tiles,
@@ -88,18 +101,20 @@ __global__ __launch_bounds__(256, PATH == CPATH_FP32 ? 3 : 2) void complex_linea
   if ((total_tiles & 7) == 0) wg = (wg & 7) * (total_tiles >> 3) + (wg >> 3);
   const int64_t m_tile = wg / n_tiles;
   const int n_tile = (int)(wg - m_tile * n_tiles);
+  constexpr int RB = rb_of(PATH);
   const int64_t row0 = m_tile * CBM;
-  const int col0 = n_tile * CBN;
+  const int col0 = n_tile * cbn_of(PATH);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wr = (wave >> 1) * 64, wc = (wave & 1) * 32;
+  // wave tile: RB 32-row blocks x one 32-column block
+  const int wr = RB == 4 ? 0 : (wave >> 1) * 64, wc = RB == 4 ? wave * 32 : (wave & 1) * 32;
 
   // four-product split: T[0] = out_r, T[1] = out_i; otherwise T1, T2, T3 of the three products
   constexpr int NT = PATH == CPATH_SPLIT4 ? 2 : 3;
-  floatx16 T[NT][2];
+  floatx16 T[NT][RB];
 #pragma unroll
   for (int p = 0; p < NT; ++p)
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < RB; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) T[p][i][r] = 0.0f;
 
@@ -161,7 +176,7 @@ __global__ __launch_bounds__(256, PATH == CPATH_FP32 ? 3 : 2) void complex_linea
       load_b(kc + 1 < nkc ? kc + 1 : nkc - 1, bn);
       const __bf16* b = sp + (kc & 1) * CBUF_PRE;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < RB; ++i) {
         const int off = plane_off(wr + 32 * i + fr, fh);
         bf16x8 af[9];  // a_r, a_i, a_s planes
 #pragma unroll
@@ -354,7 +369,7 @@ __global__ __launch_bounds__(256, PATH == CPATH_FP32 ? 3 : 2) void complex_linea
                 "epilogue staging must fit in the operand buffers");
   float* ws = smem + wave * 32 * CES;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < RB; ++i) {
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -417,7 +432,7 @@ static int complex_check(const float* A_r, const float* A_i, int64_t lda, const 
   if (!A_r || !A_i || !P || !Q || !Y_r || !Y_i) return set_error(FU_ERR_NULL, "%s: NULL operand", who);
   if (!aligned16(A_r) || !aligned16(A_i) || !aligned16(P) || !aligned16(Q) || !aligned16(Y_r) || !aligned16(Y_i))
     return set_error(FU_ERR_ALIGN, "%s: operands must be 16-byte aligned", who);
-  const int64_t total = ((M + CBM - 1) / CBM) * ((Nc + CBN - 1) / CBN);
+  const int64_t total = ((M + CBM - 1) / CBM) * ((Nc + CBN - 1) / CBN);   // the larger tile count
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
   return FU_OK;
 }
@@ -440,10 +455,13 @@ static int complex_launch(const float* A_r, const float* A_i, int64_t lda, const
                           const void* W3, float* Y_r, float* Y_i, int64_t ldy, int64_t M, int32_t Nc, int32_t Kc,
                           CGate g, void* stream, const char* who) {
   if (W3 && !aligned16(W3)) return set_error(FU_ERR_ALIGN, "%s: W3 must be 16-byte aligned", who);
-  const int n_tiles = (Nc + CBN - 1) / CBN;
+  const bool fp32 = matmul_mode() == FU_MATMUL_FP32;
+  const int path = fp32 ? CPATH_FP32 : W3 ? CPATH_SPLIT3_PRE : CPATH_SPLIT4;
+  const int tile_n = path == CPATH_SPLIT3_PRE ? CBN_PRE : CBN;
+  const int n_tiles = (Nc + tile_n - 1) / tile_n;
   const int64_t total = ((M + CBM - 1) / CBM) * n_tiles;
   const bool tail = Kc % 16 != 0;
-  auto kern = matmul_mode() == FU_MATMUL_FP32 ? complex_linear_kernel<MODE, CPATH_FP32>
+  auto kern = fp32 ? complex_linear_kernel<MODE, CPATH_FP32>
               : W3 ? (tail ? complex_linear_kernel<MODE, CPATH_SPLIT3_PRE, true>
                            : complex_linear_kernel<MODE, CPATH_SPLIT3_PRE, false>)
                    : (tail ? complex_linear_kernel<MODE, CPATH_SPLIT4, true>
