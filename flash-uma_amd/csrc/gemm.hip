@@ -31,6 +31,12 @@ constexpr int G_LDS_FLOATS = 2 * (GBM + GBN) * GLDS > 4 * 32 * GES ? 2 * (GBM + 
 constexpr int G_PLANE = GBM * GBK;                       // bf16 per split plane of one tile
 constexpr int G_LDS_FLOATS_SPLIT = 2 * 6 * G_PLANE / 2;  // [buf][A planes | W planes], 48 KB
 static_assert(GBM == GBN, "the split planes of A and W tiles share one layout");
+// Tall split tiles (TALL): 256 rows x 128 columns, each wave 128 x 64 (4 x 2 blocks of 32):
+// per 16-wide K chunk a wave issues 48 MFMAs for 12 A and 6 W fragment reads, and a
+// workgroup stages 256 + 128 rows.  A planes of 256 rows, W planes of 128 rows, 72 KB
+// double-buffered (two workgroups per CU).
+constexpr int G_PLANE_A_TALL = 2 * GBM * GBK;
+constexpr int G_LDS_FLOATS_TALL = 2 * 3 * (G_PLANE_A_TALL + G_PLANE) / 2;
 static_assert(4 * 32 * GES <= G_LDS_FLOATS_SPLIT, "epilogue staging must fit in the split planes");
 
 // Float offset of 16-byte chunk `chunk` of LDS operand row `row`.
@@ -82,7 +88,7 @@ struct Resid {
 // wave's 64 staged columns are a gate and its values; the epilogue writes Y (kept for the
 // backward), Z and S.  MODE 2 (gate backward): see GateBwd; Y receives g_Y_m0 ((2L+1)C
 // columns).
-template <int MODE, bool SPLIT, bool KTAIL = false>
+template <int MODE, bool SPLIT, bool KTAIL = false, bool TALL = false>
 __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const float* __restrict__ A, int64_t lda, int64_t sA,
                                                           const float* __restrict__ W, int64_t ldw, int64_t sW,
                                                           const float* __restrict__ bias, int64_t sBias,
@@ -98,7 +104,11 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
     bias = (bias != nullptr && bt < bias_batches) ? bias + bt * sBias : nullptr;
     if (rs.R) rs.R += bt * rs.sR;
   }
-  __shared__ __attribute__((aligned(16))) float smem[SPLIT ? G_LDS_FLOATS_SPLIT : G_LDS_FLOATS];
+  static_assert(SPLIT || !TALL, "tall tiles exist in the split mode only");
+  constexpr int RB = TALL ? 4 : 2;          // 32-row blocks per wave
+  constexpr int BM = 64 * RB;               // tile rows
+  constexpr int PA = BM * GBK, PW = G_PLANE;  // bf16 per A plane, per W plane
+  __shared__ __attribute__((aligned(16))) float smem[TALL ? G_LDS_FLOATS_TALL : SPLIT ? G_LDS_FLOATS_SPLIT : G_LDS_FLOATS];
 
   // XCD-aware tile order: hardware deals consecutive workgroups round-robin over the 8 XCDs;
   // remap so that each XCD walks a contiguous range of tiles (the column tiles of one A
@@ -107,18 +117,18 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
   if ((total_tiles & 7) == 0) wg = (wg & 7) * (total_tiles >> 3) + (wg >> 3);
   const int64_t m_tile = wg / n_tiles;
   const int n_tile = (int)(wg - m_tile * n_tiles);
-  const int64_t row0 = m_tile * GBM;
+  const int64_t row0 = m_tile * BM;
   const int col0 = n_tile * GBN;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wr = (wave >> 1) * 64;  // wave's row offset inside the tile
-  const int wc = (wave & 1) * 64;   // wave's col offset inside the tile
+  const int wr = (wave >> 1) * 32 * RB;  // wave's row offset inside the tile
+  const int wc = (wave & 1) * 64;        // wave's col offset inside the tile
 
-  floatx16 acc[2][2];
+  floatx16 acc[RB][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < RB; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -126,11 +136,11 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
   const int fr = lane & 31;  // operand row (A) / column (W) within a 32-block
   const int fh = lane >> 5;  // this lane feeds chunk columns 8 fh .. 8 fh + 7
   if constexpr (SPLIT) {
-    __bf16* sp = reinterpret_cast<__bf16*>(smem);  // [buf][A hi, mid, lo | W hi, mid, lo][G_PLANE]
-    const int sr = tid >> 1, sh = tid & 1;         // staging: tile row sr, k 8 sh .. 8 sh + 7
+    __bf16* sp = reinterpret_cast<__bf16*>(smem);  // [buf][A hi, mid, lo (PA) | W hi, mid, lo (PW)]
+    const int sr = tid >> 1, sh = tid & 1;         // staging: tile row sr (+128 if TALL), k 8 sh ..
     const int soff = plane_off(sr, sh);
     const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 ga[2], gw[2];
+    float4 ga[2], gw[2], ga2[2];
     // A thread stages the same tile row (of A and of W) for the whole K loop, so its row
     // pointers are fixed: a row past M (N) reads row M-1 (N-1) instead, whose products land in
     // output rows (columns) that are never stored.  Without a K tail (KTAIL false: K a multiple
@@ -139,14 +149,19 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
     // loads would be scalarised into dword loads).  The loader has no branch either way:
     // an if/else here, selecting between the two forms per chunk, was miscompiled in the
     // pre-split complex kernel (a prefetched operand register reused before its read).
-    const int64_t gr = row0 + sr;
+    const int64_t gr = row0 + sr, gr2 = row0 + 128 + sr;
     const int gn = col0 + sr;
     const float* pa = A + (gr < M ? gr : M - 1) * lda + 8 * sh;
+    const float* pa2 = A + (gr2 < M ? gr2 : M - 1) * lda + 8 * sh;   // second staged row (TALL)
     const float* pw = W + (int64_t)(gn < N ? gn : N - 1) * ldw + 8 * sh;
     auto load_chunk = [&](int k0) {
       if constexpr (!KTAIL) {
         ga[0] = ld4(pa + k0);
         ga[1] = ld4(pa + k0 + 4);
+        if constexpr (TALL) {
+          ga2[0] = ld4(pa2 + k0);
+          ga2[1] = ld4(pa2 + k0 + 4);
+        }
         gw[0] = ld4(pw + k0);
         gw[1] = ld4(pw + k0 + 4);
       } else {
@@ -158,15 +173,24 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
         ga[1] = k1ok ? va1 : z4;
         gw[0] = k0ok ? vw0 : z4;
         gw[1] = k1ok ? vw1 : z4;
+        if constexpr (TALL) {
+          const float4 vb0 = ld4(k0ok ? pa2 + k0 : A), vb1 = ld4(k1ok ? pa2 + k0 + 4 : A);
+          ga2[0] = k0ok ? vb0 : z4;
+          ga2[1] = k1ok ? vb1 : z4;
+        }
       }
     };
     auto store_chunk = [&](int buf) {
-      __bf16* b = sp + buf * 6 * G_PLANE;
+      __bf16* b = sp + buf * 3 * (PA + PW);
       uint4 h, m, l;
       split3(ga[0], ga[1], h, m, l);
-      st_planes(b, G_PLANE, soff, h, m, l);
+      st_planes(b, PA, soff, h, m, l);
+      if constexpr (TALL) {
+        split3(ga2[0], ga2[1], h, m, l);
+        st_planes(b, PA, plane_off(128 + sr, sh), h, m, l);
+      }
       split3(gw[0], gw[1], h, m, l);
-      st_planes(b + 3 * G_PLANE, G_PLANE, soff, h, m, l);
+      st_planes(b + 3 * PA, PW, soff, h, m, l);
     };
     const int nk = (K + GBK - 1) / GBK;
     load_chunk(0);
@@ -174,14 +198,14 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
     load_chunk((nk > 1 ? 1 : 0) * GBK);
     __syncthreads();
     for (int kc = 0; kc < nk; ++kc) {
-      const __bf16* b = sp + (kc & 1) * 6 * G_PLANE;
+      const __bf16* b = sp + (kc & 1) * 3 * (PA + PW);
       bf16x8 bq[2][3];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) ld_planes(b + 3 * G_PLANE, G_PLANE, plane_off(wc + 32 * j + fr, fh), bq[j]);
+      for (int j = 0; j < 2; ++j) ld_planes(b + 3 * PA, PW, plane_off(wc + 32 * j + fr, fh), bq[j]);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < RB; ++i) {
         bf16x8 aq[3];
-        ld_planes(b, G_PLANE, plane_off(wr + 32 * i + fr, fh), aq);
+        ld_planes(b, PA, plane_off(wr + 32 * i + fr, fh), aq);
 #pragma unroll
         for (int q = 0; q < 6; ++q)
 #pragma unroll
@@ -264,7 +288,7 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
     const int C = gb.C, n1 = C / 32, L = gb.L;
     float* ws = smem + wave * 32 * GES;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < RB; ++i) {
       __syncthreads();
 #pragma unroll
       for (int j = 0; j < 2; ++j)
@@ -322,7 +346,7 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
     const bool live = q0 < N;
     float* ws = smem + wave * 32 * GES;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < RB; ++i) {
       __syncthreads();
 #pragma unroll
       for (int j = 0; j < 2; ++j)
@@ -365,7 +389,7 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
   // stores.
   float* ws = smem + wave * 32 * GES;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < RB; ++i) {
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -395,12 +419,22 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
 
 using namespace fu;
 
+// Rows from which the split mode uses tall (256-row) tiles: below it the 128-row tiles keep
+// more workgroups in flight than the CU count (the node GEMMs have 8,192 rows).
+constexpr int64_t TALL_MIN_ROWS = 65536;
+
+// Rows per tile of the kernel linear_kernel picks.
+static int64_t linear_tile_rows(int64_t M) {
+  return (matmul_mode() != FU_MATMUL_FP32 && M >= TALL_MIN_ROWS) ? 2 * GBM : GBM;
+}
+
 // The kernel for MODE in the current matrix-core mode; KTAIL instances handle K % 16 != 0.
 template <int MODE>
-static auto linear_kernel(int32_t K) {
+static auto linear_kernel(int32_t K, int64_t M) {
+  const bool tall = linear_tile_rows(M) != GBM;
   return matmul_mode() == FU_MATMUL_FP32 ? linear_mfma_kernel<MODE, false>
-         : (K % GBK != 0)               ? linear_mfma_kernel<MODE, true, true>
-                                          : linear_mfma_kernel<MODE, true, false>;
+         : (K % GBK != 0) ? (tall ? linear_mfma_kernel<MODE, true, true, true> : linear_mfma_kernel<MODE, true, true>)
+                          : (tall ? linear_mfma_kernel<MODE, true, false, true> : linear_mfma_kernel<MODE, true, false>);
 }
 
 static int linear_check(const float* A, int64_t lda, const float* W, int64_t ldw, const float* Y, int64_t ldy,
@@ -425,10 +459,11 @@ static int linear_launch(const float* A, int64_t lda, int64_t sA, const float* W
                          int64_t M, int32_t N, int32_t K, int32_t batch, hipStream_t stream, const char* who,
                          Resid rs = Resid{}) {
   const int n_tiles = (N + GBN - 1) / GBN;
-  const int64_t m_tiles = (M + GBM - 1) / GBM;
+  const int64_t bm = linear_tile_rows(M);
+  const int64_t m_tiles = (M + bm - 1) / bm;
   const int64_t total = m_tiles * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
-  auto kern = linear_kernel<0>(K);
+  auto kern = linear_kernel<0>(K, M);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, (unsigned)batch), dim3(256), 0, stream, A, lda, sA, W, ldw, sW, bias,
                      sBias, bias_batches, Y, ldy, sY, M, N, K, n_tiles, total, GateOut{}, GateBwd{}, rs);
   return check_launch(who);
@@ -474,9 +509,10 @@ extern "C" int fu_linear_gate(const float* A, int64_t lda, const float* W, int64
   if (ldz % 4 != 0 || !aligned16(Z) || (S && (lds % 4 != 0 || !aligned16(S))) || (bias && !aligned16(bias)))
     return set_error(FU_ERR_ALIGN, "%s: Z, S and bias must be 16-byte aligned with row strides multiples of 4", who);
   const int n_tiles = (N + GBN - 1) / GBN;
-  const int64_t total = ((M + GBM - 1) / GBM) * n_tiles;
+  const int64_t bm = linear_tile_rows(M);
+  const int64_t total = ((M + bm - 1) / bm) * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
-  auto kern = linear_kernel<1>(K);
+  auto kern = linear_kernel<1>(K, M);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), A, lda,
                      (int64_t)0, W, ldw, (int64_t)0, bias, (int64_t)0, 1, Y, ldy, (int64_t)0, M, N, K, n_tiles, total,
                      GateOut{Z, ldz, S, lds, C, lmax}, GateBwd{}, Resid{});
@@ -501,9 +537,10 @@ extern "C" int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* W
   if ((ldy0 | ldp1 | ldp2) % 4 != 0 || !aligned16(Y0) || !aligned16(P1) || !aligned16(P2))
     return set_error(FU_ERR_ALIGN, "%s: operands must be 16-byte aligned with row strides multiples of 4", who);
   const int n_tiles = (N + GBN - 1) / GBN;
-  const int64_t total = ((M + GBM - 1) / GBM) * n_tiles;
+  const int64_t bm = linear_tile_rows(M);
+  const int64_t total = ((M + bm - 1) / bm) * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
-  auto kern = linear_kernel<2>(K);
+  auto kern = linear_kernel<2>(K, M);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), gZo, ldgz,
                      (int64_t)0, Wt, ldw, (int64_t)0, (const float*)nullptr, (int64_t)0, 1, gY0, ldg, (int64_t)0, M, N,
                      K, n_tiles, total, GateOut{}, GateBwd{Y0, ldy0, P1, ldp1, P2, ldp2, C, lmax}, Resid{});
