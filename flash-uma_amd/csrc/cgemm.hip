@@ -368,6 +368,31 @@ __global__ __launch_bounds__(256, wg_per_cu(PATH)) void complex_linear_kernel(
   static_assert(4 * 32 * CES <= C_LDS_FLOATS && 4 * 32 * CES <= C_LDS_FLOATS_SPLIT,
                 "epilogue staging must fit in the operand buffers");
   float* ws = smem + wave * 32 * CES;
+  // The gate epilogues' global operands (the gate column; for MODE 2 also F_r and F_i) of a
+  // lane's four 16-byte pieces of a 32-row block are loaded one block ahead, into alternating
+  // register sets, so their latency overlaps the staging of the block before (with one
+  // workgroup per CU nothing else would hide it): 1.04-1.33x on the gate shapes of the model.
+  // A piece past M or Nc loads from row M - 1 / column 0 and is not stored.
+  float4 eg[2][4], efr[2][4], efi[2][4];
+  auto load_gate_operands = [&](int i, int set) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int lin = lane + 64 * q;
+      int64_t row = row0 + wr + i * 32 + (lin >> 3);
+      row = row < M ? row : M - 1;
+      int gc = col0 + wc + (lin & 7) * 4;
+      gc = gc < Nc ? gc : 0;
+      const int t = g.s_off + gc, l1 = t / g.C, ch = t - l1 * g.C;
+      eg[set][q] = ld4(g.G + row * g.ldg + 64 * (l1 * (g.C >> 5) + (ch >> 5)) + (ch & 31));
+      if constexpr (MODE == 2) {
+        efr[set][q] = ld4(g.Fr + row * g.ldf + gc);
+        efi[set][q] = ld4(g.Fi + row * g.ldf + gc);
+      }
+    }
+  };
+  // (the fp32 path, three workgroups per CU, loads them after the staging instead: a set
+  // ahead would spill)
+  if constexpr (MODE != 0 && PATH != CPATH_FP32) load_gate_operands(0, 0);
 #pragma unroll
   for (int i = 0; i < RB; ++i) {
     __syncthreads();
@@ -384,6 +409,10 @@ __global__ __launch_bounds__(256, wg_per_cu(PATH)) void complex_linear_kernel(
       }
     }
     __syncthreads();
+    if constexpr (MODE != 0) {
+      if constexpr (PATH == CPATH_FP32) load_gate_operands(i, i & 1);
+      else if (i + 1 < RB) load_gate_operands(i + 1, (i + 1) & 1);
+    }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int lin = lane + 64 * q;
@@ -395,14 +424,13 @@ __global__ __launch_bounds__(256, wg_per_cu(PATH)) void complex_linear_kernel(
       const float4 yr = ld4(&ws[r * CES + c]), yi = ld4(&ws[r * CES + 32 + c]);
       float4 sg;
       if constexpr (MODE != 0) {
-        const int t = g.s_off + gc, l1 = t / g.C, ch = t - l1 * g.C;
-        const float4 gp = ld4(g.G + row * g.ldg + 64 * (l1 * (g.C >> 5) + (ch >> 5)) + (ch & 31));
+        const float4 gp = eg[i & 1][q];
         sg = make_float4(sigmoidf_(gp.x), sigmoidf_(gp.y), sigmoidf_(gp.z), sigmoidf_(gp.w));
       }
       if constexpr (MODE == 2) {
         st4(Yr + row * ldy + gc, yr * sg);
         st4(Yi + row * ldy + gc, yi * sg);
-        st4(g.Pout + row * g.ldp + gc, yr * ld4(g.Fr + row * g.ldf + gc) + yi * ld4(g.Fi + row * g.ldf + gc));
+        st4(g.Pout + row * g.ldp + gc, yr * efr[i & 1][q] + yi * efi[i & 1][q]);
         continue;
       }
       st4(Yr + row * ldy + gc, yr);
