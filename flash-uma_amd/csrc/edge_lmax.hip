@@ -140,21 +140,22 @@ __global__ __launch_bounds__(256) void gather_fwd_lmax_kernel(
 // ---------------------------------------------------------------------------------------
 
 // reduce n <= 64 per-lane partial sums over the wave and store lane k's total to out[k]
+// (added to out[k] when accumulating)
 template <int n>
-__device__ __forceinline__ void reduce_store(float (&part)[n], float* out, int lane) {
+__device__ __forceinline__ void reduce_store(float (&part)[n], float* out, int lane, bool accumulate) {
   constexpr int V = n <= 16 ? 16 : n <= 32 ? 32 : 64;
   float p[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) p[k] = k < n ? part[k] : 0.0f;
   const float tot = wave_multi_sum<V>(p, lane);
-  if (lane < n) out[lane] = tot;
+  if (lane < n) out[lane] = accumulate ? out[lane] + tot : tot;
 }
 
 template <int L, int CPL, int l>
 __device__ __forceinline__ void gather_bwd_block(const float* sv, const float* wl, const float* we,
                                                  const float* gX0e, const float* gX1e, const float* gX2e,
                                                  const float* rade, float* grade, Vec<CPL> (&acc)[ncoef(L)],
-                                                 float* gw_l, int so, int c, int lane) {
+                                                 float* gw_l, int so, int c, int lane, bool accw) {
   constexpr int C = 64 * CPL;
   constexpr int nk = 2 * l + 1, mm = mmx(l), nr = 2 * mm + 1;
   Vec<CPL> v[nk];
@@ -195,7 +196,7 @@ __device__ __forceinline__ void gather_bwd_block(const float* sv, const float* w
 #pragma unroll
     for (int mp = 0; mp < nk; ++mp) part[m * nk + mp] = vdot(grv[m], v[mp]);
   static_assert(nr * nk <= 64, "one multi-value reduction per degree");
-  reduce_store<nr * nk>(part, gw_l, lane);
+  reduce_store<nr * nk>(part, gw_l, lane, accw);
 }
 
 template <int CPL, int L>
@@ -205,7 +206,7 @@ __device__ __forceinline__ void gather_bwd_segment(const float* __restrict__ gX0
                                                    const int32_t* __restrict__ ptr, const int32_t* __restrict__ idx,
                                                    int64_t n, int so, const float* sv, Vec<CPL> (&acc)[ncoef(L)],
                                                    float* __restrict__ g_rad, float* __restrict__ gw,
-                                                   float* __restrict__ gext, int c, int lane) {
+                                                   float* __restrict__ gext, int c, int lane, bool accw) {
   constexpr int C = 64 * CPL, EW = extw(L);
   const int32_t k0 = ptr[n], k1 = ptr[n + 1];
   for (int32_t k = k0; k < k1; ++k) {
@@ -224,12 +225,13 @@ __device__ __forceinline__ void gather_bwd_segment(const float* __restrict__ gX0
 #pragma unroll
       for (int q = 0; q < CPL; ++q) acc[0][q] += g[q] * r[q];
     }
-    gather_bwd_block<L, CPL, 1>(sv, wl, we, gX0e, gX1e, gX2e, rade, grade, acc, gw + e * 34, so, c, lane);
-    gather_bwd_block<L, CPL, 2>(sv, wl, we, gX0e, gX1e, gX2e, rade, grade, acc, gw + e * 34 + 9, so, c, lane);
+    gather_bwd_block<L, CPL, 1>(sv, wl, we, gX0e, gX1e, gX2e, rade, grade, acc, gw + e * 34, so, c, lane, accw);
+    gather_bwd_block<L, CPL, 2>(sv, wl, we, gX0e, gX1e, gX2e, rade, grade, acc, gw + e * 34 + 9, so, c, lane, accw);
     if constexpr (L >= 3)
-      gather_bwd_block<L, CPL, 3>(sv, wl, we, gX0e, gX1e, gX2e, rade, grade, acc, gext + e * EW, so, c, lane);
+      gather_bwd_block<L, CPL, 3>(sv, wl, we, gX0e, gX1e, gX2e, rade, grade, acc, gext + e * EW, so, c, lane, accw);
     if constexpr (L >= 4)
-      gather_bwd_block<L, CPL, 4>(sv, wl, we, gX0e, gX1e, gX2e, rade, grade, acc, gext + e * EW + 35, so, c, lane);
+      gather_bwd_block<L, CPL, 4>(sv, wl, we, gX0e, gX1e, gX2e, rade, grade, acc, gext + e * EW + 35, so, c, lane,
+                                  accw);
   }
 }
 
@@ -244,7 +246,7 @@ __global__ __launch_bounds__(128) void gather_bwd_lmax_kernel(
     const int32_t* __restrict__ rptr, const int32_t* __restrict__ ridx, const int32_t* __restrict__ sptr,
     const int32_t* __restrict__ sidx, float* __restrict__ g_x, float* __restrict__ gw_recv,
     float* __restrict__ gext_recv, float* __restrict__ gw_send, float* __restrict__ gext_send,
-    float* __restrict__ g_rad, int64_t N) {
+    float* __restrict__ g_rad, int64_t N, int32_t acc_flags) {
   constexpr int C = 64 * CPL, K = ncoef(L);
   __shared__ __attribute__((aligned(16))) float s_v[2][K * C];
   __shared__ __attribute__((aligned(16))) float s_send[K * C];
@@ -264,11 +266,14 @@ __global__ __launch_bounds__(128) void gather_bwd_lmax_kernel(
     vstore(sv + k * C + c, r);
   }
   if (wave == 0) {
+    // the receiver half goes into the caller's g_wigner / g_wig_ext (added to their contents
+    // when accumulating: only this wave writes an edge's entries there), the sender half into
+    // the workspace, added afterwards
     gather_bwd_segment<CPL, L>(gX0, gX1, gX2, wig, ext, rad, rptr, ridx, n, 1, sv, acc, g_rad, gw_recv, gext_recv, c,
-                               lane);
+                               lane, (acc_flags & 1) != 0);
   } else {
     gather_bwd_segment<CPL, L>(gX0, gX1, gX2, wig, ext, rad, sptr, sidx, n, 0, sv, acc, g_rad, gw_send, gext_send, c,
-                               lane);
+                               lane, false);
 #pragma unroll
     for (int k = 0; k < K; ++k) vstore(&s_send[k * C + c], acc[k]);
   }
@@ -358,7 +363,7 @@ __global__ __launch_bounds__(256) void scatter_fwd_lmax_kernel(
 template <int L, int CPL, int l>
 __device__ __forceinline__ float scatter_bwd_block(const float* wl, const float* we, float en, const float* gn,
                                                    const float* Z0e, const float* Z1e, const float* Z2e, float* gZ0e,
-                                                   float* gZ1e, float* gZ2e, float* gw_l, int lane) {
+                                                   float* gZ1e, float* gZ2e, float* gw_l, int lane, bool accw) {
   constexpr int C = 64 * CPL;
   constexpr int nk = 2 * l + 1, mm = mmx(l), nr = 2 * mm + 1;
   Vec<CPL> g[nk], z[nr];
@@ -388,7 +393,7 @@ __device__ __forceinline__ float scatter_bwd_block(const float* wl, const float*
   for (int m = 0; m < nr; ++m)
 #pragma unroll
     for (int mp = 0; mp < nk; ++mp) part[m * nk + mp] = vdot(z[m], g[mp]) * en;
-  reduce_store<nr * nk>(part, gw_l, lane);
+  reduce_store<nr * nk>(part, gw_l, lane, accw);
   return ge;
 }
 
@@ -398,8 +403,9 @@ __global__ __launch_bounds__(256) void scatter_bwd_lmax_kernel(
     const float* __restrict__ Z1, const float* __restrict__ Z2, const float* __restrict__ wig,
     const float* __restrict__ ext, const float* __restrict__ env, float* __restrict__ gZ0, float* __restrict__ gZ1,
     float* __restrict__ gZ2, float* __restrict__ g_wig, float* __restrict__ g_ext, float* __restrict__ g_env,
-    int64_t E) {
+    int64_t E, int32_t acc) {
   constexpr int C = 64 * CPL, K = ncoef(L), EW = extw(L);
+  const bool accw = (acc & 1) != 0, acce = (acc & 2) != 0;
   const int lane = threadIdx.x & 63;
   const int c = lane * CPL;
   int64_t e0, e1;
@@ -418,14 +424,16 @@ __global__ __launch_bounds__(256) void scatter_bwd_lmax_kernel(
     const Vec<CPL> g0 = vload<CPL>(gn), z0 = vload<CPL>(Z0e);
     vstore(gZ0e, vscale(g0, en));
     float ge = vdot(g0, z0);
-    ge += scatter_bwd_block<L, CPL, 1>(wl, we, en, gn, Z0e, Z1e, Z2e, gZ0e, gZ1e, gZ2e, g_wig + e * 34, lane);
-    ge += scatter_bwd_block<L, CPL, 2>(wl, we, en, gn, Z0e, Z1e, Z2e, gZ0e, gZ1e, gZ2e, g_wig + e * 34 + 9, lane);
+    ge += scatter_bwd_block<L, CPL, 1>(wl, we, en, gn, Z0e, Z1e, Z2e, gZ0e, gZ1e, gZ2e, g_wig + e * 34, lane, accw);
+    ge += scatter_bwd_block<L, CPL, 2>(wl, we, en, gn, Z0e, Z1e, Z2e, gZ0e, gZ1e, gZ2e, g_wig + e * 34 + 9, lane,
+                                       accw);
     if constexpr (L >= 3)
-      ge += scatter_bwd_block<L, CPL, 3>(wl, we, en, gn, Z0e, Z1e, Z2e, gZ0e, gZ1e, gZ2e, g_ext + e * EW, lane);
+      ge += scatter_bwd_block<L, CPL, 3>(wl, we, en, gn, Z0e, Z1e, Z2e, gZ0e, gZ1e, gZ2e, g_ext + e * EW, lane, accw);
     if constexpr (L >= 4)
-      ge += scatter_bwd_block<L, CPL, 4>(wl, we, en, gn, Z0e, Z1e, Z2e, gZ0e, gZ1e, gZ2e, g_ext + e * EW + 35, lane);
+      ge += scatter_bwd_block<L, CPL, 4>(wl, we, en, gn, Z0e, Z1e, Z2e, gZ0e, gZ1e, gZ2e, g_ext + e * EW + 35, lane,
+                                         accw);
     ge = wave_sum(ge);
-    if (lane == 0) g_env[e] = ge;
+    if (lane == 0) g_env[e] = acce ? g_env[e] + ge : ge;
   }
 }
 
@@ -519,8 +527,9 @@ __global__ __launch_bounds__(256) void init_scatter_bwd_lmax_kernel(
     const float* __restrict__ g_out, const int64_t* __restrict__ idx_j, const float* __restrict__ rad,
     const float* __restrict__ wig, const float* __restrict__ ext, const float* __restrict__ env,
     float* __restrict__ g_rad, float* __restrict__ g_wig, float* __restrict__ g_ext, float* __restrict__ g_env,
-    int64_t E) {
+    int64_t E, int32_t acc) {
   constexpr int C = 64 * CPL, K = ncoef(L), EW = extw(L);
+  const bool accw = (acc & 1) != 0, acce = (acc & 2) != 0;
   // m = 0 row partials of degrees 1..L, then the g_env partial: 3 + 5 + 7 + 9 + 1 <= 32
   constexpr int NP = (L + 1) * (L + 1) - 1 + 1;
   const int lane = threadIdx.x & 63;
@@ -558,13 +567,14 @@ __global__ __launch_bounds__(256) void init_scatter_bwd_lmax_kernel(
       const float v = __shfl(tot, src, 64) * en;
       if (lane < nk) {
         const int w = widx(l, 0, lane - l);
-        if (l <= 2) gw[w] = v;
-        else gx[w] = v;
+        float* o = l <= 2 ? gw + w : gx + w;
+        *o = accw ? *o + v : v;
       }
     }
     const float get = __shfl(tot, NP - 1, 64);
-    if (lane == 0) g_env[e] = get;
-    // entries the forward does not read are zero
+    if (lane == 0) g_env[e] = acce ? g_env[e] + get : get;
+    // entries the forward does not read are zero (left as they are when accumulating)
+    if (accw) continue;
     for (int k = lane; k < 34; k += 64) {
       const bool row0 = (k >= 3 && k < 6) || (k >= 19 && k < 24);
       if (!row0) gw[k] = 0.0f;
@@ -751,8 +761,10 @@ extern "C" int fu_gather_bwd_lmax(const float* g_X_m0, const float* g_X_m1, cons
                                   const int64_t* batch, const int32_t* recv_ptr, const int32_t* recv_idx,
                                   const int32_t* send_ptr, const int32_t* send_idx, float* g_x, float* g_wigner,
                                   float* g_wig_ext, float* g_rad, float* ws, int64_t E, int64_t N, int64_t S,
-                                  int32_t C, int32_t lmax, void* stream) {
+                                  int32_t C, int32_t lmax, int32_t accumulate, void* stream) {
   if (E < 0 || N < 0 || S < 1) return set_error(FU_ERR_SHAPE, "fu_gather_bwd_lmax: bad shape");
+  if (accumulate < 0 || accumulate > 3)
+    return set_error(FU_ERR_UNSUPPORTED, "fu_gather_bwd_lmax: accumulate=%d (0..3)", accumulate);
   int st = check_cl(C, lmax, "fu_gather_bwd_lmax");
   if (st != FU_OK) return st;
   if (N == 0) return FU_OK;
@@ -770,7 +782,7 @@ extern "C" int fu_gather_bwd_lmax(const float* g_X_m0, const float* g_X_m1, cons
     constexpr int P = decltype(cpl)::value, L = decltype(lv)::value;
     hipLaunchKernelGGL((gather_bwd_lmax_kernel<P, L>), dim3((unsigned)N), dim3(128), 0, s, g_X_m0, g_X_m1, g_X_m2, x,
                        wigner, wig_ext, rad, csd_emb, batch, recv_ptr, recv_idx, send_ptr, send_idx, g_x, g_wigner,
-                       g_wig_ext, ws_w, ws_x, g_rad, N);
+                       g_wig_ext, ws_w, ws_x, g_rad, N, accumulate);
   });
   st = check_launch("fu_gather_bwd_lmax");
   if (st != FU_OK || E == 0) return st;
@@ -805,8 +817,11 @@ extern "C" int fu_scatter_fwd_lmax(const int32_t* row_ptr, const int32_t* col_id
 extern "C" int fu_scatter_bwd_lmax(const float* g_out, const int64_t* idx_j, const float* Z_m0, const float* Z_m1,
                                    const float* Z_m2, const float* wigner, const float* wig_ext, const float* env,
                                    float* g_Z_m0, float* g_Z_m1, float* g_Z_m2, float* g_wigner, float* g_wig_ext,
-                                   float* g_env, int64_t E, int64_t N, int32_t C, int32_t lmax, void* stream) {
+                                   float* g_env, int64_t E, int64_t N, int32_t C, int32_t lmax, int32_t accumulate,
+                                   void* stream) {
   if (N < 0 || E < 0) return set_error(FU_ERR_SHAPE, "fu_scatter_bwd_lmax: bad shape");
+  if (accumulate < 0 || accumulate > 3)
+    return set_error(FU_ERR_UNSUPPORTED, "fu_scatter_bwd_lmax: accumulate=%d (0..3)", accumulate);
   int st = check_cl(C, lmax, "fu_scatter_bwd_lmax");
   if (st != FU_OK) return st;
   if (E == 0) return FU_OK;
@@ -818,7 +833,7 @@ extern "C" int fu_scatter_bwd_lmax(const float* g_out, const int64_t* idx_j, con
     constexpr int P = decltype(cpl)::value, L = decltype(lv)::value;
     hipLaunchKernelGGL((scatter_bwd_lmax_kernel<P, L>), dim3(edge_grid(E)),
                        dim3(256), 0, s, g_out, idx_j, Z_m0, Z_m1, Z_m2, wigner, wig_ext, env, g_Z_m0, g_Z_m1, g_Z_m2,
-                       g_wigner, g_wig_ext, g_env, E);
+                       g_wigner, g_wig_ext, g_env, E, accumulate);
   });
   return check_launch("fu_scatter_bwd_lmax");
 }
@@ -847,8 +862,10 @@ extern "C" int fu_init_scatter_fwd_lmax(const int32_t* row_ptr, const int32_t* c
 extern "C" int fu_init_scatter_bwd_lmax(const float* g_out, const int64_t* idx_j, const float* rad,
                                         const float* wigner, const float* wig_ext, const float* env, float* g_rad,
                                         float* g_wigner, float* g_wig_ext, float* g_env, int64_t E, int64_t N,
-                                        int32_t C, int32_t lmax, void* stream) {
+                                        int32_t C, int32_t lmax, int32_t accumulate, void* stream) {
   if (N < 0 || E < 0) return set_error(FU_ERR_SHAPE, "fu_init_scatter_bwd_lmax: bad shape");
+  if (accumulate < 0 || accumulate > 3)
+    return set_error(FU_ERR_UNSUPPORTED, "fu_init_scatter_bwd_lmax: accumulate=%d (0..3)", accumulate);
   int st = check_cl(C, lmax, "fu_init_scatter_bwd_lmax");
   if (st != FU_OK) return st;
   if (E == 0) return FU_OK;
@@ -859,7 +876,8 @@ extern "C" int fu_init_scatter_bwd_lmax(const float* g_out, const int64_t* idx_j
   with_c_lmax(C, lmax, [&](auto cpl, auto lv) {
     constexpr int P = decltype(cpl)::value, L = decltype(lv)::value;
     hipLaunchKernelGGL((init_scatter_bwd_lmax_kernel<P, L>), dim3(edge_grid(E)),
-                       dim3(256), 0, s, g_out, idx_j, rad, wigner, wig_ext, env, g_rad, g_wigner, g_wig_ext, g_env, E);
+                       dim3(256), 0, s, g_out, idx_j, rad, wigner, wig_ext, env, g_rad, g_wigner, g_wig_ext, g_env, E,
+                       accumulate);
   });
   return check_launch("fu_init_scatter_bwd_lmax");
 }

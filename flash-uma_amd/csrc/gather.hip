@@ -183,7 +183,7 @@ __device__ __forceinline__ Vec<CPL> lds_row(const float* sv, int k, int c) {
 template <int CPL, int L>
 __device__ __forceinline__ void side_apply(const SideEdge<CPL>& d, int64_t e, int so, int c, const float* sv,
                                            Rows9<CPL>& acc, float* __restrict__ g_rad, float* __restrict__ gw_out,
-                                           int lane) {
+                                           int lane, bool accw) {
   constexpr int C = 64 * CPL;
   float w[34];
 #pragma unroll
@@ -233,7 +233,7 @@ __device__ __forceinline__ void side_apply(const SideEdge<CPL>& d, int64_t e, in
 #pragma unroll
     for (int q = 24; q < 32; ++q) part[q] = 0.0f;
     const float tot = wave_multi_sum<32>(part, lane);
-    if (lane < 24) gw_out[e * 34 + lane] = tot;
+    if (lane < 24) gw_out[e * 34 + lane] = accw ? gw_out[e * 34 + lane] + tot : tot;
   }
   {
     float part[16];
@@ -246,7 +246,7 @@ __device__ __forceinline__ void side_apply(const SideEdge<CPL>& d, int64_t e, in
 #pragma unroll
     for (int q = 10; q < 16; ++q) part[q] = 0.0f;
     const float tot = wave_multi_sum<16>(part, lane);
-    if (lane < 10) gw_out[e * 34 + 24 + lane] = tot;
+    if (lane < 10) gw_out[e * 34 + 24 + lane] = accw ? gw_out[e * 34 + 24 + lane] + tot : tot;
   }
 }
 
@@ -259,7 +259,7 @@ __device__ __forceinline__ void gather_bwd_side(const float* __restrict__ gX0, c
                                                 const float* __restrict__ rad, const int32_t* __restrict__ ptr,
                                                 const int32_t* __restrict__ idx, int64_t n, int so, const float* sv,
                                                 Rows9<CPL>& acc, float* __restrict__ g_rad,
-                                                float* __restrict__ gw_out, int lane) {
+                                                float* __restrict__ gw_out, int lane, bool accw) {
   const int c = lane * CPL;
   const int32_t k0 = ptr[n], k1 = ptr[n + 1];
   for (int32_t base = k0; base < k1; base += 64) {
@@ -275,17 +275,17 @@ __device__ __forceinline__ void gather_bwd_side(const float* __restrict__ gX0, c
       const int64_t e1 = __builtin_amdgcn_readlane(ids, t + 1);
       side_load<CPL, L>(gX0, gX1, gX2, wig, rad, e1, so, c, lane, d1);
       __builtin_amdgcn_sched_barrier(0);
-      side_apply<CPL, L>(d0, e0, so, c, sv, acc, g_rad, gw_out, lane);
+      side_apply<CPL, L>(d0, e0, so, c, sv, acc, g_rad, gw_out, lane, accw);
       __builtin_amdgcn_sched_barrier(0);
       if (t + 2 < cnt) {
         e0 = __builtin_amdgcn_readlane(ids, t + 2);
         side_load<CPL, L>(gX0, gX1, gX2, wig, rad, e0, so, c, lane, d0);
       }
       __builtin_amdgcn_sched_barrier(0);
-      side_apply<CPL, L>(d1, e1, so, c, sv, acc, g_rad, gw_out, lane);
+      side_apply<CPL, L>(d1, e1, so, c, sv, acc, g_rad, gw_out, lane, accw);
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (t < cnt) side_apply<CPL, L>(d0, e0, so, c, sv, acc, g_rad, gw_out, lane);
+    if (t < cnt) side_apply<CPL, L>(d0, e0, so, c, sv, acc, g_rad, gw_out, lane, accw);
   }
 }
 
@@ -298,7 +298,7 @@ __global__ __launch_bounds__(128, 3) void gather_bwd_kernel(
     const float* __restrict__ csd, const int64_t* __restrict__ batch, const int32_t* __restrict__ rptr,
     const int32_t* __restrict__ ridx, const int32_t* __restrict__ sptr, const int32_t* __restrict__ sidx,
     float* __restrict__ g_x, float* __restrict__ g_wig, float* __restrict__ g_rad, float* __restrict__ ws,
-    int64_t N) {
+    int64_t N, int32_t acc_flags) {
   constexpr int C = 64 * CPL;
   __shared__ __attribute__((aligned(16))) float s_send[1][9 * C];
   __shared__ __attribute__((aligned(16))) float s_v[2][9 * C];
@@ -323,9 +323,12 @@ __global__ __launch_bounds__(128, 3) void gather_bwd_kernel(
       vstore(sv + k * C + c, r);
     }
     if (side == 0) {
-      gather_bwd_side<CPL, L>(gX0, gX1, gX2, wig, rad, rptr, ridx, n, 1, sv, acc, g_rad, g_wig, lane);
+      // receiver half into g_wigner (added to its contents when accumulating: only this wave
+      // writes an edge's entries there); sender half into the workspace, added afterwards
+      gather_bwd_side<CPL, L>(gX0, gX1, gX2, wig, rad, rptr, ridx, n, 1, sv, acc, g_rad, g_wig, lane,
+                              (acc_flags & 1) != 0);
     } else {
-      gather_bwd_side<CPL, L>(gX0, gX1, gX2, wig, rad, sptr, sidx, n, 0, sv, acc, g_rad, ws, lane);
+      gather_bwd_side<CPL, L>(gX0, gX1, gX2, wig, rad, sptr, sidx, n, 0, sv, acc, g_rad, ws, lane, false);
 #pragma unroll
       for (int k = 0; k < 9; ++k) vstore(&s_send[node_local][k * C + c], acc.r[k]);
     }
@@ -356,9 +359,10 @@ template <int CPL, int L>
 static void launch_gather_bwd(const float* gX0, const float* gX1, const float* gX2, const float* x,
                               const float* wigner, const float* rad, const float* csd, const int64_t* batch,
                               const int32_t* rptr, const int32_t* ridx, const int32_t* sptr, const int32_t* sidx,
-                              float* g_x, float* g_wig, float* g_rad, float* ws, int64_t N, hipStream_t st) {
+                              float* g_x, float* g_wig, float* g_rad, float* ws, int64_t N, int32_t acc,
+                              hipStream_t st) {
   hipLaunchKernelGGL((gather_bwd_kernel<CPL, L>), dim3((unsigned)N), dim3(128), 0, st, gX0, gX1, gX2, x, wigner, rad, csd,
-                     batch, rptr, ridx, sptr, sidx, g_x, g_wig, g_rad, ws, N);
+                     batch, rptr, ridx, sptr, sidx, g_x, g_wig, g_rad, ws, N, acc);
 }
 
 }  // namespace fu
@@ -411,10 +415,12 @@ extern "C" int fu_gather_bwd(const float* g_X_m0, const float* g_X_m1, const flo
                              const float* csd_emb, const int64_t* batch, const int32_t* recv_ptr,
                              const int32_t* recv_idx, const int32_t* send_ptr, const int32_t* send_idx, float* g_x,
                              float* g_wigner, float* g_rad, float* g_wig_ws, int64_t E, int64_t N, int64_t S,
-                             int32_t C, int32_t layout, void* stream) {
+                             int32_t C, int32_t layout, int32_t accumulate, void* stream) {
   (void)idx_i;
   (void)idx_j;
   if (E < 0 || N < 0 || S < 1) return set_error(FU_ERR_SHAPE, "fu_gather_bwd: bad shape");
+  if (accumulate < 0 || accumulate > 3)
+    return set_error(FU_ERR_UNSUPPORTED, "fu_gather_bwd: accumulate=%d (0..3)", accumulate);
   if (layout != 0 && layout != 1) return set_error(FU_ERR_UNSUPPORTED, "fu_gather_bwd: layout %d", layout);
   int st = check_c(C, "fu_gather_bwd");
   if (st != FU_OK) return st;
@@ -429,7 +435,7 @@ extern "C" int fu_gather_bwd(const float* g_X_m0, const float* g_X_m1, const flo
   with_c_layout(C, layout, [&](auto cpl, auto lay) {
     launch_gather_bwd<decltype(cpl)::value, decltype(lay)::value>(g_X_m0, g_X_m1, g_X_m2, x, wigner, rad, csd_emb,
                                                                   batch, recv_ptr, recv_idx, send_ptr, send_idx, g_x,
-                                                                  g_wigner, g_rad, g_wig_ws, N, s);
+                                                                  g_wigner, g_rad, g_wig_ws, N, accumulate, s);
   });
   st = check_launch("fu_gather_bwd");
   if (st != FU_OK || E == 0) return st;

@@ -118,8 +118,9 @@ __global__ __launch_bounds__(256) void scatter_bwd_kernel(const float* __restric
                                                           const float* __restrict__ env, float* __restrict__ gZ0,
                                                           float* __restrict__ gZ1, float* __restrict__ gZ2,
                                                           float* __restrict__ g_wig, float* __restrict__ g_env,
-                                                          int64_t E) {
+                                                          int64_t E, int32_t acc) {
   constexpr int C = 64 * CPL;
+  const bool accw = (acc & 1) != 0, acce = (acc & 2) != 0;
   const int lane = threadIdx.x & 63;
   const int c = lane * CPL;
   int64_t e0, e1;
@@ -188,8 +189,8 @@ __global__ __launch_bounds__(256) void scatter_bwd_kernel(const float* __restric
 #pragma unroll
     for (int q = 35; q < 64; ++q) part[q] = 0.0f;
     const float tot = wave_multi_sum<64>(part, lane);
-    if (lane < 34) g_wig[e * 34 + lane] = tot * en;
-    if (lane == 34) g_env[e] = tot;
+    if (lane < 34) g_wig[e * 34 + lane] = accw ? g_wig[e * 34 + lane] + tot * en : tot * en;
+    if (lane == 34) g_env[e] = acce ? g_env[e] + tot : tot;
   }
 }
 
@@ -254,8 +255,9 @@ __global__ __launch_bounds__(256) void init_scatter_bwd_kernel(const float* __re
                                                                const float* __restrict__ wig,
                                                                const float* __restrict__ env, float* __restrict__ g_rad,
                                                                float* __restrict__ g_wig, float* __restrict__ g_env,
-                                                               int64_t E) {
+                                                               int64_t E, int32_t acc) {
   constexpr int C = 64 * CPL;
+  const bool accw = (acc & 1) != 0, acce = (acc & 2) != 0;
   const int lane = threadIdx.x & 63;
   const int c = lane * CPL;
   int64_t e0, e1;
@@ -301,8 +303,8 @@ __global__ __launch_bounds__(256) void init_scatter_bwd_kernel(const float* __re
     const float sh = __shfl(tot, src, 64);
     const float outv = (in1 || in2) ? sh : 0.0f;
     const float ge = __shfl(tot, 8, 64);
-    if (lane < 34) g_wig[e * 34 + lane] = outv * en;
-    if (lane == 0) g_env[e] = ge;
+    if (lane < 34) g_wig[e * 34 + lane] = accw ? g_wig[e * 34 + lane] + outv * en : outv * en;
+    if (lane == 0) g_env[e] = acce ? g_env[e] + ge : ge;
   }
 }
 
@@ -317,9 +319,9 @@ static void launch_scatter_fwd(const int32_t* rptr, const int32_t* col, const fl
 template <int CPL>
 static void launch_scatter_bwd(const float* g_out, const int64_t* idx_j, const float* Z0, const float* Z1,
                                const float* Z2, const float* wig, const float* env, float* gZ0, float* gZ1, float* gZ2,
-                               float* g_wig, float* g_env, int64_t E, hipStream_t st) {
+                               float* g_wig, float* g_env, int64_t E, int32_t acc, hipStream_t st) {
   hipLaunchKernelGGL(scatter_bwd_kernel<CPL>, dim3(edge_grid(E)), dim3(256), 0, st, g_out, idx_j, Z0, Z1, Z2, wig,
-                     env, gZ0, gZ1, gZ2, g_wig, g_env, E);
+                     env, gZ0, gZ1, gZ2, g_wig, g_env, E, acc);
 }
 
 }  // namespace fu
@@ -351,8 +353,10 @@ extern "C" int fu_scatter_fwd(const int32_t* row_ptr, const int32_t* col_idx, co
 extern "C" int fu_scatter_bwd(const float* g_out, const int64_t* idx_j, const float* Z_m0, const float* Z_m1,
                               const float* Z_m2, const float* wigner, const float* env, float* g_Z_m0, float* g_Z_m1,
                               float* g_Z_m2, float* g_wigner, float* g_env, int64_t E, int64_t N, int32_t C,
-                              void* stream) {
+                              int32_t accumulate, void* stream) {
   if (N < 0 || E < 0) return set_error(FU_ERR_SHAPE, "fu_scatter_bwd: bad shape");
+  if (accumulate < 0 || accumulate > 3)
+    return set_error(FU_ERR_UNSUPPORTED, "fu_scatter_bwd: accumulate=%d (0..3)", accumulate);
   int st = check_c_s(C, "fu_scatter_bwd");
   if (st != FU_OK) return st;
   if (E == 0) return FU_OK;
@@ -361,11 +365,14 @@ extern "C" int fu_scatter_bwd(const float* g_out, const int64_t* idx_j, const fl
     return set_error(FU_ERR_NULL, "fu_scatter_bwd: NULL argument");
   hipStream_t s = as_stream(stream);
   if (C == 64)
-    launch_scatter_bwd<1>(g_out, idx_j, Z_m0, Z_m1, Z_m2, wigner, env, g_Z_m0, g_Z_m1, g_Z_m2, g_wigner, g_env, E, s);
+    launch_scatter_bwd<1>(g_out, idx_j, Z_m0, Z_m1, Z_m2, wigner, env, g_Z_m0, g_Z_m1, g_Z_m2, g_wigner, g_env, E,
+                          accumulate, s);
   else if (C == 128)
-    launch_scatter_bwd<2>(g_out, idx_j, Z_m0, Z_m1, Z_m2, wigner, env, g_Z_m0, g_Z_m1, g_Z_m2, g_wigner, g_env, E, s);
+    launch_scatter_bwd<2>(g_out, idx_j, Z_m0, Z_m1, Z_m2, wigner, env, g_Z_m0, g_Z_m1, g_Z_m2, g_wigner, g_env, E,
+                          accumulate, s);
   else
-    launch_scatter_bwd<4>(g_out, idx_j, Z_m0, Z_m1, Z_m2, wigner, env, g_Z_m0, g_Z_m1, g_Z_m2, g_wigner, g_env, E, s);
+    launch_scatter_bwd<4>(g_out, idx_j, Z_m0, Z_m1, Z_m2, wigner, env, g_Z_m0, g_Z_m1, g_Z_m2, g_wigner, g_env, E,
+                          accumulate, s);
   return check_launch("fu_scatter_bwd");
 }
 
@@ -395,8 +402,10 @@ extern "C" int fu_init_scatter_fwd(const int32_t* row_ptr, const int32_t* col_id
 
 extern "C" int fu_init_scatter_bwd(const float* g_out, const int64_t* idx_j, const float* rad, const float* wigner,
                                    const float* env, float* g_rad, float* g_wigner, float* g_env, int64_t E, int64_t N,
-                                   int32_t C, void* stream) {
+                                   int32_t C, int32_t accumulate, void* stream) {
   if (N < 0 || E < 0) return set_error(FU_ERR_SHAPE, "fu_init_scatter_bwd: bad shape");
+  if (accumulate < 0 || accumulate > 3)
+    return set_error(FU_ERR_UNSUPPORTED, "fu_init_scatter_bwd: accumulate=%d (0..3)", accumulate);
   int st = check_c_s(C, "fu_init_scatter_bwd");
   if (st != FU_OK) return st;
   if (E == 0) return FU_OK;
@@ -406,12 +415,12 @@ extern "C" int fu_init_scatter_bwd(const float* g_out, const int64_t* idx_j, con
   const dim3 grid(edge_grid(E));
   if (C == 64)
     hipLaunchKernelGGL(init_scatter_bwd_kernel<1>, grid, dim3(256), 0, s, g_out, idx_j, rad, wigner, env, g_rad,
-                       g_wigner, g_env, E);
+                       g_wigner, g_env, E, accumulate);
   else if (C == 128)
     hipLaunchKernelGGL(init_scatter_bwd_kernel<2>, grid, dim3(256), 0, s, g_out, idx_j, rad, wigner, env, g_rad,
-                       g_wigner, g_env, E);
+                       g_wigner, g_env, E, accumulate);
   else
     hipLaunchKernelGGL(init_scatter_bwd_kernel<4>, grid, dim3(256), 0, s, g_out, idx_j, rad, wigner, env, g_rad,
-                       g_wigner, g_env, E);
+                       g_wigner, g_env, E, accumulate);
   return check_launch("fu_init_scatter_bwd");
 }

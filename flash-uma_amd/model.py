@@ -31,6 +31,7 @@ import torch.nn as nn
 
 from ops.gather import LAYOUT1_PERM, block_permutation
 from ops.gating import edge_block, gate_paired_rows
+from ops.edge_grad import EdgeGradSink
 from ops.geom import precompute_geometry
 from ops.linear import complex_linear, complex_weight_split, linear
 from ops.lmax import init_node_scatter_lmax, rotate_scatter_lmax, wigner_extend
@@ -259,7 +260,7 @@ class Packed_eSCN_Layer(nn.Module):
                 self.gamma_rad1_2, self.beta_rad1_2, self.W_rad1_3, self.b_rad1_3)
 
     def forward(self, x_in, x_edge_raw, wigner, env, idx_i, idx_j, row_ptr, col_idx, csd_emb, batch,
-                topology=None, rad_out=None, wig_ext=None, rad_src=None):
+                topology=None, rad_out=None, wig_ext=None, rad_src=None, sink=None):
         """rad_out, when given, is this block's radial-MLP output (computed by the model's
         RadialBank); otherwise it is computed here from x_edge_raw (E, B+2C).  wig_ext: the
         degree-3/4 Wigner rows (ops/lmax.wigner_extend), needed for lmax > 2."""
@@ -275,14 +276,14 @@ class Packed_eSCN_Layer(nn.Module):
             [getattr(self, "W_conv2_m" + m + x) for m in "12" for x in sfx]
         Zo_m0, Zo_m1, Zo_m2 = edge_block(x_norm, wigner, wig_ext, rad_out, idx_i, idx_j, csd_emb, batch, topology,
                                          self.layout, self.lmax, c1, c2, self.C, self._complex_splits(x_norm.device),
-                                         rad_src)
+                                         rad_src, sink)
         del rad_out
         if self.lmax == 2:
             x_mid = rotate_scatter_split(Zo_m0, Zo_m1, Zo_m2, wigner, env, x_skip, idx_j, row_ptr, col_idx,
-                                         x_skip.shape[0])
+                                         x_skip.shape[0], sink)
         else:
             x_mid = rotate_scatter_lmax(Zo_m0, Zo_m1, Zo_m2, wigner, wig_ext, env, x_skip, idx_j, row_ptr, col_idx,
-                                        x_skip.shape[0], self.lmax)
+                                        x_skip.shape[0], self.lmax, sink)
         return self._ffn_residual(x_mid)
 
     def _norm_skip(self, x_in):
@@ -308,6 +309,10 @@ class eSCN_Inference_Model(nn.Module):
     # instead of keeping it (about 100 KB per edge are held otherwise, e.g. 138 GiB at 1.5 M
     # edges; the recompute lowers that by ~22 KB per edge for ~5 % more step time).
     RAD_RECOMPUTE_MIN_EDGES = 1_000_000
+    # The blocks' backward kernels add dE/dwigner, dE/dwig_ext and dE/denv into one buffer
+    # each (ops/edge_grad.py); False returns per-block gradients for autograd to sum instead
+    # (the same values up to the order of the fp32 additions).
+    SUM_EDGE_GRADS_IN_PLACE = True
 
     def __init__(self, num_layers=4, sphere_channels=128, edge_channels=128, num_distance_basis=32, cutoff=5.0,
                  coeff_g=-0.5, lmax=2):
@@ -389,8 +394,11 @@ class eSCN_Inference_Model(nn.Module):
 
         # 2. Per-edge geometry: Gaussians, Wigner blocks, envelope.  The element-embedding
         #    columns of x_edge_raw are folded into the radial bank's per-element tables.
+        # Every block's backward adds its dE/dwigner and dE/denv into one accumulator each
+        # (ops/edge_grad.py) instead of autograd summing per-block gradients with add kernels.
+        sink = EdgeGradSink() if torch.is_grad_enabled() and self.SUM_EDGE_GRADS_IN_PLACE else None
         gauss, wigner, env = precompute_geometry(pos_s, Z_s, idx_i_s, idx_j_s, shifts_s, self.W_src, self.W_tgt,
-                                                 self.offset_g, self.coeff_g, self.cutoff, topo, False)
+                                                 self.offset_g, self.coeff_g, self.cutoff, topo, False, sink)
         # 3. Every radial MLP (edge-degree embedding + one per block) as one bank.  On large
         #    graphs the blocks keep each radial output's (E, C) source instead of the (E, 12C)
         #    output and recompute it in their backward (one GEMM per block, ~5 % of the step,
@@ -405,11 +413,11 @@ class eSCN_Inference_Model(nn.Module):
         wig_ext = None
         if self.lmax == 2:
             x_node_s = init_node_scatter(rads[0], wigner, env, Z_s, batch_s, self.W_sphere, csd_emb, idx_j_s,
-                                         row_ptr, col_idx, N)
+                                         row_ptr, col_idx, N, sink)
         else:
-            wig_ext = wigner_extend(wigner, self.lmax)
+            wig_ext = wigner_extend(wigner, self.lmax, sink)
             x_node_s = init_node_scatter_lmax(rads[0], wigner, wig_ext, env, Z_s, batch_s, self.W_sphere, csd_emb,
-                                              idx_j_s, row_ptr, col_idx, N, self.lmax)
+                                              idx_j_s, row_ptr, col_idx, N, self.lmax, sink)
         # 5. Message-passing blocks, each followed by the charge / spin channel balancing when
         #    the backbone reserves channels for them (model.py:213-216)
         balance = self.charge_end > self.charge_start or self.spin_end > self.spin_start
@@ -419,7 +427,7 @@ class eSCN_Inference_Model(nn.Module):
             rad, rads[k + 1] = rads[k + 1], None
             x_node_s = layer(x_node_s, None, wigner, env, idx_i_s, idx_j_s, row_ptr, col_idx, csd_emb,
                              batch_s, topo, rad_out=rad, wig_ext=wig_ext,
-                             rad_src=srcs[k + 1] if srcs else None)
+                             rad_src=srcs[k + 1] if srcs else None, sink=sink)
             del rad
             if self.charge_end > self.charge_start:
                 x_node_s = balance_channels_batched(x_node_s, charge, natoms, batch_s, self.charge_start,

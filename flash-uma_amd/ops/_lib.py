@@ -32,13 +32,13 @@ SIGNATURES: dict[str, list] = {
     "fu_geom_bwd": [P, P, P, P, P, P, I64, P, P, P, I64, I64, I32, F32, F32, P],
     "fu_edge_vec_reduce": [P, P, P, P, P, P, I64, I64, P],
     "fu_gather_fwd": [P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, I32, P],
-    "fu_gather_bwd": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, I32, P],
+    "fu_gather_bwd": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, I32, I32, P],
     "fu_gating_fwd": [P, P, P, P, P, P, I64, I32, I32, P],
     "fu_gating_bwd": [P, P, P, P, P, P, P, P, P, I64, I32, I32, P],
     "fu_scatter_fwd": [P, P, P, P, P, P, P, P, P, I64, I64, I32, P],
-    "fu_scatter_bwd": [P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I32, P],
+    "fu_scatter_bwd": [P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I32, I32, P],
     "fu_init_scatter_fwd": [P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, I32, P],
-    "fu_init_scatter_bwd": [P, P, P, P, P, P, P, P, I64, I64, I32, P],
+    "fu_init_scatter_bwd": [P, P, P, P, P, P, P, P, I64, I64, I32, I32, P],
     "fu_ln_silu_fwd": [P, P, P, P, P, P, I64, I32, F32, P],
     "fu_ln_silu_bwd": [P, P, P, P, P, P, P, I64, I32, P],
     "fu_ln_silu_grouped_fwd": [P, I64, P, P, I64, P, P, P, P, P, P, P, I64, P, P, I64, I32, I32, F32, P],
@@ -76,11 +76,11 @@ SIGNATURES: dict[str, list] = {
     "fu_wigner_ext_fwd": [P, P, I64, I32, P],
     "fu_wigner_ext_bwd": [P, P, P, I64, I32, P],
     "fu_gather_fwd_lmax": [P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, I32, P],
-    "fu_gather_bwd_lmax": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, I32, P],
+    "fu_gather_bwd_lmax": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, I32, I32, P],
     "fu_scatter_fwd_lmax": [P, P, P, P, P, P, P, P, P, P, I64, I64, I32, I32, P],
-    "fu_scatter_bwd_lmax": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I32, I32, P],
+    "fu_scatter_bwd_lmax": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I32, I32, I32, P],
     "fu_init_scatter_fwd_lmax": [P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, I32, I32, P],
-    "fu_init_scatter_bwd_lmax": [P, P, P, P, P, P, P, P, P, P, I64, I64, I32, I32, P],
+    "fu_init_scatter_bwd_lmax": [P, P, P, P, P, P, P, P, P, P, I64, I64, I32, I32, I32, P],
     "fu_gating_fwd_lmax": [P, P, P, P, P, P, I64, I32, I32, P],
     "fu_gating_bwd_lmax": [P, P, P, P, P, P, P, P, P, I64, I32, I32, P],
 }

@@ -13,8 +13,9 @@ from __future__ import annotations
 
 import torch
 
-from . import _lib
+from . import _lib, edge_grad
 from .constants import RAD_MULT, X_M0_MULT, X_M1_MULT, X_M2_MULT
+from .edge_grad import WIGNER
 from .topology import receiver_csr, sender_csr
 
 
@@ -48,8 +49,10 @@ def gather_fwd(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch, layout):
     return X_m0, X_m1, X_m2
 
 
-def gather_bwd(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology, layout, g_x_m0, g_x_m1, g_x_m2):
-    """fu_gather_bwd (node-centric over both CSRs): (g_x, g_wigner, g_rad)."""
+def gather_bwd(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology, layout, g_x_m0, g_x_m1, g_x_m2,
+               sink=None):
+    """fu_gather_bwd (node-centric over both CSRs): (g_x, g_wigner, g_rad); with a sink
+    (ops/edge_grad.py) g_wigner is added to its accumulator and None is returned for it."""
     N, _, C = x_in.shape
     E = idx_i.shape[0]
     dev = x_in.device
@@ -63,15 +66,15 @@ def gather_bwd(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology, la
         rptr, ridx = receiver_csr(idx_j, N)
         sptr, sidx = sender_csr(idx_i, N)
     g_x = torch.empty_like(x_in)
-    g_wigner = torch.empty_like(wigner)
+    bufs, acc = edge_grad.outputs(sink, {WIGNER: wigner})
     g_rad = torch.empty_like(rad_out)
     ws = torch.empty_like(wigner)
     _lib.call("fu_gather_bwd", g_x_m0.data_ptr(), g_x_m1.data_ptr(), g_x_m2.data_ptr(), x_in.data_ptr(),
               idx_i.data_ptr(), idx_j.data_ptr(), wigner.data_ptr(), rad_out.data_ptr(), csd_emb.data_ptr(),
               batch.data_ptr(), rptr.data_ptr(), ridx.data_ptr(), sptr.data_ptr(), sidx.data_ptr(),
-              g_x.data_ptr(), g_wigner.data_ptr(), g_rad.data_ptr(), ws.data_ptr(), E, N, csd_emb.shape[0], C,
-              int(layout), _lib.stream_ptr(dev))
-    return g_x, g_wigner, g_rad
+              g_x.data_ptr(), bufs[WIGNER].data_ptr(), g_rad.data_ptr(), ws.data_ptr(), E, N, csd_emb.shape[0], C,
+              int(layout), acc, _lib.stream_ptr(dev))
+    return g_x, (None if sink is not None else bufs[WIGNER]), g_rad
 
 
 def gather_operands(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch):

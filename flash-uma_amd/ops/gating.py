@@ -253,7 +253,7 @@ class EdgeBlock(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x_in, wigner, wig_ext, rad_out, idx_i, idx_j, csd_emb, batch, topology, layout, lmax, conv1,
-                conv2, C, splits, rad_src):
+                conv2, C, splits, rad_src, sink=None):
         from .gather import gather_fwd, gather_operands
         from .lmax import gather_lmax_fwd, gather_lmax_operands
         L = int(lmax)
@@ -273,7 +273,7 @@ class EdgeBlock(torch.autograd.Function):
             ctx.rad_w = None
         ctx.save_for_backward(*ops, *Y)
         ctx.n_ops, ctx.r, ctx.topology, ctx.layout, ctx.L = len(ops), r, topology, int(layout), L
-        ctx.conv1, ctx.conv2, ctx.C, ctx.sp = conv1, conv2, C, splits
+        ctx.conv1, ctx.conv2, ctx.C, ctx.sp, ctx.sink = conv1, conv2, C, splits, sink
         return Zo
 
     @staticmethod
@@ -296,18 +296,20 @@ class EdgeBlock(torch.autograd.Function):
                 t.untyped_storage().resize_(0)
         del g0, g1, g2, gz
         if ctx.L == 2:
-            g_x, g_w, g_rad = gather_bwd(*ops, ctx.topology, ctx.layout, *gx)
+            g_x, g_w, g_rad = gather_bwd(*ops, ctx.topology, ctx.layout, *gx, sink=ctx.sink)
             g_ext = None
         else:
-            g_x, g_w, g_ext, g_rad = gather_lmax_bwd(*ops, ctx.topology, ctx.L, *gx)
-        return g_x, g_w, g_ext, g_rad, None, None, None, None, None, None, None, None, None, None, None, None
+            g_x, g_w, g_ext, g_rad = gather_lmax_bwd(*ops, ctx.topology, ctx.L, *gx, sink=ctx.sink)
+        return (g_x, g_w, g_ext, g_rad, None, None, None, None, None, None, None, None, None, None, None, None,
+                None)
 
 
 def edge_block(x_in, wigner, wig_ext, rad_out, idx_i, idx_j, csd_emb, batch, topology, layout, lmax, conv1, conv2, C,
-               splits=None, rad_src=None):
+               splits=None, rad_src=None, sink=None):
     """gather_wigner_split (or gather_rotate_lmax) followed by conv1_gate_conv2, as one node
     whose gather output never outlives the block: returns (Zout_m0, Zout_m1, Zout_m2).
     rad_src: None, or the radial bank's (h2_k, W3_k, b3_k) source of rad_out; the backward
-    then recomputes rad_out from it instead of keeping it (memory for one extra GEMM)."""
+    then recomputes rad_out from it instead of keeping it (memory for one extra GEMM).
+    sink: accumulators of the Wigner-row gradients (ops/edge_grad.py) or None."""
     return EdgeBlock.apply(x_in, wigner, wig_ext, rad_out, idx_i, idx_j, csd_emb, batch, topology, layout, lmax,
-                           tuple(conv1), tuple(conv2), C, splits, rad_src)
+                           tuple(conv1), tuple(conv2), C, splits, rad_src, sink)

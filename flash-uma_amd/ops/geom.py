@@ -7,14 +7,15 @@ from __future__ import annotations
 
 import torch
 
-from . import _lib
+from . import _lib, edge_grad
+from .edge_grad import ENV, WIGNER
 from .topology import receiver_csr, sender_csr
 
 
 class PrecomputeGeometry(torch.autograd.Function):
     @staticmethod
     def forward(ctx, pos, Z, idx_i, idx_j, shifts, W_src, W_tgt, offset_g, coeff_g, cutoff, topology=None,
-                embeddings=True):
+                embeddings=True, sink=None):
         pos = _lib.require(pos, torch.float32, "pos")
         shifts = _lib.require(shifts, torch.float32, "shifts")
         Z = _lib.require(Z, torch.int64, "Z")
@@ -38,7 +39,10 @@ class PrecomputeGeometry(torch.autograd.Function):
                   _lib.stream_ptr(dev))
         ctx.save_for_backward(pos, idx_i, idx_j, shifts, offset_g)
         ctx.cutoff, ctx.coeff_g, ctx.B = float(cutoff), float(coeff_g), B
-        ctx.topology = topology
+        ctx.topology, ctx.sink = topology, sink
+        # outputs whose readers all add into the sink receive no gradient from autograd: keep
+        # those None instead of zero-filled arrays
+        ctx.set_materialize_grads(False)
         return x_edge_raw, wigner, env
 
     @staticmethod
@@ -47,6 +51,9 @@ class PrecomputeGeometry(torch.autograd.Function):
         E, N, B = idx_i.shape[0], pos.shape[0], ctx.B
         dev = pos.device
         st = _lib.stream_ptr(dev)
+        # the readers that took part in the sink (ops/edge_grad.py) added their gradients there
+        g_wigner = edge_grad.merge(ctx.sink, WIGNER, g_wigner)
+        g_env = edge_grad.merge(ctx.sink, ENV, g_env)
         gxe = None if g_x_edge_raw is None else g_x_edge_raw.contiguous()
         gw = None if g_wigner is None else g_wigner.contiguous()
         ge = None if g_env is None else g_env.contiguous()
@@ -66,12 +73,13 @@ class PrecomputeGeometry(torch.autograd.Function):
             _lib.call("fu_edge_vec_reduce", g_d.data_ptr(), rptr.data_ptr(), ridx.data_ptr(), sptr.data_ptr(),
                       sidx.data_ptr(), g_pos.data_ptr(), N, E, st)
         g_shifts = g_d if ctx.needs_input_grad[4] else None
-        return g_pos, None, None, None, g_shifts, None, None, None, None, None, None, None
+        return g_pos, None, None, None, g_shifts, None, None, None, None, None, None, None, None
 
 
 def precompute_geometry(pos, Z, idx_i, idx_j, shifts, W_src, W_tgt, offset_g, coeff_g, cutoff, topology=None,
-                        embeddings=True):
+                        embeddings=True, sink=None):
     """Returns (x_edge_raw (E, B+2C), wigner (E, 34), env (E)); with embeddings=False the
-    element-embedding columns are left out and x_edge_raw is (E, B)."""
+    element-embedding columns are left out and x_edge_raw is (E, B).  sink: the readers'
+    accumulators of dE/dwigner and dE/denv (ops/edge_grad.py), taken in the backward."""
     return PrecomputeGeometry.apply(pos, Z, idx_i, idx_j, shifts, W_src, W_tgt, offset_g, coeff_g, cutoff,
-                                    topology, embeddings)
+                                    topology, embeddings, sink)

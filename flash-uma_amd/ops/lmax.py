@@ -17,7 +17,8 @@ from __future__ import annotations
 
 import torch
 
-from . import _lib
+from . import _lib, edge_grad
+from .edge_grad import ENV, WIG_EXT, WIGNER
 from .topology import receiver_csr, sender_csr
 
 
@@ -31,27 +32,31 @@ def _ext_ptr(t):
 
 class WignerExtend(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, wigner, lmax):
+    def forward(ctx, wigner, lmax, sink=None):
         wigner = _lib.require(wigner, torch.float32, "wigner")
         E = wigner.shape[0]
         ext = torch.empty(E, ext_width(lmax), device=wigner.device, dtype=torch.float32)
         _lib.call("fu_wigner_ext_fwd", wigner.data_ptr(), ext.data_ptr(), E, int(lmax), _lib.stream_ptr(wigner.device))
         ctx.save_for_backward(wigner)
-        ctx.lmax = int(lmax)
+        ctx.lmax, ctx.sink = int(lmax), sink
+        ctx.set_materialize_grads(False)   # g_ext stays None when every reader used the sink
         return ext
 
     @staticmethod
     def backward(ctx, g_ext):
         (wigner,) = ctx.saved_tensors
+        g_ext = edge_grad.merge(ctx.sink, WIG_EXT, g_ext)
+        if g_ext is None:
+            return None, None, None
         E = wigner.shape[0]
         g_w = torch.empty_like(wigner)
         _lib.call("fu_wigner_ext_bwd", wigner.data_ptr(), g_ext.contiguous().data_ptr(), g_w.data_ptr(), E, ctx.lmax,
                   _lib.stream_ptr(wigner.device))
-        return g_w, None
+        return g_w, None, None
 
 
-def wigner_extend(wigner, lmax: int):
-    return WignerExtend.apply(wigner, int(lmax))
+def wigner_extend(wigner, lmax: int, sink=None):
+    return WignerExtend.apply(wigner, int(lmax), sink)
 
 
 def _csrs(topology, idx_i, idx_j, N, E):
@@ -88,8 +93,10 @@ def gather_lmax_fwd(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch
     return X_m0, X_m1, X_m2
 
 
-def gather_lmax_bwd(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, topology, L, g0, g1, g2):
-    """fu_gather_bwd_lmax: (g_x, g_wigner, g_wig_ext, g_rad)."""
+def gather_lmax_bwd(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, topology, L, g0, g1, g2,
+                    sink=None):
+    """fu_gather_bwd_lmax: (g_x, g_wigner, g_wig_ext, g_rad); with a sink (ops/edge_grad.py) the
+    Wigner gradients are added to its accumulators and None is returned for them."""
     N, _, C = x_in.shape
     E = idx_i.shape[0]
     dev = x_in.device
@@ -98,16 +105,17 @@ def gather_lmax_bwd(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch
     g2 = torch.zeros(E, 4 * (L - 1) * C, device=dev) if g2 is None else g2.contiguous()
     rptr, ridx, sptr, sidx = _csrs(topology, idx_i, idx_j, N, E)
     g_x = torch.empty_like(x_in)
-    g_w = torch.empty_like(wigner)
-    g_ext = torch.empty_like(wig_ext)
+    bufs, acc = edge_grad.outputs(sink, {WIGNER: wigner, WIG_EXT: wig_ext})
     g_rad = torch.empty_like(rad_out)
     ws = torch.empty(E * (34 + ext_width(L)), device=dev)
     _lib.call("fu_gather_bwd_lmax", g0.data_ptr(), g1.data_ptr(), g2.data_ptr(), x_in.data_ptr(),
               wigner.data_ptr(), _ext_ptr(wig_ext), rad_out.data_ptr(), csd_emb.data_ptr(), batch.data_ptr(),
-              rptr.data_ptr(), ridx.data_ptr(), sptr.data_ptr(), sidx.data_ptr(), g_x.data_ptr(), g_w.data_ptr(),
-              _ext_ptr(g_ext), g_rad.data_ptr(), ws.data_ptr(), E, N, csd_emb.shape[0], C, L,
-              _lib.stream_ptr(dev))
-    return g_x, g_w, g_ext, g_rad
+              rptr.data_ptr(), ridx.data_ptr(), sptr.data_ptr(), sidx.data_ptr(), g_x.data_ptr(),
+              bufs[WIGNER].data_ptr(), _ext_ptr(bufs[WIG_EXT]), g_rad.data_ptr(), ws.data_ptr(), E, N,
+              csd_emb.shape[0], C, L, acc, _lib.stream_ptr(dev))
+    if sink is not None:
+        return g_x, None, None, g_rad
+    return g_x, bufs[WIGNER], bufs[WIG_EXT], g_rad
 
 
 class GatherRotateLmax(torch.autograd.Function):
@@ -169,7 +177,7 @@ def gating_lmax(Y_m0, Y_m1, Y_m2, C: int, lmax: int):
 
 class RotateScatterLmax(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, Z_m0, Z_m1, Z_m2, wigner, wig_ext, env, x_res, idx_j, row_ptr, col_idx, N, lmax):
+    def forward(ctx, Z_m0, Z_m1, Z_m2, wigner, wig_ext, env, x_res, idx_j, row_ptr, col_idx, N, lmax, sink=None):
         L = int(lmax)
         Z_m0 = _lib.require(Z_m0, torch.float32, "Z_m0")
         Z_m1 = _lib.require(Z_m1, torch.float32, "Z_m1")
@@ -189,7 +197,7 @@ class RotateScatterLmax(torch.autograd.Function):
                   Z_m2.data_ptr(), wigner.data_ptr(), _ext_ptr(wig_ext), env.data_ptr(), x_res.data_ptr(),
                   x_out.data_ptr(), N, E, C, L, _lib.stream_ptr(Z_m0.device))
         ctx.save_for_backward(Z_m0, Z_m1, Z_m2, wigner, wig_ext, env, _lib.require(idx_j, torch.int64, "idx_j"))
-        ctx.C, ctx.N, ctx.lmax = C, N, L
+        ctx.C, ctx.N, ctx.lmax, ctx.sink = C, N, L, sink
         return x_out
 
     @staticmethod
@@ -198,22 +206,24 @@ class RotateScatterLmax(torch.autograd.Function):
         E, C, N, L = Z_m0.shape[0], ctx.C, ctx.N, ctx.lmax
         g_out = g_out.contiguous()
         gZ0, gZ1, gZ2 = torch.empty_like(Z_m0), torch.empty_like(Z_m1), torch.empty_like(Z_m2)
-        g_w, g_ext, g_env = torch.empty_like(wigner), torch.empty_like(wig_ext), torch.empty_like(env)
+        bufs, acc = edge_grad.outputs(ctx.sink, {WIGNER: wigner, WIG_EXT: wig_ext, ENV: env})
         _lib.call("fu_scatter_bwd_lmax", g_out.data_ptr(), idx_j.data_ptr(), Z_m0.data_ptr(), Z_m1.data_ptr(),
                   Z_m2.data_ptr(), wigner.data_ptr(), _ext_ptr(wig_ext), env.data_ptr(), gZ0.data_ptr(),
-                  gZ1.data_ptr(), gZ2.data_ptr(), g_w.data_ptr(), _ext_ptr(g_ext), g_env.data_ptr(), E, N, C, L,
-                  _lib.stream_ptr(g_out.device))
-        return gZ0, gZ1, gZ2, g_w, g_ext, g_env, g_out, None, None, None, None, None
+                  gZ1.data_ptr(), gZ2.data_ptr(), bufs[WIGNER].data_ptr(), _ext_ptr(bufs[WIG_EXT]),
+                  bufs[ENV].data_ptr(), E, N, C, L, acc, _lib.stream_ptr(g_out.device))
+        g_w, g_ext, g_env = (None,) * 3 if ctx.sink is not None else (bufs[WIGNER], bufs[WIG_EXT], bufs[ENV])
+        return gZ0, gZ1, gZ2, g_w, g_ext, g_env, g_out, None, None, None, None, None, None
 
 
-def rotate_scatter_lmax(Z_m0, Z_m1, Z_m2, wigner, wig_ext, env, x_res, idx_j, row_ptr, col_idx, N, lmax):
+def rotate_scatter_lmax(Z_m0, Z_m1, Z_m2, wigner, wig_ext, env, x_res, idx_j, row_ptr, col_idx, N, lmax, sink=None):
     return RotateScatterLmax.apply(Z_m0, Z_m1, Z_m2, wigner, wig_ext, env, x_res, idx_j, row_ptr, col_idx, N,
-                                   int(lmax))
+                                   int(lmax), sink)
 
 
 class InitNodeScatterLmax(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, rad_out, wigner, wig_ext, env, Z, batch, W_sphere, csd_emb, idx_j, row_ptr, col_idx, N, lmax):
+    def forward(ctx, rad_out, wigner, wig_ext, env, Z, batch, W_sphere, csd_emb, idx_j, row_ptr, col_idx, N, lmax,
+                sink=None):
         L = int(lmax)
         rad_out = _lib.require(rad_out, torch.float32, "rad_out")
         wigner = _lib.require(wigner, torch.float32, "wigner")
@@ -233,7 +243,7 @@ class InitNodeScatterLmax(torch.autograd.Function):
                   W_sphere.data_ptr(), csd_emb.data_ptr(), x_out.data_ptr(), N, E, W_sphere.shape[0],
                   csd_emb.shape[0], C, L, _lib.stream_ptr(rad_out.device))
         ctx.save_for_backward(rad_out, wigner, wig_ext, env, _lib.require(idx_j, torch.int64, "idx_j"))
-        ctx.C, ctx.N, ctx.lmax = C, N, L
+        ctx.C, ctx.N, ctx.lmax, ctx.sink = C, N, L, sink
         return x_out
 
     @staticmethod
@@ -241,15 +251,16 @@ class InitNodeScatterLmax(torch.autograd.Function):
         rad_out, wigner, wig_ext, env, idx_j = ctx.saved_tensors
         E, C, N, L = rad_out.shape[0], ctx.C, ctx.N, ctx.lmax
         g_out = g_out.contiguous()
-        g_rad, g_w, g_ext, g_env = (torch.empty_like(rad_out), torch.empty_like(wigner), torch.empty_like(wig_ext),
-                                    torch.empty_like(env))
+        g_rad = torch.empty_like(rad_out)
+        bufs, acc = edge_grad.outputs(ctx.sink, {WIGNER: wigner, WIG_EXT: wig_ext, ENV: env})
         _lib.call("fu_init_scatter_bwd_lmax", g_out.data_ptr(), idx_j.data_ptr(), rad_out.data_ptr(),
-                  wigner.data_ptr(), _ext_ptr(wig_ext), env.data_ptr(), g_rad.data_ptr(), g_w.data_ptr(),
-                  _ext_ptr(g_ext), g_env.data_ptr(), E, N, C, L, _lib.stream_ptr(g_out.device))
-        return g_rad, g_w, g_ext, g_env, None, None, None, None, None, None, None, None, None
+                  wigner.data_ptr(), _ext_ptr(wig_ext), env.data_ptr(), g_rad.data_ptr(), bufs[WIGNER].data_ptr(),
+                  _ext_ptr(bufs[WIG_EXT]), bufs[ENV].data_ptr(), E, N, C, L, acc, _lib.stream_ptr(g_out.device))
+        g_w, g_ext, g_env = (None,) * 3 if ctx.sink is not None else (bufs[WIGNER], bufs[WIG_EXT], bufs[ENV])
+        return g_rad, g_w, g_ext, g_env, None, None, None, None, None, None, None, None, None, None
 
 
 def init_node_scatter_lmax(rad_out, wigner, wig_ext, env, Z, batch, W_sphere, csd_emb, idx_j, row_ptr, col_idx, N,
-                           lmax):
+                           lmax, sink=None):
     return InitNodeScatterLmax.apply(rad_out, wigner, wig_ext, env, Z, batch, W_sphere, csd_emb, idx_j, row_ptr,
-                                     col_idx, N, int(lmax))
+                                     col_idx, N, int(lmax), sink)

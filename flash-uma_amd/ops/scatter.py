@@ -4,13 +4,14 @@ from __future__ import annotations
 
 import torch
 
-from . import _lib
+from . import _lib, edge_grad
 from .constants import INIT_RAD_MULT, Z_M0_MULT
+from .edge_grad import ENV, WIGNER
 
 
 class RotateScatterSplit(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, Z_m0, Z_m1, Z_m2, wigner, env, x_res, idx_j, row_ptr, col_idx, N):
+    def forward(ctx, Z_m0, Z_m1, Z_m2, wigner, env, x_res, idx_j, row_ptr, col_idx, N, sink=None):
         Z_m0 = _lib.require(Z_m0, torch.float32, "Z_m0")
         Z_m1 = _lib.require(Z_m1, torch.float32, "Z_m1")
         Z_m2 = _lib.require(Z_m2, torch.float32, "Z_m2")
@@ -26,7 +27,7 @@ class RotateScatterSplit(torch.autograd.Function):
                   Z_m2.data_ptr(), wigner.data_ptr(), env.data_ptr(), x_res.data_ptr(), x_out.data_ptr(), N, E, C,
                   _lib.stream_ptr(Z_m0.device))
         ctx.save_for_backward(Z_m0, Z_m1, Z_m2, wigner, env, _lib.require(idx_j, torch.int64, "idx_j"))
-        ctx.C, ctx.N = C, N
+        ctx.C, ctx.N, ctx.sink = C, N, sink
         return x_out
 
     @staticmethod
@@ -37,12 +38,15 @@ class RotateScatterSplit(torch.autograd.Function):
         g_Z_m0 = torch.empty_like(Z_m0)
         g_Z_m1 = torch.empty_like(Z_m1)
         g_Z_m2 = torch.empty_like(Z_m2)
-        g_wigner = torch.empty_like(wigner)
-        g_env = torch.empty_like(env)
+        # with a sink (the model's path) the Wigner and envelope gradients are added to its
+        # accumulators and not returned
+        bufs, acc = edge_grad.outputs(ctx.sink, {WIGNER: wigner, ENV: env})
         _lib.call("fu_scatter_bwd", g_out.data_ptr(), idx_j.data_ptr(), Z_m0.data_ptr(), Z_m1.data_ptr(),
                   Z_m2.data_ptr(), wigner.data_ptr(), env.data_ptr(), g_Z_m0.data_ptr(), g_Z_m1.data_ptr(),
-                  g_Z_m2.data_ptr(), g_wigner.data_ptr(), g_env.data_ptr(), E, N, C, _lib.stream_ptr(g_out.device))
-        return g_Z_m0, g_Z_m1, g_Z_m2, g_wigner, g_env, g_out, None, None, None, None
+                  g_Z_m2.data_ptr(), bufs[WIGNER].data_ptr(), bufs[ENV].data_ptr(), E, N, C, acc,
+                  _lib.stream_ptr(g_out.device))
+        g_wigner, g_env = (None, None) if ctx.sink is not None else (bufs[WIGNER], bufs[ENV])
+        return g_Z_m0, g_Z_m1, g_Z_m2, g_wigner, g_env, g_out, None, None, None, None, None
 
 
 rotate_scatter_split = RotateScatterSplit.apply
@@ -50,7 +54,7 @@ rotate_scatter_split = RotateScatterSplit.apply
 
 class InitNodeScatter(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, rad_out, wigner, env, Z, batch, W_sphere, csd_emb, idx_j, row_ptr, col_idx, N):
+    def forward(ctx, rad_out, wigner, env, Z, batch, W_sphere, csd_emb, idx_j, row_ptr, col_idx, N, sink=None):
         rad_out = _lib.require(rad_out, torch.float32, "rad_out")
         wigner = _lib.require(wigner, torch.float32, "wigner")
         env = _lib.require(env, torch.float32, "env")
@@ -68,7 +72,7 @@ class InitNodeScatter(torch.autograd.Function):
                   csd_emb.data_ptr(), x_out.data_ptr(), N, E, W_sphere.shape[0], csd_emb.shape[0], C,
                   _lib.stream_ptr(rad_out.device))
         ctx.save_for_backward(rad_out, wigner, env, _lib.require(idx_j, torch.int64, "idx_j"), Z, batch)
-        ctx.C, ctx.N = C, N
+        ctx.C, ctx.N, ctx.sink = C, N, sink
         ctx.num_z, ctx.num_batches = W_sphere.shape[0], csd_emb.shape[0]
         return x_out
 
@@ -78,11 +82,11 @@ class InitNodeScatter(torch.autograd.Function):
         E, C, N = rad_out.shape[0], ctx.C, ctx.N
         g_out = g_out.contiguous()
         g_rad = torch.empty_like(rad_out)
-        g_wigner = torch.empty_like(wigner)
-        g_env = torch.empty_like(env)
+        bufs, acc = edge_grad.outputs(ctx.sink, {WIGNER: wigner, ENV: env})
         _lib.call("fu_init_scatter_bwd", g_out.data_ptr(), idx_j.data_ptr(), rad_out.data_ptr(), wigner.data_ptr(),
-                  env.data_ptr(), g_rad.data_ptr(), g_wigner.data_ptr(), g_env.data_ptr(), E, N, C,
+                  env.data_ptr(), g_rad.data_ptr(), bufs[WIGNER].data_ptr(), bufs[ENV].data_ptr(), E, N, C, acc,
                   _lib.stream_ptr(g_out.device))
+        g_wigner, g_env = (None, None) if ctx.sink is not None else (bufs[WIGNER], bufs[ENV])
         g_W_sphere = g_csd = None
         if ctx.needs_input_grad[5] or ctx.needs_input_grad[6]:
             # parameter-side gradients (ops/scatter.py:519-523); not on the force path
@@ -91,7 +95,7 @@ class InitNodeScatter(torch.autograd.Function):
                 g_W_sphere = torch.zeros(ctx.num_z, C, device=g_out.device).index_add_(0, Z, g_l0)
             if ctx.needs_input_grad[6]:
                 g_csd = torch.zeros(ctx.num_batches, C, device=g_out.device).index_add_(0, batch, g_l0)
-        return g_rad, g_wigner, g_env, None, None, g_W_sphere, g_csd, None, None, None, None
+        return g_rad, g_wigner, g_env, None, None, g_W_sphere, g_csd, None, None, None, None, None
 
 
 init_node_scatter = InitNodeScatter.apply

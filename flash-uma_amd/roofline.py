@@ -42,9 +42,14 @@ def _gather_fwd(a):
     return E * (30 * C * 4 + 34 * 4 + 16) + N * (9 * C * 4 + 8), 0
 
 
+def _acc_read(E, acc, wig, env=1):
+    """Bytes an accumulating call reads back: the Wigner rows (bit 0) and envelope (bit 1)."""
+    return E * ((wig * 4 if acc & 1 else 0) + (env * 4 if acc & 2 else 0))
+
+
 def _gather_bwd(a):
     E, N, C = a[18], a[19], a[21]
-    return E * (42 * C * 4 + 2 * 34 * 4 + 8) + N * (2 * 9 * C * 4 + 16), 0
+    return E * (42 * C * 4 + 2 * 34 * 4 + 8) + N * (2 * 9 * C * 4 + 16) + _acc_read(E, a[23], 34, 0), 0
 
 
 def _scatter_fwd(a):
@@ -54,7 +59,7 @@ def _scatter_fwd(a):
 
 def _scatter_bwd(a):
     E, N, C = a[12], a[13], a[14]
-    return E * (2 * 9 * C * 4 + 2 * 34 * 4 + 8 + 8) + N * 9 * C * 4, 0
+    return E * (2 * 9 * C * 4 + 2 * 34 * 4 + 8 + 8) + N * 9 * C * 4 + _acc_read(E, a[15], 34), 0
 
 
 def _init_fwd(a):
@@ -64,7 +69,7 @@ def _init_fwd(a):
 
 def _init_bwd(a):
     E, N, C = a[8], a[9], a[10]
-    return E * (2 * 3 * C * 4 + 8 * 4 + 34 * 4 + 8 + 8) + N * 9 * C * 4, 0
+    return E * (2 * 3 * C * 4 + 8 * 4 + 34 * 4 + 8 + 8) + N * 9 * C * 4 + _acc_read(E, a[11], 8), 0
 
 
 def _geom_fwd(a):
@@ -121,7 +126,8 @@ def _gather_fwd_l(a):
 
 def _gather_bwd_l(a):
     E, N, C, L = a[18], a[19], a[21], a[22]
-    return E * ((22 * L - 2) * C * 4 + 2 * (34 + _ext(L)) * 4 + 8) + N * (2 * (L + 1) ** 2 * C * 4 + 16), 0
+    return (E * ((22 * L - 2) * C * 4 + 2 * (34 + _ext(L)) * 4 + 8) + N * (2 * (L + 1) ** 2 * C * 4 + 16)
+            + _acc_read(E, a[23], 34 + _ext(L), 0)), 0
 
 
 def _scatter_fwd_l(a):
@@ -131,7 +137,8 @@ def _scatter_fwd_l(a):
 
 def _scatter_bwd_l(a):
     E, N, C, L = a[14], a[15], a[16], a[17]
-    return E * (2 * (5 * L - 1) * C * 4 + 2 * (34 + _ext(L)) * 4 + 16) + N * (L + 1) ** 2 * C * 4, 0
+    return (E * (2 * (5 * L - 1) * C * 4 + 2 * (34 + _ext(L)) * 4 + 16) + N * (L + 1) ** 2 * C * 4
+            + _acc_read(E, a[18], 34 + _ext(L))), 0
 
 
 def _init_fwd_l(a):
@@ -141,7 +148,8 @@ def _init_fwd_l(a):
 
 def _init_bwd_l(a):
     E, N, C, L = a[10], a[11], a[12], a[13]
-    return E * (2 * (L + 1) * C * 4 + ((L + 1) ** 2 - 1) * 4 + (34 + _ext(L)) * 4 + 16) + N * (L + 1) ** 2 * C * 4, 0
+    return (E * (2 * (L + 1) * C * 4 + ((L + 1) ** 2 - 1) * 4 + (34 + _ext(L)) * 4 + 16) + N * (L + 1) ** 2 * C * 4
+            + _acc_read(E, a[14], (L + 1) ** 2 - 1)), 0
 
 
 def _gating_fwd_l(a):

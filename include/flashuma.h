@@ -112,13 +112,17 @@ int fu_gather_fwd(const float* x, const int64_t* idx_i, const int64_t* idx_j, co
  * sums the node's receiver segment (recv CSR) and sender segment (send CSR) in CSR order,
  * writing g_x (N, 9, C), g_rad (E, 12C) and g_wigner (E, 34).  g_wig_ws is an (E, 34)
  * scratch array for the sender-side halves of g_wigner.  layout as in fu_gather_fwd (g_X and
- * g_rad use the same order as X and rad). */
+ * g_rad use the same order as X and rad).  accumulate: bit 0 set adds this call's g_wigner to
+ * the array's contents instead of overwriting it (the model sums the contributions of all its
+ * blocks in place this way, replacing the per-tensor sums autograd would add; bit 1, used by
+ * the scatters for g_env, is ignored here). */
 int fu_gather_bwd(const float* g_X_m0, const float* g_X_m1, const float* g_X_m2, const float* x,
                   const int64_t* idx_i, const int64_t* idx_j, const float* wigner, const float* rad,
                   const float* csd_emb, const int64_t* batch, const int32_t* recv_ptr,
                   const int32_t* recv_idx, const int32_t* send_ptr, const int32_t* send_idx,
                   float* g_x, float* g_wigner, float* g_rad, float* g_wig_ws, int64_t E,
-                  int64_t N, int64_t S, int32_t C, int32_t layout, void* stream);
+                  int64_t N, int64_t S, int32_t C, int32_t layout, int32_t accumulate,
+                  void* stream);
 
 /* ------------------------------------------------------------------------------------
  * Gate activation (replaces FusedGatingSplit, ops/gating.py:188-234)
@@ -149,11 +153,12 @@ int fu_scatter_fwd(const int32_t* row_ptr, const int32_t* col_idx, const float* 
                    void* stream);
 
 /* ops/scatter.py:146-292 (both backward kernels, fused into one pass over the edges):
- * g_Z = env * D * g_out[idx_j], g_wigner and g_env channel reductions. */
+ * g_Z = env * D * g_out[idx_j], g_wigner and g_env channel reductions.  accumulate: bit 0
+ * adds g_wigner to the array's contents, bit 1 adds g_env (as in fu_gather_bwd). */
 int fu_scatter_bwd(const float* g_out, const int64_t* idx_j, const float* Z_m0, const float* Z_m1,
                    const float* Z_m2, const float* wigner, const float* env, float* g_Z_m0,
                    float* g_Z_m1, float* g_Z_m2, float* g_wigner, float* g_env, int64_t E,
-                   int64_t N, int32_t C, void* stream);
+                   int64_t N, int32_t C, int32_t accumulate, void* stream);
 
 /* ops/scatter.py:360-423 (_init_scatter_fwd_kernel): edge-degree embedding,
  * x0[j] = [W_sphere[Z_j] + csd_emb[batch_j], 0...] + sum_e env/5 * (r0; r1 D1[1,:]; r2 D2[2,:]). */
@@ -164,10 +169,12 @@ int fu_init_scatter_fwd(const int32_t* row_ptr, const int32_t* col_idx, const fl
                         void* stream);
 
 /* ops/scatter.py:426-481 (_init_scatter_bwd_kernel): g_rad (E, 3C), g_wigner (E, 34; the
- * 26 entries the forward does not read are written as 0) and g_env (E). */
+ * 26 entries the forward does not read are written as 0, or left as they are when
+ * accumulating) and g_env (E).  accumulate as in fu_scatter_bwd. */
 int fu_init_scatter_bwd(const float* g_out, const int64_t* idx_j, const float* rad,
                         const float* wigner, const float* env, float* g_rad, float* g_wigner,
-                        float* g_env, int64_t E, int64_t N, int32_t C, void* stream);
+                        float* g_env, int64_t E, int64_t N, int32_t C, int32_t accumulate,
+                        void* stream);
 
 /* ------------------------------------------------------------------------------------
  * LayerNorm + SiLU (replaces _LayerNormSiLUFn, ops/ln_silu.py:126-185)
@@ -462,13 +469,15 @@ int fu_gather_fwd_lmax(const float* x, const int64_t* idx_i, const int64_t* idx_
                        void* stream);
 
 /* fu_gather_bwd for lmax 2..4 (ops/gather.py:160-405, node-centric, no atomics).  ws is a
- * scratch array of E * (34 + fu_wigner_ext_width(lmax)) floats. */
+ * scratch array of E * (34 + fu_wigner_ext_width(lmax)) floats.  accumulate: bit 0 adds
+ * g_wigner and g_wig_ext to the arrays' contents. */
 int fu_gather_bwd_lmax(const float* g_X_m0, const float* g_X_m1, const float* g_X_m2,
                        const float* x, const float* wigner, const float* wig_ext, const float* rad,
                        const float* csd_emb, const int64_t* batch, const int32_t* recv_ptr,
                        const int32_t* recv_idx, const int32_t* send_ptr, const int32_t* send_idx,
                        float* g_x, float* g_wigner, float* g_wig_ext, float* g_rad, float* ws,
-                       int64_t E, int64_t N, int64_t S, int32_t C, int32_t lmax, void* stream);
+                       int64_t E, int64_t N, int64_t S, int32_t C, int32_t lmax, int32_t accumulate,
+                       void* stream);
 
 /* fu_scatter_fwd for lmax 2..4 (ops/scatter.py:45-140, fp64 CSR accumulation). */
 int fu_scatter_fwd_lmax(const int32_t* row_ptr, const int32_t* col_idx, const float* Z_m0,
@@ -476,12 +485,13 @@ int fu_scatter_fwd_lmax(const int32_t* row_ptr, const int32_t* col_idx, const fl
                         const float* wig_ext, const float* env, const float* x_res, float* x_out,
                         int64_t N, int64_t E, int32_t C, int32_t lmax, void* stream);
 
-/* fu_scatter_bwd for lmax 2..4 (ops/scatter.py:146-292). */
+/* fu_scatter_bwd for lmax 2..4 (ops/scatter.py:146-292).  accumulate: bit 0 adds g_wigner
+ * and g_wig_ext, bit 1 adds g_env to the arrays' contents. */
 int fu_scatter_bwd_lmax(const float* g_out, const int64_t* idx_j, const float* Z_m0,
                         const float* Z_m1, const float* Z_m2, const float* wigner,
                         const float* wig_ext, const float* env, float* g_Z_m0, float* g_Z_m1,
                         float* g_Z_m2, float* g_wigner, float* g_wig_ext, float* g_env, int64_t E,
-                        int64_t N, int32_t C, int32_t lmax, void* stream);
+                        int64_t N, int32_t C, int32_t lmax, int32_t accumulate, void* stream);
 
 /* fu_init_scatter_fwd for lmax 2..4 (ops/scatter.py:360-423): rad (E, (L+1) C). */
 int fu_init_scatter_fwd_lmax(const int32_t* row_ptr, const int32_t* col_idx, const float* rad,
@@ -491,11 +501,13 @@ int fu_init_scatter_fwd_lmax(const int32_t* row_ptr, const int32_t* col_idx, con
                              int64_t num_z, int64_t S, int32_t C, int32_t lmax, void* stream);
 
 /* fu_init_scatter_bwd for lmax 2..4 (ops/scatter.py:426-481); g_wigner / g_wig_ext entries the
- * forward does not read are written as 0. */
+ * forward does not read are written as 0 (left as they are when accumulating).  accumulate as
+ * in fu_scatter_bwd_lmax. */
 int fu_init_scatter_bwd_lmax(const float* g_out, const int64_t* idx_j, const float* rad,
                              const float* wigner, const float* wig_ext, const float* env,
                              float* g_rad, float* g_wigner, float* g_wig_ext, float* g_env,
-                             int64_t E, int64_t N, int32_t C, int32_t lmax, void* stream);
+                             int64_t E, int64_t N, int32_t C, int32_t lmax, int32_t accumulate,
+                             void* stream);
 
 /* fu_gating_fwd / fu_gating_bwd (layout 0) for lmax 2..4 (ops/gating.py:32-185). */
 int fu_gating_fwd_lmax(const float* Y_m0, const float* Y_m1, const float* Y_m2, float* Z_m0,

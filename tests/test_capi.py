@@ -61,6 +61,16 @@ def test_error_codes():
     assert st == -1  # ld_xe smaller than the embedding row width
     st, _ = _status("fu_scatter_fwd", *([None] * 9), 3, 3, 192, None)
     assert st == -2
+    # accumulate flags: bit 0 (wigner rows), bit 1 (env); nothing else
+    for name, args in (("fu_scatter_bwd", (*([None] * 12), 0, 5, 128)),
+                       ("fu_init_scatter_bwd", (*([None] * 8), 0, 5, 128)),
+                       ("fu_gather_bwd", (*([None] * 18), 0, 0, 1, 128, 1)),
+                       ("fu_scatter_bwd_lmax", (*([None] * 14), 0, 5, 128, 4)),
+                       ("fu_init_scatter_bwd_lmax", (*([None] * 10), 0, 5, 128, 4)),
+                       ("fu_gather_bwd_lmax", (*([None] * 18), 0, 0, 1, 128, 4))):
+        for acc, want in ((3, 0), (4, -2), (-1, -2)):
+            st, msg = _status(name, *args, acc, None)
+            assert st == want, (name, acc, msg)
 
 
 def test_zero_sized_calls_are_no_ops():
@@ -97,14 +107,14 @@ def test_zero_rows_accept_empty_arrays():
                                    5, 128, f(1e-7), None),
         "fu_ln_silu_grouped_bwd": (None, 640, 16, 16, 128, 16, None, None, None, None, None, None, None, None, 640,
                                    None, 640, 0, 5, 128, None),
-        "fu_scatter_bwd": (*([None] * 12), 0, 5, 128, None),
-        "fu_init_scatter_bwd": (*([None] * 8), 0, 5, 128, None),
+        "fu_scatter_bwd": (*([None] * 12), 0, 5, 128, 0, None),
+        "fu_init_scatter_bwd": (*([None] * 8), 0, 5, 128, 0, None),
         "fu_gather_fwd": (*([None] * 10), 0, 5, 1, 128, 1, None),
         "fu_edge_shifts": (None, None, None, None, 0, None),
         "fu_wigner_ext_fwd": (None, None, 0, 4, None),
         "fu_wigner_ext_bwd": (None, None, None, 0, 4, None),
         "fu_gating_fwd_lmax": (*([None] * 6), 0, 128, 4, None),
-        "fu_scatter_bwd_lmax": (*([None] * 14), 0, 5, 128, 4, None),
+        "fu_scatter_bwd_lmax": (*([None] * 14), 0, 5, 128, 4, 0, None),
     }
     for name, args in calls.items():
         st, msg = _status(name, *args)
@@ -159,7 +169,7 @@ def test_lmax_entry_points_reject_bad_arguments():
                                   None) != 0
     assert b"NULL" in lib.fu_last_error()
     # lmax 3 and 4 need the extension rows; lmax 2 accepts NULL there (checked before any launch)
-    assert lib.fu_init_scatter_bwd_lmax(None, None, None, None, None, None, None, None, None, None, 0, 4, 128, 4,
+    assert lib.fu_init_scatter_bwd_lmax(None, None, None, None, None, None, None, None, None, None, 0, 4, 128, 4, 0,
                                         None) == 0
 
 

@@ -358,3 +358,43 @@ def test_radial_recompute_mode_is_bitwise_equal(cuda):
         ce.RAD_RECOMPUTE_MIN_EDGES = old
     for k in ("energy", "forces", "stress", "node_embedding"):
         assert torch.equal(a[k], b[k]), k
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("lmax", [2, 4])
+def test_edge_grads_summed_in_place(cuda, lmax):
+    """The blocks' backward kernels add their Wigner-row and envelope gradients into one buffer
+    each (accumulate flags) instead of returning them for autograd to sum: the energy is
+    unchanged and forces and stress agree with the autograd sums to fp32 rounding (lmax 2 and
+    the lmax 4 path with the degree-3/4 Wigner rows)."""
+    import escn_md
+    import heads
+    import systems
+    from ops import edge_grad
+    from wrapper import ZeroAllocBackbone
+    bb = escn_md.eSCNMDBackbone(seed=0, lmax=lmax, num_layers=2)
+    hd = heads.MLPEnergyHead(bb.sphere_channels, bb.hidden_channels, seed=1)
+    model = heads.PotentialModel(ZeroAllocBackbone(bb.to(cuda)), hd.to(cuda))
+    s = systems.water_box(n_mol=64, L=12.42, seed=5)
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, 6.0, 30)
+    ce = model.backbone.ce
+    a = _run(model, s, ei, off, cuda)
+    old = ce.SUM_EDGE_GRADS_IN_PLACE
+    try:
+        ce.SUM_EDGE_GRADS_IN_PLACE = False
+        b = _run(model, s, ei, off, cuda)
+    finally:
+        ce.SUM_EDGE_GRADS_IN_PLACE = old
+    assert torch.equal(a["energy"], b["energy"])
+    fs = b["forces"].abs().max().item()
+    assert (a["forces"] - b["forces"]).abs().max().item() <= 1e-5 * fs
+    ss = b["stress"].abs().max().item()
+    assert (a["stress"] - b["stress"]).abs().max().item() <= 1e-5 * ss
+    # the sink forgets each sum once the geometry backward has taken it
+    sink = edge_grad.EdgeGradSink()
+    w = torch.ones(7, 34, device=cuda)
+    buf, acc = sink.target(edge_grad.WIGNER, w)
+    assert acc == 0
+    buf2, acc2 = sink.target(edge_grad.WIGNER, w)
+    assert buf2 is buf and acc2 == 1
+    assert sink.take(edge_grad.WIGNER) is buf and sink.take(edge_grad.WIGNER) is None
