@@ -60,12 +60,14 @@ def make_system(config: str):
     raise SystemExit(f"unknown config {config}")
 
 
-def cpu_baseline(budget_s: float = 20.0, model_kw: dict | None = None, stress: bool = True, n_rep: int = 6) -> dict:
-    """float32 torch-CPU oracle (reference-algorithm restatement) on a bcc Fe n_rep^3 cell, the
-    headline material with the same per-atom work (30 edges/atom), E+F+S.  Its cost per atom
-    grows with the cell (the eager CPU path's element-wise passes leave the caches): with 8
-    threads 128 atoms run at 170 atom-steps/s, 432 atoms at 44 and 1,024 at 37, so the default
-    sample is the 432-atom cell, about the largest whose warm-up and timed steps fit the budget."""
+def cpu_baseline(budget_s: float = 30.0, model_kw: dict | None = None, stress: bool = True, n_rep: int = 16) -> dict:
+    """float32 torch-CPU oracle (reference-algorithm restatement) on a bcc Fe n_rep^3 cell, E+F+S:
+    by default the headline cell itself (8,192 atoms, ~35 s per step on 16 EPYC cores, ~70 GB of
+    host memory), timed for one step (more while within budget_s) after a warm-up on a 4^3 cell.
+    The oracle's cost per atom grows with the cell (its eager element-wise passes leave the
+    caches: 16 cores ran 128 atoms at 520-590 atom-steps/s, 432 at 364, 1,024 at 273 and 3,456 at
+    241), so a small cell would overstate it.  With less free host memory than the cell needs,
+    the largest of 12^3 / 8^3 that fits is timed instead (the sample field says which)."""
     import torch
     import escn_md
     import heads
@@ -78,11 +80,26 @@ def cpu_baseline(budget_s: float = 20.0, model_kw: dict | None = None, stress: b
     affinity = len(os.sched_getaffinity(0))
     cores = min(affinity, int(os.environ.get("OMP_NUM_THREADS", affinity)))
     torch.set_num_threads(cores)
+    try:
+        import psutil
+        avail = psutil.virtual_memory().available
+    except ImportError:
+        avail = float("inf")
+    # ~9 MB of host memory per atom at lmax 2 (measured: 10.2 GB at 1,024 atoms, 29.6 at 3,456)
+    per_atom = 9e6 * (1 if not model_kw else 6)
+    for cand in (n_rep, 12, 8, 6, 4):
+        if cand <= n_rep and 2 * cand ** 3 * per_atom * 1.5 <= avail:
+            n_rep = cand
+            break
+    else:
+        n_rep = 4
     bb = escn_md.eSCNMDBackbone(seed=0, **(model_kw or {}))
     hd = heads.MLPEnergyHead(bb.sphere_channels, bb.hidden_channels, seed=1)
+    w = systems.bcc_fe(n_rep=4)
+    wei, woff = systems.neighbor_list(w.pos, w.cell, w.pbc, bb.cutoff, bb.max_neighbors)
+    energy_forces_stress(bb, hd, w.pos, w.Z, w.cell, wei, woff, dtype=torch.float32, stress=stress)   # warm-up
     s = systems.bcc_fe(n_rep=n_rep)
     ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, bb.cutoff, bb.max_neighbors)
-    energy_forces_stress(bb, hd, s.pos, s.Z, s.cell, ei, off, dtype=torch.float32, stress=stress)   # warm-up
     times = []
     t_start = time.perf_counter()
     while len(times) < 5 and (not times or time.perf_counter() - t_start < budget_s):
@@ -104,7 +121,7 @@ def cpu_baseline(budget_s: float = 20.0, model_kw: dict | None = None, stress: b
             "sample": f"bcc Fe {n_rep}x{n_rep}x{n_rep} ({s.n_atoms} atoms, {ei.shape[1]} edges), "
                       f"{'E+F+S' if stress else 'E+F'}, "
                       f"lmax={bb.lmax}, {bb.num_layers} layers, float32 torch-CPU oracle "
-                      f"(oracle/model_ref.py), median of {len(times)} steps after 1 warm-up; CPU: {model}"}
+                      f"(oracle/model_ref.py), median of {len(times)} step(s) after a 4x4x4 warm-up; CPU: {model}"}
 
 
 def main() -> None:
@@ -229,8 +246,8 @@ def main() -> None:
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (float32 torch-CPU oracle) ...")
-        # lmax 4 with 8 layers costs ~10x more per atom on the CPU: the 128-atom cell there
-        cpu = cpu_baseline(model_kw=model_kw, stress=with_stress, n_rep=4 if model_kw else 6)
+        # lmax 4 with 8 layers costs ~10x more per atom on the CPU: a 6^3 cell there
+        cpu = cpu_baseline(model_kw=model_kw, stress=with_stress, n_rep=6 if model_kw else 16)
         log(f"[bench] CPU baseline: {cpu['value']} atom-steps/s on {cpu['cores']} cores")
 
     rec = {
