@@ -229,7 +229,7 @@ def main() -> None:
         rl = {"kernel": dom, "bound": d["bound"], "achieved": d["achieved"], "peak": d["peak"], "unit": d["unit"],
               "frac": d["frac"], "traffic": None}
         if "matrix_op" in d:
-            rl.update(matrix_op=d["matrix_op"], fp32_tflops=d["fp32_tflops"])
+            rl.update(matrix_op=d["matrix_op"], fp32_tflops=d["fp32_tflops"], roofline_frac=d["roofline_frac"])
         # HBM bytes per launch of the dominant kernel from two rocprofv3 counter passes
         # (FETCH_SIZE, WRITE_SIZE; profiles/<config>_pmc_traffic.md), labelled with the
         # commit they were measured at: counters cannot be read inside this process

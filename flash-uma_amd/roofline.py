@@ -260,17 +260,32 @@ MFMA_BOUND = {"fu_linear", "fu_linear_batched", "fu_complex_linear", "fu_linear_
 
 def summarize(durations, matmul_mode: int = MATMUL_SPLIT_BF16) -> dict:
     """Per entry point: calls, total/avg ms, algorithmic bytes/flops per launch and the
-    achieved fraction of the bounding roofline (matrix-core kernels in `matmul_mode`)."""
+    achieved fraction of the bounding roofline (matrix-core kernels in `matmul_mode`).
+
+    For the matrix-core entry points `frac` is the executed rate against the matrix peak.
+    `roofline_frac` is the standard roofline reading: the sum over launches of
+    max(executed flops / matrix peak, algorithmic bytes / HBM peak) over the measured time,
+    which differs from `frac` where a launch's arithmetic intensity puts it under the HBM
+    slope (the K = 128 shapes, whose operands and output are as large as their work);
+    `hbm_bound_launches` counts those launches."""
+    if matmul_mode == MATMUL_FP32:
+        mul, mpeak = 1, FP32_MFMA_PEAK_TFLOPS
+    else:
+        mul, mpeak = SPLIT_PRODUCTS, BF16_MFMA_PEAK_TFLOPS
     agg: dict = {}
     for name, args, ms in durations:
         if name not in WORK:
             continue
         nbytes, flops = WORK[name](args)
-        a = agg.setdefault(name, {"calls": 0, "ms": 0.0, "bytes": 0, "flops": 0})
+        a = agg.setdefault(name, {"calls": 0, "ms": 0.0, "bytes": 0, "flops": 0, "ideal_s": 0.0, "hbm_bound": 0})
         a["calls"] += 1
         a["ms"] += ms
         a["bytes"] += nbytes
         a["flops"] += flops
+        if name in MFMA_BOUND:
+            t_mfma, t_hbm = mul * flops / (mpeak * 1e12), nbytes / (HBM_PEAK_GBS * 1e9)
+            a["ideal_s"] += max(t_mfma, t_hbm)
+            a["hbm_bound"] += int(t_hbm > t_mfma)
     out = {}
     for name, a in agg.items():
         sec = a["ms"] / 1e3
@@ -283,7 +298,9 @@ def summarize(durations, matmul_mode: int = MATMUL_SPLIT_BF16) -> dict:
                 ach, peak, op = SPLIT_PRODUCTS * fp32_rate, BF16_MFMA_PEAK_TFLOPS, "bf16 mfma, 6 products per fp32 product"
             rec.update(bound="mfma", unit="TFLOP/s", achieved=round(ach, 2), peak=peak, frac=round(ach / peak, 4),
                        matrix_op=op, fp32_tflops=round(fp32_rate, 2), flops_per_launch=a["flops"] // a["calls"],
-                       hbm_gbs=round(a["bytes"] / sec / 1e9, 1) if sec > 0 else 0.0)
+                       hbm_gbs=round(a["bytes"] / sec / 1e9, 1) if sec > 0 else 0.0,
+                       roofline_frac=round(a["ideal_s"] / sec, 4) if sec > 0 else 0.0,
+                       hbm_bound_launches=a["hbm_bound"])
         else:
             ach = a["bytes"] / sec / 1e9 if sec > 0 else 0.0
             rec.update(bound="hbm", unit="GB/s", achieved=round(ach, 1), peak=HBM_PEAK_GBS,

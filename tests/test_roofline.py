@@ -65,3 +65,33 @@ def test_split_mode_accounting():
     assert fp32["peak"] == 157.3 and abs(fp32["achieved"] - rate) < 0.01
     assert split["peak"] == 2500.0 and abs(split["achieved"] - 6 * rate) < 0.05
     assert abs(split["fp32_tflops"] - rate) < 0.01
+
+
+def test_roofline_frac_takes_the_larger_of_the_two_bounds():
+    """roofline_frac = sum over launches of max(executed flops / matrix peak, bytes / HBM peak)
+    over the measured time: equal to frac for a high-intensity GEMM, larger where the launch
+    sits under the HBM slope (K = 128 with as many output columns as input)."""
+    import roofline
+    big = _args("fu_linear", M=245760, N=640, K=768)
+    small = _args("fu_linear_batched", M=245760, N=128, K=128, batch=5)
+    ms = 1.0
+    r = roofline.summarize([("fu_linear", big, ms)])["fu_linear"]
+    assert r["hbm_bound_launches"] == 0 and abs(r["roofline_frac"] - r["frac"]) < 1e-3
+    nbytes, flops = roofline.WORK["fu_linear_batched"](small)
+    t_hbm = nbytes / (roofline.HBM_PEAK_GBS * 1e9)
+    t_mfma = 6 * flops / (roofline.BF16_MFMA_PEAK_TFLOPS * 1e12)
+    assert t_hbm > t_mfma
+    r = roofline.summarize([("fu_linear_batched", small, ms)])["fu_linear_batched"]
+    assert r["hbm_bound_launches"] == 1 and abs(r["roofline_frac"] - t_hbm / 1e-3) < 1e-3
+
+
+@pytest.mark.parametrize("name,sizes,per_edge", [
+    ("fu_scatter_bwd", dict(E=1000, N=50, C=128), (34 + 1) * 4),
+    ("fu_init_scatter_bwd", dict(E=1000, N=50, C=128), (8 + 1) * 4),
+    ("fu_gather_bwd", dict(E=1000, N=50, C=128), 34 * 4),
+])
+def test_accumulating_calls_count_the_read_back(name, sizes, per_edge):
+    import roofline
+    b0, _ = roofline.WORK[name](_args(name, **sizes, accumulate=0))
+    b3, _ = roofline.WORK[name](_args(name, **sizes, accumulate=3))
+    assert b3 - b0 == sizes["E"] * per_edge
