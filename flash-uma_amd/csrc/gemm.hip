@@ -79,6 +79,39 @@ struct Resid {
   int64_t sR;
 };
 
+// LayerNorm + SiLU epilogues over groups of LN_D = 128 columns (the radial-MLP hidden layers,
+// ops/ln_silu.py:29-123, in the grouped form of fu_ln_silu_grouped_*).  Each N-tile is one
+// group: group g = n_tile + batch index (a launch has either several N-tiles or several
+// batches).  The LayerNorm input of row e, group g, column c is
+//   v = (A W^T)[e][c] (+ GEMM bias) + tab_src[z[isrc[e]]][gD + c] + tab_dst[z[idst[e]]][gD + c]
+//       + ln_bias[gD + c]
+// (tables and ln_bias optional).  MODE 3 writes silu(LN(v) gamma + beta) to Y, the row
+// statistics to mean / rstd[e G + g] and, when pre is set, the GEMM output (before tables
+// and ln_bias) to pre (batch stride s_pre).  MODE 4 is the input gradient: with the forward's
+// mean / rstd and the output gradient g_out (row stride ldgo, group g at column gD), Y
+// receives dL/dv.
+constexpr int LN_D = 128;
+struct LnEpi {
+  const float* tab_src;
+  const float* tab_dst;
+  int64_t ldt;
+  const int64_t* z;
+  const int64_t* isrc;
+  const int64_t* idst;
+  const float* ln_bias;
+  const float* gamma;
+  const float* beta;
+  float* mean;
+  float* rstd;
+  int32_t G;
+  float eps;
+  float* pre;
+  int64_t ldpre;
+  int64_t s_pre;
+  const float* g_out;
+  int64_t ldgo;
+};
+
 // Batch index blockIdx.y offsets A, W and Y by sA, sW and sY floats; bias (stride sBias) is
 // added in batches [0, bias_batches).
 //
@@ -95,12 +128,13 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
                                                           int32_t bias_batches, float* __restrict__ Y, int64_t ldy,
                                                           int64_t sY, int64_t M, int32_t N, int32_t K,
                                                           int32_t n_tiles, int64_t total_tiles, GateOut go,
-                                                          GateBwd gb, Resid rs) {
+                                                          GateBwd gb, Resid rs, LnEpi ln) {
   {
     const int64_t bt = blockIdx.y;
     A += bt * sA;
     W += bt * sW;
     Y += bt * sY;
+    if (ln.pre) ln.pre += bt * ln.s_pre;
     bias = (bias != nullptr && bt < bias_batches) ? bias + bt * sBias : nullptr;
     if (rs.R) rs.R += bt * rs.sR;
   }
@@ -282,6 +316,125 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
   // row 8*(r/4) + 4*(l/32) + r%4.
   const int oc = lane & 31;
   const int orow = (lane >> 5) * 4;
+  if constexpr (MODE == 3 || MODE == 4) {
+    // The two waves of a row half (2p: columns 0-63, 2p + 1: columns 64-127 of the group)
+    // stage one 32-row slab each; then each of them normalises 16 of the slab's rows, 32
+    // lanes per row and 4 columns per lane, with 32-lane butterfly sums for the statistics.
+    const int grp = (int)blockIdx.y + n_tile;
+    const int pair = wave >> 1;
+    const float* wsl = smem + (2 * pair) * 32 * GES;
+    const float* wsr = smem + (2 * pair + 1) * 32 * GES;
+    const int sub = lane & 31, hl = lane >> 5;
+    const int cl = 4 * sub;
+    const float* src = (cl < 64 ? wsl : wsr) + (cl & 63);
+    const float4 gm = ld4(ln.gamma + grp * LN_D + cl), bt = ld4(ln.beta + grp * LN_D + cl);
+    float4 cb = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (bias) cb = ld4(bias + col0 + cl);
+    float4 lb = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (ln.ln_bias) lb = ld4(ln.ln_bias + grp * LN_D + cl);
+    float* ws = smem + wave * 32 * GES;
+    const bool tabs = ln.tab_src != nullptr;
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      // this wave's 16 rows of the slab: lane k < 16 fetches row k's element ids (two
+      // dependent loads) and, for the backward, its statistics, once per slab; each row's
+      // values are then taken by shuffle.  The table rows and g_out of a row pair are loaded
+      // one pair ahead of their use (the first before the slab is staged; loading all 8 pairs
+      // ahead measured slower for the backward, 616 against 553 us at bcc Fe)
+      const int64_t rbase = row0 + wr + i * 32 + (wave & 1) * 16;
+      int64_t rk = rbase + (lane & 15);
+      rk = rk < M ? rk : M - 1;
+      int zs = 0, zd = 0;
+      float mu = 0.0f, rsd = 0.0f;
+      if (tabs) {
+        zs = (int)ln.z[ln.isrc[rk]];
+        zd = (int)ln.z[ln.idst[rk]];
+      }
+      if constexpr (MODE == 4) {
+        mu = ln.mean[rk * ln.G + grp];
+        rsd = ln.rstd[rk * ln.G + grp];
+      }
+      // operands of row pair `it` (lanes 0-31: row 2 it, 32-63: row 2 it + 1)
+      auto fetch = [&](int it, float4& t, float4& go) {
+        const int k = 2 * it + hl;
+        const int64_t gr = rbase + k;
+        const int64_t rc = gr < M ? gr : M - 1;
+        t = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (tabs) {
+          const int a = __shfl(zs, k, 64), b = __shfl(zd, k, 64);
+          t = ld4(ln.tab_src + (int64_t)a * ln.ldt + grp * LN_D + cl) + ld4(ln.tab_dst + (int64_t)b * ln.ldt + grp * LN_D + cl);
+        }
+        if constexpr (MODE == 4) go = ld4(ln.g_out + rc * ln.ldgo + grp * LN_D + cl);
+      };
+      constexpr int PD = 2;   // ring of row-pair operands: PD - 1 pairs in flight
+      float4 tq[PD], gq[PD];
+#pragma unroll
+      for (int it = 0; it < PD - 1; ++it) fetch(it, tq[it], gq[it]);
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ws[(8 * (r >> 2) + orow + (r & 3)) * GES + j * 32 + oc] = acc[i][j][r];
+      __syncthreads();
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        if (it + PD - 1 < 8) fetch(it + PD - 1, tq[(it + PD - 1) % PD], gq[(it + PD - 1) % PD]);
+        const float4 tcur = tq[it % PD], gcur = gq[it % PD];
+        const int k = 2 * it + hl;
+        const int r = (wave & 1) * 16 + k;
+        const int64_t gr = rbase + k;
+        const bool live = gr < M;
+        // the same additions in the same order as fu_ln_silu_grouped_* on a stored product
+        const float4 p = ld4(src + r * GES) + cb;
+        float4 v = p;
+        if (tabs) v = v + tcur;
+        if (ln.ln_bias) v = v + lb;
+        if constexpr (MODE == 3) {
+          if (ln.pre && live) st4(ln.pre + gr * ln.ldpre + col0 + cl, p);
+          const float mean = group_sum<32>(v.x + v.y + v.z + v.w) / LN_D;
+          const float4 xc = make_float4(v.x - mean, v.y - mean, v.z - mean, v.w - mean);
+          const float var = group_sum<32>(xc.x * xc.x + xc.y * xc.y + xc.z * xc.z + xc.w * xc.w) / LN_D;
+          const float rstd = 1.0f / sqrtf(var + ln.eps);
+          float4 y;
+          y.x = xc.x * rstd * gm.x + bt.x;
+          y.y = xc.y * rstd * gm.y + bt.y;
+          y.z = xc.z * rstd * gm.z + bt.z;
+          y.w = xc.w * rstd * gm.w + bt.w;
+          if (live) {
+            st4(Y + gr * ldy + col0 + cl, make_float4(y.x * sigmoidf_(y.x), y.y * sigmoidf_(y.y),
+                                                      y.z * sigmoidf_(y.z), y.w * sigmoidf_(y.w)));
+            if (sub == 0) {
+              ln.mean[gr * ln.G + grp] = mean;
+              ln.rstd[gr * ln.G + grp] = rstd;
+            }
+          }
+        } else {
+          const float mean = __shfl(mu, k, 64), rstd = __shfl(rsd, k, 64);
+          const float4 go = gcur;
+          const float xh[4] = {(v.x - mean) * rstd, (v.y - mean) * rstd, (v.z - mean) * rstd, (v.w - mean) * rstd};
+          const float gg[4] = {gm.x, gm.y, gm.z, gm.w}, bb[4] = {bt.x, bt.y, bt.z, bt.w};
+          const float gov[4] = {go.x, go.y, go.z, go.w};
+          float gxh[4];
+          float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float y = xh[q] * gg[q] + bb[q];
+            const float sg = sigmoidf_(y);
+            gxh[q] = gov[q] * (sg + y * sg * (1.0f - sg)) * gg[q];
+            s1 += gxh[q];
+            s2 += gxh[q] * xh[q];
+          }
+          s1 = group_sum<32>(s1);
+          s2 = group_sum<32>(s2);
+          if (live)
+            st4(Y + gr * ldy + col0 + cl,
+                make_float4(rstd * (gxh[0] - (s1 + xh[0] * s2) / LN_D), rstd * (gxh[1] - (s1 + xh[1] * s2) / LN_D),
+                            rstd * (gxh[2] - (s1 + xh[2] * s2) / LN_D), rstd * (gxh[3] - (s1 + xh[3] * s2) / LN_D)));
+        }
+      }
+    }
+    return;
+  }
   if constexpr (MODE == 2) {
     // Stage 32-row slabs of g_Z in LDS; each lane then handles 16-byte pieces (4 channels of
     // one degree, inside one 32-channel group of the gate-paired order).
@@ -465,7 +618,7 @@ static int linear_launch(const float* A, int64_t lda, int64_t sA, const float* W
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
   auto kern = linear_kernel<0>(K, M);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, (unsigned)batch), dim3(256), 0, stream, A, lda, sA, W, ldw, sW, bias,
-                     sBias, bias_batches, Y, ldy, sY, M, N, K, n_tiles, total, GateOut{}, GateBwd{}, rs);
+                     sBias, bias_batches, Y, ldy, sY, M, N, K, n_tiles, total, GateOut{}, GateBwd{}, rs, LnEpi{});
   return check_launch(who);
 }
 
@@ -515,7 +668,7 @@ extern "C" int fu_linear_gate(const float* A, int64_t lda, const float* W, int64
   auto kern = linear_kernel<1>(K, M);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), A, lda,
                      (int64_t)0, W, ldw, (int64_t)0, bias, (int64_t)0, 1, Y, ldy, (int64_t)0, M, N, K, n_tiles, total,
-                     GateOut{Z, ldz, S, lds, C, lmax}, GateBwd{}, Resid{});
+                     GateOut{Z, ldz, S, lds, C, lmax}, GateBwd{}, Resid{}, LnEpi{});
   return check_launch(who);
 }
 
@@ -543,6 +696,87 @@ extern "C" int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* W
   auto kern = linear_kernel<2>(K, M);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), gZo, ldgz,
                      (int64_t)0, Wt, ldw, (int64_t)0, (const float*)nullptr, (int64_t)0, 1, gY0, ldg, (int64_t)0, M, N,
-                     K, n_tiles, total, GateOut{}, GateBwd{Y0, ldy0, P1, ldp1, P2, ldp2, C, lmax}, Resid{});
+                     K, n_tiles, total, GateOut{}, GateBwd{Y0, ldy0, P1, ldp1, P2, ldp2, C, lmax}, Resid{}, LnEpi{});
+  return check_launch(who);
+}
+
+// Shared checks of the LayerNorm-SiLU GEMMs: whole 128-column groups, one per N-tile or per
+// batch, and the LayerNorm operands.
+static int ln_epi_check(const char* who, int64_t M, int32_t N, int32_t batch, int32_t G, const float* tab_src,
+                        const float* tab_dst, int64_t ldt, const int64_t* z, const int64_t* isrc, const int64_t* idst,
+                        const float* ln_bias, const float* gamma, const float* beta, const float* mean,
+                        const float* rstd) {
+  if (N % LN_D != 0 || G < 1 || !((batch == 1 && N == LN_D * G) || (N == LN_D && batch == G)))
+    return set_error(FU_ERR_UNSUPPORTED,
+                     "%s: N=%d, batch=%d, G=%d: the row must be G groups of 128 columns, one per N-tile or per batch",
+                     who, N, batch, G);
+  if (M == 0) return FU_OK;  // no rows: the per-row arrays may be empty (NULL)
+  if (!gamma || !beta || !mean || !rstd) return set_error(FU_ERR_NULL, "%s: NULL LayerNorm operand", who);
+  if (tab_src && (!tab_dst || !z || !isrc || !idst || ldt < (int64_t)G * LN_D || ldt % 4 != 0))
+    return set_error(FU_ERR_SHAPE, "%s: element tables need tab_dst, z, isrc, idst and ldt >= %d (multiple of 4)", who,
+                     G * LN_D);
+  if (!aligned16(gamma) || !aligned16(beta) || (ln_bias && !aligned16(ln_bias)) ||
+      (tab_src && (!aligned16(tab_src) || !aligned16(tab_dst))))
+    return set_error(FU_ERR_ALIGN, "%s: gamma, beta, ln_bias and the tables must be 16-byte aligned", who);
+  return FU_OK;
+}
+
+extern "C" int fu_linear_ln_silu(const float* A, int64_t lda, int64_t stride_a, const float* W, int64_t ldw,
+                                 int64_t stride_w, const float* bias, int64_t stride_bias, int32_t bias_batches,
+                                 float* Y, int64_t ldy, int64_t stride_y, float* pre, int64_t ldpre, int64_t stride_pre,
+                                 int64_t M, int32_t N, int32_t K, int32_t batch, const float* tab_src,
+                                 const float* tab_dst, int64_t ldt, const int64_t* z, const int64_t* isrc,
+                                 const int64_t* idst, const float* ln_bias, const float* gamma, const float* beta,
+                                 float* mean, float* rstd, int32_t G, float eps, void* stream) {
+  const char* who = "fu_linear_ln_silu";
+  int st = linear_check(A, lda, W, ldw, Y, ldy, M, N, K, who);
+  if (st != FU_OK) return st;
+  if (batch < 1 || batch > 65535) return set_error(FU_ERR_SHAPE, "%s: batch=%d out of range", who, batch);
+  st = ln_epi_check(who, M, N, batch, G, tab_src, tab_dst, ldt, z, isrc, idst, ln_bias, gamma, beta, mean, rstd);
+  if (st != FU_OK) return st;
+  if ((stride_a | stride_w | stride_y | stride_pre) % 4 != 0 || stride_a < 0 || stride_w < 0 || stride_y < 0 ||
+      stride_pre < 0)
+    return set_error(FU_ERR_ALIGN, "%s: batch strides must be non-negative multiples of 4", who);
+  if (pre && (ldpre < N || ldpre % 4 != 0 || !aligned16(pre)))
+    return set_error(FU_ERR_ALIGN, "%s: pre must be 16-byte aligned with ldpre >= N, a multiple of 4", who);
+  if (bias && !aligned16(bias)) return set_error(FU_ERR_ALIGN, "%s: bias must be 16-byte aligned", who);
+  if (M == 0) return FU_OK;
+  const int n_tiles = (N + GBN - 1) / GBN;
+  const int64_t bm = linear_tile_rows(M);
+  const int64_t total = ((M + bm - 1) / bm) * n_tiles;
+  if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
+  auto kern = linear_kernel<3>(K, M);
+  hipLaunchKernelGGL(kern, dim3((unsigned)total, (unsigned)batch), dim3(256), 0, as_stream(stream), A, lda, stride_a,
+                     W, ldw, stride_w, bias, stride_bias, bias_batches, Y, ldy, stride_y, M, N, K, n_tiles, total,
+                     GateOut{}, GateBwd{}, Resid{},
+                     LnEpi{tab_src, tab_dst, ldt, z, isrc, idst, ln_bias, gamma, beta, mean, rstd, G, eps, pre, ldpre,
+                           stride_pre, nullptr, 0});
+  return check_launch(who);
+}
+
+extern "C" int fu_linear_ln_silu_bwd(const float* A, int64_t lda, const float* W, int64_t ldw, float* g_x, int64_t ldgx,
+                                     int64_t M, int32_t N, int32_t K, const float* g_out, int64_t ldgo,
+                                     const float* tab_src, const float* tab_dst, int64_t ldt, const int64_t* z,
+                                     const int64_t* isrc, const int64_t* idst, const float* ln_bias,
+                                     const float* gamma, const float* beta, const float* mean, const float* rstd,
+                                     int32_t G, void* stream) {
+  const char* who = "fu_linear_ln_silu_bwd";
+  int st = linear_check(A, lda, W, ldw, g_x, ldgx, M, N, K, who);
+  if (st != FU_OK) return st;
+  st = ln_epi_check(who, M, N, 1, G, tab_src, tab_dst, ldt, z, isrc, idst, ln_bias, gamma, beta, mean, rstd);
+  if (st != FU_OK) return st;
+  if (M == 0) return FU_OK;
+  if (!g_out || ldgo < N || ldgo % 4 != 0 || !aligned16(g_out))
+    return set_error(FU_ERR_ALIGN, "%s: g_out must be 16-byte aligned with ldgo >= N, a multiple of 4", who);
+  const int n_tiles = (N + GBN - 1) / GBN;
+  const int64_t bm = linear_tile_rows(M);
+  const int64_t total = ((M + bm - 1) / bm) * n_tiles;
+  if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
+  auto kern = linear_kernel<4>(K, M);
+  hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), A, lda, (int64_t)0, W, ldw,
+                     (int64_t)0, (const float*)nullptr, (int64_t)0, 0, g_x, ldgx, (int64_t)0, M, N, K, n_tiles, total,
+                     GateOut{}, GateBwd{}, Resid{},
+                     LnEpi{tab_src, tab_dst, ldt, z, isrc, idst, ln_bias, gamma, beta, const_cast<float*>(mean),
+                           const_cast<float*>(rstd), G, 0.0f, nullptr, 0, 0, g_out, ldgo});
   return check_launch(who);
 }

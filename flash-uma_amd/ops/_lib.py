@@ -51,6 +51,10 @@ SIGNATURES: dict[str, list] = {
     "fu_linear_gate": [P, I64, P, I64, P, P, I64, P, I64, P, I64, I64, I32, I32, I32, P],
     "fu_complex_linear_gate": [P, P, I64, P, P, I64, P, P, P, I64, P, P, I64, P, I64, I32, I32, I64, I32, I32, P],
     "fu_linear_gate_bwd": [P, I64, P, I64, P, I64, P, I64, P, I64, P, I64, I64, I32, I32, I32, P],
+    "fu_linear_ln_silu": [P, I64, I64, P, I64, I64, P, I64, I32, P, I64, I64, P, I64, I64, I64, I32, I32, I32,
+                          P, P, I64, P, P, P, P, P, P, P, P, I32, F32, P],
+    "fu_linear_ln_silu_bwd": [P, I64, P, I64, P, I64, I64, I32, I32, P, I64, P, P, I64, P, P, P, P, P, P, P, P,
+                              I32, P],
     "fu_complex_linear_gate_bwd": [P, P, I64, P, P, I64, P, P, P, I64, P, P, I64, P, I64, I32, I32, P, I64, I64, I32, I32, P],
     "fu_rms_norm_sh_fwd": [P, P, P, P, P, I64, I32, I32, F32, P],
     "fu_rms_norm_sh_bwd": [P, P, P, P, P, P, I64, I32, I32, P],

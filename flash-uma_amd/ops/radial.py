@@ -57,6 +57,65 @@ def _batched(A, W, bias, G, C_in, C_out, out):
     return out
 
 
+# Channel count of the one-kernel GEMM + LayerNorm-SiLU path (one 128-column GEMM tile per
+# LayerNorm group); other widths run the GEMM and the grouped LayerNorm kernel one after the other.
+LN_FUSED_C = 128
+
+
+def _layer1_fwd(gauss, bank, Z, idx_i, idx_j):
+    """h1 = silu(LN(gauss W1g^T + tables + b1)) per group: (h1, mean1, rstd1)."""
+    E, G, C = gauss.shape[0], bank.G, bank.C
+    dev = gauss.device
+    tabs = (bank.tab_src, bank.tab_tgt)
+    if C != LN_FUSED_C:
+        p1 = _gemm(gauss, bank.W1g, None, torch.empty(E, G * C, device=dev, dtype=torch.float32))
+        return _ln_grouped_fwd(p1, tabs, Z, idx_i, idx_j, bank.b1, bank.gamma1, bank.beta1, G, C, bank.eps)
+    h1 = torch.empty(E, G * C, device=dev, dtype=torch.float32)
+    m1 = torch.empty(E * G, device=dev, dtype=torch.float32)
+    r1 = torch.empty(E * G, device=dev, dtype=torch.float32)
+    _lib.call("fu_linear_ln_silu", gauss.data_ptr(), gauss.stride(0), 0, bank.W1g.data_ptr(), bank.W1g.stride(0), 0,
+              None, 0, 0, h1.data_ptr(), h1.stride(0), 0, None, 0, 0, E, G * C, bank.B, 1,
+              bank.tab_src.data_ptr(), bank.tab_tgt.data_ptr(), bank.tab_src.stride(0), Z.data_ptr(),
+              idx_i.data_ptr(), idx_j.data_ptr(), bank.b1.data_ptr(), bank.gamma1.data_ptr(), bank.beta1.data_ptr(),
+              m1.data_ptr(), r1.data_ptr(), G, float(bank.eps), _lib.stream_ptr(dev))
+    return h1, m1, r1
+
+
+def _layer2_fwd(h1, bank):
+    """p2 = h1_g W2_g^T + b2_g per group, h2 = silu(LN(p2)): (h2, mean2, rstd2, p2)."""
+    E, G, C = h1.shape[0], bank.G, bank.C
+    if C != LN_FUSED_C:
+        p2 = _batched(h1, bank.W2, bank.b2, G, C, C, torch.empty_like(h1))
+        h2, m2, r2 = _ln_grouped_fwd(p2, None, None, None, None, None, bank.gamma2, bank.beta2, G, C, bank.eps)
+        return h2, m2, r2, p2
+    dev = h1.device
+    h2, p2 = torch.empty_like(h1), torch.empty_like(h1)
+    m2 = torch.empty(E * G, device=dev, dtype=torch.float32)
+    r2 = torch.empty(E * G, device=dev, dtype=torch.float32)
+    _lib.call("fu_linear_ln_silu", h1.data_ptr(), h1.stride(0), C, bank.W2.data_ptr(), C, C * C, bank.b2.data_ptr(),
+              C, G, h2.data_ptr(), h2.stride(0), C, p2.data_ptr(), p2.stride(0), C, E, C, C, G,
+              None, None, 0, None, None, None, None, bank.gamma2.data_ptr(), bank.beta2.data_ptr(),
+              m2.data_ptr(), r2.data_ptr(), G, float(bank.eps), _lib.stream_ptr(dev))
+    return h2, m2, r2, p2
+
+
+def _layer1_bwd(gauss, bank, Z, idx_i, idx_j, m1, r1, g_h1):
+    """dL/d(first-layer LayerNorm input) from g_h1, recomputing gauss W1g^T."""
+    E, G, C = gauss.shape[0], bank.G, bank.C
+    dev = gauss.device
+    tabs = (bank.tab_src, bank.tab_tgt)
+    if C != LN_FUSED_C:
+        p1 = _gemm(gauss, bank.W1g, None, torch.empty(E, G * C, device=dev, dtype=torch.float32))
+        return _ln_grouped_bwd(p1, tabs, Z, idx_i, idx_j, bank.b1, bank.gamma1, bank.beta1, m1, r1, g_h1, G, C)
+    g_p1 = torch.empty(E, G * C, device=dev, dtype=torch.float32)
+    _lib.call("fu_linear_ln_silu_bwd", gauss.data_ptr(), gauss.stride(0), bank.W1g.data_ptr(), bank.W1g.stride(0),
+              g_p1.data_ptr(), g_p1.stride(0), E, G * C, bank.B, g_h1.data_ptr(), g_h1.stride(0),
+              bank.tab_src.data_ptr(), bank.tab_tgt.data_ptr(), bank.tab_src.stride(0), Z.data_ptr(),
+              idx_i.data_ptr(), idx_j.data_ptr(), bank.b1.data_ptr(), bank.gamma1.data_ptr(), bank.beta1.data_ptr(),
+              m1.data_ptr(), r1.data_ptr(), G, _lib.stream_ptr(dev))
+    return g_p1
+
+
 def _gemm(A, W, bias, out):
     M, K = A.shape
     N = W.shape[0]
@@ -160,19 +219,17 @@ class _RadialTrunkFn(torch.autograd.Function):
         dev = gauss.device
         if gauss.shape[1] != bank.B:
             raise _lib.FlashUMAError(f"radial bank: expected {bank.B} Gaussians per edge, got {gauss.shape[1]}")
-        tabs = (bank.tab_src, bank.tab_tgt)
-        p1 = _gemm(gauss, bank.W1g, None, torch.empty(E, G * C, device=dev, dtype=torch.float32))
-        h1, m1, r1 = _ln_grouped_fwd(p1, tabs, Z, idx_i, idx_j, bank.b1, bank.gamma1, bank.beta1, G, C, bank.eps)
-        p2 = _batched(h1, bank.W2, bank.b2, G, C, C, torch.empty_like(h1))
+        # each hidden layer is one kernel at C = 128: the GEMM's epilogue applies the
+        # LayerNorm-SiLU (the first layer's (E, G*C) product is never stored)
+        h1, m1, r1 = _layer1_fwd(gauss, bank, Z, idx_i, idx_j)
+        h2, m2, r2, p2 = _layer2_fwd(h1, bank)
         del h1
-        h2, m2, r2 = _ln_grouped_fwd(p2, None, None, None, None, None, bank.gamma2, bank.beta2, G, C, bank.eps)
         # the trunk gradient buffer is allocated by the first output-layer backward, not here:
         # it is not needed before the backward, and the forward's end is a memory peak
         holder.shape = tuple(p2.shape) if ctx.needs_input_grad[0] else None
         holder.device = p2.device
-        # p1 (E, G*C) is not kept: the backward recomputes it from the (E, B) Gaussians with
-        # the K = B GEMM (10x fewer bytes held through the step for one small GEMM)
-        del p1
+        # the first layer's product (E, G*C) is not kept: the backward recomputes it from the
+        # (E, B) Gaussians with the K = B GEMM (10x fewer bytes held through the step)
         ctx.save_for_backward(gauss, m1, r1, p2, m2, r2, Z, idx_i, idx_j)
         ctx.bank, ctx.holder = bank, holder
         return tuple(h2[:, k * C:(k + 1) * C] for k in range(G))
@@ -194,10 +251,8 @@ class _RadialTrunkFn(torch.autograd.Function):
         del g_h2
         g_h1 = _batched(g_p2, bank.W2_t, None, G, C, C, torch.empty_like(g_p2))
         del g_p2
-        p1 = _gemm(gauss, bank.W1g, None, torch.empty(E, G * C, device=gauss.device, dtype=torch.float32))
-        g_p1 = _ln_grouped_bwd(p1, (bank.tab_src, bank.tab_tgt), Z, idx_i, idx_j, bank.b1, bank.gamma1, bank.beta1,
-                               m1, r1, g_h1, G, C)
-        del g_h1, p1
+        g_p1 = _layer1_bwd(gauss, bank, Z, idx_i, idx_j, m1, r1, g_h1)
+        del g_h1
         g_gauss = _gemm(g_p1, bank.W1g_t, None, torch.empty(E, bank.B, device=gauss.device, dtype=torch.float32))
         return g_gauss, None, None, None, None, None
 

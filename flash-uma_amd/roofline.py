@@ -183,6 +183,22 @@ def _linear_batched(a):
     return 4 * B * (M * K + M * N + N * K + r), 2 * B * M * N * K
 
 
+def _linear_ln_silu(a):
+    # the GEMM (batch B) plus the LayerNorm epilogue: Y written once (pre too when stored),
+    # the statistics, and with tables two int64 edge ids per row (tables L2-resident)
+    M, N, K, B, G = a[15], a[16], a[17], a[18], a[30]
+    pre = B * M * N if a[12] else 0
+    tab = M * 16 if a[19] else 0
+    return 4 * (B * (M * K + M * N + N * K) + pre) + 8 * M * G + tab, 2 * B * M * N * K
+
+
+def _linear_ln_silu_bwd(a):
+    # the recomputed GEMM plus the LayerNorm backward epilogue: g_out read, g_x written
+    M, N, K, G = a[6], a[7], a[8], a[22]
+    tab = M * 16 if a[11] else 0
+    return 4 * (M * K + N * K + 2 * M * N) + 8 * M * G + tab, 2 * M * N * K
+
+
 def _complex_linear(a):
     # three real (M x Kc) x (Kc x Nc) products (the packed real form of the reference would be
     # four; so is the split path without a pre-split weight, which executes 4/3 of this)
@@ -237,6 +253,8 @@ WORK = {
     "fu_ln_silu_grouped_bwd": _ln_grouped_bwd,
     "fu_linear": _linear,
     "fu_linear_batched": _linear_batched,
+    "fu_linear_ln_silu": _linear_ln_silu,
+    "fu_linear_ln_silu_bwd": _linear_ln_silu_bwd,
     "fu_complex_linear": _complex_linear,
     "fu_linear_gate": _linear_gate,
     "fu_linear_gate_bwd": _linear_gate_bwd,
@@ -255,7 +273,7 @@ WORK = {
 }
 
 MFMA_BOUND = {"fu_linear", "fu_linear_batched", "fu_complex_linear", "fu_linear_gate", "fu_complex_linear_gate",
-              "fu_linear_gate_bwd", "fu_complex_linear_gate_bwd"}
+              "fu_linear_gate_bwd", "fu_complex_linear_gate_bwd", "fu_linear_ln_silu", "fu_linear_ln_silu_bwd"}
 
 
 def summarize(durations, matmul_mode: int = MATMUL_SPLIT_BF16) -> dict:

@@ -209,6 +209,34 @@ int fu_ln_silu_grouped_bwd(const float* x, int64_t ldx, const float* tab_src, co
                            const float* mean, const float* rstd, const float* g_out, int64_t ldg,
                            float* g_x, int64_t ldgx, int64_t M, int32_t G, int32_t D, void* stream);
 
+/* A radial-MLP linear followed by its LayerNorm + SiLU in one kernel (model.py:147-149 with
+ * ops/ln_silu.py:29-76 per group): fu_linear / fu_linear_batched whose epilogue applies
+ * fu_ln_silu_grouped_fwd to the GEMM output instead of storing it.  Row e holds G groups of
+ * 128 columns, one per N-tile (batch = 1, N = 128 G) or one per batch (N = 128, batch = G,
+ * strides as in fu_linear_batched).  The LayerNorm input is the GEMM output (+ bias) plus the
+ * optional element-table rows and ln_bias, as in fu_ln_silu_grouped_fwd; Y receives the
+ * SiLU output, mean / rstd (M x G) the statistics, and pre (optional, batch stride
+ * stride_pre) the GEMM output before tables and ln_bias. */
+int fu_linear_ln_silu(const float* A, int64_t lda, int64_t stride_a, const float* W, int64_t ldw,
+                      int64_t stride_w, const float* bias, int64_t stride_bias, int32_t bias_batches,
+                      float* Y, int64_t ldy, int64_t stride_y, float* pre, int64_t ldpre,
+                      int64_t stride_pre, int64_t M, int32_t N, int32_t K, int32_t batch,
+                      const float* tab_src, const float* tab_dst, int64_t ldt, const int64_t* z,
+                      const int64_t* isrc, const int64_t* idst, const float* ln_bias,
+                      const float* gamma, const float* beta, float* mean, float* rstd, int32_t G,
+                      float eps, void* stream);
+
+/* The LayerNorm-SiLU input gradient fused the same way (ops/ln_silu.py:77-123 per group):
+ * the GEMM (batch 1, N = 128 G) recomputes the LayerNorm input's product part A W^T, and the
+ * epilogue applies fu_ln_silu_grouped_bwd with the forward's mean / rstd and the output
+ * gradient g_out (row stride ldgo), writing g_x. */
+int fu_linear_ln_silu_bwd(const float* A, int64_t lda, const float* W, int64_t ldw, float* g_x,
+                          int64_t ldgx, int64_t M, int32_t N, int32_t K, const float* g_out,
+                          int64_t ldgo, const float* tab_src, const float* tab_dst, int64_t ldt,
+                          const int64_t* z, const int64_t* isrc, const int64_t* idst,
+                          const float* ln_bias, const float* gamma, const float* beta,
+                          const float* mean, const float* rstd, int32_t G, void* stream);
+
 /* ------------------------------------------------------------------------------------
  * Dense contractions on fp32 MFMA (replaces torch F.linear at model.py:147-154,203-205)
  * ------------------------------------------------------------------------------------ */

@@ -61,6 +61,13 @@ def test_error_codes():
     assert st == -1  # ld_xe smaller than the embedding row width
     st, _ = _status("fu_scatter_fwd", *([None] * 9), 3, 3, 192, None)
     assert st == -2
+    # LayerNorm-SiLU GEMMs: whole 128-column groups, one per N-tile or per batch
+    st, msg = _status("fu_linear_ln_silu", None, 64, 0, None, 64, 0, None, 0, 0, None, 600, 0, None, 0, 0, 0, 600,
+                      64, 1, *([None] * 2), 0, *([None] * 8), 5, ctypes.c_float(1e-5), None)
+    assert st == -2 and "groups of 128" in msg
+    st, msg = _status("fu_linear_ln_silu", None, 640, 128, None, 128, 0, None, 0, 0, None, 640, 128, None, 0, 0, 0,
+                      128, 128, 4, *([None] * 2), 0, *([None] * 8), 5, ctypes.c_float(1e-5), None)
+    assert st == -2 and "groups of 128" in msg
     # accumulate flags: bit 0 (wigner rows), bit 1 (env); nothing else
     for name, args in (("fu_scatter_bwd", (*([None] * 12), 0, 5, 128)),
                        ("fu_init_scatter_bwd", (*([None] * 8), 0, 5, 128)),
@@ -115,6 +122,10 @@ def test_zero_rows_accept_empty_arrays():
         "fu_wigner_ext_bwd": (None, None, None, 0, 4, None),
         "fu_gating_fwd_lmax": (*([None] * 6), 0, 128, 4, None),
         "fu_scatter_bwd_lmax": (*([None] * 14), 0, 5, 128, 4, 0, None),
+        "fu_linear_ln_silu": (None, 64, 0, None, 64, 0, None, 0, 0, None, 640, 0, None, 0, 0, 0, 640, 64, 1,
+                              *([None] * 2), 0, *([None] * 8), 5, f(1e-5), None),
+        "fu_linear_ln_silu_bwd": (None, 64, None, 64, None, 640, 0, 640, 64, None, 640, *([None] * 2), 0,
+                                  *([None] * 8), 5, None),
     }
     for name, args in calls.items():
         st, msg = _status(name, *args)

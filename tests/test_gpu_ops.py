@@ -659,3 +659,56 @@ def test_complex_linear_cancellation_bound(cuda, presplit):
     assert rel_r < 5e-6
     if not presplit:
         assert rel_i < 5e-6
+
+
+@pytest.mark.parametrize("M", [1000, 70001])
+def test_linear_ln_silu_matches_two_kernels(cuda, matmul_mode, M):
+    """fu_linear_ln_silu / fu_linear_ln_silu_bwd (the radial MLP's hidden layers with the
+    LayerNorm-SiLU in the GEMM epilogue) against the GEMM followed by the grouped LayerNorm
+    kernels, on both tile heights (70,001 rows: 256-row tiles and a ragged last tile): the
+    first layer with element tables and LN bias (one group per N-tile), the second as a
+    batched GEMM with bias and the pre-LN product stored (one group per batch), and the
+    first layer's input gradient."""
+    from ops import _lib
+    from ops.radial import _batched, _gemm, _ln_grouped_bwd, _ln_grouped_fwd
+    g = torch.Generator(device=cuda).manual_seed(M)
+    G, C, B, N, eps = 5, 128, 64, 300, 1e-5
+    r = lambda *s: torch.randn(*s, device=cuda, generator=g)
+    gauss = torch.rand(M, B, device=cuda, generator=g)
+    W1, b1 = r(G * C, B) / B ** 0.5, r(G * C) * 0.1
+    ts, td = r(100, G * C) * 0.3, r(100, G * C) * 0.3
+    gm1, bt1 = r(G * C).abs() + 0.5, r(G * C) * 0.1
+    Z = torch.randint(1, 100, (N,), device=cuda, generator=g)
+    ii = torch.randint(0, N, (M,), device=cuda, generator=g)
+    jj = torch.randint(0, N, (M,), device=cuda, generator=g)
+    st = _lib.stream_ptr(cuda)
+    # layer 1 forward
+    p1 = _gemm(gauss, W1, None, torch.empty(M, G * C, device=cuda))
+    h1r, m1r, r1r = _ln_grouped_fwd(p1, (ts, td), Z, ii, jj, b1, gm1, bt1, G, C, eps)
+    h1, m1, r1 = torch.empty(M, G * C, device=cuda), torch.empty(M * G, device=cuda), torch.empty(M * G, device=cuda)
+    _lib.call("fu_linear_ln_silu", gauss.data_ptr(), B, 0, W1.data_ptr(), B, 0, None, 0, 0, h1.data_ptr(), G * C, 0,
+              None, 0, 0, M, G * C, B, 1, ts.data_ptr(), td.data_ptr(), G * C, Z.data_ptr(), ii.data_ptr(),
+              jj.data_ptr(), b1.data_ptr(), gm1.data_ptr(), bt1.data_ptr(), m1.data_ptr(), r1.data_ptr(), G, eps, st)
+    for got, ref, what in ((h1, h1r, "h1"), (m1, m1r, "mean1"), (r1, r1r, "rstd1")):
+        assert_close(got, ref, 2e-6, what)
+    # layer 2 forward: batched, GEMM bias, pre-LN product kept
+    W2, b2 = r(G, C, C) / C ** 0.5, r(G, C) * 0.1
+    gm2, bt2 = r(G * C).abs() + 0.5, r(G * C) * 0.1
+    p2r = _batched(h1r, W2, b2, G, C, C, torch.empty_like(h1r))
+    h2r, m2r, r2r = _ln_grouped_fwd(p2r, None, None, None, None, None, gm2, bt2, G, C, eps)
+    h2, p2 = torch.empty_like(h1r), torch.empty_like(h1r)
+    m2, r2 = torch.empty(M * G, device=cuda), torch.empty(M * G, device=cuda)
+    _lib.call("fu_linear_ln_silu", h1r.data_ptr(), G * C, C, W2.data_ptr(), C, C * C, b2.data_ptr(), C, G,
+              h2.data_ptr(), G * C, C, p2.data_ptr(), G * C, C, M, C, C, G, None, None, 0, None, None, None, None,
+              gm2.data_ptr(), bt2.data_ptr(), m2.data_ptr(), r2.data_ptr(), G, eps, st)
+    assert torch.equal(p2, p2r), "pre-LN product"
+    for got, ref, what in ((h2, h2r, "h2"), (m2, m2r, "mean2"), (r2, r2r, "rstd2")):
+        assert_close(got, ref, 2e-6, what)
+    # layer 1 input gradient with the product recomputed in the GEMM
+    g_h1 = r(M, G * C)
+    gref = _ln_grouped_bwd(p1, (ts, td), Z, ii, jj, b1, gm1, bt1, m1r, r1r, g_h1, G, C)
+    gx = torch.empty(M, G * C, device=cuda)
+    _lib.call("fu_linear_ln_silu_bwd", gauss.data_ptr(), B, W1.data_ptr(), B, gx.data_ptr(), G * C, M, G * C, B,
+              g_h1.data_ptr(), G * C, ts.data_ptr(), td.data_ptr(), G * C, Z.data_ptr(), ii.data_ptr(), jj.data_ptr(),
+              b1.data_ptr(), gm1.data_ptr(), bt1.data_ptr(), m1r.data_ptr(), r1r.data_ptr(), G, st)
+    assert_close(gx, gref, 2e-6, "layer-1 LayerNorm input gradient")

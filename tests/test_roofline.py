@@ -35,6 +35,8 @@ GEMMS = {
     "fu_complex_linear": (dict(M=1000, Nc=256, Kc=512), 6 * 1000 * 256 * 512),
     "fu_complex_linear_gate": (dict(M=1000, Nc=256, Kc=512), 6 * 1000 * 256 * 512),
     "fu_complex_linear_gate_bwd": (dict(M=1000, Nc=128, Kc=256), 6 * 1000 * 128 * 256),
+    "fu_linear_ln_silu": (dict(M=1000, N=128, K=128, batch=5, G=5), 2 * 5 * 1000 * 128 * 128),
+    "fu_linear_ln_silu_bwd": (dict(M=1000, N=640, K=64, G=5), 2 * 1000 * 640 * 64),
 }
 
 
