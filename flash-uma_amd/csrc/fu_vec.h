@@ -29,6 +29,44 @@ __device__ __forceinline__ Vec<CPL> vload(const float* p) {
   return r;
 }
 
+// vload with the nontemporal hint: for large read-once streams, so that they do not evict
+// rows that other waves read again (the node rows of a gather).
+template <int CPL>
+__device__ __forceinline__ Vec<CPL> vload_nt(const float* p) {
+  Vec<CPL> r;
+  if constexpr (CPL == 4) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4 t = __builtin_nontemporal_load(reinterpret_cast<const f4*>(p));
+    r.v[0] = t.x; r.v[1] = t.y; r.v[2] = t.z; r.v[3] = t.w;
+  } else if constexpr (CPL == 2) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const f2 t = __builtin_nontemporal_load(reinterpret_cast<const f2*>(p));
+    r.v[0] = t.x; r.v[1] = t.y;
+  } else {
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) r.v[k] = __builtin_nontemporal_load(p + k);
+  }
+  return r;
+}
+
+// vstore with the nontemporal hint: for large write-once streams that no kernel re-reads
+// while they could still sit in L2.
+template <int CPL>
+__device__ __forceinline__ void vstore_nt(float* p, const Vec<CPL>& a) {
+  if constexpr (CPL == 4) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4 v = {a.v[0], a.v[1], a.v[2], a.v[3]};
+    __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p));
+  } else if constexpr (CPL == 2) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const f2 v = {a.v[0], a.v[1]};
+    __builtin_nontemporal_store(v, reinterpret_cast<f2*>(p));
+  } else {
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) __builtin_nontemporal_store(a.v[k], p + k);
+  }
+}
+
 template <int CPL>
 __device__ __forceinline__ void vstore(float* p, const Vec<CPL>& a) {
   if constexpr (CPL == 4) {

@@ -113,7 +113,7 @@ __global__ __launch_bounds__(256) void gather_fwd_kernel(
     const float* rr = rad + e * 12 * C + c;
     Vec<CPL> r[12];
 #pragma unroll
-    for (int k = 0; k < 12; ++k) r[k] = vload<CPL>(rr + slot_rad<L>(k & 1, k >> 1) * C);
+    for (int k = 0; k < 12; ++k) r[k] = vload_nt<CPL>(rr + slot_rad<L>(k & 1, k >> 1) * C);
     float* o0 = X0 + e * 6 * C + c;
     float* o1 = X1 + e * 8 * C + c;
     float* o2 = X2 + e * 4 * C + c;
@@ -121,18 +121,18 @@ __global__ __launch_bounds__(256) void gather_fwd_kernel(
     constexpr int K0[3] = {0, 2, 6}, K1[4] = {3, 7, 1, 5}, K2[2] = {8, 4};
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
-      vstore(o0 + slot_m0<L>(0, q) * C, vmul(rs.r[K0[q]], r[2 * q]));
-      vstore(o0 + slot_m0<L>(1, q) * C, vmul(rt.r[K0[q]], r[2 * q + 1]));
+      vstore_nt(o0 + slot_m0<L>(0, q) * C, vmul(rs.r[K0[q]], r[2 * q]));
+      vstore_nt(o0 + slot_m0<L>(1, q) * C, vmul(rt.r[K0[q]], r[2 * q + 1]));
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      vstore(o1 + slot_m1<L>(0, q) * C, vmul(rs.r[K1[q]], r[6 + 2 * (q & 1)]));
-      vstore(o1 + slot_m1<L>(1, q) * C, vmul(rt.r[K1[q]], r[7 + 2 * (q & 1)]));
+      vstore_nt(o1 + slot_m1<L>(0, q) * C, vmul(rs.r[K1[q]], r[6 + 2 * (q & 1)]));
+      vstore_nt(o1 + slot_m1<L>(1, q) * C, vmul(rt.r[K1[q]], r[7 + 2 * (q & 1)]));
     }
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      vstore(o2 + slot_m2<L>(0, q) * C, vmul(rs.r[K2[q]], r[10]));
-      vstore(o2 + slot_m2<L>(1, q) * C, vmul(rt.r[K2[q]], r[11]));
+      vstore_nt(o2 + slot_m2<L>(0, q) * C, vmul(rs.r[K2[q]], r[10]));
+      vstore_nt(o2 + slot_m2<L>(1, q) * C, vmul(rt.r[K2[q]], r[11]));
     }
   }
 }
@@ -163,14 +163,14 @@ __device__ __forceinline__ void side_load(const float* __restrict__ gX0, const f
   const float* g1 = gX1 + e * 8 * C + c;
   const float* g2 = gX2 + e * 4 * C + c;
 #pragma unroll
-  for (int q = 0; q < 3; ++q) d.g[q] = vload<CPL>(g0 + slot_m0<L>(so, q) * C);
+  for (int q = 0; q < 3; ++q) d.g[q] = vload_nt<CPL>(g0 + slot_m0<L>(so, q) * C);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) d.g[3 + q] = vload<CPL>(g1 + slot_m1<L>(so, q) * C);
+  for (int q = 0; q < 4; ++q) d.g[3 + q] = vload_nt<CPL>(g1 + slot_m1<L>(so, q) * C);
 #pragma unroll
-  for (int q = 0; q < 2; ++q) d.g[7 + q] = vload<CPL>(g2 + slot_m2<L>(so, q) * C);
+  for (int q = 0; q < 2; ++q) d.g[7 + q] = vload_nt<CPL>(g2 + slot_m2<L>(so, q) * C);
   const float* rp = rad + e * 12 * C + c;
 #pragma unroll
-  for (int q = 0; q < 6; ++q) d.r[q] = vload<CPL>(rp + slot_rad<L>(so, q) * C);
+  for (int q = 0; q < 6; ++q) d.r[q] = vload_nt<CPL>(rp + slot_rad<L>(so, q) * C);
 }
 
 // v (the node's own row, csd added) is read from the wave's LDS copy, so that it holds no
@@ -195,12 +195,12 @@ __device__ __forceinline__ void side_apply(const SideEdge<CPL>& d, int64_t e, in
     rotate9(w, v, rv);
     // this side's radial gradients (reference blocks so, 2+so, ..., 10+so)
     float* gr = g_rad + e * 12 * C + c;
-    vstore(gr + slot_rad<L>(so, 0) * C, vmul(d.g[0], rv.r[0]));
-    vstore(gr + slot_rad<L>(so, 1) * C, vmul(d.g[1], rv.r[2]));
-    vstore(gr + slot_rad<L>(so, 2) * C, vmul(d.g[2], rv.r[6]));
-    vstore(gr + slot_rad<L>(so, 3) * C, vadd(vmul(d.g[3], rv.r[3]), vmul(d.g[5], rv.r[1])));
-    vstore(gr + slot_rad<L>(so, 4) * C, vadd(vmul(d.g[4], rv.r[7]), vmul(d.g[6], rv.r[5])));
-    vstore(gr + slot_rad<L>(so, 5) * C, vadd(vmul(d.g[7], rv.r[8]), vmul(d.g[8], rv.r[4])));
+    vstore_nt(gr + slot_rad<L>(so, 0) * C, vmul(d.g[0], rv.r[0]));
+    vstore_nt(gr + slot_rad<L>(so, 1) * C, vmul(d.g[1], rv.r[2]));
+    vstore_nt(gr + slot_rad<L>(so, 2) * C, vmul(d.g[2], rv.r[6]));
+    vstore_nt(gr + slot_rad<L>(so, 3) * C, vadd(vmul(d.g[3], rv.r[3]), vmul(d.g[5], rv.r[1])));
+    vstore_nt(gr + slot_rad<L>(so, 4) * C, vadd(vmul(d.g[4], rv.r[7]), vmul(d.g[6], rv.r[5])));
+    vstore_nt(gr + slot_rad<L>(so, 5) * C, vadd(vmul(d.g[7], rv.r[8]), vmul(d.g[8], rv.r[4])));
   }
   // gradient w.r.t. the rotated coefficients of this node's row
   Rows9<CPL> grv;

@@ -154,15 +154,15 @@ __global__ __launch_bounds__(256) void scatter_bwd_kernel(const float* __restric
     float* o0 = gZ0 + e * 3 * C + c;
     float* o1 = gZ1 + e * 4 * C + c;
     float* o2 = gZ2 + e * 2 * C + c;
-    vstore(o0, gz[0]);
-    vstore(o0 + C, gz[2]);
-    vstore(o0 + 2 * C, gz[6]);
-    vstore(o1, gz[3]);
-    vstore(o1 + C, gz[7]);
-    vstore(o1 + 2 * C, gz[1]);
-    vstore(o1 + 3 * C, gz[5]);
-    vstore(o2, gz[8]);
-    vstore(o2 + C, gz[4]);
+    vstore_nt(o0, gz[0]);
+    vstore_nt(o0 + C, gz[2]);
+    vstore_nt(o0 + 2 * C, gz[6]);
+    vstore_nt(o1, gz[3]);
+    vstore_nt(o1 + C, gz[7]);
+    vstore_nt(o1 + 2 * C, gz[1]);
+    vstore_nt(o1 + 3 * C, gz[5]);
+    vstore_nt(o2, gz[8]);
+    vstore_nt(o2 + C, gz[4]);
     // channel reductions: dL/dD1[a][b] = env sum_c zr[1+a] g[1+b], dL/dD2 likewise, and
     // dL/denv = sum_c sum_k g[k] (D^T zr)[k]
     float part[64];
@@ -283,9 +283,9 @@ __global__ __launch_bounds__(256) void init_scatter_bwd_kernel(const float* __re
       p2[q] = g[4][q] * w2[0] + g[5][q] * w2[1] + g[6][q] * w2[2] + g[7][q] * w2[3] + g[8][q] * w2[4];
     }
     float* gr = g_rad + e * 3 * C + c;
-    vstore(gr, vscale(g[0], en));
-    vstore(gr + C, vscale(p1, en));
-    vstore(gr + 2 * C, vscale(p2, en));
+    vstore_nt(gr, vscale(g[0], en));
+    vstore_nt(gr + C, vscale(p1, en));
+    vstore_nt(gr + 2 * C, vscale(p2, en));
     float part[16];
 #pragma unroll
     for (int b = 0; b < 3; ++b) part[b] = vdot(g[1 + b], r1);
