@@ -428,16 +428,16 @@ __global__ __launch_bounds__(256, wg_per_cu(PATH)) void complex_linear_kernel(
         sg = make_float4(sigmoidf_(gp.x), sigmoidf_(gp.y), sigmoidf_(gp.z), sigmoidf_(gp.w));
       }
       if constexpr (MODE == 2) {
-        st4(Yr + row * ldy + gc, yr * sg);
-        st4(Yi + row * ldy + gc, yi * sg);
-        st4(g.Pout + row * g.ldp + gc, yr * efr[i & 1][q] + yi * efi[i & 1][q]);
+        st4_nt(Yr + row * ldy + gc, yr * sg);
+        st4_nt(Yi + row * ldy + gc, yi * sg);
+        st4_nt(g.Pout + row * g.ldp + gc, yr * efr[i & 1][q] + yi * efi[i & 1][q]);
         continue;
       }
-      st4(Yr + row * ldy + gc, yr);
-      st4(Yi + row * ldy + gc, yi);
+      st4_nt(Yr + row * ldy + gc, yr);
+      st4_nt(Yi + row * ldy + gc, yi);
       if constexpr (MODE == 1) {
-        st4(g.Zr + row * g.ldz + gc, yr * sg);
-        st4(g.Zi + row * g.ldz + gc, yi * sg);
+        st4_nt(g.Zr + row * g.ldz + gc, yr * sg);
+        st4_nt(g.Zi + row * g.ldz + gc, yi * sg);
       }
     }
   }

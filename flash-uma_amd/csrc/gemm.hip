@@ -390,7 +390,7 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
         if (tabs) v = v + tcur;
         if (ln.ln_bias) v = v + lb;
         if constexpr (MODE == 3) {
-          if (ln.pre && live) st4(ln.pre + gr * ln.ldpre + col0 + cl, p);
+          if (ln.pre && live) st4_nt(ln.pre + gr * ln.ldpre + col0 + cl, p);
           const float mean = group_sum<32>(v.x + v.y + v.z + v.w) / LN_D;
           const float4 xc = make_float4(v.x - mean, v.y - mean, v.z - mean, v.w - mean);
           const float var = group_sum<32>(xc.x * xc.x + xc.y * xc.y + xc.z * xc.z + xc.w * xc.w) / LN_D;
@@ -401,7 +401,7 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
           y.z = xc.z * rstd * gm.z + bt.z;
           y.w = xc.w * rstd * gm.w + bt.w;
           if (live) {
-            st4(Y + gr * ldy + col0 + cl, make_float4(y.x * sigmoidf_(y.x), y.y * sigmoidf_(y.y),
+            st4_nt(Y + gr * ldy + col0 + cl, make_float4(y.x * sigmoidf_(y.x), y.y * sigmoidf_(y.y),
                                                       y.z * sigmoidf_(y.z), y.w * sigmoidf_(y.w)));
             if (sub == 0) {
               ln.mean[gr * ln.G + grp] = mean;
@@ -427,7 +427,7 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
           s1 = group_sum<32>(s1);
           s2 = group_sum<32>(s2);
           if (live)
-            st4(Y + gr * ldy + col0 + cl,
+            st4_nt(Y + gr * ldy + col0 + cl,
                 make_float4(rstd * (gxh[0] - (s1 + xh[0] * s2) / LN_D), rstd * (gxh[1] - (s1 + xh[1] * s2) / LN_D),
                             rstd * (gxh[2] - (s1 + xh[2] * s2) / LN_D), rstd * (gxh[3] - (s1 + xh[3] * s2) / LN_D)));
         }
@@ -468,7 +468,7 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
             const float yt = (&y.x)[t], sl = sigmoidf_(yt);
             (&o.x)[t] = (&g.x)[t] * (sl + yt * (sl * (1.0f - sl)));
           }
-          st4(out + 2 * L * C + ch, o);
+          st4_nt(out + 2 * L * C + ch, o);
         } else {
           const int gate_col = 64 * ((kb - 1) * n1 + (ch >> 5)) + (ch & 31);
           const float4 gp = ld4(y0 + gate_col);
@@ -483,8 +483,8 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
             (&ov.x)[t] = gt * st;
             (&og.x)[t] = (st * (1.0f - st)) * (gt * (&y.x)[t] + (&p.x)[t]);
           }
-          st4(out + gate_col, og);
-          st4(out + gate_col + 32, ov);
+          st4_nt(out + gate_col, og);
+          st4_nt(out + gate_col + 32, ov);
         }
       }
     }
@@ -519,19 +519,19 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
           g = g + ld4(bias + q0 + c);
           v = v + ld4(bias + q0 + 32 + c);
         }
-        st4(Y + row * ldy + q0 + c, g);
-        st4(Y + row * ldy + q0 + 32 + c, v);
+        st4_nt(Y + row * ldy + q0 + c, g);
+        st4_nt(Y + row * ldy + q0 + 32 + c, v);
         if (p < L * n1) {
           const int kind = p / n1;
           const int ch = 32 * (p - kind * n1) + c;
           const float4 sg = make_float4(sigmoidf_(g.x), sigmoidf_(g.y), sigmoidf_(g.z), sigmoidf_(g.w));
-          if (go.S) st4(go.S + row * go.lds + kind * C + ch, sg);
-          st4(go.Z + row * go.ldz + (1 + kind) * C + ch, v * sg);
+          if (go.S) st4_nt(go.S + row * go.lds + kind * C + ch, sg);
+          st4_nt(go.Z + row * go.ldz + (1 + kind) * C + ch, v * sg);
         } else {
           const int ch = q0 - 2 * L * C + c;
-          st4(go.Z + row * go.ldz + ch,
+          st4_nt(go.Z + row * go.ldz + ch,
               make_float4(g.x * sigmoidf_(g.x), g.y * sigmoidf_(g.y), g.z * sigmoidf_(g.z), g.w * sigmoidf_(g.w)));
-          st4(go.Z + row * go.ldz + ch + 32,
+          st4_nt(go.Z + row * go.ldz + ch + 32,
               make_float4(v.x * sigmoidf_(v.x), v.y * sigmoidf_(v.y), v.z * sigmoidf_(v.z), v.w * sigmoidf_(v.w)));
         }
       }
@@ -562,7 +562,7 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
           v.x += bias[gc]; v.y += bias[gc + 1]; v.z += bias[gc + 2]; v.w += bias[gc + 3];
         }
         if (rs.R) v = v + ld4(rs.R + gr * rs.ldr + gc);
-        st4(Y + gr * ldy + gc, v);
+        st4_nt(Y + gr * ldy + gc, v);
       }
     }
   }
