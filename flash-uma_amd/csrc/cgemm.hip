@@ -9,23 +9,27 @@
 // MFMA flops for the same result up to fp32 rounding.  The sums a_r + a_i and P + Q are
 // formed in registers from the operands already staged in LDS, so no extra memory traffic.
 //
-// Tiling: 256 threads (4 waves); K advances in chunks of 16 through double-buffered LDS.
-// Three main loops:
+// K advances in chunks of 16 through double-buffered LDS.  Three main loops:
 //  * split bf16 with a pre-split weight (default when the caller passes W3, built once per
 //    frozen weight by fu_complex_weight_split): P, Q and S = P + Q are stored as bf16 planes
 //    in MFMA-fragment order ([32-column block][16-k chunk][P, Q, S][hi, mid, lo][lane], 16 B
 //    per lane), so each wave loads its B fragments with 1 KB coalesced loads straight into
 //    registers, one chunk ahead.  Only a_r, a_i and a_s = a_r + a_i are split in the kernel
 //    and staged as planes in LDS (36 KB per buffer).  The output tile is 128 rows x 128
-//    columns of both out_r and out_i, the four waves side by side: each wave owns all 128
-//    rows of one 32-column block (four 32-row blocks x T1, T2, T3: twelve accumulator chains,
-//    192 accumulator registers, one workgroup per CU), so every B fragment it loads feeds
-//    4 x 6 MFMAs and every staged A chunk feeds four waves.  Against 64 x 32 per wave (two
-//    workgroups per CU) this halves the global loads per MFMA: 1.08-1.13x faster on the
-//    model's shapes (fetching the operands, not the MFMAs, was the limit: the same kernel
-//    without its B loads, or without its A loads, ran 1.25-1.35x faster).
-//  The two loops below keep an output tile of 128 rows x 64 columns (2 x 2 waves of
-//  64 x 32):
+//    columns of both out_r and out_i, computed by 512 threads (8 waves, two per SIMD, one
+//    workgroup per CU): wave (h, b) owns rows 64 h .. 64 h + 63 of 32-column block b (two
+//    32-row blocks x T1, T2, T3: six accumulator chains, 96 registers), so every staged A
+//    chunk feeds eight waves.  Measured on the model's shapes:
+//      - against 64 x 32 per wave in 128 x 64 tiles (two workgroups of 4 waves per CU),
+//        one 128 x 128 tile per CU halves the global loads per MFMA: 1.08-1.13x faster
+//        (fetching the operands, not the MFMAs, was the limit: the same kernel without its
+//        B loads, or without its A loads, ran 1.25-1.35x faster);
+//      - against four waves of 128 rows each (12 chains, 192 accumulators, one wave per
+//        SIMD), the second wave on each SIMD issues while the first waits on its LDS reads
+//        and the chunk barrier: 1.01-1.10x faster, at the cost of loading each B fragment
+//        twice (once per row half; the second load mostly hits the L1).
+//  The two loops below use 256 threads and an output tile of 128 rows x 64 columns (2 x 2
+//  waves of 64 x 32):
 //  * split bf16 without W3: a_r, a_i, P and Q are all split as they are staged (36 KB of
 //    planes per buffer); planes of a_r + a_i and P + Q as well would not fit two workgroups
 //    per CU, so this loop runs the four products directly,
@@ -85,11 +89,11 @@ struct CGate {
 
 // Output columns per tile, 32-row blocks per wave and workgroups per CU of each path.
 constexpr int cbn_of(int path) { return path == CPATH_SPLIT3_PRE ? CBN_PRE : CBN; }
-constexpr int rb_of(int path) { return path == CPATH_SPLIT3_PRE ? 4 : 2; }
 constexpr int wg_per_cu(int path) { return path == CPATH_FP32 ? 3 : path == CPATH_SPLIT3_PRE ? 1 : 2; }
+constexpr int threads_of(int path) { return path == CPATH_SPLIT3_PRE ? 512 : 256; }
 
 template <int MODE, int PATH, bool KTAIL = false>
-__global__ __launch_bounds__(256, wg_per_cu(PATH)) void complex_linear_kernel(
+__global__ __launch_bounds__(threads_of(PATH), wg_per_cu(PATH)) void complex_linear_kernel(
     const float* __restrict__ Ar, const float* __restrict__ Ai, int64_t lda, const float* __restrict__ P,
     const float* __restrict__ Q, int64_t ldw, const uint4* __restrict__ W3, float* __restrict__ Yr,
     float* __restrict__ Yi, int64_t ldy, int64_t M, int32_t Nc, int32_t Kc, int32_t n_tiles, int64_t total_tiles,
@@ -101,12 +105,14 @@ __global__ __launch_bounds__(256, wg_per_cu(PATH)) void complex_linear_kernel(
   if ((total_tiles & 7) == 0) wg = (wg & 7) * (total_tiles >> 3) + (wg >> 3);
   const int64_t m_tile = wg / n_tiles;
   const int n_tile = (int)(wg - m_tile * n_tiles);
-  constexpr int RB = rb_of(PATH);
+  constexpr int RB = 2;  // 32-row blocks per wave
   const int64_t row0 = m_tile * CBM;
   const int col0 = n_tile * cbn_of(PATH);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // wave tile: RB 32-row blocks x one 32-column block
-  const int wr = RB == 4 ? 0 : (wave >> 1) * 64, wc = RB == 4 ? wave * 32 : (wave & 1) * 32;
+  // wave tile: RB 32-row blocks x one 32-column block (pre-split: 2 row halves x 4 column
+  // blocks; otherwise 2 x 2)
+  constexpr bool W8 = threads_of(PATH) == 512;
+  const int wr = (wave >> (W8 ? 2 : 1)) * 64, wc = (wave & (W8 ? 3 : 1)) * 32;
 
   // four-product split: T[0] = out_r, T[1] = out_i; otherwise T1, T2, T3 of the three products
   constexpr int NT = PATH == CPATH_SPLIT4 ? 2 : 3;
@@ -122,46 +128,41 @@ __global__ __launch_bounds__(256, wg_per_cu(PATH)) void complex_linear_kernel(
   if constexpr (PATH == CPATH_SPLIT3_PRE) {
     // [buf][a_r hi, mid, lo | a_i hi, mid, lo | a_s hi, mid, lo][CTA]
     __bf16* sp = reinterpret_cast<__bf16*>(smem);
-    const int sr = tid >> 1, sh = tid & 1;  // tile row sr, k 8 sh .. 8 sh + 7
-    const int soff = plane_off(sr, sh);
+    // staging: thread -> tile row sr, k 4 sq .. 4 sq + 3 of the chunk (8-byte plane pieces)
+    const int sr = tid >> 2, sq = tid & 3;
+    const int soff = plane_off(sr, sq >> 1) + 4 * (sq & 1);
     const int nkc = (Kc + 15) / 16;
     const int nbt = (Nc + 31) / 32;
     const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 gr[2], gi[2];
+    float4 gr, gi;
     // fixed row pointers (a row past M reads row M-1; its outputs are never stored).  Without a
     // K tail: plain 16-byte loads; with one (KTAIL): unconditional loads from a valid address
     // and selects zeroing the pieces at or past Kc.  No branch in the loader (an if/else
     // choosing the form per chunk was miscompiled here: a prefetched operand register reused
     // before its read).
     const int64_t row = row0 + sr;
-    const int64_t ao = (row < M ? row : M - 1) * lda + 8 * sh;
+    const int64_t ao = (row < M ? row : M - 1) * lda + 4 * sq;
     const float *par = Ar + ao, *pai = Ai + ao;
     auto load_chunk = [&](int k0) {
       if constexpr (!KTAIL) {
-        gr[0] = ld4(par + k0);
-        gr[1] = ld4(par + k0 + 4);
-        gi[0] = ld4(pai + k0);
-        gi[1] = ld4(pai + k0 + 4);
-      } else {
-        const int gk = k0 + 8 * sh;
-        const bool a0 = gk < Kc, a1 = gk + 4 < Kc;
-        const float4 r0 = ld4(a0 ? par + k0 : Ar), r1 = ld4(a1 ? par + k0 + 4 : Ar);
-        const float4 i0 = ld4(a0 ? pai + k0 : Ai), i1 = ld4(a1 ? pai + k0 + 4 : Ai);
-        gr[0] = a0 ? r0 : z4;
-        gr[1] = a1 ? r1 : z4;
-        gi[0] = a0 ? i0 : z4;
-        gi[1] = a1 ? i1 : z4;
+        gr = ld4(par + k0);
+        gi = ld4(pai + k0);
+      } else {  // Kc is a multiple of 4: a thread's 4 k are all in or all past Kc
+        const bool ok = k0 + 4 * sq < Kc;
+        const float4 r = ld4(ok ? par + k0 : Ar), i = ld4(ok ? pai + k0 : Ai);
+        gr = ok ? r : z4;
+        gi = ok ? i : z4;
       }
     };
     auto store_chunk = [&](int buf) {
       __bf16* b = sp + buf * CBUF_PRE;
-      uint4 h, m, l;
-      split3(gr[0], gr[1], h, m, l);
-      st_planes(b, CTA, soff, h, m, l);
-      split3(gi[0], gi[1], h, m, l);
-      st_planes(b + 3 * CTA, CTA, soff, h, m, l);
-      split3(gr[0] + gi[0], gr[1] + gi[1], h, m, l);
-      st_planes(b + 6 * CTA, CTA, soff, h, m, l);
+      uint2 h, m, l;
+      split3_4(gr, h, m, l);
+      st_planes4(b, CTA, soff, h, m, l);
+      split3_4(gi, h, m, l);
+      st_planes4(b + 3 * CTA, CTA, soff, h, m, l);
+      split3_4(gr + gi, h, m, l);
+      st_planes4(b + 6 * CTA, CTA, soff, h, m, l);
     };
     // this wave's B fragments of chunk kc (a column block past Nc reads block 0; its outputs
     // are never stored)
@@ -365,7 +366,7 @@ __global__ __launch_bounds__(256, wg_per_cu(PATH)) void complex_linear_kernel(
   // 8 (r / 4) + 4 (l / 32) + r % 4.  Each wave stages a 32-row slab of [out_r | out_i] (32 + 32
   // columns) in LDS and writes it back as 16-byte row pieces (plus the gated copies).
   constexpr int CES = 64 + 8;
-  static_assert(4 * 32 * CES <= C_LDS_FLOATS && 4 * 32 * CES <= C_LDS_FLOATS_SPLIT,
+  static_assert(4 * 32 * CES <= C_LDS_FLOATS && 8 * 32 * CES <= C_LDS_FLOATS_SPLIT,
                 "epilogue staging must fit in the operand buffers");
   float* ws = smem + wave * 32 * CES;
   // The gate epilogues' global operands (the gate column; for MODE 2 also F_r and F_i) of a
@@ -494,7 +495,8 @@ static int complex_launch(const float* A_r, const float* A_i, int64_t lda, const
                            : complex_linear_kernel<MODE, CPATH_SPLIT3_PRE, false>)
                    : (tail ? complex_linear_kernel<MODE, CPATH_SPLIT4, true>
                            : complex_linear_kernel<MODE, CPATH_SPLIT4, false>);
-  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(256), 0, as_stream(stream), A_r, A_i, lda, P, Q, ldw,
+  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(path == CPATH_SPLIT3_PRE ? threads_of(CPATH_SPLIT3_PRE) : 256),
+                     0, as_stream(stream), A_r, A_i, lda, P, Q, ldw,
                      static_cast<const uint4*>(W3), Y_r, Y_i, ldy, M, Nc, Kc, n_tiles, total, g);
   return check_launch(who);
 }

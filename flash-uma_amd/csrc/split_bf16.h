@@ -52,6 +52,22 @@ __device__ __forceinline__ void split3(const float4& a, const float4& b, uint4& 
   }
 }
 
+// Split 4 floats into three planes of 4 bf16 each (as split3).
+__device__ __forceinline__ void split3_4(const float4& a, uint2& H, uint2& Mi, uint2& L) {
+  uint4 h, m, l;
+  split3(a, a, h, m, l);
+  H = make_uint2(h.x, h.y);
+  Mi = make_uint2(m.x, m.y);
+  L = make_uint2(l.x, l.y);
+}
+
+__device__ __forceinline__ void st_planes4(__bf16* p0, int plane_stride, int off, const uint2& H, const uint2& Mi,
+                                           const uint2& L) {
+  *reinterpret_cast<uint2*>(p0 + off) = H;
+  *reinterpret_cast<uint2*>(p0 + plane_stride + off) = Mi;
+  *reinterpret_cast<uint2*>(p0 + 2 * plane_stride + off) = L;
+}
+
 __device__ __forceinline__ void st_planes(__bf16* p0, int plane_stride, int off, const uint4& H, const uint4& Mi,
                                           const uint4& L) {
   *reinterpret_cast<uint4*>(p0 + off) = H;
