@@ -89,7 +89,8 @@ struct Resid {
 // statistics to mean / rstd[e G + g] and, when pre is set, the GEMM output (before tables
 // and ln_bias) to pre (batch stride s_pre).  MODE 4 is the input gradient: with the forward's
 // mean / rstd and the output gradient g_out (row stride ldgo, group g at column gD), Y
-// receives dL/dv.
+// receives dL/dv.  MODE 5 is the input gradient when the GEMM product is the output gradient
+// g_out: v is then read from pre (row stride ldpre, group g at column gD).
 constexpr int LN_D = 128;
 struct LnEpi {
   const float* tab_src;
@@ -316,7 +317,7 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
   // row 8*(r/4) + 4*(l/32) + r%4.
   const int oc = lane & 31;
   const int orow = (lane >> 5) * 4;
-  if constexpr (MODE == 3 || MODE == 4) {
+  if constexpr (MODE >= 3) {
     // The two waves of a row half (2p: columns 0-63, 2p + 1: columns 64-127 of the group)
     // stage one 32-row slab each; then each of them normalises 16 of the slab's rows, 32
     // lanes per row and 4 columns per lane, with 32-lane butterfly sums for the statistics.
@@ -350,7 +351,7 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
         zs = (int)ln.z[ln.isrc[rk]];
         zd = (int)ln.z[ln.idst[rk]];
       }
-      if constexpr (MODE == 4) {
+      if constexpr (MODE >= 4) {
         mu = ln.mean[rk * ln.G + grp];
         rsd = ln.rstd[rk * ln.G + grp];
       }
@@ -365,6 +366,7 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
           t = ld4(ln.tab_src + (int64_t)a * ln.ldt + grp * LN_D + cl) + ld4(ln.tab_dst + (int64_t)b * ln.ldt + grp * LN_D + cl);
         }
         if constexpr (MODE == 4) go = ld4(ln.g_out + rc * ln.ldgo + grp * LN_D + cl);
+        if constexpr (MODE == 5) go = ld4(ln.pre + rc * ln.ldpre + grp * LN_D + cl);  // v
       };
       constexpr int PD = 2;   // ring of row-pair operands: PD - 1 pairs in flight
       float4 tq[PD], gq[PD];
@@ -410,8 +412,9 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
           }
         } else {
           const float mean = __shfl(mu, k, 64), rstd = __shfl(rsd, k, 64);
-          const float4 go = gcur;
-          const float xh[4] = {(v.x - mean) * rstd, (v.y - mean) * rstd, (v.z - mean) * rstd, (v.w - mean) * rstd};
+          // MODE 4: v from the product, g_out loaded; MODE 5: the other way round
+          const float4 x = MODE == 5 ? gcur : v, go = MODE == 5 ? v : gcur;
+          const float xh[4] = {(x.x - mean) * rstd, (x.y - mean) * rstd, (x.z - mean) * rstd, (x.w - mean) * rstd};
           const float gg[4] = {gm.x, gm.y, gm.z, gm.w}, bb[4] = {bt.x, bt.y, bt.z, bt.w};
           const float gov[4] = {go.x, go.y, go.z, go.w};
           float gxh[4];
@@ -778,5 +781,36 @@ extern "C" int fu_linear_ln_silu_bwd(const float* A, int64_t lda, const float* W
                      GateOut{}, GateBwd{}, Resid{},
                      LnEpi{tab_src, tab_dst, ldt, z, isrc, idst, ln_bias, gamma, beta, const_cast<float*>(mean),
                            const_cast<float*>(rstd), G, 0.0f, nullptr, 0, 0, g_out, ldgo});
+  return check_launch(who);
+}
+
+extern "C" int fu_linear_dgrad_ln_silu_bwd(const float* A, int64_t lda, const float* W, int64_t ldw, float* g_x,
+                                           int64_t ldgx, int64_t M, int32_t K, const float* x, int64_t ldx,
+                                           const float* gamma, const float* beta, const float* mean, const float* rstd,
+                                           int32_t G, int32_t group, void* stream) {
+  const char* who = "fu_linear_dgrad_ln_silu_bwd";
+  int st = linear_check(A, lda, W, ldw, g_x, ldgx, M, LN_D, K, who);
+  if (st != FU_OK) return st;
+  if (G < 1 || group < 0 || group >= G)
+    return set_error(FU_ERR_SHAPE, "%s: group=%d outside [0, G=%d)", who, group, G);
+  if (ldx < (int64_t)G * LN_D || ldx % 4 != 0)
+    return set_error(FU_ERR_SHAPE, "%s: ldx=%lld must be >= 128 G and a multiple of 4", who, (long long)ldx);
+  if (M == 0) return FU_OK;
+  if (!x || !gamma || !beta || !mean || !rstd) return set_error(FU_ERR_NULL, "%s: NULL LayerNorm operand", who);
+  if (!aligned16(x) || !aligned16(gamma) || !aligned16(beta))
+    return set_error(FU_ERR_ALIGN, "%s: x, gamma and beta must be 16-byte aligned", who);
+  const int64_t bm = linear_tile_rows(M);
+  const int64_t total = (M + bm - 1) / bm;
+  if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
+  // the kernel addresses group 0 of its operands; the group's columns and statistics are
+  // selected here
+  const int64_t go = (int64_t)group * LN_D;
+  auto kern = linear_kernel<5>(K, M);
+  hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), A, lda, (int64_t)0, W, ldw,
+                     (int64_t)0, (const float*)nullptr, (int64_t)0, 0, g_x, ldgx, (int64_t)0, M, (int32_t)LN_D, K, 1,
+                     total, GateOut{}, GateBwd{}, Resid{},
+                     LnEpi{nullptr, nullptr, 0, nullptr, nullptr, nullptr, nullptr, gamma + go, beta + go,
+                           const_cast<float*>(mean) + group, const_cast<float*>(rstd) + group, G, 0.0f,
+                           const_cast<float*>(x) + go, ldx, 0, nullptr, 0});
   return check_launch(who);
 }

@@ -55,6 +55,7 @@ SIGNATURES: dict[str, list] = {
                           P, P, I64, P, P, P, P, P, P, P, P, I32, F32, P],
     "fu_linear_ln_silu_bwd": [P, I64, P, I64, P, I64, I64, I32, I32, P, I64, P, P, I64, P, P, P, P, P, P, P, P,
                               I32, P],
+    "fu_linear_dgrad_ln_silu_bwd": [P, I64, P, I64, P, I64, I64, I32, P, I64, P, P, P, P, I32, I32, P],
     "fu_complex_linear_gate_bwd": [P, P, I64, P, P, I64, P, P, P, I64, P, P, I64, P, I64, I32, I32, P, I64, I64, I32, I32, P],
     "fu_rms_norm_sh_fwd": [P, P, P, P, P, I64, I32, I32, F32, P],
     "fu_rms_norm_sh_bwd": [P, P, P, P, P, P, I64, I32, I32, P],

@@ -179,6 +179,7 @@ class RadialBank(torch.nn.Module):
             W, Wt, b = getattr(self, f"W3_{k}"), getattr(self, f"W3_{k}_t"), getattr(self, f"b3_{k}")
             outs.append(_RadialOutFn.apply(h2s[k], W, b, Wt, holder, k))
             srcs.append((h2s[k].detach(), W, b))
+        holder.ln = None
         return (tuple(outs), tuple(srcs)) if with_sources else tuple(outs)
 
 
@@ -190,15 +191,22 @@ def recompute_output(src) -> torch.Tensor:
 
 
 class _GradHolder:
-    """The (E, G*C) gradient of the trunk output: allocated by the first output-layer backward,
+    """The (E, G*C) gradient buffer of the trunk: allocated by the first output-layer backward,
     filled slice by slice by the blocks' output-layer backwards and released by the trunk
     backward that consumes it (the holder outlives the backward inside the autograd graph,
-    which the returned outputs keep referenced, so it must not keep device memory)."""
+    which the returned outputs keep referenced, so it must not keep device memory).
+
+    At C = 128 the slices hold the gradient of the second hidden layer's LayerNorm input
+    (each output-layer backward applies that layer's LayerNorm-SiLU backward for its group in
+    the GEMM epilogue); otherwise the gradient of the trunk outputs.  `ln` carries the
+    LayerNorm operands (p2, mean, rstd, gamma, beta, G) from the trunk's forward to the output
+    layers' forwards only."""
 
     def __init__(self):
         self.g = None
         self.shape = None
         self.device = None
+        self.ln = None
 
     def buffer(self) -> torch.Tensor:
         if self.g is None:
@@ -228,6 +236,10 @@ class _RadialTrunkFn(torch.autograd.Function):
         # it is not needed before the backward, and the forward's end is a memory peak
         holder.shape = tuple(p2.shape) if ctx.needs_input_grad[0] else None
         holder.device = p2.device
+        ctx.dgrad_fused = C == LN_FUSED_C
+        # an output without a gradient arrives as None (not a materialised zero tensor)
+        ctx.set_materialize_grads(False)
+        holder.ln = (p2, m2, r2, bank.gamma2, bank.beta2, G) if ctx.dgrad_fused else None
         # the first layer's product (E, G*C) is not kept: the backward recomputes it from the
         # (E, B) Gaussians with the K = B GEMM (10x fewer bytes held through the step)
         ctx.save_for_backward(gauss, m1, r1, p2, m2, r2, Z, idx_i, idx_j)
@@ -239,16 +251,22 @@ class _RadialTrunkFn(torch.autograd.Function):
         gauss, m1, r1, p2, m2, r2, Z, idx_i, idx_j = ctx.saved_tensors
         bank, holder = ctx.bank, ctx.holder
         E, G, C = gauss.shape[0], bank.G, bank.C
-        g_h2 = holder.g if holder.g is not None else torch.empty_like(p2)
+        g_buf = holder.g if holder.g is not None else torch.empty_like(p2)
         holder.g = None   # a retained graph's next backward allocates a fresh buffer
         for k, gv in enumerate(g_views):
-            sl = g_h2[:, k * C:(k + 1) * C]
+            sl = g_buf[:, k * C:(k + 1) * C]
             if gv is None:
-                sl.zero_()
+                sl.zero_()   # zero in either meaning of the slice
             elif gv.data_ptr() != sl.data_ptr() or gv.stride() != sl.stride():
+                if ctx.dgrad_fused:
+                    # the views are internal to RadialBank.forward: only the output layers read them
+                    raise _lib.FlashUMAError("radial bank: a trunk output has a reader besides its output layer")
                 sl.copy_(gv)
-        g_p2 = _ln_grouped_bwd(p2, None, None, None, None, None, bank.gamma2, bank.beta2, m2, r2, g_h2, G, C)
-        del g_h2
+        if ctx.dgrad_fused:
+            g_p2 = g_buf   # the output layers' epilogues applied the LayerNorm-SiLU backward
+        else:
+            g_p2 = _ln_grouped_bwd(p2, None, None, None, None, None, bank.gamma2, bank.beta2, m2, r2, g_buf, G, C)
+        del g_buf
         g_h1 = _batched(g_p2, bank.W2_t, None, G, C, C, torch.empty_like(g_p2))
         del g_p2
         g_p1 = _layer1_bwd(gauss, bank, Z, idx_i, idx_j, m1, r1, g_h1)
@@ -258,13 +276,16 @@ class _RadialTrunkFn(torch.autograd.Function):
 
 
 class _RadialOutFn(torch.autograd.Function):
-    """Output layer of block k: rad = h2_k W3^T + b3.  Its backward writes g_h2_k straight into
-    the trunk's gradient buffer and returns that slice."""
+    """Output layer of block k: rad = h2_k W3^T + b3.  Its backward writes into the trunk's
+    gradient buffer and returns that slice: at C = 128 the gradient of the LayerNorm input of
+    group k of the second hidden layer (fu_linear_dgrad_ln_silu_bwd: the g_h2_k GEMM with that
+    LayerNorm-SiLU backward in its epilogue, g_h2_k never stored), otherwise g_h2_k."""
 
     @staticmethod
     def forward(ctx, h2k, W, b, Wt, holder, k):
         ctx.save_for_backward(Wt)
         ctx.holder, ctx.k = holder, k
+        ctx.ln = holder.ln   # (p2, mean, rstd, gamma, beta, G) of the trunk's forward, or None
         return _gemm(h2k, W, b, torch.empty(h2k.shape[0], W.shape[0], device=h2k.device, dtype=torch.float32))
 
     @staticmethod
@@ -272,6 +293,14 @@ class _RadialOutFn(torch.autograd.Function):
         (Wt,) = ctx.saved_tensors
         g_rad = g_rad.contiguous()
         C = Wt.shape[0]
-        sl = ctx.holder.buffer()[:, ctx.k * C:(ctx.k + 1) * C]
-        _gemm(g_rad, Wt, None, sl)
+        buf = ctx.holder.buffer()
+        sl = buf[:, ctx.k * C:(ctx.k + 1) * C]
+        if ctx.ln is None:
+            _gemm(g_rad, Wt, None, sl)
+        else:
+            p2, m2, r2, gamma, beta, G = ctx.ln
+            M, K = g_rad.shape
+            _lib.call("fu_linear_dgrad_ln_silu_bwd", g_rad.data_ptr(), g_rad.stride(0), Wt.data_ptr(), Wt.stride(0),
+                      sl.data_ptr(), buf.stride(0), M, K, p2.data_ptr(), p2.stride(0), gamma.data_ptr(),
+                      beta.data_ptr(), m2.data_ptr(), r2.data_ptr(), G, ctx.k, _lib.stream_ptr(g_rad.device))
         return sl, None, None, None, None, None

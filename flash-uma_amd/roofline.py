@@ -199,6 +199,13 @@ def _linear_ln_silu_bwd(a):
     return 4 * (M * K + N * K + 2 * M * N) + 8 * M * G + tab, 2 * M * N * K
 
 
+def _linear_dgrad_ln_silu_bwd(a):
+    # the output-layer input-gradient GEMM (N = 128) plus the LayerNorm backward epilogue:
+    # the LayerNorm input x read, g_x written, the row statistics read
+    M, K, N = a[6], a[7], 128
+    return 4 * (M * K + N * K + 2 * M * N) + 8 * M, 2 * M * N * K
+
+
 def _complex_linear(a):
     # three real (M x Kc) x (Kc x Nc) products (the packed real form of the reference would be
     # four; so is the split path without a pre-split weight, which executes 4/3 of this)
@@ -255,6 +262,7 @@ WORK = {
     "fu_linear_batched": _linear_batched,
     "fu_linear_ln_silu": _linear_ln_silu,
     "fu_linear_ln_silu_bwd": _linear_ln_silu_bwd,
+    "fu_linear_dgrad_ln_silu_bwd": _linear_dgrad_ln_silu_bwd,
     "fu_complex_linear": _complex_linear,
     "fu_linear_gate": _linear_gate,
     "fu_linear_gate_bwd": _linear_gate_bwd,
@@ -273,7 +281,8 @@ WORK = {
 }
 
 MFMA_BOUND = {"fu_linear", "fu_linear_batched", "fu_complex_linear", "fu_linear_gate", "fu_complex_linear_gate",
-              "fu_linear_gate_bwd", "fu_complex_linear_gate_bwd", "fu_linear_ln_silu", "fu_linear_ln_silu_bwd"}
+              "fu_linear_gate_bwd", "fu_complex_linear_gate_bwd", "fu_linear_ln_silu", "fu_linear_ln_silu_bwd",
+              "fu_linear_dgrad_ln_silu_bwd"}
 
 
 def summarize(durations, matmul_mode: int = MATMUL_SPLIT_BF16) -> dict:

@@ -237,6 +237,19 @@ int fu_linear_ln_silu_bwd(const float* A, int64_t lda, const float* W, int64_t l
                           const float* ln_bias, const float* gamma, const float* beta,
                           const float* mean, const float* rstd, int32_t G, void* stream);
 
+/* The LayerNorm-SiLU input gradient of one group when its output gradient is a GEMM product
+ * (the radial MLP's output layer backward followed by the second hidden layer's LayerNorm-SiLU
+ * backward, model.py:147-149 and ops/ln_silu.py:77-123): g = A W^T (M x 128, W 128 x K) is
+ * dL/dy for y = silu(LN(x_group) gamma + beta) on columns 128 group .. 128 group + 127 of x
+ * (M x ldx, ldx >= 128 G; gamma, beta of length 128 G; mean / rstd (M x G) the forward's
+ * statistics); the epilogue writes dL/dx_group to g_x (M x 128, row stride ldgx).  g is never
+ * stored. */
+int fu_linear_dgrad_ln_silu_bwd(const float* A, int64_t lda, const float* W, int64_t ldw,
+                                float* g_x, int64_t ldgx, int64_t M, int32_t K, const float* x,
+                                int64_t ldx, const float* gamma, const float* beta,
+                                const float* mean, const float* rstd, int32_t G, int32_t group,
+                                void* stream);
+
 /* ------------------------------------------------------------------------------------
  * Dense contractions on fp32 MFMA (replaces torch F.linear at model.py:147-154,203-205)
  * ------------------------------------------------------------------------------------ */

@@ -68,6 +68,13 @@ def test_error_codes():
     st, msg = _status("fu_linear_ln_silu", None, 640, 128, None, 128, 0, None, 0, 0, None, 640, 128, None, 0, 0, 0,
                       128, 128, 4, *([None] * 2), 0, *([None] * 8), 5, ctypes.c_float(1e-5), None)
     assert st == -2 and "groups of 128" in msg
+    # the output-layer gradient GEMM with the LayerNorm backward: one group of G
+    st, msg = _status("fu_linear_dgrad_ln_silu_bwd", None, 64, None, 64, None, 640, 0, 64, None, 640, *([None] * 4),
+                      5, 5, None)
+    assert st == -1 and "group=5" in msg
+    st, msg = _status("fu_linear_dgrad_ln_silu_bwd", None, 64, None, 64, None, 640, 0, 64, None, 512, *([None] * 4),
+                      5, 0, None)
+    assert st == -1 and "ldx=512" in msg
     # accumulate flags: bit 0 (wigner rows), bit 1 (env); nothing else
     for name, args in (("fu_scatter_bwd", (*([None] * 12), 0, 5, 128)),
                        ("fu_init_scatter_bwd", (*([None] * 8), 0, 5, 128)),
@@ -126,6 +133,7 @@ def test_zero_rows_accept_empty_arrays():
                               *([None] * 2), 0, *([None] * 8), 5, f(1e-5), None),
         "fu_linear_ln_silu_bwd": (None, 64, None, 64, None, 640, 0, 640, 64, None, 640, *([None] * 2), 0,
                                   *([None] * 8), 5, None),
+        "fu_linear_dgrad_ln_silu_bwd": (None, 64, None, 64, None, 640, 0, 64, None, 640, *([None] * 4), 5, 4, None),
     }
     for name, args in calls.items():
         st, msg = _status(name, *args)

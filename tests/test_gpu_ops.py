@@ -667,8 +667,9 @@ def test_linear_ln_silu_matches_two_kernels(cuda, matmul_mode, M):
     LayerNorm-SiLU in the GEMM epilogue) against the GEMM followed by the grouped LayerNorm
     kernels, on both tile heights (70,001 rows: 256-row tiles and a ragged last tile): the
     first layer with element tables and LN bias (one group per N-tile), the second as a
-    batched GEMM with bias and the pre-LN product stored (one group per batch), and the
-    first layer's input gradient."""
+    batched GEMM with bias and the pre-LN product stored (one group per batch), the first
+    layer's input gradient, and the second layer's input gradient per group from the output
+    layers' input-gradient GEMMs (fu_linear_dgrad_ln_silu_bwd)."""
     from ops import _lib
     from ops.radial import _batched, _gemm, _ln_grouped_bwd, _ln_grouped_fwd
     g = torch.Generator(device=cuda).manual_seed(M)
@@ -712,3 +713,16 @@ def test_linear_ln_silu_matches_two_kernels(cuda, matmul_mode, M):
               g_h1.data_ptr(), G * C, ts.data_ptr(), td.data_ptr(), G * C, Z.data_ptr(), ii.data_ptr(), jj.data_ptr(),
               b1.data_ptr(), gm1.data_ptr(), bt1.data_ptr(), m1r.data_ptr(), r1r.data_ptr(), G, st)
     assert_close(gx, gref, 2e-6, "layer-1 LayerNorm input gradient")
+    # layer 2 input gradient: per group k, g_h2_k = g_rad_k W3_k (output width n_k) and the
+    # LayerNorm-SiLU backward of group k, against fu_linear + fu_ln_silu_grouped_bwd
+    widths = [3 * C, 12 * C, 12 * C, 12 * C, 12 * C]
+    g_h2 = torch.empty(M, G * C, device=cuda)
+    g_p2 = torch.empty(M, G * C, device=cuda)
+    for k, n in enumerate(widths):
+        g_rad, W3t = r(M, n), r(C, n) / n ** 0.5
+        _gemm(g_rad, W3t, None, g_h2[:, k * C:(k + 1) * C])
+        _lib.call("fu_linear_dgrad_ln_silu_bwd", g_rad.data_ptr(), n, W3t.data_ptr(), n, g_p2[:, k * C:].data_ptr(),
+                  G * C, M, n, p2.data_ptr(), G * C, gm2.data_ptr(), bt2.data_ptr(), m2.data_ptr(), r2.data_ptr(), G,
+                  k, st)
+    gref2 = _ln_grouped_bwd(p2, None, None, None, None, None, gm2, bt2, m2, r2, g_h2, G, C)
+    assert_close(g_p2, gref2, 2e-6, "layer-2 LayerNorm input gradient")

@@ -37,6 +37,7 @@ GEMMS = {
     "fu_complex_linear_gate_bwd": (dict(M=1000, Nc=128, Kc=256), 6 * 1000 * 128 * 256),
     "fu_linear_ln_silu": (dict(M=1000, N=128, K=128, batch=5, G=5), 2 * 5 * 1000 * 128 * 128),
     "fu_linear_ln_silu_bwd": (dict(M=1000, N=640, K=64, G=5), 2 * 1000 * 640 * 64),
+    "fu_linear_dgrad_ln_silu_bwd": (dict(M=1000, K=1536, G=5, group=2), 2 * 1000 * 128 * 1536),
 }
 
 
