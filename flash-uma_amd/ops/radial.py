@@ -283,22 +283,26 @@ class _RadialOutFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, h2k, W, b, Wt, holder, k):
-        ctx.save_for_backward(Wt)
         ctx.holder, ctx.k = holder, k
-        ctx.ln = holder.ln   # (p2, mean, rstd, gamma, beta, G) of the trunk's forward, or None
+        # (p2, mean, rstd, gamma, beta) of the trunk's forward are saved like the weight, so
+        # that they are released after the backward (a plain ctx attribute would keep p2 alive
+        # as long as the graph's nodes, i.e. into the next step)
+        ctx.ln_groups = None if holder.ln is None else holder.ln[-1]
+        ctx.save_for_backward(Wt, *(() if holder.ln is None else holder.ln[:-1]))
         return _gemm(h2k, W, b, torch.empty(h2k.shape[0], W.shape[0], device=h2k.device, dtype=torch.float32))
 
     @staticmethod
     def backward(ctx, g_rad):
-        (Wt,) = ctx.saved_tensors
+        Wt, *ln = ctx.saved_tensors
         g_rad = g_rad.contiguous()
         C = Wt.shape[0]
         buf = ctx.holder.buffer()
         sl = buf[:, ctx.k * C:(ctx.k + 1) * C]
-        if ctx.ln is None:
+        if ctx.ln_groups is None:
             _gemm(g_rad, Wt, None, sl)
         else:
-            p2, m2, r2, gamma, beta, G = ctx.ln
+            p2, m2, r2, gamma, beta = ln
+            G = ctx.ln_groups
             M, K = g_rad.shape
             _lib.call("fu_linear_dgrad_ln_silu_bwd", g_rad.data_ptr(), g_rad.stride(0), Wt.data_ptr(), Wt.stride(0),
                       sl.data_ptr(), buf.stride(0), M, K, p2.data_ptr(), p2.stride(0), gamma.data_ptr(),
