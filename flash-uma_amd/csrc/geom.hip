@@ -205,22 +205,17 @@ __global__ __launch_bounds__(GEOM_BLOCK) void geom_bwd_kernel(
     int64_t E, int32_t B, float cutoff, float coeff_g) {
   extern __shared__ float s_dyn[];
   float* s_gw = s_dyn;                          // [GEOM_BLOCK][34]
-  float* s_gg = s_dyn + GEOM_BLOCK * 34;        // [GEOM_BLOCK][B+1]
   const int64_t e0 = (int64_t)blockIdx.x * GEOM_BLOCK;
   const int nloc = (int)min<int64_t>(GEOM_BLOCK, E - e0);
   const int t = threadIdx.x;
-  const int ldg = B + 1;
 
-  // cooperative, coalesced staging of the block's g_wigner rows and Gaussian gradients
+  // cooperative, coalesced staging of the block's g_wigner rows.  The Gaussian gradients are
+  // read by each thread from its own row below: a wave's 64 rows are 64 whole cache-line pairs,
+  // and staging them too (33 KB per block) limited the kernel to 3 blocks per CU (167-172
+  // against 99-101 us at bcc Fe).
   if (g_wig != nullptr) {
     const float* src = g_wig + e0 * 34;
     for (int k = t; k < nloc * 34; k += GEOM_BLOCK) s_gw[k] = src[k];
-  }
-  if (g_xe != nullptr) {
-    for (int k = t; k < nloc * B; k += GEOM_BLOCK) {
-      const int el = k / B, col = k - el * B;
-      s_gg[el * ldg + col] = g_xe[(e0 + el) * ld_gxe + col];
-    }
   }
   __syncthreads();
   if (t >= nloc) return;
@@ -314,7 +309,7 @@ __global__ __launch_bounds__(GEOM_BLOCK) void geom_bwd_kernel(
   // radial terms: Gaussians and envelope (ops/geom.py:453-471)
   float g_dist = 0.0f;
   if (g_xe != nullptr) {
-    const float* gg = s_gg + t * ldg;
+    const float* gg = g_xe + e * ld_gxe;
     for (int b = 0; b < B; ++b) {
       const float diff = dist - offset_g[b];
       const float gauss = expf(coeff_g * diff * diff);
@@ -392,7 +387,7 @@ extern "C" int fu_geom_bwd(const float* pos, const int64_t* idx_i, const int64_t
   if (g_x_edge_raw && ld_gxe < B) return set_error(FU_ERR_SHAPE, "fu_geom_bwd: ld_gxe < B");
   if (E == 0) return FU_OK;
   if (!pos || !idx_i || !idx_j || !shifts || !offset_g || !g_d) return set_error(FU_ERR_NULL, "fu_geom_bwd: NULL argument");
-  const size_t lds = sizeof(float) * (GEOM_BLOCK * 34 + GEOM_BLOCK * (B + 1));
+  const size_t lds = sizeof(float) * GEOM_BLOCK * 34;
   hipLaunchKernelGGL(geom_bwd_kernel, dim3(cdiv(E, GEOM_BLOCK)), dim3(GEOM_BLOCK), lds, as_stream(stream), pos, idx_i,
                      idx_j, shifts, offset_g, g_x_edge_raw, ld_gxe, g_wigner, g_env, g_d, E, B, cutoff, coeff_g);
   return check_launch("fu_geom_bwd");
