@@ -290,9 +290,12 @@ __device__ __forceinline__ void gather_bwd_side(const float* __restrict__ gX0, c
 }
 
 // One node per 128-thread workgroup (wave 0: receiver segment, wave 1: sender segment); at
-// least 3 waves per SIMD, since the loop is bound by the number of edge loads in flight.
+// least 3 waves per SIMD, since the loop is bound by the number of edge loads in flight.  At
+// C = 256 two edges in flight need more than the 170 registers of 3 waves per SIMD (449
+// spilled to scratch) or the 256 of 2 (116): one wave per SIMD keeps them in registers and
+// accumulation registers (2.26x faster at 245,760 edges: 5,160 -> 2,285 us).
 template <int CPL, int L>
-__global__ __launch_bounds__(128, 3) void gather_bwd_kernel(
+__global__ __launch_bounds__(128, CPL >= 4 ? 1 : 3) void gather_bwd_kernel(
     const float* __restrict__ gX0, const float* __restrict__ gX1, const float* __restrict__ gX2,
     const float* __restrict__ x, const float* __restrict__ wig, const float* __restrict__ rad,
     const float* __restrict__ csd, const int64_t* __restrict__ batch, const int32_t* __restrict__ rptr,
