@@ -81,7 +81,9 @@ __device__ __forceinline__ constexpr int slot_m2(int so, int q) { return 2 * q +
 template <int L>
 __device__ __forceinline__ constexpr int slot_rad(int so, int q) { return L ? so * 6 + q : 2 * q + so; }
 
-template <int CPL, int L>
+// M0 false: the m = 0 slots are neither computed nor stored (X0 unused), nor are their radial
+// blocks read: conv1 m = 0 gathers its operand itself (fu_gather_linear_gate).
+template <int CPL, int L, bool M0 = true>
 __global__ __launch_bounds__(256) void gather_fwd_kernel(
     const float* __restrict__ x, const int64_t* __restrict__ idx_i, const int64_t* __restrict__ idx_j,
     const float* __restrict__ wig, const float* __restrict__ rad, const float* __restrict__ csd,
@@ -113,16 +115,18 @@ __global__ __launch_bounds__(256) void gather_fwd_kernel(
     const float* rr = rad + e * 12 * C + c;
     Vec<CPL> r[12];
 #pragma unroll
-    for (int k = 0; k < 12; ++k) r[k] = vload_nt<CPL>(rr + slot_rad<L>(k & 1, k >> 1) * C);
+    for (int k = M0 ? 0 : 6; k < 12; ++k) r[k] = vload_nt<CPL>(rr + slot_rad<L>(k & 1, k >> 1) * C);
     float* o0 = X0 + e * 6 * C + c;
     float* o1 = X1 + e * 8 * C + c;
     float* o2 = X2 + e * 4 * C + c;
     // m0 slots: rotated coefficient k0, k2, k6; m1: k3, k7 (R) and k1, k5 (I); m2: k8 (R), k4 (I)
     constexpr int K0[3] = {0, 2, 6}, K1[4] = {3, 7, 1, 5}, K2[2] = {8, 4};
+    if constexpr (M0) {
 #pragma unroll
-    for (int q = 0; q < 3; ++q) {
-      vstore_nt(o0 + slot_m0<L>(0, q) * C, vmul(rs.r[K0[q]], r[2 * q]));
-      vstore_nt(o0 + slot_m0<L>(1, q) * C, vmul(rt.r[K0[q]], r[2 * q + 1]));
+      for (int q = 0; q < 3; ++q) {
+        vstore_nt(o0 + slot_m0<L>(0, q) * C, vmul(rs.r[K0[q]], r[2 * q]));
+        vstore_nt(o0 + slot_m0<L>(1, q) * C, vmul(rt.r[K0[q]], r[2 * q + 1]));
+      }
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -354,8 +358,12 @@ template <int CPL, int L>
 static void launch_gather_fwd(const float* x, const int64_t* idx_i, const int64_t* idx_j, const float* wigner,
                               const float* rad, const float* csd, const int64_t* batch, float* X0, float* X1,
                               float* X2, int64_t E, hipStream_t st) {
-  hipLaunchKernelGGL((gather_fwd_kernel<CPL, L>), dim3(edge_grid(E)), dim3(256), 0, st, x, idx_i, idx_j, wigner, rad,
-                     csd, batch, X0, X1, X2, E);
+  if (X0)
+    hipLaunchKernelGGL((gather_fwd_kernel<CPL, L>), dim3(edge_grid(E)), dim3(256), 0, st, x, idx_i, idx_j, wigner,
+                       rad, csd, batch, X0, X1, X2, E);
+  else
+    hipLaunchKernelGGL((gather_fwd_kernel<CPL, L, false>), dim3(edge_grid(E)), dim3(256), 0, st, x, idx_i, idx_j,
+                       wigner, rad, csd, batch, X0, X1, X2, E);
 }
 
 template <int CPL, int L>
@@ -400,9 +408,10 @@ extern "C" int fu_gather_fwd(const float* x, const int64_t* idx_i, const int64_t
   int st = check_c(C, "fu_gather_fwd");
   if (st != FU_OK) return st;
   if (E == 0) return FU_OK;
-  if (!x || !idx_i || !idx_j || !wigner || !rad || !csd_emb || !batch || !X_m0 || !X_m1 || !X_m2)
+  // X_m0 may be NULL: the m = 0 part is then skipped (its GEMM gathers it, fu_gather_linear_gate)
+  if (!x || !idx_i || !idx_j || !wigner || !rad || !csd_emb || !batch || !X_m1 || !X_m2)
     return set_error(FU_ERR_NULL, "fu_gather_fwd: NULL argument");
-  const void* al[] = {x, rad, csd_emb, X_m0, X_m1, X_m2};
+  const void* al[] = {x, rad, csd_emb, X_m0 ? X_m0 : X_m1, X_m1, X_m2};
   for (const void* p : al)
     if (!aligned16(p)) return set_error(FU_ERR_ALIGN, "fu_gather_fwd: feature arrays must be 16-byte aligned");
   hipStream_t s = as_stream(stream);

@@ -113,6 +113,22 @@ struct LnEpi {
   int64_t ldgo;
 };
 
+// conv1 m = 0's A operand gathered in the loader (fu_gather_linear_gate, lmax = 2): row e,
+// column k = (so * 3 + q) C + c is the layout-1 gather output X_m0 of ops/gather.py,
+//   rot_q(x[node_so(e)])[c] * rad[e][(so * 6 + q) C + c],   node_0 = idx_i, node_1 = idx_j,
+// with rot_0 = x_l0 + csd[batch], rot_1 = (row 1 of D1) x_l1, rot_2 = (row 2 of D2) x_l2 (the
+// m = 0 rows of the Wigner blocks, wigner[e][3..5] and [19..23]), so X_m0 is never stored.
+struct GatherA {
+  const float* x;
+  const int64_t* idx_i;
+  const int64_t* idx_j;
+  const float* wig;
+  const float* rad;
+  const float* csd;
+  const int64_t* batch;
+  int32_t C;
+};
+
 // Batch index blockIdx.y offsets A, W and Y by sA, sW and sY floats; bias (stride sBias) is
 // added in batches [0, bias_batches).
 //
@@ -122,14 +138,15 @@ struct LnEpi {
 // wave's 64 staged columns are a gate and its values; the epilogue writes Y (kept for the
 // backward), Z and S.  MODE 2 (gate backward): see GateBwd; Y receives g_Y_m0 ((2L+1)C
 // columns).
-template <int MODE, bool SPLIT, bool KTAIL = false, bool TALL = false>
+template <int MODE, bool SPLIT, bool KTAIL = false, bool TALL = false, bool GATHER = false>
 __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const float* __restrict__ A, int64_t lda, int64_t sA,
                                                           const float* __restrict__ W, int64_t ldw, int64_t sW,
                                                           const float* __restrict__ bias, int64_t sBias,
                                                           int32_t bias_batches, float* __restrict__ Y, int64_t ldy,
                                                           int64_t sY, int64_t M, int32_t N, int32_t K,
                                                           int32_t n_tiles, int64_t total_tiles, GateOut go,
-                                                          GateBwd gb, Resid rs, LnEpi ln) {
+                                                          GateBwd gb, Resid rs, LnEpi ln,
+                                                          GatherA gx = GatherA{}) {
   {
     const int64_t bt = blockIdx.y;
     A += bt * sA;
@@ -140,6 +157,7 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
     if (rs.R) rs.R += bt * rs.sR;
   }
   static_assert(SPLIT || !TALL, "tall tiles exist in the split mode only");
+  static_assert(!GATHER || (SPLIT && !KTAIL && MODE == 1), "the gathered A operand feeds the split gate GEMM");
   constexpr int RB = TALL ? 4 : 2;          // 32-row blocks per wave
   constexpr int BM = 64 * RB;               // tile rows
   constexpr int PA = BM * GBK, PW = G_PLANE;  // bf16 per A plane, per W plane
@@ -189,8 +207,64 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
     const float* pa = A + (gr < M ? gr : M - 1) * lda + 8 * sh;
     const float* pa2 = A + (gr2 < M ? gr2 : M - 1) * lda + 8 * sh;   // second staged row (TALL)
     const float* pw = W + (int64_t)(gn < N ? gn : N - 1) * ldw + 8 * sh;
+    // GATHER: per staged row, its two node rows (csd rows for l = 0), its radial row and the
+    // m = 0 Wigner rows, fixed for the whole K loop
+    const float* xn[2][2];
+    const float* cn[2][2];
+    const float* rr[2];
+    float w1[2][3], w2[2][5];
+    if constexpr (GATHER) {
+      const int64_t ers[2] = {gr < M ? gr : M - 1, gr2 < M ? gr2 : M - 1};
+#pragma unroll
+      for (int t = 0; t < (TALL ? 2 : 1); ++t) {
+        const int64_t e = ers[t];
+        const int64_t nd[2] = {gx.idx_i[e], gx.idx_j[e]};
+#pragma unroll
+        for (int so = 0; so < 2; ++so) {
+          xn[t][so] = gx.x + nd[so] * 9 * gx.C + 8 * sh;
+          cn[t][so] = gx.csd + gx.batch[nd[so]] * gx.C + 8 * sh;
+        }
+        rr[t] = gx.rad + e * 12 * gx.C + 8 * sh;
+#pragma unroll
+        for (int b = 0; b < 3; ++b) w1[t][b] = gx.wig[e * 34 + 3 + b];
+#pragma unroll
+        for (int b = 0; b < 5; ++b) w2[t][b] = gx.wig[e * 34 + 19 + b];
+      }
+    }
+    // the 8 gathered values of staged row t at K offset k0 (+ 8 sh): the slot (so, q) of a
+    // chunk is uniform, so the branch on q is a scalar one; the products and sums run in the
+    // order of the gather kernel's rotation
+    auto gather_row = [&](int t, int k0, float4& o0, float4& o1) {
+      const int C = gx.C;
+      const int so = k0 / (3 * C), q = (k0 - so * 3 * C) / C, c = k0 - (so * 3 + q) * C;
+      const float* xb = xn[t][so] + c;
+      float4 a0, a1;
+      if (q == 0) {
+        a0 = ld4(xb) + ld4(cn[t][so] + c);
+        a1 = ld4(xb + 4) + ld4(cn[t][so] + c + 4);
+      } else if (q == 1) {
+        a0 = scale4(ld4(xb + C), w1[t][0]) + scale4(ld4(xb + 2 * C), w1[t][1]) + scale4(ld4(xb + 3 * C), w1[t][2]);
+        a1 = scale4(ld4(xb + C + 4), w1[t][0]) + scale4(ld4(xb + 2 * C + 4), w1[t][1]) +
+             scale4(ld4(xb + 3 * C + 4), w1[t][2]);
+      } else {
+        a0 = scale4(ld4(xb + 4 * C), w2[t][0]) + scale4(ld4(xb + 5 * C), w2[t][1]) + scale4(ld4(xb + 6 * C), w2[t][2]) +
+             scale4(ld4(xb + 7 * C), w2[t][3]) + scale4(ld4(xb + 8 * C), w2[t][4]);
+        a1 = scale4(ld4(xb + 4 * C + 4), w2[t][0]) + scale4(ld4(xb + 5 * C + 4), w2[t][1]) +
+             scale4(ld4(xb + 6 * C + 4), w2[t][2]) + scale4(ld4(xb + 7 * C + 4), w2[t][3]) +
+             scale4(ld4(xb + 8 * C + 4), w2[t][4]);
+      }
+      // plain loads: every column tile of the row panel reads the radial row again (from L2)
+      const float* rp = rr[t] + (so * 6 + q) * C + c;
+      o0 = a0 * ld4(rp);
+      o1 = a1 * ld4(rp + 4);
+    };
     auto load_chunk = [&](int k0) {
-      if constexpr (!KTAIL) {
+      if constexpr (GATHER) {
+        gather_row(0, k0, ga[0], ga[1]);
+        if constexpr (TALL) gather_row(1, k0, ga2[0], ga2[1]);
+        gw[0] = ld4(pw + k0);
+        gw[1] = ld4(pw + k0 + 4);
+      } else if constexpr (!KTAIL) {
         ga[0] = ld4(pa + k0);
         ga[1] = ld4(pa + k0 + 4);
         if constexpr (TALL) {
@@ -621,7 +695,7 @@ static int linear_launch(const float* A, int64_t lda, int64_t sA, const float* W
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
   auto kern = linear_kernel<0>(K, M);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, (unsigned)batch), dim3(256), 0, stream, A, lda, sA, W, ldw, sW, bias,
-                     sBias, bias_batches, Y, ldy, sY, M, N, K, n_tiles, total, GateOut{}, GateBwd{}, rs, LnEpi{});
+                     sBias, bias_batches, Y, ldy, sY, M, N, K, n_tiles, total, GateOut{}, GateBwd{}, rs, LnEpi{}, GatherA{});
   return check_launch(who);
 }
 
@@ -671,7 +745,38 @@ extern "C" int fu_linear_gate(const float* A, int64_t lda, const float* W, int64
   auto kern = linear_kernel<1>(K, M);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), A, lda,
                      (int64_t)0, W, ldw, (int64_t)0, bias, (int64_t)0, 1, Y, ldy, (int64_t)0, M, N, K, n_tiles, total,
-                     GateOut{Z, ldz, S, lds, C, lmax}, GateBwd{}, Resid{}, LnEpi{});
+                     GateOut{Z, ldz, S, lds, C, lmax}, GateBwd{}, Resid{}, LnEpi{}, GatherA{});
+  return check_launch(who);
+}
+
+extern "C" int fu_gather_linear_gate(const float* x, const int64_t* idx_i, const int64_t* idx_j, const float* wigner,
+                                     const float* rad, const float* csd, const int64_t* batch, const float* W,
+                                     int64_t ldw, const float* bias, float* Y, int64_t ldy, float* Z, int64_t ldz,
+                                     int64_t E, int32_t C, void* stream) {
+  const char* who = "fu_gather_linear_gate";
+  if (C <= 0 || C % 64 != 0) return set_error(FU_ERR_UNSUPPORTED, "%s: C=%d must be a multiple of 64", who, C);
+  if (matmul_mode() == FU_MATMUL_FP32)
+    return set_error(FU_ERR_UNSUPPORTED, "%s: only in the split-bf16 matrix-core mode", who);
+  const int32_t lmax = 2, K = 6 * C, N = 5 * C;
+  if (E < 0) return set_error(FU_ERR_SHAPE, "%s: E=%lld", who, (long long)E);
+  if (ldw < K || ldy < N || ldz < 3 * C || (ldw | ldy | ldz) % 4 != 0)
+    return set_error(FU_ERR_SHAPE, "%s: ldw >= 6C, ldy >= 5C, ldz >= 3C (multiples of 4) required", who);
+  if (E == 0) return FU_OK;
+  if (!x || !idx_i || !idx_j || !wigner || !rad || !csd || !batch || !W || !Y || !Z)
+    return set_error(FU_ERR_NULL, "%s: NULL operand", who);
+  if (!aligned16(x) || !aligned16(rad) || !aligned16(csd) || !aligned16(W) || !aligned16(Y) || !aligned16(Z) ||
+      (bias && !aligned16(bias)))
+    return set_error(FU_ERR_ALIGN, "%s: x, rad, csd, W, bias, Y and Z must be 16-byte aligned", who);
+  const int n_tiles = (N + GBN - 1) / GBN;
+  const int64_t bm = linear_tile_rows(E);
+  const int64_t total = ((E + bm - 1) / bm) * n_tiles;
+  if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: E too large", who);
+  auto kern = bm != GBM ? linear_mfma_kernel<1, true, false, true, true> : linear_mfma_kernel<1, true, false, false, true>;
+  // A is unused (the loader gathers it); x stands in as a valid pointer
+  hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), x, (int64_t)0, (int64_t)0, W,
+                     ldw, (int64_t)0, bias, (int64_t)0, 1, Y, ldy, (int64_t)0, E, N, K, n_tiles, total,
+                     GateOut{Z, ldz, nullptr, 0, C, lmax}, GateBwd{}, Resid{}, LnEpi{},
+                     GatherA{x, idx_i, idx_j, wigner, rad, csd, batch, C});
   return check_launch(who);
 }
 
@@ -699,7 +804,7 @@ extern "C" int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* W
   auto kern = linear_kernel<2>(K, M);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), gZo, ldgz,
                      (int64_t)0, Wt, ldw, (int64_t)0, (const float*)nullptr, (int64_t)0, 1, gY0, ldg, (int64_t)0, M, N,
-                     K, n_tiles, total, GateOut{}, GateBwd{Y0, ldy0, P1, ldp1, P2, ldp2, C, lmax}, Resid{}, LnEpi{});
+                     K, n_tiles, total, GateOut{}, GateBwd{Y0, ldy0, P1, ldp1, P2, ldp2, C, lmax}, Resid{}, LnEpi{}, GatherA{});
   return check_launch(who);
 }
 
@@ -753,7 +858,7 @@ extern "C" int fu_linear_ln_silu(const float* A, int64_t lda, int64_t stride_a, 
                      W, ldw, stride_w, bias, stride_bias, bias_batches, Y, ldy, stride_y, M, N, K, n_tiles, total,
                      GateOut{}, GateBwd{}, Resid{},
                      LnEpi{tab_src, tab_dst, ldt, z, isrc, idst, ln_bias, gamma, beta, mean, rstd, G, eps, pre, ldpre,
-                           stride_pre, nullptr, 0});
+                           stride_pre, nullptr, 0}, GatherA{});
   return check_launch(who);
 }
 
@@ -780,7 +885,7 @@ extern "C" int fu_linear_ln_silu_bwd(const float* A, int64_t lda, const float* W
                      (int64_t)0, (const float*)nullptr, (int64_t)0, 0, g_x, ldgx, (int64_t)0, M, N, K, n_tiles, total,
                      GateOut{}, GateBwd{}, Resid{},
                      LnEpi{tab_src, tab_dst, ldt, z, isrc, idst, ln_bias, gamma, beta, const_cast<float*>(mean),
-                           const_cast<float*>(rstd), G, 0.0f, nullptr, 0, 0, g_out, ldgo});
+                           const_cast<float*>(rstd), G, 0.0f, nullptr, 0, 0, g_out, ldgo}, GatherA{});
   return check_launch(who);
 }
 
@@ -811,6 +916,6 @@ extern "C" int fu_linear_dgrad_ln_silu_bwd(const float* A, int64_t lda, const fl
                      total, GateOut{}, GateBwd{}, Resid{},
                      LnEpi{nullptr, nullptr, 0, nullptr, nullptr, nullptr, nullptr, gamma + go, beta + go,
                            const_cast<float*>(mean) + group, const_cast<float*>(rstd) + group, G, 0.0f,
-                           const_cast<float*>(x) + go, ldx, 0, nullptr, 0});
+                           const_cast<float*>(x) + go, ldx, 0, nullptr, 0}, GatherA{});
   return check_launch(who);
 }

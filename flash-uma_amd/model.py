@@ -260,7 +260,7 @@ class Packed_eSCN_Layer(nn.Module):
                 self.gamma_rad1_2, self.beta_rad1_2, self.W_rad1_3, self.b_rad1_3)
 
     def forward(self, x_in, x_edge_raw, wigner, env, idx_i, idx_j, row_ptr, col_idx, csd_emb, batch,
-                topology=None, rad_out=None, wig_ext=None, rad_src=None, sink=None):
+                topology=None, rad_out=None, wig_ext=None, rad_src=None, sink=None, gather_m0=False):
         """rad_out, when given, is this block's radial-MLP output (computed by the model's
         RadialBank); otherwise it is computed here from x_edge_raw (E, B+2C).  wig_ext: the
         degree-3/4 Wigner rows (ops/lmax.wigner_extend), needed for lmax > 2."""
@@ -276,7 +276,7 @@ class Packed_eSCN_Layer(nn.Module):
             [getattr(self, "W_conv2_m" + m + x) for m in "12" for x in sfx]
         Zo_m0, Zo_m1, Zo_m2 = edge_block(x_norm, wigner, wig_ext, rad_out, idx_i, idx_j, csd_emb, batch, topology,
                                          self.layout, self.lmax, c1, c2, self.C, self._complex_splits(x_norm.device),
-                                         rad_src, sink)
+                                         rad_src, sink, gather_m0)
         del rad_out
         if self.lmax == 2:
             x_mid = rotate_scatter_split(Zo_m0, Zo_m1, Zo_m2, wigner, env, x_skip, idx_j, row_ptr, col_idx,
@@ -313,6 +313,11 @@ class eSCN_Inference_Model(nn.Module):
     # each (ops/edge_grad.py); False returns per-block gradients for autograd to sum instead
     # (the same values up to the order of the fp32 additions).
     SUM_EDGE_GRADS_IN_PLACE = True
+    # conv1 m = 0 gathers its operand in the GEMM loader (fu_gather_linear_gate; lmax 2,
+    # split-bf16 mode) instead of reading the gather's X_m0.  Off by default: at bcc Fe the
+    # fused GEMM costs more than the gather traffic it removes (each rotated element is
+    # produced once per 128-column tile of the 640 outputs).
+    GATHER_IN_CONV1 = False
 
     def __init__(self, num_layers=4, sphere_channels=128, edge_channels=128, num_distance_basis=32, cutoff=5.0,
                  coeff_g=-0.5, lmax=2):
@@ -427,7 +432,7 @@ class eSCN_Inference_Model(nn.Module):
             rad, rads[k + 1] = rads[k + 1], None
             x_node_s = layer(x_node_s, None, wigner, env, idx_i_s, idx_j_s, row_ptr, col_idx, csd_emb,
                              batch_s, topo, rad_out=rad, wig_ext=wig_ext,
-                             rad_src=srcs[k + 1] if srcs else None, sink=sink)
+                             rad_src=srcs[k + 1] if srcs else None, sink=sink, gather_m0=self.GATHER_IN_CONV1)
             del rad
             if self.charge_end > self.charge_start:
                 x_node_s = balance_channels_batched(x_node_s, charge, natoms, batch_s, self.charge_start,

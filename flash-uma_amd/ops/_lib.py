@@ -49,6 +49,7 @@ SIGNATURES: dict[str, list] = {
     "fu_complex_weight_split_bytes": [I32, I32],
     "fu_complex_weight_split": [P, P, I64, I32, I32, P, P],
     "fu_linear_gate": [P, I64, P, I64, P, P, I64, P, I64, P, I64, I64, I32, I32, I32, P],
+    "fu_gather_linear_gate": [P, P, P, P, P, P, P, P, I64, P, P, I64, P, I64, I64, I32, P],
     "fu_complex_linear_gate": [P, P, I64, P, P, I64, P, P, P, I64, P, P, I64, P, I64, I32, I32, I64, I32, I32, P],
     "fu_linear_gate_bwd": [P, I64, P, I64, P, I64, P, I64, P, I64, P, I64, I64, I32, I32, I32, P],
     "fu_linear_ln_silu": [P, I64, I64, P, I64, I64, P, I64, I32, P, I64, I64, P, I64, I64, I64, I32, I32, I32,

@@ -33,18 +33,19 @@ def block_permutation(perm, C: int) -> torch.Tensor:
     return torch.cat([torch.arange(p * C, (p + 1) * C) for p in perm])
 
 
-def gather_fwd(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch, layout):
-    """fu_gather_fwd: (X_m0, X_m1, X_m2) for contiguous, correctly typed operands."""
+def gather_fwd(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch, layout, skip_m0=False):
+    """fu_gather_fwd: (X_m0, X_m1, X_m2) for contiguous, correctly typed operands; with
+    skip_m0, X_m0 is None (not formed: conv1 m = 0 gathers it, fu_gather_linear_gate)."""
     N, _, C = x_in.shape
     E = idx_i.shape[0]
     if rad_out.shape != (E, RAD_MULT * C):
         raise _lib.FlashUMAError(f"rad_out must be ({E}, {RAD_MULT * C}), got {tuple(rad_out.shape)}")
     dev = x_in.device
-    X_m0 = torch.empty((E, X_M0_MULT * C), device=dev, dtype=torch.float32)
+    X_m0 = None if skip_m0 else torch.empty((E, X_M0_MULT * C), device=dev, dtype=torch.float32)
     X_m1 = torch.empty((E, X_M1_MULT * C), device=dev, dtype=torch.float32)
     X_m2 = torch.empty((E, X_M2_MULT * C), device=dev, dtype=torch.float32)
     _lib.call("fu_gather_fwd", x_in.data_ptr(), idx_i.data_ptr(), idx_j.data_ptr(), wigner.data_ptr(),
-              rad_out.data_ptr(), csd_emb.data_ptr(), batch.data_ptr(), X_m0.data_ptr(), X_m1.data_ptr(),
+              rad_out.data_ptr(), csd_emb.data_ptr(), batch.data_ptr(), _lib.ptr(X_m0), X_m1.data_ptr(),
               X_m2.data_ptr(), E, N, csd_emb.shape[0], C, int(layout), _lib.stream_ptr(dev))
     return X_m0, X_m1, X_m2
 

@@ -78,6 +78,19 @@ def fused_gating_split(Y_m0, Y_m1, Y_m2, C, layout=0):
     return FusedGatingSplit.apply(Y_m0, Y_m1, Y_m2, C, layout)
 
 
+def _gather_conv1_gate_m0(ops, W0, b0, C, st):
+    """fu_gather_linear_gate: (Y0, Z0) of conv1 m = 0 with X_m0 gathered in the GEMM loader
+    from the gather operands (x, idx_i, idx_j, wigner, rad, csd, batch; layout 1, lmax 2)."""
+    x, idx_i, idx_j, wigner, rad, csd, batch = ops
+    E = idx_i.shape[0]
+    Y0 = torch.empty(E, 5 * C, device=x.device, dtype=torch.float32)
+    Z0 = torch.empty(E, 3 * C, device=x.device, dtype=torch.float32)
+    _lib.call("fu_gather_linear_gate", x.data_ptr(), idx_i.data_ptr(), idx_j.data_ptr(), wigner.data_ptr(),
+              rad.data_ptr(), csd.data_ptr(), batch.data_ptr(), W0.data_ptr(), W0.stride(0), _lib.ptr(b0),
+              Y0.data_ptr(), Y0.stride(0), Z0.data_ptr(), Z0.stride(0), E, C, st)
+    return Y0, Z0
+
+
 def _conv1_gate_m0(X0, W0, b0, C, L, st):
     """fu_linear_gate: Y0 (gate-paired pre-activations, kept for the backward) and Z0."""
     E = X0.shape[0]
@@ -144,17 +157,21 @@ def conv1_gate(X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C,
     return Conv1Gate.apply(X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C, splits)
 
 
-def conv_pair_fwd(X: list, conv1, conv2, C: int, splits):
+def conv_pair_fwd(X: list, conv1, conv2, C: int, splits, m0=None):
     """conv1 + gate + conv2 of one block on X = [X_m0, X_m1, X_m2].  Each entry of X is set
     to None once its GEMM has read it, so a caller that hands over its only references
-    frees the (E, 18C) gather output while the block runs.  Returns (Zo0, Zo1, Zo2) and the
+    frees the (E, 18C) gather output while the block runs.  m0: None, or conv1 m = 0's
+    (Y0, Z0) computed already (X_m0 is then None).  Returns (Zo0, Zo1, Zo2) and the
     pre-activations (Y0, Y1, Y2) the backward needs."""
     W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn = conv1
     V0, c0, V0t, R1, I1, R1t, I1tn, R2, I2, R2t, I2tn = conv2
-    st = _lib.stream_ptr(X[0].device)
+    st = _lib.stream_ptr(X[1].device)
     L = _degrees(W0, C)
     sp = splits or (None,) * 8
-    Y0, Z0 = _conv1_gate_m0(_lib.require(X[0], torch.float32, "X_m0"), W0, b0, C, L, st)
+    if m0 is None:
+        Y0, Z0 = _conv1_gate_m0(_lib.require(X[0], torch.float32, "X_m0"), W0, b0, C, L, st)
+    else:
+        Y0, Z0 = m0
     X[0] = None
     X1, X2 = _lib.require(X[1], torch.float32, "X_m1"), _lib.require(X[2], torch.float32, "X_m2")
     X[1] = X[2] = None
@@ -249,21 +266,27 @@ class EdgeBlock(torch.autograd.Function):
     gate + conv2 (model.py:150-154).  The (E, 18C) gather output X lives only inside the
     forward (each part freed after its GEMM) and its gradient only inside the backward, which
     runs conv_pair_bwd and then the node-centric gather backward.  lmax = 2 (layout 0 or 1) or
-    lmax = 3, 4 (reference block order with the degree-3/4 Wigner rows wig_ext)."""
+    lmax = 3, 4 (reference block order with the degree-3/4 Wigner rows wig_ext).  gather_m0
+    (lmax 2, layout 1, split-bf16 mode): conv1 m = 0 gathers its operand in the GEMM loader
+    (fu_gather_linear_gate) and the gather forms X_m1, X_m2 only."""
 
     @staticmethod
     def forward(ctx, x_in, wigner, wig_ext, rad_out, idx_i, idx_j, csd_emb, batch, topology, layout, lmax, conv1,
-                conv2, C, splits, rad_src, sink=None):
+                conv2, C, splits, rad_src, sink=None, gather_m0=False):
         from .gather import gather_fwd, gather_operands
         from .lmax import gather_lmax_fwd, gather_lmax_operands
         L = int(lmax)
+        m0 = None
         if L == 2:
             ops = gather_operands(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch)
-            X = list(gather_fwd(*ops, layout))
+            fuse = gather_m0 and int(layout) == 1 and _lib.get_matmul_mode() == _lib.MATMUL_SPLIT_BF16
+            X = list(gather_fwd(*ops, layout, skip_m0=fuse))
+            if fuse:
+                m0 = _gather_conv1_gate_m0(ops, conv1[0], conv1[1], C, _lib.stream_ptr(x_in.device))
         else:
             ops = gather_lmax_operands(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, L)
             X = list(gather_lmax_fwd(*ops, L))
-        Zo, Y = conv_pair_fwd(X, conv1, conv2, C, splits)
+        Zo, Y = conv_pair_fwd(X, conv1, conv2, C, splits, m0)
         r = 4 if L == 2 else 5   # position of rad_out among the gather operands
         if rad_src is not None:
             # keep the (E, C) source of the radial output instead of the (E, 6 L C) output
@@ -301,15 +324,16 @@ class EdgeBlock(torch.autograd.Function):
         else:
             g_x, g_w, g_ext, g_rad = gather_lmax_bwd(*ops, ctx.topology, ctx.L, *gx, sink=ctx.sink)
         return (g_x, g_w, g_ext, g_rad, None, None, None, None, None, None, None, None, None, None, None, None,
-                None)
+                None, None)
 
 
 def edge_block(x_in, wigner, wig_ext, rad_out, idx_i, idx_j, csd_emb, batch, topology, layout, lmax, conv1, conv2, C,
-               splits=None, rad_src=None, sink=None):
+               splits=None, rad_src=None, sink=None, gather_m0=False):
     """gather_wigner_split (or gather_rotate_lmax) followed by conv1_gate_conv2, as one node
     whose gather output never outlives the block: returns (Zout_m0, Zout_m1, Zout_m2).
     rad_src: None, or the radial bank's (h2_k, W3_k, b3_k) source of rad_out; the backward
     then recomputes rad_out from it instead of keeping it (memory for one extra GEMM).
-    sink: accumulators of the Wigner-row gradients (ops/edge_grad.py) or None."""
+    sink: accumulators of the Wigner-row gradients (ops/edge_grad.py) or None.  gather_m0: conv1
+    m = 0 gathers its own operand (see EdgeBlock)."""
     return EdgeBlock.apply(x_in, wigner, wig_ext, rad_out, idx_i, idx_j, csd_emb, batch, topology, layout, lmax,
-                           tuple(conv1), tuple(conv2), C, splits, rad_src, sink)
+                           tuple(conv1), tuple(conv2), C, splits, rad_src, sink, gather_m0)

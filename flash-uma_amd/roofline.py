@@ -38,8 +38,11 @@ def _gating_bwd(a):
 
 
 def _gather_fwd(a):
+    # rad (12C) read and X (18C) written per edge; without X_m0 (conv1 m = 0 gathers its own
+    # operand) 6C fewer of each
     E, N, C = a[10], a[11], a[13]
-    return E * (30 * C * 4 + 34 * 4 + 16) + N * (9 * C * 4 + 8), 0
+    per_edge = 30 * C if a[7] is not None else 18 * C
+    return E * (per_edge * 4 + 34 * 4 + 16) + N * (9 * C * 4 + 8), 0
 
 
 def _acc_read(E, acc, wig, env=1):
@@ -222,6 +225,14 @@ def _linear_gate(a):
     return 4 * (M * K + N * K + M * N + zs * M * C), 2 * M * N * K
 
 
+def _gather_linear_gate(a):
+    # conv1 m = 0 with its operand gathered: the m = 0 radial blocks (6C), the edge's two ids
+    # and 8 Wigner scalars read, Y (5C) and Z (3C) written, W once (the node rows are the
+    # gather's per-node bytes, L2-resident across a node's edges, and not counted)
+    E, C = a[14], a[15]
+    return 4 * E * (6 * C + 5 * C + 3 * C + 8) + 16 * E + 4 * 30 * C * C, 2 * E * 5 * C * 6 * C
+
+
 def _complex_linear_gate(a):
     # complex product plus the gate columns of Y0 read (Nc) and the gated copies Z_r, Z_i (2 Nc)
     M, Nc, Kc = a[17], a[18], a[19]
@@ -265,6 +276,7 @@ WORK = {
     "fu_linear_dgrad_ln_silu_bwd": _linear_dgrad_ln_silu_bwd,
     "fu_complex_linear": _complex_linear,
     "fu_linear_gate": _linear_gate,
+    "fu_gather_linear_gate": _gather_linear_gate,
     "fu_linear_gate_bwd": _linear_gate_bwd,
     "fu_complex_linear_gate_bwd": _complex_linear_gate_bwd,
     "fu_gather_fwd_lmax": _gather_fwd_l,
@@ -282,7 +294,7 @@ WORK = {
 
 MFMA_BOUND = {"fu_linear", "fu_linear_batched", "fu_complex_linear", "fu_linear_gate", "fu_complex_linear_gate",
               "fu_linear_gate_bwd", "fu_complex_linear_gate_bwd", "fu_linear_ln_silu", "fu_linear_ln_silu_bwd",
-              "fu_linear_dgrad_ln_silu_bwd"}
+              "fu_linear_dgrad_ln_silu_bwd", "fu_gather_linear_gate"}
 
 
 def summarize(durations, matmul_mode: int = MATMUL_SPLIT_BF16) -> dict:

@@ -102,7 +102,8 @@ int fu_edge_vec_reduce(const float* g_d, const int32_t* recv_ptr, const int32_t*
  * interleaved, ops/gather.py:132-154).  layout 1: X_m0 and rad side-major (all sender
  * blocks, then all receiver blocks); X_m1 as [real half | imaginary half], each half
  * side-major; X_m2 in reference order.  The model pairs it with conv1 / radial weights
- * permuted the same way, which leaves every product unchanged. */
+ * permuted the same way, which leaves every product unchanged.  X_m0 may be NULL: the m = 0
+ * blocks are then not formed (fu_gather_linear_gate gathers them inside conv1 m = 0). */
 int fu_gather_fwd(const float* x, const int64_t* idx_i, const int64_t* idx_j, const float* wigner,
                   const float* rad, const float* csd_emb, const int64_t* batch, float* X_m0,
                   float* X_m1, float* X_m2, int64_t E, int64_t N, int64_t S, int32_t C,
@@ -306,6 +307,19 @@ int fu_complex_weight_split(const float* P, const float* Q, int64_t ldw, int32_t
 int fu_linear_gate(const float* A, int64_t lda, const float* W, int64_t ldw, const float* bias,
                    float* Y, int64_t ldy, float* Z, int64_t ldz, float* S, int64_t lds, int64_t M,
                    int32_t C, int32_t K, int32_t lmax, void* stream);
+
+/* conv1 m = 0 with its A operand gathered in the GEMM loader (the gather-rotate fused with the
+ * m = 0 SO(2) linear, ops/gather.py:128-154 -> model.py:152, lmax 2): the result of
+ * fu_gather_fwd (layout 1) followed by fu_linear_gate on X_m0 (W: 5C x 6C gate-paired, ldw),
+ * without X_m0 ever being stored: each loader chunk rotates the two node rows of its edges by
+ * the m = 0 Wigner rows (csd_emb[batch] added on l = 0) and scales them by the radial row.
+ * Y (E x 5C) and Z (E x 3C) as fu_linear_gate.  Split-bf16 matrix-core mode only
+ * (FU_ERR_UNSUPPORTED in the fp32 mode); C a multiple of 64. */
+int fu_gather_linear_gate(const float* x, const int64_t* idx_i, const int64_t* idx_j,
+                          const float* wigner, const float* rad, const float* csd_emb,
+                          const int64_t* batch, const float* W, int64_t ldw, const float* bias,
+                          float* Y, int64_t ldy, float* Z, int64_t ldz, int64_t E, int32_t C,
+                          void* stream);
 
 /* conv1 m = 1, 2 fused with the gate activation: fu_complex_linear, then
  * Z_r = Y_r s, Z_i = Y_i s with s = sigmoid(gate) of gate column t = s_off + column (degree

@@ -68,6 +68,11 @@ def test_error_codes():
     st, msg = _status("fu_linear_ln_silu", None, 640, 128, None, 128, 0, None, 0, 0, None, 640, 128, None, 0, 0, 0,
                       128, 128, 4, *([None] * 2), 0, *([None] * 8), 5, ctypes.c_float(1e-5), None)
     assert st == -2 and "groups of 128" in msg
+    # conv1 m = 0 with its operand gathered: C a multiple of 64, strides of whole rows
+    st, msg = _status("fu_gather_linear_gate", *([None] * 7), None, 576, None, None, 480, None, 288, 0, 96, None)
+    assert st == -2 and "C=96" in msg
+    st, msg = _status("fu_gather_linear_gate", *([None] * 7), None, 700, None, None, 640, None, 384, 0, 128, None)
+    assert st == -1 and "ldw" in msg
     # the output-layer gradient GEMM with the LayerNorm backward: one group of G
     st, msg = _status("fu_linear_dgrad_ln_silu_bwd", None, 64, None, 64, None, 640, 0, 64, None, 640, *([None] * 4),
                       5, 5, None)
@@ -134,6 +139,7 @@ def test_zero_rows_accept_empty_arrays():
         "fu_linear_ln_silu_bwd": (None, 64, None, 64, None, 640, 0, 640, 64, None, 640, *([None] * 2), 0,
                                   *([None] * 8), 5, None),
         "fu_linear_dgrad_ln_silu_bwd": (None, 64, None, 64, None, 640, 0, 64, None, 640, *([None] * 4), 5, 4, None),
+        "fu_gather_linear_gate": (*([None] * 7), None, 768, None, None, 640, None, 384, 0, 128, None),
     }
     for name, args in calls.items():
         st, msg = _status(name, *args)

@@ -398,3 +398,32 @@ def test_edge_grads_summed_in_place(cuda, lmax):
     buf2, acc2 = sink.target(edge_grad.WIGNER, w)
     assert buf2 is buf and acc2 == 1
     assert sink.take(edge_grad.WIGNER) is buf and sink.take(edge_grad.WIGNER) is None
+
+
+@pytest.mark.gpu
+def test_gather_in_conv1_matches_default(cuda):
+    """GATHER_IN_CONV1 (conv1 m = 0 gathering its operand in the GEMM loader, the gather forming
+    X_m1, X_m2 only) against the default path on a bcc Fe cell large enough for the 256-row
+    tiles (4,096 atoms, 122,880 edges): energy, forces and stress agree to fp32 rounding."""
+    import escn_md
+    import heads
+    import systems
+    from wrapper import ZeroAllocBackbone
+    bb = escn_md.eSCNMDBackbone(seed=0, num_layers=2)
+    hd = heads.MLPEnergyHead(bb.sphere_channels, bb.hidden_channels, seed=1)
+    model = heads.PotentialModel(ZeroAllocBackbone(bb.to(cuda)), hd.to(cuda))
+    s = systems.bcc_fe(n_rep=8)
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, 6.0, 30)
+    ce = model.backbone.ce
+    a = _run(model, s, ei, off, cuda)
+    old = ce.GATHER_IN_CONV1
+    try:
+        ce.GATHER_IN_CONV1 = True
+        b = _run(model, s, ei, off, cuda)
+    finally:
+        ce.GATHER_IN_CONV1 = old
+    assert abs(a["energy"].item() - b["energy"].item()) <= 1e-6 * abs(a["energy"].item())
+    fs = a["forces"].abs().max().item()
+    assert (a["forces"] - b["forces"]).abs().max().item() <= 1e-5 * fs
+    ss = a["stress"].abs().max().item()
+    assert (a["stress"] - b["stress"]).abs().max().item() <= 1e-5 * ss

@@ -726,3 +726,43 @@ def test_linear_ln_silu_matches_two_kernels(cuda, matmul_mode, M):
                   k, st)
     gref2 = _ln_grouped_bwd(p2, None, None, None, None, None, gm2, bt2, m2, r2, g_h2, G, C)
     assert_close(g_p2, gref2, 2e-6, "layer-2 LayerNorm input gradient")
+
+
+@pytest.mark.parametrize("E", [1000, 70001])
+def test_gather_linear_gate_matches_gather_then_gemm(cuda, E):
+    """fu_gather_linear_gate (conv1 m = 0 with X_m0 gathered in the GEMM loader) against
+    fu_gather_fwd (layout 1) followed by fu_linear_gate, on both tile heights (70,001 rows:
+    256-row tiles and a ragged last tile), two systems' csd rows; and the gather without its
+    m = 0 part leaves X_m1 and X_m2 bit for bit as they were."""
+    from ops import _lib
+    from ops.gather import gather_fwd
+    g = torch.Generator().manual_seed(E)
+    N, C, S = 2000, 128, 2
+    q = torch.randn(E, 4, generator=g, dtype=torch.float64)
+    q = q / q.norm(dim=1, keepdim=True)
+    wig = torch.cat([R.rotation_from_quaternion(q).reshape(E, 9), R.wigner_l2_from_quaternion(q).reshape(E, 25)],
+                    1).float().to(cuda)
+    x = torch.randn(N, 9, C, generator=g).to(cuda)
+    ii = torch.randint(0, N, (E,), generator=g).to(cuda)
+    jj = torch.randint(0, N, (E,), generator=g).to(cuda)
+    rad = torch.randn(E, 12 * C, generator=g).to(cuda)
+    csd = torch.randn(S, C, generator=g).to(cuda)
+    batch = torch.randint(0, S, (N,), generator=g).to(cuda)
+    W = (torch.randn(5 * C, 6 * C, generator=g) / (6 * C) ** 0.5).to(cuda)
+    b = (torch.randn(5 * C, generator=g) * 0.1).to(cuda)
+    st = _lib.stream_ptr(cuda)
+    X0, X1, X2 = gather_fwd(x, ii, jj, wig, rad, csd, batch, 1)
+    Y, Z = torch.empty(E, 5 * C, device=cuda), torch.empty(E, 3 * C, device=cuda)
+    _lib.call("fu_linear_gate", X0.data_ptr(), 6 * C, W.data_ptr(), 6 * C, b.data_ptr(), Y.data_ptr(), 5 * C,
+              Z.data_ptr(), 3 * C, None, 0, E, C, 6 * C, 2, st)
+    none, X1s, X2s = gather_fwd(x, ii, jj, wig, rad, csd, batch, 1, skip_m0=True)
+    assert none is None and torch.equal(X1s, X1) and torch.equal(X2s, X2)
+    Yf, Zf = torch.empty_like(Y), torch.empty_like(Z)
+    args = (x.data_ptr(), ii.data_ptr(), jj.data_ptr(), wig.data_ptr(), rad.data_ptr(), csd.data_ptr(),
+            batch.data_ptr(), W.data_ptr(), 6 * C, b.data_ptr(), Yf.data_ptr(), 5 * C, Zf.data_ptr(), 3 * C, E, C, st)
+    _lib.call("fu_gather_linear_gate", *args)
+    assert_close(Yf, Y, 2e-6, "Y (pre-activations)")
+    assert_close(Zf, Z, 2e-6, "Z (gated)")
+    with _lib.matmul_mode(_lib.MATMUL_FP32):
+        with pytest.raises(_lib.FlashUMAError, match="split-bf16"):
+            _lib.call("fu_gather_linear_gate", *args)

@@ -38,6 +38,7 @@ GEMMS = {
     "fu_linear_ln_silu": (dict(M=1000, N=128, K=128, batch=5, G=5), 2 * 5 * 1000 * 128 * 128),
     "fu_linear_ln_silu_bwd": (dict(M=1000, N=640, K=64, G=5), 2 * 1000 * 640 * 64),
     "fu_linear_dgrad_ln_silu_bwd": (dict(M=1000, K=1536, G=5, group=2), 2 * 1000 * 128 * 1536),
+    "fu_gather_linear_gate": (dict(E=1000, C=128), 2 * 1000 * 640 * 768),
 }
 
 
