@@ -81,12 +81,6 @@ __device__ __forceinline__ void st4_nt(float* p, float4 v) {
   const f4 t = {v.x, v.y, v.z, v.w};
   __builtin_nontemporal_store(t, reinterpret_cast<f4*>(p));
 }
-// 16-byte load with the nontemporal hint (large read-once inputs)
-__device__ __forceinline__ float4 ld4_nt(const float* p) {
-  typedef float f4 __attribute__((ext_vector_type(4)));
-  const f4 t = __builtin_nontemporal_load(reinterpret_cast<const f4*>(p));
-  return make_float4(t.x, t.y, t.z, t.w);
-}
 
 __device__ __forceinline__ float4 operator*(float4 a, float4 b) {
   return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
