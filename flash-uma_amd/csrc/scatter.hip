@@ -216,27 +216,52 @@ __global__ __launch_bounds__(256) void init_scatter_fwd_kernel(
 #pragma unroll
       for (int q = 0; q < CPL; ++q) acc[k][q] = 0.0;
   }
-  const int32_t k0 = rptr[n], k1 = rptr[n + 1];
-  for (int32_t k = k0; k < k1; ++k) {
+  // The receiver's edges in CSR order; the next edge's loads are issued before the current
+  // edge is accumulated (two register sets, sched_barrier keeping the scheduler from sinking
+  // them), since one edge's arithmetic is short next to its load latency.
+  struct EdgeData {
+    float en, w1[3], w2[5];
+    Vec<CPL> r[3];
+  };
+  auto load = [&](int32_t k, EdgeData& d) {
     const int64_t e = col[k];
-    const float en = env[e];
-    float w1[3], w2[5];
+    d.en = env[e];
 #pragma unroll
-    for (int b = 0; b < 3; ++b) w1[b] = wig[e * 34 + 3 + b];   // L=1 row 1
+    for (int b = 0; b < 3; ++b) d.w1[b] = wig[e * 34 + 3 + b];   // L=1 row 1
 #pragma unroll
-    for (int b = 0; b < 5; ++b) w2[b] = wig[e * 34 + 19 + b];  // L=2 row 2
+    for (int b = 0; b < 5; ++b) d.w2[b] = wig[e * 34 + 19 + b];  // L=2 row 2
     const float* rp = rad + e * 3 * C + c;
-    const Vec<CPL> r0 = vload<CPL>(rp), r1 = vload<CPL>(rp + C), r2 = vload<CPL>(rp + 2 * C);
-    // messages summed in fp64 and divided by the rescale factor 5 once per node (the
-    // reference divides each message, ops/scatter.py:409-411; same value to fp32 rounding)
+#pragma unroll
+    for (int t = 0; t < 3; ++t) d.r[t] = vload_nt<CPL>(rp + t * C);
+  };
+  // messages summed in fp64 and divided by the rescale factor 5 once per node (the reference
+  // divides each message, ops/scatter.py:409-411; same value to fp32 rounding)
+  auto add = [&](const EdgeData& d) {
 #pragma unroll
     for (int q = 0; q < CPL; ++q) {
-      acc[0][q] += (double)(r0[q] * en);
+      acc[0][q] += (double)(d.r[0][q] * d.en);
 #pragma unroll
-      for (int b = 0; b < 3; ++b) acc[1 + b][q] += (double)(r1[q] * w1[b] * en);
+      for (int b = 0; b < 3; ++b) acc[1 + b][q] += (double)(d.r[1][q] * d.w1[b] * d.en);
 #pragma unroll
-      for (int b = 0; b < 5; ++b) acc[4 + b][q] += (double)(r2[q] * w2[b] * en);
+      for (int b = 0; b < 5; ++b) acc[4 + b][q] += (double)(d.r[2][q] * d.w2[b] * d.en);
     }
+  };
+  const int32_t k0 = rptr[n], k1 = rptr[n + 1];
+  if (k0 < k1) {
+    EdgeData d0, d1;
+    load(k0, d0);
+    int32_t k = k0;
+    for (; k + 2 <= k1; k += 2) {
+      load(k + 1, d1);
+      __builtin_amdgcn_sched_barrier(0);
+      add(d0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (k + 2 < k1) load(k + 2, d0);
+      __builtin_amdgcn_sched_barrier(0);
+      add(d1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (k < k1) add(d0);
   }
   float* xo = x_out + n * 9 * C + c;
 #pragma unroll
