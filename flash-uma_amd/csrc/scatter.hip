@@ -16,6 +16,8 @@ __device__ __forceinline__ int wave_id_u() { return __builtin_amdgcn_readfirstla
 
 // Rotated-frame values zr[0..8] of one edge from the three Zout m-blocks:
 // Z_m0 = [k0, k2, k6], Z_m1 = [k3, k7, k1, k5], Z_m2 = [k8, k4].
+// The conv2 outputs are read once by each scatter pass, so they carry the nontemporal hint
+// (scatter forward 231 -> 215 us at bcc Fe).
 template <int CPL>
 __device__ __forceinline__ void load_zr(const float* Z0, const float* Z1, const float* Z2, int64_t e, int c,
                                         Vec<CPL> (&zr)[9]) {
@@ -23,15 +25,15 @@ __device__ __forceinline__ void load_zr(const float* Z0, const float* Z1, const 
   const float* z0 = Z0 + e * 3 * C + c;
   const float* z1 = Z1 + e * 4 * C + c;
   const float* z2 = Z2 + e * 2 * C + c;
-  zr[0] = vload<CPL>(z0);
-  zr[2] = vload<CPL>(z0 + C);
-  zr[6] = vload<CPL>(z0 + 2 * C);
-  zr[3] = vload<CPL>(z1);
-  zr[7] = vload<CPL>(z1 + C);
-  zr[1] = vload<CPL>(z1 + 2 * C);
-  zr[5] = vload<CPL>(z1 + 3 * C);
-  zr[8] = vload<CPL>(z2);
-  zr[4] = vload<CPL>(z2 + C);
+  zr[0] = vload_nt<CPL>(z0);
+  zr[2] = vload_nt<CPL>(z0 + C);
+  zr[6] = vload_nt<CPL>(z0 + 2 * C);
+  zr[3] = vload_nt<CPL>(z1);
+  zr[7] = vload_nt<CPL>(z1 + C);
+  zr[1] = vload_nt<CPL>(z1 + 2 * C);
+  zr[5] = vload_nt<CPL>(z1 + 3 * C);
+  zr[8] = vload_nt<CPL>(z2);
+  zr[4] = vload_nt<CPL>(z2 + C);
 }
 
 template <int CPL>
@@ -300,7 +302,7 @@ __global__ __launch_bounds__(256) void init_scatter_bwd_kernel(const float* __re
 #pragma unroll
     for (int k = 0; k < 9; ++k) g[k] = vscale(vload<CPL>(go + k * C), 1.0f / 5.0f);
     const float* rp = rad + e * 3 * C + c;
-    const Vec<CPL> r0 = vload<CPL>(rp), r1 = vload<CPL>(rp + C), r2 = vload<CPL>(rp + 2 * C);
+    const Vec<CPL> r0 = vload_nt<CPL>(rp), r1 = vload_nt<CPL>(rp + C), r2 = vload_nt<CPL>(rp + 2 * C);
     Vec<CPL> p1, p2;  // projections of g onto the L=1 row 1 and L=2 row 2
 #pragma unroll
     for (int q = 0; q < CPL; ++q) {
