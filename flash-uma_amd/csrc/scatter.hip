@@ -77,30 +77,31 @@ __global__ __launch_bounds__(256) void scatter_fwd_kernel(const int32_t* __restr
     }
   };
   int32_t k = k0;
-  // two edges in flight per iteration (their loads overlap); summed in CSR order
-  for (; k + 1 < k1; k += 2) {
-    const int64_t ea = col[k], eb = col[k + 1];
-    float wa[34], wb[34];
-#pragma unroll
-    for (int q = 0; q < 34; ++q) {
-      wa[q] = wig[ea * 34 + q];
-      wb[q] = wig[eb * 34 + q];
-    }
-    const float ena = env[ea], enb = env[eb];
-    Vec<CPL> za[9], zb[9];
-    load_zr<CPL>(Z0, Z1, Z2, ea, c, za);
-    load_zr<CPL>(Z0, Z1, Z2, eb, c, zb);
-    accumulate(wa, ena, za);
-    accumulate(wb, enb, zb);
-  }
+  // summed in CSR order; the next edge's loads are issued before the current edge is summed
+  // (two register sets, sched_barrier keeping the scheduler from sinking them: 214.6 ->
+  // 211.2 us at bcc Fe against two edges loaded together and then summed)
   if (k < k1) {
-    const int64_t e = col[k];
-    float w[34];
+    float wa[34], wb[34];
+    float ena, enb;
+    Vec<CPL> za[9], zb[9];
+    auto load = [&](int64_t e, float (&w)[34], float& en, Vec<CPL> (&z)[9]) {
 #pragma unroll
-    for (int q = 0; q < 34; ++q) w[q] = wig[e * 34 + q];
-    Vec<CPL> zr[9];
-    load_zr<CPL>(Z0, Z1, Z2, e, c, zr);
-    accumulate(w, env[e], zr);
+      for (int q = 0; q < 34; ++q) w[q] = wig[e * 34 + q];
+      en = env[e];
+      load_zr<CPL>(Z0, Z1, Z2, e, c, z);
+    };
+    load(col[k], wa, ena, za);
+    for (; k + 2 <= k1; k += 2) {
+      load(col[k + 1], wb, enb, zb);
+      __builtin_amdgcn_sched_barrier(0);
+      accumulate(wa, ena, za);
+      __builtin_amdgcn_sched_barrier(0);
+      if (k + 2 < k1) load(col[k + 2], wa, ena, za);
+      __builtin_amdgcn_sched_barrier(0);
+      accumulate(wb, enb, zb);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (k < k1) accumulate(wa, ena, za);
   }
   float* xo = x_out + n * 9 * C + c;
 #pragma unroll
