@@ -13,7 +13,7 @@ CPU baseline (the float32 torch-CPU oracle on a bounded sample of the same workl
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config bcc_fe] [--no-cpu-baseline]
 
---config bcc_fe_lmax4 runs BASELINE config 5 instead (same input, lmax = 4, 8 layers, E+F).
+--config bcc_fe_lmax4 runs the lmax-4 workload instead (same input, lmax = 4, 8 layers, E+F).
 """
 from __future__ import annotations
 
@@ -34,7 +34,7 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-# backbone shape per workload: the UMA-s-shaped headline model, and BASELINE config 5
+# backbone shape per workload: the UMA-s-shaped headline model, and the lmax-4 workload
 # (lmax = 4, 8 layers, E+F) on the same bcc Fe input
 MODELS = {"bcc_fe_lmax4": dict(lmax=4, num_layers=8)}
 

@@ -1,6 +1,6 @@
 """One energy + forces (+ stress) step captured in a HIP graph and replayed with new positions.
 
-For MD and other loops that evaluate the same graph many times (the BASELINE water workload
+For MD and other loops that evaluate the same graph many times (the water-box workload
 holds its step-0 graph for 100 steps): after capture, each step is one graph launch instead
 of several hundred kernel launches plus the Python that issues them, which dominates small
 systems (a 29-atom cell spends ~3.9 ms per eager step, almost all of it launch and host

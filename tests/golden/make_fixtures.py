@@ -9,7 +9,7 @@ construction: every pair within the cutoff, no per-receiver cap, up to 171 edges
 unit cell, random cell offsets) with the same backbone, head and oracle outputs.
 Fixture fe432_oracle.npz: bcc Fe 6x6x6 (432 atoms, 12,960 edges; the headline workload's
 local structure) with the same backbone and head.
-Fixture fe54_lmax4_oracle.npz: bcc Fe 3x3x3 with BASELINE config 5's backbone (lmax = 4,
+Fixture fe54_lmax4_oracle.npz: bcc Fe 3x3x3 with the lmax-4 benchmark workload's backbone (lmax = 4,
 8 layers)."""
 import os
 import sys
@@ -73,7 +73,7 @@ def fe432():
 
 
 def fe54_lmax4():
-    """BASELINE config 5's model (lmax = 4, 8 layers) on bcc Fe 3x3x3 (54 atoms), E+F+S."""
+    """The lmax-4 benchmark workload's model (lmax = 4, 8 layers) on bcc Fe 3x3x3 (54 atoms), E+F+S."""
     _fe(3, "fe54_lmax4_oracle.npz", lmax=4, num_layers=8)
 
 

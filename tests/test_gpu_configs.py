@@ -1,4 +1,4 @@
-"""The BASELINE workloads run through the GPU path at full size.
+"""The benchmark workloads run through the GPU path at full size.
 
 * Liquid water, 333 H2O (999 atoms, cubic 21.5 A): a 100-step velocity-Verlet MD loop of
   energy + forces with the graph built once at step 0 and the topology cached (one build,

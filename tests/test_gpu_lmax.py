@@ -1,4 +1,4 @@
-"""GPU parity of the lmax = 3, 4 path (the reference rejects lmax != 2).
+"""GPU parity of the lmax = 3, 4 path (the bcc Fe lmax-4 benchmark workload; the reference rejects lmax != 2).
 
 Op level: every lmax-general entry point (Wigner extension, gather, gate, scatter, edge-degree
 scatter; forward and backward) against the float64 oracle restatements (oracle/ops_ref.py
@@ -249,7 +249,7 @@ def test_model_lmax_parity(cuda, L, layers):
 
 
 def test_config5_model_on_fe54_fixture(cuda):
-    """BASELINE config 5's backbone (lmax = 4, mmax = 2, 8 layers, C = 128) on bcc Fe 3x3x3
+    """The lmax-4 benchmark workload's backbone (lmax = 4, mmax = 2, 8 layers, C = 128) on bcc Fe 3x3x3
     (54 atoms, 30 edges per atom, E+F+S) against the committed float64 oracle fixture
     (tests/golden/fe54_lmax4_oracle.npz).  Bars as for lmax = 2; per-atom contributions rel
     1e-5 (a float32 oracle run is 1.6e-6 from float64 here)."""
@@ -269,7 +269,7 @@ def test_config5_model_on_fe54_fixture(cuda):
 
 
 def test_config5_bcc_fe_lmax4_invariants(cuda):
-    """BASELINE config 5 at full size: bcc Fe 16^3 (8,192 atoms), lmax = 4, 8 layers, C = 128,
+    """The lmax-4 benchmark workload at full size: bcc Fe 16^3 (8,192 atoms), lmax = 4, 8 layers, C = 128,
     energy + forces.  No CPU oracle finishes at this size; checked through invariants."""
     import systems
     bb, hd, model = _model(cuda, 4, 8)

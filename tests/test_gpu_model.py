@@ -1,7 +1,7 @@
 """End-to-end GPU parity: ZeroAllocBackbone + energy head (energy, forces, stress through
 the HIP kernels) against the float64 CPU oracle of the whole model.
 
-Tolerances (north star, fp32 with no TF32 anywhere): energy per atom rel <= 1e-6,
+Tolerances (the target bars, fp32 with no TF32 anywhere): energy per atom rel <= 1e-6,
 forces and stress max-abs <= 1e-4.  Per-atom energy contributions are also reported and
 held to rel 2e-5, which is what the oracle itself reaches in fp32 against fp64 on these
 random-init weights (a float32 oracle run shows up to ~5e-6)."""
