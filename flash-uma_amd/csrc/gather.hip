@@ -4,7 +4,8 @@
 // Forward: one wave64 per edge, lanes across channels (CPL = C/64 per lane); each workgroup
 // takes a contiguous edge range, XCD-aware (block_edge_range).  The edge's indices and its 34
 // Wigner scalars are wave-uniform (scalar loads); every node row, radial row and output slot
-// is one coalesced row access.
+// is one coalesced row access.  At C = 128 a wave takes two edges, 32 lanes of 4 channels
+// each (gather_fwd_pair_kernel).
 //
 // Backward: node-centric.  A 128-thread workgroup owns one node: one wave walks the node's
 // receiver segment (edges e with idx_j[e] = n, receiver CSR) and the other its sender
@@ -120,6 +121,72 @@ __global__ __launch_bounds__(256) void gather_fwd_kernel(
     float* o1 = X1 + e * 8 * C + c;
     float* o2 = X2 + e * 4 * C + c;
     // m0 slots: rotated coefficient k0, k2, k6; m1: k3, k7 (R) and k1, k5 (I); m2: k8 (R), k4 (I)
+    constexpr int K0[3] = {0, 2, 6}, K1[4] = {3, 7, 1, 5}, K2[2] = {8, 4};
+    if constexpr (M0) {
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        vstore_nt(o0 + slot_m0<L>(0, q) * C, vmul(rs.r[K0[q]], r[2 * q]));
+        vstore_nt(o0 + slot_m0<L>(1, q) * C, vmul(rt.r[K0[q]], r[2 * q + 1]));
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      vstore_nt(o1 + slot_m1<L>(0, q) * C, vmul(rs.r[K1[q]], r[6 + 2 * (q & 1)]));
+      vstore_nt(o1 + slot_m1<L>(1, q) * C, vmul(rt.r[K1[q]], r[7 + 2 * (q & 1)]));
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      vstore_nt(o2 + slot_m2<L>(0, q) * C, vmul(rs.r[K2[q]], r[10]));
+      vstore_nt(o2 + slot_m2<L>(1, q) * C, vmul(rt.r[K2[q]], r[11]));
+    }
+  }
+}
+
+// C = 128 with two edges per wave: lanes 0-31 take edge e, lanes 32-63 edge e + 1, four
+// channels per lane, so every access is 16 bytes per lane (against 8 with one edge per wave:
+// 748-752 against 772-776 us at bcc Fe, bitwise equal outputs).  The Wigner scalars are then
+// per-lane loads (two edges per wave), which the L1 serves.
+template <int L, bool M0 = true>
+__global__ __launch_bounds__(256) void gather_fwd_pair_kernel(
+    const float* __restrict__ x, const int64_t* __restrict__ idx_i, const int64_t* __restrict__ idx_j,
+    const float* __restrict__ wig, const float* __restrict__ rad, const float* __restrict__ csd,
+    const int64_t* __restrict__ batch, float* __restrict__ X0, float* __restrict__ X1,
+    float* __restrict__ X2, int64_t E) {
+  constexpr int CPL = 4, C = 128;
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5;
+  const int c = (lane & 31) * CPL;
+  int64_t e0, e1;
+  block_edge_range(E, e0, e1);
+  const int nw = blockDim.x >> 6;
+  for (int64_t eb = e0 + 2 * wave_id_uniform(); eb < e1; eb += 2 * nw) {
+    // the second half of a wave at the range's odd end recomputes edge eb and stores nothing
+    const bool live = eb + half < e1;
+    const int64_t e = live ? eb + half : eb;
+    const int64_t i = idx_i[e], j = idx_j[e];
+    float w[34];
+#pragma unroll
+    for (int k = 0; k < 34; ++k) w[k] = wig[e * 34 + k];
+    Rows9<CPL> vs, vt, rs, rt;
+    const float* xs = x + i * 9 * C + c;
+    const float* xt = x + j * 9 * C + c;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+      vs.r[k] = vload<CPL>(xs + k * C);
+      vt.r[k] = vload<CPL>(xt + k * C);
+    }
+    vs.r[0] = vadd(vs.r[0], vload<CPL>(csd + batch[i] * C + c));
+    vt.r[0] = vadd(vt.r[0], vload<CPL>(csd + batch[j] * C + c));
+    rotate9(w, vs, rs);
+    rotate9(w, vt, rt);
+    const float* rr = rad + e * 12 * C + c;
+    Vec<CPL> r[12];
+#pragma unroll
+    for (int k = M0 ? 0 : 6; k < 12; ++k) r[k] = vload_nt<CPL>(rr + slot_rad<L>(k & 1, k >> 1) * C);
+    if (!live) continue;
+    float* o0 = X0 + e * 6 * C + c;
+    float* o1 = X1 + e * 8 * C + c;
+    float* o2 = X2 + e * 4 * C + c;
     constexpr int K0[3] = {0, 2, 6}, K1[4] = {3, 7, 1, 5}, K2[2] = {8, 4};
     if constexpr (M0) {
 #pragma unroll
@@ -358,12 +425,20 @@ template <int CPL, int L>
 static void launch_gather_fwd(const float* x, const int64_t* idx_i, const int64_t* idx_j, const float* wigner,
                               const float* rad, const float* csd, const int64_t* batch, float* X0, float* X1,
                               float* X2, int64_t E, hipStream_t st) {
-  if (X0)
+  if constexpr (CPL == 2) {
+    if (X0)
+      hipLaunchKernelGGL((gather_fwd_pair_kernel<L>), dim3(edge_grid(E)), dim3(256), 0, st, x, idx_i, idx_j, wigner,
+                         rad, csd, batch, X0, X1, X2, E);
+    else
+      hipLaunchKernelGGL((gather_fwd_pair_kernel<L, false>), dim3(edge_grid(E)), dim3(256), 0, st, x, idx_i, idx_j,
+                         wigner, rad, csd, batch, X0, X1, X2, E);
+  } else if (X0) {
     hipLaunchKernelGGL((gather_fwd_kernel<CPL, L>), dim3(edge_grid(E)), dim3(256), 0, st, x, idx_i, idx_j, wigner,
                        rad, csd, batch, X0, X1, X2, E);
-  else
+  } else {
     hipLaunchKernelGGL((gather_fwd_kernel<CPL, L, false>), dim3(edge_grid(E)), dim3(256), 0, st, x, idx_i, idx_j,
                        wigner, rad, csd, batch, X0, X1, X2, E);
+  }
 }
 
 template <int CPL, int L>
