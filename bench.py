@@ -28,6 +28,12 @@ PKG = os.path.join(ROOT, "flash-uma_amd")
 sys.path[:0] = [ROOT, PKG]
 
 METRIC = "atom-steps/sec (energy+forces) on 1 MI355X; % HBM roofline per kernel"
+MATMUL_TEXT = {
+    0: "fp32 operands split exactly into three bf16 planes, six bf16 MFMA products, fp32 accumulation",
+    1: "fp32 MFMA",
+    2: "fp32 operands scaled by per-row powers of two and split into two fp16 planes, three fp16 MFMA "
+       "products, fp32 accumulation",
+}
 
 
 def log(msg: str) -> None:
@@ -135,9 +141,10 @@ def main() -> None:
     ap.add_argument("--graph", action="store_true",
                     help="time the step captured once in a HIP graph and replayed (captured.py); "
                          "the per-kernel profile is not available then")
-    ap.add_argument("--matmul", choices=["split_bf16", "fp32"], default="split_bf16",
+    ap.add_argument("--matmul", choices=["split_bf16", "fp32", "split_f16"], default="split_bf16",
                     help="matrix-core mode of the fp32 contractions: exact three-way bf16 split with six "
-                         "bf16 MFMA products and fp32 accumulation (default), or fp32 MFMA")
+                         "bf16 MFMA products and fp32 accumulation (default), fp32 MFMA, or power-of-two "
+                         "row scales with a two-way fp16 split and three fp16 MFMA products")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="first copy a 256 MiB buffer (a plain copy kernel of known size, the scale "
                          "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -158,7 +165,7 @@ def main() -> None:
 
     dev = torch.device("cuda:0")
     _lib.load()
-    mm_mode = _lib.MATMUL_SPLIT_BF16 if args.matmul == "split_bf16" else _lib.MATMUL_FP32
+    mm_mode = _lib.MATMUL_MODES[args.matmul]
     _lib.set_matmul_mode(mm_mode)
     system, with_stress, wl_name = make_system(args.config)
     model_kw = MODELS.get(args.config, {})
@@ -261,8 +268,7 @@ def main() -> None:
                                   else "max_neighbors 30)"),
                    "atoms": system.n_atoms, "edges": int(ei.shape[1]), "parallelism": "single GPU",
                    "execution": "hip graph replay" if args.graph else "eager",
-                   "matmul": ("fp32 operands split exactly into three bf16 planes, six bf16 MFMA products, "
-                              "fp32 accumulation" if mm_mode == _lib.MATMUL_SPLIT_BF16 else "fp32 MFMA")},
+                   "matmul": MATMUL_TEXT[mm_mode]},
         "roofline": rl, "cpu_baseline": cpu, "kernels": kernels,
         "peak_memory_mib": round(peak_mib, 1),   # torch allocator peak over the timed steps
         "energy": round(float(out["energy"].item()), 8),

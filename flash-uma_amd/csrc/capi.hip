@@ -16,8 +16,9 @@ extern "C" int fu_version(void) { return 100; }  // 0.1.0
 extern "C" const char* fu_last_error(void) { return fu::g_last_error; }
 
 extern "C" int fu_set_matmul_mode(int32_t mode) {
-  if (mode != fu::FU_MATMUL_SPLIT_BF16 && mode != fu::FU_MATMUL_FP32)
-    return fu::set_error(FU_ERR_UNSUPPORTED, "fu_set_matmul_mode: mode=%d (0: split bf16, 1: fp32)", mode);
+  if (mode != fu::FU_MATMUL_SPLIT_BF16 && mode != fu::FU_MATMUL_FP32 && mode != fu::FU_MATMUL_SPLIT_F16)
+    return fu::set_error(FU_ERR_UNSUPPORTED, "fu_set_matmul_mode: mode=%d (0: split bf16, 1: fp32, 2: split fp16)",
+                         mode);
   fu::g_matmul_mode.store(mode, std::memory_order_relaxed);
   return FU_OK;
 }

@@ -20,7 +20,7 @@
 //    the row-wise tile stores and the column-of-rows operand reads are free of bank
 //    conflicts (32 KB of operands, 36 KB with the epilogue staging: four workgroups per CU).
 // The epilogue stages each wave's 32-row slabs through LDS and writes rows with 16-byte stores.
-#include "split_bf16.h"
+#include "split_f16.h"
 
 namespace fu {
 
@@ -37,6 +37,10 @@ static_assert(GBM == GBN, "the split planes of A and W tiles share one layout");
 // double-buffered (two workgroups per CU).
 constexpr int G_PLANE_A_TALL = 2 * GBM * GBK;
 constexpr int G_LDS_FLOATS_TALL = 2 * 3 * (G_PLANE_A_TALL + G_PLANE) / 2;
+// fp16 split (F16): two planes per operand, 32 KB (the epilogue staging needs 36 KB) and 48 KB
+constexpr int G_LDS_FLOATS_SPLIT_F16 = 2 * 2 * G_PLANE > 4 * 32 * GES ? 2 * 2 * G_PLANE : 4 * 32 * GES;
+constexpr int G_LDS_FLOATS_TALL_F16 = 2 * 2 * (G_PLANE_A_TALL + G_PLANE) / 2;
+static_assert(4 * 32 * GES <= G_LDS_FLOATS_TALL_F16, "epilogue staging must fit in the fp16 tall planes");
 static_assert(4 * 32 * GES <= G_LDS_FLOATS_SPLIT, "epilogue staging must fit in the split planes");
 
 // Float offset of 16-byte chunk `chunk` of LDS operand row `row`.
@@ -138,8 +142,8 @@ struct GatherA {
 // wave's 64 staged columns are a gate and its values; the epilogue writes Y (kept for the
 // backward), Z and S.  MODE 2 (gate backward): see GateBwd; Y receives g_Y_m0 ((2L+1)C
 // columns).
-template <int MODE, bool SPLIT, bool KTAIL = false, bool TALL = false, bool GATHER = false>
-__global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const float* __restrict__ A, int64_t lda, int64_t sA,
+template <int MODE, bool SPLIT, bool KTAIL = false, bool TALL = false, bool GATHER = false, bool F16 = false>
+__global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_kernel(const float* __restrict__ A, int64_t lda, int64_t sA,
                                                           const float* __restrict__ W, int64_t ldw, int64_t sW,
                                                           const float* __restrict__ bias, int64_t sBias,
                                                           int32_t bias_batches, float* __restrict__ Y, int64_t ldy,
@@ -158,10 +162,13 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
   }
   static_assert(SPLIT || !TALL, "tall tiles exist in the split mode only");
   static_assert(!GATHER || (SPLIT && !KTAIL && MODE == 1), "the gathered A operand feeds the split gate GEMM");
+  static_assert(!F16 || (SPLIT && !GATHER), "the fp16 split is a split mode without the gathered loader");
   constexpr int RB = TALL ? 4 : 2;          // 32-row blocks per wave
   constexpr int BM = 64 * RB;               // tile rows
   constexpr int PA = BM * GBK, PW = G_PLANE;  // bf16 per A plane, per W plane
-  __shared__ __attribute__((aligned(16))) float smem[TALL ? G_LDS_FLOATS_TALL : SPLIT ? G_LDS_FLOATS_SPLIT : G_LDS_FLOATS];
+  __shared__ __attribute__((aligned(16))) float smem[TALL ? (F16 ? G_LDS_FLOATS_TALL_F16 : G_LDS_FLOATS_TALL)
+                                                     : SPLIT ? (F16 ? G_LDS_FLOATS_SPLIT_F16 : G_LDS_FLOATS_SPLIT)
+                                                             : G_LDS_FLOATS];
 
   // XCD-aware tile order: hardware deals consecutive workgroups round-robin over the 8 XCDs;
   // remap so that each XCD walks a contiguous range of tiles (the column tiles of one A
@@ -189,7 +196,9 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
   const int fr = lane & 31;  // operand row (A) / column (W) within a 32-block
   const int fh = lane >> 5;  // this lane feeds chunk columns 8 fh .. 8 fh + 7
   if constexpr (SPLIT) {
-    __bf16* sp = reinterpret_cast<__bf16*>(smem);  // [buf][A hi, mid, lo (PA) | W hi, mid, lo (PW)]
+    // [buf][A planes (NP x PA) | W planes (NP x PW)]: hi, mid, lo bf16, or hi, lo fp16 (F16)
+    constexpr int NP = F16 ? 2 : 3;
+    __bf16* sp = reinterpret_cast<__bf16*>(smem);
     const int sr = tid >> 1, sh = tid & 1;         // staging: tile row sr (+128 if TALL), k 8 sh ..
     const int soff = plane_off(sr, sh);
     const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -289,42 +298,144 @@ __global__ __launch_bounds__(256, SPLIT ? 2 : 4) void linear_mfma_kernel(const f
         }
       }
     };
+    // F16: the power-of-two scales of the staged rows (A row, second A row if TALL, W row) and
+    // their running maxima, this thread's half of each row (split_f16.h)
+    float scA = 1.0f, scA2 = 1.0f, scW = 1.0f, RA = 0.0f, RA2 = 0.0f, RW = 0.0f;
+    int eA = 0, eA2 = 0, eW = 0;
     auto store_chunk = [&](int buf) {
-      __bf16* b = sp + buf * 3 * (PA + PW);
-      uint4 h, m, l;
-      split3(ga[0], ga[1], h, m, l);
-      st_planes(b, PA, soff, h, m, l);
-      if constexpr (TALL) {
-        split3(ga2[0], ga2[1], h, m, l);
-        st_planes(b, PA, plane_off(128 + sr, sh), h, m, l);
+      __bf16* b = sp + buf * NP * (PA + PW);
+      if constexpr (F16) {
+        RA = fmaxf(RA, fmaxf(amax4(ga[0]), amax4(ga[1])));
+        RW = fmaxf(RW, fmaxf(amax4(gw[0]), amax4(gw[1])));
+        uint4 h, l;
+        split2h(scale4(ga[0], scA), scale4(ga[1], scA), h, l);
+        st_planes2(b, PA, soff, h, l);
+        if constexpr (TALL) {
+          RA2 = fmaxf(RA2, fmaxf(amax4(ga2[0]), amax4(ga2[1])));
+          split2h(scale4(ga2[0], scA2), scale4(ga2[1], scA2), h, l);
+          st_planes2(b, PA, plane_off(128 + sr, sh), h, l);
+        }
+        split2h(scale4(gw[0], scW), scale4(gw[1], scW), h, l);
+        st_planes2(b + 2 * PA, PW, soff, h, l);
+      } else {
+        uint4 h, m, l;
+        split3(ga[0], ga[1], h, m, l);
+        st_planes(b, PA, soff, h, m, l);
+        if constexpr (TALL) {
+          split3(ga2[0], ga2[1], h, m, l);
+          st_planes(b, PA, plane_off(128 + sr, sh), h, m, l);
+        }
+        split3(gw[0], gw[1], h, m, l);
+        st_planes(b + 3 * PA, PW, soff, h, m, l);
       }
-      split3(gw[0], gw[1], h, m, l);
-      st_planes(b + 3 * PA, PW, soff, h, m, l);
     };
+    // the larger magnitude of this thread's and its partner's half of a staged row
+    auto row_max = [&](float v) { return fmaxf(v, __shfl_xor(v, 1, 64)); };
     const int nk = (K + GBK - 1) / GBK;
-    load_chunk(0);
-    store_chunk(0);
-    load_chunk((nk > 1 ? 1 : 0) * GBK);
-    __syncthreads();
-    for (int kc = 0; kc < nk; ++kc) {
-      const __bf16* b = sp + (kc & 1) * 3 * (PA + PW);
-      bf16x8 bq[2][3];
+    // F16: exact scales from a pre-pass when the rows are short, else scales from the first
+    // chunk and, if any staged row ended outside the window, a second pass with exact scales
+    const bool prepass = F16 && nk <= F16_PREPASS_CHUNKS;
+    __shared__ unsigned f16_redo[4];
+    for (int pass = 0; pass < (F16 ? 2 : 1); ++pass) {
+      if constexpr (F16) {
+        if (pass == 0 && !prepass) {
+          load_chunk(0);
+          eA = f16_exp_chunk(row_max(fmaxf(amax4(ga[0]), amax4(ga[1]))));
+          if constexpr (TALL) eA2 = f16_exp_chunk(row_max(fmaxf(amax4(ga2[0]), amax4(ga2[1]))));
+          eW = f16_exp_chunk(row_max(fmaxf(amax4(gw[0]), amax4(gw[1]))));
+        } else {
+          if (pass == 0) {
+#pragma unroll 4
+            for (int kc = 0; kc < nk; ++kc) {
+              load_chunk(kc * GBK);
+              RA = fmaxf(RA, fmaxf(amax4(ga[0]), amax4(ga[1])));
+              if constexpr (TALL) RA2 = fmaxf(RA2, fmaxf(amax4(ga2[0]), amax4(ga2[1])));
+              RW = fmaxf(RW, fmaxf(amax4(gw[0]), amax4(gw[1])));
+            }
+          } else {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) ld_planes(b + 3 * PA, PW, plane_off(wc + 32 * j + fr, fh), bq[j]);
+            for (int i = 0; i < RB; ++i)
 #pragma unroll
-      for (int i = 0; i < RB; ++i) {
-        bf16x8 aq[3];
-        ld_planes(b, PA, plane_off(wr + 32 * i + fr, fh), aq);
+              for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int q = 0; q < 6; ++q)
-#pragma unroll
-          for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16(aq[kSplitA[q]], bq[j][kSplitB[q]], acc[i][j]);
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+          }
+          eA = f16_exp_row(row_max(RA));
+          if constexpr (TALL) eA2 = f16_exp_row(row_max(RA2));
+          eW = f16_exp_row(row_max(RW));
+        }
+        scA = pow2i(eA);
+        scA2 = pow2i(eA2);
+        scW = pow2i(eW);
       }
-      // chunk kc + 1 (loaded during the previous iteration) into the other buffer, whose last
-      // readers finished before the previous barrier; then prefetch chunk kc + 2
-      store_chunk((kc & 1) ^ 1);
-      load_chunk((kc + 2 < nk ? kc + 2 : nk - 1) * GBK);
+      load_chunk(0);
+      store_chunk(0);
+      load_chunk((nk > 1 ? 1 : 0) * GBK);
       __syncthreads();
+      for (int kc = 0; kc < nk; ++kc) {
+        const __bf16* b = sp + (kc & 1) * NP * (PA + PW);
+        if constexpr (F16) {
+          f16x8 bq[2][2];
+#pragma unroll
+          for (int j = 0; j < 2; ++j) ld_planes2(b + 2 * PA, PW, plane_off(wc + 32 * j + fr, fh), bq[j]);
+#pragma unroll
+          for (int i = 0; i < RB; ++i) {
+            f16x8 aq[2];
+            ld_planes2(b, PA, plane_off(wr + 32 * i + fr, fh), aq);
+#pragma unroll
+            for (int q = 0; q < 3; ++q)
+#pragma unroll
+              for (int j = 0; j < 2; ++j) acc[i][j] = mfma_f16(aq[kF16A[q]], bq[j][kF16B[q]], acc[i][j]);
+          }
+        } else {
+          bf16x8 bq[2][3];
+#pragma unroll
+          for (int j = 0; j < 2; ++j) ld_planes(b + 3 * PA, PW, plane_off(wc + 32 * j + fr, fh), bq[j]);
+#pragma unroll
+          for (int i = 0; i < RB; ++i) {
+            bf16x8 aq[3];
+            ld_planes(b, PA, plane_off(wr + 32 * i + fr, fh), aq);
+#pragma unroll
+            for (int q = 0; q < 6; ++q)
+#pragma unroll
+              for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16(aq[kSplitA[q]], bq[j][kSplitB[q]], acc[i][j]);
+          }
+        }
+        // chunk kc + 1 (loaded during the previous iteration) into the other buffer, whose last
+        // readers finished before the previous barrier; then prefetch chunk kc + 2
+        store_chunk((kc & 1) ^ 1);
+        load_chunk((kc + 2 < nk ? kc + 2 : nk - 1) * GBK);
+        __syncthreads();
+      }
+      if constexpr (F16) {
+        if (pass == 1 || prepass) break;
+        // every wave has left the loop (barrier above): its buffers may be restaged
+        const bool out = f16_outside(row_max(RA) * scA) || (TALL && f16_outside(row_max(RA2) * scA2)) ||
+                         f16_outside(row_max(RW) * scW);
+        const bool wave_out = __ballot(out) != 0;
+        if (lane == 0) f16_redo[wave] = wave_out;
+        __syncthreads();
+        if (!(f16_redo[0] | f16_redo[1] | f16_redo[2] | f16_redo[3])) break;
+      }
+    }
+    if constexpr (F16) {
+      // undo the scales: output (row, column) times 2^-e(row) 2^-e(column), exact
+      __shared__ float f16_rinv[2 * GBM], f16_cinv[GBN];
+      if (sh == 0) {
+        f16_rinv[sr] = pow2i(-eA);
+        if constexpr (TALL) f16_rinv[128 + sr] = pow2i(-eA2);
+        f16_cinv[sr] = pow2i(-eW);
+      }
+      __syncthreads();
+      const float c0 = f16_cinv[wc + fr], c1 = f16_cinv[wc + 32 + fr];
+#pragma unroll
+      for (int i = 0; i < RB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float rs = f16_rinv[wr + 32 * i + 8 * (r >> 2) + 4 * fh + (r & 3)];
+          acc[i][0][r] = acc[i][0][r] * rs * c0;
+          acc[i][1][r] = acc[i][1][r] * rs * c1;
+        }
     }
   } else {
     // Global -> register staging: 2 float4 of A and 2 float4 of W per thread per chunk
@@ -659,12 +770,18 @@ static int64_t linear_tile_rows(int64_t M) {
 }
 
 // The kernel for MODE in the current matrix-core mode; KTAIL instances handle K % 16 != 0.
+template <int MODE, bool F16>
+static auto split_kernel(int32_t K, bool tall) {
+  return (K % GBK != 0)
+             ? (tall ? linear_mfma_kernel<MODE, true, true, true, false, F16> : linear_mfma_kernel<MODE, true, true, false, false, F16>)
+             : (tall ? linear_mfma_kernel<MODE, true, false, true, false, F16> : linear_mfma_kernel<MODE, true, false, false, false, F16>);
+}
 template <int MODE>
 static auto linear_kernel(int32_t K, int64_t M) {
   const bool tall = linear_tile_rows(M) != GBM;
-  return matmul_mode() == FU_MATMUL_FP32 ? linear_mfma_kernel<MODE, false>
-         : (K % GBK != 0) ? (tall ? linear_mfma_kernel<MODE, true, true, true> : linear_mfma_kernel<MODE, true, true>)
-                          : (tall ? linear_mfma_kernel<MODE, true, false, true> : linear_mfma_kernel<MODE, true, false>);
+  const int mode = matmul_mode();
+  return mode == FU_MATMUL_FP32 ? linear_mfma_kernel<MODE, false>
+         : mode == FU_MATMUL_SPLIT_F16 ? split_kernel<MODE, true>(K, tall) : split_kernel<MODE, false>(K, tall);
 }
 
 static int linear_check(const float* A, int64_t lda, const float* W, int64_t ldw, const float* Y, int64_t ldy,
@@ -756,7 +873,7 @@ extern "C" int fu_gather_linear_gate(const float* x, const int64_t* idx_i, const
   const char* who = "fu_gather_linear_gate";
   if (C <= 0 || C % 64 != 0) return set_error(FU_ERR_UNSUPPORTED, "%s: C=%d must be a multiple of 64", who, C);
   if (matmul_mode() == FU_MATMUL_FP32)
-    return set_error(FU_ERR_UNSUPPORTED, "%s: only in the split-bf16 matrix-core mode", who);
+    return set_error(FU_ERR_UNSUPPORTED, "%s: only in the split matrix-core modes", who);
   const int32_t lmax = 2, K = 6 * C, N = 5 * C;
   if (E < 0) return set_error(FU_ERR_SHAPE, "%s: E=%lld", who, (long long)E);
   if (ldw < K || ldy < N || ldz < 3 * C || (ldw | ldy | ldz) % 4 != 0)
@@ -771,6 +888,8 @@ extern "C" int fu_gather_linear_gate(const float* x, const int64_t* idx_i, const
   const int64_t bm = linear_tile_rows(E);
   const int64_t total = ((E + bm - 1) / bm) * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: E too large", who);
+  // the gathered loader keeps the bf16 split in both split modes: its per-row gather state and
+  // the fp16 scales together exceed the register file of the tall tile
   auto kern = bm != GBM ? linear_mfma_kernel<1, true, false, true, true> : linear_mfma_kernel<1, true, false, false, true>;
   // A is unused (the loader gathers it); x stands in as a valid pointer
   hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), x, (int64_t)0, (int64_t)0, W,

@@ -90,7 +90,7 @@ __device__ __forceinline__ floatx16 mfma_bf16(const bf16x8& a, const bf16x8& b, 
 }
 
 // Matrix-core mode for every fp32 contraction of the library (fu_set_matmul_mode).
-enum { FU_MATMUL_SPLIT_BF16 = 0, FU_MATMUL_FP32 = 1 };
+enum { FU_MATMUL_SPLIT_BF16 = 0, FU_MATMUL_FP32 = 1, FU_MATMUL_SPLIT_F16 = 2 };
 int matmul_mode();
 
 }  // namespace fu

@@ -1,0 +1,98 @@
+// fp32 products on the fp16 matrix cores (v_mfma_f32_32x32x16_f16): three MFMAs per 16-wide
+// K step instead of the six of the bf16 split (split_bf16.h).
+//
+// Every fp32 operand row (a row of A, or a row of W, i.e. one output column) gets a power-of-two
+// scale 2^e, and each element x of it is split into two fp16 values
+//     x 2^e = hi + lo,   hi = fp16(x 2^e),   lo = fp16(x 2^e - hi)
+// (round to nearest even; the subtraction is exact in fp32).  While lo is a normal fp16
+// (|x 2^e| >= 2^-3) hi + lo carries 22 significant bits of x 2^e; below that it is within 2^-25
+// of it.  A product is then
+//     a b 2^(ea + eb) ~ hi_a hi_b + hi_a lo_b + lo_a hi_b
+// with each partial product exact in the fp32 accumulator and the dropped lo_a lo_b of relative
+// size 2^-22.  The accumulated output is multiplied by 2^-ea and 2^-eb afterwards (exact).
+//
+// The scale of a row keeps its largest magnitude R inside the window [2^-3, 2^15): below 2^15 hi
+// cannot overflow (the largest fp16 is 65504); from 2^-3 up the row's largest elements keep all 22
+// bits, and every smaller element's error (at most 2^-25 after scaling) stays below 2^-22 R.  The
+// kernels pick the scale one of two ways:
+//  * exact: R from a pre-pass over the row, e = 14 - floor(log2 R) (R 2^e in [2^14, 2^15));
+//  * from the first chunk: the maximum m of the row's first 16 elements is mapped to [2^6, 2^7),
+//    the running maximum R is tracked while the chunks are staged, and a tile in which any row
+//    or column ends outside the window is computed again with the exact scale.  That leaves
+//    256x of headroom above the first chunk and keeps elements down to 2^-9 m at full precision.
+// A row of zeros keeps e = 0.
+#pragma once
+#include "split_bf16.h"
+
+namespace fu {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Split 8 floats (already scaled) into the hi and lo planes of packed fp16 pairs.
+__device__ __forceinline__ void split2h(const float4& a, const float4& b, uint4& H, uint4& L) {
+  const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const float2v v = {x[2 * t], x[2 * t + 1]};
+    const f16x2 h = __builtin_convertvector(v, f16x2);
+    const float2v r = v - __builtin_convertvector(h, float2v);
+    (&H.x)[t] = __builtin_bit_cast(unsigned, h);
+    (&L.x)[t] = __builtin_bit_cast(unsigned, __builtin_convertvector(r, f16x2));
+  }
+}
+
+// Split 4 floats (already scaled) into 4 fp16 of each plane.
+__device__ __forceinline__ void split2h_4(const float4& a, uint2& H, uint2& L) {
+  uint4 h, l;
+  split2h(a, a, h, l);
+  H = make_uint2(h.x, h.y);
+  L = make_uint2(l.x, l.y);
+}
+
+__device__ __forceinline__ void st_planes2(__bf16* p0, int plane_stride, int off, const uint4& H, const uint4& L) {
+  *reinterpret_cast<uint4*>(p0 + off) = H;
+  *reinterpret_cast<uint4*>(p0 + plane_stride + off) = L;
+}
+
+__device__ __forceinline__ void st_planes2_4(__bf16* p0, int plane_stride, int off, const uint2& H, const uint2& L) {
+  *reinterpret_cast<uint2*>(p0 + off) = H;
+  *reinterpret_cast<uint2*>(p0 + plane_stride + off) = L;
+}
+
+__device__ __forceinline__ void ld_planes2(const __bf16* p0, int plane_stride, int off, f16x8 (&f)[2]) {
+  f[0] = *reinterpret_cast<const f16x8*>(p0 + off);
+  f[1] = *reinterpret_cast<const f16x8*>(p0 + plane_stride + off);
+}
+
+// The three partial products (plane of a, plane of b), smallest first: lo*hi, hi*lo, hi*hi.
+constexpr int kF16A[3] = {1, 0, 0};
+constexpr int kF16B[3] = {0, 1, 0};
+
+__device__ __forceinline__ floatx16 mfma_f16(const f16x8& a, const f16x8& b, const floatx16& acc) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
+}
+
+// 2^e for e in [-126, 127].
+__device__ __forceinline__ float pow2i(int e) { return __uint_as_float((unsigned)(127 + e) << 23); }
+
+__device__ __forceinline__ int f16_exp_of(float m, int target) {
+  const int E = (int)((__float_as_uint(m) >> 23) & 0xff) - 127;  // floor(log2 m) for normal m
+  const int e = target - E;
+  return m > 0.0f ? (e < -126 ? -126 : e > 126 ? 126 : e) : 0;
+}
+// exact scale of a row whose largest magnitude is R: R 2^e in [2^14, 2^15)
+__device__ __forceinline__ int f16_exp_row(float R) { return f16_exp_of(R, 14); }
+// scale from a first chunk whose largest magnitude is m: m 2^e in [2^6, 2^7)
+__device__ __forceinline__ int f16_exp_chunk(float m) { return f16_exp_of(m, 6); }
+// a row whose scaled largest magnitude Rs left the window (Rs = 0: a row of zeros, in the window)
+__device__ __forceinline__ bool f16_outside(float Rs) { return !(Rs < 32768.0f) || (Rs > 0.0f && Rs < 0.125f); }
+
+__device__ __forceinline__ float amax4(const float4& v) {
+  return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+
+// Rows (or operands) of up to this many 16-wide chunks get the exact scale from a pre-pass.
+constexpr int F16_PREPASS_CHUNKS = 4;
+
+}  // namespace fu

@@ -172,10 +172,12 @@ def call(name: str, *args) -> None:
 
 MATMUL_SPLIT_BF16 = 0  # fp32 operands split exactly into three bf16 planes, six MFMA products
 MATMUL_FP32 = 1        # v_mfma_f32_32x32x2_f32
+MATMUL_SPLIT_F16 = 2   # power-of-two row scales, two fp16 planes, three MFMA products
+MATMUL_MODES = {"split_bf16": MATMUL_SPLIT_BF16, "fp32": MATMUL_FP32, "split_f16": MATMUL_SPLIT_F16}
 
 
 def get_matmul_mode() -> int:
-    """Matrix-core mode of the library's fp32 contractions (MATMUL_SPLIT_BF16 or MATMUL_FP32)."""
+    """Matrix-core mode of the library's fp32 contractions (one of MATMUL_MODES)."""
     return load().fu_matmul_mode()
 
 

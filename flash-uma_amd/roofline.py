@@ -6,11 +6,13 @@ GEMMs count 2*M*N*K flops; the complex layer counts the 6*M*Nc*Kc flops of its t
 products.  These are the denominators of the roofline fractions:
 achieved = algorithmic bytes (flops) / measured kernel time.
 
-Matrix-core kernels run in one of two modes (fu_set_matmul_mode).  fp32 mode executes the
-fp32 flops on v_mfma_f32_32x32x2_f32 (peak 157.3 TFLOP/s).  The default split mode executes
-each fp32 product as six bf16 products of the operands' exact three-way bf16 splits, so the
-matrix cores execute 6x the fp32 flops at the dense bf16 peak (2.5 PFLOP/s); its roofline
-is that executed bf16 work against 2.5 PFLOP/s, with the fp32-equivalent rate alongside.
+Matrix-core kernels run in one of three modes (fu_set_matmul_mode).  fp32 mode executes the
+fp32 flops on v_mfma_f32_32x32x2_f32 (peak 157.3 TFLOP/s).  The split-bf16 mode executes each
+fp32 product as six bf16 products of the operands' exact three-way bf16 splits; the split-fp16
+mode as three fp16 products of two-way fp16 splits of power-of-two-scaled operands.  The
+matrix cores then execute 6x (3x) the fp32 flops at the dense bf16 (fp16) peak of 2.5 PFLOP/s;
+the roofline is that executed work against 2.5 PFLOP/s, with the fp32-equivalent rate alongside.
+fu_gather_linear_gate keeps the bf16 split in both split modes.
 
 Per-unit figures at C = 128, B = 64 (bytes per edge + bytes per node):
   gating fwd 10240 / bwd 15872; gather fwd 15512 + 4616, bwd 21784 + 9232;
@@ -23,8 +25,18 @@ from __future__ import annotations
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix
-SPLIT_PRODUCTS = 6              # bf16 products per fp32 product in the split mode
-MATMUL_SPLIT_BF16, MATMUL_FP32 = 0, 1
+SPLIT_PRODUCTS = 6              # bf16 products per fp32 product in the split-bf16 mode
+F16_PRODUCTS = 3                # fp16 products per fp32 product in the split-fp16 mode
+MATMUL_SPLIT_BF16, MATMUL_FP32, MATMUL_SPLIT_F16 = 0, 1, 2
+
+
+def _products(name: str, matmul_mode: int) -> tuple[int, str]:
+    """Matrix-core products per fp32 product of entry `name` in `matmul_mode`, and their kind."""
+    if matmul_mode == MATMUL_FP32:
+        return 1, "fp32 mfma"
+    if matmul_mode == MATMUL_SPLIT_F16 and name != "fu_gather_linear_gate":
+        return F16_PRODUCTS, "fp16 mfma, 3 products per fp32 product"
+    return SPLIT_PRODUCTS, "bf16 mfma, 6 products per fp32 product"
 
 
 def _gating_fwd(a):
@@ -307,10 +319,7 @@ def summarize(durations, matmul_mode: int = MATMUL_SPLIT_BF16) -> dict:
     which differs from `frac` where a launch's arithmetic intensity puts it under the HBM
     slope (the K = 128 shapes, whose operands and output are as large as their work);
     `hbm_bound_launches` counts those launches."""
-    if matmul_mode == MATMUL_FP32:
-        mul, mpeak = 1, FP32_MFMA_PEAK_TFLOPS
-    else:
-        mul, mpeak = SPLIT_PRODUCTS, BF16_MFMA_PEAK_TFLOPS
+    mpeak = FP32_MFMA_PEAK_TFLOPS if matmul_mode == MATMUL_FP32 else BF16_MFMA_PEAK_TFLOPS
     agg: dict = {}
     for name, args, ms in durations:
         if name not in WORK:
@@ -322,6 +331,7 @@ def summarize(durations, matmul_mode: int = MATMUL_SPLIT_BF16) -> dict:
         a["bytes"] += nbytes
         a["flops"] += flops
         if name in MFMA_BOUND:
+            mul = _products(name, matmul_mode)[0]
             t_mfma, t_hbm = mul * flops / (mpeak * 1e12), nbytes / (HBM_PEAK_GBS * 1e9)
             a["ideal_s"] += max(t_mfma, t_hbm)
             a["hbm_bound"] += int(t_hbm > t_mfma)
@@ -331,10 +341,8 @@ def summarize(durations, matmul_mode: int = MATMUL_SPLIT_BF16) -> dict:
         rec = {"calls": a["calls"], "total_ms": round(a["ms"], 4), "avg_us": round(1e3 * a["ms"] / a["calls"], 2)}
         if name in MFMA_BOUND:
             fp32_rate = a["flops"] / sec / 1e12 if sec > 0 else 0.0
-            if matmul_mode == MATMUL_FP32:
-                ach, peak, op = fp32_rate, FP32_MFMA_PEAK_TFLOPS, "fp32 mfma"
-            else:
-                ach, peak, op = SPLIT_PRODUCTS * fp32_rate, BF16_MFMA_PEAK_TFLOPS, "bf16 mfma, 6 products per fp32 product"
+            mul, op = _products(name, matmul_mode)
+            ach, peak = mul * fp32_rate, mpeak
             rec.update(bound="mfma", unit="TFLOP/s", achieved=round(ach, 2), peak=peak, frac=round(ach / peak, 4),
                        matrix_op=op, fp32_tflops=round(fp32_rate, 2), flops_per_launch=a["flops"] // a["calls"],
                        hbm_gbs=round(a["bytes"] / sec / 1e9, 1) if sec > 0 else 0.0,

@@ -72,10 +72,10 @@ def test_channel_widths_parity(cuda, C, H, B):
     _check(out, ref, s.n_atoms)
 
 
-@pytest.mark.parametrize("mode", [0, 1], ids=["split_bf16", "fp32"])
+@pytest.mark.parametrize("mode", [0, 1, 2], ids=["split_bf16", "fp32", "split_f16"])
 def test_water_fixture_parity(cuda, mode):
-    """Against the committed float64 oracle fixture (tests/golden/water64_oracle.npz), in both
-    matrix-core modes of the fp32 contractions."""
+    """Against the committed float64 oracle fixture (tests/golden/water64_oracle.npz), in every
+    matrix-core mode of the fp32 contractions."""
     import os
     import systems
     from ops import _lib
@@ -89,11 +89,11 @@ def test_water_fixture_parity(cuda, mode):
     _check(out, ref, s.n_atoms)
 
 
-@pytest.mark.parametrize("mode", [0, 1], ids=["split_bf16", "fp32"])
+@pytest.mark.parametrize("mode", [0, 1, 2], ids=["split_bf16", "fp32", "split_f16"])
 def test_fe432_fixture_parity(cuda, mode):
     """The headline workload's local structure (bcc Fe, a = 2.87, 30 edges per atom, E+F+S)
     at 6x6x6 = 432 atoms against the committed float64 oracle fixture
-    (tests/golden/fe432_oracle.npz), in both matrix-core modes.  Bars: energy per atom rel
+    (tests/golden/fe432_oracle.npz), in every matrix-core mode.  Bars: energy per atom rel
     1e-6, forces and stress max-abs 1e-4, each atom's energy contribution rel 1e-5 (a float32
     run of the oracle itself is 1.2e-7 / 5.9e-8 / 2.4e-9 / 2.3e-6 from float64 here)."""
     import os

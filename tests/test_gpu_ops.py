@@ -149,9 +149,9 @@ def test_ln_silu(cuda):
     assert_close(g, gref, 1e-4, "ln_silu bwd")
 
 
-@pytest.fixture(params=[0, 1], ids=["split_bf16", "fp32"])
+@pytest.fixture(params=[0, 1, 2], ids=["split_bf16", "fp32", "split_f16"])
 def matmul_mode(request, cuda):
-    """Both matrix-core modes of the fp32 contractions (fu_set_matmul_mode)."""
+    """Every matrix-core mode of the fp32 contractions (fu_set_matmul_mode)."""
     from ops import _lib
     with _lib.matmul_mode(request.param):
         yield request.param
@@ -200,12 +200,15 @@ def test_complex_linear(cuda, matmul_mode, presplit, M, Kc, Nc):
     assert_close(gx, gref, TOL, "complex linear bwd")
 
 
+@pytest.mark.parametrize("split", [0, 2], ids=["split_bf16", "split_f16"])
 @pytest.mark.parametrize("N,K", [(640, 768), (384, 384)])
-def test_split_gemm_accuracy(cuda, N, K):
-    """The split-bf16 product (x = hi + mid + lo exactly; six of the nine partial products) is
-    an fp32-accurate GEMM: on an SO(2) layer shape its error against float64 is at most that
-    of the fp32 MFMA on the same inputs (rms within 10 %, max within 50 %), and well inside the
-    fp32 class (rms-relative 1e-6); dropping a plane (a two-term split) would give ~4e-6."""
+def test_split_gemm_accuracy(cuda, split, N, K):
+    """Both split products are fp32-accurate GEMMs: the bf16 one (x = hi + mid + lo exactly;
+    six of the nine partial products) and the fp16 one (x 2^e = hi + lo with a power-of-two
+    row scale; three of the four partial products).  On an SO(2) layer shape the error against
+    float64 is at most that of the fp32 MFMA on the same inputs (rms within 10 %, max within
+    50 %), and well inside the fp32 class (rms-relative 1e-6); dropping a bf16 plane (a
+    two-term bf16 split) would give ~4e-6."""
     from ops import _lib
     *_, linear, _ = _ops()
     g = torch.Generator().manual_seed(N + K)
@@ -214,15 +217,49 @@ def test_split_gemm_accuracy(cuda, N, K):
     W = (torch.randn(N, K, generator=g) / K ** 0.5).to(cuda)
     ref = x.double() @ W.double().T
     err = {}
-    for mode in (_lib.MATMUL_SPLIT_BF16, _lib.MATMUL_FP32):
+    for mode in (split, _lib.MATMUL_FP32):
         with _lib.matmul_mode(mode):
             y = linear.gemm(x, W)
         d = y.double() - ref
         err[mode] = (d.norm().item() / ref.norm().item(), d.abs().max().item() / ref.abs().max().item())
-    rms_s, max_s = err[_lib.MATMUL_SPLIT_BF16]
+    rms_s, max_s = err[split]
     rms_f, max_f = err[_lib.MATMUL_FP32]
     assert rms_s < 1e-6 and max_s < 5e-6, err
     assert rms_s <= 1.1 * rms_f and max_s <= 1.5 * max_f, err
+
+
+@pytest.mark.parametrize("M,N,K", [(70000, 256, 768), (70000, 128, 64), (3000, 256, 768), (3000, 128, 64),
+                                   (70000, 128, 100)])
+def test_f16_split_dynamic_range(cuda, M, N, K):
+    """The fp16 split's power-of-two scales on rows far from 1 and rows whose magnitude changes
+    along K (the first-chunk scale then leaves the window and the tile is computed again with
+    the exact scale), zero rows and columns, and the short-K pre-pass (K = 64) and K tail
+    (K = 100) forms, on tall (M >= 65,536) and 128-row tiles: every row's error against float64,
+    relative to that row's norm, within 1.5x the fp32 MFMA's worst row plus 1e-7, and finite."""
+    from ops import _lib
+    *_, linear, _ = _ops()
+    g = torch.Generator().manual_seed(M + N + K)
+    x = torch.randn(M, K, generator=g)
+    W = torch.randn(N, K, generator=g) / K ** 0.5
+    q = M // 8
+    x[:q] *= torch.exp2(torch.randint(-40, 40, (q, 1), generator=g).double()).float()
+    ramp = torch.linspace(-24, 24, K)
+    x[q:2 * q:2] *= torch.exp2(ramp)
+    x[q + 1:2 * q:2] *= torch.exp2(-ramp)
+    x[2 * q:2 * q + 64, : K // 2] = 0.0      # zero first chunks, then values
+    x[2 * q + 64:2 * q + 128] = 0.0          # zero rows
+    x[2 * q + 128:2 * q + 192] *= 1e-20      # tiny rows (scaled up by 2^70 and more)
+    W[: N // 4] *= torch.exp2(torch.randint(-30, 30, (N // 4, 1), generator=g).double()).float()
+    W[N // 4: N // 4 + 8] = 0.0
+    ref = x.double() @ W.double().T
+    rn = ref.norm(dim=1).clamp_min(1e-300)
+    worst = {}
+    for mode in (_lib.MATMUL_SPLIT_F16, _lib.MATMUL_FP32):
+        with _lib.matmul_mode(mode):
+            y = linear.gemm(x.to(cuda), W.to(cuda)).cpu()
+        assert torch.isfinite(y).all(), mode
+        worst[mode] = ((y.double() - ref).norm(dim=1) / rn).max().item()
+    assert worst[_lib.MATMUL_SPLIT_F16] <= 1.5 * worst[_lib.MATMUL_FP32] + 1e-7, worst
 
 
 @pytest.mark.parametrize("presplit", [False, True], ids=["in_kernel", "presplit"])
@@ -255,8 +292,9 @@ def test_matmul_mode_switch(cuda):
     from ops import _lib
     prev = _lib.get_matmul_mode()
     assert prev == _lib.MATMUL_SPLIT_BF16
-    with _lib.matmul_mode(_lib.MATMUL_FP32):
-        assert _lib.get_matmul_mode() == _lib.MATMUL_FP32
+    for mode in (_lib.MATMUL_FP32, _lib.MATMUL_SPLIT_F16):
+        with _lib.matmul_mode(mode):
+            assert _lib.get_matmul_mode() == mode
     assert _lib.get_matmul_mode() == prev
     with pytest.raises(_lib.FlashUMAError, match="mode=7"):
         _lib.set_matmul_mode(7)
@@ -764,5 +802,5 @@ def test_gather_linear_gate_matches_gather_then_gemm(cuda, E):
     assert_close(Yf, Y, 2e-6, "Y (pre-activations)")
     assert_close(Zf, Z, 2e-6, "Z (gated)")
     with _lib.matmul_mode(_lib.MATMUL_FP32):
-        with pytest.raises(_lib.FlashUMAError, match="split-bf16"):
+        with pytest.raises(_lib.FlashUMAError, match="split matrix-core"):
             _lib.call("fu_gather_linear_gate", *args)

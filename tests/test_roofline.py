@@ -65,10 +65,16 @@ def test_split_mode_accounting():
     ms = 1.0
     split = roofline.summarize([("fu_linear", args, ms)], roofline.MATMUL_SPLIT_BF16)["fu_linear"]
     fp32 = roofline.summarize([("fu_linear", args, ms)], roofline.MATMUL_FP32)["fu_linear"]
+    f16 = roofline.summarize([("fu_linear", args, ms)], roofline.MATMUL_SPLIT_F16)["fu_linear"]
     rate = flops / 1e-3 / 1e12
     assert fp32["peak"] == 157.3 and abs(fp32["achieved"] - rate) < 0.01
     assert split["peak"] == 2500.0 and abs(split["achieved"] - 6 * rate) < 0.05
-    assert abs(split["fp32_tflops"] - rate) < 0.01
+    assert f16["peak"] == 2500.0 and abs(f16["achieved"] - 3 * rate) < 0.05 and "fp16" in f16["matrix_op"]
+    assert abs(split["fp32_tflops"] - rate) < 0.01 and abs(f16["fp32_tflops"] - rate) < 0.01
+    # the gathered conv1 loader keeps the bf16 split in both split modes
+    g = _args("fu_gather_linear_gate", E=1000, C=128)
+    gf = roofline.summarize([("fu_gather_linear_gate", g, ms)], roofline.MATMUL_SPLIT_F16)["fu_gather_linear_gate"]
+    assert "bf16" in gf["matrix_op"]
 
 
 def test_roofline_frac_takes_the_larger_of_the_two_bounds():
