@@ -141,10 +141,10 @@ def main() -> None:
     ap.add_argument("--graph", action="store_true",
                     help="time the step captured once in a HIP graph and replayed (captured.py); "
                          "the per-kernel profile is not available then")
-    ap.add_argument("--matmul", choices=["split_bf16", "fp32", "split_f16"], default="split_bf16",
-                    help="matrix-core mode of the fp32 contractions: exact three-way bf16 split with six "
-                         "bf16 MFMA products and fp32 accumulation (default), fp32 MFMA, or power-of-two "
-                         "row scales with a two-way fp16 split and three fp16 MFMA products")
+    ap.add_argument("--matmul", choices=["split_f16", "split_bf16", "fp32"], default="split_f16",
+                    help="matrix-core mode of the fp32 contractions: power-of-two row scales with a two-way "
+                         "fp16 split and three fp16 MFMA products (default), exact three-way bf16 split with "
+                         "six bf16 MFMA products, or fp32 MFMA; fp32 accumulation in all three")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="first copy a 256 MiB buffer (a plain copy kernel of known size, the scale "
                          "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")

@@ -7,7 +7,7 @@
 namespace fu {
 thread_local char g_last_error[512] = {0};
 
-static std::atomic<int> g_matmul_mode{FU_MATMUL_SPLIT_BF16};
+static std::atomic<int> g_matmul_mode{FU_MATMUL_SPLIT_F16};
 int matmul_mode() { return g_matmul_mode.load(std::memory_order_relaxed); }
 }  // namespace fu
 

@@ -38,7 +38,7 @@
 //  * fp32 (fu_set_matmul_mode(1)): the three products on v_mfma_f32_32x32x2_f32, fp32 LDS
 //    rows as in the real GEMM (a_r, a_i: 128 rows; P, Q: 64 rows).
 // The epilogue stages the outputs through LDS and writes 16-byte row pieces.
-#include "split_bf16.h"
+#include "split_f16.h"
 
 namespace fu {
 
@@ -53,13 +53,23 @@ constexpr int C_LDS_FLOATS_SPLIT = CBUF_SPLIT;   // two buffers of bf16 = CBUF_S
 static_assert(CBUF_PRE == CBUF_SPLIT, "both split loops use the same LDS size");
 
 // Main loops of complex_linear_kernel.
-enum { CPATH_FP32 = 0, CPATH_SPLIT4 = 1, CPATH_SPLIT3_PRE = 2 };
+enum { CPATH_FP32 = 0, CPATH_SPLIT4 = 1, CPATH_SPLIT3_PRE = 2, CPATH_F16_PRE = 3 };
+constexpr bool pre_split(int path) { return path == CPATH_SPLIT3_PRE || path == CPATH_F16_PRE; }
 
-// Fragment-order planes of a pre-split complex weight: per (32-column block, 16-k chunk),
-// 9 x 64 lanes x 16 B (P, Q, S = P + Q, each hi, mid, lo).
+// A pre-split complex weight holds, one after the other:
+//  * bf16 planes in fragment order: per (32-column block, 16-k chunk), 9 x 64 lanes x 16 B
+//    (P, Q, S = P + Q, each hi, mid, lo);
+//  * fp16 planes in the same order: per (block, chunk), 6 x 64 lanes x 16 B (P, Q, S, each hi,
+//    lo) of the columns scaled by their power of two 2^e(n) (split_f16.h; one scale per output
+//    column n, shared by P, Q and S so that the three products stay combinable);
+//  * the unscale factors 2^-e(n), one float per column of the 32-column blocks.
 __host__ __device__ inline int64_t complex_weight_split_vectors(int32_t Nc, int32_t Kc) {
   return (int64_t)((Nc + 31) / 32) * ((Kc + 15) / 16) * 9 * 64;
 }
+__host__ __device__ inline int64_t complex_weight_f16_vectors(int32_t Nc, int32_t Kc) {
+  return (int64_t)((Nc + 31) / 32) * ((Kc + 15) / 16) * 6 * 64;
+}
+__host__ __device__ inline int64_t complex_weight_scale_vectors(int32_t Nc) { return (int64_t)((Nc + 31) / 32) * 8; }
 
 __device__ __forceinline__ int clds(int row, int chunk) {
   return row * 16 + 4 * (chunk ^ (((row >> 1) ^ (row >> 2)) & 3));
@@ -88,9 +98,9 @@ struct CGate {
 };
 
 // Output columns per tile, 32-row blocks per wave and workgroups per CU of each path.
-constexpr int cbn_of(int path) { return path == CPATH_SPLIT3_PRE ? CBN_PRE : CBN; }
-constexpr int wg_per_cu(int path) { return path == CPATH_FP32 ? 3 : path == CPATH_SPLIT3_PRE ? 1 : 2; }
-constexpr int threads_of(int path) { return path == CPATH_SPLIT3_PRE ? 512 : 256; }
+constexpr int cbn_of(int path) { return pre_split(path) ? CBN_PRE : CBN; }
+constexpr int wg_per_cu(int path) { return path == CPATH_FP32 ? 3 : pre_split(path) ? 1 : 2; }
+constexpr int threads_of(int path) { return pre_split(path) ? 512 : 256; }
 
 template <int MODE, int PATH, bool KTAIL = false>
 __global__ __launch_bounds__(threads_of(PATH), wg_per_cu(PATH)) void complex_linear_kernel(
@@ -125,8 +135,13 @@ __global__ __launch_bounds__(threads_of(PATH), wg_per_cu(PATH)) void complex_lin
       for (int r = 0; r < 16; ++r) T[p][i][r] = 0.0f;
 
   const int fr = lane & 31, fh = lane >> 5;
-  if constexpr (PATH == CPATH_SPLIT3_PRE) {
-    // [buf][a_r hi, mid, lo | a_i hi, mid, lo | a_s hi, mid, lo][CTA]
+  if constexpr (pre_split(PATH)) {
+    // [buf][a_r planes | a_i planes | a_s planes][CTA]: hi, mid, lo bf16, or hi, lo fp16 (F16,
+    // the rows scaled by 2^e(row) as in split_f16.h)
+    constexpr bool F16 = PATH == CPATH_F16_PRE;
+    constexpr int NPL = F16 ? 2 : 3;     // planes per operand
+    constexpr int NB = 3 * NPL;          // B fragments per chunk
+    constexpr int BUF = 3 * NPL * CTA;   // bf16 per LDS buffer
     __bf16* sp = reinterpret_cast<__bf16*>(smem);
     // staging: thread -> tile row sr, k 4 sq .. 4 sq + 3 of the chunk (8-byte plane pieces)
     const int sr = tid >> 2, sq = tid & 3;
@@ -154,40 +169,70 @@ __global__ __launch_bounds__(threads_of(PATH), wg_per_cu(PATH)) void complex_lin
         gi = ok ? i : z4;
       }
     };
+    // F16: the row's scale and the running maximum of |a_r|, |a_i|, |a_s| (this thread's quarter)
+    float sc = 1.0f, R = 0.0f;
+    int e = 0;
+    auto chunk_max = [&]() { return fmaxf(fmaxf(amax4(gr), amax4(gi)), amax4(gr + gi)); };
+    auto row_max = [&](float v) {  // over the row's four staging threads
+      v = fmaxf(v, __shfl_xor(v, 1, 64));
+      return fmaxf(v, __shfl_xor(v, 2, 64));
+    };
     auto store_chunk = [&](int buf) {
-      __bf16* b = sp + buf * CBUF_PRE;
-      uint2 h, m, l;
-      split3_4(gr, h, m, l);
-      st_planes4(b, CTA, soff, h, m, l);
-      split3_4(gi, h, m, l);
-      st_planes4(b + 3 * CTA, CTA, soff, h, m, l);
-      split3_4(gr + gi, h, m, l);
-      st_planes4(b + 6 * CTA, CTA, soff, h, m, l);
+      __bf16* b = sp + buf * BUF;
+      if constexpr (F16) {
+        R = fmaxf(R, chunk_max());
+        uint2 h, l;
+        split2h_4(scale4(gr, sc), h, l);
+        st_planes2_4(b, CTA, soff, h, l);
+        split2h_4(scale4(gi, sc), h, l);
+        st_planes2_4(b + 2 * CTA, CTA, soff, h, l);
+        split2h_4(scale4(gr + gi, sc), h, l);
+        st_planes2_4(b + 4 * CTA, CTA, soff, h, l);
+      } else {
+        uint2 h, m, l;
+        split3_4(gr, h, m, l);
+        st_planes4(b, CTA, soff, h, m, l);
+        split3_4(gi, h, m, l);
+        st_planes4(b + 3 * CTA, CTA, soff, h, m, l);
+        split3_4(gr + gi, h, m, l);
+        st_planes4(b + 6 * CTA, CTA, soff, h, m, l);
+      }
     };
     // this wave's B fragments of chunk kc (a column block past Nc reads block 0; its outputs
     // are never stored)
     int nb = (col0 + wc) / 32;
     nb = nb < nbt ? nb : 0;
-    const uint4* wb = W3 + (int64_t)nb * nkc * 9 * 64 + lane;
-    auto load_b = [&](int kc, uint4 (&bf)[9]) {
+    const uint4* wb = W3 + (int64_t)nb * nkc * NB * 64 + lane;
+    auto load_b = [&](int kc, uint4 (&bf)[NB]) {
 #pragma unroll
-      for (int u = 0; u < 9; ++u) bf[u] = wb[(kc * 9 + u) * 64];
+      for (int u = 0; u < NB; ++u) bf[u] = wb[(kc * NB + u) * 64];
     };
-    auto step = [&](int kc, const uint4 (&bc)[9], uint4 (&bn)[9]) {
+    auto step = [&](int kc, const uint4 (&bc)[NB], uint4 (&bn)[NB]) {
       load_b(kc + 1 < nkc ? kc + 1 : nkc - 1, bn);
-      const __bf16* b = sp + (kc & 1) * CBUF_PRE;
+      const __bf16* b = sp + (kc & 1) * BUF;
 #pragma unroll
       for (int i = 0; i < RB; ++i) {
         const int off = plane_off(wr + 32 * i + fr, fh);
-        bf16x8 af[9];  // a_r, a_i, a_s planes
+        if constexpr (F16) {
+          f16x8 af[6];  // a_r, a_i, a_s planes
 #pragma unroll
-        for (int u = 0; u < 9; ++u) af[u] = *reinterpret_cast<const bf16x8*>(b + u * CTA + off);
+          for (int u = 0; u < 6; ++u) af[u] = *reinterpret_cast<const f16x8*>(b + u * CTA + off);
 #pragma unroll
-        for (int q = 0; q < 6; ++q)
+          for (int q = 0; q < 3; ++q)
 #pragma unroll
-          for (int op = 0; op < 3; ++op)
-            T[op][i] = mfma_bf16(af[3 * op + kSplitA[q]], __builtin_bit_cast(bf16x8, bc[3 * op + kSplitB[q]]),
-                                 T[op][i]);
+            for (int op = 0; op < 3; ++op)
+              T[op][i] = mfma_f16(af[2 * op + kF16A[q]], __builtin_bit_cast(f16x8, bc[2 * op + kF16B[q]]), T[op][i]);
+        } else {
+          bf16x8 af[9];  // a_r, a_i, a_s planes
+#pragma unroll
+          for (int u = 0; u < 9; ++u) af[u] = *reinterpret_cast<const bf16x8*>(b + u * CTA + off);
+#pragma unroll
+          for (int q = 0; q < 6; ++q)
+#pragma unroll
+            for (int op = 0; op < 3; ++op)
+              T[op][i] = mfma_bf16(af[3 * op + kSplitA[q]], __builtin_bit_cast(bf16x8, bc[3 * op + kSplitB[q]]),
+                                   T[op][i]);
+        }
       }
       // chunk kc + 1 into the other buffer (its last readers finished before the previous
       // barrier), then prefetch chunk kc + 2
@@ -195,16 +240,72 @@ __global__ __launch_bounds__(threads_of(PATH), wg_per_cu(PATH)) void complex_lin
       load_chunk((kc + 2 < nkc ? kc + 2 : nkc - 1) * 16);
       __syncthreads();
     };
-    uint4 b0[9], b1[9];
-    load_chunk(0);
-    store_chunk(0);
-    load_chunk((nkc > 1 ? 1 : 0) * 16);
-    load_b(0, b0);
-    __syncthreads();
-    // unrolled by two so that the fragment double buffer stays in fixed registers
-    for (int kc = 0; kc < nkc; kc += 2) {
-      step(kc, b0, b1);
-      if (kc + 1 < nkc) step(kc + 1, b1, b0);
+    uint4 b0[NB], b1[NB];
+    // F16: exact row scales from a pre-pass when the rows are short, else scales from the first
+    // chunk and, if any row of the tile ended outside the window, a second pass with exact ones
+    const bool prepass = F16 && nkc <= F16_PREPASS_CHUNKS;
+    __shared__ unsigned f16_redo[8];
+    for (int pass = 0; pass < (F16 ? 2 : 1); ++pass) {
+      if constexpr (F16) {
+        if (pass == 0 && !prepass) {
+          load_chunk(0);
+          e = f16_exp_chunk(row_max(chunk_max()));
+        } else {
+          if (pass == 0) {
+#pragma unroll 4
+            for (int kc = 0; kc < nkc; ++kc) {
+              load_chunk(kc * 16);
+              R = fmaxf(R, chunk_max());
+            }
+          } else {
+#pragma unroll
+            for (int p = 0; p < NT; ++p)
+#pragma unroll
+              for (int i = 0; i < RB; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) T[p][i][r] = 0.0f;
+          }
+          e = f16_exp_row(row_max(R));
+        }
+        sc = pow2i(e);
+      }
+      load_chunk(0);
+      store_chunk(0);
+      load_chunk((nkc > 1 ? 1 : 0) * 16);
+      load_b(0, b0);
+      __syncthreads();
+      // unrolled by two so that the fragment double buffer stays in fixed registers
+      for (int kc = 0; kc < nkc; kc += 2) {
+        step(kc, b0, b1);
+        if (kc + 1 < nkc) step(kc + 1, b1, b0);
+      }
+      if constexpr (F16) {
+        if (pass == 1 || prepass) break;
+        // every wave has left the loop (barrier in the last step): its buffers may be restaged
+        const bool wave_out = __ballot(f16_outside(row_max(R) * sc)) != 0;
+        if (lane == 0) f16_redo[wave] = wave_out;
+        __syncthreads();
+        unsigned any = 0;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) any |= f16_redo[w];
+        if (!any) break;
+      }
+    }
+    if constexpr (F16) {
+      // undo the scales: row factor from the staging threads, column factor from the weight
+      __shared__ float f16_rinv[CBM];
+      if (sq == 0) f16_rinv[sr] = pow2i(-e);
+      __syncthreads();
+      const float* cinv = reinterpret_cast<const float*>(W3 + complex_weight_f16_vectors(Nc, Kc));
+      const float cs = cinv[nb * 32 + fr];
+#pragma unroll
+      for (int i = 0; i < RB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float rs = f16_rinv[wr + 32 * i + 8 * (r >> 2) + 4 * fh + (r & 3)];
+#pragma unroll
+          for (int p = 0; p < NT; ++p) T[p][i][r] = T[p][i][r] * rs * cs;
+        }
     }
   } else if constexpr (PATH == CPATH_SPLIT4) {
     // [buf][a_r hi, mid, lo | a_i hi, mid, lo (CTA each) | P hi, mid, lo | Q hi, mid, lo (CTB each)]
@@ -484,25 +585,48 @@ static int complex_launch(const float* A_r, const float* A_i, int64_t lda, const
                           const void* W3, float* Y_r, float* Y_i, int64_t ldy, int64_t M, int32_t Nc, int32_t Kc,
                           CGate g, void* stream, const char* who) {
   if (W3 && !aligned16(W3)) return set_error(FU_ERR_ALIGN, "%s: W3 must be 16-byte aligned", who);
-  const bool fp32 = matmul_mode() == FU_MATMUL_FP32;
-  const int path = fp32 ? CPATH_FP32 : W3 ? CPATH_SPLIT3_PRE : CPATH_SPLIT4;
-  const int tile_n = path == CPATH_SPLIT3_PRE ? CBN_PRE : CBN;
+  const int mode = matmul_mode();
+  // without a pre-split weight both split modes run the in-kernel bf16 four-product loop
+  const int path = mode == FU_MATMUL_FP32 ? CPATH_FP32
+                   : !W3                  ? CPATH_SPLIT4
+                   : mode == FU_MATMUL_SPLIT_F16 ? CPATH_F16_PRE : CPATH_SPLIT3_PRE;
+  const int tile_n = pre_split(path) ? CBN_PRE : CBN;
   const int n_tiles = (Nc + tile_n - 1) / tile_n;
   const int64_t total = ((M + CBM - 1) / CBM) * n_tiles;
   const bool tail = Kc % 16 != 0;
-  auto kern = fp32 ? complex_linear_kernel<MODE, CPATH_FP32>
-              : W3 ? (tail ? complex_linear_kernel<MODE, CPATH_SPLIT3_PRE, true>
-                           : complex_linear_kernel<MODE, CPATH_SPLIT3_PRE, false>)
-                   : (tail ? complex_linear_kernel<MODE, CPATH_SPLIT4, true>
-                           : complex_linear_kernel<MODE, CPATH_SPLIT4, false>);
-  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(path == CPATH_SPLIT3_PRE ? threads_of(CPATH_SPLIT3_PRE) : 256),
-                     0, as_stream(stream), A_r, A_i, lda, P, Q, ldw,
-                     static_cast<const uint4*>(W3), Y_r, Y_i, ldy, M, Nc, Kc, n_tiles, total, g);
+  auto kern = path == CPATH_FP32 ? complex_linear_kernel<MODE, CPATH_FP32>
+              : path == CPATH_SPLIT4 ? (tail ? complex_linear_kernel<MODE, CPATH_SPLIT4, true>
+                                             : complex_linear_kernel<MODE, CPATH_SPLIT4, false>)
+              : path == CPATH_F16_PRE ? (tail ? complex_linear_kernel<MODE, CPATH_F16_PRE, true>
+                                              : complex_linear_kernel<MODE, CPATH_F16_PRE, false>)
+                                      : (tail ? complex_linear_kernel<MODE, CPATH_SPLIT3_PRE, true>
+                                              : complex_linear_kernel<MODE, CPATH_SPLIT3_PRE, false>);
+  // the fp16 path reads the fp16 planes (and, after them, the column factors)
+  const uint4* w3 = static_cast<const uint4*>(W3);
+  if (path == CPATH_F16_PRE) w3 += complex_weight_split_vectors(Nc, Kc);
+  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(threads_of(path)), 0, as_stream(stream), A_r, A_i, lda, P, Q,
+                     ldw, w3, Y_r, Y_i, ldy, M, Nc, Kc, n_tiles, total, g);
   return check_launch(who);
 }
 
-// Builds the fragment-order bf16 planes of (P, Q, P + Q): one thread per (32-column block,
-// 16-k chunk, lane) writes the lane's 8 consecutive k of one column, zero-padded past Nc / Kc.
+// The unscale factor 2^-e(n) of every column of the 32-column blocks (1 past Nc): e(n) is the
+// exact scale (split_f16.h) of the column's largest magnitude over P, Q and P + Q.
+__global__ void complex_weight_scale_kernel(const float* __restrict__ P, const float* __restrict__ Q, int64_t ldw,
+                                            int32_t Nc, int32_t Kc, float* __restrict__ cinv) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= ((Nc + 31) / 32) * 32) return;
+  float m = 0.0f;
+  if (n < Nc)
+    for (int k = 0; k < Kc; ++k) {
+      const float p = P[(int64_t)n * ldw + k], q = Q[(int64_t)n * ldw + k];
+      m = fmaxf(m, fmaxf(fmaxf(fabsf(p), fabsf(q)), fabsf(p + q)));
+    }
+  cinv[n] = pow2i(-f16_exp_row(m));
+}
+
+// Builds the fragment-order planes of (P, Q, P + Q), bf16 and scaled fp16: one thread per
+// (32-column block, 16-k chunk, lane) writes the lane's 8 consecutive k of one column,
+// zero-padded past Nc / Kc.
 __global__ void complex_weight_split_kernel(const float* __restrict__ P, const float* __restrict__ Q, int64_t ldw,
                                             int32_t Nc, int32_t Kc, uint4* __restrict__ W3) {
   const int nkc = (Kc + 15) / 16;
@@ -528,11 +652,31 @@ __global__ void complex_weight_split_kernel(const float* __restrict__ P, const f
   split3(make_float4(p[0] + r[0], p[1] + r[1], p[2] + r[2], p[3] + r[3]),
          make_float4(p[4] + r[4], p[5] + r[5], p[6] + r[6], p[7] + r[7]), h, m, l);
   o[384] = h; o[448] = m; o[512] = l;
+  // fp16 planes of the scaled column (the factor 2^-e(n) is an exact power of two)
+  uint4* f = W3 + complex_weight_split_vectors(Nc, Kc) + q * 6 * 64 + lane;
+  const float* cinv = reinterpret_cast<const float*>(W3 + complex_weight_split_vectors(Nc, Kc) +
+                                                     complex_weight_f16_vectors(Nc, Kc));
+  const float sc = 1.0f / cinv[n];
+  float ps[8], rs[8], ss[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    ps[u] = p[u] * sc;
+    rs[u] = r[u] * sc;
+    ss[u] = (p[u] + r[u]) * sc;
+  }
+  uint4 fh, fl;
+  split2h(make_float4(ps[0], ps[1], ps[2], ps[3]), make_float4(ps[4], ps[5], ps[6], ps[7]), fh, fl);
+  f[0] = fh; f[64] = fl;
+  split2h(make_float4(rs[0], rs[1], rs[2], rs[3]), make_float4(rs[4], rs[5], rs[6], rs[7]), fh, fl);
+  f[128] = fh; f[192] = fl;
+  split2h(make_float4(ss[0], ss[1], ss[2], ss[3]), make_float4(ss[4], ss[5], ss[6], ss[7]), fh, fl);
+  f[256] = fh; f[320] = fl;
 }
 
 extern "C" int64_t fu_complex_weight_split_bytes(int32_t Nc, int32_t Kc) {
   if (Nc <= 0 || Kc <= 0) return set_error(FU_ERR_SHAPE, "fu_complex_weight_split_bytes: Nc=%d Kc=%d", Nc, Kc);
-  return complex_weight_split_vectors(Nc, Kc) * 16;
+  return (complex_weight_split_vectors(Nc, Kc) + complex_weight_f16_vectors(Nc, Kc) +
+          complex_weight_scale_vectors(Nc)) * 16;
 }
 
 extern "C" int fu_complex_weight_split(const float* P, const float* Q, int64_t ldw, int32_t Nc, int32_t Kc, void* W3,
@@ -541,9 +685,13 @@ extern "C" int fu_complex_weight_split(const float* P, const float* Q, int64_t l
   if (Nc <= 0 || Kc <= 0 || ldw < Kc) return set_error(FU_ERR_SHAPE, "%s: Nc=%d Kc=%d ldw=%lld", who, Nc, Kc, (long long)ldw);
   if (!P || !Q || !W3) return set_error(FU_ERR_NULL, "%s: NULL argument", who);
   if (!aligned16(W3)) return set_error(FU_ERR_ALIGN, "%s: W3 must be 16-byte aligned", who);
+  uint4* w3 = static_cast<uint4*>(W3);
+  float* cinv = reinterpret_cast<float*>(w3 + complex_weight_split_vectors(Nc, Kc) + complex_weight_f16_vectors(Nc, Kc));
+  hipLaunchKernelGGL(complex_weight_scale_kernel, dim3(cdiv((int64_t)((Nc + 31) / 32) * 32, 256)), dim3(256), 0,
+                     as_stream(stream), P, Q, ldw, Nc, Kc, cinv);
   const int64_t threads = complex_weight_split_vectors(Nc, Kc) / 9;
   hipLaunchKernelGGL(complex_weight_split_kernel, dim3(cdiv(threads, 256)), dim3(256), 0, as_stream(stream), P, Q, ldw,
-                     Nc, Kc, static_cast<uint4*>(W3));
+                     Nc, Kc, w3);
   return check_launch(who);
 }
 

@@ -313,10 +313,10 @@ class eSCN_Inference_Model(nn.Module):
     # each (ops/edge_grad.py); False returns per-block gradients for autograd to sum instead
     # (the same values up to the order of the fp32 additions).
     SUM_EDGE_GRADS_IN_PLACE = True
-    # conv1 m = 0 gathers its operand in the GEMM loader (fu_gather_linear_gate; lmax 2,
-    # split-bf16 mode) instead of reading the gather's X_m0.  Off by default: at bcc Fe the
-    # fused GEMM costs more than the gather traffic it removes (each rotated element is
-    # produced once per 128-column tile of the 640 outputs).
+    # conv1 m = 0 gathers its operand in the GEMM loader (fu_gather_linear_gate; lmax 2, a
+    # split matrix-core mode, with the bf16 split in both) instead of reading the gather's
+    # X_m0.  Off by default: at bcc Fe the fused GEMM costs more than the gather traffic it
+    # removes (each rotated element is produced once per 128-column tile of the 640 outputs).
     GATHER_IN_CONV1 = False
 
     def __init__(self, num_layers=4, sphere_channels=128, edge_channels=128, num_distance_basis=32, cutoff=5.0,

@@ -267,8 +267,8 @@ class EdgeBlock(torch.autograd.Function):
     forward (each part freed after its GEMM) and its gradient only inside the backward, which
     runs conv_pair_bwd and then the node-centric gather backward.  lmax = 2 (layout 0 or 1) or
     lmax = 3, 4 (reference block order with the degree-3/4 Wigner rows wig_ext).  gather_m0
-    (lmax 2, layout 1, split-bf16 mode): conv1 m = 0 gathers its operand in the GEMM loader
-    (fu_gather_linear_gate) and the gather forms X_m1, X_m2 only."""
+    (lmax 2, layout 1, a split matrix-core mode): conv1 m = 0 gathers its operand in the GEMM
+    loader (fu_gather_linear_gate, bf16 split) and the gather forms X_m1, X_m2 only."""
 
     @staticmethod
     def forward(ctx, x_in, wigner, wig_ext, rad_out, idx_i, idx_j, csd_emb, batch, topology, layout, lmax, conv1,
@@ -279,7 +279,7 @@ class EdgeBlock(torch.autograd.Function):
         m0 = None
         if L == 2:
             ops = gather_operands(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch)
-            fuse = gather_m0 and int(layout) == 1 and _lib.get_matmul_mode() == _lib.MATMUL_SPLIT_BF16
+            fuse = gather_m0 and int(layout) == 1 and _lib.get_matmul_mode() != _lib.MATMUL_FP32
             X = list(gather_fwd(*ops, layout, skip_m0=fuse))
             if fuse:
                 m0 = _gather_conv1_gate_m0(ops, conv1[0], conv1[1], C, _lib.stream_ptr(x_in.device))

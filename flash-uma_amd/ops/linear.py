@@ -46,7 +46,9 @@ def linear(x: torch.Tensor, W: torch.Tensor, bias: torch.Tensor | None, Wt: torc
 
 def complex_weight_split(P: torch.Tensor, Q: torch.Tensor) -> torch.Tensor:
     """The frozen complex weight P + iQ (Nc, Kc each) pre-split for fu_complex_linear's W3
-    argument: exact three-way bf16 splits of P, Q and P + Q in MFMA-fragment order."""
+    argument: exact three-way bf16 splits of P, Q and P + Q in MFMA-fragment order, then their
+    two-way fp16 splits with power-of-two column scales and the columns' unscale factors (one
+    buffer for both split modes)."""
     P = _lib.require(P, torch.float32, "P")
     Q = _lib.require(Q, torch.float32, "Q")
     Nc, Kc = P.shape

@@ -309,7 +309,7 @@ MFMA_BOUND = {"fu_linear", "fu_linear_batched", "fu_complex_linear", "fu_linear_
               "fu_linear_dgrad_ln_silu_bwd", "fu_gather_linear_gate"}
 
 
-def summarize(durations, matmul_mode: int = MATMUL_SPLIT_BF16) -> dict:
+def summarize(durations, matmul_mode: int = MATMUL_SPLIT_F16) -> dict:
     """Per entry point: calls, total/avg ms, algorithmic bytes/flops per launch and the
     achieved fraction of the bounding roofline (matrix-core kernels in `matmul_mode`).
 

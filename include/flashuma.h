@@ -51,10 +51,18 @@ const char* fu_last_error(void);
 /* Matrix-core mode of every fp32 contraction (fu_linear*, fu_complex_linear*); no reference
  * counterpart (the reference's dense layers are cuBLAS fp32 GEMMs with TF32 off, model.py:152,154,
  * reached through torch.nn.functional.linear).
- *   0 (default): each fp32 operand is split exactly into three bf16 planes (x = hi + mid + lo)
+ *   0: each fp32 operand is split exactly into three bf16 planes (x = hi + mid + lo)
  *      and the six significant partial products run on v_mfma_f32_32x32x16_bf16 with fp32
  *      accumulation; error against fp64 at or below that of the fp32 MFMA.
  *   1: v_mfma_f32_32x32x2_f32.
+ *   2 (default): each operand row (a row of A, or a row of W: an output column) is scaled by a power of
+ *      two that puts its largest magnitude in [2^-3, 2^15), each element split into two fp16
+ *      values (x 2^e = hi + lo, 22 significant bits) and three partial products run on
+ *      v_mfma_f32_32x32x16_f16 with fp32 accumulation, unscaled exactly afterwards.  Scales come
+ *      from the row's first 16 elements (or, for K <= 64, from the whole row); a tile whose rows
+ *      end outside the window is computed again with exact scales.  Error against fp64 at or
+ *      below that of the fp32 MFMA on the model's shapes.  fu_gather_linear_gate and
+ *      fu_complex_linear* without W3 keep the bf16 split in this mode.
  * The mode is process-wide and read at each launch; switch it only between launches.
  * fu_set_matmul_mode returns FU_OK or FU_ERR_UNSUPPORTED; fu_matmul_mode returns the mode. */
 int fu_set_matmul_mode(int32_t mode);
@@ -280,9 +288,10 @@ int fu_linear_batched(const float* A, int64_t lda, int64_t stride_a, const float
  * with three real products (Gauss) instead of four.  The input gradient of the layer is
  * the same operation with (P^T, -Q^T).  Kc, lda, ldw multiples of 4; A_r, A_i, P, Q 16-byte
  * aligned.  W3: NULL, or the same weight pre-split by fu_complex_weight_split (16-byte
- * aligned); in the split matrix-core mode (fu_set_matmul_mode) it is read instead of P and Q
- * (three split products, B fragments loaded straight into registers); without it the
- * operands are split in the kernel (four split products).  The fp32 mode ignores W3. */
+ * aligned); in the split matrix-core modes (fu_set_matmul_mode) it is read instead of P and Q
+ * (three split products, B fragments loaded straight into registers: its bf16 planes in mode 0,
+ * its fp16 planes and column scales in mode 2); without it the operands are split in the kernel
+ * (four bf16 split products).  The fp32 mode ignores W3. */
 int fu_complex_linear(const float* A_r, const float* A_i, int64_t lda, const float* P, const float* Q,
                       int64_t ldw, const void* W3, float* Y_r, float* Y_i, int64_t ldy, int64_t M,
                       int32_t Nc, int32_t Kc, void* stream);
@@ -291,8 +300,11 @@ int fu_complex_linear(const float* A_r, const float* A_i, int64_t lda, const flo
  * (a frozen weight of model.py:108-138, prepared once at freeze time).  P, Q (Nc, Kc) with row
  * stride ldw; W3 receives the exact three-way bf16 splits of P, Q and P + Q in MFMA-fragment
  * order ([32-column block][16-k chunk][P, Q, P + Q][hi, mid, lo][64 lanes] x 16 bytes, zero
- * padded to Nc = 32 n, Kc = 16 k), fu_complex_weight_split_bytes(Nc, Kc) bytes, 16-byte
- * aligned.  The bytes query returns a negative FU_ERR_* for Nc or Kc <= 0. */
+ * padded to Nc = 32 n, Kc = 16 k), then the two-way fp16 splits of the same three operands with
+ * each column n scaled by a power of two 2^e(n) (same order, [hi, lo]), then the factors
+ * 2^-e(n) (one float per padded column): fu_complex_weight_split_bytes(Nc, Kc) bytes, 16-byte
+ * aligned, valid in every matrix-core mode.  The bytes query returns a negative FU_ERR_* for Nc
+ * or Kc <= 0. */
 int64_t fu_complex_weight_split_bytes(int32_t Nc, int32_t Kc);
 int fu_complex_weight_split(const float* P, const float* Q, int64_t ldw, int32_t Nc, int32_t Kc, void* W3,
                             void* stream);

@@ -199,11 +199,12 @@ def test_lmax_entry_points_reject_bad_arguments():
 
 
 def test_complex_weight_split_arguments():
-    # one (32-column, 16-k) block holds 9 planes x 64 lanes x 16 B; sizes round up to whole blocks
+    # one (32-column, 16-k) block holds 9 bf16 and 6 fp16 planes x 64 lanes x 16 B, and each
+    # 32-column block 32 column factors (128 B); sizes round up to whole blocks
     st, _ = _status("fu_complex_weight_split_bytes", 32, 16)
-    assert st == 9 * 64 * 16
+    assert st == (9 + 6) * 64 * 16 + 128
     st, _ = _status("fu_complex_weight_split_bytes", 33, 17)
-    assert st == 4 * 9 * 64 * 16
+    assert st == 4 * (9 + 6) * 64 * 16 + 2 * 128
     st, _ = _status("fu_complex_weight_split_bytes", 0, 16)
     assert st == -1
     st, _ = _status("fu_complex_weight_split", None, None, 16, 32, 16, None, None)
@@ -221,7 +222,7 @@ def test_matmul_mode_rejects_unknown():
     st, msg = _status("fu_set_matmul_mode", 5)
     assert st == -2 and "mode=5" in msg
     st, _ = _status("fu_matmul_mode")
-    assert st in (0, 1)
+    assert st in (0, 1, 2)
 
 
 def test_binding_types_match_header():

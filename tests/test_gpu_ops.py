@@ -262,11 +262,13 @@ def test_f16_split_dynamic_range(cuda, M, N, K):
     assert worst[_lib.MATMUL_SPLIT_F16] <= 1.5 * worst[_lib.MATMUL_FP32] + 1e-7, worst
 
 
-@pytest.mark.parametrize("presplit", [False, True], ids=["in_kernel", "presplit"])
-def test_split_complex_accuracy(cuda, presplit):
-    """The complex layer in split mode -- four split products with the weight split in the
-    kernel, or three with a pre-split weight -- against the fp32 mode (three fp32 products) on
-    an m = 1 conv1 shape: both fp32-class against float64, the split one no less accurate."""
+@pytest.mark.parametrize("split,presplit", [(0, False), (0, True), (2, True)],
+                         ids=["bf16_in_kernel", "bf16_presplit", "f16_presplit"])
+def test_split_complex_accuracy(cuda, split, presplit):
+    """The complex layer in the split modes -- four bf16 split products with the weight split in
+    the kernel, or three with a pre-split weight (bf16, or scaled fp16 in mode 2) -- against the
+    fp32 mode (three fp32 products) on an m = 1 conv1 shape: both fp32-class against float64,
+    the split one no less accurate."""
     from ops import _lib
     from ops.linear import complex_gemm, complex_weight_split
     g = torch.Generator().manual_seed(7)
@@ -277,22 +279,58 @@ def test_split_complex_accuracy(cuda, presplit):
     ref = (x.double() @ R.pack_so2(Rw.double(), Iw.double()).T).to(cuda)
     err = {}
     W3 = complex_weight_split(Rw.to(cuda), Iw.to(cuda)) if presplit else None
-    for mode in (_lib.MATMUL_SPLIT_BF16, _lib.MATMUL_FP32):
+    for mode in (split, _lib.MATMUL_FP32):
         with _lib.matmul_mode(mode):
             y = complex_gemm(x.to(cuda), Rw.to(cuda), Iw.to(cuda), W3)
         d = y.double() - ref
         err[mode] = (d.norm().item() / ref.norm().item(), d.abs().max().item() / ref.abs().max().item())
-    rms_s, max_s = err[_lib.MATMUL_SPLIT_BF16]
+    rms_s, max_s = err[split]
     rms_f, max_f = err[_lib.MATMUL_FP32]
     assert rms_s < 1e-6 and max_s < 5e-6, err
     assert rms_s <= 1.1 * rms_f and max_s <= 1.5 * max_f, err
 
 
+@pytest.mark.parametrize("M,Kc,Nc", [(20000, 512, 256), (3000, 64, 128), (3000, 100, 68)])
+def test_f16_complex_dynamic_range(cuda, M, Kc, Nc):
+    """The pre-split complex layer in the fp16 mode on rows far from 1, rows whose magnitude
+    changes along K (second pass with exact scales), zero and tiny rows, columns of very
+    different scales, the short-K pre-pass (Kc = 64) and K-tail / partial-block (Kc = 100,
+    Nc = 68) forms: every row's error against float64, relative to that row's norm, within 1.5x
+    the fp32 mode's worst row plus 1e-7, and finite."""
+    from ops import _lib
+    from ops.linear import complex_gemm, complex_weight_split
+    g = torch.Generator().manual_seed(M + Kc + Nc)
+    x = torch.randn(M, 2 * Kc, generator=g)
+    Rw = torch.randn(Nc, Kc, generator=g) / Kc ** 0.5
+    Iw = torch.randn(Nc, Kc, generator=g) / Kc ** 0.5
+    q = M // 8
+    x[:q] *= torch.exp2(torch.randint(-40, 40, (q, 1), generator=g).double()).float()
+    ramp = torch.linspace(-24, 24, Kc).repeat(2)
+    x[q:2 * q:2] *= torch.exp2(ramp)
+    x[q + 1:2 * q:2] *= torch.exp2(-ramp)
+    x[2 * q:2 * q + 64] = 0.0
+    x[2 * q + 64:2 * q + 128] *= 1e-20
+    cs = torch.exp2(torch.randint(-30, 30, (Nc, 1), generator=g).double()).float()
+    Rw, Iw = Rw * cs, Iw * cs
+    Rw[:4] = 0.0
+    Iw[:4] = 0.0
+    ref = x.double() @ R.pack_so2(Rw.double(), Iw.double()).T
+    rn = ref.norm(dim=1).clamp_min(1e-300)
+    W3 = complex_weight_split(Rw.to(cuda), Iw.to(cuda))
+    worst = {}
+    for mode in (_lib.MATMUL_SPLIT_F16, _lib.MATMUL_FP32):
+        with _lib.matmul_mode(mode):
+            y = complex_gemm(x.to(cuda), Rw.to(cuda), Iw.to(cuda), W3).cpu()
+        assert torch.isfinite(y).all(), mode
+        worst[mode] = ((y.double() - ref).norm(dim=1) / rn).max().item()
+    assert worst[_lib.MATMUL_SPLIT_F16] <= 1.5 * worst[_lib.MATMUL_FP32] + 1e-7, worst
+
+
 def test_matmul_mode_switch(cuda):
     from ops import _lib
     prev = _lib.get_matmul_mode()
-    assert prev == _lib.MATMUL_SPLIT_BF16
-    for mode in (_lib.MATMUL_FP32, _lib.MATMUL_SPLIT_F16):
+    assert prev == _lib.MATMUL_SPLIT_F16
+    for mode in (_lib.MATMUL_FP32, _lib.MATMUL_SPLIT_BF16):
         with _lib.matmul_mode(mode):
             assert _lib.get_matmul_mode() == mode
     assert _lib.get_matmul_mode() == prev
