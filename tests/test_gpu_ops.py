@@ -224,6 +224,7 @@ def test_split_gemm_accuracy(cuda, split, N, K):
         err[mode] = (d.norm().item() / ref.norm().item(), d.abs().max().item() / ref.abs().max().item())
     rms_s, max_s = err[split]
     rms_f, max_f = err[_lib.MATMUL_FP32]
+    print(f"gemm {N}x{K} mode {split}: rms {rms_s:.2e} max {max_s:.2e}; fp32 MFMA rms {rms_f:.2e} max {max_f:.2e}")
     assert rms_s < 1e-6 and max_s < 5e-6, err
     assert rms_s <= 1.1 * rms_f and max_s <= 1.5 * max_f, err
 
@@ -259,6 +260,8 @@ def test_f16_split_dynamic_range(cuda, M, N, K):
             y = linear.gemm(x.to(cuda), W.to(cuda)).cpu()
         assert torch.isfinite(y).all(), mode
         worst[mode] = ((y.double() - ref).norm(dim=1) / rn).max().item()
+    print(f"dynamic range {tuple(x.shape)} x {tuple(W.shape)}: worst row f16 "
+          f"{worst[_lib.MATMUL_SPLIT_F16]:.2e}, fp32 MFMA {worst[_lib.MATMUL_FP32]:.2e}")
     assert worst[_lib.MATMUL_SPLIT_F16] <= 1.5 * worst[_lib.MATMUL_FP32] + 1e-7, worst
 
 
@@ -286,6 +289,8 @@ def test_split_complex_accuracy(cuda, split, presplit):
         err[mode] = (d.norm().item() / ref.norm().item(), d.abs().max().item() / ref.abs().max().item())
     rms_s, max_s = err[split]
     rms_f, max_f = err[_lib.MATMUL_FP32]
+    print(f"complex mode {split} presplit {presplit}: rms {rms_s:.2e} max {max_s:.2e}; "
+          f"fp32 MFMA rms {rms_f:.2e} max {max_f:.2e}")
     assert rms_s < 1e-6 and max_s < 5e-6, err
     assert rms_s <= 1.1 * rms_f and max_s <= 1.5 * max_f, err
 
@@ -323,6 +328,8 @@ def test_f16_complex_dynamic_range(cuda, M, Kc, Nc):
             y = complex_gemm(x.to(cuda), Rw.to(cuda), Iw.to(cuda), W3).cpu()
         assert torch.isfinite(y).all(), mode
         worst[mode] = ((y.double() - ref).norm(dim=1) / rn).max().item()
+    print(f"complex dynamic range {tuple(x.shape)}, Nc {Nc}: worst row f16 "
+          f"{worst[_lib.MATMUL_SPLIT_F16]:.2e}, fp32 MFMA {worst[_lib.MATMUL_FP32]:.2e}")
     assert worst[_lib.MATMUL_SPLIT_F16] <= 1.5 * worst[_lib.MATMUL_FP32] + 1e-7, worst
 
 
