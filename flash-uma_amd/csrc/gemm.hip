@@ -628,8 +628,70 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
     // one degree, inside one 32-channel group of the gate-paired order).
     const int C = gb.C, n1 = C / 32, L = gb.L;
     float* ws = smem + wave * 32 * GES;
+    // A wave's 64 columns lie in one degree block kb (C is a multiple of 64), so the branch on
+    // kb is uniform.  The global operands of a lane's pieces (the gate column and y of Y0, the
+    // gate sums P1 (+ P2)) do not depend on the product: those of pieces 0-3 are loaded before
+    // the slab is staged and those of pieces 4-7 before pieces 0-3 are computed, so their
+    // latency overlaps the staging and the work before them.  A row past M loads row M - 1 and
+    // is not stored.
+    const int gcw = col0 + wc;
+    const int kb = gcw / C;
+    auto load_ops = [&](int i, int q, float4& gp, float4& y, float4& p) {
+      const int lin = lane + 64 * q;
+      int64_t gr = row0 + wr + i * 32 + (lin >> 4);
+      gr = gr < M ? gr : M - 1;
+      const int ch = gcw + (lin & 15) * 4 - kb * C;
+      const float* y0 = gb.Y0 + gr * gb.ldy0;
+      if (kb == 0) {
+        y = ld4(y0 + 2 * L * C + ch);
+      } else {
+        const int gate_col = 64 * ((kb - 1) * n1 + (ch >> 5)) + (ch & 31);
+        gp = ld4(y0 + gate_col);
+        y = ld4(y0 + gate_col + 32);
+        p = ld4(gb.P1 + gr * gb.ldp1 + (kb - 1) * C + ch);
+        if (kb >= 2) p = p + ld4(gb.P2 + gr * gb.ldp2 + (kb - 2) * C + ch);
+      }
+    };
+    auto piece = [&](int i, int q, const float4& gp, const float4& y, const float4& p) {
+      const int lin = lane + 64 * q;
+      const int r = lin >> 4;
+      const int c = (lin & 15) * 4;
+      const int64_t gr = row0 + wr + i * 32 + r;
+      const int gc = gcw + c;
+      if (gr >= M || gc >= N) return;
+      const float4 g = ld4(&ws[r * GES + c]);
+      const int ch = gc - kb * C;
+      float* out = Y + gr * ldy;
+      if (kb == 0) {
+        float4 o;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float yt = (&y.x)[t], sl = sigmoidf_(yt);
+          (&o.x)[t] = (&g.x)[t] * (sl + yt * (sl * (1.0f - sl)));
+        }
+        st4_nt(out + 2 * L * C + ch, o);
+      } else {
+        const int gate_col = 64 * ((kb - 1) * n1 + (ch >> 5)) + (ch & 31);
+        float4 og, ov;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float st = sigmoidf_((&gp.x)[t]), gt = (&g.x)[t];
+          (&ov.x)[t] = gt * st;
+          (&og.x)[t] = (st * (1.0f - st)) * (gt * (&y.x)[t] + (&p.x)[t]);
+        }
+        st4_nt(out + gate_col, og);
+        st4_nt(out + gate_col + 32, ov);
+      }
+    };
+    // split modes: a ring of four operand slots, two filled before the staging; piece q + 4 is
+    // loaded into piece q's slot once q is done.  The fp32 mode (four workgroups per CU, 128
+    // VGPRs) keeps one slot.
+    constexpr int SLOTS = SPLIT ? 4 : 1, PRE = SPLIT ? 2 : 0;
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
+      float4 gp[SLOTS], yv[SLOTS], pv[SLOTS];
+#pragma unroll
+      for (int q = 0; q < PRE; ++q) load_ops(i, q, gp[q], yv[q], pv[q]);
       __syncthreads();
 #pragma unroll
       for (int j = 0; j < 2; ++j)
@@ -637,43 +699,11 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
         for (int r = 0; r < 16; ++r) ws[(8 * (r >> 2) + orow + (r & 3)) * GES + j * 32 + oc] = acc[i][j][r];
       __syncthreads();
 #pragma unroll
+      for (int q = PRE; q < SLOTS; ++q) load_ops(i, q, gp[q], yv[q], pv[q]);
+#pragma unroll
       for (int q = 0; q < 8; ++q) {
-        const int lin = lane + 64 * q;
-        const int r = lin >> 4;
-        const int c = (lin & 15) * 4;
-        const int64_t gr = row0 + wr + i * 32 + r;
-        const int gc = col0 + wc + c;
-        if (gr >= M || gc >= N) continue;
-        const float4 g = ld4(&ws[r * GES + c]);
-        const int kb = gc / C, ch = gc - kb * C;
-        const float* y0 = gb.Y0 + gr * gb.ldy0;
-        float* out = Y + gr * ldy;
-        if (kb == 0) {
-          const float4 y = ld4(y0 + 2 * L * C + ch);
-          float4 o;
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const float yt = (&y.x)[t], sl = sigmoidf_(yt);
-            (&o.x)[t] = (&g.x)[t] * (sl + yt * (sl * (1.0f - sl)));
-          }
-          st4_nt(out + 2 * L * C + ch, o);
-        } else {
-          const int gate_col = 64 * ((kb - 1) * n1 + (ch >> 5)) + (ch & 31);
-          const float4 gp = ld4(y0 + gate_col);
-          const float4 sg = make_float4(sigmoidf_(gp.x), sigmoidf_(gp.y), sigmoidf_(gp.z), sigmoidf_(gp.w));
-          const float4 y = ld4(y0 + gate_col + 32);
-          float4 p = ld4(gb.P1 + gr * gb.ldp1 + (kb - 1) * C + ch);
-          if (kb >= 2) p = p + ld4(gb.P2 + gr * gb.ldp2 + (kb - 2) * C + ch);
-          float4 og, ov;
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const float st = (&sg.x)[t], gt = (&g.x)[t];
-            (&ov.x)[t] = gt * st;
-            (&og.x)[t] = (st * (1.0f - st)) * (gt * (&y.x)[t] + (&p.x)[t]);
-          }
-          st4_nt(out + gate_col, og);
-          st4_nt(out + gate_col + 32, ov);
-        }
+        piece(i, q, gp[q % SLOTS], yv[q % SLOTS], pv[q % SLOTS]);
+        if (q + SLOTS < 8) load_ops(i, q + SLOTS, gp[q % SLOTS], yv[q % SLOTS], pv[q % SLOTS]);
       }
     }
     return;
