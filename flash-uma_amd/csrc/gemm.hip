@@ -636,7 +636,11 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
     // is not stored.
     const int gcw = col0 + wc;
     const int kb = gcw / C;
+    // N is a multiple of 64, so a wave's columns are all below N or all at or past it; a wave
+    // past N (the last column tile when N is not a multiple of 128) loads and stores nothing
+    const bool wave_live = gcw < N;
     auto load_ops = [&](int i, int q, float4& gp, float4& y, float4& p) {
+      if (!wave_live) return;
       const int lin = lane + 64 * q;
       int64_t gr = row0 + wr + i * 32 + (lin >> 4);
       gr = gr < M ? gr : M - 1;
