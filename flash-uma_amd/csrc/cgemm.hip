@@ -9,8 +9,15 @@
 // MFMA flops for the same result up to fp32 rounding.  The sums a_r + a_i and P + Q are
 // formed in registers from the operands already staged in LDS, so no extra memory traffic.
 //
-// K advances in chunks of 16 through double-buffered LDS.  Three main loops:
-//  * split bf16 with a pre-split weight (default when the caller passes W3, built once per
+// K advances in chunks of 16 through double-buffered LDS.  Four main loops:
+//  * split fp16 with a pre-split weight (the default matrix-core mode, with W3): as the bf16
+//    form below, with two fp16 planes per operand (split_f16.h).  The weight's planes hold
+//    its columns scaled by one power of two per output column (shared by P, Q and S, so the
+//    three products stay combinable), computed when the weight is split; a row of
+//    (a_r, a_i, a_s) gets one scale from its first chunk (or, for Kc <= 64, from a pre-pass),
+//    with a second pass of the tile at exact scales if a row leaves the window.  Three MFMAs
+//    per product and 32-row block instead of six; 24 KB of A planes per buffer.
+//  * split bf16 with a pre-split weight (mode 0 when the caller passes W3, built once per
 //    frozen weight by fu_complex_weight_split): P, Q and S = P + Q are stored as bf16 planes
 //    in MFMA-fragment order ([32-column block][16-k chunk][P, Q, S][hi, mid, lo][lane], 16 B
 //    per lane), so each wave loads its B fragments with 1 KB coalesced loads straight into

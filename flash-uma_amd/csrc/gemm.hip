@@ -7,9 +7,14 @@
 //
 // Tiling: a 256-thread workgroup (4 wave64s in a 2x2 grid) owns a 128x128 output tile; each
 // wave owns 64x64 = 2x2 MFMA blocks of 32x32 (64 fp32 accumulators per lane, in VGPRs).
-// K advances in chunks of 16 staged through double-buffered LDS.  Two main loops share the
+// K advances in chunks of 16 staged through double-buffered LDS.  Three main loops share the
 // tiling and the epilogues (fu_set_matmul_mode):
-//  * split bf16 (default): each staged fp32 element is split into three bf16 planes
+//  * split fp16 (default, F16): each staged row is scaled by its power of two and split into
+//    two fp16 planes (split_f16.h); three v_mfma_f32_32x32x16_f16 per 32x32 block and chunk.
+//    The scales come from the first chunk (a pre-pass over the row when K <= 64), every staged
+//    row's running maximum is kept, and a tile with a row or column outside the window runs
+//    its K loop again at exact scales.  The accumulators are unscaled before the epilogue.
+//  * split bf16: each staged fp32 element is split into three bf16 planes
 //    (split_bf16.h) as it is written to LDS (48 KB of planes, two workgroups per CU); per chunk
 //    a wave reads 3 planes of each operand fragment and issues six v_mfma_f32_32x32x16_bf16
 //    per 32x32 block.  The loop body has no branches (the last prefetch re-reads the last
