@@ -11,9 +11,10 @@
 // tiling and the epilogues (fu_set_matmul_mode):
 //  * split fp16 (default, F16): each staged row is scaled by its power of two and split into
 //    two fp16 planes (split_f16.h); three v_mfma_f32_32x32x16_f16 per 32x32 block and chunk.
-//    The scales come from the first chunk (a pre-pass over the row when K <= 64), every staged
-//    row's running maximum is kept, and a tile with a row or column outside the window runs
-//    its K loop again at exact scales.  The accumulators are unscaled before the epilogue.
+//    The scales come from the first chunk (from a pre-pass over the rows when K <= 64 or when a
+//    row's first chunk is zero); a tile whose accumulators came out non-finite (an fp16 piece
+//    overflowed) runs its K loop again at exact scales.  The accumulators are unscaled before
+//    the epilogue.
 //  * split bf16: each staged fp32 element is split into three bf16 planes
 //    (split_bf16.h) as it is written to LDS (48 KB of planes, two workgroups per CU); per chunk
 //    a wave reads 3 planes of each operand fragment and issues six v_mfma_f32_32x32x16_bf16
@@ -303,20 +304,16 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
         }
       }
     };
-    // F16: the power-of-two scales of the staged rows (A row, second A row if TALL, W row) and
-    // their running maxima, this thread's half of each row (split_f16.h)
-    float scA = 1.0f, scA2 = 1.0f, scW = 1.0f, RA = 0.0f, RA2 = 0.0f, RW = 0.0f;
+    // F16: the power-of-two scales of the staged rows (A row, second A row if TALL, W row)
+    float scA = 1.0f, scA2 = 1.0f, scW = 1.0f;
     int eA = 0, eA2 = 0, eW = 0;
     auto store_chunk = [&](int buf) {
       __bf16* b = sp + buf * NP * (PA + PW);
       if constexpr (F16) {
-        RA = fmaxf(RA, fmaxf(amax4(ga[0]), amax4(ga[1])));
-        RW = fmaxf(RW, fmaxf(amax4(gw[0]), amax4(gw[1])));
         uint4 h, l;
         split2h(scale4(ga[0], scA), scale4(ga[1], scA), h, l);
         st_planes2(b, PA, soff, h, l);
         if constexpr (TALL) {
-          RA2 = fmaxf(RA2, fmaxf(amax4(ga2[0]), amax4(ga2[1])));
           split2h(scale4(ga2[0], scA2), scale4(ga2[1], scA2), h, l);
           st_planes2(b, PA, plane_off(128 + sr, sh), h, l);
         }
@@ -337,27 +334,48 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
     // the larger magnitude of this thread's and its partner's half of a staged row
     auto row_max = [&](float v) { return fmaxf(v, __shfl_xor(v, 1, 64)); };
     const int nk = (K + GBK - 1) / GBK;
-    // F16: exact scales from a pre-pass when the rows are short, else scales from the first
-    // chunk and, if any staged row ended outside the window, a second pass with exact scales
-    const bool prepass = F16 && nk <= F16_PREPASS_CHUNKS;
-    __shared__ unsigned f16_redo[4];
-    for (int pass = 0; pass < (F16 ? 2 : 1); ++pass) {
-      if constexpr (F16) {
-        if (pass == 0 && !prepass) {
-          load_chunk(0);
-          eA = f16_exp_chunk(row_max(fmaxf(amax4(ga[0]), amax4(ga[1]))));
-          if constexpr (TALL) eA2 = f16_exp_chunk(row_max(fmaxf(amax4(ga2[0]), amax4(ga2[1]))));
-          eW = f16_exp_chunk(row_max(fmaxf(amax4(gw[0]), amax4(gw[1]))));
-        } else {
-          if (pass == 0) {
+    // F16 scales: from the rows' first chunk; exact (a pass over the whole rows) when the rows
+    // are short, when a row's first chunk is zero (nothing to scale from), and in the second
+    // pass, which runs when a row or column overflowed fp16 with the first-chunk scale (the
+    // overflowed piece made its accumulators non-finite).  With a nonzero first chunk the
+    // row's largest magnitude is at least 2^6 after scaling, so without overflow the row is
+    // inside the window.
+    const bool short_k = F16 && nk <= F16_PREPASS_CHUNKS;
+    __shared__ unsigned f16_any[4];
+    auto tile_any = [&](bool v) {  // v on any thread of the workgroup (every thread calls this)
+      const bool w = __ballot(v) != 0;
+      if (lane == 0) f16_any[wave] = w;
+      __syncthreads();
+      return (f16_any[0] | f16_any[1] | f16_any[2] | f16_any[3]) != 0;
+    };
+    auto exact_scales = [&]() {
+      float RA = 0.0f, RA2 = 0.0f, RW = 0.0f;
 #pragma unroll 4
-            for (int kc = 0; kc < nk; ++kc) {
-              load_chunk(kc * GBK);
-              RA = fmaxf(RA, fmaxf(amax4(ga[0]), amax4(ga[1])));
-              if constexpr (TALL) RA2 = fmaxf(RA2, fmaxf(amax4(ga2[0]), amax4(ga2[1])));
-              RW = fmaxf(RW, fmaxf(amax4(gw[0]), amax4(gw[1])));
-            }
-          } else {
+      for (int kc = 0; kc < nk; ++kc) {
+        load_chunk(kc * GBK);
+        RA = fmaxf(RA, fmaxf(amax4(ga[0]), amax4(ga[1])));
+        if constexpr (TALL) RA2 = fmaxf(RA2, fmaxf(amax4(ga2[0]), amax4(ga2[1])));
+        RW = fmaxf(RW, fmaxf(amax4(gw[0]), amax4(gw[1])));
+      }
+      eA = f16_exp_row(row_max(RA));
+      if constexpr (TALL) eA2 = f16_exp_row(row_max(RA2));
+      eW = f16_exp_row(row_max(RW));
+    };
+    for (int pass = 0; pass < (F16 ? 2 : 1); ++pass) {
+      bool exact = short_k || pass == 1;
+      if constexpr (F16) {
+        if (!exact) {
+          load_chunk(0);
+          const float mA = row_max(fmaxf(amax4(ga[0]), amax4(ga[1])));
+          const float mA2 = TALL ? row_max(fmaxf(amax4(ga2[0]), amax4(ga2[1]))) : 1.0f;
+          const float mW = row_max(fmaxf(amax4(gw[0]), amax4(gw[1])));
+          eA = f16_exp_chunk(mA);
+          if constexpr (TALL) eA2 = f16_exp_chunk(mA2);
+          eW = f16_exp_chunk(mW);
+          exact = tile_any(mA == 0.0f || mA2 == 0.0f || mW == 0.0f);
+        }
+        if (exact) {
+          if (pass == 1) {
 #pragma unroll
             for (int i = 0; i < RB; ++i)
 #pragma unroll
@@ -365,9 +383,7 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
           }
-          eA = f16_exp_row(row_max(RA));
-          if constexpr (TALL) eA2 = f16_exp_row(row_max(RA2));
-          eW = f16_exp_row(row_max(RW));
+          exact_scales();
         }
         scA = pow2i(eA);
         scA2 = pow2i(eA2);
@@ -413,14 +429,16 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
         __syncthreads();
       }
       if constexpr (F16) {
-        if (pass == 1 || prepass) break;
+        if (exact) break;  // exact scales cannot overflow (non-finite inputs stay non-finite)
         // every wave has left the loop (barrier above): its buffers may be restaged
-        const bool out = f16_outside(row_max(RA) * scA) || (TALL && f16_outside(row_max(RA2) * scA2)) ||
-                         f16_outside(row_max(RW) * scW);
-        const bool wave_out = __ballot(out) != 0;
-        if (lane == 0) f16_redo[wave] = wave_out;
-        __syncthreads();
-        if (!(f16_redo[0] | f16_redo[1] | f16_redo[2] | f16_redo[3])) break;
+        bool bad = false;
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) bad = bad || !__builtin_isfinite(acc[i][j][r]);
+        if (!tile_any(bad)) break;
       }
     }
     if constexpr (F16) {

@@ -16,10 +16,14 @@
 // bits, and every smaller element's error (at most 2^-25 after scaling) stays below 2^-22 R.  The
 // kernels pick the scale one of two ways:
 //  * exact: R from a pre-pass over the row, e = 14 - floor(log2 R) (R 2^e in [2^14, 2^15));
-//  * from the first chunk: the maximum m of the row's first 16 elements is mapped to [2^6, 2^7),
-//    the running maximum R is tracked while the chunks are staged, and a tile in which any row
-//    or column ends outside the window is computed again with the exact scale.  That leaves
-//    256x of headroom above the first chunk and keeps elements down to 2^-9 m at full precision.
+//  * from the first chunk: the maximum m of the row's first 16 elements is mapped to [2^6, 2^7).
+//    That leaves 256x of headroom above the first chunk and keeps elements down to 2^-9 m at
+//    full precision; the row's largest magnitude is then at least 2^6 after scaling, so only
+//    overflow can take it out of the window.  A tile with such a row or column is computed
+//    again with exact scales.  The complex layer finds those rows from the running maximum kept
+//    while the chunks are staged; the real GEMM from its accumulators (an overflowed fp16 piece
+//    makes its row's or column's outputs non-finite) and sends a tile that has a row with a
+//    zero first chunk (nothing to scale from) to the exact scales from the start.
 // A row of zeros keeps e = 0.
 #pragma once
 #include "split_bf16.h"
