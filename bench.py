@@ -32,7 +32,8 @@ MATMUL_TEXT = {
     0: "fp32 operands split exactly into three bf16 planes, six bf16 MFMA products, fp32 accumulation",
     1: "fp32 MFMA",
     2: "fp32 operands scaled by per-row powers of two and split into two fp16 planes, three fp16 MFMA "
-       "products, fp32 accumulation",
+       "products, fp32 accumulation; error against float64 below the fp32 MFMA's "
+       "(tests/test_gpu_ops.py::test_split_gemm_accuracy, test_split_complex_accuracy)",
 }
 
 
