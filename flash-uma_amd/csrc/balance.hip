@@ -121,22 +121,30 @@ constexpr int64_t kBalanceScratchFloats = FU_BALANCE_NOALLOC_MAX_CORR;
 __device__ __align__(256) float scratch[kBalanceScratchFloats];
 
 // Device address of `scratch` on each GPU, looked up once per device (with that device
-// current) on the first call there.
+// current) on the first call there.  The device is the one the launch stream belongs to
+// (the null stream: the current device), so a caller whose current device is another one
+// still gets the copy on the stream's GPU.
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 float* g_scratch_ptr[kMaxDevices] = {nullptr};
 
-int scratch_for_current_device(float** ptr) {
+int scratch_for_stream(hipStream_t stream, float** ptr) {
+  const char* who = "fu_balance_channels_noalloc";
   int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
-    return set_error(FU_ERR_LAUNCH, "fu_balance_channels_noalloc: no current HIP device (or device id >= %d)",
-                     kMaxDevices);
+  const hipError_t ge = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (ge != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(FU_ERR_LAUNCH, "%s: cannot find the stream's HIP device (or device id >= %d)", who, kMaxDevices);
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return set_error(FU_ERR_LAUNCH, "%s: no current HIP device", who);
+    if (cur != dev && hipSetDevice(dev) != hipSuccess)
+      return set_error(FU_ERR_LAUNCH, "%s: cannot make device %d current", who, dev);
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
     if (e != hipSuccess || !p)
-      return set_error(FU_ERR_LAUNCH, "fu_balance_channels_noalloc: hipGetSymbolAddress failed on device %d: %s", dev,
+      return set_error(FU_ERR_LAUNCH, "%s: hipGetSymbolAddress failed on device %d: %s", who, dev,
                        hipGetErrorString(e));
     g_scratch_ptr[dev] = static_cast<float*>(p);
   }
@@ -171,7 +179,7 @@ extern "C" int fu_balance_channels_noalloc(const float* x, float* out, const int
                      (long long)S * (c1 - c0), (long long)kBalanceScratchFloats);
   if (N == 0) return FU_OK;
   float* corr = nullptr;
-  st = scratch_for_current_device(&corr);
+  st = scratch_for_stream(as_stream(stream), &corr);
   if (st != FU_OK) return st;
   return balance_launch(who, x, out, batch, sys_ptr, target, target_offset, corr, N, K, C, S, c0, c1,
                         as_stream(stream));

@@ -66,15 +66,19 @@ constexpr bool pre_split(int path) { return path == CPATH_SPLIT3_PRE || path == 
 // A pre-split complex weight holds, one after the other:
 //  * bf16 planes in fragment order: per (32-column block, 16-k chunk), 9 x 64 lanes x 16 B
 //    (P, Q, S = P + Q, each hi, mid, lo);
-//  * fp16 planes in the same order: per (block, chunk), 6 x 64 lanes x 16 B (P, Q, S, each hi,
-//    lo) of the columns scaled by their power of two 2^e(n) (split_f16.h; one scale per output
-//    column n, shared by P, Q and S so that the three products stay combinable);
-//  * the unscale factors 2^-e(n), one float per column of the 32-column blocks.
+//  * fp16 planes in the same order: per (block, chunk), 9 x 64 lanes x 16 B: P hi, P lo, Q hi,
+//    Q lo, S hi, S lo of the columns scaled by their power of two 2^e(n) (split_f16.h; one exact
+//    scale per output column n, shared by P, Q and S so that the three products stay
+//    combinable), then the lo' = 2^11 lo planes of P, Q and S (pass 2 of split_f16.h);
+//  * the unscale factors 2^-e(n), one float per column of the 32-column blocks;
+//  * one int per column of the 32-column blocks: bit 0 set when a piece of 8 consecutive k of
+//    P or Q of that column is nonzero and below the window (2^-3) at the column's scale, bit 1
+//    when the column is not flat (split_f16.h); the kernels' pass rules read them.
 __host__ __device__ inline int64_t complex_weight_split_vectors(int32_t Nc, int32_t Kc) {
   return (int64_t)((Nc + 31) / 32) * ((Kc + 15) / 16) * 9 * 64;
 }
 __host__ __device__ inline int64_t complex_weight_f16_vectors(int32_t Nc, int32_t Kc) {
-  return (int64_t)((Nc + 31) / 32) * ((Kc + 15) / 16) * 6 * 64;
+  return (int64_t)((Nc + 31) / 32) * ((Kc + 15) / 16) * 9 * 64;
 }
 __host__ __device__ inline int64_t complex_weight_scale_vectors(int32_t Nc) { return (int64_t)((Nc + 31) / 32) * 8; }
 
@@ -176,25 +180,38 @@ __global__ __launch_bounds__(threads_of(PATH), wg_per_cu(PATH)) void complex_lin
         gi = ok ? i : z4;
       }
     };
-    // F16: the row's scale and the running maximum of |a_r|, |a_i|, |a_s| (this thread's quarter)
-    float sc = 1.0f, R = 0.0f;
+    // F16: the row's scale, the running maximum of |a_r|, |a_i|, |a_s| (this thread's quarter)
+    // and whether a piece staged in pass 0 fell below the window (split_f16.h)
+    float sc = 1.0f, R = 0.0f, pmin = __builtin_huge_valf();
     int e = 0;
+    bool lossy = false;
     auto chunk_max = [&]() { return fmaxf(fmaxf(amax4(gr), amax4(gi)), amax4(gr + gi)); };
     auto row_max = [&](float v) {  // over the row's four staging threads
       v = fmaxf(v, __shfl_xor(v, 1, 64));
       return fmaxf(v, __shfl_xor(v, 2, 64));
     };
-    auto store_chunk = [&](int buf) {
+    // ps: the pass kind (0: hi + lo planes, the pieces' window tracked; 1: hi and lo' = 2^11 lo
+    // planes; 2: hi planes)
+    auto store_chunk = [&](int buf, auto ps) {
+      constexpr int PS = decltype(ps)::value;
       __bf16* b = sp + buf * BUF;
       if constexpr (F16) {
-        R = fmaxf(R, chunk_max());
-        uint2 h, l;
-        split2h_4(scale4(gr, sc), h, l);
-        st_planes2_4(b, CTA, soff, h, l);
-        split2h_4(scale4(gi, sc), h, l);
-        st_planes2_4(b + 2 * CTA, CTA, soff, h, l);
-        split2h_4(scale4(gr + gi, sc), h, l);
-        st_planes2_4(b + 4 * CTA, CTA, soff, h, l);
+        auto put = [&](const float4& v, int plane) {
+          uint2 h, l;
+          if constexpr (PS == 0) split2h_4(v, h, l);
+          else split2h_4_up(v, h, l);
+          st_planes2_4(b + plane * CTA, CTA, soff, h, l);
+        };
+        const float4 vr = scale4(gr, sc), vi = scale4(gi, sc);
+        if constexpr (PS == 0) {
+          R = fmaxf(R, chunk_max());
+          const float mr = amax4(vr), mi = amax4(vi);
+          pmin = fminf(pmin, fminf(mr, mi));
+          lossy |= f16_lossy(mr) || f16_lossy(mi);
+        }
+        put(vr, 0);
+        put(vi, 2);
+        put(scale4(gr + gi, sc), 4);
       } else {
         uint2 h, m, l;
         split3_4(gr, h, m, l);
@@ -206,16 +223,24 @@ __global__ __launch_bounds__(threads_of(PATH), wg_per_cu(PATH)) void complex_lin
       }
     };
     // this wave's B fragments of chunk kc (a column block past Nc reads block 0; its outputs
-    // are never stored)
-    int nb = (col0 + wc) / 32;
-    nb = nb < nbt ? nb : 0;
-    const uint4* wb = W3 + (int64_t)nb * nkc * NB * 64 + lane;
-    auto load_b = [&](int kc, uint4 (&bf)[NB]) {
+    // are never stored).  F16: per (block, chunk) the weight holds NBS vectors of 64 lanes, the
+    // hi and lo planes of P, Q, S and then their lo' planes (pass kind 1 loads hi and lo').
+    constexpr int NBS = F16 ? 9 : NB;
+    const int nb_raw = (col0 + wc) / 32;
+    const int nb = nb_raw < nbt ? nb_raw : 0;
+    const uint4* wb = W3 + (int64_t)nb * nkc * NBS * 64 + lane;
+    auto load_b = [&](int kc, uint4 (&bf)[NB], auto ps) {
+      constexpr int PS = decltype(ps)::value;
 #pragma unroll
-      for (int u = 0; u < NB; ++u) bf[u] = wb[(kc * NB + u) * 64];
+      for (int u = 0; u < NB; ++u) {
+        const int v = (F16 && PS == 1 && (u & 1)) ? 6 + (u >> 1) : u;
+        bf[u] = wb[(kc * NBS + v) * 64];
+      }
     };
-    auto step = [&](int kc, const uint4 (&bc)[NB], uint4 (&bn)[NB]) {
-      load_b(kc + 1 < nkc ? kc + 1 : nkc - 1, bn);
+    auto step = [&](int kc, const uint4 (&bc)[NB], uint4 (&bn)[NB], auto ps) {
+      constexpr int PS = decltype(ps)::value;
+      constexpr int QB = PS == 2 ? 2 : 0, QE = PS == 1 ? 2 : 3;
+      load_b(kc + 1 < nkc ? kc + 1 : nkc - 1, bn, ps);
       const __bf16* b = sp + (kc & 1) * BUF;
 #pragma unroll
       for (int i = 0; i < RB; ++i) {
@@ -225,7 +250,7 @@ __global__ __launch_bounds__(threads_of(PATH), wg_per_cu(PATH)) void complex_lin
 #pragma unroll
           for (int u = 0; u < 6; ++u) af[u] = *reinterpret_cast<const f16x8*>(b + u * CTA + off);
 #pragma unroll
-          for (int q = 0; q < 3; ++q)
+          for (int q = QB; q < QE; ++q)
 #pragma unroll
             for (int op = 0; op < 3; ++op)
               T[op][i] = mfma_f16(af[2 * op + kF16A[q]], __builtin_bit_cast(f16x8, bc[2 * op + kF16B[q]]), T[op][i]);
@@ -243,67 +268,107 @@ __global__ __launch_bounds__(threads_of(PATH), wg_per_cu(PATH)) void complex_lin
       }
       // chunk kc + 1 into the other buffer (its last readers finished before the previous
       // barrier), then prefetch chunk kc + 2
-      store_chunk((kc & 1) ^ 1);
+      store_chunk((kc & 1) ^ 1, ps);
       load_chunk((kc + 2 < nkc ? kc + 2 : nkc - 1) * 16);
       __syncthreads();
     };
     uint4 b0[NB], b1[NB];
-    // F16: exact row scales from a pre-pass when the rows are short, else scales from the first
-    // chunk and, if any row of the tile ended outside the window, a second pass with exact ones
-    const bool prepass = F16 && nkc <= F16_PREPASS_CHUNKS;
-    __shared__ unsigned f16_redo[8];
-    for (int pass = 0; pass < (F16 ? 2 : 1); ++pass) {
-      if constexpr (F16) {
-        if (pass == 0 && !prepass) {
+    auto kloop = [&](auto ps) {
+      load_chunk(0);
+      store_chunk(0, ps);
+      load_chunk((nkc > 1 ? 1 : 0) * 16);
+      load_b(0, b0, ps);
+      __syncthreads();
+      // unrolled by two so that the fragment double buffer stays in fixed registers
+      for (int kc = 0; kc < nkc; kc += 2) {
+        step(kc, b0, b1, ps);
+        if (kc + 1 < nkc) step(kc + 1, b1, b0, ps);
+      }
+    };
+    if constexpr (!F16) {
+      kloop(std::integral_constant<int, 0>{});
+    } else {
+      // The passes of split_f16.h.  Pass 0: scales from the rows' first chunk (rows of at most
+      // F16_PREPASS_CHUNKS chunks skip it).  The tile is computed again at exact scales when a
+      // row's running maximum overflowed, or when one operand has a piece below the window while
+      // the other is not flat (the weight's columns carry both properties from
+      // fu_complex_weight_split, at their exact scales); the exact scan applies the same rule at
+      // its scales: pass 1 (one loop) or pass 2 (two loops).
+      __shared__ unsigned f16_any[8];
+      auto tile_bits = [&](unsigned v) {  // OR over the workgroup (every thread calls this)
+        unsigned w = 0;
+#pragma unroll
+        for (int bit = 0; bit < 5; ++bit) w |= (__ballot((v >> bit) & 1u) != 0 ? 1u : 0u) << bit;
+        __syncthreads();  // the previous call's readers are done with f16_any
+        if (lane == 0) f16_any[wave] = w;
+        __syncthreads();
+        unsigned any = 0;
+#pragma unroll
+        for (int w8 = 0; w8 < 8; ++w8) any |= f16_any[w8];
+        return any;
+      };
+      const float* cinv = reinterpret_cast<const float*>(W3 + complex_weight_f16_vectors(Nc, Kc));
+      const int* cflag = reinterpret_cast<const int*>(cinv + nbt * 32);
+      const int cf = nb_raw < nbt ? cflag[nb * 32 + fr] : 0;
+      const unsigned wbits = tile_bits(((cf & 1) ? F16_LOW_W : 0u) | ((cf & 2) ? F16_ROUGH_W : 0u));
+      // verdict bits of this thread's row (row-level over its four staging threads)
+      auto verdict_a = [&](float pmn, float pmx, bool low) {
+        pmn = fminf(pmn, __shfl_xor(pmn, 1, 64));
+        pmn = fminf(pmn, __shfl_xor(pmn, 2, 64));
+        return (low ? F16_LOW_A : 0u) | (f16_flat(pmn, row_max(pmx)) ? 0u : F16_ROUGH_A);
+      };
+      bool exact = nkc <= F16_PREPASS_CHUNKS;
+      // one call site of the pass-0/1 loop (pass 0, or pass 1 after an exact scan); pass 2 has
+      // its own two loops
+      for (int pass = 0; pass < 2; ++pass) {
+        if (!exact) {
           load_chunk(0);
           e = f16_exp_chunk(row_max(chunk_max()));
+          sc = pow2i(e);
         } else {
-          if (pass == 0) {
+          // exact scales from a pass over the rows, and the verdict at them
+          const float inf = __builtin_huge_valf();
+          float Rx = 0.0f, gmin = inf, zmin = inf;
 #pragma unroll 4
-            for (int kc = 0; kc < nkc; ++kc) {
-              load_chunk(kc * 16);
-              R = fmaxf(R, chunk_max());
-            }
-          } else {
+          for (int kc = 0; kc < nkc; ++kc) {
+            load_chunk(kc * 16);
+            const float mr = amax4(gr), mi = amax4(gi);
+            Rx = fmaxf(Rx, fmaxf(fmaxf(mr, mi), amax4(gr + gi)));
+            zmin = fminf(zmin, fminf(mr, mi));
+            gmin = fminf(gmin, fminf(mr > 0.0f ? mr : inf, mi > 0.0f ? mi : inf));
+          }
+          e = f16_exp_row(row_max(Rx));
+          sc = pow2i(e);
+          if (f16_needs_exact(tile_bits(verdict_a(zmin, Rx, f16_lossy(gmin * sc))) | wbits)) {
+            kloop(std::integral_constant<int, 1>{});
 #pragma unroll
             for (int p = 0; p < NT; ++p)
 #pragma unroll
               for (int i = 0; i < RB; ++i)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) T[p][i][r] = 0.0f;
+                for (int r = 0; r < 16; ++r) T[p][i][r] *= F16_LO_DOWN;
+            kloop(std::integral_constant<int, 2>{});
+            break;
           }
-          e = f16_exp_row(row_max(R));
         }
-        sc = pow2i(e);
-      }
-      load_chunk(0);
-      store_chunk(0);
-      load_chunk((nkc > 1 ? 1 : 0) * 16);
-      load_b(0, b0);
-      __syncthreads();
-      // unrolled by two so that the fragment double buffer stays in fixed registers
-      for (int kc = 0; kc < nkc; kc += 2) {
-        step(kc, b0, b1);
-        if (kc + 1 < nkc) step(kc + 1, b1, b0);
-      }
-      if constexpr (F16) {
-        if (pass == 1 || prepass) break;
+        kloop(std::integral_constant<int, 0>{});
+        if (exact) break;
         // every wave has left the loop (barrier in the last step): its buffers may be restaged
-        const bool wave_out = __ballot(f16_outside(row_max(R) * sc)) != 0;
-        if (lane == 0) f16_redo[wave] = wave_out;
-        __syncthreads();
-        unsigned any = 0;
+        const unsigned t = tile_bits(verdict_a(pmin, R * sc, lossy) |
+                                     (f16_outside(row_max(R) * sc) ? F16_OVERFLOW : 0u)) | wbits;
+        exact = (t & F16_OVERFLOW) != 0 || f16_needs_exact(t);
+        if (!exact) break;
 #pragma unroll
-        for (int w = 0; w < 8; ++w) any |= f16_redo[w];
-        if (!any) break;
+        for (int p = 0; p < NT; ++p)
+#pragma unroll
+          for (int i = 0; i < RB; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) T[p][i][r] = 0.0f;
       }
-    }
-    if constexpr (F16) {
       // undo the scales: row factor from the staging threads, column factor from the weight
       __shared__ float f16_rinv[CBM];
       if (sq == 0) f16_rinv[sr] = pow2i(-e);
       __syncthreads();
-      const float* cinv = reinterpret_cast<const float*>(W3 + complex_weight_f16_vectors(Nc, Kc));
       const float cs = cinv[nb * 32 + fr];
 #pragma unroll
       for (int i = 0; i < RB; ++i)
@@ -617,9 +682,12 @@ static int complex_launch(const float* A_r, const float* A_i, int64_t lda, const
 }
 
 // The unscale factor 2^-e(n) of every column of the 32-column blocks (1 past Nc): e(n) is the
-// exact scale (split_f16.h) of the column's largest magnitude over P, Q and P + Q.
+// exact scale (split_f16.h) of the column's largest magnitude over P, Q and P + Q.  flag[n]
+// bit 0 marks a column with a piece (8 consecutive k from a multiple of 8, as the fragments
+// hold them) of P or Q that is nonzero and below 2^-3 at that scale, bit 1 a column that is not
+// flat (a piece maximum, zero pieces included, below 2^-6 of the largest).
 __global__ void complex_weight_scale_kernel(const float* __restrict__ P, const float* __restrict__ Q, int64_t ldw,
-                                            int32_t Nc, int32_t Kc, float* __restrict__ cinv) {
+                                            int32_t Nc, int32_t Kc, float* __restrict__ cinv, int* __restrict__ flag) {
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
   if (n >= ((Nc + 31) / 32) * 32) return;
   float m = 0.0f;
@@ -628,7 +696,22 @@ __global__ void complex_weight_scale_kernel(const float* __restrict__ P, const f
       const float p = P[(int64_t)n * ldw + k], q = Q[(int64_t)n * ldw + k];
       m = fmaxf(m, fmaxf(fmaxf(fabsf(p), fabsf(q)), fabsf(p + q)));
     }
-  cinv[n] = pow2i(-f16_exp_row(m));
+  const int e = f16_exp_row(m);
+  cinv[n] = pow2i(-e);
+  bool low = false;
+  float pmin = m, pmax = 0.0f;
+  if (n < Nc)
+    for (int k0 = 0; k0 < Kc; k0 += 8) {
+      float mp = 0.0f, mq = 0.0f;
+      for (int k = k0; k < k0 + 8 && k < Kc; ++k) {
+        mp = fmaxf(mp, fabsf(P[(int64_t)n * ldw + k]));
+        mq = fmaxf(mq, fabsf(Q[(int64_t)n * ldw + k]));
+      }
+      low = low || f16_lossy(mp * pow2i(e)) || f16_lossy(mq * pow2i(e));
+      pmin = fminf(pmin, fminf(mp, mq));
+      pmax = fmaxf(pmax, fmaxf(mp, mq));
+    }
+  flag[n] = (low ? 1 : 0) | (f16_flat(pmin, pmax) ? 0 : 2);
 }
 
 // Builds the fragment-order planes of (P, Q, P + Q), bf16 and scaled fp16: one thread per
@@ -660,7 +743,7 @@ __global__ void complex_weight_split_kernel(const float* __restrict__ P, const f
          make_float4(p[4] + r[4], p[5] + r[5], p[6] + r[6], p[7] + r[7]), h, m, l);
   o[384] = h; o[448] = m; o[512] = l;
   // fp16 planes of the scaled column (the factor 2^-e(n) is an exact power of two)
-  uint4* f = W3 + complex_weight_split_vectors(Nc, Kc) + q * 6 * 64 + lane;
+  uint4* f = W3 + complex_weight_split_vectors(Nc, Kc) + q * 9 * 64 + lane;
   const float* cinv = reinterpret_cast<const float*>(W3 + complex_weight_split_vectors(Nc, Kc) +
                                                      complex_weight_f16_vectors(Nc, Kc));
   const float sc = 1.0f / cinv[n];
@@ -672,18 +755,23 @@ __global__ void complex_weight_split_kernel(const float* __restrict__ P, const f
     ss[u] = (p[u] + r[u]) * sc;
   }
   uint4 fh, fl;
-  split2h(make_float4(ps[0], ps[1], ps[2], ps[3]), make_float4(ps[4], ps[5], ps[6], ps[7]), fh, fl);
-  f[0] = fh; f[64] = fl;
-  split2h(make_float4(rs[0], rs[1], rs[2], rs[3]), make_float4(rs[4], rs[5], rs[6], rs[7]), fh, fl);
-  f[128] = fh; f[192] = fl;
-  split2h(make_float4(ss[0], ss[1], ss[2], ss[3]), make_float4(ss[4], ss[5], ss[6], ss[7]), fh, fl);
-  f[256] = fh; f[320] = fl;
+  const float* planes[3] = {ps, rs, ss};
+#pragma unroll
+  for (int op = 0; op < 3; ++op) {
+    const float* v = planes[op];
+    const float4 v0 = make_float4(v[0], v[1], v[2], v[3]), v1 = make_float4(v[4], v[5], v[6], v[7]);
+    split2h(v0, v1, fh, fl);
+    f[128 * op] = fh;
+    f[128 * op + 64] = fl;
+    split2h_up(v0, v1, fh, fl);
+    f[384 + 64 * op] = fl;
+  }
 }
 
 extern "C" int64_t fu_complex_weight_split_bytes(int32_t Nc, int32_t Kc) {
   if (Nc <= 0 || Kc <= 0) return set_error(FU_ERR_SHAPE, "fu_complex_weight_split_bytes: Nc=%d Kc=%d", Nc, Kc);
   return (complex_weight_split_vectors(Nc, Kc) + complex_weight_f16_vectors(Nc, Kc) +
-          complex_weight_scale_vectors(Nc)) * 16;
+          2 * complex_weight_scale_vectors(Nc)) * 16;
 }
 
 extern "C" int fu_complex_weight_split(const float* P, const float* Q, int64_t ldw, int32_t Nc, int32_t Kc, void* W3,
@@ -694,8 +782,9 @@ extern "C" int fu_complex_weight_split(const float* P, const float* Q, int64_t l
   if (!aligned16(W3)) return set_error(FU_ERR_ALIGN, "%s: W3 must be 16-byte aligned", who);
   uint4* w3 = static_cast<uint4*>(W3);
   float* cinv = reinterpret_cast<float*>(w3 + complex_weight_split_vectors(Nc, Kc) + complex_weight_f16_vectors(Nc, Kc));
+  int* flag = reinterpret_cast<int*>(cinv + (int64_t)((Nc + 31) / 32) * 32);
   hipLaunchKernelGGL(complex_weight_scale_kernel, dim3(cdiv((int64_t)((Nc + 31) / 32) * 32, 256)), dim3(256), 0,
-                     as_stream(stream), P, Q, ldw, Nc, Kc, cinv);
+                     as_stream(stream), P, Q, ldw, Nc, Kc, cinv, flag);
   const int64_t threads = complex_weight_split_vectors(Nc, Kc) / 9;
   hipLaunchKernelGGL(complex_weight_split_kernel, dim3(cdiv(threads, 256)), dim3(256), 0, as_stream(stream), P, Q, ldw,
                      Nc, Kc, w3);

@@ -11,6 +11,7 @@
 #include <cstdarg>
 #include <cstring>
 #include <algorithm>
+#include <type_traits>
 
 #include "../../include/flashuma.h"
 

@@ -304,21 +304,39 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
         }
       }
     };
-    // F16: the power-of-two scales of the staged rows (A row, second A row if TALL, W row)
+    // F16: the power-of-two scales of the staged rows (A row, second A row if TALL, W row), and
+    // the window tracking of pass 0 (split_f16.h) per staged row, on its scaled pieces of 8
+    // consecutive k: the largest and the smallest piece maximum (zero pieces included), and
+    // whether a nonzero piece fell below the window (lowA for A, lowW for W)
     float scA = 1.0f, scA2 = 1.0f, scW = 1.0f;
     int eA = 0, eA2 = 0, eW = 0;
-    auto store_chunk = [&](int buf) {
+    float pmaxA = 0.0f, pminA = __builtin_huge_valf(), pmaxA2 = 0.0f, pminA2 = __builtin_huge_valf();
+    float pmaxW = 0.0f, pminW = __builtin_huge_valf();
+    bool lowA = false, lowW = false;
+    // ps: the pass kind of the K loop (0: hi + lo planes, the window tracked; 1: hi and
+    // lo' = 2^11 lo planes of pass 2; 2: the hi planes of pass 2)
+    auto store_chunk = [&](int buf, auto ps) {
+      constexpr int PS = decltype(ps)::value;
       __bf16* b = sp + buf * NP * (PA + PW);
       if constexpr (F16) {
-        uint4 h, l;
-        split2h(scale4(ga[0], scA), scale4(ga[1], scA), h, l);
-        st_planes2(b, PA, soff, h, l);
-        if constexpr (TALL) {
-          split2h(scale4(ga2[0], scA2), scale4(ga2[1], scA2), h, l);
-          st_planes2(b, PA, plane_off(128 + sr, sh), h, l);
-        }
-        split2h(scale4(gw[0], scW), scale4(gw[1], scW), h, l);
-        st_planes2(b + 2 * PA, PW, soff, h, l);
+        auto put = [&](const float4& x0, const float4& x1, float s, __bf16* p0, int plane, int off, float& pmax,
+                       float& pmin, bool& low) {
+          const float4 v0 = scale4(x0, s), v1 = scale4(x1, s);
+          uint4 h, l;
+          if constexpr (PS == 0) {
+            const float m = fmaxf(amax4(v0), amax4(v1));
+            pmax = fmaxf(pmax, m);
+            pmin = fminf(pmin, m);
+            low |= f16_lossy(m);
+            split2h(v0, v1, h, l);
+          } else {
+            split2h_up(v0, v1, h, l);
+          }
+          st_planes2(p0, plane, off, h, l);
+        };
+        put(ga[0], ga[1], scA, b, PA, soff, pmaxA, pminA, lowA);
+        if constexpr (TALL) put(ga2[0], ga2[1], scA2, b, PA, plane_off(128 + sr, sh), pmaxA2, pminA2, lowA);
+        put(gw[0], gw[1], scW, b + 2 * PA, PW, soff, pmaxW, pminW, lowW);
       } else {
         uint4 h, m, l;
         split3(ga[0], ga[1], h, m, l);
@@ -331,66 +349,17 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
         st_planes(b + 3 * PA, PW, soff, h, m, l);
       }
     };
-    // the larger magnitude of this thread's and its partner's half of a staged row
+    // the larger (smaller) value of this thread's and its partner's half of a staged row
     auto row_max = [&](float v) { return fmaxf(v, __shfl_xor(v, 1, 64)); };
+    auto row_min = [&](float v) { return fminf(v, __shfl_xor(v, 1, 64)); };
     const int nk = (K + GBK - 1) / GBK;
-    // F16 scales: from the rows' first chunk; exact (a pass over the whole rows) when the rows
-    // are short, when a row's first chunk is zero (nothing to scale from), and in the second
-    // pass, which runs when a row or column overflowed fp16 with the first-chunk scale (the
-    // overflowed piece made its accumulators non-finite).  With a nonzero first chunk the
-    // row's largest magnitude is at least 2^6 after scaling, so without overflow the row is
-    // inside the window.
-    const bool short_k = F16 && nk <= F16_PREPASS_CHUNKS;
-    __shared__ unsigned f16_any[4];
-    auto tile_any = [&](bool v) {  // v on any thread of the workgroup (every thread calls this)
-      const bool w = __ballot(v) != 0;
-      if (lane == 0) f16_any[wave] = w;
-      __syncthreads();
-      return (f16_any[0] | f16_any[1] | f16_any[2] | f16_any[3]) != 0;
-    };
-    auto exact_scales = [&]() {
-      float RA = 0.0f, RA2 = 0.0f, RW = 0.0f;
-#pragma unroll 4
-      for (int kc = 0; kc < nk; ++kc) {
-        load_chunk(kc * GBK);
-        RA = fmaxf(RA, fmaxf(amax4(ga[0]), amax4(ga[1])));
-        if constexpr (TALL) RA2 = fmaxf(RA2, fmaxf(amax4(ga2[0]), amax4(ga2[1])));
-        RW = fmaxf(RW, fmaxf(amax4(gw[0]), amax4(gw[1])));
-      }
-      eA = f16_exp_row(row_max(RA));
-      if constexpr (TALL) eA2 = f16_exp_row(row_max(RA2));
-      eW = f16_exp_row(row_max(RW));
-    };
-    for (int pass = 0; pass < (F16 ? 2 : 1); ++pass) {
-      bool exact = short_k || pass == 1;
-      if constexpr (F16) {
-        if (!exact) {
-          load_chunk(0);
-          const float mA = row_max(fmaxf(amax4(ga[0]), amax4(ga[1])));
-          const float mA2 = TALL ? row_max(fmaxf(amax4(ga2[0]), amax4(ga2[1]))) : 1.0f;
-          const float mW = row_max(fmaxf(amax4(gw[0]), amax4(gw[1])));
-          eA = f16_exp_chunk(mA);
-          if constexpr (TALL) eA2 = f16_exp_chunk(mA2);
-          eW = f16_exp_chunk(mW);
-          exact = tile_any(mA == 0.0f || mA2 == 0.0f || mW == 0.0f);
-        }
-        if (exact) {
-          if (pass == 1) {
-#pragma unroll
-            for (int i = 0; i < RB; ++i)
-#pragma unroll
-              for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-          }
-          exact_scales();
-        }
-        scA = pow2i(eA);
-        scA2 = pow2i(eA2);
-        scW = pow2i(eW);
-      }
+    // One K loop.  F16 products per pass kind: 0 lo*hi + hi*lo + hi*hi, 1 lo'*hi + hi*lo',
+    // 2 hi*hi.
+    auto kloop = [&](auto ps) {
+      constexpr int PS = decltype(ps)::value;
+      constexpr int QB = PS == 2 ? 2 : 0, QE = PS == 1 ? 2 : 3;
       load_chunk(0);
-      store_chunk(0);
+      store_chunk(0, ps);
       load_chunk((nk > 1 ? 1 : 0) * GBK);
       __syncthreads();
       for (int kc = 0; kc < nk; ++kc) {
@@ -404,7 +373,7 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
             f16x8 aq[2];
             ld_planes2(b, PA, plane_off(wr + 32 * i + fr, fh), aq);
 #pragma unroll
-            for (int q = 0; q < 3; ++q)
+            for (int q = QB; q < QE; ++q)
 #pragma unroll
               for (int j = 0; j < 2; ++j) acc[i][j] = mfma_f16(aq[kF16A[q]], bq[j][kF16B[q]], acc[i][j]);
           }
@@ -424,12 +393,106 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
         }
         // chunk kc + 1 (loaded during the previous iteration) into the other buffer, whose last
         // readers finished before the previous barrier; then prefetch chunk kc + 2
-        store_chunk((kc & 1) ^ 1);
+        store_chunk((kc & 1) ^ 1, ps);
         load_chunk((kc + 2 < nk ? kc + 2 : nk - 1) * GBK);
         __syncthreads();
       }
-      if constexpr (F16) {
-        if (exact) break;  // exact scales cannot overflow (non-finite inputs stay non-finite)
+    };
+    if constexpr (!F16) {
+      kloop(std::integral_constant<int, 0>{});
+    } else {
+      // The passes of split_f16.h.  Pass 0 takes the scales from the rows' first chunk.  Its
+      // tile is computed again at exact scales when an fp16 piece overflowed (its accumulators
+      // are then non-finite) or when one operand has a piece below the window while the other
+      // is not flat; exact scales come from a pass over the rows, which also applies the same
+      // rule at those scales: pass 1 (one K loop) or pass 2 (two loops).
+      const bool short_k = nk <= F16_PREPASS_CHUNKS;
+      __shared__ unsigned f16_any[4];
+      // OR over the workgroup of each thread's verdict bits (every thread calls this)
+      auto tile_bits = [&](unsigned v) {
+        unsigned w = 0;
+#pragma unroll
+        for (int bit = 0; bit < 5; ++bit) w |= (__ballot((v >> bit) & 1u) != 0 ? 1u : 0u) << bit;
+        __syncthreads();  // the previous call's readers are done with f16_any
+        if (lane == 0) f16_any[wave] = w;
+        __syncthreads();
+        return f16_any[0] | f16_any[1] | f16_any[2] | f16_any[3];
+      };
+      // a thread's verdict bits for its rows (row-level max / min over the two staging threads)
+      auto verdict = [&](float pa, float ga, float pa2, float ga2, float pw, float gw, bool la, bool lw) {
+        bool flatA = f16_flat(row_min(ga), row_max(pa));
+        if constexpr (TALL) flatA = flatA && f16_flat(row_min(ga2), row_max(pa2));
+        const bool flatW = f16_flat(row_min(gw), row_max(pw));
+        return (la ? F16_LOW_A : 0u) | (flatA ? 0u : F16_ROUGH_A) | (lw ? F16_LOW_W : 0u) | (flatW ? 0u : F16_ROUGH_W);
+      };
+      // exact scales, and the verdict bits at them
+      auto exact_scales = [&]() {
+        const float inf = __builtin_huge_valf();
+        float RA = 0.0f, RA2 = 0.0f, RW = 0.0f, gA = inf, gA2 = inf, gW = inf, zA = inf, zA2 = inf, zW = inf;
+#pragma unroll 4
+        for (int kc = 0; kc < nk; ++kc) {
+          load_chunk(kc * GBK);
+          const float mA = fmaxf(amax4(ga[0]), amax4(ga[1])), mW = fmaxf(amax4(gw[0]), amax4(gw[1]));
+          RA = fmaxf(RA, mA);
+          RW = fmaxf(RW, mW);
+          zA = fminf(zA, mA);
+          zW = fminf(zW, mW);
+          gA = fminf(gA, mA > 0.0f ? mA : inf);
+          gW = fminf(gW, mW > 0.0f ? mW : inf);
+          if constexpr (TALL) {
+            const float mA2 = fmaxf(amax4(ga2[0]), amax4(ga2[1]));
+            RA2 = fmaxf(RA2, mA2);
+            zA2 = fminf(zA2, mA2);
+            gA2 = fminf(gA2, mA2 > 0.0f ? mA2 : inf);
+          }
+        }
+        eA = f16_exp_row(row_max(RA));
+        eW = f16_exp_row(row_max(RW));
+        bool la = f16_lossy(gA * pow2i(eA));
+        if constexpr (TALL) {
+          eA2 = f16_exp_row(row_max(RA2));
+          la = la || f16_lossy(gA2 * pow2i(eA2));
+        }
+        return verdict(RA, zA, RA2, zA2, RW, zW, la, f16_lossy(gW * pow2i(eW)));
+      };
+      auto set_scales = [&]() {
+        scA = pow2i(eA);
+        scA2 = pow2i(eA2);
+        scW = pow2i(eW);
+      };
+      // one call site of the pass-0/1 loop (pass 0, or pass 1 after an exact scan); pass 2 has
+      // its own two loops
+      bool exact = short_k;
+      for (int pass = 0; pass < 2; ++pass) {
+        if (!exact) {
+          load_chunk(0);
+          const float mA = row_max(fmaxf(amax4(ga[0]), amax4(ga[1])));
+          const float mA2 = TALL ? row_max(fmaxf(amax4(ga2[0]), amax4(ga2[1]))) : 1.0f;
+          const float mW = row_max(fmaxf(amax4(gw[0]), amax4(gw[1])));
+          eA = f16_exp_chunk(mA);
+          if constexpr (TALL) eA2 = f16_exp_chunk(mA2);
+          eW = f16_exp_chunk(mW);
+          exact = tile_bits(mA == 0.0f || mA2 == 0.0f || mW == 0.0f) != 0;
+        }
+        if (exact) {
+          const bool two = f16_needs_exact(tile_bits(exact_scales()));
+          set_scales();
+          if (two) {
+            kloop(std::integral_constant<int, 1>{});
+#pragma unroll
+            for (int i = 0; i < RB; ++i)
+#pragma unroll
+              for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] *= F16_LO_DOWN;
+            kloop(std::integral_constant<int, 2>{});
+            break;
+          }
+        } else {
+          set_scales();
+        }
+        kloop(std::integral_constant<int, 0>{});
+        if (exact) break;
         // every wave has left the loop (barrier above): its buffers may be restaged
         bool bad = false;
 #pragma unroll
@@ -438,7 +501,16 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
           for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) bad = bad || !__builtin_isfinite(acc[i][j][r]);
-        if (!tile_any(bad)) break;
+        const unsigned t = tile_bits(verdict(pmaxA, pminA, pmaxA2, pminA2, pmaxW, pminW, lowA, lowW) |
+                                     (bad ? F16_OVERFLOW : 0u));
+        exact = (t & F16_OVERFLOW) != 0 || f16_needs_exact(t);
+        if (!exact) break;
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
       }
     }
     if constexpr (F16) {

@@ -11,19 +11,32 @@
 // with each partial product exact in the fp32 accumulator and the dropped lo_a lo_b of relative
 // size 2^-22.  The accumulated output is multiplied by 2^-ea and 2^-eb afterwards (exact).
 //
-// The scale of a row keeps its largest magnitude R inside the window [2^-3, 2^15): below 2^15 hi
-// cannot overflow (the largest fp16 is 65504); from 2^-3 up the row's largest elements keep all 22
-// bits, and every smaller element's error (at most 2^-25 after scaling) stays below 2^-22 R.  The
-// kernels pick the scale one of two ways:
-//  * exact: R from a pre-pass over the row, e = 14 - floor(log2 R) (R 2^e in [2^14, 2^15));
-//  * from the first chunk: the maximum m of the row's first 16 elements is mapped to [2^6, 2^7).
-//    That leaves 256x of headroom above the first chunk and keeps elements down to 2^-9 m at
-//    full precision; the row's largest magnitude is then at least 2^6 after scaling, so only
-//    overflow can take it out of the window.  A tile with such a row or column is computed
-//    again with exact scales.  The complex layer finds those rows from the running maximum kept
-//    while the chunks are staged; the real GEMM from its accumulators (an overflowed fp16 piece
-//    makes its row's or column's outputs non-finite) and sends a tile that has a row with a
-//    zero first chunk (nothing to scale from) to the exact scales from the start.
+// Window.  The kernels stage a row in pieces (8 consecutive k of a row in the real GEMM, 4 of
+// each of a_r and a_i in the complex layer).  A piece is inside the window at a scale when its
+// largest scaled magnitude is at or above 2^-3 (or it is zero) and no piece overflowed (largest
+// fp16 65504).  Inside it every element keeps 22 bits relative to the largest element of its
+// piece: |error(x)| <= 2^-22 max(|x|, max |piece|) 2^-e.  A piece below the window has the
+// absolute error 2^-25 2^-e of the scale instead, which matters only when it meets elements of
+// the other operand that are large next to those its row's large pieces meet.  So a row is
+// called flat when its smallest piece maximum (zero pieces included) is at least 2^-6 of its
+// largest, and a tile is accepted from a pass unless an operand has a piece below the window
+// while the other operand has a row that is not flat (or a piece overflowed).  The passes:
+//  0. scales from the first chunk: the maximum m of the row's first 16 elements is mapped to
+//     [2^6, 2^7) (256x of headroom above it), with no pass over the data; the pieces are
+//     tracked as they are staged;
+//  1. exact scales, from a pass over the rows: e = 14 - floor(log2 R), R the row's largest
+//     magnitude (R 2^e in [2^14, 2^15)), so pieces down to 2^-17 R stay in the window.  Pass 0
+//     is skipped for rows of up to F16_PREPASS_CHUNKS chunks and for a tile with a zero first
+//     chunk (nothing to scale from);
+//  2. for a tile that pass 1 cannot hold (a piece below 2^-17 of its row's maximum against a
+//     rough other operand): exact scales, and the K loop runs twice, first with the products
+//     hi_a lo'_b + lo'_a hi_b of the residuals scaled up, lo' = fp16((x 2^e - hi) 2^11),
+//     accumulated, then multiplied by 2^-11 (exact), then hi_a hi_b added.  lo' is normal down
+//     to |x 2^e| ~ 2^-13, so every element down to 2^-27 R keeps 22 bits:
+//     |error(x)| <= 2^-22 |x| + 2^-50 R.
+// The rules work on pieces, not elements: an element far below the largest one of its own
+// piece that meets a large element of the other operand is not seen.  Rows whose magnitude
+// changes by blocks or smoothly along K are covered.
 // A row of zeros keeps e = 0.
 #pragma once
 #include "split_bf16.h"
@@ -46,10 +59,31 @@ __device__ __forceinline__ void split2h(const float4& a, const float4& b, uint4&
   }
 }
 
+// As split2h, with the lo pieces scaled by 2^11 (pass 2 of the window rules above: the
+// residual x - hi is exact, and so is its product with a power of two).
+__device__ __forceinline__ void split2h_up(const float4& a, const float4& b, uint4& H, uint4& L) {
+  const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const float2v v = {x[2 * t], x[2 * t + 1]};
+    const f16x2 h = __builtin_convertvector(v, f16x2);
+    const float2v r = (v - __builtin_convertvector(h, float2v)) * 2048.0f;
+    (&H.x)[t] = __builtin_bit_cast(unsigned, h);
+    (&L.x)[t] = __builtin_bit_cast(unsigned, __builtin_convertvector(r, f16x2));
+  }
+}
+
 // Split 4 floats (already scaled) into 4 fp16 of each plane.
 __device__ __forceinline__ void split2h_4(const float4& a, uint2& H, uint2& L) {
   uint4 h, l;
   split2h(a, a, h, l);
+  H = make_uint2(h.x, h.y);
+  L = make_uint2(l.x, l.y);
+}
+
+__device__ __forceinline__ void split2h_4_up(const float4& a, uint2& H, uint2& L) {
+  uint4 h, l;
+  split2h_up(a, a, h, l);
   H = make_uint2(h.x, h.y);
   L = make_uint2(l.x, l.y);
 }
@@ -91,6 +125,23 @@ __device__ __forceinline__ int f16_exp_row(float R) { return f16_exp_of(R, 14); 
 __device__ __forceinline__ int f16_exp_chunk(float m) { return f16_exp_of(m, 6); }
 // a row whose scaled largest magnitude Rs left the window (Rs = 0: a row of zeros, in the window)
 __device__ __forceinline__ bool f16_outside(float Rs) { return !(Rs < 32768.0f) || (Rs > 0.0f && Rs < 0.125f); }
+
+// A staged piece whose largest scaled magnitude m (>= 0) is nonzero and below 2^-3: its lo
+// pieces are fp16 subnormals, so the piece is outside the window (m = 0: zeros, exact).
+__device__ __forceinline__ bool f16_lossy(float m) { return (__float_as_uint(m) - 1u) < 0x3dffffffu; }
+// A row is flat when its smallest piece maximum (zero pieces included) is at least 2^-6 of its
+// largest (a row of zeros is flat).
+__device__ __forceinline__ bool f16_flat(float pmin, float pmax) { return pmin >= pmax * 0.015625f; }
+// Window verdict bits of a tile (OR over its rows): a piece of A (W) below the window; a row of A
+// (W) that is not flat; an overflowed piece.
+constexpr unsigned F16_LOW_A = 1u, F16_ROUGH_A = 2u, F16_LOW_W = 4u, F16_ROUGH_W = 8u, F16_OVERFLOW = 16u;
+// Pieces below the window count only against a rough other operand: a flat operand's elements
+// that meet them are within 2^6 of those that meet its large pieces.
+__device__ __forceinline__ bool f16_needs_exact(unsigned t) {
+  return ((t & F16_LOW_A) && (t & F16_ROUGH_W)) || ((t & F16_LOW_W) && (t & F16_ROUGH_A));
+}
+// The residual factor of pass 2 and its inverse.
+constexpr float F16_LO_UP = 2048.0f, F16_LO_DOWN = 1.0f / 2048.0f;
 
 __device__ __forceinline__ float amax4(const float4& v) {
   return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));

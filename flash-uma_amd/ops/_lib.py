@@ -22,6 +22,9 @@ I32 = ctypes.c_int32
 F32 = ctypes.c_float
 SZ_P = ctypes.POINTER(ctypes.c_size_t)
 
+# fu_version() of the library these signatures describe (major*10000 + minor*100 + patch).
+ABI_VERSION = 300
+
 # Argument types of every exported entry point, in header order.
 SIGNATURES: dict[str, list] = {
     "fu_version": [],
@@ -108,6 +111,10 @@ def load() -> ctypes.CDLL:
             f"{LIB_PATH} is missing: build it first (python flash-uma_amd/build_lib.py or "
             "__graft_entry__.build()); there is no non-HIP fallback")
     lib = ctypes.CDLL(str(LIB_PATH))
+    lib.fu_version.restype = ctypes.c_int
+    if lib.fu_version() != ABI_VERSION:
+        raise FlashUMAError(f"{LIB_PATH} has ABI version {lib.fu_version()}, these bindings expect "
+                            f"{ABI_VERSION}: rebuild the library")
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes

@@ -292,16 +292,26 @@ class BalanceChannels(torch.autograd.Function):
 def balance_channels_batched(emb, target, natoms, batch, start_idx: int, end_idx: int, target_offset: float = 0.0,
                              sys_ptr=None):
     """FAIRChem's balance_channels_batched with its argument meaning (emb (N, K, C), target
-    (S,) per-system charge or spin, natoms (S,) atoms per system, batch (N,) sorted
-    ascending).  The divisor n_s is the length of system s's batch segment, which equals
-    natoms[s] for consistent inputs.  sys_ptr: the system segments of batch when already
-    known (system_ptr)."""
+    (S,) per-system charge or spin, natoms (S,) atoms per system, batch (N,) system of each
+    atom).  The divisor n_s is the number of atoms of system s in batch, which equals
+    natoms[s] for consistent inputs.  The kernel works on system segments of a batch sorted
+    ascending; an unsorted batch (which FAIRChem's index_add form accepts) is balanced
+    through a stable sort of the atoms and the result put back in the input order.
+    sys_ptr: the system segments of a batch already known to be sorted (system_ptr); it is
+    then trusted without a check, as the model does with its Morton-ordered systems."""
     if target is None:
         raise ValueError("balance_channels_batched: the backbone balances channels but no per-system target "
                          "(charge or spin) was given")
     S = int(target.numel())
     if natoms is not None and int(natoms.numel()) != S:
         raise ValueError(f"balance_channels_batched: {int(natoms.numel())} systems in natoms, {S} targets")
+    args = (int(start_idx), int(end_idx), float(target_offset))
     if sys_ptr is None:
+        batch = _lib.require(batch, torch.int64, "batch")
+        if batch.numel() > 1 and bool((batch[1:] < batch[:-1]).any()):   # one host sync, public path only
+            perm = torch.sort(batch, stable=True).indices
+            sb = batch.index_select(0, perm)
+            out = BalanceChannels.apply(emb.index_select(0, perm), target, sb, system_ptr(sb, S), *args)
+            return out.index_select(0, torch.argsort(perm))
         sys_ptr = system_ptr(batch, S)
-    return BalanceChannels.apply(emb, target, batch, sys_ptr, int(start_idx), int(end_idx), float(target_offset))
+    return BalanceChannels.apply(emb, target, batch, sys_ptr, *args)

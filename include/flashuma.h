@@ -42,7 +42,12 @@ extern "C" {
 #define FU_ERR_NULL (-5)        /* a required pointer is NULL */
 #define FU_ERR_WORKSPACE (-6)   /* the workspace is too small */
 
-/* Library version (major*10000 + minor*100 + patch). */
+/* Library version (major*10000 + minor*100 + patch): 300 (0.3.0) for the signatures in this
+ * header.  0.2.0 added the int32 `accumulate` argument (before the stream) of fu_gather_bwd,
+ * fu_scatter_bwd, fu_init_scatter_bwd, their _lmax forms and fu_complex_linear_gate(_bwd), and
+ * dropped one pointer/stride pair of fu_linear_gate_bwd; 0.3.0 changed the layout and size of
+ * the fu_complex_weight_split buffer (fu_complex_weight_split_bytes).  A caller built against
+ * another version must not call into this library. */
 int fu_version(void);
 
 /* Message of the last error returned on the calling host thread ("" if none). */
@@ -301,8 +306,12 @@ int fu_complex_linear(const float* A_r, const float* A_i, int64_t lda, const flo
  * stride ldw; W3 receives the exact three-way bf16 splits of P, Q and P + Q in MFMA-fragment
  * order ([32-column block][16-k chunk][P, Q, P + Q][hi, mid, lo][64 lanes] x 16 bytes, zero
  * padded to Nc = 32 n, Kc = 16 k), then the two-way fp16 splits of the same three operands with
- * each column n scaled by a power of two 2^e(n) (same order, [hi, lo]), then the factors
- * 2^-e(n) (one float per padded column): fu_complex_weight_split_bytes(Nc, Kc) bytes, 16-byte
+ * each column n scaled by a power of two 2^e(n) ([block][chunk][P hi, P lo, Q hi, Q lo, S hi,
+ * S lo, P lo', Q lo', S lo'][64 lanes], lo' = 2^11 lo for the two-loop pass of the fp16 mode),
+ * then the factors 2^-e(n) (one float per padded column), then one int32 per padded column:
+ * bit 0 when 8 consecutive k of P or Q in that column are below the fp16 window at its scale,
+ * bit 1 when the column is not flat (a piece of 8 k more than 2^6 below its largest; the fp16
+ * mode's pass rules read both): fu_complex_weight_split_bytes(Nc, Kc) bytes, 16-byte
  * aligned, valid in every matrix-core mode.  The bytes query returns a negative FU_ERR_* for Nc
  * or Kc <= 0. */
 int64_t fu_complex_weight_split_bytes(int32_t Nc, int32_t Kc);

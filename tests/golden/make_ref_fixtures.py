@@ -47,6 +47,8 @@ CHOICE = {"BLOCK_E": 16, "BLOCK_C": 16, "BLOCK_NB": 16}
 
 
 def _load_reference(path: str):
+    # nothing may be written into the read-only reference tree (no __pycache__ there)
+    sys.dont_write_bytecode = True
     sys.path.insert(0, path)
     torch.cuda.synchronize = lambda *a, **k: None
     import triton

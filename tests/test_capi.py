@@ -26,7 +26,7 @@ def test_library_exports_all_symbols():
     lib = _lib.load()
     for name in header_symbols():
         assert hasattr(lib, name), f"{name} not exported"
-    assert lib.fu_version() >= 100
+    assert lib.fu_version() == _lib.ABI_VERSION
 
 
 def _status(name, *args):
@@ -199,12 +199,13 @@ def test_lmax_entry_points_reject_bad_arguments():
 
 
 def test_complex_weight_split_arguments():
-    # one (32-column, 16-k) block holds 9 bf16 and 6 fp16 planes x 64 lanes x 16 B, and each
-    # 32-column block 32 column factors (128 B); sizes round up to whole blocks
+    # one (32-column, 16-k) block holds 9 bf16 and 9 fp16 planes (hi, lo, lo' of P, Q, P + Q)
+    # x 64 lanes x 16 B, and each 32-column block 32 column factors and 32 column flags
+    # (2 x 128 B); sizes round up to whole blocks
     st, _ = _status("fu_complex_weight_split_bytes", 32, 16)
-    assert st == (9 + 6) * 64 * 16 + 128
+    assert st == (9 + 9) * 64 * 16 + 2 * 128
     st, _ = _status("fu_complex_weight_split_bytes", 33, 17)
-    assert st == 4 * (9 + 6) * 64 * 16 + 2 * 128
+    assert st == 4 * (9 + 9) * 64 * 16 + 2 * 2 * 128
     st, _ = _status("fu_complex_weight_split_bytes", 0, 16)
     assert st == -1
     st, _ = _status("fu_complex_weight_split", None, None, 16, 32, 16, None, None)

@@ -333,6 +333,102 @@ def test_f16_complex_dynamic_range(cuda, M, Kc, Nc):
     assert worst[_lib.MATMUL_SPLIT_F16] <= 1.5 * worst[_lib.MATMUL_FP32] + 1e-7, worst
 
 
+def _ramp(K, T, orient):
+    return torch.linspace(-T, T, K, dtype=torch.float64) * orient
+
+
+@pytest.mark.parametrize("M", [70000, 3000], ids=["tall", "rows128"])
+@pytest.mark.parametrize("T", [4, 8, 12])
+@pytest.mark.parametrize("orient", [1, -1], ids=["max_last", "max_first"])
+def test_f16_split_anticorrelated_range(cuda, M, T, orient):
+    """Rows of A and W whose magnitudes ramp against each other along K, x ~ 2^t N(0,1) and
+    w ~ 2^-t N(0,1) with t over [-T, T] (row maximum in the first chunk or in the last), so
+    every product is of the same size and the small elements of each row matter as much as
+    the large ones.  Spreads of 2^8 fit the first-chunk scales, 2^16 need the exact-scale pass
+    and 2^24 the two-loop pass of the split (split_f16.h).  Bar: every row's error against
+    float64, relative to that row's norm, within 1.5x the fp32 MFMA's worst row plus 1e-7, on
+    tall (M >= 65,536) and 128-row tiles."""
+    from ops import _lib
+    *_, linear, _ = _ops()
+    N, K = 256, 768
+    g = torch.Generator().manual_seed(M + 31 * T + orient)
+    t = _ramp(K, T, orient)
+    x = (torch.randn(M, K, generator=g, dtype=torch.float64) * torch.exp2(t)).float().to(cuda)
+    W = (torch.randn(N, K, generator=g, dtype=torch.float64) * torch.exp2(-t) / K ** 0.5).float().to(cuda)
+    ref = x.double() @ W.double().T
+    rn = ref.norm(dim=1).clamp_min(1e-300)
+    worst = {}
+    for mode in (_lib.MATMUL_SPLIT_F16, _lib.MATMUL_FP32):
+        with _lib.matmul_mode(mode):
+            y = linear.gemm(x, W)
+        assert torch.isfinite(y).all(), mode
+        worst[mode] = ((y.double() - ref).norm(dim=1) / rn).max().item()
+    print(f"anticorrelated +-2^{T} orient {orient} M {M}: worst row f16 {worst[_lib.MATMUL_SPLIT_F16]:.2e}, "
+          f"fp32 MFMA {worst[_lib.MATMUL_FP32]:.2e}")
+    assert worst[_lib.MATMUL_SPLIT_F16] <= 1.5 * worst[_lib.MATMUL_FP32] + 1e-7, worst
+
+
+@pytest.mark.parametrize("Kc,Nc", [(512, 256), (64, 128)], ids=["long", "prepass"])
+@pytest.mark.parametrize("T", [4, 8, 12])
+@pytest.mark.parametrize("orient", [1, -1], ids=["max_last", "max_first"])
+def test_f16_complex_anticorrelated_range(cuda, Kc, Nc, T, orient):
+    """The pre-split complex layer on the anti-correlated ramps of
+    test_f16_split_anticorrelated_range: x_r, x_i ~ 2^t N(0,1) and R, I ~ 2^-t N(0,1) along Kc.
+    The weight's columns are flagged at split time (a piece below the window at the column's
+    exact scale) and their tiles run the two-loop pass.  Same bar, on the long (Kc = 512) and
+    pre-pass (Kc = 64) forms."""
+    from ops import _lib
+    from ops.linear import complex_gemm, complex_weight_split
+    M = 20000
+    g = torch.Generator().manual_seed(Kc + 31 * T + orient)
+    t = _ramp(Kc, T, orient)
+    x = (torch.randn(M, 2 * Kc, generator=g, dtype=torch.float64) * torch.exp2(t.repeat(2))).float()
+    Rw = (torch.randn(Nc, Kc, generator=g, dtype=torch.float64) * torch.exp2(-t) / Kc ** 0.5).float()
+    Iw = (torch.randn(Nc, Kc, generator=g, dtype=torch.float64) * torch.exp2(-t) / Kc ** 0.5).float()
+    x, Rw, Iw = x.to(cuda), Rw.to(cuda), Iw.to(cuda)
+    ref = x.double() @ R.pack_so2(Rw.double(), Iw.double()).T
+    rn = ref.norm(dim=1).clamp_min(1e-300)
+    W3 = complex_weight_split(Rw, Iw)
+    worst = {}
+    for mode in (_lib.MATMUL_SPLIT_F16, _lib.MATMUL_FP32):
+        with _lib.matmul_mode(mode):
+            y = complex_gemm(x, Rw, Iw, W3)
+        assert torch.isfinite(y).all(), mode
+        worst[mode] = ((y.double() - ref).norm(dim=1) / rn).max().item()
+    print(f"complex anticorrelated +-2^{T} orient {orient} Kc {Kc}: worst row f16 "
+          f"{worst[_lib.MATMUL_SPLIT_F16]:.2e}, fp32 MFMA {worst[_lib.MATMUL_FP32]:.2e}")
+    assert worst[_lib.MATMUL_SPLIT_F16] <= 1.5 * worst[_lib.MATMUL_FP32] + 1e-7, worst
+
+
+@pytest.mark.parametrize("M", [70000, 3000], ids=["tall", "rows128"])
+@pytest.mark.parametrize("s", [16, 20, 26])
+def test_f16_split_small_entries_elementwise(cuda, M, s):
+    """Outputs made only of a row's small entries: each row's first chunk is O(1) and meets
+    zero weights, the rest of the row is 2^-s smaller and meets O(1) weights.  Error is taken
+    per element against the componentwise scale sum_k |x_ik| |w_jk| of that element (the
+    large first chunk does not enter it).  Bar: the worst element within 1.5x the fp32 MFMA's
+    plus 2^-22."""
+    from ops import _lib
+    *_, linear, _ = _ops()
+    N, K = 256, 768
+    g = torch.Generator().manual_seed(M + s)
+    x = torch.randn(M, K, generator=g, dtype=torch.float64)
+    x[:, 16:] *= 2.0 ** -s
+    W = torch.randn(N, K, generator=g, dtype=torch.float64) / K ** 0.5
+    W[:, :16] = 0.0
+    x, W = x.float().to(cuda), W.float().to(cuda)
+    ref = x.double() @ W.double().T
+    scale = (x.double().abs() @ W.double().abs().T).clamp_min(1e-300)
+    worst = {}
+    for mode in (_lib.MATMUL_SPLIT_F16, _lib.MATMUL_FP32):
+        with _lib.matmul_mode(mode):
+            y = linear.gemm(x, W)
+        worst[mode] = ((y.double() - ref).abs() / scale).max().item()
+    print(f"small entries 2^-{s} M {M}: worst element f16 {worst[_lib.MATMUL_SPLIT_F16]:.2e}, "
+          f"fp32 MFMA {worst[_lib.MATMUL_FP32]:.2e}")
+    assert worst[_lib.MATMUL_SPLIT_F16] <= 1.5 * worst[_lib.MATMUL_FP32] + 2.0 ** -22, worst
+
+
 def test_matmul_mode_switch(cuda):
     from ops import _lib
     prev = _lib.get_matmul_mode()
@@ -687,14 +783,19 @@ def test_edge_shifts_and_permutation(cuda):
     assert torch.equal(gs.cpu(), ref_g)
 
 
-@pytest.mark.parametrize("start,end,offset", [(0, 16, 0.0), (5, 13, 1.0), (120, 128, 1.0)])
-def test_balance_channels(cuda, start, end, offset):
+@pytest.mark.parametrize("start,end,offset,shuffled", [(0, 16, 0.0, False), (5, 13, 1.0, False),
+                                                       (120, 128, 1.0, False), (5, 13, 1.0, True)])
+def test_balance_channels(cuda, start, end, offset, shuffled):
     """fu_balance_channels against the float64 restatement (forward and input gradient) on
-    three systems of different sizes, and the defining property on the GPU output."""
+    three systems of different sizes, and the defining property on the GPU output; shuffled:
+    the atoms of the systems interleaved (an unsorted batch, which the public function sorts
+    and puts back)."""
     from ops.node import balance_channels_batched
     g = torch.Generator().manual_seed(start)
     sizes = [37, 5, 130]
     batch = torch.repeat_interleave(torch.arange(3), torch.tensor(sizes))
+    if shuffled:
+        batch = batch[torch.randperm(batch.numel(), generator=g)]
     emb = torch.randn(sum(sizes), 9, 128, generator=g)
     target = torch.tensor([1, -2, 0])
     cot = torch.randn(emb.shape, generator=g)
