@@ -17,25 +17,37 @@ WIGNER, WIG_EXT, ENV = "wigner", "wig_ext", "env"
 _BIT = {WIGNER: 1, WIG_EXT: 1, ENV: 2}
 
 
+def _pass_id() -> int:
+    """Id of the backward pass (autograd graph task) running on this thread; -1 outside one."""
+    return torch._C._current_graph_task_id()
+
+
 class EdgeGradSink:
     """Accumulators of one forward pass.  `target(name, like)` hands out the buffer the next
     contribution goes to (allocated on first use, uninitialised: the first writer overwrites)
-    with its accumulate bit; `take(name)` returns the sum and forgets it, so that a second
-    backward through a retained graph starts afresh."""
+    with its accumulate bit; `take(name)` returns the sum and forgets it.  Each buffer belongs
+    to the backward pass that started it: a contribution from another pass starts afresh, and
+    the producer takes only its own pass's sum.  So a backward through a retained graph that
+    stopped before the producer (a gradient toward an intermediate tensor) leaves nothing that
+    a later backward would add onto."""
 
     def __init__(self):
         self._buf = {}
 
     def target(self, name: str, like: torch.Tensor):
-        t = self._buf.get(name)
-        if t is None:
+        pid = _pass_id()
+        entry = self._buf.get(name)
+        if entry is None or entry[1] != pid:
             t = torch.empty_like(like)
-            self._buf[name] = t
+            self._buf[name] = (t, pid)
             return t, 0
-        return t, _BIT[name]
+        return entry[0], _BIT[name]
 
     def take(self, name: str):
-        return self._buf.pop(name, None)
+        entry = self._buf.pop(name, None)
+        if entry is None or entry[1] != _pass_id():
+            return None
+        return entry[0]
 
 
 def outputs(sink, ctx_like: dict):

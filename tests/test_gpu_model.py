@@ -401,6 +401,42 @@ def test_edge_grads_summed_in_place(cuda, lmax):
 
 
 @pytest.mark.gpu
+def test_edge_grads_retained_partial_backward(cuda):
+    """A backward through a retained graph toward an intermediate tensor runs the blocks' edge
+    gradients into the sink but not the geometry backward that takes them.  The next backward
+    to the positions must start afresh (each sink buffer belongs to one backward pass): forces
+    and stress equal those of a fresh step bit for bit."""
+    import escn_md
+    import heads
+    import systems
+    from wrapper import ZeroAllocBackbone
+    bb = escn_md.eSCNMDBackbone(seed=0, num_layers=2)
+    hd = heads.MLPEnergyHead(bb.sphere_channels, bb.hidden_channels, seed=1)
+    model = heads.PotentialModel(ZeroAllocBackbone(bb.to(cuda)), hd.to(cuda))
+    s = systems.water_box(n_mol=64, L=12.42, seed=5)
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, 6.0, 30)
+    ref = _run(model, s, ei, off, cuda)
+    ce = model.backbone.ce
+    seen = {}
+    def keep_input(mod, args):   # returns None: the layer's arguments stay as they are
+        seen.setdefault("x", args[0])
+
+    hook = ce.layers[1].register_forward_pre_hook(keep_input)
+    try:
+        data = heads.make_atomic_data(s, ei, off, cuda)
+        emb = model.backbone(data)
+    finally:
+        hook.remove()
+    energy = model.head.atom_energy(emb["node_embedding"]).sum()
+    # partial: only the second block's backward runs (its edge gradients go into the sink)
+    torch.autograd.grad(energy, seen["x"], retain_graph=True)
+    g_pos, g_cell = torch.autograd.grad(energy, [data.pos, data.cell])
+    assert torch.equal(-g_pos.cpu(), ref["forces"])
+    stress = heads.stress_from_gradients(data.pos, data.cell, g_pos, g_cell, [int(data.pos.shape[0])])
+    assert torch.equal(stress.cpu(), ref["stress"])
+
+
+@pytest.mark.gpu
 def test_gather_in_conv1_matches_default(cuda):
     """GATHER_IN_CONV1 (conv1 m = 0 gathering its operand in the GEMM loader, the gather forming
     X_m1, X_m2 only) against the default path on a bcc Fe cell large enough for the 256-row
