@@ -324,7 +324,7 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
           const float4 v0 = scale4(x0, s), v1 = scale4(x1, s);
           uint4 h, l;
           if constexpr (PS == 0) {
-            const float m = fmaxf(amax4(v0), amax4(v1));
+            const float m = amax8(v0, v1);
             pmax = fmaxf(pmax, m);
             pmin = fminf(pmin, m);
             low |= f16_lossy(m);
@@ -432,7 +432,7 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
 #pragma unroll 4
         for (int kc = 0; kc < nk; ++kc) {
           load_chunk(kc * GBK);
-          const float mA = fmaxf(amax4(ga[0]), amax4(ga[1])), mW = fmaxf(amax4(gw[0]), amax4(gw[1]));
+          const float mA = amax8(ga[0], ga[1]), mW = amax8(gw[0], gw[1]);
           RA = fmaxf(RA, mA);
           RW = fmaxf(RW, mW);
           zA = fminf(zA, mA);
@@ -440,7 +440,7 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
           gA = fminf(gA, mA > 0.0f ? mA : inf);
           gW = fminf(gW, mW > 0.0f ? mW : inf);
           if constexpr (TALL) {
-            const float mA2 = fmaxf(amax4(ga2[0]), amax4(ga2[1]));
+            const float mA2 = amax8(ga2[0], ga2[1]);
             RA2 = fmaxf(RA2, mA2);
             zA2 = fminf(zA2, mA2);
             gA2 = fminf(gA2, mA2 > 0.0f ? mA2 : inf);

@@ -146,6 +146,13 @@ constexpr float F16_LO_UP = 2048.0f, F16_LO_DOWN = 1.0f / 2048.0f;
 __device__ __forceinline__ float amax4(const float4& v) {
   return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 }
+// largest magnitude of 8 values as a tree of three-operand maxima (v_max3 with |.| modifiers)
+__device__ __forceinline__ float amax8(const float4& a, const float4& b) {
+  const float m0 = fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fabsf(a.z));
+  const float m1 = fmaxf(fmaxf(fabsf(a.w), fabsf(b.x)), fabsf(b.y));
+  const float m2 = fmaxf(fmaxf(fabsf(b.z), fabsf(b.w)), m0);
+  return fmaxf(m1, m2);
+}
 
 // Rows (or operands) of up to this many 16-wide chunks get the exact scale from a pre-pass.
 constexpr int F16_PREPASS_CHUNKS = 4;
