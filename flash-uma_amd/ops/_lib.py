@@ -84,7 +84,7 @@ SIGNATURES: dict[str, list] = {
     "fu_wigner_ext_width": [I32],
     "fu_wigner_ext_fwd": [P, P, I64, I32, P],
     "fu_wigner_ext_bwd": [P, P, P, I64, I32, P],
-    "fu_gather_fwd_lmax": [P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, I32, P],
+    "fu_gather_fwd_lmax": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, I32, P],
     "fu_gather_bwd_lmax": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, I32, I32, P],
     "fu_scatter_fwd_lmax": [P, P, P, P, P, P, P, P, P, P, I64, I64, I32, I32, P],
     "fu_scatter_bwd_lmax": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I32, I32, I32, P],

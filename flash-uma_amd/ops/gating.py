@@ -285,7 +285,7 @@ class EdgeBlock(torch.autograd.Function):
                 m0 = _gather_conv1_gate_m0(ops, conv1[0], conv1[1], C, _lib.stream_ptr(x_in.device))
         else:
             ops = gather_lmax_operands(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, L)
-            X = list(gather_lmax_fwd(*ops, L))
+            X = list(gather_lmax_fwd(*ops, L, topology))
         Zo, Y = conv_pair_fwd(X, conv1, conv2, C, splits, m0)
         r = 4 if L == 2 else 5   # position of rad_out among the gather operands
         if rad_src is not None:

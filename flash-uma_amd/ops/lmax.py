@@ -79,17 +79,21 @@ def gather_lmax_operands(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, 
     return ops
 
 
-def gather_lmax_fwd(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, L):
-    """fu_gather_fwd_lmax: (X_m0, X_m1, X_m2) for operands from gather_lmax_operands."""
+def gather_lmax_fwd(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, L, topology=None):
+    """fu_gather_fwd_lmax: (X_m0, X_m1, X_m2) for operands from gather_lmax_operands.  The kernel
+    walks each node's receiver and sender CSR segments (from the topology, or built here), so
+    every node row is read once per side."""
     N, _, C = x_in.shape
     E = idx_i.shape[0]
     dev = x_in.device
     X_m0 = torch.empty(E, 2 * (L + 1) * C, device=dev)
     X_m1 = torch.empty(E, 4 * L * C, device=dev)
     X_m2 = torch.empty(E, 4 * (L - 1) * C, device=dev)
+    rptr, ridx, sptr, sidx = _csrs(topology, idx_i, idx_j, N, E)
     _lib.call("fu_gather_fwd_lmax", x_in.data_ptr(), idx_i.data_ptr(), idx_j.data_ptr(), wigner.data_ptr(),
-              _ext_ptr(wig_ext), rad_out.data_ptr(), csd_emb.data_ptr(), batch.data_ptr(), X_m0.data_ptr(),
-              X_m1.data_ptr(), X_m2.data_ptr(), E, N, csd_emb.shape[0], C, L, _lib.stream_ptr(dev))
+              _ext_ptr(wig_ext), rad_out.data_ptr(), csd_emb.data_ptr(), batch.data_ptr(), rptr.data_ptr(),
+              ridx.data_ptr(), sptr.data_ptr(), sidx.data_ptr(), X_m0.data_ptr(), X_m1.data_ptr(), X_m2.data_ptr(),
+              E, N, csd_emb.shape[0], C, L, _lib.stream_ptr(dev))
     return X_m0, X_m1, X_m2
 
 
@@ -123,7 +127,7 @@ class GatherRotateLmax(torch.autograd.Function):
     def forward(ctx, x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, topology, lmax):
         L = int(lmax)
         ops = gather_lmax_operands(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, L)
-        X = gather_lmax_fwd(*ops, L)
+        X = gather_lmax_fwd(*ops, L, topology)
         ctx.save_for_backward(*ops)
         ctx.topology, ctx.lmax = topology, L
         return X

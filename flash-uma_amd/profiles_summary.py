@@ -42,7 +42,8 @@ KERNEL_ENTRY = {
     "nlist_bin_kernel": "fu_nlist_bin", "nlist_search_kernel": "fu_nlist_search", "nlist_scan_kernel": "fu_nlist_scan",
     "nlist_emit_kernel": "fu_nlist_emit",
     "wigner_ext_fwd_kernel": "fu_wigner_ext_fwd", "wigner_ext_bwd_kernel": "fu_wigner_ext_bwd",
-    "gather_fwd_lmax_kernel": "fu_gather_fwd_lmax", "gather_bwd_lmax_kernel": "fu_gather_bwd_lmax",
+    "gather_fwd_lmax_kernel": "fu_gather_fwd_lmax", "gather_fwd_node_lmax_kernel": "fu_gather_fwd_lmax",
+    "gather_bwd_lmax_kernel": "fu_gather_bwd_lmax",
     "add_rows_kernel": "fu_gather_bwd_lmax(add)",
     "scatter_fwd_lmax_kernel": "fu_scatter_fwd_lmax", "scatter_bwd_lmax_kernel": "fu_scatter_bwd_lmax",
     "init_scatter_fwd_lmax_kernel": "fu_init_scatter_fwd_lmax", "init_scatter_bwd_lmax_kernel": "fu_init_scatter_bwd_lmax",
@@ -134,12 +135,14 @@ def _joined(counters: str, trace: str) -> list[tuple[dict, int]]:
 
 
 def _calibration(rows: list[tuple[dict, int]]) -> float:
-    """Counter value (KiB) of the 256 MiB copy kernel bench.py --pmc-calibration dispatches."""
+    """Counter value (KiB) of the 256 MiB copy kernel bench.py --pmc-calibration dispatches: the
+    largest reading among the copy kernels of its grid (model set-up copies smaller buffers with
+    the same grid)."""
     vals = [float(r["Counter_Value"]) for r, _ in rows
             if "copyBuffer" in r["Kernel_Name"] and int(r["Grid_Size"]) == 131072]
     if not vals:
         raise SystemExit("no 256 MiB copy kernel in the counter file: run bench.py with --pmc-calibration")
-    return vals[0]
+    return max(vals)
 
 
 def _in_steps(rows: list[tuple[dict, int]]) -> list[tuple[dict, str]]:

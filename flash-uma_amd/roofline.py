@@ -135,7 +135,7 @@ def _ext(L):
 
 
 def _gather_fwd_l(a):
-    E, N, C, L = a[11], a[12], a[14], a[15]
+    E, N, C, L = a[15], a[16], a[18], a[19]
     return E * ((16 * L - 2) * C * 4 + (34 + _ext(L)) * 4 + 16) + N * ((L + 1) ** 2 * C * 4 + 8), 0
 
 

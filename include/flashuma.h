@@ -46,7 +46,8 @@ extern "C" {
  * header.  0.2.0 added the int32 `accumulate` argument (before the stream) of fu_gather_bwd,
  * fu_scatter_bwd, fu_init_scatter_bwd, their _lmax forms and fu_complex_linear_gate(_bwd), and
  * dropped one pointer/stride pair of fu_linear_gate_bwd; 0.3.0 changed the layout and size of
- * the fu_complex_weight_split buffer (fu_complex_weight_split_bytes).  A caller built against
+ * the fu_complex_weight_split buffer (fu_complex_weight_split_bytes) and added the four CSR
+ * arguments of fu_gather_fwd_lmax.  A caller built against
  * another version must not call into this library. */
 int fu_version(void);
 
@@ -537,12 +538,16 @@ int fu_wigner_ext_fwd(const float* wigner, float* wig_ext, int64_t E, int32_t lm
 int fu_wigner_ext_bwd(const float* wigner, const float* g_wig_ext, float* g_wigner, int64_t E,
                       int32_t lmax, void* stream);
 
-/* fu_gather_fwd for lmax 2..4 in the extended reference order (ops/gather.py:34-154). */
+/* fu_gather_fwd for lmax 2..4 in the extended reference order (ops/gather.py:34-154).  With the
+ * receiver and sender CSRs of the graph (all four non-NULL, as fu_gather_bwd_lmax takes them)
+ * the kernel walks each node's two segments and reads every node row once per side; with all
+ * four NULL it runs edge-parallel from idx_i / idx_j.  The outputs are the same either way. */
 int fu_gather_fwd_lmax(const float* x, const int64_t* idx_i, const int64_t* idx_j,
                        const float* wigner, const float* wig_ext, const float* rad,
-                       const float* csd_emb, const int64_t* batch, float* X_m0, float* X_m1,
-                       float* X_m2, int64_t E, int64_t N, int64_t S, int32_t C, int32_t lmax,
-                       void* stream);
+                       const float* csd_emb, const int64_t* batch, const int32_t* recv_ptr,
+                       const int32_t* recv_idx, const int32_t* send_ptr, const int32_t* send_idx,
+                       float* X_m0, float* X_m1, float* X_m2, int64_t E, int64_t N, int64_t S, int32_t C,
+                       int32_t lmax, void* stream);
 
 /* fu_gather_bwd for lmax 2..4 (ops/gather.py:160-405, node-centric, no atomics).  ws is a
  * scratch array of E * (34 + fu_wigner_ext_width(lmax)) floats.  accumulate: bit 0 adds

@@ -190,8 +190,8 @@ def test_lmax_entry_points_reject_bad_arguments():
     assert b"lmax" in lib.fu_last_error()
     assert lib.fu_scatter_fwd_lmax(None, None, None, None, None, None, None, None, None, None, 4, 8, 96, 4, None) != 0
     assert b"C=96" in lib.fu_last_error()
-    assert lib.fu_gather_fwd_lmax(None, None, None, None, None, None, None, None, None, None, None, 8, 4, 1, 128, 4,
-                                  None) != 0
+    assert lib.fu_gather_fwd_lmax(None, None, None, None, None, None, None, None, None, None, None, None, None, None,
+                                  None, 8, 4, 1, 128, 4, None) != 0
     assert b"NULL" in lib.fu_last_error()
     # lmax 3 and 4 need the extension rows; lmax 2 accepts NULL there (checked before any launch)
     assert lib.fu_init_scatter_bwd_lmax(None, None, None, None, None, None, None, None, None, None, 0, 4, 128, 4, 0,

@@ -119,6 +119,34 @@ def test_gather_lmax(cuda, L, C):
         assert_close(a, b, TOL, "gather bwd")
 
 
+@pytest.mark.parametrize("L,C", [(2, 128), (3, 64), (4, 128)])
+def test_gather_lmax_node_and_edge_forms(cuda, L, C):
+    """fu_gather_fwd_lmax with the graph's CSRs (each node's receiver and sender segments, node
+    rows read once per side) and without them (edge-parallel): bitwise equal outputs, both
+    equal to the float64 oracle.  The graph has nodes without incoming or outgoing edges."""
+    from ops import _lib
+    from ops.lmax import _csrs, _ext_ptr
+    x, ei, wig, ext, rad, csd, batch = _inputs(L, C=C, N=60, E=250)
+    xg, wg, eg, rg, cg, bg = (t.to(cuda) for t in (x, wig, ext, rad, csd, batch))
+    ii, jj = ei[0].to(cuda), ei[1].to(cuda)
+    N, E = x.shape[0], ii.shape[0]
+    assert (torch.bincount(ei[0], minlength=N) == 0).any() and (torch.bincount(ei[1], minlength=N) == 0).any()
+    rptr, ridx, sptr, sidx = _csrs(None, ii, jj, N, E)
+    outs = []
+    for csr in (True, False):
+        X = [torch.full((E, w * C), float("nan"), device=cuda) for w in (2 * (L + 1), 4 * L, 4 * (L - 1))]
+        p = [t.data_ptr() for t in (rptr, ridx, sptr, sidx)] if csr else [None] * 4
+        _lib.call("fu_gather_fwd_lmax", xg.data_ptr(), ii.data_ptr(), jj.data_ptr(), wg.data_ptr(), _ext_ptr(eg),
+                  rg.data_ptr(), cg.data_ptr(), bg.data_ptr(), *p, X[0].data_ptr(), X[1].data_ptr(), X[2].data_ptr(),
+                  E, N, 1, C, L, _lib.stream_ptr(cuda))
+        outs.append([t.cpu() for t in X])
+    ref = R.gather_rotate_lmax(x.double(), ei[0], ei[1], wig.double(), ext.double(), rad.double(), csd.double(),
+                               batch, L)
+    for a, b, r in zip(*outs, ref):
+        assert torch.equal(a, b)
+        assert_close(a, r, TOL, "gather fwd (node-centric)")
+
+
 @pytest.mark.parametrize("L", [2, 3, 4])
 def test_gating_lmax(cuda, L):
     from ops.lmax import gating_lmax
