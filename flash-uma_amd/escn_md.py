@@ -7,13 +7,12 @@ installed offline.  This module provides an object with exactly the attributes
 UMA-s, with seeded random weights, plus the node modules the reference attaches by
 reference (norm_1, norm_2, atom_wise, final norm, charge/spin embeddings).
 
-The node modules restate the published FAIRChem eSCN-MD designs (no FAIRChem code or
-fixtures exist here).  Their GPU forward and backward are checked against the CPU oracle's
-restatement, which is itself checked against the library routines the modules reduce to at
-lmax = 0 (LayerNorm, Linear, a Linear-SiLU-Linear MLP), hand-derived known answers and
-equivariance.  Their forward passes run on the gfx950 node kernels
-(ops/node.py: RMS norm, batched per-degree MFMA GEMM, gate activation); like the rest of
-the backbone they need GPU tensors.
+The node modules are the HIP-backed ones of node_layers.py, which restate the published
+FAIRChem eSCN-MD designs (no FAIRChem code or fixtures exist here).  Their GPU forward and
+backward are checked against the CPU oracle's restatement, which is itself checked against the
+library routines the modules reduce to at lmax = 0 (LayerNorm, Linear, a Linear-SiLU-Linear
+MLP), hand-derived known answers and equivariance; like the rest of the backbone they need GPU
+tensors.
 
 Initialisation (seeded CPU torch.Generator, fixed creation order): nn.Linear default
 (kaiming-uniform weights, uniform bias), nn.Embedding N(0, 1), LayerNorm/affine weights 1,
@@ -21,137 +20,13 @@ biases 0.
 """
 from __future__ import annotations
 
-import math
 from types import SimpleNamespace
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
-from ops.linear import linear
-from ops.node import (gate_act, rms_norm_sh, rms_norm_sh_residual, scalar_gemm_so3, so3_linear,
-                      so3_linear_residual)
-
-
-def num_coefficients(lmax: int) -> int:
-    return (lmax + 1) ** 2
-
-
-def degree_index(lmax: int) -> torch.Tensor:
-    """Degree l of every SH coefficient k (k = l^2 + l + m)."""
-    return torch.cat([torch.full((2 * l + 1,), l, dtype=torch.long) for l in range(lmax + 1)])
-
-
-class EquivariantRMSNormArraySphericalHarmonicsV2(nn.Module):
-    """Equivariant RMS norm over SH coefficients (FAIRChem's "rms_norm_sh" layer, recalled):
-    subtract the channel mean of l=0, scale every coefficient by
-    (mean_c sum_l w_l mean_{m} x_{lm,c}^2 + eps)^(-1/2) with degree-balanced weights
-    w_l = 1/(lmax+1), apply a per-(l, c) affine weight and an l=0 bias."""
-
-    def __init__(self, lmax: int, num_channels: int, eps: float = 1e-5):
-        super().__init__()
-        self.lmax = lmax
-        self.num_channels = num_channels
-        self.eps = eps
-        self.affine_weight = nn.Parameter(torch.ones(lmax + 1, num_channels))
-        self.affine_bias = nn.Parameter(torch.zeros(num_channels))
-        self.register_buffer("expand_index", degree_index(lmax), persistent=False)
-        bal = torch.zeros(num_coefficients(lmax), 1)
-        for l in range(lmax + 1):
-            bal[l * l:(l + 1) * (l + 1)] = 1.0 / (2 * l + 1)
-        self.register_buffer("balance_degree_weight", bal / (lmax + 1), persistent=False)
-
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return rms_norm_sh(x, self.affine_weight, self.affine_bias, self.lmax, self.eps)
-
-    def forward_with_residual(self, x: torch.Tensor):
-        """(norm(x), x) for an x that also feeds a residual skip; the backward sums the two
-        gradients inside the norm's backward kernel."""
-        return rms_norm_sh_residual(x, self.affine_weight, self.affine_bias, self.lmax, self.eps)
-
-
-class SO3_Linear(nn.Module):
-    """Per-degree linear map: coefficient (l, m) of the output is W_l x_(l, m); l=0 has a bias."""
-
-    def __init__(self, in_features: int, out_features: int, lmax: int, generator=None):
-        super().__init__()
-        self.lmax = lmax
-        bound = 1.0 / math.sqrt(in_features)
-        self.weight = nn.Parameter(torch.empty(lmax + 1, out_features, in_features).uniform_(
-            -bound, bound, generator=generator))
-        self.bias = nn.Parameter(torch.empty(out_features).uniform_(-bound, bound, generator=generator))
-        self.register_buffer("expand_index", degree_index(lmax), persistent=False)
-
-    def per_coefficient_weights(self):
-        """(W_k, W_k^T) stacked over the (lmax+1)^2 coefficients (weights are frozen)."""
-        w = self.weight.detach().index_select(0, self.expand_index).contiguous()
-        return w, w.transpose(1, 2).contiguous()
-
-    def weights(self, device) -> tuple:
-        """(W_k, W_k^T, bias) on `device`, built once per device (weights are frozen)."""
-        if getattr(self, "_wk", None) is None or self._wk[0].device != device:
-            self._wk = self.per_coefficient_weights()
-        return self._wk[0], self._wk[1], self.bias.detach()
-
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return so3_linear(x, *self.weights(x.device))
-
-
-class GateActivation(nn.Module):
-    """l=0 -> SiLU; coefficients of degree l>0 scaled by sigmoid(gate_l) per channel."""
-
-    def __init__(self, lmax: int, num_channels: int):
-        super().__init__()
-        self.lmax = lmax
-        self.num_channels = num_channels
-        self.register_buffer("gate_index", (degree_index(lmax)[1:] - 1), persistent=False)
-
-    def forward(self, pre: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
-        """pre: the scalar MLP's pre-activation (N, lmax * H); the gate is
-        sigmoid(silu(pre)) per degree (FAIRChem applies SiLU in the scalar MLP and the
-        sigmoid here)."""
-        return gate_act(pre, x, self.lmax)
-
-
-class SpectralAtomwise(nn.Module):
-    """Per-node gated SO(3) feed-forward block (FAIRChem's spectral atom-wise FFN, recalled)."""
-
-    def __init__(self, sphere_channels: int, hidden_channels: int, lmax: int, generator=None):
-        super().__init__()
-        self.scalar_mlp = nn.Sequential(_linear(sphere_channels, lmax * hidden_channels, True, generator), nn.SiLU())
-        self.so3_linear_1 = SO3_Linear(sphere_channels, hidden_channels, lmax, generator)
-        self.act = GateActivation(lmax, hidden_channels)
-        self.so3_linear_2 = SO3_Linear(hidden_channels, sphere_channels, lmax, generator)
-
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        lin = self.scalar_mlp[0]
-        if getattr(self, "_wt", None) is None or self._wt.device != x.device:
-            self._wt = lin.weight.detach().t().contiguous()
-        pre = linear(x[:, 0, :], lin.weight.detach(), lin.bias.detach(), self._wt)
-        h = self.so3_linear_1(x)
-        h = self.act(pre, h)
-        return self.so3_linear_2(h)
-
-    def forward_residual(self, x: torch.Tensor, skip: torch.Tensor) -> torch.Tensor:
-        """forward(x) + skip with no node-sized elementwise pass: the scalar and SO(3) reads of
-        x share one backward, and skip is added in the last GEMM's epilogue."""
-        lin = self.scalar_mlp[0]
-        if getattr(self, "_wt", None) is None or self._wt.device != x.device:
-            self._wt = lin.weight.detach().t().contiguous()
-        pre, h = scalar_gemm_so3(x, lin.weight.detach(), lin.bias.detach(), self._wt,
-                                 *self.so3_linear_1.weights(x.device))
-        h = self.act(pre, h)
-        return so3_linear_residual(h, *self.so3_linear_2.weights(x.device), skip)
-
-
-def _linear(i: int, o: int, bias: bool, generator) -> nn.Linear:
-    lin = nn.Linear(i, o, bias=bias)
-    bound = 1.0 / math.sqrt(i)
-    with torch.no_grad():
-        lin.weight.uniform_(-bound, bound, generator=generator)
-        if bias:
-            lin.bias.uniform_(-bound, bound, generator=generator)
-    return lin
+from node_layers import (EquivariantRMSNormArraySphericalHarmonicsV2, GateActivation, SO3_Linear,  # noqa: F401
+                         SpectralAtomwise, _linear, degree_index, num_coefficients)
 
 
 def _embedding(n: int, d: int, generator) -> nn.Embedding:

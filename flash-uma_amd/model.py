@@ -3,9 +3,9 @@
 Public names and signatures follow the reference: reorder_graph_morton, build_csr_cached,
 clear_csr_cache (model.py:17-74), Packed_eSCN_Layer (model.py:81-157) and
 eSCN_Inference_Model (model.py:160-221).  Every per-edge and per-CSR operation runs in
-libflashuma_hip.so; the node-level FAIRChem modules attached by transfer_weights (norm_1,
-norm_2, atom_wise, final_norm) are called as given (the stand-ins in escn_md.py run on the
-node kernels of ops/node.py).
+libflashuma_hip.so; the node-level modules set by transfer_weights (norm_1, norm_2,
+atom_wise, final_norm) are the HIP-backed ones of node_layers.py, rebuilt from FAIRChem's
+modules by parameter name (a module without FAIRChem's parameters is called as given).
 
 Differences in mechanism (not in results):
   - the graph topology (Morton order, receiver-sorted edge order, receiver and sender CSRs)

@@ -11,6 +11,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from model import eSCN_Inference_Model
+from node_layers import adopt_atom_wise, adopt_rms_norm
 from ops.node import edge_shifts
 
 
@@ -45,11 +46,13 @@ def transfer_weights(off_model, cust_model):
         cust_blk.W2_m1_R.copy_(w[:L * C, :]); cust_blk.W2_m1_I.copy_(w[L * C:, :])
         w = so2_2.so2_m_conv[1].fc.weight
         cust_blk.W2_m2_R.copy_(w[:(L - 1) * C, :]); cust_blk.W2_m2_I.copy_(w[(L - 1) * C:, :])
-        # node-level modules are attached by reference
-        cust_blk.norm_1 = off_blk.norm_1
-        cust_blk.norm_2 = off_blk.norm_2
-        cust_blk.atom_wise = off_blk.atom_wise
-    cust_model.final_norm = off_model.norm
+        # The reference attaches the node-level modules by reference (wrapper.py:74-79); here
+        # they are rebuilt on the HIP node kernels from their parameters, by FAIRChem's names
+        # (node_layers.py), so later edits of the original modules' weights are not seen.
+        cust_blk.norm_1 = adopt_rms_norm(off_blk.norm_1, L, C)
+        cust_blk.norm_2 = adopt_rms_norm(off_blk.norm_2, L, C)
+        cust_blk.atom_wise = adopt_atom_wise(off_blk.atom_wise, L, C)
+    cust_model.final_norm = adopt_rms_norm(off_model.norm, L, C)
     cust_model.charge_start = off_model.charge_channel_start
     cust_model.charge_end = off_model.charge_channel_end
     cust_model.spin_start = off_model.spin_channel_start

@@ -33,7 +33,7 @@ def degree_index(lmax: int) -> torch.Tensor:
 
 
 def rms_norm_sh(x, weight, bias, lmax: int, eps: float):
-    """Equivariant RMS norm (see flash-uma_amd/escn_md.py): centre l=0 over channels, scale
+    """Equivariant RMS norm (flash-uma_amd/node_layers.py): centre l=0 over channels, scale
     by the degree-balanced mean square, per-(l, c) weight, l=0 bias."""
     l0 = x[:, :1] - x[:, :1].mean(dim=2, keepdim=True)
     feat = torch.cat([l0, x[:, 1:]], 1)

@@ -463,3 +463,47 @@ def test_gather_in_conv1_matches_default(cuda):
     assert (a["forces"] - b["forces"]).abs().max().item() <= 1e-5 * fs
     ss = a["stress"].abs().max().item()
     assert (a["stress"] - b["stress"]).abs().max().item() <= 1e-5 * ss
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("lmax", [2, 4])
+def test_fairchem_named_node_modules_run_on_node_kernels(cuda, monkeypatch, lmax):
+    """A backbone whose node modules are plain-PyTorch ones with FAIRChem's parameter names
+    (tests/_fairchem_like.py) is wrapped onto the HIP node kernels: the norms and atom-wise
+    blocks call fu_rms_norm_sh_*, fu_linear_batched and fu_gate_act_* in the forward and the
+    backward, the results equal those of the stand-in's own modules bit for bit, and E, F, S
+    match the float64 oracle of the wrapped backbone."""
+    import _fairchem_like as fc
+    import escn_md
+    import heads
+    import systems
+    from ops import _lib
+    from oracle.model_ref import energy_forces_stress
+    from wrapper import ZeroAllocBackbone
+    kw = dict(seed=2, num_layers=2, lmax=lmax)
+    own = escn_md.eSCNMDBackbone(**kw)
+    foreign = fc.fairchem_like(escn_md.eSCNMDBackbone(**kw))
+    hd = heads.MLPEnergyHead(own.sphere_channels, own.hidden_channels, seed=3)
+    s = systems.cu_slab_co()
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, own.cutoff, own.max_neighbors)
+    ref = energy_forces_stress(foreign, hd, s.pos, s.Z, s.cell, ei, off, dtype=torch.float64)
+    want = _run(heads.PotentialModel(ZeroAllocBackbone(own.to(cuda)), hd.to(cuda)), s, ei, off, cuda)
+
+    model = heads.PotentialModel(ZeroAllocBackbone(foreign.to(cuda)), hd)
+    calls = []
+    real_call = _lib.call
+
+    def spy(name, *args):
+        calls.append(name)
+        return real_call(name, *args)
+
+    monkeypatch.setattr(_lib, "call", spy)
+    out = _run(model, s, ei, off, cuda)
+    monkeypatch.setattr(_lib, "call", real_call)
+    n_norm = 2 * 2 + 1
+    assert calls.count("fu_rms_norm_sh_fwd") == n_norm and calls.count("fu_rms_norm_sh_bwd") == n_norm
+    assert calls.count("fu_gate_act_fwd") == 2 and calls.count("fu_gate_act_bwd") == 2
+    assert calls.count("fu_linear_batched") >= 2 * 2 * 2
+    for k in ("energy", "forces", "stress"):
+        assert torch.equal(out[k], want[k]), k
+    _check(out, ref, s.n_atoms)
