@@ -44,6 +44,40 @@ def linear(x: torch.Tensor, W: torch.Tensor, bias: torch.Tensor | None, Wt: torc
     return _LinearFn.apply(x, W, bias, Wt)
 
 
+def resident_ok(K: int) -> bool:
+    """fu_linear_resident takes K in 16..128, a multiple of 16."""
+    return 16 <= K <= 128 and K % 16 == 0
+
+
+def linear_weight_split(W: torch.Tensor) -> torch.Tensor:
+    """The frozen weight W (N, K) pre-split for fu_linear_resident: fp16 hi, lo and 2^11 lo
+    planes of the columns at their exact power-of-two scales in MFMA-fragment order, the unscale
+    factors and the window flags."""
+    W = _lib.require(W, torch.float32, "W")
+    N, K = W.shape
+    nbytes = _lib.load().fu_linear_weight_split_bytes(N, K)
+    if nbytes < 0:
+        raise _lib.FlashUMAError(f"linear_weight_split: bad shape {(N, K)} (16 <= K <= 128, K % 16 == 0)")
+    W2 = torch.empty(nbytes // 16, 4, device=W.device, dtype=torch.int32)
+    _lib.call("fu_linear_weight_split", W.data_ptr(), W.stride(0), N, K, W2.data_ptr(), _lib.stream_ptr(W.device))
+    return W2
+
+
+def gemm_resident(x: torch.Tensor, W2: torch.Tensor, N: int, bias: torch.Tensor | None = None,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[M, N] = x[M, K] @ W^T (+ bias) for K <= 128 with W pre-split by linear_weight_split
+    (fu_linear_resident: split-fp16 products, each workgroup's rows of x resident in LDS across
+    all N).  x may be a row-strided view with 16-byte aligned rows."""
+    M, K = x.shape
+    if x.stride(-1) != 1 or x.stride(0) % 4 != 0 or x.data_ptr() % 16 != 0:
+        x = x.contiguous()
+    if out is None:
+        out = torch.empty((M, N), device=x.device, dtype=torch.float32)
+    _lib.call("fu_linear_resident", x.data_ptr(), x.stride(0), W2.data_ptr(), _lib.ptr(bias), out.data_ptr(),
+              out.stride(0), M, N, K, _lib.stream_ptr(x.device))
+    return out
+
+
 def complex_weight_split(P: torch.Tensor, Q: torch.Tensor) -> torch.Tensor:
     """The frozen complex weight P + iQ (Nc, Kc each) pre-split for fu_complex_linear's W3
     argument: exact three-way bf16 splits of P, Q and P + Q in MFMA-fragment order, then their

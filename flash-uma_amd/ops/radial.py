@@ -21,6 +21,7 @@ import torch
 
 from . import _lib
 from .constants import LN_EPS
+from .linear import gemm_resident, linear_weight_split, resident_ok
 
 
 def _ln_grouped_fwd(x, tabs, z, isrc, idst, bias, gamma, beta, G, D, eps):
@@ -124,6 +125,16 @@ def _gemm(A, W, bias, out):
     return out
 
 
+def _out_gemm(A, W, bias, W2):
+    """An output layer's product: in the split-fp16 mode, with the weight pre-split (W2), on
+    fu_linear_resident (the (E, C) input read and split once per 128-row panel instead of once
+    per 128-column tile); otherwise fu_linear."""
+    out = torch.empty(A.shape[0], W.shape[0], device=A.device, dtype=torch.float32)
+    if W2 is not None and _lib.get_matmul_mode() == _lib.MATMUL_SPLIT_F16:
+        return gemm_resident(A, W2, W.shape[0], bias, out)
+    return _gemm(A, W, bias, out)
+
+
 class RadialBank(torch.nn.Module):
     """Frozen bank of G radial MLPs sharing the edge features.
 
@@ -164,6 +175,17 @@ class RadialBank(torch.nn.Module):
     # reserve then grew from 31 to 230 GB on the 8,192-atom Fe cell, and the allocations
     # on that path stalled the host for seconds in some processes.
 
+    def out_split(self, k: int):
+        """Output layer k's weight pre-split for fu_linear_resident, built on first use on a device
+        (None when its K is outside that kernel's range).  Weights are frozen."""
+        W = getattr(self, f"W3_{k}")
+        if not resident_ok(W.shape[1]):
+            return None
+        cache = self.__dict__.setdefault("_out_splits", {})
+        if k not in cache or cache[k].device != W.device:
+            cache[k] = linear_weight_split(W)
+        return cache[k]
+
     def forward(self, gauss, Z, idx_i, idx_j, with_sources: bool = False):
         """gauss (E, B) -> tuple of G radial outputs (E, n_k).
 
@@ -177,17 +199,18 @@ class RadialBank(torch.nn.Module):
         outs, srcs = [], []
         for k in range(self.G):
             W, Wt, b = getattr(self, f"W3_{k}"), getattr(self, f"W3_{k}_t"), getattr(self, f"b3_{k}")
-            outs.append(_RadialOutFn.apply(h2s[k], W, b, Wt, holder, k))
-            srcs.append((h2s[k].detach(), W, b))
+            W2 = self.out_split(k)
+            outs.append(_RadialOutFn.apply(h2s[k], W, b, Wt, holder, k, W2))
+            srcs.append((h2s[k].detach(), W, b, W2))
         holder.ln = None
         return (tuple(outs), tuple(srcs)) if with_sources else tuple(outs)
 
 
 def recompute_output(src) -> torch.Tensor:
-    """A block's radial output from its (h2_k, W3_k, b3_k) source: the forward's GEMM on the
-    same operands, so bitwise the tensor the bank returned."""
-    h2k, W, b = src
-    return _gemm(h2k, W, b, torch.empty(h2k.shape[0], W.shape[0], device=h2k.device, dtype=torch.float32))
+    """A block's radial output from its (h2_k, W3_k, b3_k, split W3_k) source: the forward's GEMM
+    on the same operands, so bitwise the tensor the bank returned."""
+    h2k, W, b, W2 = src
+    return _out_gemm(h2k, W, b, W2)
 
 
 class _GradHolder:
@@ -282,14 +305,14 @@ class _RadialOutFn(torch.autograd.Function):
     LayerNorm-SiLU backward in its epilogue, g_h2_k never stored), otherwise g_h2_k."""
 
     @staticmethod
-    def forward(ctx, h2k, W, b, Wt, holder, k):
+    def forward(ctx, h2k, W, b, Wt, holder, k, W2=None):
         ctx.holder, ctx.k = holder, k
         # (p2, mean, rstd, gamma, beta) of the trunk's forward are saved like the weight, so
         # that they are released after the backward (a plain ctx attribute would keep p2 alive
         # as long as the graph's nodes, i.e. into the next step)
         ctx.ln_groups = None if holder.ln is None else holder.ln[-1]
         ctx.save_for_backward(Wt, *(() if holder.ln is None else holder.ln[:-1]))
-        return _gemm(h2k, W, b, torch.empty(h2k.shape[0], W.shape[0], device=h2k.device, dtype=torch.float32))
+        return _out_gemm(h2k, W, b, W2)
 
     @staticmethod
     def backward(ctx, g_rad):
@@ -307,4 +330,4 @@ class _RadialOutFn(torch.autograd.Function):
             _lib.call("fu_linear_dgrad_ln_silu_bwd", g_rad.data_ptr(), g_rad.stride(0), Wt.data_ptr(), Wt.stride(0),
                       sl.data_ptr(), buf.stride(0), M, K, p2.data_ptr(), p2.stride(0), gamma.data_ptr(),
                       beta.data_ptr(), m2.data_ptr(), r2.data_ptr(), G, ctx.k, _lib.stream_ptr(g_rad.device))
-        return sl, None, None, None, None, None
+        return sl, None, None, None, None, None, None

@@ -32,6 +32,8 @@ MATMUL_SPLIT_BF16, MATMUL_FP32, MATMUL_SPLIT_F16 = 0, 1, 2
 
 def _products(name: str, matmul_mode: int) -> tuple[int, str]:
     """Matrix-core products per fp32 product of entry `name` in `matmul_mode`, and their kind."""
+    if name == "fu_linear_resident":   # split-fp16 in every mode
+        return F16_PRODUCTS, "fp16 mfma, 3 products per fp32 product"
     if matmul_mode == MATMUL_FP32:
         return 1, "fp32 mfma"
     if matmul_mode == MATMUL_SPLIT_F16 and name != "fu_gather_linear_gate":
@@ -192,6 +194,11 @@ def _linear(a):
     return 4 * (M * K + M * N + N * K), 2 * M * N * K
 
 
+def _linear_resident(a):
+    M, N, K = a[6], a[7], a[8]
+    return 4 * (M * K + M * N + N * K), 2 * M * N * K
+
+
 def _linear_batched(a):
     M, N, K, B = a[15], a[16], a[17], a[18]
     r = M * N if a[9] else 0   # the residual, read once
@@ -283,6 +290,7 @@ WORK = {
     "fu_ln_silu_grouped_bwd": _ln_grouped_bwd,
     "fu_linear": _linear,
     "fu_linear_batched": _linear_batched,
+    "fu_linear_resident": _linear_resident,
     "fu_linear_ln_silu": _linear_ln_silu,
     "fu_linear_ln_silu_bwd": _linear_ln_silu_bwd,
     "fu_linear_dgrad_ln_silu_bwd": _linear_dgrad_ln_silu_bwd,
@@ -306,7 +314,7 @@ WORK = {
 
 MFMA_BOUND = {"fu_linear", "fu_linear_batched", "fu_complex_linear", "fu_linear_gate", "fu_complex_linear_gate",
               "fu_linear_gate_bwd", "fu_complex_linear_gate_bwd", "fu_linear_ln_silu", "fu_linear_ln_silu_bwd",
-              "fu_linear_dgrad_ln_silu_bwd", "fu_gather_linear_gate"}
+              "fu_linear_dgrad_ln_silu_bwd", "fu_gather_linear_gate", "fu_linear_resident"}
 
 
 def summarize(durations, matmul_mode: int = MATMUL_SPLIT_F16) -> dict:

@@ -42,12 +42,13 @@ extern "C" {
 #define FU_ERR_NULL (-5)        /* a required pointer is NULL */
 #define FU_ERR_WORKSPACE (-6)   /* the workspace is too small */
 
-/* Library version (major*10000 + minor*100 + patch): 300 (0.3.0) for the signatures in this
+/* Library version (major*10000 + minor*100 + patch): 400 (0.4.0) for the signatures in this
  * header.  0.2.0 added the int32 `accumulate` argument (before the stream) of fu_gather_bwd,
  * fu_scatter_bwd, fu_init_scatter_bwd, their _lmax forms and fu_complex_linear_gate(_bwd), and
  * dropped one pointer/stride pair of fu_linear_gate_bwd; 0.3.0 changed the layout and size of
  * the fu_complex_weight_split buffer (fu_complex_weight_split_bytes) and added the four CSR
- * arguments of fu_gather_fwd_lmax.  A caller built against
+ * arguments of fu_gather_fwd_lmax; 0.4.0 added fu_linear_weight_split_bytes,
+ * fu_linear_weight_split and fu_linear_resident (nothing changed).  A caller built against
  * another version must not call into this library. */
 int fu_version(void);
 
@@ -62,12 +63,14 @@ const char* fu_last_error(void);
  *      accumulation; error against fp64 at or below that of the fp32 MFMA.
  *   1: v_mfma_f32_32x32x2_f32.
  *   2 (default): each operand row (a row of A, or a row of W: an output column) is scaled by a power of
- *      two that puts its largest magnitude in [2^-3, 2^15), each element split into two fp16
- *      values (x 2^e = hi + lo, 22 significant bits) and three partial products run on
- *      v_mfma_f32_32x32x16_f16 with fp32 accumulation, unscaled exactly afterwards.  Scales come
- *      from the row's first 16 elements (or, for K <= 64, from the whole row); a tile whose rows
- *      end outside the window is computed again with exact scales.  Error against fp64 at or
- *      below that of the fp32 MFMA on the model's shapes.  fu_gather_linear_gate and
+ *      two, each element split into two fp16 values (x 2^e = hi + lo, 22 significant bits) and
+ *      three partial products run on v_mfma_f32_32x32x16_f16 with fp32 accumulation, unscaled
+ *      exactly afterwards.  Scales come from the row's first 16 elements (or, for K <= 64, from
+ *      the whole row); a tile whose 8-element pieces leave the fp16 window while the other
+ *      operand is not flat (or that overflows) is computed again with exact scales, in two K
+ *      loops with 2^11-scaled residuals when needed (split_f16.h states the rules).  Row-relative
+ *      error against fp64 at most 1.1x (rms) / 1.5x (max) that of the fp32 MFMA on the tested
+ *      shapes and operand families.  fu_gather_linear_gate and
  *      fu_complex_linear* without W3 keep the bf16 split in this mode.
  * The mode is process-wide and read at each launch; switch it only between launches.
  * fu_set_matmul_mode returns FU_OK or FU_ERR_UNSUPPORTED; fu_matmul_mode returns the mode. */
@@ -318,6 +321,30 @@ int fu_complex_linear(const float* A_r, const float* A_i, int64_t lda, const flo
 int64_t fu_complex_weight_split_bytes(int32_t Nc, int32_t Kc);
 int fu_complex_weight_split(const float* P, const float* Q, int64_t ldw, int32_t Nc, int32_t Kc, void* W3,
                             void* stream);
+
+/* Pre-split real weight for fu_linear_resident; no reference counterpart (a frozen weight of
+ * model.py:147-149, 203-205, prepared once at freeze time).  W (N, K) with row stride ldw,
+ * 16 <= K <= 128, K % 16 == 0.  W2 receives the fp16 splits of every column n scaled by its
+ * exact power of two 2^e(n) in MFMA-fragment order ([32-column block][16-k chunk][hi, lo, lo'
+ * = 2^11 lo][64 lanes] x 16 bytes, zero padded to N = 32 n), then the factors 2^-e(n) (one float
+ * per padded column), then one int32 per padded column (bit 0: 8 consecutive k below the fp16
+ * window at the column's scale; bit 1: the column is not flat), then their OR (one int32,
+ * padded to 16 bytes): fu_linear_weight_split_bytes(N, K) bytes, 16-byte aligned.  The bytes
+ * query returns a negative FU_ERR_* for a shape outside those bounds. */
+int64_t fu_linear_weight_split_bytes(int32_t N, int32_t K);
+int fu_linear_weight_split(const float* W, int64_t ldw, int32_t N, int32_t K, void* W2, void* stream);
+
+/* Y[M, N] = A[M, K] W^T (+ bias[N]) for short K, replacing F.linear of the radial output layers
+ * (model.py:149, 205: rad_out = h2 W_rad1_3^T + b_rad1_3, K = C, N = 6 lmax C).  W is given
+ * pre-split by fu_linear_weight_split.  Always computed in the split-fp16 form of matrix-core
+ * mode 2, whatever fu_set_matmul_mode selects, with each row of A at its exact scale (taken from
+ * the whole row) and the two-loop pass of split_f16.h for a 128-row panel whose pieces leave the
+ * window against a rough weight column (or the reverse): a workgroup keeps its 128-row panel of
+ * A, split, in LDS and walks all N, so A is read and split once instead of once per 128-column
+ * tile.  16 <= K <= 128, K % 16 == 0; A 16-byte aligned, lda a multiple of 4; ldy >= N; bias
+ * may be NULL.  M = 0 is a no-op. */
+int fu_linear_resident(const float* A, int64_t lda, const void* W2, const float* bias, float* Y, int64_t ldy,
+                       int64_t M, int32_t N, int32_t K, void* stream);
 
 /* conv1 m = 0 fused with the gate activation (model.py:152-153 with ops/gating.py:32-103):
  * Y = A W^T + bias with N = (2L+1)C columns (L = lmax) in the gate-paired order: 64-column
