@@ -26,7 +26,7 @@ namespace fu {
 constexpr int RBM = 128;          // rows per workgroup
 constexpr int RKC_MAX = 8;        // 16-wide K chunks: K <= 128
 constexpr int RPLANE = RBM * 16;  // fp16 per plane (one chunk of the panel)
-constexpr int RES = 64 + 4;       // floats per row of a wave's epilogue slice
+constexpr int RES = 64 + 8;       // floats per row of a wave's epilogue slice: 4 RES = 32 mod 64 banks
 
 // The pre-split weight (fu_linear_weight_split), one after the other:
 //  * fp16 planes in MFMA-fragment order: per (32-column block, 16-k chunk), 3 x 64 lanes x 16 B:
