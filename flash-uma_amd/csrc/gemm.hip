@@ -148,7 +148,8 @@ struct GatherA {
 // wave's 64 staged columns are a gate and its values; the epilogue writes Y (kept for the
 // backward), Z and S.  MODE 2 (gate backward): see GateBwd; Y receives g_Y_m0 ((2L+1)C
 // columns).
-template <int MODE, bool SPLIT, bool KTAIL = false, bool TALL = false, bool GATHER = false, bool F16 = false>
+template <int MODE, bool SPLIT, bool KTAIL = false, bool TALL = false, bool GATHER = false, bool F16 = false,
+          bool WF = false>
 __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_kernel(const float* __restrict__ A, int64_t lda, int64_t sA,
                                                           const float* __restrict__ W, int64_t ldw, int64_t sW,
                                                           const float* __restrict__ bias, int64_t sBias,
@@ -156,7 +157,8 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
                                                           int64_t sY, int64_t M, int32_t N, int32_t K,
                                                           int32_t n_tiles, int64_t total_tiles, GateOut go,
                                                           GateBwd gb, Resid rs, LnEpi ln,
-                                                          GatherA gx = GatherA{}) {
+                                                          GatherA gx = GatherA{},
+                                                          const uint4* __restrict__ W2 = nullptr) {
   {
     const int64_t bt = blockIdx.y;
     A += bt * sA;
@@ -169,6 +171,7 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
   static_assert(SPLIT || !TALL, "tall tiles exist in the split mode only");
   static_assert(!GATHER || (SPLIT && !KTAIL && MODE == 1), "the gathered A operand feeds the split gate GEMM");
   static_assert(!F16 || (SPLIT && !GATHER), "the fp16 split is a split mode without the gathered loader");
+  static_assert(!WF || (F16 && TALL && !KTAIL), "pre-split weight fragments feed the tall fp16 tile without a K tail");
   constexpr int RB = TALL ? 4 : 2;          // 32-row blocks per wave
   constexpr int BM = 64 * RB;               // tile rows
   constexpr int PA = BM * GBK, PW = G_PLANE;  // bf16 per A plane, per W plane
@@ -286,8 +289,10 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
           ga2[0] = ld4(pa2 + k0);
           ga2[1] = ld4(pa2 + k0 + 4);
         }
-        gw[0] = ld4(pw + k0);
-        gw[1] = ld4(pw + k0 + 4);
+        if constexpr (!WF) {
+          gw[0] = ld4(pw + k0);
+          gw[1] = ld4(pw + k0 + 4);
+        }
       } else {
         const int gk = k0 + 8 * sh;
         const bool k0ok = gk < K, k1ok = gk + 4 < K;
@@ -336,7 +341,7 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
         };
         put(ga[0], ga[1], scA, b, PA, soff, pmaxA, pminA, lowA);
         if constexpr (TALL) put(ga2[0], ga2[1], scA2, b, PA, plane_off(128 + sr, sh), pmaxA2, pminA2, lowA);
-        put(gw[0], gw[1], scW, b + 2 * PA, PW, soff, pmaxW, pminW, lowW);
+        if constexpr (!WF) put(gw[0], gw[1], scW, b + 2 * PA, PW, soff, pmaxW, pminW, lowW);
       } else {
         uint4 h, m, l;
         split3(ga[0], ga[1], h, m, l);
@@ -355,9 +360,32 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
     const int nk = (K + GBK - 1) / GBK;
     // One K loop.  F16 products per pass kind: 0 lo*hi + hi*lo + hi*hi, 1 lo'*hi + hi*lo',
     // 2 hi*hi.
+    // WF: this wave's two 32-column blocks of the pre-split weight (a block past N reads the
+    // last one; its outputs are never stored)
+    int wfb[2] = {0, 0};
+    if constexpr (WF) {
+      const int nb = (N + 31) / 32;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int b_ = (col0 + wc) / 32 + j;
+        wfb[j] = b_ < nb ? b_ : nb - 1;
+      }
+    }
     auto kloop = [&](auto ps) {
       constexpr int PS = decltype(ps)::value;
       constexpr int QB = PS == 2 ? 2 : 0, QE = PS == 1 ? 2 : 3;
+      // WF: the fragments of chunk kc (hi, and lo or lo' in pass kind 1) straight from the
+      // weight buffer into registers, one chunk ahead
+      f16x8 bnx[2][2];
+      auto load_frags = [&](int kc) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int64_t base = ((int64_t)wfb[j] * nk + kc) * 3 * 64 + lane;
+          bnx[j][0] = __builtin_bit_cast(f16x8, W2[base]);
+          bnx[j][1] = __builtin_bit_cast(f16x8, W2[base + (PS == 1 ? 128 : 64)]);
+        }
+      };
+      if constexpr (WF) load_frags(0);
       load_chunk(0);
       store_chunk(0, ps);
       load_chunk((nk > 1 ? 1 : 0) * GBK);
@@ -366,8 +394,17 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
         const __bf16* b = sp + (kc & 1) * NP * (PA + PW);
         if constexpr (F16) {
           f16x8 bq[2][2];
+          if constexpr (WF) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) ld_planes2(b + 2 * PA, PW, plane_off(wc + 32 * j + fr, fh), bq[j]);
+            for (int j = 0; j < 2; ++j) {
+              bq[j][0] = bnx[j][0];
+              bq[j][1] = bnx[j][1];
+            }
+            load_frags(kc + 1 < nk ? kc + 1 : nk - 1);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) ld_planes2(b + 2 * PA, PW, plane_off(wc + 32 * j + fr, fh), bq[j]);
+          }
 #pragma unroll
           for (int i = 0; i < RB; ++i) {
             f16x8 aq[2];
@@ -419,10 +456,22 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
         return f16_any[0] | f16_any[1] | f16_any[2] | f16_any[3];
       };
       // a thread's verdict bits for its rows (row-level max / min over the two staging threads)
+      // WF: the weight's side from its precomputed flags (the staged column of this thread)
+      int wflag = 0;
+      if constexpr (WF) {
+        const int* flags = reinterpret_cast<const int*>(W2 + resident_frag_vectors(N, K)) + resident_cols(N);
+        wflag = flags[gn < N ? gn : N - 1];
+      }
       auto verdict = [&](float pa, float ga, float pa2, float ga2, float pw, float gw, bool la, bool lw) {
         bool flatA = f16_flat(row_min(ga), row_max(pa));
         if constexpr (TALL) flatA = flatA && f16_flat(row_min(ga2), row_max(pa2));
-        const bool flatW = f16_flat(row_min(gw), row_max(pw));
+        bool flatW;
+        if constexpr (WF) {
+          flatW = (wflag & 2) == 0;
+          lw = (wflag & 1) != 0;
+        } else {
+          flatW = f16_flat(row_min(gw), row_max(pw));
+        }
         return (la ? F16_LOW_A : 0u) | (flatA ? 0u : F16_ROUGH_A) | (lw ? F16_LOW_W : 0u) | (flatW ? 0u : F16_ROUGH_W);
       };
       // exact scales, and the verdict bits at them
@@ -432,13 +481,16 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
 #pragma unroll 4
         for (int kc = 0; kc < nk; ++kc) {
           load_chunk(kc * GBK);
-          const float mA = amax8(ga[0], ga[1]), mW = amax8(gw[0], gw[1]);
+          const float mA = amax8(ga[0], ga[1]);
           RA = fmaxf(RA, mA);
-          RW = fmaxf(RW, mW);
           zA = fminf(zA, mA);
-          zW = fminf(zW, mW);
           gA = fminf(gA, mA > 0.0f ? mA : inf);
-          gW = fminf(gW, mW > 0.0f ? mW : inf);
+          if constexpr (!WF) {
+            const float mW = amax8(gw[0], gw[1]);
+            RW = fmaxf(RW, mW);
+            zW = fminf(zW, mW);
+            gW = fminf(gW, mW > 0.0f ? mW : inf);
+          }
           if constexpr (TALL) {
             const float mA2 = amax8(ga2[0], ga2[1]);
             RA2 = fmaxf(RA2, mA2);
@@ -447,7 +499,7 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
           }
         }
         eA = f16_exp_row(row_max(RA));
-        eW = f16_exp_row(row_max(RW));
+        if constexpr (!WF) eW = f16_exp_row(row_max(RW));
         bool la = f16_lossy(gA * pow2i(eA));
         if constexpr (TALL) {
           eA2 = f16_exp_row(row_max(RA2));
@@ -468,10 +520,10 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
           load_chunk(0);
           const float mA = row_max(fmaxf(amax4(ga[0]), amax4(ga[1])));
           const float mA2 = TALL ? row_max(fmaxf(amax4(ga2[0]), amax4(ga2[1]))) : 1.0f;
-          const float mW = row_max(fmaxf(amax4(gw[0]), amax4(gw[1])));
+          const float mW = WF ? 1.0f : row_max(fmaxf(amax4(gw[0]), amax4(gw[1])));
           eA = f16_exp_chunk(mA);
           if constexpr (TALL) eA2 = f16_exp_chunk(mA2);
-          eW = f16_exp_chunk(mW);
+          if constexpr (!WF) eW = f16_exp_chunk(mW);
           exact = tile_bits(mA == 0.0f || mA2 == 0.0f || mW == 0.0f) != 0;
         }
         if (exact) {
@@ -519,7 +571,10 @@ __global__ __launch_bounds__(256, SPLIT ? (TALL ? 2 : 3) : 4) void linear_mfma_k
       if (sh == 0) {
         f16_rinv[sr] = pow2i(-eA);
         if constexpr (TALL) f16_rinv[128 + sr] = pow2i(-eA2);
-        f16_cinv[sr] = pow2i(-eW);
+        if constexpr (WF)
+          f16_cinv[sr] = reinterpret_cast<const float*>(W2 + resident_frag_vectors(N, K))[gn < N ? gn : N - 1];
+        else
+          f16_cinv[sr] = pow2i(-eW);
       }
       __syncthreads();
       const float c0 = f16_cinv[wc + fr], c1 = f16_cinv[wc + 32 + fr];
@@ -913,6 +968,20 @@ static auto linear_kernel(int32_t K, int64_t M) {
          : mode == FU_MATMUL_SPLIT_F16 ? split_kernel<MODE, true>(K, tall) : split_kernel<MODE, false>(K, tall);
 }
 
+// With a pre-split weight (W2, fu_linear_weight_split of the same N x K weight): the tall fp16
+// tile reading its weight fragments from W2 (split-fp16 mode, tall tiles, K % 16 == 0);
+// otherwise W2 is not used.
+static bool use_w2(const void* W2, int32_t K, int64_t M) {
+  return W2 != nullptr && matmul_mode() == FU_MATMUL_SPLIT_F16 && linear_tile_rows(M) != GBM && K % GBK == 0;
+}
+template <int MODE>
+static auto linear_kernel_w2(int32_t K, int64_t M, const void* W2) {
+  return use_w2(W2, K, M) ? linear_mfma_kernel<MODE, true, false, true, false, true, true> : linear_kernel<MODE>(K, M);
+}
+static int w2_check(const void* W2, const char* who) {
+  return (W2 && !aligned16(W2)) ? set_error(FU_ERR_ALIGN, "%s: W2 must be 16-byte aligned", who) : FU_OK;
+}
+
 static int linear_check(const float* A, int64_t lda, const float* W, int64_t ldw, const float* Y, int64_t ldy,
                         int64_t M, int32_t N, int32_t K, const char* who) {
   if (M < 0 || N <= 0 || K <= 0)
@@ -933,24 +1002,27 @@ static int linear_check(const float* A, int64_t lda, const float* W, int64_t ldw
 static int linear_launch(const float* A, int64_t lda, int64_t sA, const float* W, int64_t ldw, int64_t sW,
                          const float* bias, int64_t sBias, int32_t bias_batches, float* Y, int64_t ldy, int64_t sY,
                          int64_t M, int32_t N, int32_t K, int32_t batch, hipStream_t stream, const char* who,
-                         Resid rs = Resid{}) {
+                         Resid rs = Resid{}, const void* W2 = nullptr) {
   const int n_tiles = (N + GBN - 1) / GBN;
   const int64_t bm = linear_tile_rows(M);
   const int64_t m_tiles = (M + bm - 1) / bm;
   const int64_t total = m_tiles * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
-  auto kern = linear_kernel<0>(K, M);
+  auto kern = linear_kernel_w2<0>(K, M, W2);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, (unsigned)batch), dim3(256), 0, stream, A, lda, sA, W, ldw, sW, bias,
-                     sBias, bias_batches, Y, ldy, sY, M, N, K, n_tiles, total, GateOut{}, GateBwd{}, rs, LnEpi{}, GatherA{});
+                     sBias, bias_batches, Y, ldy, sY, M, N, K, n_tiles, total, GateOut{}, GateBwd{}, rs, LnEpi{}, GatherA{},
+                     static_cast<const uint4*>(W2));
   return check_launch(who);
 }
 
 extern "C" int fu_linear(const float* A, int64_t lda, const float* W, int64_t ldw, const float* bias, float* Y,
-                         int64_t ldy, int64_t M, int32_t N, int32_t K, void* stream) {
+                         int64_t ldy, int64_t M, int32_t N, int32_t K, const void* W2, void* stream) {
   int st = linear_check(A, lda, W, ldw, Y, ldy, M, N, K, "fu_linear");
+  if (st == FU_OK) st = w2_check(W2, "fu_linear");
   if (st != FU_OK) return st;
   if (M == 0) return FU_OK;
-  return linear_launch(A, lda, 0, W, ldw, 0, bias, 0, 1, Y, ldy, 0, M, N, K, 1, as_stream(stream), "fu_linear");
+  return linear_launch(A, lda, 0, W, ldw, 0, bias, 0, 1, Y, ldy, 0, M, N, K, 1, as_stream(stream), "fu_linear",
+                       Resid{}, W2);
 }
 
 extern "C" int fu_linear_batched(const float* A, int64_t lda, int64_t stride_a, const float* W, int64_t ldw,
@@ -971,8 +1043,9 @@ extern "C" int fu_linear_batched(const float* A, int64_t lda, int64_t stride_a, 
 
 extern "C" int fu_linear_gate(const float* A, int64_t lda, const float* W, int64_t ldw, const float* bias, float* Y,
                               int64_t ldy, float* Z, int64_t ldz, float* S, int64_t lds, int64_t M, int32_t C,
-                              int32_t K, int32_t lmax, void* stream) {
+                              int32_t K, int32_t lmax, const void* W2, void* stream) {
   const char* who = "fu_linear_gate";
+  if (w2_check(W2, who) != FU_OK) return FU_ERR_ALIGN;
   if (C <= 0 || C % 64 != 0) return set_error(FU_ERR_UNSUPPORTED, "%s: C=%d must be a multiple of 64", who, C);
   if (lmax < 2 || lmax > 4) return set_error(FU_ERR_UNSUPPORTED, "%s: lmax=%d unsupported (2, 3 or 4)", who, lmax);
   const int32_t N = (2 * lmax + 1) * C;
@@ -988,10 +1061,11 @@ extern "C" int fu_linear_gate(const float* A, int64_t lda, const float* W, int64
   const int64_t bm = linear_tile_rows(M);
   const int64_t total = ((M + bm - 1) / bm) * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
-  auto kern = linear_kernel<1>(K, M);
+  auto kern = linear_kernel_w2<1>(K, M, W2);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), A, lda,
                      (int64_t)0, W, ldw, (int64_t)0, bias, (int64_t)0, 1, Y, ldy, (int64_t)0, M, N, K, n_tiles, total,
-                     GateOut{Z, ldz, S, lds, C, lmax}, GateBwd{}, Resid{}, LnEpi{}, GatherA{});
+                     GateOut{Z, ldz, S, lds, C, lmax}, GateBwd{}, Resid{}, LnEpi{}, GatherA{},
+                     static_cast<const uint4*>(W2));
   return check_launch(who);
 }
 
@@ -1024,15 +1098,16 @@ extern "C" int fu_gather_linear_gate(const float* x, const int64_t* idx_i, const
   hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), x, (int64_t)0, (int64_t)0, W,
                      ldw, (int64_t)0, bias, (int64_t)0, 1, Y, ldy, (int64_t)0, E, N, K, n_tiles, total,
                      GateOut{Z, ldz, nullptr, 0, C, lmax}, GateBwd{}, Resid{}, LnEpi{},
-                     GatherA{x, idx_i, idx_j, wigner, rad, csd, batch, C});
+                     GatherA{x, idx_i, idx_j, wigner, rad, csd, batch, C}, (const uint4*)nullptr);
   return check_launch(who);
 }
 
 extern "C" int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* Wt, int64_t ldw, const float* Y0,
                                   int64_t ldy0, const float* P1, int64_t ldp1, const float* P2, int64_t ldp2,
                                   float* gY0, int64_t ldg, int64_t M, int32_t C, int32_t K, int32_t lmax,
-                                  void* stream) {
+                                  const void* W2, void* stream) {
   const char* who = "fu_linear_gate_bwd";
+  if (w2_check(W2, who) != FU_OK) return FU_ERR_ALIGN;
   if (C <= 0 || C % 64 != 0) return set_error(FU_ERR_UNSUPPORTED, "%s: C=%d must be a multiple of 64", who, C);
   if (lmax < 2 || lmax > 4) return set_error(FU_ERR_UNSUPPORTED, "%s: lmax=%d unsupported (2, 3 or 4)", who, lmax);
   const int32_t N = (lmax + 1) * C;
@@ -1049,10 +1124,11 @@ extern "C" int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* W
   const int64_t bm = linear_tile_rows(M);
   const int64_t total = ((M + bm - 1) / bm) * n_tiles;
   if (total > 0x7fffffffLL) return set_error(FU_ERR_SHAPE, "%s: M too large", who);
-  auto kern = linear_kernel<2>(K, M);
+  auto kern = linear_kernel_w2<2>(K, M, W2);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), gZo, ldgz,
                      (int64_t)0, Wt, ldw, (int64_t)0, (const float*)nullptr, (int64_t)0, 1, gY0, ldg, (int64_t)0, M, N,
-                     K, n_tiles, total, GateOut{}, GateBwd{Y0, ldy0, P1, ldp1, P2, ldp2, C, lmax}, Resid{}, LnEpi{}, GatherA{});
+                     K, n_tiles, total, GateOut{}, GateBwd{Y0, ldy0, P1, ldp1, P2, ldp2, C, lmax}, Resid{}, LnEpi{}, GatherA{},
+                     static_cast<const uint4*>(W2));
   return check_launch(who);
 }
 
@@ -1106,7 +1182,7 @@ extern "C" int fu_linear_ln_silu(const float* A, int64_t lda, int64_t stride_a, 
                      W, ldw, stride_w, bias, stride_bias, bias_batches, Y, ldy, stride_y, M, N, K, n_tiles, total,
                      GateOut{}, GateBwd{}, Resid{},
                      LnEpi{tab_src, tab_dst, ldt, z, isrc, idst, ln_bias, gamma, beta, mean, rstd, G, eps, pre, ldpre,
-                           stride_pre, nullptr, 0}, GatherA{});
+                           stride_pre, nullptr, 0}, GatherA{}, (const uint4*)nullptr);
   return check_launch(who);
 }
 
@@ -1133,15 +1209,17 @@ extern "C" int fu_linear_ln_silu_bwd(const float* A, int64_t lda, const float* W
                      (int64_t)0, (const float*)nullptr, (int64_t)0, 0, g_x, ldgx, (int64_t)0, M, N, K, n_tiles, total,
                      GateOut{}, GateBwd{}, Resid{},
                      LnEpi{tab_src, tab_dst, ldt, z, isrc, idst, ln_bias, gamma, beta, const_cast<float*>(mean),
-                           const_cast<float*>(rstd), G, 0.0f, nullptr, 0, 0, g_out, ldgo}, GatherA{});
+                           const_cast<float*>(rstd), G, 0.0f, nullptr, 0, 0, g_out, ldgo}, GatherA{},
+                     (const uint4*)nullptr);
   return check_launch(who);
 }
 
 extern "C" int fu_linear_dgrad_ln_silu_bwd(const float* A, int64_t lda, const float* W, int64_t ldw, float* g_x,
                                            int64_t ldgx, int64_t M, int32_t K, const float* x, int64_t ldx,
                                            const float* gamma, const float* beta, const float* mean, const float* rstd,
-                                           int32_t G, int32_t group, void* stream) {
+                                           int32_t G, int32_t group, const void* W2, void* stream) {
   const char* who = "fu_linear_dgrad_ln_silu_bwd";
+  if (w2_check(W2, who) != FU_OK) return FU_ERR_ALIGN;
   int st = linear_check(A, lda, W, ldw, g_x, ldgx, M, LN_D, K, who);
   if (st != FU_OK) return st;
   if (G < 1 || group < 0 || group >= G)
@@ -1158,12 +1236,12 @@ extern "C" int fu_linear_dgrad_ln_silu_bwd(const float* A, int64_t lda, const fl
   // the kernel addresses group 0 of its operands; the group's columns and statistics are
   // selected here
   const int64_t go = (int64_t)group * LN_D;
-  auto kern = linear_kernel<5>(K, M);
+  auto kern = linear_kernel_w2<5>(K, M, W2);
   hipLaunchKernelGGL(kern, dim3((unsigned)total, 1u), dim3(256), 0, as_stream(stream), A, lda, (int64_t)0, W, ldw,
                      (int64_t)0, (const float*)nullptr, (int64_t)0, 0, g_x, ldgx, (int64_t)0, M, (int32_t)LN_D, K, 1,
                      total, GateOut{}, GateBwd{}, Resid{},
                      LnEpi{nullptr, nullptr, 0, nullptr, nullptr, nullptr, nullptr, gamma + go, beta + go,
                            const_cast<float*>(mean) + group, const_cast<float*>(rstd) + group, G, 0.0f,
-                           const_cast<float*>(x) + go, ldx, 0, nullptr, 0}, GatherA{});
+                           const_cast<float*>(x) + go, ldx, 0, nullptr, 0}, GatherA{}, static_cast<const uint4*>(W2));
   return check_launch(who);
 }

@@ -28,18 +28,7 @@ constexpr int RKC_MAX = 8;        // 16-wide K chunks: K <= 128
 constexpr int RPLANE = RBM * 16;  // fp16 per plane (one chunk of the panel)
 constexpr int RES = 64 + 8;       // floats per row of a wave's epilogue slice: 4 RES = 32 mod 64 banks
 
-// The pre-split weight (fu_linear_weight_split), one after the other:
-//  * fp16 planes in MFMA-fragment order: per (32-column block, 16-k chunk), 3 x 64 lanes x 16 B:
-//    hi, lo and lo' = 2^11 lo of the column scaled by its exact power of two 2^e(n);
-//  * the unscale factors 2^-e(n), one float per column of the 32-column blocks;
-//  * one int per column of the 32-column blocks: bit 0 set when a piece (8 consecutive k from a
-//    multiple of 8) of the column is nonzero and below the window at the column's scale, bit 1
-//    when the column is not flat (split_f16.h);
-//  * one int (padded to 16 bytes): the OR of the column flags.
-__host__ __device__ inline int64_t resident_frag_vectors(int32_t N, int32_t K) {
-  return (int64_t)((N + 31) / 32) * (K / 16) * 3 * 64;
-}
-__host__ __device__ inline int64_t resident_cols(int32_t N) { return (int64_t)((N + 31) / 32) * 32; }
+// The pre-split weight's layout: split_f16.h (resident_frag_vectors, resident_cols).
 
 __global__ void resident_weight_scale_kernel(const float* __restrict__ W, int64_t ldw, int32_t N, int32_t K,
                                              float* __restrict__ cinv, int* __restrict__ flag) {
@@ -287,15 +276,15 @@ __global__ __launch_bounds__(256, 2) void linear_resident_kernel(const float* __
 }
 
 extern "C" int64_t fu_linear_weight_split_bytes(int32_t N, int32_t K) {
-  if (N <= 0 || K < 16 || K > 16 * RKC_MAX || K % 16 != 0)
-    return set_error(FU_ERR_SHAPE, "fu_linear_weight_split_bytes: N=%d K=%d (16 <= K <= 128, K %% 16 == 0)", N, K);
+  if (N <= 0 || K < 16 || K % 16 != 0)
+    return set_error(FU_ERR_SHAPE, "fu_linear_weight_split_bytes: N=%d K=%d (K a positive multiple of 16)", N, K);
   return resident_frag_vectors(N, K) * 16 + resident_cols(N) * 8 + 16;
 }
 
 extern "C" int fu_linear_weight_split(const float* W, int64_t ldw, int32_t N, int32_t K, void* W2, void* stream) {
   const char* who = "fu_linear_weight_split";
-  if (N <= 0 || K < 16 || K > 16 * RKC_MAX || K % 16 != 0 || ldw < K)
-    return set_error(FU_ERR_SHAPE, "%s: N=%d K=%d ldw=%lld (16 <= K <= 128, K %% 16 == 0)", who, N, K, (long long)ldw);
+  if (N <= 0 || K < 16 || K % 16 != 0 || ldw < K)
+    return set_error(FU_ERR_SHAPE, "%s: N=%d K=%d ldw=%lld (K a positive multiple of 16)", who, N, K, (long long)ldw);
   if (!W || !W2) return set_error(FU_ERR_NULL, "%s: NULL argument", who);
   if (!aligned16(W2)) return set_error(FU_ERR_ALIGN, "%s: W2 must be 16-byte aligned", who);
   uint4* w2 = static_cast<uint4*>(W2);

@@ -157,4 +157,17 @@ __device__ __forceinline__ float amax8(const float4& a, const float4& b) {
 // Rows (or operands) of up to this many 16-wide chunks get the exact scale from a pre-pass.
 constexpr int F16_PREPASS_CHUNKS = 4;
 
+// A pre-split real weight W (N, K) (fu_linear_weight_split), one after the other:
+//  * fp16 planes in MFMA-fragment order: per (32-column block, 16-k chunk), 3 x 64 lanes x 16 B:
+//    hi, lo and lo' = 2^11 lo of the column scaled by its exact power of two 2^e(n);
+//  * the unscale factors 2^-e(n), one float per column of the 32-column blocks;
+//  * one int per column of the 32-column blocks: bit 0 set when a piece (8 consecutive k from a
+//    multiple of 8) of the column is nonzero and below the window at the column's scale, bit 1
+//    when the column is not flat;
+//  * one int (padded to 16 bytes): the OR of the column flags.
+__host__ __device__ inline int64_t resident_frag_vectors(int32_t N, int32_t K) {
+  return (int64_t)((N + 31) / 32) * (K / 16) * 3 * 64;
+}
+__host__ __device__ inline int64_t resident_cols(int32_t N) { return (int64_t)((N + 31) / 32) * 32; }
+
 }  // namespace fu

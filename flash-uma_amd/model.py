@@ -33,7 +33,7 @@ from ops.gather import LAYOUT1_PERM, block_permutation
 from ops.gating import edge_block, gate_paired_rows
 from ops.edge_grad import EdgeGradSink
 from ops.geom import precompute_geometry
-from ops.linear import complex_linear, complex_weight_split, linear
+from ops.linear import complex_linear, complex_weight_split, linear, linear_weight_split
 from ops.lmax import init_node_scatter_lmax, rotate_scatter_lmax, wigner_extend
 from ops.ln_silu import layer_norm_silu
 from ops.node import balance_channels_batched, permute_rows, system_ptr
@@ -137,6 +137,7 @@ class Packed_eSCN_Layer(nn.Module):
 
     def _register(self, name: str, W: torch.Tensor, dtype) -> None:
         W = W.to(dtype).contiguous()
+        self._splits_dev = None  # pre-split copies are rebuilt from the new buffers on next use
         self.register_buffer(name, W)
         self.register_buffer(name + "_t", W.t().contiguous())
 
@@ -166,11 +167,16 @@ class Packed_eSCN_Layer(nn.Module):
     # factor keeps the four-product kernel (no pre-split copy).
     GAUSS_MAX_NORM_RATIO = 10.0
 
+    # the real m = 0 weights whose tall GEMMs read pre-split fragments (linear_weight_split), in
+    # the order conv1_gate_conv2 takes them after the complex splits
+    _REAL = ("W_conv1_m0", "W_conv1_m0_t", "W_conv2_m0", "W_conv2_m0_t")
+
     def _complex_splits(self, dev: torch.device) -> tuple:
         """complex_weight_split of each frozen complex weight and of its transpose pair, in the
-        order conv1_gate_conv2 takes them; built on first use on a device (the weights are
-        frozen), not part of the state dict.  None (four-product kernel) for an unbalanced
-        weight."""
+        order conv1_gate_conv2 takes them, then linear_weight_split of the m = 0 weights and
+        their transposes; built on first use on a device (the weights are frozen), not part of
+        the state dict.  None (four-product kernel) for an unbalanced complex weight, and for a
+        real weight whose K is not a multiple of 16."""
         if getattr(self, "_splits_dev", None) != dev:
             sp = []
             for name in self._COMPLEX:
@@ -182,6 +188,9 @@ class Packed_eSCN_Layer(nn.Module):
                     continue
                 sp.append(complex_weight_split(R, I))
                 sp.append(complex_weight_split(getattr(self, name + "_Rt"), getattr(self, name + "_It_neg")))
+            for name in self._REAL:
+                W = getattr(self, name)
+                sp.append(linear_weight_split(W) if W.shape[1] % 16 == 0 else None)
             self._splits, self._splits_dev = tuple(sp), dev
         return self._splits
 

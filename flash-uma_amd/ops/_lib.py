@@ -23,7 +23,7 @@ F32 = ctypes.c_float
 SZ_P = ctypes.POINTER(ctypes.c_size_t)
 
 # fu_version() of the library these signatures describe (major*10000 + minor*100 + patch).
-ABI_VERSION = 400
+ABI_VERSION = 500
 
 # Argument types of every exported entry point, in header order.
 SIGNATURES: dict[str, list] = {
@@ -46,7 +46,7 @@ SIGNATURES: dict[str, list] = {
     "fu_ln_silu_bwd": [P, P, P, P, P, P, P, I64, I32, P],
     "fu_ln_silu_grouped_fwd": [P, I64, P, P, I64, P, P, P, P, P, P, P, I64, P, P, I64, I32, I32, F32, P],
     "fu_ln_silu_grouped_bwd": [P, I64, P, P, I64, P, P, P, P, P, P, P, P, P, I64, P, I64, I64, I32, I32, P],
-    "fu_linear": [P, I64, P, I64, P, P, I64, I64, I32, I32, P],
+    "fu_linear": [P, I64, P, I64, P, P, I64, I64, I32, I32, P, P],
     "fu_linear_batched": [P, I64, I64, P, I64, I64, P, I64, I32, P, I64, I64, P, I64, I64, I64, I32, I32, I32, P],
     "fu_complex_linear": [P, P, I64, P, P, I64, P, P, P, I64, I64, I32, I32, P],
     "fu_complex_weight_split_bytes": [I32, I32],
@@ -54,15 +54,15 @@ SIGNATURES: dict[str, list] = {
     "fu_linear_weight_split_bytes": [I32, I32],
     "fu_linear_weight_split": [P, I64, I32, I32, P, P],
     "fu_linear_resident": [P, I64, P, P, P, I64, I64, I32, I32, P],
-    "fu_linear_gate": [P, I64, P, I64, P, P, I64, P, I64, P, I64, I64, I32, I32, I32, P],
+    "fu_linear_gate": [P, I64, P, I64, P, P, I64, P, I64, P, I64, I64, I32, I32, I32, P, P],
     "fu_gather_linear_gate": [P, P, P, P, P, P, P, P, I64, P, P, I64, P, I64, I64, I32, P],
     "fu_complex_linear_gate": [P, P, I64, P, P, I64, P, P, P, I64, P, P, I64, P, I64, I32, I32, I64, I32, I32, P],
-    "fu_linear_gate_bwd": [P, I64, P, I64, P, I64, P, I64, P, I64, P, I64, I64, I32, I32, I32, P],
+    "fu_linear_gate_bwd": [P, I64, P, I64, P, I64, P, I64, P, I64, P, I64, I64, I32, I32, I32, P, P],
     "fu_linear_ln_silu": [P, I64, I64, P, I64, I64, P, I64, I32, P, I64, I64, P, I64, I64, I64, I32, I32, I32,
                           P, P, I64, P, P, P, P, P, P, P, P, I32, F32, P],
     "fu_linear_ln_silu_bwd": [P, I64, P, I64, P, I64, I64, I32, I32, P, I64, P, P, I64, P, P, P, P, P, P, P, P,
                               I32, P],
-    "fu_linear_dgrad_ln_silu_bwd": [P, I64, P, I64, P, I64, I64, I32, P, I64, P, P, P, P, I32, I32, P],
+    "fu_linear_dgrad_ln_silu_bwd": [P, I64, P, I64, P, I64, I64, I32, P, I64, P, P, P, P, I32, I32, P, P],
     "fu_complex_linear_gate_bwd": [P, P, I64, P, P, I64, P, P, P, I64, P, P, I64, P, I64, I32, I32, P, I64, I64, I32, I32, P],
     "fu_rms_norm_sh_fwd": [P, P, P, P, P, I64, I32, I32, F32, P],
     "fu_rms_norm_sh_bwd": [P, P, P, P, P, P, I64, I32, I32, P],

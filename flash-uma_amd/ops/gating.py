@@ -91,13 +91,15 @@ def _gather_conv1_gate_m0(ops, W0, b0, C, st):
     return Y0, Z0
 
 
-def _conv1_gate_m0(X0, W0, b0, C, L, st):
-    """fu_linear_gate: Y0 (gate-paired pre-activations, kept for the backward) and Z0."""
+def _conv1_gate_m0(X0, W0, b0, C, L, st, W2=None):
+    """fu_linear_gate: Y0 (gate-paired pre-activations, kept for the backward) and Z0; W2: W0
+    pre-split (linear_weight_split) or None."""
     E = X0.shape[0]
     Y0 = torch.empty(E, (2 * L + 1) * C, device=X0.device, dtype=torch.float32)
     Z0 = torch.empty(E, (L + 1) * C, device=X0.device, dtype=torch.float32)
     _lib.call("fu_linear_gate", X0.data_ptr(), X0.stride(0), W0.data_ptr(), W0.stride(0), _lib.ptr(b0),
-              Y0.data_ptr(), Y0.stride(0), Z0.data_ptr(), Z0.stride(0), None, 0, E, C, W0.shape[1], L, st)
+              Y0.data_ptr(), Y0.stride(0), Z0.data_ptr(), Z0.stride(0), None, 0, E, C, W0.shape[1], L, _lib.ptr(W2),
+              st)
     return Y0, Z0
 
 
@@ -157,6 +159,14 @@ def conv1_gate(X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C,
     return Conv1Gate.apply(X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C, splits)
 
 
+def _splits12(splits):
+    """The 12 pre-split weights of a conv pair: the complex W3 of conv1 m = 1, 2 and conv2
+    m = 1, 2 with their transpose pairs, then linear_weight_split of W0, W0t, V0, V0t (None
+    where absent)."""
+    sp = tuple(splits) if splits else ()
+    return sp + (None,) * (12 - len(sp))
+
+
 def conv_pair_fwd(X: list, conv1, conv2, C: int, splits, m0=None):
     """conv1 + gate + conv2 of one block on X = [X_m0, X_m1, X_m2].  Each entry of X is set
     to None once its GEMM has read it, so a caller that hands over its only references
@@ -167,9 +177,9 @@ def conv_pair_fwd(X: list, conv1, conv2, C: int, splits, m0=None):
     V0, c0, V0t, R1, I1, R1t, I1tn, R2, I2, R2t, I2tn = conv2
     st = _lib.stream_ptr(X[1].device)
     L = _degrees(W0, C)
-    sp = splits or (None,) * 8
+    sp = _splits12(splits)
     if m0 is None:
-        Y0, Z0 = _conv1_gate_m0(_lib.require(X[0], torch.float32, "X_m0"), W0, b0, C, L, st)
+        Y0, Z0 = _conv1_gate_m0(_lib.require(X[0], torch.float32, "X_m0"), W0, b0, C, L, st, sp[8])
     else:
         Y0, Z0 = m0
     X[0] = None
@@ -177,7 +187,7 @@ def conv_pair_fwd(X: list, conv1, conv2, C: int, splits, m0=None):
     X[1] = X[2] = None
     Y1, Z1, Y2, Z2 = _conv1_gate_m12(X1, X2, P1, Q1, P2, Q2, sp[0], sp[2], Y0, C, st)
     del X1, X2
-    Zo0 = gemm(Z0, V0, c0)
+    Zo0 = gemm(Z0, V0, c0, W2=sp[10])
     del Z0
     Zo1 = complex_gemm(Z1, R1, I1, sp[4])
     del Z1
@@ -199,7 +209,7 @@ def conv_pair_bwd(Y, conv1, conv2, C: int, splits, g: list):
     dev = Y0.device
     st = _lib.stream_ptr(dev)
     f = lambda *s: torch.empty(*s, device=dev, dtype=torch.float32)
-    sp = splits or (None,) * 8
+    sp = _splits12(splits)
     g0 = torch.zeros(E, (L + 1) * C, device=dev) if g[0] is None else g[0].contiguous()
     g1 = torch.zeros(E, 2 * L * C, device=dev) if g[1] is None else g[1].contiguous()
     g2 = torch.zeros(E, 2 * (L - 1) * C, device=dev) if g[2] is None else g[2].contiguous()
@@ -218,11 +228,11 @@ def conv_pair_bwd(Y, conv1, conv2, C: int, splits, g: list):
     gy0 = f(E, (2 * L + 1) * C)
     _lib.call("fu_linear_gate_bwd", g0.data_ptr(), g0.stride(0), V0t.data_ptr(), V0t.stride(0), Y0.data_ptr(),
               Y0.stride(0), psums[0].data_ptr(), psums[0].stride(0), psums[1].data_ptr(), psums[1].stride(0),
-              gy0.data_ptr(), gy0.stride(0), E, C, V0t.shape[1], L, st)
+              gy0.data_ptr(), gy0.stride(0), E, C, V0t.shape[1], L, _lib.ptr(sp[11]), st)
     # release each intermediate as soon as it is consumed: the backward of a block runs near
     # the step's memory peak (every earlier layer's saved tensors are still alive)
     del psums, g0
-    g_x0 = gemm(gy0, W0t)
+    g_x0 = gemm(gy0, W0t, W2=sp[9])
     del gy0
     g_x1 = complex_gemm(gys[0], P1t, Q1tn, sp[1])
     gys[0] = None

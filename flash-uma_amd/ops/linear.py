@@ -10,8 +10,9 @@ from . import _lib
 
 
 def gemm(x: torch.Tensor, W: torch.Tensor, bias: torch.Tensor | None = None,
-         out: torch.Tensor | None = None) -> torch.Tensor:
-    """out[M, N] = x[M, K] @ W[N, K]^T (+ bias).  x may be a row-strided view."""
+         out: torch.Tensor | None = None, W2: torch.Tensor | None = None) -> torch.Tensor:
+    """out[M, N] = x[M, K] @ W[N, K]^T (+ bias).  x may be a row-strided view.  W2: W pre-split by
+    linear_weight_split, read instead of W where fu_linear can (split-fp16 mode, tall tiles)."""
     if x.stride(-1) != 1:
         x = x.contiguous()
     M, K = x.shape
@@ -22,7 +23,7 @@ def gemm(x: torch.Tensor, W: torch.Tensor, bias: torch.Tensor | None = None,
         out = torch.empty((M, N), device=x.device, dtype=torch.float32)
     _lib.call("fu_linear", x.data_ptr(), x.stride(0), W.data_ptr(), W.stride(0),
               None if bias is None else bias.data_ptr(), out.data_ptr(), out.stride(0), M, N, K,
-              _lib.stream_ptr(x.device))
+              _lib.ptr(W2), _lib.stream_ptr(x.device))
     return out
 
 

@@ -117,11 +117,11 @@ def _layer1_bwd(gauss, bank, Z, idx_i, idx_j, m1, r1, g_h1):
     return g_p1
 
 
-def _gemm(A, W, bias, out):
+def _gemm(A, W, bias, out, W2=None):
     M, K = A.shape
     N = W.shape[0]
     _lib.call("fu_linear", A.data_ptr(), A.stride(0), W.data_ptr(), W.stride(0), _lib.ptr(bias), out.data_ptr(),
-              out.stride(0), M, N, K, _lib.stream_ptr(A.device))
+              out.stride(0), M, N, K, _lib.ptr(W2), _lib.stream_ptr(A.device))
     return out
 
 
@@ -175,16 +175,24 @@ class RadialBank(torch.nn.Module):
     # reserve then grew from 31 to 230 GB on the 8,192-atom Fe cell, and the allocations
     # on that path stalled the host for seconds in some processes.
 
-    def out_split(self, k: int):
-        """Output layer k's weight pre-split for fu_linear_resident, built on first use on a device
-        (None when its K is outside that kernel's range).  Weights are frozen."""
-        W = getattr(self, f"W3_{k}")
-        if not resident_ok(W.shape[1]):
+    def _split(self, name: str, ok):
+        """linear_weight_split of buffer `name`, built on first use on its device (None when `ok`
+        rejects its K).  Weights are frozen."""
+        W = getattr(self, name)
+        if not ok(W.shape[1]):
             return None
-        cache = self.__dict__.setdefault("_out_splits", {})
-        if k not in cache or cache[k].device != W.device:
-            cache[k] = linear_weight_split(W)
-        return cache[k]
+        cache = self.__dict__.setdefault("_weight_splits", {})
+        if name not in cache or cache[name].device != W.device:
+            cache[name] = linear_weight_split(W)
+        return cache[name]
+
+    def out_split(self, k: int):
+        """Output layer k's weight pre-split for fu_linear_resident (None outside its K range)."""
+        return self._split(f"W3_{k}", resident_ok)
+
+    def out_t_split(self, k: int):
+        """Output layer k's transposed weight pre-split for its input-gradient GEMM."""
+        return self._split(f"W3_{k}_t", lambda K: K % 16 == 0)
 
     def forward(self, gauss, Z, idx_i, idx_j, with_sources: bool = False):
         """gauss (E, B) -> tuple of G radial outputs (E, n_k).
@@ -200,7 +208,7 @@ class RadialBank(torch.nn.Module):
         for k in range(self.G):
             W, Wt, b = getattr(self, f"W3_{k}"), getattr(self, f"W3_{k}_t"), getattr(self, f"b3_{k}")
             W2 = self.out_split(k)
-            outs.append(_RadialOutFn.apply(h2s[k], W, b, Wt, holder, k, W2))
+            outs.append(_RadialOutFn.apply(h2s[k], W, b, Wt, holder, k, W2, self.out_t_split(k)))
             srcs.append((h2s[k].detach(), W, b, W2))
         holder.ln = None
         return (tuple(outs), tuple(srcs)) if with_sources else tuple(outs)
@@ -294,7 +302,8 @@ class _RadialTrunkFn(torch.autograd.Function):
         del g_p2
         g_p1 = _layer1_bwd(gauss, bank, Z, idx_i, idx_j, m1, r1, g_h1)
         del g_h1
-        g_gauss = _gemm(g_p1, bank.W1g_t, None, torch.empty(E, bank.B, device=gauss.device, dtype=torch.float32))
+        g_gauss = _gemm(g_p1, bank.W1g_t, None, torch.empty(E, bank.B, device=gauss.device, dtype=torch.float32),
+                        bank._split("W1g_t", lambda K: K % 16 == 0))
         return g_gauss, None, None, None, None, None
 
 
@@ -305,8 +314,8 @@ class _RadialOutFn(torch.autograd.Function):
     LayerNorm-SiLU backward in its epilogue, g_h2_k never stored), otherwise g_h2_k."""
 
     @staticmethod
-    def forward(ctx, h2k, W, b, Wt, holder, k, W2=None):
-        ctx.holder, ctx.k = holder, k
+    def forward(ctx, h2k, W, b, Wt, holder, k, W2=None, W2t=None):
+        ctx.holder, ctx.k, ctx.W2t = holder, k, W2t
         # (p2, mean, rstd, gamma, beta) of the trunk's forward are saved like the weight, so
         # that they are released after the backward (a plain ctx attribute would keep p2 alive
         # as long as the graph's nodes, i.e. into the next step)
@@ -322,12 +331,13 @@ class _RadialOutFn(torch.autograd.Function):
         buf = ctx.holder.buffer()
         sl = buf[:, ctx.k * C:(ctx.k + 1) * C]
         if ctx.ln_groups is None:
-            _gemm(g_rad, Wt, None, sl)
+            _gemm(g_rad, Wt, None, sl, ctx.W2t)
         else:
             p2, m2, r2, gamma, beta = ln
             G = ctx.ln_groups
             M, K = g_rad.shape
             _lib.call("fu_linear_dgrad_ln_silu_bwd", g_rad.data_ptr(), g_rad.stride(0), Wt.data_ptr(), Wt.stride(0),
                       sl.data_ptr(), buf.stride(0), M, K, p2.data_ptr(), p2.stride(0), gamma.data_ptr(),
-                      beta.data_ptr(), m2.data_ptr(), r2.data_ptr(), G, ctx.k, _lib.stream_ptr(g_rad.device))
-        return sl, None, None, None, None, None, None
+                      beta.data_ptr(), m2.data_ptr(), r2.data_ptr(), G, ctx.k, _lib.ptr(ctx.W2t),
+                      _lib.stream_ptr(g_rad.device))
+        return sl, None, None, None, None, None, None, None

@@ -42,13 +42,15 @@ extern "C" {
 #define FU_ERR_NULL (-5)        /* a required pointer is NULL */
 #define FU_ERR_WORKSPACE (-6)   /* the workspace is too small */
 
-/* Library version (major*10000 + minor*100 + patch): 400 (0.4.0) for the signatures in this
+/* Library version (major*10000 + minor*100 + patch): 500 (0.5.0) for the signatures in this
  * header.  0.2.0 added the int32 `accumulate` argument (before the stream) of fu_gather_bwd,
  * fu_scatter_bwd, fu_init_scatter_bwd, their _lmax forms and fu_complex_linear_gate(_bwd), and
  * dropped one pointer/stride pair of fu_linear_gate_bwd; 0.3.0 changed the layout and size of
  * the fu_complex_weight_split buffer (fu_complex_weight_split_bytes) and added the four CSR
  * arguments of fu_gather_fwd_lmax; 0.4.0 added fu_linear_weight_split_bytes,
- * fu_linear_weight_split and fu_linear_resident (nothing changed).  A caller built against
+ * fu_linear_weight_split and fu_linear_resident (nothing changed); 0.5.0 added the W2 argument
+ * (before the stream) of fu_linear, fu_linear_gate, fu_linear_gate_bwd and
+ * fu_linear_dgrad_ln_silu_bwd.  A caller built against
  * another version must not call into this library. */
 int fu_version(void);
 
@@ -266,7 +268,7 @@ int fu_linear_dgrad_ln_silu_bwd(const float* A, int64_t lda, const float* W, int
                                 float* g_x, int64_t ldgx, int64_t M, int32_t K, const float* x,
                                 int64_t ldx, const float* gamma, const float* beta,
                                 const float* mean, const float* rstd, int32_t G, int32_t group,
-                                void* stream);
+                                const void* W2, void* stream);
 
 /* ------------------------------------------------------------------------------------
  * Dense contractions on fp32 MFMA (replaces torch F.linear at model.py:147-154,203-205)
@@ -274,9 +276,15 @@ int fu_linear_dgrad_ln_silu_bwd(const float* A, int64_t lda, const float* W, int
 
 /* Y[M, N] = A[M, K] @ W[N, K]^T (+ bias[N] when non-NULL), fp32 in and out, fp32 MFMA
  * accumulation.  lda/ldw/ldy are row strides in floats; K, N, lda, ldw and ldy must be
- * multiples of 4 and A, W, Y 16-byte aligned. */
+ * multiples of 4 and A, W, Y 16-byte aligned.
+ * W2 (here and in fu_linear_gate, fu_linear_gate_bwd, fu_linear_dgrad_ln_silu_bwd): NULL, or
+ * the same weight pre-split by fu_linear_weight_split (16-byte aligned).  In matrix-core mode 2
+ * with tall tiles (M >= 65,536) and K % 16 == 0 the kernel then loads its weight fragments from
+ * W2 straight into registers (exact column scales and window flags from W2) instead of staging
+ * and splitting W; otherwise W2 is not read.  No reference counterpart (an argument of this
+ * build's kernels). */
 int fu_linear(const float* A, int64_t lda, const float* W, int64_t ldw, const float* bias,
-              float* Y, int64_t ldy, int64_t M, int32_t N, int32_t K, void* stream);
+              float* Y, int64_t ldy, int64_t M, int32_t N, int32_t K, const void* W2, void* stream);
 
 /* Strided batch of fu_linear in one launch: for b < batch,
  * Y_b = A_b @ W_b^T (+ bias_b for b < bias_batches) (+ R_b), X_b = X + b * stride_x (floats).
@@ -322,9 +330,10 @@ int64_t fu_complex_weight_split_bytes(int32_t Nc, int32_t Kc);
 int fu_complex_weight_split(const float* P, const float* Q, int64_t ldw, int32_t Nc, int32_t Kc, void* W3,
                             void* stream);
 
-/* Pre-split real weight for fu_linear_resident; no reference counterpart (a frozen weight of
- * model.py:147-149, 203-205, prepared once at freeze time).  W (N, K) with row stride ldw,
- * 16 <= K <= 128, K % 16 == 0.  W2 receives the fp16 splits of every column n scaled by its
+/* Pre-split real weight for fu_linear_resident and the W2 argument of fu_linear and its
+ * relatives; no reference counterpart (a frozen weight of model.py:147-154, 203-205, prepared
+ * once at freeze time).  W (N, K) with row stride ldw, K a positive multiple of 16
+ * (fu_linear_resident: K <= 128).  W2 receives the fp16 splits of every column n scaled by its
  * exact power of two 2^e(n) in MFMA-fragment order ([32-column block][16-k chunk][hi, lo, lo'
  * = 2^11 lo][64 lanes] x 16 bytes, zero padded to N = 32 n), then the factors 2^-e(n) (one float
  * per padded column), then one int32 per padded column (bit 0: 8 consecutive k below the fp16
@@ -355,7 +364,7 @@ int fu_linear_resident(const float* A, int64_t lda, const void* W2, const float*
  * lmax 2..4; C a multiple of 64; other constraints as fu_linear. */
 int fu_linear_gate(const float* A, int64_t lda, const float* W, int64_t ldw, const float* bias,
                    float* Y, int64_t ldy, float* Z, int64_t ldz, float* S, int64_t lds, int64_t M,
-                   int32_t C, int32_t K, int32_t lmax, void* stream);
+                   int32_t C, int32_t K, int32_t lmax, const void* W2, void* stream);
 
 /* conv1 m = 0 with its A operand gathered in the GEMM loader (the gather-rotate fused with the
  * m = 0 SO(2) linear, ops/gather.py:128-154 -> model.py:152, lmax 2): the result of
@@ -391,7 +400,7 @@ int fu_complex_linear_gate(const float* A_r, const float* A_i, int64_t lda, cons
 int fu_linear_gate_bwd(const float* gZo, int64_t ldgz, const float* Wt, int64_t ldw, const float* Y0,
                        int64_t ldy0, const float* P1, int64_t ldp1, const float* P2, int64_t ldp2,
                        float* gY0, int64_t ldg, int64_t M, int32_t C, int32_t K, int32_t lmax,
-                       void* stream);
+                       const void* W2, void* stream);
 
 /* conv2 m = 1 or 2 input gradient fused with the gate backward: the complex product
  * g_Z = (A_r + i A_i)(P + iQ)^T (P = R^T, Q = -I^T of the conv2 weight) is not stored;

@@ -43,9 +43,9 @@ def test_error_codes():
     assert st == -5
     st, _ = _status("fu_gating_fwd", None, None, None, None, None, None, -1, 128, 0, None)
     assert st == -1
-    st, msg = _status("fu_linear", 16, 8, 16, 8, None, 16, 8, 10, 8, 6, None)
+    st, msg = _status("fu_linear", 16, 8, 16, 8, None, 16, 8, 10, 8, 6, None, None)
     assert st == -2 and "multiples of 4" in msg
-    st, _ = _status("fu_linear", 3, 8, 16, 8, None, 16, 8, 10, 8, 8, None)
+    st, _ = _status("fu_linear", 3, 8, 16, 8, None, 16, 8, 10, 8, 8, None, None)
     assert st == -3
     st, _ = _status("fu_gather_fwd", *([None] * 10), 5, 5, 1, 96, 0, None)
     assert st == -2
@@ -75,10 +75,10 @@ def test_error_codes():
     assert st == -1 and "ldw" in msg
     # the output-layer gradient GEMM with the LayerNorm backward: one group of G
     st, msg = _status("fu_linear_dgrad_ln_silu_bwd", None, 64, None, 64, None, 640, 0, 64, None, 640, *([None] * 4),
-                      5, 5, None)
+                      5, 5, None, None)
     assert st == -1 and "group=5" in msg
     st, msg = _status("fu_linear_dgrad_ln_silu_bwd", None, 64, None, 64, None, 640, 0, 64, None, 512, *([None] * 4),
-                      5, 0, None)
+                      5, 0, None, None)
     assert st == -1 and "ldx=512" in msg
     # accumulate flags: bit 0 (wigner rows), bit 1 (env); nothing else
     for name, args in (("fu_scatter_bwd", (*([None] * 12), 0, 5, 128)),
@@ -96,7 +96,7 @@ def test_zero_sized_calls_are_no_ops():
     # E == 0 returns before any launch
     st, _ = _status("fu_gating_fwd", 16, 16, 16, 16, 16, 16, 0, 128, 0, None)
     assert st == 0
-    st, _ = _status("fu_linear", 16, 8, 16, 8, None, 16, 8, 0, 8, 8, None)
+    st, _ = _status("fu_linear", 16, 8, 16, 8, None, 16, 8, 0, 8, 8, None, None)
     assert st == 0
 
 
@@ -110,12 +110,12 @@ def test_zero_rows_accept_empty_arrays():
         "fu_geom_bwd": (*([None] * 6), 8, None, None, None, 0, 5, 8, f(6.0), f(-1.0), None),
         "fu_gating_fwd": (*([None] * 6), 0, 128, 1, None),
         "fu_gating_bwd": (*([None] * 9), 0, 128, 1, None),
-        "fu_linear": (None, 16, None, 16, None, None, 16, 0, 16, 16, None),
+        "fu_linear": (None, 16, None, 16, None, None, 16, 0, 16, 16, None, None),
         "fu_linear_batched": (None, 640, 128, None, 128, 16384, None, 128, 5, None, 0, 0, None, 640, 128, 0, 128,
                               128, 5, None),
-        "fu_linear_gate": (None, 768, None, 768, None, None, 640, None, 384, None, 256, 0, 128, 768, 2, None),
+        "fu_linear_gate": (None, 768, None, 768, None, None, 640, None, 384, None, 256, 0, 128, 768, 2, None, None),
         "fu_linear_gate_bwd": (None, 384, None, 384, None, 640, None, 256, None, 128, None, 640, 0, 128, 384, 2,
-                               None),
+                               None, None),
         "fu_complex_linear": (None, None, 256, None, None, 256, None, None, None, 128, 0, 128, 256, None),
         "fu_complex_linear_gate": (None, None, 256, None, None, 256, None, None, None, 128, None, None, 128, None,
                                    640, 0, 128, 0, 128, 256, None),
@@ -138,14 +138,15 @@ def test_zero_rows_accept_empty_arrays():
                               *([None] * 2), 0, *([None] * 8), 5, f(1e-5), None),
         "fu_linear_ln_silu_bwd": (None, 64, None, 64, None, 640, 0, 640, 64, None, 640, *([None] * 2), 0,
                                   *([None] * 8), 5, None),
-        "fu_linear_dgrad_ln_silu_bwd": (None, 64, None, 64, None, 640, 0, 64, None, 640, *([None] * 4), 5, 4, None),
+        "fu_linear_dgrad_ln_silu_bwd": (None, 64, None, 64, None, 640, 0, 64, None, 640, *([None] * 4), 5, 4, None,
+                                        None),
         "fu_gather_linear_gate": (*([None] * 7), None, 768, None, None, 640, None, 384, 0, 128, None),
     }
     for name, args in calls.items():
         st, msg = _status(name, *args)
         assert st == 0, (name, msg)
     # the shape checks still run with zero rows
-    st, _ = _status("fu_linear", None, 16, None, 16, None, None, 16, 0, 16, 6, None)
+    st, _ = _status("fu_linear", None, 16, None, 16, None, None, 16, 0, 16, 6, None, None)
     assert st == -2
     st, _ = _status("fu_complex_linear_gate", None, None, 256, None, None, 256, None, None, None, 128, None, None,
                     64, None, 640, 0, 128, 0, 128, 256, None)

@@ -907,7 +907,7 @@ def test_linear_ln_silu_matches_two_kernels(cuda, matmul_mode, M):
         _gemm(g_rad, W3t, None, g_h2[:, k * C:(k + 1) * C])
         _lib.call("fu_linear_dgrad_ln_silu_bwd", g_rad.data_ptr(), n, W3t.data_ptr(), n, g_p2[:, k * C:].data_ptr(),
                   G * C, M, n, p2.data_ptr(), G * C, gm2.data_ptr(), bt2.data_ptr(), m2.data_ptr(), r2.data_ptr(), G,
-                  k, st)
+                  k, None, st)
     gref2 = _ln_grouped_bwd(p2, None, None, None, None, None, gm2, bt2, m2, r2, g_h2, G, C)
     assert_close(g_p2, gref2, 2e-6, "layer-2 LayerNorm input gradient")
 
@@ -938,7 +938,7 @@ def test_gather_linear_gate_matches_gather_then_gemm(cuda, E):
     X0, X1, X2 = gather_fwd(x, ii, jj, wig, rad, csd, batch, 1)
     Y, Z = torch.empty(E, 5 * C, device=cuda), torch.empty(E, 3 * C, device=cuda)
     _lib.call("fu_linear_gate", X0.data_ptr(), 6 * C, W.data_ptr(), 6 * C, b.data_ptr(), Y.data_ptr(), 5 * C,
-              Z.data_ptr(), 3 * C, None, 0, E, C, 6 * C, 2, st)
+              Z.data_ptr(), 3 * C, None, 0, E, C, 6 * C, 2, None, st)
     none, X1s, X2s = gather_fwd(x, ii, jj, wig, rad, csd, batch, 1, skip_m0=True)
     assert none is None and torch.equal(X1s, X1) and torch.equal(X2s, X2)
     Yf, Zf = torch.empty_like(Y), torch.empty_like(Z)

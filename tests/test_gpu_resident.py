@@ -152,8 +152,13 @@ def test_resident_dynamic_range(cuda):
 def test_resident_rejects_bad_shapes(cuda):
     _lib, linear = _ops()
     lib = _lib.load()
-    for N, K in ((0, 128), (64, 8), (64, 100), (64, 144)):
+    for N, K in ((0, 128), (64, 8), (64, 100)):
         assert lib.fu_linear_weight_split_bytes(N, K) < 0, (N, K)
+    # the split serves any K % 16 == 0 (the tall GEMMs' W2); the resident GEMM takes K <= 128
+    W144 = linear.linear_weight_split(torch.randn(64, 144, device=cuda))
+    x144 = torch.randn(10, 144, device=cuda)
+    with pytest.raises(_lib.FlashUMAError):
+        linear.gemm_resident(x144, W144, 64)
     W = torch.randn(64, 100, device=cuda)
     with pytest.raises(_lib.FlashUMAError):
         linear.linear_weight_split(W)
