@@ -557,10 +557,10 @@ __global__ __launch_bounds__(threads_of(PATH), wg_per_cu(PATH)) void complex_lin
       int gc = col0 + wc + (lin & 7) * 4;
       gc = gc < Nc ? gc : 0;
       const int t = g.s_off + gc, l1 = t / g.C, ch = t - l1 * g.C;
-      eg[set][q] = ld4(g.G + row * g.ldg + 64 * (l1 * (g.C >> 5) + (ch >> 5)) + (ch & 31));
+      eg[set][q] = ld4_nt(g.G + row * g.ldg + 64 * (l1 * (g.C >> 5) + (ch >> 5)) + (ch & 31));
       if constexpr (MODE == 2) {
-        efr[set][q] = ld4(g.Fr + row * g.ldf + gc);
-        efi[set][q] = ld4(g.Fi + row * g.ldf + gc);
+        efr[set][q] = ld4_nt(g.Fr + row * g.ldf + gc);
+        efi[set][q] = ld4_nt(g.Fi + row * g.ldf + gc);
       }
     }
   };

@@ -83,6 +83,12 @@ __device__ __forceinline__ float sigmoidf_(float x) {
 }
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+// 16-byte load with the nontemporal hint (operands streamed once)
+__device__ __forceinline__ float4 ld4_nt(const float* p) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const f4 t = __builtin_nontemporal_load(reinterpret_cast<const f4*>(p));
+  return make_float4(t.x, t.y, t.z, t.w);
+}
 __device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
 // 16-byte store with the nontemporal hint (large write-once outputs)
 __device__ __forceinline__ void st4_nt(float* p, float4 v) {
