@@ -255,3 +255,34 @@ def test_binding_types_match_header():
                 assert g is w, (name, k, g, w)
         checked += 1
     assert checked == len(_lib.SIGNATURES)
+
+
+def test_linear_weight_split_arguments():
+    # per (32-column, 16-k) block: hi, lo and lo' planes x 64 lanes x 16 B; then 32 column
+    # factors and 32 column flags per block (2 x 128 B) and the 16-byte summary word
+    st, _ = _status("fu_linear_weight_split_bytes", 32, 16)
+    assert st == 3 * 64 * 16 + 2 * 128 + 16
+    st, _ = _status("fu_linear_weight_split_bytes", 33, 768)
+    assert st == 2 * 48 * 3 * 64 * 16 + 2 * 2 * 128 + 16
+    for N, K in ((0, 16), (32, 8), (32, 100)):
+        st, _ = _status("fu_linear_weight_split_bytes", N, K)
+        assert st == -1, (N, K)
+    st, _ = _status("fu_linear_weight_split", None, 16, 32, 16, None, None)
+    assert st == -5
+    st, msg = _status("fu_linear_weight_split", 16, 16, 32, 16, 8, None)
+    assert st == -3 and "aligned" in msg
+    # a misaligned W2 is rejected before any launch, by every entry point that takes one
+    st, msg = _status("fu_linear", 16, 16, 16, 16, None, 16, 16, 10, 16, 16, 8, None)
+    assert st == -3 and "W2" in msg
+    st, msg = _status("fu_linear_gate", 16, 768, 16, 768, None, 16, 640, 16, 384, None, 256, 10, 128, 768, 2, 8,
+                      None)
+    assert st == -3 and "W2" in msg
+    st, msg = _status("fu_linear_gate_bwd", 16, 384, 16, 384, 16, 640, 16, 256, 16, 128, 16, 640, 10, 128, 384, 2,
+                      8, None)
+    assert st == -3 and "W2" in msg
+    st, msg = _status("fu_linear_dgrad_ln_silu_bwd", 16, 64, 16, 64, 16, 640, 10, 64, 16, 640, 16, 16, 16, 16, 5,
+                      0, 8, None)
+    assert st == -3 and "W2" in msg
+    # the resident GEMM takes K <= 128 only
+    st, msg = _status("fu_linear_resident", 16, 144, 16, None, 16, 64, 10, 64, 144, None)
+    assert st == -1 and "K=144" in msg
