@@ -23,7 +23,8 @@
 // while the other operand has a row that is not flat (or a piece overflowed).  The passes:
 //  0. scales from the first chunk: the maximum m of the row's first 16 elements is mapped to
 //     [2^6, 2^7) (256x of headroom above it), with no pass over the data; the pieces are
-//     tracked as they are staged;
+//     tracked as they are staged (A's are not when a pre-split weight's columns are all flat
+//     with no piece below the window: the rule above can then not fail on A's account);
 //  1. exact scales, from a pass over the rows: e = 14 - floor(log2 R), R the row's largest
 //     magnitude (R 2^e in [2^14, 2^15)), so pieces down to 2^-17 R stay in the window.  Pass 0
 //     is skipped for rows of up to F16_PREPASS_CHUNKS chunks and for a tile with a zero first
