@@ -180,6 +180,52 @@ def call(name: str, *args) -> None:
         raise FlashUMAError(f"{name} failed with status {status}: {msg}")
 
 
+# Independent library calls of one SO(2) convolution (ops/gating.py) run on a second stream of
+# the device, so that each kernel's tail overlaps the next one's start.  Off under graph
+# capture and while a KernelProfiler records (its per-call events would time overlapped
+# kernels); set_overlap(False) turns it off.
+_overlap = True
+_side_streams: dict = {}
+
+
+def set_overlap(on: bool) -> None:
+    global _overlap
+    _overlap = bool(on)
+
+
+def side_stream(device: torch.device) -> torch.cuda.Stream | None:
+    """The device's second stream (default priority) for calls independent of the work queued
+    next on the current stream, or None when they should stay on the current stream."""
+    if not _overlap or _profiler is not None or torch.cuda.is_current_stream_capturing():
+        return None
+    idx = torch.device(device).index
+    idx = torch.cuda.current_device() if idx is None else idx
+    s = _side_streams.get(idx)
+    if s is None:
+        s = _side_streams[idx] = torch.cuda.Stream(device=idx)
+    return s
+
+
+@contextlib.contextmanager
+def on_side(side: torch.cuda.Stream | None):
+    """Queue the enclosed calls on `side` after everything queued so far on the current stream
+    (no-op for None).  The caller allocates their outputs before, keeps every tensor they touch
+    alive until join(side), and allocates nothing inside (the side stream has no pool of its
+    own then, and no tensor needs record_stream)."""
+    if side is None:
+        yield
+        return
+    side.wait_stream(torch.cuda.current_stream(side.device))
+    with torch.cuda.stream(side):
+        yield
+
+
+def join(side: torch.cuda.Stream | None) -> None:
+    """Make the current stream wait for the calls queued on `side`."""
+    if side is not None:
+        torch.cuda.current_stream(side.device).wait_stream(side)
+
+
 MATMUL_SPLIT_BF16 = 0  # fp32 operands split exactly into three bf16 planes, six MFMA products
 MATMUL_FP32 = 1        # v_mfma_f32_32x32x2_f32
 MATMUL_SPLIT_F16 = 2   # power-of-two row scales, two fp16 planes, three MFMA products

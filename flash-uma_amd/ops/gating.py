@@ -103,19 +103,25 @@ def _conv1_gate_m0(X0, W0, b0, C, L, st, W2=None):
     return Y0, Z0
 
 
-def _conv1_gate_m12(X1, X2, P1, Q1, P2, Q2, W3_1, W3_2, Y0, C, st):
-    """fu_complex_linear_gate for m = 1 (gates of degrees 1..L, s_off 0) and m = 2 (degrees
-    2..L, s_off C), the sigmoids recomputed from the gate columns of Y0: (Y1, Z1, Y2, Z2)."""
-    E = X1.shape[0]
+def _conv1_gate_mc(X, P, Q, W3, Y0, s_off, C, Y, Z):
+    """fu_complex_linear_gate for m = 1 (gates of degrees 1..L, s_off 0) or m = 2 (degrees
+    2..L, s_off C) into Y, Z (E, 2 Nc), the sigmoids recomputed from the gate columns of Y0;
+    on torch's current stream."""
+    E = X.shape[0]
+    Nc, Kc = P.shape
+    _lib.call("fu_complex_linear_gate", X.data_ptr(), X[:, Kc:].data_ptr(), X.stride(0), P.data_ptr(),
+              Q.data_ptr(), P.stride(0), _lib.ptr(W3), Y.data_ptr(), Y[:, Nc:].data_ptr(), Y.stride(0),
+              Z.data_ptr(), Z[:, Nc:].data_ptr(), Z.stride(0), Y0.data_ptr(), Y0.stride(0), s_off, C, E, Nc,
+              Kc, _lib.stream_ptr(X.device))
+
+
+def _conv1_gate_m12(X1, X2, P1, Q1, P2, Q2, W3_1, W3_2, Y0, C):
+    """Both complex conv1 GEMMs with their gates: (Y1, Z1, Y2, Z2)."""
     outs = []
     for X, P, Q, W3, s_off in ((X1, P1, Q1, W3_1, 0), (X2, P2, Q2, W3_2, C)):
-        Nc, Kc = P.shape
-        Y = torch.empty(E, 2 * Nc, device=X.device, dtype=torch.float32)
-        Z = torch.empty(E, 2 * Nc, device=X.device, dtype=torch.float32)
-        _lib.call("fu_complex_linear_gate", X.data_ptr(), X[:, Kc:].data_ptr(), X.stride(0), P.data_ptr(),
-                  Q.data_ptr(), P.stride(0), _lib.ptr(W3), Y.data_ptr(), Y[:, Nc:].data_ptr(), Y.stride(0),
-                  Z.data_ptr(), Z[:, Nc:].data_ptr(), Z.stride(0), Y0.data_ptr(), Y0.stride(0), s_off, C, E, Nc,
-                  Kc, st)
+        Y = torch.empty(X.shape[0], 2 * P.shape[0], device=X.device, dtype=torch.float32)
+        Z = torch.empty_like(Y)
+        _conv1_gate_mc(X, P, Q, W3, Y0, s_off, C, Y, Z)
         outs += [Y, Z]
     return tuple(outs)
 
@@ -138,7 +144,7 @@ class Conv1Gate(torch.autograd.Function):
         L = _degrees(W0, C)
         Y0, Z0 = _conv1_gate_m0(X0, W0, b0, C, L, st)
         sp = splits or (None,) * 4
-        Y1, Z1, Y2, Z2 = _conv1_gate_m12(X1, X2, P1, Q1, P2, Q2, sp[0], sp[2], Y0, C, st)
+        Y1, Z1, Y2, Z2 = _conv1_gate_m12(X1, X2, P1, Q1, P2, Q2, sp[0], sp[2], Y0, C)
         if L != 2:
             raise _lib.FlashUMAError("conv1_gate: lmax 2 only (use conv1_gate_conv2 for lmax 3, 4)")
         ctx.save_for_backward(Y0, Y1, Y2, W0t, P1t, Q1tn, P2t, Q2tn)
@@ -159,6 +165,17 @@ def conv1_gate(X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C,
     return Conv1Gate.apply(X0, X1, X2, W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn, C, splits)
 
 
+def _conv2_gate_bwd_mc(gz, Rt, Itn, W3, F, Y0, s_off, C, gy, ps):
+    """fu_complex_linear_gate_bwd of conv2 m = 1 (s_off 0) or m = 2 (s_off C): g_Y = g_Z s into
+    gy (E, 2 Nc) and the per-degree gate sums into ps (E, Nc); on torch's current stream."""
+    E = gz.shape[0]
+    Nc, Kc = Rt.shape
+    _lib.call("fu_complex_linear_gate_bwd", gz.data_ptr(), gz[:, Kc:].data_ptr(), gz.stride(0), Rt.data_ptr(),
+              Itn.data_ptr(), Rt.stride(0), _lib.ptr(W3), gy.data_ptr(), gy[:, Nc:].data_ptr(), gy.stride(0),
+              F.data_ptr(), F[:, Nc:].data_ptr(), F.stride(0), Y0.data_ptr(), Y0.stride(0), s_off, C,
+              ps.data_ptr(), ps.stride(0), E, Nc, Kc, _lib.stream_ptr(gz.device))
+
+
 def _splits12(splits):
     """The 12 pre-split weights of a conv pair: the complex W3 of conv1 m = 1, 2 and conv2
     m = 1, 2 with their transpose pairs, then linear_weight_split of W0, W0t, V0, V0t (None
@@ -172,26 +189,42 @@ def conv_pair_fwd(X: list, conv1, conv2, C: int, splits, m0=None):
     to None once its GEMM has read it, so a caller that hands over its only references
     frees the (E, 18C) gather output while the block runs.  m0: None, or conv1 m = 0's
     (Y0, Z0) computed already (X_m0 is then None).  Returns (Zo0, Zo1, Zo2) and the
-    pre-activations (Y0, Y1, Y2) the backward needs."""
+    pre-activations (Y0, Y1, Y2) the backward needs.
+
+    After conv1 m = 0 (whose gate columns the complex gate epilogues read), conv1 m = 1 and
+    conv2 m = 1 run on the current stream while conv1 m = 2, conv2 m = 2 and conv2 m = 0 run
+    on the device's side stream (_lib.side_stream; one stream when it is off): they are
+    independent, and each kernel's tail overlaps the other stream's work."""
     W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn = conv1
     V0, c0, V0t, R1, I1, R1t, I1tn, R2, I2, R2t, I2tn = conv2
-    st = _lib.stream_ptr(X[1].device)
+    dev = X[1].device
     L = _degrees(W0, C)
     sp = _splits12(splits)
     if m0 is None:
-        Y0, Z0 = _conv1_gate_m0(_lib.require(X[0], torch.float32, "X_m0"), W0, b0, C, L, st, sp[8])
+        Y0, Z0 = _conv1_gate_m0(_lib.require(X[0], torch.float32, "X_m0"), W0, b0, C, L, _lib.stream_ptr(dev),
+                                sp[8])
     else:
         Y0, Z0 = m0
     X[0] = None
     X1, X2 = _lib.require(X[1], torch.float32, "X_m1"), _lib.require(X[2], torch.float32, "X_m2")
     X[1] = X[2] = None
-    Y1, Z1, Y2, Z2 = _conv1_gate_m12(X1, X2, P1, Q1, P2, Q2, sp[0], sp[2], Y0, C, st)
-    del X1, X2
-    Zo0 = gemm(Z0, V0, c0, W2=sp[10])
-    del Z0
+    E = X1.shape[0]
+    f = lambda n: torch.empty(E, n, device=dev, dtype=torch.float32)
+    # the side stream's outputs, allocated on the current stream; its operands stay referenced
+    # until the join
+    Y2, Z2, Zo2, Zo0 = f(2 * P2.shape[0]), f(2 * P2.shape[0]), f(2 * R2.shape[0]), f(V0.shape[0])
+    side = _lib.side_stream(dev)
+    with _lib.on_side(side):
+        _conv1_gate_mc(X2, P2, Q2, sp[2], Y0, C, C, Y2, Z2)
+        complex_gemm(Z2, R2, I2, sp[6], out=Zo2)
+        gemm(Z0, V0, c0, out=Zo0, W2=sp[10])
+    Y1, Z1 = f(2 * P1.shape[0]), f(2 * P1.shape[0])
+    _conv1_gate_mc(X1, P1, Q1, sp[0], Y0, 0, C, Y1, Z1)
+    del X1
     Zo1 = complex_gemm(Z1, R1, I1, sp[4])
     del Z1
-    Zo2 = complex_gemm(Z2, R2, I2, sp[6])
+    _lib.join(side)
+    del X2, Z2, Z0
     return (Zo0, Zo1, Zo2), (Y0, Y1, Y2)
 
 
@@ -200,7 +233,9 @@ def conv_pair_bwd(Y, conv1, conv2, C: int, splits, g: list):
     gate backward runs in the conv2 input-gradient epilogues (the m = 1, 2 complex GEMMs write
     g_Y = g_Z s and their gate sums, then the m = 0 GEMM finishes the gate-paired g_Y_m0 with
     the gate gradients, s recomputed from Y0); g_Z is never stored.  The entries of g are
-    released once read."""
+    released once read.  The m = 2 gate backward and the m = 1 conv1 input gradient run on the
+    device's side stream beside the independent calls on the current stream (as in
+    conv_pair_fwd)."""
     Y0, Y1, Y2 = Y
     W0, b0, W0t, P1, Q1, P1t, Q1tn, P2, Q2, P2t, Q2tn = conv1
     V0, c0, V0t, R1, I1, R1t, I1tn, R2, I2, R2t, I2tn = conv2
@@ -214,30 +249,30 @@ def conv_pair_bwd(Y, conv1, conv2, C: int, splits, g: list):
     g1 = torch.zeros(E, 2 * L * C, device=dev) if g[1] is None else g[1].contiguous()
     g2 = torch.zeros(E, 2 * (L - 1) * C, device=dev) if g[2] is None else g[2].contiguous()
     g[0] = g[1] = g[2] = None
-    gys, psums = [], []
-    for gz, Rt, Itn, W3, F, s_off in ((g1, R1t, I1tn, sp[5], Y1, 0), (g2, R2t, I2tn, sp[7], Y2, C)):
-        Nc, Kc = Rt.shape
-        gy, ps = f(E, 2 * Nc), f(E, Nc)
-        _lib.call("fu_complex_linear_gate_bwd", gz.data_ptr(), gz[:, Kc:].data_ptr(), gz.stride(0), Rt.data_ptr(),
-                  Itn.data_ptr(), Rt.stride(0), _lib.ptr(W3), gy.data_ptr(), gy[:, Nc:].data_ptr(),
-                  gy.stride(0), F.data_ptr(), F[:, Nc:].data_ptr(), F.stride(0), Y0.data_ptr(), Y0.stride(0),
-                  s_off, C, ps.data_ptr(), ps.stride(0), E, Nc, Kc, st)
-        gys.append(gy)
-        psums.append(ps)
-    del g1, g2, gz
+    gy1, ps1 = f(E, 2 * R1t.shape[0]), f(E, R1t.shape[0])
+    gy2, ps2 = f(E, 2 * R2t.shape[0]), f(E, R2t.shape[0])
+    side = _lib.side_stream(dev)
+    with _lib.on_side(side):
+        _conv2_gate_bwd_mc(g2, R2t, I2tn, sp[7], Y2, Y0, C, C, gy2, ps2)
+    _conv2_gate_bwd_mc(g1, R1t, I1tn, sp[5], Y1, Y0, 0, C, gy1, ps1)
+    _lib.join(side)
+    del g1, g2
     gy0 = f(E, (2 * L + 1) * C)
     _lib.call("fu_linear_gate_bwd", g0.data_ptr(), g0.stride(0), V0t.data_ptr(), V0t.stride(0), Y0.data_ptr(),
-              Y0.stride(0), psums[0].data_ptr(), psums[0].stride(0), psums[1].data_ptr(), psums[1].stride(0),
+              Y0.stride(0), ps1.data_ptr(), ps1.stride(0), ps2.data_ptr(), ps2.stride(0),
               gy0.data_ptr(), gy0.stride(0), E, C, V0t.shape[1], L, _lib.ptr(sp[11]), st)
     # release each intermediate as soon as it is consumed: the backward of a block runs near
     # the step's memory peak (every earlier layer's saved tensors are still alive)
-    del psums, g0
+    del ps1, ps2, g0
+    g_x1 = f(E, 2 * P1t.shape[0])
+    with _lib.on_side(side):
+        complex_gemm(gy1, P1t, Q1tn, sp[1], out=g_x1)
     g_x0 = gemm(gy0, W0t, W2=sp[9])
     del gy0
-    g_x1 = complex_gemm(gys[0], P1t, Q1tn, sp[1])
-    gys[0] = None
-    g_x2 = complex_gemm(gys[1], P2t, Q2tn, sp[3])
-    del gys
+    g_x2 = complex_gemm(gy2, P2t, Q2tn, sp[3])
+    del gy2
+    _lib.join(side)
+    del gy1
     return g_x0, g_x1, g_x2
 
 

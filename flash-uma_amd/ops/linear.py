@@ -98,17 +98,20 @@ def complex_weight_split(P: torch.Tensor, Q: torch.Tensor) -> torch.Tensor:
     return W3
 
 
-def complex_gemm(x: torch.Tensor, P: torch.Tensor, Q: torch.Tensor, W3: torch.Tensor | None = None) -> torch.Tensor:
+def complex_gemm(x: torch.Tensor, P: torch.Tensor, Q: torch.Tensor, W3: torch.Tensor | None = None,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
     """[y_r | y_i] = complex product of x = [x_r | x_i] (M, 2 Kc) with (P + iQ)^T, P, Q (Nc, Kc):
     y_r = x_r P^T - x_i Q^T, y_i = x_r Q^T + x_i P^T (fu_complex_linear; W3 = complex_weight_split(P, Q)
-    or None)."""
+    or None; out: an (M, 2 Nc) float32 array with unit column stride to write, or None)."""
     if x.stride(-1) != 1:
         x = x.contiguous()
     M = x.shape[0]
     Nc, Kc = P.shape
     if x.shape[1] != 2 * Kc or Q.shape != P.shape:
         raise _lib.FlashUMAError(f"complex_gemm: x {tuple(x.shape)} vs P {tuple(P.shape)}, Q {tuple(Q.shape)}")
-    y = torch.empty((M, 2 * Nc), device=x.device, dtype=torch.float32)
+    if out is not None and (out.shape != (M, 2 * Nc) or out.dtype != torch.float32 or out.stride(-1) != 1):
+        raise _lib.FlashUMAError(f"complex_gemm: out {tuple(out.shape)} {out.dtype}, expected ({M}, {2 * Nc}) float32")
+    y = torch.empty((M, 2 * Nc), device=x.device, dtype=torch.float32) if out is None else out
     _lib.call("fu_complex_linear", x.data_ptr(), x[:, Kc:].data_ptr(), x.stride(0), P.data_ptr(), Q.data_ptr(),
               P.stride(0), _lib.ptr(W3), y.data_ptr(), y[:, Nc:].data_ptr(), y.stride(0), M, Nc, Kc, _lib.stream_ptr(x.device))
     return y

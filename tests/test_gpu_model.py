@@ -143,6 +143,34 @@ def test_deterministic_and_translation(cuda):
     assert a["forces"].double().sum(0).abs().max().item() < 1e-5
 
 
+@pytest.mark.parametrize("lmax", [2, 4])
+def test_side_stream_overlap_is_bitwise_equal(cuda, lmax):
+    """The independent SO(2) GEMMs of each convolution on two streams (ops/_lib.side_stream)
+    against the same step on one stream: E, F, S and the node embedding bitwise equal, at
+    lmax 2 and 4, over two steps (the second reuses the first's freed memory)."""
+    import escn_md
+    import heads
+    import systems
+    from ops import _lib
+    from wrapper import ZeroAllocBackbone
+    bb = escn_md.eSCNMDBackbone(seed=0, lmax=lmax, num_layers=2)
+    hd = heads.MLPEnergyHead(bb.sphere_channels, bb.hidden_channels, seed=1)
+    model = heads.PotentialModel(ZeroAllocBackbone(bb.to(cuda)), hd.to(cuda))
+    s = systems.bcc_fe(n_rep=4)
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, 6.0, 30)
+    assert _lib.side_stream(cuda) is not None
+    outs = {}
+    try:
+        for on in (False, True):
+            _lib.set_overlap(on)
+            outs[on] = [_run(model, s, ei, off, cuda) for _ in range(2)]
+    finally:
+        _lib.set_overlap(True)
+    for k in ("energy", "forces", "stress", "node_embedding"):
+        for a, b in zip(outs[False], outs[True]):
+            assert torch.equal(a[k], b[k]), f"lmax {lmax}: {k} differs with the side stream"
+
+
 def test_batch_of_three_systems(cuda):
     """A FAIRChem-style batch of three systems with different cells, sizes, charges and
     spins (per-edge cell shifts, per-system charge/spin embedding through the kernels,
