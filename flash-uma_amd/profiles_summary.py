@@ -93,14 +93,26 @@ def _steps(rows: list[dict], marker: str = "geom_fwd_kernel") -> list[int]:
     return [i for i, r in enumerate(rows) if marker in r["Kernel_Name"]]
 
 
-def timed(trace: str, warmup: int, steps: int, title: str, command: str, out: str, top: int = 40) -> None:
+def _streams(rows: list[dict]) -> int:
+    return len({r.get("Stream_Id", "0") for r in rows})
+
+
+def timed(trace: str, warmup: int, steps: int, title: str, command: str, out: str, top: int = 40,
+          which: str = "timed") -> None:
     """Kernel time per step over the timed steps of a kernel trace: a step starts at its
-    geom_fwd_kernel dispatch, the first `warmup` steps are left out."""
+    geom_fwd_kernel dispatch, the first `warmup` steps are left out.  which="profiled": the
+    trace also holds bench.py's per-kernel profiling pass (the same number of steps after the
+    timed ones, every call on one stream with the HIP-event profiler on); the table is built
+    from that pass, whose kernel durations are those of bench.py's roofline figures, and the
+    header gives the timed pass's wall time beside it."""
     rows = sorted(_read(trace), key=lambda r: int(r["Start_Timestamp"]))
     starts = _steps(rows)
-    if len(starts) != warmup + steps:
-        raise SystemExit(f"{trace}: {len(starts)} steps found, expected {warmup} + {steps}")
-    sel = rows[starts[warmup]:]
+    n_pass = 2 if which == "profiled" else 1
+    if len(starts) != warmup + n_pass * steps:
+        raise SystemExit(f"{trace}: {len(starts)} steps found, expected {warmup} + {n_pass} x {steps}")
+    timed_rows = rows[starts[warmup]:starts[warmup + steps]] if n_pass == 2 else rows[starts[warmup]:]
+    sel = rows[starts[warmup + steps]:] if n_pass == 2 else timed_rows
+    w0, w1 = int(timed_rows[0]["Start_Timestamp"]), max(int(r["End_Timestamp"]) for r in timed_rows)
     t0, t1 = int(sel[0]["Start_Timestamp"]), max(int(r["End_Timestamp"]) for r in sel)
     agg = collections.defaultdict(lambda: [0, 0])
     for r in sel:
@@ -109,12 +121,25 @@ def timed(trace: str, warmup: int, steps: int, title: str, command: str, out: st
         agg[key][1] += int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
     tot = sum(v[1] for v in agg.values())
     lines = [f"# Kernel time per step — {title}", "", "Command (run from the repository root on one MI355X):", "",
-             "```", command, "```", "",
-             f"rocprofv3 kernel trace, the {steps} timed steps only (each step starts at its `geom_fwd_kernel` "
-             f"dispatch; the {warmup} warm-up steps are left out). Kernel time {tot / 1e6 / steps:.2f} ms/step; "
-             f"first dispatch to last completion {(t1 - t0) / 1e6 / steps:.2f} ms/step. Every kernel runs on one "
-             "stream. Summarised by `python flash-uma_amd/profiles_summary.py timed`.", "",
-             "| ms/step | calls/step | avg us | share | kernel | entry point |", "|---:|---:|---:|---:|---|---|"]
+             "```", command, "```", ""]
+    if n_pass == 1:
+        nst = _streams(sel)
+        lines += [f"rocprofv3 kernel trace, the {steps} timed steps only (each step starts at its `geom_fwd_kernel` "
+                  f"dispatch; the {warmup} warm-up steps are left out). Kernel time {tot / 1e6 / steps:.2f} ms/step; "
+                  f"first dispatch to last completion {(t1 - t0) / 1e6 / steps:.2f} ms/step. Kernels ran on {nst} "
+                  f"stream{'s' if nst > 1 else ''}. Summarised by `python flash-uma_amd/profiles_summary.py timed`.",
+                  ""]
+    else:
+        nst = _streams(timed_rows)
+        lines += [f"rocprofv3 kernel trace of bench.py's two passes (each step starts at its `geom_fwd_kernel` "
+                  f"dispatch; the {warmup} warm-up steps are left out). Timed pass ({steps} steps, kernels on {nst} "
+                  f"stream{'s' if nst > 1 else ''}): first dispatch to last completion {(w1 - w0) / 1e6 / steps:.2f} "
+                  f"ms/step. The table is the per-kernel profiling pass ({steps} steps, every kernel on one stream, "
+                  f"HIP events around each call: the durations behind bench.py's roofline figures): kernel time "
+                  f"{tot / 1e6 / steps:.2f} ms/step, first dispatch to last completion "
+                  f"{(t1 - t0) / 1e6 / steps:.2f} ms/step. Summarised by "
+                  f"`python flash-uma_amd/profiles_summary.py timed --pass profiled`.", ""]
+    lines += ["| ms/step | calls/step | avg us | share | kernel | entry point |", "|---:|---:|---:|---:|---|---|"]
     for (nm, ent), (n, t) in sorted(agg.items(), key=lambda kv: -kv[1][1])[:top]:
         lines.append(f"| {t / 1e6 / steps:.3f} | {n / steps:.1f} | {t / n / 1e3:.1f} | {100 * t / tot:.1f}% | `{nm}` | "
                      f"{ent or '(torch / rocBLAS)'} |")
@@ -268,6 +293,7 @@ def main(argv=None) -> None:
     t.add_argument("--title", required=True)
     t.add_argument("--command", required=True)
     t.add_argument("--out", required=True)
+    t.add_argument("--pass", dest="which", choices=("timed", "profiled"), default="timed")
     p = sub.add_parser("pmc")
     for k in ("fetch", "fetch-trace", "write", "write-trace", "config", "cmd-fetch", "cmd-write", "out", "commit"):
         p.add_argument(f"--{k}", required=True)
@@ -278,7 +304,7 @@ def main(argv=None) -> None:
         q.add_argument(f"--{k}", required=True)
     a = ap.parse_args(argv)
     if a.cmd == "timed":
-        timed(a.trace, a.warmup, a.steps, a.title, a.command, a.out)
+        timed(a.trace, a.warmup, a.steps, a.title, a.command, a.out, which=a.which)
     elif a.cmd == "pmc":
         pmc(a.fetch, a.fetch_trace, a.write, a.write_trace, a.config, a.cmd_fetch, a.cmd_write, a.out, a.json,
             a.commit)

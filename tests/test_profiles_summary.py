@@ -40,7 +40,7 @@ def test_template_instances_map_to_their_entry_points():
 
 
 def _trace(path, rows):
-    keys = ["Dispatch_Id", "Kernel_Name", "Start_Timestamp", "End_Timestamp", "Grid_Size_Y"]
+    keys = ["Dispatch_Id", "Kernel_Name", "Start_Timestamp", "End_Timestamp", "Grid_Size_Y", "Stream_Id"][:len(rows[0])]
     with open(path, "w", newline="") as f:
         w = csv.DictWriter(f, keys)
         w.writeheader()
@@ -64,3 +64,24 @@ def test_timed_table_from_a_trace(tmp_path):
     assert "| fu_linear | 1.0 | 500.0 | 0.500 |" in text
     assert "| fu_linear_batched | 1.0 | 30.0 | 0.030 |" in text
     assert "Kernel time 0.57 ms/step" in text
+
+
+def test_profiled_pass_table_from_a_trace(tmp_path):
+    """--pass profiled: the table comes from the steps after the timed ones (bench.py's per-kernel
+    profiling pass, one stream); the header gives the timed pass's wall time and stream count."""
+    rows, t = [], 0
+    for step in range(5):   # one warm-up, two timed steps on two streams, two profiled steps on one
+        timed_pass = 1 <= step <= 2
+        for name, us, gy, sid in (("void fu::geom_fwd_kernel(x)", 40, 1, 0),
+                                  ("void fu::complex_linear_kernel<0, 3, false>(x)", 400 if timed_pass else 420, 1, 0),
+                                  ("void fu::complex_linear_kernel<0, 3, false>(x)", 150, 1, 1 if timed_pass else 0)):
+            rows.append((len(rows), name, t, t + us * 1000, gy, sid))
+            t += us * 1000 + 1000
+    tr = tmp_path / "t.csv"
+    _trace(tr, rows)
+    out = tmp_path / "t.md"
+    ps.timed(str(tr), 1, 2, "test", "cmd", str(out), which="profiled")
+    text = out.read_text()
+    assert "| fu_complex_linear | 2.0 | 285.0 | 0.570 |" in text
+    assert "kernels on 2 streams" in text
+    assert "first dispatch to last completion 0.59 ms/step. The table" in text
