@@ -269,10 +269,13 @@ class Packed_eSCN_Layer(nn.Module):
                 self.gamma_rad1_2, self.beta_rad1_2, self.W_rad1_3, self.b_rad1_3)
 
     def forward(self, x_in, x_edge_raw, wigner, env, idx_i, idx_j, row_ptr, col_idx, csd_emb, batch,
-                topology=None, rad_out=None, wig_ext=None, rad_src=None, sink=None, gather_m0=False):
+                topology=None, rad_out=None, wig_ext=None, rad_src=None, sink=None, gather_m0=False,
+                before_ffn=None):
         """rad_out, when given, is this block's radial-MLP output (computed by the model's
         RadialBank); otherwise it is computed here from x_edge_raw (E, B+2C).  wig_ext: the
-        degree-3/4 Wigner rows (ops/lmax.wigner_extend), needed for lmax > 2."""
+        degree-3/4 Wigner rows (ops/lmax.wigner_extend), needed for lmax > 2.  before_ffn: a
+        callable run after the edge-wise part is queued, before the node-side block (the model
+        queues the next block's radial output there, RadialOutputs.prelaunch)."""
         x_norm, x_skip = self._norm_skip(x_in)
         if rad_out is None:
             rad_out = self.radial(x_edge_raw)
@@ -293,6 +296,8 @@ class Packed_eSCN_Layer(nn.Module):
         else:
             x_mid = rotate_scatter_lmax(Zo_m0, Zo_m1, Zo_m2, wigner, wig_ext, env, x_skip, idx_j, row_ptr, col_idx,
                                         x_skip.shape[0], self.lmax, sink)
+        if before_ffn is not None:
+            before_ffn()
         return self._ffn_residual(x_mid)
 
     def _norm_skip(self, x_in):
@@ -417,31 +422,32 @@ class eSCN_Inference_Model(nn.Module):
         #    graphs the blocks keep each radial output's (E, C) source instead of the (E, 12C)
         #    output and recompute it in their backward (one GEMM per block, ~5 % of the step,
         #    for ~22 KB less per edge held through the step).
+        #    Each block's output layer is made when the block runs (its GEMM queued on the
+        #    side stream during the previous block's node-side work, ops/radial.RadialOutputs).
         recompute = idx_i_s.shape[0] >= self.RAD_RECOMPUTE_MIN_EDGES
-        if recompute:
-            rads, srcs = self.radial_bank(gauss, Z_s, idx_i_s, idx_j_s, with_sources=True)
-        else:
-            rads, srcs = self.radial_bank(gauss, Z_s, idx_i_s, idx_j_s), None
-        rads = list(rads)
+        rads = self.radial_bank(gauss, Z_s, idx_i_s, idx_j_s, lazy=True)
+        rad = rads.get(0)
+        rads.prelaunch(1)
         # 4. Edge-degree embedding (lmax > 2: with the degree-3/4 Wigner rows)
         wig_ext = None
         if self.lmax == 2:
-            x_node_s = init_node_scatter(rads[0], wigner, env, Z_s, batch_s, self.W_sphere, csd_emb, idx_j_s,
+            x_node_s = init_node_scatter(rad, wigner, env, Z_s, batch_s, self.W_sphere, csd_emb, idx_j_s,
                                          row_ptr, col_idx, N, sink)
         else:
             wig_ext = wigner_extend(wigner, self.lmax, sink)
-            x_node_s = init_node_scatter_lmax(rads[0], wigner, wig_ext, env, Z_s, batch_s, self.W_sphere, csd_emb,
+            x_node_s = init_node_scatter_lmax(rad, wigner, wig_ext, env, Z_s, batch_s, self.W_sphere, csd_emb,
                                               idx_j_s, row_ptr, col_idx, N, self.lmax, sink)
+        del rad
         # 5. Message-passing blocks, each followed by the charge / spin channel balancing when
         #    the backbone reserves channels for them (model.py:213-216)
         balance = self.charge_end > self.charge_start or self.spin_end > self.spin_start
         sys_ptr = system_ptr(batch_s, csd_emb.shape[0]) if balance else None   # batch_s is sorted
-        rads[0] = None
         for k, layer in enumerate(self.layers):
-            rad, rads[k + 1] = rads[k + 1], None
+            rad = rads.get(k + 1)
             x_node_s = layer(x_node_s, None, wigner, env, idx_i_s, idx_j_s, row_ptr, col_idx, csd_emb,
                              batch_s, topo, rad_out=rad, wig_ext=wig_ext,
-                             rad_src=srcs[k + 1] if srcs else None, sink=sink, gather_m0=self.GATHER_IN_CONV1)
+                             rad_src=rads.source(k + 1) if recompute else None, sink=sink,
+                             gather_m0=self.GATHER_IN_CONV1, before_ffn=lambda n=k + 2: rads.prelaunch(n))
             del rad
             if self.charge_end > self.charge_start:
                 x_node_s = balance_channels_batched(x_node_s, charge, natoms, batch_s, self.charge_start,

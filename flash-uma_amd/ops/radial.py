@@ -125,11 +125,12 @@ def _gemm(A, W, bias, out, W2=None):
     return out
 
 
-def _out_gemm(A, W, bias, W2):
+def _out_gemm(A, W, bias, W2, out=None):
     """An output layer's product: in the split-fp16 mode, with the weight pre-split (W2), on
     fu_linear_resident (the (E, C) input read and split once per 128-row panel instead of once
-    per 128-column tile); otherwise fu_linear."""
-    out = torch.empty(A.shape[0], W.shape[0], device=A.device, dtype=torch.float32)
+    per 128-column tile); otherwise fu_linear.  out: the (E, n_k) result array, or None."""
+    if out is None:
+        out = torch.empty(A.shape[0], W.shape[0], device=A.device, dtype=torch.float32)
     if W2 is not None and _lib.get_matmul_mode() == _lib.MATMUL_SPLIT_F16:
         return gemm_resident(A, W2, W.shape[0], bias, out)
     return _gemm(A, W, bias, out)
@@ -168,12 +169,12 @@ class RadialBank(torch.nn.Module):
             reg(f"W3_{k}_t", m[8].t())
             reg(f"b3_{k}", m[9])
 
-    # All layers run on the caller's stream.  A side stream for the output layers (tried:
-    # under 1 % of step time at best) makes the caching allocator hold every block it
-    # touched across streams until the other stream's events complete; with the host
-    # enqueueing steps ahead of the GPU, as it does in an MD loop without host reads, the
-    # reserve then grew from 31 to 230 GB on the 8,192-atom Fe cell, and the allocations
-    # on that path stalled the host for seconds in some processes.
+    # The output layers' GEMMs may run on a side stream (RadialOutputs), but every array they
+    # write is allocated on the caller's stream and every array they read stays referenced
+    # until the caller's stream waits for them: a tensor that crossed streams otherwise makes
+    # the caching allocator hold its block until the other stream's events complete, and with
+    # the host enqueueing steps ahead of the GPU (an MD loop without host reads) an earlier
+    # side-stream version grew the reserve from 31 to 230 GB on the 8,192-atom Fe cell.
 
     def _split(self, name: str, ok):
         """linear_weight_split of buffer `name`, built on first use on its device (None when `ok`
@@ -194,24 +195,73 @@ class RadialBank(torch.nn.Module):
         """Output layer k's transposed weight pre-split for its input-gradient GEMM."""
         return self._split(f"W3_{k}_t", lambda K: K % 16 == 0)
 
-    def forward(self, gauss, Z, idx_i, idx_j, with_sources: bool = False):
+    def forward(self, gauss, Z, idx_i, idx_j, with_sources: bool = False, lazy: bool = False):
         """gauss (E, B) -> tuple of G radial outputs (E, n_k).
 
         The trunk (first two layers of all MLPs) is one autograd node; each block's output
         layer is its own node, whose backward writes its input gradient straight into the
         trunk's gradient buffer.  with_sources: also return, per block, (h2_k, W3_k, b3_k), from
         which a consumer can recompute the output bit for bit (source(...)) instead of keeping
-        it for its backward."""
+        it for its backward.  lazy: return the RadialOutputs instead, which create each block's
+        output node when the block asks for it."""
         holder = _GradHolder()
         h2s = _RadialTrunkFn.apply(gauss, Z, idx_i, idx_j, self, holder)
-        outs, srcs = [], []
-        for k in range(self.G):
-            W, Wt, b = getattr(self, f"W3_{k}"), getattr(self, f"W3_{k}_t"), getattr(self, f"b3_{k}")
-            W2 = self.out_split(k)
-            outs.append(_RadialOutFn.apply(h2s[k], W, b, Wt, holder, k, W2, self.out_t_split(k)))
-            srcs.append((h2s[k].detach(), W, b, W2))
-        holder.ln = None
-        return (tuple(outs), tuple(srcs)) if with_sources else tuple(outs)
+        lo = RadialOutputs(self, h2s, holder)
+        if lazy:
+            return lo
+        outs = tuple(lo.get(k) for k in range(self.G))
+        srcs = tuple(lo.source(k) for k in range(self.G))
+        return (outs, srcs) if with_sources else outs
+
+
+class RadialOutputs:
+    """The radial bank's block outputs, made on demand.  get(k) creates block k's output node
+    and returns its output; creating it just before block k runs puts its backward right after
+    that block's in the autograd engine's order (later-created nodes first), so the output
+    layer's input gradient is formed while the next block's backward runs (the backward
+    launches it on the device's side stream, ops/_lib.side_stream) instead of after all of
+    them, and its (E, n_k) output gradient is released a block later instead of at the end.
+    prelaunch(k) queues block k's output GEMM early on the side stream, into an array
+    allocated on the current stream, so that it runs beside the previous block's node-side
+    work (small GEMMs on 8,192 rows that leave most CUs idle); get(k) then waits for it."""
+
+    def __init__(self, bank, h2s, holder):
+        self.bank, self.h2s, self.holder = bank, h2s, holder
+        self._pre = {}
+        self._made = 0
+
+    def _w(self, k):
+        b = self.bank
+        return getattr(b, f"W3_{k}"), getattr(b, f"b3_{k}"), getattr(b, f"W3_{k}_t"), b.out_split(k), b.out_t_split(k)
+
+    def source(self, k: int):
+        """(h2_k, W3_k, b3_k, split W3_k): recompute_output(source(k)) equals get(k) bit for bit."""
+        W, b, _, W2, _ = self._w(k)
+        return self.h2s[k].detach(), W, b, W2
+
+    def prelaunch(self, k: int) -> None:
+        if k >= self.bank.G or k in self._pre:
+            return
+        h2k = self.h2s[k]
+        side = _lib.side_stream(h2k.device)
+        if side is None:
+            return
+        W, b, _, W2, _ = self._w(k)
+        out = torch.empty(h2k.shape[0], W.shape[0], device=h2k.device, dtype=torch.float32)
+        with _lib.on_side(side):
+            _out_gemm(h2k, W, b, W2, out)
+        self._pre[k] = (out, side)
+
+    def get(self, k: int) -> torch.Tensor:
+        W, b, Wt, W2, W2t = self._w(k)
+        pre = self._pre.pop(k, None)
+        if pre is not None:
+            _lib.join(pre[1])
+        out = _RadialOutFn.apply(self.h2s[k], W, b, Wt, self.holder, k, W2, W2t, None if pre is None else pre[0])
+        self._made += 1
+        if self._made == self.bank.G:
+            self.holder.ln = None   # every output node holds what it needs
+        return out
 
 
 def recompute_output(src) -> torch.Tensor:
@@ -238,6 +288,15 @@ class _GradHolder:
         self.shape = None
         self.device = None
         self.ln = None
+        self.side = None      # stream of the output-layer backward in flight, if any
+        self.pending = ()     # the tensors it reads, kept alive until settle()
+
+    def settle(self) -> None:
+        """Make the current stream wait for the output-layer backward queued on the side stream
+        and release the tensors it read."""
+        if self.side is not None:
+            _lib.join(self.side)
+        self.side, self.pending = None, ()
 
     def buffer(self) -> torch.Tensor:
         if self.g is None:
@@ -281,6 +340,7 @@ class _RadialTrunkFn(torch.autograd.Function):
     def backward(ctx, *g_views):
         gauss, m1, r1, p2, m2, r2, Z, idx_i, idx_j = ctx.saved_tensors
         bank, holder = ctx.bank, ctx.holder
+        holder.settle()
         E, G, C = gauss.shape[0], bank.G, bank.C
         g_buf = holder.g if holder.g is not None else torch.empty_like(p2)
         holder.g = None   # a retained graph's next backward allocates a fresh buffer
@@ -311,33 +371,44 @@ class _RadialOutFn(torch.autograd.Function):
     """Output layer of block k: rad = h2_k W3^T + b3.  Its backward writes into the trunk's
     gradient buffer and returns that slice: at C = 128 the gradient of the LayerNorm input of
     group k of the second hidden layer (fu_linear_dgrad_ln_silu_bwd: the g_h2_k GEMM with that
-    LayerNorm-SiLU backward in its epilogue, g_h2_k never stored), otherwise g_h2_k."""
+    LayerNorm-SiLU backward in its epilogue, g_h2_k never stored), otherwise g_h2_k.  The
+    backward runs on the device's side stream when there is one (RadialOutputs); the trunk's
+    backward, which reads the buffer, waits for it.  pre: the output already computed
+    (RadialOutputs.prelaunch), or None."""
 
     @staticmethod
-    def forward(ctx, h2k, W, b, Wt, holder, k, W2=None, W2t=None):
+    def forward(ctx, h2k, W, b, Wt, holder, k, W2=None, W2t=None, pre=None):
         ctx.holder, ctx.k, ctx.W2t = holder, k, W2t
         # (p2, mean, rstd, gamma, beta) of the trunk's forward are saved like the weight, so
         # that they are released after the backward (a plain ctx attribute would keep p2 alive
         # as long as the graph's nodes, i.e. into the next step)
         ctx.ln_groups = None if holder.ln is None else holder.ln[-1]
         ctx.save_for_backward(Wt, *(() if holder.ln is None else holder.ln[:-1]))
-        return _out_gemm(h2k, W, b, W2)
+        return pre if pre is not None else _out_gemm(h2k, W, b, W2)
 
     @staticmethod
     def backward(ctx, g_rad):
         Wt, *ln = ctx.saved_tensors
         g_rad = g_rad.contiguous()
         C = Wt.shape[0]
-        buf = ctx.holder.buffer()
+        holder = ctx.holder
+        buf = holder.buffer()
         sl = buf[:, ctx.k * C:(ctx.k + 1) * C]
-        if ctx.ln_groups is None:
-            _gemm(g_rad, Wt, None, sl, ctx.W2t)
-        else:
-            p2, m2, r2, gamma, beta = ln
-            G = ctx.ln_groups
-            M, K = g_rad.shape
-            _lib.call("fu_linear_dgrad_ln_silu_bwd", g_rad.data_ptr(), g_rad.stride(0), Wt.data_ptr(), Wt.stride(0),
-                      sl.data_ptr(), buf.stride(0), M, K, p2.data_ptr(), p2.stride(0), gamma.data_ptr(),
-                      beta.data_ptr(), m2.data_ptr(), r2.data_ptr(), G, ctx.k, _lib.ptr(ctx.W2t),
-                      _lib.stream_ptr(g_rad.device))
-        return sl, None, None, None, None, None, None, None
+        # the previous output layer's backward (a block later in the forward) is done by now;
+        # its operands are released here
+        holder.settle()
+        side = _lib.side_stream(g_rad.device)
+        with _lib.on_side(side):
+            if ctx.ln_groups is None:
+                _gemm(g_rad, Wt, None, sl, ctx.W2t)
+            else:
+                p2, m2, r2, gamma, beta = ln
+                G = ctx.ln_groups
+                M, K = g_rad.shape
+                _lib.call("fu_linear_dgrad_ln_silu_bwd", g_rad.data_ptr(), g_rad.stride(0), Wt.data_ptr(),
+                          Wt.stride(0), sl.data_ptr(), buf.stride(0), M, K, p2.data_ptr(), p2.stride(0),
+                          gamma.data_ptr(), beta.data_ptr(), m2.data_ptr(), r2.data_ptr(), G, ctx.k,
+                          _lib.ptr(ctx.W2t), _lib.stream_ptr(g_rad.device))
+        if side is not None:
+            holder.side, holder.pending = side, (g_rad, Wt, *ln)
+        return sl, None, None, None, None, None, None, None, None
