@@ -11,7 +11,7 @@ static std::atomic<int> g_matmul_mode{FU_MATMUL_SPLIT_F16};
 int matmul_mode() { return g_matmul_mode.load(std::memory_order_relaxed); }
 }  // namespace fu
 
-extern "C" int fu_version(void) { return 500; }  // 0.5.0
+extern "C" int fu_version(void) { return 600; }  // 0.6.0
 
 extern "C" const char* fu_last_error(void) { return fu::g_last_error; }
 

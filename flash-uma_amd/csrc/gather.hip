@@ -13,6 +13,7 @@
 // writes its half of g_rad, accumulates D^T g into the node gradient in CSR order, and
 // reduces its half of g_wigner across lanes.  The two node partials are added through LDS
 // (receiver part + sender part) and g_x[n] is written once: deterministic, no atomics.
+#include "edge_layout.h"
 #include "fu_vec.h"
 
 namespace fu {
@@ -64,23 +65,6 @@ __device__ __forceinline__ void add_rotate9_t(const float* w, const Rows9<CPL>& 
 __device__ __forceinline__ int wave_id_uniform() {
   return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
 }
-
-// Column block of slot q of side so (0 = sender, 1 = receiver) in each edge array.  Layout 0
-// is the reference order, sides interleaved (2q + so, ops/gather.py:132-154).  Layout 1:
-//   X_m0, rad: each side's slots contiguous (so * per_side + q);
-//   X_m1: real slots (q = 0, 1) then imaginary slots (q = 2, 3), each half side-major, so
-//         that x_r and x_i are the two contiguous halves the complex layer reads;
-//   X_m2: reference order (already [x_r | x_i]).
-template <int L>
-__device__ __forceinline__ constexpr int slot_m0(int so, int q) { return L ? so * 3 + q : 2 * q + so; }
-template <int L>
-__device__ __forceinline__ constexpr int slot_m1(int so, int q) {
-  return L ? (q >> 1) * 4 + so * 2 + (q & 1) : 2 * q + so;
-}
-template <int L>
-__device__ __forceinline__ constexpr int slot_m2(int so, int q) { return 2 * q + so; }
-template <int L>
-__device__ __forceinline__ constexpr int slot_rad(int so, int q) { return L ? so * 6 + q : 2 * q + so; }
 
 // M0 false: the m = 0 slots are neither computed nor stored (X0 unused), nor are their radial
 // blocks read: conv1 m = 0 gathers its operand itself (fu_gather_linear_gate).

@@ -270,14 +270,20 @@ class Packed_eSCN_Layer(nn.Module):
 
     def forward(self, x_in, x_edge_raw, wigner, env, idx_i, idx_j, row_ptr, col_idx, csd_emb, batch,
                 topology=None, rad_out=None, wig_ext=None, rad_src=None, sink=None, gather_m0=False,
-                before_ffn=None):
+                before_ffn=None, rad_gather=None):
         """rad_out, when given, is this block's radial-MLP output (computed by the model's
         RadialBank); otherwise it is computed here from x_edge_raw (E, B+2C).  wig_ext: the
         degree-3/4 Wigner rows (ops/lmax.wigner_extend), needed for lmax > 2.  before_ffn: a
         callable run after the edge-wise part is queued, before the node-side block (the model
-        queues the next block's radial output there, RadialOutputs.prelaunch)."""
+        queues the next block's radial output there, RadialOutputs.prelaunch).  rad_gather:
+        lmax 2, a callable (x_norm, layout) -> (rad_out, [X_m0, X_m1, X_m2]) that makes this
+        block's radial output and the gather's outputs in one kernel (RadialOutputs.
+        get_with_gather), used instead of rad_out."""
         x_norm, x_skip = self._norm_skip(x_in)
-        if rad_out is None:
+        X_pre = None
+        if rad_gather is not None:
+            rad_out, X_pre = rad_gather(x_norm, self.layout)
+        elif rad_out is None:
             rad_out = self.radial(x_edge_raw)
         # gather -> conv1 + gate -> conv2 as one node: the (E, 18C) gather output X never
         # outlives the block (model.py:150-154)
@@ -288,7 +294,7 @@ class Packed_eSCN_Layer(nn.Module):
             [getattr(self, "W_conv2_m" + m + x) for m in "12" for x in sfx]
         Zo_m0, Zo_m1, Zo_m2 = edge_block(x_norm, wigner, wig_ext, rad_out, idx_i, idx_j, csd_emb, batch, topology,
                                          self.layout, self.lmax, c1, c2, self.C, self._complex_splits(x_norm.device),
-                                         rad_src, sink, gather_m0)
+                                         rad_src, sink, gather_m0, X_pre)
         del rad_out
         if self.lmax == 2:
             x_mid = rotate_scatter_split(Zo_m0, Zo_m1, Zo_m2, wigner, env, x_skip, idx_j, row_ptr, col_idx,
@@ -332,6 +338,11 @@ class eSCN_Inference_Model(nn.Module):
     # X_m0.  Off by default: at bcc Fe the fused GEMM costs more than the gather traffic it
     # removes (each rotated element is produced once per 128-column tile of the 640 outputs).
     GATHER_IN_CONV1 = False
+    # lmax 2, C = 128, split-fp16 mode: each block's radial output layer writes the gather's
+    # outputs from its GEMM epilogue (fu_radial_gather_fwd: the separate gather kernel and its
+    # read of the radial output are gone; X bitwise as before).  False runs the output GEMM
+    # and the gather as two kernels (the output GEMM then queued early on the side stream).
+    RADIAL_GATHER = True
 
     def __init__(self, num_layers=4, sphere_channels=128, edge_channels=128, num_distance_basis=32, cutoff=5.0,
                  coeff_g=-0.5, lmax=2):
@@ -378,6 +389,16 @@ class eSCN_Inference_Model(nn.Module):
         h2 = layer_norm_silu(linear(h1, self.W_rad1_2, self.b_rad1_2, self.W_rad1_2_t),
                              self.gamma_rad1_2, self.beta_rad1_2)
         return linear(h2, self.W_rad1_3, self.b_rad1_3, self.W_rad1_3_t)
+
+    def _radial_gather(self, layer, k: int) -> bool:
+        """Whether block `layer` (radial output k of the bank) makes its radial output and its
+        gather's outputs in one kernel (RADIAL_GATHER)."""
+        return (self.RADIAL_GATHER and not self.GATHER_IN_CONV1 and self.lmax == 2 and layer.layout in (0, 1)
+                and self.radial_bank.gather_ok(k))
+
+    def _radial_gather_next(self, k: int) -> bool:
+        """The same for the block that reads radial output k (False past the last block)."""
+        return 1 <= k <= len(self.layers) and self._radial_gather(self.layers[k - 1], k)
 
     def _check_atoms(self, Z, batch, n_systems: int) -> None:
         """Atomic numbers index the 100-row element tables and batch ids the per-system
@@ -427,7 +448,8 @@ class eSCN_Inference_Model(nn.Module):
         recompute = idx_i_s.shape[0] >= self.RAD_RECOMPUTE_MIN_EDGES
         rads = self.radial_bank(gauss, Z_s, idx_i_s, idx_j_s, lazy=True)
         rad = rads.get(0)
-        rads.prelaunch(1)
+        if not self._radial_gather_next(1):
+            rads.prelaunch(1)
         # 4. Edge-degree embedding (lmax > 2: with the degree-3/4 Wigner rows)
         wig_ext = None
         if self.lmax == 2:
@@ -443,12 +465,18 @@ class eSCN_Inference_Model(nn.Module):
         balance = self.charge_end > self.charge_start or self.spin_end > self.spin_start
         sys_ptr = system_ptr(batch_s, csd_emb.shape[0]) if balance else None   # batch_s is sorted
         for k, layer in enumerate(self.layers):
-            rad = rads.get(k + 1)
+            if self._radial_gather(layer, k + 1):
+                rad, before = None, None
+                rg = lambda xn, lay, n=k + 1: rads.get_with_gather(n, xn, idx_i_s, idx_j_s, wigner, csd_emb, batch_s,
+                                                                  lay)
+            else:
+                rad, rg = rads.get(k + 1), None
+                before = None if self._radial_gather_next(k + 2) else (lambda n=k + 2: rads.prelaunch(n))
             x_node_s = layer(x_node_s, None, wigner, env, idx_i_s, idx_j_s, row_ptr, col_idx, csd_emb,
                              batch_s, topo, rad_out=rad, wig_ext=wig_ext,
                              rad_src=rads.source(k + 1) if recompute else None, sink=sink,
-                             gather_m0=self.GATHER_IN_CONV1, before_ffn=lambda n=k + 2: rads.prelaunch(n))
-            del rad
+                             gather_m0=self.GATHER_IN_CONV1, before_ffn=before, rad_gather=rg)
+            del rad, rg
             if self.charge_end > self.charge_start:
                 x_node_s = balance_channels_batched(x_node_s, charge, natoms, batch_s, self.charge_start,
                                                     self.charge_end, 0.0, sys_ptr)

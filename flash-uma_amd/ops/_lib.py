@@ -23,7 +23,7 @@ F32 = ctypes.c_float
 SZ_P = ctypes.POINTER(ctypes.c_size_t)
 
 # fu_version() of the library these signatures describe (major*10000 + minor*100 + patch).
-ABI_VERSION = 500
+ABI_VERSION = 600
 
 # Argument types of every exported entry point, in header order.
 SIGNATURES: dict[str, list] = {
@@ -54,6 +54,8 @@ SIGNATURES: dict[str, list] = {
     "fu_linear_weight_split_bytes": [I32, I32],
     "fu_linear_weight_split": [P, I64, I32, I32, P, P],
     "fu_linear_resident": [P, I64, P, P, P, I64, I64, I32, I32, P],
+    "fu_radial_gather_fwd": [P, I64, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, I32, I32, P],
+    "fu_radial_gather_perm": [I32, I32, P],
     "fu_linear_gate": [P, I64, P, I64, P, P, I64, P, I64, P, I64, I64, I32, I32, I32, P, P],
     "fu_gather_linear_gate": [P, P, P, P, P, P, P, P, I64, P, P, I64, P, I64, I64, I32, P],
     "fu_complex_linear_gate": [P, P, I64, P, P, I64, P, P, P, I64, P, P, I64, P, I64, I32, I32, I64, I32, I32, P],

@@ -78,6 +78,36 @@ def gather_bwd(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch, topology, la
     return g_x, (None if sink is not None else bufs[WIGNER]), g_rad
 
 
+def radial_gather_perm(C: int, layout: int) -> torch.Tensor:
+    """(12C,) int64 on the host: row p of the weight that radial_gather_fwd takes is row perm[p]
+    of the radial output layer's weight (fu_radial_gather_perm)."""
+    import ctypes
+    buf = (ctypes.c_int32 * (RAD_MULT * C))()
+    _lib.call("fu_radial_gather_perm", C, int(layout), ctypes.addressof(buf))
+    return torch.tensor(list(buf), dtype=torch.int64)
+
+
+def radial_gather_fwd(h2, W2p, bias_p, x_in, idx_i, idx_j, wigner, csd_emb, batch, layout):
+    """fu_radial_gather_fwd: the radial output layer rad = h2 W3^T + b3 and the gather's
+    (X_m0, X_m1, X_m2) from it in one kernel; returns (rad, X_m0, X_m1, X_m2).  W2p / bias_p:
+    the weight with its rows permuted by radial_gather_perm, pre-split by linear_weight_split,
+    and the bias permuted the same way.  h2 may be a row-strided view with 16-byte aligned rows."""
+    E, K = h2.shape
+    N, _, C = x_in.shape
+    if h2.stride(-1) != 1 or h2.stride(0) % 4 != 0 or h2.data_ptr() % 16 != 0:
+        h2 = h2.contiguous()
+    dev = x_in.device
+    rad = torch.empty((E, RAD_MULT * C), device=dev, dtype=torch.float32)
+    X_m0 = torch.empty((E, X_M0_MULT * C), device=dev, dtype=torch.float32)
+    X_m1 = torch.empty((E, X_M1_MULT * C), device=dev, dtype=torch.float32)
+    X_m2 = torch.empty((E, X_M2_MULT * C), device=dev, dtype=torch.float32)
+    _lib.call("fu_radial_gather_fwd", h2.data_ptr(), h2.stride(0), W2p.data_ptr(), _lib.ptr(bias_p), x_in.data_ptr(),
+              idx_i.data_ptr(), idx_j.data_ptr(), wigner.data_ptr(), csd_emb.data_ptr(), batch.data_ptr(),
+              rad.data_ptr(), X_m0.data_ptr(), X_m1.data_ptr(), X_m2.data_ptr(), E, N, csd_emb.shape[0], C, K,
+              int(layout), _lib.stream_ptr(dev))
+    return rad, X_m0, X_m1, X_m2
+
+
 def gather_operands(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch):
     """The gather's operands as contiguous tensors of the kernel's types."""
     return (_lib.require(x_in, torch.float32, "x_in"), _lib.require(idx_i, torch.int64, "idx_i"),

@@ -317,15 +317,20 @@ class EdgeBlock(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x_in, wigner, wig_ext, rad_out, idx_i, idx_j, csd_emb, batch, topology, layout, lmax, conv1,
-                conv2, C, splits, rad_src, sink=None, gather_m0=False):
+                conv2, C, splits, rad_src, sink=None, gather_m0=False, X_pre=None):
         from .gather import gather_fwd, gather_operands
         from .lmax import gather_lmax_fwd, gather_lmax_operands
         L = int(lmax)
         m0 = None
         if L == 2:
             ops = gather_operands(x_in, idx_i, idx_j, wigner, rad_out, csd_emb, batch)
-            fuse = gather_m0 and int(layout) == 1 and _lib.get_matmul_mode() != _lib.MATMUL_FP32
-            X = list(gather_fwd(*ops, layout, skip_m0=fuse))
+            fuse = gather_m0 and X_pre is None and int(layout) == 1 and _lib.get_matmul_mode() != _lib.MATMUL_FP32
+            if X_pre is not None:
+                # take over the caller's references, so that each part is freed after its GEMM
+                X = list(X_pre)
+                X_pre.clear()
+            else:
+                X = list(gather_fwd(*ops, layout, skip_m0=fuse))
             if fuse:
                 m0 = _gather_conv1_gate_m0(ops, conv1[0], conv1[1], C, _lib.stream_ptr(x_in.device))
         else:
@@ -369,16 +374,19 @@ class EdgeBlock(torch.autograd.Function):
         else:
             g_x, g_w, g_ext, g_rad = gather_lmax_bwd(*ops, ctx.topology, ctx.L, *gx, sink=ctx.sink)
         return (g_x, g_w, g_ext, g_rad, None, None, None, None, None, None, None, None, None, None, None, None,
-                None, None)
+                None, None, None)
 
 
 def edge_block(x_in, wigner, wig_ext, rad_out, idx_i, idx_j, csd_emb, batch, topology, layout, lmax, conv1, conv2, C,
-               splits=None, rad_src=None, sink=None, gather_m0=False):
+               splits=None, rad_src=None, sink=None, gather_m0=False, X_pre=None):
     """gather_wigner_split (or gather_rotate_lmax) followed by conv1_gate_conv2, as one node
     whose gather output never outlives the block: returns (Zout_m0, Zout_m1, Zout_m2).
     rad_src: None, or the radial bank's (h2_k, W3_k, b3_k) source of rad_out; the backward
     then recomputes rad_out from it instead of keeping it (memory for one extra GEMM).
     sink: accumulators of the Wigner-row gradients (ops/edge_grad.py) or None.  gather_m0: conv1
-    m = 0 gathers its own operand (see EdgeBlock)."""
+    m = 0 gathers its own operand (see EdgeBlock).  X_pre: lmax 2, a list of the gather's
+    [X_m0, X_m1, X_m2] already formed from these operands (ops/radial.RadialOutputs.
+    get_with_gather), emptied here; the forward then skips the gather kernel, the backward is the
+    same."""
     return EdgeBlock.apply(x_in, wigner, wig_ext, rad_out, idx_i, idx_j, csd_emb, batch, topology, layout, lmax,
-                           tuple(conv1), tuple(conv2), C, splits, rad_src, sink, gather_m0)
+                           tuple(conv1), tuple(conv2), C, splits, rad_src, sink, gather_m0, X_pre)

@@ -16,6 +16,9 @@ fu_gather_linear_gate keeps the bf16 split in both split modes.
 
 Per-unit figures at C = 128, B = 64 (bytes per edge + bytes per node):
   gating fwd 10240 / bwd 15872; gather fwd 15512 + 4616, bwd 21784 + 9232;
+  radial output layer + gather fwd (fu_radial_gather_fwd, K = 128) 16,024 + 4,616, with
+  2 * 12C * K flops per edge on the matrix cores (HBM-bound: 3.9 GB against 0.29 PFLOP
+  executed per launch at bcc Fe);
   scatter fwd 4752 + 9220, bwd 9504 + 4608; init scatter fwd 1576 + 5640, bwd 3256 + 4608;
   geom fwd 1448 (+ 1024 with embeddings) + 20, bwd 436 + 12; ln_silu 1032 / 1544 per row
   (grouped: per row and group, plus 16 B of edge ids per row when the tables are used).
@@ -179,6 +182,14 @@ def _gating_bwd_l(a):
     return E * C * (17 * L - 3) * 4, 0
 
 
+def _radial_gather(a):
+    # the radial output layer fused with the gather: h2 (E, K) read, rad (12C) and X (18C)
+    # written per edge, the edge's two ids and 34 Wigner scalars read, the weight once, the node
+    # rows counted once per launch (as the gather's)
+    E, N, C, K = a[14], a[15], a[17], a[18]
+    return E * ((K + 30 * C + 34) * 4 + 16) + N * (9 * C * 4 + 8) + 12 * C * K * 4, 2 * E * 12 * C * K
+
+
 def _wig_ext_fwd(a):
     E, L = a[2], a[3]
     return E * (34 + _ext(L)) * 4, 0
@@ -291,6 +302,7 @@ WORK = {
     "fu_linear": _linear,
     "fu_linear_batched": _linear_batched,
     "fu_linear_resident": _linear_resident,
+    "fu_radial_gather_fwd": _radial_gather,
     "fu_linear_ln_silu": _linear_ln_silu,
     "fu_linear_ln_silu_bwd": _linear_ln_silu_bwd,
     "fu_linear_dgrad_ln_silu_bwd": _linear_dgrad_ln_silu_bwd,

@@ -42,7 +42,7 @@ extern "C" {
 #define FU_ERR_NULL (-5)        /* a required pointer is NULL */
 #define FU_ERR_WORKSPACE (-6)   /* the workspace is too small */
 
-/* Library version (major*10000 + minor*100 + patch): 500 (0.5.0) for the signatures in this
+/* Library version (major*10000 + minor*100 + patch): 600 (0.6.0) for the signatures in this
  * header.  0.2.0 added the int32 `accumulate` argument (before the stream) of fu_gather_bwd,
  * fu_scatter_bwd, fu_init_scatter_bwd, their _lmax forms and fu_complex_linear_gate(_bwd), and
  * dropped one pointer/stride pair of fu_linear_gate_bwd; 0.3.0 changed the layout and size of
@@ -50,7 +50,8 @@ extern "C" {
  * arguments of fu_gather_fwd_lmax; 0.4.0 added fu_linear_weight_split_bytes,
  * fu_linear_weight_split and fu_linear_resident (nothing changed); 0.5.0 added the W2 argument
  * (before the stream) of fu_linear, fu_linear_gate, fu_linear_gate_bwd and
- * fu_linear_dgrad_ln_silu_bwd.  A caller built against
+ * fu_linear_dgrad_ln_silu_bwd; 0.6.0 added fu_radial_gather_fwd and fu_radial_gather_perm
+ * (nothing changed).  A caller built against
  * another version must not call into this library. */
 int fu_version(void);
 
@@ -354,6 +355,26 @@ int fu_linear_weight_split(const float* W, int64_t ldw, int32_t N, int32_t K, vo
  * may be NULL.  M = 0 is a no-op. */
 int fu_linear_resident(const float* A, int64_t lda, const void* W2, const float* bias, float* Y, int64_t ldy,
                        int64_t M, int32_t N, int32_t K, void* stream);
+
+/* The radial output layer fused with the gather-rotate forward (lmax 2, C = 128; replaces
+ * model.py:149 rad_out = h2 W_rad1_3^T + b_rad1_3 followed by ops/gather.py:34-154
+ * gather_wigner_split, whose only reader of rad_out in the forward is the gather): writes rad
+ * (E, 12C) in the natural order (as fu_linear_resident with the unpermuted weight would, for the
+ * gather backward) and X_m0 (E, 6C), X_m1 (E, 8C), X_m2 (E, 4C) exactly as fu_gather_fwd with
+ * that rad (bitwise).  W2 is the radial weight (12C x K) with its rows permuted by
+ * fu_radial_gather_perm, pre-split by fu_linear_weight_split; bias is the bias permuted the same
+ * way (may be NULL).  h2: (E, K) rows with stride ldh.  C = K = 128, layout 0 or 1 (as
+ * fu_gather_fwd); every array 16-byte aligned, ldh a multiple of 4.  Split-fp16 products as
+ * fu_linear_resident, whatever fu_set_matmul_mode selects.  E = 0 is a no-op. */
+int fu_radial_gather_fwd(const float* h2, int64_t ldh, const void* W2, const float* bias, const float* x,
+                         const int64_t* idx_i, const int64_t* idx_j, const float* wigner, const float* csd_emb,
+                         const int64_t* batch, float* rad, float* X_m0, float* X_m1, float* X_m2, int64_t E,
+                         int64_t N, int64_t S, int32_t C, int32_t K, int32_t layout, void* stream);
+
+/* Host-only: perm[p] (12C entries) = the radial column that fu_radial_gather_fwd computes as its
+ * weight's row p.  Output tile t (96 columns) holds three radial blocks of one side for 32
+ * channels (see radial_gather.hip).  C = 128, layout 0 or 1. */
+int fu_radial_gather_perm(int32_t C, int32_t layout, int32_t* perm);
 
 /* conv1 m = 0 fused with the gate activation (model.py:152-153 with ops/gating.py:32-103):
  * Y = A W^T + bias with N = (2L+1)C columns (L = lmax) in the gate-paired order: 64-column

@@ -286,3 +286,41 @@ def test_linear_weight_split_arguments():
     # the resident GEMM takes K <= 128 only
     st, msg = _status("fu_linear_resident", 16, 144, 16, None, 16, 64, 10, 64, 144, None)
     assert st == -1 and "K=144" in msg
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+def test_radial_gather_perm(layout):
+    """fu_radial_gather_perm (host only): a permutation of the 12C radial columns whose 96-column
+    tiles each hold three radial blocks of one side for 32 consecutive channels, the m = 0 blocks
+    (l = 0, 1, 2) in even tiles and the |m| = 1, 1, 2 blocks in odd ones, in the slot order of
+    the gather's layout (layout 0: block 2q + side; layout 1: 6 side + q)."""
+    from ops.gather import radial_gather_perm
+    C = 128
+    perm = radial_gather_perm(C, layout).tolist()
+    assert sorted(perm) == list(range(12 * C))
+    for t in range(16):
+        so, cg, hq = t >> 3, (t >> 1) & 3, t & 1
+        for j in range(3):
+            q = 3 * hq + j
+            block = 2 * q + so if layout == 0 else 6 * so + q
+            cols = perm[96 * t + 32 * j:96 * t + 32 * j + 32]
+            assert cols == [block * C + 32 * cg + c for c in range(32)]
+    st, msg = _status("fu_radial_gather_perm", 64, layout, None)
+    assert st == -2 and "C=64" in msg
+    st, msg = _status("fu_radial_gather_perm", C, 2, None)
+    assert st == -2 and "layout=2" in msg
+    st, msg = _status("fu_radial_gather_perm", C, layout, None)
+    assert st == -5
+
+
+def test_radial_gather_fwd_argument_checks():
+    """Shape, layout and NULL checks of fu_radial_gather_fwd, before any launch."""
+    args = lambda ldh, C, K, layout: (None, ldh, *([None] * 12), 10, 4, 1, C, K, layout, None)
+    st, msg = _status("fu_radial_gather_fwd", *args(128, 64, 128, 1))
+    assert st == -2 and "C=64" in msg
+    st, msg = _status("fu_radial_gather_fwd", *args(128, 128, 64, 1))
+    assert st == -2 and "K=64" in msg
+    st, msg = _status("fu_radial_gather_fwd", *args(64, 128, 128, 1))
+    assert st == -1
+    st, msg = _status("fu_radial_gather_fwd", *args(128, 128, 128, 1))
+    assert st == -5

@@ -175,7 +175,8 @@ def test_resident_rejects_bad_shapes(cuda):
 
 def test_model_output_layers_use_resident_kernel(cuda, monkeypatch):
     """In the default (split-fp16) mode the radial bank's output layers run on
-    fu_linear_resident (one launch per MLP in the forward), in the other modes on fu_linear."""
+    fu_linear_resident or, for the blocks' layers (RADIAL_GATHER), fu_radial_gather_fwd (one
+    launch per MLP in the forward), in the other modes on fu_linear."""
     import escn_md
     import heads
     import systems
@@ -187,7 +188,7 @@ def test_model_output_layers_use_resident_kernel(cuda, monkeypatch):
     s = systems.cu_slab_co()
     ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, bb.cutoff, bb.max_neighbors)
     real = _lib.call
-    for mode, want in ((_lib.MATMUL_SPLIT_F16, 3), (_lib.MATMUL_SPLIT_BF16, 0)):
+    for mode, want, fused in ((_lib.MATMUL_SPLIT_F16, 1, 2), (_lib.MATMUL_SPLIT_BF16, 0, 0)):
         calls = []
 
         def spy(name, *args):
@@ -200,4 +201,5 @@ def test_model_output_layers_use_resident_kernel(cuda, monkeypatch):
             torch.cuda.synchronize()
         monkeypatch.setattr(_lib, "call", real)
         assert calls.count("fu_linear_resident") == want, (mode, calls.count("fu_linear_resident"))
+        assert calls.count("fu_radial_gather_fwd") == fused, (mode, calls.count("fu_radial_gather_fwd"))
         assert torch.isfinite(out["forces"]).all()
