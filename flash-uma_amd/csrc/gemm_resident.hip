@@ -19,13 +19,13 @@
 //    nontemporal stores (the outputs are read once, by a later kernel); the 4-byte stores of
 //    the accumulator layout (two 128-byte row pieces per instruction) held the kernel at
 //    2.8 TB/s of output.
-#include "split_f16.h"
+#include "resident_panel.h"
 
 namespace fu {
 
-constexpr int RBM = 128;          // rows per workgroup
+constexpr int RBM = kResRows;     // rows per workgroup
 constexpr int RKC_MAX = 8;        // 16-wide K chunks: K <= 128
-constexpr int RPLANE = RBM * 16;  // fp16 per plane (one chunk of the panel)
+constexpr int RPLANE = kResPlane;  // fp16 per plane (one chunk of the panel)
 constexpr int RES = 64 + 8;       // floats per row of a wave's epilogue slice: 4 RES = 32 mod 64 banks
 
 // The pre-split weight's layout: split_f16.h (resident_frag_vectors, resident_cols).
@@ -104,58 +104,7 @@ __global__ __launch_bounds__(256, 2) void linear_resident_kernel(const float* __
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row0 = (int64_t)blockIdx.x * RBM;
 
-  // ---- the A panel: thread (r, h) holds k = 16 kc + 8 h .. + 7 of row r for every chunk kc
-  // (one piece per chunk); a row past M reads the last row, whose outputs are not stored
-  const int r = tid >> 1, h = tid & 1;
-  const int64_t gr = row0 + r < M ? row0 + r : M - 1;
-  const float* pa = A + gr * lda + 8 * h;
-  float4 v[KC][2];
-#pragma unroll
-  for (int kc = 0; kc < KC; ++kc) {
-    v[kc][0] = ld4(pa + 16 * kc);
-    v[kc][1] = ld4(pa + 16 * kc + 4);
-  }
-  float pm[KC];
-  float R = 0.0f;
-#pragma unroll
-  for (int kc = 0; kc < KC; ++kc) {
-    pm[kc] = amax8(v[kc][0], v[kc][1]);
-    R = fmaxf(R, pm[kc]);
-  }
-  R = fmaxf(R, __shfl_xor(R, 1));
-  const int e = f16_exp_row(R);
-  const float sc = pow2i(e);
-  bool low = false;
-  float pmin = R, pmax = 0.0f;
-#pragma unroll
-  for (int kc = 0; kc < KC; ++kc) {
-    low = low || f16_lossy(pm[kc] * sc);
-    pmin = fminf(pmin, pm[kc]);
-    pmax = fmaxf(pmax, pm[kc]);
-  }
-  pmin = fminf(pmin, __shfl_xor(pmin, 1));
-  pmax = fmaxf(pmax, __shfl_xor(pmax, 1));
-  const bool rough = !f16_flat(pmin, pmax);
-  // pass 2 of split_f16.h for the whole panel when a piece below the window meets a rough
-  // operand on the other side (the weight side from its summary word)
-  const int ws = *wsum;
-  const bool mine = (low && (ws & 2)) || ((ws & 1) && rough);
-  const unsigned long long bal = __ballot(mine);
-  if (lane == 0) s_need[wave] = bal != 0ull;
-  if (h == 0) s_rinv[r] = pow2i(-e);
-  __syncthreads();
-  const bool need2 = (s_need[0] | s_need[1] | s_need[2] | s_need[3]) != 0u;
-#pragma unroll
-  for (int kc = 0; kc < KC; ++kc) {
-    uint4 H, L;
-    const float4 a0 = scale4(v[kc][0], sc), a1 = scale4(v[kc][1], sc);
-    if (need2)
-      split2h_up(a0, a1, H, L);
-    else
-      split2h(a0, a1, H, L);
-    st_planes2(sp + kc * 2 * RPLANE, RPLANE, plane_off(r, h), H, L);
-  }
-  __syncthreads();
+  const bool need2 = resident_panel<KC>(A, lda, wsum, sp, s_rinv, s_need, row0, M);
 
   // ---- every 128-column tile of the output
   const int fr = lane & 31, fh = lane >> 5;
@@ -163,31 +112,6 @@ __global__ __launch_bounds__(256, 2) void linear_resident_kernel(const float* __
   const int nb = (N + 31) / 32;
   const int ntiles = (N + 127) / 128;
   const uint4* wf = W2 + lane;
-  // K loop over the products q in [Q0, Q1) of kF16A / kF16B; LOP: the lo planes are lo'
-  auto kloop = [&](auto q0c, auto q1c, auto lopc, const int (&cb)[2], floatx16 (&acc)[2][2]) {
-    constexpr int Q0 = decltype(q0c)::value, Q1 = decltype(q1c)::value;
-    constexpr bool LOP = decltype(lopc)::value;
-#pragma unroll
-    for (int kc = 0; kc < KC; ++kc) {
-      f16x8 bq[2][2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int64_t base = ((int64_t)cb[j] * KC + kc) * 3 * 64;
-        bq[j][0] = __builtin_bit_cast(f16x8, wf[base]);
-        bq[j][1] = __builtin_bit_cast(f16x8, wf[base + (LOP ? 128 : 64)]);
-      }
-      f16x8 aq[2][2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        ld_planes2(reinterpret_cast<const __bf16*>(sp) + kc * 2 * RPLANE, RPLANE, plane_off(wr + 32 * i + fr, fh), aq[i]);
-#pragma unroll
-      for (int q = Q0; q < Q1; ++q)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j) acc[i][j] = mfma_f16(aq[i][kF16A[q]], bq[j][kF16B[q]], acc[i][j]);
-    }
-  };
   for (int nt = 0; nt < ntiles; ++nt) {
     int cb[2];
 #pragma unroll
@@ -196,24 +120,7 @@ __global__ __launch_bounds__(256, 2) void linear_resident_kernel(const float* __
       cb[j] = b < nb ? b : nb - 1;  // a block past N reads the last one; nothing of it is stored
     }
     floatx16 acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int t = 0; t < 16; ++t) acc[i][j][t] = 0.0f;
-    if (!need2) {
-      kloop(std::integral_constant<int, 0>{}, std::integral_constant<int, 3>{}, std::false_type{}, cb, acc);
-    } else {
-      kloop(std::integral_constant<int, 0>{}, std::integral_constant<int, 2>{}, std::true_type{}, cb, acc);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int t = 0; t < 16; ++t) acc[i][j][t] *= F16_LO_DOWN;
-      kloop(std::integral_constant<int, 2>{}, std::integral_constant<int, 3>{}, std::true_type{}, cb, acc);
-    }
+    resident_tile<KC, 2, 2, KC>(sp, wf, cb, acc, need2, wr, fr, fh);
     // epilogue, 8 rows at a time: lane (fr, fh) holds column fr of each block and rows
     // 8 (t / 4) + 4 fh + t % 4; it stages them in its wave's slice, then reads back 4 consecutive
     // columns (c4 = lane % 16) of rows lane / 16 and lane / 16 + 4 for 16-byte stores (VEC), or
