@@ -10,15 +10,18 @@
 //
 // Column order.  The weight's 12 C rows are permuted (fu_radial_gather_perm) so that output
 // tile t (96 columns, t = 0..15) holds three radial blocks of one side for 32 channels: side
-// so = t / 8, channel group cg = (t / 2) % 4, blocks q = 3 (t % 2) + j, j = 0..2 (the m = 0 blocks
-// q = 0, 1, 2 or the |m| = 1, 1, 2 blocks q = 3, 4, 5); column 96 t + 32 j + ch is radial column
-// slot_rad(so, q) C + 32 cg + ch of the natural order.  Each of the 4 waves computes 32 rows of
-// every tile (three 32 x 32 blocks: 48 accumulators, so that the epilogue's node rows and Wigner
-// scalars fit beside them at two workgroups per CU).  In the epilogue a lane takes one edge
-// (slice row) and 4 channels: it reads the edge's node row pieces (9 or 8 coefficients x 16
-// bytes) and Wigner scalars, rotates them exactly as the gather kernel does (same products in
-// the same order, so X is bitwise the gather's) and writes rad and the tile's X slots as
-// 16-byte pieces (8 lanes of one edge cover 128 contiguous bytes).
+// so = t / 8, channel group cg = (t / 2) % 4, and the blocks of degrees 0 and 1 ((l, |m|) =
+// (0, 0), (1, 0), (1, 1)) for even t or of degree 2 ((2, 0), (2, 1), (2, 2)) for odd t; column
+// 96 t + 32 j + ch is radial column slot_rad(so, q) C + 32 cg + ch of the natural order, q =
+// tile_block(t % 2, j).  Grouping by degree lets a tile read each node coefficient it rotates
+// once (rows 0..3 or 4..8; grouped by |m| instead, rows 1..8 were read by both tiles of a pair:
+// 877 against 831 us at bcc Fe).  Each of the 4 waves computes 32 rows of every tile (three
+// 32 x 32 blocks: 48 accumulators, so that the epilogue's node rows and Wigner scalars fit
+// beside them at two workgroups per CU).  In the epilogue a lane takes one edge (slice row)
+// and 4 channels: it reads the edge's node row pieces (4 or 5 coefficients x 16 bytes) and
+// Wigner scalars, rotates them exactly as the gather kernel does (same products in the same
+// order, so X is bitwise the gather's) and writes rad and the tile's X slots as 16-byte pieces
+// (8 lanes of one edge cover 128 contiguous bytes).
 //
 // The K loop and the panel are those of fu_linear_resident (split-fp16, weight fragments
 // straight from global memory, pass 2 of split_f16.h for a panel the window rule sends there).
@@ -48,6 +51,10 @@ __device__ __forceinline__ float4 rot5(const float* w, const float4 (&v)[9]) {
                      w[0] * v[4].z + w[1] * v[5].z + w[2] * v[6].z + w[3] * v[7].z + w[4] * v[8].z,
                      w[0] * v[4].w + w[1] * v[5].w + w[2] * v[6].w + w[3] * v[7].w + w[4] * v[8].w);
 }
+
+// radial block (slot q of a side) of column block j of a tile of degree group hq: degrees 0, 1
+// (blocks (0, 0), (1, 0), (1, 1)) or degree 2 ((2, 0), (2, 1), (2, 2))
+__host__ __device__ constexpr int tile_block(int hq, int j) { return hq == 0 ? (j < 2 ? j : 3) : (j == 0 ? 2 : j + 3); }
 
 __device__ __forceinline__ float4 mul4(const float4& a, const float4& b) {
   return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
@@ -90,7 +97,7 @@ __global__ __launch_bounds__(256, 2) void radial_gather_kernel(
     bid[1][g8] = (int32_t)batch[nid[1][g8]];
   }
   for (int t = 0; t < NT; ++t) {
-    // tile t: side so, channel group cg, radial blocks q = 3 hq .. 3 hq + 2 (hq 0: m = 0)
+    // tile t: side so, channel group cg, the radial blocks of degrees 0, 1 (hq 0) or 2 (hq 1)
     const int so = t >> 3, cg = (t >> 1) & 3, hq = t & 1;
     int cb[3];
 #pragma unroll
@@ -126,28 +133,33 @@ __global__ __launch_bounds__(256, 2) void radial_gather_kernel(
         }
         float* re = rad + e * 12 * CH + ch;
 #pragma unroll
-        for (int j = 0; j < 3; ++j) st4_nt(re + slot_rad<LAYOUT>(so, 3 * hq + j) * CH, rv[j]);
+        for (int j = 0; j < 3; ++j) st4_nt(re + slot_rad<LAYOUT>(so, tile_block(hq, j)) * CH, rv[j]);
         const int64_t node = so ? nid[1][g8] : nid[0][g8];
         const float* xn = x + node * 9 * CH + ch;
         const float* w = wig + e * 34;
         float4 v[9];
-#pragma unroll
-        for (int k = 1; k < 9; ++k) v[k] = ld4(xn + k * CH);
         if (hq == 0) {
-          // X_m0 slots q = 0, 1, 2: rotated coefficients 0, 2, 6
+          // degrees 0 and 1: X_m0 slots 0, 1 (rotated coefficients 0, 2), X_m1 slots 0, 2
+          // (coefficients 3, 1)
+#pragma unroll
+          for (int k = 1; k < 4; ++k) v[k] = ld4(xn + k * CH);
           const float4 x0 = ld4(xn), c0 = ld4(csd + (int64_t)(so ? bid[1][g8] : bid[0][g8]) * CH + ch);
           v[0] = make_float4(x0.x + c0.x, x0.y + c0.y, x0.z + c0.z, x0.w + c0.w);
           float* o0 = X0 + e * 6 * CH + ch;
+          float* o1 = X1 + e * 8 * CH + ch;
           st4_nt(o0 + slot_m0<LAYOUT>(so, 0) * CH, mul4(v[0], rv[0]));
           st4_nt(o0 + slot_m0<LAYOUT>(so, 1) * CH, mul4(rot3(w[3], w[4], w[5], v[1], v[2], v[3]), rv[1]));
-          st4_nt(o0 + slot_m0<LAYOUT>(so, 2) * CH, mul4(rot5(w + 19, v), rv[2]));
+          st4_nt(o1 + slot_m1<LAYOUT>(so, 0) * CH, mul4(rot3(w[6], w[7], w[8], v[1], v[2], v[3]), rv[2]));
+          st4_nt(o1 + slot_m1<LAYOUT>(so, 2) * CH, mul4(rot3(w[0], w[1], w[2], v[1], v[2], v[3]), rv[2]));
         } else {
-          // X_m1 slots q = 0..3: rotated coefficients 3, 7, 1, 5 (radial blocks 3, 4, 3, 4);
-          // X_m2 slots q = 0, 1: coefficients 8, 4 (radial block 5)
+          // degree 2: X_m0 slot 2 (coefficient 6), X_m1 slots 1, 3 (coefficients 7, 5), X_m2
+          // slots 0, 1 (coefficients 8, 4)
+#pragma unroll
+          for (int k = 4; k < 9; ++k) v[k] = ld4(xn + k * CH);
+          float* o0 = X0 + e * 6 * CH + ch;
           float* o1 = X1 + e * 8 * CH + ch;
           float* o2 = X2 + e * 4 * CH + ch;
-          st4_nt(o1 + slot_m1<LAYOUT>(so, 0) * CH, mul4(rot3(w[6], w[7], w[8], v[1], v[2], v[3]), rv[0]));
-          st4_nt(o1 + slot_m1<LAYOUT>(so, 2) * CH, mul4(rot3(w[0], w[1], w[2], v[1], v[2], v[3]), rv[0]));
+          st4_nt(o0 + slot_m0<LAYOUT>(so, 2) * CH, mul4(rot5(w + 19, v), rv[0]));
           st4_nt(o1 + slot_m1<LAYOUT>(so, 1) * CH, mul4(rot5(w + 24, v), rv[1]));
           st4_nt(o1 + slot_m1<LAYOUT>(so, 3) * CH, mul4(rot5(w + 14, v), rv[1]));
           st4_nt(o2 + slot_m2<LAYOUT>(so, 0) * CH, mul4(rot5(w + 29, v), rv[2]));
@@ -169,7 +181,7 @@ static void radial_gather_perm_fill(int32_t* perm) {
   for (int t = 0; t < rg::NT; ++t)
     for (int j = 0; j < 3; ++j)
       for (int c = 0; c < 32; ++c)
-        perm[t * rg::TN + 32 * j + c] = slot_rad<LAYOUT>(t >> 3, 3 * (t & 1) + j) * rg::CH + 32 * ((t >> 1) & 3) + c;
+        perm[t * rg::TN + 32 * j + c] = slot_rad<LAYOUT>(t >> 3, rg::tile_block(t & 1, j)) * rg::CH + 32 * ((t >> 1) & 3) + c;
 }
 
 extern "C" int fu_radial_gather_perm(int32_t C, int32_t layout, int32_t* perm) {

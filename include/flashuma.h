@@ -372,8 +372,9 @@ int fu_radial_gather_fwd(const float* h2, int64_t ldh, const void* W2, const flo
                          int64_t N, int64_t S, int32_t C, int32_t K, int32_t layout, void* stream);
 
 /* Host-only: perm[p] (12C entries) = the radial column that fu_radial_gather_fwd computes as its
- * weight's row p.  Output tile t (96 columns) holds three radial blocks of one side for 32
- * channels (see radial_gather.hip).  C = 128, layout 0 or 1. */
+ * weight's row p.  Output tile t (96 columns) holds the three radial blocks of degrees 0 and 1
+ * (even t) or of degree 2 (odd t) of side t / 8 for channels 32 ((t / 2) % 4) .. + 31
+ * (radial_gather.hip).  C = 128, layout 0 or 1. */
 int fu_radial_gather_perm(int32_t C, int32_t layout, int32_t* perm);
 
 /* conv1 m = 0 fused with the gate activation (model.py:152-153 with ops/gating.py:32-103):

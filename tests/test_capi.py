@@ -291,9 +291,10 @@ def test_linear_weight_split_arguments():
 @pytest.mark.parametrize("layout", [0, 1])
 def test_radial_gather_perm(layout):
     """fu_radial_gather_perm (host only): a permutation of the 12C radial columns whose 96-column
-    tiles each hold three radial blocks of one side for 32 consecutive channels, the m = 0 blocks
-    (l = 0, 1, 2) in even tiles and the |m| = 1, 1, 2 blocks in odd ones, in the slot order of
-    the gather's layout (layout 0: block 2q + side; layout 1: 6 side + q)."""
+    tiles each hold three radial blocks of one side for 32 consecutive channels, those of
+    degrees 0 and 1 ((l, |m|) = (0, 0), (1, 0), (1, 1): slots 0, 1, 3) in even tiles and of
+    degree 2 ((2, 0), (2, 1), (2, 2): slots 2, 4, 5) in odd ones, in the slot order of the
+    gather's layout (layout 0: block 2q + side; layout 1: 6 side + q)."""
     from ops.gather import radial_gather_perm
     C = 128
     perm = radial_gather_perm(C, layout).tolist()
@@ -301,7 +302,7 @@ def test_radial_gather_perm(layout):
     for t in range(16):
         so, cg, hq = t >> 3, (t >> 1) & 3, t & 1
         for j in range(3):
-            q = 3 * hq + j
+            q = ((0, 1, 3), (2, 4, 5))[hq][j]
             block = 2 * q + so if layout == 0 else 6 * so + q
             cols = perm[96 * t + 32 * j:96 * t + 32 * j + 32]
             assert cols == [block * C + 32 * cg + c for c in range(32)]
