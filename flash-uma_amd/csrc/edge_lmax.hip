@@ -22,35 +22,11 @@
 // accumulators, segments in CSR order; backward gather node-centric (one wave per CSR
 // segment of the node, as receiver and as sender), so no kernel uses atomics.  The l blocks
 // are processed one at a time to bound registers.
+#include "edge_lmax_layout.h"
 #include "fu_vec.h"
 
 namespace fu {
 namespace lm {
-
-constexpr int mmx(int l) { return l < 2 ? l : 2; }
-constexpr int ncoef(int L) { return (L + 1) * (L + 1); }
-constexpr int extw(int L) { return L >= 4 ? 80 : L == 3 ? 35 : 0; }
-constexpr int wx0(int L) { return 2 * (L + 1); }
-constexpr int wx1(int L) { return 4 * L; }
-constexpr int wx2(int L) { return 4 * (L - 1); }
-constexpr int wrad(int L) { return 6 * L; }
-constexpr int xblk(int L, int l, int m, int so) {
-  return m == 0 ? 2 * l + so
-         : (m == 1 || m == -1) ? 2 * ((m > 0 ? 0 : L) + l - 1) + so
-                               : 2 * ((m > 0 ? 0 : L - 1) + l - 2) + so;
-}
-constexpr int radblk(int L, int l, int am, int so) {
-  return am == 0 ? 2 * l + so : am == 1 ? 2 * (L + 1) + 2 * (l - 1) + so : 4 * L + 2 + 2 * (l - 2) + so;
-}
-// block of (l, m) in Z_m0 / Z_m1 / Z_m2 (no sides)
-constexpr int zblk(int L, int l, int m) {
-  return m == 0 ? l : (m == 1 || m == -1) ? (m > 0 ? 0 : L) + l - 1 : (m > 0 ? 0 : L - 1) + l - 2;
-}
-// index of D^l[m][mp] in the reference's 34 scalars (l <= 2) or in the ext array (l >= 3)
-constexpr int widx(int l, int m, int mp) {
-  return l == 1 ? 3 * (1 + m) + 1 + mp : l == 2 ? 9 + 5 * (2 + m) + 2 + mp
-         : l == 3 ? 7 * (2 + m) + 3 + mp : 35 + 9 * (2 + m) + 4 + mp;
-}
 
 template <int l>
 __device__ __forceinline__ float dwig(const float* wl, const float* we, int m, int mp) {

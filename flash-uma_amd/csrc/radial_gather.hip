@@ -26,6 +26,7 @@
 // The K loop and the panel are those of fu_linear_resident (split-fp16, weight fragments
 // straight from global memory, pass 2 of split_f16.h for a panel the window rule sends there).
 #include "edge_layout.h"
+#include "edge_lmax_layout.h"
 #include "resident_panel.h"
 
 namespace fu {
@@ -173,6 +174,149 @@ __global__ __launch_bounds__(256, 2) void radial_gather_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// lmax 3 and 4 (the reference block order extended by degree, edge_lmax_layout.h).  Tiles per
+// side and channel group: degree group g = 0 (degrees 0 and 1: radial (0, 0), (1, 0), (1, 1)),
+// then g = 1 .. L - 1 (degree g + 1: (l, 0), (l, 1), (l, 2)); tile t = ((so 4 + cg) L + g).
+// The epilogue rotates each degree's node coefficients with the lmax gather's arithmetic
+// (gather_fwd_block of edge_lmax.hip: rv = 0, rv += D[m][mp] v[mp] for mp = -l .. l).
+// ---------------------------------------------------------------------------------------
+
+// (l, |m|) of column block j of degree group g
+__host__ __device__ constexpr int grp_l(int g, int j) { return g == 0 ? (j == 0 ? 0 : 1) : g + 1; }
+__host__ __device__ constexpr int grp_am(int g, int j) { return g == 0 ? (j == 2 ? 1 : 0) : j; }
+
+// X slots (l, m), |m| <= min(l, 2), of one edge side for degree l >= 1 from its node row
+// pieces v (row l^2 + l + mp at v[l + mp]) and the radial values rv[|m|]
+template <int L, int l>
+__device__ __forceinline__ void lm_slots(const float4 (&v)[2 * l + 1], const float4* rv, const float* wl,
+                                         const float* we, float* X0e, float* X1e, float* X2e, int so) {
+  constexpr int mm = lm::mmx(l);
+#pragma unroll
+  for (int am = 0; am <= mm; ++am) {
+#pragma unroll
+    for (int s2 = 0; s2 < (am == 0 ? 1 : 2); ++s2) {
+      const int m = s2 == 0 ? am : -am;
+      float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int mp = -l; mp <= l; ++mp) {
+        const float w = l <= 2 ? wl[lm::widx(l, m, mp)] : we[lm::widx(l, m, mp)];
+        r.x += w * v[l + mp].x;
+        r.y += w * v[l + mp].y;
+        r.z += w * v[l + mp].z;
+        r.w += w * v[l + mp].w;
+      }
+      float* base = am == 0 ? X0e : am == 1 ? X1e : X2e;
+      st4_nt(base + lm::xblk(L, l, m, so) * CH, mul4(r, rv[am]));
+    }
+  }
+}
+
+template <int L, int l>
+__device__ __forceinline__ void lm_degree(const float* xn, const float4* rv, const float* wl, const float* we,
+                                          float* X0e, float* X1e, float* X2e, int so) {
+  float4 v[2 * l + 1];
+#pragma unroll
+  for (int k = 0; k < 2 * l + 1; ++k) v[k] = ld4(xn + (l * l + k) * CH);
+  lm_slots<L, l>(v, rv, wl, we, X0e, X1e, X2e, so);
+}
+
+template <int L>
+__global__ __launch_bounds__(256, 2) void radial_gather_lmax_kernel(
+    const float* __restrict__ A, int64_t lda, const uint4* __restrict__ W2, const float* __restrict__ cinv,
+    const int* __restrict__ wsum, const float* __restrict__ bias, const float* __restrict__ x,
+    const int64_t* __restrict__ idx_i, const int64_t* __restrict__ idx_j, const float* __restrict__ wig,
+    const float* __restrict__ ext, const float* __restrict__ csd, const int64_t* __restrict__ batch,
+    float* __restrict__ rad, float* __restrict__ X0, float* __restrict__ X1, float* __restrict__ X2, int64_t M) {
+  constexpr int NK = lm::ncoef(L), EW = lm::extw(L), NTL = 8 * L;
+  __shared__ __attribute__((aligned(16))) __bf16 sp[KC * 2 * RPLANE];  // [chunk][hi, lo or lo'][plane]
+  __shared__ float s_rinv[RBM];
+  __shared__ unsigned s_need[4];
+  __shared__ __attribute__((aligned(16))) float s_ep[4][8 * RES3];  // one slice per wave
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row0 = (int64_t)blockIdx.x * RBM;
+  const bool need2 = resident_panel<KC>(A, lda, wsum, sp, s_rinv, s_need, row0, M);
+
+  const int fr = lane & 31, fh = lane >> 5;
+  const int wr = 32 * wave;                 // this wave's 32 rows of every tile
+  const int rr = lane >> 3, c4 = lane & 7;  // epilogue: slice row (edge), channel quad
+  const uint4* wf = W2 + lane;
+  float* ep = s_ep[wave];
+  int32_t nid[2][4], bid[2][4];  // as in radial_gather_kernel
+#pragma unroll
+  for (int g8 = 0; g8 < 4; ++g8) {
+    const int64_t e = row0 + wr + 8 * g8 + rr;
+    const int64_t ec = e < M ? e : M - 1;
+    nid[0][g8] = (int32_t)idx_i[ec];
+    nid[1][g8] = (int32_t)idx_j[ec];
+  }
+#pragma unroll
+  for (int g8 = 0; g8 < 4; ++g8) {
+    bid[0][g8] = (int32_t)batch[nid[0][g8]];
+    bid[1][g8] = (int32_t)batch[nid[1][g8]];
+  }
+  for (int t = 0; t < NTL; ++t) {
+    const int g = t % L, cg = (t / L) & 3, so = t / (4 * L);
+    int cb[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) cb[j] = 3 * t + j;
+    floatx16 acc[1][3];
+    resident_tile<KC, 1, 3, 2>(sp, wf, cb, acc, need2, wr, fr, fh);
+    const int ch = 32 * cg + 4 * c4;
+    const int col0 = t * TN + 4 * c4;
+#pragma unroll
+    for (int g8 = 0; g8 < 4; ++g8) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < 3; ++j)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) ep[(4 * fh + s) * RES3 + 32 * j + fr] = acc[0][j][4 * g8 + s];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int rb = wr + 8 * g8;
+      const int64_t e = row0 + rb + rr;
+      if (e < M) {
+        const float rf = s_rinv[rb + rr];
+        float4 rv[3];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          const float4 a4 = ld4(ep + rr * RES3 + 32 * j + 4 * c4);
+          const float4 cs = ld4(cinv + col0 + 32 * j);
+          const float4 bv = bias ? ld4(bias + col0 + 32 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
+          rv[j] = make_float4(a4.x * rf * cs.x + bv.x, a4.y * rf * cs.y + bv.y, a4.z * rf * cs.z + bv.z,
+                              a4.w * rf * cs.w + bv.w);
+        }
+        float* re = rad + e * lm::wrad(L) * CH + ch;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) st4_nt(re + lm::radblk(L, grp_l(g, j), grp_am(g, j), so) * CH, rv[j]);
+        const float* xn = x + (int64_t)(so ? nid[1][g8] : nid[0][g8]) * NK * CH + ch;
+        const float* wl = wig + e * 34;
+        const float* we = ext + e * EW;
+        float* X0e = X0 + e * lm::wx0(L) * CH + ch;
+        float* X1e = X1 + e * lm::wx1(L) * CH + ch;
+        float* X2e = X2 + e * lm::wx2(L) * CH + ch;
+        if (g == 0) {
+          // degree 0 (csd added) with radial block (0, 0), degree 1 with (1, 0), (1, 1)
+          const float4 x0 = ld4(xn), c0 = ld4(csd + (int64_t)(so ? bid[1][g8] : bid[0][g8]) * CH + ch);
+          const float4 v0 = make_float4(x0.x + c0.x, x0.y + c0.y, x0.z + c0.z, x0.w + c0.w);
+          st4_nt(X0e + lm::xblk(L, 0, 0, so) * CH, mul4(v0, rv[0]));
+          lm_degree<L, 1>(xn, rv + 1, wl, we, X0e, X1e, X2e, so);
+        } else if (g == 1) {
+          lm_degree<L, 2>(xn, rv, wl, we, X0e, X1e, X2e, so);
+        } else if (g == 2) {
+          lm_degree<L, 3>(xn, rv, wl, we, X0e, X1e, X2e, so);
+        } else if constexpr (L >= 4) {
+          lm_degree<L, 4>(xn, rv, wl, we, X0e, X1e, X2e, so);
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  }
+}
+
 }  // namespace rg
 
 // Host side of the column order: perm[p] = natural radial column of permuted column p.
@@ -192,6 +336,63 @@ extern "C" int fu_radial_gather_perm(int32_t C, int32_t layout, int32_t* perm) {
   if (layout) radial_gather_perm_fill<1>(perm);
   else radial_gather_perm_fill<0>(perm);
   return FU_OK;
+}
+
+// perm[p] = natural radial column of permuted column p, lmax 3 or 4
+template <int L>
+static void radial_gather_lmax_perm_fill(int32_t* perm) {
+  for (int t = 0; t < 8 * L; ++t) {
+    const int g = t % L, cg = (t / L) & 3, so = t / (4 * L);
+    for (int j = 0; j < 3; ++j)
+      for (int c = 0; c < 32; ++c)
+        perm[t * rg::TN + 32 * j + c] =
+            lm::radblk(L, rg::grp_l(g, j), rg::grp_am(g, j), so) * rg::CH + 32 * cg + c;
+  }
+}
+
+extern "C" int fu_radial_gather_perm_lmax(int32_t C, int32_t lmax, int32_t* perm) {
+  const char* who = "fu_radial_gather_perm_lmax";
+  if (C != rg::CH) return set_error(FU_ERR_UNSUPPORTED, "%s: C=%d (the fused kernel takes C = 128)", who, C);
+  if (lmax != 3 && lmax != 4) return set_error(FU_ERR_UNSUPPORTED, "%s: lmax=%d (3 or 4)", who, lmax);
+  if (!perm) return set_error(FU_ERR_NULL, "%s: NULL argument", who);
+  if (lmax == 3) radial_gather_lmax_perm_fill<3>(perm);
+  else radial_gather_lmax_perm_fill<4>(perm);
+  return FU_OK;
+}
+
+extern "C" int fu_radial_gather_fwd_lmax(const float* h2, int64_t ldh, const void* W2, const float* bias,
+                                         const float* x, const int64_t* idx_i, const int64_t* idx_j,
+                                         const float* wigner, const float* wig_ext, const float* csd_emb,
+                                         const int64_t* batch, float* rad, float* X_m0, float* X_m1, float* X_m2,
+                                         int64_t E, int64_t N, int64_t S, int32_t C, int32_t K, int32_t lmax,
+                                         void* stream) {
+  const char* who = "fu_radial_gather_fwd_lmax";
+  if (E < 0 || N < 0 || S < 1 || ldh < K || N > 0x7fffffffLL || S > 0x7fffffffLL)
+    return set_error(FU_ERR_SHAPE, "%s: bad shape", who);
+  if (C != rg::CH || K != 16 * rg::KC)
+    return set_error(FU_ERR_UNSUPPORTED, "%s: C=%d K=%d (the fused kernel takes C = K = 128)", who, C, K);
+  if (lmax != 3 && lmax != 4) return set_error(FU_ERR_UNSUPPORTED, "%s: lmax=%d (3 or 4)", who, lmax);
+  if (E == 0) return FU_OK;
+  if (!h2 || !W2 || !x || !idx_i || !idx_j || !wigner || !wig_ext || !csd_emb || !batch || !rad || !X_m0 ||
+      !X_m1 || !X_m2)
+    return set_error(FU_ERR_NULL, "%s: NULL argument", who);
+  if (!aligned16(h2) || ldh % 4 != 0 || !aligned16(W2) || (bias && !aligned16(bias)) || !aligned16(x) ||
+      !aligned16(csd_emb) || !aligned16(rad) || !aligned16(X_m0) || !aligned16(X_m1) || !aligned16(X_m2))
+    return set_error(FU_ERR_ALIGN, "%s: h2, W2, bias, x, csd_emb, rad and X must be 16-byte aligned (ldh % 4 == 0)",
+                     who);
+  const int Nc = 6 * lmax * C;
+  const uint4* w2 = static_cast<const uint4*>(W2);
+  const float* cinv = reinterpret_cast<const float*>(w2 + resident_frag_vectors(Nc, K));
+  const int* summary = reinterpret_cast<const int*>(cinv + resident_cols(Nc)) + resident_cols(Nc);
+  const dim3 grid((unsigned)cdiv(E, rg::RBM)), block(256);
+  hipStream_t s = as_stream(stream);
+  if (lmax == 3)
+    hipLaunchKernelGGL(rg::radial_gather_lmax_kernel<3>, grid, block, 0, s, h2, ldh, w2, cinv, summary, bias, x,
+                       idx_i, idx_j, wigner, wig_ext, csd_emb, batch, rad, X_m0, X_m1, X_m2, E);
+  else
+    hipLaunchKernelGGL(rg::radial_gather_lmax_kernel<4>, grid, block, 0, s, h2, ldh, w2, cinv, summary, bias, x,
+                       idx_i, idx_j, wigner, wig_ext, csd_emb, batch, rad, X_m0, X_m1, X_m2, E);
+  return check_launch(who);
 }
 
 extern "C" int fu_radial_gather_fwd(const float* h2, int64_t ldh, const void* W2, const float* bias, const float* x,

@@ -275,10 +275,10 @@ class Packed_eSCN_Layer(nn.Module):
         RadialBank); otherwise it is computed here from x_edge_raw (E, B+2C).  wig_ext: the
         degree-3/4 Wigner rows (ops/lmax.wigner_extend), needed for lmax > 2.  before_ffn: a
         callable run after the edge-wise part is queued, before the node-side block (the model
-        queues the next block's radial output there, RadialOutputs.prelaunch).  rad_gather:
-        lmax 2, a callable (x_norm, layout) -> (rad_out, [X_m0, X_m1, X_m2]) that makes this
-        block's radial output and the gather's outputs in one kernel (RadialOutputs.
-        get_with_gather), used instead of rad_out."""
+        queues the next block's radial output there, RadialOutputs.prelaunch).  rad_gather: a
+        callable (x_norm, layout) -> (rad_out, [X_m0, X_m1, X_m2]) that makes this block's
+        radial output and the gather's outputs in one kernel (RadialOutputs.get_with_gather),
+        used instead of rad_out."""
         x_norm, x_skip = self._norm_skip(x_in)
         X_pre = None
         if rad_gather is not None:
@@ -338,10 +338,11 @@ class eSCN_Inference_Model(nn.Module):
     # X_m0.  Off by default: at bcc Fe the fused GEMM costs more than the gather traffic it
     # removes (each rotated element is produced once per 128-column tile of the 640 outputs).
     GATHER_IN_CONV1 = False
-    # lmax 2, C = 128, split-fp16 mode: each block's radial output layer writes the gather's
-    # outputs from its GEMM epilogue (fu_radial_gather_fwd: the separate gather kernel and its
-    # read of the radial output are gone; X bitwise as before).  False runs the output GEMM
-    # and the gather as two kernels (the output GEMM then queued early on the side stream).
+    # C = 128, split-fp16 mode: each block's radial output layer writes the gather's outputs
+    # from its GEMM epilogue (fu_radial_gather_fwd, lmax 2; fu_radial_gather_fwd_lmax, lmax 3,
+    # 4: the separate gather kernel and its read of the radial output are gone; X bitwise as
+    # before).  False runs the output GEMM and the gather as two kernels (the output GEMM then
+    # queued early on the side stream).
     RADIAL_GATHER = True
 
     def __init__(self, num_layers=4, sphere_channels=128, edge_channels=128, num_distance_basis=32, cutoff=5.0,
@@ -393,8 +394,10 @@ class eSCN_Inference_Model(nn.Module):
     def _radial_gather(self, layer, k: int) -> bool:
         """Whether block `layer` (radial output k of the bank) makes its radial output and its
         gather's outputs in one kernel (RADIAL_GATHER)."""
-        return (self.RADIAL_GATHER and not self.GATHER_IN_CONV1 and self.lmax == 2 and layer.layout in (0, 1)
-                and self.radial_bank.gather_ok(k))
+        if not self.RADIAL_GATHER or (self.lmax == 2 and self.GATHER_IN_CONV1):
+            return False
+        layouts = (0, 1) if self.lmax == 2 else (0,)
+        return layer.layout in layouts and self.radial_bank.gather_ok(k, self.lmax)
 
     def _radial_gather_next(self, k: int) -> bool:
         """The same for the block that reads radial output k (False past the last block)."""
@@ -468,7 +471,7 @@ class eSCN_Inference_Model(nn.Module):
             if self._radial_gather(layer, k + 1):
                 rad, before = None, None
                 rg = lambda xn, lay, n=k + 1: rads.get_with_gather(n, xn, idx_i_s, idx_j_s, wigner, csd_emb, batch_s,
-                                                                  lay)
+                                                                  lay, self.lmax, wig_ext)
             else:
                 rad, rg = rads.get(k + 1), None
                 before = None if self._radial_gather_next(k + 2) else (lambda n=k + 2: rads.prelaunch(n))

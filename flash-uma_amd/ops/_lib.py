@@ -56,6 +56,8 @@ SIGNATURES: dict[str, list] = {
     "fu_linear_resident": [P, I64, P, P, P, I64, I64, I32, I32, P],
     "fu_radial_gather_fwd": [P, I64, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, I32, I32, P],
     "fu_radial_gather_perm": [I32, I32, P],
+    "fu_radial_gather_fwd_lmax": [P, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32, I32, I32, P],
+    "fu_radial_gather_perm_lmax": [I32, I32, P],
     "fu_linear_gate": [P, I64, P, I64, P, P, I64, P, I64, P, I64, I64, I32, I32, I32, P, P],
     "fu_gather_linear_gate": [P, P, P, P, P, P, P, P, I64, P, P, I64, P, I64, I64, I32, P],
     "fu_complex_linear_gate": [P, P, I64, P, P, I64, P, P, P, I64, P, P, I64, P, I64, I32, I32, I64, I32, I32, P],

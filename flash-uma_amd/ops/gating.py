@@ -335,7 +335,11 @@ class EdgeBlock(torch.autograd.Function):
                 m0 = _gather_conv1_gate_m0(ops, conv1[0], conv1[1], C, _lib.stream_ptr(x_in.device))
         else:
             ops = gather_lmax_operands(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, L)
-            X = list(gather_lmax_fwd(*ops, L, topology))
+            if X_pre is not None:
+                X = list(X_pre)
+                X_pre.clear()
+            else:
+                X = list(gather_lmax_fwd(*ops, L, topology))
         Zo, Y = conv_pair_fwd(X, conv1, conv2, C, splits, m0)
         r = 4 if L == 2 else 5   # position of rad_out among the gather operands
         if rad_src is not None:
@@ -384,7 +388,7 @@ def edge_block(x_in, wigner, wig_ext, rad_out, idx_i, idx_j, csd_emb, batch, top
     rad_src: None, or the radial bank's (h2_k, W3_k, b3_k) source of rad_out; the backward
     then recomputes rad_out from it instead of keeping it (memory for one extra GEMM).
     sink: accumulators of the Wigner-row gradients (ops/edge_grad.py) or None.  gather_m0: conv1
-    m = 0 gathers its own operand (see EdgeBlock).  X_pre: lmax 2, a list of the gather's
+    m = 0 gathers its own operand (see EdgeBlock).  X_pre: a list of the gather's
     [X_m0, X_m1, X_m2] already formed from these operands (ops/radial.RadialOutputs.
     get_with_gather), emptied here; the forward then skips the gather kernel, the backward is the
     same."""

@@ -79,6 +79,36 @@ def gather_lmax_operands(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, 
     return ops
 
 
+def radial_gather_lmax_perm(C: int, L: int) -> torch.Tensor:
+    """(6 L C,) int64 on the host: row p of the weight that radial_gather_lmax_fwd takes is row
+    perm[p] of the radial output layer's weight (fu_radial_gather_perm_lmax)."""
+    import ctypes
+    buf = (ctypes.c_int32 * (6 * L * C))()
+    _lib.call("fu_radial_gather_perm_lmax", C, int(L), ctypes.addressof(buf))
+    return torch.tensor(list(buf), dtype=torch.int64)
+
+
+def radial_gather_lmax_fwd(h2, W2p, bias_p, x_in, idx_i, idx_j, wigner, wig_ext, csd_emb, batch, L):
+    """fu_radial_gather_fwd_lmax: the radial output layer and the lmax 3 / 4 gather's
+    (X_m0, X_m1, X_m2) from it in one kernel; returns (rad, X_m0, X_m1, X_m2).  W2p / bias_p:
+    the weight with its rows permuted by radial_gather_lmax_perm, pre-split by
+    linear_weight_split, and the bias permuted the same way."""
+    E, K = h2.shape
+    N, _, C = x_in.shape
+    if h2.stride(-1) != 1 or h2.stride(0) % 4 != 0 or h2.data_ptr() % 16 != 0:
+        h2 = h2.contiguous()
+    dev = x_in.device
+    rad = torch.empty(E, 6 * L * C, device=dev)
+    X_m0 = torch.empty(E, 2 * (L + 1) * C, device=dev)
+    X_m1 = torch.empty(E, 4 * L * C, device=dev)
+    X_m2 = torch.empty(E, 4 * (L - 1) * C, device=dev)
+    _lib.call("fu_radial_gather_fwd_lmax", h2.data_ptr(), h2.stride(0), W2p.data_ptr(), _lib.ptr(bias_p),
+              x_in.data_ptr(), idx_i.data_ptr(), idx_j.data_ptr(), wigner.data_ptr(), wig_ext.data_ptr(),
+              csd_emb.data_ptr(), batch.data_ptr(), rad.data_ptr(), X_m0.data_ptr(), X_m1.data_ptr(),
+              X_m2.data_ptr(), E, N, csd_emb.shape[0], C, K, int(L), _lib.stream_ptr(dev))
+    return rad, X_m0, X_m1, X_m2
+
+
 def gather_lmax_fwd(x_in, idx_i, idx_j, wigner, wig_ext, rad_out, csd_emb, batch, L, topology=None):
     """fu_gather_fwd_lmax: (X_m0, X_m1, X_m2) for operands from gather_lmax_operands.  The kernel
     walks each node's receiver and sender CSR segments (from the topology, or built here), so

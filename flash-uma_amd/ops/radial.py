@@ -195,25 +195,32 @@ class RadialBank(torch.nn.Module):
         """Output layer k's transposed weight pre-split for its input-gradient GEMM."""
         return self._split(f"W3_{k}_t", lambda K: K % 16 == 0)
 
-    def gather_split(self, k: int, layout: int):
-        """(W2p, b3p): output layer k's weight with its rows in the column order of
-        fu_radial_gather_fwd (ops/gather.radial_gather_perm), pre-split, and its bias in that
-        order; built on first use on the weight's device (weights are frozen)."""
-        from .gather import radial_gather_perm
+    def gather_split(self, k: int, layout: int, lmax: int = 2):
+        """(W2p, b3p): output layer k's weight with its rows in the column order of the fused
+        kernel (lmax 2: ops/gather.radial_gather_perm for `layout`; lmax 3, 4:
+        ops/lmax.radial_gather_lmax_perm), pre-split, and its bias in that order; built on first
+        use on the weight's device (weights are frozen)."""
         W, b = getattr(self, f"W3_{k}"), getattr(self, f"b3_{k}")
         cache = self.__dict__.setdefault("_gather_splits", {})
-        key = (k, int(layout))
+        key = (k, int(layout), int(lmax))
         if key not in cache or cache[key][0].device != W.device:
-            perm = radial_gather_perm(self.C, layout).to(W.device)
+            if lmax == 2:
+                from .gather import radial_gather_perm
+                perm = radial_gather_perm(self.C, layout)
+            else:
+                from .lmax import radial_gather_lmax_perm
+                perm = radial_gather_lmax_perm(self.C, lmax)
+            perm = perm.to(W.device)
             cache[key] = (linear_weight_split(W[perm].contiguous()), b[perm].contiguous())
         return cache[key]
 
-    def gather_ok(self, k: int) -> bool:
-        """Whether block k's output layer can run fused with the lmax = 2 gather
-        (fu_radial_gather_fwd): C = 128 and a 12C-wide output, in the split-fp16 mode (the mode
-        whose output GEMM, fu_linear_resident, the fused kernel's products equal bit for bit)."""
+    def gather_ok(self, k: int, lmax: int = 2) -> bool:
+        """Whether block k's output layer can run fused with the gather (fu_radial_gather_fwd,
+        lmax 2; fu_radial_gather_fwd_lmax, lmax 3, 4): C = 128 and a 6 lmax C-wide output, in the
+        split-fp16 mode (the mode whose output GEMM, fu_linear_resident, the fused kernel's
+        products equal bit for bit)."""
         W = getattr(self, f"W3_{k}")
-        return (self.C == 128 and tuple(W.shape) == (12 * self.C, self.C)
+        return (self.C == 128 and lmax in (2, 3, 4) and tuple(W.shape) == (6 * lmax * self.C, self.C)
                 and _lib.get_matmul_mode() == _lib.MATMUL_SPLIT_F16)
 
     def forward(self, gauss, Z, idx_i, idx_j, with_sources: bool = False, lazy: bool = False):
@@ -273,20 +280,27 @@ class RadialOutputs:
             _out_gemm(h2k, W, b, W2, out)
         self._pre[k] = (out, side)
 
-    def get_with_gather(self, k: int, x_in, idx_i, idx_j, wigner, csd_emb, batch, layout):
-        """Block k's output together with the lmax = 2 gather's (X_m0, X_m1, X_m2) of node
-        features x_in, from one kernel (fu_radial_gather_fwd; bank.gather_ok(k) must hold).
-        The output node is the one get(k) makes (same backward); the X arrays carry no autograd
-        history: the consumer's gather backward (ops/gating.EdgeBlock) returns the gradients of
-        x_in, wigner and the output."""
-        from .gather import radial_gather_fwd
+    def get_with_gather(self, k: int, x_in, idx_i, idx_j, wigner, csd_emb, batch, layout, lmax=2, wig_ext=None):
+        """Block k's output together with the gather's (X_m0, X_m1, X_m2) of node features x_in,
+        from one kernel (fu_radial_gather_fwd, or fu_radial_gather_fwd_lmax with the degree-3/4
+        Wigner rows wig_ext for lmax 3, 4; bank.gather_ok(k, lmax) must hold).  The output node
+        is the one get(k) makes (same backward); the X arrays carry no autograd history: the
+        consumer's gather backward (ops/gating.EdgeBlock) returns the gradients of x_in, wigner,
+        wig_ext and the output."""
         W, b, Wt, W2, W2t = self._w(k)
-        W2p, b3p = self.bank.gather_split(k, layout)
+        W2p, b3p = self.bank.gather_split(k, layout, lmax)
         rq = _lib.require
-        rad, *X = radial_gather_fwd(self.h2s[k].detach(), W2p, b3p, rq(x_in.detach(), torch.float32, "x_in"),
-                                    rq(idx_i, torch.int64, "idx_i"), rq(idx_j, torch.int64, "idx_j"),
-                                    rq(wigner.detach(), torch.float32, "wigner"),
-                                    rq(csd_emb, torch.float32, "csd_emb"), rq(batch, torch.int64, "batch"), layout)
+        h2k = self.h2s[k].detach()
+        xs = (rq(x_in.detach(), torch.float32, "x_in"), rq(idx_i, torch.int64, "idx_i"),
+              rq(idx_j, torch.int64, "idx_j"), rq(wigner.detach(), torch.float32, "wigner"))
+        nodes = (rq(csd_emb, torch.float32, "csd_emb"), rq(batch, torch.int64, "batch"))
+        if lmax == 2:
+            from .gather import radial_gather_fwd
+            rad, *X = radial_gather_fwd(h2k, W2p, b3p, *xs, *nodes, layout)
+        else:
+            from .lmax import radial_gather_lmax_fwd
+            ext = rq(wig_ext.detach(), torch.float32, "wig_ext")
+            rad, *X = radial_gather_lmax_fwd(h2k, W2p, b3p, *xs, ext, *nodes, lmax)
         out = _RadialOutFn.apply(self.h2s[k], W, b, Wt, self.holder, k, W2, W2t, rad)
         self._made += 1
         if self._made == self.bank.G:

@@ -34,7 +34,7 @@ KERNEL_ENTRY = {
     "complex_weight_scale_kernel": "fu_complex_weight_split", "complex_weight_split_kernel": "fu_complex_weight_split",
     "resident_weight_scale_kernel": "fu_linear_weight_split", "resident_weight_summary_kernel": "fu_linear_weight_split",
     "resident_weight_split_kernel": "fu_linear_weight_split", "linear_resident_kernel": "fu_linear_resident",
-    "radial_gather_kernel": "fu_radial_gather_fwd",
+    "radial_gather_kernel": "fu_radial_gather_fwd", "radial_gather_lmax_kernel": "fu_radial_gather_fwd_lmax",
     "rms_norm_fwd_kernel": "fu_rms_norm_sh_fwd", "rms_norm_bwd_kernel": "fu_rms_norm_sh_bwd",
     "gate_fwd_kernel": "fu_gate_act_fwd", "gate_bwd_kernel": "fu_gate_act_bwd",
     "gather_rows_kernel": "fu_gather_rows", "scatter_rows_kernel": "fu_scatter_rows",

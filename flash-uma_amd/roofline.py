@@ -190,6 +190,14 @@ def _radial_gather(a):
     return E * ((K + 30 * C + 34) * 4 + 16) + N * (9 * C * 4 + 8) + 12 * C * K * 4, 2 * E * 12 * C * K
 
 
+def _radial_gather_l(a):
+    # lmax 3, 4: h2 read, rad (6L C) and X (2(5L - 1) C) written per edge, the ids, the 34 + ext
+    # Wigner scalars read, the weight once, the node rows once per launch
+    E, N, C, K, L = a[15], a[16], a[18], a[19], a[20]
+    per_edge = (K + 6 * L * C + 2 * (5 * L - 1) * C + 34 + _ext(L)) * 4 + 16
+    return E * per_edge + N * ((L + 1) ** 2 * C * 4 + 8) + 6 * L * C * K * 4, 2 * E * 6 * L * C * K
+
+
 def _wig_ext_fwd(a):
     E, L = a[2], a[3]
     return E * (34 + _ext(L)) * 4, 0
@@ -303,6 +311,7 @@ WORK = {
     "fu_linear_batched": _linear_batched,
     "fu_linear_resident": _linear_resident,
     "fu_radial_gather_fwd": _radial_gather,
+    "fu_radial_gather_fwd_lmax": _radial_gather_l,
     "fu_linear_ln_silu": _linear_ln_silu,
     "fu_linear_ln_silu_bwd": _linear_ln_silu_bwd,
     "fu_linear_dgrad_ln_silu_bwd": _linear_dgrad_ln_silu_bwd,

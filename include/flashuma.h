@@ -50,8 +50,8 @@ extern "C" {
  * arguments of fu_gather_fwd_lmax; 0.4.0 added fu_linear_weight_split_bytes,
  * fu_linear_weight_split and fu_linear_resident (nothing changed); 0.5.0 added the W2 argument
  * (before the stream) of fu_linear, fu_linear_gate, fu_linear_gate_bwd and
- * fu_linear_dgrad_ln_silu_bwd; 0.6.0 added fu_radial_gather_fwd and fu_radial_gather_perm
- * (nothing changed).  A caller built against
+ * fu_linear_dgrad_ln_silu_bwd; 0.6.0 added fu_radial_gather_fwd, fu_radial_gather_perm and
+ * their _lmax forms (nothing changed).  A caller built against
  * another version must not call into this library. */
 int fu_version(void);
 
@@ -376,6 +376,25 @@ int fu_radial_gather_fwd(const float* h2, int64_t ldh, const void* W2, const flo
  * (even t) or of degree 2 (odd t) of side t / 8 for channels 32 ((t / 2) % 4) .. + 31
  * (radial_gather.hip).  C = 128, layout 0 or 1. */
 int fu_radial_gather_perm(int32_t C, int32_t layout, int32_t* perm);
+
+/* The radial output layer fused with the lmax 3 / 4 gather forward (replaces model.py:149 and
+ * the lmax form of the gather, fu_gather_fwd_lmax): rad (E, 6 lmax C) and X_m0 (E, 2(lmax+1)C),
+ * X_m1 (E, 4 lmax C), X_m2 (E, 4(lmax-1)C) in the lmax kernels' block order, bitwise as
+ * fu_linear_resident with the unpermuted weight followed by fu_gather_fwd_lmax.  W2: the
+ * weight (6 lmax C x K) with its rows permuted by fu_radial_gather_perm_lmax, pre-split by
+ * fu_linear_weight_split; bias permuted the same way (may be NULL).  wig_ext: the degree-3/4
+ * Wigner rows (fu_wigner_ext_fwd).  C = K = 128; 16-byte alignment as fu_radial_gather_fwd. */
+int fu_radial_gather_fwd_lmax(const float* h2, int64_t ldh, const void* W2, const float* bias, const float* x,
+                              const int64_t* idx_i, const int64_t* idx_j, const float* wigner, const float* wig_ext,
+                              const float* csd_emb, const int64_t* batch, float* rad, float* X_m0, float* X_m1,
+                              float* X_m2, int64_t E, int64_t N, int64_t S, int32_t C, int32_t K, int32_t lmax,
+                              void* stream);
+
+/* Host-only: perm[p] (6 lmax C entries) = the radial column that fu_radial_gather_fwd_lmax
+ * computes as its weight's row p: tile t (96 columns) holds, for side t / (4 lmax) and
+ * channels 32 ((t / lmax) % 4) .. + 31, the radial blocks of degrees 0 and 1 (t % lmax = 0)
+ * or of degree t % lmax + 1.  C = 128, lmax 3 or 4. */
+int fu_radial_gather_perm_lmax(int32_t C, int32_t lmax, int32_t* perm);
 
 /* conv1 m = 0 fused with the gate activation (model.py:152-153 with ops/gating.py:32-103):
  * Y = A W^T + bias with N = (2L+1)C columns (L = lmax) in the gate-paired order: 64-column

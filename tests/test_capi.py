@@ -325,3 +325,37 @@ def test_radial_gather_fwd_argument_checks():
     assert st == -1
     st, msg = _status("fu_radial_gather_fwd", *args(128, 128, 128, 1))
     assert st == -5
+
+
+@pytest.mark.parametrize("L", [3, 4])
+def test_radial_gather_lmax_perm(L):
+    """fu_radial_gather_perm_lmax (host only): a permutation of the 6 L C radial columns whose
+    96-column tiles hold, for one side and 32 consecutive channels, the radial blocks of degrees
+    0 and 1 ((l, |m|) = (0, 0), (1, 0), (1, 1)) or of one degree l >= 2 ((l, 0), (l, 1), (l, 2)),
+    each block at its place in the lmax kernels' order (|m| = 0: 2l + side; 1: 2(L+1) + 2(l-1)
+    + side; 2: 4L + 2 + 2(l-2) + side)."""
+    from ops.lmax import radial_gather_lmax_perm
+    C = 128
+    perm = radial_gather_lmax_perm(C, L).tolist()
+    assert sorted(perm) == list(range(6 * L * C))
+
+    def radblk(l, am, so):
+        return 2 * l + so if am == 0 else (2 * (L + 1) + 2 * (l - 1) + so if am == 1 else 4 * L + 2 + 2 * (l - 2) + so)
+
+    for t in range(8 * L):
+        g, cg, so = t % L, (t // L) % 4, t // (4 * L)
+        blocks = [(0, 0), (1, 0), (1, 1)] if g == 0 else [(g + 1, 0), (g + 1, 1), (g + 1, 2)]
+        for j, (l, am) in enumerate(blocks):
+            cols = perm[96 * t + 32 * j:96 * t + 32 * j + 32]
+            assert cols == [radblk(l, am, so) * C + 32 * cg + c for c in range(32)]
+    st, msg = _status("fu_radial_gather_perm_lmax", C, 2, None)
+    assert st == -2 and "lmax=2" in msg
+    st, msg = _status("fu_radial_gather_perm_lmax", C, L, None)
+    assert st == -5
+    args = lambda C_, K_, L_: (None, 128, *([None] * 13), 10, 4, 1, C_, K_, L_, None)
+    st, msg = _status("fu_radial_gather_fwd_lmax", *args(128, 128, 5))
+    assert st == -2 and "lmax=5" in msg
+    st, msg = _status("fu_radial_gather_fwd_lmax", *args(64, 128, L))
+    assert st == -2 and "C=64" in msg
+    st, msg = _status("fu_radial_gather_fwd_lmax", *args(128, 128, L))
+    assert st == -5

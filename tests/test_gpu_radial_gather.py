@@ -109,3 +109,75 @@ def test_model_radial_gather_matches_two_kernels(cuda, monkeypatch):
         assert calls.count("fu_gather_fwd") == (0 if fused else 2)
     for k in ("energy", "forces", "stress"):
         assert torch.equal(outs[False][k], outs[True][k]), k
+
+
+def _lmax_inputs(cuda, E, N, L, seed):
+    from ops.lmax import ext_width
+    g = torch.Generator().manual_seed(seed)
+    C, K = 128, 128
+    wide = torch.randn(E, 5 * K, generator=g)
+    h2 = wide.to(cuda)[:, K:2 * K]
+    W3 = (torch.randn(6 * L * C, K, generator=g) / K ** 0.5).to(cuda)
+    b3 = torch.randn(6 * L * C, generator=g).to(cuda)
+    x = torch.randn(N, (L + 1) ** 2, C, generator=g).to(cuda)
+    idx_i = torch.randint(0, N, (E,), generator=g).to(cuda)
+    idx_j = torch.sort(torch.randint(0, N, (E,), generator=g)).values.to(cuda)
+    wig = torch.randn(E, 34, generator=g).to(cuda)
+    ext = torch.randn(E, ext_width(L), generator=g).to(cuda)
+    csd = torch.randn(2, C, generator=g).to(cuda)
+    batch = torch.randint(0, 2, (N,), generator=g).to(cuda)
+    return h2, W3, b3, x, idx_i, idx_j, wig, ext, csd, batch
+
+
+@pytest.mark.parametrize("L", [3, 4])
+@pytest.mark.parametrize("E,N", [(20000, 700), (1001, 64), (1, 1)])
+def test_radial_gather_lmax_bitwise(cuda, L, E, N):
+    """fu_radial_gather_fwd_lmax against fu_linear_resident (unpermuted weight) followed by
+    fu_gather_fwd_lmax (edge-parallel and node-centric forms): rad and X bitwise equal."""
+    from ops import linear, lmax
+    h2, W3, b3, x, idx_i, idx_j, wig, ext, csd, batch = _lmax_inputs(cuda, E, N, L, seed=7 * E + N + L)
+    rad_ref = linear.gemm_resident(h2, linear.linear_weight_split(W3), W3.shape[0], b3)
+    perm = lmax.radial_gather_lmax_perm(128, L).to(cuda)
+    got = lmax.radial_gather_lmax_fwd(h2, linear.linear_weight_split(W3[perm].contiguous()), b3[perm].contiguous(),
+                                      x, idx_i, idx_j, wig, ext, csd, batch, L)
+    for topology in (None,):
+        X_ref = lmax.gather_lmax_fwd(x, idx_i, idx_j, wig, ext, rad_ref, csd, batch, L, topology)
+        _assert_equal((rad_ref, *X_ref), got)
+
+
+@pytest.mark.parametrize("L", [3, 4])
+def test_model_radial_gather_lmax_matches_two_kernels(cuda, monkeypatch, L):
+    """lmax 3 / 4 backbone (2 layers) on bcc Fe 6^3 (432 atoms): energy, forces and stress bit for
+    bit equal with the fused radial-gather kernel on and off; the fused kernel called once per
+    block and the lmax gather forward not at all."""
+    import escn_md
+    import heads
+    import systems
+    from ops import _lib
+    from wrapper import ZeroAllocBackbone
+    bb = escn_md.eSCNMDBackbone(num_layers=2, sphere_channels=128, hidden_channels=128, lmax=L, seed=0)
+    hd = heads.MLPEnergyHead(128, 128, seed=1)
+    model = heads.PotentialModel(ZeroAllocBackbone(bb.to(cuda)), hd.to(cuda))
+    s = systems.bcc_fe(n_rep=6)
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, 6.0, 30)
+    data = heads.make_atomic_data(s, ei, off, cuda)
+    ce = model.backbone.ce
+    real = _lib.call
+    outs = {}
+    for fused in (False, True):
+        calls = []
+
+        def spy(name, *args):
+            calls.append(name)
+            return real(name, *args)
+
+        monkeypatch.setattr(ce, "RADIAL_GATHER", fused)
+        monkeypatch.setattr(_lib, "call", spy)
+        out = model(data, compute_forces=True, compute_stress=True)
+        torch.cuda.synchronize()
+        monkeypatch.setattr(_lib, "call", real)
+        outs[fused] = {k: v.detach().cpu() for k, v in out.items() if torch.is_tensor(v)}
+        assert calls.count("fu_radial_gather_fwd_lmax") == (2 if fused else 0)
+        assert calls.count("fu_gather_fwd_lmax") == (0 if fused else 2)
+    for k in ("energy", "forces", "stress"):
+        assert torch.equal(outs[False][k], outs[True][k]), k
