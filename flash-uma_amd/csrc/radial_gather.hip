@@ -1,4 +1,5 @@
-// Radial output layer fused with the gather-rotate forward (lmax = 2, C = 128).
+// Radial output layer fused with the gather-rotate forward (C = 128; lmax 2 below, lmax 3 and 4
+// further down, radial_gather_lmax_kernel).
 //
 // Each block's radial output rad = h2 W3^T + b3 (model.py:149, K = C = 128, N = 12 C) is read
 // exactly once in the forward, by the gather (ops/gather.py:114-154: X = rad * (D x[node]) per
@@ -36,7 +37,7 @@ constexpr int RBM = kResRows;     // rows (edges) per workgroup
 constexpr int KC = 8;             // 16-wide K chunks: K = 128
 constexpr int RPLANE = kResPlane;  // fp16 per plane (one chunk of the panel)
 constexpr int CH = 128;           // channels
-constexpr int NT = 16;            // output tiles: 2 sides x 4 channel groups x 2 halves of the radial blocks
+constexpr int NT = 16;            // output tiles (lmax 2): 2 sides x 4 channel groups x 2 degree groups
 constexpr int TN = 96;            // columns per tile: 3 radial blocks x 32 channels
 constexpr int RES3 = 96 + 8;      // floats per row of a wave's epilogue slice: 4 RES3 = 32 mod 64 banks
 
