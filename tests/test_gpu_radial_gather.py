@@ -181,3 +181,29 @@ def test_model_radial_gather_lmax_matches_two_kernels(cuda, monkeypatch, L):
         assert calls.count("fu_gather_fwd_lmax") == (0 if fused else 2)
     for k in ("energy", "forces", "stress"):
         assert torch.equal(outs[False][k], outs[True][k]), k
+
+
+def test_radial_gather_with_recomputed_radial_outputs(cuda, monkeypatch):
+    """The large-graph path that keeps each block's (E, C) radial source and recomputes the
+    radial output in the backward (RAD_RECOMPUTE_MIN_EDGES) together with the fused forward:
+    the recomputed output (fu_linear_resident, unpermuted weight) is the one the fused kernel
+    wrote, so energy, forces and stress are bit for bit those of the path that keeps it."""
+    import escn_md
+    import heads
+    import systems
+    from wrapper import ZeroAllocBackbone
+    bb = escn_md.eSCNMDBackbone(seed=0, num_layers=2)
+    hd = heads.MLPEnergyHead(bb.sphere_channels, bb.hidden_channels, seed=1)
+    model = heads.PotentialModel(ZeroAllocBackbone(bb.to(cuda)), hd.to(cuda))
+    s = systems.bcc_fe(n_rep=6)
+    ei, off = systems.neighbor_list(s.pos, s.cell, s.pbc, 6.0, 30)
+    data = heads.make_atomic_data(s, ei, off, cuda)
+    ce = model.backbone.ce
+    assert ce.RADIAL_GATHER
+    outs = []
+    for threshold in (ce.RAD_RECOMPUTE_MIN_EDGES, 0):
+        monkeypatch.setattr(ce, "RAD_RECOMPUTE_MIN_EDGES", threshold)
+        out = model(data, compute_forces=True, compute_stress=True)
+        outs.append({k: v.detach().cpu() for k, v in out.items() if torch.is_tensor(v)})
+    for k in ("energy", "forces", "stress"):
+        assert torch.equal(outs[0][k], outs[1][k]), k
